@@ -1,0 +1,210 @@
+/* mk2.h -- C ABI of the MI355X (gfx950) K2 decode-layer kernels.
+ *
+ * One GPU's share of the sgl-amd-mono decoder-layer monokernel: the FP4 indexer
+ * scores and exact top-k, sparse-MLA decode over the selected FP8 latent-KV rows,
+ * W_UV and o_proj, RMSNorm, the router top-k and the FP8 / MXFP4 routed and shared
+ * experts.  The TP all-reduces of the reference are omitted (one GPU).
+ *
+ * Every entry point takes plain device pointers and sizes, enqueues work on the
+ * given HIP stream and returns 0, or a nonzero MK2_E* code with a message readable
+ * through mk2_last_error() (thread-local).  Nothing here allocates device memory or
+ * synchronizes the host: scratch is a caller-owned workspace whose size the
+ * *_workspace_bytes queries report, so every launch can be captured in a HIP graph.
+ * Buffers are caller-owned and must stay alive until the stream work completes.
+ *
+ * Reference interfaces replaced (paths in sgl-project/sgl-amd-mono):
+ *   mk2_layer_launch          Glm53LayerOp.launch -> glm5_monokernel(...).launch
+ *                             sgl_amd_mono/glm53/gfx950/runner.py:374-470,
+ *                             sgl_amd_mono/glm53/gfx950/kernel.py:7155-7245
+ *   mk2_moe_launch            the router/ug/down stages of that launch
+ *                             kernel.py:5471-7152
+ *   mk2_indexer_topk_launch   index_score + index_slice stages, kernel.py:3577-4883,
+ *                             with the FP4 keys of deepseek_v4/gfx950/kernels/stages/
+ *                             indexer.py:412-803
+ *   mk2_sparse_mla_launch     split + uv + o stages, kernel.py:4885-5469
+ *   *_workspace_bytes         the scratch layout of glm53/gfx950/layout.py:181-318
+ *   mk2_last_error            the ValueError/RuntimeError text the reference's host
+ *                             raises before a launch (runner.py:312-318,388-421)
+ */
+#ifndef MK2_H
+#define MK2_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MK2_ABI_VERSION 1
+
+/* return codes */
+#define MK2_OK 0
+#define MK2_EINVAL 1   /* a shape, pointer or size argument is invalid */
+#define MK2_ELAUNCH 2  /* the HIP runtime refused a launch */
+#define MK2_ENOSPACE 3 /* the workspace is smaller than *_workspace_bytes reports */
+
+/* router kinds */
+#define MK2_ROUTER_SOFTMAX 0      /* top-k of logits, softmax over the k picked */
+#define MK2_ROUTER_SIGMOID_BIAS 1 /* top-k of sigmoid + bias, sigmoid / sum * scale */
+
+/* expert weight formats */
+#define MK2_FMT_FP8 0   /* E4M3, f32 scale per 128 x 128 block, bf16 activations */
+#define MK2_FMT_MXFP4 1 /* E2M1, E8M0 per 32, activations quantized to MXFP8 per 32 */
+
+typedef void* mk2_stream_t; /* a hipStream_t */
+
+/* ---------------------------------------------------------------------- MoE
+ * Weight layouts (see DESIGN.md "tile packing"): every weight matrix [N, K] is
+ * stored as tiles [N/16][K/128][64 lanes][chunk] where lane l holds row l%16 and
+ * k = 32*(l/16) .. +31 of the 128-k block; chunk = 64 B (bf16), 32 B (E4M3),
+ * 16 B (E2M1).  MXFP4 E8M0 scales: [N/16][ceil(K/512)][64 lanes][4 B].
+ * gate and up are stacked as one [2*inter, hidden] matrix (gate first). */
+typedef struct mk2_moe_shape {
+  int rows;         /* M: decode rows, 1..32 */
+  int hidden;       /* H, multiple of 512 */
+  int n_experts;    /* E, multiple of 64, <= 256 */
+  int top_k;        /* 1..8 */
+  int inter;        /* routed expert intermediate size */
+  int router;       /* MK2_ROUTER_* */
+  int expert_fmt;   /* MK2_FMT_* of the routed experts */
+  int n_shared;     /* 0 or 1 shared expert, always MK2_FMT_FP8 */
+  int shared_inter; /* shared expert intermediate size */
+  int norm;         /* 1: RMSNorm(x) * gamma feeds the router and experts */
+  int residual;     /* 1: out = x + moe, else out = moe */
+  float route_scale;
+  float eps;
+} mk2_moe_shape;
+
+typedef struct mk2_moe_weights {
+  const void* gamma;       /* bf16 [H] (norm only) */
+  const void* w_router;    /* bf16 tiles of [E, H] */
+  const float* router_bias;/* f32 [E] (sigmoid_bias only) */
+  const void* w13;         /* routed gate|up: [E] x tiles of [2*inter, H] */
+  const void* s13;         /* FP8: f32 [E][2*inter/128][H/128]; MXFP4: E8M0 tiles */
+  const void* w2;          /* routed down: [E] x tiles of [H, inter] */
+  const void* s2;          /* FP8: f32 [E][H/128][inter/128]; MXFP4: E8M0 tiles */
+  const void* ws13;        /* shared gate|up E4M3 tiles of [2*shared_inter, H] */
+  const float* ss13;       /* f32 [2*shared_inter/128][H/128] */
+  const void* ws2;         /* shared down E4M3 tiles of [H, shared_inter] */
+  const float* ss2;        /* f32 [H/128][shared_inter/128] */
+} mk2_moe_weights;
+
+typedef struct mk2_moe_args {
+  mk2_moe_shape shape;
+  mk2_moe_weights w;
+  const void* x;           /* bf16 [M][H] input rows (the residual when residual=1) */
+  void* out;               /* bf16 [M][H]; must not alias x */
+  void* workspace;
+  size_t workspace_bytes;
+  /* optional outputs for checking; NULL skips each */
+  float* logits;           /* f32 [M][E] router logits */
+  int32_t* topk_ids;       /* [M][top_k], rank order */
+  float* topk_weights;     /* [M][top_k] */
+} mk2_moe_args;
+
+int mk2_moe_workspace_bytes(const mk2_moe_shape* shape, size_t* bytes);
+int mk2_moe_launch(const mk2_moe_args* args, mk2_stream_t stream);
+
+/* ------------------------------------------------------------ indexer + top-k
+ * Index cache pages: [pages][64 tokens][64 B E2M1 codes] followed by
+ * [64 tokens][4 B E8M0, one per 32 dims]: 4352 B a page.  Page table int32
+ * [requests][table_stride], logical page -> physical page.  Row r scores the
+ * context positions 0 .. ctx_len[r]-1 of request req_ids[r]. */
+typedef struct mk2_indexer_shape {
+  int rows;        /* 1..32 */
+  int heads;       /* index heads, multiple of 16, <= 64 */
+  int dim;         /* 128 */
+  int topk;        /* multiple of 64, 64..4096 */
+  int max_ctx;     /* upper bound of ctx_len, <= 65536, multiple of 64 */
+  int table_stride;/* page table row stride (entries) */
+} mk2_indexer_shape;
+
+typedef struct mk2_indexer_args {
+  mk2_indexer_shape shape;
+  const void* q;            /* bf16 [rows][heads][128] */
+  const void* w;            /* bf16 [rows][heads] head weights */
+  const uint8_t* cache;     /* index pages */
+  const int32_t* page_table;/* [requests][table_stride] */
+  const int32_t* req_ids;   /* [rows] */
+  const int32_t* ctx_len;   /* [rows] */
+  float* scores;            /* f32 [rows][max_ctx] (written for 0..ctx_len-1) */
+  int32_t* topk;            /* [rows][topk] positions, -1 padded */
+  void* workspace;
+  size_t workspace_bytes;
+} mk2_indexer_args;
+
+int mk2_indexer_workspace_bytes(const mk2_indexer_shape* shape, size_t* bytes);
+int mk2_indexer_topk_launch(const mk2_indexer_args* args, mk2_stream_t stream);
+
+/* --------------------------------------------------------------- sparse MLA
+ * Latent KV pages: [pages][64 tokens][576 B E4M3] with one f32 scale per token
+ * in kv_scale [pages][64].  Row r attends the positions sel[r][0..topk-1] (-1 =
+ * unused) of request req_ids[r]; then W_UV (bf16 [heads][v_dim][512]) and W_o
+ * (bf16 tiles of [hidden, heads*v_dim]); out = bf16(h + o W_o^T) (h may be NULL). */
+typedef struct mk2_mla_shape {
+  int rows;        /* 1..32 */
+  int heads;       /* 16 */
+  int kv_lora;     /* 512 */
+  int rope;        /* 64 */
+  int v_dim;       /* multiple of 16 */
+  int hidden;      /* multiple of 16 */
+  int topk;        /* selected positions a row, multiple of 64 */
+  int table_stride;
+  float sm_scale;
+} mk2_mla_shape;
+
+typedef struct mk2_mla_args {
+  mk2_mla_shape shape;
+  const void* q;            /* bf16 [rows][heads][576] (W_UK absorbed) */
+  const uint8_t* kv;        /* latent KV pages */
+  const float* kv_scale;    /* [pages][64] */
+  const int32_t* page_table;
+  const int32_t* req_ids;   /* [rows] */
+  const int32_t* sel;       /* [rows][topk] positions */
+  const void* w_uv;         /* bf16 [heads][v_dim][512] */
+  const void* w_o;          /* bf16 tiles of [hidden, heads*v_dim] */
+  const void* h;            /* bf16 [rows][hidden] residual or NULL */
+  void* out;                /* bf16 [rows][hidden] */
+  void* workspace;
+  size_t workspace_bytes;
+  float* o_latent;          /* optional f32 [rows][heads][512] merged latent output */
+} mk2_mla_args;
+
+int mk2_mla_workspace_bytes(const mk2_mla_shape* shape, size_t* bytes);
+int mk2_sparse_mla_launch(const mk2_mla_args* args, mk2_stream_t stream);
+
+/* ------------------------------------------------------------ the K2 layer
+ * indexer -> top-k -> sparse MLA -> o_proj + residual h -> RMSNorm(eps) -> MoE +
+ * residual.  The three argument blocks are the ones above; their q/sel/out fields
+ * that the chain produces itself are ignored.  out: bf16 [rows][hidden]. */
+typedef struct mk2_layer_args {
+  mk2_indexer_args indexer; /* scores/topk may be NULL (then kept in the workspace) */
+  mk2_mla_args mla;         /* sel, out are ignored: the chain supplies them */
+  mk2_moe_args moe;         /* x is ignored (the attention output); norm=1, residual=1 */
+  void* attn_out;           /* optional bf16 [rows][hidden]: the residual after attention */
+  void* out;
+  void* workspace;
+  size_t workspace_bytes;
+} mk2_layer_args;
+
+int mk2_layer_workspace_bytes(const mk2_layer_args* args, size_t* bytes);
+int mk2_layer_launch(const mk2_layer_args* args, mk2_stream_t stream);
+
+/* ------------------------------------------------------------------ misc */
+const char* mk2_last_error(void);
+int mk2_abi_version(void);
+
+/* Matrix-core operand self-test: one 16x16 tile product per mode, for the layout
+ * checks of the test suite (no counterpart in the reference).  mode 0: bf16 x bf16
+ * over K=128 (a, b: bf16 [16][128]); mode 1: E2M1 x E4M3 over K=128 with E8M0
+ * scales (a: [16][64 B], sa: [16][4], b: [16][128 B], sb: [16][4]); mode 2: E4M3
+ * widened to bf16 x bf16 (a: [16][128 B] E4M3, b: bf16 [16][128]).  d: f32
+ * [16][16], d[i][j] = sum_k A[i][k] B[j][k]. */
+int mk2_selftest_mfma(int mode, const void* a, const void* sa, const void* b,
+                      const void* sb, float* d, mk2_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MK2_H */

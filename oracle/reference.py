@@ -1,0 +1,213 @@
+"""The K2 layer's arithmetic on the CPU (test infrastructure only).
+
+Each function restates one piece of the reference's decode layer and cites where.
+Rounding points that are part of the dataflow (bf16 hand-offs between stages,
+activation quantization) are stated here explicitly, because the HIP path rounds
+at the same points; everything between them is computed in f32 (f64 for scores).
+
+Pinned by tests/test_oracle_reference.py:
+  index_scores      -- explicit loops on tiny inputs; f64 closed form
+  exact_topk        -- brute force, torch.sort (stable) and torch.topk set equality
+  sparse_mla        -- dense softmax attention on the gathered rows (brute force),
+                       key-order invariance
+  rmsnorm           -- torch.nn.functional.rms_norm
+  route_softmax     -- softmax over all experts, top-k, renormalize (closed form)
+  route_sigmoid_bias-- sigmoid, top-k by sigmoid + bias, normalized * scale
+  swiglu            -- torch.nn.functional.silu
+  moe_block         -- a single expert with hand-built weights; linearity in the
+                       route weights
+  k2_layer          -- composition of the above (checked piecewise)
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import codecs
+
+
+# ------------------------------------------------------------------- indexer scores
+def index_scores(q: torch.Tensor, w: torch.Tensor, keys: torch.Tensor) -> torch.Tensor:
+    """score[c] = sum_h relu(q[h] . k[c]) * w[h], in f64.
+
+    q [H, D] (bf16 values), w [H], keys [N, D] (dequantized FP4 keys).  Restates
+    deepseek_v4/gfx950/kernels/stages/indexer.py:461-602 (relu(MFMA) * w, head sum)
+    and the f64 check of test/kernels/glm53/check_topk.py:107-113.
+    """
+    s = torch.relu(keys.double() @ q.double().T) @ w.double()
+    return s + 0.0  # -0.0 -> +0.0: a sum that starts from +0 never ends at -0
+
+
+def radix_lists(scores_f32: torch.Tensor, k: int) -> torch.Tensor:
+    """The exact top-k of f32 scores, as the 12-bit radix select lists it.
+
+    Keys are the radix keys of the f32 bits; the selected set is the first k of a
+    stable descending sort (ties: lowest index first, check_topk.py:116-123).  The
+    list order is check_topk.radix_lists at a 12-bit prefix (check_topk.py:72-85):
+    keys whose top 12 bits exceed the k-th key's, in position order; then keys with
+    the same 12-bit prefix that exceed the k-th key, in position order; then keys
+    equal to the k-th key, in position order, as many as fill k.  When the row has
+    k or fewer entries every entry is kept, in position order
+    (deepseek_v4/gfx950/kernels/stages/indexer.py:466-469).
+    """
+    n = scores_f32.numel()
+    if n <= k:
+        return torch.arange(n, dtype=torch.int64)
+    keys = codecs.radix_keys(scores_f32.float())
+    kth = torch.sort(keys, descending=True, stable=True).values[k - 1]
+    hi, khi = keys >> 20, kth >> 20
+    above = (hi > khi).nonzero().flatten()
+    under = ((hi == khi) & (keys > kth)).nonzero().flatten()
+    ties = (keys == kth).nonzero().flatten()[: k - len(above) - len(under)]
+    return torch.cat([above, under, ties])
+
+
+def exact_topk_set(scores_f32: torch.Tensor, k: int) -> torch.Tensor:
+    """The selected positions as a sorted set: the first k of the stable descending
+    sort of radix keys (glm53/check.py:111-114, check_topk.py:116-123)."""
+    n = scores_f32.numel()
+    if n <= k:
+        return torch.arange(n, dtype=torch.int64)
+    keys = codecs.radix_keys(scores_f32.float())
+    idx = torch.sort(keys, descending=True, stable=True).indices[:k]
+    return torch.sort(idx).values
+
+
+# ----------------------------------------------------------------------- sparse MLA
+def sparse_mla(q: torch.Tensor, kv: torch.Tensor, sm_scale: float, kv_lora: int) -> torch.Tensor:
+    """Softmax attention of one request over its selected latent-KV rows.
+
+    q [Hq, kv_lora + rope] (bf16 values, W_UK already absorbed), kv [n, kv_lora + rope]
+    dequantized rows; scores = (q . kv) * sm_scale; the values are the first kv_lora
+    dims of the same rows.  Returns the f32 latent output [Hq, kv_lora] before W_UV.
+    Restates the split softmax + merge of glm53/gfx950/kernel.py:5147-5237,5282-5340
+    (a split softmax merged exactly equals one softmax over all keys).
+    """
+    s = (q.double() @ kv.double().T) * sm_scale
+    p = torch.softmax(s, dim=-1)
+    return (p @ kv[:, :kv_lora].double()).float()
+
+
+def mla_output(o_lat: torch.Tensor, w_uv: torch.Tensor) -> torch.Tensor:
+    """o[h, v] = sum_c W_UV[h, v, c] * bf16(o_lat[h, c]), rounded to bf16; flattened to
+    [Hq * v_dim] (glm53/gfx950/kernel.py:5239-5389: the merged o_lat is handed to
+    W_UV as bf16, W_UV's output to W_o as bf16)."""
+    ol = codecs.bf16_round(o_lat)
+    o = torch.einsum("hvc,hc->hv", w_uv.float(), ol)
+    return codecs.bf16_round(o).flatten()
+
+
+def o_proj(o: torch.Tensor, w_o: torch.Tensor, h: torch.Tensor | None) -> torch.Tensor:
+    """a = bf16(h + o . W_o^T) (glm53/gfx950/kernel.py:5391-5469, the 1-GPU reduce path
+    :2069-2074); without a residual, bf16(o . W_o^T)."""
+    y = o.float() @ w_o.float().T
+    if h is not None:
+        y = h.float() + y
+    return codecs.bf16_round(y)
+
+
+# ---------------------------------------------------------------- RMSNorm and router
+def rmsnorm(a: torch.Tensor, gamma: torch.Tensor, eps: float) -> torch.Tensor:
+    """x = bf16(a * rsqrt(mean(a^2) + eps) * gamma) over the last dim, in f32
+    (glm53/check.py:391-393; glm53/gfx950/kernel.py:5471-5562)."""
+    a = a.float()
+    rstd = torch.rsqrt(a.pow(2).mean(-1, keepdim=True) + eps)
+    return codecs.bf16_round(a * rstd * gamma.float())
+
+
+def _topk_by_key(keys: torch.Tensor, k: int) -> torch.Tensor:
+    """Per row, the indices of the k largest keys, equal keys by the lower index, in
+    rank order (glm53/gfx950/kernel.py:1967-1999)."""
+    return torch.sort(keys, dim=-1, descending=True, stable=True).indices[..., :k]
+
+
+def route_softmax(logits: torch.Tensor, k: int):
+    """Top-k of the f32 logits (all bits; ties -> lower expert id), weights = softmax over
+    the k picked logits (qwen38_a95b_mxfp4/gfx950/layer.py:806-849, which is softmax
+    over all experts, top-k, renormalized).  Returns (ids [M, k] int64, weights f32)."""
+    ids = _topk_by_key(codecs.radix_keys(logits.float()), k)
+    picked = torch.gather(logits.float(), -1, ids).double()
+    w = torch.softmax(picked, dim=-1).float()
+    return ids, w
+
+
+def route_sigmoid_bias(logits: torch.Tensor, bias: torch.Tensor, k: int, scale: float):
+    """s = sigmoid(logit); top-k by the f32 bits of s + bias (ties -> lower id);
+    weight = s / sum of the k picked s * scale (glm53/gfx950/kernel.py:1937-1965,
+    5635-5639).  Returns (ids [M, k] int64, weights f32)."""
+    s = torch.sigmoid(logits.float())
+    ids = _topk_by_key(codecs.radix_keys(s + bias.float()), k)
+    picked = torch.gather(s, -1, ids).double()
+    w = (picked / picked.sum(-1, keepdim=True) * scale).float()
+    return ids, w
+
+
+# -------------------------------------------------------------------------- experts
+def swiglu(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
+    """mid = silu(g) * u = g / (1 + exp(-g)) * u, f32 (glm53/gfx950/kernel.py:5719-5724)."""
+    g = g.float()
+    return g / (1.0 + torch.exp(-g)) * u.float()
+
+
+def expert_fp8(x: torch.Tensor, w13: torch.Tensor, w2: torch.Tensor) -> torch.Tensor:
+    """One FP8-weight expert on bf16 rows: g|u = x . W13^T (W13 = [gate; up] dequantized),
+    mid = bf16(silu(g) * u), y = mid . W2^T (f32).  glm53's block-scaled FP8 on bf16
+    activations (glm53/gfx950/kernel.py:28-34 docstring, 1008-1120)."""
+    inter = w13.shape[0] // 2
+    gu = x.float() @ w13.T
+    mid = codecs.bf16_round(swiglu(gu[..., :inter], gu[..., inter:]))
+    return mid @ w2.T
+
+
+def expert_mxfp4(x: torch.Tensor, w13: torch.Tensor, w2: torch.Tensor) -> torch.Tensor:
+    """One MXFP4-weight expert on MXFP8 rows: x and mid are quantized to MXFP8 per 32
+    before each product (glm53 "native_fp4" A8W4: glm53/gfx950/kernel.py:1284-1307,
+    1752-1766, 7032-7060)."""
+    inter = w13.shape[0] // 2
+    xq = codecs.mxfp8_dequant(*codecs.mxfp8_quant(x.float()))
+    gu = xq @ w13.T
+    mid = swiglu(gu[..., :inter], gu[..., inter:])
+    mq = codecs.mxfp8_dequant(*codecs.mxfp8_quant(mid))
+    return mq @ w2.T
+
+
+def moe_block(x, logits_fn, route_fn, experts, shared, residual=None):
+    """y = sum_k w_k * expert_{id_k}(x) + shared(x); out = bf16(residual + y) or bf16(y).
+
+    x [M, H] bf16 values (already normalized); logits_fn(x) -> f32 [M, E]; route_fn ->
+    (ids, weights); experts(e, rows_x) -> f32 [rows, H]; shared(x) -> f32 or None.
+    glm53/gfx950/kernel.py:5662-7152 (up/gate, mid, down + route weighting, residual).
+    Returns (out f32 of bf16 values, ids, weights, logits).
+    """
+    logits = logits_fn(x)
+    ids, w = route_fn(logits)
+    m = x.shape[0]
+    y = torch.zeros(m, x.shape[1], dtype=torch.float64)
+    for r in range(m):
+        for j in range(ids.shape[1]):
+            y[r] += w[r, j].double() * experts(int(ids[r, j]), x[r : r + 1])[0].double()
+    if shared is not None:
+        y += shared(x).double()
+    if residual is not None:
+        y = residual.double() + y
+    return codecs.bf16_round(y.float()), ids, w, logits
+
+
+# ------------------------------------------------------------------ K2 chained layer
+def k2_layer(h, indexer_scores_fn, topk, attention_fn, eps, gamma, moe_fn):
+    """The chained layer of BASELINE configs[4]: index scores -> exact top-k ->
+    sparse MLA + W_UV + W_o + residual h -> RMSNorm(eps) -> MoE + residual.
+    (glm53/gfx950/kernel.py:6-47 stage order; TP reduces omitted.)"""
+    scores = indexer_scores_fn()
+    sel = [radix_lists(scores[r].float(), topk) for r in range(scores.shape[0])]
+    a = attention_fn(sel)
+    x = rmsnorm(a, gamma, eps)
+    out = moe_fn(x, a)
+    return out, a, sel, scores
+
+
+def rel_l2(a: torch.Tensor, b: torch.Tensor) -> float:
+    """||a - b|| / ||b||."""
+    a, b = a.double(), b.double()
+    return float((a - b).norm() / b.norm().clamp_min(1e-30))
+

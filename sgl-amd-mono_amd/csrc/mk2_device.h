@@ -1,0 +1,154 @@
+// Device helpers of the K2 kernels: CDNA4 (gfx950) matrix-core operands, number
+// formats and wavefront reductions.  Every kernel in this library includes it.
+//
+// Operand convention (one 64-lane wavefront, 16x16 MFMA tiles):
+//   A (16 rows x K): lane l owns row l % 16 and the K slice of lane group l / 16.
+//   B (K x 16 cols): lane l owns column l % 16 and the same K slice.
+//   D (16 x 16 f32): lane l holds D[4 * (l / 16) + i][l % 16], i = 0..3.
+// For v_mfma_scale_f32_16x16x128_f8f6f4 an E2M1 operand (low 4 dwords) holds
+// k = 32g .. 32g+31 in group g; an E4M3 operand (8 dwords) holds k = 16g .. 16g+15 in
+// dwords 0-3 and k = 64+16g .. 64+16g+15 in dwords 4-7.  The E8M0 a lane supplies
+// scales the 32-block k = 32g .. 32g+31 of its row (A) or column (B) in both cases
+// (measured with mk2_selftest_mfma).
+// For v_mfma_f32_16x16x32_bf16 it is 8 bf16; a 128-k block is fed as four steps
+// s = 0..3 where lane group g supplies k = 32g + 8s .. +7, so one lane reads 32
+// consecutive k of its row (the dot product is order-free over k as long as A and
+// B use the same map).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef uint16_t bf16_t;  // storage type of bf16 in memory
+
+#define MK2_WAVE 64
+#define MK2_DEV __device__ __forceinline__
+
+namespace mk2 {
+
+// ----------------------------------------------------------------- bf16 / f32
+MK2_DEV float bf16_to_f32(bf16_t v) { return __uint_as_float(((uint32_t)v) << 16); }
+MK2_DEV bf16_t f32_to_bf16(float f) {  // round to nearest even (finite inputs)
+  uint32_t u = __float_as_uint(f);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (bf16_t)(u >> 16);
+}
+MK2_DEV uint32_t pack_bf16x2(float lo, float hi) {
+  return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+}
+// two f32 that are exactly representable in bf16 -> packed pair (truncation is exact)
+MK2_DEV uint32_t pack_bf16x2_exact(float lo, float hi) {
+  return (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
+}
+
+// ----------------------------------------------------------------- E4M3 / E2M1
+// 4 E4M3 bytes of a dword -> 4 f32 (exact)
+MK2_DEV void e4m3x4_to_f32(uint32_t w, float* o) {
+  f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
+  f32x2 b = __builtin_amdgcn_cvt_pk_f32_fp8(w, true);
+  o[0] = a.x; o[1] = a.y; o[2] = b.x; o[3] = b.y;
+}
+// 8 E4M3 bytes (two dwords) -> 8 bf16 (exact widening)
+MK2_DEV bf16x8 e4m3x8_to_bf16(uint32_t w0, uint32_t w1) {
+  float f[8];
+  e4m3x4_to_f32(w0, f);
+  e4m3x4_to_f32(w1, f + 4);
+  i32x4 r;
+  r[0] = (int)pack_bf16x2_exact(f[0], f[1]);
+  r[1] = (int)pack_bf16x2_exact(f[2], f[3]);
+  r[2] = (int)pack_bf16x2_exact(f[4], f[5]);
+  r[3] = (int)pack_bf16x2_exact(f[6], f[7]);
+  return __builtin_bit_cast(bf16x8, r);
+}
+// 8 E2M1 codes (one dword, element 0 in the low nibble) times 2^(code - 127) -> 8 bf16.
+// Exact: an E2M1 value times a power of two has at most 2 significant bits.
+MK2_DEV bf16x8 e2m1x8_to_bf16(uint32_t w, float scale) {
+  i32x4 r;
+  r[0] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 0));
+  r[1] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 1));
+  r[2] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 2));
+  r[3] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 3));
+  return __builtin_bit_cast(bf16x8, r);
+}
+MK2_DEV float e8m0_to_f32(uint32_t code) { return __uint_as_float((code & 0xFFu) << 23); }
+
+// f32 -> E4M3 byte, clamped to +-448, round to nearest even
+MK2_DEV uint32_t f32_to_e4m3(float v) {
+  v = fminf(fmaxf(v, -448.0f), 448.0f);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v, 0.0f, 0, false) & 0xFFu;
+}
+MK2_DEV uint32_t f32x4_to_e4m3x4(float a, float b, float c, float d) {
+  a = fminf(fmaxf(a, -448.0f), 448.0f);
+  b = fminf(fmaxf(b, -448.0f), 448.0f);
+  c = fminf(fmaxf(c, -448.0f), 448.0f);
+  d = fminf(fmaxf(d, -448.0f), 448.0f);
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+  return (uint32_t)w;
+}
+
+// E8M0 code of an MXFP8 activation block: ceil-pow2 exponent of amax * f32(1/448),
+// clamped to [1, 254] (the rule of the reference's quant_mxfp8).
+MK2_DEV uint32_t mxfp8_scale_code(float amax) {
+  uint32_t bits = __float_as_uint(amax * (1.0f / 448.0f));
+  int e = (int)((bits >> 23) & 0xFFu) + ((bits & 0x7FFFFFu) != 0u ? 1 : 0);
+  e = e < 1 ? 1 : (e > 254 ? 254 : e);
+  return (uint32_t)e;
+}
+// exact 1 / 2^(code - 127) for code in [1, 254]
+MK2_DEV float e8m0_inverse(uint32_t code) {
+  int e = 254 - (int)code;  // biased exponent of the reciprocal
+  if (e >= 1) return __uint_as_float((uint32_t)e << 23);
+  return __uint_as_float(0x00400000u);  // code 254: 2^-127 (subnormal)
+}
+
+// ----------------------------------------------------------------- MFMA
+MK2_DEV f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+// A = 32 E2M1 (low 4 dwords of a), B = 32 E4M3; scale bytes selected by SA / SB
+template <int SA, int SB>
+MK2_DEV f32x4 mfma_fp4_fp8(i32x8 a, i32x8 b, f32x4 c, int sa, int sb) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 4, 0, SA, sa, SB, sb);
+}
+
+// ----------------------------------------------------------------- reductions
+MK2_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+MK2_DEV float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+// reduce over the 16 lanes of a lane row (lanes with equal l / 16)
+MK2_DEV float row16_max(float v) {
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+MK2_DEV float row16_sum(float v) {
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// order-preserving u32 of f32 bits: larger keys rank first
+MK2_DEV uint32_t radix_key(float f) {
+  uint32_t b = __float_as_uint(f);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+MK2_DEV float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+
+template <typename T>
+MK2_DEV T ld_nt(const T* p) { return __builtin_nontemporal_load(p); }
+
+}  // namespace mk2

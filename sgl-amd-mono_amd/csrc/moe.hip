@@ -1,0 +1,169 @@
+// Standalone MoE block launch (BASELINE configs[0] and [1]): five kernels on one
+// stream -- prep (RMSNorm + MXFP8 quant), router GEMV, route (top-k + distinct
+// experts), up/gate + SwiGLU, down + combine.
+#include "mk2_host.h"
+#include "moe_stages.h"
+
+namespace mk2 {
+
+constexpr int MOE_NT = 512;
+constexpr int ROUTE_NT = 256;
+
+__global__ __launch_bounds__(256) void k_moe_prep(MoeDev p) {
+  __shared__ float lds[8];
+  moe_prep<256>(p, blockIdx.x, lds);
+}
+
+template <int NCG>
+__global__ __launch_bounds__(256) void k_moe_router(MoeDev p) {
+  __shared__ float red[4 * NCG * 64 * 4];
+  moe_router<256, NCG>(p, blockIdx.x, blockIdx.y, red);
+}
+
+__global__ __launch_bounds__(ROUTE_NT) void k_moe_route(MoeDev p) {
+  extern __shared__ float dyn[];
+  float* logits = dyn;
+  int* slot = (int*)(dyn + p.M * p.E);
+  moe_route<ROUTE_NT>(p, logits, slot);
+}
+
+template <int NCG>
+__global__ __launch_bounds__(MOE_NT) void k_moe_upgate(MoeDev p) {
+  __shared__ float red[(MOE_NT / 64) * 4 * NCG * 64 * 4];
+  __shared__ float midf[32 * 33];
+  moe_upgate<MOE_NT, NCG>(p, blockIdx.x, red, midf);
+}
+
+template <int NCG>
+__global__ __launch_bounds__(MOE_NT) void k_moe_down(MoeDev p) {
+  __shared__ float red[(MOE_NT / 64) * NCG * 64 * 4];
+  moe_down<MOE_NT, NCG>(p, blockIdx.x, red);
+}
+
+// ----------------------------------------------------------------- host side
+int moe_check_shape(const mk2_moe_shape* s) {
+  MK2_REQUIRE(s != nullptr, "moe: shape is NULL");
+  MK2_REQUIRE(s->rows >= 1 && s->rows <= 32, "moe: rows must be in [1, 32], got %d", s->rows);
+  MK2_REQUIRE(s->hidden >= 512 && s->hidden % 512 == 0, "moe: hidden must be a positive multiple of 512, got %d", s->hidden);
+  MK2_REQUIRE(s->n_experts >= 64 && s->n_experts <= 256 && s->n_experts % 64 == 0,
+              "moe: n_experts must be 64, 128, 192 or 256, got %d", s->n_experts);
+  MK2_REQUIRE(s->top_k >= 1 && s->top_k <= 8, "moe: top_k must be in [1, 8], got %d", s->top_k);
+  MK2_REQUIRE(s->router == MK2_ROUTER_SOFTMAX || s->router == MK2_ROUTER_SIGMOID_BIAS, "moe: unknown router %d", s->router);
+  MK2_REQUIRE(s->expert_fmt == MK2_FMT_FP8 || s->expert_fmt == MK2_FMT_MXFP4, "moe: unknown expert format %d", s->expert_fmt);
+  const int iq = s->expert_fmt == MK2_FMT_FP8 ? 128 : 128;
+  MK2_REQUIRE(s->inter >= iq && s->inter % iq == 0 && s->inter <= 4096, "moe: inter must be a multiple of 128 in [128, 4096], got %d", s->inter);
+  MK2_REQUIRE(s->n_shared == 0 || s->n_shared == 1, "moe: n_shared must be 0 or 1");
+  if (s->n_shared)
+    MK2_REQUIRE(s->shared_inter >= 128 && s->shared_inter % 128 == 0 && s->shared_inter <= 4096,
+                "moe: shared_inter must be a multiple of 128 in [128, 4096], got %d", s->shared_inter);
+  MK2_REQUIRE(s->norm == 0 || s->norm == 1, "moe: norm must be 0 or 1");
+  MK2_REQUIRE(s->residual == 0 || s->residual == 1, "moe: residual must be 0 or 1");
+  return MK2_OK;
+}
+
+static int router_chunks(int hidden) {
+  const int kb = hidden / 128;  // multiple of 4
+  return kb / 4;                // 4 k-blocks (one a wave) a task
+}
+
+// carve the MoE scratch; with base == nullptr only sizes are computed
+size_t moe_carve(const mk2_moe_shape* s, void* base, MoeDev* d) {
+  Carver c(base);
+  const int M = s->rows, H = s->hidden, E = s->n_experts, I = s->inter;
+  const int KC = router_chunks(H);
+  const int Dmax = E < M * s->top_k ? E : M * s->top_k;
+  MoeDev t{};
+  t.KC = KC;
+  t.Dmax = Dmax;
+  t.xn = c.take<bf16_t>((size_t)M * H);
+  t.xq = c.take<uint8_t>((size_t)M * H);
+  t.xs = c.take<uint8_t>((size_t)M * H / 32);
+  t.logit_part = c.take<float>((size_t)KC * M * E);
+  t.logits = c.take<float>((size_t)M * E);
+  t.topk_ids = c.take<int>((size_t)M * s->top_k);
+  t.topk_w = c.take<float>((size_t)M * s->top_k);
+  t.act = c.take<int>((size_t)1 + E);
+  t.rw = c.take<float>((size_t)Dmax * 32);
+  if (s->expert_fmt == MK2_FMT_MXFP4) {
+    t.mid_q = c.take<uint8_t>((size_t)Dmax * M * I);
+    t.mid_s = c.take<uint8_t>((size_t)Dmax * M * I / 32);
+  } else {
+    t.mid_b = c.take<bf16_t>((size_t)Dmax * M * I);
+  }
+  t.mid_sh = c.take<bf16_t>((size_t)M * (s->n_shared ? s->shared_inter : 0) + 1);
+  if (d) {
+    d->KC = t.KC; d->Dmax = t.Dmax; d->xn = t.xn; d->xq = t.xq; d->xs = t.xs;
+    d->logit_part = t.logit_part; d->logits = t.logits; d->topk_ids = t.topk_ids;
+    d->topk_w = t.topk_w; d->act = t.act; d->rw = t.rw; d->mid_q = t.mid_q;
+    d->mid_s = t.mid_s; d->mid_b = t.mid_b; d->mid_sh = t.mid_sh;
+  }
+  return c.bytes();
+}
+
+int moe_fill(const mk2_moe_args* a, MoeDev* d) {
+  const mk2_moe_shape* s = &a->shape;
+  int rc = moe_check_shape(s);
+  if (rc) return rc;
+  const mk2_moe_weights* w = &a->w;
+  MK2_REQUIRE(w->w_router && w->w13 && w->s13 && w->w2 && w->s2, "moe: a routed or router weight pointer is NULL");
+  MK2_REQUIRE(s->router != MK2_ROUTER_SIGMOID_BIAS || w->router_bias, "moe: the sigmoid_bias router needs router_bias");
+  MK2_REQUIRE(!s->n_shared || (w->ws13 && w->ss13 && w->ws2 && w->ss2), "moe: a shared-expert pointer is NULL");
+  MK2_REQUIRE(!s->norm || w->gamma, "moe: norm=1 needs gamma");
+  *d = MoeDev{};
+  d->M = s->rows; d->H = s->hidden; d->E = s->n_experts; d->topk = s->top_k; d->I = s->inter;
+  d->router = s->router; d->fmt = s->expert_fmt; d->n_shared = s->n_shared;
+  d->SI = s->n_shared ? s->shared_inter : 0; d->norm = s->norm; d->residual = s->residual;
+  d->route_scale = s->route_scale; d->eps = s->eps;
+  d->gamma = (const bf16_t*)w->gamma; d->w_router = (const uint8_t*)w->w_router;
+  d->bias = w->router_bias; d->w13 = (const uint8_t*)w->w13; d->s13 = (const uint8_t*)w->s13;
+  d->w2 = (const uint8_t*)w->w2; d->s2 = (const uint8_t*)w->s2;
+  d->ws13 = (const uint8_t*)w->ws13; d->ss13 = w->ss13; d->ws2 = (const uint8_t*)w->ws2; d->ss2 = w->ss2;
+  d->x = (const bf16_t*)a->x; d->out = (bf16_t*)a->out;
+  return MK2_OK;
+}
+
+int moe_enqueue(const MoeDev& d, hipStream_t st) {
+  const int ncg = d.M > 16 ? 2 : 1;
+  k_moe_prep<<<d.M, 256, 0, st>>>(d);
+  if (ncg == 1) k_moe_router<1><<<dim3(d.E / 16, d.KC), 256, 0, st>>>(d);
+  else k_moe_router<2><<<dim3(d.E / 16, d.KC), 256, 0, st>>>(d);
+  const size_t route_lds = (size_t)d.M * d.E * 4 + (size_t)(d.E + 8) * 4;
+  k_moe_route<<<1, ROUTE_NT, route_lds, st>>>(d);
+  const int up_tasks = d.Dmax * (d.I / 32) + d.n_shared * (d.SI / 32);
+  if (ncg == 1) k_moe_upgate<1><<<up_tasks, MOE_NT, 0, st>>>(d);
+  else k_moe_upgate<2><<<up_tasks, MOE_NT, 0, st>>>(d);
+  if (ncg == 1) k_moe_down<1><<<d.H / 16, MOE_NT, 0, st>>>(d);
+  else k_moe_down<2><<<d.H / 16, MOE_NT, 0, st>>>(d);
+  return check_launch("moe");
+}
+
+}  // namespace mk2
+
+using namespace mk2;
+
+extern "C" int mk2_moe_workspace_bytes(const mk2_moe_shape* shape, size_t* bytes) {
+  clear_error();
+  int rc = moe_check_shape(shape);
+  if (rc) return rc;
+  MK2_REQUIRE(bytes != nullptr, "moe: bytes is NULL");
+  *bytes = moe_carve(shape, nullptr, nullptr);
+  return MK2_OK;
+}
+
+extern "C" int mk2_moe_launch(const mk2_moe_args* a, mk2_stream_t stream) {
+  clear_error();
+  MK2_REQUIRE(a != nullptr, "moe: args is NULL");
+  MoeDev d;
+  int rc = moe_fill(a, &d);
+  if (rc) return rc;
+  MK2_REQUIRE(a->x && a->out && a->workspace, "moe: x, out and workspace must be set");
+  MK2_REQUIRE(a->x != a->out, "moe: out must not alias x");
+  const size_t need = moe_carve(&a->shape, nullptr, nullptr);
+  if (a->workspace_bytes < need)
+    return set_error(MK2_ENOSPACE, "moe: workspace has %zu bytes, needs %zu", a->workspace_bytes, need);
+  moe_carve(&a->shape, a->workspace, &d);
+  if (a->logits) d.logits = a->logits;
+  if (a->topk_ids) d.topk_ids = a->topk_ids;
+  if (a->topk_weights) d.topk_w = a->topk_weights;
+  return moe_enqueue(d, (hipStream_t)stream);
+}

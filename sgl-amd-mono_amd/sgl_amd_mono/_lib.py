@@ -1,0 +1,158 @@
+"""ctypes binding of ``libmk2.so`` (the C ABI in ``include/mk2.h``).
+
+The structures below mirror the C structs field for field.  torch is imported
+first on purpose: its ROCm wheel ships the HIP runtime under the same SONAME
+(``libamdhip64.so.7``) that libmk2 links against, so loading libmk2 after torch
+binds both to one runtime -- one device context, one set of streams.  The loader
+checks that only one HIP runtime is mapped and refuses otherwise.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_char_p, c_float, c_int, c_size_t, c_void_p
+from pathlib import Path
+
+import torch  # noqa: F401  (must precede the CDLL load, see the module docstring)
+
+LIB_PATH = Path(__file__).resolve().parent / "libmk2.so"
+
+MK2_OK, MK2_EINVAL, MK2_ELAUNCH, MK2_ENOSPACE = 0, 1, 2, 3
+
+
+class Mk2Error(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"mk2 error {code}: {msg}")
+        self.code = code
+
+
+class MoeShape(ctypes.Structure):
+    _fields_ = [
+        ("rows", c_int), ("hidden", c_int), ("n_experts", c_int), ("top_k", c_int),
+        ("inter", c_int), ("router", c_int), ("expert_fmt", c_int), ("n_shared", c_int),
+        ("shared_inter", c_int), ("norm", c_int), ("residual", c_int),
+        ("route_scale", c_float), ("eps", c_float),
+    ]
+
+
+class MoeWeights(ctypes.Structure):
+    _fields_ = [
+        ("gamma", c_void_p), ("w_router", c_void_p), ("router_bias", c_void_p),
+        ("w13", c_void_p), ("s13", c_void_p), ("w2", c_void_p), ("s2", c_void_p),
+        ("ws13", c_void_p), ("ss13", c_void_p), ("ws2", c_void_p), ("ss2", c_void_p),
+    ]
+
+
+class MoeArgs(ctypes.Structure):
+    _fields_ = [
+        ("shape", MoeShape), ("w", MoeWeights), ("x", c_void_p), ("out", c_void_p),
+        ("workspace", c_void_p), ("workspace_bytes", c_size_t),
+        ("logits", c_void_p), ("topk_ids", c_void_p), ("topk_weights", c_void_p),
+    ]
+
+
+class IndexerShape(ctypes.Structure):
+    _fields_ = [
+        ("rows", c_int), ("heads", c_int), ("dim", c_int), ("topk", c_int),
+        ("max_ctx", c_int), ("table_stride", c_int),
+    ]
+
+
+class IndexerArgs(ctypes.Structure):
+    _fields_ = [
+        ("shape", IndexerShape), ("q", c_void_p), ("w", c_void_p), ("cache", c_void_p),
+        ("page_table", c_void_p), ("req_ids", c_void_p), ("ctx_len", c_void_p),
+        ("scores", c_void_p), ("topk", c_void_p),
+        ("workspace", c_void_p), ("workspace_bytes", c_size_t),
+    ]
+
+
+class MlaShape(ctypes.Structure):
+    _fields_ = [
+        ("rows", c_int), ("heads", c_int), ("kv_lora", c_int), ("rope", c_int),
+        ("v_dim", c_int), ("hidden", c_int), ("topk", c_int), ("table_stride", c_int),
+        ("sm_scale", c_float),
+    ]
+
+
+class MlaArgs(ctypes.Structure):
+    _fields_ = [
+        ("shape", MlaShape), ("q", c_void_p), ("kv", c_void_p), ("kv_scale", c_void_p),
+        ("page_table", c_void_p), ("req_ids", c_void_p), ("sel", c_void_p),
+        ("w_uv", c_void_p), ("w_o", c_void_p), ("h", c_void_p), ("out", c_void_p),
+        ("workspace", c_void_p), ("workspace_bytes", c_size_t), ("o_latent", c_void_p),
+    ]
+
+
+class LayerArgs(ctypes.Structure):
+    _fields_ = [
+        ("indexer", IndexerArgs), ("mla", MlaArgs), ("moe", MoeArgs),
+        ("attn_out", c_void_p), ("out", c_void_p),
+        ("workspace", c_void_p), ("workspace_bytes", c_size_t),
+    ]
+
+
+# entry point -> (argtypes); every one returns int
+SIGNATURES = {
+    "mk2_moe_workspace_bytes": [POINTER(MoeShape), POINTER(c_size_t)],
+    "mk2_moe_launch": [POINTER(MoeArgs), c_void_p],
+    "mk2_indexer_workspace_bytes": [POINTER(IndexerShape), POINTER(c_size_t)],
+    "mk2_indexer_topk_launch": [POINTER(IndexerArgs), c_void_p],
+    "mk2_mla_workspace_bytes": [POINTER(MlaShape), POINTER(c_size_t)],
+    "mk2_sparse_mla_launch": [POINTER(MlaArgs), c_void_p],
+    "mk2_layer_workspace_bytes": [POINTER(LayerArgs), POINTER(c_size_t)],
+    "mk2_layer_launch": [POINTER(LayerArgs), c_void_p],
+    "mk2_abi_version": [],
+    "mk2_selftest_mfma": [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],
+}
+
+_LIB = None
+
+
+def _hip_runtimes_mapped() -> set:
+    try:
+        with open("/proc/self/maps") as f:
+            return {ln.split()[-1] for ln in f if "libamdhip64" in ln}
+    except OSError:
+        return set()
+
+
+def lib(required_symbols=None):
+    """Load libmk2.so once; raise if it is missing (there is no fallback path)."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"{LIB_PATH} is not built: run `python __graft_entry__.py build` "
+            "(or sgl_amd_mono._build.build()) first; the K2 ops have no CPU fallback"
+        )
+    handle = ctypes.CDLL(str(LIB_PATH), mode=os.RTLD_NOW | os.RTLD_GLOBAL)
+    for name, argtypes in SIGNATURES.items():
+        if not hasattr(handle, name):
+            continue  # tests/test_abi.py requires every symbol; callers fail at use
+        fn = getattr(handle, name)
+        fn.argtypes = argtypes
+        fn.restype = c_int
+    handle.mk2_last_error.argtypes = []
+    handle.mk2_last_error.restype = c_char_p
+    runtimes = _hip_runtimes_mapped()
+    if len(runtimes) > 1:
+        raise RuntimeError(f"two HIP runtimes are mapped ({sorted(runtimes)}); import torch first")
+    _LIB = handle
+    return handle
+
+
+def check(rc: int) -> None:
+    if rc != MK2_OK:
+        raise Mk2Error(rc, lib().mk2_last_error().decode())
+
+
+def ptr(t) -> int | None:
+    """Device address of a tensor (None for None)."""
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(device=None) -> int:
+    return torch.cuda.current_stream(device).cuda_stream

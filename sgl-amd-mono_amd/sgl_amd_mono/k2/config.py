@@ -1,0 +1,144 @@
+"""Geometry of the K2 decode layer (one GPU's share) and the five benchmark shapes.
+
+The reference fixes one geometry per model in ``glm53/gfx950/config.py:184-197``
+(hidden 6144, kv_lora 512, rope 64, 256 experts, top-8, inter 256 a rank, route
+scale 2.5).  Here each piece of the layer is a frozen dataclass so the same
+kernels serve the FP8 MoE block, the MXFP4 MoE shard,
+sparse MLA, the FP4 indexer and the chained layer
+(configs[4]).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field, replace
+
+PAGE = 64  # tokens a KV / index page (glm53/gfx950/config.py page size 64)
+
+ROUTER_SOFTMAX = 0  # softmax over the picked logits (qwen38 style)
+ROUTER_SIGMOID_BIAS = 1  # sigmoid, picked by sigmoid + bias, * route_scale (glm53)
+FMT_FP8 = 0  # E4M3 weights, f32 128 x 128 block scales, bf16 activations
+FMT_MXFP4 = 1  # E2M1 weights, E8M0 per 32, MXFP8 activations
+
+MAX_ROWS = 32  # decode rows a launch serves (verify: 8 requests x 4 draft tokens)
+
+
+@dataclass(frozen=True)
+class MoEConfig:
+    hidden: int
+    n_experts: int
+    top_k: int
+    inter: int
+    router: int
+    route_scale: float
+    expert_fmt: int
+    n_shared: int
+    shared_inter: int
+
+    def validate(self, rows: int) -> None:
+        if not 1 <= rows <= MAX_ROWS:
+            raise ValueError(f"rows must be in [1, {MAX_ROWS}], got {rows}")
+        if self.hidden % 512:
+            raise ValueError(f"hidden must be a multiple of 512, got {self.hidden}")
+        if self.inter % 32 or self.shared_inter % 32:
+            raise ValueError("expert intermediate sizes must be multiples of 32")
+        if self.expert_fmt == FMT_FP8 and self.inter % 128:
+            raise ValueError("FP8 experts need an intermediate size that is a multiple of 128")
+        if self.n_shared and self.shared_inter % 128:
+            raise ValueError("the FP8 shared expert needs an intermediate multiple of 128")
+        if self.n_experts % 16 or not 16 <= self.n_experts <= 256:
+            raise ValueError(f"n_experts must be a multiple of 16 in [16, 256], got {self.n_experts}")
+        if not 1 <= self.top_k <= 8:
+            raise ValueError(f"top_k must be in [1, 8], got {self.top_k}")
+        if self.n_shared not in (0, 1):
+            raise ValueError("at most one shared expert")
+
+
+@dataclass(frozen=True)
+class MlaConfig:
+    heads: int = 16
+    kv_lora: int = 512
+    rope: int = 64
+    v_dim: int = 128
+    hidden: int = 6144
+    topk: int = 2048
+    context: int = 32768
+
+    @property
+    def qk_dim(self) -> int:
+        return self.kv_lora + self.rope
+
+    @property
+    def sm_scale(self) -> float:
+        return 1.0 / math.sqrt(self.qk_dim)
+
+    def validate(self, rows: int) -> None:
+        if (self.heads, self.kv_lora, self.rope) != (16, 512, 64):
+            raise ValueError("the MLA kernels serve 16 heads of 512 + 64 latent dims")
+        if self.v_dim % 16 or self.hidden % 16:
+            raise ValueError("v_dim and hidden must be multiples of 16")
+        if (self.heads * self.v_dim) % 128:
+            raise ValueError("heads * v_dim must be a multiple of 128")
+        if self.topk % 64 or self.topk <= 0:
+            raise ValueError("topk must be a positive multiple of 64")
+        if not 1 <= rows <= MAX_ROWS:
+            raise ValueError(f"rows must be in [1, {MAX_ROWS}]")
+
+
+@dataclass(frozen=True)
+class IndexerConfig:
+    heads: int = 64
+    dim: int = 128
+    topk: int = 2048
+    context: int = 65536
+
+    def validate(self, rows: int) -> None:
+        if self.dim != 128:
+            raise ValueError("index keys are 128 dims")
+        if self.heads % 16 or not 16 <= self.heads <= 64:
+            raise ValueError("index heads must be a multiple of 16 in [16, 64]")
+        if self.context > 65536 or self.context % PAGE:
+            raise ValueError("context must be a multiple of 64 and at most 65536")
+        if self.topk % 64 or not 64 <= self.topk <= 4096:
+            raise ValueError("topk must be a multiple of 64 in [64, 4096]")
+        if not 1 <= rows <= MAX_ROWS:
+            raise ValueError(f"rows must be in [1, {MAX_ROWS}]")
+
+
+@dataclass(frozen=True)
+class K2Config:
+    mla: MlaConfig = field(default_factory=MlaConfig)
+    indexer: IndexerConfig = field(default_factory=IndexerConfig)
+    moe: MoEConfig = None  # type: ignore[assignment]
+    eps: float = 1e-6
+
+    def validate(self, rows: int) -> None:
+        self.mla.validate(rows)
+        self.indexer.validate(rows)
+        self.moe.validate(rows)
+        if self.mla.hidden != self.moe.hidden:
+            raise ValueError("attention and MoE hidden sizes differ")
+        if self.mla.topk != self.indexer.topk:
+            raise ValueError("the attention attends the indexer's top-k")
+        if self.mla.context != self.indexer.context:
+            raise ValueError("the indexer and the attention share one context")
+
+
+# FP8 MoE block, CPU-runnable
+C1_MOE = MoEConfig(
+    hidden=2048, n_experts=64, top_k=8, inter=768, router=ROUTER_SOFTMAX,
+    route_scale=1.0, expert_fmt=FMT_FP8, n_shared=1, shared_inter=768,
+)
+# MXFP4 MoE decode shard (one GPU's share: inter 2048 / 8)
+C2_MOE = MoEConfig(
+    hidden=6144, n_experts=256, top_k=8, inter=256, router=ROUTER_SIGMOID_BIAS,
+    route_scale=2.5, expert_fmt=FMT_MXFP4, n_shared=1, shared_inter=256,
+)
+# sparse-MLA decode attention + o_proj
+C3_MLA = MlaConfig(context=32768)
+# FP4 indexer + exact top-2048
+C4_INDEXER = IndexerConfig(context=65536)
+# the chained layer (3 + 4 + 2), one context for indexer and attention
+C5_LAYER = K2Config(
+    mla=replace(C3_MLA, context=65536), indexer=C4_INDEXER, moe=C2_MOE, eps=1e-6
+)

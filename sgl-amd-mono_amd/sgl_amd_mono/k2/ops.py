@@ -1,0 +1,69 @@
+"""Host wrappers of the C ABI: argument structs, workspace, launch on the current
+stream.  Shapes and dtypes are validated here before anything is enqueued, as the
+reference's runner does (glm53/gfx950/runner.py:312-318,388-421); the library
+validates again on its side of the boundary.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from .. import _lib
+from . import config as C
+
+
+def _need(t, name, dtype=None, shape=None):
+    if t is None:
+        raise ValueError(f"{name} is required")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if dtype is not None and t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
+    return t
+
+
+def _p(t):
+    return None if t is None else t.data_ptr()
+
+
+class MoEOp:
+    """The MoE block of one layer (router -> top-k -> routed + shared experts)."""
+
+    def __init__(self, cfg: C.MoEConfig, w, rows: int, *, norm: bool = False,
+                 residual: bool = False, eps: float = 1e-6, device=None):
+        cfg.validate(rows)
+        self.cfg, self.rows, self.w = cfg, rows, w
+        self.device = torch.device(device or w.w13_p.device)
+        self.shape = _lib.MoeShape(
+            rows, cfg.hidden, cfg.n_experts, cfg.top_k, cfg.inter, cfg.router,
+            cfg.expert_fmt, cfg.n_shared, cfg.shared_inter, int(norm), int(residual),
+            cfg.route_scale, eps,
+        )
+        if norm:
+            _need(w.gamma, "gamma", torch.bfloat16, (cfg.hidden,))
+        self.weights = _lib.MoeWeights(
+            _p(w.gamma), _p(w.w_router_p), _p(w.bias), _p(w.w13_p), _p(w.s13_p),
+            _p(w.w2_p), _p(w.s2_p), _p(w.ws13_p), _p(w.ws13s), _p(w.ws2_p), _p(w.ws2s),
+        )
+        nbytes = ctypes.c_size_t()
+        _lib.check(_lib.lib().mk2_moe_workspace_bytes(ctypes.byref(self.shape), ctypes.byref(nbytes)))
+        self.workspace = torch.empty(nbytes.value, dtype=torch.uint8, device=self.device)
+
+    def __call__(self, x, out=None, *, logits=None, topk_ids=None, topk_weights=None):
+        H = self.cfg.hidden
+        _need(x, "x", torch.bfloat16, (self.rows, H))
+        if out is None:
+            out = torch.empty_like(x)
+        _need(out, "out", torch.bfloat16, (self.rows, H))
+        args = _lib.MoeArgs(
+            self.shape, self.weights, _p(x), _p(out), _p(self.workspace),
+            self.workspace.numel(), _p(logits), _p(topk_ids), _p(topk_weights),
+        )
+        _lib.check(_lib.lib().mk2_moe_launch(ctypes.byref(args), _lib.stream_handle(self.device)))
+        return out

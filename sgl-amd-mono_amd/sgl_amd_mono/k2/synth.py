@@ -1,0 +1,137 @@
+"""Seeded synthetic layers in the kernels' formats (tests and the benchmark).
+
+There are no checkpoints offline, so every benchmark and parity case runs on
+random-init weights of the right architecture: weights ~ N(0, 0.02) before
+quantization, activations ~ N(0, 1), shuffled page tables whose page 0 is never
+used, and selected positions drawn uniformly without replacement (the input
+conventions of test/kernels/glm53/check_layer.py:69-101,248-261).
+
+Each ``make_*`` returns a plain namespace holding the canonical (row-major)
+quantized tensors -- what an oracle dequantizes -- and the packed tensors the
+kernels stream.  Generation runs on ``device`` with a torch.Generator seeded there.
+"""
+
+from __future__ import annotations
+
+from types import SimpleNamespace
+
+import torch
+
+from . import config as C
+from .packing import pack_e8m0, pack_tiles
+from .quant import quant_fp8_block, quant_fp8_rows, quant_mxfp4
+
+WEIGHT_STD = 0.02
+
+
+def _gen(seed: int, device) -> torch.Generator:
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    return g
+
+
+def _randn(g, *shape, device, std=1.0):
+    return torch.randn(*shape, generator=g, device=device) * std
+
+
+def pack_bf16(w: torch.Tensor) -> torch.Tensor:
+    """bf16 [..., N, K] -> tiles of 64 B a lane."""
+    return pack_tiles(w.contiguous().view(torch.uint8), 64)
+
+
+def make_moe(cfg: C.MoEConfig, rows: int, seed: int, device, norm: bool = False):
+    """Router, routed experts (FP8 or MXFP4), one FP8 shared expert, input rows."""
+    g = _gen(seed, device)
+    H, E, I, SI = cfg.hidden, cfg.n_experts, cfg.inter, cfg.shared_inter
+    ns = SimpleNamespace(cfg=cfg, rows=rows)
+    ns.x = _randn(g, rows, H, device=device).to(torch.bfloat16)
+    ns.gamma = (1.0 + _randn(g, H, device=device, std=0.1)).to(torch.bfloat16) if norm else None
+    ns.w_router = _randn(g, E, H, device=device, std=WEIGHT_STD).to(torch.bfloat16)
+    ns.bias = (
+        _randn(g, E, device=device, std=0.05).float()
+        if cfg.router == C.ROUTER_SIGMOID_BIAS
+        else None
+    )
+    ns.w_router_p = pack_bf16(ns.w_router)
+    if cfg.expert_fmt == C.FMT_MXFP4:
+        w13q = torch.empty(E, 2 * I, H // 2, dtype=torch.uint8, device=device)
+        w13s = torch.empty(E, 2 * I, H // 32, dtype=torch.uint8, device=device)
+        w2q = torch.empty(E, H, I // 2, dtype=torch.uint8, device=device)
+        w2s = torch.empty(E, H, I // 32, dtype=torch.uint8, device=device)
+        for e in range(E):
+            w13q[e], w13s[e] = quant_mxfp4(_randn(g, 2 * I, H, device=device, std=WEIGHT_STD))
+            w2q[e], w2s[e] = quant_mxfp4(_randn(g, H, I, device=device, std=WEIGHT_STD))
+        ns.w13_p, ns.s13_p = pack_tiles(w13q, 16), pack_e8m0(w13s)
+        ns.w2_p, ns.s2_p = pack_tiles(w2q, 16), pack_e8m0(w2s)
+    else:
+        w13q = torch.empty(E, 2 * I, H, dtype=torch.uint8, device=device)
+        w13s = torch.empty(E, 2 * I // 128, H // 128, dtype=torch.float32, device=device)
+        w2q = torch.empty(E, H, I, dtype=torch.uint8, device=device)
+        w2s = torch.empty(E, H // 128, I // 128, dtype=torch.float32, device=device)
+        for e in range(E):
+            w13q[e], w13s[e] = quant_fp8_block(_randn(g, 2 * I, H, device=device, std=WEIGHT_STD))
+            w2q[e], w2s[e] = quant_fp8_block(_randn(g, H, I, device=device, std=WEIGHT_STD))
+        ns.w13_p, ns.s13_p = pack_tiles(w13q, 32), w13s
+        ns.w2_p, ns.s2_p = pack_tiles(w2q, 32), w2s
+    ns.w13q, ns.w13s, ns.w2q, ns.w2s = w13q, w13s, w2q, w2s
+    if cfg.n_shared:
+        ns.ws13q, ns.ws13s = quant_fp8_block(_randn(g, 2 * SI, H, device=device, std=WEIGHT_STD))
+        ns.ws2q, ns.ws2s = quant_fp8_block(_randn(g, H, SI, device=device, std=WEIGHT_STD))
+        ns.ws13_p, ns.ws2_p = pack_tiles(ns.ws13q, 32), pack_tiles(ns.ws2q, 32)
+    else:
+        ns.ws13q = ns.ws13s = ns.ws2q = ns.ws2s = ns.ws13_p = ns.ws2_p = None
+    return ns
+
+
+def _page_table(g, requests: int, pages_per_req: int, device) -> torch.Tensor:
+    """Shuffled physical pages 1 .. requests * pages_per_req (page 0 never used)."""
+    perm = torch.randperm(requests * pages_per_req, generator=g, device=device) + 1
+    return perm.view(requests, pages_per_req).to(torch.int32).contiguous()
+
+
+def make_indexer(cfg: C.IndexerConfig, rows: int, seed: int, device, ctx_len=None):
+    """FP4 index-key pages (E2M1 codes + E8M0 per 32 dims), bf16 queries and head
+    weights ~ N(0, 1), one request a row."""
+    g = _gen(seed, device)
+    ctx = cfg.context
+    ppr = ctx // C.PAGE
+    ns = SimpleNamespace(cfg=cfg, rows=rows)
+    ns.q = _randn(g, rows, cfg.heads, cfg.dim, device=device).to(torch.bfloat16)
+    ns.w = _randn(g, rows, cfg.heads, device=device).to(torch.bfloat16)
+    ns.page_table = _page_table(g, rows, ppr, device)
+    n_pages = rows * ppr + 1
+    keys = _randn(g, n_pages, C.PAGE, cfg.dim, device=device)
+    codes, scales = quant_mxfp4(keys)  # [P, 64, 64], [P, 64, 4]
+    ns.cache = torch.cat([codes.view(n_pages, -1), scales.view(n_pages, -1)], dim=1).contiguous()
+    ns.req_ids = torch.arange(rows, dtype=torch.int32, device=device)
+    if ctx_len is None:
+        ctx_len = [ctx] * rows
+    ns.ctx_len = torch.tensor(ctx_len, dtype=torch.int32, device=device)
+    return ns
+
+
+def make_mla(cfg: C.MlaConfig, rows: int, seed: int, device, residual: bool = True):
+    """FP8 latent-KV pages with per-token f32 scales, absorbed bf16 queries,
+    selected positions, W_UV and W_o (bf16, ~ N(0, 0.02)), residual rows."""
+    g = _gen(seed, device)
+    ctx = cfg.context
+    ppr = ctx // C.PAGE
+    ns = SimpleNamespace(cfg=cfg, rows=rows)
+    ns.q = _randn(g, rows, cfg.heads, cfg.qk_dim, device=device).to(torch.bfloat16)
+    ns.page_table = _page_table(g, rows, ppr, device)
+    n_pages = rows * ppr + 1
+    kv = _randn(g, n_pages, C.PAGE, cfg.qk_dim, device=device)
+    ns.kv, ns.kv_scale = quant_fp8_rows(kv)
+    ns.req_ids = torch.arange(rows, dtype=torch.int32, device=device)
+    ns.sel = torch.stack(
+        [torch.randperm(ctx, generator=g, device=device)[: cfg.topk] for _ in range(rows)]
+    ).to(torch.int32).contiguous()
+    ns.w_uv = _randn(g, cfg.heads, cfg.v_dim, cfg.kv_lora, device=device, std=WEIGHT_STD).to(
+        torch.bfloat16
+    )
+    ns.w_o = _randn(g, cfg.hidden, cfg.heads * cfg.v_dim, device=device, std=WEIGHT_STD).to(
+        torch.bfloat16
+    )
+    ns.w_o_p = pack_bf16(ns.w_o)
+    ns.h = _randn(g, rows, cfg.hidden, device=device).to(torch.bfloat16) if residual else None
+    return ns

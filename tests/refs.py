@@ -1,0 +1,74 @@
+"""Oracle evaluations of synthetic cases (tests, smoke and the CPU baseline only).
+
+Takes the canonical quantized tensors a ``sgl_amd_mono.k2.synth`` namespace holds,
+dequantizes them with the oracle's own decoders and runs ``oracle.reference``.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from oracle import codecs as oc
+from oracle import reference as R
+
+
+def cpu(t):
+    return None if t is None else t.detach().to("cpu")
+
+
+class MoEOracle:
+    """The MoE block of a synth namespace on the CPU (experts dequantized lazily)."""
+
+    def __init__(self, w):
+        from sgl_amd_mono.k2 import config as C
+
+        self.cfg = w.cfg
+        self.C = C
+        self.w_router = cpu(w.w_router).float()
+        self.bias = cpu(w.bias)
+        self.gamma = cpu(w.gamma)
+        self.w13q, self.w13s, self.w2q, self.w2s = map(cpu, (w.w13q, w.w13s, w.w2q, w.w2s))
+        self.shared = None
+        if self.cfg.n_shared:
+            self.shared = (
+                oc.fp8_block_dequant(cpu(w.ws13q), cpu(w.ws13s)),
+                oc.fp8_block_dequant(cpu(w.ws2q), cpu(w.ws2s)),
+            )
+        self._cache = {}
+
+    def expert_weights(self, e):
+        if e not in self._cache:
+            if self.cfg.expert_fmt == self.C.FMT_MXFP4:
+                w13 = oc.mxfp4_dequant(self.w13q[e], self.w13s[e])
+                w2 = oc.mxfp4_dequant(self.w2q[e], self.w2s[e])
+            else:
+                w13 = oc.fp8_block_dequant(self.w13q[e], self.w13s[e])
+                w2 = oc.fp8_block_dequant(self.w2q[e], self.w2s[e])
+            self._cache[e] = (w13, w2)
+        return self._cache[e]
+
+    def dequant_all(self):
+        for e in range(self.cfg.n_experts):
+            self.expert_weights(e)
+
+    def __call__(self, x, *, norm=False, residual=False, eps=1e-6):
+        cfg = self.cfg
+        x = cpu(x).float()
+        xn = R.rmsnorm(x, self.gamma, eps) if norm else x
+        if cfg.router == self.C.ROUTER_SIGMOID_BIAS:
+            route = lambda lg: R.route_sigmoid_bias(lg, self.bias, cfg.top_k, cfg.route_scale)  # noqa: E731
+        else:
+            route = lambda lg: R.route_softmax(lg, cfg.top_k)  # noqa: E731
+        fp4 = cfg.expert_fmt == self.C.FMT_MXFP4
+
+        def expert(e, xr):
+            w13, w2 = self.expert_weights(e)
+            return R.expert_mxfp4(xr, w13, w2) if fp4 else R.expert_fp8(xr, w13, w2)
+
+        shared = None
+        if self.shared is not None:
+            shared = lambda xr: R.expert_fp8(xr, *self.shared)  # noqa: E731
+        return R.moe_block(
+            xn, lambda v: v @ self.w_router.T, route, expert, shared,
+            residual=x if residual else None,
+        )

@@ -1,0 +1,136 @@
+"""MoE block on the GPU against the CPU oracle.
+
+Contract (the reference's own checks, test/kernels/glm53/check_layer.py:631-698 and
+glm53/gfx950/kernel.py:1967-1999):
+  * expert ids: the kernel's picks equal the exact top-k of its own router scores
+    (key desc, lower id first), and equal the oracle's where the k-th / k+1-th gap
+    exceeds the logit tolerance;
+  * router logits within 1e-4 of the largest logit of the row against the oracle;
+  * bf16 outputs within rel-L2 <= 1e-2 of the oracle (after FP8/FP4 dequant).
+"""
+
+import pytest
+import torch
+
+from refs import MoEOracle, cpu
+from oracle import reference as R
+from oracle import codecs as oc
+
+pytestmark = pytest.mark.gpu
+
+REL_L2 = 1e-2
+LOGIT_TOL = 1e-4
+
+
+def _dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda:0")
+
+
+def _run(cfg, rows, seed, norm=False, residual=False):
+    from sgl_amd_mono.k2 import synth
+    from sgl_amd_mono.k2.ops import MoEOp
+
+    dev = _dev()
+    w = synth.make_moe(cfg, rows, seed, dev, norm=norm)
+    op = MoEOp(cfg, w, rows, norm=norm, residual=residual, eps=1e-6)
+    logits = torch.empty(rows, cfg.n_experts, dtype=torch.float32, device=dev)
+    ids = torch.empty(rows, cfg.top_k, dtype=torch.int32, device=dev)
+    wts = torch.empty(rows, cfg.top_k, dtype=torch.float32, device=dev)
+    out = op(w.x, logits=logits, topk_ids=ids, topk_weights=wts)
+    torch.cuda.synchronize()
+    return w, cpu(out).float(), cpu(logits), cpu(ids).long(), cpu(wts)
+
+
+def _check(cfg, w, out, logits, ids, wts, norm=False, residual=False):
+    from sgl_amd_mono.k2 import config as C
+
+    orc = MoEOracle(w)
+    ref, rids, rw, rlogits = orc(w.x, norm=norm, residual=residual, eps=1e-6)
+    # logits against the oracle
+    scale = rlogits.abs().amax(-1, keepdim=True)
+    assert ((logits - rlogits).abs() / scale).max() <= LOGIT_TOL
+    # ids: exact top-k of the kernel's own scores
+    if cfg.router == C.ROUTER_SIGMOID_BIAS:
+        own_keys = oc.radix_keys(torch.sigmoid(logits) + orc.bias)
+        ref_keys = torch.sigmoid(rlogits) + orc.bias
+    else:
+        own_keys = oc.radix_keys(logits)
+        ref_keys = rlogits
+    own = torch.sort(own_keys, dim=-1, descending=True, stable=True).indices[:, : cfg.top_k]
+    assert torch.equal(ids, own), (ids, own)
+    # ids: equal to the oracle's wherever the selection boundary is not a near tie
+    srt = torch.sort(ref_keys, dim=-1, descending=True).values
+    gap = srt[:, cfg.top_k - 1] - srt[:, cfg.top_k]
+    clear = gap > 1e-4 * ref_keys.abs().amax(-1)
+    assert clear.any()
+    assert torch.equal(ids[clear], rids[clear])
+    assert torch.allclose(wts[clear], rw[clear], rtol=1e-4, atol=1e-6)
+    err = R.rel_l2(out, ref)
+    assert err <= REL_L2, err
+    return err
+
+
+@pytest.mark.parametrize("rows", [1, 4, 8])
+def test_moe_fp8_config1(rows):
+    from sgl_amd_mono.k2 import config as C
+
+    cfg = C.C1_MOE
+    w, out, logits, ids, wts = _run(cfg, rows, seed=100 + rows)
+    _check(cfg, w, out, logits, ids, wts)
+
+
+@pytest.mark.parametrize("rows", [1, 8, 32])
+def test_moe_mxfp4_config2(rows):
+    from sgl_amd_mono.k2 import config as C
+
+    cfg = C.C2_MOE
+    w, out, logits, ids, wts = _run(cfg, rows, seed=200 + rows)
+    _check(cfg, w, out, logits, ids, wts)
+
+
+def test_moe_mxfp4_norm_residual():
+    from sgl_amd_mono.k2 import config as C
+
+    cfg = C.C2_MOE
+    w, out, logits, ids, wts = _run(cfg, 8, seed=7, norm=True, residual=True)
+    _check(cfg, w, out, logits, ids, wts, norm=True, residual=True)
+
+
+def test_selftest_mfma_layouts():
+    """The three matrix-core operand modes against torch on one 16x16 tile."""
+    import ctypes  # noqa: F401
+
+    from sgl_amd_mono import _lib
+    from sgl_amd_mono.k2.quant import quant_mxfp4
+
+    dev = _dev()
+    g = torch.Generator().manual_seed(3)
+    a = torch.randn(16, 128, generator=g)
+    b = torch.randn(16, 128, generator=g)
+    d = torch.empty(16, 16, device=dev)
+    L = _lib.lib()
+    st = _lib.stream_handle(dev)
+
+    def run(mode, a_, sa_, b_, sb_):
+        keep = [t.to(dev).contiguous() if t is not None else None for t in (a_, sa_, b_, sb_)]
+        ptrs = [t.data_ptr() if t is not None else None for t in keep]
+        _lib.check(L.mk2_selftest_mfma(mode, ptrs[0], ptrs[1], ptrs[2], ptrs[3], d.data_ptr(), st))
+        torch.cuda.synchronize()
+        return cpu(d).clone()
+
+    # mode 0: bf16 x bf16
+    ab, bb = a.bfloat16(), b.bfloat16()
+    got = run(0, ab, None, bb, None)
+    assert torch.allclose(got, ab.float() @ bb.float().T, rtol=1e-5, atol=1e-4)
+    # mode 2: E4M3 widened x bf16
+    a8 = oc.e4m3_encode(a * 10)
+    got = run(2, a8, None, bb, None)
+    assert torch.allclose(got, oc.e4m3_decode(a8) @ bb.float().T, rtol=1e-5, atol=1e-3)
+    # mode 1: E2M1 x E4M3 with E8M0 scales
+    aq, asc = quant_mxfp4(a)
+    bq, bsc = oc.mxfp8_quant(b)
+    got = run(1, aq, asc, bq, bsc)
+    ref = oc.mxfp4_dequant(aq, asc) @ oc.mxfp8_dequant(bq, bsc).T
+    assert torch.allclose(got, ref, rtol=1e-4, atol=2e-3), (got - ref).abs().max()

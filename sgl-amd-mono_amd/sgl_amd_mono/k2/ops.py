@@ -67,3 +67,39 @@ class MoEOp:
         )
         _lib.check(_lib.lib().mk2_moe_launch(ctypes.byref(args), _lib.stream_handle(self.device)))
         return out
+
+
+class IndexerOp:
+    """FP4 index-key scores and the exact top-k of every row."""
+
+    def __init__(self, cfg: C.IndexerConfig, rows: int, table_stride: int, device=None):
+        cfg.validate(rows)
+        self.cfg, self.rows = cfg, rows
+        self.device = torch.device(device or "cuda")
+        self.shape = _lib.IndexerShape(rows, cfg.heads, cfg.dim, cfg.topk, cfg.context, table_stride)
+        nbytes = ctypes.c_size_t()
+        _lib.check(_lib.lib().mk2_indexer_workspace_bytes(ctypes.byref(self.shape), ctypes.byref(nbytes)))
+        self.workspace = torch.empty(nbytes.value, dtype=torch.uint8, device=self.device)
+
+    def __call__(self, q, w, cache, page_table, req_ids, ctx_len, scores=None, topk=None):
+        cfg, rows = self.cfg, self.rows
+        _need(q, "q", torch.bfloat16, (rows, cfg.heads, cfg.dim))
+        _need(w, "w", torch.bfloat16, (rows, cfg.heads))
+        _need(cache, "cache", torch.uint8)
+        _need(page_table, "page_table", torch.int32)
+        if page_table.shape[1] != self.shape.table_stride:
+            raise ValueError("page_table row stride differs from the op's table_stride")
+        _need(req_ids, "req_ids", torch.int32, (rows,))
+        _need(ctx_len, "ctx_len", torch.int32, (rows,))
+        if scores is None:
+            scores = torch.empty(rows, cfg.context, dtype=torch.float32, device=self.device)
+        if topk is None:
+            topk = torch.empty(rows, cfg.topk, dtype=torch.int32, device=self.device)
+        _need(scores, "scores", torch.float32, (rows, cfg.context))
+        _need(topk, "topk", torch.int32, (rows, cfg.topk))
+        args = _lib.IndexerArgs(
+            self.shape, _p(q), _p(w), _p(cache), _p(page_table), _p(req_ids), _p(ctx_len),
+            _p(scores), _p(topk), _p(self.workspace), self.workspace.numel(),
+        )
+        _lib.check(_lib.lib().mk2_indexer_topk_launch(ctypes.byref(args), _lib.stream_handle(self.device)))
+        return scores, topk

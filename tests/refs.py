@@ -72,3 +72,21 @@ class MoEOracle:
             xn, lambda v: v @ self.w_router.T, route, expert, shared,
             residual=x if residual else None,
         )
+
+
+def index_keys_f32(cache, page_table, req, n, dim=128):
+    """Dequantized FP4 keys of positions 0..n-1 of request `req` (oracle decoders)."""
+    cache, page_table = cpu(cache), cpu(page_table)
+    pages = page_table[req, : (n + 63) // 64].long()
+    raw = cache[pages]  # [np, 4352]
+    codes = raw[:, :4096].reshape(-1, 64, 64)
+    scales = raw[:, 4096:].reshape(-1, 64, 4)
+    keys = oc.mxfp4_dequant(codes, scales).reshape(-1, dim)
+    return keys[:n]
+
+
+def indexer_oracle_scores(ns, r):
+    """f64 scores of row r of a synth indexer namespace."""
+    n = int(ns.ctx_len[r])
+    keys = index_keys_f32(ns.cache, ns.page_table, int(ns.req_ids[r]), n)
+    return R.index_scores(cpu(ns.q[r]).float(), cpu(ns.w[r]).float(), keys)

@@ -1,0 +1,118 @@
+"""FP4 indexer + exact top-k on the GPU.
+
+Contract, after test/kernels/glm53/check_topk.py:56,116-165:
+  * scores within 1e-4 of the row's largest |score| against the f64 oracle;
+  * the list is exactly the oracle's radix-select list (12-bit prefix order, lowest
+    position first on ties) of the kernel's OWN f32 scores -- bit-exact indices;
+  * the selected set equals the oracle's exact top-k of its f64-then-f32 scores on
+    rows whose k-th / k+1-th gap is clear of the score tolerance;
+  * caches: random, ties (every key identical), zeros, ragged and short contexts.
+"""
+
+import pytest
+import torch
+
+from oracle import codecs as oc
+from oracle import reference as R
+from refs import cpu, indexer_oracle_scores
+
+pytestmark = pytest.mark.gpu
+
+SCORE_BOUND = 1e-4
+
+
+def _dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda:0")
+
+
+def _run(cfg, rows, seed, ctx_len=None, mode="random"):
+    from sgl_amd_mono.k2 import synth
+    from sgl_amd_mono.k2.ops import IndexerOp
+
+    dev = _dev()
+    ns = synth.make_indexer(cfg, rows, seed, dev, ctx_len=ctx_len)
+    if mode == "ties":
+        codes, scales = ns.cache[1, :64].clone(), ns.cache[1, 4096:4100].clone()
+        ns.cache[:, :4096] = codes.repeat(64)
+        ns.cache[:, 4096:] = scales.repeat(64)
+    elif mode == "zeros":
+        ns.cache[:, :4096] = 0
+    op = IndexerOp(cfg, rows, ns.page_table.shape[1], device=dev)
+    scores, topk = op(ns.q, ns.w, ns.cache, ns.page_table, ns.req_ids, ns.ctx_len)
+    torch.cuda.synchronize()
+    return ns, cpu(scores), cpu(topk).long()
+
+
+def _check_rows(cfg, ns, scores, topk, expect_clear=True):
+    k = cfg.topk
+    n_clear = 0
+    for r in range(ns.rows):
+        n = int(ns.ctx_len[r])
+        got = scores[r, :n]
+        ref = indexer_oracle_scores(ns, r)
+        err = ((got.double() - ref).abs().max() / ref.abs().max().clamp_min(1e-30)).item()
+        assert err <= SCORE_BOUND, (r, err)
+        # the list: exact radix order of the kernel's own scores
+        want = R.radix_lists(got, k)
+        sel = topk[r]
+        m = min(n, k)
+        assert torch.equal(sel[:m], want), (r, sel[:8], want[:8])
+        assert bool((sel[m:] == -1).all())
+        # the set against the oracle's own scores when the boundary is clear
+        if n > k:
+            keys = torch.sort(ref, descending=True).values
+            gap = (keys[k - 1] - keys[k]).item()
+            if gap > 2 * SCORE_BOUND * ref.abs().max().item():
+                n_clear += 1
+                oset = R.exact_topk_set(ref.float(), k)
+                assert torch.equal(torch.sort(sel).values, oset), r
+    if expect_clear:
+        assert n_clear >= 1
+
+
+def test_indexer_config4_full():
+    from sgl_amd_mono.k2 import config as C
+
+    cfg = C.C4_INDEXER
+    ns, scores, topk = _run(cfg, 8, seed=41)
+    _check_rows(cfg, ns, scores, topk)
+
+
+def test_indexer_ragged_and_short_rows():
+    from sgl_amd_mono.k2 import config as C
+
+    cfg = C.IndexerConfig(heads=64, dim=128, topk=2048, context=8192)
+    ns, scores, topk = _run(cfg, 5, seed=42, ctx_len=[8192, 5003, 2049, 2048, 100])
+    _check_rows(cfg, ns, scores, topk)
+
+
+def test_indexer_fewer_heads_small_topk():
+    from sgl_amd_mono.k2 import config as C
+
+    cfg = C.IndexerConfig(heads=32, dim=128, topk=64, context=4096)
+    ns, scores, topk = _run(cfg, 3, seed=43, ctx_len=[4096, 1000, 65])
+    _check_rows(cfg, ns, scores, topk)
+
+
+def test_indexer_ties_take_lowest_positions():
+    from sgl_amd_mono.k2 import config as C
+
+    cfg = C.IndexerConfig(heads=64, dim=128, topk=256, context=4096)
+    ns, scores, topk = _run(cfg, 2, seed=44, mode="ties")
+    for r in range(2):
+        assert torch.unique(scores[r]).numel() == 1
+        assert torch.equal(topk[r], torch.arange(256))
+    _check_rows(cfg, ns, scores, topk, expect_clear=False)
+
+
+def test_indexer_zero_keys():
+    from sgl_amd_mono.k2 import config as C
+
+    cfg = C.IndexerConfig(heads=64, dim=128, topk=128, context=2048)
+    ns, scores, topk = _run(cfg, 2, seed=45, mode="zeros")
+    assert bool((scores == 0).all())
+    assert bool((oc.radix_keys(scores) == (1 << 31)).all())  # +0.0 everywhere, never -0.0
+    for r in range(2):
+        assert torch.equal(topk[r], torch.arange(128))

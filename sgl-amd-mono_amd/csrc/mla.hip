@@ -1,0 +1,104 @@
+// Standalone sparse-MLA launch: split attention, merge,
+// W_UV, W_o + residual.
+#include "mk2_host.h"
+#include "mla_stages.h"
+
+namespace mk2 {
+
+__global__ __launch_bounds__(MLA_NT) void k_mla_split(MlaDev p) {
+  __shared__ MlaSplitLds L;
+  mla_split(p, blockIdx.y, blockIdx.x, L);
+}
+__global__ __launch_bounds__(MLA_NT) void k_mla_merge(MlaDev p) { mla_merge(p, blockIdx.y, blockIdx.x); }
+template <int NCG>
+__global__ __launch_bounds__(MLA_NT) void k_mla_uv(MlaDev p) {
+  __shared__ float red[4 * NCG * 64 * 4];
+  mla_uv<NCG>(p, blockIdx.y, blockIdx.x, red);
+}
+template <int NCG>
+__global__ __launch_bounds__(MLA_NT) void k_mla_oproj(MlaDev p) {
+  __shared__ float red[4 * NCG * 64 * 4];
+  mla_oproj<NCG>(p, blockIdx.x, red);
+}
+
+int mla_check_shape(const mk2_mla_shape* s) {
+  MK2_REQUIRE(s != nullptr, "mla: shape is NULL");
+  MK2_REQUIRE(s->rows >= 1 && s->rows <= 32, "mla: rows must be in [1, 32], got %d", s->rows);
+  MK2_REQUIRE(s->heads == 16 && s->kv_lora == 512 && s->rope == 64,
+              "mla: the kernels serve 16 heads of 512 + 64 latent dims");
+  MK2_REQUIRE(s->v_dim >= 16 && s->v_dim % 16 == 0 && (s->heads * s->v_dim) % 128 == 0 && s->v_dim <= 512,
+              "mla: v_dim must be a multiple of 16 (heads * v_dim a multiple of 128), got %d", s->v_dim);
+  MK2_REQUIRE(s->hidden >= 16 && s->hidden % 16 == 0, "mla: hidden must be a multiple of 16, got %d", s->hidden);
+  MK2_REQUIRE(s->topk >= 64 && s->topk % 64 == 0 && s->topk <= 65536, "mla: topk must be a multiple of 64, got %d", s->topk);
+  MK2_REQUIRE(s->table_stride >= 1, "mla: table_stride must be positive");
+  MK2_REQUIRE(s->sm_scale > 0.f, "mla: sm_scale must be positive");
+  return MK2_OK;
+}
+
+size_t mla_carve(const mk2_mla_shape* s, void* base, MlaDev* d) {
+  Carver c(base);
+  const int ns = s->topk / MLA_SPLIT;
+  float* po = c.take<float>((size_t)s->rows * ns * MLA_HEADS * MLA_LAT);
+  float* pml = c.take<float>((size_t)s->rows * ns * MLA_HEADS * 2);
+  bf16_t* ol = c.take<bf16_t>((size_t)s->rows * MLA_HEADS * MLA_LAT);
+  bf16_t* o = c.take<bf16_t>((size_t)s->rows * MLA_HEADS * s->v_dim);
+  if (d) { d->part_o = po; d->part_ml = pml; d->o_lat = ol; d->o = o; d->nsplit = ns; }
+  return c.bytes();
+}
+
+int mla_fill(const mk2_mla_args* a, MlaDev* d) {
+  const mk2_mla_shape* s = &a->shape;
+  int rc = mla_check_shape(s);
+  if (rc) return rc;
+  MK2_REQUIRE(a->q && a->kv && a->kv_scale && a->page_table && a->req_ids && a->w_uv && a->w_o,
+              "mla: q, kv, kv_scale, page_table, req_ids, w_uv and w_o must be set");
+  *d = MlaDev{};
+  d->rows = s->rows; d->v_dim = s->v_dim; d->hidden = s->hidden; d->topk = s->topk;
+  d->stride = s->table_stride; d->sm_scale = s->sm_scale;
+  d->q = (const bf16_t*)a->q; d->kv = a->kv; d->kv_scale = a->kv_scale; d->pt = a->page_table;
+  d->req = a->req_ids; d->sel = a->sel; d->w_uv = (const bf16_t*)a->w_uv;
+  d->w_o = (const uint8_t*)a->w_o; d->h = (const bf16_t*)a->h; d->out = (bf16_t*)a->out;
+  d->o_lat_f32 = a->o_latent;
+  return MK2_OK;
+}
+
+void mla_enqueue(const MlaDev& d, hipStream_t st) {
+  k_mla_split<<<dim3(d.nsplit, d.rows), MLA_NT, 0, st>>>(d);
+  k_mla_merge<<<dim3(MLA_HEADS, d.rows), MLA_NT, 0, st>>>(d);
+  if (d.rows > 16) {
+    k_mla_uv<2><<<dim3(d.v_dim / 16, MLA_HEADS), MLA_NT, 0, st>>>(d);
+    k_mla_oproj<2><<<d.hidden / 16, MLA_NT, 0, st>>>(d);
+  } else {
+    k_mla_uv<1><<<dim3(d.v_dim / 16, MLA_HEADS), MLA_NT, 0, st>>>(d);
+    k_mla_oproj<1><<<d.hidden / 16, MLA_NT, 0, st>>>(d);
+  }
+}
+
+}  // namespace mk2
+
+using namespace mk2;
+
+extern "C" int mk2_mla_workspace_bytes(const mk2_mla_shape* shape, size_t* bytes) {
+  clear_error();
+  int rc = mla_check_shape(shape);
+  if (rc) return rc;
+  MK2_REQUIRE(bytes != nullptr, "mla: bytes is NULL");
+  *bytes = mla_carve(shape, nullptr, nullptr);
+  return MK2_OK;
+}
+
+extern "C" int mk2_sparse_mla_launch(const mk2_mla_args* a, mk2_stream_t stream) {
+  clear_error();
+  MK2_REQUIRE(a != nullptr, "mla: args is NULL");
+  MlaDev d;
+  int rc = mla_fill(a, &d);
+  if (rc) return rc;
+  MK2_REQUIRE(a->sel && a->out && a->workspace, "mla: sel, out and workspace must be set");
+  MK2_REQUIRE(a->out != a->h, "mla: out must not alias h");
+  const size_t need = mla_carve(&a->shape, nullptr, nullptr);
+  if (a->workspace_bytes < need)
+    return set_error(MK2_ENOSPACE, "mla: workspace has %zu bytes, needs %zu", a->workspace_bytes, need);
+  mla_carve(&a->shape, a->workspace, &d);
+  mla_enqueue(d, (hipStream_t)stream);
+  return check_launch("mla");
+}

@@ -1,0 +1,287 @@
+// Sparse-MLA stages of the K2 layer: split attention over gathered FP8 latent-KV
+// rows, the merge of the splits, W_UV, and W_o with the residual.
+//
+// split task (row r, split s): 64 selected positions -> page table -> 576-byte E4M3
+// rows, gathered with 16-byte loads into LDS twice: row-major (the QK operand) and,
+// for the first 512 dims, transposed to [dim][key] (the PV operand, 8 keys a lane
+// read).  S = q . k on bf16 MFMA (E4M3 widens exactly), x (scale_k * sm_scale); a
+// split-local softmax per head; P' = p * scale_k rounded to bf16; O = P' V on bf16
+// MFMA.  The split writes O (unnormalized), its max m and sum l.
+// merge task (row r, head h): exact combination of the splits -> o_lat (bf16).
+// uv task (head h, 16 v rows): o = W_UV[h] o_lat on bf16 MFMA (rows as columns).
+// oproj task (16 hidden rows): a = bf16(h + W_o o) on bf16 MFMA.
+#pragma once
+#include "mk2_device.h"
+
+namespace mk2 {
+
+constexpr int MLA_D = 576;        // latent 512 + rope 64
+constexpr int MLA_LAT = 512;
+constexpr int MLA_HEADS = 16;
+constexpr int MLA_SPLIT = 64;     // keys a split task
+constexpr int MLA_KROW = 584;     // LDS row stride of the gathered rows (bytes)
+constexpr int MLA_VROW = 72;      // LDS row stride of the transposed latent (bytes)
+constexpr int MLA_NT = 256;
+
+struct MlaDev {
+  int rows, v_dim, hidden, topk, stride, nsplit;
+  float sm_scale;
+  const bf16_t* q;       // [rows][16][576]
+  const uint8_t* kv;     // [pages][64][576]
+  const float* kv_scale; // [pages][64]
+  const int* pt;
+  const int* req;
+  const int* sel;        // [rows][topk]
+  const bf16_t* w_uv;    // [16][v_dim][512]
+  const uint8_t* w_o;    // tiles of [hidden][16*v_dim]
+  const bf16_t* h;       // [rows][hidden] or null
+  bf16_t* out;           // [rows][hidden]
+  // workspace
+  float* part_o;         // [rows][nsplit][16][512]
+  float* part_ml;        // [rows][nsplit][16][2]
+  bf16_t* o_lat;         // [rows][16][512]
+  float* o_lat_f32;      // optional [rows][16][512]
+  bf16_t* o;             // [rows][16 * v_dim]
+};
+
+struct MlaSplitLds {
+  uint8_t k[MLA_SPLIT * MLA_KROW];       // gathered rows, row-major
+  uint8_t vt[MLA_LAT * MLA_VROW];        // latent dims transposed: [dim][key]
+  bf16_t p[MLA_HEADS * (MLA_SPLIT + 8)]; // P' [head][key]
+  float sc[MLA_SPLIT];                   // per-key scale * sm_scale
+  float kscale[MLA_SPLIT];
+  float red[4][MLA_HEADS];
+};
+
+// ---------------------------------------------------------------- stage: split
+MK2_DEV void mla_split(const MlaDev& p, int r, int s, MlaSplitLds& L) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, c16 = lane & 15;
+  const int* selr = p.sel + (size_t)r * p.topk + s * MLA_SPLIT;
+  const int* ptr = p.pt + (size_t)p.req[r] * p.stride;
+  // q operands for this wave's QK: head c16, dims 8g + 32ks .. +7
+  bf16x8 qa[18];
+  const bf16_t* qr = p.q + ((size_t)r * MLA_HEADS + c16) * MLA_D + 8 * g;
+#pragma unroll
+  for (int ks = 0; ks < 18; ++ks) qa[ks] = __builtin_bit_cast(bf16x8, *(const uint4*)(qr + 32 * ks));
+  // per-key scales
+  if (tid < MLA_SPLIT) {
+    const int pos = selr[tid];
+    float ksc = 0.f;
+    if (pos >= 0) ksc = p.kv_scale[(size_t)ptr[pos >> 6] * 64 + (pos & 63)];
+    L.kscale[tid] = ksc;
+    L.sc[tid] = pos >= 0 ? ksc * p.sm_scale : 0.f;
+  }
+  // gather: job = (4-key group kg, 16-byte dim chunk dc); 16 x 36 jobs
+  for (int job = tid; job < 16 * 36; job += MLA_NT) {
+    const int kg = job / 36, dc = job % 36;
+    uint4 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int pos = selr[kg * 4 + j];
+      if (pos >= 0) {
+        const size_t row = (size_t)ptr[pos >> 6] * 64 + (pos & 63);
+        v[j] = *(const uint4*)(p.kv + row * MLA_D + dc * 16);
+      } else {
+        v[j] = make_uint4(0, 0, 0, 0);
+      }
+      uint8_t* dst = L.k + (kg * 4 + j) * MLA_KROW + dc * 16;
+      *(uint2*)dst = make_uint2(v[j].x, v[j].y);
+      *(uint2*)(dst + 8) = make_uint2(v[j].z, v[j].w);
+    }
+    if (dc < 32) {
+      // transpose 4 keys x 16 dims of bytes -> 16 words of 4 keys
+      uint32_t w[4][4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) { w[j][0] = v[j].x; w[j][1] = v[j].y; w[j][2] = v[j].z; w[j][3] = v[j].w; }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const uint32_t sh = 8 * b;
+          const uint32_t word = ((w[0][q] >> sh) & 0xFF) | (((w[1][q] >> sh) & 0xFF) << 8) |
+                                (((w[2][q] >> sh) & 0xFF) << 16) | (((w[3][q] >> sh) & 0xFF) << 24);
+          const int d = dc * 16 + q * 4 + b;
+          *(uint32_t*)(L.vt + d * MLA_VROW + kg * 4) = word;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  // QK: wave w takes keys 16w .. 16w+15 as the MFMA columns
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  const uint8_t* krow = L.k + (wave * 16 + c16) * MLA_KROW + 8 * g;
+#pragma unroll
+  for (int ks = 0; ks < 18; ++ks) {
+    const uint2 kw = *(const uint2*)(krow + 32 * ks);
+    acc = mfma_bf16(qa[ks], e4m3x8_to_bf16(kw.x, kw.y), acc);
+  }
+  const int key = wave * 16 + c16;
+  const bool valid = selr[key] >= 0;
+  float sv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) sv[i] = valid ? acc[i] * L.sc[key] : -INFINITY;
+  // split-local softmax per head (heads 4g + i)
+  float mx[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) mx[i] = row16_max(sv[i]);
+  if (c16 == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) L.red[wave][4 * g + i] = mx[i];
+  }
+  __syncthreads();
+  float m[4], pe[4], ls[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int hd = 4 * g + i;
+    m[i] = fmaxf(fmaxf(L.red[0][hd], L.red[1][hd]), fmaxf(L.red[2][hd], L.red[3][hd]));
+    pe[i] = (valid && m[i] != -INFINITY) ? expf(sv[i] - m[i]) : 0.f;
+    ls[i] = row16_sum(pe[i]);
+    L.p[hd * (MLA_SPLIT + 8) + key] = f32_to_bf16(pe[i] * L.kscale[key]);
+  }
+  __syncthreads();
+  if (c16 == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) L.red[wave][4 * g + i] = ls[i];
+  }
+  __syncthreads();
+  float* mlo = p.part_ml + (((size_t)r * p.nsplit + s) * MLA_HEADS) * 2;
+  if (wave == 0 && c16 == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int hd = 4 * g + i;
+      mlo[hd * 2] = m[i];
+      mlo[hd * 2 + 1] = L.red[0][hd] + L.red[1][hd] + L.red[2][hd] + L.red[3][hd];
+    }
+  }
+  // PV: wave w takes dim tiles 8w .. 8w+7 (16 dims each), 2 key steps of 32
+  bf16x8 pa[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+    pa[ks] = __builtin_bit_cast(bf16x8, *(const uint4*)(L.p + c16 * (MLA_SPLIT + 8) + 32 * ks + 8 * g));
+  float* orow = p.part_o + ((size_t)r * p.nsplit + s) * MLA_HEADS * MLA_LAT;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const int d0 = (wave * 8 + t) * 16;
+    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const uint2 vw = *(const uint2*)(L.vt + (d0 + c16) * MLA_VROW + 32 * ks + 8 * g);
+      o = mfma_bf16(pa[ks], e4m3x8_to_bf16(vw.x, vw.y), o);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) orow[(4 * g + i) * MLA_LAT + d0 + c16] = o[i];
+  }
+  __syncthreads();
+}
+
+// ---------------------------------------------------------------- stage: merge
+MK2_DEV void mla_merge(const MlaDev& p, int r, int h) {
+  const int tid = threadIdx.x;
+  float M = -INFINITY;
+  for (int s = 0; s < p.nsplit; ++s)
+    M = fmaxf(M, p.part_ml[(((size_t)r * p.nsplit + s) * MLA_HEADS + h) * 2]);
+  float Lsum = 0.f, o0 = 0.f, o1 = 0.f;
+  for (int s = 0; s < p.nsplit; ++s) {
+    const float* ml = p.part_ml + (((size_t)r * p.nsplit + s) * MLA_HEADS + h) * 2;
+    const float ms = ml[0];
+    const float wgt = ms == -INFINITY ? 0.f : expf(ms - M);
+    Lsum += ml[1] * wgt;
+    const float2 ov = *(const float2*)(p.part_o + (((size_t)r * p.nsplit + s) * MLA_HEADS + h) * MLA_LAT + 2 * tid);
+    o0 += ov.x * wgt;
+    o1 += ov.y * wgt;
+  }
+  const float inv = Lsum > 0.f ? 1.0f / Lsum : 0.f;
+  o0 *= inv;
+  o1 *= inv;
+  const size_t at = ((size_t)r * MLA_HEADS + h) * MLA_LAT + 2 * tid;
+  *(uint32_t*)(p.o_lat + at) = pack_bf16x2(o0, o1);
+  if (p.o_lat_f32) *(float2*)(p.o_lat_f32 + at) = make_float2(o0, o1);
+}
+
+// ---------------------------------------------------------------- stage: W_UV
+template <int NCG>
+MK2_DEV void mla_uv(const MlaDev& p, int h, int vt, float* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, c16 = lane & 15;
+  const int kb = wave;  // 4 waves x 128 of the 512 latent dims
+  bf16x8 a[4];
+  const bf16_t* wrow = p.w_uv + ((size_t)h * p.v_dim + vt * 16 + c16) * MLA_LAT + kb * 128 + 32 * g;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) a[q] = __builtin_bit_cast(bf16x8, *(const uint4*)(wrow + 8 * q));
+  f32x4 acc[NCG];
+#pragma unroll
+  for (int cg = 0; cg < NCG; ++cg) {
+    const int row = cg * 16 + c16;
+    bf16x8 b[4];
+    if (row < p.rows) {
+      const bf16_t* src = p.o_lat + ((size_t)row * MLA_HEADS + h) * MLA_LAT + kb * 128 + 32 * g;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) b[q] = __builtin_bit_cast(bf16x8, *(const uint4*)(src + 8 * q));
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) b[q] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
+    }
+    f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) c = mfma_bf16(a[q], b[q], c);
+    acc[cg] = c;
+  }
+#pragma unroll
+  for (int cg = 0; cg < NCG; ++cg) *(f32x4*)(red + ((wave * NCG + cg) * 64 + lane) * 4) = acc[cg];
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < 16 * p.rows; idx += MLA_NT) {
+    const int n16 = idx & 15, row = idx >> 4, cg = row >> 4, s16 = row & 15;
+    const int l = (n16 >> 2) * 16 + s16, i = n16 & 3;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) v += red[((w * NCG + cg) * 64 + l) * 4 + i];
+    p.o[(size_t)row * (MLA_HEADS * p.v_dim) + h * p.v_dim + vt * 16 + n16] = f32_to_bf16(v);
+  }
+  __syncthreads();
+}
+
+// ---------------------------------------------------------------- stage: W_o
+template <int NCG>
+MK2_DEV void mla_oproj(const MlaDev& p, int nt, float* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, c16 = lane & 15;
+  const int K = MLA_HEADS * p.v_dim, KB = K / 128;
+  f32x4 acc[NCG];
+#pragma unroll
+  for (int cg = 0; cg < NCG; ++cg) acc[cg] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int kb = wave; kb < KB; kb += 4) {
+    bf16x8 a[4];
+    const uint4* t = (const uint4*)(p.w_o + (((size_t)nt * KB + kb) * 64 + lane) * 64);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) a[q] = __builtin_bit_cast(bf16x8, t[q]);
+#pragma unroll
+    for (int cg = 0; cg < NCG; ++cg) {
+      const int row = cg * 16 + c16;
+      bf16x8 b[4];
+      if (row < p.rows) {
+        const uint4* src = (const uint4*)(p.o + (size_t)row * K + kb * 128 + 32 * g);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) b[q] = __builtin_bit_cast(bf16x8, src[q]);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) b[q] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[cg] = mfma_bf16(a[q], b[q], acc[cg]);
+    }
+  }
+#pragma unroll
+  for (int cg = 0; cg < NCG; ++cg) *(f32x4*)(red + ((wave * NCG + cg) * 64 + lane) * 4) = acc[cg];
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < 16 * p.rows; idx += MLA_NT) {
+    const int n16 = idx & 15, row = idx >> 4, cg = row >> 4, s16 = row & 15;
+    const int l = (n16 >> 2) * 16 + s16, i = n16 & 3;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) v += red[((w * NCG + cg) * 64 + l) * 4 + i];
+    const size_t o = (size_t)row * p.hidden + nt * 16 + n16;
+    if (p.h) v += bf16_to_f32(p.h[o]);
+    p.out[o] = f32_to_bf16(v);
+  }
+  __syncthreads();
+}
+
+}  // namespace mk2

@@ -103,3 +103,41 @@ class IndexerOp:
         )
         _lib.check(_lib.lib().mk2_indexer_topk_launch(ctypes.byref(args), _lib.stream_handle(self.device)))
         return scores, topk
+
+
+class SparseMlaOp:
+    """Sparse MLA over selected latent-KV rows, W_UV, then W_o (+ residual)."""
+
+    def __init__(self, cfg: C.MlaConfig, w, rows: int, table_stride: int, device=None):
+        cfg.validate(rows)
+        self.cfg, self.rows, self.w = cfg, rows, w
+        self.device = torch.device(device or w.w_o_p.device)
+        _need(w.w_uv, "w_uv", torch.bfloat16, (cfg.heads, cfg.v_dim, cfg.kv_lora))
+        self.shape = _lib.MlaShape(
+            rows, cfg.heads, cfg.kv_lora, cfg.rope, cfg.v_dim, cfg.hidden, cfg.topk,
+            table_stride, cfg.sm_scale,
+        )
+        nbytes = ctypes.c_size_t()
+        _lib.check(_lib.lib().mk2_mla_workspace_bytes(ctypes.byref(self.shape), ctypes.byref(nbytes)))
+        self.workspace = torch.empty(nbytes.value, dtype=torch.uint8, device=self.device)
+
+    def __call__(self, q, kv, kv_scale, page_table, req_ids, sel, h=None, out=None, o_latent=None):
+        cfg, rows = self.cfg, self.rows
+        _need(q, "q", torch.bfloat16, (rows, cfg.heads, cfg.qk_dim))
+        _need(kv, "kv", torch.uint8)
+        _need(kv_scale, "kv_scale", torch.float32)
+        _need(page_table, "page_table", torch.int32)
+        _need(req_ids, "req_ids", torch.int32, (rows,))
+        _need(sel, "sel", torch.int32, (rows, cfg.topk))
+        if h is not None:
+            _need(h, "h", torch.bfloat16, (rows, cfg.hidden))
+        if out is None:
+            out = torch.empty(rows, cfg.hidden, dtype=torch.bfloat16, device=self.device)
+        _need(out, "out", torch.bfloat16, (rows, cfg.hidden))
+        args = _lib.MlaArgs(
+            self.shape, _p(q), _p(kv), _p(kv_scale), _p(page_table), _p(req_ids), _p(sel),
+            _p(self.w.w_uv), _p(self.w.w_o_p), _p(h), _p(out), _p(self.workspace),
+            self.workspace.numel(), _p(o_latent),
+        )
+        _lib.check(_lib.lib().mk2_sparse_mla_launch(ctypes.byref(args), _lib.stream_handle(self.device)))
+        return out

@@ -90,3 +90,23 @@ def indexer_oracle_scores(ns, r):
     n = int(ns.ctx_len[r])
     keys = index_keys_f32(ns.cache, ns.page_table, int(ns.req_ids[r]), n)
     return R.index_scores(cpu(ns.q[r]).float(), cpu(ns.w[r]).float(), keys)
+
+
+def mla_oracle(ns, sel=None, h="auto"):
+    """(o_lat f32 [rows, 16, 512], out f32-of-bf16 [rows, hidden]) of a synth MLA case."""
+    cfg = ns.cfg
+    sel = cpu(ns.sel if sel is None else sel).long()
+    kv, ksc, pt = cpu(ns.kv), cpu(ns.kv_scale), cpu(ns.page_table)
+    q, w_uv, w_o = cpu(ns.q).float(), cpu(ns.w_uv).float(), cpu(ns.w_o).float()
+    hres = cpu(ns.h) if h == "auto" else (cpu(h) if h is not None else None)
+    olats, outs = [], []
+    for r in range(ns.rows):
+        pos = sel[r][sel[r] >= 0]
+        req = int(ns.req_ids[r])
+        pages = pt[req, pos // 64].long()
+        rows_kv = oc.fp8_row_dequant(kv[pages, pos % 64], ksc[pages, pos % 64])
+        ol = R.sparse_mla(q[r], rows_kv, cfg.sm_scale, cfg.kv_lora)
+        o = R.mla_output(ol, w_uv)
+        outs.append(R.o_proj(o[None], w_o, None if hres is None else hres[r : r + 1])[0])
+        olats.append(ol)
+    return torch.stack(olats), torch.stack(outs)

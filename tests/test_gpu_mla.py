@@ -1,0 +1,65 @@
+"""Sparse MLA + W_UV + W_o on the GPU.
+
+Bar: the merged latent output and the bf16 layer output within rel-L2 1e-2 of the
+CPU oracle (f64 softmax over the same gathered, dequantized FP8 rows); the kernel
+rounds P' and the stage hand-offs to bf16 where the oracle states the same points.
+"""
+
+import pytest
+import torch
+
+from oracle import reference as R
+from refs import cpu, mla_oracle
+
+pytestmark = pytest.mark.gpu
+
+REL_L2 = 1e-2
+
+
+def _dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda:0")
+
+
+def _run(cfg, rows, seed, residual=True, holes=False):
+    from sgl_amd_mono.k2 import synth
+    from sgl_amd_mono.k2.ops import SparseMlaOp
+
+    dev = _dev()
+    ns = synth.make_mla(cfg, rows, seed, dev, residual=residual)
+    if holes:  # unused slots (-1) inside and at the end of the list
+        ns.sel[:, 5:70] = -1
+        ns.sel[0, -64:] = -1
+    op = SparseMlaOp(cfg, ns, rows, ns.page_table.shape[1], device=dev)
+    olat = torch.empty(rows, cfg.heads, cfg.kv_lora, dtype=torch.float32, device=dev)
+    out = op(ns.q, ns.kv, ns.kv_scale, ns.page_table, ns.req_ids, ns.sel, h=ns.h, o_latent=olat)
+    torch.cuda.synchronize()
+    ref_lat, ref_out = mla_oracle(ns)
+    e_lat = R.rel_l2(cpu(olat), ref_lat)
+    e_out = R.rel_l2(cpu(out).float(), ref_out)
+    return e_lat, e_out
+
+
+@pytest.mark.parametrize("rows", [1, 8])
+def test_mla_config3(rows):
+    from sgl_amd_mono.k2 import config as C
+
+    e_lat, e_out = _run(C.C3_MLA, rows, seed=300 + rows)
+    assert e_lat <= REL_L2 and e_out <= REL_L2, (e_lat, e_out)
+
+
+def test_mla_unused_slots_and_no_residual():
+    from sgl_amd_mono.k2 import config as C
+
+    cfg = C.MlaConfig(context=8192, topk=512)
+    e_lat, e_out = _run(cfg, 3, seed=310, residual=False, holes=True)
+    assert e_lat <= REL_L2 and e_out <= REL_L2, (e_lat, e_out)
+
+
+def test_mla_32_rows():
+    from sgl_amd_mono.k2 import config as C
+
+    cfg = C.MlaConfig(context=4096, topk=2048)
+    e_lat, e_out = _run(cfg, 32, seed=320)
+    assert e_lat <= REL_L2 and e_out <= REL_L2, (e_lat, e_out)

@@ -1,0 +1,105 @@
+// The chained K2 layer as a stream of stage kernels: indexer scores -> exact
+// top-k -> sparse MLA -> W_UV -> W_o + residual -> RMSNorm -> router -> top-k
+// routing -> up/gate -> down + residual.  (The single persistent launch is in
+// k2_persistent.hip; this path is its stage-by-stage twin.)
+#include "indexer_stages.h"
+#include "mla_stages.h"
+#include "mk2_host.h"
+#include "moe_stages.h"
+
+namespace mk2 {
+
+int idx_fill(const mk2_indexer_args* a, IdxDev* d);
+size_t idx_carve(const mk2_indexer_shape* s, void* base, float** scores, int** topk);
+void idx_enqueue(const IdxDev& d, hipStream_t st);
+int mla_fill(const mk2_mla_args* a, MlaDev* d);
+size_t mla_carve(const mk2_mla_shape* s, void* base, MlaDev* d);
+void mla_enqueue(const MlaDev& d, hipStream_t st);
+int moe_fill(const mk2_moe_args* a, MoeDev* d);
+size_t moe_carve(const mk2_moe_shape* s, void* base, MoeDev* d);
+int moe_enqueue(const MoeDev& d, hipStream_t st);
+
+struct LayerPlan {
+  IdxDev idx;
+  MlaDev mla;
+  MoeDev moe;
+};
+
+// validate the three blocks against each other and carve one workspace for all
+int layer_plan(const mk2_layer_args* a, void* ws, LayerPlan* L, size_t* bytes) {
+  MK2_REQUIRE(a != nullptr, "layer: args is NULL");
+  const mk2_indexer_shape& is = a->indexer.shape;
+  const mk2_mla_shape& ms = a->mla.shape;
+  const mk2_moe_shape& es = a->moe.shape;
+  MK2_REQUIRE(is.rows == ms.rows && ms.rows == es.rows, "layer: rows differ between blocks (%d, %d, %d)",
+              is.rows, ms.rows, es.rows);
+  MK2_REQUIRE(is.topk == ms.topk, "layer: indexer topk %d != attention topk %d", is.topk, ms.topk);
+  MK2_REQUIRE(ms.hidden == es.hidden, "layer: attention hidden %d != MoE hidden %d", ms.hidden, es.hidden);
+  MK2_REQUIRE(es.norm == 1 && es.residual == 1, "layer: the MoE block runs with norm=1 and residual=1");
+  int rc = idx_fill(&a->indexer, &L->idx);
+  if (rc) return rc;
+  rc = mla_fill(&a->mla, &L->mla);
+  if (rc) return rc;
+  MK2_REQUIRE(a->mla.h != nullptr, "layer: the attention residual h must be set");
+  // the MoE input is the attention output; give moe_fill a stand-in to validate
+  mk2_moe_args ma = a->moe;
+  ma.x = (const void*)1;
+  ma.out = (void*)2;
+  rc = moe_fill(&ma, &L->moe);
+  if (rc) return rc;
+  Carver c(ws);
+  const size_t b_idx = idx_carve(&is, nullptr, nullptr, nullptr);
+  const size_t b_mla = mla_carve(&ms, nullptr, nullptr);
+  const size_t b_moe = moe_carve(&es, nullptr, nullptr);
+  char* p_idx = c.take<char>(b_idx);
+  char* p_mla = c.take<char>(b_mla);
+  char* p_moe = c.take<char>(b_moe);
+  bf16_t* attn = c.take<bf16_t>((size_t)ms.rows * ms.hidden);
+  *bytes = c.bytes();
+  if (!ws) return MK2_OK;
+  float* sc;
+  int* tk;
+  idx_carve(&is, p_idx, &sc, &tk);
+  if (!L->idx.scores) L->idx.scores = sc;
+  if (!L->idx.out) L->idx.out = tk;
+  mla_carve(&ms, p_mla, &L->mla);
+  moe_carve(&es, p_moe, &L->moe);
+  if (a->moe.logits) L->moe.logits = a->moe.logits;
+  if (a->moe.topk_ids) L->moe.topk_ids = a->moe.topk_ids;
+  if (a->moe.topk_weights) L->moe.topk_w = a->moe.topk_weights;
+  L->mla.sel = L->idx.out;
+  bf16_t* a_out = a->attn_out ? (bf16_t*)a->attn_out : attn;
+  L->mla.out = a_out;
+  L->moe.x = a_out;
+  L->moe.out = (bf16_t*)a->out;
+  return MK2_OK;
+}
+
+}  // namespace mk2
+
+using namespace mk2;
+
+extern "C" int mk2_layer_workspace_bytes(const mk2_layer_args* a, size_t* bytes) {
+  clear_error();
+  MK2_REQUIRE(bytes != nullptr, "layer: bytes is NULL");
+  LayerPlan L;
+  return layer_plan(a, nullptr, &L, bytes);
+}
+
+extern "C" int mk2_layer_launch(const mk2_layer_args* a, mk2_stream_t stream) {
+  clear_error();
+  LayerPlan L;
+  size_t need = 0;
+  int rc = layer_plan(a, nullptr, &L, &need);
+  if (rc) return rc;
+  MK2_REQUIRE(a->out && a->workspace, "layer: out and workspace must be set");
+  MK2_REQUIRE(a->out != a->mla.h, "layer: out must not alias the residual h");
+  if (a->workspace_bytes < need)
+    return set_error(MK2_ENOSPACE, "layer: workspace has %zu bytes, needs %zu", a->workspace_bytes, need);
+  rc = layer_plan(a, a->workspace, &L, &need);
+  if (rc) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  idx_enqueue(L.idx, st);
+  mla_enqueue(L.mla, st);
+  return moe_enqueue(L.moe, st);
+}

@@ -141,3 +141,53 @@ class SparseMlaOp:
         )
         _lib.check(_lib.lib().mk2_sparse_mla_launch(ctypes.byref(args), _lib.stream_handle(self.device)))
         return out
+
+
+class LayerOp:
+    """The chained K2 layer: indexer -> top-k -> sparse MLA -> o_proj + residual ->
+    RMSNorm -> MoE + residual (the reference's Glm53LayerOp.launch without the TP
+    reduces, glm53/gfx950/runner.py:374-470)."""
+
+    def __init__(self, cfg: C.K2Config, layer, rows: int, device=None):
+        cfg.validate(rows)
+        self.cfg, self.rows, self.L = cfg, rows, layer
+        self.device = torch.device(device or layer.h.device)
+        self.idx = IndexerOp(cfg.indexer, rows, layer.idx.page_table.shape[1], self.device)
+        self.mla = SparseMlaOp(cfg.mla, layer.mla, rows, layer.mla.page_table.shape[1], self.device)
+        self.moe = MoEOp(cfg.moe, layer.moe, rows, norm=True, residual=True, eps=cfg.eps,
+                         device=self.device)
+        self._args = None
+        nbytes = ctypes.c_size_t()
+        _lib.check(_lib.lib().mk2_layer_workspace_bytes(ctypes.byref(self._make_args()),
+                                                        ctypes.byref(nbytes)))
+        self.workspace = torch.empty(nbytes.value, dtype=torch.uint8, device=self.device)
+
+    def _make_args(self, out=None, attn_out=None, scores=None, topk=None, logits=None,
+                   topk_ids=None, topk_weights=None, workspace=None):
+        L = self.L
+        ia = _lib.IndexerArgs(
+            self.idx.shape, _p(L.idx.q), _p(L.idx.w), _p(L.idx.cache), _p(L.idx.page_table),
+            _p(L.idx.req_ids), _p(L.idx.ctx_len), _p(scores), _p(topk), None, 0,
+        )
+        ma = _lib.MlaArgs(
+            self.mla.shape, _p(L.mla.q), _p(L.mla.kv), _p(L.mla.kv_scale), _p(L.mla.page_table),
+            _p(L.mla.req_ids), None, _p(L.mla.w_uv), _p(L.mla.w_o_p), _p(L.h), None, None, 0, None,
+        )
+        ea = _lib.MoeArgs(
+            self.moe.shape, self.moe.weights, None, None, None, 0,
+            _p(logits), _p(topk_ids), _p(topk_weights),
+        )
+        ws = workspace
+        return _lib.LayerArgs(ia, ma, ea, _p(attn_out), _p(out), _p(ws),
+                              0 if ws is None else ws.numel())
+
+    def __call__(self, out=None, *, attn_out=None, scores=None, topk=None, logits=None,
+                 topk_ids=None, topk_weights=None):
+        H = self.cfg.mla.hidden
+        if out is None:
+            out = torch.empty(self.rows, H, dtype=torch.bfloat16, device=self.device)
+        _need(out, "out", torch.bfloat16, (self.rows, H))
+        args = self._make_args(out, attn_out, scores, topk, logits, topk_ids, topk_weights,
+                               self.workspace)
+        _lib.check(_lib.lib().mk2_layer_launch(ctypes.byref(args), _lib.stream_handle(self.device)))
+        return out

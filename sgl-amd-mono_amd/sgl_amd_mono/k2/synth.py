@@ -135,3 +135,16 @@ def make_mla(cfg: C.MlaConfig, rows: int, seed: int, device, residual: bool = Tr
     ns.w_o_p = pack_bf16(ns.w_o)
     ns.h = _randn(g, rows, cfg.hidden, device=device).to(torch.bfloat16) if residual else None
     return ns
+
+
+def make_layer(cfg: C.K2Config, rows: int, seed: int, device):
+    """One chained layer: indexer keys and queries, latent-KV pages sharing the
+    indexer's page table, attention weights, residual rows, MoE weights with the
+    post-attention RMSNorm weight."""
+    idx = make_indexer(cfg.indexer, rows, seed, device)
+    mla = make_mla(cfg.mla, rows, seed + 1, device, residual=True)
+    mla.page_table = idx.page_table
+    mla.req_ids = idx.req_ids
+    mla.sel = None  # the chain supplies the indexer's selection
+    moe = make_moe(cfg.moe, rows, seed + 2, device, norm=True)
+    return SimpleNamespace(cfg=cfg, rows=rows, idx=idx, mla=mla, moe=moe, h=mla.h)

@@ -110,3 +110,37 @@ def mla_oracle(ns, sel=None, h="auto"):
         outs.append(R.o_proj(o[None], w_o, None if hres is None else hres[r : r + 1])[0])
         olats.append(ol)
     return torch.stack(olats), torch.stack(outs)
+
+
+def check_layer(L, out, attn, scores, topk, logits, ids, wts, *, rel_l2=1e-2, score_bound=1e-4):
+    """Piecewise parity of a chained K2 layer run (kernel outputs on the CPU):
+      indexer -- scores vs f64, the list == radix_lists of the kernel's own scores;
+      attention -- on the kernel's selection, rel-L2 of the attention output;
+      MoE -- on the kernel's attention output, router logits, ids, rel-L2 of out.
+    Returns a dict of the measured errors."""
+    cfg = L.cfg
+    k = cfg.indexer.topk
+    worst = 0.0
+    for r in range(L.rows):
+        n = int(L.idx.ctx_len[r])
+        got = scores[r, :n]
+        ref = indexer_oracle_scores(L.idx, r)
+        err = ((got.double() - ref).abs().max() / ref.abs().max().clamp_min(1e-30)).item()
+        worst = max(worst, err)
+        assert err <= score_bound, ("index score", r, err)
+        assert torch.equal(topk[r, : min(n, k)].long(), R.radix_lists(got, k)), ("top-k list", r)
+    _, ref_attn = mla_oracle(L.mla, sel=topk, h=L.h)
+    e_attn = R.rel_l2(attn.float(), ref_attn)
+    assert e_attn <= rel_l2, ("attention", e_attn)
+    orc = MoEOracle(L.moe)
+    ref_out, rids, rw, rlogits = orc(attn, norm=True, residual=True, eps=cfg.eps)
+    e_logit = ((logits - rlogits).abs() / rlogits.abs().amax(-1, keepdim=True)).max().item()
+    assert e_logit <= 1e-4, ("router logits", e_logit)
+    s = torch.sigmoid(rlogits) + orc.bias
+    srt = torch.sort(s, dim=-1, descending=True).values
+    clear = (srt[:, cfg.moe.top_k - 1] - srt[:, cfg.moe.top_k]) > 1e-4 * s.abs().amax(-1)
+    assert torch.equal(ids.long()[clear], rids[clear]), "expert ids"
+    e_out = R.rel_l2(out.float(), ref_out)
+    assert e_out <= rel_l2, ("layer out", e_out)
+    return {"score_err": worst, "attn_rel_l2": e_attn, "logit_err": e_logit, "out_rel_l2": e_out,
+            "clear_rows": int(clear.sum())}

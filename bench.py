@@ -1,0 +1,193 @@
+#!/usr/bin/env python3
+"""Benchmark of the K2 decode layer on one MI355X (M=8).
+
+A step is one launch of the chained layer (indexer scores -> exact top-2048 ->
+sparse MLA -> W_UV -> W_o + residual -> RMSNorm -> router top-8 -> MXFP4 routed +
+FP8 shared experts -> residual) over 8 decode rows.  Weights and caches of
+several distinct layers are resident in HBM and the steps cycle through them, so
+no step finds its weights in the 256 MB last-level cache a previous step left.
+Steps are replayed from one HIP graph and timed with events on the launch stream.
+
+Prints ONE JSON line (see the driver contract): value = us per layer.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "sgl-amd-mono_amd"), os.path.join(ROOT, "tests")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_HBM_GBS = 8000.0
+METRIC = "us per fused decoder layer @8 decode rows, 1 GPU; % of peak HBM GB/s"
+
+
+def algorithmic_bytes(cfg, rows, distinct_experts):
+    """HBM bytes a layer must move at least once (SURVEY 8(d) accounting): index keys
+    of every request, the gathered latent-KV rows with their scales, W_UV and W_o,
+    the router, the shared expert and each distinct routed expert's weights+scales,
+    plus queries and the top-k list."""
+    ic, mc, ec = cfg.indexer, cfg.mla, cfg.moe
+    keys = rows * ic.context * (ic.dim // 2 + ic.dim // 32)
+    idx_io = rows * ic.heads * ic.dim * 2 + rows * ic.heads * 2 + rows * ic.topk * 4
+    kv = rows * mc.topk * (mc.qk_dim + 4)
+    attn_w = mc.heads * mc.v_dim * mc.kv_lora * 2 + mc.hidden * mc.heads * mc.v_dim * 2
+    q = rows * mc.heads * mc.qk_dim * 2
+    router = ec.n_experts * ec.hidden * 2
+    shared = 3 * ec.hidden * ec.shared_inter * (1 + 4 / (128 * 128)) if ec.n_shared else 0
+    per_expert = 3 * ec.hidden * ec.inter * (0.5 + 1 / 32)
+    total = keys + idx_io + kv + attn_w + q + router + shared + distinct_experts * per_expert
+    return int(total)
+
+
+def cpu_baseline(layer, reps):
+    import torch
+
+    from refs import CpuLayer
+
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    t0 = time.perf_counter()
+    cl = CpuLayer(layer)
+    prep = time.perf_counter() - t0
+    cl.forward()  # warm-up
+    times = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        cl.forward()
+        times.append(time.perf_counter() - t)
+    med = statistics.median(times)
+    return {
+        "value": round(med * 1e6, 1),
+        "unit": "us/layer",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"1 warm-up + median of {reps} oracle forwards of one configs[4] layer at M=8 "
+                  f"(f64 index scores over 8 x 65536 keys); expert dequant {prep:.1f}s outside timing",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--rows", type=int, default=8)
+    ap.add_argument("--layers", type=int, default=4, help="distinct resident layers cycled")
+    ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU's share of the layer; --gpus {args.gpus} "
+              "is not supported (TP all-reduce omitted by design)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from sgl_amd_mono.k2 import config as C
+    from sgl_amd_mono.k2 import synth
+    from sgl_amd_mono.k2.ops import LayerOp
+
+    dev = torch.device("cuda:0")
+    cfg, rows = C.C5_LAYER, args.rows
+    layers, ops, outs, ids = [], [], [], []
+    for i in range(args.layers):
+        L = synth.make_layer(cfg, rows, seed=1000 + 17 * i, device=dev)
+        layers.append(L)
+        ops.append(LayerOp(cfg, L, rows, device=dev))
+        outs.append(torch.empty(rows, cfg.mla.hidden, dtype=torch.bfloat16, device=dev))
+        ids.append(torch.empty(rows, cfg.moe.top_k, dtype=torch.int32, device=dev))
+    torch.cuda.synchronize()
+    # realized routing of each layer (distinct experts it streams)
+    for op, o, t in zip(ops, outs, ids):
+        op(o, topk_ids=t)
+    torch.cuda.synchronize()
+    distinct = [int(torch.unique(t).numel()) for t in ids]
+    bytes_per_layer = statistics.mean(algorithmic_bytes(cfg, rows, d) for d in distinct)
+
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        for op, o in zip(ops, outs):  # one eager pass on the capture stream first
+            op(o)
+        stream.synchronize()
+        with torch.cuda.graph(g, stream=stream):
+            for op, o in zip(ops, outs):
+                op(o)
+    torch.cuda.synchronize()
+    per_replay = len(ops)
+    warm_replays = max(1, -(-args.warmup // per_replay))
+    replays = max(1, -(-args.steps // per_replay))
+    steps = replays * per_replay
+    with torch.cuda.stream(stream):
+        for _ in range(warm_replays):
+            g.replay()
+    torch.cuda.synchronize()
+    trials = []
+    for _ in range(5):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            start.record(stream)
+            for _ in range(replays):
+                g.replay()
+            end.record(stream)
+        torch.cuda.synchronize()
+        trials.append(start.elapsed_time(end) / steps)
+    ms = statistics.median(trials)
+    us = ms * 1000.0
+    gbs = bytes_per_layer / (us * 1e-6) / 1e9
+
+    result = {
+        "metric": METRIC,
+        "value": round(us, 2),
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warm_replays * per_replay,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "mxfp4+fp8 weights, bf16/fp8 MFMA, f32 accumulate",
+        "data": "synthetic (seeded random-init weights ~N(0,0.02), rows ~N(0,1), shuffled pages)",
+        "config": {
+            "workload": "configs[4] chained K2 layer: indexer 64x128 FP4 keys ctx 65536 top-2048 -> "
+                        "sparse MLA 16 heads 512+64 FP8 KV -> W_UV/W_o -> RMSNorm 1e-6 -> "
+                        "MXFP4 MoE 256 experts top-8 inter 256 + FP8 shared",
+            "rows": rows,
+            "distinct_layers_cycled": len(ops),
+            "parallelism": "1 GPU (TP reduce omitted)",
+        },
+        "tokens_per_s_per_layer": round(rows / (us * 1e-6), 1),
+        "trials_us": [round(t * 1000, 2) for t in trials],
+        "distinct_experts": distinct,
+        "algorithmic_bytes_per_layer": int(bytes_per_layer),
+        "hbm_gbps": round(gbs, 1),
+        "pct_peak_hbm": round(100.0 * gbs / PEAK_HBM_GBS, 2),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "k2 layer (stage kernels replayed from one graph)",
+            "achieved": round(gbs, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(gbs / PEAK_HBM_GBS, 4),
+            "traffic": None,
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(layers[0], args.cpu_reps)
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

@@ -144,3 +144,31 @@ def check_layer(L, out, attn, scores, topk, logits, ids, wts, *, rel_l2=1e-2, sc
     assert e_out <= rel_l2, ("layer out", e_out)
     return {"score_err": worst, "attn_rel_l2": e_attn, "logit_err": e_logit, "out_rel_l2": e_out,
             "clear_rows": int(clear.sum())}
+
+
+class CpuLayer:
+    """The oracle's forward of one chained layer with every input already on the CPU
+    and every expert dequantized (the CPU baseline of bench.py)."""
+
+    def __init__(self, L):
+        from types import SimpleNamespace
+
+        self.cfg, self.rows = L.cfg, L.rows
+        self.idx = SimpleNamespace(**{k: cpu(v) if torch.is_tensor(v) else v for k, v in vars(L.idx).items()})
+        self.mla = SimpleNamespace(**{k: cpu(v) if torch.is_tensor(v) else v for k, v in vars(L.mla).items()})
+        self.h = cpu(L.h)
+        self.moe = MoEOracle(L.moe)
+        self.keys = [index_keys_f32(self.idx.cache, self.idx.page_table, int(self.idx.req_ids[r]),
+                                    int(self.idx.ctx_len[r])) for r in range(self.rows)]
+        self.moe.dequant_all()
+
+    def forward(self):
+        cfg = self.cfg
+        sel = torch.full((self.rows, cfg.indexer.topk), -1, dtype=torch.int64)
+        for r in range(self.rows):
+            s = R.index_scores(self.idx.q[r].float(), self.idx.w[r].float(), self.keys[r]).float()
+            lst = R.radix_lists(s, cfg.indexer.topk)
+            sel[r, : lst.numel()] = lst
+        _, attn = mla_oracle(self.mla, sel=sel, h=self.h)
+        out, *_ = self.moe(attn, norm=True, residual=True, eps=cfg.eps)
+        return out

@@ -8,13 +8,13 @@ namespace mk2 {
 constexpr int IDX_NT = 512;
 
 __global__ __launch_bounds__(IDX_NT) void k_idx_score(IdxDev p) {
-  idx_score<IDX_NT>(p, blockIdx.y, blockIdx.x);
+  __shared__ int pages[IDX_CHUNK / 64];
+  idx_score<IDX_NT>(p, blockIdx.y, blockIdx.x, pages);
 }
 
 __global__ __launch_bounds__(TOPK_NT) void k_idx_topk(IdxDev p) {
-  __shared__ int hist[4096];
-  __shared__ int scratch[TOPK_NT + TOPK_NT / 64 + 8];
-  idx_topk<TOPK_NT>(p, blockIdx.x, hist, scratch);
+  __shared__ TopkLds S;
+  idx_topk<TOPK_NT>(p, blockIdx.x, S);
 }
 
 int idx_check_shape(const mk2_indexer_shape* s) {

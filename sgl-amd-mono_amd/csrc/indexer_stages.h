@@ -9,10 +9,10 @@
 // for one key, then two cross-row shuffles finish it.
 //
 // top-k: one workgroup of 1024 threads a row, 64 consecutive positions a thread in
-// registers.  Three LDS histogram passes (12, 12, 8 bits of the radix key) find the
-// k-th key T exactly; the list is written in the radix select's order -- keys whose
-// top 12 bits exceed T's, then keys sharing T's top 12 bits that exceed T, then keys
-// equal to T (lowest positions first) -- each group in position order.
+// registers.  LDS histogram passes over at most 12 bits at a time of (key - row min)
+// find the k-th key T exactly; the list is written in the radix select's order --
+// keys whose top 12 bits exceed T's, then keys sharing T's top 12 bits that exceed
+// T, then keys equal to T (lowest positions first) -- each group in position order.
 #pragma once
 #include "mk2_device.h"
 
@@ -37,14 +37,42 @@ struct IdxDev {
 };
 
 // ------------------------------------------------------------- stage: scores
+// One task: IDX_CHUNK positions of row r; each wave owns 16 groups of 16 keys and
+// issues all of their loads before the first MFMA.
+// lds: IDX_CHUNK / 64 ints (the chunk's physical pages)
 template <int NT>
-MK2_DEV void idx_score(const IdxDev& p, int r, int chunk) {
+MK2_DEV void idx_score(const IdxDev& p, int r, int chunk, int* lds_pages) {
   constexpr int NW = NT / 64;
+  constexpr int GPW = IDX_CHUNK / 16 / NW;  // 16-key groups a wave
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, c16 = lane & 15;
   const int n = p.ctx[r];
   const int k_begin = chunk * IDX_CHUNK;
   if (k_begin >= n) return;
   const int k_end = min(n, k_begin + IDX_CHUNK);
+  const int ngroups = (k_end - k_begin + 15) >> 4;
+  // the chunk's page ids first, through LDS: every key load below then issues
+  // without waiting on another vector-memory load
+  if (threadIdx.x < IDX_CHUNK / 64) {
+    const int pg = (k_begin >> 6) + threadIdx.x;
+    lds_pages[threadIdx.x] = pg * 64 < k_end ? p.pt[(size_t)p.req[r] * p.stride + pg] : 0;
+  }
+  __syncthreads();
+  const int gw0 = wave * GPW;  // this wave's first group
+  uint4 code[GPW];
+  uint32_t sw[GPW];
+#pragma unroll
+  for (int j = 0; j < GPW; ++j) {
+    const int key0 = k_begin + (gw0 + j) * 16;
+    if (gw0 + j < ngroups) {
+      const uint8_t* pg = p.cache + (size_t)lds_pages[(key0 - k_begin) >> 6] * IDX_PAGE_BYTES;
+      const int tok = (key0 & 63) + c16;
+      code[j] = *(const uint4*)(pg + tok * 64 + 16 * g);
+      sw[j] = *(const uint32_t*)(pg + 4096 + tok * 4);
+    } else {
+      code[j] = make_uint4(0, 0, 0, 0);
+      sw[j] = 0x7F7F7F7Fu;
+    }
+  }
   const int nhg = p.heads >> 4;
   // A operands: q of head 16*hg + c16, dims 32g + 8s .. +7; head weights of rows 4g+i
   bf16x8 qa[4][4];
@@ -55,8 +83,11 @@ MK2_DEV void idx_score(const IdxDev& p, int r, int chunk) {
       const bf16_t* qr = p.q + ((size_t)r * p.heads + hg * 16 + c16) * 128 + 32 * g;
 #pragma unroll
       for (int s = 0; s < 4; ++s) qa[hg][s] = __builtin_bit_cast(bf16x8, *(const uint4*)(qr + 8 * s));
-#pragma unroll
-      for (int i = 0; i < 4; ++i) wt[hg][i] = bf16_to_f32(p.w[(size_t)r * p.heads + hg * 16 + 4 * g + i]);
+      const uint2 wv = *(const uint2*)(p.w + (size_t)r * p.heads + hg * 16 + 4 * g);
+      wt[hg][0] = __uint_as_float(wv.x << 16);
+      wt[hg][1] = __uint_as_float(wv.x & 0xFFFF0000u);
+      wt[hg][2] = __uint_as_float(wv.y << 16);
+      wt[hg][3] = __uint_as_float(wv.y & 0xFFFF0000u);
     } else {
 #pragma unroll
       for (int s = 0; s < 4; ++s) qa[hg][s] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
@@ -64,52 +95,32 @@ MK2_DEV void idx_score(const IdxDev& p, int r, int chunk) {
       for (int i = 0; i < 4; ++i) wt[hg][i] = 0.f;
     }
   }
-  const int* ptr = p.pt + (size_t)p.req[r] * p.stride;
   float* srow = p.scores + (size_t)r * p.max_ctx;
-  constexpr int U = 4;  // 16-key groups in flight a wave
-  const int ngroups = (k_end - k_begin + 15) >> 4;
-  for (int g0 = wave * U; g0 < ngroups; g0 += NW * U) {
-    uint4 code[U];
-    uint32_t sw[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int key0 = k_begin + (g0 + u) * 16;
-      if (g0 + u < ngroups) {
-        const int page = ptr[key0 >> 6];
-        const uint8_t* pg = p.cache + (size_t)page * IDX_PAGE_BYTES;
-        const int tok = (key0 & 63) + c16;
-        code[u] = *(const uint4*)(pg + tok * 64 + 16 * g);
-        sw[u] = *(const uint32_t*)(pg + 4096 + tok * 4);
-      } else {
-        code[u] = make_uint4(0, 0, 0, 0);
-        sw[u] = 0x7F7F7F7Fu;
-      }
+  for (int j = 0; j < GPW; ++j) {
+    if (gw0 + j >= ngroups) break;
+    const float sc = e8m0_to_f32(sw[j] >> (8 * g));
+    bf16x8 kb[4];
+    kb[0] = e2m1x8_to_bf16(code[j].x, sc);
+    kb[1] = e2m1x8_to_bf16(code[j].y, sc);
+    kb[2] = e2m1x8_to_bf16(code[j].z, sc);
+    kb[3] = e2m1x8_to_bf16(code[j].w, sc);
+    float s = 0.f;
+#pragma unroll
+    for (int hg = 0; hg < 4; ++hg) {
+      if (hg >= nhg) break;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc = mfma_bf16(qa[hg][q], kb[q], acc);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s += fmaxf(acc[i], 0.f) * wt[hg][i];
     }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (g0 + u >= ngroups) break;
-      const float sc = e8m0_to_f32(sw[u] >> (8 * g));
-      bf16x8 kb[4];
-      kb[0] = e2m1x8_to_bf16(code[u].x, sc);
-      kb[1] = e2m1x8_to_bf16(code[u].y, sc);
-      kb[2] = e2m1x8_to_bf16(code[u].z, sc);
-      kb[3] = e2m1x8_to_bf16(code[u].w, sc);
-      float s = 0.f;
-#pragma unroll
-      for (int hg = 0; hg < 4; ++hg) {
-        if (hg >= nhg) break;
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) acc = mfma_bf16(qa[hg][q], kb[q], acc);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s += fmaxf(acc[i], 0.f) * wt[hg][i];
-      }
-      s += __shfl_xor(s, 16, 64);
-      s += __shfl_xor(s, 32, 64);
-      const int key = k_begin + (g0 + u) * 16 + c16;
-      if (g == 0 && key < k_end) srow[key] = s;
-    }
+    s += __shfl_xor(s, 16, 64);
+    s += __shfl_xor(s, 32, 64);
+    const int key = k_begin + (gw0 + j) * 16 + c16;
+    if (g == 0 && key < k_end) srow[key] = s;
   }
+  __syncthreads();
 }
 
 // ------------------------------------------------------------- stage: top-k
@@ -142,6 +153,21 @@ MK2_DEV Scan3 block_scan3(Scan3 v, Scan3* tot, int* lds /* 3 * NT/64 */) {
   return Scan3{before.a + inc.a - v.a, before.b + inc.b - v.b, before.c + inc.c - v.c};
 }
 
+template <int NT>
+MK2_DEV int block_sum_int(int v, int* lds) {
+  constexpr int NW = NT / 64;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  __syncthreads();
+  if (lane == 0) lds[wave] = v;
+  __syncthreads();
+  int t = 0;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) t += lds[w];
+  return t;
+}
+
 // The bin (of nbins, highest first) where the count from the top reaches `need`;
 // returns the bin and, through *above, the count of the bins above it.  Each thread
 // owns nbins / NT consecutive bins.
@@ -149,7 +175,7 @@ template <int NT>
 MK2_DEV int find_bin(const int* hist, int nbins, int need, int* above_out, int* lds) {
   constexpr int NW = NT / 64;
   const int tid = threadIdx.x, lane = tid & 63;
-  const int per = nbins / NT;  // 4 (4096 bins) or 0 (256 bins: threads < 256 own 1)
+  const int per = nbins / NT;  // nbins >= NT: NT-aligned runs; else threads < nbins own 1
   const int mine_n = per ? per : (tid < nbins ? 1 : 0);
   const int first = per ? tid * per : tid;
   int local = 0;
@@ -196,10 +222,129 @@ MK2_DEV int find_bin(const int* hist, int nbins, int need, int* above_out, int* 
   return b;
 }
 
-// One row; NT == TOPK_NT.  lds: hist[4096] + scratch[NT + NT/64 + 8]
-template <int NT>
-MK2_DEV void idx_topk(const IdxDev& p, int r, int* hist, int* scratch) {
+// Exact top-k over values held in registers, PER a thread, in position order over
+// (thread, i).  d[i] = key - kbase for the values taking part (d >= 1), 0 for the
+// rest; more than k values take part.  Radix select over at most 12 bits of d at a
+// time finds the k-th d; the list is written in the radix select's order: keys whose
+// top 12 bits exceed the k-th key's, then keys sharing those 12 bits that exceed it,
+// then keys equal to it (lowest positions first) -- each group in position order.
+template <int NT, int PER, typename Pos>
+MK2_DEV void select_emit(uint32_t (&d)[PER], Pos pos, uint32_t kbase, uint32_t dmax, int k,
+                         int* hist, int* scratch, int* orow) {
   const int tid = threadIdx.x;
+  int hib = dmax ? 32 - __clz(dmax) : 32;
+  uint32_t prefix = 0;
+  int need = k;
+  while (hib > 0) {
+    const int lob = hib > 12 ? hib - 12 : 0;
+    const int nb = 1 << (hib - lob);
+    __syncthreads();
+    for (int i = tid; i < nb; i += NT) hist[i] = 0;
+    __syncthreads();
+    {
+      int run_bin = -1, run_n = 0;
+      const uint32_t mask = (uint32_t)(nb - 1);
+      const uint32_t hmask = hib >= 32 ? 0u : ~((1u << hib) - 1u);  // bits above this digit
+      const uint32_t hpfx = hib >= 32 ? 0u : (prefix << hib);
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const uint32_t v = d[i];
+        if ((v & hmask) == hpfx) {
+          const int b = (int)((v >> lob) & mask);
+          if (b != run_bin) {
+            if (run_n) atomicAdd(&hist[run_bin], run_n);
+            run_bin = b;
+            run_n = 0;
+          }
+          ++run_n;
+        }
+      }
+      if (run_n) atomicAdd(&hist[run_bin], run_n);
+    }
+    __syncthreads();
+    int above;
+    const int b = find_bin<NT>(hist, nb, need, &above, scratch);
+    need -= above;
+    prefix = (prefix << (hib - lob)) | (uint32_t)b;
+    hib = lob;
+  }
+  const uint32_t T = prefix;     // the k-th d (>= 1)
+  const int above = k - need;    // values > T
+  const int ties_needed = need;  // values == T taken, lowest positions first
+  // the 12-bit groups are defined on the true keys d + kbase; d = 0 is in no group
+  Scan3 c = {0, 0, 0};
+  const uint32_t tb = (T + kbase) >> 20;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const uint32_t v = d[i];
+    const uint32_t hi = (v + kbase) >> 20;
+    c.a += v != 0u && hi > tb;
+    c.b += v != 0u && hi == tb && v > T;
+    c.c += v == T;
+  }
+  Scan3 tot;
+  Scan3 off = block_scan3<NT>(c, &tot, scratch);
+  int o1 = off.a, o2 = tot.a + off.b, r3 = off.c;
+  // an opaque copy: the group tests below are recomputed, not kept from the count
+  // loop (keeping 3 x PER lane masks alive across the scan overflows the SGPRs)
+#pragma unroll
+  for (int i = 0; i < PER; ++i) asm volatile("" : "+v"(d[i]));
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const uint32_t v = d[i];
+    const bool g1 = v != 0u && ((v + kbase) >> 20) > tb;
+    const bool g2 = !g1 && v > T;
+    const bool g3 = v == T;
+    const int dst = g1 ? o1 : (g2 ? o2 : ((g3 && r3 < ties_needed) ? above + r3 : -1));
+    o1 += g1;
+    o2 += g2;
+    r3 += g3;
+    if (dst >= 0) orow[dst] = pos(i);
+  }
+}
+
+constexpr int TOPK_CAP = 8192;              // candidates kept for the exact select
+constexpr int TOPK_CPT = TOPK_CAP / TOPK_NT;  // candidates a thread
+
+struct TopkLds {
+  int hist[4096];
+  int scratch[TOPK_NT + TOPK_NT / 64 + 8];
+  uint32_t ckey[TOPK_CAP];
+  uint16_t cpos[TOPK_CAP];
+};
+
+// The select over a whole row (when the sampled bound does not hold): the keys are
+// read again from the scores, in a function of its own so that the fast path does
+// not carry its registers.
+template <int NT>
+__device__ __attribute__((noinline)) void topk_whole_row(const IdxDev& p, int r, uint32_t kmin,
+                                                         uint32_t kmax, TopkLds& S) {
+  const int n = p.ctx[r];
+  const int base = threadIdx.x * TOPK_PER;
+  const int nvalid = max(0, min(TOPK_PER, n - base));
+  const float* srow = p.scores + (size_t)r * p.max_ctx;
+  uint32_t d[TOPK_PER];
+#pragma unroll
+  for (int q = 0; q < TOPK_PER / 4; ++q) {
+    uint4 v = nvalid > 0 ? *(const uint4*)(srow + base + 4 * q) : make_uint4(0, 0, 0, 0);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      d[4 * q + j] = 4 * q + j < nvalid ? radix_key(__uint_as_float(w[j])) - kmin + 1u : 0u;
+  }
+  select_emit<NT, TOPK_PER>(d, [&](int i) { return base + i; }, kmin - 1u, kmax - kmin + 1u, p.topk,
+                            S.hist, S.scratch, p.out + (size_t)r * p.topk);
+}
+
+// One row; NT == TOPK_NT, 64 consecutive positions a thread in registers.  A sample
+// (every 64th position) gives a lower bound L for the k-th key (about twice k's share
+// of the sample above it, located to 24 bits with two histograms); the keys >= L
+// (checked: at least k, at most TOPK_CAP) are compacted in position order into LDS
+// and the exact select runs over them.  Otherwise the select runs over the whole row.
+template <int NT>
+MK2_DEV void idx_topk(const IdxDev& p, int r, TopkLds& S) {
+  constexpr int NW = NT / 64;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = p.ctx[r];
   const int k = p.topk;
   int* orow = p.out + (size_t)r * k;
@@ -224,106 +369,79 @@ MK2_DEV void idx_topk(const IdxDev& p, int r, int* hist, int* scratch) {
 #pragma unroll
     for (int i = 0; i < TOPK_PER; ++i) key[i] = 0u;
   }
-  // ---- pass 1: top 12 bits
-  for (int i = tid; i < 4096; i += NT) hist[i] = 0;
-  __syncthreads();
-  {
-    int run_bin = -1, run_n = 0;
-#pragma unroll
-    for (int i = 0; i < TOPK_PER; ++i) {
-      if (i < nvalid) {
-        const int b = (int)(key[i] >> 20);
-        if (b != run_bin) {
-          if (run_n) atomicAdd(&hist[run_bin], run_n);
-          run_bin = b;
-          run_n = 0;
-        }
-        ++run_n;
-      }
-    }
-    if (run_n) atomicAdd(&hist[run_bin], run_n);
-  }
-  __syncthreads();
-  int a1;
-  const int b1 = find_bin<NT>(hist, 4096, k, &a1, scratch);
-  // ---- pass 2: next 12 bits among keys with prefix b1
-  for (int i = tid; i < 4096; i += NT) hist[i] = 0;
-  __syncthreads();
-  {
-    int run_bin = -1, run_n = 0;
-#pragma unroll
-    for (int i = 0; i < TOPK_PER; ++i) {
-      if (i < nvalid && (int)(key[i] >> 20) == b1) {
-        const int b = (int)((key[i] >> 8) & 0xFFFu);
-        if (b != run_bin) {
-          if (run_n) atomicAdd(&hist[run_bin], run_n);
-          run_bin = b;
-          run_n = 0;
-        }
-        ++run_n;
-      }
-    }
-    if (run_n) atomicAdd(&hist[run_bin], run_n);
-  }
-  __syncthreads();
-  int a2;
-  const int b2 = find_bin<NT>(hist, 4096, k - a1, &a2, scratch);
-  const uint32_t pre24 = ((uint32_t)b1 << 12) | (uint32_t)b2;
-  // ---- pass 3: last 8 bits among keys with prefix (b1, b2)
-  for (int i = tid; i < 256; i += NT) hist[i] = 0;
-  __syncthreads();
-  {
-    int run_bin = -1, run_n = 0;
-#pragma unroll
-    for (int i = 0; i < TOPK_PER; ++i) {
-      if (i < nvalid && (key[i] >> 8) == pre24) {
-        const int b = (int)(key[i] & 0xFFu);
-        if (b != run_bin) {
-          if (run_n) atomicAdd(&hist[run_bin], run_n);
-          run_bin = b;
-          run_n = 0;
-        }
-        ++run_n;
-      }
-    }
-    if (run_n) atomicAdd(&hist[run_bin], run_n);
-  }
-  __syncthreads();
-  int a3;
-  const int b3 = find_bin<NT>(hist, 256, k - a1 - a2, &a3, scratch);
-  const uint32_t T = (pre24 << 8) | (uint32_t)b3;
-  const int above = a1 + a2 + a3;  // keys > T
-  const int ties_needed = k - above;
-  // ---- the list
-  Scan3 c = {0, 0, 0};
-  const uint32_t tb = T >> 20;
+  // row min / max
+  uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
 #pragma unroll
   for (int i = 0; i < TOPK_PER; ++i) {
     if (i < nvalid) {
-      const uint32_t kk = key[i];
-      c.a += (kk >> 20) > tb;
-      c.b += ((kk >> 20) == tb) && kk > T;
-      c.c += kk == T;
+      kmin = min(kmin, key[i]);
+      kmax = max(kmax, key[i]);
     }
   }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, o, 64));
+    kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o, 64));
+  }
+  __syncthreads();
+  if (lane == 0) { S.scratch[wave] = (int)kmin; S.scratch[NW + wave] = (int)kmax; }
+  for (int i = tid; i < 4096; i += NT) S.hist[i] = 0;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    kmin = min(kmin, (uint32_t)S.scratch[w]);
+    kmax = max(kmax, (uint32_t)S.scratch[NW + w]);
+  }
+  uint32_t L = kmin;
+  bool ok = true;
+  if (n > TOPK_CAP) {
+    const uint32_t smp = key[0];
+    const int nsamp = (n + TOPK_PER - 1) / TOPK_PER;
+    const int target = min(nsamp, (int)(2ll * k * nsamp / n) + 16);
+    if (nvalid > 0) atomicAdd(&S.hist[smp >> 20], 1);
+    __syncthreads();
+    int a1, a2;
+    const int b1 = find_bin<NT>(S.hist, 4096, target, &a1, S.scratch);
+    for (int i = tid; i < 4096; i += NT) S.hist[i] = 0;
+    __syncthreads();
+    if (nvalid > 0 && (int)(smp >> 20) == b1) atomicAdd(&S.hist[(smp >> 8) & 0xFFFu], 1);
+    __syncthreads();
+    const int b2 = find_bin<NT>(S.hist, 4096, target - a1, &a2, S.scratch);
+    L = max(kmin, ((uint32_t)b1 << 20) | ((uint32_t)b2 << 8));
+    int cnt = 0;
+#pragma unroll
+    for (int i = 0; i < TOPK_PER; ++i) cnt += (i < nvalid && key[i] >= L) ? 1 : 0;
+    cnt = block_sum_int<NT>(cnt, S.scratch);
+    ok = cnt >= k && cnt <= TOPK_CAP;
+  }
+  if (!ok) {
+    topk_whole_row<NT>(p, r, kmin, kmax, S);
+    return;
+  }
+  // compact the keys >= L (position order) into LDS
+  int mine = 0;
+#pragma unroll
+  for (int i = 0; i < TOPK_PER; ++i) mine += (i < nvalid && key[i] >= L) ? 1 : 0;
   Scan3 tot;
-  Scan3 off = block_scan3<NT>(c, &tot, scratch);
-  int o1 = off.a, o2 = a1 + off.b, r3 = off.c;
+  int at = block_scan3<NT>(Scan3{mine, 0, 0}, &tot, S.scratch).a;
 #pragma unroll
   for (int i = 0; i < TOPK_PER; ++i) {
-    if (i < nvalid) {
-      const uint32_t kk = key[i];
-      const int pos = base + i;
-      if ((kk >> 20) > tb) {
-        orow[o1++] = pos;
-      } else if (kk > T) {
-        orow[o2++] = pos;
-      } else if (kk == T) {
-        if (r3 < ties_needed) orow[above + r3] = pos;
-        ++r3;
-      }
+    if (i < nvalid && key[i] >= L) {
+      S.ckey[at] = key[i];
+      S.cpos[at] = (uint16_t)(base + i);
+      ++at;
     }
   }
+  const int cnt = tot.a;
+  __syncthreads();
+  uint32_t d[TOPK_CPT];
+#pragma unroll
+  for (int i = 0; i < TOPK_CPT; ++i) {
+    const int idx = tid * TOPK_CPT + i;
+    d[i] = idx < cnt ? S.ckey[idx] - L + 1u : 0u;
+  }
+  select_emit<NT, TOPK_CPT>(d, [&](int i) { return (int)S.cpos[tid * TOPK_CPT + i]; }, L - 1u,
+                            kmax - L + 1u, k, S.hist, S.scratch, orow);
 }
 
 }  // namespace mk2

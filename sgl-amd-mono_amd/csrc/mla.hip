@@ -9,7 +9,10 @@ __global__ __launch_bounds__(MLA_NT) void k_mla_split(MlaDev p) {
   __shared__ MlaSplitLds L;
   mla_split(p, blockIdx.y, blockIdx.x, L);
 }
-__global__ __launch_bounds__(MLA_NT) void k_mla_merge(MlaDev p) { mla_merge(p, blockIdx.y, blockIdx.x); }
+__global__ __launch_bounds__(MLA_NT) void k_mla_merge(MlaDev p) {
+  extern __shared__ float lds[];
+  mla_merge(p, blockIdx.y, blockIdx.x, lds);
+}
 template <int NCG>
 __global__ __launch_bounds__(MLA_NT) void k_mla_uv(MlaDev p) {
   __shared__ float red[4 * NCG * 64 * 4];
@@ -64,7 +67,7 @@ int mla_fill(const mk2_mla_args* a, MlaDev* d) {
 
 void mla_enqueue(const MlaDev& d, hipStream_t st) {
   k_mla_split<<<dim3(d.nsplit, d.rows), MLA_NT, 0, st>>>(d);
-  k_mla_merge<<<dim3(MLA_HEADS, d.rows), MLA_NT, 0, st>>>(d);
+  k_mla_merge<<<dim3(MLA_HEADS, d.rows), MLA_NT, (2 * d.nsplit + 8) * sizeof(float), st>>>(d);
   if (d.rows > 16) {
     k_mla_uv<2><<<dim3(d.v_dim / 16, MLA_HEADS), MLA_NT, 0, st>>>(d);
     k_mla_oproj<2><<<d.hidden / 16, MLA_NT, 0, st>>>(d);

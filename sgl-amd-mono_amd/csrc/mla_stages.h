@@ -48,6 +48,7 @@ struct MlaSplitLds {
   uint8_t k[MLA_SPLIT * MLA_KROW];       // gathered rows, row-major
   uint8_t vt[MLA_LAT * MLA_VROW];        // latent dims transposed: [dim][key]
   bf16_t p[MLA_HEADS * (MLA_SPLIT + 8)]; // P' [head][key]
+  int row[MLA_SPLIT];                    // cache row of each key (-1: unused)
   float sc[MLA_SPLIT];                   // per-key scale * sm_scale
   float kscale[MLA_SPLIT];
   float red[4][MLA_HEADS];
@@ -63,46 +64,60 @@ MK2_DEV void mla_split(const MlaDev& p, int r, int s, MlaSplitLds& L) {
   const bf16_t* qr = p.q + ((size_t)r * MLA_HEADS + c16) * MLA_D + 8 * g;
 #pragma unroll
   for (int ks = 0; ks < 18; ++ks) qa[ks] = __builtin_bit_cast(bf16x8, *(const uint4*)(qr + 32 * ks));
-  // per-key scales
+  // resolve the 64 positions to cache rows (one dependent round), with their scales
   if (tid < MLA_SPLIT) {
     const int pos = selr[tid];
+    int row = -1;
     float ksc = 0.f;
-    if (pos >= 0) ksc = p.kv_scale[(size_t)ptr[pos >> 6] * 64 + (pos & 63)];
+    if (pos >= 0) {
+      row = ptr[pos >> 6] * 64 + (pos & 63);
+      ksc = p.kv_scale[row];
+    }
+    L.row[tid] = row;
     L.kscale[tid] = ksc;
-    L.sc[tid] = pos >= 0 ? ksc * p.sm_scale : 0.f;
+    L.sc[tid] = ksc * p.sm_scale;
   }
-  // gather: job = (4-key group kg, 16-byte dim chunk dc); 16 x 36 jobs
-  for (int job = tid; job < 16 * 36; job += MLA_NT) {
+  __syncthreads();
+  // gather: job = (4-key group kg, 16-byte dim chunk dc), 16 x 36 jobs; every load of
+  // a thread is issued before the first LDS store
+  constexpr int JOBS = 16 * 36, JPT = (JOBS + MLA_NT - 1) / MLA_NT;
+  uint4 v[JPT][4];
+#pragma unroll
+  for (int it = 0; it < JPT; ++it) {
+    const int job = tid + it * MLA_NT;
     const int kg = job / 36, dc = job % 36;
-    uint4 v[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int pos = selr[kg * 4 + j];
-      if (pos >= 0) {
-        const size_t row = (size_t)ptr[pos >> 6] * 64 + (pos & 63);
-        v[j] = *(const uint4*)(p.kv + row * MLA_D + dc * 16);
-      } else {
-        v[j] = make_uint4(0, 0, 0, 0);
-      }
+      const int row = job < JOBS ? L.row[kg * 4 + j] : -1;
+      v[it][j] = row >= 0 ? *(const uint4*)(p.kv + (size_t)row * MLA_D + dc * 16) : make_uint4(0, 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < JPT; ++it) {
+    const int job = tid + it * MLA_NT;
+    if (job >= JOBS) break;
+    const int kg = job / 36, dc = job % 36;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
       uint8_t* dst = L.k + (kg * 4 + j) * MLA_KROW + dc * 16;
-      *(uint2*)dst = make_uint2(v[j].x, v[j].y);
-      *(uint2*)(dst + 8) = make_uint2(v[j].z, v[j].w);
+      *(uint2*)dst = make_uint2(v[it][j].x, v[it][j].y);
+      *(uint2*)(dst + 8) = make_uint2(v[it][j].z, v[it][j].w);
     }
     if (dc < 32) {
       // transpose 4 keys x 16 dims of bytes -> 16 words of 4 keys
-      uint32_t w[4][4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) { w[j][0] = v[j].x; w[j][1] = v[j].y; w[j][2] = v[j].z; w[j][3] = v[j].w; }
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          const uint32_t sh = 8 * b;
-          const uint32_t word = ((w[0][q] >> sh) & 0xFF) | (((w[1][q] >> sh) & 0xFF) << 8) |
-                                (((w[2][q] >> sh) & 0xFF) << 16) | (((w[3][q] >> sh) & 0xFF) << 24);
-          const int d = dc * 16 + q * 4 + b;
-          *(uint32_t*)(L.vt + d * MLA_VROW + kg * 4) = word;
-        }
+        const uint32_t w0 = ((const uint32_t*)&v[it][0])[q], w1 = ((const uint32_t*)&v[it][1])[q];
+        const uint32_t w2 = ((const uint32_t*)&v[it][2])[q], w3 = ((const uint32_t*)&v[it][3])[q];
+        const uint32_t lo01 = __builtin_amdgcn_perm(w1, w0, 0x05010400u);  // b0 of w0,w1 | b1 of w0,w1
+        const uint32_t hi01 = __builtin_amdgcn_perm(w1, w0, 0x07030602u);  // b2.. | b3..
+        const uint32_t lo23 = __builtin_amdgcn_perm(w3, w2, 0x05010400u);
+        const uint32_t hi23 = __builtin_amdgcn_perm(w3, w2, 0x07030602u);
+        const int d = dc * 16 + q * 4;
+        *(uint32_t*)(L.vt + (d + 0) * MLA_VROW + kg * 4) = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
+        *(uint32_t*)(L.vt + (d + 1) * MLA_VROW + kg * 4) = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);
+        *(uint32_t*)(L.vt + (d + 2) * MLA_VROW + kg * 4) = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
+        *(uint32_t*)(L.vt + (d + 3) * MLA_VROW + kg * 4) = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
       }
     }
   }
@@ -116,7 +131,7 @@ MK2_DEV void mla_split(const MlaDev& p, int r, int s, MlaSplitLds& L) {
     acc = mfma_bf16(qa[ks], e4m3x8_to_bf16(kw.x, kw.y), acc);
   }
   const int key = wave * 16 + c16;
-  const bool valid = selr[key] >= 0;
+  const bool valid = L.row[key] >= 0;
   float sv[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) sv[i] = valid ? acc[i] * L.sc[key] : -INFINITY;
@@ -175,20 +190,40 @@ MK2_DEV void mla_split(const MlaDev& p, int r, int s, MlaSplitLds& L) {
 }
 
 // ---------------------------------------------------------------- stage: merge
-MK2_DEV void mla_merge(const MlaDev& p, int r, int h) {
+// lds: >= 2 * nsplit + 8 floats
+MK2_DEV void mla_merge(const MlaDev& p, int r, int h, float* lds) {
   const int tid = threadIdx.x;
+  const int ns = p.nsplit;
+  float* wgt = lds;          // [ns] exp(m_s - M)
+  float* lsum = lds + ns;    // [ns] l_s
+  const float* ml = p.part_ml + ((size_t)r * ns * MLA_HEADS + h) * 2;
+  for (int s = tid; s < ns; s += MLA_NT) {
+    const float2 v = *(const float2*)(ml + (size_t)s * MLA_HEADS * 2);
+    wgt[s] = v.x;
+    lsum[s] = v.y;
+  }
+  __syncthreads();
   float M = -INFINITY;
-  for (int s = 0; s < p.nsplit; ++s)
-    M = fmaxf(M, p.part_ml[(((size_t)r * p.nsplit + s) * MLA_HEADS + h) * 2]);
-  float Lsum = 0.f, o0 = 0.f, o1 = 0.f;
-  for (int s = 0; s < p.nsplit; ++s) {
-    const float* ml = p.part_ml + (((size_t)r * p.nsplit + s) * MLA_HEADS + h) * 2;
-    const float ms = ml[0];
-    const float wgt = ms == -INFINITY ? 0.f : expf(ms - M);
-    Lsum += ml[1] * wgt;
-    const float2 ov = *(const float2*)(p.part_o + (((size_t)r * p.nsplit + s) * MLA_HEADS + h) * MLA_LAT + 2 * tid);
-    o0 += ov.x * wgt;
-    o1 += ov.y * wgt;
+  for (int s = 0; s < ns; ++s) M = fmaxf(M, wgt[s]);
+  __syncthreads();
+  for (int s = tid; s < ns; s += MLA_NT) wgt[s] = wgt[s] == -INFINITY ? 0.f : expf(wgt[s] - M);
+  __syncthreads();
+  float Lsum = 0.f;
+  for (int s = 0; s < ns; ++s) Lsum += lsum[s] * wgt[s];
+  const float* po = p.part_o + ((size_t)r * ns * MLA_HEADS + h) * MLA_LAT + 2 * tid;
+  float o0 = 0.f, o1 = 0.f;
+  constexpr int U = 8;
+  for (int s0 = 0; s0 < ns; s0 += U) {
+    float2 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      v[u] = s0 + u < ns ? *(const float2*)(po + (size_t)(s0 + u) * MLA_HEADS * MLA_LAT) : make_float2(0.f, 0.f);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float w = s0 + u < ns ? wgt[s0 + u] : 0.f;
+      o0 += v[u].x * w;
+      o1 += v[u].y * w;
+    }
   }
   const float inv = Lsum > 0.f ? 1.0f / Lsum : 0.f;
   o0 *= inv;
@@ -196,6 +231,7 @@ MK2_DEV void mla_merge(const MlaDev& p, int r, int h) {
   const size_t at = ((size_t)r * MLA_HEADS + h) * MLA_LAT + 2 * tid;
   *(uint32_t*)(p.o_lat + at) = pack_bf16x2(o0, o1);
   if (p.o_lat_f32) *(float2*)(p.o_lat_f32 + at) = make_float2(o0, o1);
+  __syncthreads();
 }
 
 // ---------------------------------------------------------------- stage: W_UV

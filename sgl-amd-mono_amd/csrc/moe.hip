@@ -7,7 +7,7 @@
 namespace mk2 {
 
 constexpr int MOE_NT = 512;
-constexpr int ROUTE_NT = 256;
+constexpr int ROUTE_NT = 512;
 
 __global__ __launch_bounds__(256) void k_moe_prep(MoeDev p) {
   __shared__ float lds[8];
@@ -37,7 +37,8 @@ __global__ __launch_bounds__(MOE_NT) void k_moe_upgate(MoeDev p) {
 template <int NCG>
 __global__ __launch_bounds__(MOE_NT) void k_moe_down(MoeDev p) {
   __shared__ float red[(MOE_NT / 64) * NCG * 64 * 4];
-  moe_down<MOE_NT, NCG>(p, blockIdx.x, red);
+  __shared__ int act_ids[256];
+  moe_down<MOE_NT, NCG>(p, blockIdx.x, red, act_ids);
 }
 
 // ----------------------------------------------------------------- host side
@@ -50,8 +51,9 @@ int moe_check_shape(const mk2_moe_shape* s) {
   MK2_REQUIRE(s->top_k >= 1 && s->top_k <= 8, "moe: top_k must be in [1, 8], got %d", s->top_k);
   MK2_REQUIRE(s->router == MK2_ROUTER_SOFTMAX || s->router == MK2_ROUTER_SIGMOID_BIAS, "moe: unknown router %d", s->router);
   MK2_REQUIRE(s->expert_fmt == MK2_FMT_FP8 || s->expert_fmt == MK2_FMT_MXFP4, "moe: unknown expert format %d", s->expert_fmt);
-  const int iq = s->expert_fmt == MK2_FMT_FP8 ? 128 : 128;
-  MK2_REQUIRE(s->inter >= iq && s->inter % iq == 0 && s->inter <= 4096, "moe: inter must be a multiple of 128 in [128, 4096], got %d", s->inter);
+  const int imax = s->expert_fmt == MK2_FMT_FP8 ? 1024 : 4096;
+  MK2_REQUIRE(s->inter >= 128 && s->inter % 128 == 0 && s->inter <= imax,
+              "moe: inter must be a multiple of 128 in [128, %d] for this format, got %d", imax, s->inter);
   MK2_REQUIRE(s->n_shared == 0 || s->n_shared == 1, "moe: n_shared must be 0 or 1");
   if (s->n_shared)
     MK2_REQUIRE(s->shared_inter >= 128 && s->shared_inter % 128 == 0 && s->shared_inter <= 4096,
@@ -127,7 +129,7 @@ int moe_enqueue(const MoeDev& d, hipStream_t st) {
   k_moe_prep<<<d.M, 256, 0, st>>>(d);
   if (ncg == 1) k_moe_router<1><<<dim3(d.E / 16, d.KC), 256, 0, st>>>(d);
   else k_moe_router<2><<<dim3(d.E / 16, d.KC), 256, 0, st>>>(d);
-  const size_t route_lds = (size_t)d.M * d.E * 4 + (size_t)(d.E + 8) * 4;
+  const size_t route_lds = (size_t)d.M * d.E * 4 + (size_t)(d.E + 4 * (ROUTE_NT / 64) + 24 * (ROUTE_NT / 64)) * 4;
   k_moe_route<<<1, ROUTE_NT, route_lds, st>>>(d);
   const int up_tasks = d.Dmax * (d.I / 32) + d.n_shared * (d.SI / 32);
   if (ncg == 1) k_moe_upgate<1><<<up_tasks, MOE_NT, 0, st>>>(d);

@@ -217,84 +217,115 @@ MK2_DEV void moe_router(const MoeDev& p, int nt, int kc, float* red) {
 }
 
 // ------------------------------------------------------------- stage: route
-// One workgroup: logits = sum of the k-chunk partials (in order), per row the top-k
-// by (key desc, expert asc), the weights, the distinct-expert list and rw.
+// One workgroup: logits = the k-chunk partials summed in chunk order; one wave a row
+// finds the top-k by (key desc, expert asc) with a bitwise search for the k-th key
+// (ballot counts, no shuffles), ranks the picks, and computes their weights; then
+// the distinct-expert list (ascending) and the dense route-weight table rw.
+// lds_logits: M*E floats; lds_slot: E + 4*NW ints (+ 24 a wave of pick scratch).
 template <int NT>
-MK2_DEV void moe_route(const MoeDev& p, float* lds_logits /*[M*E]*/, int* lds_slot /*[E+NT/64]*/) {
+MK2_DEV void moe_route(const MoeDev& p, float* lds_logits, int* lds_slot) {
   constexpr int NW = NT / 64;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int ME = p.M * p.E;
-  for (int idx = tid; idx < ME; idx += NT) {
-    float v = 0.f;
-    for (int kc = 0; kc < p.KC; ++kc) v += p.logit_part[(size_t)kc * ME + idx];
-    lds_logits[idx] = v;
-    if (p.logits) p.logits[idx] = v;
+  for (int idx = tid * 4; idx < ME; idx += NT * 4) {
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int kc0 = 0; kc0 < p.KC; kc0 += 8) {
+      float4 t[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        t[u] = kc0 + u < p.KC ? *(const float4*)(p.logit_part + (size_t)(kc0 + u) * ME + idx)
+                              : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        v.x += t[u].x; v.y += t[u].y; v.z += t[u].z; v.w += t[u].w;
+      }
+    }
+    *(float4*)(lds_logits + idx) = v;
+    if (p.logits) *(float4*)(p.logits + idx) = v;
   }
   for (int e = tid; e < p.E; e += NT) lds_slot[e] = 0;
   __syncthreads();
   const int per = p.E / 64;  // experts a lane holds: e = lane + 64 * i
+  int* pick = lds_slot + p.E + 4 * NW + wave * 24;  // [8 keys][8 ids][8 values]
   for (int r = wave; r < p.M; r += NW) {
     uint32_t key[4] = {0u, 0u, 0u, 0u};
     float sv[4] = {0.f, 0.f, 0.f, 0.f};
-    bool taken[4] = {false, false, false, false};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       if (i >= per) break;
       const int e = lane + 64 * i;
       const float lg = lds_logits[r * p.E + e];
       if (p.router == MK2_ROUTER_SIGMOID_BIAS) {
-        const float s = 1.0f / (1.0f + expf(-lg));
-        sv[i] = s;
-        key[i] = radix_key(s + p.bias[e]);
+        const float sg = 1.0f / (1.0f + expf(-lg));
+        sv[i] = sg;
+        key[i] = radix_key(sg + p.bias[e]);
       } else {
         sv[i] = lg;
         key[i] = radix_key(lg);
       }
     }
-    float picked_v = 0.f;  // lane j < topk: the value of pick j
-    int picked_e = 0;
-    for (int k = 0; k < p.topk; ++k) {
-      // best of this lane: max key, then lowest expert id
-      uint64_t best = 0;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (i >= per || taken[i]) continue;
-        const uint64_t c = ((uint64_t)key[i] << 32) | (uint32_t)(0xFFFFu - (lane + 64 * i));
-        best = c > best ? c : best;
-      }
-      uint64_t m = best;
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) {
-        uint32_t lo = __shfl_xor((uint32_t)m, o, 64), hi = __shfl_xor((uint32_t)(m >> 32), o, 64);
-        uint64_t other = ((uint64_t)hi << 32) | lo;
-        m = other > m ? other : m;
-      }
-      const int e = 0xFFFF - (int)(m & 0xFFFFu);
-      const int ei = e >> 6;
-      const float mine_v = ei == 0 ? sv[0] : (ei == 1 ? sv[1] : (ei == 2 ? sv[2] : sv[3]));
-      const float val = __shfl(mine_v, e & 63, 64);
+    // the k-th largest key: the largest T with count(key >= T) >= topk
+    uint32_t T = 0u;
+    for (int bit = 31; bit >= 0; --bit) {
+      const uint32_t cand = T | (1u << bit);
+      int cnt = 0;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        if (e == lane + 64 * i) taken[i] = true;
-      if (lane == k) { picked_v = val; picked_e = e; }
+        if (i < per) cnt += __popcll(__ballot(key[i] >= cand));
+      if (cnt >= p.topk) T = cand;
     }
-    // weights of the picks (lanes < topk)
-    float w = 0.f;
+    int n_gt = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (i < per) n_gt += __popcll(__ballot(key[i] > T));
+    const int ties = p.topk - n_gt;  // keys == T taken in expert order
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    int tie_before = 0, sel_before = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (i >= per) break;
+      const uint64_t tm = __ballot(key[i] == T);
+      const bool is_tie = key[i] == T;
+      const int tie_rank = tie_before + __popcll(tm & below);
+      const bool sel = key[i] > T || (is_tie && tie_rank < ties);
+      const uint64_t sm = __ballot(sel);
+      if (sel) {  // compacted in expert order
+        const int at = sel_before + __popcll(sm & below);
+        pick[at] = (int)key[i];
+        pick[8 + at] = lane + 64 * i;
+        pick[16 + at] = __float_as_int(sv[i]);
+      }
+      tie_before += __popcll(tm);
+      sel_before += __popcll(sm);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    float v = 0.f;
+    int e = 0, rank = 0;
+    if (lane < p.topk) {
+      const uint32_t kj = (uint32_t)pick[lane];
+      e = pick[8 + lane];
+      v = __int_as_float(pick[16 + lane]);
+      for (int j = 0; j < p.topk; ++j) {
+        const uint32_t ko = (uint32_t)pick[j];
+        rank += (ko > kj) || (ko == kj && pick[8 + j] < e);
+      }
+    }
+    float w;
     if (p.router == MK2_ROUTER_SIGMOID_BIAS) {
-      float tot = lane < p.topk ? picked_v : 0.f;
-      tot = wave_sum(tot);
-      w = picked_v / tot * p.route_scale;
+      const float tot = wave_sum(lane < p.topk ? v : 0.f);
+      w = v / tot * p.route_scale;
     } else {
-      const float top = __shfl(picked_v, 0, 64);
-      float ex = lane < p.topk ? expf(picked_v - top) : 0.f;
-      const float tot = wave_sum(ex);
-      w = ex / tot;
+      const float top = wave_max(lane < p.topk ? v : -INFINITY);
+      const float ex = lane < p.topk ? expf(v - top) : 0.f;
+      w = ex / wave_sum(ex);
     }
     if (lane < p.topk) {
-      p.topk_ids[r * p.topk + lane] = picked_e;
-      p.topk_w[r * p.topk + lane] = w;
-      lds_slot[picked_e] = 1;
+      p.topk_ids[r * p.topk + rank] = e;
+      p.topk_w[r * p.topk + rank] = w;
+      lds_slot[e] = 1;
     }
+    __builtin_amdgcn_wave_barrier();
   }
   __syncthreads();
   // distinct experts, ascending: exclusive scan of the flags
@@ -343,6 +374,8 @@ MK2_DEV void moe_route(const MoeDev& p, float* lds_logits /*[M*E]*/, int* lds_sl
 // ------------------------------------------------------- stage: up/gate + SwiGLU
 // task t < Dmax * I/32: routed slot j = t / (I/32), 32-row chunk c; past that the
 // shared expert's chunks.  mid = silu(gate) * up for the chunk's 32 rows x all rows.
+// Each wave owns every NW-th 128-k block and issues the weight loads of a whole
+// batch of its blocks before the first MFMA.
 template <int NT, int NCG>
 MK2_DEV void moe_upgate(const MoeDev& p, int t, float* red, float* midf) {
   constexpr int NW = NT / 64;
@@ -362,7 +395,7 @@ MK2_DEV void moe_upgate(const MoeDev& p, int t, float* red, float* midf) {
   }
   const int I = shared ? p.SI : p.I;
   const int NT16 = 2 * I / 16;  // 16-row tiles of the stacked gate|up
-  int nts[4] = {2 * c, 2 * c + 1, I / 16 + 2 * c, I / 16 + 2 * c + 1};
+  const int nts[4] = {2 * c, 2 * c + 1, I / 16 + 2 * c, I / 16 + 2 * c + 1};
   f32x4 acc[4][NCG];
 #pragma unroll
   for (int q = 0; q < 4; ++q)
@@ -370,46 +403,83 @@ MK2_DEV void moe_upgate(const MoeDev& p, int t, float* red, float* midf) {
     for (int cg = 0; cg < NCG; ++cg) acc[q][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   if (!shared && p.fmt == MK2_FMT_MXFP4) {
+    constexpr int B = NCG == 1 ? 4 : 3;  // k-blocks a wave holds in flight
     const int G = (KB + 3) / 4;
     const uint8_t* wbase = p.w13 + (size_t)e * NT16 * KB * 1024;
     const uint8_t* sbase = p.s13 + (size_t)e * NT16 * G * 256;
-    for (int kb = wave; kb < KB; kb += NW) {
-      i32x8 a[4];
-      int sa[4];
+    for (int kb0 = wave; kb0 < KB; kb0 += NW * B) {
+      // every load of the batch (weights, scales, activations) before the first MFMA
+      i32x8 a[B][4], b[B][NCG];
+      int sa[B][4], sb[B][NCG];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        a[q] = load_a_fp4(wbase + ((size_t)nts[q] * KB + kb) * 1024, lane);
-        sa[q] = (int)(*(const uint32_t*)(sbase + (((size_t)nts[q] * G + kb / 4) * 64 + lane) * 4) >>
-                      (8 * (kb & 3)));
+      for (int u = 0; u < B; ++u) {
+        const int kb = kb0 + u * NW;
+        if (kb < KB) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            a[u][q] = load_a_fp4(wbase + ((size_t)nts[q] * KB + kb) * 1024, lane);
+            sa[u][q] = (int)(*(const uint32_t*)(sbase + (((size_t)nts[q] * G + kb / 4) * 64 + lane) * 4) >>
+                             (8 * (kb & 3)));
+          }
+#pragma unroll
+          for (int cg = 0; cg < NCG; ++cg) {
+            const int row = cg * 16 + (lane & 15);
+            b[u][cg] = load_b_fp8(p.xq, row, p.M, p.H, kb * 128, g);
+            sb[u][cg] = row < p.M ? p.xs[(size_t)row * (p.H / 32) + kb * 4 + g] : 127;
+          }
+        }
       }
 #pragma unroll
-      for (int cg = 0; cg < NCG; ++cg) {
-        const int row = cg * 16 + (lane & 15);
-        i32x8 b = load_b_fp8(p.xq, row, p.M, p.H, kb * 128, g);
-        const int sb = row < p.M ? p.xs[(size_t)row * (p.H / 32) + kb * 4 + g] : 127;
+      for (int u = 0; u < B; ++u) {
+        const int kb = kb0 + u * NW;
+        if (kb >= KB) break;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) acc[q][cg] = mfma_fp4_fp8<0, 0>(a[q], b, acc[q][cg], sa[q], sb);
+        for (int cg = 0; cg < NCG; ++cg)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            acc[q][cg] = mfma_fp4_fp8<0, 0>(a[u][q], b[u][cg], acc[q][cg], sa[u][q], sb[u][cg]);
       }
     }
   } else {
+    constexpr int B = NCG == 1 ? 3 : 2;
     const uint8_t* wbase = shared ? p.ws13 : p.w13 + (size_t)e * NT16 * KB * 2048;
     const float* sbase = shared ? p.ss13 : (const float*)p.s13 + (size_t)e * (2 * I / 128) * KB;
-    for (int kb = wave; kb < KB; kb += NW) {
-      bf16x8 a[4][4];
-      float sc[4];
+    for (int kb0 = wave; kb0 < KB; kb0 += NW * B) {
+      uint4 raw[B][4][2];
+      bf16x8 bx[B][NCG][4];
+      float sc[B][4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        load_a_fp8(wbase + ((size_t)nts[q] * KB + kb) * 2048, lane, a[q]);
-        sc[q] = sbase[(nts[q] * 16 / 128) * KB + kb];
+      for (int u = 0; u < B; ++u) {
+        const int kb = kb0 + u * NW;
+        if (kb < KB) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint4* tl = (const uint4*)(wbase + ((size_t)nts[q] * KB + kb) * 2048 + lane * 32);
+            raw[u][q][0] = tl[0];
+            raw[u][q][1] = tl[1];
+            sc[u][q] = sbase[(nts[q] * 16 / 128) * KB + kb];
+          }
+#pragma unroll
+          for (int cg = 0; cg < NCG; ++cg)
+            load_b_bf16(p.xn, cg * 16 + (lane & 15), p.M, p.H, kb * 128 + 32 * g, bx[u][cg]);
+        }
       }
 #pragma unroll
-      for (int cg = 0; cg < NCG; ++cg) {
-        bf16x8 b[4];
-        load_b_bf16(p.xn, cg * 16 + (lane & 15), p.M, p.H, kb * 128 + 32 * g, b);
+      for (int u = 0; u < B; ++u) {
+        const int kb = kb0 + u * NW;
+        if (kb >= KB) break;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          f32x4 tmp = mfma4_bf16(a[q], b, f32x4{0.f, 0.f, 0.f, 0.f});
-          acc[q][cg] += tmp * sc[q];
+        for (int cg = 0; cg < NCG; ++cg) {
+          const bf16x8* b = bx[u][cg];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            bf16x8 a[4];
+            a[0] = e4m3x8_to_bf16(raw[u][q][0].x, raw[u][q][0].y);
+            a[1] = e4m3x8_to_bf16(raw[u][q][0].z, raw[u][q][0].w);
+            a[2] = e4m3x8_to_bf16(raw[u][q][1].x, raw[u][q][1].y);
+            a[3] = e4m3x8_to_bf16(raw[u][q][1].z, raw[u][q][1].w);
+            acc[q][cg] += mfma4_bf16(a, b, f32x4{0.f, 0.f, 0.f, 0.f}) * sc[u][q];
+          }
         }
       }
     }
@@ -460,70 +530,123 @@ MK2_DEV void moe_upgate(const MoeDev& p, int t, float* red, float* midf) {
 
 // ---------------------------------------------------------- stage: down + combine
 // task nt: 16 hidden rows; every slot (shared, then the D routed experts) adds
-// rw * W_down[e] . mid into the rows' accumulators; out = bf16(y [+ x]).
+// rw * W_down[e] . mid into the rows' accumulators; out = bf16(y [+ x]).  Waves
+// take every NW-th slot, a batch of slots' weight tiles in flight at once.
+// act_ids: LDS >= E ints
 template <int NT, int NCG>
-MK2_DEV void moe_down(const MoeDev& p, int nt, float* red) {
+MK2_DEV void moe_down(const MoeDev& p, int nt, float* red, int* act_ids) {
   constexpr int NW = NT / 64;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, c16 = lane & 15;
   const int D = p.act[0];
-  const int slots = p.n_shared + D;
+  for (int j = threadIdx.x; j < D; j += NT) act_ids[j] = p.act[1 + j];
+  __syncthreads();
   const int HT = p.H / 16;
   f32x4 acc[NCG];
 #pragma unroll
   for (int cg = 0; cg < NCG; ++cg) acc[cg] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int sl = wave; sl < slots; sl += NW) {
-    if (sl < p.n_shared) {
-      const int KB2 = p.SI / 128;
-      for (int kb = 0; kb < KB2; ++kb) {
-        bf16x8 a[4];
-        load_a_fp8(p.ws2 + ((size_t)nt * KB2 + kb) * 2048, lane, a);
-        const float sc = p.ss2[(nt * 16 / 128) * KB2 + kb];
+  // the shared expert (FP8, bf16 mid): its k-blocks spread over the waves
+  if (p.n_shared) {
+    const int KB2 = p.SI / 128;
+    for (int kb = wave; kb < KB2; kb += NW) {
+      bf16x8 a[4];
+      load_a_fp8(p.ws2 + ((size_t)nt * KB2 + kb) * 2048, lane, a);
+      const float sc = p.ss2[(nt * 16 / 128) * KB2 + kb];
 #pragma unroll
-        for (int cg = 0; cg < NCG; ++cg) {
-          bf16x8 b[4];
-          load_b_bf16(p.mid_sh, cg * 16 + (lane & 15), p.M, p.SI, kb * 128 + 32 * g, b);
-          acc[cg] += mfma4_bf16(a, b, f32x4{0.f, 0.f, 0.f, 0.f}) * sc;
-        }
+      for (int cg = 0; cg < NCG; ++cg) {
+        bf16x8 b[4];
+        load_b_bf16(p.mid_sh, cg * 16 + c16, p.M, p.SI, kb * 128 + 32 * g, b);
+        acc[cg] += mfma4_bf16(a, b, f32x4{0.f, 0.f, 0.f, 0.f}) * sc;
       }
-      continue;
     }
-    const int j = sl - p.n_shared;
-    const int e = p.act[1 + j];
-    const int KB2 = p.I / 128;
-    if (p.fmt == MK2_FMT_MXFP4) {
-      const int G2 = (KB2 + 3) / 4;
-      const uint8_t* wbase = p.w2 + ((size_t)e * HT + nt) * KB2 * 1024;
-      const uint8_t* sbase = p.s2 + ((size_t)e * HT + nt) * G2 * 256;
-      f32x4 tmp[NCG];
+  }
+  const int KB2 = p.I / 128;
+  if (p.fmt == MK2_FMT_MXFP4) {
+    constexpr int B = NCG == 1 ? 4 : 2;  // slots in flight a wave
+    constexpr int KC = 2;                // k-blocks of a slot a pass
+    const int G2 = (KB2 + 3) / 4;
+    for (int j0 = wave; j0 < D; j0 += NW * B) {
+      f32x4 tmp[B][NCG];
 #pragma unroll
-      for (int cg = 0; cg < NCG; ++cg) tmp[cg] = f32x4{0.f, 0.f, 0.f, 0.f};
-      for (int kb = 0; kb < KB2; ++kb) {
-        i32x8 a = load_a_fp4(wbase + (size_t)kb * 1024, lane);
-        const int sa = (int)(*(const uint32_t*)(sbase + ((kb / 4) * 64 + lane) * 4) >> (8 * (kb & 3)));
+      for (int u = 0; u < B; ++u)
 #pragma unroll
-        for (int cg = 0; cg < NCG; ++cg) {
-          const int row = cg * 16 + (lane & 15);
-          i32x8 b = load_b_fp8(p.mid_q + (size_t)j * p.M * p.I, row, p.M, p.I, kb * 128, g);
-          const int sb = row < p.M ? p.mid_s[((size_t)j * p.M + row) * (p.I / 32) + kb * 4 + g] : 127;
-          tmp[cg] = mfma_fp4_fp8<0, 0>(a, b, tmp[cg], sa, sb);
+        for (int cg = 0; cg < NCG; ++cg) tmp[u][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int kb0 = 0; kb0 < KB2; kb0 += KC) {
+        i32x8 a[B][KC], bq[B][KC][NCG];
+        int sa[B], sbq[B][KC][NCG];
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+          const int j = j0 + u * NW;
+          if (j < D) {
+            const int e = act_ids[j];
+            const uint8_t* wb = p.w2 + ((size_t)e * HT + nt) * KB2 * 1024;
+#pragma unroll
+            for (int c = 0; c < KC; ++c) {
+              const int kb = kb0 + c;
+              if (kb < KB2) {
+                a[u][c] = load_a_fp4(wb + (size_t)kb * 1024, lane);
+#pragma unroll
+                for (int cg = 0; cg < NCG; ++cg) {
+                  const int row = cg * 16 + c16;
+                  bq[u][c][cg] = load_b_fp8(p.mid_q + (size_t)j * p.M * p.I, row, p.M, p.I, kb * 128, g);
+                  sbq[u][c][cg] = row < p.M ? p.mid_s[((size_t)j * p.M + row) * (p.I / 32) + kb * 4 + g] : 127;
+                }
+              }
+            }
+            sa[u] = (int)*(const uint32_t*)(p.s2 + ((((size_t)e * HT + nt) * G2 + kb0 / 4) * 64 + lane) * 4);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+          const int j = j0 + u * NW;
+          if (j >= D) break;
+#pragma unroll
+          for (int c = 0; c < KC; ++c) {
+            const int kb = kb0 + c;
+            if (kb >= KB2) break;
+            const int sak = sa[u] >> (8 * (kb & 3));
+#pragma unroll
+            for (int cg = 0; cg < NCG; ++cg)
+              tmp[u][cg] = mfma_fp4_fp8<0, 0>(a[u][c], bq[u][c][cg], tmp[u][cg], sak, sbq[u][c][cg]);
+          }
         }
       }
 #pragma unroll
-      for (int cg = 0; cg < NCG; ++cg) acc[cg] += tmp[cg] * p.rw[j * 32 + cg * 16 + (lane & 15)];
-    } else {
-      const uint8_t* wbase = p.w2 + ((size_t)e * HT + nt) * KB2 * 2048;
-      const float* sbase = (const float*)p.s2 + (size_t)e * (p.H / 128) * KB2;
-      for (int kb = 0; kb < KB2; ++kb) {
+      for (int u = 0; u < B; ++u) {
+        const int j = j0 + u * NW;
+        if (j >= D) break;
+#pragma unroll
+        for (int cg = 0; cg < NCG; ++cg) acc[cg] += tmp[u][cg] * p.rw[j * 32 + cg * 16 + c16];
+      }
+    }
+  } else {
+    constexpr int KMAX = 8;  // FP8 experts: inter <= 1024
+    for (int j = wave; j < D; j += NW) {
+      const int e = act_ids[j];
+      const uint8_t* wb = p.w2 + ((size_t)e * HT + nt) * KB2 * 2048;
+      const float* sbase = (const float*)p.s2 + (size_t)e * (p.H / 128) * KB2 + (nt * 16 / 128) * KB2;
+      uint4 raw[KMAX][2];
+#pragma unroll
+      for (int kb = 0; kb < KMAX; ++kb) {
+        if (kb < KB2) {
+          const uint4* tl = (const uint4*)(wb + (size_t)kb * 2048 + lane * 32);
+          raw[kb][0] = tl[0];
+          raw[kb][1] = tl[1];
+        }
+      }
+#pragma unroll
+      for (int kb = 0; kb < KMAX; ++kb) {
+        if (kb >= KB2) break;
         bf16x8 a[4];
-        load_a_fp8(wbase + (size_t)kb * 2048, lane, a);
-        const float sc = sbase[(nt * 16 / 128) * KB2 + kb];
+        a[0] = e4m3x8_to_bf16(raw[kb][0].x, raw[kb][0].y);
+        a[1] = e4m3x8_to_bf16(raw[kb][0].z, raw[kb][0].w);
+        a[2] = e4m3x8_to_bf16(raw[kb][1].x, raw[kb][1].y);
+        a[3] = e4m3x8_to_bf16(raw[kb][1].z, raw[kb][1].w);
+        const float sc = sbase[kb];
 #pragma unroll
         for (int cg = 0; cg < NCG; ++cg) {
           bf16x8 b[4];
-          load_b_bf16(p.mid_b + (size_t)j * p.M * p.I, cg * 16 + (lane & 15), p.M, p.I,
-                      kb * 128 + 32 * g, b);
-          acc[cg] += mfma4_bf16(a, b, f32x4{0.f, 0.f, 0.f, 0.f}) *
-                     (sc * p.rw[j * 32 + cg * 16 + (lane & 15)]);
+          load_b_bf16(p.mid_b + (size_t)j * p.M * p.I, cg * 16 + c16, p.M, p.I, kb * 128 + 32 * g, b);
+          acc[cg] += mfma4_bf16(a, b, f32x4{0.f, 0.f, 0.f, 0.f}) * (sc * p.rw[j * 32 + cg * 16 + c16]);
         }
       }
     }

@@ -1,0 +1,104 @@
+"""The C-ABI library on the CPU: it loads, exports every entry point include/mk2.h
+declares, its ctypes mirrors have the C layouts, and argument errors come back as
+codes with a message before anything reaches the GPU."""
+
+import ctypes
+import os
+import re
+import subprocess
+import tempfile
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mk2.h")
+
+
+def _declared():
+    src = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(mk2_\w+)\s*\(", src, re.M)))
+
+
+def _lib():
+    from sgl_amd_mono import _lib
+
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libmk2.so not built (run __graft_entry__.build())")
+    return _lib, _lib.lib()
+
+
+def test_every_declared_symbol_is_exported():
+    _l, L = _lib()
+    names = _declared()
+    assert len(names) >= 10
+    for n in names:
+        assert hasattr(L, n), n
+    assert L.mk2_abi_version() == 1
+
+
+def test_ctypes_layouts_match_the_header():
+    _l, _ = _lib()
+    prog = r'''
+#include <stdio.h>
+#include <stddef.h>
+#include "mk2.h"
+int main(void) {
+  printf("%zu %zu %zu %zu %zu %zu %zu %zu\n", sizeof(mk2_moe_shape), sizeof(mk2_moe_weights),
+         sizeof(mk2_moe_args), sizeof(mk2_indexer_shape), sizeof(mk2_indexer_args),
+         sizeof(mk2_mla_shape), sizeof(mk2_mla_args), sizeof(mk2_layer_args));
+  printf("%zu %zu %zu\n", offsetof(mk2_moe_args, logits), offsetof(mk2_mla_args, o_latent),
+         offsetof(mk2_layer_args, workspace_bytes));
+  return 0;
+}
+'''
+    with tempfile.TemporaryDirectory() as d:
+        c, exe = os.path.join(d, "t.c"), os.path.join(d, "t")
+        open(c, "w").write(prog)
+        subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), c, "-o", exe], check=True)
+        out = subprocess.run([exe], capture_output=True, text=True, check=True).stdout.split("\n")
+    sizes = [int(x) for x in out[0].split()]
+    offs = [int(x) for x in out[1].split()]
+    mine = [ctypes.sizeof(t) for t in (_l.MoeShape, _l.MoeWeights, _l.MoeArgs, _l.IndexerShape,
+                                       _l.IndexerArgs, _l.MlaShape, _l.MlaArgs, _l.LayerArgs)]
+    assert sizes == mine
+    assert offs == [_l.MoeArgs.logits.offset, _l.MlaArgs.o_latent.offset,
+                    _l.LayerArgs.workspace_bytes.offset]
+
+
+def _moe_shape(_l, **kw):
+    base = dict(rows=8, hidden=6144, n_experts=256, top_k=8, inter=256, router=1, expert_fmt=1,
+                n_shared=1, shared_inter=256, norm=0, residual=0, route_scale=2.5, eps=1e-6)
+    base.update(kw)
+    return _l.MoeShape(**base)
+
+
+def test_workspace_queries_and_shape_errors():
+    _l, L = _lib()
+    n = ctypes.c_size_t()
+    assert L.mk2_moe_workspace_bytes(ctypes.byref(_moe_shape(_l)), ctypes.byref(n)) == 0
+    assert n.value > 0
+    for bad in (dict(rows=0), dict(rows=33), dict(hidden=1000), dict(n_experts=100), dict(top_k=9),
+                dict(router=5), dict(expert_fmt=7), dict(inter=100)):
+        rc = L.mk2_moe_workspace_bytes(ctypes.byref(_moe_shape(_l, **bad)), ctypes.byref(n))
+        assert rc == _l.MK2_EINVAL, bad
+        assert L.mk2_last_error().decode().startswith("moe:"), bad
+    ish = _l.IndexerShape(8, 64, 128, 2048, 65536, 1024)
+    assert L.mk2_indexer_workspace_bytes(ctypes.byref(ish), ctypes.byref(n)) == 0
+    assert L.mk2_indexer_workspace_bytes(ctypes.byref(_l.IndexerShape(8, 64, 128, 2048, 131072, 2048)),
+                                         ctypes.byref(n)) == _l.MK2_EINVAL
+    msh = _l.MlaShape(8, 16, 512, 64, 128, 6144, 2048, 512, 576**-0.5)
+    assert L.mk2_mla_workspace_bytes(ctypes.byref(msh), ctypes.byref(n)) == 0
+    assert L.mk2_mla_workspace_bytes(ctypes.byref(_l.MlaShape(8, 8, 512, 64, 128, 6144, 2048, 512, 0.1)),
+                                     ctypes.byref(n)) == _l.MK2_EINVAL
+
+
+def test_launch_argument_errors_never_reach_the_device():
+    _l, L = _lib()
+    assert L.mk2_moe_launch(None, None) == _l.MK2_EINVAL
+    args = _l.MoeArgs(_moe_shape(_l), _l.MoeWeights(), None, None, None, 0, None, None, None)
+    assert L.mk2_moe_launch(ctypes.byref(args), None) == _l.MK2_EINVAL
+    assert "NULL" in L.mk2_last_error().decode()
+    assert L.mk2_sparse_mla_launch(None, None) == _l.MK2_EINVAL
+    assert L.mk2_indexer_topk_launch(None, None) == _l.MK2_EINVAL
+    assert L.mk2_layer_launch(None, None) == _l.MK2_EINVAL
+    assert L.mk2_selftest_mfma(9, None, None, None, None, None, None) == _l.MK2_EINVAL

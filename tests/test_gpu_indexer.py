@@ -39,6 +39,12 @@ def _run(cfg, rows, seed, ctx_len=None, mode="random"):
         ns.cache[:, 4096:] = scales.repeat(64)
     elif mode == "zeros":
         ns.cache[:, :4096] = 0
+    elif mode == "recent":  # the last 4096 positions of every row score 16x higher
+        for r in range(rows):
+            n = int(ns.ctx_len[r])
+            pages = ns.page_table[r, (n - 4096) // 64 : n // 64].long()
+            sc = ns.cache[pages, 4096:]
+            ns.cache[pages, 4096:] = (sc.int() + 4).clamp(max=254).to(torch.uint8)
     op = IndexerOp(cfg, rows, ns.page_table.shape[1], device=dev)
     scores, topk = op(ns.q, ns.w, ns.cache, ns.page_table, ns.req_ids, ns.ctx_len)
     torch.cuda.synchronize()
@@ -116,3 +122,15 @@ def test_indexer_zero_keys():
     assert bool((oc.radix_keys(scores) == (1 << 31)).all())  # +0.0 everywhere, never -0.0
     for r in range(2):
         assert torch.equal(topk[r], torch.arange(128))
+
+
+def test_indexer_recent_cluster():
+    """Top keys clustered at the end of the context (the reference's 'recent' cache,
+    check_topk.py:168-189): the sampled bound still holds and the list is exact."""
+    from sgl_amd_mono.k2 import config as C
+
+    cfg = C.IndexerConfig(heads=64, dim=128, topk=2048, context=65536)
+    ns, scores, topk = _run(cfg, 2, seed=46, mode="recent")
+    _check_rows(cfg, ns, scores, topk, expect_clear=False)
+    for r in range(2):
+        assert int((topk[r] >= 65536 - 4096).sum()) > 1500

@@ -20,7 +20,7 @@ SPECS = {
 }
 
 
-def _registry():
+def _registry_module():
     """SGLang's monokernel registry, its legacy location, or the local stand-in."""
     try:
         from sglang.kernels.plugin_kernels.amd import spec as reg  # type: ignore
@@ -34,6 +34,6 @@ def _registry():
 
 def register_specs() -> None:
     """The plugin entry point, which SGLang runs in every process."""
-    reg = _registry()
+    reg = _registry_module()
     for (architecture, model_type), path in SPECS.items():
         reg.register(backend=BACKEND, architecture=architecture, path=path, model_type=model_type)

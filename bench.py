@@ -1,5 +1,5 @@
 #!/usr/bin/env python3
-"""Benchmark of the K2 decode layer on one MI355X (M=8).
+"""Benchmark of the K2 decode layer on one MI355X (the chained layer at M=8 rows).
 
 A step is one launch of the chained layer (indexer scores -> exact top-2048 ->
 sparse MLA -> W_UV -> W_o + residual -> RMSNorm -> router top-8 -> MXFP4 routed +
@@ -30,7 +30,7 @@ METRIC = "us per fused decoder layer @8 decode rows, 1 GPU; % of peak HBM GB/s"
 
 
 def algorithmic_bytes(cfg, rows, distinct_experts):
-    """HBM bytes a layer must move at least once (SURVEY 8(d) accounting): index keys
+    """HBM bytes a layer must move at least once: index keys
     of every request, the gathered latent-KV rows with their scales, W_UV and W_o,
     the router, the shared expert and each distinct routed expert's weights+scales,
     plus queries and the top-k list."""
@@ -83,6 +83,7 @@ def main():
     ap.add_argument("--layers", type=int, default=4, help="distinct resident layers cycled")
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--staged", action="store_true", help="one kernel a stage instead of one launch")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU's share of the layer; --gpus {args.gpus} "
@@ -101,7 +102,7 @@ def main():
     for i in range(args.layers):
         L = synth.make_layer(cfg, rows, seed=1000 + 17 * i, device=dev)
         layers.append(L)
-        ops.append(LayerOp(cfg, L, rows, device=dev))
+        ops.append(LayerOp(cfg, L, rows, device=dev, staged=args.staged))
         outs.append(torch.empty(rows, cfg.mla.hidden, dtype=torch.bfloat16, device=dev))
         ids.append(torch.empty(rows, cfg.moe.top_k, dtype=torch.int32, device=dev))
     torch.cuda.synchronize()
@@ -175,7 +176,8 @@ def main():
         "pct_peak_hbm": round(100.0 * gbs / PEAK_HBM_GBS, 2),
         "roofline": {
             "bound": "hbm",
-            "kernel": "k2 layer (stage kernels replayed from one graph)",
+            "kernel": "k2 layer: " + ("11 stage kernels a layer" if args.staged else
+                                      "one persistent launch a layer (k_k2_layer)"),
             "achieved": round(gbs, 1),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",

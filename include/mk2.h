@@ -55,7 +55,7 @@ extern "C" {
 typedef void* mk2_stream_t; /* a hipStream_t */
 
 /* ---------------------------------------------------------------------- MoE
- * Weight layouts (see DESIGN.md "tile packing"): every weight matrix [N, K] is
+ * Weight layouts (tile packing): every weight matrix [N, K] is
  * stored as tiles [N/16][K/128][64 lanes][chunk] where lane l holds row l%16 and
  * k = 32*(l/16) .. +31 of the 128-k block; chunk = 64 B (bf16), 32 B (E4M3),
  * 16 B (E2M1).  MXFP4 E8M0 scales: [N/16][ceil(K/512)][64 lanes][4 B].
@@ -178,14 +178,22 @@ int mk2_sparse_mla_launch(const mk2_mla_args* args, mk2_stream_t stream);
  * indexer -> top-k -> sparse MLA -> o_proj + residual h -> RMSNorm(eps) -> MoE +
  * residual.  The three argument blocks are the ones above; their q/sel/out fields
  * that the chain produces itself are ignored.  out: bf16 [rows][hidden]. */
+#define MK2_LAYER_PERSISTENT 0 /* one persistent launch (default) */
+#define MK2_LAYER_STAGED 1     /* the same stages as one kernel each, stream-ordered */
+
 typedef struct mk2_layer_args {
   mk2_indexer_args indexer; /* scores/topk may be NULL (then kept in the workspace) */
   mk2_mla_args mla;         /* sel, out are ignored: the chain supplies them */
   mk2_moe_args moe;         /* x is ignored (the attention output); norm=1, residual=1 */
   void* attn_out;           /* optional bf16 [rows][hidden]: the residual after attention */
   void* out;
-  void* workspace;
+  void* workspace;          /* its first 512 bytes must be zero before the first
+                               persistent launch; every launch leaves them zero */
   size_t workspace_bytes;
+  int mode;                 /* MK2_LAYER_PERSISTENT or MK2_LAYER_STAGED */
+  int spin_limit;           /* persistent: polls a dependency wait may take before the
+                               launch gives up (0: default, about a second) */
+  int32_t* status;          /* optional device word: 0 ok, 1 a wait gave up */
 } mk2_layer_args;
 
 int mk2_layer_workspace_bytes(const mk2_layer_args* args, size_t* bytes);

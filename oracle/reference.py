@@ -195,7 +195,7 @@ def moe_block(x, logits_fn, route_fn, experts, shared, residual=None):
 
 # ------------------------------------------------------------------ K2 chained layer
 def k2_layer(h, indexer_scores_fn, topk, attention_fn, eps, gamma, moe_fn):
-    """The chained layer of BASELINE configs[4]: index scores -> exact top-k ->
+    """The chained decode layer: index scores -> exact top-k ->
     sparse MLA + W_UV + W_o + residual h -> RMSNorm(eps) -> MoE + residual.
     (glm53/gfx950/kernel.py:6-47 stage order; TP reduces omitted.)"""
     scores = indexer_scores_fn()

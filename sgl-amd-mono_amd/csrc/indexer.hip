@@ -1,4 +1,4 @@
-// Standalone indexer launch: FP4 key scores, then the exact
+// Standalone indexer launch (FP4 index keys, 64 heads x 128): key scores, then the exact
 // top-k of every row.
 #include "indexer_stages.h"
 #include "mk2_host.h"
@@ -25,8 +25,8 @@ int idx_check_shape(const mk2_indexer_shape* s) {
   MK2_REQUIRE(s->dim == 128, "indexer: dim must be 128, got %d", s->dim);
   MK2_REQUIRE(s->topk >= 64 && s->topk <= 4096 && s->topk % 64 == 0,
               "indexer: topk must be a multiple of 64 in [64, 4096], got %d", s->topk);
-  MK2_REQUIRE(s->max_ctx >= 64 && s->max_ctx <= TOPK_NT * TOPK_PER && s->max_ctx % 64 == 0,
-              "indexer: max_ctx must be a multiple of 64 in [64, %d], got %d", TOPK_NT * TOPK_PER, s->max_ctx);
+  MK2_REQUIRE(s->max_ctx >= 64 && s->max_ctx <= TOPK_MAXN && s->max_ctx % 64 == 0,
+              "indexer: max_ctx must be a multiple of 64 in [64, %d], got %d", TOPK_MAXN, s->max_ctx);
   MK2_REQUIRE(s->table_stride >= s->max_ctx / 64, "indexer: table_stride %d < max_ctx / 64", s->table_stride);
   return MK2_OK;
 }

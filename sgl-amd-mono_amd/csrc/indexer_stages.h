@@ -21,8 +21,7 @@ namespace mk2 {
 constexpr int IDX_PAGE = 64;
 constexpr int IDX_PAGE_BYTES = 64 * 64 + 64 * 4;  // codes, then E8M0
 constexpr int IDX_CHUNK = 2048;                    // positions a score task
-constexpr int TOPK_NT = 1024;
-constexpr int TOPK_PER = 64;                       // positions a thread
+constexpr int TOPK_NT = 1024;                      // top-k workgroup of the standalone launch
 
 struct IdxDev {
   int rows, heads, topk, max_ctx, stride;
@@ -303,12 +302,12 @@ MK2_DEV void select_emit(uint32_t (&d)[PER], Pos pos, uint32_t kbase, uint32_t d
   }
 }
 
-constexpr int TOPK_CAP = 8192;              // candidates kept for the exact select
-constexpr int TOPK_CPT = TOPK_CAP / TOPK_NT;  // candidates a thread
+constexpr int TOPK_CAP = 8192;   // candidates kept for the exact select
+constexpr int TOPK_MAXN = 65536; // positions a row (a thread holds TOPK_MAXN / NT)
 
 struct TopkLds {
   int hist[4096];
-  int scratch[TOPK_NT + TOPK_NT / 64 + 8];
+  int scratch[1024 + 1024 / 64 + 8];
   uint32_t ckey[TOPK_CAP];
   uint16_t cpos[TOPK_CAP];
 };
@@ -319,24 +318,25 @@ struct TopkLds {
 template <int NT>
 __device__ __attribute__((noinline)) void topk_whole_row(const IdxDev& p, int r, uint32_t kmin,
                                                          uint32_t kmax, TopkLds& S) {
+  constexpr int PER = TOPK_MAXN / NT;
   const int n = p.ctx[r];
-  const int base = threadIdx.x * TOPK_PER;
-  const int nvalid = max(0, min(TOPK_PER, n - base));
+  const int base = threadIdx.x * PER;
+  const int nvalid = max(0, min(PER, n - base));
   const float* srow = p.scores + (size_t)r * p.max_ctx;
-  uint32_t d[TOPK_PER];
+  uint32_t d[PER];
 #pragma unroll
-  for (int q = 0; q < TOPK_PER / 4; ++q) {
+  for (int q = 0; q < PER / 4; ++q) {
     uint4 v = nvalid > 0 ? *(const uint4*)(srow + base + 4 * q) : make_uint4(0, 0, 0, 0);
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       d[4 * q + j] = 4 * q + j < nvalid ? radix_key(__uint_as_float(w[j])) - kmin + 1u : 0u;
   }
-  select_emit<NT, TOPK_PER>(d, [&](int i) { return base + i; }, kmin - 1u, kmax - kmin + 1u, p.topk,
-                            S.hist, S.scratch, p.out + (size_t)r * p.topk);
+  select_emit<NT, PER>(d, [&](int i) { return base + i; }, kmin - 1u, kmax - kmin + 1u, p.topk,
+                       S.hist, S.scratch, p.out + (size_t)r * p.topk);
 }
 
-// One row; NT == TOPK_NT, 64 consecutive positions a thread in registers.  A sample
+// One row; NT threads, 65536 / NT consecutive positions a thread in registers.  A sample
 // (every 64th position) gives a lower bound L for the k-th key (about twice k's share
 // of the sample above it, located to 24 bits with two histograms); the keys >= L
 // (checked: at least k, at most TOPK_CAP) are compacted in position order into LDS
@@ -344,6 +344,9 @@ __device__ __attribute__((noinline)) void topk_whole_row(const IdxDev& p, int r,
 template <int NT>
 MK2_DEV void idx_topk(const IdxDev& p, int r, TopkLds& S) {
   constexpr int NW = NT / 64;
+  constexpr int TOPK_PER = TOPK_MAXN / NT;  // positions a thread
+  constexpr int TOPK_CPT = TOPK_CAP / NT;   // candidates a thread
+  constexpr int SPT = TOPK_PER / 64;        // samples a thread (one per 64 positions)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = p.ctx[r];
   const int k = p.topk;
@@ -395,16 +398,19 @@ MK2_DEV void idx_topk(const IdxDev& p, int r, TopkLds& S) {
   uint32_t L = kmin;
   bool ok = true;
   if (n > TOPK_CAP) {
-    const uint32_t smp = key[0];
-    const int nsamp = (n + TOPK_PER - 1) / TOPK_PER;
+    const int nsamp = (n + 63) / 64;  // positions 64j that exist
     const int target = min(nsamp, (int)(2ll * k * nsamp / n) + 16);
-    if (nvalid > 0) atomicAdd(&S.hist[smp >> 20], 1);
+#pragma unroll
+    for (int j = 0; j < SPT; ++j)
+      if (64 * j < nvalid) atomicAdd(&S.hist[key[64 * j] >> 20], 1);
     __syncthreads();
     int a1, a2;
     const int b1 = find_bin<NT>(S.hist, 4096, target, &a1, S.scratch);
     for (int i = tid; i < 4096; i += NT) S.hist[i] = 0;
     __syncthreads();
-    if (nvalid > 0 && (int)(smp >> 20) == b1) atomicAdd(&S.hist[(smp >> 8) & 0xFFFu], 1);
+#pragma unroll
+    for (int j = 0; j < SPT; ++j)
+      if (64 * j < nvalid && (int)(key[64 * j] >> 20) == b1) atomicAdd(&S.hist[(key[64 * j] >> 8) & 0xFFFu], 1);
     __syncthreads();
     const int b2 = find_bin<NT>(S.hist, 4096, target - a1, &a2, S.scratch);
     L = max(kmin, ((uint32_t)b1 << 20) | ((uint32_t)b2 << 8));

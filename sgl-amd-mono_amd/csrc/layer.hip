@@ -1,7 +1,6 @@
-// The chained K2 layer as a stream of stage kernels: indexer scores -> exact
-// top-k -> sparse MLA -> W_UV -> W_o + residual -> RMSNorm -> router -> top-k
-// routing -> up/gate -> down + residual.  (The single persistent launch is in
-// k2_persistent.hip; this path is its stage-by-stage twin.)
+// The chained K2 layer: indexer scores -> exact top-k -> sparse MLA -> W_UV -> W_o +
+// residual -> RMSNorm -> router -> top-k routing -> up/gate -> down + residual, as
+// one persistent launch (k2_persistent.hip) or as one kernel a stage.
 #include "indexer_stages.h"
 #include "mla_stages.h"
 #include "mk2_host.h"
@@ -18,11 +17,16 @@ void mla_enqueue(const MlaDev& d, hipStream_t st);
 int moe_fill(const mk2_moe_args* a, MoeDev* d);
 size_t moe_carve(const mk2_moe_shape* s, void* base, MoeDev* d);
 int moe_enqueue(const MoeDev& d, hipStream_t st);
+int k2_persistent_enqueue(const IdxDev& idx, const MlaDev& mla, const MoeDev& moe, int* sync,
+                          int* status, int rows, int spin_limit, hipStream_t st);
+
+constexpr int LAYER_SYNC_BYTES = 512;
 
 struct LayerPlan {
   IdxDev idx;
   MlaDev mla;
   MoeDev moe;
+  int* sync;
 };
 
 // validate the three blocks against each other and carve one workspace for all
@@ -47,7 +51,10 @@ int layer_plan(const mk2_layer_args* a, void* ws, LayerPlan* L, size_t* bytes) {
   ma.out = (void*)2;
   rc = moe_fill(&ma, &L->moe);
   if (rc) return rc;
+  MK2_REQUIRE(a->mode == MK2_LAYER_PERSISTENT || a->mode == MK2_LAYER_STAGED, "layer: unknown mode %d", a->mode);
+  MK2_REQUIRE(a->spin_limit >= 0, "layer: spin_limit must be >= 0");
   Carver c(ws);
+  int* sync = c.take<int>(LAYER_SYNC_BYTES / 4);
   const size_t b_idx = idx_carve(&is, nullptr, nullptr, nullptr);
   const size_t b_mla = mla_carve(&ms, nullptr, nullptr);
   const size_t b_moe = moe_carve(&es, nullptr, nullptr);
@@ -57,6 +64,7 @@ int layer_plan(const mk2_layer_args* a, void* ws, LayerPlan* L, size_t* bytes) {
   bf16_t* attn = c.take<bf16_t>((size_t)ms.rows * ms.hidden);
   *bytes = c.bytes();
   if (!ws) return MK2_OK;
+  L->sync = sync;
   float* sc;
   int* tk;
   idx_carve(&is, p_idx, &sc, &tk);
@@ -99,6 +107,9 @@ extern "C" int mk2_layer_launch(const mk2_layer_args* a, mk2_stream_t stream) {
   rc = layer_plan(a, a->workspace, &L, &need);
   if (rc) return rc;
   hipStream_t st = (hipStream_t)stream;
+  if (a->mode == MK2_LAYER_PERSISTENT)
+    return k2_persistent_enqueue(L.idx, L.mla, L.moe, L.sync, a->status, a->mla.shape.rows,
+                                 a->spin_limit ? a->spin_limit : (1 << 20), st);
   idx_enqueue(L.idx, st);
   mla_enqueue(L.mla, st);
   return moe_enqueue(L.moe, st);

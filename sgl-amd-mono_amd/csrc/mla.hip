@@ -1,4 +1,4 @@
-// Standalone sparse-MLA launch: split attention, merge,
+// Standalone sparse-MLA launch (16 heads, 512 + 64 latent dims): split attention, merge,
 // W_UV, W_o + residual.
 #include "mk2_host.h"
 #include "mla_stages.h"
@@ -7,21 +7,21 @@ namespace mk2 {
 
 __global__ __launch_bounds__(MLA_NT) void k_mla_split(MlaDev p) {
   __shared__ MlaSplitLds L;
-  mla_split(p, blockIdx.y, blockIdx.x, L);
+  mla_split<MLA_NT>(p, blockIdx.y, blockIdx.x, L);
 }
 __global__ __launch_bounds__(MLA_NT) void k_mla_merge(MlaDev p) {
   extern __shared__ float lds[];
-  mla_merge(p, blockIdx.y, blockIdx.x, lds);
+  mla_merge<MLA_NT>(p, blockIdx.y, blockIdx.x, lds);
 }
 template <int NCG>
 __global__ __launch_bounds__(MLA_NT) void k_mla_uv(MlaDev p) {
   __shared__ float red[4 * NCG * 64 * 4];
-  mla_uv<NCG>(p, blockIdx.y, blockIdx.x, red);
+  mla_uv<MLA_NT, NCG>(p, blockIdx.y, blockIdx.x, red);
 }
 template <int NCG>
 __global__ __launch_bounds__(MLA_NT) void k_mla_oproj(MlaDev p) {
   __shared__ float red[4 * NCG * 64 * 4];
-  mla_oproj<NCG>(p, blockIdx.x, red);
+  mla_oproj<MLA_NT, NCG>(p, blockIdx.x, red);
 }
 
 int mla_check_shape(const mk2_mla_shape* s) {

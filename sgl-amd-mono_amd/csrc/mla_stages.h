@@ -55,15 +55,22 @@ struct MlaSplitLds {
 };
 
 // ---------------------------------------------------------------- stage: split
+// NT = 256 or 512: waves 0-3 run QK and the softmax (16 keys each), every wave
+// gathers and takes a share of the PV dim tiles.
+template <int NT>
 MK2_DEV void mla_split(const MlaDev& p, int r, int s, MlaSplitLds& L) {
+  constexpr int NW = NT / 64;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, c16 = lane & 15;
+  const bool qk_wave = wave < 4;
   const int* selr = p.sel + (size_t)r * p.topk + s * MLA_SPLIT;
   const int* ptr = p.pt + (size_t)p.req[r] * p.stride;
   // q operands for this wave's QK: head c16, dims 8g + 32ks .. +7
   bf16x8 qa[18];
   const bf16_t* qr = p.q + ((size_t)r * MLA_HEADS + c16) * MLA_D + 8 * g;
+  if (qk_wave) {
 #pragma unroll
-  for (int ks = 0; ks < 18; ++ks) qa[ks] = __builtin_bit_cast(bf16x8, *(const uint4*)(qr + 32 * ks));
+    for (int ks = 0; ks < 18; ++ks) qa[ks] = __builtin_bit_cast(bf16x8, *(const uint4*)(qr + 32 * ks));
+  }
   // resolve the 64 positions to cache rows (one dependent round), with their scales
   if (tid < MLA_SPLIT) {
     const int pos = selr[tid];
@@ -80,11 +87,11 @@ MK2_DEV void mla_split(const MlaDev& p, int r, int s, MlaSplitLds& L) {
   __syncthreads();
   // gather: job = (4-key group kg, 16-byte dim chunk dc), 16 x 36 jobs; every load of
   // a thread is issued before the first LDS store
-  constexpr int JOBS = 16 * 36, JPT = (JOBS + MLA_NT - 1) / MLA_NT;
+  constexpr int JOBS = 16 * 36, JPT = (JOBS + NT - 1) / NT;
   uint4 v[JPT][4];
 #pragma unroll
   for (int it = 0; it < JPT; ++it) {
-    const int job = tid + it * MLA_NT;
+    const int job = tid + it * NT;
     const int kg = job / 36, dc = job % 36;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -94,7 +101,7 @@ MK2_DEV void mla_split(const MlaDev& p, int r, int s, MlaSplitLds& L) {
   }
 #pragma unroll
   for (int it = 0; it < JPT; ++it) {
-    const int job = tid + it * MLA_NT;
+    const int job = tid + it * NT;
     if (job >= JOBS) break;
     const int kg = job / 36, dc = job % 36;
 #pragma unroll
@@ -122,39 +129,41 @@ MK2_DEV void mla_split(const MlaDev& p, int r, int s, MlaSplitLds& L) {
     }
   }
   __syncthreads();
-  // QK: wave w takes keys 16w .. 16w+15 as the MFMA columns
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  const uint8_t* krow = L.k + (wave * 16 + c16) * MLA_KROW + 8 * g;
-#pragma unroll
-  for (int ks = 0; ks < 18; ++ks) {
-    const uint2 kw = *(const uint2*)(krow + 32 * ks);
-    acc = mfma_bf16(qa[ks], e4m3x8_to_bf16(kw.x, kw.y), acc);
-  }
-  const int key = wave * 16 + c16;
+  // QK: wave w < 4 takes keys 16w .. 16w+15 as the MFMA columns
+  const int key = (wave & 3) * 16 + c16;
   const bool valid = L.row[key] >= 0;
-  float sv[4];
+  float sv[4], m[4];
+  if (qk_wave) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    const uint8_t* krow = L.k + key * MLA_KROW + 8 * g;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) sv[i] = valid ? acc[i] * L.sc[key] : -INFINITY;
-  // split-local softmax per head (heads 4g + i)
-  float mx[4];
+    for (int ks = 0; ks < 18; ++ks) {
+      const uint2 kw = *(const uint2*)(krow + 32 * ks);
+      acc = mfma_bf16(qa[ks], e4m3x8_to_bf16(kw.x, kw.y), acc);
+    }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) mx[i] = row16_max(sv[i]);
-  if (c16 == 0) {
+    for (int i = 0; i < 4; ++i) sv[i] = valid ? acc[i] * L.sc[key] : -INFINITY;
+    // split-local softmax per head (heads 4g + i)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) L.red[wave][4 * g + i] = mx[i];
+    for (int i = 0; i < 4; ++i) {
+      const float mx = row16_max(sv[i]);
+      if (c16 == 0) L.red[wave][4 * g + i] = mx;
+    }
   }
   __syncthreads();
-  float m[4], pe[4], ls[4];
+  float ls[4];
+  if (qk_wave) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int hd = 4 * g + i;
-    m[i] = fmaxf(fmaxf(L.red[0][hd], L.red[1][hd]), fmaxf(L.red[2][hd], L.red[3][hd]));
-    pe[i] = (valid && m[i] != -INFINITY) ? expf(sv[i] - m[i]) : 0.f;
-    ls[i] = row16_sum(pe[i]);
-    L.p[hd * (MLA_SPLIT + 8) + key] = f32_to_bf16(pe[i] * L.kscale[key]);
+    for (int i = 0; i < 4; ++i) {
+      const int hd = 4 * g + i;
+      m[i] = fmaxf(fmaxf(L.red[0][hd], L.red[1][hd]), fmaxf(L.red[2][hd], L.red[3][hd]));
+      const float pe = (valid && m[i] != -INFINITY) ? expf(sv[i] - m[i]) : 0.f;
+      ls[i] = row16_sum(pe);
+      L.p[hd * (MLA_SPLIT + 8) + key] = f32_to_bf16(pe * L.kscale[key]);
+    }
   }
   __syncthreads();
-  if (c16 == 0) {
+  if (qk_wave && c16 == 0) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) L.red[wave][4 * g + i] = ls[i];
   }
@@ -168,15 +177,16 @@ MK2_DEV void mla_split(const MlaDev& p, int r, int s, MlaSplitLds& L) {
       mlo[hd * 2 + 1] = L.red[0][hd] + L.red[1][hd] + L.red[2][hd] + L.red[3][hd];
     }
   }
-  // PV: wave w takes dim tiles 8w .. 8w+7 (16 dims each), 2 key steps of 32
+  // PV: wave w takes dim tiles TPW*w .. +TPW-1 (16 dims each), 2 key steps of 32
+  constexpr int TPW = 32 / NW;
   bf16x8 pa[2];
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks)
     pa[ks] = __builtin_bit_cast(bf16x8, *(const uint4*)(L.p + c16 * (MLA_SPLIT + 8) + 32 * ks + 8 * g));
   float* orow = p.part_o + ((size_t)r * p.nsplit + s) * MLA_HEADS * MLA_LAT;
 #pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    const int d0 = (wave * 8 + t) * 16;
+  for (int t = 0; t < TPW; ++t) {
+    const int d0 = (wave * TPW + t) * 16;
     f32x4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
@@ -190,14 +200,16 @@ MK2_DEV void mla_split(const MlaDev& p, int r, int s, MlaSplitLds& L) {
 }
 
 // ---------------------------------------------------------------- stage: merge
-// lds: >= 2 * nsplit + 8 floats
+// lds: >= 2 * nsplit + 8 floats; a thread takes 512 / NT latent dims
+template <int NT>
 MK2_DEV void mla_merge(const MlaDev& p, int r, int h, float* lds) {
+  constexpr int DPT = MLA_LAT / NT;
   const int tid = threadIdx.x;
   const int ns = p.nsplit;
   float* wgt = lds;          // [ns] exp(m_s - M)
   float* lsum = lds + ns;    // [ns] l_s
   const float* ml = p.part_ml + ((size_t)r * ns * MLA_HEADS + h) * 2;
-  for (int s = tid; s < ns; s += MLA_NT) {
+  for (int s = tid; s < ns; s += NT) {
     const float2 v = *(const float2*)(ml + (size_t)s * MLA_HEADS * 2);
     wgt[s] = v.x;
     lsum[s] = v.y;
@@ -206,44 +218,53 @@ MK2_DEV void mla_merge(const MlaDev& p, int r, int h, float* lds) {
   float M = -INFINITY;
   for (int s = 0; s < ns; ++s) M = fmaxf(M, wgt[s]);
   __syncthreads();
-  for (int s = tid; s < ns; s += MLA_NT) wgt[s] = wgt[s] == -INFINITY ? 0.f : expf(wgt[s] - M);
+  for (int s = tid; s < ns; s += NT) wgt[s] = wgt[s] == -INFINITY ? 0.f : expf(wgt[s] - M);
   __syncthreads();
   float Lsum = 0.f;
   for (int s = 0; s < ns; ++s) Lsum += lsum[s] * wgt[s];
-  const float* po = p.part_o + ((size_t)r * ns * MLA_HEADS + h) * MLA_LAT + 2 * tid;
-  float o0 = 0.f, o1 = 0.f;
+  const float* po = p.part_o + ((size_t)r * ns * MLA_HEADS + h) * MLA_LAT + DPT * tid;
+  float o[DPT];
+#pragma unroll
+  for (int d = 0; d < DPT; ++d) o[d] = 0.f;
   constexpr int U = 8;
   for (int s0 = 0; s0 < ns; s0 += U) {
-    float2 v[U];
+    float v[U][DPT];
 #pragma unroll
-    for (int u = 0; u < U; ++u)
-      v[u] = s0 + u < ns ? *(const float2*)(po + (size_t)(s0 + u) * MLA_HEADS * MLA_LAT) : make_float2(0.f, 0.f);
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+      for (int d = 0; d < DPT; ++d)
+        v[u][d] = s0 + u < ns ? po[(size_t)(s0 + u) * MLA_HEADS * MLA_LAT + d] : 0.f;
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const float w = s0 + u < ns ? wgt[s0 + u] : 0.f;
-      o0 += v[u].x * w;
-      o1 += v[u].y * w;
+#pragma unroll
+      for (int d = 0; d < DPT; ++d) o[d] += v[u][d] * w;
     }
   }
   const float inv = Lsum > 0.f ? 1.0f / Lsum : 0.f;
-  o0 *= inv;
-  o1 *= inv;
-  const size_t at = ((size_t)r * MLA_HEADS + h) * MLA_LAT + 2 * tid;
-  *(uint32_t*)(p.o_lat + at) = pack_bf16x2(o0, o1);
-  if (p.o_lat_f32) *(float2*)(p.o_lat_f32 + at) = make_float2(o0, o1);
+  const size_t at = ((size_t)r * MLA_HEADS + h) * MLA_LAT + DPT * tid;
+#pragma unroll
+  for (int d = 0; d < DPT; ++d) {
+    o[d] *= inv;
+    p.o_lat[at + d] = f32_to_bf16(o[d]);
+    if (p.o_lat_f32) p.o_lat_f32[at + d] = o[d];
+  }
   __syncthreads();
 }
 
 // ---------------------------------------------------------------- stage: W_UV
-template <int NCG>
+template <int NT, int NCG>
 MK2_DEV void mla_uv(const MlaDev& p, int h, int vt, float* red) {
+  constexpr int NW = NT / 64;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, c16 = lane & 15;
-  const int kb = wave;  // 4 waves x 128 of the 512 latent dims
+  const int kb = wave & 3;  // waves 0-3: 128 of the 512 latent dims each (4-7 idle)
+  f32x4 acc[NCG];
+  if (wave < 4) {
   bf16x8 a[4];
   const bf16_t* wrow = p.w_uv + ((size_t)h * p.v_dim + vt * 16 + c16) * MLA_LAT + kb * 128 + 32 * g;
 #pragma unroll
   for (int q = 0; q < 4; ++q) a[q] = __builtin_bit_cast(bf16x8, *(const uint4*)(wrow + 8 * q));
-  f32x4 acc[NCG];
 #pragma unroll
   for (int cg = 0; cg < NCG; ++cg) {
     const int row = cg * 16 + c16;
@@ -262,9 +283,10 @@ MK2_DEV void mla_uv(const MlaDev& p, int h, int vt, float* red) {
     acc[cg] = c;
   }
 #pragma unroll
-  for (int cg = 0; cg < NCG; ++cg) *(f32x4*)(red + ((wave * NCG + cg) * 64 + lane) * 4) = acc[cg];
+    for (int cg = 0; cg < NCG; ++cg) *(f32x4*)(red + ((wave * NCG + cg) * 64 + lane) * 4) = acc[cg];
+  }
   __syncthreads();
-  for (int idx = threadIdx.x; idx < 16 * p.rows; idx += MLA_NT) {
+  for (int idx = threadIdx.x; idx < 16 * p.rows; idx += NT) {
     const int n16 = idx & 15, row = idx >> 4, cg = row >> 4, s16 = row & 15;
     const int l = (n16 >> 2) * 16 + s16, i = n16 & 3;
     float v = 0.f;
@@ -276,14 +298,15 @@ MK2_DEV void mla_uv(const MlaDev& p, int h, int vt, float* red) {
 }
 
 // ---------------------------------------------------------------- stage: W_o
-template <int NCG>
+template <int NT, int NCG>
 MK2_DEV void mla_oproj(const MlaDev& p, int nt, float* red) {
+  constexpr int NW = NT / 64;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, c16 = lane & 15;
   const int K = MLA_HEADS * p.v_dim, KB = K / 128;
   f32x4 acc[NCG];
 #pragma unroll
   for (int cg = 0; cg < NCG; ++cg) acc[cg] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int kb = wave; kb < KB; kb += 4) {
+  for (int kb = wave; kb < KB; kb += NW) {
     bf16x8 a[4];
     const uint4* t = (const uint4*)(p.w_o + (((size_t)nt * KB + kb) * 64 + lane) * 64);
 #pragma unroll
@@ -307,12 +330,12 @@ MK2_DEV void mla_oproj(const MlaDev& p, int nt, float* red) {
 #pragma unroll
   for (int cg = 0; cg < NCG; ++cg) *(f32x4*)(red + ((wave * NCG + cg) * 64 + lane) * 4) = acc[cg];
   __syncthreads();
-  for (int idx = threadIdx.x; idx < 16 * p.rows; idx += MLA_NT) {
+  for (int idx = threadIdx.x; idx < 16 * p.rows; idx += NT) {
     const int n16 = idx & 15, row = idx >> 4, cg = row >> 4, s16 = row & 15;
     const int l = (n16 >> 2) * 16 + s16, i = n16 & 3;
     float v = 0.f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) v += red[((w * NCG + cg) * 64 + l) * 4 + i];
+    for (int w = 0; w < NW; ++w) v += red[((w * NCG + cg) * 64 + l) * 4 + i];
     const size_t o = (size_t)row * p.hidden + nt * 16 + n16;
     if (p.h) v += bf16_to_f32(p.h[o]);
     p.out[o] = f32_to_bf16(v);

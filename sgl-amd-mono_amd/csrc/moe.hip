@@ -1,4 +1,4 @@
-// Standalone MoE block launch (BASELINE configs[0] and [1]): five kernels on one
+// Standalone MoE block launch (FP8 or MXFP4 experts): five kernels on one
 // stream -- prep (RMSNorm + MXFP8 quant), router GEMV, route (top-k + distinct
 // experts), up/gate + SwiGLU, down + combine.
 #include "mk2_host.h"

@@ -85,11 +85,15 @@ class MlaArgs(ctypes.Structure):
     ]
 
 
+MK2_LAYER_PERSISTENT, MK2_LAYER_STAGED = 0, 1
+
+
 class LayerArgs(ctypes.Structure):
     _fields_ = [
         ("indexer", IndexerArgs), ("mla", MlaArgs), ("moe", MoeArgs),
         ("attn_out", c_void_p), ("out", c_void_p),
         ("workspace", c_void_p), ("workspace_bytes", c_size_t),
+        ("mode", c_int), ("spin_limit", c_int), ("status", c_void_p),
     ]
 
 

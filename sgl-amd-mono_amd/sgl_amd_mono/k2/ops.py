@@ -148,9 +148,12 @@ class LayerOp:
     RMSNorm -> MoE + residual (the reference's Glm53LayerOp.launch without the TP
     reduces, glm53/gfx950/runner.py:374-470)."""
 
-    def __init__(self, cfg: C.K2Config, layer, rows: int, device=None):
+    def __init__(self, cfg: C.K2Config, layer, rows: int, device=None, *, staged: bool = False,
+                 spin_limit: int = 0):
         cfg.validate(rows)
         self.cfg, self.rows, self.L = cfg, rows, layer
+        self.mode = _lib.MK2_LAYER_STAGED if staged else _lib.MK2_LAYER_PERSISTENT
+        self.spin_limit = spin_limit
         self.device = torch.device(device or layer.h.device)
         self.idx = IndexerOp(cfg.indexer, rows, layer.idx.page_table.shape[1], self.device)
         self.mla = SparseMlaOp(cfg.mla, layer.mla, rows, layer.mla.page_table.shape[1], self.device)
@@ -160,10 +163,12 @@ class LayerOp:
         nbytes = ctypes.c_size_t()
         _lib.check(_lib.lib().mk2_layer_workspace_bytes(ctypes.byref(self._make_args()),
                                                         ctypes.byref(nbytes)))
-        self.workspace = torch.empty(nbytes.value, dtype=torch.uint8, device=self.device)
+        # zeroed once: the persistent launch's counters start at zero and every launch
+        # leaves them at zero
+        self.workspace = torch.zeros(nbytes.value, dtype=torch.uint8, device=self.device)
 
     def _make_args(self, out=None, attn_out=None, scores=None, topk=None, logits=None,
-                   topk_ids=None, topk_weights=None, workspace=None):
+                   topk_ids=None, topk_weights=None, workspace=None, status=None):
         L = self.L
         ia = _lib.IndexerArgs(
             self.idx.shape, _p(L.idx.q), _p(L.idx.w), _p(L.idx.cache), _p(L.idx.page_table),
@@ -179,15 +184,15 @@ class LayerOp:
         )
         ws = workspace
         return _lib.LayerArgs(ia, ma, ea, _p(attn_out), _p(out), _p(ws),
-                              0 if ws is None else ws.numel())
+                              0 if ws is None else ws.numel(), self.mode, self.spin_limit, _p(status))
 
     def __call__(self, out=None, *, attn_out=None, scores=None, topk=None, logits=None,
-                 topk_ids=None, topk_weights=None):
+                 topk_ids=None, topk_weights=None, status=None):
         H = self.cfg.mla.hidden
         if out is None:
             out = torch.empty(self.rows, H, dtype=torch.bfloat16, device=self.device)
         _need(out, "out", torch.bfloat16, (self.rows, H))
         args = self._make_args(out, attn_out, scores, topk, logits, topk_ids, topk_weights,
-                               self.workspace)
+                               self.workspace, status)
         _lib.check(_lib.lib().mk2_layer_launch(ctypes.byref(args), _lib.stream_handle(self.device)))
         return out

@@ -1,4 +1,4 @@
-"""The chained K2 layer on the GPU against the CPU oracle,
+"""The chained K2 layer on the GPU (indexer -> MLA -> MoE) against the CPU oracle,
 checked piecewise (refs.check_layer): exact top-k lists of the kernel's own scores,
 scores within 1e-4 of f64, attention and layer outputs within rel-L2 1e-2, router
 logits within 1e-4 and expert ids exact on rows with a clear top-8 boundary."""
@@ -17,13 +17,14 @@ def _dev():
     return torch.device("cuda:0")
 
 
-def run_layer(cfg, rows, seed):
+def run_layer(cfg, rows, seed, staged=False):
     from sgl_amd_mono.k2 import synth
     from sgl_amd_mono.k2.ops import LayerOp
 
     dev = _dev()
     L = synth.make_layer(cfg, rows, seed, dev)
-    op = LayerOp(cfg, L, rows, device=dev)
+    op = LayerOp(cfg, L, rows, device=dev, staged=staged)
+    status = torch.full((1,), -1, dtype=torch.int32, device=dev)
     H, E, K = cfg.mla.hidden, cfg.moe.n_experts, cfg.moe.top_k
     attn = torch.empty(rows, H, dtype=torch.bfloat16, device=dev)
     scores = torch.empty(rows, cfg.indexer.context, dtype=torch.float32, device=dev)
@@ -31,16 +32,20 @@ def run_layer(cfg, rows, seed):
     logits = torch.empty(rows, E, dtype=torch.float32, device=dev)
     ids = torch.empty(rows, K, dtype=torch.int32, device=dev)
     wts = torch.empty(rows, K, dtype=torch.float32, device=dev)
-    out = op(attn_out=attn, scores=scores, topk=topk, logits=logits, topk_ids=ids, topk_weights=wts)
+    out = op(attn_out=attn, scores=scores, topk=topk, logits=logits, topk_ids=ids, topk_weights=wts,
+             status=status)
     torch.cuda.synchronize()
+    if not staged:
+        assert int(status.item()) == 0, "a dependency wait of the persistent launch gave up"
     return L, [cpu(t) for t in (out, attn, scores, topk, logits, ids, wts)]
 
 
+@pytest.mark.parametrize("staged", [False, True])
 @pytest.mark.parametrize("rows", [1, 4, 8])
-def test_layer_config5(rows):
+def test_layer_config5(rows, staged):
     from sgl_amd_mono.k2 import config as C
 
-    L, res = run_layer(C.C5_LAYER, rows, seed=500 + rows)
+    L, res = run_layer(C.C5_LAYER, rows, seed=500 + rows, staged=staged)
     stats = check_layer(L, *res)
     print(stats)
 
@@ -54,3 +59,25 @@ def test_layer_small_context_32_rows():
                   indexer=replace(C.C5_LAYER.indexer, context=8192))
     L, res = run_layer(cfg, 32, seed=532)
     print(check_layer(L, *res))
+
+
+def test_persistent_layer_repeats_and_matches_staged():
+    """Back-to-back persistent launches (counters reset by the launch itself) give the
+    same bits each time and the same bits as the stage-by-stage path."""
+    from sgl_amd_mono.k2 import config as C
+    from sgl_amd_mono.k2 import synth
+    from sgl_amd_mono.k2.ops import LayerOp
+
+    dev = _dev()
+    cfg = C.C5_LAYER
+    L = synth.make_layer(cfg, 8, 777, dev)
+    p_op = LayerOp(cfg, L, 8, device=dev)
+    s_op = LayerOp(cfg, L, 8, device=dev, staged=True)
+    status = torch.full((1,), -1, dtype=torch.int32, device=dev)
+    outs = [p_op(status=status).clone() for _ in range(3)]
+    ref = s_op()
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0
+    for o in outs:
+        assert torch.equal(o, outs[0])
+    assert torch.equal(outs[0], ref)

@@ -1,4 +1,4 @@
-"""Sparse MLA + W_UV + W_o on the GPU.
+"""Sparse MLA + W_UV + W_o on the GPU (8 rows x 2048 selected of 32768).
 
 Bar: the merged latent output and the bf16 layer output within rel-L2 1e-2 of the
 CPU oracle (f64 softmax over the same gathered, dequantized FP8 rows); the kernel

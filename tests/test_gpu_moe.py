@@ -1,4 +1,4 @@
-"""MoE block on the GPU against the CPU oracle.
+"""MoE block on the GPU against the CPU oracle (the FP8 block and the MXFP4 shard).
 
 Contract (the reference's own checks, test/kernels/glm53/check_layer.py:631-698 and
 glm53/gfx950/kernel.py:1967-1999):

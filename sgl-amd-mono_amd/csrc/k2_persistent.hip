@@ -44,9 +44,17 @@ struct K2Dev {
   MoeDev moe;
   int* sync;
   int* status;    // optional: the launch's error word
+  uint64_t* timeline;  // optional: [grid][K2_STAMPS] s_memrealtime stamps (100 MHz)
   int rows;
   int spin_limit;
 };
+
+// timeline: per stage s, stamps 3s (enter), 3s+1 (first input ready), 3s+2 (leave)
+constexpr int K2_STAGES = 11, K2_STAMPS = 3 * K2_STAGES + 1;
+
+MK2_DEV void k2_stamp(const K2Dev& p, int i) {
+  if (p.timeline && threadIdx.x == 0) p.timeline[(size_t)blockIdx.x * K2_STAMPS + i] = __builtin_amdgcn_s_memrealtime();
+}
 
 union K2Lds {
   int pages[IDX_CHUNK / 64];
@@ -76,7 +84,7 @@ MK2_DEV void k2_signal(int* c) {
   }
 }
 
-MK2_DEV void k2_wait(const K2Dev& p, int slot, int target) {
+MK2_DEV void k2_wait(const K2Dev& p, int slot, int target, int stamp = -1) {
   if (threadIdx.x == 0) {
     const int* c = p.sync + slot;
     int* err = p.sync + SY_ERR;
@@ -90,6 +98,7 @@ MK2_DEV void k2_wait(const K2Dev& p, int slot, int target) {
       __builtin_amdgcn_s_sleep(2);
     }
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    if (stamp >= 0 && p.timeline) p.timeline[(size_t)blockIdx.x * K2_STAMPS + stamp] = __builtin_amdgcn_s_memrealtime();
   }
   __syncthreads();
 }
@@ -100,80 +109,102 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
   const int G = gridDim.x, b = blockIdx.x;
   const int R = p.rows;
   // ---- index scores
+  k2_stamp(p, 0);
   const int nchk = (p.idx.max_ctx + IDX_CHUNK - 1) / IDX_CHUNK;
   for (int t = b; t < R * nchk; t += G) {
     idx_score<K2_NT>(p.idx, t / nchk, t % nchk, S.pages);
     k2_signal(p.sync + SY_SCORE + t / nchk);
   }
+  k2_stamp(p, 2);
   // ---- exact top-k of each row
+  k2_stamp(p, 3);
   for (int t = b; t < R; t += G) {
-    k2_wait(p, SY_SCORE + t, nchk);
+    k2_wait(p, SY_SCORE + t, nchk, t == b ? 4 : -1);
     idx_topk<K2_NT>(p.idx, t, S.topk);
     k2_signal(p.sync + SY_TOPK + t);
   }
+  k2_stamp(p, 5);
   // ---- sparse-MLA splits
+  k2_stamp(p, 6);
   const int ns = p.mla.nsplit;
   for (int t = b; t < R * ns; t += G) {
     const int r = t / ns;
-    k2_wait(p, SY_TOPK + r, 1);
+    k2_wait(p, SY_TOPK + r, 1, t == b ? 7 : -1);
     mla_split<K2_NT>(p.mla, r, t % ns, S.split);
     k2_signal(p.sync + SY_SPLIT + r);
   }
+  k2_stamp(p, 8);
   // ---- merge of the splits, per (row, head)
+  k2_stamp(p, 9);
   for (int t = b; t < R * MLA_HEADS; t += G) {
     const int r = t / MLA_HEADS, h = t % MLA_HEADS;
-    k2_wait(p, SY_SPLIT + r, ns);
+    k2_wait(p, SY_SPLIT + r, ns, t == b ? 10 : -1);
     mla_merge<K2_NT>(p.mla, r, h, S.merge);
     k2_signal(p.sync + SY_MERGE + h);
   }
+  k2_stamp(p, 11);
   // ---- W_UV, per (head, 16 v rows)
+  k2_stamp(p, 12);
   const int vtn = p.mla.v_dim / 16;
   for (int t = b; t < MLA_HEADS * vtn; t += G) {
     const int h = t / vtn;
-    k2_wait(p, SY_MERGE + h, R);
+    k2_wait(p, SY_MERGE + h, R, t == b ? 13 : -1);
     mla_uv<K2_NT, NCG>(p.mla, h, t % vtn, S.red);
     k2_signal(p.sync + SY_UV);
   }
+  k2_stamp(p, 14);
   // ---- W_o + residual, per 16 hidden rows
+  k2_stamp(p, 15);
   const int ht = p.mla.hidden / 16;
   for (int t = b; t < ht; t += G) {
-    k2_wait(p, SY_UV, MLA_HEADS * vtn);
+    k2_wait(p, SY_UV, MLA_HEADS * vtn, t == b ? 16 : -1);
     mla_oproj<K2_NT, NCG>(p.mla, t, S.red);
     k2_signal(p.sync + SY_OPROJ);
   }
+  k2_stamp(p, 17);
   // ---- RMSNorm + activation quant, per row
+  k2_stamp(p, 18);
   for (int t = b; t < R; t += G) {
-    k2_wait(p, SY_OPROJ, ht);
+    k2_wait(p, SY_OPROJ, ht, t == b ? 19 : -1);
     moe_prep<K2_NT>(p.moe, t, S.red);
     k2_signal(p.sync + SY_PREP);
   }
+  k2_stamp(p, 20);
   // ---- router GEMV, per (16 experts, k-chunk)
+  k2_stamp(p, 21);
   const int et = p.moe.E / 16, nrt = et * p.moe.KC;
   for (int t = b; t < nrt; t += G) {
-    k2_wait(p, SY_PREP, R);
+    k2_wait(p, SY_PREP, R, t == b ? 22 : -1);
     moe_router<K2_NT, NCG>(p.moe, t % et, t / et, S.red);
     k2_signal(p.sync + SY_ROUTER);
   }
+  k2_stamp(p, 23);
   // ---- top-k routing (one task)
+  k2_stamp(p, 24);
   for (int t = b; t < 1; t += G) {
-    k2_wait(p, SY_ROUTER, nrt);
+    k2_wait(p, SY_ROUTER, nrt, t == b ? 25 : -1);
     moe_route<K2_NT>(p.moe, S.route.logits, S.route.slot);
     k2_signal(p.sync + SY_ROUTE);
   }
+  k2_stamp(p, 26);
   // ---- up/gate + SwiGLU: routed slots (after routing), then the shared expert
+  k2_stamp(p, 27);
   const int up_r = p.moe.Dmax * (p.moe.I / 32);
   const int up_total = up_r + p.moe.n_shared * (p.moe.SI / 32);
   for (int t = b; t < up_total; t += G) {
-    if (t < up_r) k2_wait(p, SY_ROUTE, 1);
-    else k2_wait(p, SY_PREP, R);
+    if (t < up_r) k2_wait(p, SY_ROUTE, 1, t == b ? 28 : -1);
+    else k2_wait(p, SY_PREP, R, t == b ? 28 : -1);
     moe_upgate<K2_NT, NCG>(p.moe, t, S.up.red, S.up.midf);
     k2_signal(p.sync + SY_UP);
   }
+  k2_stamp(p, 29);
   // ---- down + route weighting + residual, per 16 hidden rows
+  k2_stamp(p, 30);
   for (int t = b; t < p.moe.H / 16; t += G) {
-    k2_wait(p, SY_UP, up_total);
+    k2_wait(p, SY_UP, up_total, t == b ? 31 : -1);
     moe_down<K2_NT, NCG>(p.moe, t, S.down.red, S.down.act);
   }
+  k2_stamp(p, 32);
   // ---- the last workgroup out resets the counters for the next launch
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -192,14 +223,14 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
 static int g_cus = 0;
 
 int k2_persistent_enqueue(const IdxDev& idx, const MlaDev& mla, const MoeDev& moe, int* sync,
-                          int* status, int rows, int spin_limit, hipStream_t st) {
+                          int* status, uint64_t* timeline, int rows, int spin_limit, hipStream_t st) {
   if (g_cus == 0) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&g_cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || g_cus <= 0)
       return set_error(MK2_ELAUNCH, "layer: cannot query the CU count");
   }
-  K2Dev p{idx, mla, moe, sync, status, rows, spin_limit};
+  K2Dev p{idx, mla, moe, sync, status, timeline, rows, spin_limit};
   const bool two = rows > 16;
   int per_cu = 0;
   hipError_t e = two ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_k2_layer<2>, K2_NT, 0)

@@ -18,7 +18,7 @@ int moe_fill(const mk2_moe_args* a, MoeDev* d);
 size_t moe_carve(const mk2_moe_shape* s, void* base, MoeDev* d);
 int moe_enqueue(const MoeDev& d, hipStream_t st);
 int k2_persistent_enqueue(const IdxDev& idx, const MlaDev& mla, const MoeDev& moe, int* sync,
-                          int* status, int rows, int spin_limit, hipStream_t st);
+                          int* status, uint64_t* timeline, int rows, int spin_limit, hipStream_t st);
 
 constexpr int LAYER_SYNC_BYTES = 512;
 
@@ -108,7 +108,8 @@ extern "C" int mk2_layer_launch(const mk2_layer_args* a, mk2_stream_t stream) {
   if (rc) return rc;
   hipStream_t st = (hipStream_t)stream;
   if (a->mode == MK2_LAYER_PERSISTENT)
-    return k2_persistent_enqueue(L.idx, L.mla, L.moe, L.sync, a->status, a->mla.shape.rows,
+    return k2_persistent_enqueue(L.idx, L.mla, L.moe, L.sync, a->status, (uint64_t*)a->timeline,
+                                 a->mla.shape.rows,
                                  a->spin_limit ? a->spin_limit : (1 << 20), st);
   idx_enqueue(L.idx, st);
   mla_enqueue(L.mla, st);

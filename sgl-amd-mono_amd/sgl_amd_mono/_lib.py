@@ -93,7 +93,7 @@ class LayerArgs(ctypes.Structure):
         ("indexer", IndexerArgs), ("mla", MlaArgs), ("moe", MoeArgs),
         ("attn_out", c_void_p), ("out", c_void_p),
         ("workspace", c_void_p), ("workspace_bytes", c_size_t),
-        ("mode", c_int), ("spin_limit", c_int), ("status", c_void_p),
+        ("mode", c_int), ("spin_limit", c_int), ("status", c_void_p), ("timeline", c_void_p),
     ]
 
 

@@ -168,7 +168,7 @@ class LayerOp:
         self.workspace = torch.zeros(nbytes.value, dtype=torch.uint8, device=self.device)
 
     def _make_args(self, out=None, attn_out=None, scores=None, topk=None, logits=None,
-                   topk_ids=None, topk_weights=None, workspace=None, status=None):
+                   topk_ids=None, topk_weights=None, workspace=None, status=None, timeline=None):
         L = self.L
         ia = _lib.IndexerArgs(
             self.idx.shape, _p(L.idx.q), _p(L.idx.w), _p(L.idx.cache), _p(L.idx.page_table),
@@ -184,15 +184,16 @@ class LayerOp:
         )
         ws = workspace
         return _lib.LayerArgs(ia, ma, ea, _p(attn_out), _p(out), _p(ws),
-                              0 if ws is None else ws.numel(), self.mode, self.spin_limit, _p(status))
+                              0 if ws is None else ws.numel(), self.mode, self.spin_limit, _p(status),
+                              _p(timeline))
 
     def __call__(self, out=None, *, attn_out=None, scores=None, topk=None, logits=None,
-                 topk_ids=None, topk_weights=None, status=None):
+                 topk_ids=None, topk_weights=None, status=None, timeline=None):
         H = self.cfg.mla.hidden
         if out is None:
             out = torch.empty(self.rows, H, dtype=torch.bfloat16, device=self.device)
         _need(out, "out", torch.bfloat16, (self.rows, H))
         args = self._make_args(out, attn_out, scores, topk, logits, topk_ids, topk_weights,
-                               self.workspace, status)
+                               self.workspace, status, timeline)
         _lib.check(_lib.lib().mk2_layer_launch(ctypes.byref(args), _lib.stream_handle(self.device)))
         return out

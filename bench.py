@@ -27,6 +27,73 @@ for _p in (ROOT, os.path.join(ROOT, "sgl-amd-mono_amd"), os.path.join(ROOT, "tes
 
 PEAK_HBM_GBS = 8000.0
 METRIC = "us per fused decoder layer @8 decode rows, 1 GPU; % of peak HBM GB/s"
+CSRC = os.path.join(ROOT, "sgl-amd-mono_amd", "csrc")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k2_layer_m8_traffic.json")
+LAYER_KERNEL = "k_k2_layer"  # the persistent layer kernel's name (rocprof)
+COPY_KERNEL = "copy"         # torch's copy kernel of the calibration
+
+
+def sources_digest():
+    """sha256 over the HIP sources: a recorded traffic figure applies to these only."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for name in sorted(os.listdir(CSRC)):
+        if name.endswith((".hip", ".h")):
+            h.update(name.encode())
+            with open(os.path.join(CSRC, name), "rb") as f:
+                h.update(f.read())
+    return h.hexdigest()
+
+
+def recorded_traffic():
+    """HBM bytes per layer launch from the committed PMC summary, if it was taken on
+    the current sources (else None)."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if rec.get("sources_sha256") != sources_digest():
+        return None
+    return rec.get("traffic_bytes_per_launch")
+
+
+def pmc_summary(dirs, calib_bytes):
+    """Mean FETCH_SIZE / WRITE_SIZE (KiB a dispatch) of the layer kernel and of the
+    calibration copy, from rocprofv3 --pmc databases; each scaled by the factor that
+    turns the copy's counter into its known byte count."""
+    import glob
+    import sqlite3
+    from collections import defaultdict
+
+    acc = defaultdict(lambda: defaultdict(list))
+    for d in dirs:
+        for f in glob.glob(os.path.join(d, "**", "*.db"), recursive=True):
+            db = sqlite3.connect(f)
+            q = ("select name, dispatch_id, counter_name, sum(counter_value) from pmc_events "
+                 "group by dispatch_id, counter_name")
+            for name, _, counter, value in db.execute(q):
+                kind = ("layer" if LAYER_KERNEL in name else
+                        "copy" if COPY_KERNEL in name.lower() else None)
+                if kind:
+                    acc[kind][counter].append(value)
+    # the calibration copies are the largest copies of the run
+    for c, v in acc.get("copy", {}).items():
+        top = max(v)
+        acc["copy"][c] = [x for x in v if x >= 0.5 * top]
+    mean = {k: {c: statistics.mean(v) for c, v in cs.items()} for k, cs in acc.items()}
+    out = {"sources_sha256": sources_digest(), "counters_kib_per_dispatch": mean,
+           "calibration_copy_bytes": calib_bytes}
+    try:
+        fetch_f = (calib_bytes / 2) / (mean["copy"]["FETCH_SIZE"] * 1024)
+        write_f = (calib_bytes / 2) / (mean["copy"]["WRITE_SIZE"] * 1024)
+        out["scale"] = {"FETCH_SIZE": fetch_f, "WRITE_SIZE": write_f}
+        out["traffic_bytes_per_launch"] = int(mean["layer"]["FETCH_SIZE"] * 1024 * fetch_f +
+                                              mean["layer"]["WRITE_SIZE"] * 1024 * write_f)
+    except (KeyError, ZeroDivisionError):
+        out["traffic_bytes_per_launch"] = None
+    return out
 
 
 def algorithmic_bytes(cfg, rows, distinct_experts):
@@ -84,7 +151,17 @@ def main():
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--staged", action="store_true", help="one kernel a stage instead of one launch")
+    ap.add_argument("--copy-calib-mib", type=int, default=0,
+                    help="after timing, copy this many MiB (x3) for a PMC calibration")
+    ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
+                    help="no GPU: summarize rocprofv3 --pmc databases into the traffic record")
+    ap.add_argument("--calib-bytes", type=int, default=512 << 20,
+                    help="bytes the calibration copy moves (read + write)")
     args = ap.parse_args()
+    if args.pmc_summary:
+        rec = pmc_summary(args.pmc_summary, args.calib_bytes)
+        print(json.dumps(rec, indent=1))
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU's share of the layer; --gpus {args.gpus} "
               "is not supported (TP all-reduce omitted by design)", file=sys.stderr)
@@ -182,10 +259,17 @@ def main():
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(gbs / PEAK_HBM_GBS, 4),
-            "traffic": None,
+            "traffic": None if args.staged else recorded_traffic(),
         },
         "cpu_baseline": None,
     }
+    if args.copy_calib_mib:
+        n = args.copy_calib_mib << 20
+        src = torch.ones(n // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(layers[0], args.cpu_reps)
     print(json.dumps(result))

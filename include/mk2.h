@@ -128,9 +128,10 @@ typedef struct mk2_indexer_args {
   const int32_t* page_table;/* [requests][table_stride] */
   const int32_t* req_ids;   /* [rows] */
   const int32_t* ctx_len;   /* [rows] */
-  float* scores;            /* f32 [rows][max_ctx] (written for 0..ctx_len-1) */
-  int32_t* topk;            /* [rows][topk] positions, -1 padded */
-  void* workspace;
+  float* scores;            /* f32 [rows][max_ctx] (written for 0..ctx_len-1) or NULL */
+  int32_t* topk;            /* [rows][topk] positions, -1 padded, or NULL */
+  void* workspace;          /* required: key histograms and top-k candidates (and the
+                               scores / lists when those are NULL) */
   size_t workspace_bytes;
 } mk2_indexer_args;
 
@@ -187,14 +188,14 @@ typedef struct mk2_layer_args {
   mk2_moe_args moe;         /* x is ignored (the attention output); norm=1, residual=1 */
   void* attn_out;           /* optional bf16 [rows][hidden]: the residual after attention */
   void* out;
-  void* workspace;          /* its first 512 bytes must be zero before the first
-                               persistent launch; every launch leaves them zero */
+  void* workspace;          /* zero-filled before its first launch; every completed
+                               launch leaves it ready for the next */
   size_t workspace_bytes;
   int mode;                 /* MK2_LAYER_PERSISTENT or MK2_LAYER_STAGED */
   int spin_limit;           /* persistent: polls a dependency wait may take before the
                                launch gives up (0: default, about a second) */
   int32_t* status;          /* optional device word: 0 ok, 1 a wait gave up */
-  uint64_t* timeline;       /* optional [grid][34] stage stamps of the persistent launch
+  uint64_t* timeline;       /* optional [grid][37] stage stamps of the persistent launch
                                (100 MHz device clock): per stage enter, input ready, leave */
 } mk2_layer_args;
 

@@ -1,5 +1,5 @@
-// Standalone indexer launch (FP4 index keys, 64 heads x 128): key scores, then the exact
-// top-k of every row.
+// Standalone indexer launch (FP4 index keys, 64 heads x 128): key scores with the
+// row histograms, the candidate slices, then the exact top-k of every row.
 #include "indexer_stages.h"
 #include "mk2_host.h"
 
@@ -7,14 +7,24 @@ namespace mk2 {
 
 constexpr int IDX_NT = 512;
 
-__global__ __launch_bounds__(IDX_NT) void k_idx_score(IdxDev p) {
-  __shared__ int pages[IDX_CHUNK / 64];
-  idx_score<IDX_NT>(p, blockIdx.y, blockIdx.x, pages);
+__global__ __launch_bounds__(256) void k_idx_clear(IdxDev p) {
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < p.rows * IDX_BINS; i += gridDim.x * 256) p.hist[i] = 0;
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < p.rows * IDX_CBINS; i += gridDim.x * 256) p.chist[i] = 0;
 }
 
-__global__ __launch_bounds__(TOPK_NT) void k_idx_topk(IdxDev p) {
+__global__ __launch_bounds__(IDX_NT) void k_idx_score(IdxDev p) {
+  __shared__ IdxScoreLds L;
+  idx_score<IDX_NT>(p, blockIdx.y, blockIdx.x, L);
+}
+
+__global__ __launch_bounds__(IDX_NT) void k_idx_slice(IdxDev p) {
   __shared__ TopkLds S;
-  idx_topk<TOPK_NT>(p, blockIdx.x, S);
+  idx_slice<IDX_NT>(p, blockIdx.y, blockIdx.x, S);
+}
+
+__global__ __launch_bounds__(TOPK_NT) void k_idx_select(IdxDev p) {
+  __shared__ TopkLds S;
+  idx_select<TOPK_NT>(p, blockIdx.x, S);
 }
 
 int idx_check_shape(const mk2_indexer_shape* s) {
@@ -31,12 +41,25 @@ int idx_check_shape(const mk2_indexer_shape* s) {
   return MK2_OK;
 }
 
-size_t idx_carve(const mk2_indexer_shape* s, void* base, float** scores, int** topk) {
+// workspace: scores, top-k lists (used when the caller gives none), row histograms (fine, coarse),
+// chunk candidate counts, candidates
+size_t idx_carve(const mk2_indexer_shape* s, void* base, IdxDev* d) {
   Carver c(base);
+  const int nchk = (s->max_ctx + IDX_CHUNK - 1) / IDX_CHUNK;
   float* sc = c.take<float>((size_t)s->rows * s->max_ctx);
   int* tk = c.take<int>((size_t)s->rows * s->topk);
-  if (scores) *scores = sc;
-  if (topk) *topk = tk;
+  int* hist = c.take<int>((size_t)s->rows * IDX_BINS);
+  int* chist = c.take<int>((size_t)s->rows * IDX_CBINS);
+  int* cnt = c.take<int>((size_t)s->rows * nchk);
+  uint2* cand = c.take<uint2>((size_t)s->rows * s->max_ctx);
+  if (d) {
+    if (!d->scores) d->scores = sc;
+    if (!d->out) d->out = tk;
+    d->hist = hist;
+    d->chist = chist;
+    d->ccount = cnt;
+    d->cand = cand;
+  }
   return c.bytes();
 }
 
@@ -51,13 +74,15 @@ int idx_fill(const mk2_indexer_args* a, IdxDev* d) {
   d->q = (const bf16_t*)a->q; d->w = (const bf16_t*)a->w; d->cache = a->cache;
   d->pt = a->page_table; d->req = a->req_ids; d->ctx = a->ctx_len;
   d->scores = a->scores; d->out = a->topk;
+  d->nchk = (d->max_ctx + IDX_CHUNK - 1) / IDX_CHUNK;
   return MK2_OK;
 }
 
 void idx_enqueue(const IdxDev& d, hipStream_t st) {
-  const int chunks = (d.max_ctx + IDX_CHUNK - 1) / IDX_CHUNK;
-  k_idx_score<<<dim3(chunks, d.rows), IDX_NT, 0, st>>>(d);
-  k_idx_topk<<<d.rows, TOPK_NT, 0, st>>>(d);
+  k_idx_clear<<<d.rows * 4, 256, 0, st>>>(d);
+  k_idx_score<<<dim3(d.nchk, d.rows), IDX_NT, 0, st>>>(d);
+  k_idx_slice<<<dim3(d.nchk, d.rows), IDX_NT, 0, st>>>(d);
+  k_idx_select<<<d.rows, TOPK_NT, 0, st>>>(d);
 }
 
 }  // namespace mk2
@@ -69,7 +94,7 @@ extern "C" int mk2_indexer_workspace_bytes(const mk2_indexer_shape* shape, size_
   int rc = idx_check_shape(shape);
   if (rc) return rc;
   MK2_REQUIRE(bytes != nullptr, "indexer: bytes is NULL");
-  *bytes = idx_carve(shape, nullptr, nullptr, nullptr);
+  *bytes = idx_carve(shape, nullptr, nullptr);
   return MK2_OK;
 }
 
@@ -79,17 +104,11 @@ extern "C" int mk2_indexer_topk_launch(const mk2_indexer_args* a, mk2_stream_t s
   IdxDev d;
   int rc = idx_fill(a, &d);
   if (rc) return rc;
-  if (!d.scores || !d.out) {
-    const size_t need = idx_carve(&a->shape, nullptr, nullptr, nullptr);
-    MK2_REQUIRE(a->workspace != nullptr, "indexer: scores/topk not given and no workspace");
-    if (a->workspace_bytes < need)
-      return set_error(MK2_ENOSPACE, "indexer: workspace has %zu bytes, needs %zu", a->workspace_bytes, need);
-    float* sc;
-    int* tk;
-    idx_carve(&a->shape, a->workspace, &sc, &tk);
-    if (!d.scores) d.scores = sc;
-    if (!d.out) d.out = tk;
-  }
+  const size_t need = idx_carve(&a->shape, nullptr, nullptr);
+  MK2_REQUIRE(a->workspace != nullptr, "indexer: workspace is NULL");
+  if (a->workspace_bytes < need)
+    return set_error(MK2_ENOSPACE, "indexer: workspace has %zu bytes, needs %zu", a->workspace_bytes, need);
+  idx_carve(&a->shape, a->workspace, &d);
   idx_enqueue(d, (hipStream_t)stream);
   return check_launch("indexer");
 }

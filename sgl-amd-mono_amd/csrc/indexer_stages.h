@@ -8,11 +8,24 @@
 // bf16.  The head sum runs in the lanes: a lane holds 4 heads of each head group
 // for one key, then two cross-row shuffles finish it.
 //
-// top-k: one workgroup of 1024 threads a row, 64 consecutive positions a thread in
-// registers.  LDS histogram passes over at most 12 bits at a time of (key - row min)
-// find the k-th key T exactly; the list is written in the radix select's order --
-// keys whose top 12 bits exceed T's, then keys sharing T's top 12 bits that exceed
-// T, then keys equal to T (lowest positions first) -- each group in position order.
+// top-k, three stages over the order-preserving u32 keys of the scores:
+//   score (row, chunk)  also counts its keys into the row's two-level histogram: 4096
+//                       bins of the top 12 bits and 256 of the top 8 (device atomics,
+//                       nonzero bins only);
+//   slice (row, chunk)  finds from the finished histogram (one wave: 256 coarse bins,
+//                       then 16 fine ones) the bin b1 that holds the k-th key and
+//                       compacts its chunk's keys with top bits >= b1, in position
+//                       order, as (key, position) candidates;
+//   select (row)        gathers the row's candidates in position order (fewer than
+//                       k, plus the keys of bin b1) and selects the k-th key exactly
+//                       with two radix passes over the low 20 bits of bin b1's keys;
+//                       the list is written in the radix select's order -- keys whose
+//                       top 12 bits exceed the k-th key's, then keys sharing those bits
+//                       that exceed it, then keys equal to it (lowest positions first)
+//                       -- each group in position order.  It leaves the histogram
+//                       zeroed for the next launch.
+// A row with more than TOPK_CAP candidates (keys crowding into the threshold bin)
+// runs the same select streamed over its candidates in global memory.
 #pragma once
 #include "mk2_device.h"
 
@@ -23,8 +36,11 @@ constexpr int IDX_PAGE_BYTES = 64 * 64 + 64 * 4;  // codes, then E8M0
 constexpr int IDX_CHUNK = 2048;                    // positions a score task
 constexpr int TOPK_NT = 1024;                      // top-k workgroup of the standalone launch
 
+constexpr int IDX_BINS = 4096;                     // top 12 bits of a key
+constexpr int IDX_CBINS = 256;                     // top 8 bits of a key
+
 struct IdxDev {
-  int rows, heads, topk, max_ctx, stride;
+  int rows, heads, topk, max_ctx, stride, nchk;
   const bf16_t* q;      // [rows][heads][128]
   const bf16_t* w;      // [rows][heads]
   const uint8_t* cache; // pages
@@ -33,14 +49,23 @@ struct IdxDev {
   const int* ctx;       // [rows]
   float* scores;        // [rows][max_ctx]
   int* out;             // [rows][topk]
+  // workspace
+  int* hist;            // [rows][IDX_BINS] key counts by top 12 bits (zero between launches)
+  int* chist;           // [rows][IDX_CBINS] key counts by top 8 bits (zero between launches)
+  int* ccount;          // [rows][nchk] candidates of each chunk
+  uint2* cand;          // [rows][max_ctx] (key, position); chunk c from c * IDX_CHUNK
+};
+
+struct IdxScoreLds {
+  int pages[IDX_CHUNK / 64];
+  int hist[IDX_BINS];
 };
 
 // ------------------------------------------------------------- stage: scores
 // One task: IDX_CHUNK positions of row r; each wave owns 16 groups of 16 keys and
 // issues all of their loads before the first MFMA.
-// lds: IDX_CHUNK / 64 ints (the chunk's physical pages)
 template <int NT>
-MK2_DEV void idx_score(const IdxDev& p, int r, int chunk, int* lds_pages) {
+MK2_DEV void idx_score(const IdxDev& p, int r, int chunk, IdxScoreLds& L) {
   constexpr int NW = NT / 64;
   constexpr int GPW = IDX_CHUNK / 16 / NW;  // 16-key groups a wave
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, c16 = lane & 15;
@@ -51,10 +76,12 @@ MK2_DEV void idx_score(const IdxDev& p, int r, int chunk, int* lds_pages) {
   const int ngroups = (k_end - k_begin + 15) >> 4;
   // the chunk's page ids first, through LDS: every key load below then issues
   // without waiting on another vector-memory load
+  int* lds_pages = L.pages;
   if (threadIdx.x < IDX_CHUNK / 64) {
     const int pg = (k_begin >> 6) + threadIdx.x;
     lds_pages[threadIdx.x] = pg * 64 < k_end ? p.pt[(size_t)p.req[r] * p.stride + pg] : 0;
   }
+  for (int b = threadIdx.x; b < IDX_BINS; b += NT) L.hist[b] = 0;
   __syncthreads();
   const int gw0 = wave * GPW;  // this wave's first group
   uint4 code[GPW];
@@ -117,7 +144,24 @@ MK2_DEV void idx_score(const IdxDev& p, int r, int chunk, int* lds_pages) {
     s += __shfl_xor(s, 16, 64);
     s += __shfl_xor(s, 32, 64);
     const int key = k_begin + (gw0 + j) * 16 + c16;
-    if (g == 0 && key < k_end) srow[key] = s;
+    if (g == 0 && key < k_end) {
+      st_dev_f32(srow + key, s);
+      atomicAdd(&L.hist[radix_key(s) >> 20], 1);
+    }
+  }
+  __syncthreads();
+  // the chunk's counts into the row's histograms (device atomics, nonzero bins)
+  int* gh = p.hist + (size_t)r * IDX_BINS;
+  for (int b = threadIdx.x; b < IDX_BINS; b += NT) {
+    const int v = L.hist[b];
+    if (v) atomicAdd(gh + b, v);
+  }
+  int* ch = p.chist + (size_t)r * IDX_CBINS;
+  for (int c = threadIdx.x; c < IDX_CBINS; c += NT) {
+    int v = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v += L.hist[16 * c + i];
+    if (v) atomicAdd(ch + c, v);
   }
   __syncthreads();
 }
@@ -165,6 +209,86 @@ MK2_DEV int block_sum_int(int v, int* lds) {
 #pragma unroll
   for (int w = 0; w < NW; ++w) t += lds[w];
   return t;
+}
+
+MK2_DEV int wave_incl_scan(int v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int x = __shfl_up(v, o, 64);
+    if (lane >= o) v += x;
+  }
+  return v;
+}
+
+// One wave: the bin of hist[nbins] (LDS, nbins a multiple of 64) where the count from
+// the top reaches `need`, and through *above the count of the bins above it.  Lane l
+// owns the bins nbins - per*(l+1) .. nbins - per*l - 1.
+MK2_DEV int wave_find_bin(const int* hist, int nbins, int need, int* above) {
+  const int lane = threadIdx.x & 63, per = nbins >> 6;
+  const int hi = nbins - per * lane - 1;  // this lane's highest bin
+  int sum = 0;
+  // the lanes' runs start `per` words apart: rotate the order so they use distinct banks
+  for (int i = 0; i < per; ++i) sum += hist[hi - ((i + lane) & (per - 1))];
+  const int inc = wave_incl_scan(sum), excl = inc - sum;
+  const uint64_t hit = __ballot(excl < need && inc >= need);
+  const int L = hit ? __ffsll((long long)hit) - 1 : 63;
+  int bin = 0, ab = 0;
+  if (lane == L) {
+    int a = excl;
+    bin = hi - per + 1;
+    ab = a;
+    for (int i = 0; i < per; ++i) {
+      const int h = hist[hi - i];
+      if (a + h >= need) {
+        bin = hi - i;
+        ab = a;
+        break;
+      }
+      a += h;
+    }
+  }
+  *above = __shfl(ab, L, 64);
+  return __shfl(bin, L, 64);
+}
+
+// One wave: the 12-bit bin b1 of row r's k-th key from the two-level histogram in
+// global memory (256 coarse bins, then the 16 fine bins of the coarse one), and the
+// count of keys above it.
+MK2_DEV int wave_threshold(const IdxDev& p, int r, int k, int* above) {
+  const int lane = threadIdx.x & 63;
+  const int* ch = p.chist + (size_t)r * IDX_CBINS;
+  const int* fh = p.hist + (size_t)r * IDX_BINS;
+  int c[4], sum = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    c[i] = ld_dev_i32(ch + IDX_CBINS - 1 - 4 * lane - i);
+    sum += c[i];
+  }
+  int inc = wave_incl_scan(sum), excl = inc - sum;
+  uint64_t hit = __ballot(excl < k && inc >= k);
+  int L = hit ? __ffsll((long long)hit) - 1 : 63;
+  int cb = 0, ca = 0;
+  if (lane == L) {
+    int a = excl;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (a < k && a + c[i] >= k) {
+        cb = IDX_CBINS - 1 - 4 * lane - i;
+        ca = a;
+      }
+      a += c[i];
+    }
+  }
+  cb = __shfl(cb, L, 64);
+  ca = __shfl(ca, L, 64);
+  const int f = lane < 16 ? ld_dev_i32(fh + 16 * cb + 15 - lane) : 0;
+  inc = ca + wave_incl_scan(f);
+  excl = inc - f;
+  hit = __ballot(lane < 16 && excl < k && inc >= k);
+  L = hit ? __ffsll((long long)hit) - 1 : 15;
+  *above = __shfl(excl, L, 64);
+  return 16 * cb + 15 - L;
 }
 
 // The bin (of nbins, highest first) where the count from the top reaches `need`;
@@ -298,156 +422,371 @@ MK2_DEV void select_emit(uint32_t (&d)[PER], Pos pos, uint32_t kbase, uint32_t d
     o1 += g1;
     o2 += g2;
     r3 += g3;
-    if (dst >= 0) orow[dst] = pos(i);
+    if (dst >= 0 && dst < k) st_dev_i32(orow + dst, pos(i));
   }
 }
 
-constexpr int TOPK_CAP = 8192;   // candidates kept for the exact select
-constexpr int TOPK_MAXN = 65536; // positions a row (a thread holds TOPK_MAXN / NT)
+constexpr int TOPK_CAP = 16384;  // candidates the select keeps in LDS
+constexpr int TOPK_MAXN = 65536; // positions a row
 
 struct TopkLds {
-  int hist[4096];
+  int hist[IDX_BINS];
   int scratch[1024 + 1024 / 64 + 8];
+  int offs[TOPK_MAXN / IDX_CHUNK + 8];
+  int res[4];
+  int np;                   // candidates listed in part
   uint32_t ckey[TOPK_CAP];
   uint16_t cpos[TOPK_CAP];
+  uint16_t part[TOPK_CAP];  // candidates in the threshold bin (indices into ckey)
+  int gcount[3][TOPK_CAP / 64];  // per (round, wave): group 1/2/3 counts, then their offsets
 };
 
-// The select over a whole row (when the sampled bound does not hold): the keys are
-// read again from the scores, in a function of its own so that the fast path does
-// not carry its registers.
+// Row r's histograms back to zero (every reader is done): the fine bins of each
+// nonzero coarse bin, then the coarse bins.
 template <int NT>
-__device__ __attribute__((noinline)) void topk_whole_row(const IdxDev& p, int r, uint32_t kmin,
-                                                         uint32_t kmax, TopkLds& S) {
-  constexpr int PER = TOPK_MAXN / NT;
-  const int n = p.ctx[r];
-  const int base = threadIdx.x * PER;
-  const int nvalid = max(0, min(PER, n - base));
-  const float* srow = p.scores + (size_t)r * p.max_ctx;
-  uint32_t d[PER];
+MK2_DEV void idx_clear_hist(const IdxDev& p, int r) {
+  int* ch = p.chist + (size_t)r * IDX_CBINS;
+  int* fh = p.hist + (size_t)r * IDX_BINS;
+  for (int c = threadIdx.x; c < IDX_CBINS; c += NT) {
+    if (ld_dev_i32(ch + c)) {
 #pragma unroll
-  for (int q = 0; q < PER / 4; ++q) {
-    uint4 v = nvalid > 0 ? *(const uint4*)(srow + base + 4 * q) : make_uint4(0, 0, 0, 0);
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      d[4 * q + j] = 4 * q + j < nvalid ? radix_key(__uint_as_float(w[j])) - kmin + 1u : 0u;
+      for (int i = 0; i < 16; ++i) st_dev_i32(fh + 16 * c + i, 0);
+      st_dev_i32(ch + c, 0);
+    }
   }
-  select_emit<NT, PER>(d, [&](int i) { return base + i; }, kmin - 1u, kmax - kmin + 1u, p.topk,
-                       S.hist, S.scratch, p.out + (size_t)r * p.topk);
 }
 
-// One row; NT threads, 65536 / NT consecutive positions a thread in registers.  A sample
-// (every 64th position) gives a lower bound L for the k-th key (about twice k's share
-// of the sample above it, located to 24 bits with two histograms); the keys >= L
-// (checked: at least k, at most TOPK_CAP) are compacted in position order into LDS
-// and the exact select runs over them.  Otherwise the select runs over the whole row.
+// ---------------------------------------------------------------- stage: slice
+// Task (row r, chunk): the chunk's keys whose top 12 bits are >= b1, in position
+// order, to cand[r][chunk * IDX_CHUNK ..]; their count to ccount[r][chunk].
 template <int NT>
-MK2_DEV void idx_topk(const IdxDev& p, int r, TopkLds& S) {
+MK2_DEV void idx_slice(const IdxDev& p, int r, int chunk, TopkLds& S) {
+  constexpr int PER = IDX_CHUNK / NT;  // consecutive positions a thread
+  static_assert(PER % 4 == 0, "a thread reads whole 16-byte groups of scores");
+  const int tid = threadIdx.x;
+  const int n = p.ctx[r], k = p.topk;
+  const int k_begin = chunk * IDX_CHUNK;
+  int* cnt_out = p.ccount + (size_t)r * p.nchk + chunk;
+  if (n <= k || k_begin >= n) {
+    if (tid == 0) st_dev_i32(cnt_out, 0);
+    return;
+  }
+  // the chunk's scores first: their loads overlap the threshold search
+  const float* srow = p.scores + (size_t)r * p.max_ctx;
+  const int base = k_begin + tid * PER;
+  uint4 raw[PER / 4];
+#pragma unroll
+  for (int q = 0; q < PER / 4; ++q)
+    raw[q] = base + 4 * q < n ? ldp_16(srow + base + 4 * q) : make_uint4(0, 0, 0, 0);
+  if (tid < 64) {
+    int above;
+    const int b1 = wave_threshold(p, r, k, &above);
+    if (tid == 0) S.res[0] = b1;
+  }
+  __syncthreads();
+  const uint32_t b1 = (uint32_t)S.res[0];
+  uint32_t key[PER];
+#pragma unroll
+  for (int q = 0; q < PER / 4; ++q) {
+    key[4 * q] = radix_key(__uint_as_float(raw[q].x));
+    key[4 * q + 1] = radix_key(__uint_as_float(raw[q].y));
+    key[4 * q + 2] = radix_key(__uint_as_float(raw[q].z));
+    key[4 * q + 3] = radix_key(__uint_as_float(raw[q].w));
+  }
+  int mine = 0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) mine += (base + i < n && (key[i] >> 20) >= b1) ? 1 : 0;
+  Scan3 tot;
+  int at = block_scan3<NT>(Scan3{mine, 0, 0}, &tot, S.scratch).a;
+  uint2* dst = p.cand + (size_t)r * p.max_ctx + k_begin;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    if (base + i < n && (key[i] >> 20) >= b1) {
+      st_dev_8(dst + at, make_uint2(key[i], (uint32_t)(base + i)));
+      ++at;
+    }
+  }
+  if (tid == 0) st_dev_i32(cnt_out, tot.a);
+}
+
+// The select when more than TOPK_CAP candidates remain (a row whose keys crowd into
+// the threshold bin): the same radix select and list, streamed over the candidates
+// in global memory, NT at a time in position order.
+template <int NT>
+MK2_DEV void topk_stream(const IdxDev& p, int r, uint32_t kbase, int m,
+                                                      TopkLds& S) {
   constexpr int NW = NT / 64;
-  constexpr int TOPK_PER = TOPK_MAXN / NT;  // positions a thread
-  constexpr int TOPK_CPT = TOPK_CAP / NT;   // candidates a thread
-  constexpr int SPT = TOPK_PER / 64;        // samples a thread (one per 64 positions)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int k = p.topk, nchk = p.nchk;
+  const uint2* cr = p.cand + (size_t)r * p.max_ctx;
+  int* orow = p.out + (size_t)r * k;
+  auto cand_d = [&](int j) -> uint32_t {  // candidate j (position order) - kbase
+    int lo = 0, hi = nchk;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (S.offs[mid] <= j) lo = mid;
+      else hi = mid;
+    }
+    return ldp_u32(cr + (size_t)lo * IDX_CHUNK + (j - S.offs[lo])) - kbase;
+  };
+  auto cand_pos = [&](int j) -> int {
+    int lo = 0, hi = nchk;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (S.offs[mid] <= j) lo = mid;
+      else hi = mid;
+    }
+    return (int)ldp_8(cr + (size_t)lo * IDX_CHUNK + (j - S.offs[lo])).y;
+  };
+  uint32_t dmax = 0;
+  for (int j = tid; j < m; j += NT) dmax = max(dmax, cand_d(j));
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) dmax = max(dmax, (uint32_t)__shfl_xor((int)dmax, o, 64));
+  __syncthreads();
+  if (lane == 0) S.scratch[wave] = (int)dmax;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < NW; ++w) dmax = max(dmax, (uint32_t)S.scratch[w]);
+  // radix select of the k-th d, 12 bits at a time
+  int hib = dmax ? 32 - __clz(dmax) : 32;
+  uint32_t prefix = 0;
+  int need = k;
+  while (hib > 0) {
+    const int lob = hib > 12 ? hib - 12 : 0;
+    const int nb = 1 << (hib - lob);
+    __syncthreads();
+    for (int i = tid; i < nb; i += NT) S.hist[i] = 0;
+    __syncthreads();
+    const uint32_t mask = (uint32_t)(nb - 1);
+    const uint32_t hmask = hib >= 32 ? 0u : ~((1u << hib) - 1u);
+    const uint32_t hpfx = hib >= 32 ? 0u : (prefix << hib);
+    for (int j = tid; j < m; j += NT) {
+      const uint32_t v = cand_d(j);
+      if ((v & hmask) == hpfx) atomicAdd(&S.hist[(v >> lob) & mask], 1);
+    }
+    __syncthreads();
+    int above;
+    const int b = find_bin<NT>(S.hist, nb, need, &above, S.scratch);
+    need -= above;
+    prefix = (prefix << (hib - lob)) | (uint32_t)b;
+    hib = lob;
+  }
+  const uint32_t T = prefix;
+  const int above_T = k - need, ties_needed = need;
+  const uint32_t tb = (T + kbase) >> 20;
+  // the list, NT candidates a round in position order
+  int o1 = 0, o2 = 0, r3 = 0;  // running group counts before this round
+  int n1 = 0;                  // keys of group 1 in all: counted first
+  for (int j = tid; j < m; j += NT) {
+    const uint32_t v = cand_d(j);
+    n1 += ((v + kbase) >> 20) > tb;
+  }
+  n1 = block_sum_int<NT>(n1, S.scratch);
+  for (int j0 = 0; j0 < m; j0 += NT) {
+    const int j = j0 + tid;
+    const uint32_t v = j < m ? cand_d(j) : 0u;
+    const bool g1 = j < m && ((v + kbase) >> 20) > tb;
+    const bool g2 = j < m && !g1 && v > T;
+    const bool g3 = j < m && v == T;
+    Scan3 tot;
+    const Scan3 off = block_scan3<NT>(Scan3{g1, g2, g3}, &tot, S.scratch);
+    int dst = -1;
+    if (g1) dst = o1 + off.a;
+    else if (g2) dst = n1 + o2 + off.b;
+    else if (g3 && r3 + off.c < ties_needed) dst = above_T + r3 + off.c;
+    if (dst >= 0 && dst < k) st_dev_i32(orow + dst, cand_pos(j));
+    o1 += tot.a;
+    o2 += tot.b;
+    r3 += tot.c;
+  }
+}
+
+// Exact selection over m <= TOPK_CAP candidates in LDS (position order).  Round i
+// gives thread t the candidate j = i * NT + t, so lanes read consecutive words; a
+// candidate's rank in its group is its wave's offset for the round (one scan over
+// all (round, wave) counts) plus the ballot count of the lanes below it.  Keys with
+// top 12 bits > b1 (above1 of them) all make the list; the keys of bin b1 are listed
+// (part) and the need = k - above1 largest of them found by three radix digits of
+// their low 20 bits (8, 8 and 4 bits), each located by one wave.
+template <int NT, int CPT>
+MK2_DEV void cand_select(TopkLds& S, int m, uint32_t b1, int above1, int k, int* orow) {
+  constexpr int NW = NT / 64;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
+  const int nr = (m + NT - 1) / NT;  // rounds that hold candidates (<= CPT)
+  if (tid == 0) S.np = 0;
+  __syncthreads();
+  // bin b1's candidates into part (any order)
+#pragma unroll 4
+  for (int i = 0; i < nr; ++i) {
+    const int j = i * NT + tid;
+    const bool in = j < m && (S.ckey[j] >> 20) == b1;
+    const uint64_t bal = __ballot(in);
+    if (bal) {
+      int base = 0;
+      if (lane == 0) base = atomicAdd(&S.np, __popcll(bal));
+      base = __shfl(base, 0, 64);
+      if (in) S.part[base + __popcll(bal & below)] = (uint16_t)j;
+    }
+  }
+  __syncthreads();
+  const int np = S.np;
+  int need = k - above1;
+  uint32_t prefix = 0;  // the digits found so far
+#pragma unroll 1
+  for (int pass = 0; pass < 3; ++pass) {
+    const int shift = pass == 0 ? 12 : (pass == 1 ? 4 : 0), width = pass == 2 ? 4 : 8;
+    const int hi = shift + width;  // bits above this digit are the prefix
+    if (tid < 256) S.hist[tid] = 0;
+    __syncthreads();
+    for (int j = tid; j < np; j += NT) {
+      const uint32_t v = S.ckey[S.part[j]] & 0xFFFFFu;
+      if ((v >> hi) == prefix) atomicAdd(&S.hist[(v >> shift) & ((1u << width) - 1u)], 1);
+    }
+    __syncthreads();
+    if (tid < 64) {
+      int ab;
+      const int b = wave_find_bin(S.hist, 256, need, &ab);
+      if (tid == 0) { S.res[0] = b; S.res[1] = ab; }
+    }
+    __syncthreads();
+    prefix = (prefix << width) | (uint32_t)S.res[0];
+    need -= S.res[1];
+    __syncthreads();
+  }
+  const uint32_t T = prefix;  // low 20 bits of the k-th key
+  const int ties_needed = need;
+  const int above_T = k - ties_needed;
+  // group counts per (round, wave): 1 = above bin b1, 2 = bin b1 and > T, 3 = == T
+#pragma unroll 4
+  for (int i = 0; i < nr; ++i) {
+    const int j = i * NT + tid;
+    const uint32_t key = j < m ? S.ckey[j] : 0u;
+    const bool valid = j < m, in = valid && (key >> 20) == b1;
+    const uint32_t low = key & 0xFFFFFu;
+    const int n1 = __popcll(__ballot(valid && (key >> 20) > b1));
+    const int n2 = __popcll(__ballot(in && low > T));
+    const int n3 = __popcll(__ballot(in && low == T));
+    if (lane == 0) {
+      S.gcount[0][i * NW + wave] = n1;
+      S.gcount[1][i * NW + wave] = n2;
+      S.gcount[2][i * NW + wave] = n3;
+    }
+  }
+  __syncthreads();
+  // exclusive scans of the three count sequences, in (round, wave) order
+  if (wave < 3) {
+    constexpr int PER = (CPT * NW + 63) / 64;
+    const int E = nr * NW;
+    int* g = S.gcount[wave];
+    int v[PER], sum = 0;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      v[e] = lane * PER + e < E ? g[lane * PER + e] : 0;
+      sum += v[e];
+    }
+    int run = wave_incl_scan(sum) - sum;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      if (lane * PER + e < E) g[lane * PER + e] = run;
+      run += v[e];
+    }
+  }
+  __syncthreads();
+  const int n1_all = above1;  // every key above bin b1 is a candidate
+  int* list = S.hist;         // the list is built in LDS (k <= IDX_BINS), then stored
+#pragma unroll 4
+  for (int i = 0; i < nr; ++i) {
+    const int j = i * NT + tid;
+    const uint32_t key = j < m ? S.ckey[j] : 0u;
+    const bool valid = j < m, in = valid && (key >> 20) == b1;
+    const uint32_t low = key & 0xFFFFFu;
+    const bool g1 = valid && (key >> 20) > b1, g2 = in && low > T, g3 = in && low == T;
+    const uint64_t b1m = __ballot(g1), b2m = __ballot(g2), b3m = __ballot(g3);
+    const int e = i * NW + wave;
+    int dst = -1;
+    if (g1) dst = S.gcount[0][e] + __popcll(b1m & below);
+    else if (g2) dst = n1_all + S.gcount[1][e] + __popcll(b2m & below);
+    else if (g3) {
+      const int r3 = S.gcount[2][e] + __popcll(b3m & below);
+      if (r3 < ties_needed) dst = above_T + r3;
+    }
+    if (dst >= 0 && dst < k) list[dst] = (int)S.cpos[j];
+  }
+  __syncthreads();
+  for (int i = 4 * tid; i < k; i += 4 * NT)
+    st_dev_16(orow + i, make_uint4(list[i], list[i + 1], list[i + 2], list[i + 3]));
+}
+
+// --------------------------------------------------------------- stage: select
+// Task (row r): the exact top-k of the row from its slices' candidates; then the
+// row's histograms are cleared for the next launch.
+template <int NT>
+MK2_DEV void idx_select(const IdxDev& p, int r, TopkLds& S) {
+  constexpr int CPT = TOPK_CAP / NT;  // candidates a thread
+  constexpr int TPC = NT / (TOPK_MAXN / IDX_CHUNK);  // gather threads a chunk
+  const int tid = threadIdx.x;
   const int n = p.ctx[r];
   const int k = p.topk;
   int* orow = p.out + (size_t)r * k;
   if (n <= k) {
-    for (int i = tid; i < k; i += NT) orow[i] = i < n ? i : -1;
+    for (int i = tid; i < k; i += NT) st_dev_i32(orow + i, i < n ? i : -1);
+    idx_clear_hist<NT>(p, r);
     return;
   }
-  const int base = tid * TOPK_PER;
-  const int nvalid = max(0, min(TOPK_PER, n - base));
-  uint32_t key[TOPK_PER];
-  const float* srow = p.scores + (size_t)r * p.max_ctx;
-  if (nvalid > 0) {
-#pragma unroll
-    for (int q = 0; q < TOPK_PER / 4; ++q) {
-      uint4 v = *(const uint4*)(srow + base + 4 * q);
-      key[4 * q] = radix_key(__uint_as_float(v.x));
-      key[4 * q + 1] = radix_key(__uint_as_float(v.y));
-      key[4 * q + 2] = radix_key(__uint_as_float(v.z));
-      key[4 * q + 3] = radix_key(__uint_as_float(v.w));
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < TOPK_PER; ++i) key[i] = 0u;
+  const int nchk = p.nchk;
+  // the threshold bin (wave 0) and the chunks' candidate offsets (position order)
+  if (tid < 64) {
+    int above;
+    const int b1 = wave_threshold(p, r, k, &above);
+    if (tid == 0) { S.res[0] = b1; S.res[1] = above; }
   }
-  // row min / max
-  uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
-#pragma unroll
-  for (int i = 0; i < TOPK_PER; ++i) {
-    if (i < nvalid) {
-      kmin = min(kmin, key[i]);
-      kmax = max(kmax, key[i]);
-    }
-  }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, o, 64));
-    kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o, 64));
+  {
+    // a chunk holds at most its own positions
+    const int c = tid < nchk ? min(max(ldp_i32(p.ccount + (size_t)r * nchk + tid), 0),
+                                   min(IDX_CHUNK, p.max_ctx - tid * IDX_CHUNK))
+                             : 0;
+    Scan3 tot;
+    const int off = block_scan3<NT>(Scan3{c, 0, 0}, &tot, S.scratch).a;
+    if (tid <= nchk) S.offs[tid] = tid < nchk ? off : tot.a;
   }
   __syncthreads();
-  if (lane == 0) { S.scratch[wave] = (int)kmin; S.scratch[NW + wave] = (int)kmax; }
-  for (int i = tid; i < 4096; i += NT) S.hist[i] = 0;
-  __syncthreads();
-#pragma unroll
-  for (int w = 0; w < NW; ++w) {
-    kmin = min(kmin, (uint32_t)S.scratch[w]);
-    kmax = max(kmax, (uint32_t)S.scratch[NW + w]);
-  }
-  uint32_t L = kmin;
-  bool ok = true;
-  if (n > TOPK_CAP) {
-    const int nsamp = (n + 63) / 64;  // positions 64j that exist
-    const int target = min(nsamp, (int)(2ll * k * nsamp / n) + 16);
-#pragma unroll
-    for (int j = 0; j < SPT; ++j)
-      if (64 * j < nvalid) atomicAdd(&S.hist[key[64 * j] >> 20], 1);
-    __syncthreads();
-    int a1, a2;
-    const int b1 = find_bin<NT>(S.hist, 4096, target, &a1, S.scratch);
-    for (int i = tid; i < 4096; i += NT) S.hist[i] = 0;
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < SPT; ++j)
-      if (64 * j < nvalid && (int)(key[64 * j] >> 20) == b1) atomicAdd(&S.hist[(key[64 * j] >> 8) & 0xFFFu], 1);
-    __syncthreads();
-    const int b2 = find_bin<NT>(S.hist, 4096, target - a1, &a2, S.scratch);
-    L = max(kmin, ((uint32_t)b1 << 20) | ((uint32_t)b2 << 8));
-    int cnt = 0;
-#pragma unroll
-    for (int i = 0; i < TOPK_PER; ++i) cnt += (i < nvalid && key[i] >= L) ? 1 : 0;
-    cnt = block_sum_int<NT>(cnt, S.scratch);
-    ok = cnt >= k && cnt <= TOPK_CAP;
-  }
-  if (!ok) {
-    topk_whole_row<NT>(p, r, kmin, kmax, S);
+  const uint32_t b1 = (uint32_t)S.res[0];
+  const int above1 = S.res[1];
+  const int m = S.offs[nchk];
+  // every slice has read the histograms before it published its count
+  idx_clear_hist<NT>(p, r);
+  if (m > TOPK_CAP) {
+    // keys relative to the bottom of bin b1: d >= 1 for every candidate
+    topk_stream<NT>(p, r, (b1 << 20) - 1u, m, S);
     return;
   }
-  // compact the keys >= L (position order) into LDS
-  int mine = 0;
+  // gather: TPC threads a chunk, 8 loads in flight a thread
+  {
+    const int c = tid / TPC, sub = tid % TPC;
+    if (c < nchk) {
+      const int cnt = S.offs[c + 1] - S.offs[c], o = S.offs[c];
+      const uint2* src = p.cand + (size_t)r * p.max_ctx + (size_t)c * IDX_CHUNK;
+      for (int i0 = 0; i0 < cnt; i0 += 8 * TPC) {
+        uint2 v[8];
 #pragma unroll
-  for (int i = 0; i < TOPK_PER; ++i) mine += (i < nvalid && key[i] >= L) ? 1 : 0;
-  Scan3 tot;
-  int at = block_scan3<NT>(Scan3{mine, 0, 0}, &tot, S.scratch).a;
+        for (int u = 0; u < 8; ++u) {
+          const int i = i0 + sub + u * TPC;
+          v[u] = i < cnt ? ldp_8(src + i) : make_uint2(0, 0);
+        }
 #pragma unroll
-  for (int i = 0; i < TOPK_PER; ++i) {
-    if (i < nvalid && key[i] >= L) {
-      S.ckey[at] = key[i];
-      S.cpos[at] = (uint16_t)(base + i);
-      ++at;
+        for (int u = 0; u < 8; ++u) {
+          const int i = i0 + sub + u * TPC;
+          if (i < cnt) {
+            S.ckey[o + i] = v[u].x;
+            S.cpos[o + i] = (uint16_t)v[u].y;
+          }
+        }
+      }
     }
   }
-  const int cnt = tot.a;
   __syncthreads();
-  uint32_t d[TOPK_CPT];
-#pragma unroll
-  for (int i = 0; i < TOPK_CPT; ++i) {
-    const int idx = tid * TOPK_CPT + i;
-    d[i] = idx < cnt ? S.ckey[idx] - L + 1u : 0u;
-  }
-  select_emit<NT, TOPK_CPT>(d, [&](int i) { return (int)S.cpos[tid * TOPK_CPT + i]; }, L - 1u,
-                            kmax - L + 1u, k, S.hist, S.scratch, orow);
+  cand_select<NT, CPT>(S, m, b1, above1, k, orow);
 }
 
 }  // namespace mk2

@@ -1,17 +1,20 @@
 // The K2 layer as ONE persistent launch: one 512-thread workgroup per CU walks the
-// stage list -- index scores, exact top-k, sparse-MLA splits, merge, W_UV, W_o +
-// residual, RMSNorm + activation quant, router, top-k routing, up/gate + SwiGLU,
-// down + residual -- taking task t of a stage when t = workgroup (mod grid).
+// stage list -- index scores (+ key histograms), top-k slices, top-k select,
+// sparse-MLA splits, merge, W_UV, W_o + residual, RMSNorm + activation quant,
+// router, top-k routing, up/gate + SwiGLU, down + residual -- taking task t of a
+// stage when t = workgroup (mod grid).
 //
 // There is no grid barrier.  A task that needs the results of earlier tasks waits
 // on a per-stage completion counter in the workspace (only for the producers it
-// reads: e.g. row r's top-k waits for row r's 32 score chunks).  A producer
-// publishes with a workgroup barrier, an agent-scope release fence and an atomic
-// increment; a consumer polls the counter, then takes an agent-scope acquire fence.
-// Dependencies point only to earlier stages and every workgroup is resident (one
-// per CU, grid = CU count), so every wait ends; each wait is also bounded (spin
-// limit) and on expiry sets a sticky error word that releases every other wait, so
-// the launch always drains.  The last workgroup to finish resets the counters.
+// reads: e.g. row r's slices wait for row r's score chunks).  Everything handed
+// from one workgroup to another is written and read with device-coherent (sc1)
+// accesses, so a hand-off needs no cache maintenance: a producer drains its stores,
+// passes a workgroup barrier and increments the counter (relaxed, agent scope); a
+// consumer polls the counter, passes a barrier and reads.  Dependencies point only
+// to earlier stages and every workgroup is resident (one per CU, grid = CU count),
+// so every wait ends; each wait is also bounded (spin limit) and on expiry sets a
+// sticky error word that releases every other wait, so the launch always drains.
+// The last workgroup to finish resets the counters.
 #include "indexer_stages.h"
 #include "mk2_host.h"
 #include "mla_stages.h"
@@ -23,11 +26,12 @@ constexpr int K2_NT = 512;
 
 // sync block (int words at the start of the layer workspace)
 enum : int {
-  SY_SCORE = 0,   // [32] score chunks done, per row
-  SY_TOPK = 32,   // [32] top-k done, per row
-  SY_SPLIT = 64,  // [32] attention splits done, per row
-  SY_MERGE = 96,  // [16] merged rows, per head
-  SY_UV = 112,
+  SY_SCORE = 0,    // [32] score chunks done, per row
+  SY_SLICE = 32,   // [32] top-k slices done, per row
+  SY_TOPK = 64,    // [32] top-k done, per row
+  SY_SPLIT = 96,   // [32] attention splits done, per row
+  SY_MERGE = 128,  // [16] merged rows, per head
+  SY_UV = 144,
   SY_OPROJ,
   SY_PREP,
   SY_ROUTER,
@@ -35,7 +39,7 @@ enum : int {
   SY_UP,
   SY_DONE,        // workgroups finished (the last one resets)
   SY_ERR,         // sticky: a wait ran out of its spin limit
-  SY_WORDS = 128
+  SY_WORDS = 256
 };
 
 struct K2Dev {
@@ -50,14 +54,14 @@ struct K2Dev {
 };
 
 // timeline: per stage s, stamps 3s (enter), 3s+1 (first input ready), 3s+2 (leave)
-constexpr int K2_STAGES = 11, K2_STAMPS = 3 * K2_STAGES + 1;
+constexpr int K2_STAGES = 12, K2_STAMPS = 3 * K2_STAGES + 1;
 
 MK2_DEV void k2_stamp(const K2Dev& p, int i) {
   if (p.timeline && threadIdx.x == 0) p.timeline[(size_t)blockIdx.x * K2_STAMPS + i] = __builtin_amdgcn_s_memrealtime();
 }
 
 union K2Lds {
-  int pages[IDX_CHUNK / 64];
+  IdxScoreLds score;
   TopkLds topk;
   MlaSplitLds split;
   float merge[2 * 1024 + 8];
@@ -71,17 +75,16 @@ union K2Lds {
   } down;
   struct {
     float logits[32 * 256];
-    int slot[256 + 4 * (K2_NT / 64) + 24 * (K2_NT / 64)];
+    int slot[256 + 28 * (K2_NT / 64) + 2 * 32 * 8];
   } route;
   float red[(K2_NT / 64) * 2 * 64 * 4];
 };
 
+// publish a finished task: every thread's stores drained, then one increment
 MK2_DEV void k2_signal(int* c) {
+  drain_memory();
   __syncthreads();
-  if (threadIdx.x == 0) {
-    __threadfence();
-    atomicAdd(c, 1);
-  }
+  if (threadIdx.x == 0) __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 MK2_DEV void k2_wait(const K2Dev& p, int slot, int target, int stamp = -1) {
@@ -95,9 +98,8 @@ MK2_DEV void k2_wait(const K2Dev& p, int slot, int target, int stamp = -1) {
         atomicOr(err, 1);
         break;
       }
-      __builtin_amdgcn_s_sleep(2);
+      __builtin_amdgcn_s_sleep(1);
     }
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     if (stamp >= 0 && p.timeline) p.timeline[(size_t)blockIdx.x * K2_STAMPS + stamp] = __builtin_amdgcn_s_memrealtime();
   }
   __syncthreads();
@@ -108,103 +110,113 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
   __shared__ K2Lds S;
   const int G = gridDim.x, b = blockIdx.x;
   const int R = p.rows;
-  // ---- index scores
-  k2_stamp(p, 0);
-  const int nchk = (p.idx.max_ctx + IDX_CHUNK - 1) / IDX_CHUNK;
+  int st = 0;  // timeline stage
+  // ---- index scores + row key histograms
+  k2_stamp(p, 3 * st);
+  const int nchk = p.idx.nchk;
   for (int t = b; t < R * nchk; t += G) {
-    idx_score<K2_NT>(p.idx, t / nchk, t % nchk, S.pages);
+    idx_score<K2_NT>(p.idx, t / nchk, t % nchk, S.score);
     k2_signal(p.sync + SY_SCORE + t / nchk);
   }
-  k2_stamp(p, 2);
-  // ---- exact top-k of each row
-  k2_stamp(p, 3);
+  k2_stamp(p, 3 * st++ + 2);
+  // ---- top-k slices: each chunk's candidates
+  k2_stamp(p, 3 * st);
+  for (int t = b; t < R * nchk; t += G) {
+    const int r = t / nchk;
+    k2_wait(p, SY_SCORE + r, nchk, t == b ? 3 * st + 1 : -1);
+    idx_slice<K2_NT>(p.idx, r, t % nchk, S.topk);
+    k2_signal(p.sync + SY_SLICE + r);
+  }
+  k2_stamp(p, 3 * st++ + 2);
+  // ---- exact top-k of each row over its candidates
+  k2_stamp(p, 3 * st);
   for (int t = b; t < R; t += G) {
-    k2_wait(p, SY_SCORE + t, nchk, t == b ? 4 : -1);
-    idx_topk<K2_NT>(p.idx, t, S.topk);
+    k2_wait(p, SY_SLICE + t, nchk, t == b ? 3 * st + 1 : -1);
+    idx_select<K2_NT>(p.idx, t, S.topk);
     k2_signal(p.sync + SY_TOPK + t);
   }
-  k2_stamp(p, 5);
+  k2_stamp(p, 3 * st++ + 2);
   // ---- sparse-MLA splits
-  k2_stamp(p, 6);
+  k2_stamp(p, 3 * st);
   const int ns = p.mla.nsplit;
   for (int t = b; t < R * ns; t += G) {
     const int r = t / ns;
-    k2_wait(p, SY_TOPK + r, 1, t == b ? 7 : -1);
+    k2_wait(p, SY_TOPK + r, 1, t == b ? 3 * st + 1 : -1);
     mla_split<K2_NT>(p.mla, r, t % ns, S.split);
     k2_signal(p.sync + SY_SPLIT + r);
   }
-  k2_stamp(p, 8);
+  k2_stamp(p, 3 * st++ + 2);
   // ---- merge of the splits, per (row, head)
-  k2_stamp(p, 9);
+  k2_stamp(p, 3 * st);
   for (int t = b; t < R * MLA_HEADS; t += G) {
     const int r = t / MLA_HEADS, h = t % MLA_HEADS;
-    k2_wait(p, SY_SPLIT + r, ns, t == b ? 10 : -1);
+    k2_wait(p, SY_SPLIT + r, ns, t == b ? 3 * st + 1 : -1);
     mla_merge<K2_NT>(p.mla, r, h, S.merge);
     k2_signal(p.sync + SY_MERGE + h);
   }
-  k2_stamp(p, 11);
+  k2_stamp(p, 3 * st++ + 2);
   // ---- W_UV, per (head, 16 v rows)
-  k2_stamp(p, 12);
+  k2_stamp(p, 3 * st);
   const int vtn = p.mla.v_dim / 16;
   for (int t = b; t < MLA_HEADS * vtn; t += G) {
     const int h = t / vtn;
-    k2_wait(p, SY_MERGE + h, R, t == b ? 13 : -1);
+    k2_wait(p, SY_MERGE + h, R, t == b ? 3 * st + 1 : -1);
     mla_uv<K2_NT, NCG>(p.mla, h, t % vtn, S.red);
     k2_signal(p.sync + SY_UV);
   }
-  k2_stamp(p, 14);
+  k2_stamp(p, 3 * st++ + 2);
   // ---- W_o + residual, per 16 hidden rows
-  k2_stamp(p, 15);
+  k2_stamp(p, 3 * st);
   const int ht = p.mla.hidden / 16;
   for (int t = b; t < ht; t += G) {
-    k2_wait(p, SY_UV, MLA_HEADS * vtn, t == b ? 16 : -1);
+    k2_wait(p, SY_UV, MLA_HEADS * vtn, t == b ? 3 * st + 1 : -1);
     mla_oproj<K2_NT, NCG>(p.mla, t, S.red);
     k2_signal(p.sync + SY_OPROJ);
   }
-  k2_stamp(p, 17);
+  k2_stamp(p, 3 * st++ + 2);
   // ---- RMSNorm + activation quant, per row
-  k2_stamp(p, 18);
+  k2_stamp(p, 3 * st);
   for (int t = b; t < R; t += G) {
-    k2_wait(p, SY_OPROJ, ht, t == b ? 19 : -1);
+    k2_wait(p, SY_OPROJ, ht, t == b ? 3 * st + 1 : -1);
     moe_prep<K2_NT>(p.moe, t, S.red);
     k2_signal(p.sync + SY_PREP);
   }
-  k2_stamp(p, 20);
+  k2_stamp(p, 3 * st++ + 2);
   // ---- router GEMV, per (16 experts, k-chunk)
-  k2_stamp(p, 21);
+  k2_stamp(p, 3 * st);
   const int et = p.moe.E / 16, nrt = et * p.moe.KC;
   for (int t = b; t < nrt; t += G) {
-    k2_wait(p, SY_PREP, R, t == b ? 22 : -1);
+    k2_wait(p, SY_PREP, R, t == b ? 3 * st + 1 : -1);
     moe_router<K2_NT, NCG>(p.moe, t % et, t / et, S.red);
     k2_signal(p.sync + SY_ROUTER);
   }
-  k2_stamp(p, 23);
+  k2_stamp(p, 3 * st++ + 2);
   // ---- top-k routing (one task)
-  k2_stamp(p, 24);
+  k2_stamp(p, 3 * st);
   for (int t = b; t < 1; t += G) {
-    k2_wait(p, SY_ROUTER, nrt, t == b ? 25 : -1);
+    k2_wait(p, SY_ROUTER, nrt, t == b ? 3 * st + 1 : -1);
     moe_route<K2_NT>(p.moe, S.route.logits, S.route.slot);
     k2_signal(p.sync + SY_ROUTE);
   }
-  k2_stamp(p, 26);
+  k2_stamp(p, 3 * st++ + 2);
   // ---- up/gate + SwiGLU: routed slots (after routing), then the shared expert
-  k2_stamp(p, 27);
+  k2_stamp(p, 3 * st);
   const int up_r = p.moe.Dmax * (p.moe.I / 32);
   const int up_total = up_r + p.moe.n_shared * (p.moe.SI / 32);
   for (int t = b; t < up_total; t += G) {
-    if (t < up_r) k2_wait(p, SY_ROUTE, 1, t == b ? 28 : -1);
-    else k2_wait(p, SY_PREP, R, t == b ? 28 : -1);
+    if (t < up_r) k2_wait(p, SY_ROUTE, 1, t == b ? 3 * st + 1 : -1);
+    else k2_wait(p, SY_PREP, R, t == b ? 3 * st + 1 : -1);
     moe_upgate<K2_NT, NCG>(p.moe, t, S.up.red, S.up.midf);
     k2_signal(p.sync + SY_UP);
   }
-  k2_stamp(p, 29);
+  k2_stamp(p, 3 * st++ + 2);
   // ---- down + route weighting + residual, per 16 hidden rows
-  k2_stamp(p, 30);
+  k2_stamp(p, 3 * st);
   for (int t = b; t < p.moe.H / 16; t += G) {
-    k2_wait(p, SY_UP, up_total, t == b ? 31 : -1);
+    k2_wait(p, SY_UP, up_total, t == b ? 3 * st + 1 : -1);
     moe_down<K2_NT, NCG>(p.moe, t, S.down.red, S.down.act);
   }
-  k2_stamp(p, 32);
+  k2_stamp(p, 3 * st + 2);
   // ---- the last workgroup out resets the counters for the next launch
   __syncthreads();
   if (threadIdx.x == 0) {

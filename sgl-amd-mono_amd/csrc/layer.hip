@@ -9,7 +9,7 @@
 namespace mk2 {
 
 int idx_fill(const mk2_indexer_args* a, IdxDev* d);
-size_t idx_carve(const mk2_indexer_shape* s, void* base, float** scores, int** topk);
+size_t idx_carve(const mk2_indexer_shape* s, void* base, IdxDev* d);
 void idx_enqueue(const IdxDev& d, hipStream_t st);
 int mla_fill(const mk2_mla_args* a, MlaDev* d);
 size_t mla_carve(const mk2_mla_shape* s, void* base, MlaDev* d);
@@ -20,7 +20,7 @@ int moe_enqueue(const MoeDev& d, hipStream_t st);
 int k2_persistent_enqueue(const IdxDev& idx, const MlaDev& mla, const MoeDev& moe, int* sync,
                           int* status, uint64_t* timeline, int rows, int spin_limit, hipStream_t st);
 
-constexpr int LAYER_SYNC_BYTES = 512;
+constexpr int LAYER_SYNC_BYTES = 1024;
 
 struct LayerPlan {
   IdxDev idx;
@@ -55,7 +55,7 @@ int layer_plan(const mk2_layer_args* a, void* ws, LayerPlan* L, size_t* bytes) {
   MK2_REQUIRE(a->spin_limit >= 0, "layer: spin_limit must be >= 0");
   Carver c(ws);
   int* sync = c.take<int>(LAYER_SYNC_BYTES / 4);
-  const size_t b_idx = idx_carve(&is, nullptr, nullptr, nullptr);
+  const size_t b_idx = idx_carve(&is, nullptr, nullptr);
   const size_t b_mla = mla_carve(&ms, nullptr, nullptr);
   const size_t b_moe = moe_carve(&es, nullptr, nullptr);
   char* p_idx = c.take<char>(b_idx);
@@ -65,11 +65,7 @@ int layer_plan(const mk2_layer_args* a, void* ws, LayerPlan* L, size_t* bytes) {
   *bytes = c.bytes();
   if (!ws) return MK2_OK;
   L->sync = sync;
-  float* sc;
-  int* tk;
-  idx_carve(&is, p_idx, &sc, &tk);
-  if (!L->idx.scores) L->idx.scores = sc;
-  if (!L->idx.out) L->idx.out = tk;
+  idx_carve(&is, p_idx, &L->idx);
   mla_carve(&ms, p_mla, &L->mla);
   moe_carve(&es, p_moe, &L->moe);
   if (a->moe.logits) L->moe.logits = a->moe.logits;

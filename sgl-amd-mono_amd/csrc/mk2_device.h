@@ -151,4 +151,40 @@ MK2_DEV float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 template <typename T>
 MK2_DEV T ld_nt(const T* p) { return __builtin_nontemporal_load(p); }
 
+// ----------------------------------------------------------------- hand-off memory
+// Data that one workgroup hands to another inside a launch.  The L2 of one XCD is not
+// coherent with the others for plain accesses, so:
+//  - producers store with device-coherent stores (relaxed agent-scope atomic stores:
+//    sc1, write-through), drain them (s_waitcnt) and only then publish a counter;
+//  - consumers read PUBLISHED data -- written once per launch and read only after its
+//    counter was seen -- with plain loads (ldp_*).  A launch starts with invalidated
+//    caches and nothing on any XCD reads such data before it is published, so the
+//    first read of a line misses the L2 and fetches the stored value;
+//  - data built by device atomics (histograms) is read device-coherently (ld_dev_*).
+// No cache write-back or invalidate is needed (an agent-scope fence costs both, for
+// the whole L2).
+#define MK2_DEV_LD(T, p) __hip_atomic_load((const T*)(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+#define MK2_DEV_ST(T, p, v) __hip_atomic_store((T*)(p), (T)(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+MK2_DEV int ld_dev_i32(const int* p) { return MK2_DEV_LD(int, p); }
+MK2_DEV uint32_t ldp_u8(const void* p) { return *(const uint8_t*)p; }
+MK2_DEV uint32_t ldp_u16(const void* p) { return *(const uint16_t*)p; }
+MK2_DEV uint32_t ldp_u32(const void* p) { return *(const uint32_t*)p; }
+MK2_DEV int ldp_i32(const int* p) { return *p; }
+MK2_DEV float ldp_f32(const float* p) { return *p; }
+MK2_DEV uint2 ldp_8(const void* p) { return *(const uint2*)p; }
+MK2_DEV uint4 ldp_16(const void* p) { return *(const uint4*)p; }
+MK2_DEV float4 ldp_f32x4(const float* p) { return *(const float4*)p; }
+MK2_DEV void st_dev_u8(void* p, uint32_t v) { MK2_DEV_ST(uint8_t, p, v); }
+MK2_DEV void st_dev_u16(void* p, uint32_t v) { MK2_DEV_ST(uint16_t, p, v); }
+MK2_DEV void st_dev_u32(void* p, uint32_t v) { MK2_DEV_ST(uint32_t, p, v); }
+MK2_DEV void st_dev_i32(int* p, int v) { MK2_DEV_ST(int, p, v); }
+MK2_DEV void st_dev_f32(float* p, float v) { MK2_DEV_ST(float, p, v); }
+MK2_DEV void st_dev_8(void* p, uint2 v) { MK2_DEV_ST(uint64_t, p, ((uint64_t)v.y << 32) | v.x); }
+MK2_DEV void st_dev_16(void* p, uint4 v) {
+  MK2_DEV_ST(uint64_t, p, ((uint64_t)v.y << 32) | v.x);
+  MK2_DEV_ST(uint64_t, (uint64_t*)p + 1, ((uint64_t)v.w << 32) | v.z);
+}
+// every memory access of this thread has completed (stores are device-visible)
+MK2_DEV void drain_memory() { __builtin_amdgcn_s_waitcnt(0); }
+
 }  // namespace mk2

@@ -73,10 +73,10 @@ MK2_DEV void mla_split(const MlaDev& p, int r, int s, MlaSplitLds& L) {
   }
   // resolve the 64 positions to cache rows (one dependent round), with their scales
   if (tid < MLA_SPLIT) {
-    const int pos = selr[tid];
+    const int pos = ldp_i32(selr + tid);
     int row = -1;
     float ksc = 0.f;
-    if (pos >= 0) {
+    if (pos >= 0 && pos < p.stride * 64) {
       row = ptr[pos >> 6] * 64 + (pos & 63);
       ksc = p.kv_scale[row];
     }
@@ -173,8 +173,8 @@ MK2_DEV void mla_split(const MlaDev& p, int r, int s, MlaSplitLds& L) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int hd = 4 * g + i;
-      mlo[hd * 2] = m[i];
-      mlo[hd * 2 + 1] = L.red[0][hd] + L.red[1][hd] + L.red[2][hd] + L.red[3][hd];
+      st_dev_f32(mlo + hd * 2, m[i]);
+      st_dev_f32(mlo + hd * 2 + 1, L.red[0][hd] + L.red[1][hd] + L.red[2][hd] + L.red[3][hd]);
     }
   }
   // PV: wave w takes dim tiles TPW*w .. +TPW-1 (16 dims each), 2 key steps of 32
@@ -194,7 +194,7 @@ MK2_DEV void mla_split(const MlaDev& p, int r, int s, MlaSplitLds& L) {
       o = mfma_bf16(pa[ks], e4m3x8_to_bf16(vw.x, vw.y), o);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) orow[(4 * g + i) * MLA_LAT + d0 + c16] = o[i];
+    for (int i = 0; i < 4; ++i) st_dev_f32(orow + (4 * g + i) * MLA_LAT + d0 + c16, o[i]);
   }
   __syncthreads();
 }
@@ -210,9 +210,9 @@ MK2_DEV void mla_merge(const MlaDev& p, int r, int h, float* lds) {
   float* lsum = lds + ns;    // [ns] l_s
   const float* ml = p.part_ml + ((size_t)r * ns * MLA_HEADS + h) * 2;
   for (int s = tid; s < ns; s += NT) {
-    const float2 v = *(const float2*)(ml + (size_t)s * MLA_HEADS * 2);
-    wgt[s] = v.x;
-    lsum[s] = v.y;
+    const uint2 v = ldp_8(ml + (size_t)s * MLA_HEADS * 2);
+    wgt[s] = __uint_as_float(v.x);
+    lsum[s] = __uint_as_float(v.y);
   }
   __syncthreads();
   float M = -INFINITY;
@@ -233,7 +233,7 @@ MK2_DEV void mla_merge(const MlaDev& p, int r, int h, float* lds) {
     for (int u = 0; u < U; ++u) {
 #pragma unroll
       for (int d = 0; d < DPT; ++d)
-        v[u][d] = s0 + u < ns ? po[(size_t)(s0 + u) * MLA_HEADS * MLA_LAT + d] : 0.f;
+        v[u][d] = s0 + u < ns ? ldp_f32(po + (size_t)(s0 + u) * MLA_HEADS * MLA_LAT + d) : 0.f;
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -247,7 +247,7 @@ MK2_DEV void mla_merge(const MlaDev& p, int r, int h, float* lds) {
 #pragma unroll
   for (int d = 0; d < DPT; ++d) {
     o[d] *= inv;
-    p.o_lat[at + d] = f32_to_bf16(o[d]);
+    st_dev_u16(p.o_lat + at + d, f32_to_bf16(o[d]));
     if (p.o_lat_f32) p.o_lat_f32[at + d] = o[d];
   }
   __syncthreads();
@@ -272,7 +272,7 @@ MK2_DEV void mla_uv(const MlaDev& p, int h, int vt, float* red) {
     if (row < p.rows) {
       const bf16_t* src = p.o_lat + ((size_t)row * MLA_HEADS + h) * MLA_LAT + kb * 128 + 32 * g;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) b[q] = __builtin_bit_cast(bf16x8, *(const uint4*)(src + 8 * q));
+      for (int q = 0; q < 4; ++q) b[q] = __builtin_bit_cast(bf16x8, ldp_16(src + 8 * q));
     } else {
 #pragma unroll
       for (int q = 0; q < 4; ++q) b[q] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
@@ -292,7 +292,7 @@ MK2_DEV void mla_uv(const MlaDev& p, int h, int vt, float* red) {
     float v = 0.f;
 #pragma unroll
     for (int w = 0; w < 4; ++w) v += red[((w * NCG + cg) * 64 + l) * 4 + i];
-    p.o[(size_t)row * (MLA_HEADS * p.v_dim) + h * p.v_dim + vt * 16 + n16] = f32_to_bf16(v);
+    st_dev_u16(p.o + (size_t)row * (MLA_HEADS * p.v_dim) + h * p.v_dim + vt * 16 + n16, f32_to_bf16(v));
   }
   __syncthreads();
 }
@@ -316,9 +316,9 @@ MK2_DEV void mla_oproj(const MlaDev& p, int nt, float* red) {
       const int row = cg * 16 + c16;
       bf16x8 b[4];
       if (row < p.rows) {
-        const uint4* src = (const uint4*)(p.o + (size_t)row * K + kb * 128 + 32 * g);
+        const bf16_t* src = p.o + (size_t)row * K + kb * 128 + 32 * g;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) b[q] = __builtin_bit_cast(bf16x8, src[q]);
+        for (int q = 0; q < 4; ++q) b[q] = __builtin_bit_cast(bf16x8, ldp_16(src + 8 * q));
       } else {
 #pragma unroll
         for (int q = 0; q < 4; ++q) b[q] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
@@ -338,7 +338,7 @@ MK2_DEV void mla_oproj(const MlaDev& p, int nt, float* red) {
     for (int w = 0; w < NW; ++w) v += red[((w * NCG + cg) * 64 + l) * 4 + i];
     const size_t o = (size_t)row * p.hidden + nt * 16 + n16;
     if (p.h) v += bf16_to_f32(p.h[o]);
-    p.out[o] = f32_to_bf16(v);
+    st_dev_u16(p.out + o, f32_to_bf16(v));
   }
   __syncthreads();
 }

@@ -129,7 +129,8 @@ int moe_enqueue(const MoeDev& d, hipStream_t st) {
   k_moe_prep<<<d.M, 256, 0, st>>>(d);
   if (ncg == 1) k_moe_router<1><<<dim3(d.E / 16, d.KC), 256, 0, st>>>(d);
   else k_moe_router<2><<<dim3(d.E / 16, d.KC), 256, 0, st>>>(d);
-  const size_t route_lds = (size_t)d.M * d.E * 4 + (size_t)(d.E + 4 * (ROUTE_NT / 64) + 24 * (ROUTE_NT / 64)) * 4;
+  const size_t route_lds =
+      (size_t)d.M * d.E * 4 + (size_t)(d.E + 28 * (ROUTE_NT / 64) + 2 * d.M * d.topk) * 4;
   k_moe_route<<<1, ROUTE_NT, route_lds, st>>>(d);
   const int up_tasks = d.Dmax * (d.I / 32) + d.n_shared * (d.SI / 32);
   if (ncg == 1) k_moe_upgate<1><<<up_tasks, MOE_NT, 0, st>>>(d);

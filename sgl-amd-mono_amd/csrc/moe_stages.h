@@ -68,7 +68,7 @@ MK2_DEV void moe_prep(const MoeDev& p, int r, float* lds) {
   if (p.norm) {
     float ss = 0.f;
     for (int k = tid * 8; k < p.H; k += NT * 8) {
-      uint4 v = *(const uint4*)(xr + k);
+      uint4 v = ldp_16(xr + k);
       uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -83,7 +83,7 @@ MK2_DEV void moe_prep(const MoeDev& p, int r, float* lds) {
     float f[32];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      uint4 v = *(const uint4*)(xr + blk * 32 + q * 8);
+      uint4 v = ldp_16(xr + blk * 32 + q * 8);
       uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -110,7 +110,7 @@ MK2_DEV void moe_prep(const MoeDev& p, int r, float* lds) {
     uint4* dst = (uint4*)(p.xn + (size_t)r * p.H + blk * 32);
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-      dst[q] = make_uint4(packed[4 * q], packed[4 * q + 1], packed[4 * q + 2], packed[4 * q + 3]);
+      st_dev_16(dst + q, make_uint4(packed[4 * q], packed[4 * q + 1], packed[4 * q + 2], packed[4 * q + 3]));
     if (p.fmt == MK2_FMT_MXFP4) {
       float amax = 0.f;
 #pragma unroll
@@ -123,19 +123,20 @@ MK2_DEV void moe_prep(const MoeDev& p, int r, float* lds) {
         qw[i] = f32x4_to_e4m3x4(f[4 * i] * inv, f[4 * i + 1] * inv, f[4 * i + 2] * inv,
                                 f[4 * i + 3] * inv);
       uint4* qd = (uint4*)(p.xq + (size_t)r * p.H + blk * 32);
-      qd[0] = make_uint4(qw[0], qw[1], qw[2], qw[3]);
-      qd[1] = make_uint4(qw[4], qw[5], qw[6], qw[7]);
-      p.xs[(size_t)r * (p.H / 32) + blk] = (uint8_t)code;
+      st_dev_16(qd, make_uint4(qw[0], qw[1], qw[2], qw[3]));
+      st_dev_16(qd + 1, make_uint4(qw[4], qw[5], qw[6], qw[7]));
+      st_dev_u8(p.xs + (size_t)r * (p.H / 32) + blk, code);
     }
   }
 }
 
+// B operands are activations produced inside the launch: device-coherent loads.
 // B operand: 32 bf16 of row `row` at k0 (4 MFMA k-steps), zeros past the last row
 MK2_DEV void load_b_bf16(const bf16_t* base, int row, int nrows, int ld, int k0, bf16x8* b) {
   if (row < nrows) {
-    const uint4* s = (const uint4*)(base + (size_t)row * ld + k0);
+    const bf16_t* s = base + (size_t)row * ld + k0;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) b[q] = __builtin_bit_cast(bf16x8, s[q]);
+    for (int q = 0; q < 4; ++q) b[q] = __builtin_bit_cast(bf16x8, ldp_16(s + 8 * q));
   } else {
 #pragma unroll
     for (int q = 0; q < 4; ++q) b[q] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
@@ -148,7 +149,7 @@ MK2_DEV i32x8 load_b_fp8(const uint8_t* base, int row, int nrows, int ld, int kb
   i32x8 b = {0, 0, 0, 0, 0, 0, 0, 0};
   if (row < nrows) {
     const uint8_t* s = base + (size_t)row * ld + kb0 + 16 * g;
-    uint4 u0 = *(const uint4*)s, u1 = *(const uint4*)(s + 64);
+    uint4 u0 = ldp_16(s), u1 = ldp_16(s + 64);
     b[0] = u0.x; b[1] = u0.y; b[2] = u0.z; b[3] = u0.w;
     b[4] = u1.x; b[5] = u1.y; b[6] = u1.z; b[7] = u1.w;
   }
@@ -211,7 +212,7 @@ MK2_DEV void moe_router(const MoeDev& p, int nt, int kc, float* red) {
     float v = 0.f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) v += red[((w * NCG + c) * 64 + l) * 4 + i];
-    p.logit_part[((size_t)kc * p.M + row) * p.E + nt * 16 + e16] = v;
+    st_dev_f32(p.logit_part + ((size_t)kc * p.M + row) * p.E + nt * 16 + e16, v);
   }
   __syncthreads();
 }
@@ -221,7 +222,8 @@ MK2_DEV void moe_router(const MoeDev& p, int nt, int kc, float* red) {
 // finds the top-k by (key desc, expert asc) with a bitwise search for the k-th key
 // (ballot counts, no shuffles), ranks the picks, and computes their weights; then
 // the distinct-expert list (ascending) and the dense route-weight table rw.
-// lds_logits: M*E floats; lds_slot: E + 4*NW ints (+ 24 a wave of pick scratch).
+// lds_logits: M*E floats; lds_slot: E + 4*NW ints, 24 a wave of pick scratch, then
+// the picks' ids and weights (2*M*topk).
 template <int NT>
 MK2_DEV void moe_route(const MoeDev& p, float* lds_logits, int* lds_slot) {
   constexpr int NW = NT / 64;
@@ -233,7 +235,7 @@ MK2_DEV void moe_route(const MoeDev& p, float* lds_logits, int* lds_slot) {
       float4 t[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u)
-        t[u] = kc0 + u < p.KC ? *(const float4*)(p.logit_part + (size_t)(kc0 + u) * ME + idx)
+        t[u] = kc0 + u < p.KC ? ldp_f32x4(p.logit_part + (size_t)(kc0 + u) * ME + idx)
                               : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
@@ -247,6 +249,8 @@ MK2_DEV void moe_route(const MoeDev& p, float* lds_logits, int* lds_slot) {
   __syncthreads();
   const int per = p.E / 64;  // experts a lane holds: e = lane + 64 * i
   int* pick = lds_slot + p.E + 4 * NW + wave * 24;  // [8 keys][8 ids][8 values]
+  int* lds_ids = lds_slot + p.E + 28 * NW;          // [M][topk]
+  float* lds_w = (float*)(lds_ids + p.M * p.topk);  // [M][topk]
   for (int r = wave; r < p.M; r += NW) {
     uint32_t key[4] = {0u, 0u, 0u, 0u};
     float sv[4] = {0.f, 0.f, 0.f, 0.f};
@@ -321,8 +325,10 @@ MK2_DEV void moe_route(const MoeDev& p, float* lds_logits, int* lds_slot) {
       w = ex / wave_sum(ex);
     }
     if (lane < p.topk) {
-      p.topk_ids[r * p.topk + rank] = e;
-      p.topk_w[r * p.topk + rank] = w;
+      st_dev_i32(p.topk_ids + r * p.topk + rank, e);
+      st_dev_f32(p.topk_w + r * p.topk + rank, w);
+      lds_ids[r * p.topk + rank] = e;
+      lds_w[r * p.topk + rank] = w;
       lds_slot[e] = 1;
     }
     __builtin_amdgcn_wave_barrier();
@@ -358,16 +364,18 @@ MK2_DEV void moe_route(const MoeDev& p, float* lds_logits, int* lds_slot) {
     const int e = tid * per_t + i;
     if (i < per_t && e < p.E) {
       lds_slot[e] = flag[i] ? pos : -1;
-      if (flag[i]) p.act[1 + pos] = e;
+      if (flag[i]) st_dev_i32(p.act + 1 + pos, e);
       pos += flag[i];
     }
   }
-  if (tid == 0) p.act[0] = total;
-  for (int idx = tid; idx < total * 32; idx += NT) p.rw[idx] = 0.f;
+  if (tid == 0) st_dev_i32(p.act, total);
+  for (int idx = tid; idx < total * 32; idx += NT) st_dev_f32(p.rw + idx, 0.f);
+  // the zeros land before any weight below overwrites one of them
+  drain_memory();
   __syncthreads();
   for (int idx = tid; idx < p.M * p.topk; idx += NT) {
     const int r = idx / p.topk;
-    p.rw[lds_slot[p.topk_ids[idx]] * 32 + r] = p.topk_w[idx];
+    st_dev_f32(p.rw + lds_slot[lds_ids[idx]] * 32 + r, lds_w[idx]);
   }
 }
 
@@ -387,8 +395,9 @@ MK2_DEV void moe_upgate(const MoeDev& p, int t, float* red, float* midf) {
   if (t < p.Dmax * chunks_r) {
     j = t / chunks_r;
     c = t % chunks_r;
-    if (j >= p.act[0]) return;
-    e = p.act[1 + j];
+    if (j >= ldp_i32(p.act)) return;
+    e = ldp_i32(p.act + 1 + j);
+    if (e < 0 || e >= p.E) return;
   } else {
     shared = true;
     c = t - p.Dmax * chunks_r;
@@ -425,7 +434,7 @@ MK2_DEV void moe_upgate(const MoeDev& p, int t, float* red, float* midf) {
           for (int cg = 0; cg < NCG; ++cg) {
             const int row = cg * 16 + (lane & 15);
             b[u][cg] = load_b_fp8(p.xq, row, p.M, p.H, kb * 128, g);
-            sb[u][cg] = row < p.M ? p.xs[(size_t)row * (p.H / 32) + kb * 4 + g] : 127;
+            sb[u][cg] = row < p.M ? (int)ldp_u8(p.xs + (size_t)row * (p.H / 32) + kb * 4 + g) : 127;
           }
         }
       }
@@ -514,15 +523,15 @@ MK2_DEV void moe_upgate(const MoeDev& p, int t, float* red, float* midf) {
         qw[i] = f32x4_to_e4m3x4(midf[s * 33 + 4 * i] * inv, midf[s * 33 + 4 * i + 1] * inv,
                                 midf[s * 33 + 4 * i + 2] * inv, midf[s * 33 + 4 * i + 3] * inv);
       uint4* dst = (uint4*)(p.mid_q + ((size_t)j * p.M + s) * p.I + c * 32);
-      dst[0] = make_uint4(qw[0], qw[1], qw[2], qw[3]);
-      dst[1] = make_uint4(qw[4], qw[5], qw[6], qw[7]);
-      p.mid_s[((size_t)j * p.M + s) * (p.I / 32) + c] = (uint8_t)code;
+      st_dev_16(dst, make_uint4(qw[0], qw[1], qw[2], qw[3]));
+      st_dev_16(dst + 1, make_uint4(qw[4], qw[5], qw[6], qw[7]));
+      st_dev_u8(p.mid_s + ((size_t)j * p.M + s) * (p.I / 32) + c, code);
     }
   } else {
     bf16_t* dst = shared ? p.mid_sh : p.mid_b + (size_t)j * p.M * p.I;
     for (int idx = threadIdx.x; idx < 32 * p.M; idx += NT) {
       const int n = idx & 31, s = idx >> 5;
-      dst[(size_t)s * I + c * 32 + n] = f32_to_bf16(midf[s * 33 + n]);
+      st_dev_u16(dst + (size_t)s * I + c * 32 + n, f32_to_bf16(midf[s * 33 + n]));
     }
   }
   __syncthreads();
@@ -537,8 +546,8 @@ template <int NT, int NCG>
 MK2_DEV void moe_down(const MoeDev& p, int nt, float* red, int* act_ids) {
   constexpr int NW = NT / 64;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, c16 = lane & 15;
-  const int D = p.act[0];
-  for (int j = threadIdx.x; j < D; j += NT) act_ids[j] = p.act[1 + j];
+  const int D = min(ldp_i32(p.act), p.Dmax);
+  for (int j = threadIdx.x; j < D; j += NT) act_ids[j] = min(max(ldp_i32(p.act + 1 + j), 0), p.E - 1);
   __syncthreads();
   const int HT = p.H / 16;
   f32x4 acc[NCG];
@@ -588,7 +597,7 @@ MK2_DEV void moe_down(const MoeDev& p, int nt, float* red, int* act_ids) {
                 for (int cg = 0; cg < NCG; ++cg) {
                   const int row = cg * 16 + c16;
                   bq[u][c][cg] = load_b_fp8(p.mid_q + (size_t)j * p.M * p.I, row, p.M, p.I, kb * 128, g);
-                  sbq[u][c][cg] = row < p.M ? p.mid_s[((size_t)j * p.M + row) * (p.I / 32) + kb * 4 + g] : 127;
+                  sbq[u][c][cg] = row < p.M ? (int)ldp_u8(p.mid_s + ((size_t)j * p.M + row) * (p.I / 32) + kb * 4 + g) : 127;
                 }
               }
             }
@@ -615,7 +624,7 @@ MK2_DEV void moe_down(const MoeDev& p, int nt, float* red, int* act_ids) {
         const int j = j0 + u * NW;
         if (j >= D) break;
 #pragma unroll
-        for (int cg = 0; cg < NCG; ++cg) acc[cg] += tmp[u][cg] * p.rw[j * 32 + cg * 16 + c16];
+        for (int cg = 0; cg < NCG; ++cg) acc[cg] += tmp[u][cg] * ldp_f32(p.rw + j * 32 + cg * 16 + c16);
       }
     }
   } else {
@@ -646,7 +655,7 @@ MK2_DEV void moe_down(const MoeDev& p, int nt, float* red, int* act_ids) {
         for (int cg = 0; cg < NCG; ++cg) {
           bf16x8 b[4];
           load_b_bf16(p.mid_b + (size_t)j * p.M * p.I, cg * 16 + c16, p.M, p.I, kb * 128 + 32 * g, b);
-          acc[cg] += mfma4_bf16(a, b, f32x4{0.f, 0.f, 0.f, 0.f}) * (sc * p.rw[j * 32 + cg * 16 + c16]);
+          acc[cg] += mfma4_bf16(a, b, f32x4{0.f, 0.f, 0.f, 0.f}) * (sc * ldp_f32(p.rw + j * 32 + cg * 16 + c16));
         }
       }
     }
@@ -661,7 +670,7 @@ MK2_DEV void moe_down(const MoeDev& p, int nt, float* red, int* act_ids) {
 #pragma unroll
     for (int w = 0; w < NW; ++w) y += red[((w * NCG + cg) * 64 + l) * 4 + i];
     const size_t o = (size_t)s * p.H + nt * 16 + n16;
-    if (p.residual) y += bf16_to_f32(p.x[o]);
+    if (p.residual) y += bf16_to_f32((bf16_t)ldp_u16(p.x + o));
     p.out[o] = f32_to_bf16(y);
   }
   __syncthreads();

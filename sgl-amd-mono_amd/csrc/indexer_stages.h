@@ -56,31 +56,57 @@ struct IdxDev {
   uint2* cand;          // [rows][max_ctx] (key, position); chunk c from c * IDX_CHUNK
 };
 
+constexpr int IDX_QROW = 136;  // LDS row stride (bf16) of the staged queries
+
 struct IdxScoreLds {
   int pages[IDX_CHUNK / 64];
   int hist[IDX_BINS];
+  bf16_t q[64 * IDX_QROW];  // the row's queries, [head][128] (padded rows)
+  bf16_t w[64];             // its head weights
+  float sc[IDX_CHUNK];      // the chunk's scores, stored once the loop is done
 };
 
 // ------------------------------------------------------------- stage: scores
-// One task: IDX_CHUNK positions of row r; each wave owns 16 groups of 16 keys and
-// issues all of their loads before the first MFMA.
+// One task: IDX_CHUNK positions of row r.  The row's queries and head weights go to
+// LDS first (coalesced, once a workgroup) with the chunk's page ids; then each wave
+// issues the loads of all its 16 groups of 16 keys, takes its A operands from LDS,
+// and computes group by group as the keys arrive.  The loads are unconditional
+// (groups past the row's end read page id 0, and their results are dropped) and the
+// scores wait in LDS until the loop is done: a store or a branch between the loads
+// would make every group wait for all memory traffic.
 template <int NT>
 MK2_DEV void idx_score(const IdxDev& p, int r, int chunk, IdxScoreLds& L) {
   constexpr int NW = NT / 64;
   constexpr int GPW = IDX_CHUNK / 16 / NW;  // 16-key groups a wave
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, c16 = lane & 15;
-  const int n = p.ctx[r];
   const int k_begin = chunk * IDX_CHUNK;
+  // prologue: the row's length and request, its queries and head weights all in
+  // flight together; then the chunk's page ids (through LDS, so that every key load
+  // below issues without waiting on another vector-memory load)
+  constexpr int QPT = (64 * 16 + NT - 1) / NT;  // 16-byte query pieces a thread
+  const int n = p.ctx[r];
+  const int req = p.req[r];
+  uint4 qv[QPT];
+  const uint4* gq = (const uint4*)(p.q + (size_t)r * p.heads * 128);
+#pragma unroll
+  for (int u = 0; u < QPT; ++u) {
+    const int i = threadIdx.x + u * NT;
+    qv[u] = i < p.heads * 16 ? gq[i] : make_uint4(0, 0, 0, 0);
+  }
+  const bf16_t wv = threadIdx.x < p.heads ? p.w[(size_t)r * p.heads + threadIdx.x] : (bf16_t)0;
   if (k_begin >= n) return;
   const int k_end = min(n, k_begin + IDX_CHUNK);
-  const int ngroups = (k_end - k_begin + 15) >> 4;
-  // the chunk's page ids first, through LDS: every key load below then issues
-  // without waiting on another vector-memory load
   int* lds_pages = L.pages;
   if (threadIdx.x < IDX_CHUNK / 64) {
     const int pg = (k_begin >> 6) + threadIdx.x;
-    lds_pages[threadIdx.x] = pg * 64 < k_end ? p.pt[(size_t)p.req[r] * p.stride + pg] : 0;
+    lds_pages[threadIdx.x] = pg * 64 < k_end ? p.pt[(size_t)req * p.stride + pg] : 0;
   }
+#pragma unroll
+  for (int u = 0; u < QPT; ++u) {
+    const int i = threadIdx.x + u * NT;
+    if (i < p.heads * 16) *(uint4*)(L.q + (i >> 4) * IDX_QROW + (i & 15) * 8) = qv[u];
+  }
+  if (threadIdx.x < p.heads) L.w[threadIdx.x] = wv;
   for (int b = threadIdx.x; b < IDX_BINS; b += NT) L.hist[b] = 0;
   __syncthreads();
   const int gw0 = wave * GPW;  // this wave's first group
@@ -89,15 +115,10 @@ MK2_DEV void idx_score(const IdxDev& p, int r, int chunk, IdxScoreLds& L) {
 #pragma unroll
   for (int j = 0; j < GPW; ++j) {
     const int key0 = k_begin + (gw0 + j) * 16;
-    if (gw0 + j < ngroups) {
-      const uint8_t* pg = p.cache + (size_t)lds_pages[(key0 - k_begin) >> 6] * IDX_PAGE_BYTES;
-      const int tok = (key0 & 63) + c16;
-      code[j] = *(const uint4*)(pg + tok * 64 + 16 * g);
-      sw[j] = *(const uint32_t*)(pg + 4096 + tok * 4);
-    } else {
-      code[j] = make_uint4(0, 0, 0, 0);
-      sw[j] = 0x7F7F7F7Fu;
-    }
+    const uint8_t* pg = p.cache + (size_t)lds_pages[(key0 - k_begin) >> 6] * IDX_PAGE_BYTES;
+    const int tok = (key0 & 63) + c16;
+    code[j] = *(const uint4*)(pg + tok * 64 + 16 * g);
+    sw[j] = *(const uint32_t*)(pg + 4096 + tok * 4);
   }
   const int nhg = p.heads >> 4;
   // A operands: q of head 16*hg + c16, dims 32g + 8s .. +7; head weights of rows 4g+i
@@ -106,10 +127,10 @@ MK2_DEV void idx_score(const IdxDev& p, int r, int chunk, IdxScoreLds& L) {
 #pragma unroll
   for (int hg = 0; hg < 4; ++hg) {
     if (hg < nhg) {
-      const bf16_t* qr = p.q + ((size_t)r * p.heads + hg * 16 + c16) * 128 + 32 * g;
+      const bf16_t* qr = L.q + (hg * 16 + c16) * IDX_QROW + 32 * g;
 #pragma unroll
       for (int s = 0; s < 4; ++s) qa[hg][s] = __builtin_bit_cast(bf16x8, *(const uint4*)(qr + 8 * s));
-      const uint2 wv = *(const uint2*)(p.w + (size_t)r * p.heads + hg * 16 + 4 * g);
+      const uint2 wv = *(const uint2*)(L.w + hg * 16 + 4 * g);
       wt[hg][0] = __uint_as_float(wv.x << 16);
       wt[hg][1] = __uint_as_float(wv.x & 0xFFFF0000u);
       wt[hg][2] = __uint_as_float(wv.y << 16);
@@ -124,7 +145,6 @@ MK2_DEV void idx_score(const IdxDev& p, int r, int chunk, IdxScoreLds& L) {
   float* srow = p.scores + (size_t)r * p.max_ctx;
 #pragma unroll
   for (int j = 0; j < GPW; ++j) {
-    if (gw0 + j >= ngroups) break;
     const float sc = e8m0_to_f32(sw[j] >> (8 * g));
     bf16x8 kb[4];
     kb[0] = e2m1x8_to_bf16(code[j].x, sc);
@@ -143,13 +163,21 @@ MK2_DEV void idx_score(const IdxDev& p, int r, int chunk, IdxScoreLds& L) {
     }
     s += __shfl_xor(s, 16, 64);
     s += __shfl_xor(s, 32, 64);
-    const int key = k_begin + (gw0 + j) * 16 + c16;
-    if (g == 0 && key < k_end) {
-      st_dev_f32(srow + key, s);
+    const int loc = (gw0 + j) * 16 + c16;
+    if (g == 0 && k_begin + loc < k_end) {
+      L.sc[loc] = s;
       atomicAdd(&L.hist[radix_key(s) >> 20], 1);
     }
   }
   __syncthreads();
+  for (int i = 4 * threadIdx.x; i < k_end - k_begin; i += 4 * NT) {
+    if (k_begin + i + 4 <= k_end) {
+      st_dev_16(srow + k_begin + i, make_uint4(__float_as_uint(L.sc[i]), __float_as_uint(L.sc[i + 1]),
+                                               __float_as_uint(L.sc[i + 2]), __float_as_uint(L.sc[i + 3])));
+    } else {
+      for (int u = 0; u < 4 && k_begin + i + u < k_end; ++u) st_dev_f32(srow + k_begin + i + u, L.sc[i + u]);
+    }
+  }
   // the chunk's counts into the row's histograms (device atomics, nonzero bins)
   int* gh = p.hist + (size_t)r * IDX_BINS;
   for (int b = threadIdx.x; b < IDX_BINS; b += NT) {

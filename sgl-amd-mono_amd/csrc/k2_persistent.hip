@@ -2,7 +2,8 @@
 // stage list -- index scores (+ key histograms), top-k slices, top-k select,
 // sparse-MLA splits, merge, W_UV, W_o + residual, RMSNorm + activation quant,
 // router, top-k routing, up/gate + SwiGLU, down + residual -- taking task t of a
-// stage when t = workgroup (mod grid).
+// stage on workgroup (base + t) mod grid, where each stage's base continues from
+// where the previous stage's tasks ended, so that work rotates over the workgroups.
 //
 // There is no grid barrier.  A task that needs the results of earlier tasks waits
 // on a per-stage completion counter in the workspace (only for the producers it
@@ -66,8 +67,8 @@ union K2Lds {
   MlaSplitLds split;
   float merge[2 * 1024 + 8];
   struct {
-    float red[(K2_NT / 64) * 4 * 2 * 64 * 4];
-    float midf[32 * 33];
+    float red[(K2_NT / 64) * 8 * 64 * 4];  // NW * 2 * CT * NCG * 256, CT * NCG <= 4
+    float midf[32 * 65];
   } up;
   struct {
     float red[(K2_NT / 64) * 2 * 64 * 4];
@@ -87,12 +88,19 @@ MK2_DEV void k2_signal(int* c) {
   if (threadIdx.x == 0) __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-MK2_DEV void k2_wait(const K2Dev& p, int slot, int target, int stamp = -1) {
+// wait until counter `slot` reaches `target`.  `seen` (LDS) caches the counts this
+// workgroup has observed (counters only grow within a launch), so a wait that an
+// earlier one already satisfied costs nothing.  The early return is uniform: seen is
+// written only just after this function's barrier, and every task ends with a barrier
+// before the next wait reads it.
+MK2_DEV void k2_wait(const K2Dev& p, int* seen, int slot, int target, int stamp = -1) {
+  if (seen[slot] >= target) return;
+  int v = 0;
   if (threadIdx.x == 0) {
     const int* c = p.sync + slot;
     int* err = p.sync + SY_ERR;
     int n = 0;
-    while (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+    while ((v = __hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) < target) {
       if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
       if (++n > p.spin_limit) {
         atomicOr(err, 1);
@@ -103,120 +111,145 @@ MK2_DEV void k2_wait(const K2Dev& p, int slot, int target, int stamp = -1) {
     if (stamp >= 0 && p.timeline) p.timeline[(size_t)blockIdx.x * K2_STAMPS + stamp] = __builtin_amdgcn_s_memrealtime();
   }
   __syncthreads();
+  if (threadIdx.x == 0) seen[slot] = v;
 }
 
 template <int NCG>
 __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
   __shared__ K2Lds S;
+  __shared__ int seen[SY_WORDS];
   const int G = gridDim.x, b = blockIdx.x;
   const int R = p.rows;
+  for (int i = threadIdx.x; i < SY_WORDS; i += K2_NT) seen[i] = 0;
+  __syncthreads();
+  int base = 0;  // this stage's first workgroup
+// the tasks of a stage of n tasks on this workgroup; `t < G` marks the first
+#define K2_TASKS(t, n) for (int t = (b - base % G + G) % G; t < (n); t += G)
+#define K2_NEXT(n) base = (base + (n)) % G
   int st = 0;  // timeline stage
   // ---- index scores + row key histograms
   k2_stamp(p, 3 * st);
   const int nchk = p.idx.nchk;
-  for (int t = b; t < R * nchk; t += G) {
+  K2_TASKS(t, R * nchk) {
     idx_score<K2_NT>(p.idx, t / nchk, t % nchk, S.score);
     k2_signal(p.sync + SY_SCORE + t / nchk);
   }
   k2_stamp(p, 3 * st++ + 2);
   // ---- top-k slices: each chunk's candidates
   k2_stamp(p, 3 * st);
-  for (int t = b; t < R * nchk; t += G) {
+  // slices on the workgroups of their score chunks (base unchanged)
+  K2_TASKS(t, R * nchk) {
     const int r = t / nchk;
-    k2_wait(p, SY_SCORE + r, nchk, t == b ? 3 * st + 1 : -1);
+    k2_wait(p, seen, SY_SCORE + r, nchk, t < G ? 3 * st + 1 : -1);
     idx_slice<K2_NT>(p.idx, r, t % nchk, S.topk);
     k2_signal(p.sync + SY_SLICE + r);
   }
+  K2_NEXT(R * nchk);
   k2_stamp(p, 3 * st++ + 2);
   // ---- exact top-k of each row over its candidates
   k2_stamp(p, 3 * st);
-  for (int t = b; t < R; t += G) {
-    k2_wait(p, SY_SLICE + t, nchk, t == b ? 3 * st + 1 : -1);
+  K2_TASKS(t, R) {
+    k2_wait(p, seen, SY_SLICE + t, nchk, t < G ? 3 * st + 1 : -1);
     idx_select<K2_NT>(p.idx, t, S.topk);
     k2_signal(p.sync + SY_TOPK + t);
   }
+  K2_NEXT(R);
   k2_stamp(p, 3 * st++ + 2);
   // ---- sparse-MLA splits
   k2_stamp(p, 3 * st);
   const int ns = p.mla.nsplit;
-  for (int t = b; t < R * ns; t += G) {
+  K2_TASKS(t, R * ns) {
     const int r = t / ns;
-    k2_wait(p, SY_TOPK + r, 1, t == b ? 3 * st + 1 : -1);
+    k2_wait(p, seen, SY_TOPK + r, 1, t < G ? 3 * st + 1 : -1);
     mla_split<K2_NT>(p.mla, r, t % ns, S.split);
     k2_signal(p.sync + SY_SPLIT + r);
   }
+  K2_NEXT(R * ns);
   k2_stamp(p, 3 * st++ + 2);
   // ---- merge of the splits, per (row, head)
   k2_stamp(p, 3 * st);
-  for (int t = b; t < R * MLA_HEADS; t += G) {
+  K2_TASKS(t, R * MLA_HEADS) {
     const int r = t / MLA_HEADS, h = t % MLA_HEADS;
-    k2_wait(p, SY_SPLIT + r, ns, t == b ? 3 * st + 1 : -1);
+    k2_wait(p, seen, SY_SPLIT + r, ns, t < G ? 3 * st + 1 : -1);
     mla_merge<K2_NT>(p.mla, r, h, S.merge);
     k2_signal(p.sync + SY_MERGE + h);
   }
+  K2_NEXT(R * MLA_HEADS);
   k2_stamp(p, 3 * st++ + 2);
   // ---- W_UV, per (head, 16 v rows)
   k2_stamp(p, 3 * st);
   const int vtn = p.mla.v_dim / 16;
-  for (int t = b; t < MLA_HEADS * vtn; t += G) {
+  K2_TASKS(t, MLA_HEADS * vtn) {
     const int h = t / vtn;
-    k2_wait(p, SY_MERGE + h, R, t == b ? 3 * st + 1 : -1);
-    mla_uv<K2_NT, NCG>(p.mla, h, t % vtn, S.red);
+    mla_uv<K2_NT, NCG>(p.mla, h, t % vtn, S.red,
+                       [&] { k2_wait(p, seen, SY_MERGE + h, R, t < G ? 3 * st + 1 : -1); });
     k2_signal(p.sync + SY_UV);
   }
+  K2_NEXT(MLA_HEADS * vtn);
   k2_stamp(p, 3 * st++ + 2);
   // ---- W_o + residual, per 16 hidden rows
   k2_stamp(p, 3 * st);
   const int ht = p.mla.hidden / 16;
-  for (int t = b; t < ht; t += G) {
-    k2_wait(p, SY_UV, MLA_HEADS * vtn, t == b ? 3 * st + 1 : -1);
-    mla_oproj<K2_NT, NCG>(p.mla, t, S.red);
+  K2_TASKS(t, ht) {
+    mla_oproj<K2_NT, NCG>(p.mla, t, S.red,
+                          [&] { k2_wait(p, seen, SY_UV, MLA_HEADS * vtn, t < G ? 3 * st + 1 : -1); });
     k2_signal(p.sync + SY_OPROJ);
   }
+  K2_NEXT(ht);
   k2_stamp(p, 3 * st++ + 2);
   // ---- RMSNorm + activation quant, per row
   k2_stamp(p, 3 * st);
-  for (int t = b; t < R; t += G) {
-    k2_wait(p, SY_OPROJ, ht, t == b ? 3 * st + 1 : -1);
+  K2_TASKS(t, R) {
+    k2_wait(p, seen, SY_OPROJ, ht, t < G ? 3 * st + 1 : -1);
     moe_prep<K2_NT>(p.moe, t, S.red);
     k2_signal(p.sync + SY_PREP);
   }
+  K2_NEXT(R);
   k2_stamp(p, 3 * st++ + 2);
   // ---- router GEMV, per (16 experts, k-chunk)
   k2_stamp(p, 3 * st);
   const int et = p.moe.E / 16, nrt = et * p.moe.KC;
-  for (int t = b; t < nrt; t += G) {
-    k2_wait(p, SY_PREP, R, t == b ? 3 * st + 1 : -1);
-    moe_router<K2_NT, NCG>(p.moe, t % et, t / et, S.red);
+  K2_TASKS(t, nrt) {
+    moe_router<K2_NT, NCG>(p.moe, t % et, t / et, S.red,
+                           [&] { k2_wait(p, seen, SY_PREP, R, t < G ? 3 * st + 1 : -1); });
     k2_signal(p.sync + SY_ROUTER);
   }
+  K2_NEXT(nrt);
   k2_stamp(p, 3 * st++ + 2);
   // ---- top-k routing (one task)
   k2_stamp(p, 3 * st);
-  for (int t = b; t < 1; t += G) {
-    k2_wait(p, SY_ROUTER, nrt, t == b ? 3 * st + 1 : -1);
+  K2_TASKS(t, 1) {
+    k2_wait(p, seen, SY_ROUTER, nrt, t < G ? 3 * st + 1 : -1);
     moe_route<K2_NT>(p.moe, S.route.logits, S.route.slot);
     k2_signal(p.sync + SY_ROUTE);
   }
+  K2_NEXT(1);
   k2_stamp(p, 3 * st++ + 2);
-  // ---- up/gate + SwiGLU: routed slots (after routing), then the shared expert
+  // ---- up/gate + SwiGLU: the shared expert's chunks first (they need only the
+  // normalized rows, so they run while routing is still pending), then the routed
+  // slots
   k2_stamp(p, 3 * st);
-  const int up_r = p.moe.Dmax * (p.moe.I / 32);
-  const int up_total = up_r + p.moe.n_shared * (p.moe.SI / 32);
-  for (int t = b; t < up_total; t += G) {
-    if (t < up_r) k2_wait(p, SY_ROUTE, 1, t == b ? 3 * st + 1 : -1);
-    else k2_wait(p, SY_PREP, R, t == b ? 3 * st + 1 : -1);
-    moe_upgate<K2_NT, NCG>(p.moe, t, S.up.red, S.up.midf);
+  const int up_r = p.moe.Dmax * (p.moe.I / p.moe.UC);
+  const int up_sh = p.moe.n_shared * (p.moe.SI / 32);
+  const int up_total = up_r + up_sh;
+  K2_TASKS(t, up_total) {
+    const bool sh = t < up_sh;
+    if (sh) k2_wait(p, seen, SY_PREP, R, t < G ? 3 * st + 1 : -1);
+    else k2_wait(p, seen, SY_ROUTE, 1, t < G ? 3 * st + 1 : -1);
+    moe_upgate<K2_NT, NCG>(p.moe, sh ? up_r + t : t - up_sh, S.up.red, S.up.midf);
     k2_signal(p.sync + SY_UP);
   }
+  K2_NEXT(up_total);
   k2_stamp(p, 3 * st++ + 2);
   // ---- down + route weighting + residual, per 16 hidden rows
   k2_stamp(p, 3 * st);
-  for (int t = b; t < p.moe.H / 16; t += G) {
-    k2_wait(p, SY_UP, up_total, t == b ? 3 * st + 1 : -1);
+  K2_TASKS(t, p.moe.H / 16) {
+    k2_wait(p, seen, SY_UP, up_total, t < G ? 3 * st + 1 : -1);
     moe_down<K2_NT, NCG>(p.moe, t, S.down.red, S.down.act);
   }
   k2_stamp(p, 3 * st + 2);
+#undef K2_TASKS
+#undef K2_NEXT
   // ---- the last workgroup out resets the counters for the next launch
   __syncthreads();
   if (threadIdx.x == 0) {

@@ -184,6 +184,13 @@ MK2_DEV void st_dev_16(void* p, uint4 v) {
   MK2_DEV_ST(uint64_t, p, ((uint64_t)v.y << 32) | v.x);
   MK2_DEV_ST(uint64_t, (uint64_t*)p + 1, ((uint64_t)v.w << 32) | v.z);
 }
+// the dependency wait a stage runs after issuing the loads of its static weights (the
+// persistent launch waits on a counter there; a stand-alone kernel has nothing to wait
+// for)
+struct NoWait {
+  MK2_DEV void operator()() const {}
+};
+
 // every memory access of this thread has completed (stores are device-visible)
 MK2_DEV void drain_memory() { __builtin_amdgcn_s_waitcnt(0); }
 

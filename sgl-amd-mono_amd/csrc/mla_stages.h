@@ -254,34 +254,38 @@ MK2_DEV void mla_merge(const MlaDev& p, int r, int h, float* lds) {
 }
 
 // ---------------------------------------------------------------- stage: W_UV
-template <int NT, int NCG>
-MK2_DEV void mla_uv(const MlaDev& p, int h, int vt, float* red) {
-  constexpr int NW = NT / 64;
+// Task (head h, 16 v rows vt): W_UV rows are static, so their loads are issued before
+// `wait` (the merged rows' dependency).
+template <int NT, int NCG, typename Wait = NoWait>
+MK2_DEV void mla_uv(const MlaDev& p, int h, int vt, float* red, Wait wait = Wait()) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, c16 = lane & 15;
   const int kb = wave & 3;  // waves 0-3: 128 of the 512 latent dims each (4-7 idle)
+  bf16x8 a[4];
+  if (wave < 4) {
+    const bf16_t* wrow = p.w_uv + ((size_t)h * p.v_dim + vt * 16 + c16) * MLA_LAT + kb * 128 + 32 * g;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) a[q] = __builtin_bit_cast(bf16x8, *(const uint4*)(wrow + 8 * q));
+  }
+  wait();
   f32x4 acc[NCG];
   if (wave < 4) {
-  bf16x8 a[4];
-  const bf16_t* wrow = p.w_uv + ((size_t)h * p.v_dim + vt * 16 + c16) * MLA_LAT + kb * 128 + 32 * g;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) a[q] = __builtin_bit_cast(bf16x8, *(const uint4*)(wrow + 8 * q));
+    for (int cg = 0; cg < NCG; ++cg) {
+      const int row = cg * 16 + c16;
+      bf16x8 b[4];
+      if (row < p.rows) {
+        const bf16_t* src = p.o_lat + ((size_t)row * MLA_HEADS + h) * MLA_LAT + kb * 128 + 32 * g;
 #pragma unroll
-  for (int cg = 0; cg < NCG; ++cg) {
-    const int row = cg * 16 + c16;
-    bf16x8 b[4];
-    if (row < p.rows) {
-      const bf16_t* src = p.o_lat + ((size_t)row * MLA_HEADS + h) * MLA_LAT + kb * 128 + 32 * g;
+        for (int q = 0; q < 4; ++q) b[q] = __builtin_bit_cast(bf16x8, ldp_16(src + 8 * q));
+      } else {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) b[q] = __builtin_bit_cast(bf16x8, ldp_16(src + 8 * q));
-    } else {
+        for (int q = 0; q < 4; ++q) b[q] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
+      }
+      f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int q = 0; q < 4; ++q) b[q] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
+      for (int q = 0; q < 4; ++q) c = mfma_bf16(a[q], b[q], c);
+      acc[cg] = c;
     }
-    f32x4 c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int q = 0; q < 4; ++q) c = mfma_bf16(a[q], b[q], c);
-    acc[cg] = c;
-  }
 #pragma unroll
     for (int cg = 0; cg < NCG; ++cg) *(f32x4*)(red + ((wave * NCG + cg) * 64 + lane) * 4) = acc[cg];
   }
@@ -298,19 +302,27 @@ MK2_DEV void mla_uv(const MlaDev& p, int h, int vt, float* red) {
 }
 
 // ---------------------------------------------------------------- stage: W_o
-template <int NT, int NCG>
-MK2_DEV void mla_oproj(const MlaDev& p, int nt, float* red) {
-  constexpr int NW = NT / 64;
+// Task (16 hidden rows nt): each wave's first PF k-blocks of W_o are loaded before
+// `wait` (the attention rows' dependency); the rest after.
+template <int NT, int NCG, typename Wait = NoWait>
+MK2_DEV void mla_oproj(const MlaDev& p, int nt, float* red, Wait wait = Wait()) {
+  constexpr int NW = NT / 64, PF = 2;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, c16 = lane & 15;
   const int K = MLA_HEADS * p.v_dim, KB = K / 128;
+  const uint8_t* tiles = p.w_o + (size_t)nt * KB * 64 * 64;
+  bf16x8 apf[PF][4];
+#pragma unroll
+  for (int u = 0; u < PF; ++u) {
+    const int kb = wave + u * NW;
+    const uint4* t = (const uint4*)(tiles + ((size_t)min(kb, KB - 1) * 64 + lane) * 64);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) apf[u][q] = __builtin_bit_cast(bf16x8, t[q]);
+  }
+  wait();
   f32x4 acc[NCG];
 #pragma unroll
   for (int cg = 0; cg < NCG; ++cg) acc[cg] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int kb = wave; kb < KB; kb += NW) {
-    bf16x8 a[4];
-    const uint4* t = (const uint4*)(p.w_o + (((size_t)nt * KB + kb) * 64 + lane) * 64);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) a[q] = __builtin_bit_cast(bf16x8, t[q]);
+  auto step = [&](int kb, const bf16x8* a) {
 #pragma unroll
     for (int cg = 0; cg < NCG; ++cg) {
       const int row = cg * 16 + c16;
@@ -326,6 +338,16 @@ MK2_DEV void mla_oproj(const MlaDev& p, int nt, float* red) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) acc[cg] = mfma_bf16(a[q], b[q], acc[cg]);
     }
+  };
+#pragma unroll
+  for (int u = 0; u < PF; ++u)
+    if (wave + u * NW < KB) step(wave + u * NW, apf[u]);
+  for (int kb = wave + PF * NW; kb < KB; kb += NW) {
+    bf16x8 a[4];
+    const uint4* t = (const uint4*)(tiles + ((size_t)kb * 64 + lane) * 64);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) a[q] = __builtin_bit_cast(bf16x8, t[q]);
+    step(kb, a);
   }
 #pragma unroll
   for (int cg = 0; cg < NCG; ++cg) *(f32x4*)(red + ((wave * NCG + cg) * 64 + lane) * 4) = acc[cg];

@@ -29,8 +29,8 @@ __global__ __launch_bounds__(ROUTE_NT) void k_moe_route(MoeDev p) {
 
 template <int NCG>
 __global__ __launch_bounds__(MOE_NT) void k_moe_upgate(MoeDev p) {
-  __shared__ float red[(MOE_NT / 64) * 4 * NCG * 64 * 4];
-  __shared__ float midf[32 * 33];
+  __shared__ float red[(MOE_NT / 64) * 8 * 64 * 4];  // NW * 2 * CT * NCG * 256, CT * NCG <= 4
+  __shared__ float midf[32 * 65];
   moe_upgate<MOE_NT, NCG>(p, blockIdx.x, red, midf);
 }
 
@@ -77,6 +77,7 @@ size_t moe_carve(const mk2_moe_shape* s, void* base, MoeDev* d) {
   MoeDev t{};
   t.KC = KC;
   t.Dmax = Dmax;
+  t.UC = (s->expert_fmt == MK2_FMT_MXFP4 && M <= 16 && I % 64 == 0) ? 64 : 32;
   t.xn = c.take<bf16_t>((size_t)M * H);
   t.xq = c.take<uint8_t>((size_t)M * H);
   t.xs = c.take<uint8_t>((size_t)M * H / 32);
@@ -94,7 +95,7 @@ size_t moe_carve(const mk2_moe_shape* s, void* base, MoeDev* d) {
   }
   t.mid_sh = c.take<bf16_t>((size_t)M * (s->n_shared ? s->shared_inter : 0) + 1);
   if (d) {
-    d->KC = t.KC; d->Dmax = t.Dmax; d->xn = t.xn; d->xq = t.xq; d->xs = t.xs;
+    d->KC = t.KC; d->Dmax = t.Dmax; d->UC = t.UC; d->xn = t.xn; d->xq = t.xq; d->xs = t.xs;
     d->logit_part = t.logit_part; d->logits = t.logits; d->topk_ids = t.topk_ids;
     d->topk_w = t.topk_w; d->act = t.act; d->rw = t.rw; d->mid_q = t.mid_q;
     d->mid_s = t.mid_s; d->mid_b = t.mid_b; d->mid_sh = t.mid_sh;
@@ -132,7 +133,7 @@ int moe_enqueue(const MoeDev& d, hipStream_t st) {
   const size_t route_lds =
       (size_t)d.M * d.E * 4 + (size_t)(d.E + 28 * (ROUTE_NT / 64) + 2 * d.M * d.topk) * 4;
   k_moe_route<<<1, ROUTE_NT, route_lds, st>>>(d);
-  const int up_tasks = d.Dmax * (d.I / 32) + d.n_shared * (d.SI / 32);
+  const int up_tasks = d.Dmax * (d.I / d.UC) + d.n_shared * (d.SI / 32);
   if (ncg == 1) k_moe_upgate<1><<<up_tasks, MOE_NT, 0, st>>>(d);
   else k_moe_upgate<2><<<up_tasks, MOE_NT, 0, st>>>(d);
   if (ncg == 1) k_moe_down<1><<<d.H / 16, MOE_NT, 0, st>>>(d);

@@ -14,6 +14,7 @@ struct MoeDev {
   int M, H, E, topk, I, router, fmt, n_shared, SI, norm, residual;
   int KC;    // router k-chunks
   int Dmax;  // capacity of the distinct-expert list
+  int UC;    // intermediate rows of a routed up/gate task (64: MXFP4 at <= 16 rows, else 32)
   float route_scale, eps;
   const bf16_t* x;
   const bf16_t* gamma;
@@ -182,19 +183,29 @@ MK2_DEV f32x4 mfma4_bf16(const bf16x8* a, const bf16x8* b, f32x4 c) {
 }
 
 // ------------------------------------------------------------- stage: router GEMV
-// task (nt, kc): 16 experts x the kc-th slice of hidden -> logit_part[kc]
-template <int NT, int NCG>
-MK2_DEV void moe_router(const MoeDev& p, int nt, int kc, float* red) {
+// task (nt, kc): 16 experts x the kc-th slice of hidden -> logit_part[kc].  The
+// router weights are static: a wave's first k-block is loaded before `wait` (the
+// normalized rows' dependency).
+template <int NT, int NCG, typename Wait = NoWait>
+MK2_DEV void moe_router(const MoeDev& p, int nt, int kc, float* red, Wait wait = Wait()) {
   constexpr int NW = NT / 64;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4;
   const int KB = p.H / 128, kbs = KB / p.KC;
+  bf16x8 a0[4];
+  load_a_bf16(p.w_router + ((size_t)nt * KB + kc * kbs + min(wave, kbs - 1)) * 4096, lane, a0);
+  wait();
   f32x4 acc[NCG];
 #pragma unroll
   for (int c = 0; c < NCG; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int i = wave; i < kbs; i += NW) {
     const int kb = kc * kbs + i;
     bf16x8 a[4];
-    load_a_bf16(p.w_router + ((size_t)nt * KB + kb) * 4096, lane, a);
+    if (i == wave) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) a[q] = a0[q];
+    } else {
+      load_a_bf16(p.w_router + ((size_t)nt * KB + kb) * 4096, lane, a);
+    }
 #pragma unroll
     for (int c = 0; c < NCG; ++c) {
       bf16x8 b[4];
@@ -380,161 +391,164 @@ MK2_DEV void moe_route(const MoeDev& p, float* lds_logits, int* lds_slot) {
 }
 
 // ------------------------------------------------------- stage: up/gate + SwiGLU
-// task t < Dmax * I/32: routed slot j = t / (I/32), 32-row chunk c; past that the
-// shared expert's chunks.  mid = silu(gate) * up for the chunk's 32 rows x all rows.
-// Each wave owns every NW-th 128-k block and issues the weight loads of a whole
-// batch of its blocks before the first MFMA.
-template <int NT, int NCG>
-MK2_DEV void moe_upgate(const MoeDev& p, int t, float* red, float* midf) {
-  constexpr int NW = NT / 64;
+// A chunk is 16*CT intermediate rows of one expert: CT gate tiles and the CT matching
+// up tiles of the stacked [gate; up] matrix, against all decode rows; mid =
+// silu(gate) * up.  Each wave owns every NW-th 128-k block and issues the loads of a
+// batch of its blocks (weights, scales, activations) before the first MFMA.
+template <int NT, int NCG, int CT>
+MK2_DEV void upgate_chunk(const MoeDev& p, bool shared, int j, int e, int c, float* red, float* midf) {
+  constexpr int NW = NT / 64, NQ = 2 * CT, R = 16 * CT;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4;
   const int KB = p.H / 128;
-  const int chunks_r = p.I / 32;
-  bool shared = false;
-  int j = 0, e = 0, c = 0;
-  if (t < p.Dmax * chunks_r) {
-    j = t / chunks_r;
-    c = t % chunks_r;
-    if (j >= ldp_i32(p.act)) return;
-    e = ldp_i32(p.act + 1 + j);
-    if (e < 0 || e >= p.E) return;
-  } else {
-    shared = true;
-    c = t - p.Dmax * chunks_r;
-  }
   const int I = shared ? p.SI : p.I;
   const int NT16 = 2 * I / 16;  // 16-row tiles of the stacked gate|up
-  const int nts[4] = {2 * c, 2 * c + 1, I / 16 + 2 * c, I / 16 + 2 * c + 1};
-  f32x4 acc[4][NCG];
+  int nts[NQ];
 #pragma unroll
-  for (int q = 0; q < 4; ++q)
+  for (int q = 0; q < CT; ++q) {
+    nts[q] = CT * c + q;
+    nts[CT + q] = I / 16 + CT * c + q;
+  }
+  f32x4 acc[NQ][NCG];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q)
 #pragma unroll
     for (int cg = 0; cg < NCG; ++cg) acc[q][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   if (!shared && p.fmt == MK2_FMT_MXFP4) {
-    constexpr int B = NCG == 1 ? 4 : 3;  // k-blocks a wave holds in flight
+    constexpr int B = CT == 4 ? (NCG == 1 ? 3 : 2) : (NCG == 1 ? 4 : 3);  // k-blocks in flight
     const int G = (KB + 3) / 4;
     const uint8_t* wbase = p.w13 + (size_t)e * NT16 * KB * 1024;
     const uint8_t* sbase = p.s13 + (size_t)e * NT16 * G * 256;
     for (int kb0 = wave; kb0 < KB; kb0 += NW * B) {
-      // every load of the batch (weights, scales, activations) before the first MFMA
-      i32x8 a[B][4], b[B][NCG];
-      int sa[B][4], sb[B][NCG];
+      i32x8 a[B][NQ], b[B][NCG];
+      int sa[B][NQ], sb[B][NCG];
 #pragma unroll
       for (int u = 0; u < B; ++u) {
-        const int kb = kb0 + u * NW;
-        if (kb < KB) {
+        const int kb = min(kb0 + u * NW, KB - 1);  // past the end: a valid block, unused
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            a[u][q] = load_a_fp4(wbase + ((size_t)nts[q] * KB + kb) * 1024, lane);
-            sa[u][q] = (int)(*(const uint32_t*)(sbase + (((size_t)nts[q] * G + kb / 4) * 64 + lane) * 4) >>
-                             (8 * (kb & 3)));
-          }
+        for (int q = 0; q < NQ; ++q) {
+          a[u][q] = load_a_fp4(wbase + ((size_t)nts[q] * KB + kb) * 1024, lane);
+          sa[u][q] = (int)(*(const uint32_t*)(sbase + (((size_t)nts[q] * G + kb / 4) * 64 + lane) * 4) >>
+                           (8 * (kb & 3)));
+        }
 #pragma unroll
-          for (int cg = 0; cg < NCG; ++cg) {
-            const int row = cg * 16 + (lane & 15);
-            b[u][cg] = load_b_fp8(p.xq, row, p.M, p.H, kb * 128, g);
-            sb[u][cg] = row < p.M ? (int)ldp_u8(p.xs + (size_t)row * (p.H / 32) + kb * 4 + g) : 127;
-          }
+        for (int cg = 0; cg < NCG; ++cg) {
+          const int row = cg * 16 + (lane & 15);
+          b[u][cg] = load_b_fp8(p.xq, row, p.M, p.H, kb * 128, g);
+          sb[u][cg] = row < p.M ? (int)ldp_u8(p.xs + (size_t)row * (p.H / 32) + kb * 4 + g) : 127;
         }
       }
 #pragma unroll
       for (int u = 0; u < B; ++u) {
-        const int kb = kb0 + u * NW;
-        if (kb >= KB) break;
+        if (kb0 + u * NW >= KB) break;
 #pragma unroll
         for (int cg = 0; cg < NCG; ++cg)
 #pragma unroll
-          for (int q = 0; q < 4; ++q)
+          for (int q = 0; q < NQ; ++q)
             acc[q][cg] = mfma_fp4_fp8<0, 0>(a[u][q], b[u][cg], acc[q][cg], sa[u][q], sb[u][cg]);
       }
     }
-  } else {
+  } else if constexpr (CT == 2) {
     constexpr int B = NCG == 1 ? 3 : 2;
     const uint8_t* wbase = shared ? p.ws13 : p.w13 + (size_t)e * NT16 * KB * 2048;
     const float* sbase = shared ? p.ss13 : (const float*)p.s13 + (size_t)e * (2 * I / 128) * KB;
     for (int kb0 = wave; kb0 < KB; kb0 += NW * B) {
-      uint4 raw[B][4][2];
+      uint4 raw[B][NQ][2];
       bf16x8 bx[B][NCG][4];
-      float sc[B][4];
+      float sc[B][NQ];
 #pragma unroll
       for (int u = 0; u < B; ++u) {
-        const int kb = kb0 + u * NW;
-        if (kb < KB) {
+        const int kb = min(kb0 + u * NW, KB - 1);
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const uint4* tl = (const uint4*)(wbase + ((size_t)nts[q] * KB + kb) * 2048 + lane * 32);
-            raw[u][q][0] = tl[0];
-            raw[u][q][1] = tl[1];
-            sc[u][q] = sbase[(nts[q] * 16 / 128) * KB + kb];
-          }
-#pragma unroll
-          for (int cg = 0; cg < NCG; ++cg)
-            load_b_bf16(p.xn, cg * 16 + (lane & 15), p.M, p.H, kb * 128 + 32 * g, bx[u][cg]);
+        for (int q = 0; q < NQ; ++q) {
+          const uint4* tl = (const uint4*)(wbase + ((size_t)nts[q] * KB + kb) * 2048 + lane * 32);
+          raw[u][q][0] = tl[0];
+          raw[u][q][1] = tl[1];
+          sc[u][q] = sbase[(nts[q] * 16 / 128) * KB + kb];
         }
+#pragma unroll
+        for (int cg = 0; cg < NCG; ++cg)
+          load_b_bf16(p.xn, cg * 16 + (lane & 15), p.M, p.H, kb * 128 + 32 * g, bx[u][cg]);
       }
 #pragma unroll
       for (int u = 0; u < B; ++u) {
-        const int kb = kb0 + u * NW;
-        if (kb >= KB) break;
+        if (kb0 + u * NW >= KB) break;
 #pragma unroll
         for (int cg = 0; cg < NCG; ++cg) {
-          const bf16x8* b = bx[u][cg];
+          const bf16x8* bb = bx[u][cg];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            bf16x8 a[4];
-            a[0] = e4m3x8_to_bf16(raw[u][q][0].x, raw[u][q][0].y);
-            a[1] = e4m3x8_to_bf16(raw[u][q][0].z, raw[u][q][0].w);
-            a[2] = e4m3x8_to_bf16(raw[u][q][1].x, raw[u][q][1].y);
-            a[3] = e4m3x8_to_bf16(raw[u][q][1].z, raw[u][q][1].w);
-            acc[q][cg] += mfma4_bf16(a, b, f32x4{0.f, 0.f, 0.f, 0.f}) * sc[u][q];
+          for (int q = 0; q < NQ; ++q) {
+            bf16x8 aa[4];
+            aa[0] = e4m3x8_to_bf16(raw[u][q][0].x, raw[u][q][0].y);
+            aa[1] = e4m3x8_to_bf16(raw[u][q][0].z, raw[u][q][0].w);
+            aa[2] = e4m3x8_to_bf16(raw[u][q][1].x, raw[u][q][1].y);
+            aa[3] = e4m3x8_to_bf16(raw[u][q][1].z, raw[u][q][1].w);
+            acc[q][cg] += mfma4_bf16(aa, bb, f32x4{0.f, 0.f, 0.f, 0.f}) * sc[u][q];
           }
         }
       }
     }
   }
 #pragma unroll
-  for (int q = 0; q < 4; ++q)
+  for (int q = 0; q < NQ; ++q)
 #pragma unroll
     for (int cg = 0; cg < NCG; ++cg)
-      *(f32x4*)(red + (((wave * 4 + q) * NCG + cg) * 64 + lane) * 4) = acc[q][cg];
+      *(f32x4*)(red + (((wave * NQ + q) * NCG + cg) * 64 + lane) * 4) = acc[q][cg];
   __syncthreads();
-  for (int idx = threadIdx.x; idx < 32 * 16 * NCG; idx += NT) {
-    const int n = idx & 31, s = idx >> 5;
+  for (int idx = threadIdx.x; idx < R * 16 * NCG; idx += NT) {
+    const int n = idx % R, s = idx / R;
     const int t2 = n >> 4, n16 = n & 15, cg = s >> 4, s16 = s & 15;
     const int l = (n16 >> 2) * 16 + s16, i = n16 & 3;
     float gs = 0.f, us = 0.f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-      gs += red[(((w * 4 + t2) * NCG + cg) * 64 + l) * 4 + i];
-      us += red[(((w * 4 + 2 + t2) * NCG + cg) * 64 + l) * 4 + i];
+      gs += red[(((w * NQ + t2) * NCG + cg) * 64 + l) * 4 + i];
+      us += red[(((w * NQ + CT + t2) * NCG + cg) * 64 + l) * 4 + i];
     }
-    midf[s * 33 + n] = silu_mul(gs, us);
+    midf[s * (R + 1) + n] = silu_mul(gs, us);
   }
   __syncthreads();
   if (!shared && p.fmt == MK2_FMT_MXFP4) {
-    for (int s = threadIdx.x; s < p.M; s += NT) {
-      float amax = 0.f;
-      for (int n = 0; n < 32; ++n) amax = fmaxf(amax, fabsf(midf[s * 33 + n]));
+    // MXFP8 per 32 values of a row: 32 lanes a block, amax by shuffles, 4 codes a store
+    for (int idx = threadIdx.x; idx < R * p.M; idx += NT) {
+      const int n = idx % R, s = idx / R;
+      const float v = midf[s * (R + 1) + n];
+      float amax = fabsf(v);
+#pragma unroll
+      for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
       const uint32_t code = mxfp8_scale_code(amax);
-      const float inv = e8m0_inverse(code);
-      uint32_t qw[8];
-      for (int i = 0; i < 8; ++i)
-        qw[i] = f32x4_to_e4m3x4(midf[s * 33 + 4 * i] * inv, midf[s * 33 + 4 * i + 1] * inv,
-                                midf[s * 33 + 4 * i + 2] * inv, midf[s * 33 + 4 * i + 3] * inv);
-      uint4* dst = (uint4*)(p.mid_q + ((size_t)j * p.M + s) * p.I + c * 32);
-      st_dev_16(dst, make_uint4(qw[0], qw[1], qw[2], qw[3]));
-      st_dev_16(dst + 1, make_uint4(qw[4], qw[5], qw[6], qw[7]));
-      st_dev_u8(p.mid_s + ((size_t)j * p.M + s) * (p.I / 32) + c, code);
+      const uint32_t q = f32_to_e4m3(v * e8m0_inverse(code));
+      const uint32_t w = q | (__shfl_down(q, 1, 64) << 8) | (__shfl_down(q, 2, 64) << 16) |
+                         (__shfl_down(q, 3, 64) << 24);
+      if ((n & 3) == 0) st_dev_u32(p.mid_q + ((size_t)j * p.M + s) * p.I + c * R + n, w);
+      if ((n & 31) == 0) st_dev_u8(p.mid_s + ((size_t)j * p.M + s) * (p.I / 32) + c * (R / 32) + (n >> 5), code);
     }
   } else {
     bf16_t* dst = shared ? p.mid_sh : p.mid_b + (size_t)j * p.M * p.I;
-    for (int idx = threadIdx.x; idx < 32 * p.M; idx += NT) {
-      const int n = idx & 31, s = idx >> 5;
-      st_dev_u16(dst + (size_t)s * I + c * 32 + n, f32_to_bf16(midf[s * 33 + n]));
+    for (int idx = threadIdx.x; idx < R * p.M; idx += NT) {
+      const int n = idx % R, s = idx / R;
+      st_dev_u16(dst + (size_t)s * I + c * R + n, f32_to_bf16(midf[s * (R + 1) + n]));
     }
   }
   __syncthreads();
+}
+
+// task t < Dmax * (I / UC): routed slot j = t / (I / UC), chunk of UC rows; past that
+// the shared expert's 32-row chunks.  red: NW * 2 * CT * NCG * 256 floats (CT = UC/16);
+// midf: 32 * (UC + 1) floats.
+template <int NT, int NCG>
+MK2_DEV void moe_upgate(const MoeDev& p, int t, float* red, float* midf) {
+  const int chunks_r = p.I / p.UC;
+  if (t < p.Dmax * chunks_r) {
+    const int j = t / chunks_r, c = t % chunks_r;
+    if (j >= ldp_i32(p.act)) return;
+    const int e = ldp_i32(p.act + 1 + j);
+    if (e < 0 || e >= p.E) return;
+    if (NCG == 1 && p.UC == 64) upgate_chunk<NT, NCG, (NCG == 1 ? 4 : 2)>(p, false, j, e, c, red, midf);
+    else upgate_chunk<NT, NCG, 2>(p, false, j, e, c, red, midf);
+  } else {
+    upgate_chunk<NT, NCG, 2>(p, true, 0, 0, t - p.Dmax * chunks_r, red, midf);
+  }
 }
 
 // ---------------------------------------------------------- stage: down + combine

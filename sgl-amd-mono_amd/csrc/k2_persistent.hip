@@ -25,22 +25,28 @@ namespace mk2 {
 
 constexpr int K2_NT = 512;
 
-// sync block (int words at the start of the layer workspace)
+// The sync block at the start of the layer workspace: one counter a 128-byte line
+// (counters that share a line serialize each other's atomics).  A counter with many
+// producers is split into K2_LANES sub-counters on lines of their own, producer t
+// adding to sub-counter t mod K2_LANES; a waiter sums them.
+constexpr int SY_LINE = 32;  // ints a line
+constexpr int K2_LANES = 16;
 enum : int {
   SY_SCORE = 0,    // [32] score chunks done, per row
   SY_SLICE = 32,   // [32] top-k slices done, per row
   SY_TOPK = 64,    // [32] top-k done, per row
   SY_SPLIT = 96,   // [32] attention splits done, per row
   SY_MERGE = 128,  // [16] merged rows, per head
-  SY_UV = 144,
-  SY_OPROJ,
-  SY_PREP,
-  SY_ROUTER,
+  SY_PREP = 144,
   SY_ROUTE,
-  SY_UP,
-  SY_DONE,        // workgroups finished (the last one resets)
-  SY_ERR,         // sticky: a wait ran out of its spin limit
-  SY_WORDS = 256
+  SY_ROUTER_LAST,  // router sub-counters completed (the last runs the routing)
+  SY_DONE,         // workgroups finished (the last one resets)
+  SY_ERR,          // sticky: a wait ran out of its spin limit
+  SY_UV = 160,     // [K2_LANES] sub-counters each
+  SY_OPROJ = SY_UV + K2_LANES,
+  SY_ROUTER = SY_OPROJ + K2_LANES,
+  SY_UP = SY_ROUTER + K2_LANES,
+  SY_LINES = SY_UP + K2_LANES  // 224 lines = 28 KiB
 };
 
 struct K2Dev {
@@ -81,46 +87,87 @@ union K2Lds {
   float red[(K2_NT / 64) * 2 * 64 * 4];
 };
 
-// publish a finished task: every thread's stores drained, then one increment
-MK2_DEV void k2_signal(int* c) {
+MK2_DEV int* k2_ctr(const K2Dev& p, int line) { return p.sync + line * SY_LINE; }
+
+// publish a finished task on counter `line` (sub-counter t mod lanes): every thread's
+// stores drained, then one increment
+MK2_DEV void k2_signal(const K2Dev& p, int line, int t = 0, int lanes = 1) {
   drain_memory();
   __syncthreads();
-  if (threadIdx.x == 0) __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0)
+    __hip_atomic_fetch_add(k2_ctr(p, line + t % lanes), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// wait until counter `slot` reaches `target`.  `seen` (LDS) caches the counts this
-// workgroup has observed (counters only grow within a launch), so a wait that an
-// earlier one already satisfied costs nothing.  The early return is uniform: seen is
-// written only just after this function's barrier, and every task ends with a barrier
-// before the next wait reads it.
-MK2_DEV void k2_wait(const K2Dev& p, int* seen, int slot, int target, int stamp = -1) {
-  if (seen[slot] >= target) return;
-  int v = 0;
+// publish task t of n on a K2_LANES counter and tell whether it completed the set: the
+// last arrival on each sub-counter counts on SY_ROUTER_LAST-style `top`, and the last of
+// those is the last overall.  That workgroup runs the stage that needs all n (no
+// further hand-off, no poll).
+MK2_DEV bool k2_signal_last(const K2Dev& p, int line, int top, int t, int n, int* flag) {
+  drain_memory();
+  __syncthreads();
   if (threadIdx.x == 0) {
-    const int* c = p.sync + slot;
-    int* err = p.sync + SY_ERR;
-    int n = 0;
-    while ((v = __hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) < target) {
-      if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
-      if (++n > p.spin_limit) {
-        atomicOr(err, 1);
-        break;
-      }
-      __builtin_amdgcn_s_sleep(1);
-    }
-    if (stamp >= 0 && p.timeline) p.timeline[(size_t)blockIdx.x * K2_STAMPS + stamp] = __builtin_amdgcn_s_memrealtime();
+    const int sub = t % K2_LANES;
+    const int expect = n / K2_LANES + (sub < n % K2_LANES ? 1 : 0);  // tasks on this sub-counter
+    const int subs = n < K2_LANES ? n : K2_LANES;
+    int last = 0;
+    if (__hip_atomic_fetch_add(k2_ctr(p, line + sub), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == expect - 1)
+      last = __hip_atomic_fetch_add(k2_ctr(p, top), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == subs - 1;
+    *flag = last;
   }
   __syncthreads();
-  if (threadIdx.x == 0) seen[slot] = v;
+  return *flag != 0;
+}
+
+// the same on a single counter of n producers
+MK2_DEV bool k2_signal_last1(const K2Dev& p, int line, int n, int* flag) {
+  drain_memory();
+  __syncthreads();
+  if (threadIdx.x == 0)
+    *flag = __hip_atomic_fetch_add(k2_ctr(p, line), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n - 1;
+  __syncthreads();
+  return *flag != 0;
+}
+
+// wait until counter `line` (summed over `lanes` sub-counters) reaches `target`.  Wave
+// 0 polls, one coherent load a lane a poll; the error word every 32 polls.  `seen`
+// (LDS, by line) caches the counts this workgroup has observed (counters only grow
+// within a launch), so a wait that an earlier one already satisfied costs nothing.  The
+// early return is uniform: seen is written only just after this function's barrier,
+// and every task ends with a barrier before the next wait reads it.
+MK2_DEV void k2_wait(const K2Dev& p, int* seen, int line, int target, int stamp = -1, int lanes = 1) {
+  if (seen[line] >= target) return;
+  int v = 0;
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    const int* err = k2_ctr(p, SY_ERR);
+    int n = 0;
+    while (true) {
+      int c = lane < lanes ? __hip_atomic_load(k2_ctr(p, line + lane), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+#pragma unroll
+      for (int o = 8; o > 0; o >>= 1) c += __shfl_xor(c, o, 64);  // lanes <= 16
+      v = __shfl(c, 0, 64);
+      if (v >= target) break;
+      if ((++n & 31) == 0 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
+      if (n > p.spin_limit) {
+        if (lane == 0) atomicOr(k2_ctr(p, SY_ERR), 1);
+        break;
+      }
+    }
+    if (lane == 0 && stamp >= 0 && p.timeline)
+      p.timeline[(size_t)blockIdx.x * K2_STAMPS + stamp] = __builtin_amdgcn_s_memrealtime();
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) seen[line] = v;
 }
 
 template <int NCG>
 __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
   __shared__ K2Lds S;
-  __shared__ int seen[SY_WORDS];
+  __shared__ int seen[SY_LINES];
+  __shared__ int last_flag;
   const int G = gridDim.x, b = blockIdx.x;
   const int R = p.rows;
-  for (int i = threadIdx.x; i < SY_WORDS; i += K2_NT) seen[i] = 0;
+  for (int i = threadIdx.x; i < SY_LINES; i += K2_NT) seen[i] = 0;
   __syncthreads();
   int base = 0;  // this stage's first workgroup
 // the tasks of a stage of n tasks on this workgroup; `t < G` marks the first
@@ -132,29 +179,28 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
   const int nchk = p.idx.nchk;
   K2_TASKS(t, R * nchk) {
     idx_score<K2_NT>(p.idx, t / nchk, t % nchk, S.score);
-    k2_signal(p.sync + SY_SCORE + t / nchk);
+    k2_signal(p, SY_SCORE + t / nchk);
   }
   k2_stamp(p, 3 * st++ + 2);
   // ---- top-k slices: each chunk's candidates
   k2_stamp(p, 3 * st);
-  // slices on the workgroups of their score chunks (base unchanged)
+  // slices on the workgroups of their score chunks (base unchanged); the last slice
+  // of a row runs the row's exact top-k over the candidates
   K2_TASKS(t, R * nchk) {
     const int r = t / nchk;
     k2_wait(p, seen, SY_SCORE + r, nchk, t < G ? 3 * st + 1 : -1);
     idx_slice<K2_NT>(p.idx, r, t % nchk, S.topk);
-    k2_signal(p.sync + SY_SLICE + r);
+    if (k2_signal_last1(p, SY_SLICE + r, nchk, &last_flag)) {
+      k2_stamp(p, 3 * (st + 1));
+      k2_stamp(p, 3 * (st + 1) + 1);
+      idx_select<K2_NT>(p.idx, r, S.topk);
+      k2_signal(p, SY_TOPK + r);
+      k2_stamp(p, 3 * (st + 1) + 2);
+    }
   }
   K2_NEXT(R * nchk);
   k2_stamp(p, 3 * st++ + 2);
-  // ---- exact top-k of each row over its candidates
-  k2_stamp(p, 3 * st);
-  K2_TASKS(t, R) {
-    k2_wait(p, seen, SY_SLICE + t, nchk, t < G ? 3 * st + 1 : -1);
-    idx_select<K2_NT>(p.idx, t, S.topk);
-    k2_signal(p.sync + SY_TOPK + t);
-  }
-  K2_NEXT(R);
-  k2_stamp(p, 3 * st++ + 2);
+  ++st;  // the select stamps are taken above
   // ---- sparse-MLA splits
   k2_stamp(p, 3 * st);
   const int ns = p.mla.nsplit;
@@ -162,7 +208,7 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
     const int r = t / ns;
     k2_wait(p, seen, SY_TOPK + r, 1, t < G ? 3 * st + 1 : -1);
     mla_split<K2_NT>(p.mla, r, t % ns, S.split);
-    k2_signal(p.sync + SY_SPLIT + r);
+    k2_signal(p, SY_SPLIT + r);
   }
   K2_NEXT(R * ns);
   k2_stamp(p, 3 * st++ + 2);
@@ -172,7 +218,7 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
     const int r = t / MLA_HEADS, h = t % MLA_HEADS;
     k2_wait(p, seen, SY_SPLIT + r, ns, t < G ? 3 * st + 1 : -1);
     mla_merge<K2_NT>(p.mla, r, h, S.merge);
-    k2_signal(p.sync + SY_MERGE + h);
+    k2_signal(p, SY_MERGE + h);
   }
   K2_NEXT(R * MLA_HEADS);
   k2_stamp(p, 3 * st++ + 2);
@@ -183,7 +229,7 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
     const int h = t / vtn;
     mla_uv<K2_NT, NCG>(p.mla, h, t % vtn, S.red,
                        [&] { k2_wait(p, seen, SY_MERGE + h, R, t < G ? 3 * st + 1 : -1); });
-    k2_signal(p.sync + SY_UV);
+    k2_signal(p, SY_UV, t, K2_LANES);
   }
   K2_NEXT(MLA_HEADS * vtn);
   k2_stamp(p, 3 * st++ + 2);
@@ -192,17 +238,17 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
   const int ht = p.mla.hidden / 16;
   K2_TASKS(t, ht) {
     mla_oproj<K2_NT, NCG>(p.mla, t, S.red,
-                          [&] { k2_wait(p, seen, SY_UV, MLA_HEADS * vtn, t < G ? 3 * st + 1 : -1); });
-    k2_signal(p.sync + SY_OPROJ);
+                          [&] { k2_wait(p, seen, SY_UV, MLA_HEADS * vtn, t < G ? 3 * st + 1 : -1, K2_LANES); });
+    k2_signal(p, SY_OPROJ, t, K2_LANES);
   }
   K2_NEXT(ht);
   k2_stamp(p, 3 * st++ + 2);
   // ---- RMSNorm + activation quant, per row
   k2_stamp(p, 3 * st);
   K2_TASKS(t, R) {
-    k2_wait(p, seen, SY_OPROJ, ht, t < G ? 3 * st + 1 : -1);
+    k2_wait(p, seen, SY_OPROJ, ht, t < G ? 3 * st + 1 : -1, K2_LANES);
     moe_prep<K2_NT>(p.moe, t, S.red);
-    k2_signal(p.sync + SY_PREP);
+    k2_signal(p, SY_PREP);
   }
   K2_NEXT(R);
   k2_stamp(p, 3 * st++ + 2);
@@ -212,19 +258,18 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
   K2_TASKS(t, nrt) {
     moe_router<K2_NT, NCG>(p.moe, t % et, t / et, S.red,
                            [&] { k2_wait(p, seen, SY_PREP, R, t < G ? 3 * st + 1 : -1); });
-    k2_signal(p.sync + SY_ROUTER);
+    // the last router task computes the routing
+    if (k2_signal_last(p, SY_ROUTER, SY_ROUTER_LAST, t, nrt, &last_flag)) {
+      k2_stamp(p, 3 * (st + 1));
+      k2_stamp(p, 3 * (st + 1) + 1);
+      moe_route<K2_NT>(p.moe, S.route.logits, S.route.slot);
+      k2_signal(p, SY_ROUTE);
+      k2_stamp(p, 3 * (st + 1) + 2);
+    }
   }
   K2_NEXT(nrt);
   k2_stamp(p, 3 * st++ + 2);
-  // ---- top-k routing (one task)
-  k2_stamp(p, 3 * st);
-  K2_TASKS(t, 1) {
-    k2_wait(p, seen, SY_ROUTER, nrt, t < G ? 3 * st + 1 : -1);
-    moe_route<K2_NT>(p.moe, S.route.logits, S.route.slot);
-    k2_signal(p.sync + SY_ROUTE);
-  }
-  K2_NEXT(1);
-  k2_stamp(p, 3 * st++ + 2);
+  ++st;  // routing: run by the last router task above
   // ---- up/gate + SwiGLU: the shared expert's chunks first (they need only the
   // normalized rows, so they run while routing is still pending), then the routed
   // slots
@@ -237,14 +282,14 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
     if (sh) k2_wait(p, seen, SY_PREP, R, t < G ? 3 * st + 1 : -1);
     else k2_wait(p, seen, SY_ROUTE, 1, t < G ? 3 * st + 1 : -1);
     moe_upgate<K2_NT, NCG>(p.moe, sh ? up_r + t : t - up_sh, S.up.red, S.up.midf);
-    k2_signal(p.sync + SY_UP);
+    k2_signal(p, SY_UP, t, K2_LANES);
   }
   K2_NEXT(up_total);
   k2_stamp(p, 3 * st++ + 2);
   // ---- down + route weighting + residual, per 16 hidden rows
   k2_stamp(p, 3 * st);
-  K2_TASKS(t, p.moe.H / 16) {
-    k2_wait(p, seen, SY_UP, up_total, t < G ? 3 * st + 1 : -1);
+  K2_TASKS(t, p.moe.H / (16 * p.moe.DT)) {
+    k2_wait(p, seen, SY_UP, up_total, t < G ? 3 * st + 1 : -1, K2_LANES);
     moe_down<K2_NT, NCG>(p.moe, t, S.down.red, S.down.act);
   }
   k2_stamp(p, 3 * st + 2);
@@ -252,16 +297,15 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
 #undef K2_NEXT
   // ---- the last workgroup out resets the counters for the next launch
   __syncthreads();
-  if (threadIdx.x == 0) {
-    __threadfence();
-    if (atomicAdd(p.sync + SY_DONE, 1) == G - 1) {
-      const int err = atomicAdd(p.sync + SY_ERR, 0);
-      for (int i = 0; i < SY_DONE; ++i) atomicExch(p.sync + i, 0);
-      if (p.status) *p.status = err;
-      atomicExch(p.sync + SY_ERR, 0);
-      atomicExch(p.sync + SY_DONE, 0);
-      __threadfence();
-    }
+  if (threadIdx.x == 0)
+    last_flag = __hip_atomic_fetch_add(k2_ctr(p, SY_DONE), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == G - 1;
+  __syncthreads();
+  if (last_flag) {
+    if (threadIdx.x == 0 && p.status)
+      *p.status = __hip_atomic_load(k2_ctr(p, SY_ERR), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    for (int l = threadIdx.x; l < SY_LINES; l += K2_NT)
+      __hip_atomic_store(k2_ctr(p, l), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 

@@ -20,7 +20,7 @@ int moe_enqueue(const MoeDev& d, hipStream_t st);
 int k2_persistent_enqueue(const IdxDev& idx, const MlaDev& mla, const MoeDev& moe, int* sync,
                           int* status, uint64_t* timeline, int rows, int spin_limit, hipStream_t st);
 
-constexpr int LAYER_SYNC_BYTES = 1024;
+constexpr int LAYER_SYNC_BYTES = 32 * 1024;  // the persistent launch's counters, a line each
 
 struct LayerPlan {
   IdxDev idx;

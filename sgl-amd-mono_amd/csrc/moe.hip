@@ -23,7 +23,7 @@ __global__ __launch_bounds__(256) void k_moe_router(MoeDev p) {
 __global__ __launch_bounds__(ROUTE_NT) void k_moe_route(MoeDev p) {
   extern __shared__ float dyn[];
   float* logits = dyn;
-  int* slot = (int*)(dyn + p.M * p.E);
+  int* slot = (int*)(dyn + (p.M * p.E > p.Dmax * 32 ? p.M * p.E : p.Dmax * 32));
   moe_route<ROUTE_NT>(p, logits, slot);
 }
 
@@ -36,7 +36,7 @@ __global__ __launch_bounds__(MOE_NT) void k_moe_upgate(MoeDev p) {
 
 template <int NCG>
 __global__ __launch_bounds__(MOE_NT) void k_moe_down(MoeDev p) {
-  __shared__ float red[(MOE_NT / 64) * NCG * 64 * 4];
+  __shared__ float red[(MOE_NT / 64) * 2 * 64 * 4];  // NW * DT * NCG * 256, DT * NCG <= 2
   __shared__ int act_ids[256];
   moe_down<MOE_NT, NCG>(p, blockIdx.x, red, act_ids);
 }
@@ -78,6 +78,7 @@ size_t moe_carve(const mk2_moe_shape* s, void* base, MoeDev* d) {
   t.KC = KC;
   t.Dmax = Dmax;
   t.UC = (s->expert_fmt == MK2_FMT_MXFP4 && M <= 16 && I % 64 == 0) ? 64 : 32;
+  t.DT = (s->expert_fmt == MK2_FMT_MXFP4 && M <= 16 && H % 32 == 0) ? 2 : 1;
   t.xn = c.take<bf16_t>((size_t)M * H);
   t.xq = c.take<uint8_t>((size_t)M * H);
   t.xs = c.take<uint8_t>((size_t)M * H / 32);
@@ -95,7 +96,7 @@ size_t moe_carve(const mk2_moe_shape* s, void* base, MoeDev* d) {
   }
   t.mid_sh = c.take<bf16_t>((size_t)M * (s->n_shared ? s->shared_inter : 0) + 1);
   if (d) {
-    d->KC = t.KC; d->Dmax = t.Dmax; d->UC = t.UC; d->xn = t.xn; d->xq = t.xq; d->xs = t.xs;
+    d->KC = t.KC; d->Dmax = t.Dmax; d->UC = t.UC; d->DT = t.DT; d->xn = t.xn; d->xq = t.xq; d->xs = t.xs;
     d->logit_part = t.logit_part; d->logits = t.logits; d->topk_ids = t.topk_ids;
     d->topk_w = t.topk_w; d->act = t.act; d->rw = t.rw; d->mid_q = t.mid_q;
     d->mid_s = t.mid_s; d->mid_b = t.mid_b; d->mid_sh = t.mid_sh;
@@ -130,14 +131,14 @@ int moe_enqueue(const MoeDev& d, hipStream_t st) {
   k_moe_prep<<<d.M, 256, 0, st>>>(d);
   if (ncg == 1) k_moe_router<1><<<dim3(d.E / 16, d.KC), 256, 0, st>>>(d);
   else k_moe_router<2><<<dim3(d.E / 16, d.KC), 256, 0, st>>>(d);
-  const size_t route_lds =
-      (size_t)d.M * d.E * 4 + (size_t)(d.E + 28 * (ROUTE_NT / 64) + 2 * d.M * d.topk) * 4;
+  const int lg = d.M * d.E > d.Dmax * 32 ? d.M * d.E : d.Dmax * 32;
+  const size_t route_lds = (size_t)lg * 4 + (size_t)(d.E + 28 * (ROUTE_NT / 64) + 2 * d.M * d.topk) * 4;
   k_moe_route<<<1, ROUTE_NT, route_lds, st>>>(d);
   const int up_tasks = d.Dmax * (d.I / d.UC) + d.n_shared * (d.SI / 32);
   if (ncg == 1) k_moe_upgate<1><<<up_tasks, MOE_NT, 0, st>>>(d);
   else k_moe_upgate<2><<<up_tasks, MOE_NT, 0, st>>>(d);
-  if (ncg == 1) k_moe_down<1><<<d.H / 16, MOE_NT, 0, st>>>(d);
-  else k_moe_down<2><<<d.H / 16, MOE_NT, 0, st>>>(d);
+  if (ncg == 1) k_moe_down<1><<<d.H / (16 * d.DT), MOE_NT, 0, st>>>(d);
+  else k_moe_down<2><<<d.H / (16 * d.DT), MOE_NT, 0, st>>>(d);
   return check_launch("moe");
 }
 

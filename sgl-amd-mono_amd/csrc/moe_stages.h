@@ -15,6 +15,7 @@ struct MoeDev {
   int KC;    // router k-chunks
   int Dmax;  // capacity of the distinct-expert list
   int UC;    // intermediate rows of a routed up/gate task (64: MXFP4 at <= 16 rows, else 32)
+  int DT;    // 16-row hidden tiles of a down task (2: MXFP4 at <= 16 rows, else 1)
   float route_scale, eps;
   const bf16_t* x;
   const bf16_t* gamma;
@@ -233,24 +234,32 @@ MK2_DEV void moe_router(const MoeDev& p, int nt, int kc, float* red, Wait wait =
 // finds the top-k by (key desc, expert asc) with a bitwise search for the k-th key
 // (ballot counts, no shuffles), ranks the picks, and computes their weights; then
 // the distinct-expert list (ascending) and the dense route-weight table rw.
-// lds_logits: M*E floats; lds_slot: E + 4*NW ints, 24 a wave of pick scratch, then
-// the picks' ids and weights (2*M*topk).
+// lds_logits: max(M*E, Dmax*32) floats (the logits, then the route-weight table);
+// lds_slot: E + 4*NW ints, 24 a wave of pick scratch, then the picks' ids and weights
+// (2*M*topk).
 template <int NT>
 MK2_DEV void moe_route(const MoeDev& p, float* lds_logits, int* lds_slot) {
   constexpr int NW = NT / 64;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int ME = p.M * p.E;
+  const int per = p.E / 64;  // experts a lane holds: e = lane + 64 * i
+  // the lane's router biases, loaded with the partials (every load unconditional and
+  // in bounds, so that none waits for another)
+  float bias[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    bias[i] = p.router == MK2_ROUTER_SIGMOID_BIAS ? p.bias[min(lane + 64 * i, p.E - 1)] : 0.f;
   for (int idx = tid * 4; idx < ME; idx += NT * 4) {
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int kc0 = 0; kc0 < p.KC; kc0 += 8) {
       float4 t[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        t[u] = kc0 + u < p.KC ? ldp_f32x4(p.logit_part + (size_t)(kc0 + u) * ME + idx)
-                              : make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int u = 0; u < 8; ++u) t[u] = ldp_f32x4(p.logit_part + (size_t)min(kc0 + u, p.KC - 1) * ME + idx);
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        v.x += t[u].x; v.y += t[u].y; v.z += t[u].z; v.w += t[u].w;
+        if (kc0 + u < p.KC) {
+          v.x += t[u].x; v.y += t[u].y; v.z += t[u].z; v.w += t[u].w;
+        }
       }
     }
     *(float4*)(lds_logits + idx) = v;
@@ -258,7 +267,6 @@ MK2_DEV void moe_route(const MoeDev& p, float* lds_logits, int* lds_slot) {
   }
   for (int e = tid; e < p.E; e += NT) lds_slot[e] = 0;
   __syncthreads();
-  const int per = p.E / 64;  // experts a lane holds: e = lane + 64 * i
   int* pick = lds_slot + p.E + 4 * NW + wave * 24;  // [8 keys][8 ids][8 values]
   int* lds_ids = lds_slot + p.E + 28 * NW;          // [M][topk]
   float* lds_w = (float*)(lds_ids + p.M * p.topk);  // [M][topk]
@@ -267,17 +275,17 @@ MK2_DEV void moe_route(const MoeDev& p, float* lds_logits, int* lds_slot) {
     float sv[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      if (i >= per) break;
-      const int e = lane + 64 * i;
-      const float lg = lds_logits[r * p.E + e];
+      const float lg = lds_logits[r * p.E + min(lane + 64 * i, p.E - 1)];
+      float sg = lg;
+      uint32_t kk;
       if (p.router == MK2_ROUTER_SIGMOID_BIAS) {
-        const float sg = 1.0f / (1.0f + expf(-lg));
-        sv[i] = sg;
-        key[i] = radix_key(sg + p.bias[e]);
+        sg = 1.0f / (1.0f + expf(-lg));
+        kk = radix_key(sg + bias[i]);
       } else {
-        sv[i] = lg;
-        key[i] = radix_key(lg);
+        kk = radix_key(lg);
       }
+      sv[i] = i < per ? sg : 0.f;
+      key[i] = i < per ? kk : 0u;
     }
     // the k-th largest key: the largest T with count(key >= T) >= topk
     uint32_t T = 0u;
@@ -286,19 +294,18 @@ MK2_DEV void moe_route(const MoeDev& p, float* lds_logits, int* lds_slot) {
       int cnt = 0;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        if (i < per) cnt += __popcll(__ballot(key[i] >= cand));
+        cnt += __popcll(__ballot(key[i] >= cand));  // lanes past E hold key 0 < cand
       if (cnt >= p.topk) T = cand;
     }
     int n_gt = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      if (i < per) n_gt += __popcll(__ballot(key[i] > T));
+      n_gt += __popcll(__ballot(key[i] > T));
     const int ties = p.topk - n_gt;  // keys == T taken in expert order
     const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     int tie_before = 0, sel_before = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      if (i >= per) break;
       const uint64_t tm = __ballot(key[i] == T);
       const bool is_tie = key[i] == T;
       const int tie_rank = tie_before + __popcll(tm & below);
@@ -380,14 +387,16 @@ MK2_DEV void moe_route(const MoeDev& p, float* lds_logits, int* lds_slot) {
     }
   }
   if (tid == 0) st_dev_i32(p.act, total);
-  for (int idx = tid; idx < total * 32; idx += NT) st_dev_f32(p.rw + idx, 0.f);
-  // the zeros land before any weight below overwrites one of them
-  drain_memory();
+  // the route-weight table, built in LDS (over the logits, which are done) and
+  // stored once
+  float* lrw = lds_logits;  // [total][32]
+  for (int idx = tid; idx < total * 32; idx += NT) lrw[idx] = 0.f;
   __syncthreads();
-  for (int idx = tid; idx < p.M * p.topk; idx += NT) {
-    const int r = idx / p.topk;
-    st_dev_f32(p.rw + lds_slot[lds_ids[idx]] * 32 + r, lds_w[idx]);
-  }
+  for (int idx = tid; idx < p.M * p.topk; idx += NT) lrw[lds_slot[lds_ids[idx]] * 32 + idx / p.topk] = lds_w[idx];
+  __syncthreads();
+  for (int idx = 4 * tid; idx < total * 32; idx += 4 * NT)
+    st_dev_16(p.rw + idx, make_uint4(__float_as_uint(lrw[idx]), __float_as_uint(lrw[idx + 1]),
+                                     __float_as_uint(lrw[idx + 2]), __float_as_uint(lrw[idx + 3])));
 }
 
 // ------------------------------------------------------- stage: up/gate + SwiGLU
@@ -552,84 +561,93 @@ MK2_DEV void moe_upgate(const MoeDev& p, int t, float* red, float* midf) {
 }
 
 // ---------------------------------------------------------- stage: down + combine
-// task nt: 16 hidden rows; every slot (shared, then the D routed experts) adds
-// rw * W_down[e] . mid into the rows' accumulators; out = bf16(y [+ x]).  Waves
-// take every NW-th slot, a batch of slots' weight tiles in flight at once.
-// act_ids: LDS >= E ints
-template <int NT, int NCG>
-MK2_DEV void moe_down(const MoeDev& p, int nt, float* red, int* act_ids) {
+// A task is 16*DT hidden rows; every slot (the shared expert, then the D routed
+// experts) adds rw * W_down[e] . mid into the rows' accumulators; out = bf16(y [+ x]).
+// Waves take every NW-th slot, a batch of slots' weight tiles (and their mid rows,
+// shared by the DT tiles) in flight at once.  act_ids: LDS >= E ints; red: NW * DT *
+// NCG * 256 floats.
+template <int NT, int NCG, int DT>
+MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids) {
   constexpr int NW = NT / 64;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, c16 = lane & 15;
   const int D = min(ldp_i32(p.act), p.Dmax);
   for (int j = threadIdx.x; j < D; j += NT) act_ids[j] = min(max(ldp_i32(p.act + 1 + j), 0), p.E - 1);
   __syncthreads();
   const int HT = p.H / 16;
-  f32x4 acc[NCG];
+  const int t0 = nt * DT;  // first 16-row tile
+  f32x4 acc[DT][NCG];
 #pragma unroll
-  for (int cg = 0; cg < NCG; ++cg) acc[cg] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int d = 0; d < DT; ++d)
+#pragma unroll
+    for (int cg = 0; cg < NCG; ++cg) acc[d][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
   // the shared expert (FP8, bf16 mid): its k-blocks spread over the waves
   if (p.n_shared) {
     const int KB2 = p.SI / 128;
     for (int kb = wave; kb < KB2; kb += NW) {
-      bf16x8 a[4];
-      load_a_fp8(p.ws2 + ((size_t)nt * KB2 + kb) * 2048, lane, a);
-      const float sc = p.ss2[(nt * 16 / 128) * KB2 + kb];
+      bf16x8 b[NCG][4];
 #pragma unroll
-      for (int cg = 0; cg < NCG; ++cg) {
-        bf16x8 b[4];
-        load_b_bf16(p.mid_sh, cg * 16 + c16, p.M, p.SI, kb * 128 + 32 * g, b);
-        acc[cg] += mfma4_bf16(a, b, f32x4{0.f, 0.f, 0.f, 0.f}) * sc;
+      for (int cg = 0; cg < NCG; ++cg) load_b_bf16(p.mid_sh, cg * 16 + c16, p.M, p.SI, kb * 128 + 32 * g, b[cg]);
+#pragma unroll
+      for (int d = 0; d < DT; ++d) {
+        bf16x8 a[4];
+        load_a_fp8(p.ws2 + ((size_t)(t0 + d) * KB2 + kb) * 2048, lane, a);
+        const float sc = p.ss2[((t0 + d) * 16 / 128) * KB2 + kb];
+#pragma unroll
+        for (int cg = 0; cg < NCG; ++cg) acc[d][cg] += mfma4_bf16(a, b[cg], f32x4{0.f, 0.f, 0.f, 0.f}) * sc;
       }
     }
   }
   const int KB2 = p.I / 128;
   if (p.fmt == MK2_FMT_MXFP4) {
-    constexpr int B = NCG == 1 ? 4 : 2;  // slots in flight a wave
-    constexpr int KC = 2;                // k-blocks of a slot a pass
+    constexpr int B = DT == 2 ? 2 : (NCG == 1 ? 4 : 2);  // slots in flight a wave
+    constexpr int KC = 2;                                // k-blocks of a slot a pass
     const int G2 = (KB2 + 3) / 4;
     for (int j0 = wave; j0 < D; j0 += NW * B) {
-      f32x4 tmp[B][NCG];
+      f32x4 tmp[B][DT][NCG];
 #pragma unroll
       for (int u = 0; u < B; ++u)
 #pragma unroll
-        for (int cg = 0; cg < NCG; ++cg) tmp[u][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int d = 0; d < DT; ++d)
+#pragma unroll
+          for (int cg = 0; cg < NCG; ++cg) tmp[u][d][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
       for (int kb0 = 0; kb0 < KB2; kb0 += KC) {
-        i32x8 a[B][KC], bq[B][KC][NCG];
-        int sa[B], sbq[B][KC][NCG];
+        i32x8 a[B][DT][KC], bq[B][KC][NCG];
+        int sa[B][DT], sbq[B][KC][NCG];
 #pragma unroll
         for (int u = 0; u < B; ++u) {
-          const int j = j0 + u * NW;
-          if (j < D) {
-            const int e = act_ids[j];
-            const uint8_t* wb = p.w2 + ((size_t)e * HT + nt) * KB2 * 1024;
+          const int j = min(j0 + u * NW, D - 1);  // past the list: a valid slot, unused
+          const int e = act_ids[j];
 #pragma unroll
-            for (int c = 0; c < KC; ++c) {
-              const int kb = kb0 + c;
-              if (kb < KB2) {
-                a[u][c] = load_a_fp4(wb + (size_t)kb * 1024, lane);
+          for (int c = 0; c < KC; ++c) {
+            const int kb = min(kb0 + c, KB2 - 1);
 #pragma unroll
-                for (int cg = 0; cg < NCG; ++cg) {
-                  const int row = cg * 16 + c16;
-                  bq[u][c][cg] = load_b_fp8(p.mid_q + (size_t)j * p.M * p.I, row, p.M, p.I, kb * 128, g);
-                  sbq[u][c][cg] = row < p.M ? (int)ldp_u8(p.mid_s + ((size_t)j * p.M + row) * (p.I / 32) + kb * 4 + g) : 127;
-                }
-              }
+            for (int d = 0; d < DT; ++d)
+              a[u][d][c] = load_a_fp4(p.w2 + (((size_t)e * HT + t0 + d) * KB2 + kb) * 1024, lane);
+#pragma unroll
+            for (int cg = 0; cg < NCG; ++cg) {
+              const int row = cg * 16 + c16;
+              bq[u][c][cg] = load_b_fp8(p.mid_q + (size_t)j * p.M * p.I, row, p.M, p.I, kb * 128, g);
+              sbq[u][c][cg] = row < p.M ? (int)ldp_u8(p.mid_s + ((size_t)j * p.M + row) * (p.I / 32) + kb * 4 + g) : 127;
             }
-            sa[u] = (int)*(const uint32_t*)(p.s2 + ((((size_t)e * HT + nt) * G2 + kb0 / 4) * 64 + lane) * 4);
           }
+#pragma unroll
+          for (int d = 0; d < DT; ++d)
+            sa[u][d] = (int)*(const uint32_t*)(p.s2 + ((((size_t)e * HT + t0 + d) * G2 + kb0 / 4) * 64 + lane) * 4);
         }
 #pragma unroll
         for (int u = 0; u < B; ++u) {
-          const int j = j0 + u * NW;
-          if (j >= D) break;
+          if (j0 + u * NW >= D) break;
 #pragma unroll
           for (int c = 0; c < KC; ++c) {
             const int kb = kb0 + c;
             if (kb >= KB2) break;
-            const int sak = sa[u] >> (8 * (kb & 3));
 #pragma unroll
-            for (int cg = 0; cg < NCG; ++cg)
-              tmp[u][cg] = mfma_fp4_fp8<0, 0>(a[u][c], bq[u][c][cg], tmp[u][cg], sak, sbq[u][c][cg]);
+            for (int d = 0; d < DT; ++d) {
+              const int sak = sa[u][d] >> (8 * (kb & 3));
+#pragma unroll
+              for (int cg = 0; cg < NCG; ++cg)
+                tmp[u][d][cg] = mfma_fp4_fp8<0, 0>(a[u][d][c], bq[u][c][cg], tmp[u][d][cg], sak, sbq[u][c][cg]);
+            }
           }
         }
       }
@@ -638,23 +656,25 @@ MK2_DEV void moe_down(const MoeDev& p, int nt, float* red, int* act_ids) {
         const int j = j0 + u * NW;
         if (j >= D) break;
 #pragma unroll
-        for (int cg = 0; cg < NCG; ++cg) acc[cg] += tmp[u][cg] * ldp_f32(p.rw + j * 32 + cg * 16 + c16);
+        for (int cg = 0; cg < NCG; ++cg) {
+          const float w = ldp_f32(p.rw + j * 32 + cg * 16 + c16);
+#pragma unroll
+          for (int d = 0; d < DT; ++d) acc[d][cg] += tmp[u][d][cg] * w;
+        }
       }
     }
-  } else {
+  } else if constexpr (DT == 1) {
     constexpr int KMAX = 8;  // FP8 experts: inter <= 1024
     for (int j = wave; j < D; j += NW) {
       const int e = act_ids[j];
-      const uint8_t* wb = p.w2 + ((size_t)e * HT + nt) * KB2 * 2048;
-      const float* sbase = (const float*)p.s2 + (size_t)e * (p.H / 128) * KB2 + (nt * 16 / 128) * KB2;
+      const uint8_t* wb = p.w2 + ((size_t)e * HT + t0) * KB2 * 2048;
+      const float* sbase = (const float*)p.s2 + (size_t)e * (p.H / 128) * KB2 + (t0 * 16 / 128) * KB2;
       uint4 raw[KMAX][2];
 #pragma unroll
       for (int kb = 0; kb < KMAX; ++kb) {
-        if (kb < KB2) {
-          const uint4* tl = (const uint4*)(wb + (size_t)kb * 2048 + lane * 32);
-          raw[kb][0] = tl[0];
-          raw[kb][1] = tl[1];
-        }
+        const uint4* tl = (const uint4*)(wb + (size_t)min(kb, KB2 - 1) * 2048 + lane * 32);
+        raw[kb][0] = tl[0];
+        raw[kb][1] = tl[1];
       }
 #pragma unroll
       for (int kb = 0; kb < KMAX; ++kb) {
@@ -669,25 +689,35 @@ MK2_DEV void moe_down(const MoeDev& p, int nt, float* red, int* act_ids) {
         for (int cg = 0; cg < NCG; ++cg) {
           bf16x8 b[4];
           load_b_bf16(p.mid_b + (size_t)j * p.M * p.I, cg * 16 + c16, p.M, p.I, kb * 128 + 32 * g, b);
-          acc[cg] += mfma4_bf16(a, b, f32x4{0.f, 0.f, 0.f, 0.f}) * (sc * ldp_f32(p.rw + j * 32 + cg * 16 + c16));
+          acc[0][cg] += mfma4_bf16(a, b, f32x4{0.f, 0.f, 0.f, 0.f}) * (sc * ldp_f32(p.rw + j * 32 + cg * 16 + c16));
         }
       }
     }
   }
 #pragma unroll
-  for (int cg = 0; cg < NCG; ++cg) *(f32x4*)(red + ((wave * NCG + cg) * 64 + lane) * 4) = acc[cg];
+  for (int d = 0; d < DT; ++d)
+#pragma unroll
+    for (int cg = 0; cg < NCG; ++cg) *(f32x4*)(red + (((wave * DT + d) * NCG + cg) * 64 + lane) * 4) = acc[d][cg];
   __syncthreads();
-  for (int idx = threadIdx.x; idx < 16 * p.M; idx += NT) {
-    const int n16 = idx & 15, s = idx >> 4, cg = s >> 4, s16 = s & 15;
+  for (int idx = threadIdx.x; idx < 16 * DT * p.M; idx += NT) {
+    const int n = idx % (16 * DT), s = idx / (16 * DT);
+    const int d = n >> 4, n16 = n & 15, cg = s >> 4, s16 = s & 15;
     const int l = (n16 >> 2) * 16 + s16, i = n16 & 3;
     float y = 0.f;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) y += red[((w * NCG + cg) * 64 + l) * 4 + i];
-    const size_t o = (size_t)s * p.H + nt * 16 + n16;
+    for (int w = 0; w < NW; ++w) y += red[(((w * DT + d) * NCG + cg) * 64 + l) * 4 + i];
+    const size_t o = (size_t)s * p.H + (t0 + d) * 16 + n16;
     if (p.residual) y += bf16_to_f32((bf16_t)ldp_u16(p.x + o));
     p.out[o] = f32_to_bf16(y);
   }
   __syncthreads();
+}
+
+// task nt of H / (16 * p.DT)
+template <int NT, int NCG>
+MK2_DEV void moe_down(const MoeDev& p, int nt, float* red, int* act_ids) {
+  if (NCG == 1 && p.DT == 2) down_rows<NT, NCG, (NCG == 1 ? 2 : 1)>(p, nt, red, act_ids);
+  else down_rows<NT, NCG, 1>(p, nt, red, act_ids);
 }
 
 }  // namespace mk2

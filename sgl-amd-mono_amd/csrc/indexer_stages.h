@@ -486,9 +486,10 @@ MK2_DEV void idx_clear_hist(const IdxDev& p, int r) {
 
 // ---------------------------------------------------------------- stage: slice
 // Task (row r, chunk): the chunk's keys whose top 12 bits are >= b1, in position
-// order, to cand[r][chunk * IDX_CHUNK ..]; their count to ccount[r][chunk].
+// order, to cand[r][chunk * IDX_CHUNK ..]; their count to ccount[r][chunk].  Returns
+// whether S.res[0..1] now hold the row's threshold bin and the count above it.
 template <int NT>
-MK2_DEV void idx_slice(const IdxDev& p, int r, int chunk, TopkLds& S) {
+MK2_DEV bool idx_slice(const IdxDev& p, int r, int chunk, TopkLds& S) {
   constexpr int PER = IDX_CHUNK / NT;  // consecutive positions a thread
   static_assert(PER % 4 == 0, "a thread reads whole 16-byte groups of scores");
   const int tid = threadIdx.x;
@@ -497,7 +498,7 @@ MK2_DEV void idx_slice(const IdxDev& p, int r, int chunk, TopkLds& S) {
   int* cnt_out = p.ccount + (size_t)r * p.nchk + chunk;
   if (n <= k || k_begin >= n) {
     if (tid == 0) st_dev_i32(cnt_out, 0);
-    return;
+    return false;
   }
   // the chunk's scores first: their loads overlap the threshold search
   const float* srow = p.scores + (size_t)r * p.max_ctx;
@@ -509,7 +510,7 @@ MK2_DEV void idx_slice(const IdxDev& p, int r, int chunk, TopkLds& S) {
   if (tid < 64) {
     int above;
     const int b1 = wave_threshold(p, r, k, &above);
-    if (tid == 0) S.res[0] = b1;
+    if (tid == 0) { S.res[0] = b1; S.res[1] = above; }
   }
   __syncthreads();
   const uint32_t b1 = (uint32_t)S.res[0];
@@ -535,6 +536,7 @@ MK2_DEV void idx_slice(const IdxDev& p, int r, int chunk, TopkLds& S) {
     }
   }
   if (tid == 0) st_dev_i32(cnt_out, tot.a);
+  return true;
 }
 
 // The select when more than TOPK_CAP candidates remain (a row whose keys crowd into
@@ -748,9 +750,11 @@ MK2_DEV void cand_select(TopkLds& S, int m, uint32_t b1, int above1, int k, int*
 
 // --------------------------------------------------------------- stage: select
 // Task (row r): the exact top-k of the row from its slices' candidates; then the
-// row's histograms are cleared for the next launch.
+// row's histograms are cleared for the next launch.  `known`: S.res[0..1] already
+// hold the row's threshold bin and the count above it (the workgroup ran one of the
+// row's slices just before).
 template <int NT>
-MK2_DEV void idx_select(const IdxDev& p, int r, TopkLds& S) {
+MK2_DEV void idx_select(const IdxDev& p, int r, TopkLds& S, bool known = false) {
   constexpr int CPT = TOPK_CAP / NT;  // candidates a thread
   constexpr int TPC = NT / (TOPK_MAXN / IDX_CHUNK);  // gather threads a chunk
   const int tid = threadIdx.x;
@@ -764,7 +768,7 @@ MK2_DEV void idx_select(const IdxDev& p, int r, TopkLds& S) {
   }
   const int nchk = p.nchk;
   // the threshold bin (wave 0) and the chunks' candidate offsets (position order)
-  if (tid < 64) {
+  if (!known && tid < 64) {
     int above;
     const int b1 = wave_threshold(p, r, k, &above);
     if (tid == 0) { S.res[0] = b1; S.res[1] = above; }

@@ -189,11 +189,12 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
   K2_TASKS(t, R * nchk) {
     const int r = t / nchk;
     k2_wait(p, seen, SY_SCORE + r, nchk, t < G ? 3 * st + 1 : -1);
-    idx_slice<K2_NT>(p.idx, r, t % nchk, S.topk);
+    const bool known = idx_slice<K2_NT>(p.idx, r, t % nchk, S.topk);
     if (k2_signal_last1(p, SY_SLICE + r, nchk, &last_flag)) {
       k2_stamp(p, 3 * (st + 1));
       k2_stamp(p, 3 * (st + 1) + 1);
-      idx_select<K2_NT>(p.idx, r, S.topk);
+      // this workgroup's own slice of row r may have left the threshold in LDS
+      idx_select<K2_NT>(p.idx, r, S.topk, known);
       k2_signal(p, SY_TOPK + r);
       k2_stamp(p, 3 * (st + 1) + 2);
     }
@@ -289,8 +290,9 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
   // ---- down + route weighting + residual, per 16 hidden rows
   k2_stamp(p, 3 * st);
   K2_TASKS(t, p.moe.H / (16 * p.moe.DT)) {
-    k2_wait(p, seen, SY_UP, up_total, t < G ? 3 * st + 1 : -1, K2_LANES);
-    moe_down<K2_NT, NCG>(p.moe, t, S.down.red, S.down.act);
+    k2_wait(p, seen, SY_ROUTE, 1);  // the routing: known long before the mid rows
+    moe_down<K2_NT, NCG>(p.moe, t, S.down.red, S.down.act,
+                         [&] { k2_wait(p, seen, SY_UP, up_total, t < G ? 3 * st + 1 : -1, K2_LANES); });
   }
   k2_stamp(p, 3 * st + 2);
 #undef K2_TASKS

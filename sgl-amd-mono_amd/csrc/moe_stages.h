@@ -566,8 +566,8 @@ MK2_DEV void moe_upgate(const MoeDev& p, int t, float* red, float* midf) {
 // Waves take every NW-th slot, a batch of slots' weight tiles (and their mid rows,
 // shared by the DT tiles) in flight at once.  act_ids: LDS >= E ints; red: NW * DT *
 // NCG * 256 floats.
-template <int NT, int NCG, int DT>
-MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids) {
+template <int NT, int NCG, int DT, typename Wait>
+MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, Wait wait) {
   constexpr int NW = NT / 64;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, c16 = lane & 15;
   const int D = min(ldp_i32(p.act), p.Dmax);
@@ -575,33 +575,80 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids) {
   __syncthreads();
   const int HT = p.H / 16;
   const int t0 = nt * DT;  // first 16-row tile
+  const int KB2s = p.n_shared ? p.SI / 128 : 0;
+  const int KB2 = p.I / 128;
+  constexpr int B = DT == 2 ? 2 : (NCG == 1 ? 4 : 2);  // MXFP4 slots in flight a wave
+  constexpr int KC = 2;                                // k-blocks of a slot a pass
+  const int G2 = (KB2 + 3) / 4;
+  // weights only (static, or known since routing): the shared expert's first k-block
+  // of this wave and its first batch of routed slots, loaded before `wait` (the mid
+  // activations' dependency)
+  uint4 shraw[DT][2];
+  float shsc[DT];
+  {
+    const int kb = min(wave, max(KB2s, 1) - 1);
+#pragma unroll
+    for (int d = 0; d < DT; ++d) {
+      if (KB2s) {
+        const uint4* tl = (const uint4*)(p.ws2 + ((size_t)(t0 + d) * KB2s + kb) * 2048 + lane * 32);
+        shraw[d][0] = tl[0];
+        shraw[d][1] = tl[1];
+        shsc[d] = p.ss2[((t0 + d) * 16 / 128) * KB2s + kb];
+      }
+    }
+  }
+  const bool mx = p.fmt == MK2_FMT_MXFP4;
+  i32x8 apf[B][DT][KC];
+  int sapf[B][DT];
+  if (mx && D > 0) {
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int e = act_ids[min(wave + u * NW, D - 1)];
+#pragma unroll
+      for (int c = 0; c < KC; ++c)
+#pragma unroll
+        for (int d = 0; d < DT; ++d)
+          apf[u][d][c] = load_a_fp4(p.w2 + (((size_t)e * HT + t0 + d) * KB2 + min(c, KB2 - 1)) * 1024, lane);
+#pragma unroll
+      for (int d = 0; d < DT; ++d)
+        sapf[u][d] = (int)*(const uint32_t*)(p.s2 + ((((size_t)e * HT + t0 + d) * G2) * 64 + lane) * 4);
+    }
+  }
+  wait();
   f32x4 acc[DT][NCG];
 #pragma unroll
   for (int d = 0; d < DT; ++d)
 #pragma unroll
     for (int cg = 0; cg < NCG; ++cg) acc[d][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
   // the shared expert (FP8, bf16 mid): its k-blocks spread over the waves
-  if (p.n_shared) {
-    const int KB2 = p.SI / 128;
-    for (int kb = wave; kb < KB2; kb += NW) {
-      bf16x8 b[NCG][4];
+  for (int kb = wave; kb < KB2s; kb += NW) {
+    bf16x8 b[NCG][4];
 #pragma unroll
-      for (int cg = 0; cg < NCG; ++cg) load_b_bf16(p.mid_sh, cg * 16 + c16, p.M, p.SI, kb * 128 + 32 * g, b[cg]);
+    for (int cg = 0; cg < NCG; ++cg) load_b_bf16(p.mid_sh, cg * 16 + c16, p.M, p.SI, kb * 128 + 32 * g, b[cg]);
 #pragma unroll
-      for (int d = 0; d < DT; ++d) {
-        bf16x8 a[4];
-        load_a_fp8(p.ws2 + ((size_t)(t0 + d) * KB2 + kb) * 2048, lane, a);
-        const float sc = p.ss2[((t0 + d) * 16 / 128) * KB2 + kb];
-#pragma unroll
-        for (int cg = 0; cg < NCG; ++cg) acc[d][cg] += mfma4_bf16(a, b[cg], f32x4{0.f, 0.f, 0.f, 0.f}) * sc;
+    for (int d = 0; d < DT; ++d) {
+      uint4 r0, r1;
+      float sc;
+      if (kb == wave) {
+        r0 = shraw[d][0];
+        r1 = shraw[d][1];
+        sc = shsc[d];
+      } else {
+        const uint4* tl = (const uint4*)(p.ws2 + ((size_t)(t0 + d) * KB2s + kb) * 2048 + lane * 32);
+        r0 = tl[0];
+        r1 = tl[1];
+        sc = p.ss2[((t0 + d) * 16 / 128) * KB2s + kb];
       }
+      bf16x8 a[4];
+      a[0] = e4m3x8_to_bf16(r0.x, r0.y);
+      a[1] = e4m3x8_to_bf16(r0.z, r0.w);
+      a[2] = e4m3x8_to_bf16(r1.x, r1.y);
+      a[3] = e4m3x8_to_bf16(r1.z, r1.w);
+#pragma unroll
+      for (int cg = 0; cg < NCG; ++cg) acc[d][cg] += mfma4_bf16(a, b[cg], f32x4{0.f, 0.f, 0.f, 0.f}) * sc;
     }
   }
-  const int KB2 = p.I / 128;
-  if (p.fmt == MK2_FMT_MXFP4) {
-    constexpr int B = DT == 2 ? 2 : (NCG == 1 ? 4 : 2);  // slots in flight a wave
-    constexpr int KC = 2;                                // k-blocks of a slot a pass
-    const int G2 = (KB2 + 3) / 4;
+  if (mx) {
     for (int j0 = wave; j0 < D; j0 += NW * B) {
       f32x4 tmp[B][DT][NCG];
 #pragma unroll
@@ -611,6 +658,7 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids) {
 #pragma unroll
           for (int cg = 0; cg < NCG; ++cg) tmp[u][d][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
       for (int kb0 = 0; kb0 < KB2; kb0 += KC) {
+        const bool pre = j0 == wave && kb0 == 0;  // the batch loaded before the wait
         i32x8 a[B][DT][KC], bq[B][KC][NCG];
         int sa[B][DT], sbq[B][KC][NCG];
 #pragma unroll
@@ -622,7 +670,8 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids) {
             const int kb = min(kb0 + c, KB2 - 1);
 #pragma unroll
             for (int d = 0; d < DT; ++d)
-              a[u][d][c] = load_a_fp4(p.w2 + (((size_t)e * HT + t0 + d) * KB2 + kb) * 1024, lane);
+              a[u][d][c] = pre ? apf[u][d][c]
+                               : load_a_fp4(p.w2 + (((size_t)e * HT + t0 + d) * KB2 + kb) * 1024, lane);
 #pragma unroll
             for (int cg = 0; cg < NCG; ++cg) {
               const int row = cg * 16 + c16;
@@ -632,7 +681,8 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids) {
           }
 #pragma unroll
           for (int d = 0; d < DT; ++d)
-            sa[u][d] = (int)*(const uint32_t*)(p.s2 + ((((size_t)e * HT + t0 + d) * G2 + kb0 / 4) * 64 + lane) * 4);
+            sa[u][d] = pre ? sapf[u][d]
+                           : (int)*(const uint32_t*)(p.s2 + ((((size_t)e * HT + t0 + d) * G2 + kb0 / 4) * 64 + lane) * 4);
         }
 #pragma unroll
         for (int u = 0; u < B; ++u) {
@@ -713,11 +763,13 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids) {
   __syncthreads();
 }
 
-// task nt of H / (16 * p.DT)
-template <int NT, int NCG>
-MK2_DEV void moe_down(const MoeDev& p, int nt, float* red, int* act_ids) {
-  if (NCG == 1 && p.DT == 2) down_rows<NT, NCG, (NCG == 1 ? 2 : 1)>(p, nt, red, act_ids);
-  else down_rows<NT, NCG, 1>(p, nt, red, act_ids);
+// task nt of H / (16 * p.DT).  Needs the routing (act, rw) on entry; `wait` is the
+// mid activations' dependency, run once the task's static and routed weight loads
+// are in flight.
+template <int NT, int NCG, typename Wait = NoWait>
+MK2_DEV void moe_down(const MoeDev& p, int nt, float* red, int* act_ids, Wait wait = Wait()) {
+  if (NCG == 1 && p.DT == 2) down_rows<NT, NCG, (NCG == 1 ? 2 : 1)>(p, nt, red, act_ids, wait);
+  else down_rows<NT, NCG, 1>(p, nt, red, act_ids, wait);
 }
 
 }  // namespace mk2

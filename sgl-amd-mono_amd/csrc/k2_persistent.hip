@@ -89,13 +89,13 @@ union K2Lds {
 
 MK2_DEV int* k2_ctr(const K2Dev& p, int line) { return p.sync + line * SY_LINE; }
 
-// publish a finished task on counter `line` (sub-counter t mod lanes): every thread's
+// publish n finished tasks on counter `line` (sub-counter t mod lanes): every thread's
 // stores drained, then one increment
-MK2_DEV void k2_signal(const K2Dev& p, int line, int t = 0, int lanes = 1) {
+MK2_DEV void k2_signal(const K2Dev& p, int line, int t = 0, int lanes = 1, int n = 1) {
   drain_memory();
   __syncthreads();
   if (threadIdx.x == 0)
-    __hip_atomic_fetch_add(k2_ctr(p, line + t % lanes), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_fetch_add(k2_ctr(p, line + t % lanes), n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // publish task t of n on a K2_LANES counter and tell whether it completed the set: the
@@ -234,13 +234,15 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
   }
   K2_NEXT(MLA_HEADS * vtn);
   k2_stamp(p, 3 * st++ + 2);
-  // ---- W_o + residual, per 16 hidden rows
+  // ---- W_o + residual, per 16 hidden rows: tasks t and t + G together (their weights
+  // all in flight before the wait)
   k2_stamp(p, 3 * st);
   const int ht = p.mla.hidden / 16;
-  K2_TASKS(t, ht) {
-    mla_oproj<K2_NT, NCG>(p.mla, t, S.red,
-                          [&] { k2_wait(p, seen, SY_UV, MLA_HEADS * vtn, t < G ? 3 * st + 1 : -1, K2_LANES); });
-    k2_signal(p, SY_OPROJ, t, K2_LANES);
+  for (int t = (b - base % G + G) % G; t < ht; t += 2 * G) {
+    const int t1 = t + G < ht ? t + G : -1;
+    mla_oproj<K2_NT, NCG, 2>(p.mla, t, t1, S.up.red,
+                             [&] { k2_wait(p, seen, SY_UV, MLA_HEADS * vtn, t < G ? 3 * st + 1 : -1, K2_LANES); });
+    k2_signal(p, SY_OPROJ, t, K2_LANES, t1 >= 0 ? 2 : 1);
   }
   K2_NEXT(ht);
   k2_stamp(p, 3 * st++ + 2);

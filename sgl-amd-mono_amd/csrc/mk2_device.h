@@ -118,26 +118,48 @@ MK2_DEV f32x4 mfma_fp4_fp8(i32x8 a, i32x8 b, f32x4 c, int sa, int sb) {
 }
 
 // ----------------------------------------------------------------- reductions
-MK2_DEV float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+
+// DPP lane moves within a 16-lane row (no LDS traffic): quad_perm [1,0,3,2] and
+// [2,3,0,1], row_half_mirror (lane i <-> 7-i of each half row), row_mirror (i <-> 15-i)
+template <int CTRL>
+MK2_DEV float dpp_f32(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
-MK2_DEV float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
-// reduce over the 16 lanes of a lane row (lanes with equal l / 16)
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
+// reduce over the 16 lanes of a lane row (lanes with equal l / 16); every lane of the
+// row gets the result: quads first, then half rows, then the row
 MK2_DEV float row16_max(float v) {
-#pragma unroll
-  for (int o = 8; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmaxf(v, dpp_f32<DPP_XOR1>(v));
+  v = fmaxf(v, dpp_f32<DPP_XOR2>(v));
+  v = fmaxf(v, dpp_f32<DPP_HALF_MIRROR>(v));
+  return fmaxf(v, dpp_f32<DPP_MIRROR>(v));
 }
 MK2_DEV float row16_sum(float v) {
-#pragma unroll
-  for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v += dpp_f32<DPP_XOR1>(v);
+  v += dpp_f32<DPP_XOR2>(v);
+  v += dpp_f32<DPP_HALF_MIRROR>(v);
+  return v + dpp_f32<DPP_MIRROR>(v);
+}
+// whole-wave reductions, the result in every lane: row totals by DPP, then lane 15's
+// row total into rows 1 and 3 (row_bcast:15) and lane 31's into rows 2 and 3
+// (row_bcast:31), so that row 3 holds the total; read from lane 63
+template <int CTRL, int ROWS>
+MK2_DEV float dpp_rows_f32(float old, float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old), __builtin_bit_cast(int, v),
+                                                               CTRL, ROWS, 0xF, false));
+}
+constexpr int DPP_BCAST15 = 0x142, DPP_BCAST31 = 0x143;
+MK2_DEV float wave_sum(float v) {
+  v = row16_sum(v);
+  v += dpp_rows_f32<DPP_BCAST15, 0xA>(0.f, v);
+  v += dpp_rows_f32<DPP_BCAST31, 0xC>(0.f, v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+MK2_DEV float wave_max(float v) {
+  v = row16_max(v);
+  v = fmaxf(v, dpp_rows_f32<DPP_BCAST15, 0xA>(-INFINITY, v));
+  v = fmaxf(v, dpp_rows_f32<DPP_BCAST31, 0xC>(-INFINITY, v));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
 // order-preserving u32 of f32 bits: larger keys rank first

@@ -21,7 +21,7 @@ __global__ __launch_bounds__(MLA_NT) void k_mla_uv(MlaDev p) {
 template <int NCG>
 __global__ __launch_bounds__(MLA_NT) void k_mla_oproj(MlaDev p) {
   __shared__ float red[4 * NCG * 64 * 4];
-  mla_oproj<MLA_NT, NCG>(p, blockIdx.x, red);
+  mla_oproj<MLA_NT, NCG>(p, blockIdx.x, -1, red);
 }
 
 int mla_check_shape(const mk2_mla_shape* s) {

@@ -21,6 +21,11 @@ constexpr int MLA_HEADS = 16;
 constexpr int MLA_SPLIT = 64;     // keys a split task
 constexpr int MLA_KROW = 584;     // LDS row stride of the gathered rows (bytes)
 constexpr int MLA_VROW = 72;      // LDS row stride of the transposed latent (bytes)
+// In the transposed latent, dim d's 4-key word w sits at word w ^ mla_vswz(d): the
+// gather writes one word of 16 consecutive dims a lane, and without the swizzle all
+// lanes of a store would hit one bank (16 rows of 18 words is 0 mod 32).  The swizzle
+// is even, so the two words of an aligned 8-key read stay an aligned pair.
+MK2_DEV int mla_vswz(int d) { return 2 * ((d >> 4) & 7); }
 constexpr int MLA_NT = 256;
 
 struct MlaDev {
@@ -71,20 +76,20 @@ MK2_DEV void mla_split(const MlaDev& p, int r, int s, MlaSplitLds& L) {
 #pragma unroll
     for (int ks = 0; ks < 18; ++ks) qa[ks] = __builtin_bit_cast(bf16x8, *(const uint4*)(qr + 32 * ks));
   }
-  // resolve the 64 positions to cache rows (one dependent round), with their scales
+  // resolve the 64 positions to cache rows (one dependent round); the rows' scales
+  // are loaded with the rows below
   if (tid < MLA_SPLIT) {
     const int pos = ldp_i32(selr + tid);
     int row = -1;
-    float ksc = 0.f;
-    if (pos >= 0 && pos < p.stride * 64) {
-      row = ptr[pos >> 6] * 64 + (pos & 63);
-      ksc = p.kv_scale[row];
-    }
+    if (pos >= 0 && pos < p.stride * 64) row = ptr[pos >> 6] * 64 + (pos & 63);
     L.row[tid] = row;
-    L.kscale[tid] = ksc;
-    L.sc[tid] = ksc * p.sm_scale;
   }
   __syncthreads();
+  float ksc = 0.f;
+  if (tid < MLA_SPLIT) {
+    const int row = L.row[tid];
+    ksc = row >= 0 ? p.kv_scale[row] : 0.f;
+  }
   // gather: job = (4-key group kg, 16-byte dim chunk dc), 16 x 36 jobs; every load of
   // a thread is issued before the first LDS store
   constexpr int JOBS = 16 * 36, JPT = (JOBS + NT - 1) / NT;
@@ -98,6 +103,10 @@ MK2_DEV void mla_split(const MlaDev& p, int r, int s, MlaSplitLds& L) {
       const int row = job < JOBS ? L.row[kg * 4 + j] : -1;
       v[it][j] = row >= 0 ? *(const uint4*)(p.kv + (size_t)row * MLA_D + dc * 16) : make_uint4(0, 0, 0, 0);
     }
+  }
+  if (tid < MLA_SPLIT) {
+    L.kscale[tid] = ksc;
+    L.sc[tid] = ksc * p.sm_scale;
   }
 #pragma unroll
   for (int it = 0; it < JPT; ++it) {
@@ -121,10 +130,11 @@ MK2_DEV void mla_split(const MlaDev& p, int r, int s, MlaSplitLds& L) {
         const uint32_t lo23 = __builtin_amdgcn_perm(w3, w2, 0x05010400u);
         const uint32_t hi23 = __builtin_amdgcn_perm(w3, w2, 0x07030602u);
         const int d = dc * 16 + q * 4;
-        *(uint32_t*)(L.vt + (d + 0) * MLA_VROW + kg * 4) = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
-        *(uint32_t*)(L.vt + (d + 1) * MLA_VROW + kg * 4) = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);
-        *(uint32_t*)(L.vt + (d + 2) * MLA_VROW + kg * 4) = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
-        *(uint32_t*)(L.vt + (d + 3) * MLA_VROW + kg * 4) = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
+        const int w = (kg ^ mla_vswz(d)) * 4;  // the four dims share d >> 4
+        *(uint32_t*)(L.vt + (d + 0) * MLA_VROW + w) = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
+        *(uint32_t*)(L.vt + (d + 1) * MLA_VROW + w) = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);
+        *(uint32_t*)(L.vt + (d + 2) * MLA_VROW + w) = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
+        *(uint32_t*)(L.vt + (d + 3) * MLA_VROW + w) = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
       }
     }
   }
@@ -134,13 +144,18 @@ MK2_DEV void mla_split(const MlaDev& p, int r, int s, MlaSplitLds& L) {
   const bool valid = L.row[key] >= 0;
   float sv[4], m[4];
   if (qk_wave) {
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    // every LDS read first, then two interleaved accumulator chains
     const uint8_t* krow = L.k + key * MLA_KROW + 8 * g;
+    uint2 kw[18];
 #pragma unroll
-    for (int ks = 0; ks < 18; ++ks) {
-      const uint2 kw = *(const uint2*)(krow + 32 * ks);
-      acc = mfma_bf16(qa[ks], e4m3x8_to_bf16(kw.x, kw.y), acc);
+    for (int ks = 0; ks < 18; ++ks) kw[ks] = *(const uint2*)(krow + 32 * ks);
+    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 18; ks += 2) {
+      acc0 = mfma_bf16(qa[ks], e4m3x8_to_bf16(kw[ks].x, kw[ks].y), acc0);
+      acc1 = mfma_bf16(qa[ks + 1], e4m3x8_to_bf16(kw[ks + 1].x, kw[ks + 1].y), acc1);
     }
+    const f32x4 acc = acc0 + acc1;
 #pragma unroll
     for (int i = 0; i < 4; ++i) sv[i] = valid ? acc[i] * L.sc[key] : -INFINITY;
     // split-local softmax per head (heads 4g + i)
@@ -190,7 +205,8 @@ MK2_DEV void mla_split(const MlaDev& p, int r, int s, MlaSplitLds& L) {
     f32x4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      const uint2 vw = *(const uint2*)(L.vt + (d0 + c16) * MLA_VROW + 32 * ks + 8 * g);
+      const int w = (8 * ks + 2 * g) ^ mla_vswz(d0);  // d0 + c16 shares d0 >> 4
+      const uint2 vw = *(const uint2*)(L.vt + (d0 + c16) * MLA_VROW + 4 * w);
       o = mfma_bf16(pa[ks], e4m3x8_to_bf16(vw.x, vw.y), o);
     }
 #pragma unroll
@@ -302,27 +318,35 @@ MK2_DEV void mla_uv(const MlaDev& p, int h, int vt, float* red, Wait wait = Wait
 }
 
 // ---------------------------------------------------------------- stage: W_o
-// Task (16 hidden rows nt): each wave's first PF k-blocks of W_o are loaded before
-// `wait` (the attention rows' dependency); the rest after.
-template <int NT, int NCG, typename Wait = NoWait>
-MK2_DEV void mla_oproj(const MlaDev& p, int nt, float* red, Wait wait = Wait()) {
+// Tasks (16 hidden rows nt0) and, with NTL = 2, (16 hidden rows nt1; -1: none): both
+// tiles' first PF k-blocks a wave are loaded before `wait` (the attention rows'
+// dependency), the rest after; the attention rows are loaded once for both.  Without
+// a second tile the first is computed twice and stored once.
+template <int NT, int NCG, int NTL = 1, typename Wait = NoWait>
+MK2_DEV void mla_oproj(const MlaDev& p, int nt0, int nt1, float* red, Wait wait = Wait()) {
   constexpr int NW = NT / 64, PF = 2;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, c16 = lane & 15;
   const int K = MLA_HEADS * p.v_dim, KB = K / 128;
-  const uint8_t* tiles = p.w_o + (size_t)nt * KB * 64 * 64;
-  bf16x8 apf[PF][4];
+  const uint8_t* tiles[NTL];
 #pragma unroll
-  for (int u = 0; u < PF; ++u) {
-    const int kb = wave + u * NW;
-    const uint4* t = (const uint4*)(tiles + ((size_t)min(kb, KB - 1) * 64 + lane) * 64);
+  for (int j = 0; j < NTL; ++j) tiles[j] = p.w_o + (size_t)(j == 0 || nt1 < 0 ? nt0 : nt1) * KB * 64 * 64;
+  bf16x8 apf[NTL][PF][4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) apf[u][q] = __builtin_bit_cast(bf16x8, t[q]);
-  }
+  for (int j = 0; j < NTL; ++j)
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+      const int kb = wave + u * NW;
+      const uint4* t = (const uint4*)(tiles[j] + ((size_t)min(kb, KB - 1) * 64 + lane) * 64);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) apf[j][u][q] = __builtin_bit_cast(bf16x8, t[q]);
+    }
   wait();
-  f32x4 acc[NCG];
+  f32x4 acc[NTL][NCG];
 #pragma unroll
-  for (int cg = 0; cg < NCG; ++cg) acc[cg] = f32x4{0.f, 0.f, 0.f, 0.f};
-  auto step = [&](int kb, const bf16x8* a) {
+  for (int j = 0; j < NTL; ++j)
+#pragma unroll
+    for (int cg = 0; cg < NCG; ++cg) acc[j][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto step = [&](int kb, bf16x8 (*a)[4]) {
 #pragma unroll
     for (int cg = 0; cg < NCG; ++cg) {
       const int row = cg * 16 + c16;
@@ -336,29 +360,45 @@ MK2_DEV void mla_oproj(const MlaDev& p, int nt, float* red, Wait wait = Wait()) 
         for (int q = 0; q < 4; ++q) b[q] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
       }
 #pragma unroll
-      for (int q = 0; q < 4; ++q) acc[cg] = mfma_bf16(a[q], b[q], acc[cg]);
+      for (int j = 0; j < NTL; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[j][cg] = mfma_bf16(a[j][q], b[q], acc[j][cg]);
     }
   };
 #pragma unroll
   for (int u = 0; u < PF; ++u)
-    if (wave + u * NW < KB) step(wave + u * NW, apf[u]);
-  for (int kb = wave + PF * NW; kb < KB; kb += NW) {
-    bf16x8 a[4];
-    const uint4* t = (const uint4*)(tiles + ((size_t)kb * 64 + lane) * 64);
+    if (wave + u * NW < KB) {
+      bf16x8 a[NTL][4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) a[q] = __builtin_bit_cast(bf16x8, t[q]);
+      for (int j = 0; j < NTL; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) a[j][q] = apf[j][u][q];
+      step(wave + u * NW, a);
+    }
+  for (int kb = wave + PF * NW; kb < KB; kb += NW) {
+    bf16x8 a[NTL][4];
+#pragma unroll
+    for (int j = 0; j < NTL; ++j) {
+      const uint4* t = (const uint4*)(tiles[j] + ((size_t)kb * 64 + lane) * 64);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) a[j][q] = __builtin_bit_cast(bf16x8, t[q]);
+    }
     step(kb, a);
   }
 #pragma unroll
-  for (int cg = 0; cg < NCG; ++cg) *(f32x4*)(red + ((wave * NCG + cg) * 64 + lane) * 4) = acc[cg];
+  for (int j = 0; j < NTL; ++j)
+#pragma unroll
+    for (int cg = 0; cg < NCG; ++cg) *(f32x4*)(red + (((j * NW + wave) * NCG + cg) * 64 + lane) * 4) = acc[j][cg];
   __syncthreads();
-  for (int idx = threadIdx.x; idx < 16 * p.rows; idx += NT) {
-    const int n16 = idx & 15, row = idx >> 4, cg = row >> 4, s16 = row & 15;
+  const int ntl = NTL > 1 && nt1 >= 0 ? 2 : 1;
+  for (int idx = threadIdx.x; idx < ntl * 16 * p.rows; idx += NT) {
+    const int j = idx / (16 * p.rows), jdx = idx - j * 16 * p.rows;
+    const int n16 = jdx & 15, row = jdx >> 4, cg = row >> 4, s16 = row & 15;
     const int l = (n16 >> 2) * 16 + s16, i = n16 & 3;
     float v = 0.f;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) v += red[((w * NCG + cg) * 64 + l) * 4 + i];
-    const size_t o = (size_t)row * p.hidden + nt * 16 + n16;
+    for (int w = 0; w < NW; ++w) v += red[(((j * NW + w) * NCG + cg) * 64 + l) * 4 + i];
+    const size_t o = (size_t)row * p.hidden + (j == 0 ? nt0 : nt1) * 16 + n16;
     if (p.h) v += bf16_to_f32(p.h[o]);
     st_dev_u16(p.out + o, f32_to_bf16(v));
   }

@@ -1,7 +1,8 @@
 // The K2 layer as ONE persistent launch: one 512-thread workgroup per CU walks the
 // stage list -- index scores (+ key histograms), top-k slices, top-k select,
-// sparse-MLA splits, merge, W_UV, W_o + residual, RMSNorm + activation quant,
-// router, top-k routing, up/gate + SwiGLU, down + residual -- taking task t of a
+// sparse-MLA splits, merge, W_UV, W_o + residual (+ the RMSNorm's partial sums),
+// router (+ RMSNorm + activation quant of its slice), top-k routing, up/gate +
+// SwiGLU, down + residual -- taking task t of a
 // stage on workgroup (base + t) mod grid, where each stage's base continues from
 // where the previous stage's tasks ended, so that work rotates over the workgroups.
 //
@@ -37,8 +38,7 @@ enum : int {
   SY_TOPK = 64,    // [32] top-k done, per row
   SY_SPLIT = 96,   // [32] attention splits done, per row
   SY_MERGE = 128,  // [16] merged rows, per head
-  SY_PREP = 144,
-  SY_ROUTE,
+  SY_ROUTE = 144,
   SY_ROUTER_LAST,  // router sub-counters completed (the last runs the routing)
   SY_DONE,         // workgroups finished (the last one resets)
   SY_ERR,          // sticky: a wait ran out of its spin limit
@@ -61,7 +61,7 @@ struct K2Dev {
 };
 
 // timeline: per stage s, stamps 3s (enter), 3s+1 (first input ready), 3s+2 (leave)
-constexpr int K2_STAGES = 12, K2_STAMPS = 3 * K2_STAGES + 1;
+constexpr int K2_STAGES = 11, K2_STAMPS = 3 * K2_STAGES + 1;
 
 MK2_DEV void k2_stamp(const K2Dev& p, int i) {
   if (p.timeline && threadIdx.x == 0) p.timeline[(size_t)blockIdx.x * K2_STAMPS + i] = __builtin_amdgcn_s_memrealtime();
@@ -80,10 +80,8 @@ union K2Lds {
     float red[(K2_NT / 64) * 2 * 64 * 4];
     int act[256];
   } down;
-  struct {
-    float logits[32 * 256];
-    int slot[256 + 28 * (K2_NT / 64) + 2 * 32 * 8];
-  } route;
+  RouterLds router;
+  RouteLds route;
   float red[(K2_NT / 64) * 2 * 64 * 4];
 };
 
@@ -246,26 +244,17 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
   }
   K2_NEXT(ht);
   k2_stamp(p, 3 * st++ + 2);
-  // ---- RMSNorm + activation quant, per row
-  k2_stamp(p, 3 * st);
-  K2_TASKS(t, R) {
-    k2_wait(p, seen, SY_OPROJ, ht, t < G ? 3 * st + 1 : -1, K2_LANES);
-    moe_prep<K2_NT>(p.moe, t, S.red);
-    k2_signal(p, SY_PREP);
-  }
-  K2_NEXT(R);
-  k2_stamp(p, 3 * st++ + 2);
-  // ---- router GEMV, per (16 experts, k-chunk)
+  // ---- router GEMV (+ RMSNorm of its slice), per (16 experts, hidden slice)
   k2_stamp(p, 3 * st);
   const int et = p.moe.E / 16, nrt = et * p.moe.KC;
   K2_TASKS(t, nrt) {
-    moe_router<K2_NT, NCG>(p.moe, t % et, t / et, S.red,
-                           [&] { k2_wait(p, seen, SY_PREP, R, t < G ? 3 * st + 1 : -1); });
+    moe_router<K2_NT, NCG>(p.moe, t % et, t / et, S.router,
+                           [&] { k2_wait(p, seen, SY_OPROJ, ht, t < G ? 3 * st + 1 : -1, K2_LANES); });
     // the last router task computes the routing
     if (k2_signal_last(p, SY_ROUTER, SY_ROUTER_LAST, t, nrt, &last_flag)) {
       k2_stamp(p, 3 * (st + 1));
       k2_stamp(p, 3 * (st + 1) + 1);
-      moe_route<K2_NT>(p.moe, S.route.logits, S.route.slot);
+      moe_route<K2_NT>(p.moe, S.route);
       k2_signal(p, SY_ROUTE);
       k2_stamp(p, 3 * (st + 1) + 2);
     }
@@ -274,15 +263,15 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
   k2_stamp(p, 3 * st++ + 2);
   ++st;  // routing: run by the last router task above
   // ---- up/gate + SwiGLU: the shared expert's chunks first (they need only the
-  // normalized rows, so they run while routing is still pending), then the routed
-  // slots
+  // normalized rows, stored by the router tasks, so they run while routing is still
+  // pending), then the routed slots
   k2_stamp(p, 3 * st);
   const int up_r = p.moe.Dmax * (p.moe.I / p.moe.UC);
   const int up_sh = p.moe.n_shared * (p.moe.SI / 32);
   const int up_total = up_r + up_sh;
   K2_TASKS(t, up_total) {
     const bool sh = t < up_sh;
-    if (sh) k2_wait(p, seen, SY_PREP, R, t < G ? 3 * st + 1 : -1);
+    if (sh) k2_wait(p, seen, SY_ROUTER, nrt, t < G ? 3 * st + 1 : -1, K2_LANES);
     else k2_wait(p, seen, SY_ROUTE, 1, t < G ? 3 * st + 1 : -1);
     moe_upgate<K2_NT, NCG>(p.moe, sh ? up_r + t : t - up_sh, S.up.red, S.up.midf);
     k2_signal(p, SY_UP, t, K2_LANES);

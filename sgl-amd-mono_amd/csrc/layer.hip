@@ -75,6 +75,7 @@ int layer_plan(const mk2_layer_args* a, void* ws, LayerPlan* L, size_t* bytes) {
   bf16_t* a_out = a->attn_out ? (bf16_t*)a->attn_out : attn;
   L->mla.out = a_out;
   L->moe.x = a_out;
+  L->mla.ssp = L->moe.norm ? L->moe.ssp : nullptr;  // W_o leaves the RMSNorm's partial sums
   L->moe.out = (bf16_t*)a->out;
   return MK2_OK;
 }

@@ -47,6 +47,7 @@ struct MlaDev {
   bf16_t* o_lat;         // [rows][16][512]
   float* o_lat_f32;      // optional [rows][16][512]
   bf16_t* o;             // [rows][16 * v_dim]
+  float* ssp;            // optional [hidden/16][rows]: sums of squares of out over 16 columns
 };
 
 struct MlaSplitLds {
@@ -321,7 +322,9 @@ MK2_DEV void mla_uv(const MlaDev& p, int h, int vt, float* red, Wait wait = Wait
 // Tasks (16 hidden rows nt0) and, with NTL = 2, (16 hidden rows nt1; -1: none): both
 // tiles' first PF k-blocks a wave are loaded before `wait` (the attention rows'
 // dependency), the rest after; the attention rows are loaded once for both.  Without
-// a second tile the first is computed twice and stored once.
+// a second tile the first is computed twice and stored once.  With `ssp` set, the
+// epilogue also leaves each output row's sum of squares over the tile's 16 columns
+// (the next RMSNorm's partial sums).
 template <int NT, int NCG, int NTL = 1, typename Wait = NoWait>
 MK2_DEV void mla_oproj(const MlaDev& p, int nt0, int nt1, float* red, Wait wait = Wait()) {
   constexpr int NW = NT / 64, PF = 2;
@@ -400,7 +403,13 @@ MK2_DEV void mla_oproj(const MlaDev& p, int nt0, int nt1, float* red, Wait wait 
     for (int w = 0; w < NW; ++w) v += red[(((j * NW + w) * NCG + cg) * 64 + l) * 4 + i];
     const size_t o = (size_t)row * p.hidden + (j == 0 ? nt0 : nt1) * 16 + n16;
     if (p.h) v += bf16_to_f32(p.h[o]);
-    st_dev_u16(p.out + o, f32_to_bf16(v));
+    const bf16_t ob = f32_to_bf16(v);
+    st_dev_u16(p.out + o, ob);
+    if (p.ssp) {  // the 16 columns of (tile, row) are one DPP row: 16 * rows and NT are multiples of 16
+      const float vb = bf16_to_f32(ob);
+      const float ss = row16_sum(vb * vb);
+      if (n16 == 0) st_dev_f32(p.ssp + (size_t)(j == 0 ? nt0 : nt1) * p.rows + row, ss);
+    }
   }
   __syncthreads();
 }

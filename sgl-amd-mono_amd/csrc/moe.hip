@@ -1,30 +1,24 @@
-// Standalone MoE block launch (FP8 or MXFP4 experts): five kernels on one
-// stream -- prep (RMSNorm + MXFP8 quant), router GEMV, route (top-k + distinct
-// experts), up/gate + SwiGLU, down + combine.
+// Standalone MoE block launch (FP8 or MXFP4 experts): up to five kernels on one
+// stream -- the rows' partial sums of squares (with RMSNorm), router GEMV (+ RMSNorm
+// + MXFP8 quant), route (top-k + distinct experts), up/gate + SwiGLU, down + combine.
 #include "mk2_host.h"
 #include "moe_stages.h"
 
 namespace mk2 {
 
 constexpr int MOE_NT = 512;
-constexpr int ROUTE_NT = 512;
 
-__global__ __launch_bounds__(256) void k_moe_prep(MoeDev p) {
-  __shared__ float lds[8];
-  moe_prep<256>(p, blockIdx.x, lds);
-}
+__global__ __launch_bounds__(256) void k_moe_sumsq(MoeDev p) { moe_sumsq<256>(p, blockIdx.x); }
 
 template <int NCG>
-__global__ __launch_bounds__(256) void k_moe_router(MoeDev p) {
-  __shared__ float red[4 * NCG * 64 * 4];
-  moe_router<256, NCG>(p, blockIdx.x, blockIdx.y, red);
+__global__ __launch_bounds__(ROUTER_NT) void k_moe_router(MoeDev p) {
+  __shared__ RouterLds lds;
+  moe_router<ROUTER_NT, NCG>(p, blockIdx.x, blockIdx.y, lds);
 }
 
-__global__ __launch_bounds__(ROUTE_NT) void k_moe_route(MoeDev p) {
-  extern __shared__ float dyn[];
-  float* logits = dyn;
-  int* slot = (int*)(dyn + (p.M * p.E > p.Dmax * 32 ? p.M * p.E : p.Dmax * 32));
-  moe_route<ROUTE_NT>(p, logits, slot);
+__global__ __launch_bounds__(512) void k_moe_route(MoeDev p) {
+  __shared__ RouteLds lds;
+  moe_route<512>(p, lds);
 }
 
 template <int NCG>
@@ -63,10 +57,8 @@ int moe_check_shape(const mk2_moe_shape* s) {
   return MK2_OK;
 }
 
-static int router_chunks(int hidden) {
-  const int kb = hidden / 128;  // multiple of 4
-  return kb / 4;                // 4 k-blocks (one a wave) a task
-}
+// router slices of 1024 columns (512 where hidden is an odd multiple of 512)
+static int router_chunks(int hidden) { return hidden / (hidden % ROUTER_CKMAX == 0 ? ROUTER_CKMAX : 512); }
 
 // carve the MoE scratch; with base == nullptr only sizes are computed
 size_t moe_carve(const mk2_moe_shape* s, void* base, MoeDev* d) {
@@ -79,6 +71,7 @@ size_t moe_carve(const mk2_moe_shape* s, void* base, MoeDev* d) {
   t.Dmax = Dmax;
   t.UC = (s->expert_fmt == MK2_FMT_MXFP4 && M <= 16 && I % 64 == 0) ? 64 : 32;
   t.DT = (s->expert_fmt == MK2_FMT_MXFP4 && M <= 16 && H % 32 == 0) ? 2 : 1;
+  t.ssp = c.take<float>((size_t)(H / 16) * M);
   t.xn = c.take<bf16_t>((size_t)M * H);
   t.xq = c.take<uint8_t>((size_t)M * H);
   t.xs = c.take<uint8_t>((size_t)M * H / 32);
@@ -96,7 +89,7 @@ size_t moe_carve(const mk2_moe_shape* s, void* base, MoeDev* d) {
   }
   t.mid_sh = c.take<bf16_t>((size_t)M * (s->n_shared ? s->shared_inter : 0) + 1);
   if (d) {
-    d->KC = t.KC; d->Dmax = t.Dmax; d->UC = t.UC; d->DT = t.DT; d->xn = t.xn; d->xq = t.xq; d->xs = t.xs;
+    d->KC = t.KC; d->Dmax = t.Dmax; d->UC = t.UC; d->DT = t.DT; d->ssp = t.ssp; d->xn = t.xn; d->xq = t.xq; d->xs = t.xs;
     d->logit_part = t.logit_part; d->logits = t.logits; d->topk_ids = t.topk_ids;
     d->topk_w = t.topk_w; d->act = t.act; d->rw = t.rw; d->mid_q = t.mid_q;
     d->mid_s = t.mid_s; d->mid_b = t.mid_b; d->mid_sh = t.mid_sh;
@@ -128,12 +121,10 @@ int moe_fill(const mk2_moe_args* a, MoeDev* d) {
 
 int moe_enqueue(const MoeDev& d, hipStream_t st) {
   const int ncg = d.M > 16 ? 2 : 1;
-  k_moe_prep<<<d.M, 256, 0, st>>>(d);
-  if (ncg == 1) k_moe_router<1><<<dim3(d.E / 16, d.KC), 256, 0, st>>>(d);
-  else k_moe_router<2><<<dim3(d.E / 16, d.KC), 256, 0, st>>>(d);
-  const int lg = d.M * d.E > d.Dmax * 32 ? d.M * d.E : d.Dmax * 32;
-  const size_t route_lds = (size_t)lg * 4 + (size_t)(d.E + 28 * (ROUTE_NT / 64) + 2 * d.M * d.topk) * 4;
-  k_moe_route<<<1, ROUTE_NT, route_lds, st>>>(d);
+  if (d.norm) k_moe_sumsq<<<d.M, 256, 0, st>>>(d);
+  if (ncg == 1) k_moe_router<1><<<dim3(d.E / 16, d.KC), ROUTER_NT, 0, st>>>(d);
+  else k_moe_router<2><<<dim3(d.E / 16, d.KC), ROUTER_NT, 0, st>>>(d);
+  k_moe_route<<<1, 512, 0, st>>>(d);
   const int up_tasks = d.Dmax * (d.I / d.UC) + d.n_shared * (d.SI / 32);
   if (ncg == 1) k_moe_upgate<1><<<up_tasks, MOE_NT, 0, st>>>(d);
   else k_moe_upgate<2><<<up_tasks, MOE_NT, 0, st>>>(d);

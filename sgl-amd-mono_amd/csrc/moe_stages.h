@@ -1,5 +1,6 @@
-// MoE block stages of the K2 layer: RMSNorm + activation quant, router GEMV,
-// top-k routing, up/gate + SwiGLU (+ mid quant), down + route weighting + residual.
+// MoE block stages of the K2 layer: RMSNorm partial sums, router GEMV (+ RMSNorm +
+// activation quant of its slice), top-k routing, up/gate + SwiGLU (+ mid quant), down
+// + route weighting + residual.
 //
 // Each stage is a device function that runs one task on one workgroup of NT
 // threads; the standalone kernels map task = blockIdx, the persistent layer kernel
@@ -31,6 +32,7 @@ struct MoeDev {
   const float* ss2;
   bf16_t* out;
   // workspace
+  float* ssp;        // [H/16][M] the rows' sums of squares over 16 columns (RMSNorm)
   bf16_t* xn;        // [M][H] normalized rows
   uint8_t* xq;       // [M][H] MXFP8 codes (MXFP4 experts)
   uint8_t* xs;       // [M][H/32] E8M0
@@ -60,75 +62,18 @@ MK2_DEV float block_sum(float v, float* lds) {
   return t;
 }
 
-// ---------------------------------------------------------------- stage: prep
-// Row r: xn = norm ? bf16(x * rstd * gamma) : x, then (MXFP4 experts) MXFP8 codes.
+// ------------------------------------------------------- stage: sums of squares
+// Row r: ssp[t][r] = sum of x^2 over columns 16t .. 16t+15, reduced across one DPP row
+// of 16 lanes.  W_o's epilogue produces the same sums of its output tiles with the
+// same reduction, so either producer gives the same bits.  NT is a multiple of 64 and
+// H of NT, so every pass runs whole 16-lane rows.
 template <int NT>
-MK2_DEV void moe_prep(const MoeDev& p, int r, float* lds) {
-  const int tid = threadIdx.x;
+MK2_DEV void moe_sumsq(const MoeDev& p, int r) {
   const bf16_t* xr = p.x + (size_t)r * p.H;
-  float rstd = 1.f;
-  if (p.norm) {
-    float ss = 0.f;
-    for (int k = tid * 8; k < p.H; k += NT * 8) {
-      uint4 v = ldp_16(xr + k);
-      uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float a = __uint_as_float(w[i] << 16), b = __uint_as_float(w[i] & 0xFFFF0000u);
-        ss += a * a + b * b;
-      }
-    }
-    ss = block_sum<NT>(ss, lds);
-    rstd = 1.0f / sqrtf(ss / (float)p.H + p.eps);
-  }
-  for (int blk = tid; blk < p.H / 32; blk += NT) {
-    float f[32];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      uint4 v = ldp_16(xr + blk * 32 + q * 8);
-      uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        f[q * 8 + 2 * i] = __uint_as_float(w[i] << 16);
-        f[q * 8 + 2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
-      }
-    }
-    if (p.norm) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        uint4 g = *(const uint4*)(p.gamma + blk * 32 + q * 8);
-        uint32_t w[4] = {g.x, g.y, g.z, g.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float g0 = __uint_as_float(w[i] << 16), g1 = __uint_as_float(w[i] & 0xFFFF0000u);
-          f[q * 8 + 2 * i] = bf16_to_f32(f32_to_bf16(f[q * 8 + 2 * i] * rstd * g0));
-          f[q * 8 + 2 * i + 1] = bf16_to_f32(f32_to_bf16(f[q * 8 + 2 * i + 1] * rstd * g1));
-        }
-      }
-    }
-    uint32_t packed[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) packed[i] = pack_bf16x2_exact(f[2 * i], f[2 * i + 1]);
-    uint4* dst = (uint4*)(p.xn + (size_t)r * p.H + blk * 32);
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      st_dev_16(dst + q, make_uint4(packed[4 * q], packed[4 * q + 1], packed[4 * q + 2], packed[4 * q + 3]));
-    if (p.fmt == MK2_FMT_MXFP4) {
-      float amax = 0.f;
-#pragma unroll
-      for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(f[i]));
-      uint32_t code = mxfp8_scale_code(amax);
-      float inv = e8m0_inverse(code);
-      uint32_t qw[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        qw[i] = f32x4_to_e4m3x4(f[4 * i] * inv, f[4 * i + 1] * inv, f[4 * i + 2] * inv,
-                                f[4 * i + 3] * inv);
-      uint4* qd = (uint4*)(p.xq + (size_t)r * p.H + blk * 32);
-      st_dev_16(qd, make_uint4(qw[0], qw[1], qw[2], qw[3]));
-      st_dev_16(qd + 1, make_uint4(qw[4], qw[5], qw[6], qw[7]));
-      st_dev_u8(p.xs + (size_t)r * (p.H / 32) + blk, code);
-    }
+  for (int c = threadIdx.x; c < p.H; c += NT) {
+    const float v = bf16_to_f32(ldp_u16(xr + c));
+    const float ss = row16_sum(v * v);
+    if ((c & 15) == 0) st_dev_f32(p.ssp + (size_t)(c >> 4) * p.M + r, ss);
   }
 }
 
@@ -184,17 +129,95 @@ MK2_DEV f32x4 mfma4_bf16(const bf16x8* a, const bf16x8* b, f32x4 c) {
 }
 
 // ------------------------------------------------------------- stage: router GEMV
-// task (nt, kc): 16 experts x the kc-th slice of hidden -> logit_part[kc].  The
-// router weights are static: a wave's first k-block is loaded before `wait` (the
-// normalized rows' dependency).
+// Task (nt, kc): 16 experts x the kc-th slice of hidden (CK = H / KC columns: 1024, or
+// 512 where H is an odd multiple of 512) -> logit_part[kc].  The task normalizes its
+// slice of the rows itself: rstd from the rows' partial sums of squares (summed in a
+// fixed order, so that every task gets the same bits), then xn = bf16(x * rstd *
+// gamma) into LDS as the MFMA B operand.  The nt == 0 task of each slice also stores
+// the slice for the expert stages (bf16 rows, and MXFP8 codes + E8M0 scales for MXFP4
+// experts).  The router weights and gamma are static: loaded before `wait` (the rows'
+// dependency).  NT = 512.
+constexpr int ROUTER_NT = 512, ROUTER_CKMAX = 1024;
+struct RouterLds {
+  float red[8 * 2 * 256];  // NW * NCG * 256
+  float rstd[32];
+  bf16_t xn[32 * (ROUTER_CKMAX + 8)];
+};
+
 template <int NT, int NCG, typename Wait = NoWait>
-MK2_DEV void moe_router(const MoeDev& p, int nt, int kc, float* red, Wait wait = Wait()) {
-  constexpr int NW = NT / 64;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4;
-  const int KB = p.H / 128, kbs = KB / p.KC;
+MK2_DEV void moe_router(const MoeDev& p, int nt, int kc, RouterLds& L, Wait wait = Wait()) {
+  static_assert(NT == ROUTER_NT, "the router task is laid out for 512 threads");
+  constexpr int NW = NT / 64, RMAX = 32 * ROUTER_CKMAX / 8 / NT;  // row passes a thread at most
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4;
+  const int KB = p.H / 128, kbs = KB / p.KC, CK = kbs * 128, XR = CK + 8, c0 = kc * CK;
+  const int cpr = CK / 8, rstep = NT / cpr;                 // 8-column groups a row, rows a pass
+  const int c8 = 8 * (tid % cpr), r0 = tid / cpr;          // this thread: columns c8.., rows r0 + rstep*i
   bf16x8 a0[4];
   load_a_bf16(p.w_router + ((size_t)nt * KB + kc * kbs + min(wave, kbs - 1)) * 4096, lane, a0);
+  const uint4 gam = p.norm ? *(const uint4*)(p.gamma + c0 + c8) : make_uint4(0, 0, 0, 0);
   wait();
+  uint4 xv[RMAX];
+#pragma unroll
+  for (int i = 0; i < RMAX; ++i)
+    xv[i] = ldp_16(p.x + (size_t)min(r0 + rstep * i, p.M - 1) * p.H + c0 + c8);
+  if (p.norm) {
+    const int nt16 = p.H / 16;
+    for (int r = wave; r < p.M; r += NW) {
+      float ss = 0.f;
+      for (int t0 = 0; t0 < nt16; t0 += 64 * 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = ldp_f32(p.ssp + (size_t)min(t0 + lane + 64 * u, nt16 - 1) * p.M + r);
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (t0 + lane + 64 * u < nt16) ss += v[u];
+      }
+      ss = wave_sum(ss);
+      if (lane == 0) L.rstd[r] = 1.0f / sqrtf(ss / (float)p.H + p.eps);
+    }
+    __syncthreads();
+  }
+  const uint32_t gw[4] = {gam.x, gam.y, gam.z, gam.w};
+#pragma unroll
+  for (int i = 0; i < RMAX; ++i) {
+    const int r = r0 + rstep * i;
+    if (r >= p.M) break;  // uniform in the wave: a wave's lanes share a row
+    const uint32_t w[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+    float f[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      f[2 * j] = __uint_as_float(w[j] << 16);
+      f[2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
+    }
+    if (p.norm) {
+      const float rs = L.rstd[r];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        f[2 * j] = bf16_to_f32(f32_to_bf16(f[2 * j] * rs * __uint_as_float(gw[j] << 16)));
+        f[2 * j + 1] = bf16_to_f32(f32_to_bf16(f[2 * j + 1] * rs * __uint_as_float(gw[j] & 0xFFFF0000u)));
+      }
+    }
+    const uint4 packed = make_uint4(pack_bf16x2_exact(f[0], f[1]), pack_bf16x2_exact(f[2], f[3]),
+                                    pack_bf16x2_exact(f[4], f[5]), pack_bf16x2_exact(f[6], f[7]));
+    *(uint4*)(L.xn + r * XR + c8) = packed;
+    if (nt == 0) {
+      st_dev_16(p.xn + (size_t)r * p.H + c0 + c8, packed);
+      if (p.fmt == MK2_FMT_MXFP4) {  // a 32-column block is 4 lanes (a DPP quad)
+        float amax = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(f[j]));
+        amax = fmaxf(amax, dpp_f32<DPP_XOR1>(amax));
+        amax = fmaxf(amax, dpp_f32<DPP_XOR2>(amax));
+        const uint32_t code = mxfp8_scale_code(amax);
+        const float inv = e8m0_inverse(code);
+        st_dev_8(p.xq + (size_t)r * p.H + c0 + c8,
+                 make_uint2(f32x4_to_e4m3x4(f[0] * inv, f[1] * inv, f[2] * inv, f[3] * inv),
+                            f32x4_to_e4m3x4(f[4] * inv, f[5] * inv, f[6] * inv, f[7] * inv)));
+        if ((lane & 3) == 0) st_dev_u8(p.xs + (size_t)r * (p.H / 32) + (c0 + c8) / 32, code);
+      }
+    }
+  }
+  __syncthreads();
   f32x4 acc[NCG];
 #pragma unroll
   for (int c = 0; c < NCG; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -209,194 +232,181 @@ MK2_DEV void moe_router(const MoeDev& p, int nt, int kc, float* red, Wait wait =
     }
 #pragma unroll
     for (int c = 0; c < NCG; ++c) {
+      const int row = c * 16 + (lane & 15);
       bf16x8 b[4];
-      load_b_bf16(p.xn, c * 16 + (lane & 15), p.M, p.H, kb * 128 + 32 * g, b);
+      if (row < p.M) {
+        const bf16_t* src = L.xn + row * XR + i * 128 + 32 * g;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) b[q] = *(const bf16x8*)(src + 8 * q);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) b[q] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
+      }
       acc[c] = mfma4_bf16(a, b, acc[c]);
     }
   }
 #pragma unroll
   for (int c = 0; c < NCG; ++c)
-    *(f32x4*)(red + ((wave * NCG + c) * 64 + lane) * 4) = acc[c];
+    *(f32x4*)(L.red + ((wave * NCG + c) * 64 + lane) * 4) = acc[c];
   __syncthreads();
+  const int nw_used = NW < kbs ? NW : kbs;
   for (int idx = threadIdx.x; idx < 16 * p.M; idx += NT) {
     const int e16 = idx & 15, row = idx >> 4, c = row >> 4, s16 = row & 15;
     const int l = (e16 >> 2) * 16 + s16, i = e16 & 3;
     float v = 0.f;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) v += red[((w * NCG + c) * 64 + l) * 4 + i];
+    for (int w = 0; w < nw_used; ++w) v += L.red[((w * NCG + c) * 64 + l) * 4 + i];
     st_dev_f32(p.logit_part + ((size_t)kc * p.M + row) * p.E + nt * 16 + e16, v);
   }
   __syncthreads();
 }
 
 // ------------------------------------------------------------- stage: route
-// One workgroup: logits = the k-chunk partials summed in chunk order; one wave a row
-// finds the top-k by (key desc, expert asc) with a bitwise search for the k-th key
-// (ballot counts, no shuffles), ranks the picks, and computes their weights; then
-// the distinct-expert list (ascending) and the dense route-weight table rw.
-// lds_logits: max(M*E, Dmax*32) floats (the logits, then the route-weight table);
-// lds_slot: E + 4*NW ints, 24 a wave of pick scratch, then the picks' ids and weights
-// (2*M*topk).
+// One workgroup of NT = 512; wave w takes rows w, w + NW, ...  Lane l holds experts
+// 4l .. 4l+3 of the row: their logits are the slice partials summed in slice order.
+// The row's top-k by (key desc, expert asc): each lane orders its 4 candidates (a
+// stable bubble pass, so equal keys keep expert order), then each of topk rounds
+// takes the largest head key of the wave (DPP max) and, among equal heads, the lowest
+// lane, whose experts all lie below a higher lane's; the winning lane moves its head
+// on.  Round k's pick lands in lane k, so the picks come out ranked.  Then the
+// distinct-expert list (ascending) from the expert flags, and the dense route-weight
+// table rw [slot][row].
+struct RouteLds {
+  int flag[256];     // expert: 1 if picked, then its slot (-1: none)
+  int ids[32 * 8];   // [M][topk]
+  float w[32 * 8];   // [M][topk]
+  float rw[256 * 32];
+  int tot;
+};
+
+template <int CTRL, int ROWS>
+MK2_DEV uint32_t dpp_u32(uint32_t old, uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)v, CTRL, ROWS, 0xF, false);
+}
+MK2_DEV uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, dpp_u32<DPP_XOR1, 0xF>(0u, v));
+  v = max(v, dpp_u32<DPP_XOR2, 0xF>(0u, v));
+  v = max(v, dpp_u32<DPP_HALF_MIRROR, 0xF>(0u, v));
+  v = max(v, dpp_u32<DPP_MIRROR, 0xF>(0u, v));
+  v = max(v, dpp_u32<DPP_BCAST15, 0xA>(0u, v));
+  v = max(v, dpp_u32<DPP_BCAST31, 0xC>(0u, v));
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
 template <int NT>
-MK2_DEV void moe_route(const MoeDev& p, float* lds_logits, int* lds_slot) {
+MK2_DEV void moe_route(const MoeDev& p, RouteLds& L) {
   constexpr int NW = NT / 64;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int ME = p.M * p.E;
-  const int per = p.E / 64;  // experts a lane holds: e = lane + 64 * i
-  // the lane's router biases, loaded with the partials (every load unconditional and
-  // in bounds, so that none waits for another)
-  float bias[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    bias[i] = p.router == MK2_ROUTER_SIGMOID_BIAS ? p.bias[min(lane + 64 * i, p.E - 1)] : 0.f;
-  for (int idx = tid * 4; idx < ME; idx += NT * 4) {
+  const int el = min(lane, p.E / 4 - 1);  // lanes past E/4 repeat the last group, unused
+  const bool sig = p.router == MK2_ROUTER_SIGMOID_BIAS;
+  const float4 bias = sig ? *(const float4*)(p.bias + 4 * el) : make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int e = tid; e < p.E; e += NT) L.flag[e] = 0;
+  for (int i = tid; i < p.Dmax * 32; i += NT) L.rw[i] = 0.f;
+  __syncthreads();
+  for (int r = wave; r < p.M; r += NW) {
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int kc0 = 0; kc0 < p.KC; kc0 += 8) {
       float4 t[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) t[u] = ldp_f32x4(p.logit_part + (size_t)min(kc0 + u, p.KC - 1) * ME + idx);
+      for (int u = 0; u < 8; ++u)
+        t[u] = ldp_f32x4(p.logit_part + ((size_t)min(kc0 + u, p.KC - 1) * p.M + r) * p.E + 4 * el);
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
+      for (int u = 0; u < 8; ++u)
         if (kc0 + u < p.KC) {
           v.x += t[u].x; v.y += t[u].y; v.z += t[u].z; v.w += t[u].w;
         }
-      }
     }
-    *(float4*)(lds_logits + idx) = v;
-    if (p.logits) *(float4*)(p.logits + idx) = v;
-  }
-  for (int e = tid; e < p.E; e += NT) lds_slot[e] = 0;
-  __syncthreads();
-  int* pick = lds_slot + p.E + 4 * NW + wave * 24;  // [8 keys][8 ids][8 values]
-  int* lds_ids = lds_slot + p.E + 28 * NW;          // [M][topk]
-  float* lds_w = (float*)(lds_ids + p.M * p.topk);  // [M][topk]
-  for (int r = wave; r < p.M; r += NW) {
-    uint32_t key[4] = {0u, 0u, 0u, 0u};
-    float sv[4] = {0.f, 0.f, 0.f, 0.f};
+    const bool live = 4 * lane < p.E;
+    if (p.logits && live) *(float4*)(p.logits + (size_t)r * p.E + 4 * lane) = v;
+    const float lg[4] = {v.x, v.y, v.z, v.w}, bs[4] = {bias.x, bias.y, bias.z, bias.w};
+    float sv[4];
+    uint32_t key[4];
+    int ix[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float lg = lds_logits[r * p.E + min(lane + 64 * i, p.E - 1)];
-      float sg = lg;
-      uint32_t kk;
-      if (p.router == MK2_ROUTER_SIGMOID_BIAS) {
-        sg = 1.0f / (1.0f + expf(-lg));
-        kk = radix_key(sg + bias[i]);
-      } else {
-        kk = radix_key(lg);
-      }
-      sv[i] = i < per ? sg : 0.f;
-      key[i] = i < per ? kk : 0u;
+      sv[i] = sig ? 1.0f / (1.0f + expf(-lg[i])) : lg[i];
+      key[i] = live ? radix_key(sig ? sv[i] + bs[i] : lg[i]) : 0u;  // live keys are > 0
+      ix[i] = i;
     }
-    // the k-th largest key: the largest T with count(key >= T) >= topk
-    uint32_t T = 0u;
-    for (int bit = 31; bit >= 0; --bit) {
-      const uint32_t cand = T | (1u << bit);
-      int cnt = 0;
+    // stable bubble order, keys descending
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        cnt += __popcll(__ballot(key[i] >= cand));  // lanes past E hold key 0 < cand
-      if (cnt >= p.topk) T = cand;
-    }
-    int n_gt = 0;
+    for (int j = 1; j < 4; ++j)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      n_gt += __popcll(__ballot(key[i] > T));
-    const int ties = p.topk - n_gt;  // keys == T taken in expert order
-    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    int tie_before = 0, sel_before = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint64_t tm = __ballot(key[i] == T);
-      const bool is_tie = key[i] == T;
-      const int tie_rank = tie_before + __popcll(tm & below);
-      const bool sel = key[i] > T || (is_tie && tie_rank < ties);
-      const uint64_t sm = __ballot(sel);
-      if (sel) {  // compacted in expert order
-        const int at = sel_before + __popcll(sm & below);
-        pick[at] = (int)key[i];
-        pick[8 + at] = lane + 64 * i;
-        pick[16 + at] = __float_as_int(sv[i]);
+      for (int k = j; k > 0; --k) {
+        const bool sw = key[k] > key[k - 1];
+        const uint32_t tk = key[k];
+        const int ti = ix[k];
+        key[k] = sw ? key[k - 1] : key[k];
+        ix[k] = sw ? ix[k - 1] : ix[k];
+        key[k - 1] = sw ? tk : key[k - 1];
+        ix[k - 1] = sw ? ti : ix[k - 1];
       }
-      tie_before += __popcll(tm);
-      sel_before += __popcll(sm);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    float v = 0.f;
-    int e = 0, rank = 0;
-    if (lane < p.topk) {
-      const uint32_t kj = (uint32_t)pick[lane];
-      e = pick[8 + lane];
-      v = __int_as_float(pick[16 + lane]);
-      for (int j = 0; j < p.topk; ++j) {
-        const uint32_t ko = (uint32_t)pick[j];
-        rank += (ko > kj) || (ko == kj && pick[8 + j] < e);
+    int my_e = 0;
+    float my_v = 0.f;
+    for (int k = 0; k < p.topk; ++k) {
+      const uint32_t top = wave_max_u32(key[0]);
+      const int wl = __ffsll((unsigned long long)__ballot(key[0] == top)) - 1;
+      const int wi = __builtin_amdgcn_readlane(ix[0], wl);
+      const float hv = wi == 0 ? sv[0] : wi == 1 ? sv[1] : wi == 2 ? sv[2] : sv[3];
+      const float wv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, hv), wl));
+      if (lane == k) {
+        my_e = 4 * wl + wi;
+        my_v = wv;
       }
+      const bool win = lane == wl;
+      key[0] = win ? key[1] : key[0];
+      ix[0] = win ? ix[1] : ix[0];
+      key[1] = win ? key[2] : key[1];
+      ix[1] = win ? ix[2] : ix[1];
+      key[2] = win ? key[3] : key[2];
+      ix[2] = win ? ix[3] : ix[2];
+      key[3] = win ? 0u : key[3];
     }
     float w;
-    if (p.router == MK2_ROUTER_SIGMOID_BIAS) {
-      const float tot = wave_sum(lane < p.topk ? v : 0.f);
-      w = v / tot * p.route_scale;
+    if (sig) {
+      const float tot = wave_sum(lane < p.topk ? my_v : 0.f);
+      w = my_v / tot * p.route_scale;
     } else {
-      const float top = wave_max(lane < p.topk ? v : -INFINITY);
-      const float ex = lane < p.topk ? expf(v - top) : 0.f;
+      const float top = wave_max(lane < p.topk ? my_v : -INFINITY);
+      const float ex = lane < p.topk ? expf(my_v - top) : 0.f;
       w = ex / wave_sum(ex);
     }
     if (lane < p.topk) {
-      st_dev_i32(p.topk_ids + r * p.topk + rank, e);
-      st_dev_f32(p.topk_w + r * p.topk + rank, w);
-      lds_ids[r * p.topk + rank] = e;
-      lds_w[r * p.topk + rank] = w;
-      lds_slot[e] = 1;
-    }
-    __builtin_amdgcn_wave_barrier();
-  }
-  __syncthreads();
-  // distinct experts, ascending: exclusive scan of the flags
-  int flag[4] = {0, 0, 0, 0}, mine = 0;
-  const int per_t = (p.E + NT - 1) / NT;  // <= 4 (E <= 256, NT >= 64)
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int e = tid * per_t + i;
-    flag[i] = (i < per_t && e < p.E) ? lds_slot[e] : 0;
-    mine += flag[i];
-  }
-  int incl = mine;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    int v = __shfl_up(incl, o, 64);
-    if (lane >= o) incl += v;
-  }
-  int* wtot = lds_slot + p.E;
-  __syncthreads();
-  if (lane == 63) wtot[wave] = incl;
-  __syncthreads();
-  int before = 0;
-  for (int w = 0; w < wave; ++w) before += wtot[w];
-  int total = 0;
-  for (int w = 0; w < NW; ++w) total += wtot[w];
-  int pos = before + incl - mine;
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int e = tid * per_t + i;
-    if (i < per_t && e < p.E) {
-      lds_slot[e] = flag[i] ? pos : -1;
-      if (flag[i]) st_dev_i32(p.act + 1 + pos, e);
-      pos += flag[i];
+      st_dev_i32(p.topk_ids + r * p.topk + lane, my_e);
+      st_dev_f32(p.topk_w + r * p.topk + lane, w);
+      L.ids[r * p.topk + lane] = my_e;
+      L.w[r * p.topk + lane] = w;
+      L.flag[my_e] = 1;
     }
   }
-  if (tid == 0) st_dev_i32(p.act, total);
-  // the route-weight table, built in LDS (over the logits, which are done) and
-  // stored once
-  float* lrw = lds_logits;  // [total][32]
-  for (int idx = tid; idx < total * 32; idx += NT) lrw[idx] = 0.f;
   __syncthreads();
-  for (int idx = tid; idx < p.M * p.topk; idx += NT) lrw[lds_slot[lds_ids[idx]] * 32 + idx / p.topk] = lds_w[idx];
+  // the distinct experts, ascending (one wave: four ballots over e = lane + 64 i)
+  if (wave == 0) {
+    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    int tot = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = lane + 64 * i;
+      const int f = e < p.E ? L.flag[e] : 0;
+      const uint64_t m = __ballot(f != 0);
+      if (e < p.E) {
+        const int pos = tot + __popcll(m & below);
+        L.flag[e] = f ? pos : -1;
+        if (f) st_dev_i32(p.act + 1 + pos, e);
+      }
+      tot += __popcll(m);
+    }
+    if (lane == 0) {
+      st_dev_i32(p.act, tot);
+      L.tot = tot;
+    }
+  }
+  __syncthreads();
+  const int total = L.tot;
+  for (int idx = tid; idx < p.M * p.topk; idx += NT) L.rw[L.flag[L.ids[idx]] * 32 + idx / p.topk] = L.w[idx];
   __syncthreads();
   for (int idx = 4 * tid; idx < total * 32; idx += 4 * NT)
-    st_dev_16(p.rw + idx, make_uint4(__float_as_uint(lrw[idx]), __float_as_uint(lrw[idx + 1]),
-                                     __float_as_uint(lrw[idx + 2]), __float_as_uint(lrw[idx + 3])));
+    st_dev_16(p.rw + idx, make_uint4(__float_as_uint(L.rw[idx]), __float_as_uint(L.rw[idx + 1]),
+                                     __float_as_uint(L.rw[idx + 2]), __float_as_uint(L.rw[idx + 3])));
 }
 
 // ------------------------------------------------------- stage: up/gate + SwiGLU

@@ -5,14 +5,16 @@ glm53/gfx950/kernel.py:1967-1999):
   * expert ids: the kernel's picks equal the exact top-k of its own router scores
     (key desc, lower id first), and equal the oracle's where the k-th / k+1-th gap
     exceeds the logit tolerance;
-  * router logits within 1e-4 of the largest logit of the row against the oracle;
+  * router logits within 1e-4 of the largest logit of the row against the oracle (with
+    RMSNorm, beyond what the bf16 rounding of near-midpoint normalized elements can
+    move them: refs.norm_rounding_slack);
   * bf16 outputs within rel-L2 <= 1e-2 of the oracle (after FP8/FP4 dequant).
 """
 
 import pytest
 import torch
 
-from refs import MoEOracle, cpu
+from refs import MoEOracle, cpu, logit_error, norm_rounding_slack
 from oracle import reference as R
 from oracle import codecs as oc
 
@@ -49,8 +51,8 @@ def _check(cfg, w, out, logits, ids, wts, norm=False, residual=False):
     orc = MoEOracle(w)
     ref, rids, rw, rlogits = orc(w.x, norm=norm, residual=residual, eps=1e-6)
     # logits against the oracle
-    scale = rlogits.abs().amax(-1, keepdim=True)
-    assert ((logits - rlogits).abs() / scale).max() <= LOGIT_TOL
+    slack = norm_rounding_slack(w.x.float(), orc.gamma, 1e-6) if norm else None
+    assert logit_error(logits, rlogits, orc.w_router, slack) <= LOGIT_TOL
     # ids: exact top-k of the kernel's own scores
     if cfg.router == C.ROUTER_SIGMOID_BIAS:
         own_keys = oc.radix_keys(torch.sigmoid(logits) + orc.bias)

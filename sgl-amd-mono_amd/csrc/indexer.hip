@@ -10,6 +10,8 @@ constexpr int IDX_NT = 512;
 __global__ __launch_bounds__(256) void k_idx_clear(IdxDev p) {
   for (int i = blockIdx.x * 256 + threadIdx.x; i < p.rows * IDX_BINS; i += gridDim.x * 256) p.hist[i] = 0;
   for (int i = blockIdx.x * 256 + threadIdx.x; i < p.rows * IDX_CBINS; i += gridDim.x * 256) p.chist[i] = 0;
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < p.rows * p.nchk; i += gridDim.x * 256) p.ccount[i] = 0;
+  if (blockIdx.x == 0 && threadIdx.x == 0) *p.ticket = 0;
 }
 
 __global__ __launch_bounds__(IDX_NT) void k_idx_score(IdxDev p) {
@@ -17,14 +19,24 @@ __global__ __launch_bounds__(IDX_NT) void k_idx_score(IdxDev p) {
   idx_score<IDX_NT>(p, blockIdx.y, blockIdx.x, L);
 }
 
+// slices take their tasks in the order the workgroups start (a ticket), so that the
+// earlier chunks a slice waits for have always started
+constexpr int IDX_SLICE_SPIN = 1 << 24;
 __global__ __launch_bounds__(IDX_NT) void k_idx_slice(IdxDev p) {
   __shared__ TopkLds S;
-  idx_slice<IDX_NT>(p, blockIdx.y, blockIdx.x, S);
+  if (threadIdx.x == 0) S.res[3] = atomicAdd(p.ticket, 1);
+  __syncthreads();
+  const int t = S.res[3];
+  __syncthreads();
+  idx_slice<IDX_NT>(p, t / p.nchk, t % p.nchk, S, IDX_SLICE_SPIN, nullptr);
 }
 
 __global__ __launch_bounds__(TOPK_NT) void k_idx_select(IdxDev p) {
   __shared__ TopkLds S;
   idx_select<TOPK_NT>(p, blockIdx.x, S);
+  __syncthreads();
+  idx_topk_reset<TOPK_NT>(p, blockIdx.x);  // the workspace left as a persistent launch leaves it
+  if (blockIdx.x == 0 && threadIdx.x == 0) *p.ticket = 0;
 }
 
 int idx_check_shape(const mk2_indexer_shape* s) {
@@ -42,7 +54,7 @@ int idx_check_shape(const mk2_indexer_shape* s) {
 }
 
 // workspace: scores, top-k lists (used when the caller gives none), row histograms (fine, coarse),
-// chunk candidate counts, candidates
+// chunk counts, bin-b1 candidates, the slices' ticket
 size_t idx_carve(const mk2_indexer_shape* s, void* base, IdxDev* d) {
   Carver c(base);
   const int nchk = (s->max_ctx + IDX_CHUNK - 1) / IDX_CHUNK;
@@ -52,6 +64,7 @@ size_t idx_carve(const mk2_indexer_shape* s, void* base, IdxDev* d) {
   int* chist = c.take<int>((size_t)s->rows * IDX_CBINS);
   int* cnt = c.take<int>((size_t)s->rows * nchk);
   uint2* cand = c.take<uint2>((size_t)s->rows * s->max_ctx);
+  int* ticket = c.take<int>(1);
   if (d) {
     if (!d->scores) d->scores = sc;
     if (!d->out) d->out = tk;
@@ -59,6 +72,7 @@ size_t idx_carve(const mk2_indexer_shape* s, void* base, IdxDev* d) {
     d->chist = chist;
     d->ccount = cnt;
     d->cand = cand;
+    d->ticket = ticket;
   }
   return c.bytes();
 }

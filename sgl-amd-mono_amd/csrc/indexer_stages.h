@@ -52,8 +52,9 @@ struct IdxDev {
   // workspace
   int* hist;            // [rows][IDX_BINS] key counts by top 12 bits (zero between launches)
   int* chist;           // [rows][IDX_CBINS] key counts by top 8 bits (zero between launches)
-  int* ccount;          // [rows][nchk] candidates of each chunk
-  uint2* cand;          // [rows][max_ctx] (key, position); chunk c from c * IDX_CHUNK
+  int* ccount;          // [rows][nchk] chunk counts: CC_FLAG | above | in-bin << 15 (zero between launches)
+  uint2* cand;          // [rows][max_ctx] (key, position) of bin b1; chunk c from c * IDX_CHUNK
+  int* ticket;          // standalone slices: the next task (zero between launches)
 };
 
 constexpr int IDX_QROW = 136;  // LDS row stride (bf16) of the staged queries
@@ -485,11 +486,18 @@ MK2_DEV void idx_clear_hist(const IdxDev& p, int r) {
 }
 
 // ---------------------------------------------------------------- stage: slice
-// Task (row r, chunk): the chunk's keys whose top 12 bits are >= b1, in position
-// order, to cand[r][chunk * IDX_CHUNK ..]; their count to ccount[r][chunk].  Returns
-// whether S.res[0..1] now hold the row's threshold bin and the count above it.
+// Task (row r, chunk), with b1 the 12-bit bin of the row's k-th key: the chunk's keys
+// above bin b1 all make the list, and go to it directly, in position order, after
+// the row's earlier chunks' (the list's first part); the keys in bin b1 go to
+// cand[r][chunk * IDX_CHUNK ..], in position order, for the row's last slice to
+// finish the list.  The chunk's two counts are published in ccount[r][chunk] first;
+// then the task waits for the earlier chunks' counts (tasks only wait on chunks of
+// lower index, which publish before they wait, so with every task started every wait
+// ends; a wait past `spin` polls, or the sticky error word `err` set, gives up and
+// sets it).  Returns whether S.res[0..1] now hold b1 and the count above it.
+constexpr int CC_FLAG = 1 << 30;
 template <int NT>
-MK2_DEV bool idx_slice(const IdxDev& p, int r, int chunk, TopkLds& S) {
+MK2_DEV bool idx_slice(const IdxDev& p, int r, int chunk, TopkLds& S, int spin, int* err) {
   constexpr int PER = IDX_CHUNK / NT;  // consecutive positions a thread
   static_assert(PER % 4 == 0, "a thread reads whole 16-byte groups of scores");
   const int tid = threadIdx.x;
@@ -497,7 +505,7 @@ MK2_DEV bool idx_slice(const IdxDev& p, int r, int chunk, TopkLds& S) {
   const int k_begin = chunk * IDX_CHUNK;
   int* cnt_out = p.ccount + (size_t)r * p.nchk + chunk;
   if (n <= k || k_begin >= n) {
-    if (tid == 0) st_dev_i32(cnt_out, 0);
+    if (tid == 0) st_dev_i32(cnt_out, CC_FLAG);
     return false;
   }
   // the chunk's scores first: their loads overlap the threshold search
@@ -522,34 +530,69 @@ MK2_DEV bool idx_slice(const IdxDev& p, int r, int chunk, TopkLds& S) {
     key[4 * q + 2] = radix_key(__uint_as_float(raw[q].z));
     key[4 * q + 3] = radix_key(__uint_as_float(raw[q].w));
   }
-  int mine = 0;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) mine += (base + i < n && (key[i] >> 20) >= b1) ? 1 : 0;
-  Scan3 tot;
-  int at = block_scan3<NT>(Scan3{mine, 0, 0}, &tot, S.scratch).a;
-  uint2* dst = p.cand + (size_t)r * p.max_ctx + k_begin;
+  int m1 = 0, mb = 0;
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
-    if (base + i < n && (key[i] >> 20) >= b1) {
+    const bool valid = base + i < n;
+    m1 += (valid && (key[i] >> 20) > b1) ? 1 : 0;
+    mb += (valid && (key[i] >> 20) == b1) ? 1 : 0;
+  }
+  Scan3 tot;
+  const Scan3 off = block_scan3<NT>(Scan3{m1, mb, 0}, &tot, S.scratch);
+  if (tid == 0) st_dev_i32(cnt_out, CC_FLAG | tot.a | (tot.b << 15));
+  uint2* dst = p.cand + (size_t)r * p.max_ctx + k_begin;
+  int at = off.b;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    if (base + i < n && (key[i] >> 20) == b1) {
       st_dev_8(dst + at, make_uint2(key[i], (uint32_t)(base + i)));
       ++at;
     }
   }
-  if (tid == 0) st_dev_i32(cnt_out, tot.a);
+  // the keys above bin b1 in the row's earlier chunks (nchk <= 64: a lane a chunk)
+  if (tid < 64) {
+    const int lane = tid;
+    int v = CC_FLAG;
+    if (chunk > 0) {
+      const int* cc = p.ccount + (size_t)r * p.nchk;
+      for (int polls = 1;; ++polls) {
+        v = lane < chunk ? ld_dev_i32(cc + lane) : CC_FLAG;
+        if (__ballot((v & CC_FLAG) == 0) == 0) break;
+        if (polls > spin || ((polls & 31) == 0 && err && ld_dev_i32(err))) {
+          if (lane == 0 && err) atomicOr(err, 1);
+          break;
+        }
+      }
+    }
+    int pre = lane < chunk ? (v & 0x7FFF) : 0;  // a count not yet published reads 0
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) pre += __shfl_xor(pre, o, 64);
+    if (tid == 0) S.res[2] = pre;
+  }
+  __syncthreads();
+  int* orow = p.out + (size_t)r * k;
+  at = S.res[2] + off.a;  // < the count above bin b1 < k
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    if (base + i < n && (key[i] >> 20) > b1) {
+      st_dev_i32(orow + at, base + i);
+      ++at;
+    }
+  }
   return true;
 }
 
-// The select when more than TOPK_CAP candidates remain (a row whose keys crowd into
-// the threshold bin): the same radix select and list, streamed over the candidates
-// in global memory, NT at a time in position order.
+// The list's bin-b1 part when more than TOPK_CAP keys share bin b1 (a row whose keys
+// crowd into one bin): the k-th key's radix select and the list entries base ..
+// base + k - 1, streamed over the candidates in global memory, NT at a time in
+// position order.
 template <int NT>
-MK2_DEV void topk_stream(const IdxDev& p, int r, uint32_t kbase, int m,
-                                                      TopkLds& S) {
+MK2_DEV void topk_stream(const IdxDev& p, int r, uint32_t kbase, int m, int k, int base, TopkLds& S) {
   constexpr int NW = NT / 64;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int k = p.topk, nchk = p.nchk;
+  const int nchk = p.nchk;
   const uint2* cr = p.cand + (size_t)r * p.max_ctx;
-  int* orow = p.out + (size_t)r * k;
+  int* orow = p.out + (size_t)r * p.topk;
   auto cand_d = [&](int j) -> uint32_t {  // candidate j (position order) - kbase
     int lo = 0, hi = nchk;
     while (hi - lo > 1) {
@@ -624,14 +667,15 @@ MK2_DEV void topk_stream(const IdxDev& p, int r, uint32_t kbase, int m,
     if (g1) dst = o1 + off.a;
     else if (g2) dst = n1 + o2 + off.b;
     else if (g3 && r3 + off.c < ties_needed) dst = above_T + r3 + off.c;
-    if (dst >= 0 && dst < k) st_dev_i32(orow + dst, cand_pos(j));
+    if (dst >= 0 && dst < k) st_dev_i32(orow + base + dst, cand_pos(j));
     o1 += tot.a;
     o2 += tot.b;
     r3 += tot.c;
   }
 }
 
-// Exact selection over m <= TOPK_CAP candidates in LDS (position order).  Round i
+// Exact selection over m <= TOPK_CAP candidates in LDS (position order); the list
+// entries lo .. k - 1 are stored (the ones before lo are written elsewhere).  Round i
 // gives thread t the candidate j = i * NT + t, so lanes read consecutive words; a
 // candidate's rank in its group is its wave's offset for the round (one scan over
 // all (round, wave) counts) plus the ballot count of the lanes below it.  Keys with
@@ -639,7 +683,7 @@ MK2_DEV void topk_stream(const IdxDev& p, int r, uint32_t kbase, int m,
 // (part) and the need = k - above1 largest of them found by three radix digits of
 // their low 20 bits (8, 8 and 4 bits), each located by one wave.
 template <int NT, int CPT>
-MK2_DEV void cand_select(TopkLds& S, int m, uint32_t b1, int above1, int k, int* orow) {
+MK2_DEV void cand_select(TopkLds& S, int m, uint32_t b1, int above1, int k, int* orow, int lo) {
   constexpr int NW = NT / 64;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
@@ -744,14 +788,14 @@ MK2_DEV void cand_select(TopkLds& S, int m, uint32_t b1, int above1, int k, int*
     if (dst >= 0 && dst < k) list[dst] = (int)S.cpos[j];
   }
   __syncthreads();
-  for (int i = 4 * tid; i < k; i += 4 * NT)
-    st_dev_16(orow + i, make_uint4(list[i], list[i + 1], list[i + 2], list[i + 3]));
+  for (int i = lo + tid; i < k; i += NT) st_dev_i32(orow + i, list[i]);
 }
 
 // --------------------------------------------------------------- stage: select
-// Task (row r): the exact top-k of the row from its slices' candidates; then the
-// row's histograms are cleared for the next launch.  `known`: S.res[0..1] already
-// hold the row's threshold bin and the count above it (the workgroup ran one of the
+// Task (row r), once every slice of the row is done: the list's bin-b1 part.  The
+// keys above bin b1 (above1 of them) are already listed by the slices; of the keys in
+// bin b1 the need = k - above1 largest follow, as list entries above1 .. k - 1.
+// `known`: S.res[0..1] already hold b1 and above1 (the workgroup ran one of the
 // row's slices just before).
 template <int NT>
 MK2_DEV void idx_select(const IdxDev& p, int r, TopkLds& S, bool known = false) {
@@ -763,11 +807,10 @@ MK2_DEV void idx_select(const IdxDev& p, int r, TopkLds& S, bool known = false) 
   int* orow = p.out + (size_t)r * k;
   if (n <= k) {
     for (int i = tid; i < k; i += NT) st_dev_i32(orow + i, i < n ? i : -1);
-    idx_clear_hist<NT>(p, r);
     return;
   }
   const int nchk = p.nchk;
-  // the threshold bin (wave 0) and the chunks' candidate offsets (position order)
+  // the threshold bin (wave 0) and the chunks' bin-b1 offsets (position order)
   if (!known && tid < 64) {
     int above;
     const int b1 = wave_threshold(p, r, k, &above);
@@ -775,7 +818,7 @@ MK2_DEV void idx_select(const IdxDev& p, int r, TopkLds& S, bool known = false) 
   }
   {
     // a chunk holds at most its own positions
-    const int c = tid < nchk ? min(max(ldp_i32(p.ccount + (size_t)r * nchk + tid), 0),
+    const int c = tid < nchk ? min((ldp_i32(p.ccount + (size_t)r * nchk + tid) >> 15) & 0x7FFF,
                                    min(IDX_CHUNK, p.max_ctx - tid * IDX_CHUNK))
                              : 0;
     Scan3 tot;
@@ -786,11 +829,9 @@ MK2_DEV void idx_select(const IdxDev& p, int r, TopkLds& S, bool known = false) 
   const uint32_t b1 = (uint32_t)S.res[0];
   const int above1 = S.res[1];
   const int m = S.offs[nchk];
-  // every slice has read the histograms before it published its count
-  idx_clear_hist<NT>(p, r);
   if (m > TOPK_CAP) {
     // keys relative to the bottom of bin b1: d >= 1 for every candidate
-    topk_stream<NT>(p, r, (b1 << 20) - 1u, m, S);
+    topk_stream<NT>(p, r, (b1 << 20) - 1u, m, k - above1, above1, S);
     return;
   }
   // gather: TPC threads a chunk, 8 loads in flight a thread
@@ -818,7 +859,15 @@ MK2_DEV void idx_select(const IdxDev& p, int r, TopkLds& S, bool known = false) 
     }
   }
   __syncthreads();
-  cand_select<NT, CPT>(S, m, b1, above1, k, orow);
+  cand_select<NT, CPT>(S, m, b1, above1, k, orow, above1);
+}
+
+// Row r's top-k state back to zero for the next launch (every reader is done): the
+// histograms and the chunk counts.
+template <int NT>
+MK2_DEV void idx_topk_reset(const IdxDev& p, int r) {
+  idx_clear_hist<NT>(p, r);
+  for (int c = threadIdx.x; c < p.nchk; c += NT) st_dev_i32(p.ccount + (size_t)r * p.nchk + c, 0);
 }
 
 }  // namespace mk2

@@ -180,14 +180,15 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
     k2_signal(p, SY_SCORE + t / nchk);
   }
   k2_stamp(p, 3 * st++ + 2);
-  // ---- top-k slices: each chunk's candidates
+  // ---- top-k slices: each chunk lists its keys above the row's threshold bin and
+  // keeps its keys in the bin
   k2_stamp(p, 3 * st);
   // slices on the workgroups of their score chunks (base unchanged); the last slice
-  // of a row runs the row's exact top-k over the candidates
+  // of a row finishes the row's list from the keys in the threshold bin
   K2_TASKS(t, R * nchk) {
     const int r = t / nchk;
     k2_wait(p, seen, SY_SCORE + r, nchk, t < G ? 3 * st + 1 : -1);
-    const bool known = idx_slice<K2_NT>(p.idx, r, t % nchk, S.topk);
+    const bool known = idx_slice<K2_NT>(p.idx, r, t % nchk, S.topk, p.spin_limit, k2_ctr(p, SY_ERR));
     if (k2_signal_last1(p, SY_SLICE + r, nchk, &last_flag)) {
       k2_stamp(p, 3 * (st + 1));
       k2_stamp(p, 3 * (st + 1) + 1);
@@ -195,6 +196,7 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
       idx_select<K2_NT>(p.idx, r, S.topk, known);
       k2_signal(p, SY_TOPK + r);
       k2_stamp(p, 3 * (st + 1) + 2);
+      idx_topk_reset<K2_NT>(p.idx, r);  // every slice of the row is done with them
     }
   }
   K2_NEXT(R * nchk);

@@ -205,12 +205,7 @@ template <int NT>
 MK2_DEV Scan3 block_scan3(Scan3 v, Scan3* tot, int* lds /* 3 * NT/64 */) {
   constexpr int NW = NT / 64;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  Scan3 inc = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    int xa = __shfl_up(inc.a, o, 64), xb = __shfl_up(inc.b, o, 64), xc = __shfl_up(inc.c, o, 64);
-    if (lane >= o) { inc.a += xa; inc.b += xb; inc.c += xc; }
-  }
+  const Scan3 inc = {wave_incl_scan(v.a), wave_incl_scan(v.b), wave_incl_scan(v.c)};
   __syncthreads();
   if (lane == 63) { lds[wave] = inc.a; lds[NW + wave] = inc.b; lds[2 * NW + wave] = inc.c; }
   __syncthreads();
@@ -238,16 +233,6 @@ MK2_DEV int block_sum_int(int v, int* lds) {
 #pragma unroll
   for (int w = 0; w < NW; ++w) t += lds[w];
   return t;
-}
-
-MK2_DEV int wave_incl_scan(int v) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int x = __shfl_up(v, o, 64);
-    if (lane >= o) v += x;
-  }
-  return v;
 }
 
 // One wave: the bin of hist[nbins] (LDS, nbins a multiple of 64) where the count from
@@ -339,12 +324,7 @@ MK2_DEV int find_bin(const int* hist, int nbins, int need, int* above_out, int* 
   sh[u] = local;
   __syncthreads();
   int v = sh[tid];         // thread tid now scans position tid of the reversed order
-  int inc = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    int x = __shfl_up(inc, o, 64);
-    if (lane >= o) inc += x;
-  }
+  const int inc = wave_incl_scan(v);
   int* wt = lds + NT;
   __syncthreads();
   if (lane == 63) wt[tid >> 6] = inc;
@@ -463,11 +443,9 @@ struct TopkLds {
   int scratch[1024 + 1024 / 64 + 8];
   int offs[TOPK_MAXN / IDX_CHUNK + 8];
   int res[4];
-  int np;                   // candidates listed in part
   uint32_t ckey[TOPK_CAP];
   uint16_t cpos[TOPK_CAP];
-  uint16_t part[TOPK_CAP];  // candidates in the threshold bin (indices into ckey)
-  int gcount[3][TOPK_CAP / 64];  // per (round, wave): group 1/2/3 counts, then their offsets
+  int gcount[2][TOPK_CAP / 64];  // per (round, wave): counts above / equal to the k-th key, then offsets
 };
 
 // Row r's histograms back to zero (every reader is done): the fine bins of each
@@ -674,121 +652,94 @@ MK2_DEV void topk_stream(const IdxDev& p, int r, uint32_t kbase, int m, int k, i
   }
 }
 
-// Exact selection over m <= TOPK_CAP candidates in LDS (position order); the list
-// entries lo .. k - 1 are stored (the ones before lo are written elsewhere).  Round i
-// gives thread t the candidate j = i * NT + t, so lanes read consecutive words; a
-// candidate's rank in its group is its wave's offset for the round (one scan over
-// all (round, wave) counts) plus the ballot count of the lanes below it.  Keys with
-// top 12 bits > b1 (above1 of them) all make the list; the keys of bin b1 are listed
-// (part) and the need = k - above1 largest of them found by three radix digits of
-// their low 20 bits (8, 8 and 4 bits), each located by one wave.
+// The list entries base .. k - 1 from the m <= TOPK_CAP keys of bin b1 in LDS
+// (position order): the need = k - base largest by their low 20 bits, ties by
+// position.  Three radix digits (8, 8 and 4 bits), each located by one wave over its
+// own histogram (S.hist[256 * pass ..], cleared by the caller); then the keys above
+// the k-th key in position order, then the keys equal to it, as many as fill.  Round
+// i gives thread t the candidate j = i * NT + t, so lanes read consecutive words; a
+// candidate's rank in its group is its wave's offset for the round (one scan over all
+// (round, wave) counts) plus the ballot count of the lanes below it.
 template <int NT, int CPT>
-MK2_DEV void cand_select(TopkLds& S, int m, uint32_t b1, int above1, int k, int* orow, int lo) {
+MK2_DEV void bin_select(TopkLds& S, int m, int base, int k, int* orow) {
   constexpr int NW = NT / 64;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
   const int nr = (m + NT - 1) / NT;  // rounds that hold candidates (<= CPT)
-  if (tid == 0) S.np = 0;
-  __syncthreads();
-  // bin b1's candidates into part (any order)
-#pragma unroll 4
-  for (int i = 0; i < nr; ++i) {
-    const int j = i * NT + tid;
-    const bool in = j < m && (S.ckey[j] >> 20) == b1;
-    const uint64_t bal = __ballot(in);
-    if (bal) {
-      int base = 0;
-      if (lane == 0) base = atomicAdd(&S.np, __popcll(bal));
-      base = __shfl(base, 0, 64);
-      if (in) S.part[base + __popcll(bal & below)] = (uint16_t)j;
-    }
-  }
-  __syncthreads();
-  const int np = S.np;
-  int need = k - above1;
+  int need = k - base;
   uint32_t prefix = 0;  // the digits found so far
 #pragma unroll 1
   for (int pass = 0; pass < 3; ++pass) {
     const int shift = pass == 0 ? 12 : (pass == 1 ? 4 : 0), width = pass == 2 ? 4 : 8;
     const int hi = shift + width;  // bits above this digit are the prefix
-    if (tid < 256) S.hist[tid] = 0;
-    __syncthreads();
-    for (int j = tid; j < np; j += NT) {
-      const uint32_t v = S.ckey[S.part[j]] & 0xFFFFFu;
-      if ((v >> hi) == prefix) atomicAdd(&S.hist[(v >> shift) & ((1u << width) - 1u)], 1);
+    int* h = S.hist + 256 * pass;
+    for (int j = tid; j < m; j += NT) {
+      const uint32_t v = S.ckey[j] & 0xFFFFFu;
+      if ((v >> hi) == prefix) atomicAdd(&h[(v >> shift) & ((1u << width) - 1u)], 1);
     }
     __syncthreads();
     if (tid < 64) {
       int ab;
-      const int b = wave_find_bin(S.hist, 256, need, &ab);
+      const int b = wave_find_bin(h, 256, need, &ab);
       if (tid == 0) { S.res[0] = b; S.res[1] = ab; }
     }
     __syncthreads();
+    // every thread reads S.res before it reaches the next pass's barrier, after which
+    // wave 0 rewrites it
     prefix = (prefix << width) | (uint32_t)S.res[0];
     need -= S.res[1];
-    __syncthreads();
   }
-  const uint32_t T = prefix;  // low 20 bits of the k-th key
-  const int ties_needed = need;
-  const int above_T = k - ties_needed;
-  // group counts per (round, wave): 1 = above bin b1, 2 = bin b1 and > T, 3 = == T
+  const uint32_t T = prefix;              // low 20 bits of the k-th key
+  const int ties = need, n_gt = k - base - need;
+  // group counts per (round, wave): 0 = above T, 1 = equal to T
 #pragma unroll 4
   for (int i = 0; i < nr; ++i) {
     const int j = i * NT + tid;
-    const uint32_t key = j < m ? S.ckey[j] : 0u;
-    const bool valid = j < m, in = valid && (key >> 20) == b1;
-    const uint32_t low = key & 0xFFFFFu;
-    const int n1 = __popcll(__ballot(valid && (key >> 20) > b1));
-    const int n2 = __popcll(__ballot(in && low > T));
-    const int n3 = __popcll(__ballot(in && low == T));
+    const bool valid = j < m;
+    const uint32_t low = valid ? S.ckey[j] & 0xFFFFFu : 0u;
+    const int n2 = __popcll(__ballot(valid && low > T));
+    const int n3 = __popcll(__ballot(valid && low == T));
     if (lane == 0) {
-      S.gcount[0][i * NW + wave] = n1;
-      S.gcount[1][i * NW + wave] = n2;
-      S.gcount[2][i * NW + wave] = n3;
+      S.gcount[0][i * NW + wave] = n2;
+      S.gcount[1][i * NW + wave] = n3;
     }
   }
   __syncthreads();
-  // exclusive scans of the three count sequences, in (round, wave) order
-  if (wave < 3) {
+  // exclusive scans of the two count sequences, in (round, wave) order
+  if (wave < 2) {
     constexpr int PER = (CPT * NW + 63) / 64;
     const int E = nr * NW;
-    int* g = S.gcount[wave];
+    int* gc = S.gcount[wave];
     int v[PER], sum = 0;
 #pragma unroll
     for (int e = 0; e < PER; ++e) {
-      v[e] = lane * PER + e < E ? g[lane * PER + e] : 0;
+      v[e] = lane * PER + e < E ? gc[lane * PER + e] : 0;
       sum += v[e];
     }
     int run = wave_incl_scan(sum) - sum;
 #pragma unroll
     for (int e = 0; e < PER; ++e) {
-      if (lane * PER + e < E) g[lane * PER + e] = run;
+      if (lane * PER + e < E) gc[lane * PER + e] = run;
       run += v[e];
     }
   }
   __syncthreads();
-  const int n1_all = above1;  // every key above bin b1 is a candidate
-  int* list = S.hist;         // the list is built in LDS (k <= IDX_BINS), then stored
 #pragma unroll 4
   for (int i = 0; i < nr; ++i) {
     const int j = i * NT + tid;
-    const uint32_t key = j < m ? S.ckey[j] : 0u;
-    const bool valid = j < m, in = valid && (key >> 20) == b1;
-    const uint32_t low = key & 0xFFFFFu;
-    const bool g1 = valid && (key >> 20) > b1, g2 = in && low > T, g3 = in && low == T;
-    const uint64_t b1m = __ballot(g1), b2m = __ballot(g2), b3m = __ballot(g3);
+    const bool valid = j < m;
+    const uint32_t low = valid ? S.ckey[j] & 0xFFFFFu : 0u;
+    const bool g2 = valid && low > T, g3 = valid && low == T;
+    const uint64_t b2m = __ballot(g2), b3m = __ballot(g3);
     const int e = i * NW + wave;
     int dst = -1;
-    if (g1) dst = S.gcount[0][e] + __popcll(b1m & below);
-    else if (g2) dst = n1_all + S.gcount[1][e] + __popcll(b2m & below);
+    if (g2) dst = base + S.gcount[0][e] + __popcll(b2m & below);
     else if (g3) {
-      const int r3 = S.gcount[2][e] + __popcll(b3m & below);
-      if (r3 < ties_needed) dst = above_T + r3;
+      const int r3 = S.gcount[1][e] + __popcll(b3m & below);
+      if (r3 < ties) dst = base + n_gt + r3;
     }
-    if (dst >= 0 && dst < k) list[dst] = (int)S.cpos[j];
+    if (dst >= 0 && dst < k) st_dev_i32(orow + dst, (int)S.cpos[j]);
   }
-  __syncthreads();
-  for (int i = lo + tid; i < k; i += NT) st_dev_i32(orow + i, list[i]);
 }
 
 // --------------------------------------------------------------- stage: select
@@ -799,8 +750,9 @@ MK2_DEV void cand_select(TopkLds& S, int m, uint32_t b1, int above1, int k, int*
 // row's slices just before).
 template <int NT>
 MK2_DEV void idx_select(const IdxDev& p, int r, TopkLds& S, bool known = false) {
-  constexpr int CPT = TOPK_CAP / NT;  // candidates a thread
-  constexpr int TPC = NT / (TOPK_MAXN / IDX_CHUNK);  // gather threads a chunk
+  constexpr int CPT = TOPK_CAP / NT;                  // candidates a thread
+  constexpr int TPC = NT / (TOPK_MAXN / IDX_CHUNK);   // gather threads a chunk
+  constexpr int SPEC = 8;                             // candidates a thread loads with the counts
   const int tid = threadIdx.x;
   const int n = p.ctx[r];
   const int k = p.topk;
@@ -810,56 +762,63 @@ MK2_DEV void idx_select(const IdxDev& p, int r, TopkLds& S, bool known = false) 
     return;
   }
   const int nchk = p.nchk;
-  // the threshold bin (wave 0) and the chunks' bin-b1 offsets (position order)
   if (!known && tid < 64) {
     int above;
     const int b1 = wave_threshold(p, r, k, &above);
     if (tid == 0) { S.res[0] = b1; S.res[1] = above; }
   }
-  {
-    // a chunk holds at most its own positions
-    const int c = tid < nchk ? min((ldp_i32(p.ccount + (size_t)r * nchk + tid) >> 15) & 0x7FFF,
-                                   min(IDX_CHUNK, p.max_ctx - tid * IDX_CHUNK))
-                             : 0;
-    Scan3 tot;
-    const int off = block_scan3<NT>(Scan3{c, 0, 0}, &tot, S.scratch).a;
-    if (tid <= nchk) S.offs[tid] = tid < nchk ? off : tot.a;
+  for (int i = tid; i < 3 * 256; i += NT) S.hist[i] = 0;  // the three digit histograms
+  // one round trip: each chunk's count of bin-b1 keys and its first SPEC * TPC of them
+  const int c = tid / TPC, sub = tid % TPC;
+  const uint2* src = p.cand + (size_t)r * p.max_ctx + (size_t)c * IDX_CHUNK;
+  int cnt = 0;
+  uint2 v[SPEC];
+  if (c < nchk) {
+    const int lim = min(IDX_CHUNK, p.max_ctx - c * IDX_CHUNK);  // the chunk's area (>= 64)
+    cnt = min((ldp_i32(p.ccount + (size_t)r * nchk + c) >> 15) & 0x7FFF, lim);
+#pragma unroll
+    for (int u = 0; u < SPEC; ++u) v[u] = ldp_8(src + min(sub + u * TPC, lim - 1));
   }
+  Scan3 tot;  // a chunk's count enters at its last thread: every thread of the chunk gets its offset
+  const int off = block_scan3<NT>(Scan3{sub == TPC - 1 ? cnt : 0, 0, 0}, &tot, S.scratch).a;
+  if (sub == 0 && c < nchk) S.offs[c] = off;
+  if (tid == 0) S.offs[nchk] = tot.a;
   __syncthreads();
   const uint32_t b1 = (uint32_t)S.res[0];
   const int above1 = S.res[1];
-  const int m = S.offs[nchk];
+  const int m = tot.a;
   if (m > TOPK_CAP) {
     // keys relative to the bottom of bin b1: d >= 1 for every candidate
     topk_stream<NT>(p, r, (b1 << 20) - 1u, m, k - above1, above1, S);
     return;
   }
-  // gather: TPC threads a chunk, 8 loads in flight a thread
-  {
-    const int c = tid / TPC, sub = tid % TPC;
-    if (c < nchk) {
-      const int cnt = S.offs[c + 1] - S.offs[c], o = S.offs[c];
-      const uint2* src = p.cand + (size_t)r * p.max_ctx + (size_t)c * IDX_CHUNK;
-      for (int i0 = 0; i0 < cnt; i0 += 8 * TPC) {
-        uint2 v[8];
+  if (c < nchk) {
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int i = i0 + sub + u * TPC;
-          v[u] = i < cnt ? ldp_8(src + i) : make_uint2(0, 0);
-        }
+    for (int u = 0; u < SPEC; ++u) {
+      const int i = sub + u * TPC;
+      if (i < cnt) {
+        S.ckey[off + i] = v[u].x;
+        S.cpos[off + i] = (uint16_t)v[u].y;
+      }
+    }
+    for (int i0 = SPEC * TPC; i0 < cnt; i0 += SPEC * TPC) {  // a crowded chunk's rest
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int i = i0 + sub + u * TPC;
-          if (i < cnt) {
-            S.ckey[o + i] = v[u].x;
-            S.cpos[o + i] = (uint16_t)v[u].y;
-          }
+      for (int u = 0; u < SPEC; ++u) {
+        const int i = i0 + sub + u * TPC;
+        v[u] = i < cnt ? ldp_8(src + i) : make_uint2(0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < SPEC; ++u) {
+        const int i = i0 + sub + u * TPC;
+        if (i < cnt) {
+          S.ckey[off + i] = v[u].x;
+          S.cpos[off + i] = (uint16_t)v[u].y;
         }
       }
     }
   }
   __syncthreads();
-  cand_select<NT, CPT>(S, m, b1, above1, k, orow, above1);
+  bin_select<NT, CPT>(S, m, above1, k, orow);
 }
 
 // Row r's top-k state back to zero for the next launch (every reader is done): the

@@ -149,6 +149,22 @@ MK2_DEV float dpp_rows_f32(float old, float v) {
                                                                CTRL, ROWS, 0xF, false));
 }
 constexpr int DPP_BCAST15 = 0x142, DPP_BCAST31 = 0x143;
+constexpr int DPP_SHR1 = 0x111, DPP_SHR2 = 0x112, DPP_SHR4 = 0x114, DPP_SHR8 = 0x118;
+template <int CTRL, int ROWS>
+MK2_DEV int dpp_i32(int v) {  // lanes without a source (or outside ROWS) read 0
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, ROWS, 0xF, false);
+}
+// inclusive scan over the wave: shifts within each 16-lane row, then each row's total
+// carried up (row_bcast:15 into rows 1 and 3, row_bcast:31 into rows 2 and 3)
+MK2_DEV int wave_incl_scan(int v) {
+  v += dpp_i32<DPP_SHR1, 0xF>(v);
+  v += dpp_i32<DPP_SHR2, 0xF>(v);
+  v += dpp_i32<DPP_SHR4, 0xF>(v);
+  v += dpp_i32<DPP_SHR8, 0xF>(v);
+  v += dpp_i32<DPP_BCAST15, 0xA>(v);
+  v += dpp_i32<DPP_BCAST31, 0xC>(v);
+  return v;
+}
 MK2_DEV float wave_sum(float v) {
   v = row16_sum(v);
   v += dpp_rows_f32<DPP_BCAST15, 0xA>(0.f, v);

@@ -573,9 +573,9 @@ MK2_DEV void moe_upgate(const MoeDev& p, int t, float* red, float* midf) {
 // ---------------------------------------------------------- stage: down + combine
 // A task is 16*DT hidden rows; every slot (the shared expert, then the D routed
 // experts) adds rw * W_down[e] . mid into the rows' accumulators; out = bf16(y [+ x]).
-// Waves take every NW-th slot, a batch of slots' weight tiles (and their mid rows,
-// shared by the DT tiles) in flight at once.  act_ids: LDS >= E ints; red: NW * DT *
-// NCG * 256 floats.
+// Waves take every NW-th slot, B slots a unit, the next unit's weight tiles and mid
+// rows (shared by the DT tiles) in flight while a unit's MFMAs run.  act_ids: LDS >=
+// E ints; red: NW * DT * NCG * 256 floats.
 template <int NT, int NCG, int DT, typename Wait>
 MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, Wait wait) {
   constexpr int NW = NT / 64;
@@ -587,7 +587,7 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, Wait w
   const int t0 = nt * DT;  // first 16-row tile
   const int KB2s = p.n_shared ? p.SI / 128 : 0;
   const int KB2 = p.I / 128;
-  constexpr int B = DT == 2 ? 2 : (NCG == 1 ? 4 : 2);  // MXFP4 slots in flight a wave
+  constexpr int B = 1;                                 // MXFP4 slots a unit
   constexpr int KC = 2;                                // k-blocks of a slot a pass
   const int G2 = (KB2 + 3) / 4;
   // weights only (static, or known since routing): the shared expert's first k-block
@@ -608,28 +608,100 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, Wait w
     }
   }
   const bool mx = p.fmt == MK2_FMT_MXFP4;
-  i32x8 apf[B][DT][KC];
-  int sapf[B][DT];
-  if (mx && D > 0) {
+  // the routed slots (MXFP4): a unit is a batch of B slots (wave + NW * (B * i + u))
+  // over KC k-blocks; units u + 1 and u + 2 (weights, mid rows, scales and route
+  // weights) are in flight while unit u's MFMAs run
+  struct Unit {
+    i32x8 a[B][DT][KC];
+    i32x8 bq[B][KC][NCG];
+    int sa[B][DT];
+    int sbq[B][KC][NCG];
+    float wr[B][NCG];
+  };
+  const int nkc = (KB2 + KC - 1) / KC;  // units a batch
+  const int nu = mx && D > wave ? (D - wave + NW * B - 1) / (NW * B) * nkc : 0;
+  auto load_w = [&](int u, Unit& x) {  // weights: known since the routing
+    const int j0 = wave + (u / nkc) * NW * B, kb0 = (u % nkc) * KC;
 #pragma unroll
-    for (int u = 0; u < B; ++u) {
-      const int e = act_ids[min(wave + u * NW, D - 1)];
+    for (int ub = 0; ub < B; ++ub) {
+      const int e = act_ids[min(j0 + ub * NW, D - 1)];  // past the list: a valid slot, unused
 #pragma unroll
       for (int c = 0; c < KC; ++c)
 #pragma unroll
         for (int d = 0; d < DT; ++d)
-          apf[u][d][c] = load_a_fp4(p.w2 + (((size_t)e * HT + t0 + d) * KB2 + min(c, KB2 - 1)) * 1024, lane);
+          x.a[ub][d][c] = load_a_fp4(p.w2 + (((size_t)e * HT + t0 + d) * KB2 + min(kb0 + c, KB2 - 1)) * 1024, lane);
 #pragma unroll
       for (int d = 0; d < DT; ++d)
-        sapf[u][d] = (int)*(const uint32_t*)(p.s2 + ((((size_t)e * HT + t0 + d) * G2) * 64 + lane) * 4);
+        x.sa[ub][d] = (int)*(const uint32_t*)(p.s2 + ((((size_t)e * HT + t0 + d) * G2 + kb0 / 4) * 64 + lane) * 4);
     }
-  }
-  wait();
-  f32x4 acc[DT][NCG];
+  };
+  auto load_m = [&](int u, Unit& x) {  // mid rows and route weights: after the wait
+    const int j0 = wave + (u / nkc) * NW * B, kb0 = (u % nkc) * KC;
+#pragma unroll
+    for (int ub = 0; ub < B; ++ub) {
+      const int j = min(j0 + ub * NW, D - 1);
+#pragma unroll
+      for (int c = 0; c < KC; ++c) {
+        const int kb = min(kb0 + c, KB2 - 1);
+#pragma unroll
+        for (int cg = 0; cg < NCG; ++cg) {
+          const int row = cg * 16 + c16;
+          x.bq[ub][c][cg] = load_b_fp8(p.mid_q + (size_t)j * p.M * p.I, row, p.M, p.I, kb * 128, g);
+          x.sbq[ub][c][cg] = row < p.M ? (int)ldp_u8(p.mid_s + ((size_t)j * p.M + row) * (p.I / 32) + kb * 4 + g) : 127;
+        }
+      }
+#pragma unroll
+      for (int cg = 0; cg < NCG; ++cg) x.wr[ub][cg] = ldp_f32(p.rw + j * 32 + cg * 16 + c16);
+    }
+  };
+  f32x4 acc[DT][NCG], tmp[B][DT][NCG];
 #pragma unroll
   for (int d = 0; d < DT; ++d)
 #pragma unroll
     for (int cg = 0; cg < NCG; ++cg) acc[d][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](int u, Unit& x) {
+    const int j0 = wave + (u / nkc) * NW * B, kb0 = (u % nkc) * KC;
+    if (kb0 == 0) {
+#pragma unroll
+      for (int ub = 0; ub < B; ++ub)
+#pragma unroll
+        for (int d = 0; d < DT; ++d)
+#pragma unroll
+          for (int cg = 0; cg < NCG; ++cg) tmp[ub][d][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int ub = 0; ub < B; ++ub) {
+      if (j0 + ub * NW >= D) break;
+#pragma unroll
+      for (int c = 0; c < KC; ++c) {
+        const int kb = kb0 + c;
+        if (kb >= KB2) break;
+#pragma unroll
+        for (int d = 0; d < DT; ++d) {
+          const int sak = x.sa[ub][d] >> (8 * (kb & 3));
+#pragma unroll
+          for (int cg = 0; cg < NCG; ++cg)
+            tmp[ub][d][cg] = mfma_fp4_fp8<0, 0>(x.a[ub][d][c], x.bq[ub][c][cg], tmp[ub][d][cg], sak, x.sbq[ub][c][cg]);
+        }
+      }
+    }
+    if (kb0 + KC >= KB2) {
+#pragma unroll
+      for (int ub = 0; ub < B; ++ub) {
+        if (j0 + ub * NW >= D) break;
+#pragma unroll
+        for (int cg = 0; cg < NCG; ++cg)
+#pragma unroll
+          for (int d = 0; d < DT; ++d) acc[d][cg] += tmp[ub][d][cg] * x.wr[ub][cg];
+      }
+    }
+  };
+  Unit x0, x1, x2;
+  if (nu > 0) load_w(0, x0);
+  if (nu > 1) load_w(1, x1);
+  wait();
+  if (nu > 0) load_m(0, x0);
+  if (nu > 1) load_m(1, x1);
   // the shared expert (FP8, bf16 mid): its k-blocks spread over the waves
   for (int kb = wave; kb < KB2s; kb += NW) {
     bf16x8 b[NCG][4];
@@ -659,69 +731,17 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, Wait w
     }
   }
   if (mx) {
-    for (int j0 = wave; j0 < D; j0 += NW * B) {
-      f32x4 tmp[B][DT][NCG];
-#pragma unroll
-      for (int u = 0; u < B; ++u)
-#pragma unroll
-        for (int d = 0; d < DT; ++d)
-#pragma unroll
-          for (int cg = 0; cg < NCG; ++cg) tmp[u][d][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
-      for (int kb0 = 0; kb0 < KB2; kb0 += KC) {
-        const bool pre = j0 == wave && kb0 == 0;  // the batch loaded before the wait
-        i32x8 a[B][DT][KC], bq[B][KC][NCG];
-        int sa[B][DT], sbq[B][KC][NCG];
-#pragma unroll
-        for (int u = 0; u < B; ++u) {
-          const int j = min(j0 + u * NW, D - 1);  // past the list: a valid slot, unused
-          const int e = act_ids[j];
-#pragma unroll
-          for (int c = 0; c < KC; ++c) {
-            const int kb = min(kb0 + c, KB2 - 1);
-#pragma unroll
-            for (int d = 0; d < DT; ++d)
-              a[u][d][c] = pre ? apf[u][d][c]
-                               : load_a_fp4(p.w2 + (((size_t)e * HT + t0 + d) * KB2 + kb) * 1024, lane);
-#pragma unroll
-            for (int cg = 0; cg < NCG; ++cg) {
-              const int row = cg * 16 + c16;
-              bq[u][c][cg] = load_b_fp8(p.mid_q + (size_t)j * p.M * p.I, row, p.M, p.I, kb * 128, g);
-              sbq[u][c][cg] = row < p.M ? (int)ldp_u8(p.mid_s + ((size_t)j * p.M + row) * (p.I / 32) + kb * 4 + g) : 127;
-            }
-          }
-#pragma unroll
-          for (int d = 0; d < DT; ++d)
-            sa[u][d] = pre ? sapf[u][d]
-                           : (int)*(const uint32_t*)(p.s2 + ((((size_t)e * HT + t0 + d) * G2 + kb0 / 4) * 64 + lane) * 4);
-        }
-#pragma unroll
-        for (int u = 0; u < B; ++u) {
-          if (j0 + u * NW >= D) break;
-#pragma unroll
-          for (int c = 0; c < KC; ++c) {
-            const int kb = kb0 + c;
-            if (kb >= KB2) break;
-#pragma unroll
-            for (int d = 0; d < DT; ++d) {
-              const int sak = sa[u][d] >> (8 * (kb & 3));
-#pragma unroll
-              for (int cg = 0; cg < NCG; ++cg)
-                tmp[u][d][cg] = mfma_fp4_fp8<0, 0>(a[u][d][c], bq[u][c][cg], tmp[u][d][cg], sak, sbq[u][c][cg]);
-            }
-          }
-        }
+    auto step = [&](int u, Unit& cur, Unit& nxt2) {
+      if (u + 2 < nu) {
+        load_w(u + 2, nxt2);
+        load_m(u + 2, nxt2);
       }
-#pragma unroll
-      for (int u = 0; u < B; ++u) {
-        const int j = j0 + u * NW;
-        if (j >= D) break;
-#pragma unroll
-        for (int cg = 0; cg < NCG; ++cg) {
-          const float w = ldp_f32(p.rw + j * 32 + cg * 16 + c16);
-#pragma unroll
-          for (int d = 0; d < DT; ++d) acc[d][cg] += tmp[u][d][cg] * w;
-        }
-      }
+      if (u < nu) compute(u, cur);
+    };
+    for (int u = 0; u < nu; u += 3) {
+      step(u, x0, x2);
+      step(u + 1, x1, x0);
+      step(u + 2, x2, x1);
     }
   } else if constexpr (DT == 1) {
     constexpr int KMAX = 8;  // FP8 experts: inter <= 1024

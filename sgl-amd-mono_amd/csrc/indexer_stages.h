@@ -144,31 +144,59 @@ MK2_DEV void idx_score(const IdxDev& p, int r, int chunk, IdxScoreLds& L) {
     }
   }
   float* srow = p.scores + (size_t)r * p.max_ctx;
-#pragma unroll
-  for (int j = 0; j < GPW; ++j) {
+  // software pipeline: group j + 1's keys widened and its MFMAs issued before group
+  // j's head sums, so that the matrix cores and the vector ALUs overlap
+  auto keys = [&](int j, bf16x8* kb) {
     const float sc = e8m0_to_f32(sw[j] >> (8 * g));
-    bf16x8 kb[4];
     kb[0] = e2m1x8_to_bf16(code[j].x, sc);
     kb[1] = e2m1x8_to_bf16(code[j].y, sc);
     kb[2] = e2m1x8_to_bf16(code[j].z, sc);
     kb[3] = e2m1x8_to_bf16(code[j].w, sc);
+  };
+  // all four head groups, absent ones with zero queries and weights: four
+  // independent MFMA chains
+  auto chain = [&](const bf16x8* kb, f32x4* acc) {
+#pragma unroll
+    for (int hg = 0; hg < 4; ++hg) acc[hg] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int hg = 0; hg < 4; ++hg) acc[hg] = mfma_bf16(qa[hg][q], kb[q], acc[hg]);
+  };
+  auto finish = [&](int j, const f32x4* acc) {
     float s = 0.f;
 #pragma unroll
-    for (int hg = 0; hg < 4; ++hg) {
-      if (hg >= nhg) break;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int hg = 0; hg < 4; ++hg)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) acc = mfma_bf16(qa[hg][q], kb[q], acc);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) s += fmaxf(acc[i], 0.f) * wt[hg][i];
-    }
-    s += __shfl_xor(s, 16, 64);
-    s += __shfl_xor(s, 32, 64);
+      for (int i = 0; i < 4; ++i) s += relu_bits(acc[hg][i]) * wt[hg][i];
+    s = add_xor32(add_xor16(s));  // the four lane groups' head sums
     const int loc = (gw0 + j) * 16 + c16;
     if (g == 0 && k_begin + loc < k_end) {
       L.sc[loc] = s;
       atomicAdd(&L.hist[radix_key(s) >> 20], 1);
     }
+  };
+  static_assert(GPW % 2 == 0, "groups go in pairs");
+  f32x4 acc0[4], acc1[4];
+  {
+    bf16x8 kb[4];
+    keys(0, kb);
+    chain(kb, acc0);
+  }
+#pragma unroll
+  for (int j = 0; j < GPW; j += 2) {
+    {
+      bf16x8 kb[4];
+      keys(j + 1, kb);
+      chain(kb, acc1);
+    }
+    finish(j, acc0);
+    if (j + 2 < GPW) {
+      bf16x8 kb[4];
+      keys(j + 2, kb);
+      chain(kb, acc0);
+    }
+    finish(j + 1, acc1);
   }
   __syncthreads();
   for (int i = 4 * threadIdx.x; i < k_end - k_begin; i += 4 * NT) {

@@ -179,6 +179,19 @@ MK2_DEV float wave_max(float v) {
 }
 
 // order-preserving u32 of f32 bits: larger keys rank first
+// max(x, 0) as one integer max on the bits (a negative float is a negative int); no
+// NaN quieting
+MK2_DEV float relu_bits(float x) { return __int_as_float(max(__float_as_int(x), 0)); }
+// v + (v of the lane 16 apart, xor) and v + (v of the lane 32 apart, xor), by the
+// row-swapping permutes
+MK2_DEV float add_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+MK2_DEV float add_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 MK2_DEV uint32_t radix_key(float f) {
   uint32_t b = __float_as_uint(f);
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);

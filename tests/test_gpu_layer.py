@@ -81,3 +81,35 @@ def test_persistent_layer_repeats_and_matches_staged():
     for o in outs:
         assert torch.equal(o, outs[0])
     assert torch.equal(outs[0], ref)
+
+
+def test_persistent_layer_one_workspace_new_inputs():
+    """One persistent op (one workspace) over alternating decode inputs (queries, key
+    and latent caches, residual rows): every launch gives the stage-by-stage path's
+    bits on the same inputs, so nothing a previous launch left in the workspace or in
+    the caches is read back."""
+    from sgl_amd_mono.k2 import config as C
+    from sgl_amd_mono.k2 import synth
+    from sgl_amd_mono.k2.ops import LayerOp
+
+    dev = _dev()
+    cfg = C.C5_LAYER
+    A = synth.make_layer(cfg, 8, 777, dev)
+    B = synth.make_layer(cfg, 8, 778, dev)
+    step = lambda L: [L.idx.q, L.idx.w, L.idx.cache, L.mla.q, L.mla.kv, L.mla.kv_scale, L.h]  # noqa: E731
+    saved = [t.clone() for t in step(A)]
+    p_op = LayerOp(cfg, A, 8, device=dev)
+    s_op = LayerOp(cfg, A, 8, device=dev, staged=True)
+    status = torch.full((1,), -1, dtype=torch.int32, device=dev)
+    outs = []
+    for src in (saved, step(B), saved, step(B)):
+        for dst, t in zip(step(A), src):
+            dst.copy_(t)
+        o = p_op(status=status).clone()
+        ref = s_op().clone()
+        torch.cuda.synchronize()
+        assert int(status.item()) == 0
+        assert torch.equal(o, ref)
+        outs.append(o)
+    assert not torch.equal(outs[0], outs[1])
+    assert torch.equal(outs[0], outs[2]) and torch.equal(outs[1], outs[3])

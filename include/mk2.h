@@ -195,7 +195,7 @@ typedef struct mk2_layer_args {
   int spin_limit;           /* persistent: polls a dependency wait may take before the
                                launch gives up (0: default, about a second) */
   int32_t* status;          /* optional device word: 0 ok, 1 a wait gave up */
-  uint64_t* timeline;       /* optional [grid][34] stage stamps of the persistent launch
+  uint64_t* timeline;       /* optional [grid][31] stage stamps of the persistent launch
                                (100 MHz device clock): per stage enter, input ready, leave */
 } mk2_layer_args;
 

@@ -1,6 +1,6 @@
 // The K2 layer as ONE persistent launch: one 512-thread workgroup per CU walks the
 // stage list -- index scores (+ key histograms), top-k slices, top-k select,
-// sparse-MLA splits, merge, W_UV, W_o + residual (+ the RMSNorm's partial sums),
+// sparse-MLA splits, merge + W_UV, W_o + residual (+ the RMSNorm's partial sums),
 // router (+ RMSNorm + activation quant of its slice), top-k routing, up/gate +
 // SwiGLU, down + residual -- taking task t of a
 // stage on workgroup (base + t) mod grid, where each stage's base continues from
@@ -37,16 +37,15 @@ enum : int {
   SY_SLICE = 32,   // [32] top-k slices done, per row
   SY_TOPK = 64,    // [32] top-k done, per row
   SY_SPLIT = 96,   // [32] attention splits done, per row
-  SY_MERGE = 128,  // [16] merged rows, per head
-  SY_ROUTE = 144,
+  SY_ROUTE = 128,
   SY_ROUTER_LAST,  // router sub-counters completed (the last runs the routing)
   SY_DONE,         // workgroups finished (the last one resets)
   SY_ERR,          // sticky: a wait ran out of its spin limit
-  SY_UV = 160,     // [K2_LANES] sub-counters each
+  SY_UV = 144,     // [K2_LANES] sub-counters each: merged + W_UV (row, head) tasks
   SY_OPROJ = SY_UV + K2_LANES,
   SY_ROUTER = SY_OPROJ + K2_LANES,
   SY_UP = SY_ROUTER + K2_LANES,
-  SY_LINES = SY_UP + K2_LANES  // 224 lines = 28 KiB
+  SY_LINES = SY_UP + K2_LANES  // 208 lines = 26 KiB
 };
 
 struct K2Dev {
@@ -61,7 +60,7 @@ struct K2Dev {
 };
 
 // timeline: per stage s, stamps 3s (enter), 3s+1 (first input ready), 3s+2 (leave)
-constexpr int K2_STAGES = 11, K2_STAMPS = 3 * K2_STAGES + 1;
+constexpr int K2_STAGES = 10, K2_STAMPS = 3 * K2_STAGES + 1;
 
 MK2_DEV void k2_stamp(const K2Dev& p, int i) {
   if (p.timeline && threadIdx.x == 0) p.timeline[(size_t)blockIdx.x * K2_STAMPS + i] = __builtin_amdgcn_s_memrealtime();
@@ -71,7 +70,7 @@ union K2Lds {
   IdxScoreLds score;
   TopkLds topk;
   MlaSplitLds split;
-  float merge[2 * 1024 + 8];
+  MlaMergeLds merge;
   struct {
     float red[(K2_NT / 64) * 8 * 64 * 4];  // NW * 2 * CT * NCG * 256, CT * NCG <= 4
     float midf[32 * 65];
@@ -213,26 +212,14 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
   }
   K2_NEXT(R * ns);
   k2_stamp(p, 3 * st++ + 2);
-  // ---- merge of the splits, per (row, head)
+  // ---- merge of the splits + W_UV, per (row, head)
   k2_stamp(p, 3 * st);
   K2_TASKS(t, R * MLA_HEADS) {
     const int r = t / MLA_HEADS, h = t % MLA_HEADS;
-    k2_wait(p, seen, SY_SPLIT + r, ns, t < G ? 3 * st + 1 : -1);
-    mla_merge<K2_NT>(p.mla, r, h, S.merge);
-    k2_signal(p, SY_MERGE + h);
-  }
-  K2_NEXT(R * MLA_HEADS);
-  k2_stamp(p, 3 * st++ + 2);
-  // ---- W_UV, per (head, 16 v rows)
-  k2_stamp(p, 3 * st);
-  const int vtn = p.mla.v_dim / 16;
-  K2_TASKS(t, MLA_HEADS * vtn) {
-    const int h = t / vtn;
-    mla_uv<K2_NT, NCG>(p.mla, h, t % vtn, S.red,
-                       [&] { k2_wait(p, seen, SY_MERGE + h, R, t < G ? 3 * st + 1 : -1); });
+    mla_merge_uv<K2_NT>(p.mla, r, h, S.merge, [&] { k2_wait(p, seen, SY_SPLIT + r, ns, t < G ? 3 * st + 1 : -1); });
     k2_signal(p, SY_UV, t, K2_LANES);
   }
-  K2_NEXT(MLA_HEADS * vtn);
+  K2_NEXT(R * MLA_HEADS);
   k2_stamp(p, 3 * st++ + 2);
   // ---- W_o + residual, per 16 hidden rows: tasks t and t + G together (their weights
   // all in flight before the wait)
@@ -241,7 +228,7 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
   for (int t = (b - base % G + G) % G; t < ht; t += 2 * G) {
     const int t1 = t + G < ht ? t + G : -1;
     mla_oproj<K2_NT, NCG, 2>(p.mla, t, t1, S.up.red,
-                             [&] { k2_wait(p, seen, SY_UV, MLA_HEADS * vtn, t < G ? 3 * st + 1 : -1, K2_LANES); });
+                             [&] { k2_wait(p, seen, SY_UV, R * MLA_HEADS, t < G ? 3 * st + 1 : -1, K2_LANES); });
     k2_signal(p, SY_OPROJ, t, K2_LANES, t1 >= 0 ? 2 : 1);
   }
   K2_NEXT(ht);

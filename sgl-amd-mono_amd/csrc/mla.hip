@@ -1,5 +1,5 @@
-// Standalone sparse-MLA launch (16 heads, 512 + 64 latent dims): split attention, merge,
-// W_UV, W_o + residual.
+// Standalone sparse-MLA launch (16 heads, 512 + 64 latent dims): split attention, merge
+// + W_UV, W_o + residual.
 #include "mk2_host.h"
 #include "mla_stages.h"
 
@@ -9,19 +9,17 @@ __global__ __launch_bounds__(MLA_NT) void k_mla_split(MlaDev p) {
   __shared__ MlaSplitLds L;
   mla_split<MLA_NT>(p, blockIdx.y, blockIdx.x, L);
 }
-__global__ __launch_bounds__(MLA_NT) void k_mla_merge(MlaDev p) {
-  extern __shared__ float lds[];
-  mla_merge<MLA_NT>(p, blockIdx.y, blockIdx.x, lds);
+// merge + W_UV and W_o run 512 threads, as in the persistent layer kernel: the same
+// waves split the same sums, so both paths give the same bits
+constexpr int MLA_NT2 = 512;
+__global__ __launch_bounds__(MLA_NT2) void k_mla_merge_uv(MlaDev p) {
+  __shared__ MlaMergeLds L;
+  mla_merge_uv<MLA_NT2>(p, blockIdx.y, blockIdx.x, L);
 }
 template <int NCG>
-__global__ __launch_bounds__(MLA_NT) void k_mla_uv(MlaDev p) {
-  __shared__ float red[4 * NCG * 64 * 4];
-  mla_uv<MLA_NT, NCG>(p, blockIdx.y, blockIdx.x, red);
-}
-template <int NCG>
-__global__ __launch_bounds__(MLA_NT) void k_mla_oproj(MlaDev p) {
-  __shared__ float red[4 * NCG * 64 * 4];
-  mla_oproj<MLA_NT, NCG>(p, blockIdx.x, -1, red);
+__global__ __launch_bounds__(MLA_NT2) void k_mla_oproj(MlaDev p) {
+  __shared__ float red[(MLA_NT2 / 64) * NCG * 64 * 4];
+  mla_oproj<MLA_NT2, NCG>(p, blockIdx.x, -1, red);
 }
 
 int mla_check_shape(const mk2_mla_shape* s) {
@@ -43,9 +41,8 @@ size_t mla_carve(const mk2_mla_shape* s, void* base, MlaDev* d) {
   const int ns = s->topk / MLA_SPLIT;
   float* po = c.take<float>((size_t)s->rows * ns * MLA_HEADS * MLA_LAT);
   float* pml = c.take<float>((size_t)s->rows * ns * MLA_HEADS * 2);
-  bf16_t* ol = c.take<bf16_t>((size_t)s->rows * MLA_HEADS * MLA_LAT);
   bf16_t* o = c.take<bf16_t>((size_t)s->rows * MLA_HEADS * s->v_dim);
-  if (d) { d->part_o = po; d->part_ml = pml; d->o_lat = ol; d->o = o; d->nsplit = ns; }
+  if (d) { d->part_o = po; d->part_ml = pml; d->o = o; d->nsplit = ns; }
   return c.bytes();
 }
 
@@ -67,14 +64,9 @@ int mla_fill(const mk2_mla_args* a, MlaDev* d) {
 
 void mla_enqueue(const MlaDev& d, hipStream_t st) {
   k_mla_split<<<dim3(d.nsplit, d.rows), MLA_NT, 0, st>>>(d);
-  k_mla_merge<<<dim3(MLA_HEADS, d.rows), MLA_NT, (2 * d.nsplit + 8) * sizeof(float), st>>>(d);
-  if (d.rows > 16) {
-    k_mla_uv<2><<<dim3(d.v_dim / 16, MLA_HEADS), MLA_NT, 0, st>>>(d);
-    k_mla_oproj<2><<<d.hidden / 16, MLA_NT, 0, st>>>(d);
-  } else {
-    k_mla_uv<1><<<dim3(d.v_dim / 16, MLA_HEADS), MLA_NT, 0, st>>>(d);
-    k_mla_oproj<1><<<d.hidden / 16, MLA_NT, 0, st>>>(d);
-  }
+  k_mla_merge_uv<<<dim3(MLA_HEADS, d.rows), MLA_NT2, 0, st>>>(d);
+  if (d.rows > 16) k_mla_oproj<2><<<d.hidden / 16, MLA_NT2, 0, st>>>(d);
+  else k_mla_oproj<1><<<d.hidden / 16, MLA_NT2, 0, st>>>(d);
 }
 
 }  // namespace mk2

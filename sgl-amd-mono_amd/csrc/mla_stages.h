@@ -7,8 +7,8 @@
 // read).  S = q . k on bf16 MFMA (E4M3 widens exactly), x (scale_k * sm_scale); a
 // split-local softmax per head; P' = p * scale_k rounded to bf16; O = P' V on bf16
 // MFMA.  The split writes O (unnormalized), its max m and sum l.
-// merge task (row r, head h): exact combination of the splits -> o_lat (bf16).
-// uv task (head h, 16 v rows): o = W_UV[h] o_lat on bf16 MFMA (rows as columns).
+// merge task (row r, head h): exact combination of the splits -> o_lat (bf16), then
+// o[r][h] = W_UV[h] o_lat on bf16 MFMA.
 // oproj task (16 hidden rows): a = bf16(h + W_o o) on bf16 MFMA.
 #pragma once
 #include "mk2_device.h"
@@ -44,7 +44,6 @@ struct MlaDev {
   // workspace
   float* part_o;         // [rows][nsplit][16][512]
   float* part_ml;        // [rows][nsplit][16][2]
-  bf16_t* o_lat;         // [rows][16][512]
   float* o_lat_f32;      // optional [rows][16][512]
   bf16_t* o;             // [rows][16 * v_dim]
   float* ssp;            // optional [hidden/16][rows]: sums of squares of out over 16 columns
@@ -216,15 +215,34 @@ MK2_DEV void mla_split(const MlaDev& p, int r, int s, MlaSplitLds& L) {
   __syncthreads();
 }
 
-// ---------------------------------------------------------------- stage: merge
-// lds: >= 2 * nsplit + 8 floats; a thread takes 512 / NT latent dims
-template <int NT>
-MK2_DEV void mla_merge(const MlaDev& p, int r, int h, float* lds) {
-  constexpr int DPT = MLA_LAT / NT;
-  const int tid = threadIdx.x;
-  const int ns = p.nsplit;
-  float* wgt = lds;          // [ns] exp(m_s - M)
-  float* lsum = lds + ns;    // [ns] l_s
+// ---------------------------------------------------------------- stage: merge + W_UV
+// Task (row r, head h): the exact combination of the row's splits for head h ->
+// o_lat (rounded to bf16, in LDS), then o[r][h] = W_UV[h] o_lat on bf16 MFMA: wave w
+// takes the 16-row W_UV tiles w, w + NW, ... over all 512 latent dims, with o_lat as
+// the B operand in every column (column 0 is kept).  The wave's first W_UV tile is
+// static and loaded before `wait` (the splits' dependency).
+struct MlaMergeLds {
+  float w[2 * 1024 + 8];  // per split: exp(m_s - M), then l_s (nsplit <= 1024)
+  bf16_t ol[MLA_LAT];
+};
+
+template <int NT, typename Wait = NoWait>
+MK2_DEV void mla_merge_uv(const MlaDev& p, int r, int h, MlaMergeLds& L, Wait wait = Wait()) {
+  constexpr int NW = NT / 64, DPT = MLA_LAT / NT;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, c16 = lane & 15;
+  const int ns = p.nsplit, nvt = p.v_dim / 16;
+  auto load_a = [&](int vt, bf16x8* a) {  // W_UV[h] rows vt*16 + c16, dims 128 kb + 32 g + 8 q
+    const bf16_t* wrow = p.w_uv + ((size_t)h * p.v_dim + vt * 16 + c16) * MLA_LAT + 32 * g;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) a[kb * 4 + q] = __builtin_bit_cast(bf16x8, *(const uint4*)(wrow + kb * 128 + 8 * q));
+  };
+  bf16x8 a[16];
+  if (wave < nvt) load_a(wave, a);
+  wait();
+  float* wgt = L.w;        // [ns] exp(m_s - M)
+  float* lsum = L.w + ns;  // [ns] l_s
   const float* ml = p.part_ml + ((size_t)r * ns * MLA_HEADS + h) * 2;
   for (int s = tid; s < ns; s += NT) {
     const uint2 v = ldp_8(ml + (size_t)s * MLA_HEADS * 2);
@@ -264,56 +282,22 @@ MK2_DEV void mla_merge(const MlaDev& p, int r, int h, float* lds) {
 #pragma unroll
   for (int d = 0; d < DPT; ++d) {
     o[d] *= inv;
-    st_dev_u16(p.o_lat + at + d, f32_to_bf16(o[d]));
+    L.ol[DPT * tid + d] = f32_to_bf16(o[d]);
     if (p.o_lat_f32) p.o_lat_f32[at + d] = o[d];
   }
   __syncthreads();
-}
-
-// ---------------------------------------------------------------- stage: W_UV
-// Task (head h, 16 v rows vt): W_UV rows are static, so their loads are issued before
-// `wait` (the merged rows' dependency).
-template <int NT, int NCG, typename Wait = NoWait>
-MK2_DEV void mla_uv(const MlaDev& p, int h, int vt, float* red, Wait wait = Wait()) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, c16 = lane & 15;
-  const int kb = wave & 3;  // waves 0-3: 128 of the 512 latent dims each (4-7 idle)
-  bf16x8 a[4];
-  if (wave < 4) {
-    const bf16_t* wrow = p.w_uv + ((size_t)h * p.v_dim + vt * 16 + c16) * MLA_LAT + kb * 128 + 32 * g;
+  for (int vt = wave; vt < nvt; vt += NW) {
+    if (vt != wave) load_a(vt, a);
+    f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int q = 0; q < 4; ++q) a[q] = __builtin_bit_cast(bf16x8, *(const uint4*)(wrow + 8 * q));
-  }
-  wait();
-  f32x4 acc[NCG];
-  if (wave < 4) {
+    for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-    for (int cg = 0; cg < NCG; ++cg) {
-      const int row = cg * 16 + c16;
-      bf16x8 b[4];
-      if (row < p.rows) {
-        const bf16_t* src = p.o_lat + ((size_t)row * MLA_HEADS + h) * MLA_LAT + kb * 128 + 32 * g;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) b[q] = __builtin_bit_cast(bf16x8, ldp_16(src + 8 * q));
-      } else {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) b[q] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
-      }
-      f32x4 c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int q = 0; q < 4; ++q) c = mfma_bf16(a[q], b[q], c);
-      acc[cg] = c;
+      for (int q = 0; q < 4; ++q)
+        c = mfma_bf16(a[kb * 4 + q], *(const bf16x8*)(L.ol + kb * 128 + 32 * g + 8 * q), c);
+    if (c16 == 0) {  // column 0: v rows 4 g + i
+      bf16_t* dst = p.o + (size_t)r * (MLA_HEADS * p.v_dim) + h * p.v_dim + vt * 16 + 4 * g;
+      st_dev_8(dst, make_uint2(pack_bf16x2(c[0], c[1]), pack_bf16x2(c[2], c[3])));
     }
-#pragma unroll
-    for (int cg = 0; cg < NCG; ++cg) *(f32x4*)(red + ((wave * NCG + cg) * 64 + lane) * 4) = acc[cg];
-  }
-  __syncthreads();
-  for (int idx = threadIdx.x; idx < 16 * p.rows; idx += NT) {
-    const int n16 = idx & 15, row = idx >> 4, cg = row >> 4, s16 = row & 15;
-    const int l = (n16 >> 2) * 16 + s16, i = n16 & 3;
-    float v = 0.f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) v += red[((w * NCG + cg) * 64 + l) * 4 + i];
-    st_dev_u16(p.o + (size_t)row * (MLA_HEADS * p.v_dim) + h * p.v_dim + vt * 16 + n16, f32_to_bf16(v));
   }
   __syncthreads();
 }

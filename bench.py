@@ -253,7 +253,7 @@ def main():
         "pct_peak_hbm": round(100.0 * gbs / PEAK_HBM_GBS, 2),
         "roofline": {
             "bound": "hbm",
-            "kernel": "k2 layer: " + ("11 stage kernels a layer" if args.staged else
+            "kernel": "k2 layer: " + ("12 stage kernels a layer" if args.staged else
                                       "one persistent launch a layer (k_k2_layer)"),
             "achieved": round(gbs, 1),
             "peak": PEAK_HBM_GBS,

@@ -137,14 +137,22 @@ MK2_DEV void k2_wait(const K2Dev& p, int* seen, int line, int target, int stamp 
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
     const int* err = k2_ctr(p, SY_ERR);
-    int n = 0;
+    const int* ctr = k2_ctr(p, line + min(lane, lanes - 1));
+    // two polls in flight: the next is issued before the last one's count is read
+    auto poll = [&]() { return __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+    auto count = [&](int c) {  // the sub-counters' sum (lanes < lanes <= 16: one DPP row)
+      return __builtin_amdgcn_readfirstlane(row16_sum_i32(lane < lanes ? c : 0));
+    };
+    int n = 0, c0 = poll();
     while (true) {
-      int c = lane < lanes ? __hip_atomic_load(k2_ctr(p, line + lane), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
-#pragma unroll
-      for (int o = 8; o > 0; o >>= 1) c += __shfl_xor(c, o, 64);  // lanes <= 16
-      v = __shfl(c, 0, 64);
+      const int c1 = poll();
+      v = count(c0);
       if (v >= target) break;
-      if ((++n & 31) == 0 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
+      c0 = poll();
+      v = count(c1);
+      if (v >= target) break;
+      n += 2;
+      if ((n & 31) == 0 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
       if (n > p.spin_limit) {
         if (lane == 0) atomicOr(k2_ctr(p, SY_ERR), 1);
         break;

@@ -154,6 +154,13 @@ template <int CTRL, int ROWS>
 MK2_DEV int dpp_i32(int v) {  // lanes without a source (or outside ROWS) read 0
   return __builtin_amdgcn_update_dpp(0, v, CTRL, ROWS, 0xF, false);
 }
+// the sum over a 16-lane row, in every lane of the row
+MK2_DEV int row16_sum_i32(int v) {
+  v += dpp_i32<DPP_XOR1, 0xF>(v);
+  v += dpp_i32<DPP_XOR2, 0xF>(v);
+  v += dpp_i32<DPP_HALF_MIRROR, 0xF>(v);
+  return v + dpp_i32<DPP_MIRROR, 0xF>(v);
+}
 // inclusive scan over the wave: shifts within each 16-lane row, then each row's total
 // carried up (row_bcast:15 into rows 1 and 3, row_bcast:31 into rows 2 and 3)
 MK2_DEV int wave_incl_scan(int v) {

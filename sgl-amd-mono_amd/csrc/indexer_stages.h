@@ -70,8 +70,8 @@ struct IdxScoreLds {
 // ------------------------------------------------------------- stage: scores
 // One task: IDX_CHUNK positions of row r.  The row's queries and head weights go to
 // LDS first (coalesced, once a workgroup) with the chunk's page ids; then each wave
-// issues the loads of all its 16 groups of 16 keys, takes its A operands from LDS,
-// and computes group by group as the keys arrive.  The loads are unconditional
+// keeps a window of its 16 groups of 16 keys in flight, takes its A operands from
+// LDS, and computes group by group as the keys arrive.  The loads are unconditional
 // (groups past the row's end read page id 0, and their results are dropped) and the
 // scores wait in LDS until the loop is done: a store or a branch between the loads
 // would make every group wait for all memory traffic.
@@ -113,14 +113,19 @@ MK2_DEV void idx_score(const IdxDev& p, int r, int chunk, IdxScoreLds& L) {
   const int gw0 = wave * GPW;  // this wave's first group
   uint4 code[GPW];
   uint32_t sw[GPW];
-#pragma unroll
-  for (int j = 0; j < GPW; ++j) {
+  // a rolling window of KWIN key groups in flight: group j + KWIN - 1 is issued as
+  // group j is widened (a full window of 16 a wave, 160 KiB a CU at once, delays every
+  // CU's first groups behind the whole chip's requests)
+  constexpr int KWIN = 4;
+  auto issue = [&](int j) {
     const int key0 = k_begin + (gw0 + j) * 16;
     const uint8_t* pg = p.cache + (size_t)lds_pages[(key0 - k_begin) >> 6] * IDX_PAGE_BYTES;
     const int tok = (key0 & 63) + c16;
     code[j] = *(const uint4*)(pg + tok * 64 + 16 * g);
     sw[j] = *(const uint32_t*)(pg + 4096 + tok * 4);
-  }
+  };
+#pragma unroll
+  for (int j = 0; j < KWIN; ++j) issue(j);
   const int nhg = p.heads >> 4;
   // A operands: q of head 16*hg + c16, dims 32g + 8s .. +7; head weights of rows 4g+i
   bf16x8 qa[4][4];
@@ -147,6 +152,7 @@ MK2_DEV void idx_score(const IdxDev& p, int r, int chunk, IdxScoreLds& L) {
   // software pipeline: group j + 1's keys widened and its MFMAs issued before group
   // j's head sums, so that the matrix cores and the vector ALUs overlap
   auto keys = [&](int j, bf16x8* kb) {
+    if (j >= 1 && j + KWIN - 1 < GPW) issue(j + KWIN - 1);
     const float sc = e8m0_to_f32(sw[j] >> (8 * g));
     kb[0] = e2m1x8_to_bf16(code[j].x, sc);
     kb[1] = e2m1x8_to_bf16(code[j].y, sc);

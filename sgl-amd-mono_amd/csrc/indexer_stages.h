@@ -296,8 +296,8 @@ MK2_DEV int wave_find_bin(const int* hist, int nbins, int need, int* above) {
       a += h;
     }
   }
-  *above = __shfl(ab, L, 64);
-  return __shfl(bin, L, 64);
+  *above = __builtin_amdgcn_readlane(ab, L);  // L is the same in every lane
+  return __builtin_amdgcn_readlane(bin, L);
 }
 
 // One wave: the 12-bit bin b1 of row r's k-th key from the two-level histogram in
@@ -328,14 +328,14 @@ MK2_DEV int wave_threshold(const IdxDev& p, int r, int k, int* above) {
       a += c[i];
     }
   }
-  cb = __shfl(cb, L, 64);
-  ca = __shfl(ca, L, 64);
+  cb = __builtin_amdgcn_readlane(cb, L);
+  ca = __builtin_amdgcn_readlane(ca, L);
   const int f = lane < 16 ? ld_dev_i32(fh + 16 * cb + 15 - lane) : 0;
   inc = ca + wave_incl_scan(f);
   excl = inc - f;
   hit = __ballot(lane < 16 && excl < k && inc >= k);
   L = hit ? __ffsll((long long)hit) - 1 : 15;
-  *above = __shfl(excl, L, 64);
+  *above = __builtin_amdgcn_readlane(excl, L);
   return 16 * cb + 15 - L;
 }
 
@@ -577,8 +577,7 @@ MK2_DEV bool idx_slice(const IdxDev& p, int r, int chunk, TopkLds& S, int spin, 
       }
     }
     int pre = lane < chunk ? (v & 0x7FFF) : 0;  // a count not yet published reads 0
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) pre += __shfl_xor(pre, o, 64);
+    pre = __builtin_amdgcn_readlane(wave_incl_scan(pre), 63);
     if (tid == 0) S.res[2] = pre;
   }
   __syncthreads();

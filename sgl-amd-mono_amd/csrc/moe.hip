@@ -8,7 +8,7 @@ namespace mk2 {
 
 constexpr int MOE_NT = 512;
 
-__global__ __launch_bounds__(256) void k_moe_sumsq(MoeDev p) { moe_sumsq<256>(p, blockIdx.x); }
+__global__ __launch_bounds__(128) void k_moe_sumsq(MoeDev p) { moe_sumsq<128>(p, blockIdx.y, blockIdx.x); }
 
 template <int NCG>
 __global__ __launch_bounds__(ROUTER_NT) void k_moe_router(MoeDev p) {
@@ -121,7 +121,7 @@ int moe_fill(const mk2_moe_args* a, MoeDev* d) {
 
 int moe_enqueue(const MoeDev& d, hipStream_t st) {
   const int ncg = d.M > 16 ? 2 : 1;
-  if (d.norm) k_moe_sumsq<<<d.M, 256, 0, st>>>(d);
+  if (d.norm) k_moe_sumsq<<<dim3(d.H / 512, d.M), 128, 0, st>>>(d);  // H: a multiple of 512
   if (ncg == 1) k_moe_router<1><<<dim3(d.E / 16, d.KC), ROUTER_NT, 0, st>>>(d);
   else k_moe_router<2><<<dim3(d.E / 16, d.KC), ROUTER_NT, 0, st>>>(d);
   k_moe_route<<<1, 512, 0, st>>>(d);

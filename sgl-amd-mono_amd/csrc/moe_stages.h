@@ -63,15 +63,20 @@ MK2_DEV float block_sum(float v, float* lds) {
 }
 
 // ------------------------------------------------------- stage: sums of squares
-// Row r: ssp[t][r] = sum of x^2 over columns 16t .. 16t+15, reduced across one DPP row
-// of 16 lanes.  W_o's epilogue produces the same sums of its output tiles with the
-// same reduction, so either producer gives the same bits.  NT is a multiple of 64 and
-// H of NT, so every pass runs whole 16-lane rows.
+// Row r, columns blk * 4 NT ..: ssp[t][r] = sum of x^2 over columns 16t .. 16t+15,
+// reduced across one DPP row of 16 lanes.  W_o's epilogue produces the same sums of
+// its output tiles with the same reduction, so either producer gives the same bits.
+// NT is a multiple of 64 and H of 4 NT, so every pass runs whole 16-lane rows.
 template <int NT>
-MK2_DEV void moe_sumsq(const MoeDev& p, int r) {
-  const bf16_t* xr = p.x + (size_t)r * p.H;
-  for (int c = threadIdx.x; c < p.H; c += NT) {
-    const float v = bf16_to_f32(ldp_u16(xr + c));
+MK2_DEV void moe_sumsq(const MoeDev& p, int r, int blk) {  // columns blk * 4 NT .. + 4 NT - 1
+  const bf16_t* xr = p.x + (size_t)r * p.H + blk * 4 * NT;
+  uint32_t x[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) x[i] = ldp_u16(xr + threadIdx.x + i * NT);  // all in flight
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = blk * 4 * NT + threadIdx.x + i * NT;
+    const float v = bf16_to_f32((bf16_t)x[i]);
     const float ss = row16_sum(v * v);
     if ((c & 15) == 0) st_dev_f32(p.ssp + (size_t)(c >> 4) * p.M + r, ss);
   }
@@ -528,17 +533,15 @@ MK2_DEV void upgate_chunk(const MoeDev& p, bool shared, int j, int e, int c, flo
   }
   __syncthreads();
   if (!shared && p.fmt == MK2_FMT_MXFP4) {
-    // MXFP8 per 32 values of a row: 32 lanes a block, amax by shuffles, 4 codes a store
+    // MXFP8 per 32 values of a row: 32 lanes (two DPP rows) a block, amax by DPP and a
+    // row swap, 4 codes a store (DPP row shifts)
     for (int idx = threadIdx.x; idx < R * p.M; idx += NT) {
       const int n = idx % R, s = idx / R;
       const float v = midf[s * (R + 1) + n];
-      float amax = fabsf(v);
-#pragma unroll
-      for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+      const float amax = max_xor16(row16_max(fabsf(v)));
       const uint32_t code = mxfp8_scale_code(amax);
       const uint32_t q = f32_to_e4m3(v * e8m0_inverse(code));
-      const uint32_t w = q | (__shfl_down(q, 1, 64) << 8) | (__shfl_down(q, 2, 64) << 16) |
-                         (__shfl_down(q, 3, 64) << 24);
+      const uint32_t w = q | (dpp_shl<1>(q) << 8) | (dpp_shl<2>(q) << 16) | (dpp_shl<3>(q) << 24);
       if ((n & 3) == 0) st_dev_u32(p.mid_q + ((size_t)j * p.M + s) * p.I + c * R + n, w);
       if ((n & 31) == 0) st_dev_u8(p.mid_s + ((size_t)j * p.M + s) * (p.I / 32) + c * (R / 32) + (n >> 5), code);
     }

@@ -251,7 +251,8 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
     if (k2_signal_last(p, SY_ROUTER, SY_ROUTER_LAST, t, nrt, &last_flag)) {
       k2_stamp(p, 3 * (st + 1));
       k2_stamp(p, 3 * (st + 1) + 1);
-      moe_route<K2_NT>(p.moe, S.route);
+      // SY_ROUTE: 1 once the distinct-expert list is out (up/gate), 2 with the table (down)
+      moe_route<K2_NT>(p.moe, S.route, [&] { k2_signal(p, SY_ROUTE); });
       k2_signal(p, SY_ROUTE);
       k2_stamp(p, 3 * (st + 1) + 2);
     }
@@ -278,7 +279,7 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
   // ---- down + route weighting + residual, per 16 hidden rows
   k2_stamp(p, 3 * st);
   K2_TASKS(t, p.moe.H / (16 * p.moe.DT)) {
-    k2_wait(p, seen, SY_ROUTE, 1);  // the routing: known long before the mid rows
+    k2_wait(p, seen, SY_ROUTE, 2);  // the routing and its table: known long before the mid rows
     moe_down<K2_NT, NCG>(p.moe, t, S.down.red, S.down.act,
                          [&] { k2_wait(p, seen, SY_UP, up_total, t < G ? 3 * st + 1 : -1, K2_LANES); });
   }

@@ -274,7 +274,8 @@ MK2_DEV void moe_router(const MoeDev& p, int nt, int kc, RouterLds& L, Wait wait
 // lane, whose experts all lie below a higher lane's; the winning lane moves its head
 // on.  Round k's pick lands in lane k, so the picks come out ranked.  Then the
 // distinct-expert list (ascending) from the expert flags, and the dense route-weight
-// table rw [slot][row].
+// table rw [slot][row].  `act_published` runs (on the whole workgroup) once the list
+// is stored, before the table is built.
 struct RouteLds {
   int flag[256];     // expert: 1 if picked, then its slot (-1: none)
   int ids[32 * 8];   // [M][topk]
@@ -297,8 +298,8 @@ MK2_DEV uint32_t wave_max_u32(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
-template <int NT>
-MK2_DEV void moe_route(const MoeDev& p, RouteLds& L) {
+template <int NT, typename Published = NoWait>
+MK2_DEV void moe_route(const MoeDev& p, RouteLds& L, Published act_published = Published()) {
   constexpr int NW = NT / 64;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int el = min(lane, p.E / 4 - 1);  // lanes past E/4 repeat the last group, unused
@@ -406,6 +407,7 @@ MK2_DEV void moe_route(const MoeDev& p, RouteLds& L) {
     }
   }
   __syncthreads();
+  act_published();  // the up/gate stage needs only the list; the table follows
   const int total = L.tot;
   for (int idx = tid; idx < p.M * p.topk; idx += NT) L.rw[L.flag[L.ids[idx]] * 32 + idx / p.topk] = L.w[idx];
   __syncthreads();

@@ -78,6 +78,7 @@ union K2Lds {
   struct {
     float red[(K2_NT / 64) * 2 * 64 * 4];
     int act[256];
+    float xres[16 * 2 * 32];
   } down;
   RouterLds router;
   RouteLds route;
@@ -280,7 +281,7 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
   k2_stamp(p, 3 * st);
   K2_TASKS(t, p.moe.H / (16 * p.moe.DT)) {
     k2_wait(p, seen, SY_ROUTE, 2);  // the routing and its table: known long before the mid rows
-    moe_down<K2_NT, NCG>(p.moe, t, S.down.red, S.down.act,
+    moe_down<K2_NT, NCG>(p.moe, t, S.down.red, S.down.act, S.down.xres,
                          [&] { k2_wait(p, seen, SY_UP, up_total, t < G ? 3 * st + 1 : -1, K2_LANES); });
   }
   k2_stamp(p, 3 * st + 2);

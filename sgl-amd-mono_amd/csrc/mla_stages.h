@@ -327,6 +327,20 @@ MK2_DEV void mla_oproj(const MlaDev& p, int nt0, int nt1, float* red, Wait wait 
 #pragma unroll
       for (int q = 0; q < 4; ++q) apf[j][u][q] = __builtin_bit_cast(bf16x8, t[q]);
     }
+  // the residual rows (the layer's input, static) for the epilogue: entry idx = tid +
+  // i * NT of the ntl * 16 * rows outputs
+  const int ntl = NTL > 1 && nt1 >= 0 ? 2 : 1;
+  constexpr int EPI = (NTL * 16 * 32 + NT - 1) / NT;
+  float hres[EPI];
+#pragma unroll
+  for (int i = 0; i < EPI; ++i) {
+    const int idx = threadIdx.x + i * NT;
+    hres[i] = 0.f;
+    if (p.h && idx < ntl * 16 * p.rows) {
+      const int j = idx / (16 * p.rows), jdx = idx - j * 16 * p.rows;
+      hres[i] = bf16_to_f32(p.h[(size_t)(jdx >> 4) * p.hidden + (j == 0 ? nt0 : nt1) * 16 + (jdx & 15)]);
+    }
+  }
   wait();
   f32x4 acc[NTL][NCG];
 #pragma unroll
@@ -377,8 +391,10 @@ MK2_DEV void mla_oproj(const MlaDev& p, int nt0, int nt1, float* red, Wait wait 
 #pragma unroll
     for (int cg = 0; cg < NCG; ++cg) *(f32x4*)(red + (((j * NW + wave) * NCG + cg) * 64 + lane) * 4) = acc[j][cg];
   __syncthreads();
-  const int ntl = NTL > 1 && nt1 >= 0 ? 2 : 1;
-  for (int idx = threadIdx.x; idx < ntl * 16 * p.rows; idx += NT) {
+#pragma unroll
+  for (int it = 0; it < EPI; ++it) {
+    const int idx = threadIdx.x + it * NT;
+    if (idx >= ntl * 16 * p.rows) break;
     const int j = idx / (16 * p.rows), jdx = idx - j * 16 * p.rows;
     const int n16 = jdx & 15, row = jdx >> 4, cg = row >> 4, s16 = row & 15;
     const int l = (n16 >> 2) * 16 + s16, i = n16 & 3;
@@ -386,7 +402,7 @@ MK2_DEV void mla_oproj(const MlaDev& p, int nt0, int nt1, float* red, Wait wait 
 #pragma unroll
     for (int w = 0; w < NW; ++w) v += red[(((j * NW + w) * NCG + cg) * 64 + l) * 4 + i];
     const size_t o = (size_t)row * p.hidden + (j == 0 ? nt0 : nt1) * 16 + n16;
-    if (p.h) v += bf16_to_f32(p.h[o]);
+    if (p.h) v += hres[it];
     const bf16_t ob = f32_to_bf16(v);
     st_dev_u16(p.out + o, ob);
     if (p.ssp) {  // the 16 columns of (tile, row) are one DPP row: 16 * rows and NT are multiples of 16

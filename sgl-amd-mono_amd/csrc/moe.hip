@@ -32,7 +32,8 @@ template <int NCG>
 __global__ __launch_bounds__(MOE_NT) void k_moe_down(MoeDev p) {
   __shared__ float red[(MOE_NT / 64) * 2 * 64 * 4];  // NW * DT * NCG * 256, DT * NCG <= 2
   __shared__ int act_ids[256];
-  moe_down<MOE_NT, NCG>(p, blockIdx.x, red, act_ids);
+  __shared__ float xres[16 * 2 * 32];
+  moe_down<MOE_NT, NCG>(p, blockIdx.x, red, act_ids, xres);
 }
 
 // ----------------------------------------------------------------- host side

@@ -565,9 +565,10 @@ MK2_DEV void moe_upgate(const MoeDev& p, int t, float* red, float* midf) {
   const int chunks_r = p.I / p.UC;
   if (t < p.Dmax * chunks_r) {
     const int j = t / chunks_r, c = t % chunks_r;
-    if (j >= ldp_i32(p.act)) return;
-    const int e = ldp_i32(p.act + 1 + j);
-    if (e < 0 || e >= p.E) return;
+    // the list's length and slot j's expert in one round trip (slot j < Dmax <= E is
+    // inside the list's area; past the length its entry is not used)
+    const int nact = ldp_i32(p.act), e = ldp_i32(p.act + 1 + j);
+    if (j >= nact || e < 0 || e >= p.E) return;
     if (NCG == 1 && p.UC == 64) upgate_chunk<NT, NCG, (NCG == 1 ? 4 : 2)>(p, false, j, e, c, red, midf);
     else upgate_chunk<NT, NCG, 2>(p, false, j, e, c, red, midf);
   } else {
@@ -580,9 +581,10 @@ MK2_DEV void moe_upgate(const MoeDev& p, int t, float* red, float* midf) {
 // experts) adds rw * W_down[e] . mid into the rows' accumulators; out = bf16(y [+ x]).
 // Waves take every NW-th slot, B slots a unit, the next unit's weight tiles and mid
 // rows (shared by the DT tiles) in flight while a unit's MFMAs run.  act_ids: LDS >=
-// E ints; red: NW * DT * NCG * 256 floats.
+// E ints; red: NW * DT * NCG * 256 floats; xres: LDS >= 8 * DT * M words (the residual
+// rows, bf16).
 template <int NT, int NCG, int DT, typename Wait>
-MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, Wait wait) {
+MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, float* xres, Wait wait) {
   constexpr int NW = NT / 64;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, c16 = lane & 15;
   const int D = min(ldp_i32(p.act), p.Dmax);
@@ -613,6 +615,14 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, Wait w
     }
   }
   const bool mx = p.fmt == MK2_FMT_MXFP4;
+  // the residual rows (the W_o output, published before the routing) for the
+  // epilogue, straight into LDS (no registers held): dword d of the 8 * DT * M is
+  // row d / (8 * DT), columns 2 (d % (8 * DT)) .. + 1 of the task's
+  const int nxd = p.residual ? 8 * DT * p.M : 0;
+  if (threadIdx.x < nxd)
+    __builtin_amdgcn_global_load_lds(
+        (const uint32_t*)(p.x + (size_t)(threadIdx.x / (8 * DT)) * p.H + t0 * 16) + threadIdx.x % (8 * DT),
+        (uint32_t*)xres + 64 * wave, 4, 0, 0);
   // the routed slots (MXFP4): a unit is a batch of B slots (wave + NW * (B * i + u))
   // over KC k-blocks; units u + 1 and u + 2 (weights, mid rows, scales and route
   // weights) are in flight while unit u's MFMAs run
@@ -783,6 +793,7 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, Wait w
   for (int d = 0; d < DT; ++d)
 #pragma unroll
     for (int cg = 0; cg < NCG; ++cg) *(f32x4*)(red + (((wave * DT + d) * NCG + cg) * 64 + lane) * 4) = acc[d][cg];
+  drain_memory();  // this wave's residual dwords have landed in LDS
   __syncthreads();
   for (int idx = threadIdx.x; idx < 16 * DT * p.M; idx += NT) {
     const int n = idx % (16 * DT), s = idx / (16 * DT);
@@ -792,7 +803,7 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, Wait w
 #pragma unroll
     for (int w = 0; w < NW; ++w) y += red[(((w * DT + d) * NCG + cg) * 64 + l) * 4 + i];
     const size_t o = (size_t)s * p.H + (t0 + d) * 16 + n16;
-    if (p.residual) y += bf16_to_f32((bf16_t)ldp_u16(p.x + o));
+    if (p.residual) y += bf16_to_f32(((const bf16_t*)xres)[idx]);
     p.out[o] = f32_to_bf16(y);
   }
   __syncthreads();
@@ -802,9 +813,9 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, Wait w
 // mid activations' dependency, run once the task's static and routed weight loads
 // are in flight.
 template <int NT, int NCG, typename Wait = NoWait>
-MK2_DEV void moe_down(const MoeDev& p, int nt, float* red, int* act_ids, Wait wait = Wait()) {
-  if (NCG == 1 && p.DT == 2) down_rows<NT, NCG, (NCG == 1 ? 2 : 1)>(p, nt, red, act_ids, wait);
-  else down_rows<NT, NCG, 1>(p, nt, red, act_ids, wait);
+MK2_DEV void moe_down(const MoeDev& p, int nt, float* red, int* act_ids, float* xres, Wait wait = Wait()) {
+  if (NCG == 1 && p.DT == 2) down_rows<NT, NCG, (NCG == 1 ? 2 : 1)>(p, nt, red, act_ids, xres, wait);
+  else down_rows<NT, NCG, 1>(p, nt, red, act_ids, xres, wait);
 }
 
 }  // namespace mk2

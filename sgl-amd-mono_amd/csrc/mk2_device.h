@@ -53,16 +53,14 @@ MK2_DEV void e4m3x4_to_f32(uint32_t w, float* o) {
   f32x2 b = __builtin_amdgcn_cvt_pk_f32_fp8(w, true);
   o[0] = a.x; o[1] = a.y; o[2] = b.x; o[3] = b.y;
 }
-// 8 E4M3 bytes (two dwords) -> 8 bf16 (exact widening)
+// 8 E4M3 bytes (two dwords) -> 8 bf16: one scaled conversion (x 1.0) a pair, exact
+// (an E4M3 value has 4 significant bits and an exponent bf16 holds)
 MK2_DEV bf16x8 e4m3x8_to_bf16(uint32_t w0, uint32_t w1) {
-  float f[8];
-  e4m3x4_to_f32(w0, f);
-  e4m3x4_to_f32(w1, f + 4);
   i32x4 r;
-  r[0] = (int)pack_bf16x2_exact(f[0], f[1]);
-  r[1] = (int)pack_bf16x2_exact(f[2], f[3]);
-  r[2] = (int)pack_bf16x2_exact(f[4], f[5]);
-  r[3] = (int)pack_bf16x2_exact(f[6], f[7]);
+  r[0] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false));
+  r[1] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true));
+  r[2] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false));
+  r[3] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true));
   return __builtin_bit_cast(bf16x8, r);
 }
 // 8 E2M1 codes (one dword, element 0 in the low nibble) times 2^(code - 127) -> 8 bf16.

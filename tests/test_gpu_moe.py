@@ -130,6 +130,18 @@ def test_selftest_mfma_layouts():
     a8 = oc.e4m3_encode(a * 10)
     got = run(2, a8, None, bb, None)
     assert torch.allclose(got, oc.e4m3_decode(a8) @ bb.float().T, rtol=1e-5, atol=1e-3)
+    # mode 2 again, every finite E4M3 code exactly: A holds code (128 i + k) mod 256
+    # (NaN codes as zero), B picks one column k per output column, so d[i][j] is the
+    # widened value of A[i][k_j] itself
+    codes = torch.arange(16 * 128, dtype=torch.int64) % 256
+    codes[(codes & 0x7F) == 0x7F] = 0
+    a_all = codes.to(torch.uint8).view(16, 128)
+    want = oc.e4m3_decode(a_all)
+    for k0 in range(0, 128, 16):
+        sel = torch.zeros(16, 128)
+        sel[torch.arange(16), k0 + torch.arange(16)] = 1.0
+        got = run(2, a_all, None, sel.bfloat16(), None)
+        assert torch.equal(got, want[:, k0:k0 + 16].float()), k0
     # mode 1: E2M1 x E4M3 with E8M0 scales
     aq, asc = quant_mxfp4(a)
     bq, bsc = oc.mxfp8_quant(b)

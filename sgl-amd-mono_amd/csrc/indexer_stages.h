@@ -6,7 +6,8 @@
 // chunk of positions; a wave takes 16 keys at a time as the MFMA B operand (16
 // columns) against all heads as A (16 heads a tile), widening E2M1 x 2^e exactly to
 // bf16.  The head sum runs in the lanes: a lane holds 4 heads of each head group
-// for one key, then two cross-row shuffles finish it.
+// for one key; every four groups, three row-swapping permutes combine the four lane
+// groups' sums of all four at once.
 //
 // top-k, three stages over the order-preserving u32 keys of the scores:
 //   score (row, chunk)  also counts its keys into the row's two-level histogram: 4096
@@ -111,6 +112,15 @@ MK2_DEV void idx_score(const IdxDev& p, int r, int chunk, IdxScoreLds& L) {
   for (int b = threadIdx.x; b < IDX_BINS; b += NT) L.hist[b] = 0;
   __syncthreads();
   const int gw0 = wave * GPW;  // this wave's first group
+  static_assert(GPW % 4 == 0, "a wave's groups fill whole pages");
+  // the wave's pages (4 groups each) as uniform base addresses: a key load is that base
+  // plus a per-lane offset plus an immediate, no vector address arithmetic
+  constexpr int PPW = GPW / 4;
+  const uint8_t* pbase[PPW];
+#pragma unroll
+  for (int q = 0; q < PPW; ++q)
+    pbase[q] = p.cache + (size_t)__builtin_amdgcn_readfirstlane(lds_pages[gw0 / 4 + q]) * IDX_PAGE_BYTES;
+  const uint32_t off_code = c16 * 64 + 16 * g, off_scale = 4096 + c16 * 4;
   uint4 code[GPW];
   uint32_t sw[GPW];
   // a rolling window of KWIN key groups in flight: group j + KWIN - 1 is issued as
@@ -118,11 +128,8 @@ MK2_DEV void idx_score(const IdxDev& p, int r, int chunk, IdxScoreLds& L) {
   // CU's first groups behind the whole chip's requests)
   constexpr int KWIN = 4;
   auto issue = [&](int j) {
-    const int key0 = k_begin + (gw0 + j) * 16;
-    const uint8_t* pg = p.cache + (size_t)lds_pages[(key0 - k_begin) >> 6] * IDX_PAGE_BYTES;
-    const int tok = (key0 & 63) + c16;
-    code[j] = *(const uint4*)(pg + tok * 64 + 16 * g);
-    sw[j] = *(const uint32_t*)(pg + 4096 + tok * 4);
+    code[j] = *(const uint4*)(pbase[j >> 2] + off_code + (j & 3) * 1024);
+    sw[j] = *(const uint32_t*)(pbase[j >> 2] + off_scale + (j & 3) * 64);
   };
 #pragma unroll
   for (int j = 0; j < KWIN; ++j) issue(j);
@@ -169,17 +176,31 @@ MK2_DEV void idx_score(const IdxDev& p, int r, int chunk, IdxScoreLds& L) {
 #pragma unroll
       for (int hg = 0; hg < 4; ++hg) acc[hg] = mfma_bf16(qa[hg][q], kb[q], acc[hg]);
   };
+  // a lane's 16 heads of group j; every fourth group the four lane groups' sums are
+  // combined for four groups at once, (g0 + g1) + (g2 + g3) as a single group's would
+  // be, leaving group j - 3 + g's scores in lane group g: one store and one count a lane
+  float part[4];
   auto finish = [&](int j, const f32x4* acc) {
     float s = 0.f;
 #pragma unroll
     for (int hg = 0; hg < 4; ++hg)
 #pragma unroll
       for (int i = 0; i < 4; ++i) s += relu_bits(acc[hg][i]) * wt[hg][i];
-    s = add_xor32(add_xor16(s));  // the four lane groups' head sums
-    const int loc = (gw0 + j) * 16 + c16;
-    if (g == 0 && k_begin + loc < k_end) {
-      L.sc[loc] = s;
-      atomicAdd(&L.hist[radix_key(s) >> 20], 1);
+    part[j & 3] = s;
+    if ((j & 3) == 3) {
+      // rows 0, 2 of the first swap hold groups 0 / 2 (row pairs 01, 23), rows 1, 3
+      // groups 1 / 3; the 32-lane swap then pairs the halves
+      const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(part[0]), __float_as_uint(part[1]), false, false);
+      const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(part[2]), __float_as_uint(part[3]), false, false);
+      const float pa = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+      const float pb = __uint_as_float(b[0]) + __uint_as_float(b[1]);
+      const auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(pa), __float_as_uint(pb), false, false);
+      const float t = __uint_as_float(c[0]) + __uint_as_float(c[1]);
+      const int loc = (gw0 + j - 3) * 16 + lane;
+      if (k_begin + loc < k_end) {
+        L.sc[loc] = t;
+        atomicAdd(&L.hist[radix_key(t) >> 20], 1);
+      }
     }
   };
   static_assert(GPW % 2 == 0, "groups go in pairs");
@@ -582,11 +603,11 @@ MK2_DEV bool idx_slice(const IdxDev& p, int r, int chunk, TopkLds& S, int spin, 
   }
   __syncthreads();
   int* orow = p.out + (size_t)r * k;
-  at = S.res[2] + off.a;  // < the count above bin b1 < k
+  at = S.res[2] + off.a;  // < the count above bin b1 < k (checked all the same)
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     if (base + i < n && (key[i] >> 20) > b1) {
-      st_dev_i32(orow + at, base + i);
+      if (at < k) st_dev_i32(orow + at, base + i);
       ++at;
     }
   }

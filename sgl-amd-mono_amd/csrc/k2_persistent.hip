@@ -279,7 +279,7 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
   k2_stamp(p, 3 * st++ + 2);
   // ---- down + route weighting + residual, per 16 hidden rows
   k2_stamp(p, 3 * st);
-  K2_TASKS(t, p.moe.H / (16 * p.moe.DT)) {
+  K2_TASKS(t, down_tasks(p.moe)) {
     k2_wait(p, seen, SY_ROUTE, 2);  // the routing and its table: known long before the mid rows
     moe_down<K2_NT, NCG>(p.moe, t, S.down.red, S.down.act, S.down.xres,
                          [&] { k2_wait(p, seen, SY_UP, up_total, t < G ? 3 * st + 1 : -1, K2_LANES); });

@@ -71,7 +71,9 @@ size_t moe_carve(const mk2_moe_shape* s, void* base, MoeDev* d) {
   t.KC = KC;
   t.Dmax = Dmax;
   t.UC = (s->expert_fmt == MK2_FMT_MXFP4 && M <= 16 && I % 64 == 0) ? 64 : 32;
-  t.DT = (s->expert_fmt == MK2_FMT_MXFP4 && M <= 16 && H % 32 == 0) ? 2 : 1;
+  // down tasks: 24 hidden rows when hidden is a multiple of 48 (6144: one task a CU of
+  // MI355X), else 32, at MXFP4 and up to 16 rows; 16 otherwise
+  t.DT = (s->expert_fmt == MK2_FMT_MXFP4 && M <= 16) ? (H % 48 == 0 ? 3 : (H % 32 == 0 ? 2 : 1)) : 1;
   t.ssp = c.take<float>((size_t)(H / 16) * M);
   t.xn = c.take<bf16_t>((size_t)M * H);
   t.xq = c.take<uint8_t>((size_t)M * H);
@@ -129,8 +131,8 @@ int moe_enqueue(const MoeDev& d, hipStream_t st) {
   const int up_tasks = d.Dmax * (d.I / d.UC) + d.n_shared * (d.SI / 32);
   if (ncg == 1) k_moe_upgate<1><<<up_tasks, MOE_NT, 0, st>>>(d);
   else k_moe_upgate<2><<<up_tasks, MOE_NT, 0, st>>>(d);
-  if (ncg == 1) k_moe_down<1><<<d.H / (16 * d.DT), MOE_NT, 0, st>>>(d);
-  else k_moe_down<2><<<d.H / (16 * d.DT), MOE_NT, 0, st>>>(d);
+  if (ncg == 1) k_moe_down<1><<<down_tasks(d), MOE_NT, 0, st>>>(d);
+  else k_moe_down<2><<<down_tasks(d), MOE_NT, 0, st>>>(d);
   return check_launch("moe");
 }
 

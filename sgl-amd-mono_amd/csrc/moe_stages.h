@@ -16,7 +16,8 @@ struct MoeDev {
   int KC;    // router k-chunks
   int Dmax;  // capacity of the distinct-expert list
   int UC;    // intermediate rows of a routed up/gate task (64: MXFP4 at <= 16 rows, else 32)
-  int DT;    // 16-row hidden tiles of a down task (2: MXFP4 at <= 16 rows, else 1)
+  int DT;    // 16-row hidden tiles of a down task (2: MXFP4 at <= 16 rows, else 1; 3: 24 rows,
+            // a tile and a half, when hidden is a multiple of 48)
   float route_scale, eps;
   const bf16_t* x;
   const bf16_t* gamma;
@@ -577,7 +578,7 @@ MK2_DEV void moe_upgate(const MoeDev& p, int t, float* red, float* midf) {
 }
 
 // ---------------------------------------------------------- stage: down + combine
-// A task is 16*DT hidden rows; every slot (the shared expert, then the D routed
+// A task is 16*DT hidden rows (24 with p.DT == 3); every slot (the shared expert, then the D routed
 // experts) adds rw * W_down[e] . mid into the rows' accumulators; out = bf16(y [+ x]).
 // Waves take every NW-th slot, B slots a unit, the next unit's weight tiles and mid
 // rows (shared by the DT tiles) in flight while a unit's MFMAs run.  act_ids: LDS >=
@@ -591,7 +592,29 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, float*
   for (int j = threadIdx.x; j < D; j += NT) act_ids[j] = min(max(ldp_i32(p.act + 1 + j), 0), p.E - 1);
   __syncthreads();
   const int HT = p.H / 16;
-  const int t0 = nt * DT;  // first 16-row tile
+  // the task's rows: tile tl[d], rows rlo[d] .. rhi[d] - 1 of it (every row of DT tiles,
+  // or with p.DT == 3 (DT 2) 24 rows: a whole tile and half of the next, in either order)
+  int tl[DT], rlo[DT], rhi[DT];
+#pragma unroll
+  for (int d = 0; d < DT; ++d) {
+    tl[d] = nt * DT + d;
+    rlo[d] = 0;
+    rhi[d] = 16;
+  }
+  if (DT == 2 && p.DT == 3) {
+    const int ta = (3 * nt) >> 1;
+    tl[0] = ta;
+    tl[DT - 1] = ta + 1;
+    rlo[0] = nt & 1 ? 8 : 0;
+    rhi[DT - 1] = nt & 1 ? 16 : 8;
+  }
+  const int c0 = tl[0] * 16 + rlo[0];  // the task's first hidden row (output column)
+  int ncol = 0;
+#pragma unroll
+  for (int d = 0; d < DT; ++d) ncol += rhi[d] - rlo[d];
+  bool live[DT];  // this lane's A row is one of the task's
+#pragma unroll
+  for (int d = 0; d < DT; ++d) live[d] = c16 >= rlo[d] && c16 < rhi[d];
   const int KB2s = p.n_shared ? p.SI / 128 : 0;
   const int KB2 = p.I / 128;
   constexpr int B = 1;                                 // MXFP4 slots a unit
@@ -606,22 +629,26 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, float*
     const int kb = min(wave, max(KB2s, 1) - 1);
 #pragma unroll
     for (int d = 0; d < DT; ++d) {
+      shraw[d][0] = shraw[d][1] = make_uint4(0, 0, 0, 0);
+      shsc[d] = 0.f;
       if (KB2s) {
-        const uint4* tl = (const uint4*)(p.ws2 + ((size_t)(t0 + d) * KB2s + kb) * 2048 + lane * 32);
-        shraw[d][0] = tl[0];
-        shraw[d][1] = tl[1];
-        shsc[d] = p.ss2[((t0 + d) * 16 / 128) * KB2s + kb];
+        const uint4* src = (const uint4*)(p.ws2 + ((size_t)tl[d] * KB2s + kb) * 2048 + lane * 32);
+        if (live[d]) {
+          shraw[d][0] = src[0];
+          shraw[d][1] = src[1];
+        }
+        shsc[d] = p.ss2[(tl[d] * 16 / 128) * KB2s + kb];
       }
     }
   }
   const bool mx = p.fmt == MK2_FMT_MXFP4;
   // the residual rows (the W_o output, published before the routing) for the
-  // epilogue, straight into LDS (no registers held): dword d of the 8 * DT * M is
-  // row d / (8 * DT), columns 2 (d % (8 * DT)) .. + 1 of the task's
-  const int nxd = p.residual ? 8 * DT * p.M : 0;
+  // epilogue, straight into LDS (no registers held): dword d of the ncol / 2 * M is
+  // row d / (ncol / 2), columns 2 (d % (ncol / 2)) .. + 1 of the task's
+  const int nxd = p.residual ? ncol / 2 * p.M : 0;
   if (threadIdx.x < nxd)
     __builtin_amdgcn_global_load_lds(
-        (const uint32_t*)(p.x + (size_t)(threadIdx.x / (8 * DT)) * p.H + t0 * 16) + threadIdx.x % (8 * DT),
+        (const uint32_t*)(p.x + (size_t)(threadIdx.x / (ncol / 2)) * p.H + c0) + threadIdx.x % (ncol / 2),
         (uint32_t*)xres + 64 * wave, 4, 0, 0);
   // the routed slots (MXFP4): a unit is a batch of B slots (wave + NW * (B * i + u))
   // over KC k-blocks; units u + 1 and u + 2 (weights, mid rows, scales and route
@@ -644,10 +671,11 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, float*
       for (int c = 0; c < KC; ++c)
 #pragma unroll
         for (int d = 0; d < DT; ++d)
-          x.a[ub][d][c] = load_a_fp4(p.w2 + (((size_t)e * HT + t0 + d) * KB2 + min(kb0 + c, KB2 - 1)) * 1024, lane);
+          x.a[ub][d][c] = live[d] ? load_a_fp4(p.w2 + (((size_t)e * HT + tl[d]) * KB2 + min(kb0 + c, KB2 - 1)) * 1024, lane)
+                                  : i32x8{0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
       for (int d = 0; d < DT; ++d)
-        x.sa[ub][d] = (int)*(const uint32_t*)(p.s2 + ((((size_t)e * HT + t0 + d) * G2 + kb0 / 4) * 64 + lane) * 4);
+        x.sa[ub][d] = live[d] ? (int)*(const uint32_t*)(p.s2 + ((((size_t)e * HT + tl[d]) * G2 + kb0 / 4) * 64 + lane) * 4) : 127;
     }
   };
   auto load_m = [&](int u, Unit& x) {  // mid rows and route weights: after the wait
@@ -731,10 +759,10 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, float*
         r1 = shraw[d][1];
         sc = shsc[d];
       } else {
-        const uint4* tl = (const uint4*)(p.ws2 + ((size_t)(t0 + d) * KB2s + kb) * 2048 + lane * 32);
-        r0 = tl[0];
-        r1 = tl[1];
-        sc = p.ss2[((t0 + d) * 16 / 128) * KB2s + kb];
+        const uint4* src = (const uint4*)(p.ws2 + ((size_t)tl[d] * KB2s + kb) * 2048 + lane * 32);
+        r0 = live[d] ? src[0] : make_uint4(0, 0, 0, 0);
+        r1 = live[d] ? src[1] : make_uint4(0, 0, 0, 0);
+        sc = p.ss2[(tl[d] * 16 / 128) * KB2s + kb];
       }
       bf16x8 a[4];
       a[0] = e4m3x8_to_bf16(r0.x, r0.y);
@@ -762,8 +790,8 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, float*
     constexpr int KMAX = 8;  // FP8 experts: inter <= 1024
     for (int j = wave; j < D; j += NW) {
       const int e = act_ids[j];
-      const uint8_t* wb = p.w2 + ((size_t)e * HT + t0) * KB2 * 2048;
-      const float* sbase = (const float*)p.s2 + (size_t)e * (p.H / 128) * KB2 + (t0 * 16 / 128) * KB2;
+      const uint8_t* wb = p.w2 + ((size_t)e * HT + tl[0]) * KB2 * 2048;
+      const float* sbase = (const float*)p.s2 + (size_t)e * (p.H / 128) * KB2 + (tl[0] * 16 / 128) * KB2;
       uint4 raw[KMAX][2];
 #pragma unroll
       for (int kb = 0; kb < KMAX; ++kb) {
@@ -795,26 +823,31 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, float*
     for (int cg = 0; cg < NCG; ++cg) *(f32x4*)(red + (((wave * DT + d) * NCG + cg) * 64 + lane) * 4) = acc[d][cg];
   drain_memory();  // this wave's residual dwords have landed in LDS
   __syncthreads();
-  for (int idx = threadIdx.x; idx < 16 * DT * p.M; idx += NT) {
-    const int n = idx % (16 * DT), s = idx / (16 * DT);
-    const int d = n >> 4, n16 = n & 15, cg = s >> 4, s16 = s & 15;
+  const int n0 = rhi[0] - rlo[0];  // the first tile's columns
+  for (int idx = threadIdx.x; idx < ncol * p.M; idx += NT) {
+    const int n = idx % ncol, s = idx / ncol;  // column c0 + n of row s
+    const int d = n < n0 ? 0 : DT - 1, n16 = n < n0 ? rlo[0] + n : rlo[DT - 1] + n - n0;
+    const int cg = s >> 4, s16 = s & 15;
     const int l = (n16 >> 2) * 16 + s16, i = n16 & 3;
     float y = 0.f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) y += red[(((w * DT + d) * NCG + cg) * 64 + l) * 4 + i];
-    const size_t o = (size_t)s * p.H + (t0 + d) * 16 + n16;
+    const size_t o = (size_t)s * p.H + c0 + n;
     if (p.residual) y += bf16_to_f32(((const bf16_t*)xres)[idx]);
     p.out[o] = f32_to_bf16(y);
   }
   __syncthreads();
 }
 
-// task nt of H / (16 * p.DT).  Needs the routing (act, rw) on entry; `wait` is the
+// down tasks of a launch: 16 * DT hidden rows each, or 24 with DT == 3
+__host__ __device__ inline int down_tasks(const MoeDev& p) { return p.DT == 3 ? p.H / 24 : p.H / (16 * p.DT); }
+
+// task nt of down_tasks(p).  Needs the routing (act, rw) on entry; `wait` is the
 // mid activations' dependency, run once the task's static and routed weight loads
 // are in flight.
 template <int NT, int NCG, typename Wait = NoWait>
 MK2_DEV void moe_down(const MoeDev& p, int nt, float* red, int* act_ids, float* xres, Wait wait = Wait()) {
-  if (NCG == 1 && p.DT == 2) down_rows<NT, NCG, (NCG == 1 ? 2 : 1)>(p, nt, red, act_ids, xres, wait);
+  if (NCG == 1 && p.DT >= 2) down_rows<NT, NCG, (NCG == 1 ? 2 : 1)>(p, nt, red, act_ids, xres, wait);
   else down_rows<NT, NCG, 1>(p, nt, red, act_ids, xres, wait);
 }
 

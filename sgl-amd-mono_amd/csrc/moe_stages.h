@@ -522,17 +522,21 @@ MK2_DEV void upgate_chunk(const MoeDev& p, bool shared, int j, int e, int c, flo
     for (int cg = 0; cg < NCG; ++cg)
       *(f32x4*)(red + (((wave * NQ + q) * NCG + cg) * 64 + lane) * 4) = acc[q][cg];
   __syncthreads();
-  for (int idx = threadIdx.x; idx < R * 16 * NCG; idx += NT) {
-    const int n = idx % R, s = idx / R;
-    const int t2 = n >> 4, n16 = n & 15, cg = s >> 4, s16 = s & 15;
-    const int l = (n16 >> 2) * 16 + s16, i = n16 & 3;
-    float gs = 0.f, us = 0.f;
+  // gate tile t2 and up tile CT + t2 summed over the waves, columns 4k .. 4k + 3 of
+  // one row a thread: a wave's lanes take consecutive rows, so every read is a whole
+  // 16-byte word and the lanes' words fall in distinct banks
+  for (int idx = threadIdx.x; idx < 64 * CT * NCG; idx += NT) {
+    const int s16 = idx & 15, k = (idx >> 4) & 3, t2 = (idx >> 6) % CT, cg = (idx >> 6) / CT;
+    const int l = k * 16 + s16;
+    f32x4 gs = {0.f, 0.f, 0.f, 0.f}, us = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-      gs += red[(((w * NQ + t2) * NCG + cg) * 64 + l) * 4 + i];
-      us += red[(((w * NQ + CT + t2) * NCG + cg) * 64 + l) * 4 + i];
+      gs += *(const f32x4*)(red + (((w * NQ + t2) * NCG + cg) * 64 + l) * 4);
+      us += *(const f32x4*)(red + (((w * NQ + CT + t2) * NCG + cg) * 64 + l) * 4);
     }
-    midf[s * (R + 1) + n] = silu_mul(gs, us);
+    const int s = cg * 16 + s16, n = t2 * 16 + 4 * k;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) midf[s * (R + 1) + n + i] = silu_mul(gs[i], us[i]);
   }
   __syncthreads();
   if (!shared && p.fmt == MK2_FMT_MXFP4) {

@@ -41,7 +41,7 @@ enum : int {
   SY_ROUTER_LAST,  // router sub-counters completed (the last runs the routing)
   SY_DONE,         // workgroups finished (the last one resets)
   SY_ERR,          // sticky: a wait ran out of its spin limit
-  SY_UV = 144,     // [K2_LANES] sub-counters each: merged + W_UV (row, head) tasks
+  SY_UV = 144,     // [K2_LANES] sub-counters each: merged + W_UV (row, head, half) tasks
   SY_OPROJ = SY_UV + K2_LANES,
   SY_ROUTER = SY_OPROJ + K2_LANES,
   SY_UP = SY_ROUTER + K2_LANES,
@@ -221,14 +221,15 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
   }
   K2_NEXT(R * ns);
   k2_stamp(p, 3 * st++ + 2);
-  // ---- merge of the splits + W_UV, per (row, head)
+  // ---- merge of the splits + W_UV, per (row, head, half of the head's outputs)
   k2_stamp(p, 3 * st);
-  K2_TASKS(t, R * MLA_HEADS) {
-    const int r = t / MLA_HEADS, h = t % MLA_HEADS;
-    mla_merge_uv<K2_NT>(p.mla, r, h, S.merge, [&] { k2_wait(p, seen, SY_SPLIT + r, ns, t < G ? 3 * st + 1 : -1); });
+  K2_TASKS(t, 2 * R * MLA_HEADS) {
+    const int r = t / (2 * MLA_HEADS), h = (t >> 1) % MLA_HEADS;
+    mla_merge_uv<K2_NT>(p.mla, r, h, t & 1, S.merge,
+                        [&] { k2_wait(p, seen, SY_SPLIT + r, ns, t < G ? 3 * st + 1 : -1); });
     k2_signal(p, SY_UV, t, K2_LANES);
   }
-  K2_NEXT(R * MLA_HEADS);
+  K2_NEXT(2 * R * MLA_HEADS);
   k2_stamp(p, 3 * st++ + 2);
   // ---- W_o + residual, per 16 hidden rows: tasks t and t + G together (their weights
   // all in flight before the wait)
@@ -237,7 +238,7 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
   for (int t = (b - base % G + G) % G; t < ht; t += 2 * G) {
     const int t1 = t + G < ht ? t + G : -1;
     mla_oproj<K2_NT, NCG, 2>(p.mla, t, t1, S.up.red,
-                             [&] { k2_wait(p, seen, SY_UV, R * MLA_HEADS, t < G ? 3 * st + 1 : -1, K2_LANES); });
+                             [&] { k2_wait(p, seen, SY_UV, 2 * R * MLA_HEADS, t < G ? 3 * st + 1 : -1, K2_LANES); });
     k2_signal(p, SY_OPROJ, t, K2_LANES, t1 >= 0 ? 2 : 1);
   }
   K2_NEXT(ht);

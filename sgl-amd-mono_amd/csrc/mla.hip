@@ -14,7 +14,7 @@ __global__ __launch_bounds__(MLA_NT) void k_mla_split(MlaDev p) {
 constexpr int MLA_NT2 = 512;
 __global__ __launch_bounds__(MLA_NT2) void k_mla_merge_uv(MlaDev p) {
   __shared__ MlaMergeLds L;
-  mla_merge_uv<MLA_NT2>(p, blockIdx.y, blockIdx.x, L);
+  mla_merge_uv<MLA_NT2>(p, blockIdx.y, blockIdx.x >> 1, blockIdx.x & 1, L);
 }
 template <int NCG>
 __global__ __launch_bounds__(MLA_NT2) void k_mla_oproj(MlaDev p) {
@@ -64,7 +64,7 @@ int mla_fill(const mk2_mla_args* a, MlaDev* d) {
 
 void mla_enqueue(const MlaDev& d, hipStream_t st) {
   k_mla_split<<<dim3(d.nsplit, d.rows), MLA_NT, 0, st>>>(d);
-  k_mla_merge_uv<<<dim3(MLA_HEADS, d.rows), MLA_NT2, 0, st>>>(d);
+  k_mla_merge_uv<<<dim3(2 * MLA_HEADS, d.rows), MLA_NT2, 0, st>>>(d);
   if (d.rows > 16) k_mla_oproj<2><<<d.hidden / 16, MLA_NT2, 0, st>>>(d);
   else k_mla_oproj<1><<<d.hidden / 16, MLA_NT2, 0, st>>>(d);
 }

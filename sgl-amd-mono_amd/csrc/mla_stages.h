@@ -216,21 +216,26 @@ MK2_DEV void mla_split(const MlaDev& p, int r, int s, MlaSplitLds& L) {
 }
 
 // ---------------------------------------------------------------- stage: merge + W_UV
-// Task (row r, head h): the exact combination of the row's splits for head h ->
-// o_lat (rounded to bf16, in LDS), then o[r][h] = W_UV[h] o_lat on bf16 MFMA: wave w
-// takes the 16-row W_UV tiles w, w + NW, ... over all 512 latent dims, with o_lat as
-// the B operand in every column (column 0 is kept).  The wave's first W_UV tile is
-// static and loaded before `wait` (the splits' dependency).
+// Task (row r, head h, half hf): the exact combination of the row's splits for head h
+// -> o_lat (rounded to bf16, in LDS), then half hf of o[r][h] = W_UV[h] o_lat on bf16
+// MFMA: the half's 16-row W_UV tiles go to waves 1, 2, ... over all 512 latent dims,
+// with o_lat as the B operand in every column (column 0 is kept).  The two halves of
+// (r, h) compute the same o_lat bits, so the output does not depend on the split; a
+// workgroup moves 64 KiB of W_UV and 64 KiB of partials instead of 128 + 64.  A wave's
+// first tile is static and loaded before `wait` (the splits' dependency); wave 0,
+// which polls the dependency, loads none.
 struct MlaMergeLds {
   float w[2 * 1024 + 8];  // per split: exp(m_s - M), then l_s (nsplit <= 1024)
   bf16_t ol[MLA_LAT];
 };
 
 template <int NT, typename Wait = NoWait>
-MK2_DEV void mla_merge_uv(const MlaDev& p, int r, int h, MlaMergeLds& L, Wait wait = Wait()) {
+MK2_DEV void mla_merge_uv(const MlaDev& p, int r, int h, int hf, MlaMergeLds& L, Wait wait = Wait()) {
   constexpr int NW = NT / 64, DPT = MLA_LAT / NT;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, c16 = lane & 15;
   const int ns = p.nsplit, nvt = p.v_dim / 16;
+  const int vlo = hf ? (nvt + 1) / 2 : 0, vhi = hf ? nvt : (nvt + 1) / 2;  // this half's tiles
+  const int vt0 = vlo + wave - 1;  // wave w >= 1 takes tiles vt0, vt0 + NW - 1, ...
   auto load_a = [&](int vt, bf16x8* a) {  // W_UV[h] rows vt*16 + c16, dims 128 kb + 32 g + 8 q
     const bf16_t* wrow = p.w_uv + ((size_t)h * p.v_dim + vt * 16 + c16) * MLA_LAT + 32 * g;
 #pragma unroll
@@ -239,7 +244,7 @@ MK2_DEV void mla_merge_uv(const MlaDev& p, int r, int h, MlaMergeLds& L, Wait wa
       for (int q = 0; q < 4; ++q) a[kb * 4 + q] = __builtin_bit_cast(bf16x8, *(const uint4*)(wrow + kb * 128 + 8 * q));
   };
   bf16x8 a[16];
-  if (wave < nvt) load_a(wave, a);
+  if (wave >= 1 && vt0 < vhi) load_a(vt0, a);
   wait();
   float* wgt = L.w;        // [ns] exp(m_s - M)
   float* lsum = L.w + ns;  // [ns] l_s
@@ -283,11 +288,11 @@ MK2_DEV void mla_merge_uv(const MlaDev& p, int r, int h, MlaMergeLds& L, Wait wa
   for (int d = 0; d < DPT; ++d) {
     o[d] *= inv;
     L.ol[DPT * tid + d] = f32_to_bf16(o[d]);
-    if (p.o_lat_f32) p.o_lat_f32[at + d] = o[d];
+    if (p.o_lat_f32 && hf == 0) p.o_lat_f32[at + d] = o[d];
   }
   __syncthreads();
-  for (int vt = wave; vt < nvt; vt += NW) {
-    if (vt != wave) load_a(vt, a);
+  for (int vt = vt0; wave >= 1 && vt < vhi; vt += NW - 1) {
+    if (vt != vt0) load_a(vt, a);
     f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)

@@ -92,6 +92,19 @@ def test_moe_mxfp4_config2(rows):
     _check(cfg, w, out, logits, ids, wts)
 
 
+@pytest.mark.parametrize("hidden", [2048, 7168])
+def test_moe_mxfp4_down_tiles(hidden):
+    """Down tasks of 32 hidden rows (hidden not a multiple of 48; 6144 takes 24-row
+    tasks), with the norm and the residual."""
+    from dataclasses import replace
+
+    from sgl_amd_mono.k2 import config as C
+
+    cfg = replace(C.C2_MOE, hidden=hidden, n_experts=64)
+    w, out, logits, ids, wts = _run(cfg, 8, seed=hidden, norm=True, residual=True)
+    _check(cfg, w, out, logits, ids, wts, norm=True, residual=True)
+
+
 def test_moe_mxfp4_norm_residual():
     from sgl_amd_mono.k2 import config as C
 

@@ -234,11 +234,15 @@ MK2_DEV void idx_score(const IdxDev& p, int r, int chunk, IdxScoreLds& L) {
       for (int u = 0; u < 4 && k_begin + i + u < k_end; ++u) st_dev_f32(srow + k_begin + i + u, L.sc[i + u]);
     }
   }
-  // the chunk's counts into the row's histograms (device atomics, nonzero bins)
-  int* gh = p.hist + (size_t)r * IDX_BINS;
-  for (int b = threadIdx.x; b < IDX_BINS; b += NT) {
-    const int v = L.hist[b];
-    if (v) atomicAdd(gh + b, v);
+  // the chunk's counts into the row's histograms (device atomics, nonzero bins): two
+  // adjacent fine bins a 64-bit add (no carry crosses: a row holds < 2^17 keys), half
+  // the atomic lanes
+  unsigned long long* gh2 = (unsigned long long*)(p.hist + (size_t)r * IDX_BINS);
+  for (int b2 = threadIdx.x; b2 < IDX_BINS / 2; b2 += NT) {
+    const uint2 v = *(const uint2*)(L.hist + 2 * b2);
+    if (v.x | v.y)
+      __hip_atomic_fetch_add(gh2 + b2, (unsigned long long)v.x | ((unsigned long long)v.y << 32), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
   }
   int* ch = p.chist + (size_t)r * IDX_CBINS;
   for (int c = threadIdx.x; c < IDX_CBINS; c += NT) {

@@ -712,9 +712,10 @@ MK2_DEV void topk_stream(const IdxDev& p, int r, uint32_t kbase, int m, int k, i
 
 // The list entries base .. k - 1 from the m <= TOPK_CAP keys of bin b1 in LDS
 // (position order): the need = k - base largest by their low 20 bits, ties by
-// position.  Three radix digits (8, 8 and 4 bits), each located by one wave over its
-// own histogram (S.hist[256 * pass ..], cleared by the caller); then the keys above
-// the k-th key in position order, then the keys equal to it, as many as fill.  Round
+// position.  Two 10-bit radix digits, each located by one wave over its own histogram
+// (S.hist[1024 * pass ..], cleared by the caller; the first digit's filled by the
+// caller as it gathers the keys); then the keys above the k-th key in position
+// order, then the keys equal to it, as many as fill.  Round
 // i gives thread t the candidate j = i * NT + t, so lanes read consecutive words; a
 // candidate's rank in its group is its wave's offset for the round (one scan over all
 // (round, wave) counts) plus the ballot count of the lanes below it.
@@ -727,24 +728,25 @@ MK2_DEV void bin_select(TopkLds& S, int m, int base, int k, int* orow) {
   int need = k - base;
   uint32_t prefix = 0;  // the digits found so far
 #pragma unroll 1
-  for (int pass = 0; pass < 3; ++pass) {
-    const int shift = pass == 0 ? 12 : (pass == 1 ? 4 : 0), width = pass == 2 ? 4 : 8;
-    const int hi = shift + width;  // bits above this digit are the prefix
-    int* h = S.hist + 256 * pass;
-    for (int j = tid; j < m; j += NT) {
-      const uint32_t v = S.ckey[j] & 0xFFFFFu;
-      if ((v >> hi) == prefix) atomicAdd(&h[(v >> shift) & ((1u << width) - 1u)], 1);
+  for (int pass = 0; pass < 2; ++pass) {
+    const int shift = pass == 0 ? 10 : 0;  // two 10-bit digits
+    int* h = S.hist + 1024 * pass;
+    if (pass == 1) {  // the first digit's histogram was built as the candidates were gathered
+      for (int j = tid; j < m; j += NT) {
+        const uint32_t v = S.ckey[j] & 0xFFFFFu;
+        if ((v >> 10) == prefix) atomicAdd(&h[v & 1023u], 1);
+      }
+      __syncthreads();
     }
-    __syncthreads();
     if (tid < 64) {
       int ab;
-      const int b = wave_find_bin(h, 256, need, &ab);
+      const int b = wave_find_bin(h, 1024, need, &ab);
       if (tid == 0) { S.res[0] = b; S.res[1] = ab; }
     }
     __syncthreads();
     // every thread reads S.res before it reaches the next pass's barrier, after which
     // wave 0 rewrites it
-    prefix = (prefix << width) | (uint32_t)S.res[0];
+    prefix = (prefix << 10) | (uint32_t)S.res[0];
     need -= S.res[1];
   }
   const uint32_t T = prefix;              // low 20 bits of the k-th key
@@ -825,7 +827,7 @@ MK2_DEV void idx_select(const IdxDev& p, int r, TopkLds& S, bool known = false) 
     const int b1 = wave_threshold(p, r, k, &above);
     if (tid == 0) { S.res[0] = b1; S.res[1] = above; }
   }
-  for (int i = tid; i < 3 * 256; i += NT) S.hist[i] = 0;  // the three digit histograms
+  for (int i = tid; i < 2 * 1024; i += NT) S.hist[i] = 0;  // the two digit histograms
   // one round trip: each chunk's count of bin-b1 keys and its first SPEC * TPC of them
   const int c = tid / TPC, sub = tid % TPC;
   const uint2* src = p.cand + (size_t)r * p.max_ctx + (size_t)c * IDX_CHUNK;
@@ -857,6 +859,7 @@ MK2_DEV void idx_select(const IdxDev& p, int r, TopkLds& S, bool known = false) 
       if (i < cnt) {
         S.ckey[off + i] = v[u].x;
         S.cpos[off + i] = (uint16_t)v[u].y;
+        atomicAdd(&S.hist[(v[u].x >> 10) & 1023u], 1);  // the first radix digit
       }
     }
     for (int i0 = SPEC * TPC; i0 < cnt; i0 += SPEC * TPC) {  // a crowded chunk's rest
@@ -871,6 +874,7 @@ MK2_DEV void idx_select(const IdxDev& p, int r, TopkLds& S, bool known = false) 
         if (i < cnt) {
           S.ckey[off + i] = v[u].x;
           S.cpos[off + i] = (uint16_t)v[u].y;
+          atomicAdd(&S.hist[(v[u].x >> 10) & 1023u], 1);
         }
       }
     }

@@ -30,7 +30,6 @@ METRIC = "us per fused decoder layer @8 decode rows, 1 GPU; % of peak HBM GB/s"
 CSRC = os.path.join(ROOT, "sgl-amd-mono_amd", "csrc")
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k2_layer_m8_traffic.json")
 LAYER_KERNEL = "k_k2_layer"  # the persistent layer kernel's name (rocprof)
-COPY_KERNEL = "copy"         # torch's copy kernel of the calibration
 
 
 def sources_digest():
@@ -59,39 +58,64 @@ def recorded_traffic():
     return rec.get("traffic_bytes_per_launch")
 
 
+def _pmc_dispatches(dirs):
+    """Per-dispatch counters from rocprofv3 --pmc databases, one list per database:
+    (dispatch_id, kernel name, {counter: value}).  GRBM counters repeat over instances
+    and take the max (as rocprof's MFMA_UTIL does); the others add up over instances."""
+    import glob
+    import sqlite3
+
+    out = []
+    for d in dirs:
+        for f in sorted(glob.glob(os.path.join(d, "**", "*.db"), recursive=True)):
+            db = sqlite3.connect(f)
+            tables = {r[0] for r in db.execute("select name from sqlite_master where type in ('table','view')")}
+            if "pmc_events" not in tables:
+                continue
+            disp = {}
+            q = ("select name, dispatch_id, counter_name, sum(counter_value), max(counter_value) "
+                 "from pmc_events group by dispatch_id, counter_name")
+            for name, did, counter, total, top in db.execute(q):
+                disp.setdefault(did, (name, {}))[1][counter] = top if counter.startswith("GRBM_") else total
+            out.append([(did, n, c) for did, (n, c) in sorted(disp.items())])
+    return out
+
+
+def _copy_scale(per_db, calib_bytes):
+    """Factor turning FETCH_SIZE / WRITE_SIZE (KiB) into bytes, from the calibration copy:
+    the last three copyBuffer dispatches of each database (bench.py --copy-calib-mib runs
+    them after everything else), each reading and writing calib_bytes / 2."""
+    vals = {}
+    for rows in per_db:
+        copies = [c for _, n, c in rows if "copyBuffer" in n][-3:]
+        for c in ("FETCH_SIZE", "WRITE_SIZE"):
+            if len(copies) == 3 and all(c in x for x in copies):
+                v = [x[c] for x in copies]
+                if max(v) > 1.02 * min(v):
+                    raise SystemExit(f"calibration copies disagree on {c}: {v}")
+                vals[c] = statistics.mean(v)
+    return {c: (calib_bytes / 2) / (v * 1024) for c, v in vals.items() if v > 0}
+
+
 def pmc_summary(dirs, calib_bytes):
     """Mean FETCH_SIZE / WRITE_SIZE (KiB a dispatch) of the layer kernel and of the
     calibration copy, from rocprofv3 --pmc databases; each scaled by the factor that
     turns the copy's counter into its known byte count."""
-    import glob
-    import sqlite3
-    from collections import defaultdict
-
-    acc = defaultdict(lambda: defaultdict(list))
-    for d in dirs:
-        for f in glob.glob(os.path.join(d, "**", "*.db"), recursive=True):
-            db = sqlite3.connect(f)
-            q = ("select name, dispatch_id, counter_name, sum(counter_value) from pmc_events "
-                 "group by dispatch_id, counter_name")
-            for name, _, counter, value in db.execute(q):
-                kind = ("layer" if LAYER_KERNEL in name else
-                        "copy" if COPY_KERNEL in name.lower() else None)
-                if kind:
-                    acc[kind][counter].append(value)
-    # the calibration copies are the largest copies of the run
-    for c, v in acc.get("copy", {}).items():
-        top = max(v)
-        acc["copy"][c] = [x for x in v if x >= 0.5 * top]
-    mean = {k: {c: statistics.mean(v) for c, v in cs.items()} for k, cs in acc.items()}
-    out = {"sources_sha256": sources_digest(), "counters_kib_per_dispatch": mean,
-           "calibration_copy_bytes": calib_bytes}
+    per_db = _pmc_dispatches(dirs)
+    layer = {}
+    for rows in per_db:
+        for _, n, c in rows:
+            if LAYER_KERNEL in n:
+                for k, v in c.items():
+                    layer.setdefault(k, []).append(v)
+    mean = {k: statistics.mean(v) for k, v in layer.items()}
+    scale = _copy_scale(per_db, calib_bytes)
+    out = {"sources_sha256": sources_digest(), "layer_kib_per_dispatch": mean,
+           "calibration_copy_bytes": calib_bytes, "scale": scale}
     try:
-        fetch_f = (calib_bytes / 2) / (mean["copy"]["FETCH_SIZE"] * 1024)
-        write_f = (calib_bytes / 2) / (mean["copy"]["WRITE_SIZE"] * 1024)
-        out["scale"] = {"FETCH_SIZE": fetch_f, "WRITE_SIZE": write_f}
-        out["traffic_bytes_per_launch"] = int(mean["layer"]["FETCH_SIZE"] * 1024 * fetch_f +
-                                              mean["layer"]["WRITE_SIZE"] * 1024 * write_f)
-    except (KeyError, ZeroDivisionError):
+        out["traffic_bytes_per_launch"] = int(mean["FETCH_SIZE"] * 1024 * scale["FETCH_SIZE"] +
+                                              mean["WRITE_SIZE"] * 1024 * scale["WRITE_SIZE"])
+    except KeyError:
         out["traffic_bytes_per_launch"] = None
     return out
 
@@ -141,6 +165,64 @@ def cpu_baseline(layer, reps):
     }
 
 
+def pmc_kernels(dirs, calib_bytes):
+    """Per-kernel counter table of this library's kernels (names with mk2::), from
+    rocprofv3 databases: a --kernel-trace run (durations) and --pmc runs.  HBM bytes are
+    FETCH_SIZE and WRITE_SIZE scaled by the calibration copy's factors (as in the
+    traffic record), and, where collected, TCC_EA0_RDREQ_DRAM_32B and
+    TCC_EA0_WRREQ_WRITE_DRAM_32B x 32 B; MFMA busy is SQ_VALU_MFMA_BUSY_CYCLES over
+    GRBM_GUI_ACTIVE x SIMDs; MFMA FLOP from the MOPS counters (512 FLOP a count)."""
+    import glob
+    import sqlite3
+    from collections import defaultdict
+
+    dur = defaultdict(list)
+    for d in dirs:
+        for f in glob.glob(os.path.join(d, "**", "*.db"), recursive=True):
+            db = sqlite3.connect(f)
+            tables = {r[0] for r in db.execute("select name from sqlite_master where type in ('table','view')")}
+            has_pmc = "pmc_events" in tables and db.execute("select count(*) from pmc_events").fetchone()[0]
+            if "kernels" in tables and not has_pmc:  # durations from the trace run only
+                for name, ns in db.execute("select name, duration from kernels"):
+                    if "mk2::" in name:
+                        dur[name].append(ns)
+    per_db = _pmc_dispatches(dirs)
+    pmc = defaultdict(lambda: defaultdict(list))
+    for rows in per_db:
+        for _, name, c in rows:
+            if "mk2::" in name:
+                for k, v in c.items():
+                    pmc[name][k].append(v)
+    scale = _copy_scale(per_db, calib_bytes)
+    simds = 4 * 256
+    out = []
+    for name in sorted(set(dur) | set(pmc), key=lambda n: -sum(dur.get(n, [0]))):
+        m = {c: statistics.mean(v) for c, v in pmc.get(name, {}).items()}
+        us = statistics.mean(dur[name]) / 1000 if dur.get(name) else None
+        row = {"kernel": name.split("(")[0].replace("void ", ""), "calls": len(dur.get(name, [])),
+               "avg_us": round(us, 2) if us else None}
+        if "FETCH_SIZE" in m and "WRITE_SIZE" in m and len(scale) == 2:
+            rd = m["FETCH_SIZE"] * 1024 * scale["FETCH_SIZE"]
+            wr = m["WRITE_SIZE"] * 1024 * scale["WRITE_SIZE"]
+            row["read_mb"], row["write_mb"] = round(rd / 1e6, 2), round(wr / 1e6, 2)
+            if us:
+                row["hbm_gbs"] = round((rd + wr) / (us * 1e-6) / 1e9, 1)
+        if "TCC_EA0_RDREQ_DRAM_32B" in m:
+            row["dram32_read_mb"] = round(m["TCC_EA0_RDREQ_DRAM_32B"] * 32 / 1e6, 2)
+        if "TCC_EA0_WRREQ_WRITE_DRAM_32B" in m:
+            row["dram32_write_mb"] = round(m["TCC_EA0_WRREQ_WRITE_DRAM_32B"] * 32 / 1e6, 2)
+        if m.get("GRBM_GUI_ACTIVE") and "SQ_VALU_MFMA_BUSY_CYCLES" in m:
+            row["mfma_busy_pct"] = round(100.0 * m["SQ_VALU_MFMA_BUSY_CYCLES"] / (m["GRBM_GUI_ACTIVE"] * simds), 2)
+        mops = {c[len("SQ_INSTS_VALU_MFMA_MOPS_"):]: v * 512 for c, v in m.items()
+                if c.startswith("SQ_INSTS_VALU_MFMA_MOPS_") and v}
+        if mops and us:
+            row["mfma_tflops"] = {k: round(v / (us * 1e-6) / 1e12, 2) for k, v in mops.items()}
+        if "SQ_LDS_BANK_CONFLICT" in m:
+            row["lds_bank_conflict_cycles"] = round(m["SQ_LDS_BANK_CONFLICT"])
+        out.append(row)
+    return {"sources_sha256": sources_digest(), "scale": scale, "kernels": out}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -157,7 +239,12 @@ def main():
                     help="no GPU: summarize rocprofv3 --pmc databases into the traffic record")
     ap.add_argument("--calib-bytes", type=int, default=512 << 20,
                     help="bytes the calibration copy moves (read + write)")
+    ap.add_argument("--pmc-kernels", nargs="+", metavar="DIR",
+                    help="no GPU: per-kernel table (durations, HBM bytes, MFMA busy) from rocprofv3 databases")
     args = ap.parse_args()
+    if args.pmc_kernels:
+        print(json.dumps(pmc_kernels(args.pmc_kernels, args.calib_bytes), indent=1))
+        return
     if args.pmc_summary:
         rec = pmc_summary(args.pmc_summary, args.calib_bytes)
         print(json.dumps(rec, indent=1))

@@ -107,8 +107,10 @@ int mk2_moe_workspace_bytes(const mk2_moe_shape* shape, size_t* bytes);
 int mk2_moe_launch(const mk2_moe_args* args, mk2_stream_t stream);
 
 /* ------------------------------------------------------------ indexer + top-k
- * Index cache pages: [pages][64 tokens][64 B E2M1 codes] followed by
- * [64 tokens][4 B E8M0, one per 32 dims]: 4352 B a page.  Page table int32
+ * Index cache: SGLang's FP4 index plane, read in place (reference:
+ * deepseek_v41/gfx950/indexer/score_fp4.py:9-12,45-49).  cache: E2M1 codes
+ * [pages][4 chunks of 32 dims][64 tokens][16 B], 4096 B a page; cache_scale:
+ * E8M0 [pages][4 chunks][64], token t's scale at (t % 16) * 4 + t / 16.  Page table int32
  * [requests][table_stride], logical page -> physical page.  Row r scores the
  * context positions 0 .. ctx_len[r]-1 of request req_ids[r]. */
 typedef struct mk2_indexer_shape {
@@ -124,7 +126,8 @@ typedef struct mk2_indexer_args {
   mk2_indexer_shape shape;
   const void* q;            /* bf16 [rows][heads][128] */
   const void* w;            /* bf16 [rows][heads] head weights */
-  const uint8_t* cache;     /* index pages */
+  const uint8_t* cache;     /* E2M1 plane [pages][4][64][16] */
+  const uint8_t* cache_scale;/* E8M0 plane [pages][4][64] */
   const int32_t* page_table;/* [requests][table_stride] */
   const int32_t* req_ids;   /* [rows] */
   const int32_t* ctx_len;   /* [rows] */
@@ -140,7 +143,8 @@ int mk2_indexer_topk_launch(const mk2_indexer_args* args, mk2_stream_t stream);
 
 /* --------------------------------------------------------------- sparse MLA
  * Latent KV pages: [pages][64 tokens][576 B E4M3] with one f32 scale per token
- * in kv_scale [pages][64].  Row r attends the positions sel[r][0..topk-1] (-1 =
+ * in kv_scale [pages][64], or kv_scale NULL for SGLang's unscaled MLA cache
+ * [slots][576] e4m3 (reference: glm53/spec.py:542-547), read as scale 1.  Row r attends the positions sel[r][0..topk-1] (-1 =
  * unused) of request req_ids[r]; then W_UV (bf16 [heads][v_dim][512]) and W_o
  * (bf16 tiles of [hidden, heads*v_dim]); out = bf16(h + o W_o^T) (h may be NULL). */
 typedef struct mk2_mla_shape {
@@ -159,7 +163,7 @@ typedef struct mk2_mla_args {
   mk2_mla_shape shape;
   const void* q;            /* bf16 [rows][heads][576] (W_UK absorbed) */
   const uint8_t* kv;        /* latent KV pages */
-  const float* kv_scale;    /* [pages][64] */
+  const float* kv_scale;    /* [pages][64], or NULL (scale 1) */
   const int32_t* page_table;
   const int32_t* req_ids;   /* [rows] */
   const int32_t* sel;       /* [rows][topk] positions */

@@ -80,12 +80,13 @@ size_t idx_carve(const mk2_indexer_shape* s, void* base, IdxDev* d) {
 int idx_fill(const mk2_indexer_args* a, IdxDev* d) {
   int rc = idx_check_shape(&a->shape);
   if (rc) return rc;
-  MK2_REQUIRE(a->q && a->w && a->cache && a->page_table && a->req_ids && a->ctx_len,
-              "indexer: q, w, cache, page_table, req_ids and ctx_len must be set");
+  MK2_REQUIRE(a->q && a->w && a->cache && a->cache_scale && a->page_table && a->req_ids && a->ctx_len,
+              "indexer: q, w, cache, cache_scale, page_table, req_ids and ctx_len must be set");
   *d = IdxDev{};
   d->rows = a->shape.rows; d->heads = a->shape.heads; d->topk = a->shape.topk;
   d->max_ctx = a->shape.max_ctx; d->stride = a->shape.table_stride;
   d->q = (const bf16_t*)a->q; d->w = (const bf16_t*)a->w; d->cache = a->cache;
+  d->cscale = a->cache_scale;
   d->pt = a->page_table; d->req = a->req_ids; d->ctx = a->ctx_len;
   d->scores = a->scores; d->out = a->topk;
   d->nchk = (d->max_ctx + IDX_CHUNK - 1) / IDX_CHUNK;

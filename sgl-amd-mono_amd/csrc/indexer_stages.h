@@ -33,7 +33,10 @@
 namespace mk2 {
 
 constexpr int IDX_PAGE = 64;
-constexpr int IDX_PAGE_BYTES = 64 * 64 + 64 * 4;  // codes, then E8M0
+// SGLang's FP4 index plane: a 64-key page is [4 chunks of 32 dims][64 keys][16 B] of
+// E2M1 codes, and apart from it [4 chunks][64] E8M0 scales, key k's at (k % 16) * 4 + k / 16
+constexpr int IDX_PAGE_CODES = 64 * 64;
+constexpr int IDX_PAGE_SCALES = 64 * 4;
 constexpr int IDX_CHUNK = 2048;                    // positions a score task
 constexpr int TOPK_NT = 1024;                      // top-k workgroup of the standalone launch
 
@@ -44,7 +47,8 @@ struct IdxDev {
   int rows, heads, topk, max_ctx, stride, nchk;
   const bf16_t* q;      // [rows][heads][128]
   const bf16_t* w;      // [rows][heads]
-  const uint8_t* cache; // pages
+  const uint8_t* cache; // E2M1 plane [pages][4][64][16 B]
+  const uint8_t* cscale;// E8M0 plane [pages][4][64]
   const int* pt;        // [requests][stride]
   const int* req;       // [rows]
   const int* ctx;       // [rows]
@@ -117,19 +121,25 @@ MK2_DEV void idx_score(const IdxDev& p, int r, int chunk, IdxScoreLds& L) {
   // plus a per-lane offset plus an immediate, no vector address arithmetic
   constexpr int PPW = GPW / 4;
   const uint8_t* pbase[PPW];
+  const uint8_t* sbase[PPW];
 #pragma unroll
-  for (int q = 0; q < PPW; ++q)
-    pbase[q] = p.cache + (size_t)__builtin_amdgcn_readfirstlane(lds_pages[gw0 / 4 + q]) * IDX_PAGE_BYTES;
-  const uint32_t off_code = c16 * 64 + 16 * g, off_scale = 4096 + c16 * 4;
+  for (int q = 0; q < PPW; ++q) {
+    const size_t pg = __builtin_amdgcn_readfirstlane(lds_pages[gw0 / 4 + q]);
+    pbase[q] = p.cache + pg * IDX_PAGE_CODES;
+    sbase[q] = p.cscale + pg * IDX_PAGE_SCALES;
+  }
+  // lane (c16, g) of group j holds chunk g of key 16 (j & 3) + c16; one scale dword a
+  // page holds the lane's four keys' E8M0 bytes (j & 3 = 0..3)
+  const uint32_t off_code = g * 1024 + c16 * 16, off_scale = g * 64 + c16 * 4;
   uint4 code[GPW];
-  uint32_t sw[GPW];
+  uint32_t sw[PPW];
   // a rolling window of KWIN key groups in flight: group j + KWIN - 1 is issued as
   // group j is widened (a full window of 16 a wave, 160 KiB a CU at once, delays every
   // CU's first groups behind the whole chip's requests)
   constexpr int KWIN = 4;
   auto issue = [&](int j) {
-    code[j] = *(const uint4*)(pbase[j >> 2] + off_code + (j & 3) * 1024);
-    sw[j] = *(const uint32_t*)(pbase[j >> 2] + off_scale + (j & 3) * 64);
+    code[j] = *(const uint4*)(pbase[j >> 2] + off_code + (j & 3) * 256);
+    if ((j & 3) == 0) sw[j >> 2] = *(const uint32_t*)(sbase[j >> 2] + off_scale);
   };
 #pragma unroll
   for (int j = 0; j < KWIN; ++j) issue(j);
@@ -160,7 +170,7 @@ MK2_DEV void idx_score(const IdxDev& p, int r, int chunk, IdxScoreLds& L) {
   // j's head sums, so that the matrix cores and the vector ALUs overlap
   auto keys = [&](int j, bf16x8* kb) {
     if (j >= 1 && j + KWIN - 1 < GPW) issue(j + KWIN - 1);
-    const float sc = e8m0_to_f32(sw[j] >> (8 * g));
+    const float sc = e8m0_to_f32(sw[j >> 2] >> (8 * (j & 3)));
     kb[0] = e2m1x8_to_bf16(code[j].x, sc);
     kb[1] = e2m1x8_to_bf16(code[j].y, sc);
     kb[2] = e2m1x8_to_bf16(code[j].z, sc);

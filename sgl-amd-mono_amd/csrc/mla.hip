@@ -50,8 +50,8 @@ int mla_fill(const mk2_mla_args* a, MlaDev* d) {
   const mk2_mla_shape* s = &a->shape;
   int rc = mla_check_shape(s);
   if (rc) return rc;
-  MK2_REQUIRE(a->q && a->kv && a->kv_scale && a->page_table && a->req_ids && a->w_uv && a->w_o,
-              "mla: q, kv, kv_scale, page_table, req_ids, w_uv and w_o must be set");
+  MK2_REQUIRE(a->q && a->kv && a->page_table && a->req_ids && a->w_uv && a->w_o,
+              "mla: q, kv, page_table, req_ids, w_uv and w_o must be set");
   *d = MlaDev{};
   d->rows = s->rows; d->v_dim = s->v_dim; d->hidden = s->hidden; d->topk = s->topk;
   d->stride = s->table_stride; d->sm_scale = s->sm_scale;

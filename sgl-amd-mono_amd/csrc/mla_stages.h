@@ -33,7 +33,7 @@ struct MlaDev {
   float sm_scale;
   const bf16_t* q;       // [rows][16][576]
   const uint8_t* kv;     // [pages][64][576]
-  const float* kv_scale; // [pages][64]
+  const float* kv_scale; // [pages][64]; null: unscaled E4M3 (scale 1)
   const int* pt;
   const int* req;
   const int* sel;        // [rows][topk]
@@ -88,7 +88,7 @@ MK2_DEV void mla_split(const MlaDev& p, int r, int s, MlaSplitLds& L) {
   float ksc = 0.f;
   if (tid < MLA_SPLIT) {
     const int row = L.row[tid];
-    ksc = row >= 0 ? p.kv_scale[row] : 0.f;
+    ksc = row < 0 ? 0.f : (p.kv_scale ? p.kv_scale[row] : 1.f);
   }
   // gather: job = (4-key group kg, 16-byte dim chunk dc), 16 x 36 jobs; every load of
   // a thread is issued before the first LDS store

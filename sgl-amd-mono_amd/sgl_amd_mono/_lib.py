@@ -61,7 +61,7 @@ class IndexerShape(ctypes.Structure):
 
 class IndexerArgs(ctypes.Structure):
     _fields_ = [
-        ("shape", IndexerShape), ("q", c_void_p), ("w", c_void_p), ("cache", c_void_p),
+        ("shape", IndexerShape), ("q", c_void_p), ("w", c_void_p), ("cache", c_void_p), ("cache_scale", c_void_p),
         ("page_table", c_void_p), ("req_ids", c_void_p), ("ctx_len", c_void_p),
         ("scores", c_void_p), ("topk", c_void_p),
         ("workspace", c_void_p), ("workspace_bytes", c_size_t),

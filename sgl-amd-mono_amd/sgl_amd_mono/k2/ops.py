@@ -81,11 +81,12 @@ class IndexerOp:
         _lib.check(_lib.lib().mk2_indexer_workspace_bytes(ctypes.byref(self.shape), ctypes.byref(nbytes)))
         self.workspace = torch.empty(nbytes.value, dtype=torch.uint8, device=self.device)
 
-    def __call__(self, q, w, cache, page_table, req_ids, ctx_len, scores=None, topk=None):
+    def __call__(self, q, w, cache, cache_scale, page_table, req_ids, ctx_len, scores=None, topk=None):
         cfg, rows = self.cfg, self.rows
         _need(q, "q", torch.bfloat16, (rows, cfg.heads, cfg.dim))
         _need(w, "w", torch.bfloat16, (rows, cfg.heads))
         _need(cache, "cache", torch.uint8)
+        _need(cache_scale, "cache_scale", torch.uint8)
         _need(page_table, "page_table", torch.int32)
         if page_table.shape[1] != self.shape.table_stride:
             raise ValueError("page_table row stride differs from the op's table_stride")
@@ -98,7 +99,7 @@ class IndexerOp:
         _need(scores, "scores", torch.float32, (rows, cfg.context))
         _need(topk, "topk", torch.int32, (rows, cfg.topk))
         args = _lib.IndexerArgs(
-            self.shape, _p(q), _p(w), _p(cache), _p(page_table), _p(req_ids), _p(ctx_len),
+            self.shape, _p(q), _p(w), _p(cache), _p(cache_scale), _p(page_table), _p(req_ids), _p(ctx_len),
             _p(scores), _p(topk), _p(self.workspace), self.workspace.numel(),
         )
         _lib.check(_lib.lib().mk2_indexer_topk_launch(ctypes.byref(args), _lib.stream_handle(self.device)))
@@ -125,7 +126,8 @@ class SparseMlaOp:
         cfg, rows = self.cfg, self.rows
         _need(q, "q", torch.bfloat16, (rows, cfg.heads, cfg.qk_dim))
         _need(kv, "kv", torch.uint8)
-        _need(kv_scale, "kv_scale", torch.float32)
+        if kv_scale is not None:  # None: SGLang's unscaled E4M3 MLA cache
+            _need(kv_scale, "kv_scale", torch.float32)
         _need(page_table, "page_table", torch.int32)
         _need(req_ids, "req_ids", torch.int32, (rows,))
         _need(sel, "sel", torch.int32, (rows, cfg.topk))
@@ -171,7 +173,7 @@ class LayerOp:
                    topk_ids=None, topk_weights=None, workspace=None, status=None, timeline=None):
         L = self.L
         ia = _lib.IndexerArgs(
-            self.idx.shape, _p(L.idx.q), _p(L.idx.w), _p(L.idx.cache), _p(L.idx.page_table),
+            self.idx.shape, _p(L.idx.q), _p(L.idx.w), _p(L.idx.cache), _p(L.idx.cache_scale), _p(L.idx.page_table),
             _p(L.idx.req_ids), _p(L.idx.ctx_len), _p(scores), _p(topk), None, 0,
         )
         ma = _lib.MlaArgs(

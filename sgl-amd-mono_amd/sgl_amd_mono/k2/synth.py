@@ -89,6 +89,16 @@ def _page_table(g, requests: int, pages_per_req: int, device) -> torch.Tensor:
     return perm.view(requests, pages_per_req).to(torch.int32).contiguous()
 
 
+def index_plane(codes: torch.Tensor, scales: torch.Tensor):
+    """Token-major FP4 keys (codes [P, 64, 64], E8M0 [P, 64, 4]) -> SGLang's FP4 index
+    plane: codes [P, 4 chunks, 64 tokens, 16 B] and scales [P, 4 chunks, 64] with token
+    t's byte at (t % 16) * 4 + t // 16 (score_fp4.py:9-12, the deepseek_v4 memory pool)."""
+    P = codes.shape[0]
+    plane = codes.view(P, 64, 4, 16).permute(0, 2, 1, 3).reshape(P, 4096).contiguous()
+    sc = scales.view(P, 4, 16, 4).permute(0, 3, 2, 1).reshape(P, 256).contiguous()
+    return plane, sc
+
+
 def make_indexer(cfg: C.IndexerConfig, rows: int, seed: int, device, ctx_len=None):
     """FP4 index-key pages (E2M1 codes + E8M0 per 32 dims), bf16 queries and head
     weights ~ N(0, 1), one request a row."""
@@ -102,7 +112,7 @@ def make_indexer(cfg: C.IndexerConfig, rows: int, seed: int, device, ctx_len=Non
     n_pages = rows * ppr + 1
     keys = _randn(g, n_pages, C.PAGE, cfg.dim, device=device)
     codes, scales = quant_mxfp4(keys)  # [P, 64, 64], [P, 64, 4]
-    ns.cache = torch.cat([codes.view(n_pages, -1), scales.view(n_pages, -1)], dim=1).contiguous()
+    ns.cache, ns.cache_scale = index_plane(codes, scales)
     ns.req_ids = torch.arange(rows, dtype=torch.int32, device=device)
     if ctx_len is None:
         ctx_len = [ctx] * rows

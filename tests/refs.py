@@ -97,13 +97,19 @@ class MoEOracle:
         )
 
 
-def index_keys_f32(cache, page_table, req, n, dim=128):
-    """Dequantized FP4 keys of positions 0..n-1 of request `req` (oracle decoders)."""
-    cache, page_table = cpu(cache), cpu(page_table)
+def index_keys_f32(cache, cache_scale, page_table, req, n, dim=128):
+    """Dequantized FP4 keys of positions 0..n-1 of request `req` (oracle decoders), read
+    from SGLang's FP4 index plane (score_fp4.py:9-12): token t of a page has its 16 code
+    bytes of chunk c at c * 1024 + t * 16 and that chunk's E8M0 at c * 64 + (t % 16) * 4
+    + t // 16 of the page's scale row."""
+    cache, cache_scale, page_table = cpu(cache), cpu(cache_scale), cpu(page_table)
     pages = page_table[req, : (n + 63) // 64].long()
-    raw = cache[pages]  # [np, 4352]
-    codes = raw[:, :4096].reshape(-1, 64, 64)
-    scales = raw[:, 4096:].reshape(-1, 64, 4)
+    t = torch.arange(64)
+    codes = torch.empty(len(pages), 64, 64, dtype=torch.uint8)
+    scales = torch.empty(len(pages), 64, 4, dtype=torch.uint8)
+    for c in range(4):
+        codes[:, :, 16 * c : 16 * c + 16] = cache[pages][:, c * 1024 : (c + 1) * 1024].reshape(-1, 64, 16)
+        scales[:, :, c] = cache_scale[pages][:, c * 64 + (t % 16) * 4 + t // 16]
     keys = oc.mxfp4_dequant(codes, scales).reshape(-1, dim)
     return keys[:n]
 
@@ -111,7 +117,7 @@ def index_keys_f32(cache, page_table, req, n, dim=128):
 def indexer_oracle_scores(ns, r):
     """f64 scores of row r of a synth indexer namespace."""
     n = int(ns.ctx_len[r])
-    keys = index_keys_f32(ns.cache, ns.page_table, int(ns.req_ids[r]), n)
+    keys = index_keys_f32(ns.cache, ns.cache_scale, ns.page_table, int(ns.req_ids[r]), n)
     return R.index_scores(cpu(ns.q[r]).float(), cpu(ns.w[r]).float(), keys)
 
 
@@ -119,7 +125,8 @@ def mla_oracle(ns, sel=None, h="auto"):
     """(o_lat f32 [rows, 16, 512], out f32-of-bf16 [rows, hidden]) of a synth MLA case."""
     cfg = ns.cfg
     sel = cpu(ns.sel if sel is None else sel).long()
-    kv, ksc, pt = cpu(ns.kv), cpu(ns.kv_scale), cpu(ns.page_table)
+    kv, pt = cpu(ns.kv), cpu(ns.page_table)
+    ksc = torch.ones(kv.shape[:2]) if ns.kv_scale is None else cpu(ns.kv_scale)
     q, w_uv, w_o = cpu(ns.q).float(), cpu(ns.w_uv).float(), cpu(ns.w_o).float()
     hres = cpu(ns.h) if h == "auto" else (cpu(h) if h is not None else None)
     olats, outs = [], []
@@ -182,7 +189,7 @@ class CpuLayer:
         self.mla = SimpleNamespace(**{k: cpu(v) if torch.is_tensor(v) else v for k, v in vars(L.mla).items()})
         self.h = cpu(L.h)
         self.moe = MoEOracle(L.moe)
-        self.keys = [index_keys_f32(self.idx.cache, self.idx.page_table, int(self.idx.req_ids[r]),
+        self.keys = [index_keys_f32(self.idx.cache, self.idx.cache_scale, self.idx.page_table, int(self.idx.req_ids[r]),
                                     int(self.idx.ctx_len[r])) for r in range(self.rows)]
         self.moe.dequant_all()
 

@@ -61,7 +61,7 @@ def test_gpu_golden_indexer():
     ns = G.to_device(ns0, dev)
     cfg = C.IndexerConfig(**meta["cfg"])
     op = IndexerOp(cfg, len(meta["ctx_len"]), ns.page_table.shape[1], device=dev)
-    scores, topk = op(ns.q, ns.w, ns.cache, ns.page_table, ns.req_ids, ns.ctx_len)
+    scores, topk = op(ns.q, ns.w, ns.cache, ns.cache_scale, ns.page_table, ns.req_ids, ns.ctx_len)
     torch.cuda.synchronize()
     for r, n in enumerate(meta["ctx_len"]):
         ref = exp["scores"][r, :n].double()

@@ -34,19 +34,20 @@ def _run(cfg, rows, seed, ctx_len=None, mode="random"):
     dev = _dev()
     ns = synth.make_indexer(cfg, rows, seed, dev, ctx_len=ctx_len)
     if mode == "ties":
-        codes, scales = ns.cache[1, :64].clone(), ns.cache[1, 4096:4100].clone()
-        ns.cache[:, :4096] = codes.repeat(64)
-        ns.cache[:, 4096:] = scales.repeat(64)
+        # every key = token 0 of page 1 (its chunk-c codes at c * 1024, scale at c * 64)
+        v, s = ns.cache.view(-1, 4, 64, 16), ns.cache_scale.view(-1, 4, 64)
+        v[:] = v[1, :, :1].clone()
+        s[:] = s[1, :, :1].clone()
     elif mode == "zeros":
-        ns.cache[:, :4096] = 0
+        ns.cache.zero_()
     elif mode == "recent":  # the last 4096 positions of every row score 16x higher
         for r in range(rows):
             n = int(ns.ctx_len[r])
             pages = ns.page_table[r, (n - 4096) // 64 : n // 64].long()
-            sc = ns.cache[pages, 4096:]
-            ns.cache[pages, 4096:] = (sc.int() + 4).clamp(max=254).to(torch.uint8)
+            sc = ns.cache_scale[pages]
+            ns.cache_scale[pages] = (sc.int() + 4).clamp(max=254).to(torch.uint8)
     op = IndexerOp(cfg, rows, ns.page_table.shape[1], device=dev)
-    scores, topk = op(ns.q, ns.w, ns.cache, ns.page_table, ns.req_ids, ns.ctx_len)
+    scores, topk = op(ns.q, ns.w, ns.cache, ns.cache_scale, ns.page_table, ns.req_ids, ns.ctx_len)
     torch.cuda.synchronize()
     return ns, cpu(scores), cpu(topk).long()
 

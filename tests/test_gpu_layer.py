@@ -96,7 +96,7 @@ def test_persistent_layer_one_workspace_new_inputs():
     cfg = C.C5_LAYER
     A = synth.make_layer(cfg, 8, 777, dev)
     B = synth.make_layer(cfg, 8, 778, dev)
-    step = lambda L: [L.idx.q, L.idx.w, L.idx.cache, L.mla.q, L.mla.kv, L.mla.kv_scale, L.h]  # noqa: E731
+    step = lambda L: [L.idx.q, L.idx.w, L.idx.cache, L.idx.cache_scale, L.mla.q, L.mla.kv, L.mla.kv_scale, L.h]  # noqa: E731
     saved = [t.clone() for t in step(A)]
     p_op = LayerOp(cfg, A, 8, device=dev)
     s_op = LayerOp(cfg, A, 8, device=dev, staged=True)

@@ -22,7 +22,7 @@ def _dev():
     return torch.device("cuda:0")
 
 
-def _run(cfg, rows, seed, residual=True, holes=False):
+def _run(cfg, rows, seed, residual=True, holes=False, unscaled=False):
     from sgl_amd_mono.k2 import synth
     from sgl_amd_mono.k2.ops import SparseMlaOp
 
@@ -31,6 +31,8 @@ def _run(cfg, rows, seed, residual=True, holes=False):
     if holes:  # unused slots (-1) inside and at the end of the list
         ns.sel[:, 5:70] = -1
         ns.sel[0, -64:] = -1
+    if unscaled:  # SGLang's MLA cache: E4M3 rows without per-token scales
+        ns.kv_scale = None
     op = SparseMlaOp(cfg, ns, rows, ns.page_table.shape[1], device=dev)
     olat = torch.empty(rows, cfg.heads, cfg.kv_lora, dtype=torch.float32, device=dev)
     out = op(ns.q, ns.kv, ns.kv_scale, ns.page_table, ns.req_ids, ns.sel, h=ns.h, o_latent=olat)
@@ -63,3 +65,23 @@ def test_mla_32_rows():
     cfg = C.MlaConfig(context=4096, topk=2048)
     e_lat, e_out = _run(cfg, 32, seed=320)
     assert e_lat <= REL_L2 and e_out <= REL_L2, (e_lat, e_out)
+
+
+def test_mla_unscaled_cache():
+    """kv_scale None (SGLang's [slots][576] e4m3 cache) reads every row at scale 1:
+    the oracle over unit scales, and bit-identical to passing a tensor of ones."""
+    from sgl_amd_mono.k2 import config as C
+    from sgl_amd_mono.k2 import synth
+    from sgl_amd_mono.k2.ops import SparseMlaOp
+
+    cfg = C.MlaConfig(context=8192, topk=1024)
+    e_lat, e_out = _run(cfg, 4, seed=330, unscaled=True)
+    assert e_lat <= REL_L2 and e_out <= REL_L2, (e_lat, e_out)
+    dev = _dev()
+    ns = synth.make_mla(cfg, 4, 331, dev)
+    op = SparseMlaOp(cfg, ns, 4, ns.page_table.shape[1], device=dev)
+    ones = torch.ones_like(ns.kv_scale)
+    a = op(ns.q, ns.kv, None, ns.page_table, ns.req_ids, ns.sel, h=ns.h).clone()
+    b = op(ns.q, ns.kv, ones, ns.page_table, ns.req_ids, ns.sel, h=ns.h)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)

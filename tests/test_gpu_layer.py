@@ -61,18 +61,22 @@ def test_layer_small_context_32_rows():
     print(check_layer(L, *res))
 
 
-def test_persistent_layer_repeats_and_matches_staged():
+@pytest.mark.parametrize("rows", [8, 32])
+def test_persistent_layer_repeats_and_matches_staged(rows):
     """Back-to-back persistent launches (counters reset by the launch itself) give the
-    same bits each time and the same bits as the stage-by-stage path."""
+    same bits each time and the same bits as the stage-by-stage path -- also at the
+    verify width, 32 rows over the full 65536-position context, where every workgroup
+    runs four score chunks and four slices and the up/gate and down take two column
+    groups."""
     from sgl_amd_mono.k2 import config as C
     from sgl_amd_mono.k2 import synth
     from sgl_amd_mono.k2.ops import LayerOp
 
     dev = _dev()
     cfg = C.C5_LAYER
-    L = synth.make_layer(cfg, 8, 777, dev)
-    p_op = LayerOp(cfg, L, 8, device=dev)
-    s_op = LayerOp(cfg, L, 8, device=dev, staged=True)
+    L = synth.make_layer(cfg, rows, 777, dev)
+    p_op = LayerOp(cfg, L, rows, device=dev)
+    s_op = LayerOp(cfg, L, rows, device=dev, staged=True)
     status = torch.full((1,), -1, dtype=torch.int32, device=dev)
     outs = [p_op(status=status).clone() for _ in range(3)]
     ref = s_op()

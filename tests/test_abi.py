@@ -100,5 +100,12 @@ def test_launch_argument_errors_never_reach_the_device():
     assert "NULL" in L.mk2_last_error().decode()
     assert L.mk2_sparse_mla_launch(None, None) == _l.MK2_EINVAL
     assert L.mk2_indexer_topk_launch(None, None) == _l.MK2_EINVAL
+    # the FP4 index plane's scales are required (pointers below are never dereferenced:
+    # the arguments are rejected first)
+    fake = 0x1000
+    ia = _l.IndexerArgs(_l.IndexerShape(8, 64, 128, 2048, 65536, 1024), fake, fake, fake, None, fake, fake,
+                        fake, None, None, fake, 1 << 30)
+    assert L.mk2_indexer_topk_launch(ctypes.byref(ia), None) == _l.MK2_EINVAL
+    assert "cache_scale" in L.mk2_last_error().decode()
     assert L.mk2_layer_launch(None, None) == _l.MK2_EINVAL
     assert L.mk2_selftest_mfma(9, None, None, None, None, None, None) == _l.MK2_EINVAL

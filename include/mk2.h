@@ -198,7 +198,8 @@ typedef struct mk2_layer_args {
   int mode;                 /* MK2_LAYER_PERSISTENT or MK2_LAYER_STAGED */
   int spin_limit;           /* persistent: polls a dependency wait may take before the
                                launch gives up (0: default, about a second) */
-  int32_t* status;          /* optional device word: 0 ok, 1 a wait gave up */
+  int32_t* status;          /* optional device word: 0 ok, 1 a wait gave up and the
+                               launch stopped (zero the workspace before the next) */
   uint64_t* timeline;       /* optional [grid][31] stage stamps of the persistent launch
                                (100 MHz device clock): per stage enter, input ready, leave */
 } mk2_layer_args;

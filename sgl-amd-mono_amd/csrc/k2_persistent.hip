@@ -132,9 +132,10 @@ MK2_DEV bool k2_signal_last1(const K2Dev& p, int line, int n, int* flag) {
 // within a launch), so a wait that an earlier one already satisfied costs nothing.  The
 // early return is uniform: seen is written only just after this function's barrier,
 // and every task ends with a barrier before the next wait reads it.
-MK2_DEV void k2_wait(const K2Dev& p, int* seen, int line, int target, int stamp = -1, int lanes = 1) {
-  if (seen[line] >= target) return;
+MK2_DEV bool k2_wait(const K2Dev& p, int* seen, int line, int target, int stamp = -1, int lanes = 1) {
+  if (seen[line] >= target) return true;
   int v = 0;
+  bool bad = false;
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
     const int* err = k2_ctr(p, SY_ERR);
@@ -153,139 +154,159 @@ MK2_DEV void k2_wait(const K2Dev& p, int* seen, int line, int target, int stamp 
       v = count(c1);
       if (v >= target) break;
       n += 2;
-      if ((n & 31) == 0 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
+      if ((n & 31) == 0 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+        bad = true;
+        break;
+      }
       if (n > p.spin_limit) {
         if (lane == 0) atomicOr(k2_ctr(p, SY_ERR), 1);
+        bad = true;
         break;
       }
     }
     if (lane == 0 && stamp >= 0 && p.timeline)
       p.timeline[(size_t)blockIdx.x * K2_STAMPS + stamp] = __builtin_amdgcn_s_memrealtime();
+    if (lane == 0) seen[SY_LINES] = bad;  // the workgroup's fail-stop flag
   }
   __syncthreads();
-  if (threadIdx.x == 0) seen[line] = v;
+  const bool ok = seen[SY_LINES] == 0;
+  __syncthreads();  // the flag is read before the next wait can write it
+  if (threadIdx.x == 0 && ok) seen[line] = v;
+  return ok;
 }
 
 template <int NCG>
 __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
   __shared__ K2Lds S;
-  __shared__ int seen[SY_LINES];
+  __shared__ int seen[SY_LINES + 1];  // counts seen by line; [SY_LINES]: a wait failed
   __shared__ int last_flag;
   const int G = gridDim.x, b = blockIdx.x;
   const int R = p.rows;
-  for (int i = threadIdx.x; i < SY_LINES; i += K2_NT) seen[i] = 0;
+  for (int i = threadIdx.x; i <= SY_LINES; i += K2_NT) seen[i] = 0;
   __syncthreads();
-  int base = 0;  // this stage's first workgroup
-// the tasks of a stage of n tasks on this workgroup; `t < G` marks the first
+  // the stages in order; a wait that fails (its spin limit, or another workgroup's
+  // failure seen while polling) returns from the walk: the workgroup skips every task
+  // left and goes straight to the counter reset (fail-stop)
+  auto walk = [&]() {
+    int base = 0;  // this stage's first workgroup
+    // the tasks of a stage of n tasks on this workgroup; `t < G` marks the first
 #define K2_TASKS(t, n) for (int t = (b - base % G + G) % G; t < (n); t += G)
 #define K2_NEXT(n) base = (base + (n)) % G
-  int st = 0;  // timeline stage
-  // ---- index scores + row key histograms
-  k2_stamp(p, 3 * st);
-  const int nchk = p.idx.nchk;
-  K2_TASKS(t, R * nchk) {
-    idx_score<K2_NT>(p.idx, t / nchk, t % nchk, S.score);
-    k2_signal(p, SY_SCORE + t / nchk);
-  }
-  k2_stamp(p, 3 * st++ + 2);
-  // ---- top-k slices: each chunk lists its keys above the row's threshold bin and
-  // keeps its keys in the bin
-  k2_stamp(p, 3 * st);
-  // slices on the workgroups of their score chunks (base unchanged); the last slice
-  // of a row finishes the row's list from the keys in the threshold bin
-  K2_TASKS(t, R * nchk) {
-    const int r = t / nchk;
-    k2_wait(p, seen, SY_SCORE + r, nchk, t < G ? 3 * st + 1 : -1);
-    const bool known = idx_slice<K2_NT>(p.idx, r, t % nchk, S.topk, p.spin_limit, k2_ctr(p, SY_ERR));
-    if (k2_signal_last1(p, SY_SLICE + r, nchk, &last_flag)) {
-      k2_stamp(p, 3 * (st + 1));
-      k2_stamp(p, 3 * (st + 1) + 1);
-      // this workgroup's own slice of row r may have left the threshold in LDS
-      idx_select<K2_NT>(p.idx, r, S.topk, known);
-      k2_signal(p, SY_TOPK + r);
-      k2_stamp(p, 3 * (st + 1) + 2);
-      idx_topk_reset<K2_NT>(p.idx, r);  // every slice of the row is done with them
+    int st = 0;  // timeline stage
+    // ---- index scores + row key histograms
+    k2_stamp(p, 3 * st);
+    const int nchk = p.idx.nchk;
+    K2_TASKS(t, R * nchk) {
+      idx_score<K2_NT>(p.idx, t / nchk, t % nchk, S.score);
+      k2_signal(p, SY_SCORE + t / nchk);
     }
-  }
-  K2_NEXT(R * nchk);
-  k2_stamp(p, 3 * st++ + 2);
-  ++st;  // the select stamps are taken above
-  // ---- sparse-MLA splits
-  k2_stamp(p, 3 * st);
-  const int ns = p.mla.nsplit;
-  K2_TASKS(t, R * ns) {
-    const int r = t / ns;
-    k2_wait(p, seen, SY_TOPK + r, 1, t < G ? 3 * st + 1 : -1);
-    mla_split<K2_NT>(p.mla, r, t % ns, S.split);
-    k2_signal(p, SY_SPLIT + r);
-  }
-  K2_NEXT(R * ns);
-  k2_stamp(p, 3 * st++ + 2);
-  // ---- merge of the splits + W_UV, per (row, head, half of the head's outputs)
-  k2_stamp(p, 3 * st);
-  K2_TASKS(t, 2 * R * MLA_HEADS) {
-    const int r = t / (2 * MLA_HEADS), h = (t >> 1) % MLA_HEADS;
-    mla_merge_uv<K2_NT>(p.mla, r, h, t & 1, S.merge,
-                        [&] { k2_wait(p, seen, SY_SPLIT + r, ns, t < G ? 3 * st + 1 : -1); });
-    k2_signal(p, SY_UV, t, K2_LANES);
-  }
-  K2_NEXT(2 * R * MLA_HEADS);
-  k2_stamp(p, 3 * st++ + 2);
-  // ---- W_o + residual, per 16 hidden rows: tasks t and t + G together (their weights
-  // all in flight before the wait)
-  k2_stamp(p, 3 * st);
-  const int ht = p.mla.hidden / 16;
-  for (int t = (b - base % G + G) % G; t < ht; t += 2 * G) {
-    const int t1 = t + G < ht ? t + G : -1;
-    mla_oproj<K2_NT, NCG, 2>(p.mla, t, t1, S.up.red,
-                             [&] { k2_wait(p, seen, SY_UV, 2 * R * MLA_HEADS, t < G ? 3 * st + 1 : -1, K2_LANES); });
-    k2_signal(p, SY_OPROJ, t, K2_LANES, t1 >= 0 ? 2 : 1);
-  }
-  K2_NEXT(ht);
-  k2_stamp(p, 3 * st++ + 2);
-  // ---- router GEMV (+ RMSNorm of its slice), per (16 experts, hidden slice)
-  k2_stamp(p, 3 * st);
-  const int et = p.moe.E / 16, nrt = et * p.moe.KC;
-  K2_TASKS(t, nrt) {
-    moe_router<K2_NT, NCG>(p.moe, t % et, t / et, S.router,
-                           [&] { k2_wait(p, seen, SY_OPROJ, ht, t < G ? 3 * st + 1 : -1, K2_LANES); });
-    // the last router task computes the routing
-    if (k2_signal_last(p, SY_ROUTER, SY_ROUTER_LAST, t, nrt, &last_flag)) {
-      k2_stamp(p, 3 * (st + 1));
-      k2_stamp(p, 3 * (st + 1) + 1);
-      // SY_ROUTE: 1 once the distinct-expert list is out (up/gate), 2 with the table (down)
-      moe_route<K2_NT>(p.moe, S.route, [&] { k2_signal(p, SY_ROUTE); });
-      k2_signal(p, SY_ROUTE);
-      k2_stamp(p, 3 * (st + 1) + 2);
+    k2_stamp(p, 3 * st++ + 2);
+    // ---- top-k slices: each chunk lists its keys above the row's threshold bin and
+    // keeps its keys in the bin
+    k2_stamp(p, 3 * st);
+    // slices on the workgroups of their score chunks (base unchanged); the last slice
+    // of a row finishes the row's list from the keys in the threshold bin
+    K2_TASKS(t, R * nchk) {
+      const int r = t / nchk;
+      if (!k2_wait(p, seen, SY_SCORE + r, nchk, t < G ? 3 * st + 1 : -1)) return;
+      const bool known = idx_slice<K2_NT>(p.idx, r, t % nchk, S.topk, p.spin_limit, k2_ctr(p, SY_ERR));
+      if (k2_signal_last1(p, SY_SLICE + r, nchk, &last_flag)) {
+        k2_stamp(p, 3 * (st + 1));
+        k2_stamp(p, 3 * (st + 1) + 1);
+        // this workgroup's own slice of row r may have left the threshold in LDS
+        idx_select<K2_NT>(p.idx, r, S.topk, known);
+        k2_signal(p, SY_TOPK + r);
+        k2_stamp(p, 3 * (st + 1) + 2);
+        idx_topk_reset<K2_NT>(p.idx, r);  // every slice of the row is done with them
+      }
     }
-  }
-  K2_NEXT(nrt);
-  k2_stamp(p, 3 * st++ + 2);
-  ++st;  // routing: run by the last router task above
-  // ---- up/gate + SwiGLU: the shared expert's chunks first (they need only the
-  // normalized rows, stored by the router tasks, so they run while routing is still
-  // pending), then the routed slots
-  k2_stamp(p, 3 * st);
-  const int up_r = p.moe.Dmax * (p.moe.I / p.moe.UC);
-  const int up_sh = p.moe.n_shared * (p.moe.SI / 32);
-  const int up_total = up_r + up_sh;
-  K2_TASKS(t, up_total) {
-    const bool sh = t < up_sh;
-    if (sh) k2_wait(p, seen, SY_ROUTER, nrt, t < G ? 3 * st + 1 : -1, K2_LANES);
-    else k2_wait(p, seen, SY_ROUTE, 1, t < G ? 3 * st + 1 : -1);
-    moe_upgate<K2_NT, NCG>(p.moe, sh ? up_r + t : t - up_sh, S.up.red, S.up.midf);
-    k2_signal(p, SY_UP, t, K2_LANES);
-  }
-  K2_NEXT(up_total);
-  k2_stamp(p, 3 * st++ + 2);
-  // ---- down + route weighting + residual, per 16 hidden rows
-  k2_stamp(p, 3 * st);
-  K2_TASKS(t, down_tasks(p.moe)) {
-    k2_wait(p, seen, SY_ROUTE, 2);  // the routing and its table: known long before the mid rows
-    moe_down<K2_NT, NCG>(p.moe, t, S.down.red, S.down.act, S.down.xres,
-                         [&] { k2_wait(p, seen, SY_UP, up_total, t < G ? 3 * st + 1 : -1, K2_LANES); });
-  }
-  k2_stamp(p, 3 * st + 2);
+    K2_NEXT(R * nchk);
+    k2_stamp(p, 3 * st++ + 2);
+    ++st;  // the select stamps are taken above
+    // ---- sparse-MLA splits
+    k2_stamp(p, 3 * st);
+    const int ns = p.mla.nsplit;
+    K2_TASKS(t, R * ns) {
+      const int r = t / ns;
+      if (!k2_wait(p, seen, SY_TOPK + r, 1, t < G ? 3 * st + 1 : -1)) return;
+      mla_split<K2_NT>(p.mla, r, t % ns, S.split);
+      k2_signal(p, SY_SPLIT + r);
+    }
+    K2_NEXT(R * ns);
+    k2_stamp(p, 3 * st++ + 2);
+    // ---- merge of the splits + W_UV, per (row, head, half of the head's outputs)
+    k2_stamp(p, 3 * st);
+    K2_TASKS(t, 2 * R * MLA_HEADS) {
+      const int r = t / (2 * MLA_HEADS), h = (t >> 1) % MLA_HEADS;
+      mla_merge_uv<K2_NT>(p.mla, r, h, t & 1, S.merge,
+                          [&] { return k2_wait(p, seen, SY_SPLIT + r, ns, t < G ? 3 * st + 1 : -1); });
+      if (seen[SY_LINES]) return;
+      k2_signal(p, SY_UV, t, K2_LANES);
+    }
+    K2_NEXT(2 * R * MLA_HEADS);
+    k2_stamp(p, 3 * st++ + 2);
+    // ---- W_o + residual, per 16 hidden rows: tasks t and t + G together (their weights
+    // all in flight before the wait)
+    k2_stamp(p, 3 * st);
+    const int ht = p.mla.hidden / 16;
+    for (int t = (b - base % G + G) % G; t < ht; t += 2 * G) {
+      const int t1 = t + G < ht ? t + G : -1;
+      mla_oproj<K2_NT, NCG, 2>(p.mla, t, t1, S.up.red,
+                               [&] { return k2_wait(p, seen, SY_UV, 2 * R * MLA_HEADS, t < G ? 3 * st + 1 : -1, K2_LANES); });
+      if (seen[SY_LINES]) return;
+      k2_signal(p, SY_OPROJ, t, K2_LANES, t1 >= 0 ? 2 : 1);
+    }
+    K2_NEXT(ht);
+    k2_stamp(p, 3 * st++ + 2);
+    // ---- router GEMV (+ RMSNorm of its slice), per (16 experts, hidden slice)
+    k2_stamp(p, 3 * st);
+    const int et = p.moe.E / 16, nrt = et * p.moe.KC;
+    K2_TASKS(t, nrt) {
+      moe_router<K2_NT, NCG>(p.moe, t % et, t / et, S.router,
+                             [&] { return k2_wait(p, seen, SY_OPROJ, ht, t < G ? 3 * st + 1 : -1, K2_LANES); });
+      if (seen[SY_LINES]) return;
+      // the last router task computes the routing
+      if (k2_signal_last(p, SY_ROUTER, SY_ROUTER_LAST, t, nrt, &last_flag)) {
+        k2_stamp(p, 3 * (st + 1));
+        k2_stamp(p, 3 * (st + 1) + 1);
+        // SY_ROUTE: 1 once the distinct-expert list is out (up/gate), 2 with the table (down)
+        moe_route<K2_NT>(p.moe, S.route, [&] { k2_signal(p, SY_ROUTE); });
+        k2_signal(p, SY_ROUTE);
+        k2_stamp(p, 3 * (st + 1) + 2);
+      }
+    }
+    K2_NEXT(nrt);
+    k2_stamp(p, 3 * st++ + 2);
+    ++st;  // routing: run by the last router task above
+    // ---- up/gate + SwiGLU: the shared expert's chunks first (they need only the
+    // normalized rows, stored by the router tasks, so they run while routing is still
+    // pending), then the routed slots
+    k2_stamp(p, 3 * st);
+    const int up_r = p.moe.Dmax * (p.moe.I / p.moe.UC);
+    const int up_sh = p.moe.n_shared * (p.moe.SI / 32);
+    const int up_total = up_r + up_sh;
+    K2_TASKS(t, up_total) {
+      const bool sh = t < up_sh;
+      if (!(sh ? k2_wait(p, seen, SY_ROUTER, nrt, t < G ? 3 * st + 1 : -1, K2_LANES)
+               : k2_wait(p, seen, SY_ROUTE, 1, t < G ? 3 * st + 1 : -1)))
+        return;
+      moe_upgate<K2_NT, NCG>(p.moe, sh ? up_r + t : t - up_sh, S.up.red, S.up.midf);
+      k2_signal(p, SY_UP, t, K2_LANES);
+    }
+    K2_NEXT(up_total);
+    k2_stamp(p, 3 * st++ + 2);
+    // ---- down + route weighting + residual, per 16 hidden rows
+    k2_stamp(p, 3 * st);
+    K2_TASKS(t, down_tasks(p.moe)) {
+      if (!k2_wait(p, seen, SY_ROUTE, 2)) return;  // the routing and its table: known long before the mid rows
+      moe_down<K2_NT, NCG>(p.moe, t, S.down.red, S.down.act, S.down.xres,
+                           [&] { return k2_wait(p, seen, SY_UP, up_total, t < G ? 3 * st + 1 : -1, K2_LANES); });
+      if (seen[SY_LINES]) return;
+    }
+    k2_stamp(p, 3 * st + 2);
+
+  };
+  walk();
 #undef K2_TASKS
 #undef K2_NEXT
   // ---- the last workgroup out resets the counters for the next launch

@@ -252,8 +252,10 @@ MK2_DEV void st_dev_16(void* p, uint4 v) {
 // the dependency wait a stage runs after issuing the loads of its static weights (the
 // persistent launch waits on a counter there; a stand-alone kernel has nothing to wait
 // for)
+// a stage's dependency wait: true once satisfied, false when the launch is failing
+// (the stage then returns at once, every thread alike)
 struct NoWait {
-  MK2_DEV void operator()() const {}
+  MK2_DEV bool operator()() const { return true; }
 };
 
 // every memory access of this thread has completed (stores are device-visible)

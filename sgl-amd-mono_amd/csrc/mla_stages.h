@@ -245,7 +245,7 @@ MK2_DEV void mla_merge_uv(const MlaDev& p, int r, int h, int hf, MlaMergeLds& L,
   };
   bf16x8 a[16];
   if (wave >= 1 && vt0 < vhi) load_a(vt0, a);
-  wait();
+  if (!wait()) return;
   float* wgt = L.w;        // [ns] exp(m_s - M)
   float* lsum = L.w + ns;  // [ns] l_s
   const float* ml = p.part_ml + ((size_t)r * ns * MLA_HEADS + h) * 2;
@@ -346,7 +346,7 @@ MK2_DEV void mla_oproj(const MlaDev& p, int nt0, int nt1, float* red, Wait wait 
       hres[i] = bf16_to_f32(p.h[(size_t)(jdx >> 4) * p.hidden + (j == 0 ? nt0 : nt1) * 16 + (jdx & 15)]);
     }
   }
-  wait();
+  if (!wait()) return;
   f32x4 acc[NTL][NCG];
 #pragma unroll
   for (int j = 0; j < NTL; ++j)

@@ -161,7 +161,7 @@ MK2_DEV void moe_router(const MoeDev& p, int nt, int kc, RouterLds& L, Wait wait
   bf16x8 a0[4];
   load_a_bf16(p.w_router + ((size_t)nt * KB + kc * kbs + min(wave, kbs - 1)) * 4096, lane, a0);
   const uint4 gam = p.norm ? *(const uint4*)(p.gamma + c0 + c8) : make_uint4(0, 0, 0, 0);
-  wait();
+  if (!wait()) return;
   uint4 xv[RMAX];
 #pragma unroll
   for (int i = 0; i < RMAX; ++i)
@@ -746,7 +746,7 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, float*
   Unit x0, x1, x2;
   if (nu > 0) load_w(0, x0);
   if (nu > 1) load_w(1, x1);
-  wait();
+  if (!wait()) return;
   if (nu > 0) load_m(0, x0);
   if (nu > 1) load_m(1, x1);
   // the shared expert (FP8, bf16 mid): its k-blocks spread over the waves

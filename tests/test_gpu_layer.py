@@ -117,3 +117,30 @@ def test_persistent_layer_one_workspace_new_inputs():
         outs.append(o)
     assert not torch.equal(outs[0], outs[1])
     assert torch.equal(outs[0], outs[2]) and torch.equal(outs[1], outs[3])
+
+
+def test_persistent_layer_fail_stop():
+    """A launch whose dependency waits may poll only a couple of times (spin limit 1)
+    gives up: it reports status 1 and ends, every workgroup skipping the tasks it has
+    left (fail-stop, as the reference's guard stops a launch).  The workspace is then
+    zeroed by the caller, and the next launch gives the staged path's bits."""
+    from sgl_amd_mono.k2 import config as C
+    from sgl_amd_mono.k2 import synth
+    from sgl_amd_mono.k2.ops import LayerOp
+
+    dev = _dev()
+    cfg = C.C5_LAYER
+    L = synth.make_layer(cfg, 8, 779, dev)
+    op = LayerOp(cfg, L, 8, device=dev, spin_limit=1)
+    ref = LayerOp(cfg, L, 8, device=dev, staged=True)()
+    status = torch.full((1,), -1, dtype=torch.int32, device=dev)
+    op(status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 1
+    op.workspace.zero_()
+    op.spin_limit = 0  # the default limit
+    status.fill_(-1)
+    out = op(status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0
+    assert torch.equal(out, ref)

@@ -192,14 +192,16 @@ typedef struct mk2_layer_args {
   mk2_moe_args moe;         /* x is ignored (the attention output); norm=1, residual=1 */
   void* attn_out;           /* optional bf16 [rows][hidden]: the residual after attention */
   void* out;
-  void* workspace;          /* zero-filled before its first launch; every completed
-                               launch leaves it ready for the next */
+  void* workspace;          /* zero-filled before its first launch; every launch
+                               (completed or stopped) leaves it ready for the next */
   size_t workspace_bytes;
   int mode;                 /* MK2_LAYER_PERSISTENT or MK2_LAYER_STAGED */
   int spin_limit;           /* persistent: polls a dependency wait may take before the
                                launch gives up (0: default, about a second) */
-  int32_t* status;          /* optional device word: 0 ok, 1 a wait gave up and the
-                               launch stopped (zero the workspace before the next) */
+  int32_t* status;          /* optional device word, sticky: a persistent launch whose
+                               wait gave up stops early (its out is not valid) and ORs 1
+                               into it; a completed launch leaves it as it is.  A stopped
+                               launch still leaves the workspace ready for the next. */
   uint64_t* timeline;       /* optional [grid][31] stage stamps of the persistent launch
                                (100 MHz device clock): per stage enter, input ready, leave */
 } mk2_layer_args;

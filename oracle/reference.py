@@ -16,7 +16,15 @@ Pinned by tests/test_oracle_reference.py:
   swiglu            -- torch.nn.functional.silu
   moe_block         -- a single expert with hand-built weights; linearity in the
                        route weights
-  k2_layer          -- composition of the above (checked piecewise)
+and by tests/test_oracle_pins.py (closed forms on hand-picked exact inputs, each with
+a planted mistake that must fail):
+  expert_mxfp4      -- E2M1 x E8M0 weights, MXFP8 x and mid on E4M3 rounding ties
+  expert_fp8        -- mid rounded to bf16 on ties
+  mla_output        -- permutation W_UV, o_lat and sums on bf16 ties
+  o_proj            -- permutation W_o, residual sums on bf16 ties
+  moe_mix           -- route-weighted sum of hand-built experts
+The chained layer is the composition of these, checked stage by stage on the GPU
+(tests/refs.check_layer).
 """
 
 from __future__ import annotations
@@ -171,16 +179,10 @@ def expert_mxfp4(x: torch.Tensor, w13: torch.Tensor, w2: torch.Tensor) -> torch.
     return mq @ w2.T
 
 
-def moe_block(x, logits_fn, route_fn, experts, shared, residual=None):
-    """y = sum_k w_k * expert_{id_k}(x) + shared(x); out = bf16(residual + y) or bf16(y).
-
-    x [M, H] bf16 values (already normalized); logits_fn(x) -> f32 [M, E]; route_fn ->
-    (ids, weights); experts(e, rows_x) -> f32 [rows, H]; shared(x) -> f32 or None.
-    glm53/gfx950/kernel.py:5662-7152 (up/gate, mid, down + route weighting, residual).
-    Returns (out f32 of bf16 values, ids, weights, logits).
-    """
-    logits = logits_fn(x)
-    ids, w = route_fn(logits)
+def moe_mix(x, ids, w, experts, shared):
+    """y = sum_k w_k * expert_{id_k}(x) + shared(x), in f64, per row: the MoE block's
+    sum before its residual add and bf16 rounding (glm53/gfx950/kernel.py:6676-7136:
+    down + route weighting, the shared expert at slot 0 with weight 1)."""
     m = x.shape[0]
     y = torch.zeros(m, x.shape[1], dtype=torch.float64)
     for r in range(m):
@@ -188,22 +190,23 @@ def moe_block(x, logits_fn, route_fn, experts, shared, residual=None):
             y[r] += w[r, j].double() * experts(int(ids[r, j]), x[r : r + 1])[0].double()
     if shared is not None:
         y += shared(x).double()
+    return y
+
+
+def moe_block(x, logits_fn, route_fn, experts, shared, residual=None):
+    """y = moe_mix(...); out = bf16(residual + y) or bf16(y).
+
+    x [M, H] bf16 values (already normalized); logits_fn(x) -> f32 [M, E]; route_fn ->
+    (ids, weights); experts(e, rows_x) -> f32 [rows, H]; shared(x) -> f32 or None.
+    glm53/gfx950/kernel.py:5662-7152 (up/gate, mid, down + route weighting, residual
+    :7140-7151).  Returns (out f32 of bf16 values, ids, weights, logits).
+    """
+    logits = logits_fn(x)
+    ids, w = route_fn(logits)
+    y = moe_mix(x, ids, w, experts, shared)
     if residual is not None:
         y = residual.double() + y
     return codecs.bf16_round(y.float()), ids, w, logits
-
-
-# ------------------------------------------------------------------ K2 chained layer
-def k2_layer(h, indexer_scores_fn, topk, attention_fn, eps, gamma, moe_fn):
-    """The chained decode layer: index scores -> exact top-k ->
-    sparse MLA + W_UV + W_o + residual h -> RMSNorm(eps) -> MoE + residual.
-    (glm53/gfx950/kernel.py:6-47 stage order; TP reduces omitted.)"""
-    scores = indexer_scores_fn()
-    sel = [radix_lists(scores[r].float(), topk) for r in range(scores.shape[0])]
-    a = attention_fn(sel)
-    x = rmsnorm(a, gamma, eps)
-    out = moe_fn(x, a)
-    return out, a, sel, scores
 
 
 def rel_l2(a: torch.Tensor, b: torch.Tensor) -> float:

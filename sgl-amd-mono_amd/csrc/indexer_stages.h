@@ -845,7 +845,9 @@ MK2_DEV void idx_select(const IdxDev& p, int r, TopkLds& S, bool known = false) 
   uint2 v[SPEC];
   if (c < nchk) {
     const int lim = min(IDX_CHUNK, p.max_ctx - c * IDX_CHUNK);  // the chunk's area (>= 64)
-    cnt = min((ldp_i32(p.ccount + (size_t)r * nchk + c) >> 15) & 0x7FFF, lim);
+    // device-coherent: the slices polled this line (ld_dev) while later chunks' counts
+    // were still unpublished, so a plain load could hit a copy taken before them
+    cnt = min((ld_dev_i32(p.ccount + (size_t)r * nchk + c) >> 15) & 0x7FFF, lim);
 #pragma unroll
     for (int u = 0; u < SPEC; ++u) v[u] = ldp_8(src + min(sub + u * TPC, lim - 1));
   }
@@ -899,6 +901,16 @@ template <int NT>
 MK2_DEV void idx_topk_reset(const IdxDev& p, int r) {
   idx_clear_hist<NT>(p, r);
   for (int c = threadIdx.x; c < p.nchk; c += NT) st_dev_i32(p.ccount + (size_t)r * p.nchk + c, 0);
+}
+
+// Every row's top-k state to zero, whatever a stopped launch left in it (one
+// workgroup, once no other is running): all fine and coarse bins and chunk counts.
+template <int NT>
+MK2_DEV void idx_reset_rows(const IdxDev& p, int rows) {
+  const uint4 z = make_uint4(0, 0, 0, 0);
+  for (int i = threadIdx.x; i < rows * IDX_BINS / 4; i += NT) st_dev_16(p.hist + 4 * i, z);
+  for (int i = threadIdx.x; i < rows * IDX_CBINS / 4; i += NT) st_dev_16(p.chist + 4 * i, z);
+  for (int i = threadIdx.x; i < rows * p.nchk; i += NT) st_dev_i32(p.ccount + i, 0);
 }
 
 }  // namespace mk2

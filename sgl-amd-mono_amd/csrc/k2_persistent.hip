@@ -310,14 +310,23 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
 #undef K2_TASKS
 #undef K2_NEXT
   // ---- the last workgroup out resets the counters for the next launch
+  drain_memory();  // this workgroup's stores and atomics have landed before it counts out
   __syncthreads();
   if (threadIdx.x == 0)
     last_flag = __hip_atomic_fetch_add(k2_ctr(p, SY_DONE), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == G - 1;
   __syncthreads();
   if (last_flag) {
-    if (threadIdx.x == 0 && p.status)
-      *p.status = __hip_atomic_load(k2_ctr(p, SY_ERR), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
+    if (threadIdx.x == 0) last_flag = __hip_atomic_load(k2_ctr(p, SY_ERR), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (last_flag) {
+      // a stopped launch skipped some rows' top-k resets: every workgroup has left, so
+      // clear all rows' top-k state here and the next launch starts clean
+      idx_reset_rows<K2_NT>(p.idx, R);
+      if (threadIdx.x == 0 && p.status) atomicOr(p.status, 1);
+      drain_memory();
+      __syncthreads();
+    }
     for (int l = threadIdx.x; l < SY_LINES; l += K2_NT)
       __hip_atomic_store(k2_ctr(p, l), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }

@@ -225,7 +225,10 @@ MK2_DEV T ld_nt(const T* p) { return __builtin_nontemporal_load(p); }
 //    counter was seen -- with plain loads (ldp_*).  A launch starts with invalidated
 //    caches and nothing on any XCD reads such data before it is published, so the
 //    first read of a line misses the L2 and fetches the stored value;
-//  - data built by device atomics (histograms) is read device-coherently (ld_dev_*).
+//  - data built by device atomics (histograms) is read device-coherently (ld_dev_*),
+//    and so is any line that a reader polled before all of it was published (the
+//    top-k chunk counts): a plain load there could hit a copy taken between two
+//    producers' stores.
 // No cache write-back or invalidate is needed (an agent-scope fence costs both, for
 // the whole L2).
 #define MK2_DEV_LD(T, p) __hip_atomic_load((const T*)(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)

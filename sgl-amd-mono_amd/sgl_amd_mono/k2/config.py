@@ -36,22 +36,26 @@ class MoEConfig:
     shared_inter: int
 
     def validate(self, rows: int) -> None:
+        """The rules of the C side (mk2_moe_workspace_bytes), checked before any call."""
         if not 1 <= rows <= MAX_ROWS:
             raise ValueError(f"rows must be in [1, {MAX_ROWS}], got {rows}")
-        if self.hidden % 512:
-            raise ValueError(f"hidden must be a multiple of 512, got {self.hidden}")
-        if self.inter % 32 or self.shared_inter % 32:
-            raise ValueError("expert intermediate sizes must be multiples of 32")
-        if self.expert_fmt == FMT_FP8 and self.inter % 128:
-            raise ValueError("FP8 experts need an intermediate size that is a multiple of 128")
-        if self.n_shared and self.shared_inter % 128:
-            raise ValueError("the FP8 shared expert needs an intermediate multiple of 128")
-        if self.n_experts % 16 or not 16 <= self.n_experts <= 256:
-            raise ValueError(f"n_experts must be a multiple of 16 in [16, 256], got {self.n_experts}")
+        if self.hidden < 512 or self.hidden % 512:
+            raise ValueError(f"hidden must be a positive multiple of 512, got {self.hidden}")
+        if self.n_experts not in (64, 128, 192, 256):
+            raise ValueError(f"n_experts must be 64, 128, 192 or 256, got {self.n_experts}")
         if not 1 <= self.top_k <= 8:
             raise ValueError(f"top_k must be in [1, 8], got {self.top_k}")
+        if self.router not in (ROUTER_SOFTMAX, ROUTER_SIGMOID_BIAS):
+            raise ValueError(f"unknown router {self.router}")
+        if self.expert_fmt not in (FMT_FP8, FMT_MXFP4):
+            raise ValueError(f"unknown expert format {self.expert_fmt}")
+        imax = 1024 if self.expert_fmt == FMT_FP8 else 4096
+        if self.inter < 128 or self.inter % 128 or self.inter > imax:
+            raise ValueError(f"inter must be a multiple of 128 in [128, {imax}] for this format, got {self.inter}")
         if self.n_shared not in (0, 1):
             raise ValueError("at most one shared expert")
+        if self.n_shared and (self.shared_inter < 128 or self.shared_inter % 128 or self.shared_inter > 4096):
+            raise ValueError(f"shared_inter must be a multiple of 128 in [128, 4096], got {self.shared_inter}")
 
 
 @dataclass(frozen=True)
@@ -73,14 +77,17 @@ class MlaConfig:
         return 1.0 / math.sqrt(self.qk_dim)
 
     def validate(self, rows: int) -> None:
+        """The rules of the C side (mk2_mla_workspace_bytes)."""
         if (self.heads, self.kv_lora, self.rope) != (16, 512, 64):
             raise ValueError("the MLA kernels serve 16 heads of 512 + 64 latent dims")
-        if self.v_dim % 16 or self.hidden % 16:
-            raise ValueError("v_dim and hidden must be multiples of 16")
-        if (self.heads * self.v_dim) % 128:
-            raise ValueError("heads * v_dim must be a multiple of 128")
-        if self.topk % 64 or self.topk <= 0:
-            raise ValueError("topk must be a positive multiple of 64")
+        if self.v_dim < 16 or self.v_dim % 16 or self.v_dim > 512 or (self.heads * self.v_dim) % 128:
+            raise ValueError("v_dim must be a multiple of 16 in [16, 512] with heads * v_dim a multiple of 128")
+        if self.hidden < 16 or self.hidden % 16:
+            raise ValueError("hidden must be a positive multiple of 16")
+        if self.topk < 64 or self.topk % 64 or self.topk > 65536:
+            raise ValueError("topk must be a multiple of 64 in [64, 65536]")
+        if self.context < 64 or self.context % PAGE:
+            raise ValueError("context must be a positive multiple of 64")
         if not 1 <= rows <= MAX_ROWS:
             raise ValueError(f"rows must be in [1, {MAX_ROWS}]")
 
@@ -97,8 +104,8 @@ class IndexerConfig:
             raise ValueError("index keys are 128 dims")
         if self.heads % 16 or not 16 <= self.heads <= 64:
             raise ValueError("index heads must be a multiple of 16 in [16, 64]")
-        if self.context > 65536 or self.context % PAGE:
-            raise ValueError("context must be a multiple of 64 and at most 65536")
+        if not 64 <= self.context <= 65536 or self.context % PAGE:
+            raise ValueError("context must be a multiple of 64 in [64, 65536]")
         if self.topk % 64 or not 64 <= self.topk <= 4096:
             raise ValueError("topk must be a multiple of 64 in [64, 4096]")
         if not 1 <= rows <= MAX_ROWS:

@@ -166,11 +166,16 @@ class LayerOp:
         _lib.check(_lib.lib().mk2_layer_workspace_bytes(ctypes.byref(self._make_args()),
                                                         ctypes.byref(nbytes)))
         # zeroed once: the persistent launch's counters start at zero and every launch
-        # leaves them at zero
+        # (completed or stopped) leaves them at zero
         self.workspace = torch.zeros(nbytes.value, dtype=torch.uint8, device=self.device)
+        # the launches' sticky status word: a persistent launch whose dependency wait
+        # gave up ORs 1 into it (the reference's guard makes a stop visible to the host,
+        # common/guard.py:100-241); check() reads it
+        self.status = torch.zeros(1, dtype=torch.int32, device=self.device)
 
     def _make_args(self, out=None, attn_out=None, scores=None, topk=None, logits=None,
-                   topk_ids=None, topk_weights=None, workspace=None, status=None, timeline=None):
+                   topk_ids=None, topk_weights=None, workspace=None, status=None, timeline=None,
+                   o_latent=None):
         L = self.L
         ia = _lib.IndexerArgs(
             self.idx.shape, _p(L.idx.q), _p(L.idx.w), _p(L.idx.cache), _p(L.idx.cache_scale), _p(L.idx.page_table),
@@ -178,7 +183,7 @@ class LayerOp:
         )
         ma = _lib.MlaArgs(
             self.mla.shape, _p(L.mla.q), _p(L.mla.kv), _p(L.mla.kv_scale), _p(L.mla.page_table),
-            _p(L.mla.req_ids), None, _p(L.mla.w_uv), _p(L.mla.w_o_p), _p(L.h), None, None, 0, None,
+            _p(L.mla.req_ids), None, _p(L.mla.w_uv), _p(L.mla.w_o_p), _p(L.h), None, None, 0, _p(o_latent),
         )
         ea = _lib.MoeArgs(
             self.moe.shape, self.moe.weights, None, None, None, 0,
@@ -190,12 +195,29 @@ class LayerOp:
                               _p(timeline))
 
     def __call__(self, out=None, *, attn_out=None, scores=None, topk=None, logits=None,
-                 topk_ids=None, topk_weights=None, status=None, timeline=None):
+                 topk_ids=None, topk_weights=None, status=None, timeline=None, o_latent=None):
+        """Enqueues one layer launch on the current stream; returns out.  `status`
+        (int32 [1], device) replaces the op's own sticky status word for this launch;
+        the other keywords are optional outputs for checking (o_latent: f32 [rows, 16,
+        512], the merged attention before W_UV)."""
         H = self.cfg.mla.hidden
         if out is None:
             out = torch.empty(self.rows, H, dtype=torch.bfloat16, device=self.device)
         _need(out, "out", torch.bfloat16, (self.rows, H))
+        if status is not None:
+            _need(status, "status", torch.int32, (1,))
+        if o_latent is not None:
+            _need(o_latent, "o_latent", torch.float32, (self.rows, self.cfg.mla.heads, self.cfg.mla.kv_lora))
         args = self._make_args(out, attn_out, scores, topk, logits, topk_ids, topk_weights,
-                               self.workspace, status, timeline)
+                               self.workspace, self.status if status is None else status, timeline,
+                               o_latent)
         _lib.check(_lib.lib().mk2_layer_launch(ctypes.byref(args), _lib.stream_handle(self.device)))
         return out
+
+    def check(self) -> None:
+        """Raises RuntimeError if a launch of this op stopped early since the last check
+        (its outputs are not valid); clears the word.  Synchronizes with the device."""
+        if int(self.status.item()) != 0:
+            self.status.zero_()
+            raise RuntimeError("K2 layer: a persistent launch stopped early (a dependency wait gave up); "
+                               "its outputs are not valid")

@@ -120,9 +120,11 @@ def make_indexer(cfg: C.IndexerConfig, rows: int, seed: int, device, ctx_len=Non
     return ns
 
 
-def make_mla(cfg: C.MlaConfig, rows: int, seed: int, device, residual: bool = True):
+def make_mla(cfg: C.MlaConfig, rows: int, seed: int, device, residual: bool = True, h_std: float = 1.0):
     """FP8 latent-KV pages with per-token f32 scales, absorbed bf16 queries,
-    selected positions, W_UV and W_o (bf16, ~ N(0, 0.02)), residual rows."""
+    selected positions, W_UV and W_o (bf16, ~ N(0, 0.02)), residual rows ~ N(0,
+    h_std^2).  A small h_std keeps the attention term o W_o^T above the bf16 rounding
+    of h + o W_o^T, so a check of the sum minus h sees the attention's own error."""
     g = _gen(seed, device)
     ctx = cfg.context
     ppr = ctx // C.PAGE
@@ -143,16 +145,16 @@ def make_mla(cfg: C.MlaConfig, rows: int, seed: int, device, residual: bool = Tr
         torch.bfloat16
     )
     ns.w_o_p = pack_bf16(ns.w_o)
-    ns.h = _randn(g, rows, cfg.hidden, device=device).to(torch.bfloat16) if residual else None
+    ns.h = _randn(g, rows, cfg.hidden, device=device, std=h_std).to(torch.bfloat16) if residual else None
     return ns
 
 
-def make_layer(cfg: C.K2Config, rows: int, seed: int, device):
+def make_layer(cfg: C.K2Config, rows: int, seed: int, device, h_std: float = 1.0):
     """One chained layer: indexer keys and queries, latent-KV pages sharing the
-    indexer's page table, attention weights, residual rows, MoE weights with the
-    post-attention RMSNorm weight."""
+    indexer's page table, attention weights, residual rows ~ N(0, h_std^2), MoE
+    weights with the post-attention RMSNorm weight."""
     idx = make_indexer(cfg.indexer, rows, seed, device)
-    mla = make_mla(cfg.mla, rows, seed + 1, device, residual=True)
+    mla = make_mla(cfg.mla, rows, seed + 1, device, residual=True, h_std=h_std)
     mla.page_table = idx.page_table
     mla.req_ids = idx.req_ids
     mla.sel = None  # the chain supplies the indexer's selection

@@ -1,0 +1,94 @@
+"""The Python configs and the C side accept the same shapes: for a grid of MoE, MLA and
+indexer configurations, ``validate()`` passes exactly when the library's workspace
+query (which runs the C argument checks, no GPU needed) returns MK2_OK.  A config the
+C side rejects must never get past ``validate()`` to fail at the launch."""
+
+import ctypes
+import itertools
+from dataclasses import replace
+
+import pytest
+
+from sgl_amd_mono.k2 import config as C
+
+
+def _lib():
+    from sgl_amd_mono import _lib
+
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libmk2.so not built (run __graft_entry__.build())")
+    return _lib, _lib.lib()
+
+
+def _py_ok(cfg, rows):
+    try:
+        cfg.validate(rows)
+        return True
+    except ValueError:
+        return False
+
+
+def _moe_c_ok(_l, L, cfg, rows):
+    s = _l.MoeShape(rows, cfg.hidden, cfg.n_experts, cfg.top_k, cfg.inter, cfg.router, cfg.expert_fmt,
+                    cfg.n_shared, cfg.shared_inter, 1, 1, cfg.route_scale, 1e-6)
+    n = ctypes.c_size_t()
+    return L.mk2_moe_workspace_bytes(ctypes.byref(s), ctypes.byref(n)) == 0
+
+
+def test_moe_validate_matches_c():
+    _l, L = _lib()
+    seen = {True: 0, False: 0}
+    for hidden, E, k, inter, fmt, ns, si, rows in itertools.product(
+        (256, 512, 2048, 6144, 7168 + 256), (16, 48, 64, 96, 192, 256, 320), (0, 1, 8, 9),
+        (32, 96, 128, 256, 768, 1024, 2048, 4096, 8192), (C.FMT_FP8, C.FMT_MXFP4), (0, 1),
+        (32, 128, 768, 4224), (1, 8, 32, 33),
+    ):
+        cfg = replace(C.C2_MOE, hidden=hidden, n_experts=E, top_k=k, inter=inter, expert_fmt=fmt,
+                      n_shared=ns, shared_inter=si)
+        py, c = _py_ok(cfg, rows), _moe_c_ok(_l, L, cfg, rows)
+        assert py == c, (cfg, rows, py, c, L.mk2_last_error())
+        seen[py] += 1
+    assert seen[True] > 100 and seen[False] > 100
+
+
+def test_mla_validate_matches_c():
+    _l, L = _lib()
+    seen = {True: 0, False: 0}
+    for v_dim, hidden, topk, rows in itertools.product(
+        (8, 16, 64, 128, 512, 528), (8, 16, 6144, 7000), (32, 64, 2048, 65536, 65600), (1, 32, 33),
+    ):
+        cfg = replace(C.C3_MLA, v_dim=v_dim, hidden=hidden, topk=topk)
+        s = _l.MlaShape(rows, cfg.heads, cfg.kv_lora, cfg.rope, cfg.v_dim, cfg.hidden, cfg.topk,
+                        cfg.context // C.PAGE, cfg.sm_scale)
+        n = ctypes.c_size_t()
+        c = L.mk2_mla_workspace_bytes(ctypes.byref(s), ctypes.byref(n)) == 0
+        py = _py_ok(cfg, rows)
+        assert py == c, (cfg, rows, py, c, L.mk2_last_error())
+        seen[py] += 1
+    assert seen[True] and seen[False]
+
+
+def test_indexer_validate_matches_c():
+    _l, L = _lib()
+    seen = {True: 0, False: 0}
+    for heads, topk, ctx, rows in itertools.product(
+        (8, 16, 48, 64, 80), (32, 64, 2048, 4096, 4160), (32, 64, 8192, 65536, 65600, 131072), (1, 32, 33),
+    ):
+        cfg = replace(C.C4_INDEXER, heads=heads, topk=topk, context=ctx)
+        s = _l.IndexerShape(rows, cfg.heads, cfg.dim, cfg.topk, cfg.context, max(1, cfg.context // C.PAGE))
+        n = ctypes.c_size_t()
+        c = L.mk2_indexer_workspace_bytes(ctypes.byref(s), ctypes.byref(n)) == 0
+        py = _py_ok(cfg, rows)
+        assert py == c, (cfg, rows, py, c, L.mk2_last_error())
+        seen[py] += 1
+    assert seen[True] and seen[False]
+
+
+def test_a_config_the_c_side_rejects_fails_validate():
+    """48 experts and inter 96 are multiples of 16 and 32 but outside the C limits
+    (multiples of 64 and 128): validate() refuses them before any launch."""
+    _l, L = _lib()
+    cfg = replace(C.C1_MOE, n_experts=48, inter=96)
+    assert not _moe_c_ok(_l, L, cfg, 4)
+    with pytest.raises(ValueError):
+        cfg.validate(4)

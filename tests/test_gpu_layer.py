@@ -1,7 +1,11 @@
 """The chained K2 layer on the GPU (indexer -> MLA -> MoE) against the CPU oracle,
 checked piecewise (refs.check_layer): exact top-k lists of the kernel's own scores,
-scores within 1e-4 of f64, attention and layer outputs within rel-L2 1e-2, router
-logits within 1e-4 and expert ids exact on rows with a clear top-8 boundary."""
+scores within 1e-4 of f64, the merged attention (o_latent), the attention term
+attn - h and the MoE term out - attn each within rel-L2 1e-2 of the oracle's own
+terms, router logits within 1e-4 and expert ids exact on rows with a clear top-8
+boundary.  The parity cases draw the residual rows h ~ N(0, (1/128)^2): with h ~ N(0,
+1) the bf16 rounding of h + o W_o^T alone would be about 10 % of the attention term,
+and a check of attn - h could not see the attention's own errors."""
 
 import pytest
 import torch
@@ -17,14 +21,17 @@ def _dev():
     return torch.device("cuda:0")
 
 
-def run_layer(cfg, rows, seed, staged=False):
+H_STD = 1.0 / 128
+
+
+def run_layer(cfg, rows, seed, staged=False, h_std=H_STD):
     from sgl_amd_mono.k2 import synth
     from sgl_amd_mono.k2.ops import LayerOp
 
     dev = _dev()
-    L = synth.make_layer(cfg, rows, seed, dev)
+    L = synth.make_layer(cfg, rows, seed, dev, h_std=h_std)
     op = LayerOp(cfg, L, rows, device=dev, staged=staged)
-    status = torch.full((1,), -1, dtype=torch.int32, device=dev)
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
     H, E, K = cfg.mla.hidden, cfg.moe.n_experts, cfg.moe.top_k
     attn = torch.empty(rows, H, dtype=torch.bfloat16, device=dev)
     scores = torch.empty(rows, cfg.indexer.context, dtype=torch.float32, device=dev)
@@ -32,12 +39,13 @@ def run_layer(cfg, rows, seed, staged=False):
     logits = torch.empty(rows, E, dtype=torch.float32, device=dev)
     ids = torch.empty(rows, K, dtype=torch.int32, device=dev)
     wts = torch.empty(rows, K, dtype=torch.float32, device=dev)
+    olat = torch.empty(rows, cfg.mla.heads, cfg.mla.kv_lora, dtype=torch.float32, device=dev)
     out = op(attn_out=attn, scores=scores, topk=topk, logits=logits, topk_ids=ids, topk_weights=wts,
-             status=status)
+             status=status, o_latent=olat)
     torch.cuda.synchronize()
     if not staged:
         assert int(status.item()) == 0, "a dependency wait of the persistent launch gave up"
-    return L, [cpu(t) for t in (out, attn, scores, topk, logits, ids, wts)]
+    return L, [cpu(t) for t in (out, attn, scores, topk, logits, ids, wts)], cpu(olat)
 
 
 @pytest.mark.parametrize("staged", [False, True])
@@ -45,8 +53,9 @@ def run_layer(cfg, rows, seed, staged=False):
 def test_layer_config5(rows, staged):
     from sgl_amd_mono.k2 import config as C
 
-    L, res = run_layer(C.C5_LAYER, rows, seed=500 + rows, staged=staged)
-    stats = check_layer(L, *res)
+    L, res, olat = run_layer(C.C5_LAYER, rows, seed=500 + rows, staged=staged)
+    stats = check_layer(L, *res, o_latent=olat)
+    assert stats["attn_term_checked"] and stats["moe_term_checked"]  # both terms were resolvable and checked
     print(stats)
 
 
@@ -57,8 +66,10 @@ def test_layer_small_context_32_rows():
 
     cfg = replace(C.C5_LAYER, mla=replace(C.C5_LAYER.mla, context=8192),
                   indexer=replace(C.C5_LAYER.indexer, context=8192))
-    L, res = run_layer(cfg, 32, seed=532)
-    print(check_layer(L, *res))
+    L, res, olat = run_layer(cfg, 32, seed=532)
+    stats = check_layer(L, *res, o_latent=olat)
+    assert stats["attn_term_checked"] and stats["moe_term_checked"]
+    print(stats)
 
 
 @pytest.mark.parametrize("rows", [8, 32])
@@ -77,7 +88,7 @@ def test_persistent_layer_repeats_and_matches_staged(rows):
     L = synth.make_layer(cfg, rows, 777, dev)
     p_op = LayerOp(cfg, L, rows, device=dev)
     s_op = LayerOp(cfg, L, rows, device=dev, staged=True)
-    status = torch.full((1,), -1, dtype=torch.int32, device=dev)
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
     outs = [p_op(status=status).clone() for _ in range(3)]
     ref = s_op()
     torch.cuda.synchronize()
@@ -104,7 +115,7 @@ def test_persistent_layer_one_workspace_new_inputs():
     saved = [t.clone() for t in step(A)]
     p_op = LayerOp(cfg, A, 8, device=dev)
     s_op = LayerOp(cfg, A, 8, device=dev, staged=True)
-    status = torch.full((1,), -1, dtype=torch.int32, device=dev)
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
     outs = []
     for src in (saved, step(B), saved, step(B)):
         for dst, t in zip(step(A), src):
@@ -121,9 +132,12 @@ def test_persistent_layer_one_workspace_new_inputs():
 
 def test_persistent_layer_fail_stop():
     """A launch whose dependency waits may poll only a couple of times (spin limit 1)
-    gives up: it reports status 1 and ends, every workgroup skipping the tasks it has
-    left (fail-stop, as the reference's guard stops a launch).  The workspace is then
-    zeroed by the caller, and the next launch gives the staged path's bits."""
+    gives up: every workgroup skips the tasks it has left (fail-stop, as the
+    reference's guard stops a launch) and the launch ORs 1 into the op's sticky status
+    word, which LayerOp.check() turns into an error.  The stopped launch leaves the
+    workspace ready by itself: the next launches, on the same workspace with nothing
+    zeroed by the caller, give the staged path's bits, and they leave the status word
+    as the stop left it until check() clears it."""
     from sgl_amd_mono.k2 import config as C
     from sgl_amd_mono.k2 import synth
     from sgl_amd_mono.k2.ops import LayerOp
@@ -132,15 +146,20 @@ def test_persistent_layer_fail_stop():
     cfg = C.C5_LAYER
     L = synth.make_layer(cfg, 8, 779, dev)
     op = LayerOp(cfg, L, 8, device=dev, spin_limit=1)
-    ref = LayerOp(cfg, L, 8, device=dev, staged=True)()
-    status = torch.full((1,), -1, dtype=torch.int32, device=dev)
-    op(status=status)
-    torch.cuda.synchronize()
-    assert int(status.item()) == 1
-    op.workspace.zero_()
-    op.spin_limit = 0  # the default limit
-    status.fill_(-1)
-    out = op(status=status)
-    torch.cuda.synchronize()
-    assert int(status.item()) == 0
-    assert torch.equal(out, ref)
+    ref = LayerOp(cfg, L, 8, device=dev, staged=True)().clone()
+    for _ in range(2):  # two stops in a row: the second starts from the first's leftovers
+        op.spin_limit = 1
+        op()
+        torch.cuda.synchronize()
+        assert int(op.status.item()) == 1
+        op.spin_limit = 0  # the default limit
+        outs = [op().clone() for _ in range(2)]
+        torch.cuda.synchronize()
+        assert int(op.status.item()) == 1, "a completed launch must not clear the sticky word"
+        with pytest.raises(RuntimeError, match="stopped early"):
+            op.check()
+        assert int(op.status.item()) == 0
+        for o in outs:
+            assert torch.equal(o, ref)
+    op()
+    op.check()  # a clean launch: no error

@@ -209,6 +209,21 @@ typedef struct mk2_layer_args {
 int mk2_layer_workspace_bytes(const mk2_layer_args* args, size_t* bytes);
 int mk2_layer_launch(const mk2_layer_args* args, mk2_stream_t stream);
 
+/* The same layer launch without a caller workspace: no counterpart in the reference.
+ * It is for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  args->workspace and
+ * workspace_bytes are ignored; the scratch is a device array of
+ * MK2_LAYER_STATIC_SCRATCH_BYTES inside the library, which each GPU the library runs
+ * on holds until the process ends.  A shape whose mk2_layer_workspace_bytes exceeds it
+ * fails with MK2_ENOSPACE (the configs[4] layer needs about 1.9 MiB a row at context
+ * 65536: 60.4 MiB at 32 rows).  Nothing is allocated: each call enqueues a small fill
+ * kernel that clears the counters and histograms a launch needs zero (the array keeps
+ * the last call's other contents), then the launch.  Every call on one GPU shares that
+ * GPU's array, so calls that overlap on one GPU (other streams, other host threads)
+ * race; calls ordered on one stream do not. */
+#define MK2_LAYER_STATIC_SCRATCH_BYTES ((size_t)64 << 20)
+int mk2_layer_launch_static(const mk2_layer_args* args, mk2_stream_t stream);
+
 /* ------------------------------------------------------------------ misc */
 const char* mk2_last_error(void);
 int mk2_abi_version(void);

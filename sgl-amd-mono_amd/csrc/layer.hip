@@ -1,6 +1,8 @@
 // The chained K2 layer: indexer scores -> exact top-k -> sparse MLA -> W_UV -> W_o +
 // residual -> RMSNorm -> router -> top-k routing -> up/gate -> down + residual, as
 // one persistent launch (k2_persistent.hip) or as one kernel a stage.
+#include <mutex>
+
 #include "indexer_stages.h"
 #include "mla_stages.h"
 #include "mk2_host.h"
@@ -80,9 +82,84 @@ int layer_plan(const mk2_layer_args* a, void* ws, LayerPlan* L, size_t* bytes) {
   return MK2_OK;
 }
 
+// ------------------------------------------------------ allocation-free entry point
+// The layer's scratch as a file-scope device array, for callers that cannot allocate
+// (code under HIP graph capture, serving loops and harnesses that forbid hipMalloc).
+// Every GPU the library runs on holds its own copy until the process ends.  In host
+// code `scratch` names a host-side stand-in, never a device address: the device
+// address comes from hipGetSymbolAddress, taken once per device with that device
+// current, and only that address is used (kernel arguments, the fill kernel).
+static __device__ __align__(256) uint8_t scratch[MK2_LAYER_STATIC_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[MAX_DEVICES];
+
+static int static_scratch(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES)
+    return set_error(MK2_ELAUNCH, "layer (static scratch): no current HIP device");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return set_error(MK2_ELAUNCH, "layer (static scratch): hipGetSymbolAddress failed on device %d: %s", dev,
+                       hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return MK2_OK;
+}
+
+// zero what a launch needs zero on entry: the persistent launch's counters and the
+// indexer's histograms, chunk counts and ticket (a fill kernel, so that a captured
+// graph holds no memset node)
+struct ZeroSpan {
+  int* p;
+  int n;
+};
+__global__ __launch_bounds__(256) void k_layer_zero(ZeroSpan a, ZeroSpan b, ZeroSpan c, ZeroSpan d, ZeroSpan e) {
+  const ZeroSpan sp[5] = {a, b, c, d, e};
+  for (int s = 0; s < 5; ++s)
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < sp[s].n; i += gridDim.x * 256) sp[s].p[i] = 0;
+}
+
 }  // namespace mk2
 
 using namespace mk2;
+
+extern "C" int mk2_layer_launch_static(const mk2_layer_args* a, mk2_stream_t stream) {
+  clear_error();
+  LayerPlan L;
+  size_t need = 0;
+  int rc = layer_plan(a, nullptr, &L, &need);
+  if (rc) return rc;
+  MK2_REQUIRE(a->out != nullptr, "layer (static scratch): out must be set");
+  MK2_REQUIRE(a->out != a->mla.h, "layer (static scratch): out must not alias the residual h");
+  if (need > MK2_LAYER_STATIC_SCRATCH_BYTES)
+    return set_error(MK2_ENOSPACE, "layer (static scratch): this shape needs %zu bytes of scratch, more than the "
+                     "%zu bytes of the static array; use mk2_layer_launch with a workspace", need,
+                     (size_t)MK2_LAYER_STATIC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  rc = static_scratch(&ws);
+  if (rc) return rc;
+  rc = layer_plan(a, ws, &L, &need);
+  if (rc) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  const IdxDev& x = L.idx;
+  k_layer_zero<<<64, 256, 0, st>>>(ZeroSpan{L.sync, LAYER_SYNC_BYTES / 4}, ZeroSpan{x.hist, x.rows * IDX_BINS},
+                                   ZeroSpan{x.chist, x.rows * IDX_CBINS}, ZeroSpan{x.ccount, x.rows * x.nchk},
+                                   ZeroSpan{x.ticket, 1});
+  rc = check_launch("layer (static scratch): clear");
+  if (rc) return rc;
+  if (a->mode == MK2_LAYER_PERSISTENT)
+    return k2_persistent_enqueue(L.idx, L.mla, L.moe, L.sync, a->status, (uint64_t*)a->timeline,
+                                 a->mla.shape.rows, a->spin_limit ? a->spin_limit : (1 << 20), st);
+  idx_enqueue(L.idx, st);
+  mla_enqueue(L.mla, st);
+  return moe_enqueue(L.moe, st);
+}
 
 extern "C" int mk2_layer_workspace_bytes(const mk2_layer_args* a, size_t* bytes) {
   clear_error();

@@ -107,6 +107,7 @@ SIGNATURES = {
     "mk2_sparse_mla_launch": [POINTER(MlaArgs), c_void_p],
     "mk2_layer_workspace_bytes": [POINTER(LayerArgs), POINTER(c_size_t)],
     "mk2_layer_launch": [POINTER(LayerArgs), c_void_p],
+    "mk2_layer_launch_static": [POINTER(LayerArgs), c_void_p],
     "mk2_abi_version": [],
     "mk2_selftest_mfma": [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],
 }

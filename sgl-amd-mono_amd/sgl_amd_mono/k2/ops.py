@@ -151,7 +151,10 @@ class LayerOp:
     reduces, glm53/gfx950/runner.py:374-470)."""
 
     def __init__(self, cfg: C.K2Config, layer, rows: int, device=None, *, staged: bool = False,
-                 spin_limit: int = 0):
+                 spin_limit: int = 0, static_scratch: bool = False):
+        """static_scratch: launch through mk2_layer_launch_static, whose scratch is the
+        library's own device array (no workspace is allocated here, and a launch
+        allocates nothing); launches of such ops that overlap on one GPU race."""
         cfg.validate(rows)
         self.cfg, self.rows, self.L = cfg, rows, layer
         self.mode = _lib.MK2_LAYER_STAGED if staged else _lib.MK2_LAYER_PERSISTENT
@@ -162,12 +165,17 @@ class LayerOp:
         self.moe = MoEOp(cfg.moe, layer.moe, rows, norm=True, residual=True, eps=cfg.eps,
                          device=self.device)
         self._args = None
+        self.static_scratch = static_scratch
         nbytes = ctypes.c_size_t()
         _lib.check(_lib.lib().mk2_layer_workspace_bytes(ctypes.byref(self._make_args()),
                                                         ctypes.byref(nbytes)))
-        # zeroed once: the persistent launch's counters start at zero and every launch
-        # (completed or stopped) leaves them at zero
-        self.workspace = torch.zeros(nbytes.value, dtype=torch.uint8, device=self.device)
+        self.workspace_bytes = nbytes.value
+        if static_scratch:
+            self.workspace = None
+        else:
+            # zeroed once: the persistent launch's counters start at zero and every
+            # launch (completed or stopped) leaves them at zero
+            self.workspace = torch.zeros(nbytes.value, dtype=torch.uint8, device=self.device)
         # the launches' sticky status word: a persistent launch whose dependency wait
         # gave up ORs 1 into it (the reference's guard makes a stop visible to the host,
         # common/guard.py:100-241); check() reads it
@@ -211,7 +219,8 @@ class LayerOp:
         args = self._make_args(out, attn_out, scores, topk, logits, topk_ids, topk_weights,
                                self.workspace, self.status if status is None else status, timeline,
                                o_latent)
-        _lib.check(_lib.lib().mk2_layer_launch(ctypes.byref(args), _lib.stream_handle(self.device)))
+        launch = _lib.lib().mk2_layer_launch_static if self.static_scratch else _lib.lib().mk2_layer_launch
+        _lib.check(launch(ctypes.byref(args), _lib.stream_handle(self.device)))
         return out
 
     def check(self) -> None:

@@ -138,12 +138,31 @@ def algorithmic_bytes(cfg, rows, distinct_experts):
     return int(total)
 
 
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), or the platform's processor string."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
 def cpu_baseline(layer, reps):
     import torch
 
     from refs import CpuLayer
 
+    # the host cores this process may use: the OMP_NUM_THREADS share when it is set (a
+    # GPU box gives each GPU a share of its cores), else every core
     cores = os.cpu_count() or 1
+    share = os.environ.get("OMP_NUM_THREADS", "")
+    if share.isdigit() and int(share) > 0:
+        cores = min(cores, int(share))
     torch.set_num_threads(cores)
     t0 = time.perf_counter()
     cl = CpuLayer(layer)
@@ -159,9 +178,11 @@ def cpu_baseline(layer, reps):
         "value": round(med * 1e6, 1),
         "unit": "us/layer",
         "cores": torch.get_num_threads(),
+        "cpu_model": cpu_model(),
         "kind": "port",
-        "sample": f"1 warm-up + median of {reps} oracle forwards of one configs[4] layer at M=8 "
-                  f"(f64 index scores over 8 x 65536 keys); expert dequant {prep:.1f}s outside timing",
+        "trials_us": [round(t * 1e6, 1) for t in times],
+        "sample": f"1 warm-up + median of {reps} oracle forwards of one configs[4] layer at M={layer.rows} "
+                  f"(f64 index scores over {layer.rows} x 65536 keys); expert dequant {prep:.1f}s outside timing",
     }
 
 
@@ -223,6 +244,82 @@ def pmc_kernels(dirs, calib_bytes):
     return {"sources_sha256": sources_digest(), "scale": scale, "kernels": out}
 
 
+TIMELINE_STAGES = ("score", "slice", "select", "split", "merge + W_UV", "W_o", "router", "route",
+                   "up/gate", "down")
+ROUTE_MARKS = ("route: logits polled", "route: top-k done", "route: list out")
+
+
+def timeline_stats(t):
+    """Per-stage figures of one persistent launch from its stamps t [grid][33] (100 MHz
+    s_memrealtime; per stage s: 3s enter, 3s+1 the first task's input ready, 3s+2
+    leave; 0 = not stamped), in us after the earliest enter of the launch: the first
+    workgroup in, the median and the last first-input-ready, the last workgroup out."""
+    import torch
+
+    t = t.to(torch.int64)
+    t0 = int(t[:, 0][t[:, 0] > 0].min())
+    rows = {}
+    for s, name in enumerate(TIMELINE_STAGES):
+        col = lambda i: t[:, i][t[:, i] > 0].double().sub(t0).div(100.0)  # noqa: E731
+        enter, ready, leave = col(3 * s), col(3 * s + 1), col(3 * s + 2)
+        rows[name] = {
+            "first_in": float(enter.min()) if enter.numel() else None,
+            "ready_median": float(ready.median()) if ready.numel() else None,
+            "ready_last": float(ready.max()) if ready.numel() else None,
+            "last_out": float(leave.max()) if leave.numel() else None,
+        }
+    for i, name in enumerate(ROUTE_MARKS):
+        extra = t[:, 3 * len(TIMELINE_STAGES) + i]
+        extra = extra[extra > 0].double().sub(t0).div(100.0)
+        rows[name] = {"first_in": None, "ready_median": None, "ready_last": None,
+                      "last_out": float(extra.max()) if extra.numel() else None}
+    return rows
+
+
+def timeline(ops, outs, launches, dev):
+    """Median over `launches` eager persistent launches (cycling the resident layers)
+    of each stage's timeline_stats."""
+    import statistics as st
+
+    import torch
+
+    G = torch.cuda.get_device_properties(dev).multi_processor_count
+    tl = torch.zeros(G, 3 * len(TIMELINE_STAGES) + len(ROUTE_MARKS), dtype=torch.int64, device=dev)
+    runs = []
+    for i in range(launches):
+        tl.zero_()
+        ops[i % len(ops)](outs[i % len(ops)], timeline=tl)
+        torch.cuda.synchronize()
+        runs.append(timeline_stats(tl.cpu()))
+    out = {}
+    for name in TIMELINE_STAGES + ROUTE_MARKS:
+        out[name] = {}
+        for k in ("first_in", "ready_median", "ready_last", "last_out"):
+            v = [r[name][k] for r in runs if r[name][k] is not None]
+            out[name][k] = round(st.median(v), 2) if v else None
+    return out
+
+
+def timeline_markdown(tl, argv, rows, launches):
+    lines = [f"# Persistent K2 layer, per-stage timeline at M={rows}", "",
+             "Command, run from the repository root on the MI355X box:", "",
+             "    python3 " + " ".join(argv), "",
+             f"HIP sources sha256 {sources_digest()}.  Median over {launches} eager launches",
+             "(4 resident layers cycled) of the stamps each workgroup takes with s_memrealtime",
+             "(100 MHz) as it enters a stage, when its first task's input is ready (its",
+             "dependency wait returned) and as it leaves; in us after the launch's first",
+             "stamp.  select and route run on one workgroup each (the last arrival of the",
+             "row's slices / of the router tasks).", "",
+             "| stage | first in | first input ready: median | first input ready: last | last out |",
+             "|---|---|---|---|---|"]
+    f = lambda v: "-" if v is None else f"{v:.2f}"  # noqa: E731
+    for name in TIMELINE_STAGES + ROUTE_MARKS:
+        r = tl[name]
+        lines.append(f"| {name} | {f(r['first_in'])} | {f(r['ready_median'])} | {f(r['ready_last'])} | "
+                     f"{f(r['last_out'])} |")
+    return "\n".join(lines) + "\n"
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -230,7 +327,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--rows", type=int, default=8)
     ap.add_argument("--layers", type=int, default=4, help="distinct resident layers cycled")
-    ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--cpu-reps", type=int, default=5)
+    ap.add_argument("--extra-rows", default="1,4,32",
+                    help="more widths measured after the headline one (reported under 'widths')")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--staged", action="store_true", help="one kernel a stage instead of one launch")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
@@ -241,6 +340,9 @@ def main():
                     help="bytes the calibration copy moves (read + write)")
     ap.add_argument("--pmc-kernels", nargs="+", metavar="DIR",
                     help="no GPU: per-kernel table (durations, HBM bytes, MFMA busy) from rocprofv3 databases")
+    ap.add_argument("--timeline", metavar="MD",
+                    help="write the persistent launch's per-stage timeline (markdown) to this file and exit")
+    ap.add_argument("--timeline-launches", type=int, default=24)
     args = ap.parse_args()
     if args.pmc_kernels:
         print(json.dumps(pmc_kernels(args.pmc_kernels, args.calib_bytes), indent=1))
@@ -258,25 +360,120 @@ def main():
 
     from sgl_amd_mono.k2 import config as C
     from sgl_amd_mono.k2 import synth
-    from sgl_amd_mono.k2.ops import LayerOp
 
     dev = torch.device("cuda:0")
     cfg, rows = C.C5_LAYER, args.rows
-    layers, ops, outs, ids = [], [], [], []
-    for i in range(args.layers):
-        L = synth.make_layer(cfg, rows, seed=1000 + 17 * i, device=dev)
-        layers.append(L)
-        ops.append(LayerOp(cfg, L, rows, device=dev, staged=args.staged))
-        outs.append(torch.empty(rows, cfg.mla.hidden, dtype=torch.bfloat16, device=dev))
-        ids.append(torch.empty(rows, cfg.moe.top_k, dtype=torch.int32, device=dev))
+    extra = [int(r) for r in args.extra_rows.split(",") if r] if args.extra_rows else []
+    extra = [r for r in extra if r != rows]
+    built = max([rows] + extra)
+    # the resident layers, built once at the widest width and viewed at each width
+    layers = [synth.make_layer(cfg, built, seed=1000 + 17 * i, device=dev) for i in range(args.layers)]
     torch.cuda.synchronize()
-    # realized routing of each layer (distinct experts it streams)
-    for op, o, t in zip(ops, outs, ids):
+    if args.timeline:
+        if args.staged:
+            raise SystemExit("--timeline needs the persistent launch")
+        ops, outs = _ops(cfg, [synth.view_rows(L, rows) for L in layers], rows, dev, args.staged)
+        for op, o in zip(ops, outs):  # warm-up
+            op(o)
+        tl = timeline(ops, outs, args.timeline_launches, dev)
+        md = timeline_markdown(tl, sys.argv, rows, args.timeline_launches)
+        with open(args.timeline, "w") as f:
+            f.write(md)
+        print(md)
+        for op in ops:
+            op.check()
+        return
+
+    head = measure(cfg, [synth.view_rows(L, rows) for L in layers], rows, dev, args)
+    us, ms = head["us"], head["us"] / 1000.0
+    gbs = head["algorithmic_bytes"] / (us * 1e-6) / 1e9
+    widths = {}
+    for r in extra:
+        m = measure(cfg, [synth.view_rows(L, r) for L in layers], r, dev, args)
+        g = m["algorithmic_bytes"] / (m["us"] * 1e-6) / 1e9
+        widths[str(r)] = {"us_per_layer": round(m["us"], 2), "tokens_per_s_per_layer": round(r / (m["us"] * 1e-6), 1),
+                          "algorithmic_bytes_per_layer": int(m["algorithmic_bytes"]), "hbm_gbps": round(g, 1),
+                          "roofline_frac": round(g / PEAK_HBM_GBS, 4), "distinct_experts": m["distinct"],
+                          "trials_us": m["trials_us"]}
+
+    result = {
+        "metric": METRIC,
+        "value": round(us, 2),
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": head["steps"],
+        "warmup": head["warmup"],
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "mxfp4+fp8 weights, bf16/fp8 MFMA, f32 accumulate",
+        "data": "synthetic (seeded random-init weights ~N(0,0.02), rows ~N(0,1), shuffled pages)",
+        "config": {
+            "workload": "configs[4] chained K2 layer: indexer 64x128 FP4 keys ctx 65536 top-2048 -> "
+                        "sparse MLA 16 heads 512+64 FP8 KV -> W_UV/W_o -> RMSNorm 1e-6 -> "
+                        "MXFP4 MoE 256 experts top-8 inter 256 + FP8 shared",
+            "rows": rows,
+            "distinct_layers_cycled": len(layers),
+            "parallelism": "1 GPU (TP reduce omitted)",
+        },
+        "tokens_per_s_per_layer": round(rows / (us * 1e-6), 1),
+        "trials_us": head["trials_us"],
+        "distinct_experts": head["distinct"],
+        "algorithmic_bytes_per_layer": int(head["algorithmic_bytes"]),
+        "hbm_gbps": round(gbs, 1),
+        "pct_peak_hbm": round(100.0 * gbs / PEAK_HBM_GBS, 2),
+        "replays_checked": "status words 0 and the last replay's outputs bit-equal to the eager launch's",
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "k2 layer: " + ("12 stage kernels a layer" if args.staged else
+                                      "one persistent launch a layer (k_k2_layer)"),
+            "achieved": round(gbs, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(gbs / PEAK_HBM_GBS, 4),
+            "traffic": None if args.staged else recorded_traffic(),
+        },
+        "widths": widths,
+        "cpu_baseline": None,
+    }
+    if args.copy_calib_mib:
+        n = args.copy_calib_mib << 20
+        src = torch.ones(n // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(synth.view_rows(layers[0], rows), args.cpu_reps)
+    print(json.dumps(result))
+
+
+def _ops(cfg, views, rows, dev, staged):
+    import torch
+
+    from sgl_amd_mono.k2.ops import LayerOp
+
+    ops = [LayerOp(cfg, L, rows, device=dev, staged=staged) for L in views]
+    outs = [torch.empty(rows, cfg.mla.hidden, dtype=torch.bfloat16, device=dev) for _ in views]
+    return ops, outs
+
+
+def measure(cfg, views, rows, dev, args):
+    """us per layer at `rows` rows: the layers' launches replayed from one HIP graph and
+    timed with events on the launch stream (median of 5 trials).  The replays carry
+    each op's sticky status word; after the trials every word must read 0 and the last
+    replay's outputs must equal, bit for bit, an eager launch's from before capture."""
+    import torch
+
+    ops, outs = _ops(cfg, views, rows, dev, args.staged)
+    ids = [torch.empty(rows, cfg.moe.top_k, dtype=torch.int32, device=dev) for _ in ops]
+    for op, o, t in zip(ops, outs, ids):  # realized routing (distinct experts streamed)
         op(o, topk_ids=t)
     torch.cuda.synchronize()
     distinct = [int(torch.unique(t).numel()) for t in ids]
-    bytes_per_layer = statistics.mean(algorithmic_bytes(cfg, rows, d) for d in distinct)
-
+    eager = [o.clone() for o in outs]
+    nbytes = statistics.mean(algorithmic_bytes(cfg, rows, d) for d in distinct)
     stream = torch.cuda.Stream()
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
@@ -307,59 +504,14 @@ def main():
             end.record(stream)
         torch.cuda.synchronize()
         trials.append(start.elapsed_time(end) / steps)
-    ms = statistics.median(trials)
-    us = ms * 1000.0
-    gbs = bytes_per_layer / (us * 1e-6) / 1e9
-
-    result = {
-        "metric": METRIC,
-        "value": round(us, 2),
-        "unit": "us/layer",
-        "n_gpus": 1,
-        "steps": steps,
-        "warmup": warm_replays * per_replay,
-        "ms_per_step": round(ms, 5),
-        "higher_is_better": False,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "mxfp4+fp8 weights, bf16/fp8 MFMA, f32 accumulate",
-        "data": "synthetic (seeded random-init weights ~N(0,0.02), rows ~N(0,1), shuffled pages)",
-        "config": {
-            "workload": "configs[4] chained K2 layer: indexer 64x128 FP4 keys ctx 65536 top-2048 -> "
-                        "sparse MLA 16 heads 512+64 FP8 KV -> W_UV/W_o -> RMSNorm 1e-6 -> "
-                        "MXFP4 MoE 256 experts top-8 inter 256 + FP8 shared",
-            "rows": rows,
-            "distinct_layers_cycled": len(ops),
-            "parallelism": "1 GPU (TP reduce omitted)",
-        },
-        "tokens_per_s_per_layer": round(rows / (us * 1e-6), 1),
-        "trials_us": [round(t * 1000, 2) for t in trials],
-        "distinct_experts": distinct,
-        "algorithmic_bytes_per_layer": int(bytes_per_layer),
-        "hbm_gbps": round(gbs, 1),
-        "pct_peak_hbm": round(100.0 * gbs / PEAK_HBM_GBS, 2),
-        "roofline": {
-            "bound": "hbm",
-            "kernel": "k2 layer: " + ("12 stage kernels a layer" if args.staged else
-                                      "one persistent launch a layer (k_k2_layer)"),
-            "achieved": round(gbs, 1),
-            "peak": PEAK_HBM_GBS,
-            "unit": "GB/s",
-            "frac": round(gbs / PEAK_HBM_GBS, 4),
-            "traffic": None if args.staged else recorded_traffic(),
-        },
-        "cpu_baseline": None,
-    }
-    if args.copy_calib_mib:
-        n = args.copy_calib_mib << 20
-        src = torch.ones(n // 4, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-    if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(layers[0], args.cpu_reps)
-    print(json.dumps(result))
+    for op in ops:
+        op.check()
+    for o, e in zip(outs, eager):
+        if not torch.equal(o, e):
+            raise SystemExit(f"bench.py: a graph replay's output differs from the eager launch's at {rows} rows")
+    return {"us": statistics.median(trials) * 1000.0, "trials_us": [round(t * 1000, 2) for t in trials],
+            "distinct": distinct, "algorithmic_bytes": nbytes, "steps": steps,
+            "warmup": warm_replays * per_replay}
 
 
 if __name__ == "__main__":

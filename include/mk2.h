@@ -202,8 +202,9 @@ typedef struct mk2_layer_args {
                                wait gave up stops early (its out is not valid) and ORs 1
                                into it; a completed launch leaves it as it is.  A stopped
                                launch still leaves the workspace ready for the next. */
-  uint64_t* timeline;       /* optional [grid][31] stage stamps of the persistent launch
-                               (100 MHz device clock): per stage enter, input ready, leave */
+  uint64_t* timeline;       /* optional [grid][33] stage stamps of the persistent launch
+                               (100 MHz device clock): per stage enter, input ready, leave;
+                               then the routing's logits polled, top-k done, list out */
 } mk2_layer_args;
 
 int mk2_layer_workspace_bytes(const mk2_layer_args* args, size_t* bytes);

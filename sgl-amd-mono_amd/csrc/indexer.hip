@@ -28,12 +28,12 @@ __global__ __launch_bounds__(IDX_NT) void k_idx_slice(IdxDev p) {
   __syncthreads();
   const int t = S.res[3];
   __syncthreads();
-  idx_slice<IDX_NT>(p, t / p.nchk, t % p.nchk, S, IDX_SLICE_SPIN, nullptr);
+  idx_slice<IDX_NT>(p, t / p.nchk, t % p.nchk, S, IDX_SLICE_SPIN, nullptr, 0u);
 }
 
 __global__ __launch_bounds__(TOPK_NT) void k_idx_select(IdxDev p) {
   __shared__ TopkLds S;
-  idx_select<TOPK_NT>(p, blockIdx.x, S);
+  idx_select<TOPK_NT>(p, blockIdx.x, S, 0u);
   __syncthreads();
   idx_topk_reset<TOPK_NT>(p, blockIdx.x);  // the workspace left as a persistent launch leaves it
   if (blockIdx.x == 0 && threadIdx.x == 0) *p.ticket = 0;

@@ -54,6 +54,8 @@ struct IdxDev {
   const int* ctx;       // [rows]
   float* scores;        // [rows][max_ctx]
   int* out;             // [rows][topk]
+  uint64_t* tlist;      // [rows][topk] the same list as tagged words (the persistent
+                        // layer's splits poll it), or null
   // workspace
   int* hist;            // [rows][IDX_BINS] key counts by top 12 bits (zero between launches)
   int* chist;           // [rows][IDX_CBINS] key counts by top 8 bits (zero between launches)
@@ -63,6 +65,21 @@ struct IdxDev {
 };
 
 constexpr int IDX_QROW = 136;  // LDS row stride (bf16) of the staged queries
+
+// Row r's top-k list as it is written: the int32 list and, where the layer hands it to
+// its splits, the same entries as tagged words.
+struct ListOut {
+  int* row;        // [k]
+  uint64_t* trow;  // [k] or null
+  uint32_t tag;
+  MK2_DEV void put(int i, int pos) const {
+    st_dev_i32(row + i, pos);
+    if (trow) st_pair(trow + i, (uint32_t)pos, tag);
+  }
+};
+MK2_DEV ListOut list_out(const IdxDev& p, int r, uint32_t tag) {
+  return ListOut{p.out + (size_t)r * p.topk, p.tlist ? p.tlist + (size_t)r * p.topk : nullptr, tag};
+}
 
 struct IdxScoreLds {
   int pages[IDX_CHUNK / 64];
@@ -423,87 +440,6 @@ MK2_DEV int find_bin(const int* hist, int nbins, int need, int* above_out, int* 
   return b;
 }
 
-// Exact top-k over values held in registers, PER a thread, in position order over
-// (thread, i).  d[i] = key - kbase for the values taking part (d >= 1), 0 for the
-// rest; more than k values take part.  Radix select over at most 12 bits of d at a
-// time finds the k-th d; the list is written in the radix select's order: keys whose
-// top 12 bits exceed the k-th key's, then keys sharing those 12 bits that exceed it,
-// then keys equal to it (lowest positions first) -- each group in position order.
-template <int NT, int PER, typename Pos>
-MK2_DEV void select_emit(uint32_t (&d)[PER], Pos pos, uint32_t kbase, uint32_t dmax, int k,
-                         int* hist, int* scratch, int* orow) {
-  const int tid = threadIdx.x;
-  int hib = dmax ? 32 - __clz(dmax) : 32;
-  uint32_t prefix = 0;
-  int need = k;
-  while (hib > 0) {
-    const int lob = hib > 12 ? hib - 12 : 0;
-    const int nb = 1 << (hib - lob);
-    __syncthreads();
-    for (int i = tid; i < nb; i += NT) hist[i] = 0;
-    __syncthreads();
-    {
-      int run_bin = -1, run_n = 0;
-      const uint32_t mask = (uint32_t)(nb - 1);
-      const uint32_t hmask = hib >= 32 ? 0u : ~((1u << hib) - 1u);  // bits above this digit
-      const uint32_t hpfx = hib >= 32 ? 0u : (prefix << hib);
-#pragma unroll
-      for (int i = 0; i < PER; ++i) {
-        const uint32_t v = d[i];
-        if ((v & hmask) == hpfx) {
-          const int b = (int)((v >> lob) & mask);
-          if (b != run_bin) {
-            if (run_n) atomicAdd(&hist[run_bin], run_n);
-            run_bin = b;
-            run_n = 0;
-          }
-          ++run_n;
-        }
-      }
-      if (run_n) atomicAdd(&hist[run_bin], run_n);
-    }
-    __syncthreads();
-    int above;
-    const int b = find_bin<NT>(hist, nb, need, &above, scratch);
-    need -= above;
-    prefix = (prefix << (hib - lob)) | (uint32_t)b;
-    hib = lob;
-  }
-  const uint32_t T = prefix;     // the k-th d (>= 1)
-  const int above = k - need;    // values > T
-  const int ties_needed = need;  // values == T taken, lowest positions first
-  // the 12-bit groups are defined on the true keys d + kbase; d = 0 is in no group
-  Scan3 c = {0, 0, 0};
-  const uint32_t tb = (T + kbase) >> 20;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const uint32_t v = d[i];
-    const uint32_t hi = (v + kbase) >> 20;
-    c.a += v != 0u && hi > tb;
-    c.b += v != 0u && hi == tb && v > T;
-    c.c += v == T;
-  }
-  Scan3 tot;
-  Scan3 off = block_scan3<NT>(c, &tot, scratch);
-  int o1 = off.a, o2 = tot.a + off.b, r3 = off.c;
-  // an opaque copy: the group tests below are recomputed, not kept from the count
-  // loop (keeping 3 x PER lane masks alive across the scan overflows the SGPRs)
-#pragma unroll
-  for (int i = 0; i < PER; ++i) asm volatile("" : "+v"(d[i]));
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const uint32_t v = d[i];
-    const bool g1 = v != 0u && ((v + kbase) >> 20) > tb;
-    const bool g2 = !g1 && v > T;
-    const bool g3 = v == T;
-    const int dst = g1 ? o1 : (g2 ? o2 : ((g3 && r3 < ties_needed) ? above + r3 : -1));
-    o1 += g1;
-    o2 += g2;
-    r3 += g3;
-    if (dst >= 0 && dst < k) st_dev_i32(orow + dst, pos(i));
-  }
-}
-
 constexpr int TOPK_CAP = 16384;  // candidates the select keeps in LDS
 constexpr int TOPK_MAXN = 65536; // positions a row
 
@@ -544,7 +480,7 @@ MK2_DEV void idx_clear_hist(const IdxDev& p, int r) {
 // sets it).  Returns whether S.res[0..1] now hold b1 and the count above it.
 constexpr int CC_FLAG = 1 << 30;
 template <int NT>
-MK2_DEV bool idx_slice(const IdxDev& p, int r, int chunk, TopkLds& S, int spin, int* err) {
+MK2_DEV bool idx_slice(const IdxDev& p, int r, int chunk, TopkLds& S, int spin, int* err, uint32_t tag) {
   constexpr int PER = IDX_CHUNK / NT;  // consecutive positions a thread
   static_assert(PER % 4 == 0, "a thread reads whole 16-byte groups of scores");
   const int tid = threadIdx.x;
@@ -616,12 +552,12 @@ MK2_DEV bool idx_slice(const IdxDev& p, int r, int chunk, TopkLds& S, int spin, 
     if (tid == 0) S.res[2] = pre;
   }
   __syncthreads();
-  int* orow = p.out + (size_t)r * k;
+  const ListOut lo = list_out(p, r, tag);
   at = S.res[2] + off.a;  // < the count above bin b1 < k (checked all the same)
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     if (base + i < n && (key[i] >> 20) > b1) {
-      if (at < k) st_dev_i32(orow + at, base + i);
+      if (at < k) lo.put(at, base + i);
       ++at;
     }
   }
@@ -633,12 +569,12 @@ MK2_DEV bool idx_slice(const IdxDev& p, int r, int chunk, TopkLds& S, int spin, 
 // base + k - 1, streamed over the candidates in global memory, NT at a time in
 // position order.
 template <int NT>
-MK2_DEV void topk_stream(const IdxDev& p, int r, uint32_t kbase, int m, int k, int base, TopkLds& S) {
+MK2_DEV void topk_stream(const IdxDev& p, int r, uint32_t kbase, int m, int k, int base, TopkLds& S,
+                         const ListOut& lo) {
   constexpr int NW = NT / 64;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nchk = p.nchk;
   const uint2* cr = p.cand + (size_t)r * p.max_ctx;
-  int* orow = p.out + (size_t)r * p.topk;
   auto cand_d = [&](int j) -> uint32_t {  // candidate j (position order) - kbase
     int lo = 0, hi = nchk;
     while (hi - lo > 1) {
@@ -713,7 +649,7 @@ MK2_DEV void topk_stream(const IdxDev& p, int r, uint32_t kbase, int m, int k, i
     if (g1) dst = o1 + off.a;
     else if (g2) dst = n1 + o2 + off.b;
     else if (g3 && r3 + off.c < ties_needed) dst = above_T + r3 + off.c;
-    if (dst >= 0 && dst < k) st_dev_i32(orow + base + dst, cand_pos(j));
+    if (dst >= 0 && dst < k) lo.put(base + dst, cand_pos(j));
     o1 += tot.a;
     o2 += tot.b;
     r3 += tot.c;
@@ -730,7 +666,7 @@ MK2_DEV void topk_stream(const IdxDev& p, int r, uint32_t kbase, int m, int k, i
 // candidate's rank in its group is its wave's offset for the round (one scan over all
 // (round, wave) counts) plus the ballot count of the lanes below it.
 template <int NT, int CPT>
-MK2_DEV void bin_select(TopkLds& S, int m, int base, int k, int* orow) {
+MK2_DEV void bin_select(TopkLds& S, int m, int base, int k, const ListOut& lo) {
   constexpr int NW = NT / 64;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
@@ -808,7 +744,7 @@ MK2_DEV void bin_select(TopkLds& S, int m, int base, int k, int* orow) {
       const int r3 = S.gcount[1][e] + __popcll(b3m & below);
       if (r3 < ties) dst = base + n_gt + r3;
     }
-    if (dst >= 0 && dst < k) st_dev_i32(orow + dst, (int)S.cpos[j]);
+    if (dst >= 0 && dst < k) lo.put(dst, (int)S.cpos[j]);
   }
 }
 
@@ -819,16 +755,16 @@ MK2_DEV void bin_select(TopkLds& S, int m, int base, int k, int* orow) {
 // `known`: S.res[0..1] already hold b1 and above1 (the workgroup ran one of the
 // row's slices just before).
 template <int NT>
-MK2_DEV void idx_select(const IdxDev& p, int r, TopkLds& S, bool known = false) {
+MK2_DEV void idx_select(const IdxDev& p, int r, TopkLds& S, uint32_t tag, bool known = false) {
   constexpr int CPT = TOPK_CAP / NT;                  // candidates a thread
   constexpr int TPC = NT / (TOPK_MAXN / IDX_CHUNK);   // gather threads a chunk
   constexpr int SPEC = 8;                             // candidates a thread loads with the counts
   const int tid = threadIdx.x;
   const int n = p.ctx[r];
   const int k = p.topk;
-  int* orow = p.out + (size_t)r * k;
+  const ListOut lo = list_out(p, r, tag);
   if (n <= k) {
-    for (int i = tid; i < k; i += NT) st_dev_i32(orow + i, i < n ? i : -1);
+    for (int i = tid; i < k; i += NT) lo.put(i, i < n ? i : -1);
     return;
   }
   const int nchk = p.nchk;
@@ -861,7 +797,7 @@ MK2_DEV void idx_select(const IdxDev& p, int r, TopkLds& S, bool known = false) 
   const int m = tot.a;
   if (m > TOPK_CAP) {
     // keys relative to the bottom of bin b1: d >= 1 for every candidate
-    topk_stream<NT>(p, r, (b1 << 20) - 1u, m, k - above1, above1, S);
+    topk_stream<NT>(p, r, (b1 << 20) - 1u, m, k - above1, above1, S, lo);
     return;
   }
   if (c < nchk) {
@@ -892,7 +828,7 @@ MK2_DEV void idx_select(const IdxDev& p, int r, TopkLds& S, bool known = false) 
     }
   }
   __syncthreads();
-  bin_select<NT, CPT>(S, m, above1, k, orow);
+  bin_select<NT, CPT>(S, m, above1, k, lo);
 }
 
 // Row r's top-k state back to zero for the next launch (every reader is done): the

@@ -35,11 +35,10 @@ constexpr int K2_LANES = 16;
 enum : int {
   SY_SCORE = 0,    // [32] score chunks done, per row
   SY_SLICE = 32,   // [32] top-k slices done, per row
-  SY_TOPK = 64,    // [32] top-k done, per row
+  // lines 64 .. 95: unused (the splits poll the tagged top-k list)
   SY_SPLIT = 96,   // [32] attention splits done, per row
-  SY_ROUTE = 128,
-  SY_ROUTER_LAST,  // router sub-counters completed (the last runs the routing)
-  SY_DONE,         // workgroups finished (the last one resets)
+  SY_ROUTE = 128,  // the routing's table and list are out (the down)
+  SY_DONE = 130,   // workgroups finished (the last one resets)
   SY_ERR,          // sticky: a wait ran out of its spin limit
   SY_UV = 144,     // [K2_LANES] sub-counters each: merged + W_UV (row, head, half) tasks
   SY_OPROJ = SY_UV + K2_LANES,
@@ -47,6 +46,7 @@ enum : int {
   SY_UP = SY_ROUTER + K2_LANES,
   SY_LINES = SY_UP + K2_LANES  // 208 lines = 26 KiB
 };
+static_assert(SY_LINES * SY_LINE <= SYNC_EPOCH, "the counters stay clear of the epoch word");
 
 struct K2Dev {
   IdxDev idx;
@@ -59,8 +59,9 @@ struct K2Dev {
   int spin_limit;
 };
 
-// timeline: per stage s, stamps 3s (enter), 3s+1 (first input ready), 3s+2 (leave)
-constexpr int K2_STAGES = 10, K2_STAMPS = 3 * K2_STAGES + 1;
+// timeline: per stage s, stamps 3s (enter), 3s+1 (first input ready), 3s+2 (leave);
+// then the routing's marks: logits polled, top-k done, list out
+constexpr int K2_STAGES = 10, K2_STAMPS = 3 * K2_STAGES + 3;
 
 MK2_DEV void k2_stamp(const K2Dev& p, int i) {
   if (p.timeline && threadIdx.x == 0) p.timeline[(size_t)blockIdx.x * K2_STAMPS + i] = __builtin_amdgcn_s_memrealtime();
@@ -96,27 +97,8 @@ MK2_DEV void k2_signal(const K2Dev& p, int line, int t = 0, int lanes = 1, int n
     __hip_atomic_fetch_add(k2_ctr(p, line + t % lanes), n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// publish task t of n on a K2_LANES counter and tell whether it completed the set: the
-// last arrival on each sub-counter counts on SY_ROUTER_LAST-style `top`, and the last of
-// those is the last overall.  That workgroup runs the stage that needs all n (no
-// further hand-off, no poll).
-MK2_DEV bool k2_signal_last(const K2Dev& p, int line, int top, int t, int n, int* flag) {
-  drain_memory();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int sub = t % K2_LANES;
-    const int expect = n / K2_LANES + (sub < n % K2_LANES ? 1 : 0);  // tasks on this sub-counter
-    const int subs = n < K2_LANES ? n : K2_LANES;
-    int last = 0;
-    if (__hip_atomic_fetch_add(k2_ctr(p, line + sub), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == expect - 1)
-      last = __hip_atomic_fetch_add(k2_ctr(p, top), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == subs - 1;
-    *flag = last;
-  }
-  __syncthreads();
-  return *flag != 0;
-}
-
-// the same on a single counter of n producers
+// publish one of n producers' tasks on a single counter and tell whether it completed
+// the set: that workgroup runs the stage that needs all n (no further hand-off)
 MK2_DEV bool k2_signal_last1(const K2Dev& p, int line, int n, int* flag) {
   drain_memory();
   __syncthreads();
@@ -180,10 +162,18 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
   __shared__ K2Lds S;
   __shared__ int seen[SY_LINES + 1];  // counts seen by line; [SY_LINES]: a wait failed
   __shared__ int last_flag;
+  __shared__ uint32_t s_tag;
   const int G = gridDim.x, b = blockIdx.x;
   const int R = p.rows;
   for (int i = threadIdx.x; i <= SY_LINES; i += K2_NT) seen[i] = 0;
+  // this launch's tag: one past the epoch the previous launch on this workspace left
+  // (never 0; a zero-filled workspace starts at 1)
+  if (threadIdx.x == 0) {
+    const uint32_t e = (uint32_t)ld_dev_i32(p.sync + SYNC_EPOCH) + 1u;
+    s_tag = e ? e : 1u;
+  }
   __syncthreads();
+  const TagPoll tp{s_tag, p.spin_limit, k2_ctr(p, SY_ERR)};
   // the stages in order; a wait that fails (its spin limit, or another workgroup's
   // failure seen while polling) returns from the walk: the workgroup skips every task
   // left and goes straight to the counter reset (fail-stop)
@@ -209,13 +199,12 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
     K2_TASKS(t, R * nchk) {
       const int r = t / nchk;
       if (!k2_wait(p, seen, SY_SCORE + r, nchk, t < G ? 3 * st + 1 : -1)) return;
-      const bool known = idx_slice<K2_NT>(p.idx, r, t % nchk, S.topk, p.spin_limit, k2_ctr(p, SY_ERR));
+      const bool known = idx_slice<K2_NT>(p.idx, r, t % nchk, S.topk, p.spin_limit, k2_ctr(p, SY_ERR), tp.tag);
       if (k2_signal_last1(p, SY_SLICE + r, nchk, &last_flag)) {
         k2_stamp(p, 3 * (st + 1));
         k2_stamp(p, 3 * (st + 1) + 1);
         // this workgroup's own slice of row r may have left the threshold in LDS
-        idx_select<K2_NT>(p.idx, r, S.topk, known);
-        k2_signal(p, SY_TOPK + r);
+        idx_select<K2_NT>(p.idx, r, S.topk, tp.tag, known);
         k2_stamp(p, 3 * (st + 1) + 2);
         idx_topk_reset<K2_NT>(p.idx, r);  // every slice of the row is done with them
       }
@@ -228,8 +217,11 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
     const int ns = p.mla.nsplit;
     K2_TASKS(t, R * ns) {
       const int r = t / ns;
-      if (!k2_wait(p, seen, SY_TOPK + r, 1, t < G ? 3 * st + 1 : -1)) return;
-      mla_split<K2_NT>(p.mla, r, t % ns, S.split);
+      // the split polls its 64 entries of the tagged list: it starts as soon as they are
+      // out (most come from the slices, ahead of the row's select)
+      const int stamp = t < G ? 3 * st + 1 : -1;
+      if (!mla_split<K2_NT>(p.mla, r, t % ns, S.split, tp, [&](int) { if (stamp >= 0) k2_stamp(p, stamp); }))
+        return;
       k2_signal(p, SY_SPLIT + r);
     }
     K2_NEXT(R * ns);
@@ -258,39 +250,41 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
     }
     K2_NEXT(ht);
     k2_stamp(p, 3 * st++ + 2);
-    // ---- router GEMV (+ RMSNorm of its slice), per (16 experts, hidden slice)
+    // ---- router GEMV (+ RMSNorm of its slice), per (16 experts, hidden slice): the
+    // partial logits go out as tagged words (the routing polls them); the counter
+    // publishes the normalized rows the tasks of the first expert tile store
     k2_stamp(p, 3 * st);
     const int et = p.moe.E / 16, nrt = et * p.moe.KC;
     K2_TASKS(t, nrt) {
-      moe_router<K2_NT, NCG>(p.moe, t % et, t / et, S.router,
+      moe_router<K2_NT, NCG>(p.moe, t % et, t / et, S.router, tp.tag,
                              [&] { return k2_wait(p, seen, SY_OPROJ, ht, t < G ? 3 * st + 1 : -1, K2_LANES); });
       if (seen[SY_LINES]) return;
-      // the last router task computes the routing
-      if (k2_signal_last(p, SY_ROUTER, SY_ROUTER_LAST, t, nrt, &last_flag)) {
-        k2_stamp(p, 3 * (st + 1));
-        k2_stamp(p, 3 * (st + 1) + 1);
-        // SY_ROUTE: 1 once the distinct-expert list is out (up/gate), 2 with the table (down)
-        moe_route<K2_NT>(p.moe, S.route, [&] { k2_signal(p, SY_ROUTE); });
-        k2_signal(p, SY_ROUTE);
-        k2_stamp(p, 3 * (st + 1) + 2);
-      }
+      k2_signal(p, SY_ROUTER, t, K2_LANES);
     }
     K2_NEXT(nrt);
     k2_stamp(p, 3 * st++ + 2);
-    ++st;  // routing: run by the last router task above
-    // ---- up/gate + SwiGLU: the shared expert's chunks first (they need only the
-    // normalized rows, stored by the router tasks, so they run while routing is still
-    // pending), then the routed slots
-    k2_stamp(p, 3 * st);
+    // ---- routing, on one workgroup (one without an up/gate task, when the up/gate
+    // stage leaves some): it polls the router tasks' logits and puts out the tagged
+    // expert list, then the route-weight table, published by SY_ROUTE for the down
     const int up_r = p.moe.Dmax * (p.moe.I / p.moe.UC);
     const int up_sh = p.moe.n_shared * (p.moe.SI / 32);
     const int up_total = up_r + up_sh;
+    if (b == (base + (up_total < G ? up_total : G - 1)) % G) {
+      k2_stamp(p, 3 * st);
+      if (!moe_route<K2_NT>(p.moe, S.route, tp, [&](int i) { k2_stamp(p, 3 * K2_STAGES + i); })) return;
+      k2_stamp(p, 3 * st + 1);
+      k2_signal(p, SY_ROUTE);
+      k2_stamp(p, 3 * st + 2);
+    }
+    ++st;
+    // ---- up/gate + SwiGLU: the shared expert's chunks first (they need only the
+    // normalized rows, so they run while routing is still pending), then the routed
+    // slots, each polling its slot of the tagged expert list
+    k2_stamp(p, 3 * st);
     K2_TASKS(t, up_total) {
       const bool sh = t < up_sh;
-      if (!(sh ? k2_wait(p, seen, SY_ROUTER, nrt, t < G ? 3 * st + 1 : -1, K2_LANES)
-               : k2_wait(p, seen, SY_ROUTE, 1, t < G ? 3 * st + 1 : -1)))
-        return;
-      moe_upgate<K2_NT, NCG>(p.moe, sh ? up_r + t : t - up_sh, S.up.red, S.up.midf);
+      if (!k2_wait(p, seen, SY_ROUTER, nrt, t < G ? 3 * st + 1 : -1, K2_LANES)) return;
+      if (!moe_upgate<K2_NT, NCG>(p.moe, sh ? up_r + t : t - up_sh, S.up.red, S.up.midf, tp)) return;
       k2_signal(p, SY_UP, t, K2_LANES);
     }
     K2_NEXT(up_total);
@@ -298,7 +292,7 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
     // ---- down + route weighting + residual, per 16 hidden rows
     k2_stamp(p, 3 * st);
     K2_TASKS(t, down_tasks(p.moe)) {
-      if (!k2_wait(p, seen, SY_ROUTE, 2)) return;  // the routing and its table: known long before the mid rows
+      if (!k2_wait(p, seen, SY_ROUTE, 1)) return;  // the routing and its table: known long before the mid rows
       moe_down<K2_NT, NCG>(p.moe, t, S.down.red, S.down.act, S.down.xres,
                            [&] { return k2_wait(p, seen, SY_UP, up_total, t < G ? 3 * st + 1 : -1, K2_LANES); });
       if (seen[SY_LINES]) return;
@@ -329,6 +323,8 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
     }
     for (int l = threadIdx.x; l < SY_LINES; l += K2_NT)
       __hip_atomic_store(k2_ctr(p, l), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // the epoch moves on: the next launch's tags differ from every tag of this one
+    if (threadIdx.x == 0) st_dev_i32(p.sync + SYNC_EPOCH, (int)s_tag);
   }
 }
 

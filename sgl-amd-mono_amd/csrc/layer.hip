@@ -22,7 +22,7 @@ int moe_enqueue(const MoeDev& d, hipStream_t st);
 int k2_persistent_enqueue(const IdxDev& idx, const MlaDev& mla, const MoeDev& moe, int* sync,
                           int* status, uint64_t* timeline, int rows, int spin_limit, hipStream_t st);
 
-constexpr int LAYER_SYNC_BYTES = 32 * 1024;  // the persistent launch's counters, a line each
+constexpr int LAYER_SYNC_BYTES = SYNC_INTS * 4;  // the persistent launch's counters and its epoch
 
 struct LayerPlan {
   IdxDev idx;
@@ -64,6 +64,7 @@ int layer_plan(const mk2_layer_args* a, void* ws, LayerPlan* L, size_t* bytes) {
   char* p_mla = c.take<char>(b_mla);
   char* p_moe = c.take<char>(b_moe);
   bf16_t* attn = c.take<bf16_t>((size_t)ms.rows * ms.hidden);
+  uint64_t* tlist = c.take<uint64_t>((size_t)is.rows * is.topk);  // the list as tagged words
   *bytes = c.bytes();
   if (!ws) return MK2_OK;
   L->sync = sync;
@@ -74,6 +75,8 @@ int layer_plan(const mk2_layer_args* a, void* ws, LayerPlan* L, size_t* bytes) {
   if (a->moe.topk_ids) L->moe.topk_ids = a->moe.topk_ids;
   if (a->moe.topk_weights) L->moe.topk_w = a->moe.topk_weights;
   L->mla.sel = L->idx.out;
+  L->idx.tlist = tlist;
+  L->mla.tsel = tlist;
   bf16_t* a_out = a->attn_out ? (bf16_t*)a->attn_out : attn;
   L->mla.out = a_out;
   L->moe.x = a_out;
@@ -112,9 +115,10 @@ static int static_scratch(void** out) {
   return MK2_OK;
 }
 
-// zero what a launch needs zero on entry: the persistent launch's counters and the
-// indexer's histograms, chunk counts and ticket (a fill kernel, so that a captured
-// graph holds no memset node)
+// zero what a launch needs zero on entry: the persistent launch's counters (not its
+// epoch: the tags of the next launch must differ from those of every earlier launch
+// on the array, whatever shape they had) and the indexer's histograms, chunk counts
+// and ticket (a fill kernel, so that a captured graph holds no memset node)
 struct ZeroSpan {
   int* p;
   int n;
@@ -148,7 +152,7 @@ extern "C" int mk2_layer_launch_static(const mk2_layer_args* a, mk2_stream_t str
   if (rc) return rc;
   hipStream_t st = (hipStream_t)stream;
   const IdxDev& x = L.idx;
-  k_layer_zero<<<64, 256, 0, st>>>(ZeroSpan{L.sync, LAYER_SYNC_BYTES / 4}, ZeroSpan{x.hist, x.rows * IDX_BINS},
+  k_layer_zero<<<64, 256, 0, st>>>(ZeroSpan{L.sync, SYNC_EPOCH}, ZeroSpan{x.hist, x.rows * IDX_BINS},
                                    ZeroSpan{x.chist, x.rows * IDX_CBINS}, ZeroSpan{x.ccount, x.rows * x.nchk},
                                    ZeroSpan{x.ticket, 1});
   rc = check_launch("layer (static scratch): clear");

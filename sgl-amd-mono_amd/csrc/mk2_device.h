@@ -260,8 +260,49 @@ MK2_DEV void st_dev_16(void* p, uint4 v) {
 struct NoWait {
   MK2_DEV bool operator()() const { return true; }
 };
+// a stage's optional progress marks (the persistent launch's timeline stamps)
+struct NoMark {
+  MK2_DEV void operator()(int) const {}
+};
 
 // every memory access of this thread has completed (stores are device-visible)
 MK2_DEV void drain_memory() { __builtin_amdgcn_s_waitcnt(0); }
+
+// ----------------------------------------------------------------- tagged hand-offs
+// A 32-bit value one workgroup hands to another inside a persistent launch can travel
+// with the launch's tag in the same 8-byte word, (tag << 32) | value, stored
+// device-coherently.  The consumer polls the word itself until it carries its
+// launch's tag: one memory round trip, with no store drain on the producer, no
+// counter and no second load.  Tags grow by one a launch and are never 0, so a word
+// an earlier launch left, or a zero-filled one, never matches.  Between stream-ordered
+// kernels (one kernel a stage) the stream publishes the words: tag 0, read unchecked.
+struct TagPoll {
+  uint32_t tag;  // this launch's tag; 0: stream-ordered, no checking
+  int spin;      // polls before giving up
+  int* err;      // the launch's sticky error word (set on giving up, seen by every poller)
+};
+MK2_DEV void st_pair(uint64_t* p, uint32_t v, uint32_t tag) {
+  MK2_DEV_ST(uint64_t, p, ((uint64_t)tag << 32) | v);
+}
+MK2_DEV uint64_t ld_pair(const uint64_t* p) { return MK2_DEV_LD(uint64_t, p); }
+MK2_DEV uint32_t pair_value(uint64_t w) { return (uint32_t)w; }
+MK2_DEV bool pair_ready(uint64_t w, const TagPoll& tp) { return tp.tag == 0 || (uint32_t)(w >> 32) == tp.tag; }
+// one wave's verdict after a poll round: all lanes ready (true), or keep polling; on
+// the spin limit or another poller's error the launch is failing: *bad = true
+MK2_DEV bool poll_done(bool ready, int polls, const TagPoll& tp, bool* bad) {
+  if (__ballot(!ready) == 0) return true;
+  if (polls > tp.spin || ((polls & 31) == 0 && tp.err && ld_dev_i32(tp.err))) {
+    if ((threadIdx.x & 63) == 0 && tp.err) atomicOr(tp.err, 1);
+    *bad = true;
+    return true;
+  }
+  return false;
+}
+
+// the sync block at the start of a layer workspace: the persistent launch's counters
+// (one a 128-byte line) and, in its last line, the launch epoch (the last tag used),
+// which no reset or clear touches
+constexpr int SYNC_INTS = 8192;
+constexpr int SYNC_EPOCH = SYNC_INTS - 32;
 
 }  // namespace mk2

@@ -7,7 +7,7 @@ namespace mk2 {
 
 __global__ __launch_bounds__(MLA_NT) void k_mla_split(MlaDev p) {
   __shared__ MlaSplitLds L;
-  mla_split<MLA_NT>(p, blockIdx.y, blockIdx.x, L);
+  mla_split<MLA_NT>(p, blockIdx.y, blockIdx.x, L, TagPoll{0u, 0, nullptr});
 }
 // merge + W_UV and W_o run 512 threads, as in the persistent layer kernel: the same
 // waves split the same sums, so both paths give the same bits

@@ -37,6 +37,8 @@ struct MlaDev {
   const int* pt;
   const int* req;
   const int* sel;        // [rows][topk]
+  const uint64_t* tsel;  // the same list as tagged words (the persistent layer polls
+                         // its split's entries), or null: sel
   const bf16_t* w_uv;    // [16][v_dim][512]
   const uint8_t* w_o;    // tiles of [hidden][16*v_dim]
   const bf16_t* h;       // [rows][hidden] or null
@@ -53,7 +55,7 @@ struct MlaSplitLds {
   uint8_t k[MLA_SPLIT * MLA_KROW];       // gathered rows, row-major
   uint8_t vt[MLA_LAT * MLA_VROW];        // latent dims transposed: [dim][key]
   bf16_t p[MLA_HEADS * (MLA_SPLIT + 8)]; // P' [head][key]
-  int row[MLA_SPLIT];                    // cache row of each key (-1: unused)
+  int row[MLA_SPLIT + 1];                // cache row of each key (-1: unused); [64]: a poll gave up
   float sc[MLA_SPLIT];                   // per-key scale * sm_scale
   float kscale[MLA_SPLIT];
   float red[4][MLA_HEADS];
@@ -62,8 +64,8 @@ struct MlaSplitLds {
 // ---------------------------------------------------------------- stage: split
 // NT = 256 or 512: waves 0-3 run QK and the softmax (16 keys each), every wave
 // gathers and takes a share of the PV dim tiles.
-template <int NT>
-MK2_DEV void mla_split(const MlaDev& p, int r, int s, MlaSplitLds& L) {
+template <int NT, typename Mark = NoMark>
+MK2_DEV bool mla_split(const MlaDev& p, int r, int s, MlaSplitLds& L, const TagPoll& tp, Mark mark = Mark()) {
   constexpr int NW = NT / 64;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, c16 = lane & 15;
   const bool qk_wave = wave < 4;
@@ -77,14 +79,35 @@ MK2_DEV void mla_split(const MlaDev& p, int r, int s, MlaSplitLds& L) {
     for (int ks = 0; ks < 18; ++ks) qa[ks] = __builtin_bit_cast(bf16x8, *(const uint4*)(qr + 32 * ks));
   }
   // resolve the 64 positions to cache rows (one dependent round); the rows' scales
-  // are loaded with the rows below
+  // are loaded with the rows below.  A tagged list is polled here, one entry a lane of
+  // wave 0: the split starts as soon as its own 64 entries are out.
   if (tid < MLA_SPLIT) {
-    const int pos = ldp_i32(selr + tid);
+    int pos;
+    bool bad = false;
+    if (p.tsel) {
+      const uint64_t* src = p.tsel + (size_t)r * p.topk + s * MLA_SPLIT + tid;
+      uint64_t w = ld_pair(src);
+      for (int polls = 1;; polls += 2) {  // two polls in flight
+        const uint64_t w1 = ld_pair(src);
+        if (poll_done(pair_ready(w, tp), polls, tp, &bad)) break;
+        w = ld_pair(src);
+        if (poll_done(pair_ready(w1, tp), polls + 1, tp, &bad)) {
+          w = w1;
+          break;
+        }
+      }
+      pos = (int)pair_value(w);
+    } else {
+      pos = ldp_i32(selr + tid);
+    }
+    if (tid == 0) L.row[MLA_SPLIT] = bad;  // wave-uniform
     int row = -1;
     if (pos >= 0 && pos < p.stride * 64) row = ptr[pos >> 6] * 64 + (pos & 63);
     L.row[tid] = row;
   }
+  if (tid == 0) mark(0);
   __syncthreads();
+  if (L.row[MLA_SPLIT]) return false;
   float ksc = 0.f;
   if (tid < MLA_SPLIT) {
     const int row = L.row[tid];
@@ -213,6 +236,7 @@ MK2_DEV void mla_split(const MlaDev& p, int r, int s, MlaSplitLds& L) {
     for (int i = 0; i < 4; ++i) st_dev_f32(orow + (4 * g + i) * MLA_LAT + d0 + c16, o[i]);
   }
   __syncthreads();
+  return true;
 }
 
 // ---------------------------------------------------------------- stage: merge + W_UV

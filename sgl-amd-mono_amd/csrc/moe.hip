@@ -13,19 +13,19 @@ __global__ __launch_bounds__(128) void k_moe_sumsq(MoeDev p) { moe_sumsq<128>(p,
 template <int NCG>
 __global__ __launch_bounds__(ROUTER_NT) void k_moe_router(MoeDev p) {
   __shared__ RouterLds lds;
-  moe_router<ROUTER_NT, NCG>(p, blockIdx.x, blockIdx.y, lds);
+  moe_router<ROUTER_NT, NCG>(p, blockIdx.x, blockIdx.y, lds, 0u);
 }
 
 __global__ __launch_bounds__(512) void k_moe_route(MoeDev p) {
   __shared__ RouteLds lds;
-  moe_route<512>(p, lds);
+  moe_route<512>(p, lds, TagPoll{0u, 0, nullptr});
 }
 
 template <int NCG>
 __global__ __launch_bounds__(MOE_NT) void k_moe_upgate(MoeDev p) {
   __shared__ float red[(MOE_NT / 64) * 8 * 64 * 4];  // NW * 2 * CT * NCG * 256, CT * NCG <= 4
   __shared__ float midf[32 * 65];
-  moe_upgate<MOE_NT, NCG>(p, blockIdx.x, red, midf);
+  moe_upgate<MOE_NT, NCG>(p, blockIdx.x, red, midf, TagPoll{0u, 0, nullptr});
 }
 
 template <int NCG>
@@ -78,11 +78,11 @@ size_t moe_carve(const mk2_moe_shape* s, void* base, MoeDev* d) {
   t.xn = c.take<bf16_t>((size_t)M * H);
   t.xq = c.take<uint8_t>((size_t)M * H);
   t.xs = c.take<uint8_t>((size_t)M * H / 32);
-  t.logit_part = c.take<float>((size_t)KC * M * E);
+  t.logit_part = c.take<uint64_t>((size_t)KC * M * E);
   t.logits = c.take<float>((size_t)M * E);
   t.topk_ids = c.take<int>((size_t)M * s->top_k);
   t.topk_w = c.take<float>((size_t)M * s->top_k);
-  t.act = c.take<int>((size_t)1 + E);
+  t.act = c.take<uint64_t>((size_t)1 + Dmax);
   t.rw = c.take<float>((size_t)Dmax * 32);
   if (s->expert_fmt == MK2_FMT_MXFP4) {
     t.mid_q = c.take<uint8_t>((size_t)Dmax * M * I);

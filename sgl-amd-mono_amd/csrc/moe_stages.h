@@ -37,11 +37,12 @@ struct MoeDev {
   bf16_t* xn;        // [M][H] normalized rows
   uint8_t* xq;       // [M][H] MXFP8 codes (MXFP4 experts)
   uint8_t* xs;       // [M][H/32] E8M0
-  float* logit_part; // [KC][M][E]
+  uint64_t* logit_part; // [KC][M][E] tagged f32 partial logits
   float* logits;     // [M][E]
   int* topk_ids;     // [M][topk]
   float* topk_w;     // [M][topk]
-  int* act;          // [1 + E]: count D, then the distinct expert ids ascending
+  uint64_t* act;     // [1 + Dmax] tagged: count D, then the distinct expert ids ascending
+                     // (-1 past D)
   float* rw;         // [Dmax][32] route weight of slot j for row r (0: not routed)
   uint8_t* mid_q;    // [Dmax][M][I] MXFP8 mid (MXFP4 experts)
   uint8_t* mid_s;    // [Dmax][M][I/32]
@@ -136,7 +137,8 @@ MK2_DEV f32x4 mfma4_bf16(const bf16x8* a, const bf16x8* b, f32x4 c) {
 
 // ------------------------------------------------------------- stage: router GEMV
 // Task (nt, kc): 16 experts x the kc-th slice of hidden (CK = H / KC columns: 1024, or
-// 512 where H is an odd multiple of 512) -> logit_part[kc].  The task normalizes its
+// 512 where H is an odd multiple of 512) -> logit_part[kc], as tagged words (the
+// routing polls them).  The task normalizes its
 // slice of the rows itself: rstd from the rows' partial sums of squares (summed in a
 // fixed order, so that every task gets the same bits), then xn = bf16(x * rstd *
 // gamma) into LDS as the MFMA B operand.  The nt == 0 task of each slice also stores
@@ -151,7 +153,7 @@ struct RouterLds {
 };
 
 template <int NT, int NCG, typename Wait = NoWait>
-MK2_DEV void moe_router(const MoeDev& p, int nt, int kc, RouterLds& L, Wait wait = Wait()) {
+MK2_DEV void moe_router(const MoeDev& p, int nt, int kc, RouterLds& L, uint32_t tag, Wait wait = Wait()) {
   static_assert(NT == ROUTER_NT, "the router task is laid out for 512 threads");
   constexpr int NW = NT / 64, RMAX = 32 * ROUTER_CKMAX / 8 / NT;  // row passes a thread at most
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4;
@@ -261,28 +263,33 @@ MK2_DEV void moe_router(const MoeDev& p, int nt, int kc, RouterLds& L, Wait wait
     const int l = (e16 >> 2) * 16 + s16, i = e16 & 3;
     float v = 0.f;
     for (int w = 0; w < nw_used; ++w) v += L.red[((w * NCG + c) * 64 + l) * 4 + i];
-    st_dev_f32(p.logit_part + ((size_t)kc * p.M + row) * p.E + nt * 16 + e16, v);
+    st_pair(p.logit_part + ((size_t)kc * p.M + row) * p.E + nt * 16 + e16, __float_as_uint(v), tag);
   }
   __syncthreads();
 }
 
 // ------------------------------------------------------------- stage: route
 // One workgroup of NT = 512; wave w takes rows w, w + NW, ...  Lane l holds experts
-// 4l .. 4l+3 of the row: their logits are the slice partials summed in slice order.
-// The row's top-k by (key desc, expert asc): each lane orders its 4 candidates (a
-// stable bubble pass, so equal keys keep expert order), then each of topk rounds
-// takes the largest head key of the wave (DPP max) and, among equal heads, the lowest
-// lane, whose experts all lie below a higher lane's; the winning lane moves its head
-// on.  Round k's pick lands in lane k, so the picks come out ranked.  Then the
-// distinct-expert list (ascending) from the expert flags, and the dense route-weight
-// table rw [slot][row].  `act_published` runs (on the whole workgroup) once the list
-// is stored, before the table is built.
+// 4l .. 4l+3 of the row: their logits are the slice partials, polled as tagged words
+// and summed in slice order.  The row's top-k by (key desc, expert asc): each lane
+// orders its 4 candidates (a stable bubble pass, so equal keys keep expert order), then
+// each of topk rounds takes the largest head key of the wave (DPP max) and, among equal
+// heads, the lowest lane, whose experts all lie below a higher lane's; the winning lane
+// moves its head on.  Round k's pick lands in lane k, so the picks come out ranked.
+// Then the distinct-expert list (ascending) from the expert flags, as tagged words
+// (every slot up to Dmax, -1 past the count, so that an up/gate task polls its own
+// slot and the count together), and the dense route-weight table rw [slot][row] for
+// the down (published by the caller's counter).  Returns false when the launch is
+// failing (a poll gave up).
 struct RouteLds {
   int flag[256];     // expert: 1 if picked, then its slot (-1: none)
   int ids[32 * 8];   // [M][topk]
   float w[32 * 8];   // [M][topk]
   float rw[256 * 32];
+  float lg[32 * 256];  // [M][E] logits
+  float bias[256];
   int tot;
+  int bad;
 };
 
 template <int CTRL, int ROWS>
@@ -299,38 +306,88 @@ MK2_DEV uint32_t wave_max_u32(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
-template <int NT, typename Published = NoWait>
-MK2_DEV void moe_route(const MoeDev& p, RouteLds& L, Published act_published = Published()) {
+template <int NT, typename Mark = NoMark>
+MK2_DEV bool moe_route(const MoeDev& p, RouteLds& L, const TagPoll& tp, Mark mark = Mark()) {
   constexpr int NW = NT / 64;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int el = min(lane, p.E / 4 - 1);  // lanes past E/4 repeat the last group, unused
   const bool sig = p.router == MK2_ROUTER_SIGMOID_BIAS;
-  const float4 bias = sig ? *(const float4*)(p.bias + 4 * el) : make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int e = tid; e < p.E; e += NT) L.flag[e] = 0;
+  // the bias through LDS: no load of it stays in flight past the polls (a wait for it
+  // later would also wait for every store issued since)
+  for (int e = tid; e < p.E; e += NT) {
+    L.flag[e] = 0;
+    L.bias[e] = sig ? p.bias[e] : 0.f;
+  }
   for (int i = tid; i < p.Dmax * 32; i += NT) L.rw[i] = 0.f;
+  if (tid == 0) L.bad = 0;
   __syncthreads();
-  for (int r = wave; r < p.M; r += NW) {
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int kc0 = 0; kc0 < p.KC; kc0 += 8) {
-      float4 t[8];
+  // the logits: each thread takes 16-byte pieces (two experts of a row) of the [M][E]
+  // plane and polls that piece in every slice's plane (coalesced device-coherent loads
+  // of two tagged words) until all carry the tag, then sums the slices in slice order
+  bool bad = false;
+  {
+    const int pieces = p.M * p.E / 2;
+    const uint32_t plane = (uint32_t)(p.M * p.E) * 8u;  // bytes a slice
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)p.logit_part, (short)0, (int)(plane * p.KC), 0x00020000);
+    for (int c0 = 0; c0 < pieces && !bad; c0 += 2 * NT) {
+      float sum[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
+      for (int kc0 = 0; kc0 < p.KC && !bad; kc0 += 4) {
+        i32x4 t[2][4];
+        for (int polls = 1;; ++polls) {
+          bool ready = true;
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        t[u] = ldp_f32x4(p.logit_part + ((size_t)min(kc0 + u, p.KC - 1) * p.M + r) * p.E + 4 * el);
+          for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (kc0 + u < p.KC) {
-          v.x += t[u].x; v.y += t[u].y; v.z += t[u].z; v.w += t[u].w;
+            for (int u = 0; u < 4; ++u) {
+              const int c = min(c0 + tid + i * NT, pieces - 1), kc = min(kc0 + u, p.KC - 1);
+              t[i][u] = __builtin_amdgcn_raw_buffer_load_b128(rs, kc * plane + (uint32_t)c * 16u, 0, 16 /* sc1 */);
+            }
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+              ready = ready && (tp.tag == 0 || ((uint32_t)t[i][u].y == tp.tag && (uint32_t)t[i][u].w == tp.tag));
+          if (poll_done(ready, polls, tp, &bad)) break;
         }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            if (kc0 + u < p.KC) {
+              sum[i][0] += __int_as_float(t[i][u].x);
+              sum[i][1] += __int_as_float(t[i][u].z);
+            }
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int c = c0 + tid + i * NT;
+        if (c < pieces) {
+          L.lg[2 * c] = sum[i][0];
+          L.lg[2 * c + 1] = sum[i][1];
+        }
+      }
     }
+  }
+  if (bad && lane == 0) L.bad = 1;
+  __syncthreads();
+  if (L.bad) return false;
+  mark(0);
+  constexpr float LOG2E = 1.4426950408889634f;
+  for (int r = wave; r < p.M; r += NW) {
+    const float4 v = *(const float4*)(L.lg + r * p.E + 4 * el);
+    const float4 bias = *(const float4*)(L.bias + 4 * el);
     const bool live = 4 * lane < p.E;
     if (p.logits && live) *(float4*)(p.logits + (size_t)r * p.E + 4 * lane) = v;
     const float lg[4] = {v.x, v.y, v.z, v.w}, bs[4] = {bias.x, bias.y, bias.z, bias.w};
+    // the score a pick is weighted by: sigmoid as the reference kernel takes it, rcp(1 +
+    // exp2(-x log2 e)) with the hardware exp2 and rcp; the softmax router's is the logit
     float sv[4];
     uint32_t key[4];
     int ix[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      sv[i] = sig ? 1.0f / (1.0f + expf(-lg[i])) : lg[i];
+      sv[i] = sig ? __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-lg[i] * LOG2E)) : lg[i];
       key[i] = live ? radix_key(sig ? sv[i] + bs[i] : lg[i]) : 0u;  // live keys are > 0
       ix[i] = i;
     }
@@ -347,46 +404,57 @@ MK2_DEV void moe_route(const MoeDev& p, RouteLds& L, Published act_published = P
         key[k - 1] = sw ? tk : key[k - 1];
         ix[k - 1] = sw ? ti : ix[k - 1];
       }
-    int my_e = 0;
-    float my_v = 0.f;
+    // round k takes the wave's largest head key; among equal heads the lowest lane,
+    // whose experts all lie below a higher lane's.  The winning lane moves its head on
+    // and notes the round in which its c-th candidate went.
+    int taken = 0, rk[4] = {-1, -1, -1, -1};
     for (int k = 0; k < p.topk; ++k) {
       const uint32_t top = wave_max_u32(key[0]);
       const int wl = __ffsll((unsigned long long)__ballot(key[0] == top)) - 1;
-      const int wi = __builtin_amdgcn_readlane(ix[0], wl);
-      const float hv = wi == 0 ? sv[0] : wi == 1 ? sv[1] : wi == 2 ? sv[2] : sv[3];
-      const float wv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, hv), wl));
-      if (lane == k) {
-        my_e = 4 * wl + wi;
-        my_v = wv;
+      if (lane == wl) {
+        rk[0] = taken == 0 ? k : rk[0];
+        rk[1] = taken == 1 ? k : rk[1];
+        rk[2] = taken == 2 ? k : rk[2];
+        rk[3] = taken == 3 ? k : rk[3];
+        ++taken;
+        key[0] = key[1];
+        key[1] = key[2];
+        key[2] = key[3];
+        key[3] = 0u;
       }
-      const bool win = lane == wl;
-      key[0] = win ? key[1] : key[0];
-      ix[0] = win ? ix[1] : ix[0];
-      key[1] = win ? key[2] : key[1];
-      ix[1] = win ? ix[2] : ix[1];
-      key[2] = win ? key[3] : key[2];
-      ix[2] = win ? ix[3] : ix[2];
-      key[3] = win ? 0u : key[3];
     }
+    // the picks to LDS by round, then lane k holds pick k
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      if (c < taken) {
+        const int i = ix[c];
+        L.ids[r * p.topk + rk[c]] = 4 * lane + i;
+        L.w[r * p.topk + rk[c]] = i == 0 ? sv[0] : i == 1 ? sv[1] : i == 2 ? sv[2] : sv[3];
+      }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are done
+    __builtin_amdgcn_wave_barrier();
+    const int my_e = lane < p.topk ? L.ids[r * p.topk + lane] : 0;
+    const float my_v = lane < p.topk ? L.w[r * p.topk + lane] : 0.f;
     float w;
     if (sig) {
       const float tot = wave_sum(lane < p.topk ? my_v : 0.f);
-      w = my_v / tot * p.route_scale;
+      w = my_v * (__builtin_amdgcn_rcpf(tot) * p.route_scale);
     } else {
       const float top = wave_max(lane < p.topk ? my_v : -INFINITY);
-      const float ex = lane < p.topk ? expf(my_v - top) : 0.f;
-      w = ex / wave_sum(ex);
+      const float ex = lane < p.topk ? __builtin_amdgcn_exp2f((my_v - top) * LOG2E) : 0.f;
+      w = ex * __builtin_amdgcn_rcpf(wave_sum(ex));
     }
     if (lane < p.topk) {
       st_dev_i32(p.topk_ids + r * p.topk + lane, my_e);
       st_dev_f32(p.topk_w + r * p.topk + lane, w);
-      L.ids[r * p.topk + lane] = my_e;
       L.w[r * p.topk + lane] = w;
       L.flag[my_e] = 1;
     }
   }
   __syncthreads();
-  // the distinct experts, ascending (one wave: four ballots over e = lane + 64 i)
+  mark(1);
+  // the distinct experts, ascending (one wave: four ballots over e = lane + 64 i); the
+  // list's slots past the count hold -1
   if (wave == 0) {
     const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
     int tot = 0;
@@ -398,23 +466,25 @@ MK2_DEV void moe_route(const MoeDev& p, RouteLds& L, Published act_published = P
       if (e < p.E) {
         const int pos = tot + __popcll(m & below);
         L.flag[e] = f ? pos : -1;
-        if (f) st_dev_i32(p.act + 1 + pos, e);
+        if (f) st_pair(p.act + 1 + pos, (uint32_t)e, tp.tag);
       }
       tot += __popcll(m);
     }
+    for (int j = tot + lane; j < p.Dmax; j += 64) st_pair(p.act + 1 + j, 0xFFFFFFFFu, tp.tag);
     if (lane == 0) {
-      st_dev_i32(p.act, tot);
+      st_pair(p.act, (uint32_t)tot, tp.tag);
       L.tot = tot;
     }
   }
   __syncthreads();
-  act_published();  // the up/gate stage needs only the list; the table follows
+  mark(2);
   const int total = L.tot;
   for (int idx = tid; idx < p.M * p.topk; idx += NT) L.rw[L.flag[L.ids[idx]] * 32 + idx / p.topk] = L.w[idx];
   __syncthreads();
   for (int idx = 4 * tid; idx < total * 32; idx += 4 * NT)
     st_dev_16(p.rw + idx, make_uint4(__float_as_uint(L.rw[idx]), __float_as_uint(L.rw[idx + 1]),
                                      __float_as_uint(L.rw[idx + 2]), __float_as_uint(L.rw[idx + 3])));
+  return true;
 }
 
 // ------------------------------------------------------- stage: up/gate + SwiGLU
@@ -565,20 +635,48 @@ MK2_DEV void upgate_chunk(const MoeDev& p, bool shared, int j, int e, int c, flo
 // task t < Dmax * (I / UC): routed slot j = t / (I / UC), chunk of UC rows; past that
 // the shared expert's 32-row chunks.  red: NW * 2 * CT * NCG * 256 floats (CT = UC/16);
 // midf: 32 * (UC + 1) floats.
+// Routed slot j's expert from the routing's tagged list: one wave polls the count and
+// the slot's word together (-1 past the list); -2 when the launch is failing.
+MK2_DEV int slot_expert(const MoeDev& p, int j, const TagPoll& tp, int* lds) {
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    bool bad = false;
+    // two polls in flight: the next is issued before the last one is looked at
+    const uint64_t* src = p.act + (lane ? 1 + j : 0);
+    uint64_t w = lane < 2 ? ld_pair(src) : 0;
+    for (int polls = 1;; polls += 2) {
+      const uint64_t w1 = lane < 2 ? ld_pair(src) : 0;
+      if (poll_done(lane >= 2 || pair_ready(w, tp), polls, tp, &bad)) break;
+      w = lane < 2 ? ld_pair(src) : 0;
+      if (poll_done(lane >= 2 || pair_ready(w1, tp), polls + 1, tp, &bad)) {
+        w = w1;
+        break;
+      }
+    }
+    const int cnt = __builtin_amdgcn_readlane((int)pair_value(w), 0);
+    const int e = __builtin_amdgcn_readlane((int)pair_value(w), 1);
+    if (lane == 0) *lds = bad ? -2 : (j >= cnt || e < 0 || e >= p.E ? -1 : e);
+  }
+  __syncthreads();
+  const int e = *lds;
+  __syncthreads();
+  return e;
+}
+
 template <int NT, int NCG>
-MK2_DEV void moe_upgate(const MoeDev& p, int t, float* red, float* midf) {
+MK2_DEV bool moe_upgate(const MoeDev& p, int t, float* red, float* midf, const TagPoll& tp) {
   const int chunks_r = p.I / p.UC;
   if (t < p.Dmax * chunks_r) {
     const int j = t / chunks_r, c = t % chunks_r;
-    // the list's length and slot j's expert in one round trip (slot j < Dmax <= E is
-    // inside the list's area; past the length its entry is not used)
-    const int nact = ldp_i32(p.act), e = ldp_i32(p.act + 1 + j);
-    if (j >= nact || e < 0 || e >= p.E) return;
+    const int e = slot_expert(p, j, tp, (int*)midf);
+    if (e == -2) return false;
+    if (e < 0) return true;
     if (NCG == 1 && p.UC == 64) upgate_chunk<NT, NCG, (NCG == 1 ? 4 : 2)>(p, false, j, e, c, red, midf);
     else upgate_chunk<NT, NCG, 2>(p, false, j, e, c, red, midf);
   } else {
     upgate_chunk<NT, NCG, 2>(p, true, 0, 0, t - p.Dmax * chunks_r, red, midf);
   }
+  return true;
 }
 
 // ---------------------------------------------------------- stage: down + combine
@@ -592,8 +690,10 @@ template <int NT, int NCG, int DT, typename Wait>
 MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, float* xres, Wait wait) {
   constexpr int NW = NT / 64;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, c16 = lane & 15;
-  const int D = min(ldp_i32(p.act), p.Dmax);
-  for (int j = threadIdx.x; j < D; j += NT) act_ids[j] = min(max(ldp_i32(p.act + 1 + j), 0), p.E - 1);
+  // the list, published by the routing's counter; read device-coherently: up/gate
+  // tasks on this XCD polled its words before all of them were out
+  const int D = min((int)pair_value(ld_pair(p.act)), p.Dmax);
+  for (int j = threadIdx.x; j < D; j += NT) act_ids[j] = min(max((int)pair_value(ld_pair(p.act + 1 + j)), 0), p.E - 1);
   __syncthreads();
   const int HT = p.H / 16;
   // the task's rows: tile tl[d], rows rlo[d] .. rhi[d] - 1 of it (every row of DT tiles,

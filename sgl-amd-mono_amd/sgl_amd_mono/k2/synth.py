@@ -160,3 +160,19 @@ def make_layer(cfg: C.K2Config, rows: int, seed: int, device, h_std: float = 1.0
     mla.sel = None  # the chain supplies the indexer's selection
     moe = make_moe(cfg.moe, rows, seed + 2, device, norm=True)
     return SimpleNamespace(cfg=cfg, rows=rows, idx=idx, mla=mla, moe=moe, h=mla.h)
+
+
+def view_rows(L, rows: int):
+    """The first `rows` decode rows of a layer built for more (weights, caches and page
+    tables shared; the per-row inputs sliced, still contiguous)."""
+    if not 1 <= rows <= L.rows:
+        raise ValueError(f"rows must be in [1, {L.rows}]")
+    idx = SimpleNamespace(**vars(L.idx))
+    mla = SimpleNamespace(**vars(L.mla))
+    for ns, names in ((idx, ("q", "w", "req_ids", "ctx_len")), (mla, ("q", "req_ids", "h"))):
+        for n in names:
+            t = getattr(ns, n)
+            if t is not None:
+                setattr(ns, n, t[:rows])
+        ns.rows = rows
+    return SimpleNamespace(cfg=L.cfg, rows=rows, idx=idx, mla=mla, moe=L.moe, h=mla.h)

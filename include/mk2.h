@@ -48,9 +48,18 @@ extern "C" {
 #define MK2_ROUTER_SOFTMAX 0      /* top-k of logits, softmax over the k picked */
 #define MK2_ROUTER_SIGMOID_BIAS 1 /* top-k of sigmoid + bias, sigmoid / sum * scale */
 
-/* expert weight formats */
-#define MK2_FMT_FP8 0   /* E4M3, f32 scale per 128 x 128 block, bf16 activations */
-#define MK2_FMT_MXFP4 1 /* E2M1, E8M0 per 32, activations quantized to MXFP8 per 32 */
+/* expert modes: the routed experts' weight format and what their activations (the
+ * normalized rows and the SwiGLU mid) are quantized to -- the reference's MoE modes
+ * (glm53/gfx950/config.py:88-93) plus MXFP4 rows (kernel.py:1768-1777).  E4M3 weights
+ * carry an f32 scale per 128 x 128 block; E2M1 weights an E8M0 per 32 (tile layouts
+ * below).  The shared expert is always E4M3 weights on bf16 rows. */
+#define MK2_FMT_FP8 0   /* W8A16: E4M3 weights, bf16 activations */
+#define MK2_FMT_MXFP4 1 /* A8W4: E2M1 weights, activations MXFP8 (E8M0 = ceil-pow2 of amax/448) */
+#define MK2_FMT_W8A8 2  /* E4M3 weights, activations E4M3 with an f32 scale per 128
+                           (amax/448; q = clamp(x * 448/amax)) */
+#define MK2_FMT_A16W4 3 /* E2M1 weights widened exactly to bf16, bf16 activations */
+#define MK2_FMT_A4W4 4  /* E2M1 weights, activations MXFP4 (E8M0 = ceil-pow2 of amax/6, at
+                           most 254: AITER's round-up rule; E2M1 round to nearest even) */
 
 typedef void* mk2_stream_t; /* a hipStream_t */
 
@@ -67,7 +76,7 @@ typedef struct mk2_moe_shape {
   int top_k;        /* 1..8 */
   int inter;        /* routed expert intermediate size */
   int router;       /* MK2_ROUTER_* */
-  int expert_fmt;   /* MK2_FMT_* of the routed experts */
+  int expert_fmt;   /* MK2_FMT_*: the routed experts' mode */
   int n_shared;     /* 0 or 1 shared expert, always MK2_FMT_FP8 */
   int shared_inter; /* shared expert intermediate size */
   int norm;         /* 1: RMSNorm(x) * gamma feeds the router and experts */
@@ -81,9 +90,9 @@ typedef struct mk2_moe_weights {
   const void* w_router;    /* bf16 tiles of [E, H] */
   const float* router_bias;/* f32 [E] (sigmoid_bias only) */
   const void* w13;         /* routed gate|up: [E] x tiles of [2*inter, H] */
-  const void* s13;         /* FP8: f32 [E][2*inter/128][H/128]; MXFP4: E8M0 tiles */
+  const void* s13;         /* E4M3 weights: f32 [E][2*inter/128][H/128]; E2M1: E8M0 tiles */
   const void* w2;          /* routed down: [E] x tiles of [H, inter] */
-  const void* s2;          /* FP8: f32 [E][H/128][inter/128]; MXFP4: E8M0 tiles */
+  const void* s2;          /* E4M3 weights: f32 [E][H/128][inter/128]; E2M1: E8M0 tiles */
   const void* ws13;        /* shared gate|up E4M3 tiles of [2*shared_inter, H] */
   const float* ss13;       /* f32 [2*shared_inter/128][H/128] */
   const void* ws2;         /* shared down E4M3 tiles of [H, shared_inter] */

@@ -13,6 +13,12 @@ Formats (all little-endian bytes):
   * MXFP8 (activations): E4M3 codes with one E8M0 per 32; the E8M0 is the
     ceil-power-of-two exponent of amax * f32(1/448), clamped to [1, 254]
     (glm53/gfx950/kernel.py:1752-1766, common/mx.py:26-37).
+  * MXFP4 activations: E2M1 codes with one E8M0 per 32; the E8M0 is AITER's round-up
+    rule, the smallest power of two >= amax * f32(1/6), at most 254 (common/mx.py:40-45,
+    kernel.py:354,1768-1777).
+  * FP8 per-128 activations: E4M3 codes with an f32 scale amax * f32(1/448) per 128;
+    q = clamp(x * 448/amax, +-448) (kernel.py:1740-1750, whose multiplier is the
+    hardware reciprocal: here, as in this build's kernels, the IEEE quotient).
   * radix key: the order-preserving u32 of f32 score bits (glm53/check.py:111-114).
 
 Every function here is pinned by tests/test_oracle_codecs.py (closed forms, brute
@@ -149,6 +155,47 @@ def mxfp8_quant(x: torch.Tensor):
 
 def mxfp8_dequant(b: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
     return e4m3_decode(b) * e8m0_value(scales).repeat_interleave(32, -1)
+
+
+# ----------------------------------------------------------------- MXFP4 activations
+def mxfp4_act_code(amax: torch.Tensor) -> torch.Tensor:
+    """E8M0 of an MXFP4 activation block: ((bits of amax * f32(1/6)) + 0x7FFFFF) >> 23,
+    at most 254 -- the code of the smallest power of two >= amax / 6, 0 for amax = 0
+    (common/mx.py:40-45)."""
+    v = _f32(amax) * torch.tensor(1.0 / FP4_MAX, dtype=torch.float32)
+    bits = v.contiguous().view(torch.int32).to(torch.int64)
+    return (((bits + 0x7FFFFF) >> 23) & 0xFF).clamp(max=254)
+
+
+def mxfp4_act_quant(x: torch.Tensor):
+    """[..., K] f32 -> (bytes [..., K/2], E8M0 [..., K/32]): E2M1 of x / 2^(code - 127),
+    round to nearest even, saturating at 6 (common/mx.py:55-66, kernel.py:1768-1777)."""
+    x = _f32(x)
+    shp = x.shape
+    blocks = x.reshape(*shp[:-1], shp[-1] // 32, 32)
+    code = mxfp4_act_code(blocks.abs().amax(-1))
+    q = (blocks / torch.exp2(code.to(torch.float32) - 127.0)[..., None]).clamp(-FP4_MAX, FP4_MAX)
+    return fp4_pack(e2m1_encode(q).reshape(shp)), code.to(torch.uint8)
+
+
+# --------------------------------------------------------------- FP8 per-128 activations
+def fp8_block_act_quant(x: torch.Tensor):
+    """[..., K] f32 -> (E4M3 bytes [..., K], f32 scales [..., K/128]): per 128 values,
+    scale = amax * f32(1/448) and q = E4M3(clamp(x * (448 / amax), +-448)), RNE; an
+    all-zero block has scale 1 (kernel.py:1740-1750)."""
+    x = _f32(x)
+    shp = x.shape
+    blocks = x.reshape(*shp[:-1], shp[-1] // 128, 128)
+    amax = blocks.abs().amax(-1)
+    nz = amax > 0
+    one = torch.ones_like(amax)
+    scale = torch.where(nz, amax * torch.tensor(1.0 / FP8_MAX, dtype=torch.float32), one)
+    inv = torch.where(nz, torch.tensor(FP8_MAX, dtype=torch.float32) / torch.where(nz, amax, one), one)
+    return e4m3_encode(blocks * inv[..., None]).reshape(shp), scale
+
+
+def fp8_block_act_dequant(b: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    return e4m3_decode(b) * scale.float().repeat_interleave(128, -1)
 
 
 # ------------------------------------------------------------ FP8 with f32 block scales

@@ -158,9 +158,10 @@ def swiglu(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
 
 
 def expert_fp8(x: torch.Tensor, w13: torch.Tensor, w2: torch.Tensor) -> torch.Tensor:
-    """One FP8-weight expert on bf16 rows: g|u = x . W13^T (W13 = [gate; up] dequantized),
-    mid = bf16(silu(g) * u), y = mid . W2^T (f32).  glm53's block-scaled FP8 on bf16
-    activations (glm53/gfx950/kernel.py:28-34 docstring, 1008-1120)."""
+    """One expert on bf16 rows: g|u = x . W13^T (W13 = [gate; up] dequantized), mid =
+    bf16(silu(g) * u), y = mid . W2^T (f32).  glm53's block-scaled FP8 on bf16
+    activations (W8A16, glm53/gfx950/kernel.py:28-34 docstring, 1008-1120); with MXFP4
+    weights dequantized, the A16W4 mode (glm53/gfx950/config.py:91)."""
     inter = w13.shape[0] // 2
     gu = x.float() @ w13.T
     mid = codecs.bf16_round(swiglu(gu[..., :inter], gu[..., inter:]))
@@ -176,6 +177,30 @@ def expert_mxfp4(x: torch.Tensor, w13: torch.Tensor, w2: torch.Tensor) -> torch.
     gu = xq @ w13.T
     mid = swiglu(gu[..., :inter], gu[..., inter:])
     mq = codecs.mxfp8_dequant(*codecs.mxfp8_quant(mid))
+    return mq @ w2.T
+
+
+def expert_a4w4(x: torch.Tensor, w13: torch.Tensor, w2: torch.Tensor) -> torch.Tensor:
+    """One MXFP4-weight expert on MXFP4 rows: x and mid are quantized to MXFP4 per 32
+    (AITER's round-up E8M0) before each product (kernel.py:1768-1777; the reference's
+    MXFP4 x MXFP4 mid, kernel.py:6958-6966)."""
+    inter = w13.shape[0] // 2
+    xq = codecs.mxfp4_dequant(*codecs.mxfp4_act_quant(x.float()))
+    gu = xq @ w13.T
+    mid = swiglu(gu[..., :inter], gu[..., inter:])
+    mq = codecs.mxfp4_dequant(*codecs.mxfp4_act_quant(mid))
+    return mq @ w2.T
+
+
+def expert_w8a8(x: torch.Tensor, w13: torch.Tensor, w2: torch.Tensor) -> torch.Tensor:
+    """One FP8-weight expert on FP8 rows: x and mid are quantized to E4M3 with an f32
+    scale per 128 before each product (MoeMode.W8A8, glm53/gfx950/config.py:89;
+    kernel.py:1740-1750,6967-6985)."""
+    inter = w13.shape[0] // 2
+    xq = codecs.fp8_block_act_dequant(*codecs.fp8_block_act_quant(x.float()))
+    gu = xq @ w13.T
+    mid = swiglu(gu[..., :inter], gu[..., inter:])
+    mq = codecs.fp8_block_act_dequant(*codecs.fp8_block_act_quant(mid))
     return mq @ w2.T
 
 

@@ -155,7 +155,7 @@ MK2_DEV void idx_score(const IdxDev& p, int r, int chunk, IdxScoreLds& L) {
   // CU's first groups behind the whole chip's requests)
   constexpr int KWIN = 4;
   auto issue = [&](int j) {
-    code[j] = *(const uint4*)(pbase[j >> 2] + off_code + (j & 3) * 256);
+    code[j] = ld_stream16(pbase[j >> 2] + off_code + (j & 3) * 256);
     if ((j & 3) == 0) sw[j >> 2] = *(const uint32_t*)(sbase[j >> 2] + off_scale);
   };
 #pragma unroll

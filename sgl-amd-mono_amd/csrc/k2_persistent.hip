@@ -157,7 +157,7 @@ MK2_DEV bool k2_wait(const K2Dev& p, int* seen, int line, int target, int stamp 
   return ok;
 }
 
-template <int NCG>
+template <int NCG, int FMT>
 __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
   __shared__ K2Lds S;
   __shared__ int seen[SY_LINES + 1];  // counts seen by line; [SY_LINES]: a wait failed
@@ -256,7 +256,7 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
     k2_stamp(p, 3 * st);
     const int et = p.moe.E / 16, nrt = et * p.moe.KC;
     K2_TASKS(t, nrt) {
-      moe_router<K2_NT, NCG>(p.moe, t % et, t / et, S.router, tp.tag,
+      moe_router<K2_NT, NCG, FMT>(p.moe, t % et, t / et, S.router, tp.tag,
                              [&] { return k2_wait(p, seen, SY_OPROJ, ht, t < G ? 3 * st + 1 : -1, K2_LANES); });
       if (seen[SY_LINES]) return;
       k2_signal(p, SY_ROUTER, t, K2_LANES);
@@ -284,7 +284,7 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
     K2_TASKS(t, up_total) {
       const bool sh = t < up_sh;
       if (!k2_wait(p, seen, SY_ROUTER, nrt, t < G ? 3 * st + 1 : -1, K2_LANES)) return;
-      if (!moe_upgate<K2_NT, NCG>(p.moe, sh ? up_r + t : t - up_sh, S.up.red, S.up.midf, tp)) return;
+      if (!moe_upgate<K2_NT, NCG, FMT>(p.moe, sh ? up_r + t : t - up_sh, S.up.red, S.up.midf, tp)) return;
       k2_signal(p, SY_UP, t, K2_LANES);
     }
     K2_NEXT(up_total);
@@ -293,7 +293,7 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
     k2_stamp(p, 3 * st);
     K2_TASKS(t, down_tasks(p.moe)) {
       if (!k2_wait(p, seen, SY_ROUTE, 1)) return;  // the routing and its table: known long before the mid rows
-      moe_down<K2_NT, NCG>(p.moe, t, S.down.red, S.down.act, S.down.xres,
+      moe_down<K2_NT, NCG, FMT>(p.moe, t, S.down.red, S.down.act, S.down.xres,
                            [&] { return k2_wait(p, seen, SY_UP, up_total, t < G ? 3 * st + 1 : -1, K2_LANES); });
       if (seen[SY_LINES]) return;
     }
@@ -340,14 +340,18 @@ int k2_persistent_enqueue(const IdxDev& idx, const MlaDev& mla, const MoeDev& mo
   }
   K2Dev p{idx, mla, moe, sync, status, timeline, rows, spin_limit};
   const bool two = rows > 16;
-  int per_cu = 0;
-  hipError_t e = two ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_k2_layer<2>, K2_NT, 0)
-                     : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_k2_layer<1>, K2_NT, 0);
-  if (e != hipSuccess || per_cu < 1)
-    return set_error(MK2_ELAUNCH, "layer: the persistent kernel does not fit one workgroup per CU");
-  if (two) k_k2_layer<2><<<g_cus, K2_NT, 0, st>>>(p);
-  else k_k2_layer<1><<<g_cus, K2_NT, 0, st>>>(p);
-  return check_launch("layer (persistent)");
+  // one instantiation a column-group count and expert mode
+  return with_moe_fmt(moe.fmt, [&](auto F) {
+    constexpr int FMT = decltype(F)::value;
+    int per_cu = 0;
+    hipError_t e = two ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_k2_layer<2, FMT>, K2_NT, 0)
+                       : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_k2_layer<1, FMT>, K2_NT, 0);
+    if (e != hipSuccess || per_cu < 1)
+      return set_error(MK2_ELAUNCH, "layer: the persistent kernel does not fit one workgroup per CU");
+    if (two) k_k2_layer<2, FMT><<<g_cus, K2_NT, 0, st>>>(p);
+    else k_k2_layer<1, FMT><<<g_cus, K2_NT, 0, st>>>(p);
+    return check_launch("layer (persistent)");
+  });
 }
 
 }  // namespace mk2

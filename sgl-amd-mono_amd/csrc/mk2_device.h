@@ -114,6 +114,40 @@ template <int SA, int SB>
 MK2_DEV f32x4 mfma_fp4_fp8(i32x8 a, i32x8 b, f32x4 c, int sa, int sb) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 4, 0, SA, sa, SB, sb);
 }
+// the same product with both operands in one format: FMT 0 = E4M3 (8 dwords each),
+// 4 = E2M1 (the low 4 dwords); E8M0 scale bytes from byte 0 of sa / sb
+template <int FMT>
+MK2_DEV f32x4 mfma_same(i32x8 a, i32x8 b, f32x4 c, int sa, int sb) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, FMT, FMT, 0, sa, 0, sb);
+}
+constexpr int E8M0_ONE = 127;
+
+// ----------------------------------------------------------------- activation quant
+// MXFP4 activations, AITER's round-up rule (the reference's e8m0_roundup): the E8M0
+// code of the smallest power of two >= amax * f32(1/6), at most 254 (0 for amax = 0)
+MK2_DEV uint32_t mxfp4_act_code(float amax) {
+  const uint32_t b = ((__float_as_uint(amax * (1.0f / 6.0f)) + 0x7FFFFFu) >> 23) & 0xFFu;
+  return b < 254u ? b : 254u;
+}
+// 8 f32 over the E8M0 scale `code` -> 8 E2M1 codes in a dword (element 0 in the low
+// nibble), rounded to nearest even and saturating at 6 by the hardware conversion
+MK2_DEV uint32_t f32x8_to_e2m1x8(const float* f, uint32_t code) {
+  const float sc = __uint_as_float(code ? code << 23 : 0x00400000u);  // 2^(code - 127)
+  uint32_t w = 0;
+  w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, f[0], f[1], sc, 0);
+  w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, f[2], f[3], sc, 1);
+  w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, f[4], f[5], sc, 2);
+  w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, f[6], f[7], sc, 3);
+  return w;
+}
+// FP8 per-128 block scale (the reference's quant_scaled): scale = amax * f32(1/448)
+// and the multiplier 448 / amax (IEEE here, where the reference takes the hardware
+// reciprocal); 1 and 1 for an all-zero block
+MK2_DEV void fp8_block_scale(float amax, float* scale, float* inv) {
+  const bool nz = amax > 0.f;
+  *scale = nz ? amax * (1.0f / 448.0f) : 1.0f;
+  *inv = nz ? 448.0f / amax : 1.0f;
+}
 
 // ----------------------------------------------------------------- reductions
 
@@ -213,8 +247,10 @@ MK2_DEV uint32_t radix_key(float f) {
 
 MK2_DEV float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
-template <typename T>
-MK2_DEV T ld_nt(const T* p) { return __builtin_nontemporal_load(p); }
+// a 16-byte piece of a stream read once a launch (weights, index keys, latent-KV
+// rows).  A plain load: the nontemporal form measured 0.8 us slower a layer (the
+// layer at 8 rows, same-box A/B).
+MK2_DEV uint4 ld_stream16(const void* p) { return *(const uint4*)p; }
 
 // ----------------------------------------------------------------- hand-off memory
 // Data that one workgroup hands to another inside a launch.  The L2 of one XCD is not

@@ -124,7 +124,7 @@ MK2_DEV bool mla_split(const MlaDev& p, int r, int s, MlaSplitLds& L, const TagP
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int row = job < JOBS ? L.row[kg * 4 + j] : -1;
-      v[it][j] = row >= 0 ? *(const uint4*)(p.kv + (size_t)row * MLA_D + dc * 16) : make_uint4(0, 0, 0, 0);
+      v[it][j] = row >= 0 ? ld_stream16(p.kv + (size_t)row * MLA_D + dc * 16) : make_uint4(0, 0, 0, 0);
     }
   }
   if (tid < MLA_SPLIT) {
@@ -265,7 +265,7 @@ MK2_DEV void mla_merge_uv(const MlaDev& p, int r, int h, int hf, MlaMergeLds& L,
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) a[kb * 4 + q] = __builtin_bit_cast(bf16x8, *(const uint4*)(wrow + kb * 128 + 8 * q));
+      for (int q = 0; q < 4; ++q) a[kb * 4 + q] = __builtin_bit_cast(bf16x8, ld_stream16(wrow + kb * 128 + 8 * q));
   };
   bf16x8 a[16];
   if (wave >= 1 && vt0 < vhi) load_a(vt0, a);
@@ -354,7 +354,7 @@ MK2_DEV void mla_oproj(const MlaDev& p, int nt0, int nt1, float* red, Wait wait 
       const int kb = wave + u * NW;
       const uint4* t = (const uint4*)(tiles[j] + ((size_t)min(kb, KB - 1) * 64 + lane) * 64);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) apf[j][u][q] = __builtin_bit_cast(bf16x8, t[q]);
+      for (int q = 0; q < 4; ++q) apf[j][u][q] = __builtin_bit_cast(bf16x8, ld_stream16(t + q));
     }
   // the residual rows (the layer's input, static) for the epilogue: entry idx = tid +
   // i * NT of the ntl * 16 * rows outputs
@@ -411,7 +411,7 @@ MK2_DEV void mla_oproj(const MlaDev& p, int nt0, int nt1, float* red, Wait wait 
     for (int j = 0; j < NTL; ++j) {
       const uint4* t = (const uint4*)(tiles[j] + ((size_t)kb * 64 + lane) * 64);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) a[j][q] = __builtin_bit_cast(bf16x8, t[q]);
+      for (int q = 0; q < 4; ++q) a[j][q] = __builtin_bit_cast(bf16x8, ld_stream16(t + q));
     }
     step(kb, a);
   }

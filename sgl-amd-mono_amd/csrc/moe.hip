@@ -10,10 +10,10 @@ constexpr int MOE_NT = 512;
 
 __global__ __launch_bounds__(128) void k_moe_sumsq(MoeDev p) { moe_sumsq<128>(p, blockIdx.y, blockIdx.x); }
 
-template <int NCG>
+template <int NCG, int FMT>
 __global__ __launch_bounds__(ROUTER_NT) void k_moe_router(MoeDev p) {
   __shared__ RouterLds lds;
-  moe_router<ROUTER_NT, NCG>(p, blockIdx.x, blockIdx.y, lds, 0u);
+  moe_router<ROUTER_NT, NCG, FMT>(p, blockIdx.x, blockIdx.y, lds, 0u);
 }
 
 __global__ __launch_bounds__(512) void k_moe_route(MoeDev p) {
@@ -21,19 +21,19 @@ __global__ __launch_bounds__(512) void k_moe_route(MoeDev p) {
   moe_route<512>(p, lds, TagPoll{0u, 0, nullptr});
 }
 
-template <int NCG>
+template <int NCG, int FMT>
 __global__ __launch_bounds__(MOE_NT) void k_moe_upgate(MoeDev p) {
   __shared__ float red[(MOE_NT / 64) * 8 * 64 * 4];  // NW * 2 * CT * NCG * 256, CT * NCG <= 4
   __shared__ float midf[32 * 65];
-  moe_upgate<MOE_NT, NCG>(p, blockIdx.x, red, midf, TagPoll{0u, 0, nullptr});
+  moe_upgate<MOE_NT, NCG, FMT>(p, blockIdx.x, red, midf, TagPoll{0u, 0, nullptr});
 }
 
-template <int NCG>
+template <int NCG, int FMT>
 __global__ __launch_bounds__(MOE_NT) void k_moe_down(MoeDev p) {
   __shared__ float red[(MOE_NT / 64) * 2 * 64 * 4];  // NW * DT * NCG * 256, DT * NCG <= 2
   __shared__ int act_ids[256];
   __shared__ float xres[16 * 2 * 32];
-  moe_down<MOE_NT, NCG>(p, blockIdx.x, red, act_ids, xres);
+  moe_down<MOE_NT, NCG, FMT>(p, blockIdx.x, red, act_ids, xres);
 }
 
 // ----------------------------------------------------------------- host side
@@ -45,10 +45,10 @@ int moe_check_shape(const mk2_moe_shape* s) {
               "moe: n_experts must be 64, 128, 192 or 256, got %d", s->n_experts);
   MK2_REQUIRE(s->top_k >= 1 && s->top_k <= 8, "moe: top_k must be in [1, 8], got %d", s->top_k);
   MK2_REQUIRE(s->router == MK2_ROUTER_SOFTMAX || s->router == MK2_ROUTER_SIGMOID_BIAS, "moe: unknown router %d", s->router);
-  MK2_REQUIRE(s->expert_fmt == MK2_FMT_FP8 || s->expert_fmt == MK2_FMT_MXFP4, "moe: unknown expert format %d", s->expert_fmt);
-  const int imax = s->expert_fmt == MK2_FMT_FP8 ? 1024 : 4096;
+  MK2_REQUIRE(s->expert_fmt >= MK2_FMT_FP8 && s->expert_fmt <= MK2_FMT_A4W4, "moe: unknown expert mode %d", s->expert_fmt);
+  const int imax = w_fp4(s->expert_fmt) ? 4096 : 1024;
   MK2_REQUIRE(s->inter >= 128 && s->inter % 128 == 0 && s->inter <= imax,
-              "moe: inter must be a multiple of 128 in [128, %d] for this format, got %d", imax, s->inter);
+              "moe: inter must be a multiple of 128 in [128, %d] for this mode, got %d", imax, s->inter);
   MK2_REQUIRE(s->n_shared == 0 || s->n_shared == 1, "moe: n_shared must be 0 or 1");
   if (s->n_shared)
     MK2_REQUIRE(s->shared_inter >= 128 && s->shared_inter % 128 == 0 && s->shared_inter <= 4096,
@@ -70,29 +70,36 @@ size_t moe_carve(const mk2_moe_shape* s, void* base, MoeDev* d) {
   MoeDev t{};
   t.KC = KC;
   t.Dmax = Dmax;
-  t.UC = (s->expert_fmt == MK2_FMT_MXFP4 && M <= 16 && I % 64 == 0) ? 64 : 32;
+  const int fmt = s->expert_fmt;
+  // up/gate chunks: 128 intermediate rows for W8A8 (its mid is quantized per 128), 64
+  // for E2M1 weights up to 16 rows, else 32
+  t.UC = fmt == MK2_FMT_W8A8 ? 128 : (w_fp4(fmt) && M <= 16 && I % 64 == 0) ? 64 : 32;
   // down tasks: 24 hidden rows when hidden is a multiple of 48 (6144: one task a CU of
-  // MI355X), else 32, at MXFP4 and up to 16 rows; 16 otherwise
-  t.DT = (s->expert_fmt == MK2_FMT_MXFP4 && M <= 16) ? (H % 48 == 0 ? 3 : (H % 32 == 0 ? 2 : 1)) : 1;
+  // MI355X), else 32, for the scaled-MFMA E2M1 modes up to 16 rows; 16 otherwise
+  const bool mx_down = fmt == MK2_FMT_MXFP4 || fmt == MK2_FMT_A4W4;
+  t.DT = (mx_down && M <= 16) ? (H % 48 == 0 ? 3 : (H % 32 == 0 ? 2 : 1)) : 1;
   t.ssp = c.take<float>((size_t)(H / 16) * M);
   t.xn = c.take<bf16_t>((size_t)M * H);
   t.xq = c.take<uint8_t>((size_t)M * H);
   t.xs = c.take<uint8_t>((size_t)M * H / 32);
+  t.xsf = c.take<float>((size_t)M * H / 128);
   t.logit_part = c.take<uint64_t>((size_t)KC * M * E);
   t.logits = c.take<float>((size_t)M * E);
   t.topk_ids = c.take<int>((size_t)M * s->top_k);
   t.topk_w = c.take<float>((size_t)M * s->top_k);
   t.act = c.take<uint64_t>((size_t)1 + Dmax);
   t.rw = c.take<float>((size_t)Dmax * 32);
-  if (s->expert_fmt == MK2_FMT_MXFP4) {
+  if (fmt == MK2_FMT_MXFP4 || fmt == MK2_FMT_A4W4 || fmt == MK2_FMT_W8A8) {
     t.mid_q = c.take<uint8_t>((size_t)Dmax * M * I);
-    t.mid_s = c.take<uint8_t>((size_t)Dmax * M * I / 32);
+    if (fmt == MK2_FMT_W8A8) t.mid_sf = c.take<float>((size_t)Dmax * M * I / 128);
+    else t.mid_s = c.take<uint8_t>((size_t)Dmax * M * I / 32);
   } else {
     t.mid_b = c.take<bf16_t>((size_t)Dmax * M * I);
   }
   t.mid_sh = c.take<bf16_t>((size_t)M * (s->n_shared ? s->shared_inter : 0) + 1);
   if (d) {
     d->KC = t.KC; d->Dmax = t.Dmax; d->UC = t.UC; d->DT = t.DT; d->ssp = t.ssp; d->xn = t.xn; d->xq = t.xq; d->xs = t.xs;
+    d->xsf = t.xsf; d->mid_sf = t.mid_sf;
     d->logit_part = t.logit_part; d->logits = t.logits; d->topk_ids = t.topk_ids;
     d->topk_w = t.topk_w; d->act = t.act; d->rw = t.rw; d->mid_q = t.mid_q;
     d->mid_s = t.mid_s; d->mid_b = t.mid_b; d->mid_sh = t.mid_sh;
@@ -125,14 +132,18 @@ int moe_fill(const mk2_moe_args* a, MoeDev* d) {
 int moe_enqueue(const MoeDev& d, hipStream_t st) {
   const int ncg = d.M > 16 ? 2 : 1;
   if (d.norm) k_moe_sumsq<<<dim3(d.H / 512, d.M), 128, 0, st>>>(d);  // H: a multiple of 512
-  if (ncg == 1) k_moe_router<1><<<dim3(d.E / 16, d.KC), ROUTER_NT, 0, st>>>(d);
-  else k_moe_router<2><<<dim3(d.E / 16, d.KC), ROUTER_NT, 0, st>>>(d);
-  k_moe_route<<<1, 512, 0, st>>>(d);
   const int up_tasks = d.Dmax * (d.I / d.UC) + d.n_shared * (d.SI / 32);
-  if (ncg == 1) k_moe_upgate<1><<<up_tasks, MOE_NT, 0, st>>>(d);
-  else k_moe_upgate<2><<<up_tasks, MOE_NT, 0, st>>>(d);
-  if (ncg == 1) k_moe_down<1><<<down_tasks(d), MOE_NT, 0, st>>>(d);
-  else k_moe_down<2><<<down_tasks(d), MOE_NT, 0, st>>>(d);
+  with_moe_fmt(d.fmt, [&](auto F) {
+    constexpr int FMT = decltype(F)::value;
+    if (ncg == 1) k_moe_router<1, FMT><<<dim3(d.E / 16, d.KC), ROUTER_NT, 0, st>>>(d);
+    else k_moe_router<2, FMT><<<dim3(d.E / 16, d.KC), ROUTER_NT, 0, st>>>(d);
+    k_moe_route<<<1, 512, 0, st>>>(d);
+    if (ncg == 1) k_moe_upgate<1, FMT><<<up_tasks, MOE_NT, 0, st>>>(d);
+    else k_moe_upgate<2, FMT><<<up_tasks, MOE_NT, 0, st>>>(d);
+    if (ncg == 1) k_moe_down<1, FMT><<<down_tasks(d), MOE_NT, 0, st>>>(d);
+    else k_moe_down<2, FMT><<<down_tasks(d), MOE_NT, 0, st>>>(d);
+    return 0;
+  });
   return check_launch("moe");
 }
 

@@ -7,9 +7,16 @@
 // walks task lists.  All expert GEMVs run on the matrix cores with the weights as
 // MFMA A (16 output rows a tile) and the decode rows as the 16 (or 32) columns.
 #pragma once
+#include <type_traits>
+
 #include "mk2_device.h"
 
 namespace mk2 {
+
+// the expert modes whose routed weights are E2M1 (the others are E4M3)
+__host__ __device__ inline bool w_fp4(int fmt) {
+  return fmt == MK2_FMT_MXFP4 || fmt == MK2_FMT_A16W4 || fmt == MK2_FMT_A4W4;
+}
 
 struct MoeDev {
   int M, H, E, topk, I, router, fmt, n_shared, SI, norm, residual;
@@ -35,8 +42,9 @@ struct MoeDev {
   // workspace
   float* ssp;        // [H/16][M] the rows' sums of squares over 16 columns (RMSNorm)
   bf16_t* xn;        // [M][H] normalized rows
-  uint8_t* xq;       // [M][H] MXFP8 codes (MXFP4 experts)
-  uint8_t* xs;       // [M][H/32] E8M0
+  uint8_t* xq;       // [M][H] E4M3 codes (A8W4, W8A8) or [M][H/2] E2M1 codes (A4W4)
+  uint8_t* xs;       // [M][H/32] E8M0 (A8W4, A4W4)
+  float* xsf;        // [M][H/128] f32 scales (W8A8)
   uint64_t* logit_part; // [KC][M][E] tagged f32 partial logits
   float* logits;     // [M][E]
   int* topk_ids;     // [M][topk]
@@ -44,9 +52,10 @@ struct MoeDev {
   uint64_t* act;     // [1 + Dmax] tagged: count D, then the distinct expert ids ascending
                      // (-1 past D)
   float* rw;         // [Dmax][32] route weight of slot j for row r (0: not routed)
-  uint8_t* mid_q;    // [Dmax][M][I] MXFP8 mid (MXFP4 experts)
-  uint8_t* mid_s;    // [Dmax][M][I/32]
-  bf16_t* mid_b;     // [Dmax][M][I] bf16 mid (FP8 experts)
+  uint8_t* mid_q;    // [Dmax][M][I] E4M3 mid (A8W4, W8A8) or [Dmax][M][I/2] E2M1 (A4W4)
+  uint8_t* mid_s;    // [Dmax][M][I/32] E8M0 (A8W4, A4W4)
+  float* mid_sf;     // [Dmax][M][I/128] f32 scales (W8A8)
+  bf16_t* mid_b;     // [Dmax][M][I] bf16 mid (W8A16, A16W4)
   bf16_t* mid_sh;    // [M][SI] shared-expert mid
 };
 
@@ -109,11 +118,34 @@ MK2_DEV i32x8 load_b_fp8(const uint8_t* base, int row, int nrows, int ld, int kb
   }
   return b;
 }
+// B operand of an E2M1 x E2M1 product: 32 E2M1 (16 B) of row `row` at byte kb0 (a
+// 128-k block is 64 B), lane group g: k = 32g .. 32g+31 in the low 4 dwords
+MK2_DEV i32x8 load_b_fp4(const uint8_t* base, int row, int nrows, int ld, int kb0, int g) {
+  i32x8 b = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (row < nrows) {
+    const uint4 u = ldp_16(base + (size_t)row * ld + kb0 + 16 * g);
+    b[0] = u.x; b[1] = u.y; b[2] = u.z; b[3] = u.w;
+  }
+  return b;
+}
+// B operand of an E4M3 x E4M3 product: 32 E4M3 of row `row` at k = k0 + 32g .. +31 in
+// 8 dwords, the same k map as the weight tiles' A operand (a dot product is free in its
+// k order as long as both operands share the map)
+MK2_DEV i32x8 load_b_fp8_same(const uint8_t* base, int row, int nrows, int ld, int k0, int g) {
+  i32x8 b = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (row < nrows) {
+    const uint8_t* s = base + (size_t)row * ld + k0 + 32 * g;
+    const uint4 u0 = ldp_16(s), u1 = ldp_16(s + 16);
+    b[0] = u0.x; b[1] = u0.y; b[2] = u0.z; b[3] = u0.w;
+    b[4] = u1.x; b[5] = u1.y; b[6] = u1.z; b[7] = u1.w;
+  }
+  return b;
+}
 // A operand of a bf16 tile: 64 B a lane -> four k-steps
 MK2_DEV void load_a_bf16(const uint8_t* tile, int lane, bf16x8* a) {
   const uint4* s = (const uint4*)(tile + lane * 64);
 #pragma unroll
-  for (int q = 0; q < 4; ++q) a[q] = __builtin_bit_cast(bf16x8, s[q]);
+  for (int q = 0; q < 4; ++q) a[q] = __builtin_bit_cast(bf16x8, ld_stream16(s + q));
 }
 // A operand of an E4M3 tile widened to bf16: 32 B a lane -> four k-steps
 MK2_DEV void load_a_fp8(const uint8_t* tile, int lane, bf16x8* a) {
@@ -125,7 +157,7 @@ MK2_DEV void load_a_fp8(const uint8_t* tile, int lane, bf16x8* a) {
   a[3] = e4m3x8_to_bf16(u1.z, u1.w);
 }
 MK2_DEV i32x8 load_a_fp4(const uint8_t* tile, int lane) {
-  uint4 u = *(const uint4*)(tile + lane * 16);
+  uint4 u = ld_stream16(tile + lane * 16);
   i32x8 a = {(int)u.x, (int)u.y, (int)u.z, (int)u.w, 0, 0, 0, 0};
   return a;
 }
@@ -152,7 +184,7 @@ struct RouterLds {
   bf16_t xn[32 * (ROUTER_CKMAX + 8)];
 };
 
-template <int NT, int NCG, typename Wait = NoWait>
+template <int NT, int NCG, int FMT, typename Wait = NoWait>
 MK2_DEV void moe_router(const MoeDev& p, int nt, int kc, RouterLds& L, uint32_t tag, Wait wait = Wait()) {
   static_assert(NT == ROUTER_NT, "the router task is laid out for 512 threads");
   constexpr int NW = NT / 64, RMAX = 32 * ROUTER_CKMAX / 8 / NT;  // row passes a thread at most
@@ -210,7 +242,7 @@ MK2_DEV void moe_router(const MoeDev& p, int nt, int kc, RouterLds& L, uint32_t 
     *(uint4*)(L.xn + r * XR + c8) = packed;
     if (nt == 0) {
       st_dev_16(p.xn + (size_t)r * p.H + c0 + c8, packed);
-      if (p.fmt == MK2_FMT_MXFP4) {  // a 32-column block is 4 lanes (a DPP quad)
+      if constexpr (FMT == MK2_FMT_MXFP4) {  // a 32-column block is 4 lanes (a DPP quad)
         float amax = 0.f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(f[j]));
@@ -222,6 +254,26 @@ MK2_DEV void moe_router(const MoeDev& p, int nt, int kc, RouterLds& L, uint32_t 
                  make_uint2(f32x4_to_e4m3x4(f[0] * inv, f[1] * inv, f[2] * inv, f[3] * inv),
                             f32x4_to_e4m3x4(f[4] * inv, f[5] * inv, f[6] * inv, f[7] * inv)));
         if ((lane & 3) == 0) st_dev_u8(p.xs + (size_t)r * (p.H / 32) + (c0 + c8) / 32, code);
+      } else if constexpr (FMT == MK2_FMT_A4W4) {  // MXFP4 per 32: a DPP quad
+        float amax = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(f[j]));
+        amax = fmaxf(amax, dpp_f32<DPP_XOR1>(amax));
+        amax = fmaxf(amax, dpp_f32<DPP_XOR2>(amax));
+        const uint32_t code = mxfp4_act_code(amax);
+        st_dev_u32(p.xq + ((size_t)r * p.H + c0 + c8) / 2, f32x8_to_e2m1x8(f, code));
+        if ((lane & 3) == 0) st_dev_u8(p.xs + (size_t)r * (p.H / 32) + (c0 + c8) / 32, code);
+      } else if constexpr (FMT == MK2_FMT_W8A8) {  // E4M3 per 128 with an f32 scale: a DPP row
+        float amax = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(f[j]));
+        amax = row16_max(amax);
+        float qs, inv;
+        fp8_block_scale(amax, &qs, &inv);
+        st_dev_8(p.xq + (size_t)r * p.H + c0 + c8,
+                 make_uint2(f32x4_to_e4m3x4(f[0] * inv, f[1] * inv, f[2] * inv, f[3] * inv),
+                            f32x4_to_e4m3x4(f[4] * inv, f[5] * inv, f[6] * inv, f[7] * inv)));
+        if ((lane & 15) == 0) st_dev_f32(p.xsf + (size_t)r * (p.H / 128) + (c0 + c8) / 128, qs);
       }
     }
   }
@@ -492,7 +544,7 @@ MK2_DEV bool moe_route(const MoeDev& p, RouteLds& L, const TagPoll& tp, Mark mar
 // up tiles of the stacked [gate; up] matrix, against all decode rows; mid =
 // silu(gate) * up.  Each wave owns every NW-th 128-k block and issues the loads of a
 // batch of its blocks (weights, scales, activations) before the first MFMA.
-template <int NT, int NCG, int CT>
+template <int NT, int NCG, int CT, int FMT>
 MK2_DEV void upgate_chunk(const MoeDev& p, bool shared, int j, int e, int c, float* red, float* midf) {
   constexpr int NW = NT / 64, NQ = 2 * CT, R = 16 * CT;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4;
@@ -511,7 +563,9 @@ MK2_DEV void upgate_chunk(const MoeDev& p, bool shared, int j, int e, int c, flo
 #pragma unroll
     for (int cg = 0; cg < NCG; ++cg) acc[q][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  if (!shared && p.fmt == MK2_FMT_MXFP4) {
+  if (!shared && (FMT == MK2_FMT_MXFP4 || FMT == MK2_FMT_A4W4)) {
+    // scaled MFMA: E2M1 weights against MXFP8 (A8W4) or MXFP4 (A4W4) activations
+    constexpr bool a4 = FMT == MK2_FMT_A4W4;
     constexpr int B = CT == 4 ? (NCG == 1 ? 3 : 2) : (NCG == 1 ? 4 : 3);  // k-blocks in flight
     const int G = (KB + 3) / 4;
     const uint8_t* wbase = p.w13 + (size_t)e * NT16 * KB * 1024;
@@ -531,8 +585,8 @@ MK2_DEV void upgate_chunk(const MoeDev& p, bool shared, int j, int e, int c, flo
 #pragma unroll
         for (int cg = 0; cg < NCG; ++cg) {
           const int row = cg * 16 + (lane & 15);
-          b[u][cg] = load_b_fp8(p.xq, row, p.M, p.H, kb * 128, g);
-          sb[u][cg] = row < p.M ? (int)ldp_u8(p.xs + (size_t)row * (p.H / 32) + kb * 4 + g) : 127;
+          b[u][cg] = a4 ? load_b_fp4(p.xq, row, p.M, p.H / 2, kb * 64, g) : load_b_fp8(p.xq, row, p.M, p.H, kb * 128, g);
+          sb[u][cg] = row < p.M ? (int)ldp_u8(p.xs + (size_t)row * (p.H / 32) + kb * 4 + g) : E8M0_ONE;
         }
       }
 #pragma unroll
@@ -542,7 +596,47 @@ MK2_DEV void upgate_chunk(const MoeDev& p, bool shared, int j, int e, int c, flo
         for (int cg = 0; cg < NCG; ++cg)
 #pragma unroll
           for (int q = 0; q < NQ; ++q)
-            acc[q][cg] = mfma_fp4_fp8<0, 0>(a[u][q], b[u][cg], acc[q][cg], sa[u][q], sb[u][cg]);
+            acc[q][cg] = a4 ? mfma_same<4>(a[u][q], b[u][cg], acc[q][cg], sa[u][q], sb[u][cg])
+                            : mfma_fp4_fp8<0, 0>(a[u][q], b[u][cg], acc[q][cg], sa[u][q], sb[u][cg]);
+      }
+    }
+  } else if (!shared && FMT == MK2_FMT_A16W4) {
+    // E2M1 weights widened exactly to bf16 (x their E8M0) right before bf16 MFMAs on the
+    // bf16 rows: no scale to apply after
+    constexpr int B = NCG == 1 ? 2 : 1;
+    const int G = (KB + 3) / 4;
+    const uint8_t* wbase = p.w13 + (size_t)e * NT16 * KB * 1024;
+    const uint8_t* sbase = p.s13 + (size_t)e * NT16 * G * 256;
+    for (int kb0 = wave; kb0 < KB; kb0 += NW * B) {
+      uint4 raw[B][NQ];
+      uint32_t sw[B][NQ];
+      bf16x8 bx[B][NCG][4];
+#pragma unroll
+      for (int u = 0; u < B; ++u) {
+        const int kb = min(kb0 + u * NW, KB - 1);
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+          raw[u][q] = ld_stream16(wbase + (((size_t)nts[q] * KB + kb) * 64 + lane) * 16);
+          sw[u][q] = (*(const uint32_t*)(sbase + (((size_t)nts[q] * G + kb / 4) * 64 + lane) * 4) >> (8 * (kb & 3))) & 0xFFu;
+        }
+#pragma unroll
+        for (int cg = 0; cg < NCG; ++cg)
+          load_b_bf16(p.xn, cg * 16 + (lane & 15), p.M, p.H, kb * 128 + 32 * g, bx[u][cg]);
+      }
+#pragma unroll
+      for (int u = 0; u < B; ++u) {
+        if (kb0 + u * NW >= KB) break;
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+          const float sc = e8m0_to_f32(sw[u][q]);
+          bf16x8 aa[4];
+          aa[0] = e2m1x8_to_bf16(raw[u][q].x, sc);
+          aa[1] = e2m1x8_to_bf16(raw[u][q].y, sc);
+          aa[2] = e2m1x8_to_bf16(raw[u][q].z, sc);
+          aa[3] = e2m1x8_to_bf16(raw[u][q].w, sc);
+#pragma unroll
+          for (int cg = 0; cg < NCG; ++cg) acc[q][cg] = mfma4_bf16(aa, bx[u][cg], acc[q][cg]);
+        }
       }
     }
   } else if constexpr (CT == 2) {
@@ -559,8 +653,8 @@ MK2_DEV void upgate_chunk(const MoeDev& p, bool shared, int j, int e, int c, flo
 #pragma unroll
         for (int q = 0; q < NQ; ++q) {
           const uint4* tl = (const uint4*)(wbase + ((size_t)nts[q] * KB + kb) * 2048 + lane * 32);
-          raw[u][q][0] = tl[0];
-          raw[u][q][1] = tl[1];
+          raw[u][q][0] = ld_stream16(tl);
+          raw[u][q][1] = ld_stream16(tl + 1);
           sc[u][q] = sbase[(nts[q] * 16 / 128) * KB + kb];
         }
 #pragma unroll
@@ -609,7 +703,21 @@ MK2_DEV void upgate_chunk(const MoeDev& p, bool shared, int j, int e, int c, flo
     for (int i = 0; i < 4; ++i) midf[s * (R + 1) + n + i] = silu_mul(gs[i], us[i]);
   }
   __syncthreads();
-  if (!shared && p.fmt == MK2_FMT_MXFP4) {
+  if (!shared && FMT == MK2_FMT_A4W4) {
+    // MXFP4 per 32 values of a row: 32 lanes a block as below, 8 codes a store
+    for (int idx = threadIdx.x; idx < R * p.M; idx += NT) {
+      const int n = idx % R, s = idx / R;
+      const float v = midf[s * (R + 1) + n];
+      const float amax = max_xor16(row16_max(fabsf(v)));
+      const uint32_t code = mxfp4_act_code(amax);
+      const float sc = __uint_as_float(code ? code << 23 : 0x00400000u);
+      const uint32_t q = (uint32_t)__builtin_amdgcn_cvt_scalef32_pk_fp4_f32(0u, v, 0.f, sc, 0) & 0xFu;
+      const uint32_t w = q | (dpp_shl<1>(q) << 4) | (dpp_shl<2>(q) << 8) | (dpp_shl<3>(q) << 12) |
+                         (dpp_shl<4>(q) << 16) | (dpp_shl<5>(q) << 20) | (dpp_shl<6>(q) << 24) | (dpp_shl<7>(q) << 28);
+      if ((n & 7) == 0) st_dev_u32(p.mid_q + (((size_t)j * p.M + s) * p.I + c * R + n) / 2, w);
+      if ((n & 31) == 0) st_dev_u8(p.mid_s + ((size_t)j * p.M + s) * (p.I / 32) + (c * R + n) / 32, code);
+    }
+  } else if (!shared && FMT == MK2_FMT_MXFP4) {
     // MXFP8 per 32 values of a row: 32 lanes (two DPP rows) a block, amax by DPP and a
     // row swap, 4 codes a store (DPP row shifts)
     for (int idx = threadIdx.x; idx < R * p.M; idx += NT) {
@@ -627,6 +735,100 @@ MK2_DEV void upgate_chunk(const MoeDev& p, bool shared, int j, int e, int c, flo
     for (int idx = threadIdx.x; idx < R * p.M; idx += NT) {
       const int n = idx % R, s = idx / R;
       st_dev_u16(dst + (size_t)s * I + c * R + n, f32_to_bf16(midf[s * (R + 1) + n]));
+    }
+  }
+  __syncthreads();
+}
+
+// W8A8 routed chunk c of slot j (expert e): 128 intermediate rows, wave w taking gate
+// tile 8c + w and its up tile over the whole hidden dim (no cross-wave sum), E4M3
+// weights against the rows' E4M3 activations on the scaled MFMA (E8M0 = 1), each
+// k-block's product times w_scale x x_scale (the x scale per decode row, one a lane).
+// mid = silu(g) u is quantized to E4M3 per 128 (the chunk's rows of a decode row: its
+// amax from all eight waves through LDS) with an f32 scale.  red: >= NW * 32 floats.
+template <int NT, int NCG>
+MK2_DEV void upgate_w8a8(const MoeDev& p, int j, int e, int c, float* red) {
+  static_assert(NT / 64 == 8, "eight gate/up tile pairs, one a wave");
+  constexpr int KBB = 2;  // k-blocks a batch
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, c16 = lane & 15;
+  const int KB = p.H / 128, I = p.I;
+  const int NT16 = 2 * I / 16;
+  const int tg = 8 * c + wave, tu = I / 16 + 8 * c + wave;
+  const uint8_t* wbase = p.w13 + (size_t)e * NT16 * KB * 2048;
+  const float* sg = (const float*)p.s13 + ((size_t)e * (2 * I / 128) + c) * KB;
+  const float* su = (const float*)p.s13 + ((size_t)e * (2 * I / 128) + I / 128 + c) * KB;
+  f32x4 ag[NCG], au[NCG];
+#pragma unroll
+  for (int cg = 0; cg < NCG; ++cg) ag[cg] = au[cg] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int kb0 = 0; kb0 < KB; kb0 += KBB) {
+    uint4 rg[KBB][2], ru[KBB][2];
+    i32x8 bq[KBB][NCG];
+    float xs[KBB][NCG], wsg[KBB], wsu[KBB];
+#pragma unroll
+    for (int u = 0; u < KBB; ++u) {
+      const int kb = min(kb0 + u, KB - 1);
+      const uint4* pg = (const uint4*)(wbase + (((size_t)tg * KB + kb) * 64 + lane) * 32);
+      const uint4* pu = (const uint4*)(wbase + (((size_t)tu * KB + kb) * 64 + lane) * 32);
+      rg[u][0] = ld_stream16(pg);
+      rg[u][1] = ld_stream16(pg + 1);
+      ru[u][0] = ld_stream16(pu);
+      ru[u][1] = ld_stream16(pu + 1);
+      wsg[u] = sg[kb];
+      wsu[u] = su[kb];
+#pragma unroll
+      for (int cg = 0; cg < NCG; ++cg) {
+        const int row = cg * 16 + c16;
+        bq[u][cg] = load_b_fp8_same(p.xq, row, p.M, p.H, kb * 128, g);
+        xs[u][cg] = row < p.M ? ldp_f32(p.xsf + (size_t)row * (p.H / 128) + kb) : 0.f;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < KBB; ++u) {
+      if (kb0 + u >= KB) break;
+      const i32x8 A = {(int)rg[u][0].x, (int)rg[u][0].y, (int)rg[u][0].z, (int)rg[u][0].w,
+                       (int)rg[u][1].x, (int)rg[u][1].y, (int)rg[u][1].z, (int)rg[u][1].w};
+      const i32x8 U = {(int)ru[u][0].x, (int)ru[u][0].y, (int)ru[u][0].z, (int)ru[u][0].w,
+                       (int)ru[u][1].x, (int)ru[u][1].y, (int)ru[u][1].z, (int)ru[u][1].w};
+#pragma unroll
+      for (int cg = 0; cg < NCG; ++cg) {
+        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+        ag[cg] += mfma_same<0>(A, bq[u][cg], z, E8M0_ONE, E8M0_ONE) * (wsg[u] * xs[u][cg]);
+        au[cg] += mfma_same<0>(U, bq[u][cg], z, E8M0_ONE, E8M0_ONE) * (wsu[u] * xs[u][cg]);
+      }
+    }
+  }
+  // lane (g, c16) holds intermediate rows 128c + 16w + 4g + i of decode row cg*16 + c16
+  float mid[NCG][4], amax[NCG];
+#pragma unroll
+  for (int cg = 0; cg < NCG; ++cg) {
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      mid[cg][i] = silu_mul(ag[cg][i], au[cg][i]);
+      m = fmaxf(m, fabsf(mid[cg][i]));
+    }
+    m = max_xor16(m);  // the column's 16 rows of this wave: over the four lane groups
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    m = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+    if (g == 0) red[wave * 32 + cg * 16 + c16] = m;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int cg = 0; cg < NCG; ++cg) {
+    float m = 0.f;
+#pragma unroll
+    for (int w = 0; w < 8; ++w) m = fmaxf(m, red[w * 32 + cg * 16 + c16]);
+    amax[cg] = m;
+  }
+#pragma unroll
+  for (int cg = 0; cg < NCG; ++cg) {
+    const int row = cg * 16 + c16;
+    float qs, inv;
+    fp8_block_scale(amax[cg], &qs, &inv);
+    if (row < p.M) {
+      const uint32_t w = f32x4_to_e4m3x4(mid[cg][0] * inv, mid[cg][1] * inv, mid[cg][2] * inv, mid[cg][3] * inv);
+      st_dev_u32(p.mid_q + ((size_t)j * p.M + row) * I + 128 * c + 16 * wave + 4 * g, w);
+      if (wave == 0 && g == 0) st_dev_f32(p.mid_sf + ((size_t)j * p.M + row) * (I / 128) + c, qs);
     }
   }
   __syncthreads();
@@ -663,7 +865,7 @@ MK2_DEV int slot_expert(const MoeDev& p, int j, const TagPoll& tp, int* lds) {
   return e;
 }
 
-template <int NT, int NCG>
+template <int NT, int NCG, int FMT>
 MK2_DEV bool moe_upgate(const MoeDev& p, int t, float* red, float* midf, const TagPoll& tp) {
   const int chunks_r = p.I / p.UC;
   if (t < p.Dmax * chunks_r) {
@@ -671,10 +873,11 @@ MK2_DEV bool moe_upgate(const MoeDev& p, int t, float* red, float* midf, const T
     const int e = slot_expert(p, j, tp, (int*)midf);
     if (e == -2) return false;
     if (e < 0) return true;
-    if (NCG == 1 && p.UC == 64) upgate_chunk<NT, NCG, (NCG == 1 ? 4 : 2)>(p, false, j, e, c, red, midf);
-    else upgate_chunk<NT, NCG, 2>(p, false, j, e, c, red, midf);
+    if constexpr (FMT == MK2_FMT_W8A8) upgate_w8a8<NT, NCG>(p, j, e, c, red);
+    else if (NCG == 1 && p.UC == 64) upgate_chunk<NT, NCG, (NCG == 1 ? 4 : 2), FMT>(p, false, j, e, c, red, midf);
+    else upgate_chunk<NT, NCG, 2, FMT>(p, false, j, e, c, red, midf);
   } else {
-    upgate_chunk<NT, NCG, 2>(p, true, 0, 0, t - p.Dmax * chunks_r, red, midf);
+    upgate_chunk<NT, NCG, 2, FMT>(p, true, 0, 0, t - p.Dmax * chunks_r, red, midf);
   }
   return true;
 }
@@ -686,7 +889,7 @@ MK2_DEV bool moe_upgate(const MoeDev& p, int t, float* red, float* midf, const T
 // rows (shared by the DT tiles) in flight while a unit's MFMAs run.  act_ids: LDS >=
 // E ints; red: NW * DT * NCG * 256 floats; xres: LDS >= 8 * DT * M words (the residual
 // rows, bf16).
-template <int NT, int NCG, int DT, typename Wait>
+template <int NT, int NCG, int DT, int FMT, typename Wait>
 MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, float* xres, Wait wait) {
   constexpr int NW = NT / 64;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, c16 = lane & 15;
@@ -745,7 +948,9 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, float*
       }
     }
   }
-  const bool mx = p.fmt == MK2_FMT_MXFP4;
+  // the scaled-MFMA unit pipeline: E2M1 weights against MXFP8 (A8W4) or MXFP4 (A4W4) mid
+  constexpr bool mx = FMT == MK2_FMT_MXFP4 || FMT == MK2_FMT_A4W4;
+  constexpr bool a4 = FMT == MK2_FMT_A4W4;
   // the residual rows (the W_o output, published before the routing) for the
   // epilogue, straight into LDS (no registers held): dword d of the ncol / 2 * M is
   // row d / (ncol / 2), columns 2 (d % (ncol / 2)) .. + 1 of the task's
@@ -793,7 +998,8 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, float*
 #pragma unroll
         for (int cg = 0; cg < NCG; ++cg) {
           const int row = cg * 16 + c16;
-          x.bq[ub][c][cg] = load_b_fp8(p.mid_q + (size_t)j * p.M * p.I, row, p.M, p.I, kb * 128, g);
+          x.bq[ub][c][cg] = a4 ? load_b_fp4(p.mid_q + (size_t)j * p.M * (p.I / 2), row, p.M, p.I / 2, kb * 64, g)
+                               : load_b_fp8(p.mid_q + (size_t)j * p.M * p.I, row, p.M, p.I, kb * 128, g);
           x.sbq[ub][c][cg] = row < p.M ? (int)ldp_u8(p.mid_s + ((size_t)j * p.M + row) * (p.I / 32) + kb * 4 + g) : 127;
         }
       }
@@ -828,7 +1034,8 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, float*
           const int sak = x.sa[ub][d] >> (8 * (kb & 3));
 #pragma unroll
           for (int cg = 0; cg < NCG; ++cg)
-            tmp[ub][d][cg] = mfma_fp4_fp8<0, 0>(x.a[ub][d][c], x.bq[ub][c][cg], tmp[ub][d][cg], sak, x.sbq[ub][c][cg]);
+            tmp[ub][d][cg] = a4 ? mfma_same<4>(x.a[ub][d][c], x.bq[ub][c][cg], tmp[ub][d][cg], sak, x.sbq[ub][c][cg])
+                                : mfma_fp4_fp8<0, 0>(x.a[ub][d][c], x.bq[ub][c][cg], tmp[ub][d][cg], sak, x.sbq[ub][c][cg]);
         }
       }
     }
@@ -877,7 +1084,7 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, float*
       for (int cg = 0; cg < NCG; ++cg) acc[d][cg] += mfma4_bf16(a, b[cg], f32x4{0.f, 0.f, 0.f, 0.f}) * sc;
     }
   }
-  if (mx) {
+  if constexpr (mx) {
     auto step = [&](int u, Unit& cur, Unit& nxt2) {
       if (u + 2 < nu) {
         load_w(u + 2, nxt2);
@@ -891,32 +1098,91 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, float*
       step(u + 2, x2, x1);
     }
   } else if constexpr (DT == 1) {
-    constexpr int KMAX = 8;  // FP8 experts: inter <= 1024
-    for (int j = wave; j < D; j += NW) {
-      const int e = act_ids[j];
-      const uint8_t* wb = p.w2 + ((size_t)e * HT + tl[0]) * KB2 * 2048;
-      const float* sbase = (const float*)p.s2 + (size_t)e * (p.H / 128) * KB2 + (tl[0] * 16 / 128) * KB2;
-      uint4 raw[KMAX][2];
+    if constexpr (FMT == MK2_FMT_A16W4) {
+      // E2M1 weights widened exactly to bf16 against the bf16 mid, 8 k-blocks a batch
+      constexpr int KMAX = 8;
+      for (int j = wave; j < D; j += NW) {
+        const int e = act_ids[j];
+        const uint8_t* wb = p.w2 + ((size_t)e * HT + tl[0]) * KB2 * 1024;
+        const uint8_t* sb = p.s2 + ((size_t)e * HT + tl[0]) * G2 * 256;
+        f32x4 t[NCG];
 #pragma unroll
-      for (int kb = 0; kb < KMAX; ++kb) {
-        const uint4* tl = (const uint4*)(wb + (size_t)min(kb, KB2 - 1) * 2048 + lane * 32);
-        raw[kb][0] = tl[0];
-        raw[kb][1] = tl[1];
+        for (int cg = 0; cg < NCG; ++cg) t[cg] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int kb0 = 0; kb0 < KB2; kb0 += KMAX) {
+          uint4 raw[KMAX];
+          uint32_t sw[KMAX];
+#pragma unroll
+          for (int u = 0; u < KMAX; ++u) {
+            const int kb = min(kb0 + u, KB2 - 1);
+            raw[u] = ld_stream16(wb + ((size_t)kb * 64 + lane) * 16);
+            sw[u] = (*(const uint32_t*)(sb + ((size_t)(kb / 4) * 64 + lane) * 4) >> (8 * (kb & 3))) & 0xFFu;
+          }
+#pragma unroll
+          for (int u = 0; u < KMAX; ++u) {
+            const int kb = kb0 + u;
+            if (kb >= KB2) break;
+            const float sc = e8m0_to_f32(sw[u]);
+            bf16x8 a[4];
+            a[0] = e2m1x8_to_bf16(raw[u].x, sc);
+            a[1] = e2m1x8_to_bf16(raw[u].y, sc);
+            a[2] = e2m1x8_to_bf16(raw[u].z, sc);
+            a[3] = e2m1x8_to_bf16(raw[u].w, sc);
+#pragma unroll
+            for (int cg = 0; cg < NCG; ++cg) {
+              bf16x8 b[4];
+              load_b_bf16(p.mid_b + (size_t)j * p.M * p.I, cg * 16 + c16, p.M, p.I, kb * 128 + 32 * g, b);
+              t[cg] = mfma4_bf16(a, b, t[cg]);
+            }
+          }
+        }
+#pragma unroll
+        for (int cg = 0; cg < NCG; ++cg) acc[0][cg] += t[cg] * ldp_f32(p.rw + j * 32 + cg * 16 + c16);
       }
+    } else {
+      // E4M3 weights (f32 scale per 128 x 128 block): widened to bf16 against the bf16
+      // mid (W8A16), or on the scaled MFMA against the E4M3 mid (W8A8, f32 scale per 128
+      // a row); each k-block's product times its scales and the route weight
+      constexpr int KMAX = 8;  // inter <= 1024
+      constexpr bool w8a8 = FMT == MK2_FMT_W8A8;
+      for (int j = wave; j < D; j += NW) {
+        const int e = act_ids[j];
+        const uint8_t* wb = p.w2 + ((size_t)e * HT + tl[0]) * KB2 * 2048;
+        const float* sbase = (const float*)p.s2 + (size_t)e * (p.H / 128) * KB2 + (tl[0] * 16 / 128) * KB2;
+        uint4 raw[KMAX][2];
 #pragma unroll
-      for (int kb = 0; kb < KMAX; ++kb) {
-        if (kb >= KB2) break;
-        bf16x8 a[4];
-        a[0] = e4m3x8_to_bf16(raw[kb][0].x, raw[kb][0].y);
-        a[1] = e4m3x8_to_bf16(raw[kb][0].z, raw[kb][0].w);
-        a[2] = e4m3x8_to_bf16(raw[kb][1].x, raw[kb][1].y);
-        a[3] = e4m3x8_to_bf16(raw[kb][1].z, raw[kb][1].w);
-        const float sc = sbase[kb];
+        for (int kb = 0; kb < KMAX; ++kb) {
+          const uint4* tl = (const uint4*)(wb + (size_t)min(kb, KB2 - 1) * 2048 + lane * 32);
+          raw[kb][0] = ld_stream16(tl);
+          raw[kb][1] = ld_stream16(tl + 1);
+        }
 #pragma unroll
-        for (int cg = 0; cg < NCG; ++cg) {
-          bf16x8 b[4];
-          load_b_bf16(p.mid_b + (size_t)j * p.M * p.I, cg * 16 + c16, p.M, p.I, kb * 128 + 32 * g, b);
-          acc[0][cg] += mfma4_bf16(a, b, f32x4{0.f, 0.f, 0.f, 0.f}) * (sc * ldp_f32(p.rw + j * 32 + cg * 16 + c16));
+        for (int kb = 0; kb < KMAX; ++kb) {
+          if (kb >= KB2) break;
+          const float sc = sbase[kb];
+          if constexpr (w8a8) {
+            const i32x8 A = {(int)raw[kb][0].x, (int)raw[kb][0].y, (int)raw[kb][0].z, (int)raw[kb][0].w,
+                             (int)raw[kb][1].x, (int)raw[kb][1].y, (int)raw[kb][1].z, (int)raw[kb][1].w};
+#pragma unroll
+            for (int cg = 0; cg < NCG; ++cg) {
+              const int row = cg * 16 + c16;
+              const i32x8 bq = load_b_fp8_same(p.mid_q + (size_t)j * p.M * p.I, row, p.M, p.I, kb * 128, g);
+              const float ms = row < p.M ? ldp_f32(p.mid_sf + ((size_t)j * p.M + row) * (p.I / 128) + kb) : 0.f;
+              acc[0][cg] += mfma_same<0>(A, bq, f32x4{0.f, 0.f, 0.f, 0.f}, E8M0_ONE, E8M0_ONE) *
+                            (sc * ms * ldp_f32(p.rw + j * 32 + row));
+            }
+          } else {
+            bf16x8 a[4];
+            a[0] = e4m3x8_to_bf16(raw[kb][0].x, raw[kb][0].y);
+            a[1] = e4m3x8_to_bf16(raw[kb][0].z, raw[kb][0].w);
+            a[2] = e4m3x8_to_bf16(raw[kb][1].x, raw[kb][1].y);
+            a[3] = e4m3x8_to_bf16(raw[kb][1].z, raw[kb][1].w);
+#pragma unroll
+            for (int cg = 0; cg < NCG; ++cg) {
+              bf16x8 b[4];
+              load_b_bf16(p.mid_b + (size_t)j * p.M * p.I, cg * 16 + c16, p.M, p.I, kb * 128 + 32 * g, b);
+              acc[0][cg] += mfma4_bf16(a, b, f32x4{0.f, 0.f, 0.f, 0.f}) * (sc * ldp_f32(p.rw + j * 32 + cg * 16 + c16));
+            }
+          }
         }
       }
     }
@@ -949,10 +1215,28 @@ __host__ __device__ inline int down_tasks(const MoeDev& p) { return p.DT == 3 ? 
 // task nt of down_tasks(p).  Needs the routing (act, rw) on entry; `wait` is the
 // mid activations' dependency, run once the task's static and routed weight loads
 // are in flight.
-template <int NT, int NCG, typename Wait = NoWait>
+template <int NT, int NCG, int FMT, typename Wait = NoWait>
 MK2_DEV void moe_down(const MoeDev& p, int nt, float* red, int* act_ids, float* xres, Wait wait = Wait()) {
-  if (NCG == 1 && p.DT >= 2) down_rows<NT, NCG, (NCG == 1 ? 2 : 1)>(p, nt, red, act_ids, xres, wait);
-  else down_rows<NT, NCG, 1>(p, nt, red, act_ids, xres, wait);
+  if constexpr (FMT == MK2_FMT_MXFP4 || FMT == MK2_FMT_A4W4) {
+    if (NCG == 1 && p.DT >= 2) {
+      down_rows<NT, NCG, (NCG == 1 ? 2 : 1), FMT>(p, nt, red, act_ids, xres, wait);
+      return;
+    }
+  }
+  down_rows<NT, NCG, 1, FMT>(p, nt, red, act_ids, xres, wait);
+}
+
+// runs f(std::integral_constant<int, FMT>) for the expert mode fmt (a kernel
+// instantiation a mode, so that each carries only its own mode's code)
+template <typename F>
+inline int with_moe_fmt(int fmt, F&& f) {
+  switch (fmt) {
+    case MK2_FMT_FP8: return f(std::integral_constant<int, MK2_FMT_FP8>{});
+    case MK2_FMT_MXFP4: return f(std::integral_constant<int, MK2_FMT_MXFP4>{});
+    case MK2_FMT_W8A8: return f(std::integral_constant<int, MK2_FMT_W8A8>{});
+    case MK2_FMT_A16W4: return f(std::integral_constant<int, MK2_FMT_A16W4>{});
+    default: return f(std::integral_constant<int, MK2_FMT_A4W4>{});
+  }
 }
 
 }  // namespace mk2

@@ -17,8 +17,13 @@ PAGE = 64  # tokens a KV / index page (glm53/gfx950/config.py page size 64)
 
 ROUTER_SOFTMAX = 0  # softmax over the picked logits (qwen38 style)
 ROUTER_SIGMOID_BIAS = 1  # sigmoid, picked by sigmoid + bias, * route_scale (glm53)
-FMT_FP8 = 0  # E4M3 weights, f32 128 x 128 block scales, bf16 activations
-FMT_MXFP4 = 1  # E2M1 weights, E8M0 per 32, MXFP8 activations
+# expert modes (the reference's MoE modes, glm53/gfx950/config.py:88-93, and MXFP4 rows)
+FMT_FP8 = 0  # W8A16: E4M3 weights, f32 128 x 128 block scales, bf16 activations
+FMT_MXFP4 = 1  # A8W4: E2M1 weights, E8M0 per 32, MXFP8 activations
+FMT_W8A8 = 2  # E4M3 weights, E4M3 activations with an f32 scale per 128
+FMT_A16W4 = 3  # E2M1 weights, bf16 activations
+FMT_A4W4 = 4  # E2M1 weights, MXFP4 activations
+FP4_WEIGHT_FMTS = (FMT_MXFP4, FMT_A16W4, FMT_A4W4)
 
 MAX_ROWS = 32  # decode rows a launch serves (verify: 8 requests x 4 draft tokens)
 
@@ -47,9 +52,9 @@ class MoEConfig:
             raise ValueError(f"top_k must be in [1, 8], got {self.top_k}")
         if self.router not in (ROUTER_SOFTMAX, ROUTER_SIGMOID_BIAS):
             raise ValueError(f"unknown router {self.router}")
-        if self.expert_fmt not in (FMT_FP8, FMT_MXFP4):
-            raise ValueError(f"unknown expert format {self.expert_fmt}")
-        imax = 1024 if self.expert_fmt == FMT_FP8 else 4096
+        if self.expert_fmt not in (FMT_FP8, FMT_MXFP4, FMT_W8A8, FMT_A16W4, FMT_A4W4):
+            raise ValueError(f"unknown expert mode {self.expert_fmt}")
+        imax = 4096 if self.expert_fmt in FP4_WEIGHT_FMTS else 1024
         if self.inter < 128 or self.inter % 128 or self.inter > imax:
             raise ValueError(f"inter must be a multiple of 128 in [128, {imax}] for this format, got {self.inter}")
         if self.n_shared not in (0, 1):

@@ -53,7 +53,7 @@ def make_moe(cfg: C.MoEConfig, rows: int, seed: int, device, norm: bool = False)
         else None
     )
     ns.w_router_p = pack_bf16(ns.w_router)
-    if cfg.expert_fmt == C.FMT_MXFP4:
+    if cfg.expert_fmt in C.FP4_WEIGHT_FMTS:
         w13q = torch.empty(E, 2 * I, H // 2, dtype=torch.uint8, device=device)
         w13s = torch.empty(E, 2 * I, H // 32, dtype=torch.uint8, device=device)
         w2q = torch.empty(E, H, I // 2, dtype=torch.uint8, device=device)

@@ -61,7 +61,7 @@ class MoEOracle:
 
     def expert_weights(self, e):
         if e not in self._cache:
-            if self.cfg.expert_fmt == self.C.FMT_MXFP4:
+            if self.cfg.expert_fmt in self.C.FP4_WEIGHT_FMTS:
                 w13 = oc.mxfp4_dequant(self.w13q[e], self.w13s[e])
                 w2 = oc.mxfp4_dequant(self.w2q[e], self.w2s[e])
             else:
@@ -84,11 +84,12 @@ class MoEOracle:
             route = lambda lg: R.route_sigmoid_bias(lg, self.bias, cfg.top_k, cfg.route_scale)  # noqa: E731
         else:
             route = lambda lg: R.route_softmax(lg, cfg.top_k)  # noqa: E731
-        fp4 = cfg.expert_fmt == self.C.FMT_MXFP4
+        fn = {self.C.FMT_FP8: R.expert_fp8, self.C.FMT_MXFP4: R.expert_mxfp4, self.C.FMT_W8A8: R.expert_w8a8,
+              self.C.FMT_A16W4: R.expert_fp8, self.C.FMT_A4W4: R.expert_a4w4}[cfg.expert_fmt]
 
         def expert(e, xr):
             w13, w2 = self.expert_weights(e)
-            return R.expert_mxfp4(xr, w13, w2) if fp4 else R.expert_fp8(xr, w13, w2)
+            return fn(xr, w13, w2)
 
         shared = None
         if self.shared is not None:

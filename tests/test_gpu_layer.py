@@ -72,6 +72,22 @@ def test_layer_small_context_32_rows():
     print(stats)
 
 
+@pytest.mark.parametrize("fmt", ["W8A8", "A16W4", "A4W4"])
+def test_layer_expert_modes(fmt):
+    """The persistent layer with each further expert mode in the MoE stages."""
+    from dataclasses import replace
+
+    from sgl_amd_mono.k2 import config as C
+
+    cfg = replace(C.C5_LAYER, mla=replace(C.C5_LAYER.mla, context=8192),
+                  indexer=replace(C.C5_LAYER.indexer, context=8192),
+                  moe=replace(C.C5_LAYER.moe, expert_fmt=getattr(C, "FMT_" + fmt)))
+    L, res, olat = run_layer(cfg, 8, seed=540 + cfg.moe.expert_fmt)
+    stats = check_layer(L, *res, o_latent=olat)
+    assert stats["attn_term_checked"] and stats["moe_term_checked"]
+    print(stats)
+
+
 @pytest.mark.parametrize("rows", [8, 32])
 def test_persistent_layer_repeats_and_matches_staged(rows):
     """Back-to-back persistent launches (counters reset by the launch itself) give the

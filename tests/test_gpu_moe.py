@@ -178,3 +178,42 @@ def test_selftest_mfma_layouts():
     got = run(1, aq, asc, bq, bsc)
     ref = oc.mxfp4_dequant(aq, asc) @ oc.mxfp8_dequant(bq, bsc).T
     assert torch.allclose(got, ref, rtol=1e-4, atol=2e-3), (got - ref).abs().max()
+
+
+@pytest.mark.parametrize("rows", [1, 8])
+def test_moe_w8a8_config1(rows):
+    """E4M3 weights with E4M3 activations, one f32 scale per 128 (the reference's W8A8
+    MoeMode): the C1 shape with its FP8 block-scaled weights."""
+    from dataclasses import replace
+
+    from sgl_amd_mono.k2 import config as C
+
+    cfg = replace(C.C1_MOE, expert_fmt=C.FMT_W8A8)
+    w, out, logits, ids, wts = _run(cfg, rows, seed=300 + rows)
+    _check(cfg, w, out, logits, ids, wts)
+
+
+@pytest.mark.parametrize("fmt", ["A16W4", "A4W4"])
+@pytest.mark.parametrize("rows", [1, 8, 32])
+def test_moe_fp4_weight_modes_config2(fmt, rows):
+    """E2M1 weights against bf16 activations (A16W4) and MXFP4 activations (A4W4), on
+    the C2 shape."""
+    from dataclasses import replace
+
+    from sgl_amd_mono.k2 import config as C
+
+    cfg = replace(C.C2_MOE, expert_fmt=getattr(C, "FMT_" + fmt))
+    w, out, logits, ids, wts = _run(cfg, rows, seed=400 + rows + 7 * cfg.expert_fmt)
+    _check(cfg, w, out, logits, ids, wts)
+
+
+@pytest.mark.parametrize("fmt", ["W8A8", "A16W4", "A4W4"])
+def test_moe_modes_norm_residual(fmt):
+    from dataclasses import replace
+
+    from sgl_amd_mono.k2 import config as C
+
+    base = C.C1_MOE if fmt == "W8A8" else C.C2_MOE
+    cfg = replace(base, expert_fmt=getattr(C, "FMT_" + fmt))
+    w, out, logits, ids, wts = _run(cfg, 8, seed=11 + cfg.expert_fmt, norm=True, residual=True)
+    _check(cfg, w, out, logits, ids, wts, norm=True, residual=True)

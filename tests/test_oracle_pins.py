@@ -1,5 +1,6 @@
 """Closed-form pins of the oracle functions that the layer's parity rests on:
-expert_mxfp4, expert_fp8, mla_output, o_proj, moe_mix and fp8_row_dequant.
+expert_mxfp4, expert_fp8, expert_a4w4, expert_w8a8, mla_output, o_proj, moe_mix,
+fp8_row_dequant and the MXFP4 / FP8 per-128 activation rules.
 
 Every input is chosen so the exact answer can be written down by hand: weights that
 E2M1 x E8M0 (or E4M3) represent exactly, activations whose MXFP8 blocks have a known
@@ -244,3 +245,116 @@ def test_fp8_row_dequant_all_codes_and_scales():
     sq = rows[:, :5]
     planted = oc.e4m3_decode(sq) * scales[None, :]
     assert not torch.equal(planted.double(), table[None, :5] * scales.double()[:, None])
+
+
+# ------------------------------------------------------ MXFP4 and FP8 per-128 activations
+def test_mxfp4_act_code_closed_form():
+    """ceil-pow2 of amax/6 through the f32 bits: 6 -> 1 (127), 6.1 -> 2 (128), 3 -> 1/2
+    (126), 24 -> 4 (129), 0 -> 0; f32(1/6) rounds up, so 6 * f32(1/6) is exactly 1."""
+    amax = torch.tensor([6.0, 6.1, 3.0, 24.0, 0.0, 12.0, 12.0001])
+    assert oc.mxfp4_act_code(amax).tolist() == [127, 128, 126, 129, 0, 128, 129]
+
+
+def test_mxfp4_act_quant_ties_to_even():
+    """A block of amax 24 (scale 4): x/4 = 6, 2.5 (tie of 2 and 3 -> 2), 3.5 (tie of 3
+    and 4 -> 4), 0.25 (tie of 0 and 0.5 -> 0), 0.75 (tie of 0.5 and 1 -> 1), 1.25 (tie of
+    1 and 1.5 -> 1), 1.75 (tie of 1.5 and 2 -> 2), -5 (tie of -4 and -6 -> -4)."""
+    x = torch.zeros(32)
+    x[:8] = torch.tensor([24.0, 10.0, 14.0, 1.0, 3.0, 5.0, 7.0, -20.0])
+    b, s = oc.mxfp4_act_quant(x)
+    assert s.tolist() == [129]
+    want = torch.zeros(32)
+    want[:8] = torch.tensor([24.0, 8.0, 16.0, 0.0, 4.0, 4.0, 8.0, -16.0])
+    assert _exact(oc.mxfp4_dequant(b, s), want)
+    # planted: ties rounded away from zero
+    q = x / 4.0
+    planted = torch.sign(q) * torch.tensor([oc.E2M1_VALUES[min(range(8), key=lambda c: (abs(abs(v) - oc.E2M1_VALUES[c]), -c))]
+                                            for v in q.tolist()]) * 4.0
+    assert not _exact(planted, want)
+
+
+def test_fp8_block_act_quant_closed_form():
+    """Block 0: amax 448 -> scale 1 (448 * f32(1/448) rounds to 1), q = x: 1.0625 -> 1
+    (tie, even), 1.1875 -> 1.25 (tie, even).  Block 1: amax 7 -> scale 1/64, x * 64:
+    1.0625 -> 1, 1.1875 -> 1.25, 0.0625 exact.  Block 2: all zero -> scale 1, codes 0."""
+    x = torch.zeros(384)
+    x[0], x[1], x[2] = 448.0, 1.0625, 1.1875
+    x[128], x[129], x[130], x[131] = 7.0, 1.0625 / 64, 1.1875 / 64, 0.0625 / 64
+    b, s = oc.fp8_block_act_quant(x)
+    assert s.tolist() == [1.0, 1.0 / 64, 1.0]
+    want = torch.zeros(384)
+    want[0], want[1], want[2] = 448.0, 1.0, 1.25
+    want[128], want[129], want[130], want[131] = 7.0, 1.0 / 64, 1.25 / 64, 0.0625 / 64
+    assert _exact(oc.fp8_block_act_dequant(b, s), want)
+    # planted: one scale for the whole row (amax 448): 2^-10 is half the smallest E4M3
+    # subnormal and rounds to 0 (even)
+    bp = oc.e4m3_encode(x)
+    assert not _exact(oc.e4m3_decode(bp), want)
+
+
+def _a4w4_case():
+    """H = 64, inter = 32.  x block A (amax 24, scale 4): 24 -> 24, 10 -> 8 (2.5 -> 2),
+    14 -> 16 (3.5 -> 4); block B (amax 3, scale 1/2): 3 -> 3, 0.625 -> 0.5 (1.25 -> 1),
+    0.875 -> 1 (1.75 -> 2).  g = 24 for every row (silu(24) = 24 in f32):
+    i=0: 1.0 * x0, up 1.0 * x32 = 3 -> mid 72;  i=1: 3.0 * x1, up 1.0 * x33 = 0.5 -> 12;
+    i=2: 1.5 * x2, up 1.0 * x34 = 1 -> 24;  i=3: 1.0 * x0, up -1.5 * x33 = -0.75 -> -18.
+    mid block: amax 72 -> 72/6 = 12 -> scale 16: 4.5 -> 4 (nearest) -> 64, 0.75 -> 1 (tie,
+    even) -> 16, 1.5 -> 24, -1.125 -> -1 -> -16.  down: w2[h, h] = 1, w2[32 + i, i] = 0.5."""
+    x = torch.zeros(1, 64)
+    x[0, 0], x[0, 1], x[0, 2] = 24.0, 10.0, 14.0
+    x[0, 32], x[0, 33], x[0, 34] = 3.0, 0.625, 0.875
+    w13 = torch.zeros(64, 64)
+    for i, (gc, gw, uc, uw) in enumerate([(0, 1.0, 32, 1.0), (1, 3.0, 33, 1.0), (2, 1.5, 34, 1.0), (0, 1.0, 33, -1.5)]):
+        w13[i, gc] = gw
+        w13[32 + i, uc] = uw
+    w2 = torch.zeros(64, 32)
+    for i in range(32):
+        w2[i, i] = 1.0
+        w2[32 + i, i] = 0.5
+    mq = torch.zeros(32)
+    mq[:4] = torch.tensor([64.0, 16.0, 24.0, -16.0])
+    return x, w13, w2, torch.cat([mq, 0.5 * mq])
+
+
+def test_expert_a4w4_closed_form():
+    x, w13, w2, y = _a4w4_case()
+    assert _exact(R.expert_a4w4(x, w13, w2)[0], y)
+    # planted: the mid not quantized (72 instead of 64), then x not quantized
+    gu = oc.mxfp4_dequant(*oc.mxfp4_act_quant(x)) @ w13.T
+    assert not _exact((R.swiglu(gu[:, :32], gu[:, 32:]) @ w2.T)[0], y)
+    gu = x @ w13.T
+    mid = R.swiglu(gu[:, :32], gu[:, 32:])
+    assert not _exact((oc.mxfp4_dequant(*oc.mxfp4_act_quant(mid)) @ w2.T)[0], y)
+
+
+def _w8a8_case():
+    """H = 256, inter = 128.  x block A: amax 448 (scale 1): 448, 1.0625 -> 1, 1.1875 ->
+    1.25; block B: amax 7 (scale 1/64): 7, 1.0625/64 -> 1/64, 1.1875/64 -> 1.25/64.
+    i=0: g = 0.25 * 448 = 112, u = 256 / 64 = 4 -> mid 448;  i=1: g = 32 * 1, u = 64 / 64
+    = 1 -> 32;  i=2: g = 16 * 1.25 = 20, u = 64 * 1.25/64 -> 25.  mid block: amax 448 ->
+    scale 1, q = mid: 448, 32, 25 -> 24 (tie of 24 and 26, even).  down: w2[h, h] = 1,
+    w2[128 + i, i] = 0.5."""
+    x = torch.zeros(1, 256)
+    x[0, 0], x[0, 1], x[0, 2] = 448.0, 1.0625, 1.1875
+    x[0, 128], x[0, 129], x[0, 130] = 7.0, 1.0625 / 64, 1.1875 / 64
+    w13 = torch.zeros(256, 256)
+    for i, (gc, gw, uc, uw) in enumerate([(0, 0.25, 129, 256.0), (1, 32.0, 129, 64.0), (2, 16.0, 130, 64.0)]):
+        w13[i, gc] = gw
+        w13[128 + i, uc] = uw
+    w2 = torch.zeros(256, 128)
+    for i in range(128):
+        w2[i, i] = 1.0
+        w2[128 + i, i] = 0.5
+    mq = torch.zeros(128)
+    mq[:3] = torch.tensor([448.0, 32.0, 24.0])
+    return x, w13, w2, torch.cat([mq, 0.5 * mq])
+
+
+def test_expert_w8a8_closed_form():
+    x, w13, w2, y = _w8a8_case()
+    assert _exact(R.expert_w8a8(x, w13, w2)[0], y)
+    gu = oc.fp8_block_act_dequant(*oc.fp8_block_act_quant(x)) @ w13.T
+    assert not _exact((R.swiglu(gu[:, :128], gu[:, 128:]) @ w2.T)[0], y)  # mid not quantized
+    gu = x @ w13.T
+    mid = R.swiglu(gu[:, :128], gu[:, 128:])
+    assert not _exact((oc.fp8_block_act_dequant(*oc.fp8_block_act_quant(mid)) @ w2.T)[0], y)  # x not quantized

@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define MK2_ABI_VERSION 1
+#define MK2_ABI_VERSION 2
 
 /* return codes */
 #define MK2_OK 0
@@ -116,12 +116,21 @@ int mk2_moe_workspace_bytes(const mk2_moe_shape* shape, size_t* bytes);
 int mk2_moe_launch(const mk2_moe_args* args, mk2_stream_t stream);
 
 /* ------------------------------------------------------------ indexer + top-k
- * Index cache: SGLang's FP4 index plane, read in place (reference:
- * deepseek_v41/gfx950/indexer/score_fp4.py:9-12,45-49).  cache: E2M1 codes
- * [pages][4 chunks of 32 dims][64 tokens][16 B], 4096 B a page; cache_scale:
- * E8M0 [pages][4 chunks][64], token t's scale at (t % 16) * 4 + t / 16.  Page table int32
- * [requests][table_stride], logical page -> physical page.  Row r scores the
- * context positions 0 .. ctx_len[r]-1 of request req_ids[r]. */
+ * Index cache, one of SGLang's two formats, read in place:
+ *  MK2_KEYS_FP4: the FP4 index plane (reference: deepseek_v41/gfx950/indexer/
+ *    score_fp4.py:9-12,45-49).  cache: E2M1 codes [pages][4 chunks of 32 dims][64
+ *    tokens][16 B], 4096 B a page; cache_scale: E8M0 [pages][4 chunks][64], token t's
+ *    scale at (t % 16) * 4 + t / 16.
+ *  MK2_KEYS_FP8: the DSA index cache, uint8 [pages][64][132] (reference:
+ *    glm53/gfx950/runner.py:28-31,412-421).  A page is 64 x 128 E4M3 values in tiles of
+ *    16 tokens x 16 dims -- token t's dim d at byte (t / 16) * 2048 + (d / 16) * 256 +
+ *    (t % 16) * 16 + d % 16 (kernel.py:698-705) -- then 64 f32 scales, token t's at
+ *    byte 8192 + 4 t; a key is its values times its scale.  cache_scale is NULL.
+ * Page table int32 [requests][table_stride], logical page -> physical page.  Row r
+ * scores the context positions 0 .. ctx_len[r]-1 of request req_ids[r]. */
+#define MK2_KEYS_FP4 0
+#define MK2_KEYS_FP8 1
+
 typedef struct mk2_indexer_shape {
   int rows;        /* 1..32 */
   int heads;       /* index heads, multiple of 16, <= 64 */
@@ -129,14 +138,15 @@ typedef struct mk2_indexer_shape {
   int topk;        /* multiple of 64, 64..4096 */
   int max_ctx;     /* upper bound of ctx_len, <= 65536, multiple of 64 */
   int table_stride;/* page table row stride (entries) */
+  int key_fmt;     /* MK2_KEYS_*: the index cache's format */
 } mk2_indexer_shape;
 
 typedef struct mk2_indexer_args {
   mk2_indexer_shape shape;
   const void* q;            /* bf16 [rows][heads][128] */
   const void* w;            /* bf16 [rows][heads] head weights */
-  const uint8_t* cache;     /* E2M1 plane [pages][4][64][16] */
-  const uint8_t* cache_scale;/* E8M0 plane [pages][4][64] */
+  const uint8_t* cache;     /* FP4: E2M1 plane [pages][4][64][16]; FP8: [pages][64][132] */
+  const uint8_t* cache_scale;/* FP4: E8M0 plane [pages][4][64]; FP8: NULL */
   const int32_t* page_table;/* [requests][table_stride] */
   const int32_t* req_ids;   /* [rows] */
   const int32_t* ctx_len;   /* [rows] */

@@ -19,6 +19,11 @@ Formats (all little-endian bytes):
   * FP8 per-128 activations: E4M3 codes with an f32 scale amax * f32(1/448) per 128;
     q = clamp(x * 448/amax, +-448) (kernel.py:1740-1750, whose multiplier is the
     hardware reciprocal: here, as in this build's kernels, the IEEE quotient).
+  * DSA index keys (SGLang's FP8 index cache, uint8 [pages, 64, 132]): per key, E4M3
+    values times one power-of-two f32 scale 2^ceil(log2(max(amax, 1e-4) / 448))
+    (kernel.py:3134-3147); a page holds 64 x 128 values in 16 x 16 tiles -- byte b is
+    token (b // 2048) * 16 + (b % 256) // 16 (glm53/check.py:75-82), dim
+    ((b % 2048) // 256) * 16 + b % 16 -- then the 64 keys' f32 scales.
   * radix key: the order-preserving u32 of f32 score bits (glm53/check.py:111-114).
 
 Every function here is pinned by tests/test_oracle_codecs.py (closed forms, brute
@@ -210,6 +215,44 @@ def fp8_block_dequant(codes: torch.Tensor, scales: torch.Tensor, block: int = 12
 def fp8_row_dequant(codes: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
     """E4M3 rows [..., D] with one f32 scale per row [...] -> f32."""
     return e4m3_decode(codes) * scales.float()[..., None]
+
+
+# ------------------------------------------------------------- DSA FP8 index cache
+INDEX_PAGE = 64
+INDEX_DIM = 128
+INDEX_VALUE_BYTES = INDEX_PAGE * INDEX_DIM  # 8192; the f32 scales follow
+INDEX_PAGE_BYTES = INDEX_PAGE * (INDEX_DIM + 4)  # 8448 (glm53/gfx950/runner.py:28-31)
+
+
+def index_key_scale_code(amax: torch.Tensor) -> torch.Tensor:
+    """The f32 exponent field of an FP8 index key's scale: ceil-pow2 of
+    max(amax, f32(1e-4)) / 448, the IEEE quotient (glm53/gfx950/kernel.py:3134-3144)."""
+    v = torch.maximum(_f32(amax), _f32(1.0e-4)) / _f32(FP8_MAX)
+    return _ceil_pow2_code(v)
+
+
+def index_key_quant(k: torch.Tensor):
+    """Index keys [..., 128] -> (E4M3 uint8 [..., 128], f32 scales [...]): the values
+    times 2^(127 - field), exactly the inverse power of two (kernel.py:3145-3147)."""
+    field = index_key_scale_code(_f32(k).abs().amax(-1))
+    scale = torch.exp2((field - 127).to(torch.float32))
+    inv = torch.exp2((127 - field).to(torch.float32))
+    return e4m3_encode(_f32(k) * inv[..., None]), scale
+
+
+def index_page_decode(pages: torch.Tensor) -> torch.Tensor:
+    """uint8 index pages [P, 64, 132] (or [P, 8448]) -> f32 keys [P, 64, 128], each
+    value times its key's scale, by the byte -> (token, dim) map of the 16 x 16 tiles
+    (glm53/check.py:75-82)."""
+    pg = pages.reshape(-1, INDEX_PAGE_BYTES)
+    b = torch.arange(INDEX_VALUE_BYTES)
+    token = (b // 2048) * 16 + (b % 256) // 16
+    dim = ((b % 2048) // 256) * 16 + b % 16
+    vals = e4m3_decode(pg[:, :INDEX_VALUE_BYTES].contiguous())
+    scales = pg[:, INDEX_VALUE_BYTES:].contiguous().view(torch.float32)  # [P, 64]
+    keys = torch.empty(pg.shape[0], INDEX_PAGE, INDEX_DIM, dtype=torch.float32)
+    keys[:, token, dim] = vals * scales[:, token]
+    return keys
 
 
 # ----------------------------------------------------------------------------- bf16

@@ -1,4 +1,4 @@
-// Standalone indexer launch (FP4 index keys, 64 heads x 128): key scores with the
+// Standalone indexer launch (FP4 or FP8 index keys, up to 64 heads x 128): key scores with the
 // row histograms, the candidate slices, then the exact top-k of every row.
 #include "indexer_stages.h"
 #include "mk2_host.h"
@@ -6,6 +6,7 @@
 namespace mk2 {
 
 constexpr int IDX_NT = 512;
+static_assert(IDX_KEYS_FP4 == MK2_KEYS_FP4 && IDX_KEYS_FP8 == MK2_KEYS_FP8, "key formats");
 
 __global__ __launch_bounds__(256) void k_idx_clear(IdxDev p) {
   for (int i = blockIdx.x * 256 + threadIdx.x; i < p.rows * IDX_BINS; i += gridDim.x * 256) p.hist[i] = 0;
@@ -50,6 +51,8 @@ int idx_check_shape(const mk2_indexer_shape* s) {
   MK2_REQUIRE(s->max_ctx >= 64 && s->max_ctx <= TOPK_MAXN && s->max_ctx % 64 == 0,
               "indexer: max_ctx must be a multiple of 64 in [64, %d], got %d", TOPK_MAXN, s->max_ctx);
   MK2_REQUIRE(s->table_stride >= s->max_ctx / 64, "indexer: table_stride %d < max_ctx / 64", s->table_stride);
+  MK2_REQUIRE(s->key_fmt == MK2_KEYS_FP4 || s->key_fmt == MK2_KEYS_FP8,
+              "indexer: key_fmt must be MK2_KEYS_FP4 or MK2_KEYS_FP8, got %d", s->key_fmt);
   return MK2_OK;
 }
 
@@ -80,13 +83,17 @@ size_t idx_carve(const mk2_indexer_shape* s, void* base, IdxDev* d) {
 int idx_fill(const mk2_indexer_args* a, IdxDev* d) {
   int rc = idx_check_shape(&a->shape);
   if (rc) return rc;
-  MK2_REQUIRE(a->q && a->w && a->cache && a->cache_scale && a->page_table && a->req_ids && a->ctx_len,
-              "indexer: q, w, cache, cache_scale, page_table, req_ids and ctx_len must be set");
+  MK2_REQUIRE(a->q && a->w && a->cache && a->page_table && a->req_ids && a->ctx_len,
+              "indexer: q, w, cache, page_table, req_ids and ctx_len must be set");
+  if (a->shape.key_fmt == MK2_KEYS_FP4)
+    MK2_REQUIRE(a->cache_scale != nullptr, "indexer: the FP4 index plane needs cache_scale");
+  else
+    MK2_REQUIRE(a->cache_scale == nullptr, "indexer: the FP8 index cache holds its scales; cache_scale must be NULL");
   *d = IdxDev{};
   d->rows = a->shape.rows; d->heads = a->shape.heads; d->topk = a->shape.topk;
   d->max_ctx = a->shape.max_ctx; d->stride = a->shape.table_stride;
   d->q = (const bf16_t*)a->q; d->w = (const bf16_t*)a->w; d->cache = a->cache;
-  d->cscale = a->cache_scale;
+  d->cscale = a->cache_scale; d->kfmt = a->shape.key_fmt;
   d->pt = a->page_table; d->req = a->req_ids; d->ctx = a->ctx_len;
   d->scores = a->scores; d->out = a->topk;
   d->nchk = (d->max_ctx + IDX_CHUNK - 1) / IDX_CHUNK;

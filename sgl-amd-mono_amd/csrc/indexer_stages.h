@@ -1,13 +1,15 @@
-// Indexer stages of the K2 layer: FP4 index-key scores on the matrix cores and the
+// Indexer stages of the K2 layer: index-key scores on the matrix cores and the
 // exact radix top-k with a lowest-position tie-break.
 //
-// score[r][c] = sum_h relu(q[r][h] . k[c]) * w[r][h] over the FP4 keys (E2M1 codes,
-// E8M0 per 32 dims) of request req[r], positions c < ctx[r].  One task scores a
-// chunk of positions; a wave takes 16 keys at a time as the MFMA B operand (16
-// columns) against all heads as A (16 heads a tile), widening E2M1 x 2^e exactly to
-// bf16.  The head sum runs in the lanes: a lane holds 4 heads of each head group
-// for one key; every four groups, three row-swapping permutes combine the four lane
-// groups' sums of all four at once.
+// score[r][c] = sum_h relu(q[r][h] . k[c]) * w[r][h] over the keys of request req[r],
+// positions c < ctx[r], from either of SGLang's index caches: the FP4 plane (E2M1
+// codes, E8M0 per 32 dims, widened exactly to bf16 with their scale) or the FP8 pages
+// (E4M3 values widened exactly to bf16; the key's f32 scale multiplies its lane's head
+// sum, as the reference scores them, glm53/gfx950/kernel.py:3830-3845).  One task
+// scores a chunk of positions; a wave takes 16 keys at a time as the MFMA B operand
+// (16 columns) against all heads as A (16 heads a tile).  The head sum runs in the
+// lanes: a lane holds 4 heads of each head group for one key; every four groups,
+// three row-swapping permutes combine the four lane groups' sums of all four at once.
 //
 // top-k, three stages over the order-preserving u32 keys of the scores:
 //   score (row, chunk)  also counts its keys into the row's two-level histogram: 4096
@@ -37,6 +39,11 @@ constexpr int IDX_PAGE = 64;
 // E2M1 codes, and apart from it [4 chunks][64] E8M0 scales, key k's at (k % 16) * 4 + k / 16
 constexpr int IDX_PAGE_CODES = 64 * 64;
 constexpr int IDX_PAGE_SCALES = 64 * 4;
+// index cache formats (MK2_KEYS_*); an FP8 page: 64 x 128 E4M3 values in 16 x 16
+// tiles, then the 64 tokens' f32 scales
+constexpr int IDX_KEYS_FP4 = 0, IDX_KEYS_FP8 = 1;
+constexpr int IDX_FP8_PAGE = 64 * 132;
+constexpr int IDX_FP8_VALUES = 64 * 128;
 constexpr int IDX_CHUNK = 2048;                    // positions a score task
 constexpr int TOPK_NT = 1024;                      // top-k workgroup of the standalone launch
 
@@ -47,8 +54,9 @@ struct IdxDev {
   int rows, heads, topk, max_ctx, stride, nchk;
   const bf16_t* q;      // [rows][heads][128]
   const bf16_t* w;      // [rows][heads]
-  const uint8_t* cache; // E2M1 plane [pages][4][64][16 B]
-  const uint8_t* cscale;// E8M0 plane [pages][4][64]
+  int kfmt;             // IDX_KEYS_*
+  const uint8_t* cache; // FP4: E2M1 plane [pages][4][64][16 B]; FP8: pages [64][132]
+  const uint8_t* cscale;// FP4: E8M0 plane [pages][4][64]; FP8: unused
   const int* pt;        // [requests][stride]
   const int* req;       // [rows]
   const int* ctx;       // [rows]
@@ -97,8 +105,9 @@ struct IdxScoreLds {
 // (groups past the row's end read page id 0, and their results are dropped) and the
 // scores wait in LDS until the loop is done: a store or a branch between the loads
 // would make every group wait for all memory traffic.
-template <int NT>
-MK2_DEV void idx_score(const IdxDev& p, int r, int chunk, IdxScoreLds& L) {
+template <int NT, int KF>
+MK2_DEV void idx_score_keys(const IdxDev& p, int r, int chunk, IdxScoreLds& L) {
+  constexpr bool F8 = KF == IDX_KEYS_FP8;
   constexpr int NW = NT / 64;
   constexpr int GPW = IDX_CHUNK / 16 / NW;  // 16-key groups a wave
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, c16 = lane & 15;
@@ -142,21 +151,38 @@ MK2_DEV void idx_score(const IdxDev& p, int r, int chunk, IdxScoreLds& L) {
 #pragma unroll
   for (int q = 0; q < PPW; ++q) {
     const size_t pg = __builtin_amdgcn_readfirstlane(lds_pages[gw0 / 4 + q]);
-    pbase[q] = p.cache + pg * IDX_PAGE_CODES;
-    sbase[q] = p.cscale + pg * IDX_PAGE_SCALES;
+    if constexpr (F8) {
+      pbase[q] = p.cache + pg * IDX_FP8_PAGE;
+      sbase[q] = pbase[q] + IDX_FP8_VALUES;
+    } else {
+      pbase[q] = p.cache + pg * IDX_PAGE_CODES;
+      sbase[q] = p.cscale + pg * IDX_PAGE_SCALES;
+    }
   }
-  // lane (c16, g) of group j holds chunk g of key 16 (j & 3) + c16; one scale dword a
-  // page holds the lane's four keys' E8M0 bytes (j & 3 = 0..3)
-  const uint32_t off_code = g * 1024 + c16 * 16, off_scale = g * 64 + c16 * 4;
+  // lane (c16, g) of group j holds dims 32g .. 32g + 31 of key 16 (j & 3) + c16.  FP4:
+  // chunk g's 16 code bytes, and one scale dword a page holds the lane's four keys'
+  // E8M0 bytes (j & 3 = 0..3).  FP8: tiles 2g and 2g + 1 of the key's 16-token block,
+  // 16 bytes each, 256 B apart, and the key's f32 scale.
+  const uint32_t off_code = F8 ? g * 512 + c16 * 16 : g * 1024 + c16 * 16;
+  const uint32_t off_scale = F8 ? c16 * 4 : g * 64 + c16 * 4;
   uint4 code[GPW];
+  uint4 code_hi[F8 ? GPW : 1];
+  float ksc[F8 ? GPW : 1];
   uint32_t sw[PPW];
   // a rolling window of KWIN key groups in flight: group j + KWIN - 1 is issued as
   // group j is widened (a full window of 16 a wave, 160 KiB a CU at once, delays every
   // CU's first groups behind the whole chip's requests)
   constexpr int KWIN = 4;
   auto issue = [&](int j) {
-    code[j] = ld_stream16(pbase[j >> 2] + off_code + (j & 3) * 256);
-    if ((j & 3) == 0) sw[j >> 2] = *(const uint32_t*)(sbase[j >> 2] + off_scale);
+    if constexpr (F8) {
+      const uint8_t* b = pbase[j >> 2] + off_code + (j & 3) * 2048;
+      code[j] = ld_stream16(b);
+      code_hi[j] = ld_stream16(b + 256);
+      ksc[j] = *(const float*)(sbase[j >> 2] + off_scale + (j & 3) * 64);
+    } else {
+      code[j] = ld_stream16(pbase[j >> 2] + off_code + (j & 3) * 256);
+      if ((j & 3) == 0) sw[j >> 2] = *(const uint32_t*)(sbase[j >> 2] + off_scale);
+    }
   };
 #pragma unroll
   for (int j = 0; j < KWIN; ++j) issue(j);
@@ -187,11 +213,18 @@ MK2_DEV void idx_score(const IdxDev& p, int r, int chunk, IdxScoreLds& L) {
   // j's head sums, so that the matrix cores and the vector ALUs overlap
   auto keys = [&](int j, bf16x8* kb) {
     if (j >= 1 && j + KWIN - 1 < GPW) issue(j + KWIN - 1);
-    const float sc = e8m0_to_f32(sw[j >> 2] >> (8 * (j & 3)));
-    kb[0] = e2m1x8_to_bf16(code[j].x, sc);
-    kb[1] = e2m1x8_to_bf16(code[j].y, sc);
-    kb[2] = e2m1x8_to_bf16(code[j].z, sc);
-    kb[3] = e2m1x8_to_bf16(code[j].w, sc);
+    if constexpr (F8) {
+      kb[0] = e4m3x8_to_bf16(code[j].x, code[j].y);
+      kb[1] = e4m3x8_to_bf16(code[j].z, code[j].w);
+      kb[2] = e4m3x8_to_bf16(code_hi[j].x, code_hi[j].y);
+      kb[3] = e4m3x8_to_bf16(code_hi[j].z, code_hi[j].w);
+    } else {
+      const float sc = e8m0_to_f32(sw[j >> 2] >> (8 * (j & 3)));
+      kb[0] = e2m1x8_to_bf16(code[j].x, sc);
+      kb[1] = e2m1x8_to_bf16(code[j].y, sc);
+      kb[2] = e2m1x8_to_bf16(code[j].z, sc);
+      kb[3] = e2m1x8_to_bf16(code[j].w, sc);
+    }
   };
   // all four head groups, absent ones with zero queries and weights: four
   // independent MFMA chains
@@ -213,6 +246,7 @@ MK2_DEV void idx_score(const IdxDev& p, int r, int chunk, IdxScoreLds& L) {
     for (int hg = 0; hg < 4; ++hg)
 #pragma unroll
       for (int i = 0; i < 4; ++i) s += relu_bits(acc[hg][i]) * wt[hg][i];
+    if constexpr (F8) s *= ksc[j];  // the lane's key's scale (column c16 of group j)
     part[j & 3] = s;
     if ((j & 3) == 3) {
       // rows 0, 2 of the first swap hold groups 0 / 2 (row pairs 01, 23), rows 1, 3
@@ -279,6 +313,15 @@ MK2_DEV void idx_score(const IdxDev& p, int r, int chunk, IdxScoreLds& L) {
     if (v) atomicAdd(ch + c, v);
   }
   __syncthreads();
+}
+
+// the scores of either index cache format (a uniform branch, once a task)
+template <int NT>
+MK2_DEV void idx_score(const IdxDev& p, int r, int chunk, IdxScoreLds& L) {
+  if (p.kfmt == IDX_KEYS_FP8)
+    idx_score_keys<NT, IDX_KEYS_FP8>(p, r, chunk, L);
+  else
+    idx_score_keys<NT, IDX_KEYS_FP4>(p, r, chunk, L);
 }
 
 // ------------------------------------------------------------- stage: top-k

@@ -19,6 +19,8 @@ import torch  # noqa: F401  (must precede the CDLL load, see the module docstrin
 LIB_PATH = Path(__file__).resolve().parent / "libmk2.so"
 
 MK2_OK, MK2_EINVAL, MK2_ELAUNCH, MK2_ENOSPACE = 0, 1, 2, 3
+ABI_VERSION = 2  # MK2_ABI_VERSION of the header these structures mirror
+MK2_KEYS_FP4, MK2_KEYS_FP8 = 0, 1
 
 
 class Mk2Error(RuntimeError):
@@ -55,7 +57,7 @@ class MoeArgs(ctypes.Structure):
 class IndexerShape(ctypes.Structure):
     _fields_ = [
         ("rows", c_int), ("heads", c_int), ("dim", c_int), ("topk", c_int),
-        ("max_ctx", c_int), ("table_stride", c_int),
+        ("max_ctx", c_int), ("table_stride", c_int), ("key_fmt", c_int),
     ]
 
 
@@ -142,6 +144,8 @@ def lib(required_symbols=None):
         fn.restype = c_int
     handle.mk2_last_error.argtypes = []
     handle.mk2_last_error.restype = c_char_p
+    if handle.mk2_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"{LIB_PATH} has ABI {handle.mk2_abi_version()}, these bindings mirror {ABI_VERSION}: rebuild it")
     runtimes = _hip_runtimes_mapped()
     if len(runtimes) > 1:
         raise RuntimeError(f"two HIP runtimes are mapped ({sorted(runtimes)}); import torch first")

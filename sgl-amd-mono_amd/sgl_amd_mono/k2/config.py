@@ -24,6 +24,9 @@ FMT_W8A8 = 2  # E4M3 weights, E4M3 activations with an f32 scale per 128
 FMT_A16W4 = 3  # E2M1 weights, bf16 activations
 FMT_A4W4 = 4  # E2M1 weights, MXFP4 activations
 FP4_WEIGHT_FMTS = (FMT_MXFP4, FMT_A16W4, FMT_A4W4)
+# index cache formats (MK2_KEYS_*)
+KEYS_FP4 = 0  # SGLang's FP4 index plane: E2M1 codes + E8M0 per 32 dims, two tensors
+KEYS_FP8 = 1  # SGLang's DSA index cache: uint8 [pages, 64, 132], E4M3 + f32 scale a key
 
 MAX_ROWS = 32  # decode rows a launch serves (verify: 8 requests x 4 draft tokens)
 
@@ -103,10 +106,13 @@ class IndexerConfig:
     dim: int = 128
     topk: int = 2048
     context: int = 65536
+    keys: int = KEYS_FP4
 
     def validate(self, rows: int) -> None:
         if self.dim != 128:
             raise ValueError("index keys are 128 dims")
+        if self.keys not in (KEYS_FP4, KEYS_FP8):
+            raise ValueError(f"unknown index cache format {self.keys}")
         if self.heads % 16 or not 16 <= self.heads <= 64:
             raise ValueError("index heads must be a multiple of 16 in [16, 64]")
         if not 64 <= self.context <= 65536 or self.context % PAGE:

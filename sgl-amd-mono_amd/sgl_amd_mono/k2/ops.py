@@ -70,13 +70,13 @@ class MoEOp:
 
 
 class IndexerOp:
-    """FP4 index-key scores and the exact top-k of every row."""
+    """Index-key scores (FP4 plane or FP8 DSA pages) and the exact top-k of every row."""
 
     def __init__(self, cfg: C.IndexerConfig, rows: int, table_stride: int, device=None):
         cfg.validate(rows)
         self.cfg, self.rows = cfg, rows
         self.device = torch.device(device or "cuda")
-        self.shape = _lib.IndexerShape(rows, cfg.heads, cfg.dim, cfg.topk, cfg.context, table_stride)
+        self.shape = _lib.IndexerShape(rows, cfg.heads, cfg.dim, cfg.topk, cfg.context, table_stride, cfg.keys)
         nbytes = ctypes.c_size_t()
         _lib.check(_lib.lib().mk2_indexer_workspace_bytes(ctypes.byref(self.shape), ctypes.byref(nbytes)))
         self.workspace = torch.empty(nbytes.value, dtype=torch.uint8, device=self.device)
@@ -86,7 +86,13 @@ class IndexerOp:
         _need(q, "q", torch.bfloat16, (rows, cfg.heads, cfg.dim))
         _need(w, "w", torch.bfloat16, (rows, cfg.heads))
         _need(cache, "cache", torch.uint8)
-        _need(cache_scale, "cache_scale", torch.uint8)
+        if cfg.keys == C.KEYS_FP8:
+            if cache_scale is not None:
+                raise ValueError("the FP8 index cache holds its scales: cache_scale must be None")
+            if cache.dim() != 3 or tuple(cache.shape[1:]) != (64, 132):
+                raise ValueError(f"the FP8 index cache must be uint8 [pages, 64, 132], got {tuple(cache.shape)}")
+        else:
+            _need(cache_scale, "cache_scale", torch.uint8)
         _need(page_table, "page_table", torch.int32)
         if page_table.shape[1] != self.shape.table_stride:
             raise ValueError("page_table row stride differs from the op's table_stride")

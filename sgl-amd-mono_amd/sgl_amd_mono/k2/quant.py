@@ -7,6 +7,8 @@ These write the byte formats the kernels read:
   * FP8 weights: E4M3 codes with one f32 scale per 128 x 128 block, scale = amax / 448
     (the layout glm53/check.py:427-432 reads).
   * FP8 latent-KV rows: E4M3 codes with one f32 scale per token, scale = amax / 448.
+  * FP8 index keys (SGLang's DSA index cache): E4M3 codes with one power-of-two f32
+    scale per key, 2^ceil(log2(max(amax, 1e-4) / 448)) (glm53/gfx950/kernel.py:3134-3147).
 Activations are quantized on the GPU by the kernels themselves.
 """
 
@@ -74,3 +76,10 @@ def quant_fp8_rows(v: torch.Tensor):
     amax = v.abs().amax(-1)
     scale = torch.where(amax > 0, amax / FP8_MAX, torch.ones_like(amax))
     return _e4m3(v / scale[..., None]).contiguous(), scale.contiguous()
+
+
+def quant_index_fp8(k: torch.Tensor):
+    """Index keys [..., 128] -> (E4M3 uint8 [..., 128], f32 power-of-two scales [...])."""
+    k = k.float()
+    e = _pow2_ceil_exponent(k.abs().amax(-1).clamp_min(1e-4) / FP8_MAX)
+    return _e4m3(k * torch.exp2(-e.float())[..., None]).contiguous(), torch.exp2(e.float()).contiguous()

@@ -19,7 +19,7 @@ import torch
 
 from . import config as C
 from .packing import pack_e8m0, pack_tiles
-from .quant import quant_fp8_block, quant_fp8_rows, quant_mxfp4
+from .quant import quant_fp8_block, quant_fp8_rows, quant_index_fp8, quant_mxfp4
 
 WEIGHT_STD = 0.02
 
@@ -99,9 +99,20 @@ def index_plane(codes: torch.Tensor, scales: torch.Tensor):
     return plane, sc
 
 
+def index_pages_fp8(codes: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+    """Token-major FP8 keys (E4M3 codes [P, 64, 128], f32 scales [P, 64]) -> SGLang's DSA
+    index pages, uint8 [P, 64, 132]: token t's dim d at byte (t // 16) * 2048 + (d // 16)
+    * 256 + (t % 16) * 16 + d % 16 (glm53/gfx950/kernel.py:698-705), then the 64 scales."""
+    P = codes.shape[0]
+    tiles = codes.view(P, 4, 16, 8, 16).permute(0, 1, 3, 2, 4).reshape(P, 64 * 128)
+    sc = scales.float().contiguous().view(torch.uint8).view(P, 256)
+    return torch.cat([tiles, sc], dim=1).view(P, 64, 132).contiguous()
+
+
 def make_indexer(cfg: C.IndexerConfig, rows: int, seed: int, device, ctx_len=None):
-    """FP4 index-key pages (E2M1 codes + E8M0 per 32 dims), bf16 queries and head
-    weights ~ N(0, 1), one request a row."""
+    """Index-key pages in the config's format (FP4: E2M1 codes + E8M0 per 32 dims in the
+    FP4 plane; FP8: the DSA pages, cache_scale None), bf16 queries and head weights ~
+    N(0, 1), one request a row."""
     g = _gen(seed, device)
     ctx = cfg.context
     ppr = ctx // C.PAGE
@@ -111,8 +122,11 @@ def make_indexer(cfg: C.IndexerConfig, rows: int, seed: int, device, ctx_len=Non
     ns.page_table = _page_table(g, rows, ppr, device)
     n_pages = rows * ppr + 1
     keys = _randn(g, n_pages, C.PAGE, cfg.dim, device=device)
-    codes, scales = quant_mxfp4(keys)  # [P, 64, 64], [P, 64, 4]
-    ns.cache, ns.cache_scale = index_plane(codes, scales)
+    if cfg.keys == C.KEYS_FP8:
+        ns.cache, ns.cache_scale = index_pages_fp8(*quant_index_fp8(keys)), None
+    else:
+        codes, scales = quant_mxfp4(keys)  # [P, 64, 64], [P, 64, 4]
+        ns.cache, ns.cache_scale = index_plane(codes, scales)
     ns.req_ids = torch.arange(rows, dtype=torch.int32, device=device)
     if ctx_len is None:
         ctx_len = [ctx] * rows

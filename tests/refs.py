@@ -105,12 +105,16 @@ class MoEOracle:
 
 
 def index_keys_f32(cache, cache_scale, page_table, req, n, dim=128):
-    """Dequantized FP4 keys of positions 0..n-1 of request `req` (oracle decoders), read
-    from SGLang's FP4 index plane (score_fp4.py:9-12): token t of a page has its 16 code
-    bytes of chunk c at c * 1024 + t * 16 and that chunk's E8M0 at c * 64 + (t % 16) * 4
-    + t // 16 of the page's scale row."""
-    cache, cache_scale, page_table = cpu(cache), cpu(cache_scale), cpu(page_table)
+    """Dequantized keys of positions 0..n-1 of request `req` (oracle decoders).  With a
+    cache_scale, from SGLang's FP4 index plane (score_fp4.py:9-12): token t of a page has
+    its 16 code bytes of chunk c at c * 1024 + t * 16 and that chunk's E8M0 at c * 64 +
+    (t % 16) * 4 + t // 16 of the page's scale row.  Without, from the FP8 DSA index
+    pages [P, 64, 132] (oc.index_page_decode)."""
+    cache, page_table = cpu(cache), cpu(page_table)
     pages = page_table[req, : (n + 63) // 64].long()
+    if cache_scale is None:
+        return oc.index_page_decode(cache[pages]).reshape(-1, dim)[:n]
+    cache_scale = cpu(cache_scale)
     t = torch.arange(64)
     codes = torch.empty(len(pages), 64, 64, dtype=torch.uint8)
     scales = torch.empty(len(pages), 64, 4, dtype=torch.uint8)

@@ -33,7 +33,7 @@ def test_every_declared_symbol_is_exported():
     assert len(names) >= 10
     for n in names:
         assert hasattr(L, n), n
-    assert L.mk2_abi_version() == 1
+    assert L.mk2_abi_version() == _l.ABI_VERSION == 2
 
 
 def test_ctypes_layouts_match_the_header():
@@ -107,5 +107,13 @@ def test_launch_argument_errors_never_reach_the_device():
                         fake, None, None, fake, 1 << 30)
     assert L.mk2_indexer_topk_launch(ctypes.byref(ia), None) == _l.MK2_EINVAL
     assert "cache_scale" in L.mk2_last_error().decode()
+    # the FP8 index cache carries its scales: a separate scale plane is refused, and an
+    # unknown key format is refused by the shape check
+    ia.shape.key_fmt, ia.cache_scale = _l.MK2_KEYS_FP8, fake
+    assert L.mk2_indexer_topk_launch(ctypes.byref(ia), None) == _l.MK2_EINVAL
+    assert "cache_scale must be NULL" in L.mk2_last_error().decode()
+    ia.shape.key_fmt = 2
+    assert L.mk2_indexer_topk_launch(ctypes.byref(ia), None) == _l.MK2_EINVAL
+    assert "key_fmt" in L.mk2_last_error().decode()
     assert L.mk2_layer_launch(None, None) == _l.MK2_EINVAL
     assert L.mk2_selftest_mfma(9, None, None, None, None, None, None) == _l.MK2_EINVAL

@@ -71,11 +71,12 @@ def test_mla_validate_matches_c():
 def test_indexer_validate_matches_c():
     _l, L = _lib()
     seen = {True: 0, False: 0}
-    for heads, topk, ctx, rows in itertools.product(
+    for heads, topk, ctx, rows, keys in itertools.product(
         (8, 16, 48, 64, 80), (32, 64, 2048, 4096, 4160), (32, 64, 8192, 65536, 65600, 131072), (1, 32, 33),
+        (C.KEYS_FP4, C.KEYS_FP8, 2),
     ):
-        cfg = replace(C.C4_INDEXER, heads=heads, topk=topk, context=ctx)
-        s = _l.IndexerShape(rows, cfg.heads, cfg.dim, cfg.topk, cfg.context, max(1, cfg.context // C.PAGE))
+        cfg = replace(C.C4_INDEXER, heads=heads, topk=topk, context=ctx, keys=keys)
+        s = _l.IndexerShape(rows, cfg.heads, cfg.dim, cfg.topk, cfg.context, max(1, cfg.context // C.PAGE), cfg.keys)
         n = ctypes.c_size_t()
         c = L.mk2_indexer_workspace_bytes(ctypes.byref(s), ctypes.byref(n)) == 0
         py = _py_ok(cfg, rows)

@@ -33,7 +33,10 @@ def _run(cfg, rows, seed, ctx_len=None, mode="random"):
 
     dev = _dev()
     ns = synth.make_indexer(cfg, rows, seed, dev, ctx_len=ctx_len)
-    if mode == "ties":
+    fp8 = ns.cache_scale is None
+    if fp8 and mode in ("ties", "recent"):
+        _fp8_mode(ns, mode, seed)
+    elif mode == "ties":
         # every key = token 0 of page 1 (its chunk-c codes at c * 1024, scale at c * 64)
         v, s = ns.cache.view(-1, 4, 64, 16), ns.cache_scale.view(-1, 4, 64)
         v[:] = v[1, :, :1].clone()
@@ -52,6 +55,28 @@ def _run(cfg, rows, seed, ctx_len=None, mode="random"):
     return ns, cpu(scores), cpu(topk).long()
 
 
+def _fp8_mode(ns, mode, seed):
+    """The FP8 pages' versions of the cases: every key identical ("ties"), or the last
+    4096 positions' scales 16x ("recent")."""
+    from sgl_amd_mono.k2 import quant, synth
+
+    P = ns.cache.shape[0]
+    if mode == "ties":
+        key = torch.randn(128, generator=torch.Generator().manual_seed(seed))
+        codes, sc = quant.quant_index_fp8(key.expand(P, 64, 128))
+        ns.cache.copy_(synth.index_pages_fp8(codes, sc))
+        return
+    # positive head weights, so that a larger key gives a larger score (with weights of
+    # mixed sign most of a row's scores can be negative, and 16x pushes those down)
+    ns.w.abs_()
+    flat = ns.cache.view(P, 64 * 132)
+    for r in range(ns.rows):
+        n = int(ns.ctx_len[r])
+        for pg in ns.page_table[r, (n - 4096) // 64 : n // 64].long().tolist():
+            s = flat[pg, 8192:].view(torch.float32) * 16
+            flat[pg, 8192:] = s.view(torch.uint8)
+
+
 def _check_rows(cfg, ns, scores, topk, expect_clear=True):
     k = cfg.topk
     n_clear = 0
@@ -67,9 +92,15 @@ def _check_rows(cfg, ns, scores, topk, expect_clear=True):
         m = min(n, k)
         assert torch.equal(sel[:m], want), (r, sel[:8], want[:8])
         assert bool((sel[m:] == -1).all())
-        # the set against the oracle's own scores when the boundary is clear
+        # the set against the oracle's own scores: on every row, within the score
+        # tolerance of the oracle's k-th score; exactly where the boundary is clear
         if n > k:
             keys = torch.sort(ref, descending=True).values
+            tol = 2 * SCORE_BOUND * ref.abs().max().item()
+            picked = torch.zeros(n, dtype=torch.bool)
+            picked[sel[:m]] = True
+            assert bool((ref[picked] >= keys[k - 1] - tol).all()), r
+            assert bool((ref[~picked] <= keys[k - 1] + tol).all()), r
             gap = (keys[k - 1] - keys[k]).item()
             if gap > 2 * SCORE_BOUND * ref.abs().max().item():
                 n_clear += 1
@@ -132,6 +163,56 @@ def test_indexer_recent_cluster():
 
     cfg = C.IndexerConfig(heads=64, dim=128, topk=2048, context=65536)
     ns, scores, topk = _run(cfg, 2, seed=46, mode="recent")
+    _check_rows(cfg, ns, scores, topk, expect_clear=False)
+    for r in range(2):
+        assert int((topk[r] >= 65536 - 4096).sum()) > 1500
+
+
+# ------------------------------------------------- SGLang's FP8 DSA index cache
+def _fp8(cfg):
+    from dataclasses import replace
+
+    from sgl_amd_mono.k2 import config as C
+
+    return replace(cfg, keys=C.KEYS_FP8)
+
+
+def test_indexer_fp8_cache_config4_full():
+    """configs[3]'s shape with the keys in SGLang's FP8 index pages [pages, 64, 132]."""
+    from sgl_amd_mono.k2 import config as C
+
+    cfg = _fp8(C.C4_INDEXER)
+    ns, scores, topk = _run(cfg, 8, seed=51)
+    assert ns.cache.shape[1:] == (64, 132)
+    # FP8 keys leave the 2048th and 2049th of 65536 scores closer than the score
+    # tolerance on most rows: the set is checked within the tolerance there
+    _check_rows(cfg, ns, scores, topk, expect_clear=False)
+
+
+def test_indexer_fp8_cache_ragged_rows():
+    from sgl_amd_mono.k2 import config as C
+
+    cfg = _fp8(C.IndexerConfig(heads=48, dim=128, topk=2048, context=8192))
+    ns, scores, topk = _run(cfg, 5, seed=52, ctx_len=[8192, 5003, 2049, 2048, 100])
+    _check_rows(cfg, ns, scores, topk)
+
+
+def test_indexer_fp8_cache_ties_take_lowest_positions():
+    from sgl_amd_mono.k2 import config as C
+
+    cfg = _fp8(C.IndexerConfig(heads=64, dim=128, topk=256, context=4096))
+    ns, scores, topk = _run(cfg, 2, seed=53, mode="ties")
+    for r in range(2):
+        assert torch.unique(scores[r]).numel() == 1
+        assert torch.equal(topk[r], torch.arange(256))
+    _check_rows(cfg, ns, scores, topk, expect_clear=False)
+
+
+def test_indexer_fp8_cache_recent_cluster():
+    from sgl_amd_mono.k2 import config as C
+
+    cfg = _fp8(C.IndexerConfig(heads=64, dim=128, topk=2048, context=65536))
+    ns, scores, topk = _run(cfg, 2, seed=54, mode="recent")
     _check_rows(cfg, ns, scores, topk, expect_clear=False)
     for r in range(2):
         assert int((topk[r] >= 65536 - 4096).sum()) > 1500

@@ -88,6 +88,22 @@ def test_layer_expert_modes(fmt):
     print(stats)
 
 
+@pytest.mark.parametrize("staged", [False, True])
+def test_layer_fp8_index_cache(staged):
+    """The layer reading its index keys from SGLang's FP8 DSA pages [pages, 64, 132]."""
+    from dataclasses import replace
+
+    from sgl_amd_mono.k2 import config as C
+
+    cfg = replace(C.C5_LAYER, mla=replace(C.C5_LAYER.mla, context=8192),
+                  indexer=replace(C.C5_LAYER.indexer, context=8192, keys=C.KEYS_FP8))
+    L, res, olat = run_layer(cfg, 8, seed=550, staged=staged)
+    assert L.idx.cache_scale is None and L.idx.cache.shape[1:] == (64, 132)
+    stats = check_layer(L, *res, o_latent=olat)
+    assert stats["attn_term_checked"] and stats["moe_term_checked"]
+    print(stats)
+
+
 @pytest.mark.parametrize("rows", [8, 32])
 def test_persistent_layer_repeats_and_matches_staged(rows):
     """Back-to-back persistent launches (counters reset by the launch itself) give the

@@ -165,3 +165,64 @@ def test_all_e2m1_pairs_decode():
         v = oc.e2m1_decode(oc.fp4_unpack(byte))
         assert v.tolist() == [oc.e2m1_decode(torch.tensor([a], dtype=torch.uint8))[0].item(),
                               oc.e2m1_decode(torch.tensor([b], dtype=torch.uint8))[0].item()]
+
+
+# ------------------------------------------------------------- DSA FP8 index cache
+@pytest.mark.parametrize("amax, field", [
+    (448.0, 127),            # 448 / 448 = 1 exactly: scale 1
+    (448.00003, 128),        # the next f32 above: scale 2
+    (224.0, 126),            # 0.5 exactly
+    (1.0, 127 - 8),          # 1/448 = 0.00223 lies in (2^-9, 2^-8]
+    (0.0, 127 - 22),         # floor 1e-4: 2.23e-7 lies in (2^-23, 2^-22]
+    (3.0e-5, 127 - 22),      # below the floor: the floor's scale
+])
+def test_index_key_scale_rule_closed_form(amax, field):
+    assert int(oc.index_key_scale_code(torch.tensor(amax))) == field
+
+
+def test_index_key_quant_is_exact_on_representable_keys():
+    """A key of E4M3 values times a power of two comes back exactly, and its scale puts
+    the largest magnitude at 448 * 2^-k for the smallest such k."""
+    vals = torch.tensor([448.0, -1.0, 0.5, 3.25, 0.0] + [0.0] * 123)
+    for e in (-12, 0, 5):
+        k = vals * 2.0**e
+        codes, scale = oc.index_key_quant(k)
+        assert float(scale) == 2.0**e
+        assert torch.equal(oc.e4m3_decode(codes) * scale, k)
+
+
+def test_index_page_single_byte_placement():
+    """One nonzero value byte: token 21, dim 37 sits at byte (21 // 16) * 2048 + (37 // 16)
+    * 256 + (21 % 16) * 16 + 37 % 16 = 2645 of the page; its scale at 8192 + 4 * 21."""
+    page = torch.zeros(1, oc.INDEX_PAGE_BYTES, dtype=torch.uint8)
+    page[0, 2645] = int(oc.e4m3_encode(torch.tensor(3.0)))
+    page[0, 8192 + 4 * 21 : 8192 + 4 * 22] = torch.tensor([0.25], dtype=torch.float32).view(torch.uint8)
+    keys = oc.index_page_decode(page)
+    assert float(keys[0, 21, 37]) == 0.75
+    assert int((keys != 0).sum()) == 1
+
+
+def _token_major_decode(pages):
+    """A planted mistake: the values read token-major (byte t * 128 + d)."""
+    pg = pages.reshape(-1, oc.INDEX_PAGE_BYTES)
+    vals = oc.e4m3_decode(pg[:, : oc.INDEX_VALUE_BYTES].contiguous()).view(-1, 64, 128)
+    return vals * pg[:, oc.INDEX_VALUE_BYTES :].contiguous().view(torch.float32)[..., None]
+
+
+def test_index_pages_writer_and_reader_agree():
+    """The package's page writer (the kernel's byte formula, glm53/gfx950/kernel.py:698-705)
+    against the oracle's reader (the check's, glm53/check.py:75-82): the round trip
+    returns every key; the planted token-major reader does not."""
+    from sgl_amd_mono.k2 import quant, synth
+
+    g = torch.Generator().manual_seed(9)
+    k = torch.randn(3, 64, 128, generator=g) * torch.logspace(-3, 2, 64).view(1, 64, 1)
+    codes, scales = quant.quant_index_fp8(k)
+    c2, s2 = oc.index_key_quant(k)
+    assert torch.equal(codes, c2) and torch.equal(scales, s2)  # product encoder == oracle rule
+    pages = synth.index_pages_fp8(codes, scales)
+    assert pages.shape == (3, 64, 132) and pages.dtype == torch.uint8
+    want = oc.e4m3_decode(codes) * scales[..., None]
+    assert torch.equal(oc.index_page_decode(pages), want)
+    assert not torch.equal(_token_major_decode(pages), want)
+    assert float((want - k).abs().max() / k.abs().amax()) < 2.0**-3

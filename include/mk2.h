@@ -244,6 +244,29 @@ int mk2_layer_launch(const mk2_layer_args* args, mk2_stream_t stream);
 #define MK2_LAYER_STATIC_SCRATCH_BYTES ((size_t)64 << 20)
 int mk2_layer_launch_static(const mk2_layer_args* args, mk2_stream_t stream);
 
+/* ------------------------------------------------------------------ tail
+ * The steps after the last layer, on this GPU's rows of the LM head: the final
+ * RMSNorm and the logits.  Replaces the reference's tail launch,
+ * Glm53HeadOp.launch (glm53/gfx950/runner.py:473-545; kernel glm53/gfx950/kernel.py:
+ * 2220-2350, run_head), without its TP gather of the logits:
+ *   normed[r]    = bf16(x[r] * rsqrt(mean(x[r]^2) + eps) * g_norm)
+ *   logits[r][v] = f32(bf16(normed[r] . w_head[v]))   (bf16 as the reference gathers)
+ * w_head is SGLang's LM head as loaded, bf16 [vocab_rows][hidden] row-major, read in
+ * place.  No workspace.  More than 16 rows stream the LM head twice. */
+typedef struct mk2_tail_args {
+  int rows;             /* 1..32 */
+  int hidden;           /* multiple of 1024 in [2048, 8192] */
+  int vocab_rows;       /* this GPU's LM-head rows, >= 1 */
+  float eps;
+  const void* x;        /* bf16 [rows][hidden]: the last layer's output rows */
+  const void* g_norm;   /* bf16 [hidden] */
+  const void* w_head;   /* bf16 [vocab_rows][hidden] */
+  float* logits;        /* f32 [rows][vocab_rows] */
+  void* normed;         /* bf16 [rows][hidden], or NULL; must not alias x */
+} mk2_tail_args;
+
+int mk2_tail_launch(const mk2_tail_args* args, mk2_stream_t stream);
+
 /* ------------------------------------------------------------------ misc */
 const char* mk2_last_error(void);
 int mk2_abi_version(void);

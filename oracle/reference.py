@@ -23,6 +23,8 @@ a planted mistake that must fail):
   mla_output        -- permutation W_UV, o_lat and sums on bf16 ties
   o_proj            -- permutation W_o, residual sums on bf16 ties
   moe_mix           -- route-weighted sum of hand-built experts
+  expert_a4w4, expert_w8a8 -- hand-worked single experts with their activation rules
+  tail              -- +-2^e rows (exact rstd at eps 0), unit-vector LM-head rows
 The chained layer is the composition of these, checked stage by stage on the GPU
 (tests/refs.check_layer).
 """
@@ -121,6 +123,16 @@ def rmsnorm(a: torch.Tensor, gamma: torch.Tensor, eps: float) -> torch.Tensor:
     a = a.float()
     rstd = torch.rsqrt(a.pow(2).mean(-1, keepdim=True) + eps)
     return codecs.bf16_round(a * rstd * gamma.float())
+
+
+def tail(x: torch.Tensor, g_norm: torch.Tensor, w_head: torch.Tensor, eps: float):
+    """The tail after the last layer: (logits f32 [rows, V], normed bf16 values as f32
+    [rows, H]).  normed = bf16(rmsnorm(x) * g), logits = bf16(normed . w_head[v]) in f64,
+    rounded to bf16 as the reference's tail gathers them (glm53/gfx950/kernel.py:
+    2220-2350; its check's torch tail, test/kernels/glm53/check_layer.py:744-757)."""
+    normed = rmsnorm(x, g_norm, eps)
+    logits = codecs.bf16_round((normed.double() @ w_head.double().t()).float())
+    return logits, normed
 
 
 def _topk_by_key(keys: torch.Tensor, k: int) -> torch.Tensor:

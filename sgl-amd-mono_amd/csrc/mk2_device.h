@@ -33,13 +33,10 @@ namespace mk2 {
 
 // ----------------------------------------------------------------- bf16 / f32
 MK2_DEV float bf16_to_f32(bf16_t v) { return __uint_as_float(((uint32_t)v) << 16); }
-MK2_DEV bf16_t f32_to_bf16(float f) {  // round to nearest even (finite inputs)
-  uint32_t u = __float_as_uint(f);
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return (bf16_t)(u >> 16);
-}
+// f32 -> bf16, round to nearest even: one v_cvt_pk_bf16_f32 (gfx950) a pair
+MK2_DEV bf16_t f32_to_bf16(float f) { return __builtin_bit_cast(bf16_t, (__bf16)f); }
 MK2_DEV uint32_t pack_bf16x2(float lo, float hi) {
-  return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
 }
 // two f32 that are exactly representable in bf16 -> packed pair (truncation is exact)
 MK2_DEV uint32_t pack_bf16x2_exact(float lo, float hi) {

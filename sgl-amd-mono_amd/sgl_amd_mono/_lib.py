@@ -99,6 +99,13 @@ class LayerArgs(ctypes.Structure):
     ]
 
 
+class TailArgs(ctypes.Structure):
+    _fields_ = [
+        ("rows", c_int), ("hidden", c_int), ("vocab_rows", c_int), ("eps", c_float),
+        ("x", c_void_p), ("g_norm", c_void_p), ("w_head", c_void_p), ("logits", c_void_p), ("normed", c_void_p),
+    ]
+
+
 # entry point -> (argtypes); every one returns int
 SIGNATURES = {
     "mk2_moe_workspace_bytes": [POINTER(MoeShape), POINTER(c_size_t)],
@@ -110,6 +117,7 @@ SIGNATURES = {
     "mk2_layer_workspace_bytes": [POINTER(LayerArgs), POINTER(c_size_t)],
     "mk2_layer_launch": [POINTER(LayerArgs), c_void_p],
     "mk2_layer_launch_static": [POINTER(LayerArgs), c_void_p],
+    "mk2_tail_launch": [POINTER(TailArgs), c_void_p],
     "mk2_abi_version": [],
     "mk2_selftest_mfma": [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],
 }

@@ -142,6 +142,26 @@ class K2Config:
             raise ValueError("the indexer and the attention share one context")
 
 
+@dataclass(frozen=True)
+class TailConfig:
+    """The tail after the last layer: final RMSNorm, then this GPU's LM-head rows."""
+
+    hidden: int = 6144
+    vocab_rows: int = 19360  # GLM-5.3's 154880-token vocabulary over 8 GPUs
+    eps: float = 1e-5
+
+    def validate(self, rows: int) -> None:
+        """The rules of the C side (mk2_tail_launch)."""
+        if not 1 <= rows <= MAX_ROWS:
+            raise ValueError(f"rows must be in [1, {MAX_ROWS}], got {rows}")
+        if self.hidden % 1024 or not 2048 <= self.hidden <= 8192:
+            raise ValueError(f"hidden must be a multiple of 1024 in [2048, 8192], got {self.hidden}")
+        if self.vocab_rows < 1:
+            raise ValueError(f"vocab_rows must be positive, got {self.vocab_rows}")
+        if not self.eps > 0:
+            raise ValueError("eps must be positive")
+
+
 # configs[0]: FP8 MoE block, CPU-runnable
 C1_MOE = MoEConfig(
     hidden=2048, n_experts=64, top_k=8, inter=768, router=ROUTER_SOFTMAX,
@@ -160,3 +180,5 @@ C4_INDEXER = IndexerConfig(context=65536)
 C5_LAYER = K2Config(
     mla=replace(C3_MLA, context=65536), indexer=C4_INDEXER, moe=C2_MOE, eps=1e-6
 )
+# the tail after the layer stack (one GPU's share of the LM head)
+C6_TAIL = TailConfig()

@@ -112,6 +112,34 @@ class IndexerOp:
         return scores, topk
 
 
+class TailOp:
+    """The tail after the last layer: the final RMSNorm of the rows and this GPU's rows
+    of the LM head, read in place from SGLang's bf16 [vocab_rows, hidden]."""
+
+    def __init__(self, cfg: C.TailConfig, g_norm, w_head, rows: int, device=None):
+        cfg.validate(rows)
+        self.cfg, self.rows = cfg, rows
+        self.device = torch.device(device or w_head.device)
+        _need(g_norm, "g_norm", torch.bfloat16, (cfg.hidden,))
+        _need(w_head, "w_head", torch.bfloat16, (cfg.vocab_rows, cfg.hidden))
+        self.g_norm, self.w_head = g_norm, w_head
+
+    def __call__(self, x, logits=None, normed=None):
+        """x bf16 [rows, hidden] -> (logits f32 [rows, vocab_rows], normed bf16 [rows, hidden])."""
+        cfg, rows = self.cfg, self.rows
+        _need(x, "x", torch.bfloat16, (rows, cfg.hidden))
+        if logits is None:
+            logits = torch.empty(rows, cfg.vocab_rows, dtype=torch.float32, device=self.device)
+        if normed is None:
+            normed = torch.empty(rows, cfg.hidden, dtype=torch.bfloat16, device=self.device)
+        _need(logits, "logits", torch.float32, (rows, cfg.vocab_rows))
+        _need(normed, "normed", torch.bfloat16, (rows, cfg.hidden))
+        args = _lib.TailArgs(rows, cfg.hidden, cfg.vocab_rows, cfg.eps, _p(x), _p(self.g_norm), _p(self.w_head),
+                             _p(logits), _p(normed))
+        _lib.check(_lib.lib().mk2_tail_launch(ctypes.byref(args), _lib.stream_handle(self.device)))
+        return logits, normed
+
+
 class SparseMlaOp:
     """Sparse MLA over selected latent-KV rows, W_UV, then W_o (+ residual)."""
 

@@ -163,6 +163,17 @@ def make_mla(cfg: C.MlaConfig, rows: int, seed: int, device, residual: bool = Tr
     return ns
 
 
+def make_tail(cfg: C.TailConfig, rows: int, seed: int, device):
+    """The last layer's rows x ~ N(0, 1) (bf16), the final norm's weight 1 + N(0,
+    0.1^2) and LM-head rows ~ N(0, 1/hidden) in SGLang's bf16 [vocab_rows, hidden]."""
+    g = _gen(seed, device)
+    ns = SimpleNamespace(cfg=cfg, rows=rows)
+    ns.x = _randn(g, rows, cfg.hidden, device=device).to(torch.bfloat16)
+    ns.g_norm = (1.0 + _randn(g, cfg.hidden, device=device, std=0.1)).to(torch.bfloat16)
+    ns.w_head = _randn(g, cfg.vocab_rows, cfg.hidden, device=device, std=cfg.hidden**-0.5).to(torch.bfloat16)
+    return ns
+
+
 def make_layer(cfg: C.K2Config, rows: int, seed: int, device, h_std: float = 1.0):
     """One chained layer: indexer keys and queries, latent-KV pages sharing the
     indexer's page table, attention weights, residual rows ~ N(0, h_std^2), MoE

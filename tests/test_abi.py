@@ -43,11 +43,12 @@ def test_ctypes_layouts_match_the_header():
 #include <stddef.h>
 #include "mk2.h"
 int main(void) {
-  printf("%zu %zu %zu %zu %zu %zu %zu %zu\n", sizeof(mk2_moe_shape), sizeof(mk2_moe_weights),
+  printf("%zu %zu %zu %zu %zu %zu %zu %zu %zu\n", sizeof(mk2_moe_shape), sizeof(mk2_moe_weights),
          sizeof(mk2_moe_args), sizeof(mk2_indexer_shape), sizeof(mk2_indexer_args),
-         sizeof(mk2_mla_shape), sizeof(mk2_mla_args), sizeof(mk2_layer_args));
-  printf("%zu %zu %zu\n", offsetof(mk2_moe_args, logits), offsetof(mk2_mla_args, o_latent),
-         offsetof(mk2_layer_args, workspace_bytes));
+         sizeof(mk2_mla_shape), sizeof(mk2_mla_args), sizeof(mk2_layer_args), sizeof(mk2_tail_args));
+  printf("%zu %zu %zu %zu %zu\n", offsetof(mk2_moe_args, logits), offsetof(mk2_mla_args, o_latent),
+         offsetof(mk2_layer_args, workspace_bytes), offsetof(mk2_indexer_shape, key_fmt),
+         offsetof(mk2_tail_args, normed));
   return 0;
 }
 '''
@@ -59,10 +60,11 @@ int main(void) {
     sizes = [int(x) for x in out[0].split()]
     offs = [int(x) for x in out[1].split()]
     mine = [ctypes.sizeof(t) for t in (_l.MoeShape, _l.MoeWeights, _l.MoeArgs, _l.IndexerShape,
-                                       _l.IndexerArgs, _l.MlaShape, _l.MlaArgs, _l.LayerArgs)]
+                                       _l.IndexerArgs, _l.MlaShape, _l.MlaArgs, _l.LayerArgs, _l.TailArgs)]
     assert sizes == mine
     assert offs == [_l.MoeArgs.logits.offset, _l.MlaArgs.o_latent.offset,
-                    _l.LayerArgs.workspace_bytes.offset]
+                    _l.LayerArgs.workspace_bytes.offset, _l.IndexerShape.key_fmt.offset,
+                    _l.TailArgs.normed.offset]
 
 
 def _moe_shape(_l, **kw):
@@ -116,4 +118,14 @@ def test_launch_argument_errors_never_reach_the_device():
     assert L.mk2_indexer_topk_launch(ctypes.byref(ia), None) == _l.MK2_EINVAL
     assert "key_fmt" in L.mk2_last_error().decode()
     assert L.mk2_layer_launch(None, None) == _l.MK2_EINVAL
+    assert L.mk2_tail_launch(None, None) == _l.MK2_EINVAL
+    ta = _l.TailArgs(8, 6144, 0, 1e-5, fake, fake, fake, fake, None)
+    assert L.mk2_tail_launch(ctypes.byref(ta), None) == _l.MK2_EINVAL
+    assert "vocab_rows" in L.mk2_last_error().decode()
+    ta.vocab_rows, ta.hidden = 19360, 6000
+    assert L.mk2_tail_launch(ctypes.byref(ta), None) == _l.MK2_EINVAL
+    assert "hidden" in L.mk2_last_error().decode()
+    ta.hidden, ta.normed = 6144, fake
+    assert L.mk2_tail_launch(ctypes.byref(ta), None) == _l.MK2_EINVAL
+    assert "alias" in L.mk2_last_error().decode()
     assert L.mk2_selftest_mfma(9, None, None, None, None, None, None) == _l.MK2_EINVAL

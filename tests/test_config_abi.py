@@ -93,3 +93,27 @@ def test_a_config_the_c_side_rejects_fails_validate():
     assert not _moe_c_ok(_l, L, cfg, 4)
     with pytest.raises(ValueError):
         cfg.validate(4)
+
+
+def test_tail_validate_matches_c():
+    """The tail's argument checks (mk2_tail_launch) against TailConfig.validate().  The C
+    side validates before it touches the device; on this CPU-only host an accepted call
+    then fails to query the CU count (MK2_ELAUNCH), a refused one returns MK2_EINVAL.
+    The pointers are never dereferenced, so the check runs only where no GPU exists."""
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("accepted calls would launch on the fake pointers")
+    _l, L = _lib()
+    fake = 0x1000
+    seen = {True: 0, False: 0}
+    for hidden, vocab_rows, rows in itertools.product((1024, 2048, 6144, 6000, 8192, 9216), (0, 16, 19360, 19361),
+                                                      (0, 1, 32, 33)):
+        cfg = C.TailConfig(hidden=hidden, vocab_rows=vocab_rows)
+        a = _l.TailArgs(rows, hidden, vocab_rows, cfg.eps, fake, fake, fake, fake, None)
+        rc = L.mk2_tail_launch(ctypes.byref(a), None)
+        c = rc != _l.MK2_EINVAL
+        py = _py_ok(cfg, rows)
+        assert py == c, (cfg, rows, py, rc, L.mk2_last_error())
+        seen[py] += 1
+    assert seen[True] and seen[False]

@@ -358,3 +358,45 @@ def test_expert_w8a8_closed_form():
     gu = x @ w13.T
     mid = R.swiglu(gu[:, :128], gu[:, 128:])
     assert not _exact((oc.fp8_block_act_dequant(*oc.fp8_block_act_quant(mid)) @ w2.T)[0], y)  # x not quantized
+
+
+# ------------------------------------------------------------------------- tail
+def _tail_case():
+    """H = 8, V = 5.  Row 0 = +-2 (mean square 4: rstd 1/2 exactly at eps 0), row 1 =
+    0.25 everywhere (rstd 4); g = (1, 1, .5, 2, 1, 1, 1, 1), so normed row 0 = (1, -1,
+    .5, -2, 1, -1, 1, -1) and row 1 = g.  LM-head rows: e0, e3, all ones, 3 e2 - e7, and
+    e0 + 2^-9 e1, whose logits 1 -+ 2^-9 round to bf16 1."""
+    x = torch.tensor([[2.0, -2, 2, -2, 2, -2, 2, -2], [0.25] * 8])
+    g = torch.tensor([1.0, 1, 0.5, 2, 1, 1, 1, 1])
+    w = torch.zeros(5, 8)
+    w[0, 0] = 1
+    w[1, 3] = 1
+    w[2] = 1
+    w[3, 2], w[3, 7] = 3, -1
+    w[4, 0], w[4, 1] = 1, 2.0**-9
+    normed = torch.tensor([[1.0, -1, 0.5, -2, 1, -1, 1, -1], [1.0, 1, 0.5, 2, 1, 1, 1, 1]])
+    logits = torch.tensor([[1.0, -2, -1.5, 2.5, 1 - 2.0**-9], [1.0, 2, 8.5, 0.5, 1]])
+    return x, g, w, normed, logits
+
+
+def test_tail_closed_form():
+    x, g, w, normed, logits = _tail_case()
+    got_l, got_n = R.tail(x, g, w, 0.0)
+    assert torch.equal(got_n, normed)
+    # row 0's last logit 1 - 2^-9 is below half an ulp of 1 away from 1: bf16 rounds it to 1
+    logits[0, 4] = 1.0
+    assert torch.equal(got_l, logits)
+
+
+@pytest.mark.parametrize("plant", ["no_gamma", "no_round", "transposed"])
+def test_tail_pin_catches_planted_mistakes(plant):
+    x, g, w, normed, logits = _tail_case()
+    logits[0, 4] = 1.0
+    if plant == "no_gamma":
+        got, _ = R.tail(x, torch.ones(8), w, 0.0)
+    elif plant == "no_round":
+        n = R.rmsnorm(x, g, 0.0)
+        got = (n.double() @ w.double().t()).float()
+    else:
+        got, _ = R.tail(x, g, w.flip(1), 0.0)  # the LM-head rows read with k reversed
+    assert not torch.equal(got, logits)

@@ -267,6 +267,46 @@ typedef struct mk2_tail_args {
 
 int mk2_tail_launch(const mk2_tail_args* args, mk2_stream_t stream);
 
+/* ------------------------------------------------------------ step tables
+ * A step's per-row tables, from SGLang's rows, in one launch before the layer stack.
+ * Replaces the reference's tables.step_rows (glm53/tables.py:26-131); the outputs
+ * are its Glm53Step's (runner.py:138-151) plus ctx_len, the layer's per-row key
+ * counts.  Row s < rows takes its slot from out_cache_loc[s] (0 = SGLang's padding
+ * slot: a pad row, slot -1), its position min(positions[s], max_position), request
+ * row s, and keys indptr[s] ..< indptr[s + 1]: min(position + 1, topk) for a row with
+ * a slot, 0 for a pad row, or with a seed (a draft step reusing a top-k: int32
+ * [rows][topk], -1 unused) the seed row's valid entries, compacted in order into
+ * topk_out (seed_by_position: its first min(position + 1, topk) entries as they
+ * are).  Rows rows ..< width are pad rows (slot -1, position 0, request 0, id -1).
+ * ctx_len[s] = position + 1 for a row with a slot, else 0. */
+typedef struct mk2_step_args {
+  int width;                 /* W: 1..32 */
+  int rows;                  /* S: SGLang's rows this step, 0..W */
+  int topk;                  /* K: the keys a row attends at most, 1..4096 */
+  int seed_by_position;      /* 0, or 1: seed entries counted by position */
+  int64_t max_position;      /* the last position of the context */
+  const int64_t* out_cache_loc; int64_t loc_stride;  /* [S] (strided views allowed) */
+  const int64_t* positions;  int64_t pos_stride;      /* [S] */
+  const void* ids_in;        int64_t ids_stride;      /* [S] token ids, or NULL */
+  int ids_in_bytes;          /* 4 or 8: int32 or int64 ids_in */
+  const int32_t* seed;       int64_t seed_stride;     /* [S][K], or NULL */
+  int64_t* slots;            /* [W] */
+  int64_t* positions_out;    /* [W] */
+  int32_t* indptr;           /* [W + 1] */
+  int32_t* req_ids;          /* [W] */
+  int32_t* topk_out;         /* [W * K + 1]: with a seed */
+  int32_t* ids;              /* [W], or NULL (needs ids_in) */
+  int32_t* ctx_len;          /* [W], or NULL */
+} mk2_step_args;
+
+int mk2_step_rows_launch(const mk2_step_args* args, mk2_stream_t stream);
+
+/* seed row s (s < rows) := the keys of step row rows_of[s], topk[indptr[src] ..<
+ * indptr[src + 1]], then -1 up to k.  Replaces tables.write_seed
+ * (glm53/tables.py:134-167). */
+int mk2_write_seed_launch(const int32_t* topk, const int32_t* indptr, int32_t* seed, int64_t seed_stride,
+                          const int32_t* rows_of, int rows, int k, mk2_stream_t stream);
+
 /* ------------------------------------------------------------------ misc */
 const char* mk2_last_error(void);
 int mk2_abi_version(void);

@@ -25,6 +25,7 @@ a planted mistake that must fail):
   moe_mix           -- route-weighted sum of hand-built experts
   expert_a4w4, expert_w8a8 -- hand-worked single experts with their activation rules
   tail              -- +-2^e rows (exact rstd at eps 0), unit-vector LM-head rows
+  step_rows, write_seed -- the reference's own cases (tests/golden/step_rows_cases.json)
 The chained layer is the composition of these, checked stage by stage on the GPU
 (tests/refs.check_layer).
 """
@@ -133,6 +134,51 @@ def tail(x: torch.Tensor, g_norm: torch.Tensor, w_head: torch.Tensor, eps: float
     normed = rmsnorm(x, g_norm, eps)
     logits = codecs.bf16_round((normed.double() @ w_head.double().t()).float())
     return logits, normed
+
+
+# -------------------------------------------------------------------- step tables
+def step_rows(loc, pos, S: int, W: int, K: int, max_position: int, ids_in=None, seed=None,
+              seed_by_position: bool = False) -> dict:
+    """A step's row tables from SGLang's rows, one row at a time (glm53/tables.py:26-131,
+    the Triton kernel _step_rows): row s < S takes slot loc[s] (0: a pad row, -1),
+    position min(pos[s], max_position), request s, id ids_in[s], and keys indptr[s] ..<
+    indptr[s + 1] -- min(position + 1, K) for a row with a slot, or with a seed the
+    row's entries >= 0 in order (by position: its first min(position + 1, K) entries as
+    they are); rows S ..< W: slot -1, position 0, request 0, id -1, no keys.  ctx_len:
+    position + 1 for a row with a slot, else 0."""
+    out = {"slots": [-1] * W, "positions": [0] * W, "req_ids": [0] * W, "ids": [-1] * W,
+           "ctx_len": [0] * W, "indptr": [0] * (W + 1), "topk": []}
+    for s in range(W):
+        count = 0
+        if s < S:
+            slot, p = int(loc[s]), min(int(pos[s]), max_position)
+            live = slot != 0
+            out["positions"][s], out["req_ids"][s] = p, s
+            if ids_in is not None:
+                out["ids"][s] = int(ids_in[s])
+            if live:
+                out["slots"][s], out["ctx_len"][s] = slot, p + 1
+                if seed is not None and not seed_by_position:
+                    kept = [int(v) for v in seed[s][:K] if int(v) >= 0]
+                    out["topk"] += kept
+                    count = len(kept)
+                else:
+                    count = min(p + 1, K)
+                    if seed is not None:
+                        out["topk"] += [int(v) for v in seed[s][:count]]
+        out["indptr"][s + 1] = out["indptr"][s] + count
+    return out
+
+
+def write_seed(topk, indptr, rows_of, K: int) -> list:
+    """Seed row s := the keys of step row rows_of[s], then -1 up to K
+    (glm53/tables.py:134-167)."""
+    rows = []
+    for src in rows_of:
+        a, b = int(indptr[src]), int(indptr[src + 1])
+        keys = [int(v) for v in topk[a:b]][:K]
+        rows.append(keys + [-1] * (K - len(keys)))
+    return rows
 
 
 def _topk_by_key(keys: torch.Tensor, k: int) -> torch.Tensor:

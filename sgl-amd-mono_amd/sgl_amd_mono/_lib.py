@@ -11,7 +11,7 @@ from __future__ import annotations
 
 import ctypes
 import os
-from ctypes import POINTER, c_char_p, c_float, c_int, c_size_t, c_void_p
+from ctypes import POINTER, c_char_p, c_float, c_int, c_int64, c_size_t, c_void_p
 from pathlib import Path
 
 import torch  # noqa: F401  (must precede the CDLL load, see the module docstring)
@@ -106,6 +106,19 @@ class TailArgs(ctypes.Structure):
     ]
 
 
+class StepArgs(ctypes.Structure):
+    _fields_ = [
+        ("width", c_int), ("rows", c_int), ("topk", c_int), ("seed_by_position", c_int),
+        ("max_position", c_int64),
+        ("out_cache_loc", c_void_p), ("loc_stride", c_int64),
+        ("positions", c_void_p), ("pos_stride", c_int64),
+        ("ids_in", c_void_p), ("ids_stride", c_int64), ("ids_in_bytes", c_int),
+        ("seed", c_void_p), ("seed_stride", c_int64),
+        ("slots", c_void_p), ("positions_out", c_void_p), ("indptr", c_void_p), ("req_ids", c_void_p),
+        ("topk_out", c_void_p), ("ids", c_void_p), ("ctx_len", c_void_p),
+    ]
+
+
 # entry point -> (argtypes); every one returns int
 SIGNATURES = {
     "mk2_moe_workspace_bytes": [POINTER(MoeShape), POINTER(c_size_t)],
@@ -118,6 +131,8 @@ SIGNATURES = {
     "mk2_layer_launch": [POINTER(LayerArgs), c_void_p],
     "mk2_layer_launch_static": [POINTER(LayerArgs), c_void_p],
     "mk2_tail_launch": [POINTER(TailArgs), c_void_p],
+    "mk2_step_rows_launch": [POINTER(StepArgs), c_void_p],
+    "mk2_write_seed_launch": [c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int, c_int, c_void_p],
     "mk2_abi_version": [],
     "mk2_selftest_mfma": [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],
 }

@@ -140,6 +140,61 @@ class TailOp:
         return logits, normed
 
 
+class StepRows:
+    """A step's row tables for width W (the reference's Glm53Step plus ctx_len), filled
+    from SGLang's rows by one launch (mk2_step_rows_launch) and read back as a seed
+    (mk2_write_seed_launch)."""
+
+    def __init__(self, width: int, topk: int = 2048, device=None):
+        if not 1 <= width <= C.MAX_ROWS:
+            raise ValueError(f"width must be in [1, {C.MAX_ROWS}], got {width}")
+        self.width, self.k = width, topk
+        self.device = torch.device(device or "cuda")
+        i32, i64 = dict(dtype=torch.int32, device=self.device), dict(dtype=torch.int64, device=self.device)
+        self.slots = torch.empty(width, **i64)
+        self.positions = torch.empty(width, **i64)
+        self.indptr = torch.empty(width + 1, **i32)
+        self.req_ids = torch.empty(width, **i32)
+        self.topk = torch.empty(width * topk + 1, **i32)
+        self.ids = torch.empty(width, **i32)
+        self.ctx_len = torch.empty(width, **i32)
+
+    def __call__(self, out_cache_loc, positions, rows: int, max_position: int, *, ids_in=None, seed=None,
+                 seed_by_position: bool = False):
+        """Fill the tables for SGLang's first `rows` rows (int64 slots and positions, 1-D
+        views of any stride; ids_in int32 or int64; seed int32 [rows, topk])."""
+        if not 0 <= rows <= self.width:
+            raise ValueError(f"rows must be in [0, {self.width}], got {rows}")
+        for t, name in ((out_cache_loc, "out_cache_loc"), (positions, "positions")):
+            if t.dtype != torch.int64 or t.dim() != 1 or t.shape[0] < rows or not t.is_cuda:
+                raise ValueError(f"{name} must be a 1-D int64 device tensor of >= {rows} entries")
+        if ids_in is not None and (ids_in.dtype not in (torch.int32, torch.int64) or ids_in.dim() != 1):
+            raise ValueError("ids_in must be a 1-D int32 or int64 tensor")
+        if seed is not None and (seed.dtype != torch.int32 or seed.dim() != 2 or seed.shape[1] != self.k
+                                 or seed.stride(1) != 1 or seed.shape[0] < rows):
+            raise ValueError(f"seed must be an int32 [rows, {self.k}] tensor with unit inner stride")
+        a = _lib.StepArgs(
+            self.width, rows, self.k, int(seed_by_position), max_position,
+            _p(out_cache_loc), out_cache_loc.stride(0), _p(positions), positions.stride(0),
+            _p(ids_in), ids_in.stride(0) if ids_in is not None else 0,
+            ids_in.element_size() if ids_in is not None else 8,
+            _p(seed), seed.stride(0) if seed is not None else 0,
+            _p(self.slots), _p(self.positions), _p(self.indptr), _p(self.req_ids),
+            _p(self.topk), _p(self.ids) if ids_in is not None else None, _p(self.ctx_len),
+        )
+        _lib.check(_lib.lib().mk2_step_rows_launch(ctypes.byref(a), _lib.stream_handle(self.device)))
+        return self
+
+    def write_seed(self, seed, rows: int, rows_of):
+        """seed row s := the keys of step row rows_of[s], then -1 (int32 [>= rows, topk])."""
+        if seed.dtype != torch.int32 or seed.dim() != 2 or seed.shape[1] != self.k or seed.stride(1) != 1:
+            raise ValueError(f"seed must be an int32 [rows, {self.k}] tensor with unit inner stride")
+        _need(rows_of, "rows_of", torch.int32)
+        _lib.check(_lib.lib().mk2_write_seed_launch(_p(self.topk), _p(self.indptr), _p(seed), seed.stride(0),
+                                                    _p(rows_of), rows, self.k, _lib.stream_handle(self.device)))
+        return seed
+
+
 class SparseMlaOp:
     """Sparse MLA over selected latent-KV rows, W_UV, then W_o (+ residual)."""
 

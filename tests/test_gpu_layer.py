@@ -104,6 +104,44 @@ def test_layer_fp8_index_cache(staged):
     print(stats)
 
 
+@pytest.mark.parametrize("staged", [False, True])
+def test_layer_pad_and_short_rows(staged):
+    """Row lengths as the step tables give them: a pad row (no keys: no list, zero
+    attention, its MoE on h alone), a one-key row, a short row and a full one."""
+    from dataclasses import replace
+
+    from sgl_amd_mono.k2 import config as C, synth
+    from sgl_amd_mono.k2.ops import LayerOp
+
+    dev = _dev()
+    cfg = replace(C.C5_LAYER, mla=replace(C.C5_LAYER.mla, context=8192),
+                  indexer=replace(C.C5_LAYER.indexer, context=8192))
+    rows = 4
+    L = synth.make_layer(cfg, rows, 560, dev, h_std=H_STD)
+    L.idx.ctx_len.copy_(torch.tensor([8192, 0, 1, 2500], dtype=torch.int32))
+    op = LayerOp(cfg, L, rows, device=dev, staged=staged)
+    H, E, K = cfg.mla.hidden, cfg.moe.n_experts, cfg.moe.top_k
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+    attn = torch.empty(rows, H, dtype=torch.bfloat16, device=dev)
+    scores = torch.empty(rows, cfg.indexer.context, dtype=torch.float32, device=dev)
+    topk = torch.empty(rows, cfg.indexer.topk, dtype=torch.int32, device=dev)
+    logits = torch.empty(rows, E, dtype=torch.float32, device=dev)
+    ids = torch.empty(rows, K, dtype=torch.int32, device=dev)
+    wts = torch.empty(rows, K, dtype=torch.float32, device=dev)
+    olat = torch.empty(rows, cfg.mla.heads, cfg.mla.kv_lora, dtype=torch.float32, device=dev)
+    out = op(attn_out=attn, scores=scores, topk=topk, logits=logits, topk_ids=ids, topk_weights=wts,
+             status=status, o_latent=olat)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0
+    res = [cpu(t) for t in (out, attn, scores, topk, logits, ids, wts)]
+    assert bool((res[3][1] == -1).all()) and res[3][2, 0] == 0 and bool((res[3][2, 1:] == -1).all())
+    assert bool((cpu(olat)[1] == 0).all())  # no keys: zero attention
+    assert torch.equal(res[1][1], cpu(L.h)[1])  # attn = h + 0
+    assert bool(torch.isfinite(res[0]).all())
+    stats = check_layer(L, *res, o_latent=cpu(olat))
+    print(stats)
+
+
 @pytest.mark.parametrize("rows", [8, 32])
 def test_persistent_layer_repeats_and_matches_staged(rows):
     """Back-to-back persistent launches (counters reset by the launch itself) give the

@@ -244,6 +244,84 @@ int mk2_layer_launch(const mk2_layer_args* args, mk2_stream_t stream);
 #define MK2_LAYER_STATIC_SCRATCH_BYTES ((size_t)64 << 20)
 int mk2_layer_launch_static(const mk2_layer_args* args, mk2_stream_t stream);
 
+/* ----------------------------------------------------------------- front
+ * The layer's front, the reference's K1 (glm53/gfx950/kernel.py:2585-3575): from the
+ * residual rows h to what mk2_layer_launch takes -- the absorbed MLA queries, the
+ * index queries and head weights -- and this step's latent-KV and index cache rows:
+ *   x_n  = bf16(rmsnorm(h) * g_in)
+ *   [q_a | kv_a | k_pe] = W_qkv_a x_n,  ik = W_ik x_n,  iw = W_iw x_n        (f32)
+ *   q_an = bf16(rmsnorm(q_a) * g_q_a)
+ *   latent row = e4m3(bf16(rmsnorm(kv_a) * g_kv_a) | bf16(rope(k_pe))) (/ its scale)
+ *   index row  = quant(fwht(rope64(layernorm(ik) * g_ik + b_ik)))
+ *   mla_q[h]   = bf16(W_UK[h] . bf16(q_nope[h])) | bf16(rope(q_pe[h])), q_b = W_q_b q_an
+ *   index_q[h] = bf16(fwht(rope64(bf16(W_iq q_an)[h]))),  index_w = bf16(iw)
+ * rope: interleaved pairs (2i, 2i+1) by rope_cos_sin[position] (SGLang's cos_sin_cache
+ * f32 [positions][rope], cos | sin); fwht: the orthonormal 128-point Hadamard
+ * transform (Sylvester order); quant: the index cache's (MK2_KEYS_FP8: ue8m0 +
+ * E4M3, MK2_KEYS_FP4: MXFP4).  Weights are SGLang's as loaded, row-major, read in
+ * place: bf16, or E4M3 with f32 128 x 128 block scales [ceil(rows/128)][K/128]
+ * (W_iw is bf16 in both).  W_UK is SGLang's w_kc, bf16 [heads][kv_lora][nope] in
+ * memory.  A row with slot < 0 (a pad row) writes no cache rows.  Four launches in
+ * stream order; the workspace holds the f32 GEMV outputs. */
+#define MK2_WFMT_BF16 0
+#define MK2_WFMT_FP8_BLOCK 1
+
+typedef struct mk2_front_shape {
+  int rows;          /* 1..32 */
+  int hidden;        /* 1024, 2048, 3072, 4096, 6144, 7168 or 8192 */
+  int q_lora;        /* as hidden */
+  int kv_lora;       /* 512 */
+  int rope;          /* 64 */
+  int nope;          /* 128, 192 or 256 */
+  int heads;         /* MLA heads of this GPU */
+  int index_heads;   /* 0 (no indexer) or a multiple of 16 up to 64; index dim 128 */
+  int weight_fmt;    /* MK2_WFMT_* of W_qkv_a, W_q_b, W_iq, W_ik */
+  int key_fmt;       /* MK2_KEYS_*: the index cache's format */
+  int kv_scaled;     /* 1: latent rows with a f32 scale (amax / 448) each; 0: SGLang's unscaled */
+  int max_position;  /* the last position of rope_cos_sin */
+  float eps;         /* the RMSNorms' */
+  float index_eps;   /* the index key LayerNorm's */
+} mk2_front_shape;
+
+typedef struct mk2_front_weights {
+  const void* g_in;      /* bf16 [hidden] */
+  const void* w_qkv_a;   /* [q_lora + kv_lora + rope][hidden] */
+  const float* s_qkv_a;
+  const void* g_q_a;     /* bf16 [q_lora] */
+  const void* g_kv_a;    /* bf16 [kv_lora] */
+  const void* w_q_b;     /* [heads * (nope + rope)][q_lora] */
+  const float* s_q_b;
+  const void* w_uk;      /* bf16 [heads][kv_lora][nope] */
+  const void* w_iq;      /* [index_heads * 128][q_lora] */
+  const float* s_iq;
+  const void* w_ik;      /* [128][hidden] */
+  const float* s_ik;
+  const float* g_ik;     /* f32 [128] */
+  const float* b_ik;     /* f32 [128] */
+  const void* w_iw;      /* bf16 [index_heads][hidden] */
+} mk2_front_weights;
+
+typedef struct mk2_front_args {
+  mk2_front_shape shape;
+  mk2_front_weights weights;
+  const void* x;             /* bf16 [rows][hidden]: the residual rows */
+  const int64_t* positions;  /* [rows] (clamped to max_position) */
+  const int64_t* slots;      /* [rows] cache slots, < 0: a pad row */
+  const float* rope_cos_sin; /* f32 [max_position + 1][rope] */
+  uint8_t* kv_cache;         /* [slots][kv_lora + rope] E4M3 */
+  float* kv_scale;           /* [slots] (kv_scaled), or NULL */
+  uint8_t* index_cache;      /* FP8: [pages][64][132]; FP4: the plane's codes [pages][4][64][16] */
+  uint8_t* index_scale;      /* FP4: the plane's E8M0 [pages][4][64]; FP8: NULL */
+  void* mla_q;               /* bf16 [rows][heads][kv_lora + rope] */
+  void* index_q;             /* bf16 [rows][index_heads][128] */
+  void* index_w;             /* bf16 [rows][index_heads] */
+  void* workspace;
+  size_t workspace_bytes;
+} mk2_front_args;
+
+int mk2_front_workspace_bytes(const mk2_front_shape* shape, size_t* bytes);
+int mk2_front_launch(const mk2_front_args* args, mk2_stream_t stream);
+
 /* ------------------------------------------------------------------ tail
  * The steps after the last layer, on this GPU's rows of the LM head: the final
  * RMSNorm and the logits.  Replaces the reference's tail launch,

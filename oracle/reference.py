@@ -26,6 +26,9 @@ a planted mistake that must fail):
   expert_a4w4, expert_w8a8 -- hand-worked single experts with their activation rules
   tail              -- +-2^e rows (exact rstd at eps 0), unit-vector LM-head rows
   step_rows, write_seed -- the reference's own cases (tests/golden/step_rows_cases.json)
+  rope_pairs, fwht128, layernorm, front -- a known rotation and its inverse, the
+                       Hadamard matrix against scipy's and H H^T = n I, torch's
+                       layer_norm, and a front worked by hand with planted mistakes
 The chained layer is the composition of these, checked stage by stage on the GPU
 (tests/refs.check_layer).
 """
@@ -134,6 +137,76 @@ def tail(x: torch.Tensor, g_norm: torch.Tensor, w_head: torch.Tensor, eps: float
     normed = rmsnorm(x, g_norm, eps)
     logits = codecs.bf16_round((normed.double() @ w_head.double().t()).float())
     return logits, normed
+
+
+# ------------------------------------------------------------------ the layer front
+def rope_pairs(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Interleaved RoPE: pairs (2i, 2i + 1) rotated by angle i (glm53/gfx950/kernel.py:
+    3107-3131,3245-3251,3358-3372); cos and sin [..., n / 2]."""
+    y = x.clone()
+    x0, x1 = x[..., 0::2], x[..., 1::2]
+    y[..., 0::2] = x0 * cos - x1 * sin
+    y[..., 1::2] = x0 * sin + x1 * cos
+    return y
+
+
+def hadamard(n: int) -> torch.Tensor:
+    """The Sylvester-order Hadamard matrix of order n (a power of two), f64."""
+    h = torch.ones(1, 1, dtype=torch.float64)
+    while h.shape[0] < n:
+        h = torch.cat([torch.cat([h, h], 1), torch.cat([h, -h], 1)], 0)
+    return h
+
+
+def fwht128(x: torch.Tensor) -> torch.Tensor:
+    """The orthonormal 128-point Hadamard transform, Sylvester order (glm53/gfx950/
+    kernel.py:778-788), of the last dim, in f64 (returned f32)."""
+    return (x.double() @ hadamard(128) * 128 ** -0.5).float()
+
+
+def layernorm(x: torch.Tensor, g: torch.Tensor, b: torch.Tensor, eps: float) -> torch.Tensor:
+    """(x - mean) * rsqrt(var + eps) * g + b over the last dim, biased var, f32
+    (the index key's norm, glm53/gfx950/kernel.py:3116-3130)."""
+    x = x.float()
+    mean = x.mean(-1, keepdim=True)
+    var = (x - mean).pow(2).mean(-1, keepdim=True)
+    return (x - mean) * torch.rsqrt(var + eps) * g.float() + b.float()
+
+
+def front(x, w, positions, cos_sin, *, eps: float, index_eps: float, nope: int, heads: int,
+          index_heads: int, kv_lora: int = 512, rope: int = 64) -> dict:
+    """The layer's front on rows x (bf16 values) with dequantized f32 weights `w` (a
+    namespace: g_in, w_qkv_a, g_q_a, g_kv_a, w_q_b, w_uk, w_iq, w_ik, g_ik, b_ik, w_iw),
+    restating the reference's K1 (glm53/gfx950/kernel.py:2585-3575) and SGLang's
+    DeepSeek-V3.2 / GLM-5 attention front it follows.  Returns mla_q [rows, heads, 576],
+    index_q [rows, ih, 128], index_w [rows, ih] (bf16 values), the latent cache rows'
+    values before E4M3 [rows, 576] and the index keys before their quant [rows, 128]."""
+    rows = x.shape[0]
+    QL = w.w_q_b.shape[1]
+    xn = rmsnorm(x.float(), w.g_in, eps).double()
+    a = (xn @ w.w_qkv_a.double().t()).float()
+    q_a, kv_a, k_pe = a[:, :QL], a[:, QL:QL + kv_lora], a[:, QL + kv_lora:]
+    q_an = rmsnorm(q_a, w.g_q_a, eps)
+    half = rope // 2
+    cs = cos_sin[positions.long()].float()
+    cos, sin = cs[:, :half], cs[:, half:]
+    kv_row = torch.cat([rmsnorm(kv_a, w.g_kv_a, eps), codecs.bf16_round(rope_pairs(k_pe, cos, sin))], dim=1)
+    q_b = (q_an.double() @ w.w_q_b.double().t()).float().view(rows, heads, nope + rope)
+    q_nope = codecs.bf16_round(q_b[..., :nope])
+    q_pe = codecs.bf16_round(rope_pairs(q_b[..., nope:], cos[:, None], sin[:, None]))
+    q_lat = torch.einsum("hcn,rhn->rhc", w.w_uk.double(), q_nope.double())
+    mla_q = torch.cat([codecs.bf16_round(q_lat.float()), q_pe], dim=-1)
+    out = {"mla_q": mla_q, "kv_row": kv_row, "q_an": q_an}
+    if index_heads:
+        ik = (xn @ w.w_ik.double().t()).float()
+        k = layernorm(ik, w.g_ik, w.b_ik, index_eps)
+        k = torch.cat([rope_pairs(k[:, :64], cos[:, :32], sin[:, :32]), k[:, 64:]], dim=1)
+        out["index_key"] = fwht128(k)
+        out["index_w"] = codecs.bf16_round((xn @ w.w_iw.double().t()).float())
+        iq = codecs.bf16_round((q_an.double() @ w.w_iq.double().t()).float()).view(rows, index_heads, 128)
+        iq = torch.cat([rope_pairs(iq[..., :64], cos[:, None, :32], sin[:, None, :32]), iq[..., 64:]], dim=-1)
+        out["index_q"] = codecs.bf16_round(fwht128(iq))
+    return out
 
 
 # -------------------------------------------------------------------- step tables

@@ -1,0 +1,640 @@
+// The layer's front (the reference's K1): from the residual rows h to what the K2 layer
+// takes -- the absorbed MLA queries, the index queries and head weights -- and this
+// step's rows of the latent-KV and index caches.  Reference: glm53/gfx950/kernel.py:
+// 2585-3575 (the front stages of its fused launch); the arithmetic is SGLang's
+// DeepSeek-V3.2 / GLM-5 attention front (DeepseekV2AttentionMLA with the DSA indexer),
+// which the reference's check runs as its truth (glm53/check.py:200-272):
+//
+//   x_n  = bf16(rmsnorm(h) * g_in)
+//   [q_a | kv_a | k_pe] = W_qkv_a x_n,  ik = W_ik x_n,  iw = W_iw x_n        (f32)
+//   q_an = bf16(rmsnorm(q_a) * g_q_a)
+//   latent cache row = e4m3(bf16(rmsnorm(kv_a) * g_kv_a)) | e4m3(bf16(rope(k_pe)))
+//   index cache row  = quant(fwht(rope64(layernorm(ik) * g_ik + b_ik)))
+//   q_b  = W_q_b q_an: per head q_nope | q_pe;  iq = W_iq q_an                 (f32)
+//   mla_q[h]   = bf16(W_UK[h] . bf16(q_nope[h])) | bf16(rope(q_pe[h]))
+//   index_q[h] = bf16(fwht(rope64(bf16(iq[h])))),  index_w = bf16(iw)
+//
+// rope: interleaved pairs (2i, 2i + 1) rotated by the position's angle i (cos/sin from
+// SGLang's cos_sin_cache [positions][rope]: cos in the first half, sin in the second;
+// kernel.py:3107-3131,3245-3251); rope64: the same on the first 64 dims; fwht: the
+// orthonormal 128-point Hadamard transform in Sylvester order (kernel.py:778-788);
+// the index key's quant is its cache's (the FP8 pages' ue8m0 rule, kernel.py:
+// 3134-3147, or the FP4 plane's MXFP4).
+//
+// Four launches in stream order:
+//   1. k_gemv over [W_qkv_a | W_ik], then over W_iw (bf16): the hidden-input GEMVs;
+//   2. k_front_rows, one workgroup a row: the norms, RoPE, the index key, the cache
+//      writes and the head weights;
+//   3. k_gemv over [W_q_b | W_iq] from q_an;
+//   4. k_front_heads: W_UK absorption on MFMA and the index queries' RoPE + Hadamard.
+// The GEMV engine is HBM-bound: each workgroup takes a contiguous range of 16-row
+// tiles and each wave a k slice; the input rows are register-resident MFMA operands;
+// FP8 weights (SGLang's row-major E4M3 with 128 x 128 f32 block scales, read in place)
+// widen exactly to bf16 and each 128-k block's partial sum takes its block scale.
+#include "mk2_device.h"
+#include "mk2_host.h"
+
+namespace mk2 {
+
+constexpr int GV_NT = 512;
+constexpr int GV_WAVES = GV_NT / 64;
+constexpr int GV_CHUNK = 8;  // tiles whose partials wait in LDS for one barrier
+constexpr int FR_NT = 512;
+
+struct GemvSeg {
+  const void* w;   // [rows][K] bf16 or E4M3, row-major
+  const float* s;  // E4M3: f32 [rows / 128][K / 128] block scales
+  float* out;      // f32 [M][ld]
+  int rows;        // multiple of 16
+  int ld;
+};
+
+struct GemvDev {
+  int M;  // rows this pass, 1..16
+  int K;
+  float eps;
+  const bf16_t* x;  // [M][K]: raw rows (with g) or the GEMV input as it is (g null)
+  const bf16_t* g;  // RMSNorm weight [K], or null
+  GemvSeg seg[2];
+  int nseg;
+  int tiles0;  // 16-row tiles of segment 0
+  int ntiles;
+};
+
+// KU: 64-k units a wave (K = 8 * 64 * KU); F8: E4M3 weights
+template <int KU, bool F8>
+__global__ __launch_bounds__(GV_NT) void k_gemv(GemvDev p) {
+  constexpr int L = F8 ? KU : 2 * KU;      // 16-byte weight loads a lane a tile
+  constexpr int WIN = L <= 24 ? L : L / 2;  // loads in flight a lane
+  static_assert(L % WIN == 0, "a window divides the loads of a tile");
+  static_assert(!F8 || KU % 2 == 0, "FP8 slices are whole 128-k blocks");
+  __shared__ float part[GV_WAVES][16];
+  __shared__ uint4 gam[8192 / 8];
+  __shared__ float red[GV_CHUNK][GV_WAVES][256];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, c16 = lane & 15, g = lane >> 4;
+  const int K = p.K, G = gridDim.x, b = blockIdx.x, M = p.M;
+  const int t0 = (int)((long long)b * p.ntiles / G), t1 = (int)((long long)(b + 1) * p.ntiles / G);
+  // k map: unit u of the wave's slice holds k = kw + 64 u + 0 .. 15 for lane group g;
+  // MFMA step 2u takes its first 8, step 2u + 1 the next 8 (A and B alike)
+  const int kw = wave * KU * 64 + 16 * g;
+  // the rows: this lane's fragments of row c16 (16 k a unit)
+  const bool live = c16 < M;
+  const bf16_t* xr = p.x + (size_t)(live ? c16 : 0) * K + kw;
+  uint4 xq[2 * KU];
+#pragma unroll
+  for (int u = 0; u < KU; ++u) {
+    xq[2 * u] = *(const uint4*)(xr + 64 * u);
+    xq[2 * u + 1] = *(const uint4*)(xr + 64 * u + 8);
+  }
+  uint4 gq[2];
+  if (p.g) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int j = threadIdx.x + i * GV_NT;
+      gq[i] = j < K / 8 ? ((const uint4*)p.g)[j] : make_uint4(0, 0, 0, 0);
+    }
+  }
+  // the tile sequence: tile t of segment sid at row (t - base) * 16; this lane's row
+  auto seg_of = [&](int t) { return t < p.tiles0 ? 0 : 1; };
+  auto w_row = [&](int t) -> const uint8_t* {
+    const int sid = seg_of(t);
+    const int row = (t - (sid ? p.tiles0 : 0)) * 16 + c16;
+    return (const uint8_t*)p.seg[sid].w + ((size_t)row * K + kw) * (F8 ? 1 : 2);
+  };
+  // a lane's load j of a tile: F8 unit j (16 E4M3); bf16 unit j / 2, half j % 2
+  auto w_off = [&](int j) { return F8 ? 64 * j : 128 * (j >> 1) + 16 * (j & 1); };
+  const uint8_t* wrow = w_row(t0 < t1 ? t0 : 0);
+  uint4 wv[WIN];
+  if (t0 < t1) {
+#pragma unroll
+    for (int j = 0; j < WIN; ++j) wv[j] = ld_stream16(wrow + w_off(j));
+  }
+  // the norm: sums of squares of the lane's fragments, the 4 lanes of the row, then
+  // the 8 waves' slices in wave order
+  float rs = 1.f;
+  if (p.g) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 2 * KU; ++i) {
+      const uint32_t u4[4] = {xq[i].x, xq[i].y, xq[i].z, xq[i].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bf16x2 v = __builtin_bit_cast(bf16x2, u4[j]);
+        ss = __builtin_amdgcn_fdot2_f32_bf16(v, v, ss, false);
+      }
+    }
+    ss += __shfl_xor(ss, 16);
+    ss += __shfl_xor(ss, 32);
+    if (g == 0) part[wave][c16] = ss;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int j = threadIdx.x + i * GV_NT;
+      if (j < K / 8) gam[j] = gq[i];
+    }
+    __syncthreads();
+    float tot = part[0][c16];
+#pragma unroll
+    for (int w = 1; w < GV_WAVES; ++w) tot += part[w][c16];
+    rs = 1.0f / sqrtf(tot / (float)K + p.eps);
+  }
+  // B operands: bf16(x * rstd * g), or x as it is; zero columns past the rows
+  bf16x8 bq[2 * KU];
+#pragma unroll
+  for (int i = 0; i < 2 * KU; ++i) {
+    uint4 ov = xq[i];
+    if (p.g) {
+      const uint4 gv = gam[(kw + 64 * (i >> 1) + 8 * (i & 1)) >> 3];
+      const uint32_t xu[4] = {xq[i].x, xq[i].y, xq[i].z, xq[i].w}, gu[4] = {gv.x, gv.y, gv.z, gv.w};
+      uint32_t o[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        o[j] = pack_bf16x2(__uint_as_float(xu[j] << 16) * rs * __uint_as_float(gu[j] << 16),
+                           __uint_as_float(xu[j] & 0xFFFF0000u) * rs * __uint_as_float(gu[j] & 0xFFFF0000u));
+      ov = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+    if (!live) ov = make_uint4(0, 0, 0, 0);
+    bq[i] = __builtin_bit_cast(bf16x8, ov);
+  }
+  // the tiles, in chunks of GV_CHUNK whose partials wait in LDS (no barrier a tile)
+  for (int c0 = t0; c0 < t1; c0 += GV_CHUNK) {
+#pragma unroll
+    for (int i = 0; i < GV_CHUNK; ++i) {
+      const int t = c0 + i;
+      if (t >= t1) break;
+      const bool more = t + 1 < t1;
+      const uint8_t* nrow = w_row(more ? t + 1 : t);
+      const int sid = seg_of(t);
+      const int row0 = (t - (sid ? p.tiles0 : 0)) * 16;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (F8) {
+        // the tile's block scales (one a 128-k block of the wave's slice; the tile's 16
+        // rows are in one 128-row block)
+        const float* sr = p.seg[sid].s + (size_t)(row0 >> 7) * (K >> 7) + (wave * KU * 64 >> 7);
+#pragma unroll
+        for (int kb = 0; kb < KU / 2; ++kb) {
+          f32x4 pa = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int j = 2 * kb + h;
+            const uint4 w = wv[j % WIN];
+            pa = mfma_bf16(e4m3x8_to_bf16(w.x, w.y), bq[2 * j], pa);
+            pa = mfma_bf16(e4m3x8_to_bf16(w.z, w.w), bq[2 * j + 1], pa);
+            const int nj = j + WIN;
+            if (nj < L)
+              wv[j % WIN] = ld_stream16(wrow + w_off(nj));
+            else if (more)
+              wv[j % WIN] = ld_stream16(nrow + w_off(nj - L));
+          }
+          const float sc = sr[kb];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[e] += pa[e] * sc;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < L; ++j) {
+          acc = mfma_bf16(__builtin_bit_cast(bf16x8, wv[j % WIN]), bq[j], acc);
+          const int nj = j + WIN;
+          if (nj < L)
+            wv[j % WIN] = ld_stream16(wrow + w_off(nj));
+          else if (more)
+            wv[j % WIN] = ld_stream16(nrow + w_off(nj - L));
+        }
+      }
+      // lane (c16, g) holds D[v = 4 g + e][m = c16]
+      float* rw = red[i][wave];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) rw[(4 * g + e) * 16 + c16] = acc[e];
+      wrow = nrow;
+    }
+    __syncthreads();
+    const int nt = min(GV_CHUNK, t1 - c0);
+    for (int e = threadIdx.x; e < nt * 256; e += GV_NT) {
+      const int i = e >> 8, m = (e >> 4) & 15, v = e & 15;
+      const int t = c0 + i, sid = seg_of(t);
+      const int row = (t - (sid ? p.tiles0 : 0)) * 16 + v;
+      float s = red[i][0][v * 16 + m];
+#pragma unroll
+      for (int w = 1; w < GV_WAVES; ++w) s += red[i][w][v * 16 + m];
+      if (m < M) p.seg[sid].out[(size_t)m * p.seg[sid].ld + row] = s;
+    }
+    __syncthreads();
+  }
+}
+
+template <int KU, bool F8>
+static void gemv_launch1(const GemvDev& d, int grid, hipStream_t st) {
+  k_gemv<KU, F8><<<grid, GV_NT, 0, st>>>(d);
+}
+
+template <bool F8>
+static int gemv_launch(const GemvDev& d, int grid, hipStream_t st) {
+  switch (d.K / 512) {
+    case 2: gemv_launch1<2, F8>(d, grid, st); break;
+    case 4: gemv_launch1<4, F8>(d, grid, st); break;
+    case 6: gemv_launch1<6, F8>(d, grid, st); break;
+    case 8: gemv_launch1<8, F8>(d, grid, st); break;
+    case 12: gemv_launch1<12, F8>(d, grid, st); break;
+    case 14: gemv_launch1<14, F8>(d, grid, st); break;
+    case 16: gemv_launch1<16, F8>(d, grid, st); break;
+    default: return set_error(MK2_EINVAL, "front: no GEMV engine for K = %d", d.K);
+  }
+  return MK2_OK;
+}
+
+// ------------------------------------------------------------------ per-row stage
+struct FrontDev {
+  int M, q_lora, kv_lora, rope, nope, heads, ih, max_position, key_fmt, kv_scaled;
+  float eps, index_eps;
+  const long long* positions;  // [M]
+  const long long* slots;      // [M], < 0: a pad row (no cache writes)
+  const float* rope_cs;        // [positions][rope]: cos | sin
+  // f32 GEMV outputs (workspace)
+  const float* qkv_a;  // [M][q_lora + kv_lora + rope]
+  const float* ik;     // [M][128]
+  const float* iw;     // [M][ih]
+  const float* q_b;    // [M][heads * (nope + rope)]
+  const float* iq;     // [M][ih * 128]
+  // weights
+  const bf16_t* g_q_a;
+  const bf16_t* g_kv_a;
+  const float* g_ik;
+  const float* b_ik;
+  const bf16_t* w_uk;  // [heads][kv_lora][nope] (SGLang's w_kc memory)
+  // outputs
+  bf16_t* q_an;           // [M][q_lora] (workspace)
+  uint8_t* kv;            // latent cache [slots][576]
+  float* kv_scale;        // [slots], or null (unscaled)
+  uint8_t* icache;        // index cache (FP8 pages, or the FP4 plane's codes)
+  uint8_t* iscale;        // FP4 plane scales, or null
+  bf16_t* mla_q;          // [M][heads][kv_lora + rope]
+  bf16_t* index_q;        // [M][ih][128]
+  bf16_t* index_w;        // [M][ih]
+};
+
+MK2_DEV float block_sum512(float v, float* sh) {  // all 512 threads; sh: 8 floats
+  v = wave_sum(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int w = 0; w < FR_NT / 64; ++w) t += sh[w];
+  return t;
+}
+
+// the orthonormal 128-point Hadamard transform (Sylvester order) of one wave's values,
+// lane l holding entries 2l and 2l + 1
+MK2_DEV void fwht128(float& v0, float& v1) {
+  const int lane = threadIdx.x & 63;
+  float a = v0 + v1, b = v0 - v1;
+#pragma unroll
+  for (int j = 0; j < 6; ++j) {
+    const int m = 1 << j;
+    const float pa = __shfl_xor(a, m), pb = __shfl_xor(b, m);
+    const bool up = (lane & m) != 0;
+    a = up ? pa - a : a + pa;
+    b = up ? pb - b : b + pb;
+  }
+  const float r = 0.08838834764831845f;  // 128^-1/2
+  v0 = a * r;
+  v1 = b * r;
+}
+
+// one row: q_a and kv_a norms, the latent cache row, the index key, the head weights
+__global__ __launch_bounds__(FR_NT) void k_front_rows(FrontDev p) {
+  __shared__ float sh[FR_NT / 64];
+  __shared__ float kvv[576];
+  const int s = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int NA = p.q_lora + p.kv_lora + p.rope;
+  const float* a = p.qkv_a + (size_t)s * NA;
+  const long long pos = p.positions[s] < p.max_position ? p.positions[s] : p.max_position;
+  const long long slot = p.slots[s];
+  const float* cs = p.rope_cs + (size_t)(pos < 0 ? 0 : pos) * p.rope;
+  // q_an = bf16(rmsnorm(q_a) * g)
+  {
+    float ss = 0.f;
+    for (int k = tid; k < p.q_lora; k += FR_NT) ss += a[k] * a[k];
+    const float rs = 1.0f / sqrtf(block_sum512(ss, sh) / (float)p.q_lora + p.eps);
+    for (int k = tid; k < p.q_lora; k += FR_NT)
+      p.q_an[(size_t)s * p.q_lora + k] = f32_to_bf16(a[k] * rs * bf16_to_f32(p.g_q_a[k]));
+  }
+  // the latent row: bf16(rmsnorm(kv_a) * g) | bf16(rope(k_pe)), then E4M3
+  {
+    const float* kva = a + p.q_lora;
+    float ss = 0.f;
+    for (int k = tid; k < p.kv_lora; k += FR_NT) ss += kva[k] * kva[k];
+    const float rs = 1.0f / sqrtf(block_sum512(ss, sh) / (float)p.kv_lora + p.eps);
+    for (int k = tid; k < p.kv_lora; k += FR_NT)
+      kvv[k] = bf16_to_f32(f32_to_bf16(kva[k] * rs * bf16_to_f32(p.g_kv_a[k])));
+    const float* pe = kva + p.kv_lora;
+    for (int i = tid; i < p.rope / 2; i += FR_NT) {
+      const float x0 = pe[2 * i], x1 = pe[2 * i + 1], c = cs[i], sn = cs[p.rope / 2 + i];
+      kvv[p.kv_lora + 2 * i] = bf16_to_f32(f32_to_bf16(x0 * c - x1 * sn));
+      kvv[p.kv_lora + 2 * i + 1] = bf16_to_f32(f32_to_bf16(x0 * sn + x1 * c));
+    }
+    __syncthreads();
+    const int D = p.kv_lora + p.rope;
+    float scale = 1.f;
+    if (p.kv_scaled) {
+      float am = 0.f;
+      for (int k = tid; k < D; k += FR_NT) am = fmaxf(am, fabsf(kvv[k]));
+      am = wave_max(am);
+      __syncthreads();
+      if (lane == 0) sh[wave] = am;
+      __syncthreads();
+      am = sh[0];
+#pragma unroll
+      for (int w = 1; w < FR_NT / 64; ++w) am = fmaxf(am, sh[w]);
+      scale = am > 0.f ? am / 448.0f : 1.0f;
+    }
+    if (slot >= 0) {
+      uint8_t* row = p.kv + (size_t)slot * D;
+      for (int k = tid; k < D; k += FR_NT) {
+        const float v = p.kv_scaled ? kvv[k] / scale : kvv[k];
+        row[k] = (uint8_t)f32_to_e4m3(v);
+      }
+      if (p.kv_scaled && tid == 0) p.kv_scale[slot] = scale;
+    }
+  }
+  // the index key (wave 0): LayerNorm, RoPE on the first 64 dims, Hadamard, quant
+  if (p.ih > 0 && wave == 0) {
+    const float* k = p.ik + (size_t)s * 128;
+    float v0 = k[2 * lane], v1 = k[2 * lane + 1];
+    const float mean = wave_sum(v0 + v1) * (1.0f / 128);
+    const float d0 = v0 - mean, d1 = v1 - mean;
+    const float rstd = 1.0f / sqrtf(wave_sum(d0 * d0 + d1 * d1) * (1.0f / 128) + p.index_eps);
+    v0 = d0 * rstd * p.g_ik[2 * lane] + p.b_ik[2 * lane];
+    v1 = d1 * rstd * p.g_ik[2 * lane + 1] + p.b_ik[2 * lane + 1];
+    if (2 * lane < 64) {
+      const float c = cs[lane], sn = cs[p.rope / 2 + lane];
+      const float r0 = v0 * c - v1 * sn, r1 = v0 * sn + v1 * c;
+      v0 = r0;
+      v1 = r1;
+    }
+    fwht128(v0, v1);
+    if (slot >= 0) {
+      const long long page = slot >> 6;
+      const int t = (int)(slot & 63);
+      if (p.key_fmt == MK2_KEYS_FP8) {
+        // ue8m0: 2^ceil(log2(max(amax, 1e-4) / 448)), the values times its inverse
+        const float am = wave_max(fmaxf(fabsf(v0), fabsf(v1)));
+        const uint32_t bits = __float_as_uint(fmaxf(am, 1.0e-4f) / 448.0f);
+        const uint32_t e = ((bits >> 23) & 0xFF) + ((bits & 0x7FFFFF) != 0);
+        const float inv = __uint_as_float((254u - e) << 23);
+        uint8_t* pg = p.icache + (size_t)page * (64 * 132);
+        const int d = 2 * lane;  // dims d, d + 1: tile d / 16, byte d % 16
+        uint8_t* at = pg + (t >> 4) * 2048 + (d >> 4) * 256 + (t & 15) * 16 + (d & 15);
+        const uint32_t q = f32x4_to_e4m3x4(v0 * inv, v1 * inv, 0.f, 0.f);
+        at[0] = (uint8_t)(q & 0xFF);
+        at[1] = (uint8_t)((q >> 8) & 0xFF);
+        if (lane == 0) *(float*)(pg + 64 * 128 + 4 * t) = __uint_as_float(e << 23);
+      } else {
+        // MXFP4 per 32 dims (16 lanes): E8M0 = pow2_ceil(max(amax, 6 * 2^-126) / 6),
+        // E2M1 codes of v * 2^-e, two a byte (the even dim in the low nibble)
+        float am = fmaxf(fabsf(v0), fabsf(v1));
+#pragma unroll
+        for (int m = 1; m < 16; m <<= 1) am = fmaxf(am, __shfl_xor(am, m));
+        const uint32_t bits = __float_as_uint(fmaxf(am, 6.0f * 1.1754944e-38f) * (1.0f / 6.0f));
+        uint32_t e = ((bits >> 23) & 0xFF) + ((bits & 0x7FFFFF) != 0);
+        e = e > 254 ? 254 : e;
+        const uint32_t byte = f32x2_to_e2m1x2(v0, v1, e);
+        const int c = lane >> 4;  // the 32-dim chunk
+        uint8_t* codes = p.icache + (size_t)page * 4096 + c * 1024 + t * 16 + (lane & 15);
+        *codes = (uint8_t)byte;
+        if ((lane & 15) == 0) p.iscale[(size_t)page * 256 + c * 64 + (t & 15) * 4 + (t >> 4)] = (uint8_t)e;
+      }
+    }
+  }
+  // the head weights
+  for (int h = tid; h < p.ih; h += FR_NT) p.index_w[(size_t)s * p.ih + h] = f32_to_bf16(p.iw[(size_t)s * p.ih + h]);
+}
+
+// ---------------------------------------------------------------- per-head stage
+// Workgroups [0, heads): head h's absorbed queries for every row, 16 latent rows a
+// wave-tile on MFMA (A = W_UK[h] rows c, k = nope; B = bf16(q_nope) of the rows), and
+// its q_pe rotated; the rest: the index queries, one (row, index head) a wave.
+template <int NS>  // nope / 32 k-steps
+__global__ __launch_bounds__(FR_NT) void k_front_heads(FrontDev p) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c16 = lane & 15, g = lane >> 4;
+  const int QD = p.nope + p.rope, D = p.kv_lora + p.rope;
+  if ((int)blockIdx.x < p.heads) {
+    const int h = blockIdx.x;
+    const bf16_t* wk = p.w_uk + (size_t)h * p.kv_lora * p.nope;
+    for (int m0 = 0; m0 < p.M; m0 += 16) {
+      // B operands: bf16(q_nope[m0 + c16][h]) at k = 32 s + 8 g
+      bf16x8 bq[NS];
+      const int m = m0 + c16;
+      const bool live = m < p.M;
+      const float* qn = p.q_b + (size_t)(live ? m : 0) * p.heads * QD + (size_t)h * QD;
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        uint32_t o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int k = 32 * s + 8 * g + 2 * j;
+          o[j] = live ? pack_bf16x2(qn[k], qn[k + 1]) : 0u;
+        }
+        bq[s] = __builtin_bit_cast(bf16x8, make_uint4(o[0], o[1], o[2], o[3]));
+      }
+      for (int c0 = wave * 16; c0 < p.kv_lora; c0 += 16 * (FR_NT / 64)) {
+        const bf16_t* wr = wk + (size_t)(c0 + c16) * p.nope + 8 * g;
+        uint4 wv[NS];
+#pragma unroll
+        for (int s = 0; s < NS; ++s) wv[s] = *(const uint4*)(wr + 32 * s);
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < NS; ++s) acc = mfma_bf16(__builtin_bit_cast(bf16x8, wv[s]), bq[s], acc);
+        // lane (c16, g): latent rows c0 + 4 g + e of row m0 + c16
+        if (live) {
+          bf16_t* out = p.mla_q + ((size_t)m * p.heads + h) * D + c0 + 4 * g;
+          *(uint2*)out = make_uint2(pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]));
+        }
+      }
+    }
+    // q_pe rotated: pairs (2i, 2i + 1) of every row
+    for (int e = tid; e < p.M * (p.rope / 2); e += FR_NT) {
+      const int m = e / (p.rope / 2), i = e % (p.rope / 2);
+      const long long pos = p.positions[m] < p.max_position ? p.positions[m] : p.max_position;
+      const float* cs = p.rope_cs + (size_t)(pos < 0 ? 0 : pos) * p.rope;
+      const float* qp = p.q_b + (size_t)m * p.heads * QD + (size_t)h * QD + p.nope;
+      const float x0 = qp[2 * i], x1 = qp[2 * i + 1], c = cs[i], sn = cs[p.rope / 2 + i];
+      *(uint32_t*)(p.mla_q + ((size_t)m * p.heads + h) * D + p.kv_lora + 2 * i) =
+          pack_bf16x2(x0 * c - x1 * sn, x0 * sn + x1 * c);
+    }
+    return;
+  }
+  // index queries: wave task (row, index head)
+  const int task = ((int)blockIdx.x - p.heads) * (FR_NT / 64) + wave;
+  if (task >= p.M * p.ih) return;
+  const int m = task / p.ih, h = task % p.ih;
+  const float* q = p.iq + ((size_t)m * p.ih + h) * 128;
+  float v0 = bf16_to_f32(f32_to_bf16(q[2 * lane])), v1 = bf16_to_f32(f32_to_bf16(q[2 * lane + 1]));
+  if (2 * lane < 64) {
+    const long long pos = p.positions[m] < p.max_position ? p.positions[m] : p.max_position;
+    const float* cs = p.rope_cs + (size_t)(pos < 0 ? 0 : pos) * p.rope;
+    const float c = cs[lane], sn = cs[p.rope / 2 + lane];
+    const float r0 = v0 * c - v1 * sn, r1 = v0 * sn + v1 * c;
+    v0 = r0;
+    v1 = r1;
+  }
+  fwht128(v0, v1);
+  *(uint32_t*)(p.index_q + ((size_t)m * p.ih + h) * 128 + 2 * lane) = pack_bf16x2(v0, v1);
+}
+
+static int front_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cus[dev] == 0 && hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    cus[dev] = 0;
+  return cus[dev];
+}
+
+// workspace: f32 GEMV outputs and the normed q_a rows
+struct FrontWs {
+  float *qkv_a, *ik, *iw, *q_b, *iq;
+  bf16_t* q_an;
+};
+static size_t front_carve(const mk2_front_shape* s, void* base, FrontWs* w) {
+  Carver c(base);
+  const int M = s->rows;
+  float* qkv_a = c.take<float>((size_t)M * (s->q_lora + s->kv_lora + s->rope));
+  float* ik = c.take<float>((size_t)M * 128);
+  float* iw = c.take<float>((size_t)M * (s->index_heads > 0 ? s->index_heads : 1));
+  float* q_b = c.take<float>((size_t)M * s->heads * (s->nope + s->rope));
+  float* iq = c.take<float>((size_t)M * (s->index_heads > 0 ? s->index_heads : 1) * 128);
+  bf16_t* q_an = c.take<bf16_t>((size_t)M * s->q_lora);
+  if (w) *w = FrontWs{qkv_a, ik, iw, q_b, iq, q_an};
+  return c.bytes();
+}
+
+static int front_check_shape(const mk2_front_shape* s) {
+  MK2_REQUIRE(s != nullptr, "front: shape is NULL");
+  MK2_REQUIRE(s->rows >= 1 && s->rows <= 32, "front: rows must be in [1, 32], got %d", s->rows);
+  auto engine_k = [](int k) { return k == 1024 || k == 2048 || k == 3072 || k == 4096 || k == 6144 || k == 7168 || k == 8192; };
+  MK2_REQUIRE(engine_k(s->hidden), "front: hidden must be 1024, 2048, 3072, 4096, 6144, 7168 or 8192, got %d",
+              s->hidden);
+  MK2_REQUIRE(engine_k(s->q_lora), "front: q_lora must be 1024, 2048, 3072, 4096, 6144, 7168 or 8192, got %d",
+              s->q_lora);
+  MK2_REQUIRE(s->kv_lora == 512 && s->rope == 64, "front: kv_lora must be 512 and rope 64");
+  MK2_REQUIRE(s->nope == 128 || s->nope == 192 || s->nope == 256, "front: nope must be 128, 192 or 256, got %d",
+              s->nope);
+  MK2_REQUIRE(s->heads >= 1 && s->heads <= 128, "front: heads must be in [1, 128], got %d", s->heads);
+  MK2_REQUIRE(s->index_heads == 0 || (s->index_heads % 16 == 0 && s->index_heads <= 64),
+              "front: index_heads must be 0 or a multiple of 16 up to 64, got %d", s->index_heads);
+  MK2_REQUIRE(s->weight_fmt == MK2_WFMT_BF16 || s->weight_fmt == MK2_WFMT_FP8_BLOCK,
+              "front: weight_fmt must be MK2_WFMT_BF16 or MK2_WFMT_FP8_BLOCK, got %d", s->weight_fmt);
+  MK2_REQUIRE(s->key_fmt == MK2_KEYS_FP4 || s->key_fmt == MK2_KEYS_FP8, "front: key_fmt must be MK2_KEYS_*");
+  MK2_REQUIRE(s->max_position >= 0, "front: max_position must be >= 0");
+  MK2_REQUIRE(s->eps > 0.f && s->index_eps > 0.f, "front: eps and index_eps must be positive");
+  return MK2_OK;
+}
+
+}  // namespace mk2
+
+using namespace mk2;
+
+extern "C" int mk2_front_workspace_bytes(const mk2_front_shape* shape, size_t* bytes) {
+  clear_error();
+  int rc = front_check_shape(shape);
+  if (rc) return rc;
+  MK2_REQUIRE(bytes != nullptr, "front: bytes is NULL");
+  *bytes = front_carve(shape, nullptr, nullptr);
+  return MK2_OK;
+}
+
+extern "C" int mk2_front_launch(const mk2_front_args* a, mk2_stream_t stream) {
+  clear_error();
+  MK2_REQUIRE(a != nullptr, "front: args is NULL");
+  int rc = front_check_shape(&a->shape);
+  if (rc) return rc;
+  const mk2_front_shape& s = a->shape;
+  const mk2_front_weights& w = a->weights;
+  const bool f8 = s.weight_fmt == MK2_WFMT_FP8_BLOCK;
+  const bool idx = s.index_heads > 0;
+  MK2_REQUIRE(a->x && a->positions && a->slots && a->rope_cos_sin && a->kv_cache && a->mla_q,
+              "front: x, positions, slots, rope_cos_sin, kv_cache and mla_q must be set");
+  MK2_REQUIRE(w.g_in && w.w_qkv_a && w.g_q_a && w.g_kv_a && w.w_q_b && w.w_uk,
+              "front: g_in, w_qkv_a, g_q_a, g_kv_a, w_q_b and w_uk must be set");
+  MK2_REQUIRE(!f8 || (w.s_qkv_a && w.s_q_b), "front: FP8 weights need s_qkv_a and s_q_b");
+  MK2_REQUIRE(!(s.kv_scaled) || a->kv_scale, "front: a scaled latent cache needs kv_scale");
+  if (idx) {
+    MK2_REQUIRE(w.w_iq && w.w_ik && w.g_ik && w.b_ik && w.w_iw && a->index_cache && a->index_q && a->index_w,
+                "front: the indexer needs w_iq, w_ik, g_ik, b_ik, w_iw, index_cache, index_q and index_w");
+    MK2_REQUIRE(!f8 || (w.s_iq && w.s_ik), "front: FP8 weights need s_iq and s_ik");
+    MK2_REQUIRE(s.key_fmt == MK2_KEYS_FP8 || a->index_scale, "front: the FP4 index plane needs index_scale");
+  }
+  const size_t need = front_carve(&s, nullptr, nullptr);
+  MK2_REQUIRE(a->workspace != nullptr, "front: workspace is NULL");
+  if (a->workspace_bytes < need)
+    return set_error(MK2_ENOSPACE, "front: workspace has %zu bytes, needs %zu", a->workspace_bytes, need);
+  const int cus = front_cus();
+  if (cus <= 0) return set_error(MK2_ELAUNCH, "front: cannot query the CU count");
+  FrontWs ws;
+  front_carve(&s, a->workspace, &ws);
+  hipStream_t st = (hipStream_t)stream;
+  const int M = s.rows, NA = s.q_lora + s.kv_lora + s.rope, QB = s.heads * (s.nope + s.rope);
+  auto grid_of = [&](int tiles) { return tiles < cus ? tiles : cus; };
+  // 1. hidden-input GEMVs (passes of 16 rows)
+  for (int r0 = 0; r0 < M; r0 += 16) {
+    const int mp = M - r0 < 16 ? M - r0 : 16;
+    GemvDev d{};
+    d.M = mp; d.K = s.hidden; d.eps = s.eps;
+    d.x = (const bf16_t*)a->x + (size_t)r0 * s.hidden; d.g = (const bf16_t*)w.g_in;
+    d.seg[0] = GemvSeg{w.w_qkv_a, w.s_qkv_a, ws.qkv_a + (size_t)r0 * NA, NA, NA};
+    d.nseg = 1; d.tiles0 = NA / 16; d.ntiles = d.tiles0;
+    if (idx) {
+      d.seg[1] = GemvSeg{w.w_ik, w.s_ik, ws.ik + (size_t)r0 * 128, 128, 128};
+      d.nseg = 2; d.ntiles += 128 / 16;
+    }
+    rc = f8 ? gemv_launch<true>(d, grid_of(d.ntiles), st) : gemv_launch<false>(d, grid_of(d.ntiles), st);
+    if (rc) return rc;
+    if (idx) {  // the head weights are bf16 in every checkpoint format
+      GemvDev e = d;
+      e.seg[0] = GemvSeg{w.w_iw, nullptr, ws.iw + (size_t)r0 * s.index_heads, s.index_heads, s.index_heads};
+      e.nseg = 1; e.tiles0 = s.index_heads / 16; e.ntiles = e.tiles0;
+      rc = gemv_launch<false>(e, grid_of(e.ntiles), st);
+      if (rc) return rc;
+    }
+  }
+  // 2. per-row stage
+  FrontDev f{};
+  f.M = M; f.q_lora = s.q_lora; f.kv_lora = s.kv_lora; f.rope = s.rope; f.nope = s.nope; f.heads = s.heads;
+  f.ih = s.index_heads; f.max_position = s.max_position; f.key_fmt = s.key_fmt; f.kv_scaled = s.kv_scaled;
+  f.eps = s.eps; f.index_eps = s.index_eps;
+  f.positions = (const long long*)a->positions; f.slots = (const long long*)a->slots;
+  f.rope_cs = a->rope_cos_sin;
+  f.qkv_a = ws.qkv_a; f.ik = ws.ik; f.iw = ws.iw; f.q_b = ws.q_b; f.iq = ws.iq;
+  f.g_q_a = (const bf16_t*)w.g_q_a; f.g_kv_a = (const bf16_t*)w.g_kv_a; f.g_ik = w.g_ik; f.b_ik = w.b_ik;
+  f.w_uk = (const bf16_t*)w.w_uk;
+  f.q_an = ws.q_an; f.kv = (uint8_t*)a->kv_cache; f.kv_scale = a->kv_scale;
+  f.icache = (uint8_t*)a->index_cache; f.iscale = (uint8_t*)a->index_scale;
+  f.mla_q = (bf16_t*)a->mla_q; f.index_q = (bf16_t*)a->index_q; f.index_w = (bf16_t*)a->index_w;
+  k_front_rows<<<M, FR_NT, 0, st>>>(f);
+  rc = check_launch("front (rows)");
+  if (rc) return rc;
+  // 3. q_an-input GEMVs
+  for (int r0 = 0; r0 < M; r0 += 16) {
+    const int mp = M - r0 < 16 ? M - r0 : 16;
+    GemvDev d{};
+    d.M = mp; d.K = s.q_lora; d.eps = s.eps;
+    d.x = ws.q_an + (size_t)r0 * s.q_lora; d.g = nullptr;
+    d.seg[0] = GemvSeg{w.w_q_b, w.s_q_b, ws.q_b + (size_t)r0 * QB, QB, QB};
+    d.nseg = 1; d.tiles0 = QB / 16; d.ntiles = d.tiles0;
+    if (idx) {
+      d.seg[1] = GemvSeg{w.w_iq, w.s_iq, ws.iq + (size_t)r0 * s.index_heads * 128, s.index_heads * 128,
+                         s.index_heads * 128};
+      d.nseg = 2; d.ntiles += s.index_heads * 128 / 16;
+    }
+    rc = f8 ? gemv_launch<true>(d, grid_of(d.ntiles), st) : gemv_launch<false>(d, grid_of(d.ntiles), st);
+    if (rc) return rc;
+  }
+  // 4. per-head stage
+  const int grid = s.heads + (idx ? (M * s.index_heads + FR_NT / 64 - 1) / (FR_NT / 64) : 0);
+  switch (s.nope / 32) {
+    case 4: k_front_heads<4><<<grid, FR_NT, 0, st>>>(f); break;
+    case 6: k_front_heads<6><<<grid, FR_NT, 0, st>>>(f); break;
+    default: k_front_heads<8><<<grid, FR_NT, 0, st>>>(f); break;
+  }
+  return check_launch("front (heads)");
+}

@@ -137,6 +137,12 @@ MK2_DEV uint32_t f32x8_to_e2m1x8(const float* f, uint32_t code) {
   w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, f[6], f[7], sc, 3);
   return w;
 }
+// 2 f32 over the E8M0 scale `code` -> 2 E2M1 codes in the low byte (element 0 in the low
+// nibble), as f32x8_to_e2m1x8
+MK2_DEV uint32_t f32x2_to_e2m1x2(float a, float b, uint32_t code) {
+  const float sc = __uint_as_float(code ? code << 23 : 0x00400000u);
+  return __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(0u, a, b, sc, 0) & 0xFFu;
+}
 // FP8 per-128 block scale (the reference's quant_scaled): scale = amax * f32(1/448)
 // and the multiplier 448 / amax (IEEE here, where the reference takes the hardware
 // reciprocal); 1 and 1 for an all-zero block

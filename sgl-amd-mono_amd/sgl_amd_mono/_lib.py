@@ -99,6 +99,35 @@ class LayerArgs(ctypes.Structure):
     ]
 
 
+MK2_WFMT_BF16, MK2_WFMT_FP8_BLOCK = 0, 1
+
+
+class FrontShape(ctypes.Structure):
+    _fields_ = [
+        ("rows", c_int), ("hidden", c_int), ("q_lora", c_int), ("kv_lora", c_int), ("rope", c_int),
+        ("nope", c_int), ("heads", c_int), ("index_heads", c_int), ("weight_fmt", c_int), ("key_fmt", c_int),
+        ("kv_scaled", c_int), ("max_position", c_int), ("eps", c_float), ("index_eps", c_float),
+    ]
+
+
+class FrontWeights(ctypes.Structure):
+    _fields_ = [
+        ("g_in", c_void_p), ("w_qkv_a", c_void_p), ("s_qkv_a", c_void_p), ("g_q_a", c_void_p),
+        ("g_kv_a", c_void_p), ("w_q_b", c_void_p), ("s_q_b", c_void_p), ("w_uk", c_void_p),
+        ("w_iq", c_void_p), ("s_iq", c_void_p), ("w_ik", c_void_p), ("s_ik", c_void_p),
+        ("g_ik", c_void_p), ("b_ik", c_void_p), ("w_iw", c_void_p),
+    ]
+
+
+class FrontArgs(ctypes.Structure):
+    _fields_ = [
+        ("shape", FrontShape), ("weights", FrontWeights), ("x", c_void_p), ("positions", c_void_p),
+        ("slots", c_void_p), ("rope_cos_sin", c_void_p), ("kv_cache", c_void_p), ("kv_scale", c_void_p),
+        ("index_cache", c_void_p), ("index_scale", c_void_p), ("mla_q", c_void_p), ("index_q", c_void_p),
+        ("index_w", c_void_p), ("workspace", c_void_p), ("workspace_bytes", c_size_t),
+    ]
+
+
 class TailArgs(ctypes.Structure):
     _fields_ = [
         ("rows", c_int), ("hidden", c_int), ("vocab_rows", c_int), ("eps", c_float),
@@ -131,6 +160,8 @@ SIGNATURES = {
     "mk2_layer_launch": [POINTER(LayerArgs), c_void_p],
     "mk2_layer_launch_static": [POINTER(LayerArgs), c_void_p],
     "mk2_tail_launch": [POINTER(TailArgs), c_void_p],
+    "mk2_front_workspace_bytes": [POINTER(FrontShape), POINTER(c_size_t)],
+    "mk2_front_launch": [POINTER(FrontArgs), c_void_p],
     "mk2_step_rows_launch": [POINTER(StepArgs), c_void_p],
     "mk2_write_seed_launch": [c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int, c_int, c_void_p],
     "mk2_abi_version": [],

@@ -142,6 +142,51 @@ class K2Config:
             raise ValueError("the indexer and the attention share one context")
 
 
+WFMT_BF16 = 0  # attention weights as loaded in bf16
+WFMT_FP8_BLOCK = 1  # E4M3 with f32 128 x 128 block scales
+_ENGINE_K = (1024, 2048, 3072, 4096, 6144, 7168, 8192)
+
+
+@dataclass(frozen=True)
+class FrontConfig:
+    """The layer's front (the reference's K1) on one GPU's heads."""
+
+    hidden: int = 6144
+    q_lora: int = 2048
+    kv_lora: int = 512
+    rope: int = 64
+    nope: int = 192
+    heads: int = 16
+    index_heads: int = 64  # 0: no indexer
+    weight_fmt: int = WFMT_FP8_BLOCK
+    keys: int = KEYS_FP4
+    kv_scaled: bool = True
+    max_position: int = 65535
+    eps: float = 1e-6
+    index_eps: float = 1e-6
+
+    def validate(self, rows: int) -> None:
+        """The rules of the C side (mk2_front_workspace_bytes)."""
+        if not 1 <= rows <= MAX_ROWS:
+            raise ValueError(f"rows must be in [1, {MAX_ROWS}], got {rows}")
+        if self.hidden not in _ENGINE_K or self.q_lora not in _ENGINE_K:
+            raise ValueError(f"hidden and q_lora must be among {_ENGINE_K}")
+        if self.kv_lora != 512 or self.rope != 64:
+            raise ValueError("kv_lora must be 512 and rope 64")
+        if self.nope not in (128, 192, 256):
+            raise ValueError("nope must be 128, 192 or 256")
+        if not 1 <= self.heads <= 128:
+            raise ValueError("heads must be in [1, 128]")
+        if self.index_heads and (self.index_heads % 16 or self.index_heads > 64):
+            raise ValueError("index_heads must be 0 or a multiple of 16 up to 64")
+        if self.weight_fmt not in (WFMT_BF16, WFMT_FP8_BLOCK):
+            raise ValueError(f"unknown weight format {self.weight_fmt}")
+        if self.keys not in (KEYS_FP4, KEYS_FP8):
+            raise ValueError(f"unknown index cache format {self.keys}")
+        if self.max_position < 0 or not (self.eps > 0 and self.index_eps > 0):
+            raise ValueError("max_position must be >= 0 and the eps positive")
+
+
 @dataclass(frozen=True)
 class TailConfig:
     """The tail after the last layer: final RMSNorm, then this GPU's LM-head rows."""
@@ -182,3 +227,5 @@ C5_LAYER = K2Config(
 )
 # the tail after the layer stack (one GPU's share of the LM head)
 C6_TAIL = TailConfig()
+# the layer's front ahead of configs[4] (GLM-5 geometry on one GPU's 16 heads)
+C7_FRONT = FrontConfig()

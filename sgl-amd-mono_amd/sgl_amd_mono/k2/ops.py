@@ -112,6 +112,62 @@ class IndexerOp:
         return scores, topk
 
 
+class FrontOp:
+    """The layer's front (the reference's K1): residual rows in; the absorbed MLA
+    queries, index queries and head weights out, and this step's cache rows written.
+    `w` holds SGLang's tensors as loaded (see sgl_amd_mono.k2.synth.make_front)."""
+
+    def __init__(self, cfg: C.FrontConfig, w, rows: int, device=None):
+        cfg.validate(rows)
+        self.cfg, self.w, self.rows = cfg, w, rows
+        self.device = torch.device(device or w.w_qkv_a.device)
+        self.shape = _lib.FrontShape(rows, cfg.hidden, cfg.q_lora, cfg.kv_lora, cfg.rope, cfg.nope, cfg.heads,
+                                     cfg.index_heads, cfg.weight_fmt, cfg.keys, int(cfg.kv_scaled),
+                                     cfg.max_position, cfg.eps, cfg.index_eps)
+        wdt = torch.uint8 if cfg.weight_fmt == C.WFMT_FP8_BLOCK else torch.bfloat16
+        NA = cfg.q_lora + cfg.kv_lora + cfg.rope
+        _need(w.g_in, "g_in", torch.bfloat16, (cfg.hidden,))
+        _need(w.w_qkv_a, "w_qkv_a", wdt, (NA, cfg.hidden))
+        _need(w.w_q_b, "w_q_b", wdt, (cfg.heads * (cfg.nope + cfg.rope), cfg.q_lora))
+        _need(w.w_uk, "w_uk", torch.bfloat16, (cfg.heads, cfg.kv_lora, cfg.nope))
+        if cfg.index_heads:
+            _need(w.w_iq, "w_iq", wdt, (cfg.index_heads * 128, cfg.q_lora))
+            _need(w.w_ik, "w_ik", wdt, (128, cfg.hidden))
+            _need(w.w_iw, "w_iw", torch.bfloat16, (cfg.index_heads, cfg.hidden))
+            _need(w.g_ik, "g_ik", torch.float32, (128,))
+            _need(w.b_ik, "b_ik", torch.float32, (128,))
+        g = lambda n: getattr(w, n, None)  # noqa: E731
+        self.weights = _lib.FrontWeights(
+            _p(w.g_in), _p(w.w_qkv_a), _p(g("s_qkv_a")), _p(w.g_q_a), _p(w.g_kv_a), _p(w.w_q_b), _p(g("s_q_b")),
+            _p(w.w_uk), _p(g("w_iq")), _p(g("s_iq")), _p(g("w_ik")), _p(g("s_ik")), _p(g("g_ik")), _p(g("b_ik")),
+            _p(g("w_iw")),
+        )
+        nbytes = ctypes.c_size_t()
+        _lib.check(_lib.lib().mk2_front_workspace_bytes(ctypes.byref(self.shape), ctypes.byref(nbytes)))
+        self.workspace = torch.empty(nbytes.value, dtype=torch.uint8, device=self.device)
+
+    def __call__(self, x, positions, slots, rope_cos_sin, kv_cache, kv_scale, index_cache, index_scale,
+                 mla_q=None, index_q=None, index_w=None):
+        cfg, rows, dev = self.cfg, self.rows, self.device
+        _need(x, "x", torch.bfloat16, (rows, cfg.hidden))
+        _need(positions, "positions", torch.int64, (rows,))
+        _need(slots, "slots", torch.int64, (rows,))
+        _need(rope_cos_sin, "rope_cos_sin", torch.float32, (cfg.max_position + 1, cfg.rope))
+        _need(kv_cache, "kv_cache", torch.uint8)
+        if mla_q is None:
+            mla_q = torch.empty(rows, cfg.heads, cfg.kv_lora + cfg.rope, dtype=torch.bfloat16, device=dev)
+        ih = cfg.index_heads
+        if ih and index_q is None:
+            index_q = torch.empty(rows, ih, 128, dtype=torch.bfloat16, device=dev)
+        if ih and index_w is None:
+            index_w = torch.empty(rows, ih, dtype=torch.bfloat16, device=dev)
+        a = _lib.FrontArgs(self.shape, self.weights, _p(x), _p(positions), _p(slots), _p(rope_cos_sin),
+                           _p(kv_cache), _p(kv_scale), _p(index_cache), _p(index_scale), _p(mla_q), _p(index_q),
+                           _p(index_w), _p(self.workspace), self.workspace.numel())
+        _lib.check(_lib.lib().mk2_front_launch(ctypes.byref(a), _lib.stream_handle(dev)))
+        return mla_q, index_q, index_w
+
+
 class TailOp:
     """The tail after the last layer: the final RMSNorm of the rows and this GPU's rows
     of the LM head, read in place from SGLang's bf16 [vocab_rows, hidden]."""

@@ -163,6 +163,58 @@ def make_mla(cfg: C.MlaConfig, rows: int, seed: int, device, residual: bool = Tr
     return ns
 
 
+def rope_cos_sin(max_position: int, rope: int, device, theta: float = 10000.0) -> torch.Tensor:
+    """SGLang's cos_sin_cache layout, f32 [max_position + 1][rope]: cos of position * f_i
+    in the first half, sin in the second, f_i = theta^(-2i / rope)."""
+    inv = theta ** (-torch.arange(0, rope, 2, dtype=torch.float64) / rope)
+    ang = torch.arange(max_position + 1, dtype=torch.float64)[:, None] * inv[None, :]
+    return torch.cat([ang.cos(), ang.sin()], dim=1).float().to(device).contiguous()
+
+
+def _front_weight(g, rows, cols, fmt, device, std=WEIGHT_STD):
+    w = _randn(g, rows, cols, device=device, std=std)
+    if fmt == C.WFMT_FP8_BLOCK:
+        return quant_fp8_block(w)
+    return w.to(torch.bfloat16).contiguous(), None
+
+
+def make_front(cfg: C.FrontConfig, rows: int, seed: int, device, n_pages: int = 64):
+    """The front's weights in SGLang's formats (row-major bf16 or E4M3 + 128 x 128 f32
+    block scales, w_kc as [heads][kv_lora][nope]), residual rows x ~ N(0, 1), distinct
+    cache slots in n_pages 64-token pages, random positions, and empty caches of both
+    the latent rows and the configured index format."""
+    g = _gen(seed, device)
+    ns = SimpleNamespace(cfg=cfg, rows=rows)
+    H, QL, NA = cfg.hidden, cfg.q_lora, cfg.q_lora + cfg.kv_lora + cfg.rope
+    ns.x = _randn(g, rows, H, device=device).to(torch.bfloat16)
+    norm = lambda n: (1.0 + _randn(g, n, device=device, std=0.1)).to(torch.bfloat16)  # noqa: E731
+    ns.g_in, ns.g_q_a, ns.g_kv_a = norm(H), norm(QL), norm(cfg.kv_lora)
+    ns.w_qkv_a, ns.s_qkv_a = _front_weight(g, NA, H, cfg.weight_fmt, device)
+    ns.w_q_b, ns.s_q_b = _front_weight(g, cfg.heads * (cfg.nope + cfg.rope), QL, cfg.weight_fmt, device)
+    ns.w_uk = _randn(g, cfg.heads, cfg.kv_lora, cfg.nope, device=device, std=0.05).to(torch.bfloat16)
+    ih = cfg.index_heads
+    if ih:
+        ns.w_iq, ns.s_iq = _front_weight(g, ih * 128, QL, cfg.weight_fmt, device)
+        ns.w_ik, ns.s_ik = _front_weight(g, 128, H, cfg.weight_fmt, device)
+        ns.g_ik = 1.0 + _randn(g, 128, device=device, std=0.1)
+        ns.b_ik = _randn(g, 128, device=device, std=0.1)
+        ns.w_iw = _randn(g, ih, H, device=device, std=WEIGHT_STD).to(torch.bfloat16)
+    else:
+        ns.w_iq = ns.s_iq = ns.w_ik = ns.s_ik = ns.g_ik = ns.b_ik = ns.w_iw = None
+    ns.rope_cos_sin = rope_cos_sin(cfg.max_position, cfg.rope, device)
+    ns.positions = torch.randint(0, cfg.max_position + 1, (rows,), generator=g, device=device).to(torch.int64)
+    ns.slots = torch.randperm(n_pages * C.PAGE, generator=g, device=device)[:rows].to(torch.int64)
+    ns.kv_cache = torch.zeros(n_pages * C.PAGE, cfg.kv_lora + cfg.rope, dtype=torch.uint8, device=device)
+    ns.kv_scale = torch.zeros(n_pages * C.PAGE, dtype=torch.float32, device=device) if cfg.kv_scaled else None
+    if cfg.keys == C.KEYS_FP8:
+        ns.index_cache = torch.zeros(n_pages, C.PAGE, 132, dtype=torch.uint8, device=device)
+        ns.index_scale = None
+    else:
+        ns.index_cache = torch.zeros(n_pages, 4096, dtype=torch.uint8, device=device)
+        ns.index_scale = torch.zeros(n_pages, 256, dtype=torch.uint8, device=device)
+    return ns
+
+
 def make_tail(cfg: C.TailConfig, rows: int, seed: int, device):
     """The last layer's rows x ~ N(0, 1) (bf16), the final norm's weight 1 + N(0,
     0.1^2) and LM-head rows ~ N(0, 1/hidden) in SGLang's bf16 [vocab_rows, hidden]."""

@@ -43,10 +43,10 @@ def test_ctypes_layouts_match_the_header():
 #include <stddef.h>
 #include "mk2.h"
 int main(void) {
-  printf("%zu %zu %zu %zu %zu %zu %zu %zu %zu %zu\n", sizeof(mk2_moe_shape), sizeof(mk2_moe_weights),
+  printf("%zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu\n", sizeof(mk2_moe_shape), sizeof(mk2_moe_weights),
          sizeof(mk2_moe_args), sizeof(mk2_indexer_shape), sizeof(mk2_indexer_args),
          sizeof(mk2_mla_shape), sizeof(mk2_mla_args), sizeof(mk2_layer_args), sizeof(mk2_tail_args),
-         sizeof(mk2_step_args));
+         sizeof(mk2_step_args), sizeof(mk2_front_shape), sizeof(mk2_front_weights), sizeof(mk2_front_args));
   printf("%zu %zu %zu %zu %zu %zu %zu\n", offsetof(mk2_moe_args, logits), offsetof(mk2_mla_args, o_latent),
          offsetof(mk2_layer_args, workspace_bytes), offsetof(mk2_indexer_shape, key_fmt),
          offsetof(mk2_tail_args, normed), offsetof(mk2_step_args, ids_in_bytes), offsetof(mk2_step_args, ctx_len));
@@ -62,7 +62,7 @@ int main(void) {
     offs = [int(x) for x in out[1].split()]
     mine = [ctypes.sizeof(t) for t in (_l.MoeShape, _l.MoeWeights, _l.MoeArgs, _l.IndexerShape,
                                        _l.IndexerArgs, _l.MlaShape, _l.MlaArgs, _l.LayerArgs, _l.TailArgs,
-                                       _l.StepArgs)]
+                                       _l.StepArgs, _l.FrontShape, _l.FrontWeights, _l.FrontArgs)]
     assert sizes == mine
     assert offs == [_l.MoeArgs.logits.offset, _l.MlaArgs.o_latent.offset,
                     _l.LayerArgs.workspace_bytes.offset, _l.IndexerShape.key_fmt.offset,
@@ -127,6 +127,13 @@ def test_launch_argument_errors_never_reach_the_device():
     sa = _l.StepArgs(width=4, rows=5, topk=2048)
     assert L.mk2_step_rows_launch(ctypes.byref(sa), None) == _l.MK2_EINVAL
     assert L.mk2_write_seed_launch(None, None, None, 0, None, 1, 2048, None) == _l.MK2_EINVAL
+    assert L.mk2_front_launch(None, None) == _l.MK2_EINVAL
+    fs = _l.FrontShape(8, 6144, 2048, 512, 64, 160, 16, 64, 1, 0, 1, 65535, 1e-6, 1e-6)
+    n = ctypes.c_size_t()
+    assert L.mk2_front_workspace_bytes(ctypes.byref(fs), ctypes.byref(n)) == _l.MK2_EINVAL
+    assert "nope" in L.mk2_last_error().decode()
+    fs.nope = 192
+    assert L.mk2_front_workspace_bytes(ctypes.byref(fs), ctypes.byref(n)) == _l.MK2_OK and n.value > 0
     assert L.mk2_tail_launch(None, None) == _l.MK2_EINVAL
     ta = _l.TailArgs(8, 6144, 0, 1e-5, fake, fake, fake, fake, None)
     assert L.mk2_tail_launch(ctypes.byref(ta), None) == _l.MK2_EINVAL

@@ -117,3 +117,23 @@ def test_tail_validate_matches_c():
         assert py == c, (cfg, rows, py, rc, L.mk2_last_error())
         seen[py] += 1
     assert seen[True] and seen[False]
+
+
+def test_front_validate_matches_c():
+    """FrontConfig.validate() against mk2_front_workspace_bytes over a grid of shapes."""
+    from dataclasses import replace as rep
+
+    _l, L = _lib()
+    seen = {True: 0, False: 0}
+    for hidden, q_lora, nope, ih, rows, fmt in itertools.product(
+        (1024, 1536, 6144, 7168, 9216), (1536, 2048), (128, 160, 192), (0, 16, 48, 80), (1, 32, 33), (0, 1, 2),
+    ):
+        cfg = rep(C.C7_FRONT, hidden=hidden, q_lora=q_lora, nope=nope, index_heads=ih, weight_fmt=fmt)
+        s = _l.FrontShape(rows, cfg.hidden, cfg.q_lora, cfg.kv_lora, cfg.rope, cfg.nope, cfg.heads, cfg.index_heads,
+                          cfg.weight_fmt, cfg.keys, int(cfg.kv_scaled), cfg.max_position, cfg.eps, cfg.index_eps)
+        n = ctypes.c_size_t()
+        c = L.mk2_front_workspace_bytes(ctypes.byref(s), ctypes.byref(n)) == 0
+        py = _py_ok(cfg, rows)
+        assert py == c, (cfg, rows, py, c, L.mk2_last_error())
+        seen[py] += 1
+    assert seen[True] and seen[False]

@@ -261,8 +261,8 @@ int mk2_layer_launch_static(const mk2_layer_args* args, mk2_stream_t stream);
  * E4M3, MK2_KEYS_FP4: MXFP4).  Weights are SGLang's as loaded, row-major, read in
  * place: bf16, or E4M3 with f32 128 x 128 block scales [ceil(rows/128)][K/128]
  * (W_iw is bf16 in both).  W_UK is SGLang's w_kc, bf16 [heads][kv_lora][nope] in
- * memory.  A row with slot < 0 (a pad row) writes no cache rows.  Four launches in
- * stream order; the workspace holds the f32 GEMV outputs. */
+ * memory.  A row with slot < 0 (a pad row) writes no cache rows.  Six launches in
+ * stream order; the workspace holds the normed rows and the f32 GEMV outputs. */
 #define MK2_WFMT_BF16 0
 #define MK2_WFMT_FP8_BLOCK 1
 

@@ -21,14 +21,17 @@
 // the index key's quant is its cache's (the FP8 pages' ue8m0 rule, kernel.py:
 // 3134-3147, or the FP4 plane's MXFP4).
 //
-// Four launches in stream order:
+// Launches in stream order:
+//   0. k_front_norm, one workgroup a row: x_n;
 //   1. k_gemv over [W_qkv_a | W_ik], then over W_iw (bf16): the hidden-input GEMVs;
-//   2. k_front_rows, one workgroup a row: the norms, RoPE, the index key, the cache
-//      writes and the head weights;
+//   2. k_front_rows, three workgroups a row: the q_a norm; the latent cache row (kv_a
+//      norm, RoPE); the index key and the head weights;
 //   3. k_gemv over [W_q_b | W_iq] from q_an;
 //   4. k_front_heads: W_UK absorption on MFMA and the index queries' RoPE + Hadamard.
-// The GEMV engine is HBM-bound: each workgroup takes a contiguous range of 16-row
-// tiles and each wave a k slice; the input rows are register-resident MFMA operands;
+// The GEMV engine is HBM-bound: each workgroup takes one K part (several when the
+// tiles are fewer than the CUs; their f32 partial planes are summed in part order by
+// the next stage) and a contiguous range of 16-row tiles, and each wave a k slice; the
+// input rows are register-resident MFMA operands;
 // FP8 weights (SGLang's row-major E4M3 with 128 x 128 f32 block scales, read in place)
 // widen exactly to bf16 and each 128-k block's partial sum takes its block scale.
 #include "mk2_device.h"
@@ -43,40 +46,42 @@ constexpr int FR_NT = 512;
 
 struct GemvSeg {
   const void* w;   // [rows][K] bf16 or E4M3, row-major
-  const float* s;  // E4M3: f32 [rows / 128][K / 128] block scales
-  float* out;      // f32 [M][ld]
+  const float* s;  // E4M3: f32 [ceil(rows / 128)][K / 128] block scales
+  float* out;      // f32 partial planes: K part p, row m at out + p * pstride + m * ld
   int rows;        // multiple of 16
   int ld;
+  long long pstride;
 };
 
 struct GemvDev {
-  int M;  // rows this pass, 1..16
+  int M;   // rows this pass, 1..16
   int K;
+  int ks;  // K parts: workgroup b takes part b % ks (the grid is a multiple of ks)
   float eps;
   const bf16_t* x;  // [M][K]: raw rows (with g) or the GEMV input as it is (g null)
   const bf16_t* g;  // RMSNorm weight [K], or null
   GemvSeg seg[2];
-  int nseg;
   int tiles0;  // 16-row tiles of segment 0
   int ntiles;
 };
 
-// KU: 64-k units a wave (K = 8 * 64 * KU); F8: E4M3 weights
+// KU: 64-k units a wave (K / ks = 8 * 64 * KU); F8: E4M3 weights
 template <int KU, bool F8>
 __global__ __launch_bounds__(GV_NT) void k_gemv(GemvDev p) {
   constexpr int L = F8 ? KU : 2 * KU;      // 16-byte weight loads a lane a tile
   constexpr int WIN = L <= 24 ? L : L / 2;  // loads in flight a lane
   static_assert(L % WIN == 0, "a window divides the loads of a tile");
   static_assert(!F8 || KU % 2 == 0, "FP8 slices are whole 128-k blocks");
-  __shared__ float part[GV_WAVES][16];
+  __shared__ float ssum[16];
   __shared__ uint4 gam[8192 / 8];
   __shared__ float red[GV_CHUNK][GV_WAVES][256];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, c16 = lane & 15, g = lane >> 4;
-  const int K = p.K, G = gridDim.x, b = blockIdx.x, M = p.M;
-  const int t0 = (int)((long long)b * p.ntiles / G), t1 = (int)((long long)(b + 1) * p.ntiles / G);
+  const int K = p.K, b = blockIdx.x, M = p.M;
+  const int part = b % p.ks, G = gridDim.x / p.ks, q = b / p.ks;
+  const int t0 = (int)((long long)q * p.ntiles / G), t1 = (int)((long long)(q + 1) * p.ntiles / G);
   // k map: unit u of the wave's slice holds k = kw + 64 u + 0 .. 15 for lane group g;
   // MFMA step 2u takes its first 8, step 2u + 1 the next 8 (A and B alike)
-  const int kw = wave * KU * 64 + 16 * g;
+  const int kw = part * (K / p.ks) + wave * KU * 64 + 16 * g;
   // the rows: this lane's fragments of row c16 (16 k a unit)
   const bool live = c16 < M;
   const bf16_t* xr = p.x + (size_t)(live ? c16 : 0) * K + kw;
@@ -85,14 +90,6 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(GemvDev p) {
   for (int u = 0; u < KU; ++u) {
     xq[2 * u] = *(const uint4*)(xr + 64 * u);
     xq[2 * u + 1] = *(const uint4*)(xr + 64 * u + 8);
-  }
-  uint4 gq[2];
-  if (p.g) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int j = threadIdx.x + i * GV_NT;
-      gq[i] = j < K / 8 ? ((const uint4*)p.g)[j] : make_uint4(0, 0, 0, 0);
-    }
   }
   // the tile sequence: tile t of segment sid at row (t - base) * 16; this lane's row
   auto seg_of = [&](int t) { return t < p.tiles0 ? 0 : 1; };
@@ -109,33 +106,34 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(GemvDev p) {
 #pragma unroll
     for (int j = 0; j < WIN; ++j) wv[j] = ld_stream16(wrow + w_off(j));
   }
-  // the norm: sums of squares of the lane's fragments, the 4 lanes of the row, then
-  // the 8 waves' slices in wave order
+  // the norm: each row's sum of squares over all K (the rows are L2-resident): 32
+  // threads a row, 16-byte pieces, every load issued before the sums
   float rs = 1.f;
   if (p.g) {
+    constexpr int PB = 12;  // pieces a thread a batch
+    const int mr = threadIdx.x >> 5, tr = threadIdx.x & 31;
+    const uint4* xrow = (const uint4*)(p.x + (size_t)(mr < M ? mr : 0) * K);
     float ss = 0.f;
+    for (int i0 = tr; i0 < K / 8; i0 += 32 * PB) {
+      uint4 v[PB];
 #pragma unroll
-    for (int i = 0; i < 2 * KU; ++i) {
-      const uint32_t u4[4] = {xq[i].x, xq[i].y, xq[i].z, xq[i].w};
+      for (int j = 0; j < PB; ++j) v[j] = i0 + 32 * j < K / 8 ? xrow[i0 + 32 * j] : make_uint4(0, 0, 0, 0);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const bf16x2 v = __builtin_bit_cast(bf16x2, u4[j]);
-        ss = __builtin_amdgcn_fdot2_f32_bf16(v, v, ss, false);
+      for (int j = 0; j < PB; ++j) {
+        const uint32_t u4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bf16x2 h = __builtin_bit_cast(bf16x2, u4[e]);
+          ss = __builtin_amdgcn_fdot2_f32_bf16(h, h, ss, false);
+        }
       }
     }
-    ss += __shfl_xor(ss, 16);
-    ss += __shfl_xor(ss, 32);
-    if (g == 0) part[wave][c16] = ss;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int j = threadIdx.x + i * GV_NT;
-      if (j < K / 8) gam[j] = gq[i];
-    }
+    for (int m = 1; m < 32; m <<= 1) ss += __shfl_xor(ss, m);
+    if (tr == 0 && mr < M) ssum[mr] = ss;
+    for (int j = threadIdx.x; j < K / 8; j += GV_NT) gam[j] = ((const uint4*)p.g)[j];
     __syncthreads();
-    float tot = part[0][c16];
-#pragma unroll
-    for (int w = 1; w < GV_WAVES; ++w) tot += part[w][c16];
-    rs = 1.0f / sqrtf(tot / (float)K + p.eps);
+    rs = live ? 1.0f / sqrtf(ssum[c16] / (float)K + p.eps) : 0.f;
   }
   // B operands: bf16(x * rstd * g), or x as it is; zero columns past the rows
   bf16x8 bq[2 * KU];
@@ -169,7 +167,7 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(GemvDev p) {
       if constexpr (F8) {
         // the tile's block scales (one a 128-k block of the wave's slice; the tile's 16
         // rows are in one 128-row block)
-        const float* sr = p.seg[sid].s + (size_t)(row0 >> 7) * (K >> 7) + (wave * KU * 64 >> 7);
+        const float* sr = p.seg[sid].s + (size_t)(row0 >> 7) * (K >> 7) + ((kw - 16 * g) >> 7);
 #pragma unroll
         for (int kb = 0; kb < KU / 2; ++kb) {
           f32x4 pa = {0.f, 0.f, 0.f, 0.f};
@@ -215,7 +213,7 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(GemvDev p) {
       float s = red[i][0][v * 16 + m];
 #pragma unroll
       for (int w = 1; w < GV_WAVES; ++w) s += red[i][w][v * 16 + m];
-      if (m < M) p.seg[sid].out[(size_t)m * p.seg[sid].ld + row] = s;
+      if (m < M) p.seg[sid].out[part * p.seg[sid].pstride + (size_t)m * p.seg[sid].ld + row] = s;
     }
     __syncthreads();
   }
@@ -226,9 +224,32 @@ static void gemv_launch1(const GemvDev& d, int grid, hipStream_t st) {
   k_gemv<KU, F8><<<grid, GV_NT, 0, st>>>(d);
 }
 
+// the engine's k-step counts: KU = K / (512 ks)
+static bool gemv_ku_ok(int ku, bool f8) {
+  return (!f8 && ku == 1) || ku == 2 || ku == 4 || ku == 6 || ku == 8 || ku == 12 || ku == 14 || ku == 16;
+}
+
+// K parts for `tiles` tiles on `cus` CUs: the fewest that give every CU a tile, among
+// those the engine instantiates
+static int gemv_parts(int K, int tiles, int cus, bool f8) {
+  int best = 1;
+  for (int ks = 1; ks <= 16; ++ks) {
+    if (K % (512 * ks) || !gemv_ku_ok(K / (512 * ks), f8)) continue;
+    best = ks;
+    if (tiles * ks >= cus) break;
+  }
+  return best;
+}
+
 template <bool F8>
-static int gemv_launch(const GemvDev& d, int grid, hipStream_t st) {
-  switch (d.K / 512) {
+static int gemv_launch(const GemvDev& d, int cus, hipStream_t st) {
+  const int per = d.ntiles < cus / d.ks ? d.ntiles : cus / d.ks;  // workgroups a K part
+  const int grid = d.ks * (per > 0 ? per : 1);
+  switch (d.K / (512 * d.ks)) {
+    case 1:
+      if constexpr (F8) return set_error(MK2_EINVAL, "front: FP8 K parts must hold whole 128-k blocks");
+      else gemv_launch1<1, false>(d, grid, st);
+      break;
     case 2: gemv_launch1<2, F8>(d, grid, st); break;
     case 4: gemv_launch1<4, F8>(d, grid, st); break;
     case 6: gemv_launch1<6, F8>(d, grid, st); break;
@@ -236,7 +257,7 @@ static int gemv_launch(const GemvDev& d, int grid, hipStream_t st) {
     case 12: gemv_launch1<12, F8>(d, grid, st); break;
     case 14: gemv_launch1<14, F8>(d, grid, st); break;
     case 16: gemv_launch1<16, F8>(d, grid, st); break;
-    default: return set_error(MK2_EINVAL, "front: no GEMV engine for K = %d", d.K);
+    default: return set_error(MK2_EINVAL, "front: no GEMV engine for K = %d in %d parts", d.K, d.ks);
   }
   return MK2_OK;
 }
@@ -248,12 +269,13 @@ struct FrontDev {
   const long long* positions;  // [M]
   const long long* slots;      // [M], < 0: a pad row (no cache writes)
   const float* rope_cs;        // [positions][rope]: cos | sin
-  // f32 GEMV outputs (workspace)
-  const float* qkv_a;  // [M][q_lora + kv_lora + rope]
-  const float* ik;     // [M][128]
-  const float* iw;     // [M][ih]
-  const float* q_b;    // [M][heads * (nope + rope)]
-  const float* iq;     // [M][ih * 128]
+  // the GEMV outputs (workspace): f32 partial planes over K parts, summed in part order
+  const float* qkv_a;  // [ksA][M][q_lora + kv_lora + rope]
+  const float* ik;     // [ksA][M][128]
+  const float* iw;     // [ksW][M][ih]
+  const float* q_b;    // [ksC][M][heads * (nope + rope)]
+  const float* iq;     // [ksC][M][ih * 128]
+  int ksA, ksW, ksC;
   // weights
   const bf16_t* g_q_a;
   const bf16_t* g_kv_a;
@@ -261,15 +283,22 @@ struct FrontDev {
   const float* b_ik;
   const bf16_t* w_uk;  // [heads][kv_lora][nope] (SGLang's w_kc memory)
   // outputs
-  bf16_t* q_an;           // [M][q_lora] (workspace)
-  uint8_t* kv;            // latent cache [slots][576]
-  float* kv_scale;        // [slots], or null (unscaled)
-  uint8_t* icache;        // index cache (FP8 pages, or the FP4 plane's codes)
-  uint8_t* iscale;        // FP4 plane scales, or null
-  bf16_t* mla_q;          // [M][heads][kv_lora + rope]
-  bf16_t* index_q;        // [M][ih][128]
-  bf16_t* index_w;        // [M][ih]
+  bf16_t* q_an;     // [M][q_lora] (workspace)
+  uint8_t* kv;      // latent cache [slots][576]
+  float* kv_scale;  // [slots], or null (unscaled)
+  uint8_t* icache;  // index cache (FP8 pages, or the FP4 plane's codes)
+  uint8_t* iscale;  // FP4 plane scales, or null
+  bf16_t* mla_q;    // [M][heads][kv_lora + rope]
+  bf16_t* index_q;  // [M][ih][128]
+  bf16_t* index_w;  // [M][ih]
 };
+
+// element i of plane row `row` (length n) summed over `parts` planes in order
+MK2_DEV float parts_sum(const float* base, int parts, long long pstride, size_t at) {
+  float v = base[at];
+  for (int k = 1; k < parts; ++k) v += base[k * pstride + at];
+  return v;
+}
 
 MK2_DEV float block_sum512(float v, float* sh) {  // all 512 threads; sh: 8 floats
   v = wave_sum(v);
@@ -300,46 +329,98 @@ MK2_DEV void fwht128(float& v0, float& v1) {
   v1 = b * r;
 }
 
-// one row: q_a and kv_a norms, the latent cache row, the index key, the head weights
+MK2_DEV const float* rope_row(const FrontDev& p, int s) {
+  const long long pos = p.positions[s] < p.max_position ? p.positions[s] : p.max_position;
+  return p.rope_cs + (size_t)(pos < 0 ? 0 : pos) * p.rope;
+}
+
+// the normed input rows x_n = bf16(x * rstd * g_in), one workgroup a row, for every
+// hidden-input GEMV (so that each of their workgroups reads only its k slice)
+__global__ __launch_bounds__(FR_NT) void k_front_norm(const bf16_t* x, const bf16_t* gw, bf16_t* xn, int K, float eps) {
+  __shared__ float sh[FR_NT / 64];
+  constexpr int PT = 2;  // 16-byte pieces a thread (K <= 8192)
+  const int s = blockIdx.x;
+  const uint4* xr = (const uint4*)(x + (size_t)s * K);
+  uint4 v[PT];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < PT; ++i) {
+    const int j = threadIdx.x + i * FR_NT;
+    v[i] = j < K / 8 ? xr[j] : make_uint4(0, 0, 0, 0);
+    const uint32_t u4[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const bf16x2 h = __builtin_bit_cast(bf16x2, u4[e]);
+      ss = __builtin_amdgcn_fdot2_f32_bf16(h, h, ss, false);
+    }
+  }
+  const float rs = 1.0f / sqrtf(block_sum512(ss, sh) / (float)K + eps);
+#pragma unroll
+  for (int i = 0; i < PT; ++i) {
+    const int j = threadIdx.x + i * FR_NT;
+    if (j >= K / 8) continue;
+    const uint4 gv = ((const uint4*)gw)[j];
+    const uint32_t xu[4] = {v[i].x, v[i].y, v[i].z, v[i].w}, gu[4] = {gv.x, gv.y, gv.z, gv.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      o[e] = pack_bf16x2(__uint_as_float(xu[e] << 16) * rs * __uint_as_float(gu[e] << 16),
+                         __uint_as_float(xu[e] & 0xFFFF0000u) * rs * __uint_as_float(gu[e] & 0xFFFF0000u));
+    ((uint4*)(xn + (size_t)s * K))[j] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+// three workgroups a row: role 0 the normed q_a; role 1 the latent cache row; role 2
+// the index key and the head weights
 __global__ __launch_bounds__(FR_NT) void k_front_rows(FrontDev p) {
   __shared__ float sh[FR_NT / 64];
   __shared__ float kvv[576];
-  const int s = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int role = blockIdx.x / p.M, s = blockIdx.x % p.M;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int NA = p.q_lora + p.kv_lora + p.rope;
-  const float* a = p.qkv_a + (size_t)s * NA;
-  const long long pos = p.positions[s] < p.max_position ? p.positions[s] : p.max_position;
+  const long long pA = (long long)p.M * NA;
+  const size_t ra = (size_t)s * NA;
   const long long slot = p.slots[s];
-  const float* cs = p.rope_cs + (size_t)(pos < 0 ? 0 : pos) * p.rope;
-  // q_an = bf16(rmsnorm(q_a) * g)
-  {
+  const float* cs = rope_row(p, s);
+  if (role == 0) {  // q_an = bf16(rmsnorm(q_a) * g)
+    constexpr int QPT = 16;  // q_lora <= 8192: 16 a thread
+    float v[QPT];
     float ss = 0.f;
-    for (int k = tid; k < p.q_lora; k += FR_NT) ss += a[k] * a[k];
+#pragma unroll
+    for (int i = 0; i < QPT; ++i) {
+      const int k = tid + i * FR_NT;
+      v[i] = k < p.q_lora ? parts_sum(p.qkv_a, p.ksA, pA, ra + k) : 0.f;
+      ss += v[i] * v[i];
+    }
     const float rs = 1.0f / sqrtf(block_sum512(ss, sh) / (float)p.q_lora + p.eps);
-    for (int k = tid; k < p.q_lora; k += FR_NT)
-      p.q_an[(size_t)s * p.q_lora + k] = f32_to_bf16(a[k] * rs * bf16_to_f32(p.g_q_a[k]));
+#pragma unroll
+    for (int i = 0; i < QPT; ++i) {
+      const int k = tid + i * FR_NT;
+      if (k < p.q_lora) p.q_an[(size_t)s * p.q_lora + k] = f32_to_bf16(v[i] * rs * bf16_to_f32(p.g_q_a[k]));
+    }
+    return;
   }
-  // the latent row: bf16(rmsnorm(kv_a) * g) | bf16(rope(k_pe)), then E4M3
-  {
-    const float* kva = a + p.q_lora;
-    float ss = 0.f;
-    for (int k = tid; k < p.kv_lora; k += FR_NT) ss += kva[k] * kva[k];
-    const float rs = 1.0f / sqrtf(block_sum512(ss, sh) / (float)p.kv_lora + p.eps);
-    for (int k = tid; k < p.kv_lora; k += FR_NT)
-      kvv[k] = bf16_to_f32(f32_to_bf16(kva[k] * rs * bf16_to_f32(p.g_kv_a[k])));
-    const float* pe = kva + p.kv_lora;
-    for (int i = tid; i < p.rope / 2; i += FR_NT) {
-      const float x0 = pe[2 * i], x1 = pe[2 * i + 1], c = cs[i], sn = cs[p.rope / 2 + i];
-      kvv[p.kv_lora + 2 * i] = bf16_to_f32(f32_to_bf16(x0 * c - x1 * sn));
-      kvv[p.kv_lora + 2 * i + 1] = bf16_to_f32(f32_to_bf16(x0 * sn + x1 * c));
+  if (role == 1) {  // the latent row: bf16(rmsnorm(kv_a) * g) | bf16(rope(k_pe)), then E4M3
+    const int D = p.kv_lora + p.rope;
+    const float v = tid < p.kv_lora ? parts_sum(p.qkv_a, p.ksA, pA, ra + p.q_lora + tid) : 0.f;
+    float x0 = 0.f, x1 = 0.f;
+    if (tid < p.rope / 2) {
+      x0 = parts_sum(p.qkv_a, p.ksA, pA, ra + p.q_lora + p.kv_lora + 2 * tid);
+      x1 = parts_sum(p.qkv_a, p.ksA, pA, ra + p.q_lora + p.kv_lora + 2 * tid + 1);
+    }
+    const float rs = 1.0f / sqrtf(block_sum512(v * v, sh) / (float)p.kv_lora + p.eps);
+    if (tid < p.kv_lora) kvv[tid] = bf16_to_f32(f32_to_bf16(v * rs * bf16_to_f32(p.g_kv_a[tid])));
+    if (tid < p.rope / 2) {
+      const float c = cs[tid], sn = cs[p.rope / 2 + tid];
+      kvv[p.kv_lora + 2 * tid] = bf16_to_f32(f32_to_bf16(x0 * c - x1 * sn));
+      kvv[p.kv_lora + 2 * tid + 1] = bf16_to_f32(f32_to_bf16(x0 * sn + x1 * c));
     }
     __syncthreads();
-    const int D = p.kv_lora + p.rope;
     float scale = 1.f;
     if (p.kv_scaled) {
       float am = 0.f;
       for (int k = tid; k < D; k += FR_NT) am = fmaxf(am, fabsf(kvv[k]));
       am = wave_max(am);
-      __syncthreads();
       if (lane == 0) sh[wave] = am;
       __syncthreads();
       am = sh[0];
@@ -347,131 +428,135 @@ __global__ __launch_bounds__(FR_NT) void k_front_rows(FrontDev p) {
       for (int w = 1; w < FR_NT / 64; ++w) am = fmaxf(am, sh[w]);
       scale = am > 0.f ? am / 448.0f : 1.0f;
     }
-    if (slot >= 0) {
-      uint8_t* row = p.kv + (size_t)slot * D;
-      for (int k = tid; k < D; k += FR_NT) {
-        const float v = p.kv_scaled ? kvv[k] / scale : kvv[k];
-        row[k] = (uint8_t)f32_to_e4m3(v);
-      }
+    if (slot >= 0 && tid < D / 4) {  // four E4M3 a thread, one dword store
+      const float* k4 = kvv + 4 * tid;
+      const uint32_t w = p.kv_scaled ? f32x4_to_e4m3x4(k4[0] / scale, k4[1] / scale, k4[2] / scale, k4[3] / scale)
+                                     : f32x4_to_e4m3x4(k4[0], k4[1], k4[2], k4[3]);
+      *(uint32_t*)(p.kv + (size_t)slot * D + 4 * tid) = w;
       if (p.kv_scaled && tid == 0) p.kv_scale[slot] = scale;
     }
+    return;
   }
-  // the index key (wave 0): LayerNorm, RoPE on the first 64 dims, Hadamard, quant
-  if (p.ih > 0 && wave == 0) {
-    const float* k = p.ik + (size_t)s * 128;
-    float v0 = k[2 * lane], v1 = k[2 * lane + 1];
-    const float mean = wave_sum(v0 + v1) * (1.0f / 128);
-    const float d0 = v0 - mean, d1 = v1 - mean;
-    const float rstd = 1.0f / sqrtf(wave_sum(d0 * d0 + d1 * d1) * (1.0f / 128) + p.index_eps);
-    v0 = d0 * rstd * p.g_ik[2 * lane] + p.b_ik[2 * lane];
-    v1 = d1 * rstd * p.g_ik[2 * lane + 1] + p.b_ik[2 * lane + 1];
-    if (2 * lane < 64) {
-      const float c = cs[lane], sn = cs[p.rope / 2 + lane];
-      const float r0 = v0 * c - v1 * sn, r1 = v0 * sn + v1 * c;
-      v0 = r0;
-      v1 = r1;
-    }
-    fwht128(v0, v1);
-    if (slot >= 0) {
-      const long long page = slot >> 6;
-      const int t = (int)(slot & 63);
-      if (p.key_fmt == MK2_KEYS_FP8) {
-        // ue8m0: 2^ceil(log2(max(amax, 1e-4) / 448)), the values times its inverse
-        const float am = wave_max(fmaxf(fabsf(v0), fabsf(v1)));
-        const uint32_t bits = __float_as_uint(fmaxf(am, 1.0e-4f) / 448.0f);
-        const uint32_t e = ((bits >> 23) & 0xFF) + ((bits & 0x7FFFFF) != 0);
-        const float inv = __uint_as_float((254u - e) << 23);
-        uint8_t* pg = p.icache + (size_t)page * (64 * 132);
-        const int d = 2 * lane;  // dims d, d + 1: tile d / 16, byte d % 16
-        uint8_t* at = pg + (t >> 4) * 2048 + (d >> 4) * 256 + (t & 15) * 16 + (d & 15);
-        const uint32_t q = f32x4_to_e4m3x4(v0 * inv, v1 * inv, 0.f, 0.f);
-        at[0] = (uint8_t)(q & 0xFF);
-        at[1] = (uint8_t)((q >> 8) & 0xFF);
-        if (lane == 0) *(float*)(pg + 64 * 128 + 4 * t) = __uint_as_float(e << 23);
-      } else {
-        // MXFP4 per 32 dims (16 lanes): E8M0 = pow2_ceil(max(amax, 6 * 2^-126) / 6),
-        // E2M1 codes of v * 2^-e, two a byte (the even dim in the low nibble)
-        float am = fmaxf(fabsf(v0), fabsf(v1));
+  // role 2: the index key (wave 0): LayerNorm, RoPE on the first 64 dims, Hadamard,
+  // quant; the head weights (the other threads)
+  if (wave > 0) {
+    const long long pW = (long long)p.M * p.ih;
+    for (int h = tid - 64; h < p.ih; h += FR_NT - 64)
+      p.index_w[(size_t)s * p.ih + h] = f32_to_bf16(parts_sum(p.iw, p.ksW, pW, (size_t)s * p.ih + h));
+    return;
+  }
+  const long long pK = (long long)p.M * 128;
+  float v0 = parts_sum(p.ik, p.ksA, pK, (size_t)s * 128 + 2 * lane);
+  float v1 = parts_sum(p.ik, p.ksA, pK, (size_t)s * 128 + 2 * lane + 1);
+  const float mean = wave_sum(v0 + v1) * (1.0f / 128);
+  const float d0 = v0 - mean, d1 = v1 - mean;
+  const float rstd = 1.0f / sqrtf(wave_sum(d0 * d0 + d1 * d1) * (1.0f / 128) + p.index_eps);
+  v0 = d0 * rstd * p.g_ik[2 * lane] + p.b_ik[2 * lane];
+  v1 = d1 * rstd * p.g_ik[2 * lane + 1] + p.b_ik[2 * lane + 1];
+  if (2 * lane < 64) {
+    const float c = cs[lane], sn = cs[p.rope / 2 + lane];
+    const float r0 = v0 * c - v1 * sn, r1 = v0 * sn + v1 * c;
+    v0 = r0;
+    v1 = r1;
+  }
+  fwht128(v0, v1);
+  if (slot < 0) return;
+  const long long page = slot >> 6;
+  const int t = (int)(slot & 63);
+  if (p.key_fmt == MK2_KEYS_FP8) {
+    // ue8m0: 2^ceil(log2(max(amax, 1e-4) / 448)), the values times its inverse
+    const float am = wave_max(fmaxf(fabsf(v0), fabsf(v1)));
+    const uint32_t bits = __float_as_uint(fmaxf(am, 1.0e-4f) / 448.0f);
+    const uint32_t e = ((bits >> 23) & 0xFF) + ((bits & 0x7FFFFF) != 0);
+    const float inv = __uint_as_float((254u - e) << 23);
+    uint8_t* pg = p.icache + (size_t)page * (64 * 132);
+    const int d = 2 * lane;  // dims d, d + 1: tile d / 16, byte d % 16
+    const uint32_t q = f32x4_to_e4m3x4(v0 * inv, v1 * inv, 0.f, 0.f);
+    *(uint16_t*)(pg + (t >> 4) * 2048 + (d >> 4) * 256 + (t & 15) * 16 + (d & 15)) = (uint16_t)(q & 0xFFFF);
+    if (lane == 0) *(float*)(pg + 64 * 128 + 4 * t) = __uint_as_float(e << 23);
+  } else {
+    // MXFP4 per 32 dims (16 lanes): E8M0 = pow2_ceil(max(amax, 6 * 2^-126) / 6),
+    // E2M1 codes of v * 2^-e, two a byte (the even dim in the low nibble)
+    float am = fmaxf(fabsf(v0), fabsf(v1));
 #pragma unroll
-        for (int m = 1; m < 16; m <<= 1) am = fmaxf(am, __shfl_xor(am, m));
-        const uint32_t bits = __float_as_uint(fmaxf(am, 6.0f * 1.1754944e-38f) * (1.0f / 6.0f));
-        uint32_t e = ((bits >> 23) & 0xFF) + ((bits & 0x7FFFFF) != 0);
-        e = e > 254 ? 254 : e;
-        const uint32_t byte = f32x2_to_e2m1x2(v0, v1, e);
-        const int c = lane >> 4;  // the 32-dim chunk
-        uint8_t* codes = p.icache + (size_t)page * 4096 + c * 1024 + t * 16 + (lane & 15);
-        *codes = (uint8_t)byte;
-        if ((lane & 15) == 0) p.iscale[(size_t)page * 256 + c * 64 + (t & 15) * 4 + (t >> 4)] = (uint8_t)e;
-      }
-    }
+    for (int m = 1; m < 16; m <<= 1) am = fmaxf(am, __shfl_xor(am, m));
+    const uint32_t bits = __float_as_uint(fmaxf(am, 6.0f * 1.1754944e-38f) * (1.0f / 6.0f));
+    uint32_t e = ((bits >> 23) & 0xFF) + ((bits & 0x7FFFFF) != 0);
+    e = e > 254 ? 254 : e;
+    const int c = lane >> 4;  // the 32-dim chunk
+    p.icache[(size_t)page * 4096 + c * 1024 + t * 16 + (lane & 15)] = (uint8_t)f32x2_to_e2m1x2(v0, v1, e);
+    if ((lane & 15) == 0) p.iscale[(size_t)page * 256 + c * 64 + (t & 15) * 4 + (t >> 4)] = (uint8_t)e;
   }
-  // the head weights
-  for (int h = tid; h < p.ih; h += FR_NT) p.index_w[(size_t)s * p.ih + h] = f32_to_bf16(p.iw[(size_t)s * p.ih + h]);
 }
 
 // ---------------------------------------------------------------- per-head stage
-// Workgroups [0, heads): head h's absorbed queries for every row, 16 latent rows a
-// wave-tile on MFMA (A = W_UK[h] rows c, k = nope; B = bf16(q_nope) of the rows), and
-// its q_pe rotated; the rest: the index queries, one (row, index head) a wave.
+// Workgroups [0, 4 heads): head h, latent rows [128 j, 128 j + 128) of every row, a
+// 16-row tile a wave on MFMA (A = W_UK[h] rows c, k = nope; B = bf16(q_nope) of the
+// rows); quarter 0 also rotates the head's q_pe.  The rest: the index queries, one
+// (row, index head) a wave.
 template <int NS>  // nope / 32 k-steps
 __global__ __launch_bounds__(FR_NT) void k_front_heads(FrontDev p) {
+  __shared__ uint4 qn[32 * NS * 4];  // bf16 q_nope of the head, [row][nope] (16-byte pieces)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c16 = lane & 15, g = lane >> 4;
-  const int QD = p.nope + p.rope, D = p.kv_lora + p.rope;
-  if ((int)blockIdx.x < p.heads) {
-    const int h = blockIdx.x;
-    const bf16_t* wk = p.w_uk + (size_t)h * p.kv_lora * p.nope;
+  const int QD = p.nope + p.rope, D = p.kv_lora + p.rope, QB = p.heads * QD;
+  const long long pC = (long long)p.M * QB;
+  if ((int)blockIdx.x < 4 * p.heads) {
+    const int h = blockIdx.x >> 2, quarter = blockIdx.x & 3;
+    const int c0 = quarter * 128 + wave * 16;
+    const bf16_t* wr = p.w_uk + ((size_t)h * p.kv_lora + c0 + c16) * p.nope + 8 * g;
+    uint4 wv[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) wv[s] = *(const uint4*)(wr + 32 * s);
+    // the head's q_nope rows as bf16 in LDS: 8 consecutive k a thread (coalesced f32 reads)
+    for (int e = tid; e < p.M * NS * 4; e += FR_NT) {
+      const int m = e / (NS * 4), k8 = (e % (NS * 4)) * 8;
+      const size_t at = (size_t)m * QB + (size_t)h * QD + k8;
+      uint32_t o[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        o[j] = pack_bf16x2(parts_sum(p.q_b, p.ksC, pC, at + 2 * j), parts_sum(p.q_b, p.ksC, pC, at + 2 * j + 1));
+      qn[e] = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+    __syncthreads();
     for (int m0 = 0; m0 < p.M; m0 += 16) {
       // B operands: bf16(q_nope[m0 + c16][h]) at k = 32 s + 8 g
-      bf16x8 bq[NS];
       const int m = m0 + c16;
       const bool live = m < p.M;
-      const float* qn = p.q_b + (size_t)(live ? m : 0) * p.heads * QD + (size_t)h * QD;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
-        uint32_t o[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int k = 32 * s + 8 * g + 2 * j;
-          o[j] = live ? pack_bf16x2(qn[k], qn[k + 1]) : 0u;
-        }
-        bq[s] = __builtin_bit_cast(bf16x8, make_uint4(o[0], o[1], o[2], o[3]));
+        const uint4 b = live ? qn[m * NS * 4 + 4 * s + g] : make_uint4(0, 0, 0, 0);
+        acc = mfma_bf16(__builtin_bit_cast(bf16x8, wv[s]), __builtin_bit_cast(bf16x8, b), acc);
       }
-      for (int c0 = wave * 16; c0 < p.kv_lora; c0 += 16 * (FR_NT / 64)) {
-        const bf16_t* wr = wk + (size_t)(c0 + c16) * p.nope + 8 * g;
-        uint4 wv[NS];
-#pragma unroll
-        for (int s = 0; s < NS; ++s) wv[s] = *(const uint4*)(wr + 32 * s);
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < NS; ++s) acc = mfma_bf16(__builtin_bit_cast(bf16x8, wv[s]), bq[s], acc);
-        // lane (c16, g): latent rows c0 + 4 g + e of row m0 + c16
-        if (live) {
-          bf16_t* out = p.mla_q + ((size_t)m * p.heads + h) * D + c0 + 4 * g;
-          *(uint2*)out = make_uint2(pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]));
-        }
+      // lane (c16, g): latent rows c0 + 4 g + e of row m0 + c16
+      if (live) {
+        bf16_t* out = p.mla_q + ((size_t)m * p.heads + h) * D + c0 + 4 * g;
+        *(uint2*)out = make_uint2(pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]));
       }
     }
-    // q_pe rotated: pairs (2i, 2i + 1) of every row
-    for (int e = tid; e < p.M * (p.rope / 2); e += FR_NT) {
-      const int m = e / (p.rope / 2), i = e % (p.rope / 2);
-      const long long pos = p.positions[m] < p.max_position ? p.positions[m] : p.max_position;
-      const float* cs = p.rope_cs + (size_t)(pos < 0 ? 0 : pos) * p.rope;
-      const float* qp = p.q_b + (size_t)m * p.heads * QD + (size_t)h * QD + p.nope;
-      const float x0 = qp[2 * i], x1 = qp[2 * i + 1], c = cs[i], sn = cs[p.rope / 2 + i];
-      *(uint32_t*)(p.mla_q + ((size_t)m * p.heads + h) * D + p.kv_lora + 2 * i) =
-          pack_bf16x2(x0 * c - x1 * sn, x0 * sn + x1 * c);
+    if (quarter == 0) {  // q_pe rotated: pairs (2i, 2i + 1) of every row
+      for (int e = tid; e < p.M * (p.rope / 2); e += FR_NT) {
+        const int m = e / (p.rope / 2), i = e % (p.rope / 2);
+        const float* cs = rope_row(p, m);
+        const size_t at = (size_t)m * QB + (size_t)h * QD + p.nope + 2 * i;
+        const float x0 = parts_sum(p.q_b, p.ksC, pC, at), x1 = parts_sum(p.q_b, p.ksC, pC, at + 1);
+        const float c = cs[i], sn = cs[p.rope / 2 + i];
+        *(uint32_t*)(p.mla_q + ((size_t)m * p.heads + h) * D + p.kv_lora + 2 * i) =
+            pack_bf16x2(x0 * c - x1 * sn, x0 * sn + x1 * c);
+      }
     }
     return;
   }
   // index queries: wave task (row, index head)
-  const int task = ((int)blockIdx.x - p.heads) * (FR_NT / 64) + wave;
+  const int task = ((int)blockIdx.x - 4 * p.heads) * (FR_NT / 64) + wave;
   if (task >= p.M * p.ih) return;
   const int m = task / p.ih, h = task % p.ih;
-  const float* q = p.iq + ((size_t)m * p.ih + h) * 128;
-  float v0 = bf16_to_f32(f32_to_bf16(q[2 * lane])), v1 = bf16_to_f32(f32_to_bf16(q[2 * lane + 1]));
+  const long long pQ = (long long)p.M * p.ih * 128;
+  const size_t at = ((size_t)m * p.ih + h) * 128 + 2 * lane;
+  float v0 = bf16_to_f32(f32_to_bf16(parts_sum(p.iq, p.ksC, pQ, at)));
+  float v1 = bf16_to_f32(f32_to_bf16(parts_sum(p.iq, p.ksC, pQ, at + 1)));
   if (2 * lane < 64) {
-    const long long pos = p.positions[m] < p.max_position ? p.positions[m] : p.max_position;
-    const float* cs = p.rope_cs + (size_t)(pos < 0 ? 0 : pos) * p.rope;
+    const float* cs = rope_row(p, m);
     const float c = cs[lane], sn = cs[p.rope / 2 + lane];
     const float r0 = v0 * c - v1 * sn, r1 = v0 * sn + v1 * c;
     v0 = r0;
@@ -490,21 +575,41 @@ static int front_cus() {
   return cus[dev];
 }
 
-// workspace: f32 GEMV outputs and the normed q_a rows
+// the K parts of the three GEMV launches, planned for MI355X's 256 CUs (so that the
+// workspace and the bits do not depend on the device)
+constexpr int FRONT_PLAN_CUS = 256;
+struct FrontPlan {
+  int ksA, ksW, ksC;
+};
+static FrontPlan front_plan(const mk2_front_shape* s) {
+  const bool f8 = s->weight_fmt == MK2_WFMT_FP8_BLOCK;
+  const int NA = s->q_lora + s->kv_lora + s->rope, QB = s->heads * (s->nope + s->rope);
+  const int tA = NA / 16 + (s->index_heads > 0 ? 128 / 16 : 0);
+  const int tC = QB / 16 + s->index_heads * 128 / 16;
+  FrontPlan pl;
+  pl.ksA = gemv_parts(s->hidden, tA, FRONT_PLAN_CUS, f8);
+  pl.ksW = s->index_heads > 0 ? gemv_parts(s->hidden, s->index_heads / 16, FRONT_PLAN_CUS, false) : 1;
+  pl.ksC = gemv_parts(s->q_lora, tC, FRONT_PLAN_CUS, f8);
+  return pl;
+}
+
+// workspace: the GEMV outputs' partial planes and the normed q_a rows
 struct FrontWs {
   float *qkv_a, *ik, *iw, *q_b, *iq;
-  bf16_t* q_an;
+  bf16_t *q_an, *x_n;
 };
 static size_t front_carve(const mk2_front_shape* s, void* base, FrontWs* w) {
   Carver c(base);
-  const int M = s->rows;
-  float* qkv_a = c.take<float>((size_t)M * (s->q_lora + s->kv_lora + s->rope));
-  float* ik = c.take<float>((size_t)M * 128);
-  float* iw = c.take<float>((size_t)M * (s->index_heads > 0 ? s->index_heads : 1));
-  float* q_b = c.take<float>((size_t)M * s->heads * (s->nope + s->rope));
-  float* iq = c.take<float>((size_t)M * (s->index_heads > 0 ? s->index_heads : 1) * 128);
-  bf16_t* q_an = c.take<bf16_t>((size_t)M * s->q_lora);
-  if (w) *w = FrontWs{qkv_a, ik, iw, q_b, iq, q_an};
+  const FrontPlan pl = front_plan(s);
+  const size_t M = s->rows, ih = s->index_heads > 0 ? s->index_heads : 1;
+  float* qkv_a = c.take<float>(pl.ksA * M * (s->q_lora + s->kv_lora + s->rope));
+  float* ik = c.take<float>(pl.ksA * M * 128);
+  float* iw = c.take<float>(pl.ksW * M * ih);
+  float* q_b = c.take<float>(pl.ksC * M * s->heads * (s->nope + s->rope));
+  float* iq = c.take<float>(pl.ksC * M * ih * 128);
+  bf16_t* q_an = c.take<bf16_t>(M * s->q_lora);
+  bf16_t* x_n = c.take<bf16_t>(M * s->hidden);
+  if (w) *w = FrontWs{qkv_a, ik, iw, q_b, iq, q_an, x_n};
   return c.bytes();
 }
 
@@ -572,65 +677,71 @@ extern "C" int mk2_front_launch(const mk2_front_args* a, mk2_stream_t stream) {
   if (cus <= 0) return set_error(MK2_ELAUNCH, "front: cannot query the CU count");
   FrontWs ws;
   front_carve(&s, a->workspace, &ws);
+  const FrontPlan pl = front_plan(&s);
   hipStream_t st = (hipStream_t)stream;
-  const int M = s.rows, NA = s.q_lora + s.kv_lora + s.rope, QB = s.heads * (s.nope + s.rope);
-  auto grid_of = [&](int tiles) { return tiles < cus ? tiles : cus; };
-  // 1. hidden-input GEMVs (passes of 16 rows)
+  const int M = s.rows, NA = s.q_lora + s.kv_lora + s.rope, QB = s.heads * (s.nope + s.rope), IH = s.index_heads;
+  auto seg = [](const void* w, const float* sc, float* out, int rows, int ld, long long pstride) {
+    return GemvSeg{w, sc, out, rows, ld, pstride};
+  };
+  // 0. the normed input rows
+  k_front_norm<<<M, FR_NT, 0, st>>>((const bf16_t*)a->x, (const bf16_t*)w.g_in, ws.x_n, s.hidden, s.eps);
+  rc = check_launch("front (norm)");
+  if (rc) return rc;
+  // 1. the hidden-input GEMVs (passes of 16 rows)
   for (int r0 = 0; r0 < M; r0 += 16) {
-    const int mp = M - r0 < 16 ? M - r0 : 16;
     GemvDev d{};
-    d.M = mp; d.K = s.hidden; d.eps = s.eps;
-    d.x = (const bf16_t*)a->x + (size_t)r0 * s.hidden; d.g = (const bf16_t*)w.g_in;
-    d.seg[0] = GemvSeg{w.w_qkv_a, w.s_qkv_a, ws.qkv_a + (size_t)r0 * NA, NA, NA};
-    d.nseg = 1; d.tiles0 = NA / 16; d.ntiles = d.tiles0;
+    d.M = M - r0 < 16 ? M - r0 : 16; d.K = s.hidden; d.ks = pl.ksA; d.eps = s.eps;
+    d.x = ws.x_n + (size_t)r0 * s.hidden; d.g = nullptr;
+    d.seg[0] = seg(w.w_qkv_a, w.s_qkv_a, ws.qkv_a + (size_t)r0 * NA, NA, NA, (long long)M * NA);
+    d.tiles0 = NA / 16; d.ntiles = d.tiles0;
     if (idx) {
-      d.seg[1] = GemvSeg{w.w_ik, w.s_ik, ws.ik + (size_t)r0 * 128, 128, 128};
-      d.nseg = 2; d.ntiles += 128 / 16;
+      d.seg[1] = seg(w.w_ik, w.s_ik, ws.ik + (size_t)r0 * 128, 128, 128, (long long)M * 128);
+      d.ntiles += 128 / 16;
     }
-    rc = f8 ? gemv_launch<true>(d, grid_of(d.ntiles), st) : gemv_launch<false>(d, grid_of(d.ntiles), st);
+    rc = f8 ? gemv_launch<true>(d, cus, st) : gemv_launch<false>(d, cus, st);
     if (rc) return rc;
     if (idx) {  // the head weights are bf16 in every checkpoint format
       GemvDev e = d;
-      e.seg[0] = GemvSeg{w.w_iw, nullptr, ws.iw + (size_t)r0 * s.index_heads, s.index_heads, s.index_heads};
-      e.nseg = 1; e.tiles0 = s.index_heads / 16; e.ntiles = e.tiles0;
-      rc = gemv_launch<false>(e, grid_of(e.ntiles), st);
+      e.ks = pl.ksW;
+      e.seg[0] = seg(w.w_iw, nullptr, ws.iw + (size_t)r0 * IH, IH, IH, (long long)M * IH);
+      e.tiles0 = IH / 16; e.ntiles = e.tiles0;
+      rc = gemv_launch<false>(e, cus, st);
       if (rc) return rc;
     }
   }
-  // 2. per-row stage
+  // 2. the per-row stage: three workgroups a row
   FrontDev f{};
   f.M = M; f.q_lora = s.q_lora; f.kv_lora = s.kv_lora; f.rope = s.rope; f.nope = s.nope; f.heads = s.heads;
-  f.ih = s.index_heads; f.max_position = s.max_position; f.key_fmt = s.key_fmt; f.kv_scaled = s.kv_scaled;
+  f.ih = IH; f.max_position = s.max_position; f.key_fmt = s.key_fmt; f.kv_scaled = s.kv_scaled;
   f.eps = s.eps; f.index_eps = s.index_eps;
   f.positions = (const long long*)a->positions; f.slots = (const long long*)a->slots;
   f.rope_cs = a->rope_cos_sin;
   f.qkv_a = ws.qkv_a; f.ik = ws.ik; f.iw = ws.iw; f.q_b = ws.q_b; f.iq = ws.iq;
+  f.ksA = pl.ksA; f.ksW = pl.ksW; f.ksC = pl.ksC;
   f.g_q_a = (const bf16_t*)w.g_q_a; f.g_kv_a = (const bf16_t*)w.g_kv_a; f.g_ik = w.g_ik; f.b_ik = w.b_ik;
   f.w_uk = (const bf16_t*)w.w_uk;
   f.q_an = ws.q_an; f.kv = (uint8_t*)a->kv_cache; f.kv_scale = a->kv_scale;
   f.icache = (uint8_t*)a->index_cache; f.iscale = (uint8_t*)a->index_scale;
   f.mla_q = (bf16_t*)a->mla_q; f.index_q = (bf16_t*)a->index_q; f.index_w = (bf16_t*)a->index_w;
-  k_front_rows<<<M, FR_NT, 0, st>>>(f);
+  k_front_rows<<<(idx ? 3 : 2) * M, FR_NT, 0, st>>>(f);
   rc = check_launch("front (rows)");
   if (rc) return rc;
-  // 3. q_an-input GEMVs
+  // 3. the q_an-input GEMVs
   for (int r0 = 0; r0 < M; r0 += 16) {
-    const int mp = M - r0 < 16 ? M - r0 : 16;
     GemvDev d{};
-    d.M = mp; d.K = s.q_lora; d.eps = s.eps;
+    d.M = M - r0 < 16 ? M - r0 : 16; d.K = s.q_lora; d.ks = pl.ksC; d.eps = s.eps;
     d.x = ws.q_an + (size_t)r0 * s.q_lora; d.g = nullptr;
-    d.seg[0] = GemvSeg{w.w_q_b, w.s_q_b, ws.q_b + (size_t)r0 * QB, QB, QB};
-    d.nseg = 1; d.tiles0 = QB / 16; d.ntiles = d.tiles0;
+    d.seg[0] = seg(w.w_q_b, w.s_q_b, ws.q_b + (size_t)r0 * QB, QB, QB, (long long)M * QB);
+    d.tiles0 = QB / 16; d.ntiles = d.tiles0;
     if (idx) {
-      d.seg[1] = GemvSeg{w.w_iq, w.s_iq, ws.iq + (size_t)r0 * s.index_heads * 128, s.index_heads * 128,
-                         s.index_heads * 128};
-      d.nseg = 2; d.ntiles += s.index_heads * 128 / 16;
+      d.seg[1] = seg(w.w_iq, w.s_iq, ws.iq + (size_t)r0 * IH * 128, IH * 128, IH * 128, (long long)M * IH * 128);
+      d.ntiles += IH * 128 / 16;
     }
-    rc = f8 ? gemv_launch<true>(d, grid_of(d.ntiles), st) : gemv_launch<false>(d, grid_of(d.ntiles), st);
+    rc = f8 ? gemv_launch<true>(d, cus, st) : gemv_launch<false>(d, cus, st);
     if (rc) return rc;
   }
-  // 4. per-head stage
-  const int grid = s.heads + (idx ? (M * s.index_heads + FR_NT / 64 - 1) / (FR_NT / 64) : 0);
+  // 4. the per-head stage
+  const int grid = 4 * s.heads + (idx ? (M * IH + FR_NT / 64 - 1) / (FR_NT / 64) : 0);
   switch (s.nope / 32) {
     case 4: k_front_heads<4><<<grid, FR_NT, 0, st>>>(f); break;
     case 6: k_front_heads<6><<<grid, FR_NT, 0, st>>>(f); break;

@@ -7,18 +7,24 @@ routes a decode (or speculative-verify) step to the spec by its CUDA-graph key
 returns an object whose ``forward(plan, ...)`` runs one K2 launch a layer.
 
 This build serves one GPU's share of the layer (TP size 1: the reference's TP
-all-reduces are not part of it).  The layer's front (input RMSNorm, q/kv
-projections, RoPE, cache writes: the reference's K1) is outside the path; the
-forward receives its products -- index queries and head weights, absorbed MLA
-queries -- with the step.
+all-reduces are not part of it).  A routed step runs, on SGLang's own tensors
+(sgl_amd_mono.k2.binding): the step tables, the embedding rows, then per layer the
+front (the reference's K1: norms, projections, RoPE, this step's cache rows) and the
+K2 layer launch, then the tail (final norm, LM head), whose logits SGLang's logits
+processor returns -- the reference's _Built.forward / _backbone / _layer
+(glm53/spec.py:395-556).
 """
 
 from __future__ import annotations
 
 from types import SimpleNamespace
 
-from .. import _registry as _local
+import torch
+
+from .. import _registry_module
 from . import config as C
+
+_local = _registry_module()  # SGLang's registry classes, or the local stand-in
 
 
 ROWS = (1, 2, 4, 8, 16, 32)  # decode rows a launch serves (verify: batch x draft tokens)
@@ -91,57 +97,166 @@ def model_disable_reasons(hf) -> list:
     return []
 
 
+def front_config_from_hf(hf, weight_fmt: int = C.WFMT_FP8_BLOCK) -> C.FrontConfig:
+    """The front's geometry of an HF config: SGLang's DSA caches (FP8 index pages,
+    unscaled E4M3 latent rows)."""
+    return C.FrontConfig(
+        hidden=hf.hidden_size, q_lora=hf.q_lora_rank, kv_lora=hf.kv_lora_rank, rope=hf.qk_rope_head_dim,
+        nope=hf.qk_nope_head_dim, heads=hf.num_attention_heads, index_heads=hf.index_n_heads,
+        weight_fmt=weight_fmt, keys=C.KEYS_FP8, kv_scaled=False,
+        max_position=getattr(hf, "max_context", 65536) - 1, eps=float(getattr(hf, "rms_norm_eps", 1e-6)),
+    )
+
+
 class K2Forward:
-    """What build() returns: one chained-layer launch a layer, per routed step."""
+    """What build() returns: a routed step on SGLang's model (the reference's _Built,
+    glm53/spec.py:395-556).  pool_of(forward_batch) and page_table_of(forward_batch,
+    rows) give SGLang's token-to-KV pool and the rows' int32 page table; by default from
+    SGLang's forward context and attention backend."""
 
-    def __init__(self, cfg: C.K2Config, layers, device):
-        self.cfg, self.layers, self.device = cfg, layers, device
-        self._ops = {}  # (layer, rows) -> LayerOp
+    def __init__(self, lm, cfg: C.K2Config, front_cfg: C.FrontConfig, tail_cfg: C.TailConfig, device,
+                 *, pool_of=None, page_table_of=None):
+        from . import binding
 
-    def op(self, li: int, rows: int):
-        from .ops import LayerOp
+        self.lm, self.cfg, self.front_cfg, self.tail_cfg, self.device = lm, cfg, front_cfg, tail_cfg, device
+        layers = lm.model.layers
+        self.fronts = [binding.bind_front(L, front_cfg) for L in layers]
+        self.mlas = [binding.bind_mla(L, cfg.mla, front_cfg.nope) for L in layers]
+        self.moes = [binding.bind_moe(L, cfg.moe) for L in layers]
+        self.emb = lm.model.embed_tokens.weight
+        self.g_norm = lm.model.norm.weight
+        self.w_head = lm.lm_head.weight
+        cs = layers[0].self_attn.rotary_emb.cos_sin_cache
+        self.cos_sin = cs.float().contiguous()[: front_cfg.max_position + 1]
+        self.max_position = front_cfg.max_position
+        self.pool_of = pool_of or _sglang_pool
+        self.page_table_of = page_table_of or _sglang_page_table
+        self._ops, self._steps, self._tails = {}, {}, {}
+        # the logits processor returns the tail's logits on a routed step (the reference
+        # hooks _get_logits the same way, glm53/spec.py:423-441)
+        lp = getattr(lm, "logits_processor", None)
+        self._logits = None
+        if lp is not None and hasattr(lp, "_get_logits"):
+            self._own_logits = lp._get_logits
+            lp._get_logits = self._get_logits
 
-        key = (li, rows)
+    def _get_logits(self, hidden_states, lm_head, logits_metadata, *args, **kwargs):
+        if self._logits is None:
+            return self._own_logits(hidden_states, lm_head, logits_metadata, *args, **kwargs)
+        return self._logits[: hidden_states.shape[0]]
+
+    def ops(self, li: int, rows: int, table_stride: int, kv=None, icache=None):
+        """(FrontOp, LayerOp) of layer li at `rows` rows, created on first use with the
+        layer's caches (kv, icache); the layer's input tensors are rebound every step."""
+        from .ops import FrontOp, LayerOp
+
+        key = (li, rows, table_stride)
         if key not in self._ops:
-            L = self.layers[li]
-            if L.rows != rows:
-                L = replace_rows(L, rows)
-            self._ops[key] = LayerOp(self.cfg, L, rows, device=self.device)
+            dev, cfg, fc = self.device, self.cfg, self.front_cfg
+            pt = torch.zeros(rows, table_stride, dtype=torch.int32, device=dev)
+            i32 = dict(dtype=torch.int32, device=dev)
+            idx = SimpleNamespace(
+                cfg=cfg.indexer, rows=rows,
+                q=torch.empty(rows, fc.index_heads, 128, dtype=torch.bfloat16, device=dev),
+                w=torch.empty(rows, fc.index_heads, dtype=torch.bfloat16, device=dev),
+                cache=icache, cache_scale=None, page_table=pt, req_ids=torch.zeros(rows, **i32),
+                ctx_len=torch.zeros(rows, **i32))
+            mla = SimpleNamespace(**vars(self.mlas[li]))
+            mla.rows = rows
+            mla.q = torch.empty(rows, fc.heads, fc.kv_lora + fc.rope, dtype=torch.bfloat16, device=dev)
+            mla.kv, mla.kv_scale, mla.page_table, mla.req_ids = kv, None, pt, idx.req_ids
+            L = SimpleNamespace(cfg=cfg, rows=rows, idx=idx, mla=mla, moe=self.moes[li],
+                                h=torch.empty(rows, cfg.mla.hidden, dtype=torch.bfloat16, device=dev))
+            self._ops[key] = (FrontOp(fc, self.fronts[li], rows, device=dev), LayerOp(cfg, L, rows, device=dev))
         return self._ops[key]
 
-    def forward(self, plan, input_ids=None, positions=None, forward_batch=None, input_embeds=None,
-                pp_proxy_tensors=None):
-        """Runs every layer on the step's rows; returns the last hidden rows (bf16)."""
-        ok, why = SPEC.accepts(plan.key)
-        if not ok:
-            raise ValueError(why)
-        rows = plan.key.rows
-        fb = forward_batch
-        h = fb.hidden
-        if tuple(h.shape) != (rows, self.cfg.mla.hidden):
-            raise ValueError(f"hidden rows {tuple(h.shape)} do not match the plan's {rows} rows")
-        for li in range(len(self.layers)):
-            op = self.op(li, rows)
-            L = op.L
-            L.h = h
-            L.idx.q, L.idx.w, L.mla.q = fb.index_q[li], fb.index_w[li], fb.mla_q[li]
-            L.idx.ctx_len = L.mla.ctx_len = fb.ctx_len
-            h = op(out=plan.state.setdefault(("out", li % 2), h.new_empty(h.shape)))
-        return h
+    def step_rows(self, rows: int):
+        from .ops import StepRows
+
+        if rows not in self._steps:
+            self._steps[rows] = StepRows(rows, self.cfg.indexer.topk, device=self.device)
+        return self._steps[rows]
+
+    def tail(self, rows: int):
+        from .ops import TailOp
+
+        if rows not in self._tails:
+            self._tails[rows] = TailOp(self.tail_cfg, self.g_norm, self.w_head, rows, device=self.device)
+        return self._tails[rows]
+
+    def backbone(self, plan, input_ids, positions, forward_batch):
+        """Every layer a front and a layer launch, then the tail: (normed rows, logits)."""
+        accepts = getattr(SPEC, "accepts", None)  # SGLang routes by the spec itself
+        if accepts is not None:
+            ok, why = accepts(plan.key)
+            if not ok:
+                raise ValueError(why)
+        S = plan.key.batch_size * plan.key.tokens_per_request
+        st = self.step_rows(S)(forward_batch.out_cache_loc, positions, S, self.max_position, ids_in=input_ids)
+        pt = self.page_table_of(forward_batch, S)
+        pool = self.pool_of(forward_batch)
+        from . import binding
+
+        h = torch.nn.functional.embedding(input_ids[:S].long(), self.emb)
+        for li in range(len(self.fronts)):
+            kv, icache = binding.layer_caches(pool, li, self.front_cfg.index_heads > 0)
+            fo, lo = self.ops(li, S, pt.shape[1], kv, icache)
+            L = lo.L
+            fo(h, st.positions, st.slots, self.cos_sin, kv, None, icache, None,
+               mla_q=L.mla.q, index_q=L.idx.q, index_w=L.idx.w)
+            L.idx.page_table.copy_(pt[:S])
+            L.idx.req_ids.copy_(st.req_ids)
+            L.idx.ctx_len.copy_(st.ctx_len)
+            L.idx.cache, L.mla.kv, L.h = icache, kv, h
+            h = lo(out=plan.state.setdefault(("h", li % 2, S), torch.empty_like(h)))
+        logits, normed = self.tail(S)(h)
+        return normed, logits
+
+    def forward(self, plan, input_ids, positions, forward_batch, input_embeds=None, pp_proxy_tensors=None):
+        """DeepseekV2ForCausalLM.forward for a routed decode or verify step; with input
+        embeddings, SGLang's own forward (as the reference, glm53/spec.py:443-461)."""
+        lm = self.lm
+        if input_embeds is not None:
+            return type(lm).forward(lm, input_ids, positions, forward_batch, input_embeds, pp_proxy_tensors)
+        normed, self._logits = self.backbone(plan, input_ids, positions, forward_batch)
+        try:
+            return lm.logits_processor(input_ids, normed, lm.lm_head, forward_batch, None)
+        finally:
+            self._logits = None
 
 
-def replace_rows(L, rows):
-    """A layer namespace viewed for a different row count (weights shared)."""
-    return SimpleNamespace(**{**vars(L), "rows": rows})
+def _sglang_pool(forward_batch):
+    from sglang.srt.model_executor.forward_context import get_token_to_kv_pool  # type: ignore
+
+    return get_token_to_kv_pool()
+
+
+def _sglang_page_table(forward_batch, rows: int):
+    from sglang.srt.model_executor.forward_context import get_attn_backend  # type: ignore
+
+    return get_attn_backend().forward_metadata.real_page_table[:rows]
 
 
 def _build(model, hf_config, ctx):
-    """Binds a model's layers (namespaces in the kernels' formats, one a layer, as
-    sgl_amd_mono.k2.synth builds them) and returns the forward."""
+    """Binds SGLang's model (``model`` is its DeepseekV2ForCausalLM / GLM-5 module
+    tree) and returns the forward; ``ctx`` may carry pool_of / page_table_of."""
+    from dataclasses import replace
+
     cfg = config_from_hf(hf_config)
-    layers = list(model.k2_layers)
-    device = getattr(ctx, "device", None) or layers[0].h.device
-    return K2Forward(cfg, layers, device)
+    layer0 = model.model.layers[0]
+    first = layer0.self_attn.fused_qkv_a_proj_with_mqa.weight
+    wfmt = C.WFMT_FP8_BLOCK if first.dtype == torch.float8_e4m3fn else C.WFMT_BF16
+    # SGLang's DSA index cache holds FP8 pages; its experts' dtype names their mode
+    efmt = C.FMT_FP8 if layer0.mlp.experts.w13_weight.dtype == torch.float8_e4m3fn else C.FMT_MXFP4
+    cfg = replace(cfg, moe=replace(cfg.moe, expert_fmt=efmt), indexer=replace(cfg.indexer, keys=C.KEYS_FP8))
+    rows = layer0.self_attn.rotary_emb.cos_sin_cache.shape[0]
+    front = front_config_from_hf(hf_config, wfmt)
+    front = replace(front, max_position=min(front.max_position, rows - 1))
+    tail = C.TailConfig(hidden=hf_config.hidden_size, vocab_rows=model.lm_head.weight.shape[0],
+                        eps=float(getattr(hf_config, "rms_norm_eps", 1e-6)))
+    device = getattr(ctx, "device", None) or first.device
+    return K2Forward(model, cfg, front, tail, device, pool_of=getattr(ctx, "pool_of", None),
+                     page_table_of=getattr(ctx, "page_table_of", None))
 
 
 SPEC = _local.MonoSpec(

@@ -139,6 +139,8 @@ def mla_oracle(ns, sel=None, h="auto", parts=False):
     cfg = ns.cfg
     sel = cpu(ns.sel if sel is None else sel).long()
     kv, pt = cpu(ns.kv), cpu(ns.page_table)
+    if kv.dim() == 2:  # SGLang's flat [slots][576]: pages of 64 slots
+        kv = kv.view(-1, 64, kv.shape[-1])
     ksc = torch.ones(kv.shape[:2]) if ns.kv_scale is None else cpu(ns.kv_scale)
     q, w_uv, w_o = cpu(ns.q).float(), cpu(ns.w_uv).float(), cpu(ns.w_o).float()
     hres = cpu(ns.h) if h == "auto" else (cpu(h) if h is not None else None)

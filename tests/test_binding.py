@@ -1,0 +1,95 @@
+"""The binding of SGLang's model (sgl_amd_mono.k2.binding) on the CPU: what is read in
+place, what is copied into the kernels' tiles, and what is refused."""
+
+from dataclasses import replace
+
+import pytest
+import torch
+
+import fake_sglang as F
+
+
+@pytest.fixture(scope="module")
+def model():
+    return F.make_model(3, torch.device("cpu"), layers=1)
+
+
+def _cfgs():
+    from sgl_amd_mono.k2 import config as C
+    from sgl_amd_mono.k2 import spec
+
+    cfg = spec.config_from_hf(F.HF)
+    cfg = replace(cfg, moe=replace(cfg.moe, expert_fmt=C.FMT_FP8))
+    return cfg, spec.front_config_from_hf(F.HF, C.WFMT_FP8_BLOCK)
+
+
+def test_front_weights_are_read_in_place(model):
+    from sgl_amd_mono.k2 import binding
+
+    _, fc = _cfgs()
+    L = model.model.layers[0]
+    w = binding.bind_front(L, fc)
+    attn = L.self_attn
+    assert w.w_qkv_a.data_ptr() == attn.fused_qkv_a_proj_with_mqa.weight.data_ptr()
+    assert w.s_qkv_a.data_ptr() == attn.fused_qkv_a_proj_with_mqa.weight_scale_inv.data_ptr()
+    assert w.w_q_b.data_ptr() == attn.q_b_proj.weight.data_ptr()
+    assert w.w_iq.data_ptr() == attn.indexer.wq_b.weight.data_ptr()
+    assert w.w_ik.data_ptr() == attn.indexer.wk.weight.data_ptr()
+    assert w.w_iw.data_ptr() == attn.indexer.weights_proj.weight.data_ptr()
+    # w_kc's memory is already [heads][kv_lora][nope]: a view, no copy
+    assert w.w_uk.data_ptr() == attn.w_kc.data_ptr() and w.w_uk.is_contiguous()
+    assert torch.equal(w.w_uk, attn.w_kc.transpose(1, 2))
+    assert w.g_ik.dtype == torch.float32
+
+
+def test_mla_and_moe_weights(model):
+    from sgl_amd_mono.k2 import binding, synth
+
+    cfg, fc = _cfgs()
+    L = model.model.layers[0]
+    m = binding.bind_mla(L, cfg.mla, fc.nope)
+    assert m.w_uv.data_ptr() == L.self_attn.w_vc.data_ptr()  # [heads][v][kv_lora] memory
+    deq = L.self_attn.o_proj.weight.float() * L.self_attn.o_proj.weight_scale_inv.repeat_interleave(
+        128, 0).repeat_interleave(128, 1)
+    assert torch.equal(m.w_o, deq.to(torch.bfloat16))
+    e = binding.bind_moe(L, cfg.moe)
+    ex = L.mlp.experts
+    E = cfg.moe.n_experts
+    # routed experts: the first E physical experts; the fused shared expert is E
+    assert torch.equal(e.w13q, ex.w13_weight[:E].view(torch.uint8))
+    assert e.w13s.data_ptr() == ex.w13_weight_scale_inv.data_ptr()  # scales in place
+    assert torch.equal(e.ws13q, ex.w13_weight[E].view(torch.uint8))
+    assert torch.equal(e.ws2s, ex.w2_weight_scale_inv[E])
+    assert torch.equal(e.w_router_p, synth.pack_bf16(L.mlp.gate.weight))
+    assert e.gamma.data_ptr() == L.post_attention_layernorm.weight.data_ptr()
+
+
+def test_refusals(model):
+    from types import SimpleNamespace
+
+    from sgl_amd_mono.k2 import binding
+
+    cfg, fc = _cfgs()
+    L = model.model.layers[0]
+    bad = SimpleNamespace(weight=L.self_attn.q_b_proj.weight, weight_scale_inv=L.self_attn.q_b_proj.weight_scale_inv,
+                          weight_shuffled=True)
+    with pytest.raises(ValueError, match="shuffled"):
+        binding.linear("q_b_proj", bad, bad.weight.shape[0], bad.weight.shape[1])
+    with pytest.raises(ValueError, match="q_b_proj"):
+        binding.linear("q_b_proj", L.self_attn.q_b_proj, 7, 7)
+    with pytest.raises(ValueError, match="one format"):
+        binding.bind_front(L, replace(fc, weight_fmt=0))
+    from sgl_amd_mono.k2 import config as C
+
+    with pytest.raises(ValueError, match="block-FP8"):
+        binding.bind_moe(L, replace(cfg.moe, expert_fmt=C.FMT_MXFP4))
+
+
+def test_caches_are_views_of_the_pool():
+    from sgl_amd_mono.k2 import binding
+
+    pool = F.Pool(1, 8, torch.device("cpu"), 5)
+    kv, idx = binding.layer_caches(pool, 0, True)
+    assert kv.shape == (8 * 64, 576) and kv.dtype == torch.uint8
+    assert kv.data_ptr() == pool.kv[0].data_ptr()
+    assert idx.shape == (8, 64, 132) and idx.data_ptr() == pool.idx[0].data_ptr()

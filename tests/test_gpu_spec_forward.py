@@ -1,0 +1,75 @@
+"""A routed decode step through the plugin on SGLang's model layout (tests/fake_sglang):
+SPEC.build binds the model, forward() runs the step tables, every layer's front and
+layer launch on the pool's caches, and the tail; its logits come back through the
+logits processor.  Checks: this step's cache rows land at out_cache_loc and nothing
+else moves; the last layer, launched again on the bound inputs with its checking
+outputs, passes the layer oracle (refs.check_layer); the logits are the tail's of
+that layer's output."""
+
+from types import SimpleNamespace
+
+import pytest
+import torch
+
+import fake_sglang as F
+from refs import check_layer, cpu
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda:0")
+
+
+@pytest.mark.parametrize("rows", [1, 8])
+def test_routed_decode_step(rows):
+    from sgl_amd_mono import _registry as reg
+    from sgl_amd_mono.k2 import spec
+    from sgl_amd_mono.k2.ops import TailOp
+
+    dev = _dev()
+    pages = rows * (F.HF.max_context // 64) + 8
+    lm = F.make_model(11, dev)
+    pool = F.Pool(F.LAYERS, pages, dev, 12)
+    st = F.make_step(rows, F.HF.max_context, pages, dev, 13 + rows)
+    kv0 = [t.clone() for t in pool.kv]
+    idx0 = [t.clone() for t in pool.idx]
+    ctx = SimpleNamespace(device=dev, pool_of=lambda fb: pool, page_table_of=lambda fb, n: st.page_table[:n])
+    fwd = spec.SPEC.build(lm, F.HF, ctx)
+    plan = reg.Plan(key=reg.ShapeKey("decode", rows, 1))
+    logits = fwd.forward(plan, st.input_ids, st.positions, st.forward_batch)
+    torch.cuda.synchronize()
+    assert logits.shape == (rows, F.VOCAB) and bool(torch.isfinite(logits).all())
+    # this step's cache rows, and only those
+    loc = cpu(st.forward_batch.out_cache_loc)
+    for i in range(F.LAYERS):
+        kv, kv_before = cpu(pool.kv[i]).view(torch.uint8).view(-1, 576), cpu(kv0[i]).view(torch.uint8).view(-1, 576)
+        moved = (kv != kv_before).any(-1).nonzero().flatten()
+        assert set(moved.tolist()) <= set(loc.tolist()) and len(moved) >= rows - 1
+        ic, ic_before = cpu(pool.idx[i]).view(-1, 64, 132), cpu(idx0[i]).view(-1, 64, 132)
+        pages_moved = (ic != ic_before).view(ic.shape[0], -1).any(-1).nonzero().flatten()
+        assert set(pages_moved.tolist()) <= set((loc // 64).tolist())
+    # the last layer again, with its checking outputs, against the oracle
+    li = F.LAYERS - 1
+    fo, lo = fwd.ops(li, rows, st.page_table.shape[1])
+    L, cfg = lo.L, lo.cfg
+    H, E, K = cfg.mla.hidden, cfg.moe.n_experts, cfg.moe.top_k
+    attn = torch.empty(rows, H, dtype=torch.bfloat16, device=dev)
+    scores = torch.empty(rows, cfg.indexer.context, dtype=torch.float32, device=dev)
+    topk = torch.empty(rows, cfg.indexer.topk, dtype=torch.int32, device=dev)
+    lg = torch.empty(rows, E, dtype=torch.float32, device=dev)
+    ids = torch.empty(rows, K, dtype=torch.int32, device=dev)
+    wts = torch.empty(rows, K, dtype=torch.float32, device=dev)
+    out = lo(attn_out=attn, scores=scores, topk=topk, logits=lg, topk_ids=ids, topk_weights=wts)
+    torch.cuda.synchronize()
+    last = plan.state[("h", li % 2, rows)]
+    assert torch.equal(out, last)  # the step's own launch gave the same rows
+    stats = check_layer(L, *[cpu(t) for t in (out, attn, scores, topk, lg, ids, wts)])
+    print(stats)
+    # every row's own new key is in its context and was scored
+    for r in range(rows):
+        assert int(L.idx.ctx_len[r]) == int(st.positions[r]) + 1
+    want, _ = TailOp(fwd.tail_cfg, fwd.g_norm, fwd.w_head, rows, device=dev)(out)
+    assert torch.equal(logits, want)

@@ -343,6 +343,8 @@ def main():
     ap.add_argument("--timeline", metavar="MD",
                     help="write the persistent launch's per-stage timeline (markdown) to this file and exit")
     ap.add_argument("--timeline-launches", type=int, default=24)
+    ap.add_argument("--standalone", metavar="MD",
+                    help="time configs[0..3], the tail and the front as their own launches; write a table")
     args = ap.parse_args()
     if args.pmc_kernels:
         print(json.dumps(pmc_kernels(args.pmc_kernels, args.calib_bytes), indent=1))
@@ -362,6 +364,9 @@ def main():
     from sgl_amd_mono.k2 import synth
 
     dev = torch.device("cuda:0")
+    if args.standalone:
+        standalone(args, dev)
+        return
     cfg, rows = C.C5_LAYER, args.rows
     extra = [int(r) for r in args.extra_rows.split(",") if r] if args.extra_rows else []
     extra = [r for r in extra if r != rows]
@@ -447,6 +452,172 @@ def main():
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(synth.view_rows(layers[0], rows), args.cpu_reps)
     print(json.dumps(result))
+
+
+def time_graph(calls, steps=200, warmup=20):
+    """us per call of `calls` (a list of no-argument launches, cycled) replayed from one
+    HIP graph on a side stream, timed with events on that stream: median of 5 trials."""
+    import torch
+
+    stream = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        for c in calls:
+            c()
+        stream.synchronize()
+        with torch.cuda.graph(g, stream=stream):
+            for c in calls:
+                c()
+    torch.cuda.synchronize()
+    replays = max(1, -(-steps // len(calls)))
+    with torch.cuda.stream(stream):
+        for _ in range(max(1, -(-warmup // len(calls)))):
+            g.replay()
+    torch.cuda.synchronize()
+    trials = []
+    for _ in range(5):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            a.record(stream)
+            for _ in range(replays):
+                g.replay()
+            b.record(stream)
+        torch.cuda.synchronize()
+        trials.append(a.elapsed_time(b) * 1000.0 / (replays * len(calls)))
+    return statistics.median(trials), [round(t, 2) for t in trials]
+
+
+def _cpu_time(fn, reps):
+    """Median us of `reps` calls of fn after one warm-up call (the oracle on the host)."""
+    fn()
+    times = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t)
+    return statistics.median(times) * 1e6
+
+
+def standalone(args, dev):
+    """configs[0..3] as their own launches (the MoE block at C1 and C2, sparse MLA at C3,
+    the indexer at C4), the tail (C6) and the front (C7), each on one resident copy:
+    GPU us (graph replay), algorithmic bytes and the share of 8 TB/s, the oracle's CPU
+    us on the same inputs, and the parity of the launch's outputs with the oracle's."""
+    import torch
+
+    from oracle import codecs as oc
+    from oracle import reference as R
+    from refs import MoEOracle, cpu, index_keys_f32, mla_oracle
+    from sgl_amd_mono.k2 import config as C
+    from sgl_amd_mono.k2 import synth
+    from sgl_amd_mono.k2.ops import FrontOp, IndexerOp, MoEOp, SparseMlaOp, TailOp
+
+    cores = os.cpu_count() or 1
+    share = os.environ.get("OMP_NUM_THREADS", "")
+    if share.isdigit() and int(share) > 0:
+        cores = min(cores, int(share))
+    torch.set_num_threads(cores)
+    reps = args.cpu_reps
+    out = []
+
+    def row(name, rows, us, trials, nbytes, cpu_us, parity):
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out.append({"config": name, "rows": rows, "us": round(us, 2), "trials_us": trials, "bytes": int(nbytes),
+                    "gbps": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4),
+                    "cpu_us": None if cpu_us is None else round(cpu_us, 1), "parity": parity})
+        print(json.dumps(out[-1]), flush=True)
+
+    # C1 / C2: the MoE block
+    for name, cfg, rows in (("C1 FP8 MoE", C.C1_MOE, 4), ("C2 MXFP4 MoE", C.C2_MOE, 8)):
+        w = synth.make_moe(cfg, rows, 100 + rows, dev)
+        op = MoEOp(cfg, w, rows)
+        ids = torch.empty(rows, cfg.top_k, dtype=torch.int32, device=dev)
+        y = op(w.x, topk_ids=ids)
+        torch.cuda.synchronize()
+        d = int(torch.unique(ids).numel())
+        fp4 = cfg.expert_fmt in C.FP4_WEIGHT_FMTS
+        per = 3 * cfg.hidden * cfg.inter * ((0.5 + 1 / 32) if fp4 else (1 + 4 / (128 * 128)))
+        nbytes = d * per + cfg.n_experts * cfg.hidden * 2 + 3 * cfg.hidden * cfg.shared_inter * (1 + 4 / 16384)
+        us, tr = time_graph([lambda: op(w.x, out=y)])
+        orc = MoEOracle(w)
+        ref = orc(w.x)[0]
+        cpu_us = _cpu_time(lambda: orc(w.x), reps)
+        row(name, rows, us, tr, nbytes, cpu_us, f"rel-L2 {R.rel_l2(cpu(y).float(), ref):.1e}, {d} experts")
+    # C3: sparse MLA over given selections + W_UV + W_o
+    cfg = C.C3_MLA
+    ns = synth.make_mla(cfg, 8, 300, dev)
+    op = SparseMlaOp(cfg, ns, 8, ns.page_table.shape[1])
+    y = op(ns.q, ns.kv, ns.kv_scale, ns.page_table, ns.req_ids, ns.sel, h=ns.h)
+    torch.cuda.synchronize()
+    nbytes = 8 * cfg.topk * (cfg.qk_dim + 4) + cfg.heads * cfg.v_dim * cfg.kv_lora * 2 \
+        + cfg.hidden * cfg.heads * cfg.v_dim * 2 + 8 * cfg.heads * cfg.qk_dim * 2
+    us, tr = time_graph([lambda: op(ns.q, ns.kv, ns.kv_scale, ns.page_table, ns.req_ids, ns.sel, h=ns.h, out=y)])
+    ref = mla_oracle(ns)[1]
+    cpu_us = _cpu_time(lambda: mla_oracle(ns), reps)
+    row("C3 sparse MLA", 8, us, tr, nbytes, cpu_us, f"rel-L2 {R.rel_l2(cpu(y).float(), ref):.1e}")
+    # C4: the indexer and the exact top-2048
+    cfg = C.C4_INDEXER
+    ns = synth.make_indexer(cfg, 8, 400, dev)
+    op = IndexerOp(cfg, 8, ns.page_table.shape[1])
+    sc, tk = op(ns.q, ns.w, ns.cache, ns.cache_scale, ns.page_table, ns.req_ids, ns.ctx_len)
+    torch.cuda.synchronize()
+    nbytes = 8 * cfg.context * (cfg.dim // 2 + cfg.dim // 32) + 8 * cfg.heads * (cfg.dim + 1) * 2 + 8 * cfg.topk * 4
+    us, tr = time_graph([lambda: op(ns.q, ns.w, ns.cache, ns.cache_scale, ns.page_table, ns.req_ids, ns.ctx_len,
+                                    scores=sc, topk=tk)])
+    keys = [index_keys_f32(ns.cache, ns.cache_scale, ns.page_table, r, cfg.context) for r in range(8)]
+    qs, ws = cpu(ns.q).float(), cpu(ns.w).float()
+
+    def idx_oracle():
+        return [R.radix_lists(R.index_scores(qs[r], ws[r], keys[r]).float(), cfg.topk) for r in range(8)]
+
+    exact = all(torch.equal(cpu(tk)[r].long(), R.radix_lists(cpu(sc)[r], cfg.topk)) for r in range(8))
+    cpu_us = _cpu_time(idx_oracle, max(1, reps // 2))
+    row("C4 indexer + top-2048", 8, us, tr, nbytes, cpu_us, f"lists exact: {exact}")
+    # C6: the tail
+    cfg = C.C6_TAIL
+    ns = synth.make_tail(cfg, 8, 600, dev)
+    op = TailOp(cfg, ns.g_norm, ns.w_head, 8)
+    lg, nm = op(ns.x)
+    torch.cuda.synchronize()
+    nbytes = cfg.vocab_rows * cfg.hidden * 2 + 8 * (2 * cfg.hidden * 2 + cfg.vocab_rows * 4)
+    us, tr = time_graph([lambda: op(ns.x, lg, nm)])
+    x, gn, wh = cpu(ns.x), cpu(ns.g_norm), cpu(ns.w_head)
+    ref = R.tail(x, gn, wh, cfg.eps)[0]
+    cpu_us = _cpu_time(lambda: R.tail(x, gn, wh, cfg.eps), reps)
+    row("C6 tail (norm + LM head)", 8, us, tr, nbytes, cpu_us, f"rel-L2 {R.rel_l2(cpu(lg), ref):.1e}")
+    # C7: the front
+    cfg = C.C7_FRONT
+    ns = synth.make_front(cfg, 8, 700, dev)
+    op = FrontOp(cfg, ns, 8)
+    args7 = (ns.x, ns.positions, ns.slots, ns.rope_cos_sin, ns.kv_cache, ns.kv_scale, ns.index_cache, ns.index_scale)
+    outs = op(*args7)
+    torch.cuda.synchronize()
+    wb = sum(t.numel() * t.element_size() for t in (ns.w_qkv_a, ns.s_qkv_a, ns.w_q_b, ns.s_q_b, ns.w_uk, ns.w_iq,
+                                                    ns.s_iq, ns.w_ik, ns.s_ik, ns.w_iw))
+    us, tr = time_graph([lambda: op(*args7, *outs)])
+    from types import SimpleNamespace as NS
+
+    deq = lambda q, s_: oc.fp8_block_dequant(cpu(q), cpu(s_))  # noqa: E731
+    wref = NS(g_in=cpu(ns.g_in), g_q_a=cpu(ns.g_q_a), g_kv_a=cpu(ns.g_kv_a), w_qkv_a=deq(ns.w_qkv_a, ns.s_qkv_a),
+              w_q_b=deq(ns.w_q_b, ns.s_q_b), w_uk=cpu(ns.w_uk).float(), w_iq=deq(ns.w_iq, ns.s_iq),
+              w_ik=deq(ns.w_ik, ns.s_ik), g_ik=cpu(ns.g_ik), b_ik=cpu(ns.b_ik), w_iw=cpu(ns.w_iw).float())
+    fr = lambda: R.front(cpu(ns.x).float(), wref, cpu(ns.positions), cpu(ns.rope_cos_sin), eps=cfg.eps,  # noqa: E731
+                         index_eps=cfg.index_eps, nope=cfg.nope, heads=cfg.heads, index_heads=cfg.index_heads)
+    ref = fr()
+    cpu_us = _cpu_time(fr, reps)
+    row("C7 front (K1)", 8, us, tr, wb, cpu_us, f"mla_q rel-L2 {R.rel_l2(cpu(outs[0]).float(), ref['mla_q']):.1e}")
+    lines = [f"# Standalone launches on MI355X: configs[0..3], the tail and the front", "",
+             f"Command: `python {' '.join(sys.argv)}` (sources {sources_digest()[:12]}).", "",
+             f"GPU: HIP-graph replay, median of 5 trials. CPU: the oracle on the same inputs, {cores} threads, "
+             f"{cpu_model()}, median of {reps} after a warm-up (C4: {max(1, reps // 2)}).", "",
+             "| config | rows | GPU us | GB/s | % of 8 TB/s | CPU us | parity |", "| --- | --- | --- | --- | --- | --- | --- |"]
+    for r in out:
+        lines.append(f"| {r['config']} | {r['rows']} | {r['us']} | {r['gbps']} | {100 * r['frac']:.1f} | "
+                     f"{r['cpu_us']} | {r['parity']} |")
+    md = "\n".join(lines) + "\n"
+    with open(args.standalone, "w") as f:
+        f.write(md)
+    print(md)
 
 
 def _ops(cfg, views, rows, dev, staged):

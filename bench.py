@@ -32,13 +32,19 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k2_layer_m8_traffic.json")
 LAYER_KERNEL = "k_k2_layer"  # the persistent layer kernel's name (rocprof)
 
 
+# the sources the layer launch is built from (its kernels and the headers they include)
+LAYER_SOURCES = ("common.hip", "indexer_stages.h", "k2_persistent.hip", "layer.hip", "mk2_device.h",
+                 "mk2_host.h", "mla_stages.h", "moe_stages.h")
+
+
 def sources_digest():
-    """sha256 over the HIP sources: a recorded traffic figure applies to these only."""
+    """sha256 over the layer launch's HIP sources: a recorded traffic figure applies to
+    these only."""
     import hashlib
 
     h = hashlib.sha256()
     for name in sorted(os.listdir(CSRC)):
-        if name.endswith((".hip", ".h")):
+        if name in LAYER_SOURCES:
             h.update(name.encode())
             with open(os.path.join(CSRC, name), "rb") as f:
                 h.update(f.read())

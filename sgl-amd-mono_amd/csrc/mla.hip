@@ -39,7 +39,7 @@ int mla_check_shape(const mk2_mla_shape* s) {
 size_t mla_carve(const mk2_mla_shape* s, void* base, MlaDev* d) {
   Carver c(base);
   const int ns = s->topk / MLA_SPLIT;
-  float* po = c.take<float>((size_t)s->rows * ns * MLA_HEADS * MLA_LAT);
+  bf16_t* po = c.take<bf16_t>((size_t)s->rows * ns * MLA_HEADS * MLA_LAT);
   float* pml = c.take<float>((size_t)s->rows * ns * MLA_HEADS * 2);
   bf16_t* o = c.take<bf16_t>((size_t)s->rows * MLA_HEADS * s->v_dim);
   if (d) { d->part_o = po; d->part_ml = pml; d->o = o; d->nsplit = ns; }

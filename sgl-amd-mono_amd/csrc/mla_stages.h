@@ -44,7 +44,7 @@ struct MlaDev {
   const bf16_t* h;       // [rows][hidden] or null
   bf16_t* out;           // [rows][hidden]
   // workspace
-  float* part_o;         // [rows][nsplit][16][512]
+  bf16_t* part_o;        // [rows][nsplit][16][512] the splits' P.V, rounded to bf16
   float* part_ml;        // [rows][nsplit][16][2]
   float* o_lat_f32;      // optional [rows][16][512]
   bf16_t* o;             // [rows][16 * v_dim]
@@ -221,19 +221,37 @@ MK2_DEV bool mla_split(const MlaDev& p, int r, int s, MlaSplitLds& L, const TagP
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks)
     pa[ks] = __builtin_bit_cast(bf16x8, *(const uint4*)(L.p + c16 * (MLA_SPLIT + 8) + 32 * ks + 8 * g));
-  float* orow = p.part_o + ((size_t)r * p.nsplit + s) * MLA_HEADS * MLA_LAT;
+  bf16_t* orow = p.part_o + ((size_t)r * p.nsplit + s) * MLA_HEADS * MLA_LAT;
+  static_assert(TPW % 2 == 0, "dim tiles go in pairs");
 #pragma unroll
-  for (int t = 0; t < TPW; ++t) {
+  for (int t = 0; t < TPW; t += 2) {
     const int d0 = (wave * TPW + t) * 16;
-    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+    f32x4 o[2];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const int w = (8 * ks + 2 * g) ^ mla_vswz(d0);  // d0 + c16 shares d0 >> 4
-      const uint2 vw = *(const uint2*)(L.vt + (d0 + c16) * MLA_VROW + 4 * w);
-      o = mfma_bf16(pa[ks], e4m3x8_to_bf16(vw.x, vw.y), o);
+    for (int tt = 0; tt < 2; ++tt) {
+      o[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int w = (8 * ks + 2 * g) ^ mla_vswz(d0 + 16 * tt);  // d0 + c16 shares d0 >> 4
+        const uint2 vw = *(const uint2*)(L.vt + (d0 + 16 * tt + c16) * MLA_VROW + 4 * w);
+        o[tt] = mfma_bf16(pa[ks], e4m3x8_to_bf16(vw.x, vw.y), o[tt]);
+      }
     }
+    // the pair's 32 columns as bf16 pairs, lane c16 taking columns 2 c16, 2 c16 + 1 of
+    // them (from lanes 2 c16 and 2 c16 + 1 of the first tile, or of the second), so
+    // that a row's 16 lanes store one whole 64-byte piece (half the bytes the merge
+    // tasks read, each (row, head) twice)
+    const int src = ((lane & 48) | ((2 * c16) & 15)) * 4;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) st_dev_f32(orow + (4 * g + i) * MLA_LAT + d0 + c16, o[i]);
+    for (int i = 0; i < 4; ++i) {
+      const int a0 = __builtin_amdgcn_ds_bpermute(src, __float_as_int(o[0][i]));
+      const int a1 = __builtin_amdgcn_ds_bpermute(src + 4, __float_as_int(o[0][i]));
+      const int b0 = __builtin_amdgcn_ds_bpermute(src, __float_as_int(o[1][i]));
+      const int b1 = __builtin_amdgcn_ds_bpermute(src + 4, __float_as_int(o[1][i]));
+      const bool first = c16 < 8;
+      st_dev_u32(orow + (4 * g + i) * MLA_LAT + d0 + 2 * c16,
+                 pack_bf16x2(__int_as_float(first ? a0 : b0), __int_as_float(first ? a1 : b1)));
+    }
   }
   __syncthreads();
   return true;
@@ -250,12 +268,13 @@ MK2_DEV bool mla_split(const MlaDev& p, int r, int s, MlaSplitLds& L, const TagP
 // which polls the dependency, loads none.
 struct MlaMergeLds {
   float w[2 * 1024 + 8];  // per split: exp(m_s - M), then l_s (nsplit <= 1024)
+  float hi[MLA_LAT];      // the second half of the splits' weighted sums
   bf16_t ol[MLA_LAT];
 };
 
 template <int NT, typename Wait = NoWait>
 MK2_DEV void mla_merge_uv(const MlaDev& p, int r, int h, int hf, MlaMergeLds& L, Wait wait = Wait()) {
-  constexpr int NW = NT / 64, DPT = MLA_LAT / NT;
+  constexpr int NW = NT / 64;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, c16 = lane & 15;
   const int ns = p.nsplit, nvt = p.v_dim / 16;
   const int vlo = hf ? (nvt + 1) / 2 : 0, vhi = hf ? nvt : (nvt + 1) / 2;  // this half's tiles
@@ -286,33 +305,40 @@ MK2_DEV void mla_merge_uv(const MlaDev& p, int r, int h, int hf, MlaMergeLds& L,
   __syncthreads();
   float Lsum = 0.f;
   for (int s = 0; s < ns; ++s) Lsum += lsum[s] * wgt[s];
-  const float* po = p.part_o + ((size_t)r * ns * MLA_HEADS + h) * MLA_LAT + DPT * tid;
-  float o[DPT];
+  // the splits' bf16 partials: thread t takes dims 2 (t % 256) and + 1 (one 32-bit load
+  // a split) over half of the splits (the first or the second), 16 loads in flight;
+  // the second half's sums go through LDS and are added to the first's
+  static_assert(NT == 2 * (MLA_LAT / 2), "two threads a dim pair");
+  const int dp = tid % (MLA_LAT / 2), sh = tid / (MLA_LAT / 2);
+  const int nh = (ns + 1) / 2, sa = sh * nh, sb = min(ns, sa + nh);
+  const uint32_t* po = (const uint32_t*)(p.part_o + ((size_t)r * ns * MLA_HEADS + h) * MLA_LAT) + dp;
+  float o0 = 0.f, o1 = 0.f;
+  constexpr int U = 16;
+  for (int s0 = sa; s0 < sb; s0 += U) {
+    uint32_t v[U];
 #pragma unroll
-  for (int d = 0; d < DPT; ++d) o[d] = 0.f;
-  constexpr int U = 8;
-  for (int s0 = 0; s0 < ns; s0 += U) {
-    float v[U][DPT];
+    for (int u = 0; u < U; ++u) v[u] = s0 + u < sb ? ldp_u32(po + (size_t)(s0 + u) * (MLA_HEADS * MLA_LAT / 2)) : 0u;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-#pragma unroll
-      for (int d = 0; d < DPT; ++d)
-        v[u][d] = s0 + u < ns ? ldp_f32(po + (size_t)(s0 + u) * MLA_HEADS * MLA_LAT + d) : 0.f;
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const float w = s0 + u < ns ? wgt[s0 + u] : 0.f;
-#pragma unroll
-      for (int d = 0; d < DPT; ++d) o[d] += v[u][d] * w;
+      const float w = s0 + u < sb ? wgt[s0 + u] : 0.f;
+      o0 += __uint_as_float(v[u] << 16) * w;
+      o1 += __uint_as_float(v[u] & 0xFFFF0000u) * w;
     }
   }
+  if (sh == 1) {
+    L.hi[2 * dp] = o0;
+    L.hi[2 * dp + 1] = o1;
+  }
+  __syncthreads();
   const float inv = Lsum > 0.f ? 1.0f / Lsum : 0.f;
-  const size_t at = ((size_t)r * MLA_HEADS + h) * MLA_LAT + DPT * tid;
-#pragma unroll
-  for (int d = 0; d < DPT; ++d) {
-    o[d] *= inv;
-    L.ol[DPT * tid + d] = f32_to_bf16(o[d]);
-    if (p.o_lat_f32 && hf == 0) p.o_lat_f32[at + d] = o[d];
+  if (sh == 0) {
+    const float f0 = (o0 + L.hi[2 * dp]) * inv, f1 = (o1 + L.hi[2 * dp + 1]) * inv;
+    *(uint32_t*)(L.ol + 2 * dp) = pack_bf16x2(f0, f1);
+    if (p.o_lat_f32 && hf == 0) {
+      const size_t at = ((size_t)r * MLA_HEADS + h) * MLA_LAT + 2 * dp;
+      p.o_lat_f32[at] = f0;
+      p.o_lat_f32[at + 1] = f1;
+    }
   }
   __syncthreads();
   for (int vt = vt0; wave >= 1 && vt < vhi; vt += NW - 1) {

@@ -384,28 +384,30 @@ MK2_DEV bool moe_route(const MoeDev& p, RouteLds& L, const TagPoll& tp, Mark mar
         __builtin_amdgcn_make_buffer_rsrc((void*)p.logit_part, (short)0, (int)(plane * p.KC), 0x00020000);
     for (int c0 = 0; c0 < pieces && !bad; c0 += 2 * NT) {
       float sum[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
-      for (int kc0 = 0; kc0 < p.KC && !bad; kc0 += 4) {
-        i32x4 t[2][4];
+      // up to eight slices a poll round: one round trip for hidden <= 8192
+      constexpr int KU = 8;
+      for (int kc0 = 0; kc0 < p.KC && !bad; kc0 += KU) {
+        i32x4 t[2][KU];
         for (int polls = 1;; ++polls) {
           bool ready = true;
 #pragma unroll
           for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
+            for (int u = 0; u < KU; ++u) {
               const int c = min(c0 + tid + i * NT, pieces - 1), kc = min(kc0 + u, p.KC - 1);
               t[i][u] = __builtin_amdgcn_raw_buffer_load_b128(rs, kc * plane + (uint32_t)c * 16u, 0, 16 /* sc1 */);
             }
 #pragma unroll
           for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int u = 0; u < 4; ++u)
+            for (int u = 0; u < KU; ++u)
               ready = ready && (tp.tag == 0 || ((uint32_t)t[i][u].y == tp.tag && (uint32_t)t[i][u].w == tp.tag));
           if (poll_done(ready, polls, tp, &bad)) break;
         }
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-          for (int u = 0; u < 4; ++u)
+          for (int u = 0; u < KU; ++u)
             if (kc0 + u < p.KC) {
               sum[i][0] += __int_as_float(t[i][u].x);
               sum[i][1] += __int_as_float(t[i][u].z);

@@ -99,9 +99,11 @@ def test_static_scratch_graph_replays():
 
 
 def test_static_scratch_refuses_an_oversized_shape():
-    """32 rows with top-k 4096 need more scratch than the 64 MiB array (the split
-    partials alone are 32 x 64 splits x 16 x 512 x 4 B = 64 MiB): MK2_ENOSPACE, with
-    the sizes in the message, and no GPU call (this runs without a GPU)."""
+    """32 rows with top-k 4096 of 65536 keys and an expert inter of 1024 need more
+    scratch than the 64 MiB array (about 68 MiB: the split partials are 32 x 64 splits
+    x 16 x 512 x 2 B = 32 MiB, the rows' scores and bin candidates 24 MiB, the
+    experts' mid rows the rest): MK2_ENOSPACE, with the sizes in the message, and no
+    GPU call (this runs without a GPU)."""
     import ctypes
 
     from sgl_amd_mono import _lib
@@ -117,7 +119,7 @@ def test_static_scratch_refuses_an_oversized_shape():
                           *([1] * 7), None, None, None, 0)
     ma = _lib.MlaArgs(_lib.MlaShape(rows, 16, 512, 64, 128, mc.hidden, topk, mc.context // 64, mc.sm_scale),
                       *([1] * 5), None, 1, 1, 1, None, None, 0, None)
-    ea = _lib.MoeArgs(_lib.MoeShape(rows, ec.hidden, ec.n_experts, ec.top_k, ec.inter, ec.router, ec.expert_fmt,
+    ea = _lib.MoeArgs(_lib.MoeShape(rows, ec.hidden, ec.n_experts, ec.top_k, 1024, ec.router, ec.expert_fmt,
                                     ec.n_shared, ec.shared_inter, 1, 1, ec.route_scale, 1e-6),
                       _lib.MoeWeights(*([1] * 11)), None, None, None, 0, None, None, None)
     la = _lib.LayerArgs(ia, ma, ea, None, 2, None, 0, 0, 0, None, None)

@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define MK2_ABI_VERSION 2
+#define MK2_ABI_VERSION 3
 
 /* return codes */
 #define MK2_OK 0
@@ -68,7 +68,20 @@ typedef void* mk2_stream_t; /* a hipStream_t */
  * stored as tiles [N/16][K/128][64 lanes][chunk] where lane l holds row l%16 and
  * k = 32*(l/16) .. +31 of the 128-k block; chunk = 64 B (bf16), 32 B (E4M3),
  * 16 B (E2M1).  MXFP4 E8M0 scales: [N/16][ceil(K/512)][64 lanes][4 B].
- * gate and up are stacked as one [2*inter, hidden] matrix (gate first). */
+ * gate and up are stacked as one [2*inter, hidden] matrix (gate first).
+ *
+ * The expert weights (routed and shared) may instead be in AITER's (16, 16) layout,
+ * as SGLang leaves them for AITER's MoE (shuffle_weight(w, (16, 16)), e8m0_shuffle):
+ * the weight bytes [N/16][K_bytes/32][2][16 rows][16 B] -- for E2M1 this is byte for
+ * byte the tile layout above; for E4M3 a lane's 32 bytes are its row's two 16-byte
+ * halves 256 bytes apart -- and the E8M0 scales of [N][K/32] (rows counted across the
+ * experts) in e8m0_shuffle's order: byte (row, col) at
+ * ((((row/32 * K/256 + col/8) * 4 + col%4) * 16 + row%16) * 2 + col/4%2) * 2 + row/16%2.
+ * The E4M3 block scales are plain in both. */
+#define MK2_WLAYOUT_TILES 0   /* the tile packing above */
+#define MK2_WLAYOUT_AITER16 1 /* AITER's (16, 16) shuffle (the reference's fp8_shuffled
+                                 mode, glm53/gfx950/kernel.py:1015-1050; E2M1 with
+                                 e8m0_shuffle, runner.py:83-89) */
 typedef struct mk2_moe_shape {
   int rows;         /* M: decode rows, 1..32 */
   int hidden;       /* H, multiple of 512 */
@@ -83,6 +96,9 @@ typedef struct mk2_moe_shape {
   int residual;     /* 1: out = x + moe, else out = moe */
   float route_scale;
   float eps;
+  int weight_layout; /* MK2_WLAYOUT_*: the routed and shared experts' weights; AITER16
+                        needs inter and shared_inter multiples of 32, and with E2M1
+                        weights inter a multiple of 256 */
 } mk2_moe_shape;
 
 typedef struct mk2_moe_weights {

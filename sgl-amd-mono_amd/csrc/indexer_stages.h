@@ -718,7 +718,6 @@ MK2_DEV void bin_select(TopkLds& S, int m, int base, int k, const ListOut& lo) {
   uint32_t prefix = 0;  // the digits found so far
 #pragma unroll 1
   for (int pass = 0; pass < 2; ++pass) {
-    const int shift = pass == 0 ? 10 : 0;  // two 10-bit digits
     int* h = S.hist + 1024 * pass;
     if (pass == 1) {  // the first digit's histogram was built as the candidates were gathered
       for (int j = tid; j < m; j += NT) {

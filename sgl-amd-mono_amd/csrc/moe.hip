@@ -55,6 +55,11 @@ int moe_check_shape(const mk2_moe_shape* s) {
                 "moe: shared_inter must be a multiple of 128 in [128, 4096], got %d", s->shared_inter);
   MK2_REQUIRE(s->norm == 0 || s->norm == 1, "moe: norm must be 0 or 1");
   MK2_REQUIRE(s->residual == 0 || s->residual == 1, "moe: residual must be 0 or 1");
+  MK2_REQUIRE(s->weight_layout == MK2_WLAYOUT_TILES || s->weight_layout == MK2_WLAYOUT_AITER16,
+              "moe: unknown weight_layout %d", s->weight_layout);
+  if (s->weight_layout == MK2_WLAYOUT_AITER16)
+    MK2_REQUIRE(!w_fp4(s->expert_fmt) || s->inter % 256 == 0,
+                "moe: AITER's E8M0 layout needs inter a multiple of 256, got %d", s->inter);
   return MK2_OK;
 }
 
@@ -120,7 +125,7 @@ int moe_fill(const mk2_moe_args* a, MoeDev* d) {
   d->M = s->rows; d->H = s->hidden; d->E = s->n_experts; d->topk = s->top_k; d->I = s->inter;
   d->router = s->router; d->fmt = s->expert_fmt; d->n_shared = s->n_shared;
   d->SI = s->n_shared ? s->shared_inter : 0; d->norm = s->norm; d->residual = s->residual;
-  d->route_scale = s->route_scale; d->eps = s->eps;
+  d->route_scale = s->route_scale; d->eps = s->eps; d->wl = s->weight_layout;
   d->gamma = (const bf16_t*)w->gamma; d->w_router = (const uint8_t*)w->w_router;
   d->bias = w->router_bias; d->w13 = (const uint8_t*)w->w13; d->s13 = (const uint8_t*)w->s13;
   d->w2 = (const uint8_t*)w->w2; d->s2 = (const uint8_t*)w->s2;

@@ -26,6 +26,7 @@ struct MoeDev {
   int DT;    // 16-row hidden tiles of a down task (2: MXFP4 at <= 16 rows, else 1; 3: 24 rows,
             // a tile and a half, when hidden is a multiple of 48)
   float route_scale, eps;
+  int wl;    // MK2_WLAYOUT_*: the expert weights' layout
   const bf16_t* x;
   const bf16_t* gamma;
   const uint8_t* w_router;
@@ -156,6 +157,39 @@ MK2_DEV void load_a_fp8(const uint8_t* tile, int lane, bf16x8* a) {
   a[2] = e4m3x8_to_bf16(u1.x, u1.y);
   a[3] = e4m3x8_to_bf16(u1.z, u1.w);
 }
+// ---- the expert weights' two layouts (MK2_WLAYOUT_*).  Both keep a 16-row group's
+// 16-row x 128-k block at the same place (2 KiB of E4M3, 1 KiB of E2M1, k-block-major
+// inside the group).  Inside a block:
+//  - E4M3: lane (g, c16) takes k 32 g .. 32 g + 31 of row c16 as two 16-byte halves
+//    at fp8_half: tiles [64 lanes][32 B], AITER [4 groups][2 halves][16 rows][16 B];
+//  - E2M1: [4 groups][16 rows][16 B] in both.
+MK2_DEV uint32_t fp8_half(int wl, int lane, int h) {
+  return wl == MK2_WLAYOUT_AITER16 ? (uint32_t)((lane >> 4) * 512 + h * 256 + (lane & 15) * 16)
+                                   : (uint32_t)(lane * 32 + h * 16);
+}
+// the lane's two halves of the E4M3 block at `blk`
+MK2_DEV void load_fp8_block(const uint8_t* blk, int wl, int lane, uint4& lo, uint4& hi) {
+  lo = ld_stream16(blk + fp8_half(wl, lane, 0));
+  hi = ld_stream16(blk + fp8_half(wl, lane, 1));
+}
+// The E8M0 scales of an expert's E2M1 [N][K] matrix: one expert's bytes; the 32-bit
+// word lane `lane` reads for 16-row tile t and k-block kb; the shift that brings kb's
+// code to the word's low byte.  Tiles: [N/16][ceil(K/512)][64 lanes] words of four
+// k-blocks.  AITER (e8m0_shuffle over the experts' rows, N a multiple of 32, K of
+// 256): [N/32][K/256][64 lanes] words, each two k-blocks of two 16-row tiles, byte
+// 2 (kb & 1) + (t & 1).
+MK2_DEV size_t e8m0_expert_bytes(int wl, int N, int K) {
+  return wl == MK2_WLAYOUT_AITER16 ? (size_t)N * (K / 32) : (size_t)(N / 16) * ((K / 128 + 3) / 4) * 256;
+}
+MK2_DEV uint32_t e8m0_word(const uint8_t* s_e, int wl, int K, int t, int kb, int lane) {
+  const size_t w = wl == MK2_WLAYOUT_AITER16 ? ((size_t)(t >> 1) * (K / 256) + (kb >> 1)) * 64 + lane
+                                             : ((size_t)t * ((K / 128 + 3) / 4) + (kb >> 2)) * 64 + lane;
+  return *(const uint32_t*)(s_e + w * 4);
+}
+MK2_DEV int e8m0_shift(int wl, int t, int kb) {
+  return wl == MK2_WLAYOUT_AITER16 ? 8 * (2 * (kb & 1) + (t & 1)) : 8 * (kb & 3);
+}
+
 MK2_DEV i32x8 load_a_fp4(const uint8_t* tile, int lane) {
   uint4 u = ld_stream16(tile + lane * 16);
   i32x8 a = {(int)u.x, (int)u.y, (int)u.z, (int)u.w, 0, 0, 0, 0};
@@ -569,9 +603,8 @@ MK2_DEV void upgate_chunk(const MoeDev& p, bool shared, int j, int e, int c, flo
     // scaled MFMA: E2M1 weights against MXFP8 (A8W4) or MXFP4 (A4W4) activations
     constexpr bool a4 = FMT == MK2_FMT_A4W4;
     constexpr int B = CT == 4 ? (NCG == 1 ? 3 : 2) : (NCG == 1 ? 4 : 3);  // k-blocks in flight
-    const int G = (KB + 3) / 4;
     const uint8_t* wbase = p.w13 + (size_t)e * NT16 * KB * 1024;
-    const uint8_t* sbase = p.s13 + (size_t)e * NT16 * G * 256;
+    const uint8_t* sbase = p.s13 + e * e8m0_expert_bytes(p.wl, 2 * I, p.H);
     for (int kb0 = wave; kb0 < KB; kb0 += NW * B) {
       i32x8 a[B][NQ], b[B][NCG];
       int sa[B][NQ], sb[B][NCG];
@@ -581,8 +614,7 @@ MK2_DEV void upgate_chunk(const MoeDev& p, bool shared, int j, int e, int c, flo
 #pragma unroll
         for (int q = 0; q < NQ; ++q) {
           a[u][q] = load_a_fp4(wbase + ((size_t)nts[q] * KB + kb) * 1024, lane);
-          sa[u][q] = (int)(*(const uint32_t*)(sbase + (((size_t)nts[q] * G + kb / 4) * 64 + lane) * 4) >>
-                           (8 * (kb & 3)));
+          sa[u][q] = (int)(e8m0_word(sbase, p.wl, p.H, nts[q], kb, lane) >> e8m0_shift(p.wl, nts[q], kb));
         }
 #pragma unroll
         for (int cg = 0; cg < NCG; ++cg) {
@@ -606,9 +638,8 @@ MK2_DEV void upgate_chunk(const MoeDev& p, bool shared, int j, int e, int c, flo
     // E2M1 weights widened exactly to bf16 (x their E8M0) right before bf16 MFMAs on the
     // bf16 rows: no scale to apply after
     constexpr int B = NCG == 1 ? 2 : 1;
-    const int G = (KB + 3) / 4;
     const uint8_t* wbase = p.w13 + (size_t)e * NT16 * KB * 1024;
-    const uint8_t* sbase = p.s13 + (size_t)e * NT16 * G * 256;
+    const uint8_t* sbase = p.s13 + e * e8m0_expert_bytes(p.wl, 2 * I, p.H);
     for (int kb0 = wave; kb0 < KB; kb0 += NW * B) {
       uint4 raw[B][NQ];
       uint32_t sw[B][NQ];
@@ -619,7 +650,7 @@ MK2_DEV void upgate_chunk(const MoeDev& p, bool shared, int j, int e, int c, flo
 #pragma unroll
         for (int q = 0; q < NQ; ++q) {
           raw[u][q] = ld_stream16(wbase + (((size_t)nts[q] * KB + kb) * 64 + lane) * 16);
-          sw[u][q] = (*(const uint32_t*)(sbase + (((size_t)nts[q] * G + kb / 4) * 64 + lane) * 4) >> (8 * (kb & 3))) & 0xFFu;
+          sw[u][q] = (e8m0_word(sbase, p.wl, p.H, nts[q], kb, lane) >> e8m0_shift(p.wl, nts[q], kb)) & 0xFFu;
         }
 #pragma unroll
         for (int cg = 0; cg < NCG; ++cg)
@@ -654,9 +685,7 @@ MK2_DEV void upgate_chunk(const MoeDev& p, bool shared, int j, int e, int c, flo
         const int kb = min(kb0 + u * NW, KB - 1);
 #pragma unroll
         for (int q = 0; q < NQ; ++q) {
-          const uint4* tl = (const uint4*)(wbase + ((size_t)nts[q] * KB + kb) * 2048 + lane * 32);
-          raw[u][q][0] = ld_stream16(tl);
-          raw[u][q][1] = ld_stream16(tl + 1);
+          load_fp8_block(wbase + ((size_t)nts[q] * KB + kb) * 2048, p.wl, lane, raw[u][q][0], raw[u][q][1]);
           sc[u][q] = sbase[(nts[q] * 16 / 128) * KB + kb];
         }
 #pragma unroll
@@ -769,12 +798,8 @@ MK2_DEV void upgate_w8a8(const MoeDev& p, int j, int e, int c, float* red) {
 #pragma unroll
     for (int u = 0; u < KBB; ++u) {
       const int kb = min(kb0 + u, KB - 1);
-      const uint4* pg = (const uint4*)(wbase + (((size_t)tg * KB + kb) * 64 + lane) * 32);
-      const uint4* pu = (const uint4*)(wbase + (((size_t)tu * KB + kb) * 64 + lane) * 32);
-      rg[u][0] = ld_stream16(pg);
-      rg[u][1] = ld_stream16(pg + 1);
-      ru[u][0] = ld_stream16(pu);
-      ru[u][1] = ld_stream16(pu + 1);
+      load_fp8_block(wbase + ((size_t)tg * KB + kb) * 2048, p.wl, lane, rg[u][0], rg[u][1]);
+      load_fp8_block(wbase + ((size_t)tu * KB + kb) * 2048, p.wl, lane, ru[u][0], ru[u][1]);
       wsg[u] = sg[kb];
       wsu[u] = su[kb];
 #pragma unroll
@@ -928,7 +953,6 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, float*
   const int KB2 = p.I / 128;
   constexpr int B = 1;                                 // MXFP4 slots a unit
   constexpr int KC = 2;                                // k-blocks of a slot a pass
-  const int G2 = (KB2 + 3) / 4;
   // weights only (static, or known since routing): the shared expert's first k-block
   // of this wave and its first batch of routed slots, loaded before `wait` (the mid
   // activations' dependency)
@@ -941,11 +965,7 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, float*
       shraw[d][0] = shraw[d][1] = make_uint4(0, 0, 0, 0);
       shsc[d] = 0.f;
       if (KB2s) {
-        const uint4* src = (const uint4*)(p.ws2 + ((size_t)tl[d] * KB2s + kb) * 2048 + lane * 32);
-        if (live[d]) {
-          shraw[d][0] = src[0];
-          shraw[d][1] = src[1];
-        }
+        if (live[d]) load_fp8_block(p.ws2 + ((size_t)tl[d] * KB2s + kb) * 2048, p.wl, lane, shraw[d][0], shraw[d][1]);
         shsc[d] = p.ss2[(tl[d] * 16 / 128) * KB2s + kb];
       }
     }
@@ -986,7 +1006,8 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, float*
                                   : i32x8{0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
       for (int d = 0; d < DT; ++d)
-        x.sa[ub][d] = live[d] ? (int)*(const uint32_t*)(p.s2 + ((((size_t)e * HT + tl[d]) * G2 + kb0 / 4) * 64 + lane) * 4) : 127;
+        x.sa[ub][d] = live[d] ? (int)e8m0_word(p.s2 + e * e8m0_expert_bytes(p.wl, p.H, p.I), p.wl, p.I, tl[d], kb0, lane)
+                              : 127;
     }
   };
   auto load_m = [&](int u, Unit& x) {  // mid rows and route weights: after the wait
@@ -1033,7 +1054,7 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, float*
         if (kb >= KB2) break;
 #pragma unroll
         for (int d = 0; d < DT; ++d) {
-          const int sak = x.sa[ub][d] >> (8 * (kb & 3));
+          const int sak = x.sa[ub][d] >> e8m0_shift(p.wl, tl[d], kb);
 #pragma unroll
           for (int cg = 0; cg < NCG; ++cg)
             tmp[ub][d][cg] = a4 ? mfma_same<4>(x.a[ub][d][c], x.bq[ub][c][cg], tmp[ub][d][cg], sak, x.sbq[ub][c][cg])
@@ -1072,9 +1093,8 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, float*
         r1 = shraw[d][1];
         sc = shsc[d];
       } else {
-        const uint4* src = (const uint4*)(p.ws2 + ((size_t)tl[d] * KB2s + kb) * 2048 + lane * 32);
-        r0 = live[d] ? src[0] : make_uint4(0, 0, 0, 0);
-        r1 = live[d] ? src[1] : make_uint4(0, 0, 0, 0);
+        r0 = r1 = make_uint4(0, 0, 0, 0);
+        if (live[d]) load_fp8_block(p.ws2 + ((size_t)tl[d] * KB2s + kb) * 2048, p.wl, lane, r0, r1);
         sc = p.ss2[(tl[d] * 16 / 128) * KB2s + kb];
       }
       bf16x8 a[4];
@@ -1106,7 +1126,7 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, float*
       for (int j = wave; j < D; j += NW) {
         const int e = act_ids[j];
         const uint8_t* wb = p.w2 + ((size_t)e * HT + tl[0]) * KB2 * 1024;
-        const uint8_t* sb = p.s2 + ((size_t)e * HT + tl[0]) * G2 * 256;
+        const uint8_t* sb = p.s2 + e * e8m0_expert_bytes(p.wl, p.H, p.I);
         f32x4 t[NCG];
 #pragma unroll
         for (int cg = 0; cg < NCG; ++cg) t[cg] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1117,7 +1137,7 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, float*
           for (int u = 0; u < KMAX; ++u) {
             const int kb = min(kb0 + u, KB2 - 1);
             raw[u] = ld_stream16(wb + ((size_t)kb * 64 + lane) * 16);
-            sw[u] = (*(const uint32_t*)(sb + ((size_t)(kb / 4) * 64 + lane) * 4) >> (8 * (kb & 3))) & 0xFFu;
+            sw[u] = (e8m0_word(sb, p.wl, p.I, tl[0], kb, lane) >> e8m0_shift(p.wl, tl[0], kb)) & 0xFFu;
           }
 #pragma unroll
           for (int u = 0; u < KMAX; ++u) {
@@ -1153,9 +1173,7 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, float*
         uint4 raw[KMAX][2];
 #pragma unroll
         for (int kb = 0; kb < KMAX; ++kb) {
-          const uint4* tl = (const uint4*)(wb + (size_t)min(kb, KB2 - 1) * 2048 + lane * 32);
-          raw[kb][0] = ld_stream16(tl);
-          raw[kb][1] = ld_stream16(tl + 1);
+          load_fp8_block(wb + (size_t)min(kb, KB2 - 1) * 2048, p.wl, lane, raw[kb][0], raw[kb][1]);
         }
 #pragma unroll
         for (int kb = 0; kb < KMAX; ++kb) {

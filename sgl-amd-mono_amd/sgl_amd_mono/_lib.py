@@ -19,8 +19,9 @@ import torch  # noqa: F401  (must precede the CDLL load, see the module docstrin
 LIB_PATH = Path(__file__).resolve().parent / "libmk2.so"
 
 MK2_OK, MK2_EINVAL, MK2_ELAUNCH, MK2_ENOSPACE = 0, 1, 2, 3
-ABI_VERSION = 2  # MK2_ABI_VERSION of the header these structures mirror
+ABI_VERSION = 3  # MK2_ABI_VERSION of the header these structures mirror
 MK2_KEYS_FP4, MK2_KEYS_FP8 = 0, 1
+MK2_WLAYOUT_TILES, MK2_WLAYOUT_AITER16 = 0, 1
 
 
 class Mk2Error(RuntimeError):
@@ -34,7 +35,7 @@ class MoeShape(ctypes.Structure):
         ("rows", c_int), ("hidden", c_int), ("n_experts", c_int), ("top_k", c_int),
         ("inter", c_int), ("router", c_int), ("expert_fmt", c_int), ("n_shared", c_int),
         ("shared_inter", c_int), ("norm", c_int), ("residual", c_int),
-        ("route_scale", c_float), ("eps", c_float),
+        ("route_scale", c_float), ("eps", c_float), ("weight_layout", c_int),
     ]
 
 

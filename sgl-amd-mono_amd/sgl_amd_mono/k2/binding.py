@@ -11,11 +11,13 @@ Mirrors the reference's weight binding and per-step cache binding
   - the experts' block scales and the rotary table;
   - the caches from SGLang's token-to-KV pool: the unscaled E4M3 latent rows
     [slots, 576] and the FP8 index pages [pages, 64, 132].
+  - the experts (block FP8 or MXFP4, routed and shared) when SGLang left them in
+    AITER's (16, 16) layout for AITER's MoE, which the expert kernels read as it is.
 - Copied once, at bind time, where a kernel takes its own tile layout:
   - the router (bf16 tiles);
   - W_o (dequantized to bf16 tiles);
-  - the routed experts (E4M3 tiles), with the fused shared expert (SGLang's
-    physical expert n_experts) split out as the shared expert.
+  - row-major experts (into E4M3 / E2M1 tiles), with the fused shared expert
+    (SGLang's physical expert n_experts) split out as the shared expert.
 """
 
 from __future__ import annotations
@@ -25,7 +27,7 @@ from types import SimpleNamespace
 import torch
 
 from . import config as C
-from .packing import pack_tiles
+from .packing import aiter_shuffle, aiter_unshuffle, pack_e8m0, pack_tiles
 from .synth import pack_bf16
 
 
@@ -48,11 +50,17 @@ def _block_dequant(w: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
     return w.view(torch.float8_e4m3fn).float() * sc
 
 
-def linear(name: str, lin, rows: int, cols: int):
+def _linear_shuffled(lin) -> bool:
+    # SGLang marks a linear it rewrote into AITER's (16, 16) layout (weights.py:142-147)
+    return bool(getattr(lin, "aiter_bpreshuffled", False) or getattr(lin.weight, "is_shuffled", False))
+
+
+def linear(name: str, lin, rows: int, cols: int, allow_shuffled: bool = False):
     """(weight bytes or bf16, f32 block scales or None, weight format) of a linear as
     SGLang keeps it after loading (the reference's _linear, weights.py:214-224), read
-    in place.  AITER's (16, 16)-shuffled layout is refused (the kernels read row-major)."""
-    if getattr(lin, "weight_shuffled", False) or getattr(lin, "is_shuffled", False):
+    in place.  AITER's (16, 16)-shuffled layout is refused unless `allow_shuffled`
+    (the front's GEMVs read row-major)."""
+    if _linear_shuffled(lin) and not allow_shuffled:
         raise ValueError(f"needs {name} row-major (not AITER's shuffled layout)")
     w = lin.weight
     if w.dtype == torch.float8_e4m3fn:
@@ -65,9 +73,13 @@ def linear(name: str, lin, rows: int, cols: int):
 
 
 def _bf16_of(name: str, lin, rows: int, cols: int) -> torch.Tensor:
-    """A linear's weight as bf16 (dequantized from block FP8): a copy for a kernel
-    that takes bf16 tiles."""
-    w, s, fmt = linear(name, lin, rows, cols)
+    """A linear's weight as bf16 (dequantized from block FP8, unshuffled from AITER's
+    layout): a copy for a kernel that takes bf16 tiles."""
+    w, s, fmt = linear(name, lin, rows, cols, allow_shuffled=True)
+    if _linear_shuffled(lin):
+        if fmt != C.WFMT_FP8_BLOCK:
+            raise ValueError(f"needs {name} row-major or block FP8 in AITER's layout")
+        w = aiter_unshuffle(w)
     return (_block_dequant(w, s) if fmt == C.WFMT_FP8_BLOCK else w.float()).to(torch.bfloat16)
 
 
@@ -130,13 +142,39 @@ def bind_mla(layer, cfg: C.MlaConfig, nope: int) -> SimpleNamespace:
     return ns
 
 
+def experts_layout(experts) -> int:
+    """The experts' weight layout as SGLang leaves them: AITER's (16, 16) shuffle when
+    it rewrote them for AITER's MoE (it marks the tensor ``is_shuffled``, as the
+    reference checks, glm53/gfx950/weights.py:142-147,310-322), else row-major."""
+    return C.WLAYOUT_AITER16 if getattr(experts.w13_weight, "is_shuffled", False) else C.WLAYOUT_TILES
+
+
+def _shared_fp8(mlp, cfg: C.MoEConfig, ns) -> None:
+    """A separate ``shared_experts`` module's block-FP8 linears in the experts' layout:
+    in place when they are in it already, else a copy."""
+    sh = mlp.shared_experts
+    H, SI = cfg.hidden, cfg.shared_inter
+    out = []
+    for name, lin, rows, cols in (("gate_up_proj", sh.gate_up_proj, 2 * SI, H), ("down_proj", sh.down_proj, H, SI)):
+        shuffled = _linear_shuffled(lin)
+        w, s, f = linear("shared_experts." + name, lin, rows, cols, allow_shuffled=True)
+        if f != C.WFMT_FP8_BLOCK:
+            raise ValueError("needs the shared expert in block FP8")
+        if cfg.weight_layout == C.WLAYOUT_AITER16:
+            out.append((w if shuffled else aiter_shuffle(w), s))
+        else:
+            out.append((pack_tiles(aiter_unshuffle(w) if shuffled else w, 32), s))
+    (ns.ws13_p, ns.ws13s), (ns.ws2_p, ns.ws2s) = out
+
+
 def bind_moe(layer, cfg: C.MoEConfig) -> SimpleNamespace:
     """The MoE weights (sgl_amd_mono.k2.ops.MoEOp's fields): the post-attention norm in
-    place, the router as bf16 tiles, the block-FP8 experts as E4M3 tiles with their
-    block scales in place; the shared expert from SGLang's fused physical expert
-    n_experts, or from a separate ``shared_experts`` module."""
-    if cfg.expert_fmt not in (C.FMT_FP8, C.FMT_W8A8):
-        raise ValueError("binds block-FP8 experts (W8A16 / W8A8 modes); SGLang keeps MXFP4 experts shuffled")
+    place, the router as bf16 tiles, and the experts -- block FP8 (W8A16 / W8A8 modes)
+    or MXFP4 (A8W4 / A16W4 / A4W4) -- in place when SGLang left them in AITER's
+    (16, 16) layout (cfg.weight_layout AITER16), else copied once into tiles; the
+    shared expert (block FP8) from SGLang's fused physical expert n_experts or from a
+    separate ``shared_experts`` module (the reference's _fp8_experts / _mxfp4_experts,
+    glm53/gfx950/weights.py:510-560)."""
     mlp = layer.mlp
     H, E, I = cfg.hidden, cfg.n_experts, cfg.inter
     ns = SimpleNamespace(cfg=cfg)
@@ -150,32 +188,51 @@ def bind_moe(layer, cfg: C.MoEConfig) -> SimpleNamespace:
     if cfg.router == C.ROUTER_SIGMOID_BIAS:
         ns.bias = _need("e_score_correction_bias", mlp.gate.e_score_correction_bias, (E,), (torch.float32,))
     ex = mlp.experts
+    if experts_layout(ex) != cfg.weight_layout:
+        raise ValueError(f"the experts' layout {experts_layout(ex)} differs from the config's {cfg.weight_layout}")
+    aiter = cfg.weight_layout == C.WLAYOUT_AITER16
     phys = ex.w13_weight.shape[0]
     fused_shared = phys == E + 1
     if phys not in (E, E + 1):
         raise ValueError(f"needs {E} routed experts (+1 fused shared), got {phys}")
-    w13 = _need("w13_weight", ex.w13_weight, (phys, 2 * I, H), (torch.float8_e4m3fn,))
-    s13 = _need("w13_weight_scale_inv", ex.w13_weight_scale_inv, (phys, 2 * I // 128, H // 128), (torch.float32,))
-    w2 = _need("w2_weight", ex.w2_weight, (phys, H, I), (torch.float8_e4m3fn,))
-    s2 = _need("w2_weight_scale_inv", ex.w2_weight_scale_inv, (phys, H // 128, I // 128), (torch.float32,))
-    ns.w13q, ns.w2q = _fp8_bytes(w13[:E]), _fp8_bytes(w2[:E])
-    ns.w13s, ns.w2s = s13[:E], s2[:E]
-    ns.w13_p, ns.s13_p = pack_tiles(ns.w13q, 32), ns.w13s
-    ns.w2_p, ns.s2_p = pack_tiles(ns.w2q, 32), ns.w2s
+    if cfg.expert_fmt in C.FP4_WEIGHT_FMTS:
+        u8 = (torch.uint8,)
+        w13 = _need("w13_weight", ex.w13_weight, (phys, 2 * I, H // 2), u8)
+        s13 = _need("w13_weight_scale", ex.w13_weight_scale.view(torch.uint8), (phys, 2 * I, H // 32), u8)
+        w2 = _need("w2_weight", ex.w2_weight, (phys, H, I // 2), u8)
+        s2 = _need("w2_weight_scale", ex.w2_weight_scale.view(torch.uint8), (phys, H, I // 32), u8)
+        if fused_shared:
+            raise ValueError("MXFP4 experts with the shared expert fused in: the shared expert runs in block FP8")
+        if aiter:  # in place: AITER's E2M1 bytes are the tiles; its E8M0 order is read as it is
+            ns.w13_p, ns.s13_p, ns.w2_p, ns.s2_p = w13, s13, w2, s2
+        else:
+            ns.w13_p, ns.s13_p = pack_tiles(w13, 16), pack_e8m0(s13)
+            ns.w2_p, ns.s2_p = pack_tiles(w2, 16), pack_e8m0(s2)
+        ns.w13q, ns.w13s, ns.w2q, ns.w2s = w13, s13, w2, s2
+    else:
+        if cfg.expert_fmt not in (C.FMT_FP8, C.FMT_W8A8):
+            raise ValueError(f"unknown expert mode {cfg.expert_fmt}")
+        w13 = _need("w13_weight", ex.w13_weight, (phys, 2 * I, H), (torch.float8_e4m3fn,))
+        s13 = _need("w13_weight_scale_inv", ex.w13_weight_scale_inv, (phys, 2 * I // 128, H // 128), (torch.float32,))
+        w2 = _need("w2_weight", ex.w2_weight, (phys, H, I), (torch.float8_e4m3fn,))
+        s2 = _need("w2_weight_scale_inv", ex.w2_weight_scale_inv, (phys, H // 128, I // 128), (torch.float32,))
+        ns.w13q, ns.w2q = _fp8_bytes(w13[:E]), _fp8_bytes(w2[:E])
+        ns.w13s, ns.w2s = s13[:E], s2[:E]
+        ns.s13_p, ns.s2_p = ns.w13s, ns.w2s
+        if aiter:  # in place (views of the first E experts)
+            ns.w13_p, ns.w2_p = ns.w13q, ns.w2q
+        else:
+            ns.w13_p, ns.w2_p = pack_tiles(ns.w13q, 32), pack_tiles(ns.w2q, 32)
     if cfg.n_shared:
         if fused_shared:
             ns.ws13q, ns.ws13s = _fp8_bytes(w13[E]), s13[E]
             ns.ws2q, ns.ws2s = _fp8_bytes(w2[E]), s2[E]
+            ns.ws13_p = ns.ws13q if aiter else pack_tiles(ns.ws13q, 32)
+            ns.ws2_p = ns.ws2q if aiter else pack_tiles(ns.ws2q, 32)
         else:
-            sh = mlp.shared_experts
-            SI = cfg.shared_inter
-            ns.ws13q, ns.ws13s, fa = linear("shared_experts.gate_up_proj", sh.gate_up_proj, 2 * SI, H)
-            ns.ws2q, ns.ws2s, fb = linear("shared_experts.down_proj", sh.down_proj, H, SI)
-            if {fa, fb} != {C.WFMT_FP8_BLOCK}:
-                raise ValueError("needs the shared expert in block FP8")
-        ns.ws13_p, ns.ws2_p = pack_tiles(ns.ws13q, 32), pack_tiles(ns.ws2q, 32)
+            _shared_fp8(mlp, cfg, ns)
     else:
-        ns.ws13q = ns.ws13s = ns.ws2q = ns.ws2s = ns.ws13_p = ns.ws2_p = None
+        ns.ws13s = ns.ws2s = ns.ws13_p = ns.ws2_p = None
     return ns
 
 

@@ -27,6 +27,9 @@ FP4_WEIGHT_FMTS = (FMT_MXFP4, FMT_A16W4, FMT_A4W4)
 # index cache formats (MK2_KEYS_*)
 KEYS_FP4 = 0  # SGLang's FP4 index plane: E2M1 codes + E8M0 per 32 dims, two tensors
 KEYS_FP8 = 1  # SGLang's DSA index cache: uint8 [pages, 64, 132], E4M3 + f32 scale a key
+# the expert weights' layouts (MK2_WLAYOUT_*)
+WLAYOUT_TILES = 0  # this build's tile packing (k2/packing.py pack_tiles / pack_e8m0)
+WLAYOUT_AITER16 = 1  # AITER's (16, 16) shuffle + e8m0_shuffle, as SGLang leaves them for AITER
 
 MAX_ROWS = 32  # decode rows a launch serves (verify: 8 requests x 4 draft tokens)
 
@@ -42,6 +45,7 @@ class MoEConfig:
     expert_fmt: int
     n_shared: int
     shared_inter: int
+    weight_layout: int = WLAYOUT_TILES
 
     def validate(self, rows: int) -> None:
         """The rules of the C side (mk2_moe_workspace_bytes), checked before any call."""
@@ -64,6 +68,10 @@ class MoEConfig:
             raise ValueError("at most one shared expert")
         if self.n_shared and (self.shared_inter < 128 or self.shared_inter % 128 or self.shared_inter > 4096):
             raise ValueError(f"shared_inter must be a multiple of 128 in [128, 4096], got {self.shared_inter}")
+        if self.weight_layout not in (WLAYOUT_TILES, WLAYOUT_AITER16):
+            raise ValueError(f"unknown weight_layout {self.weight_layout}")
+        if self.weight_layout == WLAYOUT_AITER16 and self.expert_fmt in FP4_WEIGHT_FMTS and self.inter % 256:
+            raise ValueError(f"AITER's E8M0 layout needs inter a multiple of 256, got {self.inter}")
 
 
 @dataclass(frozen=True)

@@ -43,7 +43,7 @@ class MoEOp:
         self.shape = _lib.MoeShape(
             rows, cfg.hidden, cfg.n_experts, cfg.top_k, cfg.inter, cfg.router,
             cfg.expert_fmt, cfg.n_shared, cfg.shared_inter, int(norm), int(residual),
-            cfg.route_scale, eps,
+            cfg.route_scale, eps, cfg.weight_layout,
         )
         if norm:
             _need(w.gamma, "gamma", torch.bfloat16, (cfg.hidden,))

@@ -14,6 +14,10 @@ the byte of the k-block with the MFMA's scale byte-select.
 
 The reference packs for the same reason with its own permutations
 (glm53/gfx950/packing.py:29-133, AITER's (16, 16) shuffle glm53/check.py:383-389).
+
+The experts can also be read in AITER's layouts, as SGLang leaves them for AITER's MoE
+(``aiter_shuffle``, ``e8m0_shuffle`` below): for E2M1 bytes that layout is byte for
+byte the tile packing; E4M3 tiles keep a lane's two 16-byte halves 256 bytes apart.
 """
 
 from __future__ import annotations
@@ -62,3 +66,55 @@ def unpack_e8m0(p: torch.Tensor, k32: int) -> torch.Tensor:
     t = p.reshape(*lead, nt, groups, 4, 16, 4)  # nt, G, g, row16, j
     t = t.permute(*range(len(lead)), -5, -2, -4, -1, -3)  # nt, row16, G, j, g
     return t.reshape(*lead, nt * 16, groups * 16)[..., :k32].contiguous()
+
+
+def aiter_shuffle(w: torch.Tensor) -> torch.Tensor:
+    """Row-major bytes [..., N, K_bytes] in AITER's (16, 16) layout, as its
+    shuffle_weight(w, (16, 16)) leaves 1-byte elements (E4M3, or E2M1 pairs):
+    [..., N/16, K_bytes/32, 2, 16 rows, 16 B], the inverse of the reference's unshuffle
+    (glm53/check.py:383-389)."""
+    b = w.contiguous().view(torch.uint8)
+    *lead, n, kb = b.shape
+    if n % 16 or kb % 32:
+        raise ValueError(f"cannot shuffle [{n}, {kb}] bytes in (16, 16) blocks")
+    d = len(lead)
+    t = b.reshape(*lead, n // 16, 16, kb // 32, 2, 16)  # [.., nt, row, c, h, byte]
+    t = t.permute(*range(d), d, d + 2, d + 3, d + 1, d + 4)  # [.., nt, c, h, row, byte]
+    return t.reshape(*lead, n, kb).contiguous()
+
+
+def aiter_unshuffle(w: torch.Tensor) -> torch.Tensor:
+    """Inverse of aiter_shuffle: AITER's (16, 16) bytes -> row-major [..., N, K_bytes]."""
+    b = w.contiguous().view(torch.uint8)
+    *lead, n, kb = b.shape
+    d = len(lead)
+    t = b.reshape(*lead, n // 16, kb // 32, 2, 16, 16)  # [.., nt, c, h, row, byte]
+    t = t.permute(*range(d), d, d + 3, d + 1, d + 2, d + 4)  # [.., nt, row, c, h, byte]
+    return t.reshape(*lead, n, kb).contiguous()
+
+
+def e8m0_shuffle(s: torch.Tensor) -> torch.Tensor:
+    """E8M0 codes [..., N, K/32] in the order of AITER's e8m0_shuffle, its rows counted
+    across the leading dims (as SGLang shuffles an [E, N, K/32] tensor flattened to
+    [E * N, K/32]): view(rows/32, 2, 16, C/8, 2, 4).permute(0, 3, 5, 2, 4, 1) with C =
+    K/32 (qwen38_a95b_mxfp4/gfx950/layout.py:84-91), so that code (row, col) sits at
+    ((((row/32 * C/8 + col/8) * 4 + col%4) * 16 + row%16) * 2 + col/4%2) * 2 + row/16%2.
+    Needs the rows a multiple of 32 and C of 8."""
+    *lead, n, c = s.shape
+    rows = n
+    for x in lead:
+        rows *= x
+    if rows % 32 or c % 8:
+        raise ValueError(f"e8m0_shuffle needs rows % 32 == 0 and K/32 % 8 == 0, got {rows} x {c}")
+    t = s.contiguous().view(torch.uint8).reshape(rows // 32, 2, 16, c // 8, 2, 4)
+    return t.permute(0, 3, 5, 2, 4, 1).reshape(*lead, n, c).contiguous()
+
+
+def e8m0_unshuffle(s: torch.Tensor) -> torch.Tensor:
+    """Inverse of e8m0_shuffle."""
+    *lead, n, c = s.shape
+    rows = n
+    for x in lead:
+        rows *= x
+    t = s.contiguous().view(torch.uint8).reshape(rows // 32, c // 8, 4, 16, 2, 2)  # r32, c8, f, b, d, a
+    return t.permute(0, 5, 3, 1, 4, 2).reshape(*lead, n, c).contiguous()

@@ -248,7 +248,12 @@ def _build(model, hf_config, ctx):
     wfmt = C.WFMT_FP8_BLOCK if first.dtype == torch.float8_e4m3fn else C.WFMT_BF16
     # SGLang's DSA index cache holds FP8 pages; its experts' dtype names their mode
     efmt = C.FMT_FP8 if layer0.mlp.experts.w13_weight.dtype == torch.float8_e4m3fn else C.FMT_MXFP4
-    cfg = replace(cfg, moe=replace(cfg.moe, expert_fmt=efmt), indexer=replace(cfg.indexer, keys=C.KEYS_FP8))
+    # experts SGLang rewrote for AITER's MoE are read in place in that layout
+    from .binding import experts_layout
+
+    layout = experts_layout(layer0.mlp.experts)
+    cfg = replace(cfg, moe=replace(cfg.moe, expert_fmt=efmt, weight_layout=layout),
+                  indexer=replace(cfg.indexer, keys=C.KEYS_FP8))
     rows = layer0.self_attn.rotary_emb.cos_sin_cache.shape[0]
     front = front_config_from_hf(hf_config, wfmt)
     front = replace(front, max_position=min(front.max_position, rows - 1))

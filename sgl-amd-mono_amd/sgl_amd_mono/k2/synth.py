@@ -13,12 +13,13 @@ kernels stream.  Generation runs on ``device`` with a torch.Generator seeded the
 
 from __future__ import annotations
 
+from dataclasses import replace
 from types import SimpleNamespace
 
 import torch
 
 from . import config as C
-from .packing import pack_e8m0, pack_tiles
+from .packing import aiter_shuffle, e8m0_shuffle, pack_e8m0, pack_tiles
 from .quant import quant_fp8_block, quant_fp8_rows, quant_index_fp8, quant_mxfp4
 
 WEIGHT_STD = 0.02
@@ -81,6 +82,23 @@ def make_moe(cfg: C.MoEConfig, rows: int, seed: int, device, norm: bool = False)
     else:
         ns.ws13q = ns.ws13s = ns.ws2q = ns.ws2s = ns.ws13_p = ns.ws2_p = None
     return ns
+
+
+def moe_in_layout(ns, layout: int):
+    """make_moe's weights (routed and shared experts) in another layout (C.WLAYOUT_*):
+    the same codes and scales re-laid; the router and the rows are shared."""
+    if layout == C.WLAYOUT_TILES:
+        return ns
+    if layout != C.WLAYOUT_AITER16:
+        raise ValueError(f"unknown layout {layout}")
+    out = SimpleNamespace(**vars(ns))
+    out.w13_p, out.w2_p = aiter_shuffle(ns.w13q), aiter_shuffle(ns.w2q)
+    if ns.cfg.expert_fmt in C.FP4_WEIGHT_FMTS:
+        out.s13_p, out.s2_p = e8m0_shuffle(ns.w13s), e8m0_shuffle(ns.w2s)
+    if ns.ws13q is not None:
+        out.ws13_p, out.ws2_p = aiter_shuffle(ns.ws13q), aiter_shuffle(ns.ws2q)
+    out.cfg = replace(ns.cfg, weight_layout=layout)
+    return out
 
 
 def _page_table(g, requests: int, pages_per_req: int, device) -> torch.Tensor:

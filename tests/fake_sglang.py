@@ -5,7 +5,10 @@ The attribute names, dtypes and memory layouts are those the reference binds
 - block-FP8 linears carry ``weight`` (E4M3) and ``weight_scale_inv``;
 - ``w_kc`` / ``w_vc`` are transposed views of [heads][kv_lora][nope] and
   [heads][v][kv_lora] memory;
-- the experts hold the shared expert fused as physical expert n_experts;
+- the experts hold the shared expert fused as physical expert n_experts (block FP8),
+  or are MXFP4 (E2M1 bytes + E8M0 codes) beside a block-FP8 ``shared_experts``
+  module; with ``shuffled`` they are in AITER's (16, 16) layout with e8m0_shuffle'd
+  codes and marked ``is_shuffled``, as SGLang leaves them for AITER's MoE;
 - the token-to-KV pool gives E4M3 rows [slots, 1, 576] and FP8 index pages.
 The caches are filled with a random history, so a step's rows have context.
 """
@@ -44,7 +47,48 @@ def _norm(g, n, device):
     return SimpleNamespace(weight=(1 + 0.1 * torch.randn(n, generator=g, device=device)).to(torch.bfloat16))
 
 
-def make_model(seed: int, device, hf=HF, vocab=VOCAB, layers=LAYERS):
+def _mark(t: torch.Tensor) -> torch.Tensor:
+    t.is_shuffled = True  # what AITER's shuffle_weight sets on the tensor it returns
+    return t
+
+
+def _experts(g, hf, device, experts: str, shuffled: bool):
+    """SGLang's fused-MoE parameters: block FP8 with the shared expert fused as expert
+    E, or MXFP4 (then the shared expert is a separate module, returned second)."""
+    from sgl_amd_mono.k2.packing import aiter_shuffle, e8m0_shuffle
+    from sgl_amd_mono.k2.quant import quant_mxfp4
+
+    H, E, I = hf.hidden_size, hf.n_routed_experts, hf.moe_intermediate_size
+    if experts == "fp8":
+        w13 = torch.empty(E + 1, 2 * I, H, dtype=torch.uint8, device=device)
+        s13 = torch.empty(E + 1, 2 * I // 128, H // 128, device=device)
+        w2 = torch.empty(E + 1, H, I, dtype=torch.uint8, device=device)
+        s2 = torch.empty(E + 1, H // 128, I // 128, device=device)
+        for e in range(E + 1):
+            a, b = _fp8_linear(g, 2 * I, H, device), _fp8_linear(g, H, I, device)
+            w13[e], s13[e] = a.weight.view(torch.uint8), a.weight_scale_inv
+            w2[e], s2[e] = b.weight.view(torch.uint8), b.weight_scale_inv
+        if shuffled:
+            w13, w2 = aiter_shuffle(w13), aiter_shuffle(w2)
+        w13, w2 = w13.view(torch.float8_e4m3fn), w2.view(torch.float8_e4m3fn)
+        if shuffled:
+            w13, w2 = _mark(w13), _mark(w2)
+        return SimpleNamespace(w13_weight=w13, w13_weight_scale_inv=s13, w2_weight=w2, w2_weight_scale_inv=s2), None
+    w13 = torch.empty(E, 2 * I, H // 2, dtype=torch.uint8, device=device)
+    s13 = torch.empty(E, 2 * I, H // 32, dtype=torch.uint8, device=device)
+    w2 = torch.empty(E, H, I // 2, dtype=torch.uint8, device=device)
+    s2 = torch.empty(E, H, I // 32, dtype=torch.uint8, device=device)
+    for e in range(E):
+        w13[e], s13[e] = quant_mxfp4(0.02 * torch.randn(2 * I, H, generator=g, device=device))
+        w2[e], s2[e] = quant_mxfp4(0.02 * torch.randn(H, I, generator=g, device=device))
+    if shuffled:
+        w13, s13, w2, s2 = _mark(aiter_shuffle(w13)), e8m0_shuffle(s13), _mark(aiter_shuffle(w2)), e8m0_shuffle(s2)
+    SI = I * hf.n_shared_experts
+    shared = SimpleNamespace(gate_up_proj=_fp8_linear(g, 2 * SI, H, device), down_proj=_fp8_linear(g, H, SI, device))
+    return SimpleNamespace(w13_weight=w13, w13_weight_scale=s13, w2_weight=w2, w2_weight_scale=s2), shared
+
+
+def make_model(seed: int, device, hf=HF, vocab=VOCAB, layers=LAYERS, experts: str = "fp8", shuffled: bool = False):
     from sgl_amd_mono.k2 import synth
 
     g = _gen(seed, device)
@@ -71,20 +115,14 @@ def make_model(seed: int, device, hf=HF, vocab=VOCAB, layers=LAYERS):
                     weight=(0.02 * torch.randn(IH, H, generator=g, device=device)).to(torch.bfloat16)),
             ),
         )
-        w13 = torch.empty(E + 1, 2 * I, H, dtype=torch.uint8, device=device)
-        s13 = torch.empty(E + 1, 2 * I // 128, H // 128, device=device)
-        w2 = torch.empty(E + 1, H, I, dtype=torch.uint8, device=device)
-        s2 = torch.empty(E + 1, H // 128, I // 128, device=device)
-        for e in range(E + 1):
-            a, b = _fp8_linear(g, 2 * I, H, device), _fp8_linear(g, H, I, device)
-            w13[e], s13[e] = a.weight.view(torch.uint8), a.weight_scale_inv
-            w2[e], s2[e] = b.weight.view(torch.uint8), b.weight_scale_inv
+        ex, shared = _experts(g, hf, device, experts, shuffled)
         mlp = SimpleNamespace(
             gate=SimpleNamespace(weight=(0.02 * torch.randn(E, H, generator=g, device=device)).to(torch.bfloat16),
                                  e_score_correction_bias=0.05 * torch.randn(E, generator=g, device=device)),
-            experts=SimpleNamespace(w13_weight=w13.view(torch.float8_e4m3fn), w13_weight_scale_inv=s13,
-                                    w2_weight=w2.view(torch.float8_e4m3fn), w2_weight_scale_inv=s2),
+            experts=ex,
         )
+        if shared is not None:
+            mlp.shared_experts = shared
         mods.append(SimpleNamespace(self_attn=attn, mlp=mlp, input_layernorm=_norm(g, H, device),
                                     post_attention_layernorm=_norm(g, H, device)))
     emb = torch.randn(vocab, H, generator=g, device=device).to(torch.bfloat16)

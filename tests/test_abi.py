@@ -33,7 +33,7 @@ def test_every_declared_symbol_is_exported():
     assert len(names) >= 10
     for n in names:
         assert hasattr(L, n), n
-    assert L.mk2_abi_version() == _l.ABI_VERSION == 2
+    assert L.mk2_abi_version() == _l.ABI_VERSION == 3
 
 
 def test_ctypes_layouts_match_the_header():
@@ -82,7 +82,8 @@ def test_workspace_queries_and_shape_errors():
     assert L.mk2_moe_workspace_bytes(ctypes.byref(_moe_shape(_l)), ctypes.byref(n)) == 0
     assert n.value > 0
     for bad in (dict(rows=0), dict(rows=33), dict(hidden=1000), dict(n_experts=100), dict(top_k=9),
-                dict(router=5), dict(expert_fmt=7), dict(inter=100)):
+                dict(router=5), dict(expert_fmt=7), dict(inter=100), dict(weight_layout=2),
+                dict(weight_layout=1, inter=128)):
         rc = L.mk2_moe_workspace_bytes(ctypes.byref(_moe_shape(_l, **bad)), ctypes.byref(n))
         assert rc == _l.MK2_EINVAL, bad
         assert L.mk2_last_error().decode().startswith("moe:"), bad

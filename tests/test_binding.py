@@ -72,7 +72,7 @@ def test_refusals(model):
     cfg, fc = _cfgs()
     L = model.model.layers[0]
     bad = SimpleNamespace(weight=L.self_attn.q_b_proj.weight, weight_scale_inv=L.self_attn.q_b_proj.weight_scale_inv,
-                          weight_shuffled=True)
+                          aiter_bpreshuffled=True)
     with pytest.raises(ValueError, match="shuffled"):
         binding.linear("q_b_proj", bad, bad.weight.shape[0], bad.weight.shape[1])
     with pytest.raises(ValueError, match="q_b_proj"):
@@ -81,8 +81,10 @@ def test_refusals(model):
         binding.bind_front(L, replace(fc, weight_fmt=0))
     from sgl_amd_mono.k2 import config as C
 
-    with pytest.raises(ValueError, match="block-FP8"):
+    with pytest.raises(ValueError, match="w13_weight"):  # block-FP8 experts bound as MXFP4
         binding.bind_moe(L, replace(cfg.moe, expert_fmt=C.FMT_MXFP4))
+    with pytest.raises(ValueError, match="layout"):  # row-major experts bound as AITER's
+        binding.bind_moe(L, replace(cfg.moe, weight_layout=C.WLAYOUT_AITER16))
 
 
 def test_caches_are_views_of_the_pool():
@@ -93,3 +95,51 @@ def test_caches_are_views_of_the_pool():
     assert kv.shape == (8 * 64, 576) and kv.dtype == torch.uint8
     assert kv.data_ptr() == pool.kv[0].data_ptr()
     assert idx.shape == (8, 64, 132) and idx.data_ptr() == pool.idx[0].data_ptr()
+
+
+def test_shuffled_fp8_experts_are_read_in_place():
+    """Block-FP8 experts SGLang rewrote for AITER's MoE (is_shuffled): bound in place,
+    routed and the fused shared expert, as views of SGLang's tensors; the row-major
+    model's experts are the same codes, copied into tiles."""
+    from sgl_amd_mono.k2 import binding
+    from sgl_amd_mono.k2 import config as C
+    from sgl_amd_mono.k2.packing import aiter_unshuffle, pack_tiles
+
+    cfg, _ = _cfgs()
+    row = F.make_model(3, torch.device("cpu"), layers=1).model.layers[0]
+    shf = F.make_model(3, torch.device("cpu"), layers=1, shuffled=True).model.layers[0]
+    assert binding.experts_layout(row.mlp.experts) == C.WLAYOUT_TILES
+    assert binding.experts_layout(shf.mlp.experts) == C.WLAYOUT_AITER16
+    E = cfg.moe.n_experts
+    a = binding.bind_moe(shf, replace(cfg.moe, weight_layout=C.WLAYOUT_AITER16))
+    ex = shf.mlp.experts
+    assert a.w13_p.data_ptr() == ex.w13_weight.data_ptr() and a.w2_p.data_ptr() == ex.w2_weight.data_ptr()
+    assert a.ws13_p.data_ptr() == ex.w13_weight[E].data_ptr()
+    t = binding.bind_moe(row, cfg.moe)
+    assert torch.equal(aiter_unshuffle(a.w13_p), t.w13q) and torch.equal(aiter_unshuffle(a.ws2_p), t.ws2q)
+    assert torch.equal(t.w13_p, pack_tiles(t.w13q, 32))
+
+
+def test_mxfp4_experts_in_both_layouts():
+    """MXFP4 experts (E2M1 bytes + E8M0 codes, the shared expert a separate block-FP8
+    module): AITER's layout in place -- its bytes are the tiles -- and row-major ones
+    copied into tiles, with the same codes; the separate shared expert is brought into
+    the experts' layout."""
+    from sgl_amd_mono.k2 import binding
+    from sgl_amd_mono.k2 import config as C
+    from sgl_amd_mono.k2.packing import aiter_shuffle, e8m0_shuffle, pack_e8m0, pack_tiles
+
+    cfg, _ = _cfgs()
+    mc = replace(cfg.moe, expert_fmt=C.FMT_MXFP4)
+    row = F.make_model(4, torch.device("cpu"), layers=1, experts="mxfp4").model.layers[0]
+    shf = F.make_model(4, torch.device("cpu"), layers=1, experts="mxfp4", shuffled=True).model.layers[0]
+    t = binding.bind_moe(row, mc)
+    a = binding.bind_moe(shf, replace(mc, weight_layout=C.WLAYOUT_AITER16))
+    ex = shf.mlp.experts
+    assert a.w13_p.data_ptr() == ex.w13_weight.data_ptr() and a.s2_p.data_ptr() == ex.w2_weight_scale.data_ptr()
+    assert torch.equal(t.w13_p.flatten(), a.w13_p.flatten())  # E2M1: the same bytes
+    assert torch.equal(e8m0_shuffle(t.w2s), a.s2_p) and torch.equal(pack_e8m0(t.w2s), t.s2_p)
+    sh = row.mlp.shared_experts
+    assert torch.equal(t.ws13_p, pack_tiles(sh.gate_up_proj.weight.view(torch.uint8), 32))
+    assert torch.equal(a.ws13_p, aiter_shuffle(shf.mlp.shared_experts.gate_up_proj.weight.view(torch.uint8)))
+    assert t.ws13s.data_ptr() == sh.gate_up_proj.weight_scale_inv.data_ptr()

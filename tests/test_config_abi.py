@@ -30,7 +30,7 @@ def _py_ok(cfg, rows):
 
 def _moe_c_ok(_l, L, cfg, rows):
     s = _l.MoeShape(rows, cfg.hidden, cfg.n_experts, cfg.top_k, cfg.inter, cfg.router, cfg.expert_fmt,
-                    cfg.n_shared, cfg.shared_inter, 1, 1, cfg.route_scale, 1e-6)
+                    cfg.n_shared, cfg.shared_inter, 1, 1, cfg.route_scale, 1e-6, cfg.weight_layout)
     n = ctypes.c_size_t()
     return L.mk2_moe_workspace_bytes(ctypes.byref(s), ctypes.byref(n)) == 0
 
@@ -38,13 +38,13 @@ def _moe_c_ok(_l, L, cfg, rows):
 def test_moe_validate_matches_c():
     _l, L = _lib()
     seen = {True: 0, False: 0}
-    for hidden, E, k, inter, fmt, ns, si, rows in itertools.product(
+    for hidden, E, k, inter, fmt, ns, si, rows, wl in itertools.product(
         (256, 512, 2048, 6144, 7168 + 256), (16, 48, 64, 96, 192, 256, 320), (0, 1, 8, 9),
         (32, 96, 128, 256, 768, 1024, 2048, 4096, 8192), (C.FMT_FP8, C.FMT_MXFP4), (0, 1),
-        (32, 128, 768, 4224), (1, 8, 32, 33),
+        (32, 128, 768, 4224), (1, 8, 32, 33), (C.WLAYOUT_TILES, C.WLAYOUT_AITER16, 2),
     ):
         cfg = replace(C.C2_MOE, hidden=hidden, n_experts=E, top_k=k, inter=inter, expert_fmt=fmt,
-                      n_shared=ns, shared_inter=si)
+                      n_shared=ns, shared_inter=si, weight_layout=wl)
         py, c = _py_ok(cfg, rows), _moe_c_ok(_l, L, cfg, rows)
         assert py == c, (cfg, rows, py, c, L.mk2_last_error())
         seen[py] += 1

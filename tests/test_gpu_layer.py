@@ -7,6 +7,8 @@ boundary.  The parity cases draw the residual rows h ~ N(0, (1/128)^2): with h ~
 1) the bf16 rounding of h + o W_o^T alone would be about 10 % of the attention term,
 and a check of attn - h could not see the attention's own errors."""
 
+from types import SimpleNamespace
+
 import pytest
 import torch
 
@@ -233,3 +235,30 @@ def test_persistent_layer_fail_stop():
             assert torch.equal(o, ref)
     op()
     op.check()  # a clean launch: no error
+
+
+@pytest.mark.parametrize("rows", [8, 32])
+def test_layer_aiter_layout_bits(rows):
+    """The persistent layer with its experts in AITER's (16, 16) layout gives the
+    tile layout's bits."""
+    from dataclasses import replace
+
+    from sgl_amd_mono.k2 import config as C
+    from sgl_amd_mono.k2 import synth
+    from sgl_amd_mono.k2.ops import LayerOp
+
+    dev = _dev()
+    cfg = replace(C.C5_LAYER, mla=replace(C.C5_LAYER.mla, context=8192),
+                  indexer=replace(C.C5_LAYER.indexer, context=8192))
+    L = synth.make_layer(cfg, rows, 560 + rows, dev)
+    La = SimpleNamespace(**vars(L))
+    La.moe = synth.moe_in_layout(L.moe, C.WLAYOUT_AITER16)
+    cfga = replace(cfg, moe=La.moe.cfg)
+    outs = []
+    for c, LL in ((cfg, L), (cfga, La)):
+        status = torch.zeros(1, dtype=torch.int32, device=dev)
+        out = LayerOp(c, LL, rows, device=dev)(status=status)
+        torch.cuda.synchronize()
+        assert int(status.item()) == 0
+        outs.append(cpu(out))
+    assert torch.equal(outs[0], outs[1])

@@ -217,3 +217,31 @@ def test_moe_modes_norm_residual(fmt):
     cfg = replace(base, expert_fmt=getattr(C, "FMT_" + fmt))
     w, out, logits, ids, wts = _run(cfg, 8, seed=11 + cfg.expert_fmt, norm=True, residual=True)
     _check(cfg, w, out, logits, ids, wts, norm=True, residual=True)
+
+
+@pytest.mark.parametrize("fmt,rows", [("FP8", 4), ("W8A8", 8), ("MXFP4", 8), ("A16W4", 8), ("A4W4", 8),
+                                      ("MXFP4", 32), ("FP8", 32)])
+def test_moe_aiter_layout_bits(fmt, rows):
+    """The experts (routed and shared) read in place in AITER's (16, 16) layout, as
+    SGLang leaves them for AITER's MoE, give the same bits as the tile layout: the
+    layouts change only where the kernels load a lane's bytes and scale codes."""
+    from dataclasses import replace
+
+    from sgl_amd_mono.k2 import config as C
+    from sgl_amd_mono.k2 import synth
+    from sgl_amd_mono.k2.ops import MoEOp
+
+    dev = _dev()
+    f = getattr(C, "FMT_" + fmt)
+    cfg = replace(C.C2_MOE if f in C.FP4_WEIGHT_FMTS else C.C1_MOE, expert_fmt=f)
+    w = synth.make_moe(cfg, rows, 720 + 10 * f + rows, dev, norm=True)
+    wa = synth.moe_in_layout(w, C.WLAYOUT_AITER16)
+    assert not torch.equal(wa.ws13_p, w.ws13_p)  # the shared expert is re-laid too
+    outs = []
+    for c, ww in ((cfg, w), (wa.cfg, wa)):
+        ids = torch.empty(rows, cfg.top_k, dtype=torch.int32, device=dev)
+        out = MoEOp(c, ww, rows, norm=True, residual=True, eps=1e-6)(w.x, topk_ids=ids)
+        outs.append((cpu(out), cpu(ids)))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0][1], outs[1][1])
+    assert torch.equal(outs[0][0], outs[1][0])

@@ -73,3 +73,32 @@ def test_routed_decode_step(rows):
         assert int(L.idx.ctx_len[r]) == int(st.positions[r]) + 1
     want, _ = TailOp(fwd.tail_cfg, fwd.g_norm, fwd.w_head, rows, device=dev)(out)
     assert torch.equal(logits, want)
+
+
+@pytest.mark.parametrize("experts", ["fp8", "mxfp4"])
+def test_shuffled_experts_step_matches_row_major(experts):
+    """The same model with its experts in AITER's (16, 16) layout (read in place) and
+    row-major (copied into tiles): one routed step gives the same logits and caches."""
+    from sgl_amd_mono import _registry as reg
+    from sgl_amd_mono.k2 import config as C
+    from sgl_amd_mono.k2 import spec
+
+    dev = _dev()
+    rows = 4
+    pages = rows * (F.HF.max_context // 64) + 8
+    res = []
+    for shuffled in (False, True):
+        lm = F.make_model(21, dev, experts=experts, shuffled=shuffled)
+        pool = F.Pool(F.LAYERS, pages, dev, 22)
+        st = F.make_step(rows, F.HF.max_context, pages, dev, 23)
+        ctx = SimpleNamespace(device=dev, pool_of=lambda fb, p=pool: p,
+                              page_table_of=lambda fb, n, s=st: s.page_table[:n])
+        fwd = spec.SPEC.build(lm, F.HF, ctx)
+        assert fwd.cfg.moe.weight_layout == (C.WLAYOUT_AITER16 if shuffled else C.WLAYOUT_TILES)
+        assert fwd.cfg.moe.expert_fmt == (C.FMT_FP8 if experts == "fp8" else C.FMT_MXFP4)
+        logits = fwd.forward(reg.Plan(key=reg.ShapeKey("decode", rows, 1)), st.input_ids, st.positions,
+                             st.forward_batch)
+        torch.cuda.synchronize()
+        res.append((cpu(logits), [cpu(t) for t in pool.kv]))
+    assert torch.equal(res[0][0], res[1][0])
+    assert all(torch.equal(a, b) for a, b in zip(res[0][1], res[1][1]))

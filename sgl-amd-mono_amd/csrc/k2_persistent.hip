@@ -78,7 +78,7 @@ union K2Lds {
   } up;
   struct {
     float red[(K2_NT / 64) * 2 * 64 * 4];
-    int act[256];
+    int act[512];  // the slots' experts, then (compacted rows) their row counts
     float xres[16 * 2 * 32];
   } down;
   RouterLds router;
@@ -271,7 +271,8 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
     const int up_total = up_r + up_sh;
     if (b == (base + (up_total < G ? up_total : G - 1)) % G) {
       k2_stamp(p, 3 * st);
-      if (!moe_route<K2_NT>(p.moe, S.route, tp, [&](int i) { k2_stamp(p, 3 * K2_STAGES + i); })) return;
+      if (!moe_route<K2_NT, kCompact<NCG, FMT>>(p.moe, S.route, tp, [&](int i) { k2_stamp(p, 3 * K2_STAGES + i); }))
+        return;
       k2_stamp(p, 3 * st + 1);
       k2_signal(p, SY_ROUTE);
       k2_stamp(p, 3 * st + 2);

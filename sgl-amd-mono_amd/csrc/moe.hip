@@ -16,9 +16,10 @@ __global__ __launch_bounds__(ROUTER_NT) void k_moe_router(MoeDev p) {
   moe_router<ROUTER_NT, NCG, FMT>(p, blockIdx.x, blockIdx.y, lds, 0u);
 }
 
+template <bool CMP>
 __global__ __launch_bounds__(512) void k_moe_route(MoeDev p) {
   __shared__ RouteLds lds;
-  moe_route<512>(p, lds, TagPoll{0u, 0, nullptr});
+  moe_route<512, CMP>(p, lds, TagPoll{0u, 0, nullptr});
 }
 
 template <int NCG, int FMT>
@@ -31,7 +32,7 @@ __global__ __launch_bounds__(MOE_NT) void k_moe_upgate(MoeDev p) {
 template <int NCG, int FMT>
 __global__ __launch_bounds__(MOE_NT) void k_moe_down(MoeDev p) {
   __shared__ float red[(MOE_NT / 64) * 2 * 64 * 4];  // NW * DT * NCG * 256, DT * NCG <= 2
-  __shared__ int act_ids[256];
+  __shared__ int act_ids[512];
   __shared__ float xres[16 * 2 * 32];
   moe_down<MOE_NT, NCG, FMT>(p, blockIdx.x, red, act_ids, xres);
 }
@@ -94,6 +95,8 @@ size_t moe_carve(const mk2_moe_shape* s, void* base, MoeDev* d) {
   t.topk_w = c.take<float>((size_t)M * s->top_k);
   t.act = c.take<uint64_t>((size_t)1 + Dmax);
   t.rw = c.take<float>((size_t)Dmax * 32);
+  t.act_rows = c.take<uint64_t>((size_t)Dmax);
+  t.rowc = c.take<int>((size_t)Dmax * 32);
   if (fmt == MK2_FMT_MXFP4 || fmt == MK2_FMT_A4W4 || fmt == MK2_FMT_W8A8) {
     t.mid_q = c.take<uint8_t>((size_t)Dmax * M * I);
     if (fmt == MK2_FMT_W8A8) t.mid_sf = c.take<float>((size_t)Dmax * M * I / 128);
@@ -107,6 +110,7 @@ size_t moe_carve(const mk2_moe_shape* s, void* base, MoeDev* d) {
     d->xsf = t.xsf; d->mid_sf = t.mid_sf;
     d->logit_part = t.logit_part; d->logits = t.logits; d->topk_ids = t.topk_ids;
     d->topk_w = t.topk_w; d->act = t.act; d->rw = t.rw; d->mid_q = t.mid_q;
+    d->act_rows = t.act_rows; d->rowc = t.rowc;
     d->mid_s = t.mid_s; d->mid_b = t.mid_b; d->mid_sh = t.mid_sh;
   }
   return c.bytes();
@@ -142,7 +146,8 @@ int moe_enqueue(const MoeDev& d, hipStream_t st) {
     constexpr int FMT = decltype(F)::value;
     if (ncg == 1) k_moe_router<1, FMT><<<dim3(d.E / 16, d.KC), ROUTER_NT, 0, st>>>(d);
     else k_moe_router<2, FMT><<<dim3(d.E / 16, d.KC), ROUTER_NT, 0, st>>>(d);
-    k_moe_route<<<1, 512, 0, st>>>(d);
+    if (compact_rows(d)) k_moe_route<true><<<1, 512, 0, st>>>(d);
+    else k_moe_route<false><<<1, 512, 0, st>>>(d);
     if (ncg == 1) k_moe_upgate<1, FMT><<<up_tasks, MOE_NT, 0, st>>>(d);
     else k_moe_upgate<2, FMT><<<up_tasks, MOE_NT, 0, st>>>(d);
     if (ncg == 1) k_moe_down<1, FMT><<<down_tasks(d), MOE_NT, 0, st>>>(d);

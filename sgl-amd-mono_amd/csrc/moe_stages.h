@@ -52,13 +52,33 @@ struct MoeDev {
   float* topk_w;     // [M][topk]
   uint64_t* act;     // [1 + Dmax] tagged: count D, then the distinct expert ids ascending
                      // (-1 past D)
-  float* rw;         // [Dmax][32] route weight of slot j for row r (0: not routed)
+  float* rw;         // [Dmax][32] route weight of slot j for row r (0: not routed); with
+                     // compacted rows (compact_rows), of slot j's c-th row
+  uint64_t* act_rows; // [Dmax] tagged: slot j's rows as a bit mask (compacted rows)
+  int* rowc;         // [Dmax][32] slot j's rows, ascending (compacted rows)
   uint8_t* mid_q;    // [Dmax][M][I] E4M3 mid (A8W4, W8A8) or [Dmax][M][I/2] E2M1 (A4W4)
   uint8_t* mid_s;    // [Dmax][M][I/32] E8M0 (A8W4, A4W4)
   float* mid_sf;     // [Dmax][M][I/128] f32 scales (W8A8)
   bf16_t* mid_b;     // [Dmax][M][I] bf16 mid (W8A16, A16W4)
   bf16_t* mid_sh;    // [M][SI] shared-expert mid
 };
+
+// Expert jobs with compacted rows: above 16 rows, the scaled-MFMA E2M1 modes (A8W4,
+// A4W4) run each routed slot's up/gate on the rows that picked its expert only (the
+// MFMA columns: the slot's c-th row, not row c), store the mid compacted, and the down
+// adds each slot's columns into its rows through LDS (the reference's expert jobs,
+// glm53/gfx950/kernel.py:6189-6305).  Every row's sums keep their order, so the bits
+// equal the uncompacted path's.
+__host__ __device__ inline bool compact_rows(const MoeDev& p) {
+  return p.M > 16 && (p.fmt == MK2_FMT_MXFP4 || p.fmt == MK2_FMT_A4W4);
+}
+template <int NCG, int FMT>
+constexpr bool kCompact = NCG == 2 && (FMT == MK2_FMT_MXFP4 || FMT == MK2_FMT_A4W4);
+// the c-th set bit of m (c < popcount(m))
+MK2_DEV int nth_bit(uint32_t m, int c) {
+  for (int i = 0; i < c; ++i) m &= m - 1;
+  return __ffs((int)m) - 1;
+}
 
 template <int NT>
 MK2_DEV float block_sum(float v, float* lds) {
@@ -190,6 +210,12 @@ MK2_DEV int e8m0_shift(int wl, int t, int kb) {
   return wl == MK2_WLAYOUT_AITER16 ? 8 * (2 * (kb & 1) + (t & 1)) : 8 * (kb & 3);
 }
 
+// the same 16 bytes through a buffer resource: an offset past its end reads zeros
+// (no branch for a lane outside the task)
+MK2_DEV i32x8 load_a_fp4_rs(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+  const i32x4 u = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+  return i32x8{u.x, u.y, u.z, u.w, 0, 0, 0, 0};
+}
 MK2_DEV i32x8 load_a_fp4(const uint8_t* tile, int lane) {
   uint4 u = ld_stream16(tile + lane * 16);
   i32x8 a = {(int)u.x, (int)u.y, (int)u.z, (int)u.w, 0, 0, 0, 0};
@@ -372,6 +398,7 @@ struct RouteLds {
   int ids[32 * 8];   // [M][topk]
   float w[32 * 8];   // [M][topk]
   float rw[256 * 32];
+  uint32_t mask[256];  // slot: its rows (compacted rows)
   float lg[32 * 256];  // [M][E] logits
   float bias[256];
   int tot;
@@ -392,7 +419,8 @@ MK2_DEV uint32_t wave_max_u32(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
-template <int NT, typename Mark = NoMark>
+// CMP: the compacted-row tables as well (compact_rows(p) must agree)
+template <int NT, bool CMP = false, typename Mark = NoMark>
 MK2_DEV bool moe_route(const MoeDev& p, RouteLds& L, const TagPoll& tp, Mark mark = Mark()) {
   constexpr int NW = NT / 64;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -403,6 +431,7 @@ MK2_DEV bool moe_route(const MoeDev& p, RouteLds& L, const TagPoll& tp, Mark mar
   for (int e = tid; e < p.E; e += NT) {
     L.flag[e] = 0;
     L.bias[e] = sig ? p.bias[e] : 0.f;
+    if (CMP) L.mask[e] = 0u;
   }
   for (int i = tid; i < p.Dmax * 32; i += NT) L.rw[i] = 0.f;
   if (tid == 0) L.bad = 0;
@@ -567,11 +596,30 @@ MK2_DEV bool moe_route(const MoeDev& p, RouteLds& L, const TagPoll& tp, Mark mar
   __syncthreads();
   mark(2);
   const int total = L.tot;
-  for (int idx = tid; idx < p.M * p.topk; idx += NT) L.rw[L.flag[L.ids[idx]] * 32 + idx / p.topk] = L.w[idx];
+  for (int idx = tid; idx < p.M * p.topk; idx += NT) {
+    const int s = L.flag[L.ids[idx]], r = idx / p.topk;
+    L.rw[s * 32 + r] = L.w[idx];
+    if (CMP) atomicOr(&L.mask[s], 1u << r);
+  }
   __syncthreads();
-  for (int idx = 4 * tid; idx < total * 32; idx += 4 * NT)
-    st_dev_16(p.rw + idx, make_uint4(__float_as_uint(L.rw[idx]), __float_as_uint(L.rw[idx + 1]),
-                                     __float_as_uint(L.rw[idx + 2]), __float_as_uint(L.rw[idx + 3])));
+  if constexpr (!CMP) {
+    for (int idx = 4 * tid; idx < total * 32; idx += 4 * NT)
+      st_dev_16(p.rw + idx, make_uint4(__float_as_uint(L.rw[idx]), __float_as_uint(L.rw[idx + 1]),
+                                       __float_as_uint(L.rw[idx + 2]), __float_as_uint(L.rw[idx + 3])));
+    return true;
+  }
+  // compacted rows: slot j's rows (a tagged mask for its up/gate tasks, which poll it
+  // with their expert id), their route weights and row ids in row order
+  for (int j = tid; j < p.Dmax; j += NT) {
+    const uint32_t m = j < total ? L.mask[j] : 0u;
+    st_pair(p.act_rows + j, m, tp.tag);
+    uint32_t mm = m;
+    for (int c = 0; mm; ++c, mm &= mm - 1) {
+      const int r = __ffs((int)mm) - 1;
+      st_dev_f32(p.rw + j * 32 + c, L.rw[j * 32 + r]);
+      st_dev_i32(p.rowc + j * 32 + c, r);
+    }
+  }
   return true;
 }
 
@@ -581,7 +629,8 @@ MK2_DEV bool moe_route(const MoeDev& p, RouteLds& L, const TagPoll& tp, Mark mar
 // silu(gate) * up.  Each wave owns every NW-th 128-k block and issues the loads of a
 // batch of its blocks (weights, scales, activations) before the first MFMA.
 template <int NT, int NCG, int CT, int FMT>
-MK2_DEV void upgate_chunk(const MoeDev& p, bool shared, int j, int e, int c, float* red, float* midf) {
+MK2_DEV void upgate_chunk(const MoeDev& p, bool shared, int j, int e, int c, float* red, float* midf,
+                          uint32_t rows = 0u) {
   constexpr int NW = NT / 64, NQ = 2 * CT, R = 16 * CT;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4;
   const int KB = p.H / 128;
@@ -605,6 +654,18 @@ MK2_DEV void upgate_chunk(const MoeDev& p, bool shared, int j, int e, int c, flo
     constexpr int B = CT == 4 ? (NCG == 1 ? 3 : 2) : (NCG == 1 ? 4 : 3);  // k-blocks in flight
     const uint8_t* wbase = p.w13 + (size_t)e * NT16 * KB * 1024;
     const uint8_t* sbase = p.s13 + e * e8m0_expert_bytes(p.wl, 2 * I, p.H);
+    // the MFMA columns: rows 16 cg + c16, or with compacted rows the slot's (16 cg +
+    // c16)-th row (p.M: none, read as zeros); a second column group only if the slot
+    // has more than 16 rows
+    constexpr bool CMP = kCompact<NCG, FMT>;
+    const int cnt = CMP ? __popc(rows) : p.M;
+    int xrow[NCG];
+#pragma unroll
+    for (int cg = 0; cg < NCG; ++cg) {
+      const int cc = cg * 16 + (lane & 15);
+      xrow[cg] = CMP ? (cc < cnt ? nth_bit(rows, cc) : p.M) : cc;
+    }
+    const bool two = !CMP || cnt > 16;
     for (int kb0 = wave; kb0 < KB; kb0 += NW * B) {
       i32x8 a[B][NQ], b[B][NCG];
       int sa[B][NQ], sb[B][NCG];
@@ -618,7 +679,7 @@ MK2_DEV void upgate_chunk(const MoeDev& p, bool shared, int j, int e, int c, flo
         }
 #pragma unroll
         for (int cg = 0; cg < NCG; ++cg) {
-          const int row = cg * 16 + (lane & 15);
+          const int row = xrow[cg];
           b[u][cg] = a4 ? load_b_fp4(p.xq, row, p.M, p.H / 2, kb * 64, g) : load_b_fp8(p.xq, row, p.M, p.H, kb * 128, g);
           sb[u][cg] = row < p.M ? (int)ldp_u8(p.xs + (size_t)row * (p.H / 32) + kb * 4 + g) : E8M0_ONE;
         }
@@ -627,11 +688,13 @@ MK2_DEV void upgate_chunk(const MoeDev& p, bool shared, int j, int e, int c, flo
       for (int u = 0; u < B; ++u) {
         if (kb0 + u * NW >= KB) break;
 #pragma unroll
-        for (int cg = 0; cg < NCG; ++cg)
+        for (int cg = 0; cg < NCG; ++cg) {
+          if (cg == 1 && !two) break;  // no rows there (uniform)
 #pragma unroll
           for (int q = 0; q < NQ; ++q)
             acc[q][cg] = a4 ? mfma_same<4>(a[u][q], b[u][cg], acc[q][cg], sa[u][q], sb[u][cg])
                             : mfma_fp4_fp8<0, 0>(a[u][q], b[u][cg], acc[q][cg], sa[u][q], sb[u][cg]);
+        }
       }
     }
   } else if (!shared && FMT == MK2_FMT_A16W4) {
@@ -866,28 +929,37 @@ MK2_DEV void upgate_w8a8(const MoeDev& p, int j, int e, int c, float* red) {
 // midf: 32 * (UC + 1) floats.
 // Routed slot j's expert from the routing's tagged list: one wave polls the count and
 // the slot's word together (-1 past the list); -2 when the launch is failing.
-MK2_DEV int slot_expert(const MoeDev& p, int j, const TagPoll& tp, int* lds) {
+// With compacted rows (CMP) lane 2 also polls the slot's row mask: *rows (else all
+// rows).
+template <bool CMP>
+MK2_DEV int slot_expert(const MoeDev& p, int j, const TagPoll& tp, int* lds, uint32_t* rows) {
+  constexpr int nl = CMP ? 3 : 2;  // lanes that poll
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
     bool bad = false;
     // two polls in flight: the next is issued before the last one is looked at
-    const uint64_t* src = p.act + (lane ? 1 + j : 0);
-    uint64_t w = lane < 2 ? ld_pair(src) : 0;
+    const uint64_t* src = lane == 2 ? p.act_rows + j : p.act + (lane ? 1 + j : 0);
+    uint64_t w = lane < nl ? ld_pair(src) : 0;
     for (int polls = 1;; polls += 2) {
-      const uint64_t w1 = lane < 2 ? ld_pair(src) : 0;
-      if (poll_done(lane >= 2 || pair_ready(w, tp), polls, tp, &bad)) break;
-      w = lane < 2 ? ld_pair(src) : 0;
-      if (poll_done(lane >= 2 || pair_ready(w1, tp), polls + 1, tp, &bad)) {
+      const uint64_t w1 = lane < nl ? ld_pair(src) : 0;
+      if (poll_done(lane >= nl || pair_ready(w, tp), polls, tp, &bad)) break;
+      w = lane < nl ? ld_pair(src) : 0;
+      if (poll_done(lane >= nl || pair_ready(w1, tp), polls + 1, tp, &bad)) {
         w = w1;
         break;
       }
     }
     const int cnt = __builtin_amdgcn_readlane((int)pair_value(w), 0);
     const int e = __builtin_amdgcn_readlane((int)pair_value(w), 1);
-    if (lane == 0) *lds = bad ? -2 : (j >= cnt || e < 0 || e >= p.E ? -1 : e);
+    const uint32_t m = (uint32_t)__builtin_amdgcn_readlane((int)pair_value(w), 2);
+    if (lane == 0) {
+      lds[0] = bad ? -2 : (j >= cnt || e < 0 || e >= p.E ? -1 : e);
+      lds[1] = nl == 3 ? (int)m : (int)(p.M >= 32 ? 0xFFFFFFFFu : (1u << p.M) - 1u);
+    }
   }
   __syncthreads();
-  const int e = *lds;
+  const int e = lds[0];
+  *rows = (uint32_t)lds[1];
   __syncthreads();
   return e;
 }
@@ -897,12 +969,13 @@ MK2_DEV bool moe_upgate(const MoeDev& p, int t, float* red, float* midf, const T
   const int chunks_r = p.I / p.UC;
   if (t < p.Dmax * chunks_r) {
     const int j = t / chunks_r, c = t % chunks_r;
-    const int e = slot_expert(p, j, tp, (int*)midf);
+    uint32_t rows;
+    const int e = slot_expert<kCompact<NCG, FMT>>(p, j, tp, (int*)midf, &rows);
     if (e == -2) return false;
     if (e < 0) return true;
     if constexpr (FMT == MK2_FMT_W8A8) upgate_w8a8<NT, NCG>(p, j, e, c, red);
-    else if (NCG == 1 && p.UC == 64) upgate_chunk<NT, NCG, (NCG == 1 ? 4 : 2), FMT>(p, false, j, e, c, red, midf);
-    else upgate_chunk<NT, NCG, 2, FMT>(p, false, j, e, c, red, midf);
+    else if (NCG == 1 && p.UC == 64) upgate_chunk<NT, NCG, (NCG == 1 ? 4 : 2), FMT>(p, false, j, e, c, red, midf, rows);
+    else upgate_chunk<NT, NCG, 2, FMT>(p, false, j, e, c, red, midf, rows);
   } else {
     upgate_chunk<NT, NCG, 2, FMT>(p, true, 0, 0, t - p.Dmax * chunks_r, red, midf);
   }
@@ -914,7 +987,7 @@ MK2_DEV bool moe_upgate(const MoeDev& p, int t, float* red, float* midf, const T
 // experts) adds rw * W_down[e] . mid into the rows' accumulators; out = bf16(y [+ x]).
 // Waves take every NW-th slot, B slots a unit, the next unit's weight tiles and mid
 // rows (shared by the DT tiles) in flight while a unit's MFMAs run.  act_ids: LDS >=
-// E ints; red: NW * DT * NCG * 256 floats; xres: LDS >= 8 * DT * M words (the residual
+// 512 ints; red: NW * DT * NCG * 256 floats; xres: LDS >= 8 * DT * M words (the residual
 // rows, bf16).
 template <int NT, int NCG, int DT, int FMT, typename Wait>
 MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, float* xres, Wait wait) {
@@ -1229,6 +1302,366 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, float*
   __syncthreads();
 }
 
+// The down with compacted rows (kCompact): as down_rows, each slot's columns being its
+// rows in order, added into per-wave [16 hidden][32 rows] accumulators in LDS.  A copy,
+// so that the uncompacted instantiations keep down_rows' code as it is.
+template <int NT, int NCG, int DT, int FMT, typename Wait>
+MK2_DEV void down_rows_cmp(const MoeDev& p, int nt, float* red, int* act_ids, float* xres, Wait wait) {
+  constexpr int NW = NT / 64;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, c16 = lane & 15;
+  // the list, published by the routing's counter; read device-coherently: up/gate
+  // tasks on this XCD polled its words before all of them were out
+  constexpr bool CMP = kCompact<NCG, FMT>;
+  static_assert(!CMP || DT == 1, "compacted rows: one 16-row hidden tile a task");
+  const int D = min((int)pair_value(ld_pair(p.act)), p.Dmax);
+  for (int j = threadIdx.x; j < D; j += NT) {
+    act_ids[j] = min(max((int)pair_value(ld_pair(p.act + 1 + j)), 0), p.E - 1);
+    if (CMP) act_ids[256 + j] = __popc((uint32_t)pair_value(ld_pair(p.act_rows + j)));  // the slot's rows
+  }
+  __syncthreads();
+  const int HT = p.H / 16;
+  // the task's rows: tile tl[d], rows rlo[d] .. rhi[d] - 1 of it (every row of DT tiles,
+  // or with p.DT == 3 (DT 2) 24 rows: a whole tile and half of the next, in either order)
+  int tl[DT], rlo[DT], rhi[DT];
+#pragma unroll
+  for (int d = 0; d < DT; ++d) {
+    tl[d] = nt * DT + d;
+    rlo[d] = 0;
+    rhi[d] = 16;
+  }
+  if (DT == 2 && p.DT == 3) {
+    const int ta = (3 * nt) >> 1;
+    tl[0] = ta;
+    tl[DT - 1] = ta + 1;
+    rlo[0] = nt & 1 ? 8 : 0;
+    rhi[DT - 1] = nt & 1 ? 16 : 8;
+  }
+  const int c0 = tl[0] * 16 + rlo[0];  // the task's first hidden row (output column)
+  int ncol = 0;
+#pragma unroll
+  for (int d = 0; d < DT; ++d) ncol += rhi[d] - rlo[d];
+  bool live[DT];  // this lane's A row is one of the task's
+#pragma unroll
+  for (int d = 0; d < DT; ++d) live[d] = c16 >= rlo[d] && c16 < rhi[d];
+  const int KB2s = p.n_shared ? p.SI / 128 : 0;
+  const int KB2 = p.I / 128;
+  constexpr int B = 1;                                 // MXFP4 slots a unit
+  constexpr int KC = 2;                                // k-blocks of a slot a pass
+  // weights only (static, or known since routing): the shared expert's first k-block
+  // of this wave and its first batch of routed slots, loaded before `wait` (the mid
+  // activations' dependency)
+  uint4 shraw[DT][2];
+  float shsc[DT];
+  {
+    const int kb = min(wave, max(KB2s, 1) - 1);
+#pragma unroll
+    for (int d = 0; d < DT; ++d) {
+      shraw[d][0] = shraw[d][1] = make_uint4(0, 0, 0, 0);
+      shsc[d] = 0.f;
+      if (KB2s) {
+        if (live[d]) load_fp8_block(p.ws2 + ((size_t)tl[d] * KB2s + kb) * 2048, p.wl, lane, shraw[d][0], shraw[d][1]);
+        shsc[d] = p.ss2[(tl[d] * 16 / 128) * KB2s + kb];
+      }
+    }
+  }
+  // the scaled-MFMA unit pipeline: E2M1 weights against MXFP8 (A8W4) or MXFP4 (A4W4) mid
+  constexpr bool mx = FMT == MK2_FMT_MXFP4 || FMT == MK2_FMT_A4W4;
+  constexpr bool a4 = FMT == MK2_FMT_A4W4;
+  // the residual rows (the W_o output, published before the routing) for the
+  // epilogue, straight into LDS (no registers held): dword d of the ncol / 2 * M is
+  // row d / (ncol / 2), columns 2 (d % (ncol / 2)) .. + 1 of the task's
+  const int nxd = p.residual ? ncol / 2 * p.M : 0;
+  if (threadIdx.x < nxd)
+    __builtin_amdgcn_global_load_lds(
+        (const uint32_t*)(p.x + (size_t)(threadIdx.x / (ncol / 2)) * p.H + c0) + threadIdx.x % (ncol / 2),
+        (uint32_t*)xres + 64 * wave, 4, 0, 0);
+  // the routed slots (MXFP4): a unit is a batch of B slots (wave + NW * (B * i + u))
+  // over KC k-blocks; units u + 1 and u + 2 (weights, mid rows, scales and route
+  // weights) are in flight while unit u's MFMAs run
+  struct Unit {
+    i32x8 a[B][DT][KC];
+    i32x8 bq[B][KC][NCG];
+    int sa[B][DT];
+    int sbq[B][KC][NCG];
+    float wr[B][NCG];
+    int rr[B][NCG];  // compacted rows: the column's row (-1: none)
+    int cnt[B];      // compacted rows: the slot's rows
+  };
+  const int nkc = (KB2 + KC - 1) / KC;  // units a batch
+  const int nu = mx && D > wave ? (D - wave + NW * B - 1) / (NW * B) * nkc : 0;
+  auto load_w = [&](int u, Unit& x) {  // weights: known since the routing
+    const int j0 = wave + (u / nkc) * NW * B, kb0 = (u % nkc) * KC;
+#pragma unroll
+    for (int ub = 0; ub < B; ++ub) {
+      // past the list: a valid slot, unused
+      const int e = __builtin_amdgcn_readfirstlane(act_ids[min(j0 + ub * NW, D - 1)]);
+      // the expert's E2M1 bytes as a buffer: a lane outside the task's rows reads
+      // zeros past its end, with no branch around the load
+      const uint32_t ebytes = (uint32_t)HT * KB2 * 1024;
+      const __amdgpu_buffer_rsrc_t rs =
+          __builtin_amdgcn_make_buffer_rsrc((void*)(p.w2 + (size_t)e * ebytes), (short)0, (int)ebytes, 0x00020000);
+#pragma unroll
+      for (int c = 0; c < KC; ++c)
+#pragma unroll
+        for (int d = 0; d < DT; ++d)
+          x.a[ub][d][c] = load_a_fp4_rs(
+              rs, live[d] ? (uint32_t)(tl[d] * KB2 + min(kb0 + c, KB2 - 1)) * 1024u + lane * 16u : ebytes);
+#pragma unroll
+      for (int d = 0; d < DT; ++d) {
+        const uint32_t w = e8m0_word(p.s2 + e * e8m0_expert_bytes(p.wl, p.H, p.I), p.wl, p.I, tl[d], kb0, lane);
+        x.sa[ub][d] = live[d] ? (int)w : 127;
+      }
+    }
+  };
+  auto load_m = [&](int u, Unit& x) {  // mid rows and route weights: after the wait
+    const int j0 = wave + (u / nkc) * NW * B, kb0 = (u % nkc) * KC;
+#pragma unroll
+    for (int ub = 0; ub < B; ++ub) {
+      const int j = min(j0 + ub * NW, D - 1);
+      // the mid's rows: all rows, or the slot's rows compacted (row c its c-th)
+      const int lim = CMP ? act_ids[256 + j] : p.M;
+      x.cnt[ub] = lim;
+#pragma unroll
+      for (int c = 0; c < KC; ++c) {
+        const int kb = min(kb0 + c, KB2 - 1);
+#pragma unroll
+        for (int cg = 0; cg < NCG; ++cg) {
+          const int row = cg * 16 + c16;
+          x.bq[ub][c][cg] = a4 ? load_b_fp4(p.mid_q + (size_t)j * p.M * (p.I / 2), row, lim, p.I / 2, kb * 64, g)
+                               : load_b_fp8(p.mid_q + (size_t)j * p.M * p.I, row, lim, p.I, kb * 128, g);
+          x.sbq[ub][c][cg] = row < lim ? (int)ldp_u8(p.mid_s + ((size_t)j * p.M + row) * (p.I / 32) + kb * 4 + g) : 127;
+        }
+      }
+#pragma unroll
+      for (int cg = 0; cg < NCG; ++cg) {
+        const int row = cg * 16 + c16;
+        x.wr[ub][cg] = !CMP || row < lim ? ldp_f32(p.rw + j * 32 + row) : 0.f;
+        x.rr[ub][cg] = CMP && row < lim ? ldp_i32(p.rowc + j * 32 + row) : -1;
+      }
+    }
+  };
+  f32x4 acc[DT][NCG], tmp[B][DT][NCG];
+#pragma unroll
+  for (int d = 0; d < DT; ++d)
+#pragma unroll
+    for (int cg = 0; cg < NCG; ++cg) acc[d][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](int u, Unit& x) {
+    const int j0 = wave + (u / nkc) * NW * B, kb0 = (u % nkc) * KC;
+    if (kb0 == 0) {
+#pragma unroll
+      for (int ub = 0; ub < B; ++ub)
+#pragma unroll
+        for (int d = 0; d < DT; ++d)
+#pragma unroll
+          for (int cg = 0; cg < NCG; ++cg) tmp[ub][d][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int ub = 0; ub < B; ++ub) {
+      if (j0 + ub * NW >= D) break;
+#pragma unroll
+      for (int c = 0; c < KC; ++c) {
+        const int kb = kb0 + c;
+        if (kb >= KB2) break;
+#pragma unroll
+        for (int d = 0; d < DT; ++d) {
+          const int sak = x.sa[ub][d] >> e8m0_shift(p.wl, tl[d], kb);
+#pragma unroll
+          for (int cg = 0; cg < NCG; ++cg) {
+            if (CMP && cg == 1 && x.cnt[ub] <= 16) break;  // no rows there (uniform)
+            tmp[ub][d][cg] = a4 ? mfma_same<4>(x.a[ub][d][c], x.bq[ub][c][cg], tmp[ub][d][cg], sak, x.sbq[ub][c][cg])
+                                : mfma_fp4_fp8<0, 0>(x.a[ub][d][c], x.bq[ub][c][cg], tmp[ub][d][cg], sak, x.sbq[ub][c][cg]);
+          }
+        }
+      }
+    }
+    if (kb0 + KC >= KB2) {
+#pragma unroll
+      for (int ub = 0; ub < B; ++ub) {
+        if (j0 + ub * NW >= D) break;
+        if constexpr (CMP) {
+          // each column into its row of this wave's accumulator [16 hidden][32 rows]
+#pragma unroll
+          for (int cg = 0; cg < NCG; ++cg)
+            if (x.rr[ub][cg] >= 0) {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) red[(wave * 16 + 4 * g + i) * 32 + x.rr[ub][cg]] += tmp[ub][0][cg][i] * x.wr[ub][cg];
+            }
+        } else {
+#pragma unroll
+          for (int cg = 0; cg < NCG; ++cg)
+#pragma unroll
+            for (int d = 0; d < DT; ++d) acc[d][cg] += tmp[ub][d][cg] * x.wr[ub][cg];
+        }
+      }
+    }
+  };
+  Unit x0, x1, x2;
+  if (nu > 0) load_w(0, x0);
+  if (nu > 1) load_w(1, x1);
+  if (!wait()) return;
+  if (nu > 0) load_m(0, x0);
+  if (nu > 1) load_m(1, x1);
+  // the shared expert (FP8, bf16 mid): its k-blocks spread over the waves
+  for (int kb = wave; kb < KB2s; kb += NW) {
+    bf16x8 b[NCG][4];
+#pragma unroll
+    for (int cg = 0; cg < NCG; ++cg) load_b_bf16(p.mid_sh, cg * 16 + c16, p.M, p.SI, kb * 128 + 32 * g, b[cg]);
+#pragma unroll
+    for (int d = 0; d < DT; ++d) {
+      uint4 r0, r1;
+      float sc;
+      if (kb == wave) {
+        r0 = shraw[d][0];
+        r1 = shraw[d][1];
+        sc = shsc[d];
+      } else {
+        r0 = r1 = make_uint4(0, 0, 0, 0);
+        if (live[d]) load_fp8_block(p.ws2 + ((size_t)tl[d] * KB2s + kb) * 2048, p.wl, lane, r0, r1);
+        sc = p.ss2[(tl[d] * 16 / 128) * KB2s + kb];
+      }
+      bf16x8 a[4];
+      a[0] = e4m3x8_to_bf16(r0.x, r0.y);
+      a[1] = e4m3x8_to_bf16(r0.z, r0.w);
+      a[2] = e4m3x8_to_bf16(r1.x, r1.y);
+      a[3] = e4m3x8_to_bf16(r1.z, r1.w);
+#pragma unroll
+      for (int cg = 0; cg < NCG; ++cg) acc[d][cg] += mfma4_bf16(a, b[cg], f32x4{0.f, 0.f, 0.f, 0.f}) * sc;
+    }
+  }
+  if constexpr (CMP) {
+    // this wave's accumulator [16 hidden][32 rows] in LDS, from its shared-expert sums;
+    // the routed slots add into their rows
+#pragma unroll
+    for (int cg = 0; cg < NCG; ++cg)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[(wave * 16 + 4 * g + i) * 32 + cg * 16 + c16] = acc[0][cg][i];
+  }
+  if constexpr (mx) {
+    auto step = [&](int u, Unit& cur, Unit& nxt2) {
+      if (u + 2 < nu) {
+        load_w(u + 2, nxt2);
+        load_m(u + 2, nxt2);
+      }
+      if (u < nu) compute(u, cur);
+    };
+    for (int u = 0; u < nu; u += 3) {
+      step(u, x0, x2);
+      step(u + 1, x1, x0);
+      step(u + 2, x2, x1);
+    }
+  } else if constexpr (DT == 1) {
+    if constexpr (FMT == MK2_FMT_A16W4) {
+      // E2M1 weights widened exactly to bf16 against the bf16 mid, 8 k-blocks a batch
+      constexpr int KMAX = 8;
+      for (int j = wave; j < D; j += NW) {
+        const int e = act_ids[j];
+        const uint8_t* wb = p.w2 + ((size_t)e * HT + tl[0]) * KB2 * 1024;
+        const uint8_t* sb = p.s2 + e * e8m0_expert_bytes(p.wl, p.H, p.I);
+        f32x4 t[NCG];
+#pragma unroll
+        for (int cg = 0; cg < NCG; ++cg) t[cg] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int kb0 = 0; kb0 < KB2; kb0 += KMAX) {
+          uint4 raw[KMAX];
+          uint32_t sw[KMAX];
+#pragma unroll
+          for (int u = 0; u < KMAX; ++u) {
+            const int kb = min(kb0 + u, KB2 - 1);
+            raw[u] = ld_stream16(wb + ((size_t)kb * 64 + lane) * 16);
+            sw[u] = (e8m0_word(sb, p.wl, p.I, tl[0], kb, lane) >> e8m0_shift(p.wl, tl[0], kb)) & 0xFFu;
+          }
+#pragma unroll
+          for (int u = 0; u < KMAX; ++u) {
+            const int kb = kb0 + u;
+            if (kb >= KB2) break;
+            const float sc = e8m0_to_f32(sw[u]);
+            bf16x8 a[4];
+            a[0] = e2m1x8_to_bf16(raw[u].x, sc);
+            a[1] = e2m1x8_to_bf16(raw[u].y, sc);
+            a[2] = e2m1x8_to_bf16(raw[u].z, sc);
+            a[3] = e2m1x8_to_bf16(raw[u].w, sc);
+#pragma unroll
+            for (int cg = 0; cg < NCG; ++cg) {
+              bf16x8 b[4];
+              load_b_bf16(p.mid_b + (size_t)j * p.M * p.I, cg * 16 + c16, p.M, p.I, kb * 128 + 32 * g, b);
+              t[cg] = mfma4_bf16(a, b, t[cg]);
+            }
+          }
+        }
+#pragma unroll
+        for (int cg = 0; cg < NCG; ++cg) acc[0][cg] += t[cg] * ldp_f32(p.rw + j * 32 + cg * 16 + c16);
+      }
+    } else {
+      // E4M3 weights (f32 scale per 128 x 128 block): widened to bf16 against the bf16
+      // mid (W8A16), or on the scaled MFMA against the E4M3 mid (W8A8, f32 scale per 128
+      // a row); each k-block's product times its scales and the route weight
+      constexpr int KMAX = 8;  // inter <= 1024
+      constexpr bool w8a8 = FMT == MK2_FMT_W8A8;
+      for (int j = wave; j < D; j += NW) {
+        const int e = act_ids[j];
+        const uint8_t* wb = p.w2 + ((size_t)e * HT + tl[0]) * KB2 * 2048;
+        const float* sbase = (const float*)p.s2 + (size_t)e * (p.H / 128) * KB2 + (tl[0] * 16 / 128) * KB2;
+        uint4 raw[KMAX][2];
+#pragma unroll
+        for (int kb = 0; kb < KMAX; ++kb) {
+          load_fp8_block(wb + (size_t)min(kb, KB2 - 1) * 2048, p.wl, lane, raw[kb][0], raw[kb][1]);
+        }
+#pragma unroll
+        for (int kb = 0; kb < KMAX; ++kb) {
+          if (kb >= KB2) break;
+          const float sc = sbase[kb];
+          if constexpr (w8a8) {
+            const i32x8 A = {(int)raw[kb][0].x, (int)raw[kb][0].y, (int)raw[kb][0].z, (int)raw[kb][0].w,
+                             (int)raw[kb][1].x, (int)raw[kb][1].y, (int)raw[kb][1].z, (int)raw[kb][1].w};
+#pragma unroll
+            for (int cg = 0; cg < NCG; ++cg) {
+              const int row = cg * 16 + c16;
+              const i32x8 bq = load_b_fp8_same(p.mid_q + (size_t)j * p.M * p.I, row, p.M, p.I, kb * 128, g);
+              const float ms = row < p.M ? ldp_f32(p.mid_sf + ((size_t)j * p.M + row) * (p.I / 128) + kb) : 0.f;
+              acc[0][cg] += mfma_same<0>(A, bq, f32x4{0.f, 0.f, 0.f, 0.f}, E8M0_ONE, E8M0_ONE) *
+                            (sc * ms * ldp_f32(p.rw + j * 32 + row));
+            }
+          } else {
+            bf16x8 a[4];
+            a[0] = e4m3x8_to_bf16(raw[kb][0].x, raw[kb][0].y);
+            a[1] = e4m3x8_to_bf16(raw[kb][0].z, raw[kb][0].w);
+            a[2] = e4m3x8_to_bf16(raw[kb][1].x, raw[kb][1].y);
+            a[3] = e4m3x8_to_bf16(raw[kb][1].z, raw[kb][1].w);
+#pragma unroll
+            for (int cg = 0; cg < NCG; ++cg) {
+              bf16x8 b[4];
+              load_b_bf16(p.mid_b + (size_t)j * p.M * p.I, cg * 16 + c16, p.M, p.I, kb * 128 + 32 * g, b);
+              acc[0][cg] += mfma4_bf16(a, b, f32x4{0.f, 0.f, 0.f, 0.f}) * (sc * ldp_f32(p.rw + j * 32 + cg * 16 + c16));
+            }
+          }
+        }
+      }
+    }
+  }
+  if constexpr (!CMP) {
+#pragma unroll
+    for (int d = 0; d < DT; ++d)
+#pragma unroll
+      for (int cg = 0; cg < NCG; ++cg) *(f32x4*)(red + (((wave * DT + d) * NCG + cg) * 64 + lane) * 4) = acc[d][cg];
+  }
+  drain_memory();  // this wave's residual dwords have landed in LDS
+  __syncthreads();
+  const int n0 = rhi[0] - rlo[0];  // the first tile's columns
+  for (int idx = threadIdx.x; idx < ncol * p.M; idx += NT) {
+    const int n = idx % ncol, s = idx / ncol;  // column c0 + n of row s
+    const int d = n < n0 ? 0 : DT - 1, n16 = n < n0 ? rlo[0] + n : rlo[DT - 1] + n - n0;
+    const int cg = s >> 4, s16 = s & 15;
+    const int l = (n16 >> 2) * 16 + s16, i = n16 & 3;
+    float y = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+      y += CMP ? red[(w * 16 + n16) * 32 + s] : red[(((w * DT + d) * NCG + cg) * 64 + l) * 4 + i];
+    const size_t o = (size_t)s * p.H + c0 + n;
+    if (p.residual) y += bf16_to_f32(((const bf16_t*)xres)[idx]);
+    p.out[o] = f32_to_bf16(y);
+  }
+  __syncthreads();
+}
+
 // down tasks of a launch: 16 * DT hidden rows each, or 24 with DT == 3
 __host__ __device__ inline int down_tasks(const MoeDev& p) { return p.DT == 3 ? p.H / 24 : p.H / (16 * p.DT); }
 
@@ -1237,13 +1670,17 @@ __host__ __device__ inline int down_tasks(const MoeDev& p) { return p.DT == 3 ? 
 // are in flight.
 template <int NT, int NCG, int FMT, typename Wait = NoWait>
 MK2_DEV void moe_down(const MoeDev& p, int nt, float* red, int* act_ids, float* xres, Wait wait = Wait()) {
-  if constexpr (FMT == MK2_FMT_MXFP4 || FMT == MK2_FMT_A4W4) {
-    if (NCG == 1 && p.DT >= 2) {
-      down_rows<NT, NCG, (NCG == 1 ? 2 : 1), FMT>(p, nt, red, act_ids, xres, wait);
-      return;
+  if constexpr (kCompact<NCG, FMT>) {
+    down_rows_cmp<NT, NCG, 1, FMT>(p, nt, red, act_ids, xres, wait);
+  } else {
+    if constexpr (FMT == MK2_FMT_MXFP4 || FMT == MK2_FMT_A4W4) {
+      if (NCG == 1 && p.DT >= 2) {
+        down_rows<NT, NCG, (NCG == 1 ? 2 : 1), FMT>(p, nt, red, act_ids, xres, wait);
+        return;
+      }
     }
+    down_rows<NT, NCG, 1, FMT>(p, nt, red, act_ids, xres, wait);
   }
-  down_rows<NT, NCG, 1, FMT>(p, nt, red, act_ids, xres, wait);
 }
 
 // runs f(std::integral_constant<int, FMT>) for the expert mode fmt (a kernel

@@ -274,13 +274,17 @@ int mk2_layer_launch_static(const mk2_layer_args* args, mk2_stream_t stream);
  * rope: interleaved pairs (2i, 2i+1) by rope_cos_sin[position] (SGLang's cos_sin_cache
  * f32 [positions][rope], cos | sin); fwht: the orthonormal 128-point Hadamard
  * transform (Sylvester order); quant: the index cache's (MK2_KEYS_FP8: ue8m0 +
- * E4M3, MK2_KEYS_FP4: MXFP4).  Weights are SGLang's as loaded, row-major, read in
- * place: bf16, or E4M3 with f32 128 x 128 block scales [ceil(rows/128)][K/128]
- * (W_iw is bf16 in both).  W_UK is SGLang's w_kc, bf16 [heads][kv_lora][nope] in
- * memory.  A row with slot < 0 (a pad row) writes no cache rows.  Six launches in
+ * E4M3, MK2_KEYS_FP4: MXFP4).  Weights are SGLang's as loaded, read in place: bf16
+ * or E4M3 row-major, or E4M3 in AITER's (16, 16) layout, with f32 128 x 128 block
+ * scales [ceil(rows/128)][K/128] (W_iw is bf16 in all).  W_UK is SGLang's w_kc, bf16
+ * [heads][kv_lora][nope] in memory.  A row with slot < 0 (a pad row) writes no cache rows.  Six launches in
  * stream order; the workspace holds the normed rows and the f32 GEMV outputs. */
 #define MK2_WFMT_BF16 0
 #define MK2_WFMT_FP8_BLOCK 1
+#define MK2_WFMT_FP8_AITER16 2 /* E4M3 with the same block scales, the weight bytes in
+                                  AITER's (16, 16) layout [rows/16][K/32][2][16][16 B], as
+                                  SGLang leaves linears it preshuffled for AITER's GEMM
+                                  (the reference's fp8_shuffled, kernel.py:1015-1050) */
 
 typedef struct mk2_front_shape {
   int rows;          /* 1..32 */
@@ -291,7 +295,7 @@ typedef struct mk2_front_shape {
   int nope;          /* 128, 192 or 256 */
   int heads;         /* MLA heads of this GPU */
   int index_heads;   /* 0 (no indexer) or a multiple of 16 up to 64; index dim 128 */
-  int weight_fmt;    /* MK2_WFMT_* of W_qkv_a, W_q_b, W_iq, W_ik */
+  int weight_fmt;    /* MK2_WFMT_* of W_qkv_a, W_q_b, W_iq, W_ik (one format for all four) */
   int key_fmt;       /* MK2_KEYS_*: the index cache's format */
   int kv_scaled;     /* 1: latent rows with a f32 scale (amax / 448) each; 0: SGLang's unscaled */
   int max_position;  /* the last position of rope_cos_sin */

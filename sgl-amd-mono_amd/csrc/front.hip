@@ -65,9 +65,11 @@ struct GemvDev {
   int ntiles;
 };
 
-// KU: 64-k units a wave (K / ks = 8 * 64 * KU); F8: E4M3 weights
-template <int KU, bool F8>
+// KU: 64-k units a wave (K / ks = 8 * 64 * KU); WF: the weights' MK2_WFMT_* (bf16,
+// E4M3 row-major, or E4M3 in AITER's (16, 16) layout)
+template <int KU, int WF>
 __global__ __launch_bounds__(GV_NT) void k_gemv(GemvDev p) {
+  constexpr bool F8 = WF != MK2_WFMT_BF16, SHUF = WF == MK2_WFMT_FP8_AITER16;
   constexpr int L = F8 ? KU : 2 * KU;      // 16-byte weight loads a lane a tile
   constexpr int WIN = L <= 24 ? L : L / 2;  // loads in flight a lane
   static_assert(L % WIN == 0, "a window divides the loads of a tile");
@@ -93,13 +95,18 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(GemvDev p) {
   }
   // the tile sequence: tile t of segment sid at row (t - base) * 16; this lane's row
   auto seg_of = [&](int t) { return t < p.tiles0 ? 0 : 1; };
+  // In AITER's (16, 16) layout ([rows/16][K/32][2][16 rows][16 B]) the 16 bytes of
+  // row c16 at k = kw + 64 u (k % 16 == 0) sit at tile * 16 K + (kw - 16 g + 64 u) * 16
+  // + lane * 16: a wave's load of a unit is one contiguous 1 KiB.
   auto w_row = [&](int t) -> const uint8_t* {
     const int sid = seg_of(t);
-    const int row = (t - (sid ? p.tiles0 : 0)) * 16 + c16;
-    return (const uint8_t*)p.seg[sid].w + ((size_t)row * K + kw) * (F8 ? 1 : 2);
+    const int nt = t - (sid ? p.tiles0 : 0);
+    if constexpr (SHUF)
+      return (const uint8_t*)p.seg[sid].w + (size_t)nt * 16 * K + (size_t)(kw - 16 * g) * 16 + lane * 16;
+    return (const uint8_t*)p.seg[sid].w + ((size_t)(nt * 16 + c16) * K + kw) * (F8 ? 1 : 2);
   };
   // a lane's load j of a tile: F8 unit j (16 E4M3); bf16 unit j / 2, half j % 2
-  auto w_off = [&](int j) { return F8 ? 64 * j : 128 * (j >> 1) + 16 * (j & 1); };
+  auto w_off = [&](int j) { return SHUF ? 1024 * j : F8 ? 64 * j : 128 * (j >> 1) + 16 * (j & 1); };
   const uint8_t* wrow = w_row(t0 < t1 ? t0 : 0);
   uint4 wv[WIN];
   if (t0 < t1) {
@@ -219,9 +226,9 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(GemvDev p) {
   }
 }
 
-template <int KU, bool F8>
+template <int KU, int WF>
 static void gemv_launch1(const GemvDev& d, int grid, hipStream_t st) {
-  k_gemv<KU, F8><<<grid, GV_NT, 0, st>>>(d);
+  k_gemv<KU, WF><<<grid, GV_NT, 0, st>>>(d);
 }
 
 // the engine's k-step counts: KU = K / (512 ks)
@@ -241,22 +248,22 @@ static int gemv_parts(int K, int tiles, int cus, bool f8) {
   return best;
 }
 
-template <bool F8>
+template <int WF>
 static int gemv_launch(const GemvDev& d, int cus, hipStream_t st) {
   const int per = d.ntiles < cus / d.ks ? d.ntiles : cus / d.ks;  // workgroups a K part
   const int grid = d.ks * (per > 0 ? per : 1);
   switch (d.K / (512 * d.ks)) {
     case 1:
-      if constexpr (F8) return set_error(MK2_EINVAL, "front: FP8 K parts must hold whole 128-k blocks");
-      else gemv_launch1<1, false>(d, grid, st);
+      if constexpr (WF != MK2_WFMT_BF16) return set_error(MK2_EINVAL, "front: FP8 K parts must hold whole 128-k blocks");
+      else gemv_launch1<1, WF>(d, grid, st);
       break;
-    case 2: gemv_launch1<2, F8>(d, grid, st); break;
-    case 4: gemv_launch1<4, F8>(d, grid, st); break;
-    case 6: gemv_launch1<6, F8>(d, grid, st); break;
-    case 8: gemv_launch1<8, F8>(d, grid, st); break;
-    case 12: gemv_launch1<12, F8>(d, grid, st); break;
-    case 14: gemv_launch1<14, F8>(d, grid, st); break;
-    case 16: gemv_launch1<16, F8>(d, grid, st); break;
+    case 2: gemv_launch1<2, WF>(d, grid, st); break;
+    case 4: gemv_launch1<4, WF>(d, grid, st); break;
+    case 6: gemv_launch1<6, WF>(d, grid, st); break;
+    case 8: gemv_launch1<8, WF>(d, grid, st); break;
+    case 12: gemv_launch1<12, WF>(d, grid, st); break;
+    case 14: gemv_launch1<14, WF>(d, grid, st); break;
+    case 16: gemv_launch1<16, WF>(d, grid, st); break;
     default: return set_error(MK2_EINVAL, "front: no GEMV engine for K = %d in %d parts", d.K, d.ks);
   }
   return MK2_OK;
@@ -582,7 +589,7 @@ struct FrontPlan {
   int ksA, ksW, ksC;
 };
 static FrontPlan front_plan(const mk2_front_shape* s) {
-  const bool f8 = s->weight_fmt == MK2_WFMT_FP8_BLOCK;
+  const bool f8 = s->weight_fmt != MK2_WFMT_BF16;
   const int NA = s->q_lora + s->kv_lora + s->rope, QB = s->heads * (s->nope + s->rope);
   const int tA = NA / 16 + (s->index_heads > 0 ? 128 / 16 : 0);
   const int tC = QB / 16 + s->index_heads * 128 / 16;
@@ -627,8 +634,10 @@ static int front_check_shape(const mk2_front_shape* s) {
   MK2_REQUIRE(s->heads >= 1 && s->heads <= 128, "front: heads must be in [1, 128], got %d", s->heads);
   MK2_REQUIRE(s->index_heads == 0 || (s->index_heads % 16 == 0 && s->index_heads <= 64),
               "front: index_heads must be 0 or a multiple of 16 up to 64, got %d", s->index_heads);
-  MK2_REQUIRE(s->weight_fmt == MK2_WFMT_BF16 || s->weight_fmt == MK2_WFMT_FP8_BLOCK,
-              "front: weight_fmt must be MK2_WFMT_BF16 or MK2_WFMT_FP8_BLOCK, got %d", s->weight_fmt);
+  MK2_REQUIRE(s->weight_fmt == MK2_WFMT_BF16 || s->weight_fmt == MK2_WFMT_FP8_BLOCK ||
+                  s->weight_fmt == MK2_WFMT_FP8_AITER16,
+              "front: weight_fmt must be MK2_WFMT_BF16, MK2_WFMT_FP8_BLOCK or MK2_WFMT_FP8_AITER16, got %d",
+              s->weight_fmt);
   MK2_REQUIRE(s->key_fmt == MK2_KEYS_FP4 || s->key_fmt == MK2_KEYS_FP8, "front: key_fmt must be MK2_KEYS_*");
   MK2_REQUIRE(s->max_position >= 0, "front: max_position must be >= 0");
   MK2_REQUIRE(s->eps > 0.f && s->index_eps > 0.f, "front: eps and index_eps must be positive");
@@ -655,7 +664,7 @@ extern "C" int mk2_front_launch(const mk2_front_args* a, mk2_stream_t stream) {
   if (rc) return rc;
   const mk2_front_shape& s = a->shape;
   const mk2_front_weights& w = a->weights;
-  const bool f8 = s.weight_fmt == MK2_WFMT_FP8_BLOCK;
+  const bool f8 = s.weight_fmt != MK2_WFMT_BF16;
   const bool idx = s.index_heads > 0;
   MK2_REQUIRE(a->x && a->positions && a->slots && a->rope_cos_sin && a->kv_cache && a->mla_q,
               "front: x, positions, slots, rope_cos_sin, kv_cache and mla_q must be set");
@@ -679,6 +688,11 @@ extern "C" int mk2_front_launch(const mk2_front_args* a, mk2_stream_t stream) {
   front_carve(&s, a->workspace, &ws);
   const FrontPlan pl = front_plan(&s);
   hipStream_t st = (hipStream_t)stream;
+  auto gemv_fmt = [&](const GemvDev& d) {
+    return s.weight_fmt == MK2_WFMT_FP8_AITER16 ? gemv_launch<MK2_WFMT_FP8_AITER16>(d, cus, st)
+           : f8                                 ? gemv_launch<MK2_WFMT_FP8_BLOCK>(d, cus, st)
+                                                : gemv_launch<MK2_WFMT_BF16>(d, cus, st);
+  };
   const int M = s.rows, NA = s.q_lora + s.kv_lora + s.rope, QB = s.heads * (s.nope + s.rope), IH = s.index_heads;
   auto seg = [](const void* w, const float* sc, float* out, int rows, int ld, long long pstride) {
     return GemvSeg{w, sc, out, rows, ld, pstride};
@@ -698,14 +712,14 @@ extern "C" int mk2_front_launch(const mk2_front_args* a, mk2_stream_t stream) {
       d.seg[1] = seg(w.w_ik, w.s_ik, ws.ik + (size_t)r0 * 128, 128, 128, (long long)M * 128);
       d.ntiles += 128 / 16;
     }
-    rc = f8 ? gemv_launch<true>(d, cus, st) : gemv_launch<false>(d, cus, st);
+    rc = gemv_fmt(d);
     if (rc) return rc;
     if (idx) {  // the head weights are bf16 in every checkpoint format
       GemvDev e = d;
       e.ks = pl.ksW;
       e.seg[0] = seg(w.w_iw, nullptr, ws.iw + (size_t)r0 * IH, IH, IH, (long long)M * IH);
       e.tiles0 = IH / 16; e.ntiles = e.tiles0;
-      rc = gemv_launch<false>(e, cus, st);
+      rc = gemv_launch<MK2_WFMT_BF16>(e, cus, st);
       if (rc) return rc;
     }
   }
@@ -737,7 +751,7 @@ extern "C" int mk2_front_launch(const mk2_front_args* a, mk2_stream_t stream) {
       d.seg[1] = seg(w.w_iq, w.s_iq, ws.iq + (size_t)r0 * IH * 128, IH * 128, IH * 128, (long long)M * IH * 128);
       d.ntiles += IH * 128 / 16;
     }
-    rc = f8 ? gemv_launch<true>(d, cus, st) : gemv_launch<false>(d, cus, st);
+    rc = gemv_fmt(d);
     if (rc) return rc;
   }
   // 4. the per-head stage

@@ -100,7 +100,7 @@ class LayerArgs(ctypes.Structure):
     ]
 
 
-MK2_WFMT_BF16, MK2_WFMT_FP8_BLOCK = 0, 1
+MK2_WFMT_BF16, MK2_WFMT_FP8_BLOCK, MK2_WFMT_FP8_AITER16 = 0, 1, 2
 
 
 class FrontShape(ctypes.Structure):

@@ -5,8 +5,9 @@ Mirrors the reference's weight binding and per-step cache binding
 ``_fp8_experts``, ``layer_weights``; glm53/spec.py:527-556 ``_bind``):
 
 - Read in place wherever the kernels read SGLang's layout as it is:
-  - the front's block-FP8 (or bf16) linears: ``fused_qkv_a_proj_with_mqa``,
-    ``q_b_proj``, and the indexer's ``wq_b`` and ``wk``;
+  - the front's block-FP8 (row-major, or preshuffled by SGLang into AITER's (16, 16)
+    layout) or bf16 linears: ``fused_qkv_a_proj_with_mqa``, ``q_b_proj``, and the
+    indexer's ``wq_b`` and ``wk``;
   - the norms, the indexer's ``weights_proj``, and ``w_kc`` / ``w_vc``;
   - the experts' block scales and the rotary table;
   - the caches from SGLang's token-to-KV pool: the unscaled E4M3 latent rows
@@ -55,19 +56,23 @@ def _linear_shuffled(lin) -> bool:
     return bool(getattr(lin, "aiter_bpreshuffled", False) or getattr(lin.weight, "is_shuffled", False))
 
 
-def linear(name: str, lin, rows: int, cols: int, allow_shuffled: bool = False):
-    """(weight bytes or bf16, f32 block scales or None, weight format) of a linear as
-    SGLang keeps it after loading (the reference's _linear, weights.py:214-224), read
-    in place.  AITER's (16, 16)-shuffled layout is refused unless `allow_shuffled`
-    (the front's GEMVs read row-major)."""
-    if _linear_shuffled(lin) and not allow_shuffled:
-        raise ValueError(f"needs {name} row-major (not AITER's shuffled layout)")
+def linear(name: str, lin, rows: int, cols: int, allow_shuffled: bool = True):
+    """(weight bytes or bf16, f32 block scales or None, weight format C.WFMT_*) of a
+    linear as SGLang keeps it after loading (the reference's _linear,
+    weights.py:214-224), read in place: bf16, block FP8 row-major, or block FP8 that
+    SGLang preshuffled into AITER's (16, 16) layout (WFMT_FP8_AITER16; refused with
+    `allow_shuffled` False).  A shuffled bf16 linear is refused."""
+    shuffled = _linear_shuffled(lin)
     w = lin.weight
     if w.dtype == torch.float8_e4m3fn:
+        if shuffled and not allow_shuffled:
+            raise ValueError(f"needs {name} row-major (not AITER's shuffled layout)")
         _need(name, w, (rows, cols), (torch.float8_e4m3fn,))
         s = _need(f"{name}.weight_scale_inv", getattr(lin, "weight_scale_inv", None),
                   ((rows + 127) // 128, (cols + 127) // 128), (torch.float32,))
-        return _fp8_bytes(w), s, C.WFMT_FP8_BLOCK
+        return _fp8_bytes(w), s, C.WFMT_FP8_AITER16 if shuffled else C.WFMT_FP8_BLOCK
+    if shuffled:
+        raise ValueError(f"needs {name} row-major or block FP8 (a shuffled bf16 linear)")
     _need(name, w, (rows, cols), (torch.bfloat16,))
     return w, None, C.WFMT_BF16
 
@@ -75,11 +80,9 @@ def linear(name: str, lin, rows: int, cols: int, allow_shuffled: bool = False):
 def _bf16_of(name: str, lin, rows: int, cols: int) -> torch.Tensor:
     """A linear's weight as bf16 (dequantized from block FP8, unshuffled from AITER's
     layout): a copy for a kernel that takes bf16 tiles."""
-    w, s, fmt = linear(name, lin, rows, cols, allow_shuffled=True)
-    if _linear_shuffled(lin):
-        if fmt != C.WFMT_FP8_BLOCK:
-            raise ValueError(f"needs {name} row-major or block FP8 in AITER's layout")
-        w = aiter_unshuffle(w)
+    w, s, fmt = linear(name, lin, rows, cols)
+    if fmt == C.WFMT_FP8_AITER16:
+        w, fmt = aiter_unshuffle(w), C.WFMT_FP8_BLOCK
     return (_block_dequant(w, s) if fmt == C.WFMT_FP8_BLOCK else w.float()).to(torch.bfloat16)
 
 
@@ -156,10 +159,10 @@ def _shared_fp8(mlp, cfg: C.MoEConfig, ns) -> None:
     H, SI = cfg.hidden, cfg.shared_inter
     out = []
     for name, lin, rows, cols in (("gate_up_proj", sh.gate_up_proj, 2 * SI, H), ("down_proj", sh.down_proj, H, SI)):
-        shuffled = _linear_shuffled(lin)
-        w, s, f = linear("shared_experts." + name, lin, rows, cols, allow_shuffled=True)
-        if f != C.WFMT_FP8_BLOCK:
+        w, s, f = linear("shared_experts." + name, lin, rows, cols)
+        if f not in (C.WFMT_FP8_BLOCK, C.WFMT_FP8_AITER16):
             raise ValueError("needs the shared expert in block FP8")
+        shuffled = f == C.WFMT_FP8_AITER16
         if cfg.weight_layout == C.WLAYOUT_AITER16:
             out.append((w if shuffled else aiter_shuffle(w), s))
         else:

@@ -152,6 +152,7 @@ class K2Config:
 
 WFMT_BF16 = 0  # attention weights as loaded in bf16
 WFMT_FP8_BLOCK = 1  # E4M3 with f32 128 x 128 block scales
+WFMT_FP8_AITER16 = 2  # the same, the bytes in AITER's (16, 16) layout (SGLang's preshuffled linears)
 _ENGINE_K = (1024, 2048, 3072, 4096, 6144, 7168, 8192)
 
 
@@ -187,7 +188,7 @@ class FrontConfig:
             raise ValueError("heads must be in [1, 128]")
         if self.index_heads and (self.index_heads % 16 or self.index_heads > 64):
             raise ValueError("index_heads must be 0 or a multiple of 16 up to 64")
-        if self.weight_fmt not in (WFMT_BF16, WFMT_FP8_BLOCK):
+        if self.weight_fmt not in (WFMT_BF16, WFMT_FP8_BLOCK, WFMT_FP8_AITER16):
             raise ValueError(f"unknown weight format {self.weight_fmt}")
         if self.keys not in (KEYS_FP4, KEYS_FP8):
             raise ValueError(f"unknown index cache format {self.keys}")

@@ -124,7 +124,7 @@ class FrontOp:
         self.shape = _lib.FrontShape(rows, cfg.hidden, cfg.q_lora, cfg.kv_lora, cfg.rope, cfg.nope, cfg.heads,
                                      cfg.index_heads, cfg.weight_fmt, cfg.keys, int(cfg.kv_scaled),
                                      cfg.max_position, cfg.eps, cfg.index_eps)
-        wdt = torch.uint8 if cfg.weight_fmt == C.WFMT_FP8_BLOCK else torch.bfloat16
+        wdt = torch.bfloat16 if cfg.weight_fmt == C.WFMT_BF16 else torch.uint8
         NA = cfg.q_lora + cfg.kv_lora + cfg.rope
         _need(w.g_in, "g_in", torch.bfloat16, (cfg.hidden,))
         _need(w.w_qkv_a, "w_qkv_a", wdt, (NA, cfg.hidden))

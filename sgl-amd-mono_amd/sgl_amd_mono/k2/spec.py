@@ -242,15 +242,17 @@ def _build(model, hf_config, ctx):
     tree) and returns the forward; ``ctx`` may carry pool_of / page_table_of."""
     from dataclasses import replace
 
+    from .binding import experts_layout, linear
+
     cfg = config_from_hf(hf_config)
     layer0 = model.model.layers[0]
-    first = layer0.self_attn.fused_qkv_a_proj_with_mqa.weight
-    wfmt = C.WFMT_FP8_BLOCK if first.dtype == torch.float8_e4m3fn else C.WFMT_BF16
+    qkv = layer0.self_attn.fused_qkv_a_proj_with_mqa
+    first = qkv.weight
+    # the front's format (bf16, block FP8, or block FP8 SGLang preshuffled for AITER)
+    _, _, wfmt = linear("fused_qkv_a_proj_with_mqa", qkv, first.shape[0], first.shape[1])
     # SGLang's DSA index cache holds FP8 pages; its experts' dtype names their mode
     efmt = C.FMT_FP8 if layer0.mlp.experts.w13_weight.dtype == torch.float8_e4m3fn else C.FMT_MXFP4
     # experts SGLang rewrote for AITER's MoE are read in place in that layout
-    from .binding import experts_layout
-
     layout = experts_layout(layer0.mlp.experts)
     cfg = replace(cfg, moe=replace(cfg.moe, expert_fmt=efmt, weight_layout=layout),
                   indexer=replace(cfg.indexer, keys=C.KEYS_FP8))

@@ -196,6 +196,19 @@ def _front_weight(g, rows, cols, fmt, device, std=WEIGHT_STD):
     return w.to(torch.bfloat16).contiguous(), None
 
 
+def front_in_layout(ns, fmt: int):
+    """make_front's block-FP8 weights (W_qkv_a, W_q_b, W_iq, W_ik) in AITER's (16, 16)
+    layout (C.WFMT_FP8_AITER16): the same codes and scales re-laid."""
+    if fmt != C.WFMT_FP8_AITER16 or ns.cfg.weight_fmt != C.WFMT_FP8_BLOCK:
+        raise ValueError("re-lays block-FP8 front weights into AITER's layout")
+    out = SimpleNamespace(**vars(ns))
+    for name in ("w_qkv_a", "w_q_b", "w_iq", "w_ik"):
+        if getattr(ns, name) is not None:
+            setattr(out, name, aiter_shuffle(getattr(ns, name)))
+    out.cfg = replace(ns.cfg, weight_fmt=fmt)
+    return out
+
+
 def make_front(cfg: C.FrontConfig, rows: int, seed: int, device, n_pages: int = 64):
     """The front's weights in SGLang's formats (row-major bf16 or E4M3 + 128 x 128 f32
     block scales, w_kc as [heads][kv_lora][nope]), residual rows x ~ N(0, 1), distinct

@@ -8,7 +8,10 @@ The attribute names, dtypes and memory layouts are those the reference binds
 - the experts hold the shared expert fused as physical expert n_experts (block FP8),
   or are MXFP4 (E2M1 bytes + E8M0 codes) beside a block-FP8 ``shared_experts``
   module; with ``shuffled`` they are in AITER's (16, 16) layout with e8m0_shuffle'd
-  codes and marked ``is_shuffled``, as SGLang leaves them for AITER's MoE;
+  codes and marked ``is_shuffled``, as SGLang leaves them for AITER's MoE, and the
+  block-FP8 linears are preshuffled into the same layout and marked
+  ``aiter_bpreshuffled`` (their scales unchanged), as SGLang leaves them for AITER's
+  preshuffled GEMM;
 - the token-to-KV pool gives E4M3 rows [slots, 1, 576] and FP8 index pages.
 The caches are filled with a random history, so a step's rows have context.
 """
@@ -36,10 +39,14 @@ def _gen(seed, device):
     return g
 
 
-def _fp8_linear(g, rows, cols, device, std=0.02):
+def _fp8_linear(g, rows, cols, device, std=0.02, shuffled=False):
+    from sgl_amd_mono.k2.packing import aiter_shuffle
     from sgl_amd_mono.k2.quant import quant_fp8_block
 
     q, s = quant_fp8_block(torch.randn(rows, cols, generator=g, device=device) * std)
+    if shuffled:
+        return SimpleNamespace(weight=aiter_shuffle(q).view(torch.float8_e4m3fn), weight_scale_inv=s,
+                               aiter_bpreshuffled=True)
     return SimpleNamespace(weight=q.view(torch.float8_e4m3fn), weight_scale_inv=s)
 
 
@@ -84,7 +91,8 @@ def _experts(g, hf, device, experts: str, shuffled: bool):
     if shuffled:
         w13, s13, w2, s2 = _mark(aiter_shuffle(w13)), e8m0_shuffle(s13), _mark(aiter_shuffle(w2)), e8m0_shuffle(s2)
     SI = I * hf.n_shared_experts
-    shared = SimpleNamespace(gate_up_proj=_fp8_linear(g, 2 * SI, H, device), down_proj=_fp8_linear(g, H, SI, device))
+    shared = SimpleNamespace(gate_up_proj=_fp8_linear(g, 2 * SI, H, device, shuffled=shuffled),
+                             down_proj=_fp8_linear(g, H, SI, device, shuffled=shuffled))
     return SimpleNamespace(w13_weight=w13, w13_weight_scale=s13, w2_weight=w2, w2_weight_scale=s2), shared
 
 
@@ -99,16 +107,17 @@ def make_model(seed: int, device, hf=HF, vocab=VOCAB, layers=LAYERS, experts: st
     mods = []
     for _ in range(layers):
         attn = SimpleNamespace(
-            fused_qkv_a_proj_with_mqa=_fp8_linear(g, QL + KV + R, H, device),
+            fused_qkv_a_proj_with_mqa=_fp8_linear(g, QL + KV + R, H, device, shuffled=shuffled),
             q_a_layernorm=_norm(g, QL, device), kv_a_layernorm=_norm(g, KV, device),
-            q_b_proj=_fp8_linear(g, NH * (NO + R), QL, device),
-            o_proj=_fp8_linear(g, H, NH * V, device),
+            q_b_proj=_fp8_linear(g, NH * (NO + R), QL, device, shuffled=shuffled),
+            o_proj=_fp8_linear(g, H, NH * V, device, shuffled=shuffled),
             # SGLang's memory order, seen through the logical shapes it keeps
             w_kc=(0.05 * torch.randn(NH, KV, NO, generator=g, device=device)).to(torch.bfloat16).transpose(1, 2),
             w_vc=(0.02 * torch.randn(NH, V, KV, generator=g, device=device)).to(torch.bfloat16).transpose(1, 2),
             rotary_emb=SimpleNamespace(cos_sin_cache=rope),
             indexer=SimpleNamespace(
-                wq_b=_fp8_linear(g, IH * 128, QL, device), wk=_fp8_linear(g, 128, H, device),
+                wq_b=_fp8_linear(g, IH * 128, QL, device, shuffled=shuffled),
+                wk=_fp8_linear(g, 128, H, device, shuffled=shuffled),
                 k_norm=SimpleNamespace(weight=1 + 0.1 * torch.randn(128, generator=g, device=device),
                                        bias=0.1 * torch.randn(128, generator=g, device=device)),
                 weights_proj=SimpleNamespace(

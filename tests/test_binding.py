@@ -42,6 +42,34 @@ def test_front_weights_are_read_in_place(model):
     assert w.g_ik.dtype == torch.float32
 
 
+def test_shuffled_front_linears_are_read_in_place():
+    """Block-FP8 front linears SGLang preshuffled for AITER's GEMM (aiter_bpreshuffled):
+    bound in place as WFMT_FP8_AITER16, the same codes as the row-major model's; W_o is
+    unshuffled into the same bf16 tiles; a front mixing the two layouts is refused."""
+    from sgl_amd_mono.k2 import binding
+    from sgl_amd_mono.k2 import config as C
+    from sgl_amd_mono.k2.packing import aiter_unshuffle
+
+    cfg, fc = _cfgs()
+    row = F.make_model(3, torch.device("cpu"), layers=1).model.layers[0]
+    shf = F.make_model(3, torch.device("cpu"), layers=1, shuffled=True).model.layers[0]
+    with pytest.raises(ValueError, match="one format"):
+        binding.bind_front(shf, fc)
+    a = binding.bind_front(shf, replace(fc, weight_fmt=C.WFMT_FP8_AITER16))
+    t = binding.bind_front(row, fc)
+    sa = shf.self_attn
+    assert a.w_qkv_a.data_ptr() == sa.fused_qkv_a_proj_with_mqa.weight.data_ptr()
+    assert a.w_ik.data_ptr() == sa.indexer.wk.weight.data_ptr()
+    for n in ("w_qkv_a", "w_q_b", "w_iq", "w_ik"):
+        assert torch.equal(aiter_unshuffle(getattr(a, n)), getattr(t, n)), n
+    for n in ("s_qkv_a", "s_q_b", "s_iq", "s_ik"):
+        assert torch.equal(getattr(a, n), getattr(t, n)), n
+    assert torch.equal(binding.bind_mla(shf, cfg.mla, fc.nope).w_o, binding.bind_mla(row, cfg.mla, fc.nope).w_o)
+    sa.q_b_proj = row.self_attn.q_b_proj  # one linear row-major, the rest shuffled
+    with pytest.raises(ValueError, match="one format"):
+        binding.bind_front(shf, replace(fc, weight_fmt=C.WFMT_FP8_AITER16))
+
+
 def test_mla_and_moe_weights(model):
     from sgl_amd_mono.k2 import binding, synth
 
@@ -74,7 +102,10 @@ def test_refusals(model):
     bad = SimpleNamespace(weight=L.self_attn.q_b_proj.weight, weight_scale_inv=L.self_attn.q_b_proj.weight_scale_inv,
                           aiter_bpreshuffled=True)
     with pytest.raises(ValueError, match="shuffled"):
-        binding.linear("q_b_proj", bad, bad.weight.shape[0], bad.weight.shape[1])
+        binding.linear("q_b_proj", bad, bad.weight.shape[0], bad.weight.shape[1], allow_shuffled=False)
+    bf = SimpleNamespace(weight=L.self_attn.q_b_proj.weight.float().to(torch.bfloat16), aiter_bpreshuffled=True)
+    with pytest.raises(ValueError, match="shuffled bf16"):
+        binding.linear("q_b_proj", bf, bf.weight.shape[0], bf.weight.shape[1])
     with pytest.raises(ValueError, match="q_b_proj"):
         binding.linear("q_b_proj", L.self_attn.q_b_proj, 7, 7)
     with pytest.raises(ValueError, match="one format"):
@@ -141,5 +172,8 @@ def test_mxfp4_experts_in_both_layouts():
     assert torch.equal(e8m0_shuffle(t.w2s), a.s2_p) and torch.equal(pack_e8m0(t.w2s), t.s2_p)
     sh = row.mlp.shared_experts
     assert torch.equal(t.ws13_p, pack_tiles(sh.gate_up_proj.weight.view(torch.uint8), 32))
-    assert torch.equal(a.ws13_p, aiter_shuffle(shf.mlp.shared_experts.gate_up_proj.weight.view(torch.uint8)))
+    # the shuffled model's shared expert is preshuffled already (in place); the
+    # row-major one, shuffled, is the same bytes
+    assert a.ws13_p.data_ptr() == shf.mlp.shared_experts.gate_up_proj.weight.data_ptr()
+    assert torch.equal(a.ws13_p, aiter_shuffle(sh.gate_up_proj.weight.view(torch.uint8)))
     assert t.ws13s.data_ptr() == sh.gate_up_proj.weight_scale_inv.data_ptr()

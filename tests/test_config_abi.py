@@ -126,7 +126,7 @@ def test_front_validate_matches_c():
     _l, L = _lib()
     seen = {True: 0, False: 0}
     for hidden, q_lora, nope, ih, rows, fmt in itertools.product(
-        (1024, 1536, 6144, 7168, 9216), (1536, 2048), (128, 160, 192), (0, 16, 48, 80), (1, 32, 33), (0, 1, 2),
+        (1024, 1536, 6144, 7168, 9216), (1536, 2048), (128, 160, 192), (0, 16, 48, 80), (1, 32, 33), (0, 1, 2, 3),
     ):
         cfg = rep(C.C7_FRONT, hidden=hidden, q_lora=q_lora, nope=nope, index_heads=ih, weight_fmt=fmt)
         s = _l.FrontShape(rows, cfg.hidden, cfg.q_lora, cfg.kv_lora, cfg.rope, cfg.nope, cfg.heads, cfg.index_heads,

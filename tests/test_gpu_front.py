@@ -165,3 +165,29 @@ def test_front_pad_rows_and_no_indexer():
     ns0, *out0 = _run(cfg0, 4, seed=713)
     assert out0[1] is None and out0[2] is None
     print(_check(cfg0, ns0, *out0))
+
+
+@pytest.mark.parametrize("rows", [8, 32])
+def test_front_aiter_layout_bits(rows):
+    """Block-FP8 weights SGLang preshuffled into AITER's (16, 16) layout
+    (WFMT_FP8_AITER16), read in place: the same codes as the row-major weights give
+    the same bits -- queries, head weights and both caches."""
+    from sgl_amd_mono.k2 import config as C
+    from sgl_amd_mono.k2 import synth
+    from sgl_amd_mono.k2.ops import FrontOp
+
+    dev = _dev()
+    cfg = C.C7_FRONT
+    ns = synth.make_front(cfg, rows, 720 + rows, dev)
+    sh = synth.front_in_layout(ns, C.WFMT_FP8_AITER16)
+    res = []
+    for n in (ns, sh):
+        kv, ic = ns.kv_cache.clone(), ns.index_cache.clone()
+        ks = None if ns.kv_scale is None else ns.kv_scale.clone()
+        isc = None if ns.index_scale is None else ns.index_scale.clone()
+        out = FrontOp(n.cfg, n, rows, device=dev)(ns.x, ns.positions, ns.slots, ns.rope_cos_sin, kv, ks, ic, isc)
+        torch.cuda.synchronize()
+        res.append([cpu(t) for t in (*out, kv, ic, ks, isc) if t is not None])
+    assert len(res[0]) == len(res[1]) >= 5
+    for a, b in zip(*res):
+        assert torch.equal(a, b)

@@ -77,8 +77,9 @@ def test_routed_decode_step(rows):
 
 @pytest.mark.parametrize("experts", ["fp8", "mxfp4"])
 def test_shuffled_experts_step_matches_row_major(experts):
-    """The same model with its experts in AITER's (16, 16) layout (read in place) and
-    row-major (copied into tiles): one routed step gives the same logits and caches."""
+    """The same model with its experts and block-FP8 linears in AITER's (16, 16)
+    layout (read in place; W_o unshuffled into bf16 tiles) and row-major (experts
+    copied into tiles): one routed step gives the same logits and caches."""
     from sgl_amd_mono import _registry as reg
     from sgl_amd_mono.k2 import config as C
     from sgl_amd_mono.k2 import spec
@@ -96,6 +97,7 @@ def test_shuffled_experts_step_matches_row_major(experts):
         fwd = spec.SPEC.build(lm, F.HF, ctx)
         assert fwd.cfg.moe.weight_layout == (C.WLAYOUT_AITER16 if shuffled else C.WLAYOUT_TILES)
         assert fwd.cfg.moe.expert_fmt == (C.FMT_FP8 if experts == "fp8" else C.FMT_MXFP4)
+        assert fwd.front_cfg.weight_fmt == (C.WFMT_FP8_AITER16 if shuffled else C.WFMT_FP8_BLOCK)
         logits = fwd.forward(reg.Plan(key=reg.ShapeKey("decode", rows, 1)), st.input_ids, st.positions,
                              st.forward_batch)
         torch.cuda.synchronize()

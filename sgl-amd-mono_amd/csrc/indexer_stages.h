@@ -364,9 +364,11 @@ MK2_DEV int block_sum_int(int v, int* lds) {
   return t;
 }
 
-// One wave: the bin of hist[nbins] (LDS, nbins a multiple of 64) where the count from
-// the top reaches `need`, and through *above the count of the bins above it.  Lane l
-// owns the bins nbins - per*(l+1) .. nbins - per*l - 1.
+// One wave: the bin of hist[nbins] (LDS, nbins a multiple of 64, at most 4096) where
+// the count from the top reaches `need`, and through *above the count of the bins
+// above it.  Lane l owns the bins nbins - per*(l+1) .. nbins - per*l - 1; the lane L
+// whose run holds the bin found, its run is spread over lanes 0 .. per - 1 (one bin a
+// lane, from the top) and scanned again.
 MK2_DEV int wave_find_bin(const int* hist, int nbins, int need, int* above) {
   const int lane = threadIdx.x & 63, per = nbins >> 6;
   const int hi = nbins - per * lane - 1;  // this lane's highest bin
@@ -376,23 +378,13 @@ MK2_DEV int wave_find_bin(const int* hist, int nbins, int need, int* above) {
   const int inc = wave_incl_scan(sum), excl = inc - sum;
   const uint64_t hit = __ballot(excl < need && inc >= need);
   const int L = hit ? __ffsll((long long)hit) - 1 : 63;
-  int bin = 0, ab = 0;
-  if (lane == L) {
-    int a = excl;
-    bin = hi - per + 1;
-    ab = a;
-    for (int i = 0; i < per; ++i) {
-      const int h = hist[hi - i];
-      if (a + h >= need) {
-        bin = hi - i;
-        ab = a;
-        break;
-      }
-      a += h;
-    }
-  }
-  *above = __builtin_amdgcn_readlane(ab, L);  // L is the same in every lane
-  return __builtin_amdgcn_readlane(bin, L);
+  const int hiL = nbins - per * L - 1, aL = __builtin_amdgcn_readlane(excl, L);
+  const int h = lane < per ? hist[hiL - lane] : 0;
+  const int a = aL + wave_incl_scan(h);  // the count down to bin hiL - lane
+  const uint64_t hit2 = __ballot(lane < per && a >= need);
+  const int i = hit2 ? __ffsll((long long)hit2) - 1 : per - 1;
+  *above = hit2 ? __builtin_amdgcn_readlane(a - h, i) : aL;
+  return hiL - i;
 }
 
 // One wave: the 12-bit bin b1 of row r's k-th key from the two-level histogram in
@@ -515,15 +507,22 @@ MK2_DEV void idx_clear_hist(const IdxDev& p, int r) {
 // Task (row r, chunk), with b1 the 12-bit bin of the row's k-th key: the chunk's keys
 // above bin b1 all make the list, and go to it directly, in position order, after
 // the row's earlier chunks' (the list's first part); the keys in bin b1 go to
-// cand[r][chunk * IDX_CHUNK ..], in position order, for the row's last slice to
-// finish the list.  The chunk's two counts are published in ccount[r][chunk] first;
-// then the task waits for the earlier chunks' counts (tasks only wait on chunks of
-// lower index, which publish before they wait, so with every task started every wait
-// ends; a wait past `spin` polls, or the sticky error word `err` set, gives up and
-// sets it).  Returns whether S.res[0..1] now hold b1 and the count above it.
+// cand[r][chunk * IDX_CHUNK ..], in position order, for the row's select to finish
+// the list.  The chunk's two counts are published in ccount[r][chunk] first, then its
+// bin-b1 keys are stored and `published()` runs (every thread, every path: the
+// persistent layer counts the chunk out there, so that the row's select can start
+// while the slices still list their keys above the bin); then the task waits for the
+// earlier chunks' counts (tasks only wait on chunks of lower index, which publish
+// before they wait, so with every task started every wait ends; a wait past `spin`
+// polls, or the sticky error word `err` set, gives up and sets it).  Returns whether
+// S.res[0..1] now hold b1 and the count above it.
 constexpr int CC_FLAG = 1 << 30;
-template <int NT>
-MK2_DEV bool idx_slice(const IdxDev& p, int r, int chunk, TopkLds& S, int spin, int* err, uint32_t tag) {
+struct NoPub {
+  MK2_DEV void operator()() const {}
+};
+template <int NT, class Pub = NoPub>
+MK2_DEV bool idx_slice(const IdxDev& p, int r, int chunk, TopkLds& S, int spin, int* err, uint32_t tag,
+                       Pub published = Pub()) {
   constexpr int PER = IDX_CHUNK / NT;  // consecutive positions a thread
   static_assert(PER % 4 == 0, "a thread reads whole 16-byte groups of scores");
   const int tid = threadIdx.x;
@@ -532,6 +531,7 @@ MK2_DEV bool idx_slice(const IdxDev& p, int r, int chunk, TopkLds& S, int spin, 
   int* cnt_out = p.ccount + (size_t)r * p.nchk + chunk;
   if (n <= k || k_begin >= n) {
     if (tid == 0) st_dev_i32(cnt_out, CC_FLAG);
+    published();
     return false;
   }
   // the chunk's scores first: their loads overlap the threshold search
@@ -575,6 +575,7 @@ MK2_DEV bool idx_slice(const IdxDev& p, int r, int chunk, TopkLds& S, int spin, 
       ++at;
     }
   }
+  published();
   // the keys above bin b1 in the row's earlier chunks (nchk <= 64: a lane a chunk)
   if (tid < 64) {
     const int lane = tid;

@@ -34,7 +34,7 @@ constexpr int SY_LINE = 32;  // ints a line
 constexpr int K2_LANES = 16;
 enum : int {
   SY_SCORE = 0,    // [32] score chunks done, per row
-  SY_SLICE = 32,   // [32] top-k slices done, per row
+  SY_SLICE = 32,   // [32] top-k slices counted out (their counts and bin keys out), per row
   // lines 64 .. 95: unused (the splits poll the tagged top-k list)
   SY_SPLIT = 96,   // [32] attention splits done, per row
   SY_ROUTE = 128,  // the routing's table and list are out (the down)
@@ -194,19 +194,25 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
     // ---- top-k slices: each chunk lists its keys above the row's threshold bin and
     // keeps its keys in the bin
     k2_stamp(p, 3 * st);
-    // slices on the workgroups of their score chunks (base unchanged); the last slice
-    // of a row finishes the row's list from the keys in the threshold bin
+    // slices on the workgroups of their score chunks (base unchanged).  A slice counts
+    // out once its chunk's counts and bin keys are out; the last to count out of a
+    // row lists its own keys above the bin, then finishes the row's list from the
+    // keys in the threshold bin, while the others still list theirs
     K2_TASKS(t, R * nchk) {
       const int r = t / nchk;
       if (!k2_wait(p, seen, SY_SCORE + r, nchk, t < G ? 3 * st + 1 : -1)) return;
-      const bool known = idx_slice<K2_NT>(p.idx, r, t % nchk, S.topk, p.spin_limit, k2_ctr(p, SY_ERR), tp.tag);
-      if (k2_signal_last1(p, SY_SLICE + r, nchk, &last_flag)) {
+      bool last = false;
+      const bool known = idx_slice<K2_NT>(p.idx, r, t % nchk, S.topk, p.spin_limit, k2_ctr(p, SY_ERR), tp.tag,
+                                          [&] { last = k2_signal_last1(p, SY_SLICE + r, nchk, &last_flag); });
+      if (last) {
         k2_stamp(p, 3 * (st + 1));
         k2_stamp(p, 3 * (st + 1) + 1);
         // this workgroup's own slice of row r may have left the threshold in LDS
         idx_select<K2_NT>(p.idx, r, S.topk, tp.tag, known);
         k2_stamp(p, 3 * (st + 1) + 2);
-        idx_topk_reset<K2_NT>(p.idx, r);  // every slice of the row is done with them
+        // every slice read the threshold before it counted out; the chunk counts are
+        // cleared by the last workgroup out (slices may still poll them here)
+        idx_clear_hist<K2_NT>(p.idx, r);
       }
     }
     K2_NEXT(R * nchk);
@@ -321,6 +327,8 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
       if (threadIdx.x == 0 && p.status) atomicOr(p.status, 1);
       drain_memory();
       __syncthreads();
+    } else {  // the chunk counts (the selects cleared the histograms)
+      for (int i = threadIdx.x; i < R * p.idx.nchk; i += K2_NT) st_dev_i32(p.idx.ccount + i, 0);
     }
     for (int l = threadIdx.x; l < SY_LINES; l += K2_NT)
       __hip_atomic_store(k2_ctr(p, l), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -269,13 +269,18 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
     }
     K2_NEXT(nrt);
     k2_stamp(p, 3 * st++ + 2);
-    // ---- routing, on one workgroup (one without an up/gate task, when the up/gate
-    // stage leaves some): it polls the router tasks' logits and puts out the tagged
-    // expert list, then the route-weight table, published by SY_ROUTE for the down
+    // ---- routing, on one workgroup: one without a router task (it polls while they
+    // run) and with the fewest up/gate tasks.  It polls the router tasks' logits and
+    // puts out the tagged expert list, then the route-weight table, published by
+    // SY_ROUTE for the down
     const int up_r = p.moe.Dmax * (p.moe.I / p.moe.UC);
     const int up_sh = p.moe.n_shared * (p.moe.SI / 32);
     const int up_total = up_r + up_sh;
-    if (b == (base + (up_total < G ? up_total : G - 1)) % G) {
+    // the up/gate tasks start at workgroup `base`; from base + up_total % G on, the
+    // workgroups hold one fewer; the router tasks ended on the nrt workgroups before base
+    int route_at = up_total % G;
+    if (nrt < G && route_at >= G - nrt) route_at = G - nrt - 1;
+    if (b == (base + route_at) % G) {
       k2_stamp(p, 3 * st);
       if (!moe_route<K2_NT, kCompact<NCG, FMT>>(p.moe, S.route, tp, [&](int i) { k2_stamp(p, 3 * K2_STAGES + i); }))
         return;

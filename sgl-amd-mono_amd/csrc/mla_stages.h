@@ -48,7 +48,7 @@ struct MlaDev {
   float* part_ml;        // [rows][nsplit][16][2]
   float* o_lat_f32;      // optional [rows][16][512]
   bf16_t* o;             // [rows][16 * v_dim]
-  float* ssp;            // optional [hidden/16][rows]: sums of squares of out over 16 columns
+  float* ssp;            // optional [rows][hidden/16]: sums of squares of out over 16 columns
 };
 
 struct MlaSplitLds {
@@ -463,7 +463,7 @@ MK2_DEV void mla_oproj(const MlaDev& p, int nt0, int nt1, float* red, Wait wait 
     if (p.ssp) {  // the 16 columns of (tile, row) are one DPP row: 16 * rows and NT are multiples of 16
       const float vb = bf16_to_f32(ob);
       const float ss = row16_sum(vb * vb);
-      if (n16 == 0) st_dev_f32(p.ssp + (size_t)(j == 0 ? nt0 : nt1) * p.rows + row, ss);
+      if (n16 == 0) st_dev_f32(p.ssp + (size_t)row * (p.hidden / 16) + (j == 0 ? nt0 : nt1), ss);
     }
   }
   __syncthreads();

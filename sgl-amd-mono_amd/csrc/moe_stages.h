@@ -41,7 +41,7 @@ struct MoeDev {
   const float* ss2;
   bf16_t* out;
   // workspace
-  float* ssp;        // [H/16][M] the rows' sums of squares over 16 columns (RMSNorm)
+  float* ssp;        // [M][H/16] the rows' sums of squares over 16 columns (RMSNorm)
   bf16_t* xn;        // [M][H] normalized rows
   uint8_t* xq;       // [M][H] E4M3 codes (A8W4, W8A8) or [M][H/2] E2M1 codes (A4W4)
   uint8_t* xs;       // [M][H/32] E8M0 (A8W4, A4W4)
@@ -95,7 +95,7 @@ MK2_DEV float block_sum(float v, float* lds) {
 }
 
 // ------------------------------------------------------- stage: sums of squares
-// Row r, columns blk * 4 NT ..: ssp[t][r] = sum of x^2 over columns 16t .. 16t+15,
+// Row r, columns blk * 4 NT ..: ssp[r][t] = sum of x^2 over columns 16t .. 16t+15,
 // reduced across one DPP row of 16 lanes.  W_o's epilogue produces the same sums of
 // its output tiles with the same reduction, so either producer gives the same bits.
 // NT is a multiple of 64 and H of 4 NT, so every pass runs whole 16-lane rows.
@@ -110,7 +110,7 @@ MK2_DEV void moe_sumsq(const MoeDev& p, int r, int blk) {  // columns blk * 4 NT
     const int c = blk * 4 * NT + threadIdx.x + i * NT;
     const float v = bf16_to_f32((bf16_t)x[i]);
     const float ss = row16_sum(v * v);
-    if ((c & 15) == 0) st_dev_f32(p.ssp + (size_t)(c >> 4) * p.M + r, ss);
+    if ((c & 15) == 0) st_dev_f32(p.ssp + (size_t)r * (p.H / 16) + (c >> 4), ss);
   }
 }
 
@@ -256,10 +256,10 @@ MK2_DEV void moe_router(const MoeDev& p, int nt, int kc, RouterLds& L, uint32_t 
   load_a_bf16(p.w_router + ((size_t)nt * KB + kc * kbs + min(wave, kbs - 1)) * 4096, lane, a0);
   const uint4 gam = p.norm ? *(const uint4*)(p.gamma + c0 + c8) : make_uint4(0, 0, 0, 0);
   if (!wait()) return;
-  uint4 xv[RMAX];
+  uint4 xv[RMAX];  // rows past M are not loaded (uniform in a wave: its lanes share a row)
 #pragma unroll
   for (int i = 0; i < RMAX; ++i)
-    xv[i] = ldp_16(p.x + (size_t)min(r0 + rstep * i, p.M - 1) * p.H + c0 + c8);
+    xv[i] = r0 + rstep * i < p.M ? ldp_16(p.x + (size_t)(r0 + rstep * i) * p.H + c0 + c8) : make_uint4(0, 0, 0, 0);
   if (p.norm) {
     const int nt16 = p.H / 16;
     for (int r = wave; r < p.M; r += NW) {
@@ -267,7 +267,7 @@ MK2_DEV void moe_router(const MoeDev& p, int nt, int kc, RouterLds& L, uint32_t 
       for (int t0 = 0; t0 < nt16; t0 += 64 * 8) {
         float v[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = ldp_f32(p.ssp + (size_t)min(t0 + lane + 64 * u, nt16 - 1) * p.M + r);
+        for (int u = 0; u < 8; ++u) v[u] = ldp_f32(p.ssp + (size_t)r * nt16 + min(t0 + lane + 64 * u, nt16 - 1));
 #pragma unroll
         for (int u = 0; u < 8; ++u)
           if (t0 + lane + 64 * u < nt16) ss += v[u];

@@ -96,6 +96,7 @@ int idx_fill(const mk2_indexer_args* a, IdxDev* d) {
   d->cscale = a->cache_scale; d->kfmt = a->shape.key_fmt;
   d->pt = a->page_table; d->req = a->req_ids; d->ctx = a->ctx_len;
   d->scores = a->scores; d->out = a->topk;
+  d->scores_out = a->scores != nullptr;
   d->nchk = (d->max_ctx + IDX_CHUNK - 1) / IDX_CHUNK;
   return MK2_OK;
 }

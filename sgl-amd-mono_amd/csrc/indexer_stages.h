@@ -61,6 +61,8 @@ struct IdxDev {
   const int* req;       // [rows]
   const int* ctx;       // [rows]
   float* scores;        // [rows][max_ctx]
+  int scores_out;       // the caller takes the scores (else the persistent layer, whose
+                        // slices read them in LDS, leaves `scores` unwritten)
   int* out;             // [rows][topk]
   uint64_t* tlist;      // [rows][topk] the same list as tagged words (the persistent
                         // layer's splits poll it), or null
@@ -104,9 +106,11 @@ struct IdxScoreLds {
 // LDS, and computes group by group as the keys arrive.  The loads are unconditional
 // (groups past the row's end read page id 0, and their results are dropped) and the
 // scores wait in LDS until the loop is done: a store or a branch between the loads
-// would make every group wait for all memory traffic.
+// would make every group wait for all memory traffic.  `keep` (LDS, IDX_CHUNK floats,
+// or null: L.sc) holds them for the chunk's slice on the same workgroup; with `keep`
+// they go to `scores` only when the caller takes them.
 template <int NT, int KF>
-MK2_DEV void idx_score_keys(const IdxDev& p, int r, int chunk, IdxScoreLds& L) {
+MK2_DEV void idx_score_keys(const IdxDev& p, int r, int chunk, IdxScoreLds& L, float* keep) {
   constexpr bool F8 = KF == IDX_KEYS_FP8;
   constexpr int NW = NT / 64;
   constexpr int GPW = IDX_CHUNK / 16 / NW;  // 16-key groups a wave
@@ -209,6 +213,7 @@ MK2_DEV void idx_score_keys(const IdxDev& p, int r, int chunk, IdxScoreLds& L) {
     }
   }
   float* srow = p.scores + (size_t)r * p.max_ctx;
+  float* sc = keep ? keep : L.sc;
   // software pipeline: group j + 1's keys widened and its MFMAs issued before group
   // j's head sums, so that the matrix cores and the vector ALUs overlap
   auto keys = [&](int j, bf16x8* kb) {
@@ -259,7 +264,7 @@ MK2_DEV void idx_score_keys(const IdxDev& p, int r, int chunk, IdxScoreLds& L) {
       const float t = __uint_as_float(c[0]) + __uint_as_float(c[1]);
       const int loc = (gw0 + j - 3) * 16 + lane;
       if (k_begin + loc < k_end) {
-        L.sc[loc] = t;
+        sc[loc] = t;
         atomicAdd(&L.hist[radix_key(t) >> 20], 1);
       }
     }
@@ -287,12 +292,12 @@ MK2_DEV void idx_score_keys(const IdxDev& p, int r, int chunk, IdxScoreLds& L) {
     finish(j + 1, acc1);
   }
   __syncthreads();
-  for (int i = 4 * threadIdx.x; i < k_end - k_begin; i += 4 * NT) {
+  for (int i = 4 * threadIdx.x; (!keep || p.scores_out) && i < k_end - k_begin; i += 4 * NT) {
     if (k_begin + i + 4 <= k_end) {
-      st_dev_16(srow + k_begin + i, make_uint4(__float_as_uint(L.sc[i]), __float_as_uint(L.sc[i + 1]),
-                                               __float_as_uint(L.sc[i + 2]), __float_as_uint(L.sc[i + 3])));
+      st_dev_16(srow + k_begin + i, make_uint4(__float_as_uint(sc[i]), __float_as_uint(sc[i + 1]),
+                                               __float_as_uint(sc[i + 2]), __float_as_uint(sc[i + 3])));
     } else {
-      for (int u = 0; u < 4 && k_begin + i + u < k_end; ++u) st_dev_f32(srow + k_begin + i + u, L.sc[i + u]);
+      for (int u = 0; u < 4 && k_begin + i + u < k_end; ++u) st_dev_f32(srow + k_begin + i + u, sc[i + u]);
     }
   }
   // the chunk's counts into the row's histograms (device atomics, nonzero bins): two
@@ -317,11 +322,11 @@ MK2_DEV void idx_score_keys(const IdxDev& p, int r, int chunk, IdxScoreLds& L) {
 
 // the scores of either index cache format (a uniform branch, once a task)
 template <int NT>
-MK2_DEV void idx_score(const IdxDev& p, int r, int chunk, IdxScoreLds& L) {
+MK2_DEV void idx_score(const IdxDev& p, int r, int chunk, IdxScoreLds& L, float* keep = nullptr) {
   if (p.kfmt == IDX_KEYS_FP8)
-    idx_score_keys<NT, IDX_KEYS_FP8>(p, r, chunk, L);
+    idx_score_keys<NT, IDX_KEYS_FP8>(p, r, chunk, L, keep);
   else
-    idx_score_keys<NT, IDX_KEYS_FP4>(p, r, chunk, L);
+    idx_score_keys<NT, IDX_KEYS_FP4>(p, r, chunk, L, keep);
 }
 
 // ------------------------------------------------------------- stage: top-k
@@ -514,15 +519,16 @@ MK2_DEV void idx_clear_hist(const IdxDev& p, int r) {
 // while the slices still list their keys above the bin); then the task waits for the
 // earlier chunks' counts (tasks only wait on chunks of lower index, which publish
 // before they wait, so with every task started every wait ends; a wait past `spin`
-// polls, or the sticky error word `err` set, gives up and sets it).  Returns whether
-// S.res[0..1] now hold b1 and the count above it.
+// polls, or the sticky error word `err` set, gives up and sets it).  `kept`: the
+// chunk's scores in LDS (its score task's `keep`), or null: read from `scores`.
+// Returns whether S.res[0..1] now hold b1 and the count above it.
 constexpr int CC_FLAG = 1 << 30;
 struct NoPub {
   MK2_DEV void operator()() const {}
 };
 template <int NT, class Pub = NoPub>
 MK2_DEV bool idx_slice(const IdxDev& p, int r, int chunk, TopkLds& S, int spin, int* err, uint32_t tag,
-                       Pub published = Pub()) {
+                       Pub published = Pub(), const float* kept = nullptr) {
   constexpr int PER = IDX_CHUNK / NT;  // consecutive positions a thread
   static_assert(PER % 4 == 0, "a thread reads whole 16-byte groups of scores");
   const int tid = threadIdx.x;
@@ -540,7 +546,9 @@ MK2_DEV bool idx_slice(const IdxDev& p, int r, int chunk, TopkLds& S, int spin, 
   uint4 raw[PER / 4];
 #pragma unroll
   for (int q = 0; q < PER / 4; ++q)
-    raw[q] = base + 4 * q < n ? ldp_16(srow + base + 4 * q) : make_uint4(0, 0, 0, 0);
+    raw[q] = base + 4 * q >= n ? make_uint4(0, 0, 0, 0)
+             : kept            ? *(const uint4*)(kept + tid * PER + 4 * q)
+                               : ldp_16(srow + base + 4 * q);
   if (tid < 64) {
     int above;
     const int b1 = wave_threshold(p, r, k, &above);

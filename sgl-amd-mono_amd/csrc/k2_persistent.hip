@@ -157,9 +157,14 @@ MK2_DEV bool k2_wait(const K2Dev& p, int* seen, int line, int target, int stamp 
   return ok;
 }
 
+// score chunks a workgroup keeps in LDS for its slices (more tasks a workgroup: the
+// rest go through the scores in the workspace)
+constexpr int K2_KEEP = 4;
+
 template <int NCG, int FMT>
 __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
   __shared__ K2Lds S;
+  __shared__ float kept[K2_KEEP][IDX_CHUNK];  // this workgroup's score tasks' scores, by t / G
   __shared__ int seen[SY_LINES + 1];  // counts seen by line; [SY_LINES]: a wait failed
   __shared__ int last_flag;
   __shared__ uint32_t s_tag;
@@ -186,8 +191,9 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
     // ---- index scores + row key histograms
     k2_stamp(p, 3 * st);
     const int nchk = p.idx.nchk;
+    auto keep_of = [&](int t) { return t / G < K2_KEEP ? kept[t / G] : nullptr; };
     K2_TASKS(t, R * nchk) {
-      idx_score<K2_NT>(p.idx, t / nchk, t % nchk, S.score);
+      idx_score<K2_NT>(p.idx, t / nchk, t % nchk, S.score, keep_of(t));
       k2_signal(p, SY_SCORE + t / nchk);
     }
     k2_stamp(p, 3 * st++ + 2);
@@ -203,7 +209,8 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
       if (!k2_wait(p, seen, SY_SCORE + r, nchk, t < G ? 3 * st + 1 : -1)) return;
       bool last = false;
       const bool known = idx_slice<K2_NT>(p.idx, r, t % nchk, S.topk, p.spin_limit, k2_ctr(p, SY_ERR), tp.tag,
-                                          [&] { last = k2_signal_last1(p, SY_SLICE + r, nchk, &last_flag); });
+                                          [&] { last = k2_signal_last1(p, SY_SLICE + r, nchk, &last_flag); },
+                                          keep_of(t));
       if (last) {
         k2_stamp(p, 3 * (st + 1));
         k2_stamp(p, 3 * (st + 1) + 1);

@@ -314,8 +314,8 @@ def timeline_markdown(tl, argv, rows, launches):
              "(4 resident layers cycled) of the stamps each workgroup takes with s_memrealtime",
              "(100 MHz) as it enters a stage, when its first task's input is ready (its",
              "dependency wait returned) and as it leaves; in us after the launch's first",
-             "stamp.  select and route run on one workgroup each (the last arrival of the",
-             "row's slices / of the router tasks).", "",
+             "stamp.  select and route run on one workgroup each (a row's select on its",
+             "last slice to count out; the route on a workgroup without a router task).", "",
              "| stage | first in | first input ready: median | first input ready: last | last out |",
              "|---|---|---|---|---|"]
     f = lambda v: "-" if v is None else f"{v:.2f}"  # noqa: E731

@@ -277,8 +277,16 @@ int mk2_layer_launch_static(const mk2_layer_args* args, mk2_stream_t stream);
  * E4M3, MK2_KEYS_FP4: MXFP4).  Weights are SGLang's as loaded, read in place: bf16
  * or E4M3 row-major, or E4M3 in AITER's (16, 16) layout, with f32 128 x 128 block
  * scales [ceil(rows/128)][K/128] (W_iw is bf16 in all).  W_UK is SGLang's w_kc, bf16
- * [heads][kv_lora][nope] in memory.  A row with slot < 0 (a pad row) writes no cache rows.  Six launches in
- * stream order; the workspace holds the normed rows and the f32 GEMV outputs. */
+ * [heads][kv_lora][nope] in memory.  A row with slot < 0 (a pad row) writes no cache
+ * rows.  mk2_front_launch runs ONE persistent launch (one workgroup a CU, the stages
+ * handing off through counters in the workspace) for the shapes whose GEMV steps it
+ * instantiates (mk2_front_is_persistent), else the six stage launches in stream
+ * order, which mk2_front_launch_staged always runs; both give the same bits.  The
+ * workspace is zero-filled before its first launch and holds the launch's counters,
+ * the normed rows and the f32 GEMV outputs; the int at byte MK2_FRONT_STATUS_OFFSET
+ * of it becomes nonzero once a persistent launch's dependency wait ran out of its
+ * spin limit (that launch's outputs are undefined) and only the caller clears it. */
+#define MK2_FRONT_STATUS_OFFSET 6528
 #define MK2_WFMT_BF16 0
 #define MK2_WFMT_FP8_BLOCK 1
 #define MK2_WFMT_FP8_AITER16 2 /* E4M3 with the same block scales, the weight bytes in
@@ -340,7 +348,13 @@ typedef struct mk2_front_args {
 } mk2_front_args;
 
 int mk2_front_workspace_bytes(const mk2_front_shape* shape, size_t* bytes);
+/* reference: the front stages of glm53/gfx950/kernel.py:2585-3575 (one launch there) */
 int mk2_front_launch(const mk2_front_args* args, mk2_stream_t stream);
+/* the same front as six stage launches in stream order (every valid shape) */
+int mk2_front_launch_staged(const mk2_front_args* args, mk2_stream_t stream);
+/* 1: mk2_front_launch runs one persistent launch for this shape; 0: the six stage
+   launches; < 0: an invalid shape (minus its MK2_E* code; mk2_last_error says why) */
+int mk2_front_is_persistent(const mk2_front_shape* shape);
 
 /* ------------------------------------------------------------------ tail
  * The steps after the last layer, on this GPU's rows of the LM head: the final

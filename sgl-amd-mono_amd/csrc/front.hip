@@ -65,34 +65,36 @@ struct GemvDev {
   int ntiles;
 };
 
-// KU: 64-k units a wave (K / ks = 8 * 64 * KU); WF: the weights' MK2_WFMT_* (bf16,
-// E4M3 row-major, or E4M3 in AITER's (16, 16) layout)
-template <int KU, int WF>
-__global__ __launch_bounds__(GV_NT) void k_gemv(GemvDev p) {
+struct GemvLds {
+  float ssum[16];
+  uint4 gam[8192 / 8];
+  float red[GV_CHUNK][GV_WAVES][256];
+};
+
+// One engine workgroup's work: workgroup b of nblocks (a multiple of p.ks).  KU: 64-k
+// units a wave (K / ks = 8 * 64 * KU); WF: the weights' MK2_WFMT_* (bf16, E4M3
+// row-major, or E4M3 in AITER's (16, 16) layout).  `wait` (the input rows'
+// dependency, in the persistent front) runs once the first tile's weights are in
+// flight; false from it returns false at once.  The f32 partial planes are stored
+// device-coherently (the next stage may run on another XCD within the same launch).
+template <int KU, int WF, typename Wait = NoWait>
+MK2_DEV bool gemv_run(const GemvDev& p, int b, int nblocks, GemvLds& S, Wait wait = Wait()) {
   constexpr bool F8 = WF != MK2_WFMT_BF16, SHUF = WF == MK2_WFMT_FP8_AITER16;
   constexpr int L = F8 ? KU : 2 * KU;      // 16-byte weight loads a lane a tile
   constexpr int WIN = L <= 24 ? L : L / 2;  // loads in flight a lane
   static_assert(L % WIN == 0, "a window divides the loads of a tile");
   static_assert(!F8 || KU % 2 == 0, "FP8 slices are whole 128-k blocks");
-  __shared__ float ssum[16];
-  __shared__ uint4 gam[8192 / 8];
-  __shared__ float red[GV_CHUNK][GV_WAVES][256];
+  float* ssum = S.ssum;
+  uint4* gam = S.gam;
+  auto& red = S.red;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, c16 = lane & 15, g = lane >> 4;
-  const int K = p.K, b = blockIdx.x, M = p.M;
-  const int part = b % p.ks, G = gridDim.x / p.ks, q = b / p.ks;
+  const int K = p.K, M = p.M;
+  const int part = b % p.ks, G = nblocks / p.ks, q = b / p.ks;
   const int t0 = (int)((long long)q * p.ntiles / G), t1 = (int)((long long)(q + 1) * p.ntiles / G);
   // k map: unit u of the wave's slice holds k = kw + 64 u + 0 .. 15 for lane group g;
   // MFMA step 2u takes its first 8, step 2u + 1 the next 8 (A and B alike)
   const int kw = part * (K / p.ks) + wave * KU * 64 + 16 * g;
-  // the rows: this lane's fragments of row c16 (16 k a unit)
   const bool live = c16 < M;
-  const bf16_t* xr = p.x + (size_t)(live ? c16 : 0) * K + kw;
-  uint4 xq[2 * KU];
-#pragma unroll
-  for (int u = 0; u < KU; ++u) {
-    xq[2 * u] = *(const uint4*)(xr + 64 * u);
-    xq[2 * u + 1] = *(const uint4*)(xr + 64 * u + 8);
-  }
   // the tile sequence: tile t of segment sid at row (t - base) * 16; this lane's row
   auto seg_of = [&](int t) { return t < p.tiles0 ? 0 : 1; };
   // In AITER's (16, 16) layout ([rows/16][K/32][2][16 rows][16 B]) the 16 bytes of
@@ -112,6 +114,15 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(GemvDev p) {
   if (t0 < t1) {
 #pragma unroll
     for (int j = 0; j < WIN; ++j) wv[j] = ld_stream16(wrow + w_off(j));
+  }
+  if (!wait()) return false;
+  // the rows: this lane's fragments of row c16 (16 k a unit)
+  const bf16_t* xr = p.x + (size_t)(live ? c16 : 0) * K + kw;
+  uint4 xq[2 * KU];
+#pragma unroll
+  for (int u = 0; u < KU; ++u) {
+    xq[2 * u] = *(const uint4*)(xr + 64 * u);
+    xq[2 * u + 1] = *(const uint4*)(xr + 64 * u + 8);
   }
   // the norm: each row's sum of squares over all K (the rows are L2-resident): 32
   // threads a row, 16-byte pieces, every load issued before the sums
@@ -220,10 +231,17 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(GemvDev p) {
       float s = red[i][0][v * 16 + m];
 #pragma unroll
       for (int w = 1; w < GV_WAVES; ++w) s += red[i][w][v * 16 + m];
-      if (m < M) p.seg[sid].out[part * p.seg[sid].pstride + (size_t)m * p.seg[sid].ld + row] = s;
+      if (m < M) st_dev_f32(p.seg[sid].out + part * p.seg[sid].pstride + (size_t)m * p.seg[sid].ld + row, s);
     }
     __syncthreads();
   }
+  return true;
+}
+
+template <int KU, int WF>
+__global__ __launch_bounds__(GV_NT) void k_gemv(GemvDev p) {
+  __shared__ GemvLds S;
+  gemv_run<KU, WF>(p, blockIdx.x, gridDim.x, S);
 }
 
 template <int KU, int WF>
@@ -306,6 +324,21 @@ MK2_DEV float parts_sum(const float* base, int parts, long long pstride, size_t 
   for (int k = 1; k < parts; ++k) v += base[k * pstride + at];
   return v;
 }
+// N elements (at[i], those with on[i]; 0 for the rest) summed over `parts` planes in
+// order, as parts_sum, with each plane's N loads issued together (one round trip a
+// plane rather than one an element)
+template <int N>
+MK2_DEV void parts_sum_n(const float* base, int parts, long long pstride, const size_t* at, const bool* on, float* v) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = on[i] ? base[at[i]] : 0.f;
+  for (int k = 1; k < parts; ++k) {
+    float w[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) w[i] = on[i] ? base[k * pstride + at[i]] : 0.f;
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] += w[i];
+  }
+}
 
 MK2_DEV float block_sum512(float v, float* sh) {  // all 512 threads; sh: 8 floats
   v = wave_sum(v);
@@ -341,12 +374,11 @@ MK2_DEV const float* rope_row(const FrontDev& p, int s) {
   return p.rope_cs + (size_t)(pos < 0 ? 0 : pos) * p.rope;
 }
 
-// the normed input rows x_n = bf16(x * rstd * g_in), one workgroup a row, for every
-// hidden-input GEMV (so that each of their workgroups reads only its k slice)
-__global__ __launch_bounds__(FR_NT) void k_front_norm(const bf16_t* x, const bf16_t* gw, bf16_t* xn, int K, float eps) {
-  __shared__ float sh[FR_NT / 64];
+// the normed input rows x_n = bf16(x * rstd * g_in), one workgroup a row (row s), for
+// every hidden-input GEMV (so that each of their workgroups reads only its k slice);
+// stored device-coherently (the GEMVs may run on another XCD in the same launch)
+MK2_DEV void front_norm_row(const bf16_t* x, const bf16_t* gw, bf16_t* xn, int K, float eps, int s, float* sh) {
   constexpr int PT = 2;  // 16-byte pieces a thread (K <= 8192)
-  const int s = blockIdx.x;
   const uint4* xr = (const uint4*)(x + (size_t)s * K);
   uint4 v[PT];
   float ss = 0.f;
@@ -373,16 +405,21 @@ __global__ __launch_bounds__(FR_NT) void k_front_norm(const bf16_t* x, const bf1
     for (int e = 0; e < 4; ++e)
       o[e] = pack_bf16x2(__uint_as_float(xu[e] << 16) * rs * __uint_as_float(gu[e] << 16),
                          __uint_as_float(xu[e] & 0xFFFF0000u) * rs * __uint_as_float(gu[e] & 0xFFFF0000u));
-    ((uint4*)(xn + (size_t)s * K))[j] = make_uint4(o[0], o[1], o[2], o[3]);
+    st_dev_16((uint4*)(xn + (size_t)s * K) + j, make_uint4(o[0], o[1], o[2], o[3]));
   }
 }
 
-// three workgroups a row: role 0 the normed q_a; role 1 the latent cache row; role 2
-// the index key and the head weights
-__global__ __launch_bounds__(FR_NT) void k_front_rows(FrontDev p) {
+__global__ __launch_bounds__(FR_NT) void k_front_norm(const bf16_t* x, const bf16_t* gw, bf16_t* xn, int K, float eps) {
   __shared__ float sh[FR_NT / 64];
-  __shared__ float kvv[576];
-  const int role = blockIdx.x / p.M, s = blockIdx.x % p.M;
+  front_norm_row(x, gw, xn, K, eps, blockIdx.x, sh);
+}
+
+// three workgroups a row (task b of 3 M): role 0 the normed q_a (stored
+// device-coherently: the q_b GEMV may run on another XCD in the same launch); role 1
+// the latent cache row; role 2 the index key and the head weights.  sh: 8 floats, kvv:
+// 576 floats of LDS.
+MK2_DEV void front_rows_task(const FrontDev& p, int b, float* sh, float* kvv) {
+  const int role = b / p.M, s = b % p.M;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int NA = p.q_lora + p.kv_lora + p.rope;
   const long long pA = (long long)p.M * NA;
@@ -392,29 +429,33 @@ __global__ __launch_bounds__(FR_NT) void k_front_rows(FrontDev p) {
   if (role == 0) {  // q_an = bf16(rmsnorm(q_a) * g)
     constexpr int QPT = 16;  // q_lora <= 8192: 16 a thread
     float v[QPT];
-    float ss = 0.f;
+    size_t at[QPT];
+    bool on[QPT];
 #pragma unroll
     for (int i = 0; i < QPT; ++i) {
-      const int k = tid + i * FR_NT;
-      v[i] = k < p.q_lora ? parts_sum(p.qkv_a, p.ksA, pA, ra + k) : 0.f;
-      ss += v[i] * v[i];
+      at[i] = ra + tid + i * FR_NT;
+      on[i] = tid + i * FR_NT < p.q_lora;
     }
+    parts_sum_n<QPT>(p.qkv_a, p.ksA, pA, at, on, v);
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < QPT; ++i) ss += v[i] * v[i];
     const float rs = 1.0f / sqrtf(block_sum512(ss, sh) / (float)p.q_lora + p.eps);
 #pragma unroll
     for (int i = 0; i < QPT; ++i) {
       const int k = tid + i * FR_NT;
-      if (k < p.q_lora) p.q_an[(size_t)s * p.q_lora + k] = f32_to_bf16(v[i] * rs * bf16_to_f32(p.g_q_a[k]));
+      if (k < p.q_lora) st_dev_u16(p.q_an + (size_t)s * p.q_lora + k, f32_to_bf16(v[i] * rs * bf16_to_f32(p.g_q_a[k])));
     }
     return;
   }
   if (role == 1) {  // the latent row: bf16(rmsnorm(kv_a) * g) | bf16(rope(k_pe)), then E4M3
     const int D = p.kv_lora + p.rope;
-    const float v = tid < p.kv_lora ? parts_sum(p.qkv_a, p.ksA, pA, ra + p.q_lora + tid) : 0.f;
-    float x0 = 0.f, x1 = 0.f;
-    if (tid < p.rope / 2) {
-      x0 = parts_sum(p.qkv_a, p.ksA, pA, ra + p.q_lora + p.kv_lora + 2 * tid);
-      x1 = parts_sum(p.qkv_a, p.ksA, pA, ra + p.q_lora + p.kv_lora + 2 * tid + 1);
-    }
+    const size_t at[3] = {ra + p.q_lora + tid, ra + p.q_lora + p.kv_lora + 2 * tid,
+                          ra + p.q_lora + p.kv_lora + 2 * tid + 1};
+    const bool on[3] = {tid < p.kv_lora, tid < p.rope / 2, tid < p.rope / 2};
+    float r3[3];
+    parts_sum_n<3>(p.qkv_a, p.ksA, pA, at, on, r3);
+    const float v = r3[0], x0 = r3[1], x1 = r3[2];
     const float rs = 1.0f / sqrtf(block_sum512(v * v, sh) / (float)p.kv_lora + p.eps);
     if (tid < p.kv_lora) kvv[tid] = bf16_to_f32(f32_to_bf16(v * rs * bf16_to_f32(p.g_kv_a[tid])));
     if (tid < p.rope / 2) {
@@ -453,8 +494,11 @@ __global__ __launch_bounds__(FR_NT) void k_front_rows(FrontDev p) {
     return;
   }
   const long long pK = (long long)p.M * 128;
-  float v0 = parts_sum(p.ik, p.ksA, pK, (size_t)s * 128 + 2 * lane);
-  float v1 = parts_sum(p.ik, p.ksA, pK, (size_t)s * 128 + 2 * lane + 1);
+  const size_t at2[2] = {(size_t)s * 128 + 2 * lane, (size_t)s * 128 + 2 * lane + 1};
+  const bool on2[2] = {true, true};
+  float r2[2];
+  parts_sum_n<2>(p.ik, p.ksA, pK, at2, on2, r2);
+  float v0 = r2[0], v1 = r2[1];
   const float mean = wave_sum(v0 + v1) * (1.0f / 128);
   const float d0 = v0 - mean, d1 = v1 - mean;
   const float rstd = 1.0f / sqrtf(wave_sum(d0 * d0 + d1 * d1) * (1.0f / 128) + p.index_eps);
@@ -496,32 +540,50 @@ __global__ __launch_bounds__(FR_NT) void k_front_rows(FrontDev p) {
   }
 }
 
+__global__ __launch_bounds__(FR_NT) void k_front_rows(FrontDev p) {
+  __shared__ float sh[FR_NT / 64];
+  __shared__ float kvv[576];
+  front_rows_task(p, blockIdx.x, sh, kvv);
+}
+
 // ---------------------------------------------------------------- per-head stage
 // Workgroups [0, 4 heads): head h, latent rows [128 j, 128 j + 128) of every row, a
 // 16-row tile a wave on MFMA (A = W_UK[h] rows c, k = nope; B = bf16(q_nope) of the
 // rows); quarter 0 also rotates the head's q_pe.  The rest: the index queries, one
 // (row, index head) a wave.
-template <int NS>  // nope / 32 k-steps
-__global__ __launch_bounds__(FR_NT) void k_front_heads(FrontDev p) {
-  __shared__ uint4 qn[32 * NS * 4];  // bf16 q_nope of the head, [row][nope] (16-byte pieces)
+// Task b: W_UK tasks below 4 heads, then index-query tasks.  qn: LDS of 32 * NS * 4
+// uint4 (the head's bf16 q_nope, [row][nope] in 16-byte pieces).  `wait` (the q_b
+// planes' dependency, in the persistent front) runs after the task's static loads;
+// false from it returns false at once.
+template <int NS, typename Wait = NoWait>  // NS: nope / 32 k-steps
+MK2_DEV bool front_heads_task(const FrontDev& p, int b, uint4* qn, Wait wait = Wait()) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c16 = lane & 15, g = lane >> 4;
   const int QD = p.nope + p.rope, D = p.kv_lora + p.rope, QB = p.heads * QD;
   const long long pC = (long long)p.M * QB;
-  if ((int)blockIdx.x < 4 * p.heads) {
-    const int h = blockIdx.x >> 2, quarter = blockIdx.x & 3;
+  if (b < 4 * p.heads) {
+    const int h = b >> 2, quarter = b & 3;
     const int c0 = quarter * 128 + wave * 16;
     const bf16_t* wr = p.w_uk + ((size_t)h * p.kv_lora + c0 + c16) * p.nope + 8 * g;
     uint4 wv[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) wv[s] = *(const uint4*)(wr + 32 * s);
+    if (!wait()) return false;
     // the head's q_nope rows as bf16 in LDS: 8 consecutive k a thread (coalesced f32 reads)
     for (int e = tid; e < p.M * NS * 4; e += FR_NT) {
       const int m = e / (NS * 4), k8 = (e % (NS * 4)) * 8;
       const size_t at = (size_t)m * QB + (size_t)h * QD + k8;
+      size_t a8[8];
+      bool on8[8];
+      float r8[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        a8[j] = at + j;
+        on8[j] = true;
+      }
+      parts_sum_n<8>(p.q_b, p.ksC, pC, a8, on8, r8);
       uint32_t o[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        o[j] = pack_bf16x2(parts_sum(p.q_b, p.ksC, pC, at + 2 * j), parts_sum(p.q_b, p.ksC, pC, at + 2 * j + 1));
+      for (int j = 0; j < 4; ++j) o[j] = pack_bf16x2(r8[2 * j], r8[2 * j + 1]);
       qn[e] = make_uint4(o[0], o[1], o[2], o[3]);
     }
     __syncthreads();
@@ -552,11 +614,12 @@ __global__ __launch_bounds__(FR_NT) void k_front_heads(FrontDev p) {
             pack_bf16x2(x0 * c - x1 * sn, x0 * sn + x1 * c);
       }
     }
-    return;
+    return true;
   }
   // index queries: wave task (row, index head)
-  const int task = ((int)blockIdx.x - 4 * p.heads) * (FR_NT / 64) + wave;
-  if (task >= p.M * p.ih) return;
+  if (!wait()) return false;
+  const int task = (b - 4 * p.heads) * (FR_NT / 64) + wave;
+  if (task >= p.M * p.ih) return true;
   const int m = task / p.ih, h = task % p.ih;
   const long long pQ = (long long)p.M * p.ih * 128;
   const size_t at = ((size_t)m * p.ih + h) * 128 + 2 * lane;
@@ -571,6 +634,180 @@ __global__ __launch_bounds__(FR_NT) void k_front_heads(FrontDev p) {
   }
   fwht128(v0, v1);
   *(uint32_t*)(p.index_q + ((size_t)m * p.ih + h) * 128 + 2 * lane) = pack_bf16x2(v0, v1);
+  return true;
+}
+
+template <int NS>
+__global__ __launch_bounds__(FR_NT) void k_front_heads(FrontDev p) {
+  __shared__ uint4 qn[32 * NS * 4];
+  front_heads_task<NS>(p, blockIdx.x, qn);
+}
+
+// ------------------------------------------------------------- the persistent front
+// The five stages in ONE launch of one workgroup a CU (the staged launches' device
+// code, task by task): task t of a stage runs on workgroup (base + t) mod grid, each
+// stage's base continuing from the previous stage's last task, and a task that needs
+// an earlier stage's results waits on that stage's completion counter, as the
+// persistent layer does: producers store their hand-off data device-coherently,
+// drain, pass a barrier and add to the counter (16 sub-counters on their own lines
+// for the wide stages); wave 0 of a consumer polls the counter (bounded; a wait that
+// runs out, or sees another's failure, stops the workgroup's walk and sets the sticky
+// error word), then the workgroup reads with plain loads.  Every dependency points
+// back and every workgroup is resident, so every wait ends.  The last workgroup out
+// resets the counters and ORs a failure into the status word.
+constexpr int FP_LINE = 32, FP_LANES = 16;
+enum : int {
+  FP_NORM = 0,                 // normed rows done
+  FP_A = 1,                    // [FP_LANES] hidden-input GEMV workgroups done
+  FP_ROWS = FP_A + FP_LANES,   // [FP_LANES] per-row tasks done
+  FP_C = FP_ROWS + FP_LANES,   // [FP_LANES] q_an-input GEMV workgroups done
+  FP_DONE = FP_C + FP_LANES,   // workgroups finished
+  FP_ERR,                      // sticky within a launch
+  FP_STATUS,                   // nonzero once a launch failed; never cleared here
+  FP_LINES
+};
+static_assert(FP_STATUS * FP_LINE * 4 == MK2_FRONT_STATUS_OFFSET, "the status word's documented offset");
+
+struct FrontPDev {
+  FrontDev f;
+  GemvDev A[2], W[2], C[2];  // passes of 16 rows
+  int passes, gridA, gridW, gridC, nheads;
+  const bf16_t* x;
+  const bf16_t* g_in;
+  bf16_t* x_n;
+  int hidden;
+  float eps;
+  int* sync;
+  int spin;
+};
+
+union FrontLds {
+  GemvLds gemv;
+  struct {
+    float sh[FR_NT / 64];
+    float kvv[576];
+  } rows;
+  uint4 qn[32 * 8 * 4];
+};
+
+MK2_DEV int* fp_ctr(const FrontPDev& p, int line) { return p.sync + line * FP_LINE; }
+
+MK2_DEV void fp_signal(const FrontPDev& p, int line, int t, int lanes) {
+  drain_memory();
+  __syncthreads();
+  if (threadIdx.x == 0)
+    __hip_atomic_fetch_add(fp_ctr(p, line + t % lanes), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// until the sub-counters of `line` sum to target; seen[k] caches what wait k saw and
+// seen[4] is the workgroup's failure flag (every thread returns the same)
+MK2_DEV bool fp_wait(const FrontPDev& p, int* seen, int k, int line, int lanes, int target) {
+  if (seen[k] >= target) return true;
+  int v = 0;
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    const int* ctr = fp_ctr(p, line + min(lane, lanes - 1));
+    const int* err = fp_ctr(p, FP_ERR);
+    auto poll = [&]() { return __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+    auto count = [&](int c) { return __builtin_amdgcn_readfirstlane(row16_sum_i32(lane < lanes ? c : 0)); };
+    bool bad = false;
+    int n = 0, c0 = poll();
+    while (true) {
+      const int c1 = poll();
+      v = count(c0);
+      if (v >= target) break;
+      c0 = poll();
+      v = count(c1);
+      if (v >= target) break;
+      n += 2;
+      if ((n & 31) == 0 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+        bad = true;
+        break;
+      }
+      if (n > p.spin) {
+        if (lane == 0) atomicOr(fp_ctr(p, FP_ERR), 1);
+        bad = true;
+        break;
+      }
+    }
+    if (lane == 0) seen[4] = bad;
+  }
+  __syncthreads();
+  const bool ok = seen[4] == 0;
+  __syncthreads();  // the flag is read before the next wait can write it
+  if (threadIdx.x == 0 && ok) seen[k] = v;
+  return ok;
+}
+
+template <int KUA, int KUC, int WF, int NS>
+__global__ __launch_bounds__(FR_NT, 1) void k_front_persistent(FrontPDev p) {
+  __shared__ FrontLds S;
+  __shared__ int seen[5];
+  __shared__ int last;
+  const int G = gridDim.x, b = blockIdx.x, M = p.f.M;
+  if (threadIdx.x < 5) seen[threadIdx.x] = 0;
+  __syncthreads();
+  auto walk = [&]() {
+    int base = 0;
+#define FP_TASKS(t, n) for (int t = (b - base % G + G) % G; t < (n); t += G)
+#define FP_NEXT(n) base = (base + (n)) % G
+    // 0. the normed input rows
+    FP_TASKS(t, M) {
+      front_norm_row(p.x, p.g_in, p.x_n, p.hidden, p.eps, t, S.rows.sh);
+      fp_signal(p, FP_NORM, 0, 1);
+    }
+    FP_NEXT(M);
+    // 1. the hidden-input GEMVs, per pass of 16 rows: [W_qkv_a | W_ik], then W_iw
+    const int nA = p.gridA + p.gridW;
+    FP_TASKS(t, p.passes * nA) {
+      const int pass = t / nA, u = t % nA;
+      auto w = [&] { return fp_wait(p, seen, 0, FP_NORM, 1, M); };
+      const bool ok = u < p.gridA ? gemv_run<KUA, WF>(p.A[pass], u, p.gridA, S.gemv, w)
+                                  : gemv_run<1, MK2_WFMT_BF16>(p.W[pass], u - p.gridA, p.gridW, S.gemv, w);
+      if (!ok) return;
+      fp_signal(p, FP_A, t, FP_LANES);
+    }
+    FP_NEXT(p.passes * nA);
+    // 2. the per-row stage
+    const int nR = (p.f.ih ? 3 : 2) * M;
+    FP_TASKS(t, nR) {
+      if (!fp_wait(p, seen, 1, FP_A, FP_LANES, p.passes * nA)) return;
+      front_rows_task(p.f, t, S.rows.sh, S.rows.kvv);
+      fp_signal(p, FP_ROWS, t, FP_LANES);
+    }
+    FP_NEXT(nR);
+    // 3. the q_an-input GEMVs
+    FP_TASKS(t, p.passes * p.gridC) {
+      const int pass = t / p.gridC, u = t % p.gridC;
+      if (!gemv_run<KUC, WF>(p.C[pass], u, p.gridC, S.gemv,
+                             [&] { return fp_wait(p, seen, 2, FP_ROWS, FP_LANES, nR); }))
+        return;
+      fp_signal(p, FP_C, t, FP_LANES);
+    }
+    FP_NEXT(p.passes * p.gridC);
+    // 4. the per-head stage
+    FP_TASKS(t, p.nheads) {
+      if (!front_heads_task<NS>(p.f, t, S.qn,
+                                [&] { return fp_wait(p, seen, 3, FP_C, FP_LANES, p.passes * p.gridC); }))
+        return;
+      __syncthreads();  // this workgroup's next head task rewrites qn
+    }
+#undef FP_TASKS
+#undef FP_NEXT
+  };
+  walk();
+  // the last workgroup out resets the counters for the next launch
+  drain_memory();
+  __syncthreads();
+  if (threadIdx.x == 0)
+    last = __hip_atomic_fetch_add(fp_ctr(p, FP_DONE), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == G - 1;
+  __syncthreads();
+  if (last) {
+    if (threadIdx.x == 0 && __hip_atomic_load(fp_ctr(p, FP_ERR), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+      atomicOr(fp_ctr(p, FP_STATUS), 1);
+    for (int l = threadIdx.x; l < FP_STATUS; l += FR_NT)
+      __hip_atomic_store(fp_ctr(p, l), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 static int front_cus() {
@@ -600,13 +837,16 @@ static FrontPlan front_plan(const mk2_front_shape* s) {
   return pl;
 }
 
-// workspace: the GEMV outputs' partial planes and the normed q_a rows
+// workspace: the persistent launch's counters, the GEMV outputs' partial planes, the
+// normed q_a rows and the normed input rows
 struct FrontWs {
+  int* sync;
   float *qkv_a, *ik, *iw, *q_b, *iq;
   bf16_t *q_an, *x_n;
 };
 static size_t front_carve(const mk2_front_shape* s, void* base, FrontWs* w) {
   Carver c(base);
+  int* sync = c.take<int>(FP_LINES * FP_LINE);
   const FrontPlan pl = front_plan(s);
   const size_t M = s->rows, ih = s->index_heads > 0 ? s->index_heads : 1;
   float* qkv_a = c.take<float>(pl.ksA * M * (s->q_lora + s->kv_lora + s->rope));
@@ -616,7 +856,7 @@ static size_t front_carve(const mk2_front_shape* s, void* base, FrontWs* w) {
   float* iq = c.take<float>(pl.ksC * M * ih * 128);
   bf16_t* q_an = c.take<bf16_t>(M * s->q_lora);
   bf16_t* x_n = c.take<bf16_t>(M * s->hidden);
-  if (w) *w = FrontWs{qkv_a, ik, iw, q_b, iq, q_an, x_n};
+  if (w) *w = FrontWs{sync, qkv_a, ik, iw, q_b, iq, q_an, x_n};
   return c.bytes();
 }
 
@@ -657,8 +897,59 @@ extern "C" int mk2_front_workspace_bytes(const mk2_front_shape* shape, size_t* b
   return MK2_OK;
 }
 
-extern "C" int mk2_front_launch(const mk2_front_args* a, mk2_stream_t stream) {
-  clear_error();
+namespace mk2 {
+
+// the persistent front's instantiations: (KUA, KUC, NS) of the hidden- and q_an-input
+// GEMVs' K steps and nope / 32, for each weight format; X(WF, KUA, KUC, NS)
+#define MK2_FRONT_PERSISTENT_SHAPES(X, WF) X(WF, 6, 4, 6) X(WF, 6, 4, 4) X(WF, 2, 2, 4) X(WF, 2, 2, 6)
+
+// the K steps of the three GEMVs and nope / 32 of a valid shape
+struct FrontSteps {
+  int kua, kuw, kuc, ns;
+};
+static FrontSteps front_steps(const mk2_front_shape* s) {
+  const FrontPlan pl = front_plan(s);
+  return FrontSteps{s->hidden / (512 * pl.ksA), s->hidden / (512 * pl.ksW), s->q_lora / (512 * pl.ksC), s->nope / 32};
+}
+static bool front_persistent_ok(const mk2_front_shape* s) {
+  const FrontSteps k = front_steps(s);
+  if (s->index_heads > 0 && k.kuw != 1) return false;
+#define MK2_FP_MATCH(WF, A, C, N) || (k.kua == A && k.kuc == C && k.ns == N)
+  return false MK2_FRONT_PERSISTENT_SHAPES(MK2_FP_MATCH, 0);
+#undef MK2_FP_MATCH
+}
+
+template <int KUA, int KUC, int WF, int NS>
+static int front_persistent_launch(const FrontPDev& d, int cus, hipStream_t st) {
+  static int fits = -1;  // one workgroup a CU
+  if (fits < 0) {
+    int per_cu = 0;
+    fits = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_front_persistent<KUA, KUC, WF, NS>, FR_NT, 0) ==
+                   hipSuccess &&
+           per_cu >= 1;
+  }
+  if (!fits) return set_error(MK2_ELAUNCH, "front: the persistent kernel does not fit one workgroup per CU");
+  k_front_persistent<KUA, KUC, WF, NS><<<cus, FR_NT, 0, st>>>(d);
+  return check_launch("front (persistent)");
+}
+
+static int front_persistent_dispatch(const FrontPDev& d, int wf, const FrontSteps& k, int cus, hipStream_t st) {
+#define MK2_FP_CASE(WF, A, C, N) \
+  if (wf == WF && k.kua == A && k.kuc == C && k.ns == N) return front_persistent_launch<A, C, WF, N>(d, cus, st);
+  MK2_FRONT_PERSISTENT_SHAPES(MK2_FP_CASE, MK2_WFMT_BF16)
+  MK2_FRONT_PERSISTENT_SHAPES(MK2_FP_CASE, MK2_WFMT_FP8_BLOCK)
+  MK2_FRONT_PERSISTENT_SHAPES(MK2_FP_CASE, MK2_WFMT_FP8_AITER16)
+#undef MK2_FP_CASE
+  return set_error(MK2_EINVAL, "front: no persistent front for these K steps");
+}
+
+// the grid of one GEMV pass as its stage launch runs it
+static int gemv_grid(const GemvDev& d, int cus) {
+  const int per = d.ntiles < cus / d.ks ? d.ntiles : cus / d.ks;
+  return d.ks * (per > 0 ? per : 1);
+}
+
+static int front_run(const mk2_front_args* a, hipStream_t st, bool persistent) {
   MK2_REQUIRE(a != nullptr, "front: args is NULL");
   int rc = front_check_shape(&a->shape);
   if (rc) return rc;
@@ -687,23 +978,17 @@ extern "C" int mk2_front_launch(const mk2_front_args* a, mk2_stream_t stream) {
   FrontWs ws;
   front_carve(&s, a->workspace, &ws);
   const FrontPlan pl = front_plan(&s);
-  hipStream_t st = (hipStream_t)stream;
-  auto gemv_fmt = [&](const GemvDev& d) {
-    return s.weight_fmt == MK2_WFMT_FP8_AITER16 ? gemv_launch<MK2_WFMT_FP8_AITER16>(d, cus, st)
-           : f8                                 ? gemv_launch<MK2_WFMT_FP8_BLOCK>(d, cus, st)
-                                                : gemv_launch<MK2_WFMT_BF16>(d, cus, st);
-  };
   const int M = s.rows, NA = s.q_lora + s.kv_lora + s.rope, QB = s.heads * (s.nope + s.rope), IH = s.index_heads;
   auto seg = [](const void* w, const float* sc, float* out, int rows, int ld, long long pstride) {
     return GemvSeg{w, sc, out, rows, ld, pstride};
   };
-  // 0. the normed input rows
-  k_front_norm<<<M, FR_NT, 0, st>>>((const bf16_t*)a->x, (const bf16_t*)w.g_in, ws.x_n, s.hidden, s.eps);
-  rc = check_launch("front (norm)");
-  if (rc) return rc;
-  // 1. the hidden-input GEMVs (passes of 16 rows)
-  for (int r0 = 0; r0 < M; r0 += 16) {
-    GemvDev d{};
+  // the GEMV passes of 16 rows: hidden-input [W_qkv_a | W_ik] and W_iw, q_an-input
+  // [W_q_b | W_iq]
+  const int passes = (M + 15) / 16;
+  GemvDev gA[2]{}, gW[2]{}, gC[2]{};
+  for (int pi = 0; pi < passes; ++pi) {
+    const int r0 = 16 * pi;
+    GemvDev& d = gA[pi];
     d.M = M - r0 < 16 ? M - r0 : 16; d.K = s.hidden; d.ks = pl.ksA; d.eps = s.eps;
     d.x = ws.x_n + (size_t)r0 * s.hidden; d.g = nullptr;
     d.seg[0] = seg(w.w_qkv_a, w.s_qkv_a, ws.qkv_a + (size_t)r0 * NA, NA, NA, (long long)M * NA);
@@ -711,19 +996,22 @@ extern "C" int mk2_front_launch(const mk2_front_args* a, mk2_stream_t stream) {
     if (idx) {
       d.seg[1] = seg(w.w_ik, w.s_ik, ws.ik + (size_t)r0 * 128, 128, 128, (long long)M * 128);
       d.ntiles += 128 / 16;
-    }
-    rc = gemv_fmt(d);
-    if (rc) return rc;
-    if (idx) {  // the head weights are bf16 in every checkpoint format
-      GemvDev e = d;
+      GemvDev& e = gW[pi];  // the head weights are bf16 in every checkpoint format
+      e = d;
       e.ks = pl.ksW;
       e.seg[0] = seg(w.w_iw, nullptr, ws.iw + (size_t)r0 * IH, IH, IH, (long long)M * IH);
       e.tiles0 = IH / 16; e.ntiles = e.tiles0;
-      rc = gemv_launch<MK2_WFMT_BF16>(e, cus, st);
-      if (rc) return rc;
+    }
+    GemvDev& c = gC[pi];
+    c.M = d.M; c.K = s.q_lora; c.ks = pl.ksC; c.eps = s.eps;
+    c.x = ws.q_an + (size_t)r0 * s.q_lora; c.g = nullptr;
+    c.seg[0] = seg(w.w_q_b, w.s_q_b, ws.q_b + (size_t)r0 * QB, QB, QB, (long long)M * QB);
+    c.tiles0 = QB / 16; c.ntiles = c.tiles0;
+    if (idx) {
+      c.seg[1] = seg(w.w_iq, w.s_iq, ws.iq + (size_t)r0 * IH * 128, IH * 128, IH * 128, (long long)M * IH * 128);
+      c.ntiles += IH * 128 / 16;
     }
   }
-  // 2. the per-row stage: three workgroups a row
   FrontDev f{};
   f.M = M; f.q_lora = s.q_lora; f.kv_lora = s.kv_lora; f.rope = s.rope; f.nope = s.nope; f.heads = s.heads;
   f.ih = IH; f.max_position = s.max_position; f.key_fmt = s.key_fmt; f.kv_scaled = s.kv_scaled;
@@ -737,29 +1025,75 @@ extern "C" int mk2_front_launch(const mk2_front_args* a, mk2_stream_t stream) {
   f.q_an = ws.q_an; f.kv = (uint8_t*)a->kv_cache; f.kv_scale = a->kv_scale;
   f.icache = (uint8_t*)a->index_cache; f.iscale = (uint8_t*)a->index_scale;
   f.mla_q = (bf16_t*)a->mla_q; f.index_q = (bf16_t*)a->index_q; f.index_w = (bf16_t*)a->index_w;
+  const int heads_grid = 4 * s.heads + (idx ? (M * IH + FR_NT / 64 - 1) / (FR_NT / 64) : 0);
+  if (persistent && front_persistent_ok(&s)) {
+    FrontPDev d{};
+    d.f = f;
+    for (int pi = 0; pi < 2; ++pi) { d.A[pi] = gA[pi]; d.W[pi] = gW[pi]; d.C[pi] = gC[pi]; }
+    d.passes = passes;
+    // one round of workgroups for a pass's hidden-input GEMVs: the W_iw workgroups
+    // first, [W_qkv_a | W_ik] on the rest (a tile's bits do not depend on which
+    // workgroup or how many take the tiles)
+    d.gridW = idx ? gemv_grid(gW[0], cus) : 0;
+    d.gridA = gemv_grid(gA[0], cus - d.gridW > gA[0].ks ? cus - d.gridW : cus);
+    d.gridC = gemv_grid(gC[0], cus);
+    d.nheads = heads_grid;
+    d.x = (const bf16_t*)a->x; d.g_in = (const bf16_t*)w.g_in; d.x_n = ws.x_n; d.hidden = s.hidden; d.eps = s.eps;
+    d.sync = ws.sync;
+    d.spin = 1 << 20;
+    return front_persistent_dispatch(d, s.weight_fmt, front_steps(&s), cus, st);
+  }
+  auto gemv_fmt = [&](const GemvDev& d) {
+    return s.weight_fmt == MK2_WFMT_FP8_AITER16 ? gemv_launch<MK2_WFMT_FP8_AITER16>(d, cus, st)
+           : f8                                 ? gemv_launch<MK2_WFMT_FP8_BLOCK>(d, cus, st)
+                                                : gemv_launch<MK2_WFMT_BF16>(d, cus, st);
+  };
+  // 0. the normed input rows
+  k_front_norm<<<M, FR_NT, 0, st>>>((const bf16_t*)a->x, (const bf16_t*)w.g_in, ws.x_n, s.hidden, s.eps);
+  rc = check_launch("front (norm)");
+  if (rc) return rc;
+  // 1. the hidden-input GEMVs
+  for (int pi = 0; pi < passes; ++pi) {
+    rc = gemv_fmt(gA[pi]);
+    if (rc) return rc;
+    if (idx) {
+      rc = gemv_launch<MK2_WFMT_BF16>(gW[pi], cus, st);
+      if (rc) return rc;
+    }
+  }
+  // 2. the per-row stage: three workgroups a row
   k_front_rows<<<(idx ? 3 : 2) * M, FR_NT, 0, st>>>(f);
   rc = check_launch("front (rows)");
   if (rc) return rc;
   // 3. the q_an-input GEMVs
-  for (int r0 = 0; r0 < M; r0 += 16) {
-    GemvDev d{};
-    d.M = M - r0 < 16 ? M - r0 : 16; d.K = s.q_lora; d.ks = pl.ksC; d.eps = s.eps;
-    d.x = ws.q_an + (size_t)r0 * s.q_lora; d.g = nullptr;
-    d.seg[0] = seg(w.w_q_b, w.s_q_b, ws.q_b + (size_t)r0 * QB, QB, QB, (long long)M * QB);
-    d.tiles0 = QB / 16; d.ntiles = d.tiles0;
-    if (idx) {
-      d.seg[1] = seg(w.w_iq, w.s_iq, ws.iq + (size_t)r0 * IH * 128, IH * 128, IH * 128, (long long)M * IH * 128);
-      d.ntiles += IH * 128 / 16;
-    }
-    rc = gemv_fmt(d);
+  for (int pi = 0; pi < passes; ++pi) {
+    rc = gemv_fmt(gC[pi]);
     if (rc) return rc;
   }
   // 4. the per-head stage
-  const int grid = 4 * s.heads + (idx ? (M * IH + FR_NT / 64 - 1) / (FR_NT / 64) : 0);
   switch (s.nope / 32) {
-    case 4: k_front_heads<4><<<grid, FR_NT, 0, st>>>(f); break;
-    case 6: k_front_heads<6><<<grid, FR_NT, 0, st>>>(f); break;
-    default: k_front_heads<8><<<grid, FR_NT, 0, st>>>(f); break;
+    case 4: k_front_heads<4><<<heads_grid, FR_NT, 0, st>>>(f); break;
+    case 6: k_front_heads<6><<<heads_grid, FR_NT, 0, st>>>(f); break;
+    default: k_front_heads<8><<<heads_grid, FR_NT, 0, st>>>(f); break;
   }
   return check_launch("front (heads)");
+}
+
+}  // namespace mk2
+
+extern "C" int mk2_front_launch(const mk2_front_args* a, mk2_stream_t stream) {
+  clear_error();
+  return front_run(a, (hipStream_t)stream, true);
+}
+
+extern "C" int mk2_front_launch_staged(const mk2_front_args* a, mk2_stream_t stream) {
+  clear_error();
+  return front_run(a, (hipStream_t)stream, false);
+}
+
+extern "C" int mk2_front_is_persistent(const mk2_front_shape* shape) {
+  clear_error();
+  int rc = front_check_shape(shape);
+  if (rc) return -rc;
+  return front_persistent_ok(shape) ? 1 : 0;
 }

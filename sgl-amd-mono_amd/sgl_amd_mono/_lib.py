@@ -101,6 +101,7 @@ class LayerArgs(ctypes.Structure):
 
 
 MK2_WFMT_BF16, MK2_WFMT_FP8_BLOCK, MK2_WFMT_FP8_AITER16 = 0, 1, 2
+MK2_FRONT_STATUS_OFFSET = 6528  # bytes into the front's workspace: the persistent launch's status word
 
 
 class FrontShape(ctypes.Structure):
@@ -163,6 +164,8 @@ SIGNATURES = {
     "mk2_tail_launch": [POINTER(TailArgs), c_void_p],
     "mk2_front_workspace_bytes": [POINTER(FrontShape), POINTER(c_size_t)],
     "mk2_front_launch": [POINTER(FrontArgs), c_void_p],
+    "mk2_front_launch_staged": [POINTER(FrontArgs), c_void_p],
+    "mk2_front_is_persistent": [POINTER(FrontShape)],
     "mk2_step_rows_launch": [POINTER(StepArgs), c_void_p],
     "mk2_write_seed_launch": [c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int, c_int, c_void_p],
     "mk2_abi_version": [],

@@ -115,11 +115,13 @@ class IndexerOp:
 class FrontOp:
     """The layer's front (the reference's K1): residual rows in; the absorbed MLA
     queries, index queries and head weights out, and this step's cache rows written.
-    `w` holds SGLang's tensors as loaded (see sgl_amd_mono.k2.synth.make_front)."""
+    `w` holds SGLang's tensors as loaded (see sgl_amd_mono.k2.synth.make_front).  One
+    persistent launch where the library instantiates the shape (`persistent`), else
+    (or with staged=True) the six stage launches; both give the same bits."""
 
-    def __init__(self, cfg: C.FrontConfig, w, rows: int, device=None):
+    def __init__(self, cfg: C.FrontConfig, w, rows: int, device=None, staged: bool = False):
         cfg.validate(rows)
-        self.cfg, self.w, self.rows = cfg, w, rows
+        self.cfg, self.w, self.rows, self.staged = cfg, w, rows, staged
         self.device = torch.device(device or w.w_qkv_a.device)
         self.shape = _lib.FrontShape(rows, cfg.hidden, cfg.q_lora, cfg.kv_lora, cfg.rope, cfg.nope, cfg.heads,
                                      cfg.index_heads, cfg.weight_fmt, cfg.keys, int(cfg.kv_scaled),
@@ -144,7 +146,18 @@ class FrontOp:
         )
         nbytes = ctypes.c_size_t()
         _lib.check(_lib.lib().mk2_front_workspace_bytes(ctypes.byref(self.shape), ctypes.byref(nbytes)))
-        self.workspace = torch.empty(nbytes.value, dtype=torch.uint8, device=self.device)
+        # zero-filled: the persistent launch's counters start at zero and each launch
+        # leaves them so
+        self.workspace = torch.zeros(nbytes.value, dtype=torch.uint8, device=self.device)
+        rc = _lib.lib().mk2_front_is_persistent(ctypes.byref(self.shape))
+        _lib.check(-rc if rc < 0 else _lib.MK2_OK)
+        self.persistent = rc == 1 and not staged
+
+    def status(self) -> int:
+        """The persistent launches' sticky status word (nonzero: a dependency wait ran
+        out of its spin limit; that launch's outputs are undefined).  Synchronizes."""
+        off = _lib.MK2_FRONT_STATUS_OFFSET
+        return int(self.workspace[off:off + 4].view(torch.int32).item())
 
     def __call__(self, x, positions, slots, rope_cos_sin, kv_cache, kv_scale, index_cache, index_scale,
                  mla_q=None, index_q=None, index_w=None):
@@ -164,7 +177,8 @@ class FrontOp:
         a = _lib.FrontArgs(self.shape, self.weights, _p(x), _p(positions), _p(slots), _p(rope_cos_sin),
                            _p(kv_cache), _p(kv_scale), _p(index_cache), _p(index_scale), _p(mla_q), _p(index_q),
                            _p(index_w), _p(self.workspace), self.workspace.numel())
-        _lib.check(_lib.lib().mk2_front_launch(ctypes.byref(a), _lib.stream_handle(dev)))
+        launch = _lib.lib().mk2_front_launch_staged if self.staged else _lib.lib().mk2_front_launch
+        _lib.check(launch(ctypes.byref(a), _lib.stream_handle(dev)))
         return mla_q, index_q, index_w
 
 

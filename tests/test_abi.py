@@ -133,8 +133,15 @@ def test_launch_argument_errors_never_reach_the_device():
     n = ctypes.c_size_t()
     assert L.mk2_front_workspace_bytes(ctypes.byref(fs), ctypes.byref(n)) == _l.MK2_EINVAL
     assert "nope" in L.mk2_last_error().decode()
+    assert L.mk2_front_is_persistent(ctypes.byref(fs)) == -_l.MK2_EINVAL
+    assert L.mk2_front_launch_staged(None, None) == _l.MK2_EINVAL
     fs.nope = 192
     assert L.mk2_front_workspace_bytes(ctypes.byref(fs), ctypes.byref(n)) == _l.MK2_OK and n.value > 0
+    # the persistent front: its counters and status word lead the workspace
+    assert n.value > _l.MK2_FRONT_STATUS_OFFSET
+    assert L.mk2_front_is_persistent(ctypes.byref(fs)) == 1  # C7: hidden 6144, q_lora 2048, nope 192
+    fs.hidden = 4096  # K steps the persistent launch does not instantiate: the stage launches
+    assert L.mk2_front_is_persistent(ctypes.byref(fs)) == 0
     assert L.mk2_tail_launch(None, None) == _l.MK2_EINVAL
     ta = _l.TailArgs(8, 6144, 0, 1e-5, fake, fake, fake, fake, None)
     assert L.mk2_tail_launch(ctypes.byref(ta), None) == _l.MK2_EINVAL

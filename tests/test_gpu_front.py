@@ -191,3 +191,51 @@ def test_front_aiter_layout_bits(rows):
     assert len(res[0]) == len(res[1]) >= 5
     for a, b in zip(*res):
         assert torch.equal(a, b)
+
+
+def _front_outputs(cfg, ns, rows, staged, repeats=1):
+    """The front's outputs and both caches (fresh copies of ns's) from `repeats`
+    launches of one op (the persistent launch resets its own counters)."""
+    from sgl_amd_mono.k2.ops import FrontOp
+
+    dev = _dev()
+    op = FrontOp(cfg, ns, rows, device=dev, staged=staged)
+    res = []
+    for _ in range(repeats):
+        kv, ic = ns.kv_cache.clone(), ns.index_cache.clone()
+        ks = None if ns.kv_scale is None else ns.kv_scale.clone()
+        isc = None if ns.index_scale is None else ns.index_scale.clone()
+        out = op(ns.x, ns.positions, ns.slots, ns.rope_cos_sin, kv, ks, ic, isc)
+        torch.cuda.synchronize()
+        res.append([cpu(t) for t in (*out, kv, ic, ks, isc) if t is not None])
+    return op, res
+
+
+@pytest.mark.parametrize("case", ["c7-1", "c7-8", "c7-32", "bf16-nope128", "aiter", "h7168-no-indexer"])
+def test_front_persistent_matches_staged(case):
+    """The persistent front (one launch, counters between its stages) gives the six
+    stage launches' bits -- outputs, latent and index cache rows and scales -- on
+    back-to-back launches (its counters reset by the launch itself), at 1, 8 and 32
+    rows (two GEMV passes), bf16 weights, AITER's layout, hidden 7168 without the
+    indexer; its status word stays 0."""
+    from sgl_amd_mono.k2 import config as C
+    from sgl_amd_mono.k2 import synth
+
+    dev = _dev()
+    rows = {"c7-1": 1, "c7-32": 32}.get(case, 8)
+    cfg = {
+        "bf16-nope128": replace(C.C7_FRONT, weight_fmt=C.WFMT_BF16, nope=128),
+        "h7168-no-indexer": replace(C.C7_FRONT, hidden=7168, q_lora=1024, index_heads=0, keys=C.KEYS_FP8),
+    }.get(case, C.C7_FRONT)
+    ns = synth.make_front(cfg, rows, 730 + rows, dev)
+    if case == "aiter":
+        ns = synth.front_in_layout(ns, C.WFMT_FP8_AITER16)
+        cfg = ns.cfg
+    p_op, p = _front_outputs(cfg, ns, rows, staged=False, repeats=3)
+    assert p_op.persistent, case
+    _, s = _front_outputs(cfg, ns, rows, staged=True)
+    assert p_op.status() == 0
+    for launch in p:
+        assert len(launch) == len(s[0])
+        for a, b in zip(launch, s[0]):
+            assert torch.equal(a, b)

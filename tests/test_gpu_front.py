@@ -239,3 +239,36 @@ def test_front_persistent_matches_staged(case):
         assert len(launch) == len(s[0])
         for a, b in zip(launch, s[0]):
             assert torch.equal(a, b)
+
+
+def test_front_persistent_new_inputs_each_launch():
+    """One persistent front op over alternating steps (residual rows, positions, slots,
+    the cache contents): each launch gives the stage launches' bits on its own inputs,
+    so nothing a previous launch left in the workspace is read back."""
+    from sgl_amd_mono.k2 import config as C
+    from sgl_amd_mono.k2 import synth
+    from sgl_amd_mono.k2.ops import FrontOp
+
+    dev = _dev()
+    cfg, rows = C.C7_FRONT, 8
+    A = synth.make_front(cfg, rows, 741, dev)
+    B = synth.make_front(cfg, rows, 742, dev)
+    p_op = FrontOp(cfg, A, rows, device=dev)  # the weights are A's; B gives the step inputs
+    s_op = FrontOp(cfg, A, rows, device=dev, staged=True)
+    assert p_op.persistent
+    outs = []
+    for src in (A, B, A, B):
+        res = []
+        for op in (p_op, s_op):
+            kv, ic = src.kv_cache.clone(), src.index_cache.clone()
+            ks = None if src.kv_scale is None else src.kv_scale.clone()
+            isc = None if src.index_scale is None else src.index_scale.clone()
+            out = op(src.x, src.positions, src.slots, src.rope_cos_sin, kv, ks, ic, isc)
+            torch.cuda.synchronize()
+            res.append([cpu(t) for t in (*out, kv, ic, ks, isc) if t is not None])
+        for a, b in zip(*res):
+            assert torch.equal(a, b)
+        outs.append(res[0][0])
+    assert p_op.status() == 0
+    assert not torch.equal(outs[0], outs[1])
+    assert torch.equal(outs[0], outs[2]) and torch.equal(outs[1], outs[3])

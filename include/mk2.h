@@ -356,6 +356,19 @@ int mk2_front_launch_staged(const mk2_front_args* args, mk2_stream_t stream);
    launches; < 0: an invalid shape (minus its MK2_E* code; mk2_last_error says why) */
 int mk2_front_is_persistent(const mk2_front_shape* shape);
 
+/* The front and the layer in ONE persistent launch: the front's stages first (as
+ * mk2_front_launch's persistent launch runs them), then the layer's, which wait for
+ * the front's per-head tasks.  The front's outputs and caches must be the layer's
+ * inputs (index_q/index_w/index_cache/index_scale = indexer q/w/cache/cache_scale,
+ * mla_q/kv_cache/kv_scale = mla q/kv/kv_scale, x = mla h) and the layer persistent;
+ * both workspaces as for their own launches.  Instanced for A8W4 experts
+ * (MK2_FMT_MXFP4) with the C7 front shape (hidden 6144, q_lora 2048, nope 192, 64
+ * index heads), block-FP8 front weights row-major or in AITER's layout; other shapes
+ * get MK2_EINVAL (launch the front and the layer on their own).  The same bits as the
+ * two launches.  Reference: its K2 launch runs the front's stages ahead of the
+ * layer's in one launch (glm53/gfx950/kernel.py:2585-3575). */
+int mk2_layer_step_launch(const mk2_front_args* front, const mk2_layer_args* layer, mk2_stream_t stream);
+
 /* ------------------------------------------------------------------ tail
  * The steps after the last layer, on this GPU's rows of the LM head: the final
  * RMSNorm and the logits.  Replaces the reference's tail launch,

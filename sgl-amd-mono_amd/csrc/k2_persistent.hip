@@ -17,6 +17,7 @@
 // so every wait ends; each wait is also bounded (spin limit) and on expiry sets a
 // sticky error word that releases every other wait, so the launch always drains.
 // The last workgroup to finish resets the counters.
+#include "front_stages.h"
 #include "indexer_stages.h"
 #include "mk2_host.h"
 #include "mla_stages.h"
@@ -84,7 +85,9 @@ union K2Lds {
   RouterLds router;
   RouteLds route;
   float red[(K2_NT / 64) * 2 * 64 * 4];
+  FrontLds front;
 };
+static_assert(sizeof(FrontLds) <= sizeof(TopkLds), "the front's LDS fits the layer's union as it is");
 
 MK2_DEV int* k2_ctr(const K2Dev& p, int line) { return p.sync + line * SY_LINE; }
 
@@ -161,8 +164,27 @@ MK2_DEV bool k2_wait(const K2Dev& p, int* seen, int line, int target, int stamp 
 // rest go through the scores in the workspace)
 constexpr int K2_KEEP = 4;
 
-template <int NCG, int FMT>
-__global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
+// What the launch runs ahead of the layer's stages: nothing, or the layer's front
+// (the persistent front's walk, its per-head tasks counting out, then a wait for all
+// of them: the scores read the index queries and keys, the splits the MLA queries
+// and latent rows, that it writes).  reset: the last workgroup out also resets its
+// counters.
+struct K2NoFront {
+  MK2_DEV bool run(FrontLds&, int*) const { return true; }
+  MK2_DEV void reset() const {}
+};
+template <int KUA, int KUC, int WF, int NS>
+struct K2Front {
+  FrontPDev f;
+  MK2_DEV bool run(FrontLds& S, int* seen) const {
+    if (!front_walk<KUA, KUC, WF, NS, true>(f, S, seen)) return false;
+    return fp_wait(f, seen, 4, FP_HEADS, FP_LANES, f.nheads);
+  }
+  MK2_DEV void reset() const { front_reset(f); }
+};
+
+template <int NCG, int FMT, class Front = K2NoFront>
+__global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p, Front front) {
   __shared__ K2Lds S;
   __shared__ float kept[K2_KEEP][IDX_CHUNK];  // this workgroup's score tasks' scores, by t / G
   __shared__ int seen[SY_LINES + 1];  // counts seen by line; [SY_LINES]: a wait failed
@@ -319,7 +341,18 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
     k2_stamp(p, 3 * st + 2);
 
   };
-  walk();
+  // the front first, when the launch runs it: a failed front stops the layer's walk and
+  // fails every layer wait at once
+  __shared__ int fseen[FP_SEEN];
+  bool front_ok = true;
+  if constexpr (!std::is_same<Front, K2NoFront>::value) {
+    if (threadIdx.x < FP_SEEN) fseen[threadIdx.x] = 0;
+    __syncthreads();
+    front_ok = front.run(S.front, fseen);
+    __syncthreads();  // the front's LDS is the stages' from here on
+    if (!front_ok && threadIdx.x == 0) atomicOr(k2_ctr(p, SY_ERR), 1);
+  }
+  if (front_ok) walk();
 #undef K2_TASKS
 #undef K2_NEXT
   // ---- the last workgroup out resets the counters for the next launch
@@ -344,6 +377,7 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
     }
     for (int l = threadIdx.x; l < SY_LINES; l += K2_NT)
       __hip_atomic_store(k2_ctr(p, l), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    front.reset();
     // the epoch moves on: the next launch's tags differ from every tag of this one
     if (threadIdx.x == 0) st_dev_i32(p.sync + SYNC_EPOCH, (int)s_tag);
   }
@@ -351,8 +385,11 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p) {
 
 static int g_cus = 0;
 
+// front: the layer's front to run ahead of the stages in the same launch, or null;
+// front_key: its instantiation (FRONT_FUSED_*)
 int k2_persistent_enqueue(const IdxDev& idx, const MlaDev& mla, const MoeDev& moe, int* sync,
-                          int* status, uint64_t* timeline, int rows, int spin_limit, hipStream_t st) {
+                          int* status, uint64_t* timeline, int rows, int spin_limit, hipStream_t st,
+                          const FrontPDev* front, int front_key) {
   if (g_cus == 0) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
@@ -361,17 +398,27 @@ int k2_persistent_enqueue(const IdxDev& idx, const MlaDev& mla, const MoeDev& mo
   }
   K2Dev p{idx, mla, moe, sync, status, timeline, rows, spin_limit};
   const bool two = rows > 16;
-  // one instantiation a column-group count and expert mode
+  // one instantiation a column-group count and expert mode (and, with the front ahead,
+  // front shape)
   return with_moe_fmt(moe.fmt, [&](auto F) {
     constexpr int FMT = decltype(F)::value;
-    int per_cu = 0;
-    hipError_t e = two ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_k2_layer<2, FMT>, K2_NT, 0)
-                       : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_k2_layer<1, FMT>, K2_NT, 0);
-    if (e != hipSuccess || per_cu < 1)
-      return set_error(MK2_ELAUNCH, "layer: the persistent kernel does not fit one workgroup per CU");
-    if (two) k_k2_layer<2, FMT><<<g_cus, K2_NT, 0, st>>>(p);
-    else k_k2_layer<1, FMT><<<g_cus, K2_NT, 0, st>>>(p);
-    return check_launch("layer (persistent)");
+    auto launch = [&](auto fr) -> int {
+      using Fr = decltype(fr);
+      int per_cu = 0;
+      hipError_t e = two ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_k2_layer<2, FMT, Fr>, K2_NT, 0)
+                         : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_k2_layer<1, FMT, Fr>, K2_NT, 0);
+      if (e != hipSuccess || per_cu < 1)
+        return set_error(MK2_ELAUNCH, "layer: the persistent kernel does not fit one workgroup per CU");
+      if (two) k_k2_layer<2, FMT, Fr><<<g_cus, K2_NT, 0, st>>>(p, fr);
+      else k_k2_layer<1, FMT, Fr><<<g_cus, K2_NT, 0, st>>>(p, fr);
+      return check_launch("layer (persistent)");
+    };
+    if (!front) return launch(K2NoFront{});
+    if constexpr (FMT == MK2_FMT_MXFP4) {
+      if (front_key == FRONT_FUSED_C7_FP8) return launch(K2Front<6, 4, MK2_WFMT_FP8_BLOCK, 6>{*front});
+      if (front_key == FRONT_FUSED_C7_AITER16) return launch(K2Front<6, 4, MK2_WFMT_FP8_AITER16, 6>{*front});
+    }
+    return set_error(MK2_EINVAL, "layer step: no front-and-layer launch for this expert mode and front shape");
   });
 }
 

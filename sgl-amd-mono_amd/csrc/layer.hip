@@ -3,6 +3,7 @@
 // one persistent launch (k2_persistent.hip) or as one kernel a stage.
 #include <mutex>
 
+#include "front_stages.h"
 #include "indexer_stages.h"
 #include "mla_stages.h"
 #include "mk2_host.h"
@@ -20,7 +21,9 @@ int moe_fill(const mk2_moe_args* a, MoeDev* d);
 size_t moe_carve(const mk2_moe_shape* s, void* base, MoeDev* d);
 int moe_enqueue(const MoeDev& d, hipStream_t st);
 int k2_persistent_enqueue(const IdxDev& idx, const MlaDev& mla, const MoeDev& moe, int* sync,
-                          int* status, uint64_t* timeline, int rows, int spin_limit, hipStream_t st);
+                          int* status, uint64_t* timeline, int rows, int spin_limit, hipStream_t st,
+                          const FrontPDev* front = nullptr, int front_key = 0);
+int front_pdev(const mk2_front_args* a, FrontPDev* d, int* key);
 
 constexpr int LAYER_SYNC_BYTES = SYNC_INTS * 4;  // the persistent launch's counters and its epoch
 
@@ -192,4 +195,38 @@ extern "C" int mk2_layer_launch(const mk2_layer_args* a, mk2_stream_t stream) {
   idx_enqueue(L.idx, st);
   mla_enqueue(L.mla, st);
   return moe_enqueue(L.moe, st);
+}
+
+extern "C" int mk2_layer_step_launch(const mk2_front_args* f, const mk2_layer_args* a, mk2_stream_t stream) {
+  clear_error();
+  MK2_REQUIRE(f != nullptr && a != nullptr, "layer step: front and layer args must be set");
+  FrontPDev fd;
+  int key = FRONT_FUSED_NONE;
+  int rc = front_pdev(f, &fd, &key);
+  if (rc) return rc;
+  MK2_REQUIRE(key != FRONT_FUSED_NONE,
+              "layer step: the front-and-layer launch has no instance for this front shape and weight format");
+  LayerPlan L;
+  size_t need = 0;
+  rc = layer_plan(a, nullptr, &L, &need);
+  if (rc) return rc;
+  MK2_REQUIRE(a->mode == MK2_LAYER_PERSISTENT, "layer step: the layer runs persistent");
+  MK2_REQUIRE(a->out && a->workspace, "layer: out and workspace must be set");
+  MK2_REQUIRE(a->out != a->mla.h, "layer: out must not alias the residual h");
+  if (a->workspace_bytes < need)
+    return set_error(MK2_ENOSPACE, "layer: workspace has %zu bytes, needs %zu", a->workspace_bytes, need);
+  // the front's outputs are the layer's inputs, its caches the layer's caches
+  MK2_REQUIRE(f->shape.rows == a->mla.shape.rows, "layer step: front rows %d != layer rows %d", f->shape.rows,
+              a->mla.shape.rows);
+  MK2_REQUIRE(f->x == a->mla.h, "layer step: the front's residual rows x must be the layer's residual h");
+  MK2_REQUIRE(f->mla_q == a->mla.q && f->kv_cache == a->mla.kv && f->kv_scale == a->mla.kv_scale,
+              "layer step: the front's mla_q, kv_cache and kv_scale must be the layer's q, kv and kv_scale");
+  MK2_REQUIRE(f->index_q == a->indexer.q && f->index_w == a->indexer.w && f->index_cache == a->indexer.cache &&
+                  f->index_scale == a->indexer.cache_scale,
+              "layer step: the front's index_q, index_w, index_cache and index_scale must be the indexer's q, w, "
+              "cache and cache_scale");
+  rc = layer_plan(a, a->workspace, &L, &need);
+  if (rc) return rc;
+  return k2_persistent_enqueue(L.idx, L.mla, L.moe, L.sync, a->status, (uint64_t*)a->timeline, a->mla.shape.rows,
+                               a->spin_limit ? a->spin_limit : (1 << 20), (hipStream_t)stream, &fd, key);
 }

@@ -159,8 +159,10 @@ class FrontOp:
         off = _lib.MK2_FRONT_STATUS_OFFSET
         return int(self.workspace[off:off + 4].view(torch.int32).item())
 
-    def __call__(self, x, positions, slots, rope_cos_sin, kv_cache, kv_scale, index_cache, index_scale,
-                 mla_q=None, index_q=None, index_w=None):
+    def _make_args(self, x, positions, slots, rope_cos_sin, kv_cache, kv_scale, index_cache, index_scale,
+                   mla_q=None, index_q=None, index_w=None):
+        """The launch's argument block (outputs allocated where not given) and the
+        outputs (mla_q, index_q, index_w)."""
         cfg, rows, dev = self.cfg, self.rows, self.device
         _need(x, "x", torch.bfloat16, (rows, cfg.hidden))
         _need(positions, "positions", torch.int64, (rows,))
@@ -177,9 +179,15 @@ class FrontOp:
         a = _lib.FrontArgs(self.shape, self.weights, _p(x), _p(positions), _p(slots), _p(rope_cos_sin),
                            _p(kv_cache), _p(kv_scale), _p(index_cache), _p(index_scale), _p(mla_q), _p(index_q),
                            _p(index_w), _p(self.workspace), self.workspace.numel())
+        return a, (mla_q, index_q, index_w)
+
+    def __call__(self, x, positions, slots, rope_cos_sin, kv_cache, kv_scale, index_cache, index_scale,
+                 mla_q=None, index_q=None, index_w=None):
+        a, outs = self._make_args(x, positions, slots, rope_cos_sin, kv_cache, kv_scale, index_cache,
+                                  index_scale, mla_q, index_q, index_w)
         launch = _lib.lib().mk2_front_launch_staged if self.staged else _lib.lib().mk2_front_launch
-        _lib.check(launch(ctypes.byref(a), _lib.stream_handle(dev)))
-        return mla_q, index_q, index_w
+        _lib.check(launch(ctypes.byref(a), _lib.stream_handle(self.device)))
+        return outs
 
 
 class TailOp:
@@ -389,3 +397,28 @@ class LayerOp:
             self.status.zero_()
             raise RuntimeError("K2 layer: a persistent launch stopped early (a dependency wait gave up); "
                                "its outputs are not valid")
+
+
+class LayerStepOp:
+    """The front and the K2 layer in ONE persistent launch (mk2_layer_step_launch): the
+    front's stages, then the layer's.  The front writes the layer's inputs: the layer
+    `layer_op.L`'s index queries, head weights, MLA queries and caches, from its
+    residual rows L.h; the same bits as front_op's launch followed by layer_op's."""
+
+    def __init__(self, front_op: FrontOp, layer_op: LayerOp):
+        if front_op.rows != layer_op.rows:
+            raise ValueError("front and layer rows differ")
+        self.front, self.layer = front_op, layer_op
+
+    def __call__(self, positions, slots, rope_cos_sin, out=None, *, status=None, **layer_outputs):
+        L, lo = self.layer.L, self.layer
+        fa, _ = self.front._make_args(L.h, positions, slots, rope_cos_sin, L.mla.kv, L.mla.kv_scale, L.idx.cache,
+                                      L.idx.cache_scale, L.mla.q, L.idx.q, L.idx.w)
+        H = lo.cfg.mla.hidden
+        if out is None:
+            out = torch.empty(lo.rows, H, dtype=torch.bfloat16, device=lo.device)
+        _need(out, "out", torch.bfloat16, (lo.rows, H))
+        la = lo._make_args(out, workspace=lo.workspace, status=lo.status if status is None else status,
+                           **layer_outputs)
+        _lib.check(_lib.lib().mk2_layer_step_launch(ctypes.byref(fa), ctypes.byref(la), _lib.stream_handle(lo.device)))
+        return out

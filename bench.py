@@ -33,8 +33,8 @@ LAYER_KERNEL = "k_k2_layer"  # the persistent layer kernel's name (rocprof)
 
 
 # the sources the layer launch is built from (its kernels and the headers they include)
-LAYER_SOURCES = ("common.hip", "indexer_stages.h", "k2_persistent.hip", "layer.hip", "mk2_device.h",
-                 "mk2_host.h", "mla_stages.h", "moe_stages.h")
+LAYER_SOURCES = ("common.hip", "front_stages.h", "indexer_stages.h", "k2_persistent.hip", "layer.hip",
+                 "mk2_device.h", "mk2_host.h", "mla_stages.h", "moe_stages.h")
 
 
 def sources_digest():

@@ -223,15 +223,24 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p, Front front) {
     // keeps its keys in the bin
     k2_stamp(p, 3 * st);
     // slices on the workgroups of their score chunks (base unchanged).  A slice counts
-    // out once its chunk's counts and bin keys are out; the last to count out of a
-    // row lists its own keys above the bin, then finishes the row's list from the
-    // keys in the threshold bin, while the others still list theirs
+    // out once its chunk's counts and bin keys are out.  With one slice a workgroup
+    // (up to 8 rows) the last to count out of a row lists its own keys above the bin,
+    // then finishes the row's list from the keys in the threshold bin, while the others
+    // still list theirs.  With several a workgroup the selects are tasks of their own
+    // after the slices: a workgroup that won one row would start its next slice late,
+    // be the last of that row too, and run every round's select in turn
+    const bool sel_tasks = R * nchk > G;
     K2_TASKS(t, R * nchk) {
       const int r = t / nchk;
       if (!k2_wait(p, seen, SY_SCORE + r, nchk, t < G ? 3 * st + 1 : -1)) return;
       bool last = false;
       const bool known = idx_slice<K2_NT>(p.idx, r, t % nchk, S.topk, p.spin_limit, k2_ctr(p, SY_ERR), tp.tag,
-                                          [&] { last = k2_signal_last1(p, SY_SLICE + r, nchk, &last_flag); },
+                                          [&] {
+                                            if (sel_tasks)
+                                              k2_signal(p, SY_SLICE + r);
+                                            else
+                                              last = k2_signal_last1(p, SY_SLICE + r, nchk, &last_flag);
+                                          },
                                           keep_of(t));
       if (last) {
         k2_stamp(p, 3 * (st + 1));
@@ -244,9 +253,19 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p, Front front) {
         idx_clear_hist<K2_NT>(p.idx, r);
       }
     }
+    k2_stamp(p, 3 * st + 2);
     K2_NEXT(R * nchk);
-    k2_stamp(p, 3 * st++ + 2);
-    ++st;  // the select stamps are taken above
+    if (sel_tasks) {
+      K2_TASKS(r, R) {
+        k2_stamp(p, 3 * (st + 1));
+        if (!k2_wait(p, seen, SY_SLICE + r, nchk, 3 * (st + 1) + 1)) return;
+        idx_select<K2_NT>(p.idx, r, S.topk, tp.tag, false);
+        k2_stamp(p, 3 * (st + 1) + 2);
+        idx_clear_hist<K2_NT>(p.idx, r);
+      }
+      K2_NEXT(R);
+    }
+    st += 2;  // the select stamps are taken above
     // ---- sparse-MLA splits
     k2_stamp(p, 3 * st);
     const int ns = p.mla.nsplit;

@@ -317,8 +317,8 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p, Front front) {
     }
     K2_NEXT(nrt);
     k2_stamp(p, 3 * st++ + 2);
-    // ---- routing, on one workgroup: one without a router task (it polls while they
-    // run) and with the fewest up/gate tasks.  It polls the router tasks' logits and
+    // ---- routing, on one workgroup up to 8 rows: one without a router task (it polls
+    // while they run) and with the fewest up/gate tasks.  It polls the router tasks' logits and
     // puts out the tagged expert list, then the route-weight table, published by
     // SY_ROUTE for the down
     const int up_r = p.moe.Dmax * (p.moe.I / p.moe.UC);
@@ -326,15 +326,29 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p, Front front) {
     const int up_total = up_r + up_sh;
     // the up/gate tasks start at workgroup `base`; from base + up_total % G on, the
     // workgroups hold one fewer; the router tasks ended on the nrt workgroups before base
+    // above 8 rows the rows' top-k runs on nq workgroups of 8 rows each, the first of
+    // which (the lead) polls the others' picks and puts out the list and the tables
+    const int nq = p.moe.M > 8 ? (p.moe.M + 7) / 8 : 1;
     int route_at = up_total % G;
-    if (nrt < G && route_at >= G - nrt) route_at = G - nrt - 1;
-    if (b == (base + route_at) % G) {
-      k2_stamp(p, 3 * st);
-      if (!moe_route<K2_NT, kCompact<NCG, FMT>>(p.moe, S.route, tp, [&](int i) { k2_stamp(p, 3 * K2_STAGES + i); }))
-        return;
-      k2_stamp(p, 3 * st + 1);
-      k2_signal(p, SY_ROUTE);
-      k2_stamp(p, 3 * st + 2);
+    if (nrt < G && route_at > G - nrt - nq) route_at = max(0, G - nrt - nq);
+    const int q = (b - base - route_at + 2 * G) % G;
+    if (q < nq) {
+      constexpr bool CMP = kCompact<NCG, FMT>;
+      if (q == 0) k2_stamp(p, 3 * st);
+      auto mark = [&](int i) { if (q == 0) k2_stamp(p, 3 * K2_STAGES + i); };
+      bool ok;
+      if (nq == 1)
+        ok = moe_route<K2_NT, CMP>(p.moe, S.route, tp, mark);
+      else if (q == 0)
+        ok = moe_route<K2_NT, CMP, ROUTE_LEAD>(p.moe, S.route, tp, mark, 0, 8);
+      else
+        ok = moe_route<K2_NT, CMP, ROUTE_PICK>(p.moe, S.route, tp, mark, 8 * q, min(p.moe.M, 8 * q + 8));
+      if (!ok) return;
+      if (q == 0) {
+        k2_stamp(p, 3 * st + 1);
+        k2_signal(p, SY_ROUTE);
+        k2_stamp(p, 3 * st + 2);
+      }
     }
     ++st;
     // ---- up/gate + SwiGLU: the shared expert's chunks first (they need only the

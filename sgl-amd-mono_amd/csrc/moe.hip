@@ -97,6 +97,7 @@ size_t moe_carve(const mk2_moe_shape* s, void* base, MoeDev* d) {
   t.rw = c.take<float>((size_t)Dmax * 32);
   t.act_rows = c.take<uint64_t>((size_t)Dmax);
   t.rowc = c.take<int>((size_t)Dmax * 32);
+  t.picks = c.take<uint64_t>((size_t)M * s->top_k * 2);
   if (fmt == MK2_FMT_MXFP4 || fmt == MK2_FMT_A4W4 || fmt == MK2_FMT_W8A8) {
     t.mid_q = c.take<uint8_t>((size_t)Dmax * M * I);
     if (fmt == MK2_FMT_W8A8) t.mid_sf = c.take<float>((size_t)Dmax * M * I / 128);
@@ -110,7 +111,7 @@ size_t moe_carve(const mk2_moe_shape* s, void* base, MoeDev* d) {
     d->xsf = t.xsf; d->mid_sf = t.mid_sf;
     d->logit_part = t.logit_part; d->logits = t.logits; d->topk_ids = t.topk_ids;
     d->topk_w = t.topk_w; d->act = t.act; d->rw = t.rw; d->mid_q = t.mid_q;
-    d->act_rows = t.act_rows; d->rowc = t.rowc;
+    d->act_rows = t.act_rows; d->rowc = t.rowc; d->picks = t.picks;
     d->mid_s = t.mid_s; d->mid_b = t.mid_b; d->mid_sh = t.mid_sh;
   }
   return c.bytes();

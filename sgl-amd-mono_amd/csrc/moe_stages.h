@@ -55,6 +55,8 @@ struct MoeDev {
   float* rw;         // [Dmax][32] route weight of slot j for row r (0: not routed); with
                      // compacted rows (compact_rows), of slot j's c-th row
   uint64_t* act_rows; // [Dmax] tagged: slot j's rows as a bit mask (compacted rows)
+  uint64_t* picks;   // [M][topk][2] tagged: row r's k-th pick, expert then weight bits
+                     // (the persistent layer's route pick tasks, above 8 rows)
   int* rowc;         // [Dmax][32] slot j's rows, ascending (compacted rows)
   uint8_t* mid_q;    // [Dmax][M][I] E4M3 mid (A8W4, W8A8) or [Dmax][M][I/2] E2M1 (A4W4)
   uint8_t* mid_s;    // [Dmax][M][I/32] E8M0 (A8W4, A4W4)
@@ -393,6 +395,10 @@ MK2_DEV void moe_router(const MoeDev& p, int nt, int kc, RouterLds& L, uint32_t 
 // slot and the count together), and the dense route-weight table rw [slot][row] for
 // the down (published by the caller's counter).  Returns false when the launch is
 // failing (a poll gave up).
+// Above 8 rows the persistent layer spreads the rows' top-k over several workgroups:
+// ROUTE_PICK takes rows r0 .. r1-1 (logits, top-k) and stores their picks as tagged
+// words; ROUTE_LEAD takes its own rows the same way, polls every other row's picks,
+// then puts out the list and the tables as ROUTE_ALL does.
 struct RouteLds {
   int flag[256];     // expert: 1 if picked, then its slot (-1: none)
   int ids[32 * 8];   // [M][topk]
@@ -419,9 +425,11 @@ MK2_DEV uint32_t wave_max_u32(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
+enum { ROUTE_ALL = 0, ROUTE_PICK = 1, ROUTE_LEAD = 2 };
 // CMP: the compacted-row tables as well (compact_rows(p) must agree)
-template <int NT, bool CMP = false, typename Mark = NoMark>
-MK2_DEV bool moe_route(const MoeDev& p, RouteLds& L, const TagPoll& tp, Mark mark = Mark()) {
+template <int NT, bool CMP = false, int MODE = ROUTE_ALL, typename Mark = NoMark>
+MK2_DEV bool moe_route(const MoeDev& p, RouteLds& L, const TagPoll& tp, Mark mark = Mark(), int r0 = 0, int r1 = 0) {
+  if (MODE == ROUTE_ALL) r0 = 0, r1 = p.M;
   constexpr int NW = NT / 64;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int el = min(lane, p.E / 4 - 1);  // lanes past E/4 repeat the last group, unused
@@ -441,11 +449,11 @@ MK2_DEV bool moe_route(const MoeDev& p, RouteLds& L, const TagPoll& tp, Mark mar
   // of two tagged words) until all carry the tag, then sums the slices in slice order
   bool bad = false;
   {
-    const int pieces = p.M * p.E / 2;
+    const int pieces = r1 * p.E / 2;
     const uint32_t plane = (uint32_t)(p.M * p.E) * 8u;  // bytes a slice
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc((void*)p.logit_part, (short)0, (int)(plane * p.KC), 0x00020000);
-    for (int c0 = 0; c0 < pieces && !bad; c0 += 2 * NT) {
+    for (int c0 = r0 * p.E / 2; c0 < pieces && !bad; c0 += 2 * NT) {
       float sum[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
       // up to eight slices a poll round: one round trip for hidden <= 8192
       constexpr int KU = 8;
@@ -491,7 +499,7 @@ MK2_DEV bool moe_route(const MoeDev& p, RouteLds& L, const TagPoll& tp, Mark mar
   if (L.bad) return false;
   mark(0);
   constexpr float LOG2E = 1.4426950408889634f;
-  for (int r = wave; r < p.M; r += NW) {
+  for (int r = r0 + wave; r < r1; r += NW) {
     const float4 v = *(const float4*)(L.lg + r * p.E + 4 * el);
     const float4 bias = *(const float4*)(L.bias + 4 * el);
     const bool live = 4 * lane < p.E;
@@ -564,9 +572,42 @@ MK2_DEV bool moe_route(const MoeDev& p, RouteLds& L, const TagPoll& tp, Mark mar
     if (lane < p.topk) {
       st_dev_i32(p.topk_ids + r * p.topk + lane, my_e);
       st_dev_f32(p.topk_w + r * p.topk + lane, w);
+      if (MODE == ROUTE_PICK) {
+        st_pair(p.picks + 2 * (r * p.topk + lane), (uint32_t)my_e, tp.tag);
+        st_pair(p.picks + 2 * (r * p.topk + lane) + 1, __float_as_uint(w), tp.tag);
+      }
       L.w[r * p.topk + lane] = w;
       L.flag[my_e] = 1;
     }
+  }
+  if (MODE == ROUTE_PICK) {
+    __syncthreads();  // the caller's next stage reuses this LDS
+    return true;
+  }
+  if (MODE == ROUTE_LEAD) {
+    // every other row's picks, one tagged word a thread a round
+    const int words = 2 * p.M * p.topk;
+    for (int i0 = 0; i0 < words && !bad; i0 += NT) {
+      const int i = min(i0 + tid, words - 1);
+      const bool own = i / (2 * p.topk) >= r0 && i / (2 * p.topk) < r1;
+      uint64_t w = 0;
+      for (int polls = 1;; ++polls) {
+        w = own ? 0 : ld_pair(p.picks + i);
+        if (poll_done(own || pair_ready(w, tp), polls, tp, &bad)) break;
+      }
+      if (i0 + tid < words && !own && !bad) {
+        const int j = i >> 1;
+        if (i & 1) {
+          L.w[j] = __uint_as_float(pair_value(w));
+        } else {
+          L.ids[j] = (int)pair_value(w);
+          L.flag[pair_value(w)] = 1;
+        }
+      }
+    }
+    if (bad && lane == 0) L.bad = 1;
+    __syncthreads();
+    if (L.bad) return false;
   }
   __syncthreads();
   mark(1);

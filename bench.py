@@ -349,6 +349,8 @@ def main():
     ap.add_argument("--timeline", metavar="MD",
                     help="write the persistent launch's per-stage timeline (markdown) to this file and exit")
     ap.add_argument("--timeline-launches", type=int, default=24)
+    ap.add_argument("--probes", metavar="MD",
+                    help="run the HBM streaming-read and XCD hand-off probes, write a markdown summary and exit")
     ap.add_argument("--standalone", metavar="MD",
                     help="time configs[0..3], the tail and the front as their own launches; write a table")
     args = ap.parse_args()
@@ -372,6 +374,9 @@ def main():
     dev = torch.device("cuda:0")
     if args.standalone:
         standalone(args, dev)
+        return
+    if args.probes:
+        run_probes(args.probes, dev)
         return
     cfg, rows = C.C5_LAYER, args.rows
     extra = [int(r) for r in args.extra_rows.split(",") if r] if args.extra_rows else []
@@ -458,6 +463,41 @@ def main():
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(synth.view_rows(layers[0], rows), args.cpu_reps)
     print(json.dumps(result))
+
+
+def run_probes(path, dev):
+    """The streaming-read ceiling and the hand-off litmus (sgl_amd_mono.k2.probes)."""
+    from sgl_amd_mono.k2 import probes
+    lines = ["# HBM streaming-read ceiling and XCD hand-off litmus", "",
+             "Command, run from the repository root on the MI355X box:", "",
+             "    python3 " + " ".join(sys.argv), "",
+             f"HIP sources sha256 {sources_digest()}.", "",
+             "Streaming read in the layer's launch shape (one 512-thread workgroup a CU, 16-B",
+             "loads, 8 in flight a lane, `mk2_probe_stream_read`), event-timed. Back to back:",
+             "20 launches in a row over distinct buffers cycled through more than 1 GiB (as",
+             "bench.py cycles its resident layers), median of 5 reps. Cold: one launch after a",
+             "1 GiB write that flushes the L2s and the 256 MB MALL, median of 5:", "",
+             "| bytes a launch | back to back GB/s | fraction of 8 TB/s | µs a launch | cold GB/s | cold µs |",
+             "|---|---|---|---|---|---|"]
+    for mib in (48, 147, 209, 512, 2048):
+        print(f"== stream {mib} MiB", flush=True)
+        nbytes, b2b, cold = probes.stream_read(mib, reps=5, dev=dev)
+        g, c = sorted(b2b)[2], sorted(cold)[2]
+        lines.append(f"| {nbytes / 2**20:.0f} MiB | {g:.0f} | {g / 8000:.3f} | {nbytes / g / 1e3:.1f} | "
+                     f"{c:.0f} | {nbytes / c / 1e3:.1f} |")
+    lines += ["", "Hand-off litmus (`mk2_probe_handoff`): one workgroup a CU, 100 rounds, 4 KiB or",
+              "8 KiB a consumer a round, producers and consumers on different XCDs; three",
+              "launches a mode:", "", "| mode | protocol | stale words | waits given up | us a round |",
+              "|---|---|---|---|---|"]
+    for mode, name in probes.HANDOFF_MODES.items():
+        print(f"== handoff mode {mode}", flush=True)
+        runs = [probes.handoff(mode, rounds=100, dev=dev) for _ in range(3)]
+        lines.append(f"| {mode} | {name} | {' / '.join(str(r[0]) for r in runs)} | "
+                     f"{' / '.join(str(r[1]) for r in runs)} | {' / '.join(f'{r[2]:.2f}' for r in runs)} |")
+    md = "\n".join(lines) + "\n"
+    with open(path, "w") as f:
+        f.write(md)
+    print(md)
 
 
 def time_graph(calls, steps=200, warmup=20):

@@ -445,6 +445,28 @@ int mk2_abi_version(void);
 int mk2_selftest_mfma(int mode, const void* a, const void* sa, const void* b,
                       const void* sb, float* d, mk2_stream_t stream);
 
+/* Measurement probes (no counterpart in the reference; used by bench.py --probes and
+ * the GPU tests to evidence two design rules of the persistent layer).
+ *
+ * mk2_probe_stream_read: one 512-thread workgroup a CU streams `bytes` from src with
+ * 16-byte loads, 8 in flight a lane (the layer's launch shape); bytes must be a
+ * positive multiple of mk2_probe_stream_unit() (CUs x 64 KiB; 0 when the device
+ * cannot be queried).  sink: one device word, practically never written.
+ *
+ * mk2_probe_handoff: a litmus of the hand-off rules across XCDs, `rounds` rounds of
+ * one workgroup a CU handing data to workgroups on other XCDs.  mode 0: write-once
+ * data, device-coherent stores, counter, plain loads; 1: the same with two producers
+ * a 128-B line; 2: a line polled device-coherently while partly published, its late
+ * half read with plain loads; 3: as 2, read with device-coherent loads.  The entry
+ * point clears buf, flags and result itself (hipMemsetAsync: not for graph capture).
+ * result[0] = mismatched words, result[1] = bounded waits that gave up (each spins at
+ * most `spin` polls).  Buffer sizes from mk2_probe_handoff_bytes. */
+size_t mk2_probe_stream_unit(void);
+int mk2_probe_stream_read(const void* src, size_t bytes, uint32_t* sink, mk2_stream_t stream);
+int mk2_probe_handoff_bytes(int rounds, size_t* buf_bytes, size_t* flag_bytes);
+int mk2_probe_handoff(int mode, uint32_t* buf, size_t buf_bytes, int* flags, size_t flag_bytes, int* result,
+                      int rounds, int spin, mk2_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -171,6 +171,9 @@ SIGNATURES = {
     "mk2_write_seed_launch": [c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int, c_int, c_void_p],
     "mk2_abi_version": [],
     "mk2_selftest_mfma": [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],
+    "mk2_probe_stream_read": [c_void_p, c_size_t, c_void_p, c_void_p],
+    "mk2_probe_handoff_bytes": [c_int, POINTER(c_size_t), POINTER(c_size_t)],
+    "mk2_probe_handoff": [c_int, c_void_p, c_size_t, c_void_p, c_size_t, c_void_p, c_int, c_int, c_void_p],
 }
 
 _LIB = None
@@ -201,6 +204,9 @@ def lib(required_symbols=None):
         fn = getattr(handle, name)
         fn.argtypes = argtypes
         fn.restype = c_int
+    if hasattr(handle, "mk2_probe_stream_unit"):
+        handle.mk2_probe_stream_unit.argtypes = []
+        handle.mk2_probe_stream_unit.restype = c_size_t
     handle.mk2_last_error.argtypes = []
     handle.mk2_last_error.restype = c_char_p
     if handle.mk2_abi_version() != ABI_VERSION:

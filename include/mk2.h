@@ -130,6 +130,30 @@ typedef struct mk2_moe_args {
 
 int mk2_moe_workspace_bytes(const mk2_moe_shape* shape, size_t* bytes);
 int mk2_moe_launch(const mk2_moe_args* args, mk2_stream_t stream);
+/* Where a launch leaves the MoE block's activations in its workspace: byte offsets
+ * from the workspace's start, -1 where the expert mode has no such buffer.  They are
+ * what the device quantizers wrote -- the normalized rows and their codes and scales
+ * (the reference's activation quant, kernel.py:1740-1777,5563-5614) and the SwiGLU
+ * mid's (kernel.py:6955-6985,7032-7060) -- and stay there until the next launch on
+ * the workspace.  The reference's checks read the same buffers through its scratch
+ * layout (glm53/gfx950/layout.py:181-318).  Slot j is the j-th distinct routed
+ * expert, ascending (act); with compact = 1 (rows > 16, A8W4 or A4W4) row c of slot
+ * j's mid is the c-th of the rows that picked its expert, ascending. */
+typedef struct mk2_moe_ws_layout {
+  int64_t xn;      /* bf16 [rows][hidden]: bf16(x * rstd * gamma) (x itself without norm) */
+  int64_t xq;      /* A8W4, W8A8: E4M3 [rows][hidden]; A4W4: E2M1 [rows][hidden/2] */
+  int64_t xs;      /* A8W4, A4W4: E8M0 [rows][hidden/32] */
+  int64_t xsf;     /* W8A8: f32 [rows][hidden/128] */
+  int64_t act;     /* u64 [1 + dmax], low 32 bits: the count D, then the experts */
+  int64_t mid_q;   /* A8W4, W8A8: E4M3 [dmax][rows][inter]; A4W4: E2M1 [dmax][rows][inter/2] */
+  int64_t mid_s;   /* A8W4, A4W4: E8M0 [dmax][rows][inter/32] */
+  int64_t mid_sf;  /* W8A8: f32 [dmax][rows][inter/128] */
+  int64_t mid_b;   /* W8A16, A16W4: bf16 [dmax][rows][inter] */
+  int64_t mid_sh;  /* bf16 [rows][shared_inter]: the shared expert's mid */
+  int32_t dmax;    /* capacity of the slot list */
+  int32_t compact; /* 1: compacted rows (see above) */
+} mk2_moe_ws_layout;
+int mk2_moe_workspace_layout(const mk2_moe_shape* shape, mk2_moe_ws_layout* layout);
 
 /* ------------------------------------------------------------ indexer + top-k
  * Index cache, one of SGLang's two formats, read in place:
@@ -244,6 +268,10 @@ typedef struct mk2_layer_args {
 
 int mk2_layer_workspace_bytes(const mk2_layer_args* args, size_t* bytes);
 int mk2_layer_launch(const mk2_layer_args* args, mk2_stream_t stream);
+/* The MoE block's part of a layer workspace: *moe_offset = the byte offset of its
+ * MoE workspace, whose buffers mk2_moe_workspace_layout(&args->moe.shape) places (the
+ * reference's scratch layout, glm53/gfx950/layout.py:181-318). */
+int mk2_layer_workspace_layout(const mk2_layer_args* args, int64_t* moe_offset);
 
 /* The same layer launch without a caller workspace: no counterpart in the reference.
  * It is for callers that cannot allocate device memory (code under HIP graph capture,
@@ -253,10 +281,11 @@ int mk2_layer_launch(const mk2_layer_args* args, mk2_stream_t stream);
  * on holds until the process ends.  A shape whose mk2_layer_workspace_bytes exceeds it
  * fails with MK2_ENOSPACE (the configs[4] layer needs about 1.9 MiB a row at context
  * 65536: 60.4 MiB at 32 rows).  Nothing is allocated: each call enqueues a small fill
- * kernel that clears the counters and histograms a launch needs zero (the array keeps
- * the last call's other contents), then the launch.  Every call on one GPU shares that
- * GPU's array, so calls that overlap on one GPU (other streams, other host threads)
- * race; calls ordered on one stream do not. */
+ * kernel that clears the counters and histograms a launch needs zero and every region
+ * of tagged hand-off words (the array keeps the last call's other contents, and calls
+ * of different shapes lay their regions over each other's), then the launch.  Every
+ * call on one GPU shares that GPU's array, so calls that overlap on one GPU (other
+ * streams, other host threads) race; calls ordered on one stream do not. */
 #define MK2_LAYER_STATIC_SCRATCH_BYTES ((size_t)64 << 20)
 int mk2_layer_launch_static(const mk2_layer_args* args, mk2_stream_t stream);
 

@@ -32,6 +32,7 @@ struct LayerPlan {
   MlaDev mla;
   MoeDev moe;
   int* sync;
+  size_t moe_off;  // the MoE block's workspace, bytes from the layer workspace's start
 };
 
 // validate the three blocks against each other and carve one workspace for all
@@ -66,6 +67,7 @@ int layer_plan(const mk2_layer_args* a, void* ws, LayerPlan* L, size_t* bytes) {
   char* p_idx = c.take<char>(b_idx);
   char* p_mla = c.take<char>(b_mla);
   char* p_moe = c.take<char>(b_moe);
+  L->moe_off = c.used - b_moe;
   bf16_t* attn = c.take<bf16_t>((size_t)ms.rows * ms.hidden);
   uint64_t* tlist = c.take<uint64_t>((size_t)is.rows * is.topk);  // the list as tagged words
   *bytes = c.bytes();
@@ -120,16 +122,24 @@ static int static_scratch(void** out) {
 
 // zero what a launch needs zero on entry: the persistent launch's counters (not its
 // epoch: the tags of the next launch must differ from those of every earlier launch
-// on the array, whatever shape they had) and the indexer's histograms, chunk counts
-// and ticket (a fill kernel, so that a captured graph holds no memset node)
+// on the array, whatever shape they had), the indexer's histograms, chunk counts and
+// ticket, and every region of tagged words (the top-k list, the router's partial
+// logits, the routing's picks, expert list and row masks).  The array is shared by
+// calls of every shape, so a tagged region may lie on bytes that another layout left
+// as plain data whose upper half happens to equal this launch's tag; cleared, a word
+// matches only once its producer wrote it.  A fill kernel, so that a captured graph
+// holds no memset node.
 struct ZeroSpan {
   int* p;
   int n;
 };
-__global__ __launch_bounds__(256) void k_layer_zero(ZeroSpan a, ZeroSpan b, ZeroSpan c, ZeroSpan d, ZeroSpan e) {
-  const ZeroSpan sp[5] = {a, b, c, d, e};
-  for (int s = 0; s < 5; ++s)
-    for (int i = blockIdx.x * 256 + threadIdx.x; i < sp[s].n; i += gridDim.x * 256) sp[s].p[i] = 0;
+constexpr int ZERO_SPANS = 10;
+struct ZeroSpans {
+  ZeroSpan s[ZERO_SPANS];
+};
+__global__ __launch_bounds__(256) void k_layer_zero(ZeroSpans a) {
+  for (int s = 0; s < ZERO_SPANS; ++s)
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < a.s[s].n; i += gridDim.x * 256) a.s[s].p[i] = 0;
 }
 
 }  // namespace mk2
@@ -155,9 +165,14 @@ extern "C" int mk2_layer_launch_static(const mk2_layer_args* a, mk2_stream_t str
   if (rc) return rc;
   hipStream_t st = (hipStream_t)stream;
   const IdxDev& x = L.idx;
-  k_layer_zero<<<64, 256, 0, st>>>(ZeroSpan{L.sync, SYNC_EPOCH}, ZeroSpan{x.hist, x.rows * IDX_BINS},
-                                   ZeroSpan{x.chist, x.rows * IDX_CBINS}, ZeroSpan{x.ccount, x.rows * x.nchk},
-                                   ZeroSpan{x.ticket, 1});
+  const MoeDev& m = L.moe;
+  auto words = [](uint64_t* p, size_t n) { return ZeroSpan{(int*)p, (int)(2 * n)}; };
+  const ZeroSpans z{{ZeroSpan{L.sync, SYNC_EPOCH}, ZeroSpan{x.hist, x.rows * IDX_BINS},
+                     ZeroSpan{x.chist, x.rows * IDX_CBINS}, ZeroSpan{x.ccount, x.rows * x.nchk},
+                     ZeroSpan{x.ticket, 1}, words(x.tlist, (size_t)x.rows * x.topk),
+                     words(m.logit_part, (size_t)m.KC * m.M * m.E), words(m.act, (size_t)1 + m.Dmax),
+                     words(m.act_rows, (size_t)m.Dmax), words(m.picks, (size_t)m.M * m.topk * 2)}};
+  k_layer_zero<<<64, 256, 0, st>>>(z);
   rc = check_launch("layer (static scratch): clear");
   if (rc) return rc;
   if (a->mode == MK2_LAYER_PERSISTENT)
@@ -173,6 +188,17 @@ extern "C" int mk2_layer_workspace_bytes(const mk2_layer_args* a, size_t* bytes)
   MK2_REQUIRE(bytes != nullptr, "layer: bytes is NULL");
   LayerPlan L;
   return layer_plan(a, nullptr, &L, bytes);
+}
+
+extern "C" int mk2_layer_workspace_layout(const mk2_layer_args* a, int64_t* moe_offset) {
+  clear_error();
+  MK2_REQUIRE(moe_offset != nullptr, "layer: moe_offset is NULL");
+  LayerPlan L;
+  size_t bytes = 0;
+  const int rc = layer_plan(a, nullptr, &L, &bytes);
+  if (rc) return rc;
+  *moe_offset = (int64_t)L.moe_off;
+  return MK2_OK;
 }
 
 extern "C" int mk2_layer_launch(const mk2_layer_args* a, mk2_stream_t stream) {

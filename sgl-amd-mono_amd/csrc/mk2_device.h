@@ -312,8 +312,11 @@ MK2_DEV void drain_memory() { __builtin_amdgcn_s_waitcnt(0); }
 // with the launch's tag in the same 8-byte word, (tag << 32) | value, stored
 // device-coherently.  The consumer polls the word itself until it carries its
 // launch's tag: one memory round trip, with no store drain on the producer, no
-// counter and no second load.  Tags grow by one a launch and are never 0, so a word
-// an earlier launch left, or a zero-filled one, never matches.  Between stream-ordered
+// counter and no second load.  Tags grow by one a launch and are never 0, so on a
+// workspace whose tagged regions hold only tagged words of earlier launches (a
+// workspace zero-filled before its first launch and used for one shape) a stale word
+// never matches; where the regions may hold other bytes (a scratch array shared by
+// shapes whose layouts differ) the caller clears them before each launch.  Between stream-ordered
 // kernels (one kernel a stage) the stream publishes the words: tag 0, read unchecked.
 struct TagPoll {
   uint32_t tag;  // this launch's tag; 0: stream-ordered, no checking

@@ -171,6 +171,35 @@ extern "C" int mk2_moe_workspace_bytes(const mk2_moe_shape* shape, size_t* bytes
   return MK2_OK;
 }
 
+extern "C" int mk2_moe_workspace_layout(const mk2_moe_shape* shape, mk2_moe_ws_layout* out) {
+  clear_error();
+  int rc = moe_check_shape(shape);
+  if (rc) return rc;
+  MK2_REQUIRE(out != nullptr, "moe: layout is NULL");
+  // carve at a stand-in base and report offsets from it (nothing is dereferenced)
+  char* const base = (char*)(uintptr_t)4096;
+  MoeDev d{};
+  d.fmt = shape->expert_fmt;
+  moe_carve(shape, base, &d);
+  auto off = [&](const void* p) -> int64_t { return p ? (int64_t)((const char*)p - base) : -1; };
+  const int fmt = shape->expert_fmt;
+  const bool q = fmt == MK2_FMT_MXFP4 || fmt == MK2_FMT_W8A8 || fmt == MK2_FMT_A4W4;
+  out->xn = off(d.xn);
+  out->xq = q ? off(d.xq) : -1;
+  out->xs = fmt == MK2_FMT_MXFP4 || fmt == MK2_FMT_A4W4 ? off(d.xs) : -1;
+  out->xsf = fmt == MK2_FMT_W8A8 ? off(d.xsf) : -1;
+  out->act = off(d.act);
+  out->mid_q = off(d.mid_q);
+  out->mid_s = off(d.mid_s);
+  out->mid_sf = off(d.mid_sf);
+  out->mid_b = off(d.mid_b);
+  out->mid_sh = shape->n_shared ? off(d.mid_sh) : -1;
+  out->dmax = d.Dmax;
+  d.M = shape->rows;
+  out->compact = compact_rows(d) ? 1 : 0;
+  return MK2_OK;
+}
+
 extern "C" int mk2_moe_launch(const mk2_moe_args* a, mk2_stream_t stream) {
   clear_error();
   MK2_REQUIRE(a != nullptr, "moe: args is NULL");

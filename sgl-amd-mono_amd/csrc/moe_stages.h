@@ -599,9 +599,10 @@ MK2_DEV bool moe_route(const MoeDev& p, RouteLds& L, const TagPoll& tp, Mark mar
         const int j = i >> 1;
         if (i & 1) {
           L.w[j] = __uint_as_float(pair_value(w));
-        } else {
-          L.ids[j] = (int)pair_value(w);
-          L.flag[pair_value(w)] = 1;
+        } else {  // an id out of range (never written by a pick task) flags nothing
+          const uint32_t e = pair_value(w);
+          L.ids[j] = e < (uint32_t)p.E ? (int)e : 0;
+          if (e < (uint32_t)p.E) L.flag[e] = 1;
         }
       }
     }

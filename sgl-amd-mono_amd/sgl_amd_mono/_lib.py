@@ -55,6 +55,14 @@ class MoeArgs(ctypes.Structure):
     ]
 
 
+class MoeWsLayout(ctypes.Structure):
+    _fields_ = [
+        ("xn", c_int64), ("xq", c_int64), ("xs", c_int64), ("xsf", c_int64), ("act", c_int64),
+        ("mid_q", c_int64), ("mid_s", c_int64), ("mid_sf", c_int64), ("mid_b", c_int64), ("mid_sh", c_int64),
+        ("dmax", c_int), ("compact", c_int),
+    ]
+
+
 class IndexerShape(ctypes.Structure):
     _fields_ = [
         ("rows", c_int), ("heads", c_int), ("dim", c_int), ("topk", c_int),
@@ -154,12 +162,14 @@ class StepArgs(ctypes.Structure):
 SIGNATURES = {
     "mk2_moe_workspace_bytes": [POINTER(MoeShape), POINTER(c_size_t)],
     "mk2_moe_launch": [POINTER(MoeArgs), c_void_p],
+    "mk2_moe_workspace_layout": [POINTER(MoeShape), POINTER(MoeWsLayout)],
     "mk2_indexer_workspace_bytes": [POINTER(IndexerShape), POINTER(c_size_t)],
     "mk2_indexer_topk_launch": [POINTER(IndexerArgs), c_void_p],
     "mk2_mla_workspace_bytes": [POINTER(MlaShape), POINTER(c_size_t)],
     "mk2_sparse_mla_launch": [POINTER(MlaArgs), c_void_p],
     "mk2_layer_workspace_bytes": [POINTER(LayerArgs), POINTER(c_size_t)],
     "mk2_layer_launch": [POINTER(LayerArgs), c_void_p],
+    "mk2_layer_workspace_layout": [POINTER(LayerArgs), POINTER(c_int64)],
     "mk2_layer_launch_static": [POINTER(LayerArgs), c_void_p],
     "mk2_tail_launch": [POINTER(TailArgs), c_void_p],
     "mk2_front_workspace_bytes": [POINTER(FrontShape), POINTER(c_size_t)],

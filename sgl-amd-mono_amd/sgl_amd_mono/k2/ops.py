@@ -32,6 +32,43 @@ def _p(t):
     return None if t is None else t.data_ptr()
 
 
+def moe_activation_views(shape, workspace, base: int = 0) -> dict:
+    """Views of what the last launch on `workspace` left of the MoE block's activations
+    (mk2_moe_workspace_layout; the MoE workspace starts `base` bytes in): xn bf16
+    [M, H]; the mode's xq / xs / xsf codes and scales; act (the distinct experts, by
+    slot); mid_q / mid_s / mid_sf or mid_b [dmax, M, ...] and mid_sh.  For checking the
+    device quantizers; the views alias the workspace (clone before the next launch)."""
+    lay = _lib.MoeWsLayout()
+    _lib.check(_lib.lib().mk2_moe_workspace_layout(ctypes.byref(shape), ctypes.byref(lay)))
+    M, H, I, SI, D = shape.rows, shape.hidden, shape.inter, shape.shared_inter, lay.dmax
+    fp4 = shape.expert_fmt == C.FMT_A4W4
+
+    def view(off, dtype, shp):
+        if off < 0:
+            return None
+        n = 1
+        for d in shp:
+            n *= d
+        nb = n * torch.empty((), dtype=dtype).element_size()
+        return workspace[base + off: base + off + nb].view(dtype).view(*shp)
+
+    out = {
+        "xn": view(lay.xn, torch.bfloat16, (M, H)),
+        "xq": view(lay.xq, torch.uint8, (M, H // 2 if fp4 else H)),
+        "xs": view(lay.xs, torch.uint8, (M, H // 32)),
+        "xsf": view(lay.xsf, torch.float32, (M, H // 128)),
+        "mid_q": view(lay.mid_q, torch.uint8, (D, M, I // 2 if fp4 else I)),
+        "mid_s": view(lay.mid_s, torch.uint8, (D, M, I // 32)),
+        "mid_sf": view(lay.mid_sf, torch.float32, (D, M, I // 128)),
+        "mid_b": view(lay.mid_b, torch.bfloat16, (D, M, I)),
+        "mid_sh": view(lay.mid_sh, torch.bfloat16, (M, SI)) if shape.n_shared else None,
+        "compact": bool(lay.compact),
+    }
+    act = view(lay.act, torch.int64, (1 + D,)).cpu() & 0xFFFFFFFF
+    out["act"] = act[1: 1 + int(act[0])].clone()
+    return out
+
+
 class MoEOp:
     """The MoE block of one layer (router -> top-k -> routed + shared experts)."""
 
@@ -67,6 +104,10 @@ class MoEOp:
         )
         _lib.check(_lib.lib().mk2_moe_launch(ctypes.byref(args), _lib.stream_handle(self.device)))
         return out
+
+    def activations(self) -> dict:
+        """What the last launch left of the activations (moe_activation_views)."""
+        return moe_activation_views(self.shape, self.workspace)
 
 
 class IndexerOp:
@@ -156,8 +197,13 @@ class FrontOp:
     def status(self) -> int:
         """The persistent launches' sticky status word (nonzero: a dependency wait ran
         out of its spin limit; that launch's outputs are undefined).  Synchronizes."""
+        return int(self.status_word().item())
+
+    def status_word(self):
+        """The persistent launches' sticky status word, a device view (int32 [1]) into
+        the workspace: read it without a host sync, or clear it with zero_()."""
         off = _lib.MK2_FRONT_STATUS_OFFSET
-        return int(self.workspace[off:off + 4].view(torch.int32).item())
+        return self.workspace[off:off + 4].view(torch.int32)
 
     def _make_args(self, x, positions, slots, rope_cos_sin, kv_cache, kv_scale, index_cache, index_scale,
                    mla_q=None, index_q=None, index_w=None):
@@ -389,6 +435,16 @@ class LayerOp:
         launch = _lib.lib().mk2_layer_launch_static if self.static_scratch else _lib.lib().mk2_layer_launch
         _lib.check(launch(ctypes.byref(args), _lib.stream_handle(self.device)))
         return out
+
+    def moe_activations(self) -> dict:
+        """What the last launch left of the MoE block's activations in this op's
+        workspace (moe_activation_views; mk2_layer_workspace_layout places the block)."""
+        if self.workspace is None:
+            raise ValueError("a static-scratch op has no workspace of its own to read")
+        off = ctypes.c_int64()
+        _lib.check(_lib.lib().mk2_layer_workspace_layout(ctypes.byref(self._make_args(workspace=self.workspace)),
+                                                         ctypes.byref(off)))
+        return moe_activation_views(self.moe.shape, self.workspace, off.value)
 
     def check(self) -> None:
         """Raises RuntimeError if a launch of this op stopped early since the last check

@@ -74,6 +74,19 @@ def test_layer_small_context_32_rows():
     print(stats)
 
 
+def test_layer_verify_width_full_context():
+    """configs[4] at the verify width, 32 rows over the full 65536-position context,
+    against the oracle: there the persistent launch runs the top-k selects as tasks of
+    their own (32 rows x 32 chunks exceed the workgroups) and each workgroup keeps
+    several score chunks in LDS for its slices."""
+    from sgl_amd_mono.k2 import config as C
+
+    L, res, olat = run_layer(C.C5_LAYER, 32, seed=533)
+    stats = check_layer(L, *res, o_latent=olat)
+    assert stats["attn_term_checked"] and stats["moe_term_checked"]
+    print(stats)
+
+
 @pytest.mark.parametrize("fmt", ["W8A8", "A16W4", "A4W4"])
 def test_layer_expert_modes(fmt):
     """The persistent layer with each further expert mode in the MoE stages."""

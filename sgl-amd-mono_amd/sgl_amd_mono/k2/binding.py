@@ -90,16 +90,21 @@ def _uk_uv(attn, heads: int, nope: int, kv_lora: int, v_dim: int):
     """W_UK as the front reads it, bf16 [heads][kv_lora][nope], and W_UV as the
     attention reads it, bf16 [heads][v][kv_lora]: SGLang's w_kc [heads, nope, kv_lora]
     and w_vc [heads, kv_lora, v] transposed -- views of its memory when that is
-    already this order, else copies; per-tensor FP8 is dequantized by w_scale
-    (weights.py:347-393)."""
+    already this order, else copies.  Per-tensor FP8 needs its scalar w_scale, as the
+    reference requires (weights.py:347-393), and is widened to bf16(e4m3 * w_scale)
+    once at bind time: the attention's MFMAs run on bf16 W_UK / W_UV, so each weight
+    carries one bf16 rounding the reference's FP8 path does not (within the layer's
+    rel-L2 tolerance; not pinned against an FP8-weight reference)."""
     w_kc, w_vc = attn.w_kc, attn.w_vc
     _need("w_kc", w_kc, (heads, nope, kv_lora), (torch.bfloat16, torch.float8_e4m3fn))
     _need("w_vc", w_vc, (heads, kv_lora, v_dim), (torch.bfloat16, torch.float8_e4m3fn))
     out = []
     for t in (w_kc.transpose(1, 2), w_vc.transpose(1, 2)):
         if t.dtype == torch.float8_e4m3fn:
-            scale = float(getattr(attn, "w_scale", 1.0))
-            t = (t.float() * scale).to(torch.bfloat16)
+            ws = getattr(attn, "w_scale", None)
+            if not torch.is_tensor(ws) or ws.numel() != 1:
+                raise ValueError("FP8 w_kc / w_vc need the layer's w_scale as a 1-element tensor")
+            t = (t.float() * ws.float().reshape(())).to(torch.bfloat16)
         out.append(t if t.is_contiguous() else t.contiguous())
     return out
 

@@ -131,7 +131,13 @@ class K2Forward:
         self.max_position = front_cfg.max_position
         self.pool_of = pool_of or _sglang_pool
         self.page_table_of = page_table_of or _sglang_page_table
-        self._ops, self._steps, self._tails = {}, {}, {}
+        self._ops, self._steps, self._tails, self._tables = {}, {}, {}, {}
+        # one sticky status word for every layer launch of a step (a persistent launch
+        # whose dependency wait gave up ORs 1 into it; the fronts keep theirs in their
+        # workspaces): a stopped launch's outputs are undefined, so a step with any
+        # word set returns NaN logits and, on the eager path, raises (the reference's
+        # guard stops visibly, common/guard.py:91-97,211-227)
+        self._status = torch.zeros(1, dtype=torch.int32, device=device)
         # the logits processor returns the tail's logits on a routed step (the reference
         # hooks _get_logits the same way, glm53/spec.py:423-441)
         lp = getattr(lm, "logits_processor", None)
@@ -145,26 +151,39 @@ class K2Forward:
             return self._own_logits(hidden_states, lm_head, logits_metadata, *args, **kwargs)
         return self._logits[: hidden_states.shape[0]]
 
-    def ops(self, li: int, rows: int, table_stride: int, kv=None, icache=None):
+    def tables(self, rows: int):
+        """The row tables every layer op of width `rows` reads: one page table of the
+        widest context (max_position + 1 tokens), into which a step copies SGLang's
+        rows once; req_ids and ctx_len are the step rows' own tensors (filled in place
+        by the step-table launch).  Shared by all layers, so a step copies nothing per
+        layer and the ops do not depend on the width of SGLang's table."""
+        if rows not in self._tables:
+            st = self.step_rows(rows)
+            pages = (self.max_position + 64) // 64
+            pt = torch.zeros(rows, pages, dtype=torch.int32, device=self.device)
+            self._tables[rows] = SimpleNamespace(page_table=pt, req_ids=st.req_ids, ctx_len=st.ctx_len)
+        return self._tables[rows]
+
+    def ops(self, li: int, rows: int, kv=None, icache=None):
         """(FrontOp, LayerOp) of layer li at `rows` rows, created on first use with the
-        layer's caches (kv, icache); the layer's input tensors are rebound every step."""
+        layer's caches (kv, icache) and the shared row tables; the layer's input tensors
+        are rebound every step."""
         from .ops import FrontOp, LayerOp
 
-        key = (li, rows, table_stride)
+        key = (li, rows)
         if key not in self._ops:
             dev, cfg, fc = self.device, self.cfg, self.front_cfg
-            pt = torch.zeros(rows, table_stride, dtype=torch.int32, device=dev)
-            i32 = dict(dtype=torch.int32, device=dev)
+            tab = self.tables(rows)
             idx = SimpleNamespace(
                 cfg=cfg.indexer, rows=rows,
                 q=torch.empty(rows, fc.index_heads, 128, dtype=torch.bfloat16, device=dev),
                 w=torch.empty(rows, fc.index_heads, dtype=torch.bfloat16, device=dev),
-                cache=icache, cache_scale=None, page_table=pt, req_ids=torch.zeros(rows, **i32),
-                ctx_len=torch.zeros(rows, **i32))
+                cache=icache, cache_scale=None, page_table=tab.page_table, req_ids=tab.req_ids,
+                ctx_len=tab.ctx_len)
             mla = SimpleNamespace(**vars(self.mlas[li]))
             mla.rows = rows
             mla.q = torch.empty(rows, fc.heads, fc.kv_lora + fc.rope, dtype=torch.bfloat16, device=dev)
-            mla.kv, mla.kv_scale, mla.page_table, mla.req_ids = kv, None, pt, idx.req_ids
+            mla.kv, mla.kv_scale, mla.page_table, mla.req_ids = kv, None, tab.page_table, tab.req_ids
             L = SimpleNamespace(cfg=cfg, rows=rows, idx=idx, mla=mla, moe=self.moes[li],
                                 h=torch.empty(rows, cfg.mla.hidden, dtype=torch.bfloat16, device=dev))
             self._ops[key] = (FrontOp(fc, self.fronts[li], rows, device=dev), LayerOp(cfg, L, rows, device=dev))
@@ -184,8 +203,15 @@ class K2Forward:
             self._tails[rows] = TailOp(self.tail_cfg, self.g_norm, self.w_head, rows, device=self.device)
         return self._tails[rows]
 
+    def status_words(self, rows: int) -> list:
+        """The device status words of a step at `rows` rows: the layers' shared word and
+        every front's (a 1-element int32 view each)."""
+        return [self._status] + [self._ops[(li, rows)][0].status_word() for li in range(len(self.fronts))
+                                 if (li, rows) in self._ops]
+
     def backbone(self, plan, input_ids, positions, forward_batch):
-        """Every layer a front and a layer launch, then the tail: (normed rows, logits)."""
+        """Every layer a front and a layer launch, then the tail: (normed rows, logits).
+        The logits are NaN when any launch of the step stopped early (gate_logits)."""
         accepts = getattr(SPEC, "accepts", None)  # SGLang routes by the spec itself
         if accepts is not None:
             ok, why = accepts(plan.key)
@@ -194,35 +220,63 @@ class K2Forward:
         S = plan.key.batch_size * plan.key.tokens_per_request
         st = self.step_rows(S)(forward_batch.out_cache_loc, positions, S, self.max_position, ids_in=input_ids)
         pt = self.page_table_of(forward_batch, S)
+        tab = self.tables(S)
+        w = min(pt.shape[1], tab.page_table.shape[1])
+        tab.page_table[:, :w].copy_(pt[:S, :w])  # once a step, for every layer
         pool = self.pool_of(forward_batch)
         from . import binding
 
         h = torch.nn.functional.embedding(input_ids[:S].long(), self.emb)
         for li in range(len(self.fronts)):
             kv, icache = binding.layer_caches(pool, li, self.front_cfg.index_heads > 0)
-            fo, lo = self.ops(li, S, pt.shape[1], kv, icache)
+            fo, lo = self.ops(li, S, kv, icache)
             L = lo.L
             fo(h, st.positions, st.slots, self.cos_sin, kv, None, icache, None,
                mla_q=L.mla.q, index_q=L.idx.q, index_w=L.idx.w)
-            L.idx.page_table.copy_(pt[:S])
-            L.idx.req_ids.copy_(st.req_ids)
-            L.idx.ctx_len.copy_(st.ctx_len)
             L.idx.cache, L.mla.kv, L.h = icache, kv, h
-            h = lo(out=plan.state.setdefault(("h", li % 2, S), torch.empty_like(h)))
+            h = lo(out=plan.state.setdefault(("h", li % 2, S), torch.empty_like(h)), status=self._status)
         logits, normed = self.tail(S)(h)
+        gate_logits(self.status_words(S), logits)
         return normed, logits
+
+    def check(self, rows: int) -> None:
+        """Raises RuntimeError when a launch of a step at `rows` rows stopped early since
+        the last check, and clears the words (synchronizes; raise_if_stopped)."""
+        raise_if_stopped(self.status_words(rows))
 
     def forward(self, plan, input_ids, positions, forward_batch, input_embeds=None, pp_proxy_tensors=None):
         """DeepseekV2ForCausalLM.forward for a routed decode or verify step; with input
-        embeddings, SGLang's own forward (as the reference, glm53/spec.py:443-461)."""
+        embeddings, SGLang's own forward (as the reference, glm53/spec.py:443-461).  On
+        the eager path a step whose launch stopped early raises instead of returning
+        logits; under graph capture its logits are NaN (no host read is possible)."""
         lm = self.lm
         if input_embeds is not None:
             return type(lm).forward(lm, input_ids, positions, forward_batch, input_embeds, pp_proxy_tensors)
         normed, self._logits = self.backbone(plan, input_ids, positions, forward_batch)
         try:
+            if not torch.cuda.is_current_stream_capturing():
+                self.check(plan.key.batch_size * plan.key.tokens_per_request)
             return lm.logits_processor(input_ids, normed, lm.lm_head, forward_batch, None)
         finally:
             self._logits = None
+
+
+def gate_logits(status_words, logits) -> None:
+    """logits := NaN where any status word is nonzero, on the device (no host read, so a
+    captured step carries it too): a stopped launch's output never becomes a token."""
+    bad = torch.stack([w.reshape(()) for w in status_words]).ne(0).any()
+    logits.masked_fill_(bad, float("nan"))
+
+
+def raise_if_stopped(status_words) -> None:
+    """Reads the status words (a host read); if any is set, clears them all and raises
+    RuntimeError: a launch of the step stopped early and its outputs are undefined."""
+    vals = [int(w.reshape(()).item()) for w in status_words]
+    if any(vals):
+        for w in status_words:
+            w.zero_()
+        raise RuntimeError(f"K2 step: a persistent launch stopped early (a dependency wait gave up; status words "
+                           f"{vals}); its outputs are not valid")
 
 
 def _sglang_pool(forward_batch):

@@ -177,3 +177,25 @@ def test_mxfp4_experts_in_both_layouts():
     assert a.ws13_p.data_ptr() == shf.mlp.shared_experts.gate_up_proj.weight.data_ptr()
     assert torch.equal(a.ws13_p, aiter_shuffle(sh.gate_up_proj.weight.view(torch.uint8)))
     assert t.ws13s.data_ptr() == sh.gate_up_proj.weight_scale_inv.data_ptr()
+
+
+def test_fp8_uk_uv_need_their_scale():
+    """Per-tensor FP8 w_kc / w_vc are widened by the layer's scalar w_scale; without one
+    (or with a non-scalar one) binding refuses, as the reference does."""
+    from types import SimpleNamespace
+
+    from sgl_amd_mono.k2 import binding
+
+    g = torch.Generator().manual_seed(5)
+    kc = (torch.randn(2, 8, 16, generator=g) * 4).to(torch.float8_e4m3fn)
+    vc = (torch.randn(2, 16, 8, generator=g) * 4).to(torch.float8_e4m3fn)
+    attn = SimpleNamespace(w_kc=kc, w_vc=vc)
+    with pytest.raises(ValueError, match="w_scale"):
+        binding._uk_uv(attn, 2, 8, 16, 8)
+    attn.w_scale = torch.tensor([0.5, 0.5])
+    with pytest.raises(ValueError, match="w_scale"):
+        binding._uk_uv(attn, 2, 8, 16, 8)
+    attn.w_scale = torch.tensor(0.25)
+    uk, uv = binding._uk_uv(attn, 2, 8, 16, 8)
+    assert torch.equal(uk.float(), (kc.float() * 0.25).bfloat16().float().transpose(1, 2))
+    assert torch.equal(uv.float(), (vc.float() * 0.25).bfloat16().float().transpose(1, 2))

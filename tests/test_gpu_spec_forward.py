@@ -53,7 +53,7 @@ def test_routed_decode_step(rows):
         assert set(pages_moved.tolist()) <= set((loc // 64).tolist())
     # the last layer again, with its checking outputs, against the oracle
     li = F.LAYERS - 1
-    fo, lo = fwd.ops(li, rows, st.page_table.shape[1])
+    fo, lo = fwd.ops(li, rows)
     L, cfg = lo.L, lo.cfg
     H, E, K = cfg.mla.hidden, cfg.moe.n_experts, cfg.moe.top_k
     attn = torch.empty(rows, H, dtype=torch.bfloat16, device=dev)
@@ -104,3 +104,38 @@ def test_shuffled_experts_step_matches_row_major(experts):
         res.append((cpu(logits), [cpu(t) for t in pool.kv]))
     assert torch.equal(res[0][0], res[1][0])
     assert all(torch.equal(a, b) for a, b in zip(res[0][1], res[1][1]))
+
+
+def test_stopped_layer_gives_no_token():
+    """A layer launch that stops early (its dependency wait given a spin limit of one
+    poll, so it gives up from the host's setting and every kernel exits normally) makes
+    the step's logits NaN and the eager forward raise; once the words are cleared, the
+    next step runs clean on the same ops and workspaces."""
+    from sgl_amd_mono import _registry as reg
+    from sgl_amd_mono.k2 import spec
+
+    dev = _dev()
+    rows = 4
+    pages = rows * (F.HF.max_context // 64) + 8
+    lm = F.make_model(31, dev)
+    pool = F.Pool(F.LAYERS, pages, dev, 32)
+    st = F.make_step(rows, F.HF.max_context, pages, dev, 33)
+    ctx = SimpleNamespace(device=dev, pool_of=lambda fb: pool, page_table_of=lambda fb, n: st.page_table[:n])
+    fwd = spec.SPEC.build(lm, F.HF, ctx)
+    plan = reg.Plan(key=reg.ShapeKey("decode", rows, 1))
+    fwd.forward(plan, st.input_ids, st.positions, st.forward_batch)  # builds the ops; a clean step
+    torch.cuda.synchronize()
+    _, lo = fwd.ops(1, rows)
+    lo.spin_limit = 1
+    _, logits = fwd.backbone(plan, st.input_ids, st.positions, st.forward_batch)
+    torch.cuda.synchronize()
+    assert int(fwd._status.item()) == 1
+    assert bool(torch.isnan(logits).all())
+    with pytest.raises(RuntimeError, match="stopped early"):
+        fwd.check(rows)  # clears the words
+    with pytest.raises(RuntimeError, match="stopped early"):
+        fwd.forward(plan, st.input_ids, st.positions, st.forward_batch)
+    lo.spin_limit = 0
+    logits = fwd.forward(plan, st.input_ids, st.positions, st.forward_batch)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(logits).all())

@@ -74,3 +74,26 @@ def test_config_from_hf_is_configs4():
     cfg = spec.config_from_hf(GLM5_LIKE)
     assert cfg.moe == C.C2_MOE
     assert cfg.mla == C.C5_LAYER.mla and cfg.indexer == C.C5_LAYER.indexer
+
+
+def test_stopped_step_gives_nan_logits_and_raises():
+    """A step whose status words (the layers' shared word, each front's) show a stopped
+    launch: the logits become NaN on the device, and the host check raises and clears
+    every word; clean words leave the logits and pass the check."""
+    import torch
+
+    from sgl_amd_mono.k2 import spec
+
+    words = [torch.zeros(1, dtype=torch.int32) for _ in range(3)]
+    logits = torch.randn(4, 16)
+    want = logits.clone()
+    spec.gate_logits(words, logits)
+    assert torch.equal(logits, want)
+    spec.raise_if_stopped(words)
+    words[2][0] = 1  # one front stopped
+    spec.gate_logits(words, logits)
+    assert bool(torch.isnan(logits).all())
+    with pytest.raises(RuntimeError, match="stopped early"):
+        spec.raise_if_stopped(words)
+    assert all(int(w.item()) == 0 for w in words)
+    spec.raise_if_stopped(words)

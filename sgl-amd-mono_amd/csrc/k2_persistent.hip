@@ -64,8 +64,12 @@ struct K2Dev {
 // then the routing's marks: logits polled, top-k done, list out
 constexpr int K2_STAGES = 10, K2_STAMPS = 3 * K2_STAGES + 3;
 
+// The stamps collect in LDS (thread 0 takes them all) and go out once the walk is done:
+// a store to memory per stamp would make thread 0's wave wait for its outstanding loads
+// and stores at every stamp and move the times it measures.
+__shared__ uint64_t k2_lds_stamps[K2_STAMPS];
 MK2_DEV void k2_stamp(const K2Dev& p, int i) {
-  if (p.timeline && threadIdx.x == 0) p.timeline[(size_t)blockIdx.x * K2_STAMPS + i] = __builtin_amdgcn_s_memrealtime();
+  if (p.timeline && threadIdx.x == 0) k2_lds_stamps[i] = __builtin_amdgcn_s_memrealtime();
 }
 
 union K2Lds {
@@ -149,8 +153,7 @@ MK2_DEV bool k2_wait(const K2Dev& p, int* seen, int line, int target, int stamp 
         break;
       }
     }
-    if (lane == 0 && stamp >= 0 && p.timeline)
-      p.timeline[(size_t)blockIdx.x * K2_STAMPS + stamp] = __builtin_amdgcn_s_memrealtime();
+    if (lane == 0 && stamp >= 0 && p.timeline) k2_lds_stamps[stamp] = __builtin_amdgcn_s_memrealtime();
     if (lane == 0) seen[SY_LINES] = bad;  // the workgroup's fail-stop flag
   }
   __syncthreads();
@@ -193,14 +196,16 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p, Front front) {
   const int G = gridDim.x, b = blockIdx.x;
   const int R = p.rows;
   for (int i = threadIdx.x; i <= SY_LINES; i += K2_NT) seen[i] = 0;
+  if (p.timeline && threadIdx.x < K2_STAMPS) k2_lds_stamps[threadIdx.x] = 0;
   // this launch's tag: one past the epoch the previous launch on this workspace left
-  // (never 0; a zero-filled workspace starts at 1)
-  if (threadIdx.x == 0) {
-    const uint32_t e = (uint32_t)ld_dev_i32(p.sync + SYNC_EPOCH) + 1u;
-    s_tag = e ? e : 1u;
-  }
+  // (never 0; a zero-filled workspace starts at 1).  The epoch's load is issued here and
+  // its value taken only after the scores, which use no tag: its round trip overlaps
+  // the scores' own loads instead of holding the launch's start
+  uint32_t epoch = 0;
+  if (threadIdx.x == 0) epoch = (uint32_t)ld_dev_i32(p.sync + SYNC_EPOCH);
+  auto tag_of = [](uint32_t e) { return e + 1u ? e + 1u : 1u; };
   __syncthreads();
-  const TagPoll tp{s_tag, p.spin_limit, k2_ctr(p, SY_ERR)};
+  TagPoll tp{0u, p.spin_limit, k2_ctr(p, SY_ERR)};
   // the stages in order; a wait that fails (its spin limit, or another workgroup's
   // failure seen while polling) returns from the walk: the workgroup skips every task
   // left and goes straight to the counter reset (fail-stop)
@@ -219,6 +224,9 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p, Front front) {
       k2_signal(p, SY_SCORE + t / nchk);
     }
     k2_stamp(p, 3 * st++ + 2);
+    if (threadIdx.x == 0) s_tag = tag_of(epoch);
+    __syncthreads();
+    tp.tag = s_tag;
     // ---- top-k slices: each chunk lists its keys above the row's threshold bin and
     // keeps its keys in the bin
     k2_stamp(p, 3 * st);
@@ -228,8 +236,11 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p, Front front) {
     // then finishes the row's list from the keys in the threshold bin, while the others
     // still list theirs.  With several a workgroup the selects are tasks of their own
     // after the slices: a workgroup that won one row would start its next slice late,
-    // be the last of that row too, and run every round's select in turn
+    // be the last of that row too, and run every round's select in turn.  A select's
+    // workgroup clears the row's histograms later, where it waits for the routing
+    // anyway (sel_rows: the rows it selected, a bit each)
     const bool sel_tasks = R * nchk > G;
+    uint32_t sel_rows = 0;
     K2_TASKS(t, R * nchk) {
       const int r = t / nchk;
       if (!k2_wait(p, seen, SY_SCORE + r, nchk, t < G ? 3 * st + 1 : -1)) return;
@@ -248,9 +259,7 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p, Front front) {
         // this workgroup's own slice of row r may have left the threshold in LDS
         idx_select<K2_NT>(p.idx, r, S.topk, tp.tag, known);
         k2_stamp(p, 3 * (st + 1) + 2);
-        // every slice read the threshold before it counted out; the chunk counts are
-        // cleared by the last workgroup out (slices may still poll them here)
-        idx_clear_hist<K2_NT>(p.idx, r);
+        sel_rows |= 1u << r;
       }
     }
     k2_stamp(p, 3 * st + 2);
@@ -261,7 +270,7 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p, Front front) {
         if (!k2_wait(p, seen, SY_SLICE + r, nchk, 3 * (st + 1) + 1)) return;
         idx_select<K2_NT>(p.idx, r, S.topk, tp.tag, false);
         k2_stamp(p, 3 * (st + 1) + 2);
-        idx_clear_hist<K2_NT>(p.idx, r);
+        sel_rows |= 1u << r;
       }
       K2_NEXT(R);
     }
@@ -355,6 +364,10 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p, Front front) {
     // normalized rows, so they run while routing is still pending), then the routed
     // slots, each polling its slot of the tagged expert list
     k2_stamp(p, 3 * st);
+    // the selects' rows' histograms back to zero, here where a workgroup waits for the
+    // routing anyway (every slice and select read them long ago; a stopped launch
+    // leaves this to the last workgroup out)
+    for (uint32_t m = sel_rows; m; m &= m - 1) idx_clear_hist<K2_NT>(p.idx, __ffs((int)m) - 1);
     K2_TASKS(t, up_total) {
       const bool sh = t < up_sh;
       if (!k2_wait(p, seen, SY_ROUTER, nrt, t < G ? 3 * st + 1 : -1, K2_LANES)) return;
@@ -388,6 +401,9 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p, Front front) {
   if (front_ok) walk();
 #undef K2_TASKS
 #undef K2_NEXT
+  __syncthreads();  // thread 0's stamps are in LDS
+  if (p.timeline && threadIdx.x < K2_STAMPS)
+    p.timeline[(size_t)blockIdx.x * K2_STAMPS + threadIdx.x] = k2_lds_stamps[threadIdx.x];
   // ---- the last workgroup out resets the counters for the next launch
   drain_memory();  // this workgroup's stores and atomics have landed before it counts out
   __syncthreads();
@@ -412,7 +428,7 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p, Front front) {
       __hip_atomic_store(k2_ctr(p, l), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     front.reset();
     // the epoch moves on: the next launch's tags differ from every tag of this one
-    if (threadIdx.x == 0) st_dev_i32(p.sync + SYNC_EPOCH, (int)s_tag);
+    if (threadIdx.x == 0) st_dev_i32(p.sync + SYNC_EPOCH, (int)tag_of(epoch));
   }
 }
 

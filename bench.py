@@ -534,7 +534,10 @@ def time_graph(calls, steps=200, warmup=20):
 
 
 def _cpu_time(fn, reps):
-    """Median us of `reps` calls of fn after one warm-up call (the oracle on the host)."""
+    """Median us of `reps` calls of fn after one warm-up call (the oracle on the host);
+    None with reps = 0 (not timed)."""
+    if reps <= 0:
+        return None
     fn()
     times = []
     for _ in range(reps):

@@ -128,6 +128,15 @@ typedef struct mk2_moe_args {
   float* topk_weights;     /* [M][top_k] */
 } mk2_moe_args;
 
+/* The block entry points below (mk2_moe_launch, mk2_indexer_topk_launch,
+ * mk2_sparse_mla_launch) each run their block as ONE persistent launch (one workgroup
+ * a CU, the stages handing off through counters, as the layer's launch does).  Their
+ * workspace is zero-filled before its first launch, and every launch (completed or
+ * stopped) leaves it ready for the next.  The int at byte MK2_BLOCK_STATUS_OFFSET of
+ * the workspace becomes nonzero once a launch's dependency wait ran out of its spin
+ * limit (about a second; that launch's outputs are undefined); only the caller clears
+ * it. */
+#define MK2_BLOCK_STATUS_OFFSET 26624
 int mk2_moe_workspace_bytes(const mk2_moe_shape* shape, size_t* bytes);
 int mk2_moe_launch(const mk2_moe_args* args, mk2_stream_t stream);
 /* Where a launch leaves the MoE block's activations in its workspace: byte offsets
@@ -268,9 +277,9 @@ typedef struct mk2_layer_args {
 
 int mk2_layer_workspace_bytes(const mk2_layer_args* args, size_t* bytes);
 int mk2_layer_launch(const mk2_layer_args* args, mk2_stream_t stream);
-/* The MoE block's part of a layer workspace: *moe_offset = the byte offset of its
- * MoE workspace, whose buffers mk2_moe_workspace_layout(&args->moe.shape) places (the
- * reference's scratch layout, glm53/gfx950/layout.py:181-318). */
+/* The MoE block's part of a layer workspace: its buffers lie at *moe_offset plus the
+ * offsets mk2_moe_workspace_layout(&args->moe.shape) reports (the reference's scratch
+ * layout, glm53/gfx950/layout.py:181-318). */
 int mk2_layer_workspace_layout(const mk2_layer_args* args, int64_t* moe_offset);
 
 /* The same layer launch without a caller workspace: no counterpart in the reference.

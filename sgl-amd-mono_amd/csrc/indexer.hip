@@ -1,7 +1,11 @@
-// Standalone indexer launch (FP4 or FP8 index keys, up to 64 heads x 128): key scores with the
-// row histograms, the candidate slices, then the exact top-k of every row.
+// Indexer launch (FP4 or FP8 index keys, up to 64 heads x 128): key scores with the row
+// histograms, the candidate slices, then the exact top-k of every row -- as one
+// persistent launch (k2_persistent.hip) for mk2_indexer_topk_launch, and as one kernel a
+// stage for the layer's staged mode.
 #include "indexer_stages.h"
+#include "mla_stages.h"
 #include "mk2_host.h"
+#include "moe_stages.h"
 
 namespace mk2 {
 
@@ -101,6 +105,11 @@ int idx_fill(const mk2_indexer_args* a, IdxDev* d) {
   return MK2_OK;
 }
 
+int k2_block_enqueue(int blk, const IdxDev* idx, const MlaDev* mla, const MoeDev* moe, int* sync, int rows,
+                     hipStream_t st);
+constexpr size_t BLOCK_SYNC_BYTES = (size_t)SYNC_INTS * 4;  // the persistent launch's sync block
+
+// the layer's staged mode: one kernel a stage, in stream order
 void idx_enqueue(const IdxDev& d, hipStream_t st) {
   k_idx_clear<<<d.rows * 4, 256, 0, st>>>(d);
   k_idx_score<<<dim3(d.nchk, d.rows), IDX_NT, 0, st>>>(d);
@@ -117,7 +126,7 @@ extern "C" int mk2_indexer_workspace_bytes(const mk2_indexer_shape* shape, size_
   int rc = idx_check_shape(shape);
   if (rc) return rc;
   MK2_REQUIRE(bytes != nullptr, "indexer: bytes is NULL");
-  *bytes = idx_carve(shape, nullptr, nullptr);
+  *bytes = BLOCK_SYNC_BYTES + idx_carve(shape, nullptr, nullptr);
   return MK2_OK;
 }
 
@@ -127,11 +136,10 @@ extern "C" int mk2_indexer_topk_launch(const mk2_indexer_args* a, mk2_stream_t s
   IdxDev d;
   int rc = idx_fill(a, &d);
   if (rc) return rc;
-  const size_t need = idx_carve(&a->shape, nullptr, nullptr);
+  const size_t need = BLOCK_SYNC_BYTES + idx_carve(&a->shape, nullptr, nullptr);
   MK2_REQUIRE(a->workspace != nullptr, "indexer: workspace is NULL");
   if (a->workspace_bytes < need)
     return set_error(MK2_ENOSPACE, "indexer: workspace has %zu bytes, needs %zu", a->workspace_bytes, need);
-  idx_carve(&a->shape, a->workspace, &d);
-  idx_enqueue(d, (hipStream_t)stream);
-  return check_launch("indexer");
+  idx_carve(&a->shape, (char*)a->workspace + BLOCK_SYNC_BYTES, &d);
+  return k2_block_enqueue(0 /* indexer */, &d, nullptr, nullptr, (int*)a->workspace, d.rows, (hipStream_t)stream);
 }

@@ -432,19 +432,30 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p, Front front) {
   }
 }
 
-static int g_cus = 0;
+// the current device's CU count (the persistent grid), queried once per device
+constexpr int K2_MAX_DEVICES = 64;
+static int g_cus[K2_MAX_DEVICES];
+static int current_cus(int* cus) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= K2_MAX_DEVICES)
+    return set_error(MK2_ELAUNCH, "persistent launch: no current HIP device");
+  if (g_cus[dev] <= 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      return set_error(MK2_ELAUNCH, "persistent launch: cannot query the CU count of device %d", dev);
+    g_cus[dev] = n;
+  }
+  *cus = g_cus[dev];
+  return MK2_OK;
+}
 
 // front: the layer's front to run ahead of the stages in the same launch, or null;
 // front_key: its instantiation (FRONT_FUSED_*)
 int k2_persistent_enqueue(const IdxDev& idx, const MlaDev& mla, const MoeDev& moe, int* sync,
                           int* status, uint64_t* timeline, int rows, int spin_limit, hipStream_t st,
                           const FrontPDev* front, int front_key) {
-  if (g_cus == 0) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&g_cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || g_cus <= 0)
-      return set_error(MK2_ELAUNCH, "layer: cannot query the CU count");
-  }
+  int ncu = 0;
+  if (const int rc = current_cus(&ncu)) return rc;
   K2Dev p{idx, mla, moe, sync, status, timeline, rows, spin_limit};
   const bool two = rows > 16;
   // one instantiation a column-group count and expert mode (and, with the front ahead,
@@ -458,8 +469,8 @@ int k2_persistent_enqueue(const IdxDev& idx, const MlaDev& mla, const MoeDev& mo
                          : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_k2_layer<1, FMT, Fr>, K2_NT, 0);
       if (e != hipSuccess || per_cu < 1)
         return set_error(MK2_ELAUNCH, "layer: the persistent kernel does not fit one workgroup per CU");
-      if (two) k_k2_layer<2, FMT, Fr><<<g_cus, K2_NT, 0, st>>>(p, fr);
-      else k_k2_layer<1, FMT, Fr><<<g_cus, K2_NT, 0, st>>>(p, fr);
+      if (two) k_k2_layer<2, FMT, Fr><<<ncu, K2_NT, 0, st>>>(p, fr);
+      else k_k2_layer<1, FMT, Fr><<<ncu, K2_NT, 0, st>>>(p, fr);
       return check_launch("layer (persistent)");
     };
     if (!front) return launch(K2NoFront{});
@@ -468,6 +479,207 @@ int k2_persistent_enqueue(const IdxDev& idx, const MlaDev& mla, const MoeDev& mo
       if (front_key == FRONT_FUSED_C7_AITER16) return launch(K2Front<6, 4, MK2_WFMT_FP8_AITER16, 6>{*front});
     }
     return set_error(MK2_EINVAL, "layer step: no front-and-layer launch for this expert mode and front shape");
+  });
+}
+
+// ------------------------------------------------------------------------------------
+// The layer's three blocks as persistent launches of their own (the entry points of
+// configs[0..3]): the same stage functions, counters, hand-offs and fail-stop as the
+// layer's launch, walking only the block's stages.  The block's sync block leads its
+// workspace (zero-filled before the first launch; every launch leaves it so); a launch
+// whose wait gave up ORs 1 into the status word at BLOCK_STATUS_INT of it.
+constexpr int BLOCK_STATUS_INT = SY_LINES * SY_LINE;
+static_assert(BLOCK_STATUS_INT * 4 == MK2_BLOCK_STATUS_OFFSET, "the header's status offset");
+static_assert(BLOCK_STATUS_INT < SYNC_EPOCH, "the status word stays clear of the epoch word");
+enum { K2_BLOCK_INDEXER = 0, K2_BLOCK_MLA = 1, K2_BLOCK_MOE = 2 };
+
+template <int BLK, int NCG, int FMT>
+__global__ __launch_bounds__(K2_NT, 1) void k_k2_block(K2Dev p) {
+  __shared__ K2Lds S;
+  __shared__ float kept[BLK == K2_BLOCK_INDEXER ? K2_KEEP : 1][IDX_CHUNK];
+  __shared__ int seen[SY_LINES + 1];
+  __shared__ int last_flag;
+  __shared__ uint32_t s_tag;
+  const int G = gridDim.x, b = blockIdx.x;
+  const int R = p.rows;
+  for (int i = threadIdx.x; i <= SY_LINES; i += K2_NT) seen[i] = 0;
+  if (threadIdx.x == 0) {
+    const uint32_t e = (uint32_t)ld_dev_i32(p.sync + SYNC_EPOCH) + 1u;
+    s_tag = e ? e : 1u;
+  }
+  __syncthreads();
+  const TagPoll tp{s_tag, p.spin_limit, k2_ctr(p, SY_ERR)};
+  uint32_t sel_rows = 0;  // the rows whose select this workgroup ran
+  auto walk = [&]() {
+    int base = 0;
+#define K2_TASKS(t, n) for (int t = (b - base % G + G) % G; t < (n); t += G)
+#define K2_NEXT(n) base = (base + (n)) % G
+    if constexpr (BLK == K2_BLOCK_INDEXER) {
+      // scores, slices (the last of a row to count out runs its select with one slice a
+      // workgroup; with several, the selects are tasks of their own): as the layer's
+      const int nchk = p.idx.nchk;
+      auto keep_of = [&](int t) { return t / G < K2_KEEP ? kept[t / G] : nullptr; };
+      K2_TASKS(t, R * nchk) {
+        idx_score<K2_NT>(p.idx, t / nchk, t % nchk, S.score, keep_of(t));
+        k2_signal(p, SY_SCORE + t / nchk);
+      }
+      const bool sel_tasks = R * nchk > G;
+      K2_TASKS(t, R * nchk) {
+        const int r = t / nchk;
+        if (!k2_wait(p, seen, SY_SCORE + r, nchk)) return;
+        bool last = false;
+        const bool known = idx_slice<K2_NT>(p.idx, r, t % nchk, S.topk, p.spin_limit, k2_ctr(p, SY_ERR), tp.tag,
+                                            [&] {
+                                              if (sel_tasks)
+                                                k2_signal(p, SY_SLICE + r);
+                                              else
+                                                last = k2_signal_last1(p, SY_SLICE + r, nchk, &last_flag);
+                                            },
+                                            keep_of(t));
+        if (last) {
+          idx_select<K2_NT>(p.idx, r, S.topk, tp.tag, known);
+          sel_rows |= 1u << r;
+        }
+      }
+      K2_NEXT(R * nchk);
+      if (sel_tasks) {
+        K2_TASKS(r, R) {
+          if (!k2_wait(p, seen, SY_SLICE + r, nchk)) return;
+          idx_select<K2_NT>(p.idx, r, S.topk, tp.tag, false);
+          sel_rows |= 1u << r;
+        }
+      }
+      // every slice and select read the histograms: the selects' rows back to zero
+      for (uint32_t m = sel_rows; m; m &= m - 1) idx_clear_hist<K2_NT>(p.idx, __ffs((int)m) - 1);
+    } else if constexpr (BLK == K2_BLOCK_MLA) {
+      // splits (the given positions), merge + W_UV, W_o + residual: as the layer's
+      const int ns = p.mla.nsplit;
+      K2_TASKS(t, R * ns) {
+        if (!mla_split<K2_NT>(p.mla, t / ns, t % ns, S.split, tp)) return;
+        k2_signal(p, SY_SPLIT + t / ns);
+      }
+      K2_NEXT(R * ns);
+      K2_TASKS(t, 2 * R * MLA_HEADS) {
+        const int r = t / (2 * MLA_HEADS), h = (t >> 1) % MLA_HEADS;
+        mla_merge_uv<K2_NT>(p.mla, r, h, t & 1, S.merge, [&] { return k2_wait(p, seen, SY_SPLIT + r, ns); });
+        if (seen[SY_LINES]) return;
+        k2_signal(p, SY_UV, t, K2_LANES);
+      }
+      K2_NEXT(2 * R * MLA_HEADS);
+      const int ht = p.mla.hidden / 16;
+      for (int t = (b - base % G + G) % G; t < ht; t += 2 * G) {
+        const int t1 = t + G < ht ? t + G : -1;
+        mla_oproj<K2_NT, NCG, 2>(p.mla, t, t1, S.up.red,
+                                 [&] { return k2_wait(p, seen, SY_UV, 2 * R * MLA_HEADS, -1, K2_LANES); });
+        if (seen[SY_LINES]) return;
+      }
+    } else {
+      // the rows' sums of squares (with the RMSNorm), router, routing, up/gate, down:
+      // as the layer's, the sums from tasks of their own (the layer's come from W_o)
+      // (512 columns a task on the first 128 threads: the staged kernel's shape, so both
+      // give the same bits for any hidden size a multiple of 512)
+      const int per = p.moe.H / 512, nss = p.moe.norm ? p.rows * per : 0;
+      K2_TASKS(t, nss) {
+        if (threadIdx.x < 128) moe_sumsq<128>(p.moe, t / per, t % per);
+        k2_signal(p, SY_OPROJ, t, K2_LANES);
+      }
+      K2_NEXT(nss);
+      const int et = p.moe.E / 16, nrt = et * p.moe.KC;
+      K2_TASKS(t, nrt) {
+        moe_router<K2_NT, NCG, FMT>(p.moe, t % et, t / et, S.router, tp.tag,
+                                    [&] { return k2_wait(p, seen, SY_OPROJ, nss, -1, K2_LANES); });
+        if (seen[SY_LINES]) return;
+        k2_signal(p, SY_ROUTER, t, K2_LANES);
+      }
+      K2_NEXT(nrt);
+      const int up_r = p.moe.Dmax * (p.moe.I / p.moe.UC);
+      const int up_sh = p.moe.n_shared * (p.moe.SI / 32);
+      const int up_total = up_r + up_sh;
+      const int nq = p.moe.M > 8 ? (p.moe.M + 7) / 8 : 1;
+      int route_at = up_total % G;
+      if (nrt < G && route_at > G - nrt - nq) route_at = max(0, G - nrt - nq);
+      const int q = (b - base - route_at + 2 * G) % G;
+      if (q < nq) {
+        constexpr bool CMP = kCompact<NCG, FMT>;
+        bool ok;
+        if (nq == 1)
+          ok = moe_route<K2_NT, CMP>(p.moe, S.route, tp);
+        else if (q == 0)
+          ok = moe_route<K2_NT, CMP, ROUTE_LEAD>(p.moe, S.route, tp, NoMark(), 0, 8);
+        else
+          ok = moe_route<K2_NT, CMP, ROUTE_PICK>(p.moe, S.route, tp, NoMark(), 8 * q, min(p.moe.M, 8 * q + 8));
+        if (!ok) return;
+        if (q == 0) k2_signal(p, SY_ROUTE);
+      }
+      K2_TASKS(t, up_total) {
+        const bool sh = t < up_sh;
+        if (!k2_wait(p, seen, SY_ROUTER, nrt, -1, K2_LANES)) return;
+        if (!moe_upgate<K2_NT, NCG, FMT>(p.moe, sh ? up_r + t : t - up_sh, S.up.red, S.up.midf, tp)) return;
+        k2_signal(p, SY_UP, t, K2_LANES);
+      }
+      K2_NEXT(up_total);
+      K2_TASKS(t, down_tasks(p.moe)) {
+        if (!k2_wait(p, seen, SY_ROUTE, 1)) return;
+        moe_down<K2_NT, NCG, FMT>(p.moe, t, S.down.red, S.down.act, S.down.xres,
+                                  [&] { return k2_wait(p, seen, SY_UP, up_total, -1, K2_LANES); });
+        if (seen[SY_LINES]) return;
+      }
+    }
+#undef K2_TASKS
+#undef K2_NEXT
+  };
+  walk();
+  // the last workgroup out resets the counters (and on a stop the top-k state it left)
+  drain_memory();
+  __syncthreads();
+  if (threadIdx.x == 0)
+    last_flag = __hip_atomic_fetch_add(k2_ctr(p, SY_DONE), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == G - 1;
+  __syncthreads();
+  if (last_flag) {
+    __syncthreads();
+    if (threadIdx.x == 0) last_flag = __hip_atomic_load(k2_ctr(p, SY_ERR), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (last_flag) {
+      if constexpr (BLK == K2_BLOCK_INDEXER) idx_reset_rows<K2_NT>(p.idx, R);
+      if (threadIdx.x == 0) atomicOr(p.sync + BLOCK_STATUS_INT, 1);
+      drain_memory();
+      __syncthreads();
+    } else if constexpr (BLK == K2_BLOCK_INDEXER) {
+      for (int i = threadIdx.x; i < R * p.idx.nchk; i += K2_NT) st_dev_i32(p.idx.ccount + i, 0);
+    }
+    for (int l = threadIdx.x; l < SY_LINES; l += K2_NT)
+      __hip_atomic_store(k2_ctr(p, l), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) st_dev_i32(p.sync + SYNC_EPOCH, (int)s_tag);
+  }
+}
+
+// One block's persistent launch on `sync` (its workspace's leading sync block).  Returns
+// MK2_ELAUNCH when the kernel would not keep one workgroup on every CU.
+int k2_block_enqueue(int blk, const IdxDev* idx, const MlaDev* mla, const MoeDev* moe, int* sync, int rows,
+                     hipStream_t st) {
+  int ncu = 0;
+  if (const int rc = current_cus(&ncu)) return rc;
+  K2Dev p{};
+  if (idx) p.idx = *idx;
+  if (mla) p.mla = *mla;
+  if (moe) p.moe = *moe;
+  p.sync = sync;
+  p.rows = rows;
+  p.spin_limit = 1 << 20;
+  const bool two = rows > 16;
+  auto launch = [&](auto kern) -> int {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, K2_NT, 0) != hipSuccess || per_cu < 1)
+      return set_error(MK2_ELAUNCH, "block: the persistent kernel does not fit one workgroup per CU");
+    kern<<<ncu, K2_NT, 0, st>>>(p);
+    return check_launch("block (persistent)");
+  };
+  if (blk == K2_BLOCK_INDEXER) return launch(k_k2_block<K2_BLOCK_INDEXER, 1, MK2_FMT_MXFP4>);
+  if (blk == K2_BLOCK_MLA)
+    return two ? launch(k_k2_block<K2_BLOCK_MLA, 2, MK2_FMT_MXFP4>) : launch(k_k2_block<K2_BLOCK_MLA, 1, MK2_FMT_MXFP4>);
+  return with_moe_fmt(moe->fmt, [&](auto F) {
+    constexpr int FMT = decltype(F)::value;
+    return two ? launch(k_k2_block<K2_BLOCK_MOE, 2, FMT>) : launch(k_k2_block<K2_BLOCK_MOE, 1, FMT>);
   });
 }
 

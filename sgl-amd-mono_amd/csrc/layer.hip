@@ -197,7 +197,8 @@ extern "C" int mk2_layer_workspace_layout(const mk2_layer_args* a, int64_t* moe_
   size_t bytes = 0;
   const int rc = layer_plan(a, nullptr, &L, &bytes);
   if (rc) return rc;
-  *moe_offset = (int64_t)L.moe_off;
+  // mk2_moe_workspace_layout's offsets count the standalone block's leading sync block
+  *moe_offset = (int64_t)L.moe_off - (int64_t)SYNC_INTS * 4;
   return MK2_OK;
 }
 

@@ -1,7 +1,10 @@
-// Standalone sparse-MLA launch (16 heads, 512 + 64 latent dims): split attention, merge
-// + W_UV, W_o + residual.
+// Sparse-MLA launch (16 heads, 512 + 64 latent dims): split attention, merge + W_UV,
+// W_o + residual -- as one persistent launch (k2_persistent.hip) for
+// mk2_sparse_mla_launch, and as one kernel a stage for the layer's staged mode.
+#include "indexer_stages.h"
 #include "mk2_host.h"
 #include "mla_stages.h"
+#include "moe_stages.h"
 
 namespace mk2 {
 
@@ -62,6 +65,11 @@ int mla_fill(const mk2_mla_args* a, MlaDev* d) {
   return MK2_OK;
 }
 
+int k2_block_enqueue(int blk, const IdxDev* idx, const MlaDev* mla, const MoeDev* moe, int* sync, int rows,
+                     hipStream_t st);
+constexpr size_t BLOCK_SYNC_BYTES = (size_t)SYNC_INTS * 4;  // the persistent launch's sync block
+
+// the layer's staged mode: one kernel a stage, in stream order
 void mla_enqueue(const MlaDev& d, hipStream_t st) {
   k_mla_split<<<dim3(d.nsplit, d.rows), MLA_NT, 0, st>>>(d);
   k_mla_merge_uv<<<dim3(2 * MLA_HEADS, d.rows), MLA_NT2, 0, st>>>(d);
@@ -78,7 +86,7 @@ extern "C" int mk2_mla_workspace_bytes(const mk2_mla_shape* shape, size_t* bytes
   int rc = mla_check_shape(shape);
   if (rc) return rc;
   MK2_REQUIRE(bytes != nullptr, "mla: bytes is NULL");
-  *bytes = mla_carve(shape, nullptr, nullptr);
+  *bytes = BLOCK_SYNC_BYTES + mla_carve(shape, nullptr, nullptr);
   return MK2_OK;
 }
 
@@ -90,10 +98,9 @@ extern "C" int mk2_sparse_mla_launch(const mk2_mla_args* a, mk2_stream_t stream)
   if (rc) return rc;
   MK2_REQUIRE(a->sel && a->out && a->workspace, "mla: sel, out and workspace must be set");
   MK2_REQUIRE(a->out != a->h, "mla: out must not alias h");
-  const size_t need = mla_carve(&a->shape, nullptr, nullptr);
+  const size_t need = BLOCK_SYNC_BYTES + mla_carve(&a->shape, nullptr, nullptr);
   if (a->workspace_bytes < need)
     return set_error(MK2_ENOSPACE, "mla: workspace has %zu bytes, needs %zu", a->workspace_bytes, need);
-  mla_carve(&a->shape, a->workspace, &d);
-  mla_enqueue(d, (hipStream_t)stream);
-  return check_launch("mla");
+  mla_carve(&a->shape, (char*)a->workspace + BLOCK_SYNC_BYTES, &d);
+  return k2_block_enqueue(1 /* mla */, nullptr, &d, nullptr, (int*)a->workspace, d.rows, (hipStream_t)stream);
 }

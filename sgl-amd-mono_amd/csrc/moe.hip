@@ -1,7 +1,11 @@
-// Standalone MoE block launch (FP8 or MXFP4 experts): up to five kernels on one
-// stream -- the rows' partial sums of squares (with RMSNorm), router GEMV (+ RMSNorm
-// + MXFP8 quant), route (top-k + distinct experts), up/gate + SwiGLU, down + combine.
+// MoE block launch (every expert mode): the rows' partial sums of squares (with
+// RMSNorm), router GEMV (+ RMSNorm + activation quant), route (top-k + distinct
+// experts), up/gate + SwiGLU, down + combine -- as one persistent launch
+// (k2_persistent.hip) for mk2_moe_launch, and as one kernel a stage for the layer's
+// staged mode.
+#include "indexer_stages.h"
 #include "mk2_host.h"
+#include "mla_stages.h"
 #include "moe_stages.h"
 
 namespace mk2 {
@@ -139,6 +143,11 @@ int moe_fill(const mk2_moe_args* a, MoeDev* d) {
   return MK2_OK;
 }
 
+int k2_block_enqueue(int blk, const IdxDev* idx, const MlaDev* mla, const MoeDev* moe, int* sync, int rows,
+                     hipStream_t st);
+constexpr size_t BLOCK_SYNC_BYTES = (size_t)SYNC_INTS * 4;  // the persistent launch's sync block
+
+// the layer's staged mode: one kernel a stage, in stream order
 int moe_enqueue(const MoeDev& d, hipStream_t st) {
   const int ncg = d.M > 16 ? 2 : 1;
   if (d.norm) k_moe_sumsq<<<dim3(d.H / 512, d.M), 128, 0, st>>>(d);  // H: a multiple of 512
@@ -167,7 +176,7 @@ extern "C" int mk2_moe_workspace_bytes(const mk2_moe_shape* shape, size_t* bytes
   int rc = moe_check_shape(shape);
   if (rc) return rc;
   MK2_REQUIRE(bytes != nullptr, "moe: bytes is NULL");
-  *bytes = moe_carve(shape, nullptr, nullptr);
+  *bytes = BLOCK_SYNC_BYTES + moe_carve(shape, nullptr, nullptr);
   return MK2_OK;
 }
 
@@ -176,11 +185,12 @@ extern "C" int mk2_moe_workspace_layout(const mk2_moe_shape* shape, mk2_moe_ws_l
   int rc = moe_check_shape(shape);
   if (rc) return rc;
   MK2_REQUIRE(out != nullptr, "moe: layout is NULL");
-  // carve at a stand-in base and report offsets from it (nothing is dereferenced)
+  // carve at a stand-in base, after the sync block, and report offsets from the
+  // workspace's start (nothing is dereferenced)
   char* const base = (char*)(uintptr_t)4096;
   MoeDev d{};
   d.fmt = shape->expert_fmt;
-  moe_carve(shape, base, &d);
+  moe_carve(shape, base + BLOCK_SYNC_BYTES, &d);
   auto off = [&](const void* p) -> int64_t { return p ? (int64_t)((const char*)p - base) : -1; };
   const int fmt = shape->expert_fmt;
   const bool q = fmt == MK2_FMT_MXFP4 || fmt == MK2_FMT_W8A8 || fmt == MK2_FMT_A4W4;
@@ -208,12 +218,12 @@ extern "C" int mk2_moe_launch(const mk2_moe_args* a, mk2_stream_t stream) {
   if (rc) return rc;
   MK2_REQUIRE(a->x && a->out && a->workspace, "moe: x, out and workspace must be set");
   MK2_REQUIRE(a->x != a->out, "moe: out must not alias x");
-  const size_t need = moe_carve(&a->shape, nullptr, nullptr);
+  const size_t need = BLOCK_SYNC_BYTES + moe_carve(&a->shape, nullptr, nullptr);
   if (a->workspace_bytes < need)
     return set_error(MK2_ENOSPACE, "moe: workspace has %zu bytes, needs %zu", a->workspace_bytes, need);
-  moe_carve(&a->shape, a->workspace, &d);
+  moe_carve(&a->shape, (char*)a->workspace + BLOCK_SYNC_BYTES, &d);
   if (a->logits) d.logits = a->logits;
   if (a->topk_ids) d.topk_ids = a->topk_ids;
   if (a->topk_weights) d.topk_w = a->topk_weights;
-  return moe_enqueue(d, (hipStream_t)stream);
+  return k2_block_enqueue(2 /* moe */, nullptr, nullptr, &d, (int*)a->workspace, d.M, (hipStream_t)stream);
 }

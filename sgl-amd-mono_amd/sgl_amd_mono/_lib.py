@@ -110,6 +110,7 @@ class LayerArgs(ctypes.Structure):
 
 MK2_WFMT_BF16, MK2_WFMT_FP8_BLOCK, MK2_WFMT_FP8_AITER16 = 0, 1, 2
 MK2_FRONT_STATUS_OFFSET = 6528  # bytes into the front's workspace: the persistent launch's status word
+MK2_BLOCK_STATUS_OFFSET = 26624  # bytes into a block entry point's workspace: its status word
 
 
 class FrontShape(ctypes.Structure):

@@ -69,6 +69,13 @@ def moe_activation_views(shape, workspace, base: int = 0) -> dict:
     return out
 
 
+def _block_status(workspace) -> int:
+    """A block launch's sticky status word (nonzero: a dependency wait of a persistent
+    launch ran out of its spin limit; that launch's outputs are undefined).  Syncs."""
+    off = _lib.MK2_BLOCK_STATUS_OFFSET
+    return int(workspace[off:off + 4].view(torch.int32).item())
+
+
 class MoEOp:
     """The MoE block of one layer (router -> top-k -> routed + shared experts)."""
 
@@ -90,7 +97,13 @@ class MoEOp:
         )
         nbytes = ctypes.c_size_t()
         _lib.check(_lib.lib().mk2_moe_workspace_bytes(ctypes.byref(self.shape), ctypes.byref(nbytes)))
-        self.workspace = torch.empty(nbytes.value, dtype=torch.uint8, device=self.device)
+        # zero-filled: the persistent launch's counters start at zero, and each launch
+        # leaves them so
+        self.workspace = torch.zeros(nbytes.value, dtype=torch.uint8, device=self.device)
+
+    def status(self) -> int:
+        """The launches' sticky status word (_block_status)."""
+        return _block_status(self.workspace)
 
     def __call__(self, x, out=None, *, logits=None, topk_ids=None, topk_weights=None):
         H = self.cfg.hidden
@@ -120,7 +133,13 @@ class IndexerOp:
         self.shape = _lib.IndexerShape(rows, cfg.heads, cfg.dim, cfg.topk, cfg.context, table_stride, cfg.keys)
         nbytes = ctypes.c_size_t()
         _lib.check(_lib.lib().mk2_indexer_workspace_bytes(ctypes.byref(self.shape), ctypes.byref(nbytes)))
-        self.workspace = torch.empty(nbytes.value, dtype=torch.uint8, device=self.device)
+        # zero-filled: the persistent launch's counters start at zero, and each launch
+        # leaves them so
+        self.workspace = torch.zeros(nbytes.value, dtype=torch.uint8, device=self.device)
+
+    def status(self) -> int:
+        """The launches' sticky status word (_block_status)."""
+        return _block_status(self.workspace)
 
     def __call__(self, q, w, cache, cache_scale, page_table, req_ids, ctx_len, scores=None, topk=None):
         cfg, rows = self.cfg, self.rows
@@ -333,7 +352,13 @@ class SparseMlaOp:
         )
         nbytes = ctypes.c_size_t()
         _lib.check(_lib.lib().mk2_mla_workspace_bytes(ctypes.byref(self.shape), ctypes.byref(nbytes)))
-        self.workspace = torch.empty(nbytes.value, dtype=torch.uint8, device=self.device)
+        # zero-filled: the persistent launch's counters start at zero, and each launch
+        # leaves them so
+        self.workspace = torch.zeros(nbytes.value, dtype=torch.uint8, device=self.device)
+
+    def status(self) -> int:
+        """The launches' sticky status word (_block_status)."""
+        return _block_status(self.workspace)
 
     def __call__(self, q, kv, kv_scale, page_table, req_ids, sel, h=None, out=None, o_latent=None):
         cfg, rows = self.cfg, self.rows

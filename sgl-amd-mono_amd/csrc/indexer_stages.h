@@ -799,6 +799,86 @@ MK2_DEV void bin_select(TopkLds& S, int m, int base, int k, const ListOut& lo) {
   }
 }
 
+// The same list part from the 2048-bin histogram of the candidates' bits 19 .. 9 (built
+// as they were gathered), when the bin b of the need-th largest holds at most 64 of them
+// (else false, and nothing is written): every candidate of a higher bin lies above the
+// k-th key; one wave ranks bin b's few by (low bits desc, candidate order) and finds the
+// k-th key T and the count above it; then one block scan of (above T, equal to T) over
+// the candidates in their order (position order) places every entry, the reference's
+// order: the keys above the k-th, then the ties, lowest positions first.
+template <int NT>
+MK2_DEV bool bin_select_fast(TopkLds& S, int m, int base, int k, const ListOut& lo) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int need = k - base;  // >= 1: the k-th key lies in bin b1
+  if (tid < 64) {
+    int ab;
+    const int bb = wave_find_bin(S.hist, 2048, need, &ab);
+    if (tid == 0) {
+      S.res[0] = bb;
+      S.res[1] = ab;
+      S.res[2] = 0;
+    }
+  }
+  __syncthreads();
+  const uint32_t bb = (uint32_t)S.res[0];
+  const int above = S.res[1];
+  const int inb = S.hist[bb];
+  if (inb > 64) return false;  // uniform: every thread read the same words
+  // bin b's candidates (their indices, in any order)
+  for (int j = tid; j < m; j += NT)
+    if (((S.ckey[j] & 0xFFFFFu) >> 9) == bb) S.scratch[atomicAdd(&S.res[2], 1)] = j;
+  __syncthreads();
+  if (tid < 64) {
+    const int j = lane < inb ? S.scratch[lane] : 0;
+    const uint32_t key = lane < inb ? (S.ckey[j] & 0x1FFu) : 0u;
+    int rank = 0;  // bin b's candidates before this one in (key desc, candidate asc)
+    for (int o = 0; o < inb; ++o) {
+      const uint32_t ko = (uint32_t)__builtin_amdgcn_readlane((int)key, o);
+      const int jo = __builtin_amdgcn_readlane(j, o);
+      rank += (ko > key || (ko == key && jo < j)) ? 1 : 0;
+    }
+    const int need2 = need - above;  // 1 .. inb
+    const uint64_t hit = __ballot(lane < inb && rank == need2 - 1);
+    const uint32_t t9 = (uint32_t)__builtin_amdgcn_readlane((int)key, __ffsll((long long)hit) - 1);
+    const int gt = __popcll(__ballot(lane < inb && key > t9));
+    if (tid == 0) {
+      S.res[0] = (int)((bb << 9) | t9);
+      S.res[1] = above + gt;
+    }
+  }
+  __syncthreads();
+  const uint32_t T = (uint32_t)S.res[0];  // low 20 bits of the k-th key
+  const int n_gt = S.res[1], ties = need - n_gt;
+  // thread t takes candidates t c .. t c + c - 1: a count pass, the scan, an emit pass
+  const int c = (m + NT - 1) / NT, j0 = tid * c;
+  int na = 0, ne = 0;
+  for (int i = 0; i < c; ++i) {
+    const int j = j0 + i;
+    if (j < m) {
+      const uint32_t low = S.ckey[j] & 0xFFFFFu;
+      na += low > T ? 1 : 0;
+      ne += low == T ? 1 : 0;
+    }
+  }
+  Scan3 tot;
+  const Scan3 off = block_scan3<NT>(Scan3{na, ne, 0}, &tot, (int*)S.gcount);
+  int ra = off.a, re = off.b;
+  for (int i = 0; i < c; ++i) {
+    const int j = j0 + i;
+    if (j >= m) break;
+    const uint32_t low = S.ckey[j] & 0xFFFFFu;
+    int dst = -1;
+    if (low > T) {
+      dst = base + ra++;
+    } else if (low == T) {
+      if (re < ties) dst = base + n_gt + re;
+      ++re;
+    }
+    if (dst >= 0 && dst < k) lo.put(dst, (int)S.cpos[j]);
+  }
+  return true;
+}
+
 // --------------------------------------------------------------- stage: select
 // Task (row r), once every slice of the row is done: the list's bin-b1 part.  The
 // keys above bin b1 (above1 of them) are already listed by the slices; of the keys in
@@ -824,7 +904,7 @@ MK2_DEV void idx_select(const IdxDev& p, int r, TopkLds& S, uint32_t tag, bool k
     const int b1 = wave_threshold(p, r, k, &above);
     if (tid == 0) { S.res[0] = b1; S.res[1] = above; }
   }
-  for (int i = tid; i < 2 * 1024; i += NT) S.hist[i] = 0;  // the two digit histograms
+  for (int i = tid; i < 2048; i += NT) S.hist[i] = 0;  // the bits-19..9 histogram
   // one round trip: each chunk's count of bin-b1 keys and its first SPEC * TPC of them
   const int c = tid / TPC, sub = tid % TPC;
   const uint2* src = p.cand + (size_t)r * p.max_ctx + (size_t)c * IDX_CHUNK;
@@ -858,7 +938,7 @@ MK2_DEV void idx_select(const IdxDev& p, int r, TopkLds& S, uint32_t tag, bool k
       if (i < cnt) {
         S.ckey[off + i] = v[u].x;
         S.cpos[off + i] = (uint16_t)v[u].y;
-        atomicAdd(&S.hist[(v[u].x >> 10) & 1023u], 1);  // the first radix digit
+        atomicAdd(&S.hist[(v[u].x >> 9) & 2047u], 1);  // bits 19 .. 9 of the key
       }
     }
     for (int i0 = SPEC * TPC; i0 < cnt; i0 += SPEC * TPC) {  // a crowded chunk's rest
@@ -873,11 +953,18 @@ MK2_DEV void idx_select(const IdxDev& p, int r, TopkLds& S, uint32_t tag, bool k
         if (i < cnt) {
           S.ckey[off + i] = v[u].x;
           S.cpos[off + i] = (uint16_t)v[u].y;
-          atomicAdd(&S.hist[(v[u].x >> 10) & 1023u], 1);
+          atomicAdd(&S.hist[(v[u].x >> 9) & 2047u], 1);
         }
       }
     }
   }
+  __syncthreads();
+  if (bin_select_fast<NT>(S, m, above1, k, lo)) return;
+  // a crowded bin (keys that tie, or lie close together): the two-digit radix select,
+  // its first digit's histogram (bits 19 .. 10) built again over the candidates
+  for (int i = tid; i < 2 * 1024; i += NT) S.hist[i] = 0;
+  __syncthreads();
+  for (int j = tid; j < m; j += NT) atomicAdd(&S.hist[(S.ckey[j] >> 10) & 1023u], 1);
   __syncthreads();
   bin_select<NT, CPT>(S, m, above1, k, lo);
 }

@@ -82,7 +82,7 @@ union K2Lds {
     float midf[32 * 65];
   } up;
   struct {
-    float red[(K2_NT / 64) * 2 * 64 * 4];
+    float red[(K2_NT / 64) * 2 * 16 * 32];  // NW * DT * NCG * 256, or NW * DT * 16 * 32
     int act[512];  // the slots' experts, then (compacted rows) their row counts
     float xres[16 * 2 * 32];
   } down;

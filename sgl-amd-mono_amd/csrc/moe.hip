@@ -35,7 +35,8 @@ __global__ __launch_bounds__(MOE_NT) void k_moe_upgate(MoeDev p) {
 
 template <int NCG, int FMT>
 __global__ __launch_bounds__(MOE_NT) void k_moe_down(MoeDev p) {
-  __shared__ float red[(MOE_NT / 64) * 2 * 64 * 4];  // NW * DT * NCG * 256, DT * NCG <= 2
+  __shared__ float red[(MOE_NT / 64) * 2 * 16 * 32];  // NW * DT * NCG * 256 (DT * NCG <= 2),
+                                                     // or NW * DT * 16 * 32 (compacted rows)
   __shared__ int act_ids[512];
   __shared__ float xres[16 * 2 * 32];
   moe_down<MOE_NT, NCG, FMT>(p, blockIdx.x, red, act_ids, xres);
@@ -85,9 +86,10 @@ size_t moe_carve(const mk2_moe_shape* s, void* base, MoeDev* d) {
   // for E2M1 weights up to 16 rows, else 32
   t.UC = fmt == MK2_FMT_W8A8 ? 128 : (w_fp4(fmt) && M <= 16 && I % 64 == 0) ? 64 : 32;
   // down tasks: 24 hidden rows when hidden is a multiple of 48 (6144: one task a CU of
-  // MI355X), else 32, for the scaled-MFMA E2M1 modes up to 16 rows; 16 otherwise
+  // MI355X), for the scaled-MFMA E2M1 modes (above 16 rows on compacted rows); else 32
+  // for them up to 16 rows; 16 otherwise
   const bool mx_down = fmt == MK2_FMT_MXFP4 || fmt == MK2_FMT_A4W4;
-  t.DT = (mx_down && M <= 16) ? (H % 48 == 0 ? 3 : (H % 32 == 0 ? 2 : 1)) : 1;
+  t.DT = !mx_down ? 1 : H % 48 == 0 ? 3 : (M <= 16 && H % 32 == 0) ? 2 : 1;
   t.ssp = c.take<float>((size_t)(H / 16) * M);
   t.xn = c.take<bf16_t>((size_t)M * H);
   t.xq = c.take<uint8_t>((size_t)M * H);

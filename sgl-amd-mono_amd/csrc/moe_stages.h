@@ -1354,7 +1354,6 @@ MK2_DEV void down_rows_cmp(const MoeDev& p, int nt, float* red, int* act_ids, fl
   // the list, published by the routing's counter; read device-coherently: up/gate
   // tasks on this XCD polled its words before all of them were out
   constexpr bool CMP = kCompact<NCG, FMT>;
-  static_assert(!CMP || DT == 1, "compacted rows: one 16-row hidden tile a task");
   const int D = min((int)pair_value(ld_pair(p.act)), p.Dmax);
   for (int j = threadIdx.x; j < D; j += NT) {
     act_ids[j] = min(max((int)pair_value(ld_pair(p.act + 1 + j)), 0), p.E - 1);
@@ -1418,8 +1417,8 @@ MK2_DEV void down_rows_cmp(const MoeDev& p, int nt, float* red, int* act_ids, fl
         (const uint32_t*)(p.x + (size_t)(threadIdx.x / (ncol / 2)) * p.H + c0) + threadIdx.x % (ncol / 2),
         (uint32_t*)xres + 64 * wave, 4, 0, 0);
   // the routed slots (MXFP4): a unit is a batch of B slots (wave + NW * (B * i + u))
-  // over KC k-blocks; units u + 1 and u + 2 (weights, mid rows, scales and route
-  // weights) are in flight while unit u's MFMAs run
+  // over KC k-blocks; units u + 1 and u + 2 (u + 1 alone for 24-row tasks: weights,
+  // mid rows, scales and route weights) are in flight while unit u's MFMAs run
   struct Unit {
     i32x8 a[B][DT][KC];
     i32x8 bq[B][KC][NCG];
@@ -1521,12 +1520,15 @@ MK2_DEV void down_rows_cmp(const MoeDev& p, int nt, float* red, int* act_ids, fl
       for (int ub = 0; ub < B; ++ub) {
         if (j0 + ub * NW >= D) break;
         if constexpr (CMP) {
-          // each column into its row of this wave's accumulator [16 hidden][32 rows]
+          // each column into its row of this wave's accumulators [DT][16 hidden][32 rows]
 #pragma unroll
           for (int cg = 0; cg < NCG; ++cg)
             if (x.rr[ub][cg] >= 0) {
 #pragma unroll
-              for (int i = 0; i < 4; ++i) red[(wave * 16 + 4 * g + i) * 32 + x.rr[ub][cg]] += tmp[ub][0][cg][i] * x.wr[ub][cg];
+              for (int d = 0; d < DT; ++d)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                  red[((wave * DT + d) * 16 + 4 * g + i) * 32 + x.rr[ub][cg]] += tmp[ub][d][cg][i] * x.wr[ub][cg];
             }
         } else {
 #pragma unroll
@@ -1537,12 +1539,14 @@ MK2_DEV void down_rows_cmp(const MoeDev& p, int nt, float* red, int* act_ids, fl
       }
     }
   };
+  // units in flight: 3, or 2 of two tiles each (24-row tasks), within the registers
+  constexpr int DEPTH = DT == 2 ? 2 : 3;
   Unit x0, x1, x2;
   if (nu > 0) load_w(0, x0);
-  if (nu > 1) load_w(1, x1);
+  if (DEPTH == 3 && nu > 1) load_w(1, x1);
   if (!wait()) return;
   if (nu > 0) load_m(0, x0);
-  if (nu > 1) load_m(1, x1);
+  if (DEPTH == 3 && nu > 1) load_m(1, x1);
   // the shared expert (FP8, bf16 mid): its k-blocks spread over the waves
   for (int kb = wave; kb < KB2s; kb += NW) {
     bf16x8 b[NCG][4];
@@ -1571,14 +1575,28 @@ MK2_DEV void down_rows_cmp(const MoeDev& p, int nt, float* red, int* act_ids, fl
     }
   }
   if constexpr (CMP) {
-    // this wave's accumulator [16 hidden][32 rows] in LDS, from its shared-expert sums;
-    // the routed slots add into their rows
+    // this wave's accumulators [DT][16 hidden][32 rows] in LDS, from its shared-expert
+    // sums; the routed slots add into their rows
 #pragma unroll
-    for (int cg = 0; cg < NCG; ++cg)
+    for (int d = 0; d < DT; ++d)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) red[(wave * 16 + 4 * g + i) * 32 + cg * 16 + c16] = acc[0][cg][i];
+      for (int cg = 0; cg < NCG; ++cg)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red[((wave * DT + d) * 16 + 4 * g + i) * 32 + cg * 16 + c16] = acc[d][cg][i];
   }
-  if constexpr (mx) {
+  if constexpr (mx && DEPTH == 2) {
+    auto step = [&](int u, Unit& cur, Unit& nxt) {
+      if (u + 1 < nu) {
+        load_w(u + 1, nxt);
+        load_m(u + 1, nxt);
+      }
+      if (u < nu) compute(u, cur);
+    };
+    for (int u = 0; u < nu; u += 2) {
+      step(u, x0, x1);
+      step(u + 1, x1, x0);
+    }
+  } else if constexpr (mx) {
     auto step = [&](int u, Unit& cur, Unit& nxt2) {
       if (u + 2 < nu) {
         load_w(u + 2, nxt2);
@@ -1696,7 +1714,7 @@ MK2_DEV void down_rows_cmp(const MoeDev& p, int nt, float* red, int* act_ids, fl
     float y = 0.f;
 #pragma unroll
     for (int w = 0; w < NW; ++w)
-      y += CMP ? red[(w * 16 + n16) * 32 + s] : red[(((w * DT + d) * NCG + cg) * 64 + l) * 4 + i];
+      y += CMP ? red[((w * DT + d) * 16 + n16) * 32 + s] : red[(((w * DT + d) * NCG + cg) * 64 + l) * 4 + i];
     const size_t o = (size_t)s * p.H + c0 + n;
     if (p.residual) y += bf16_to_f32(((const bf16_t*)xres)[idx]);
     p.out[o] = f32_to_bf16(y);
@@ -1713,7 +1731,10 @@ __host__ __device__ inline int down_tasks(const MoeDev& p) { return p.DT == 3 ? 
 template <int NT, int NCG, int FMT, typename Wait = NoWait>
 MK2_DEV void moe_down(const MoeDev& p, int nt, float* red, int* act_ids, float* xres, Wait wait = Wait()) {
   if constexpr (kCompact<NCG, FMT>) {
-    down_rows_cmp<NT, NCG, 1, FMT>(p, nt, red, act_ids, xres, wait);
+    // 24 hidden rows a task where hidden is a multiple of 48 (one task a CU at 6144),
+    // else 16
+    if (p.DT == 3) down_rows_cmp<NT, NCG, 2, FMT>(p, nt, red, act_ids, xres, wait);
+    else down_rows_cmp<NT, NCG, 1, FMT>(p, nt, red, act_ids, xres, wait);
   } else {
     if constexpr (FMT == MK2_FMT_MXFP4 || FMT == MK2_FMT_A4W4) {
       if (NCG == 1 && p.DT >= 2) {

@@ -36,7 +36,11 @@
 extern "C" {
 #endif
 
-#define MK2_ABI_VERSION 3
+#define MK2_ABI_VERSION 4
+
+/* the longest dependency-wait deadline a persistent launch takes (its waits compare
+ * 32-bit differences of the 100 MHz clock) */
+#define MK2_MAX_WAIT_US 40000000
 
 /* return codes */
 #define MK2_OK 0
@@ -133,9 +137,9 @@ typedef struct mk2_moe_args {
  * a CU, the stages handing off through counters, as the layer's launch does).  Their
  * workspace is zero-filled before its first launch, and every launch (completed or
  * stopped) leaves it ready for the next.  The int at byte MK2_BLOCK_STATUS_OFFSET of
- * the workspace becomes nonzero once a launch's dependency wait ran out of its spin
- * limit (about a second; that launch's outputs are undefined); only the caller clears
- * it. */
+ * the workspace becomes nonzero once a launch's dependency wait passed its deadline
+ * (one second of the device clock; that launch's outputs are undefined); only the
+ * caller clears it. */
 #define MK2_BLOCK_STATUS_OFFSET 26624
 int mk2_moe_workspace_bytes(const mk2_moe_shape* shape, size_t* bytes);
 int mk2_moe_launch(const mk2_moe_args* args, mk2_stream_t stream);
@@ -264,8 +268,9 @@ typedef struct mk2_layer_args {
                                (completed or stopped) leaves it ready for the next */
   size_t workspace_bytes;
   int mode;                 /* MK2_LAYER_PERSISTENT or MK2_LAYER_STAGED */
-  int spin_limit;           /* persistent: polls a dependency wait may take before the
-                               launch gives up (0: default, about a second) */
+  int wait_us;              /* persistent: a dependency wait's deadline in microseconds
+                               of the device's 100 MHz clock, from the wait's first
+                               unmet poll (0: one second; at most MK2_MAX_WAIT_US) */
   int32_t* status;          /* optional device word, sticky: a persistent launch whose
                                wait gave up stops early (its out is not valid) and ORs 1
                                into it; a completed launch leaves it as it is.  A stopped
@@ -322,8 +327,8 @@ int mk2_layer_launch_static(const mk2_layer_args* args, mk2_stream_t stream);
  * order, which mk2_front_launch_staged always runs; both give the same bits.  The
  * workspace is zero-filled before its first launch and holds the launch's counters,
  * the normed rows and the f32 GEMV outputs; the int at byte MK2_FRONT_STATUS_OFFSET
- * of it becomes nonzero once a persistent launch's dependency wait ran out of its
- * spin limit (that launch's outputs are undefined) and only the caller clears it. */
+ * of it becomes nonzero once a persistent launch's dependency wait passed its
+ * deadline (that launch's outputs are undefined) and only the caller clears it. */
 #define MK2_FRONT_STATUS_OFFSET 6528
 #define MK2_WFMT_BF16 0
 #define MK2_WFMT_FP8_BLOCK 1

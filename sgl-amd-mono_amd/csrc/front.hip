@@ -371,7 +371,7 @@ static FrontPDev front_pdev_of(const mk2_front_args* a, const FrontPrep& P) {
   d.x = (const bf16_t*)a->x; d.g_in = (const bf16_t*)a->weights.g_in; d.x_n = P.ws.x_n; d.hidden = s.hidden;
   d.eps = s.eps;
   d.sync = P.ws.sync;
-  d.spin = 1 << 20;
+  d.wait_ticks = DEFAULT_WAIT_TICKS;
   return d;
 }
 

@@ -586,7 +586,7 @@ struct FrontPDev {
   int hidden;
   float eps;
   int* sync;
-  int spin;
+  uint32_t wait_ticks;  // a dependency wait's deadline (WaitClock ticks)
 };
 
 union FrontLds {
@@ -622,6 +622,7 @@ MK2_DEV bool fp_wait(const FrontPDev& p, int* seen, int k, int line, int lanes, 
     auto count = [&](int c) { return __builtin_amdgcn_readfirstlane(row16_sum_i32(lane < lanes ? c : 0)); };
     bool bad = false;
     int n = 0, c0 = poll();
+    WaitClock wc;
     while (true) {
       const int c1 = poll();
       v = count(c0);
@@ -634,7 +635,7 @@ MK2_DEV bool fp_wait(const FrontPDev& p, int* seen, int k, int line, int lanes, 
         bad = true;
         break;
       }
-      if (n > p.spin) {
+      if (wc.expired(p.wait_ticks)) {
         if (lane == 0) atomicOr(fp_ctr(p, FP_ERR), 1);
         bad = true;
         break;

@@ -26,14 +26,13 @@ __global__ __launch_bounds__(IDX_NT) void k_idx_score(IdxDev p) {
 
 // slices take their tasks in the order the workgroups start (a ticket), so that the
 // earlier chunks a slice waits for have always started
-constexpr int IDX_SLICE_SPIN = 1 << 24;
 __global__ __launch_bounds__(IDX_NT) void k_idx_slice(IdxDev p) {
   __shared__ TopkLds S;
   if (threadIdx.x == 0) S.res[3] = atomicAdd(p.ticket, 1);
   __syncthreads();
   const int t = S.res[3];
   __syncthreads();
-  idx_slice<IDX_NT>(p, t / p.nchk, t % p.nchk, S, IDX_SLICE_SPIN, nullptr, 0u);
+  idx_slice<IDX_NT>(p, t / p.nchk, t % p.nchk, S, DEFAULT_WAIT_TICKS, nullptr, 0u);
 }
 
 __global__ __launch_bounds__(TOPK_NT) void k_idx_select(IdxDev p) {

@@ -518,8 +518,9 @@ MK2_DEV void idx_clear_hist(const IdxDev& p, int r) {
 // persistent layer counts the chunk out there, so that the row's select can start
 // while the slices still list their keys above the bin); then the task waits for the
 // earlier chunks' counts (tasks only wait on chunks of lower index, which publish
-// before they wait, so with every task started every wait ends; a wait past `spin`
-// polls, or the sticky error word `err` set, gives up and sets it).  `kept`: the
+// before they wait, so with every task started every wait ends; a wait past its
+// deadline of `wait_ticks` (WaitClock), or the sticky error word `err` set, gives up
+// and sets it).  `kept`: the
 // chunk's scores in LDS (its score task's `keep`), or null: read from `scores`.
 // Returns whether S.res[0..1] now hold b1 and the count above it.
 constexpr int CC_FLAG = 1 << 30;
@@ -527,7 +528,7 @@ struct NoPub {
   MK2_DEV void operator()() const {}
 };
 template <int NT, class Pub = NoPub>
-MK2_DEV bool idx_slice(const IdxDev& p, int r, int chunk, TopkLds& S, int spin, int* err, uint32_t tag,
+MK2_DEV bool idx_slice(const IdxDev& p, int r, int chunk, TopkLds& S, uint32_t wait_ticks, int* err, uint32_t tag,
                        Pub published = Pub(), const float* kept = nullptr) {
   constexpr int PER = IDX_CHUNK / NT;  // consecutive positions a thread
   static_assert(PER % 4 == 0, "a thread reads whole 16-byte groups of scores");
@@ -590,10 +591,11 @@ MK2_DEV bool idx_slice(const IdxDev& p, int r, int chunk, TopkLds& S, int spin, 
     int v = CC_FLAG;
     if (chunk > 0) {
       const int* cc = p.ccount + (size_t)r * p.nchk;
+      WaitClock wc;
       for (int polls = 1;; ++polls) {
         v = lane < chunk ? ld_dev_i32(cc + lane) : CC_FLAG;
         if (__ballot((v & CC_FLAG) == 0) == 0) break;
-        if (polls > spin || ((polls & 31) == 0 && err && ld_dev_i32(err))) {
+        if (wc.expired(wait_ticks) || ((polls & 31) == 0 && err && ld_dev_i32(err))) {
           if (lane == 0 && err) atomicOr(err, 1);
           break;
         }

@@ -14,7 +14,7 @@
 // passes a workgroup barrier and increments the counter (relaxed, agent scope); a
 // consumer polls the counter, passes a barrier and reads.  Dependencies point only
 // to earlier stages and every workgroup is resident (one per CU, grid = CU count),
-// so every wait ends; each wait is also bounded (spin limit) and on expiry sets a
+// so every wait ends; each wait is also bounded (a deadline) and on expiry sets a
 // sticky error word that releases every other wait, so the launch always drains.
 // The last workgroup to finish resets the counters.
 #include "front_stages.h"
@@ -40,7 +40,7 @@ enum : int {
   SY_SPLIT = 96,   // [32] attention splits done, per row
   SY_ROUTE = 128,  // the routing's table and list are out (the down)
   SY_DONE = 130,   // workgroups finished (the last one resets)
-  SY_ERR,          // sticky: a wait ran out of its spin limit
+  SY_ERR,          // sticky: a wait passed its deadline
   SY_UV = 144,     // [K2_LANES] sub-counters each: merged + W_UV (row, head, half) tasks
   SY_OPROJ = SY_UV + K2_LANES,
   SY_ROUTER = SY_OPROJ + K2_LANES,
@@ -57,7 +57,7 @@ struct K2Dev {
   int* status;    // optional: the launch's error word
   uint64_t* timeline;  // optional: [grid][K2_STAMPS] s_memrealtime stamps (100 MHz)
   int rows;
-  int spin_limit;
+  uint32_t wait_ticks;  // a dependency wait's deadline (WaitClock ticks)
 };
 
 // timeline: per stage s, stamps 3s (enter), 3s+1 (first input ready), 3s+2 (leave);
@@ -135,6 +135,7 @@ MK2_DEV bool k2_wait(const K2Dev& p, int* seen, int line, int target, int stamp 
       return __builtin_amdgcn_readfirstlane(row16_sum_i32(lane < lanes ? c : 0));
     };
     int n = 0, c0 = poll();
+    WaitClock wc;
     while (true) {
       const int c1 = poll();
       v = count(c0);
@@ -147,7 +148,7 @@ MK2_DEV bool k2_wait(const K2Dev& p, int* seen, int line, int target, int stamp 
         bad = true;
         break;
       }
-      if (n > p.spin_limit) {
+      if (wc.expired(p.wait_ticks)) {
         if (lane == 0) atomicOr(k2_ctr(p, SY_ERR), 1);
         bad = true;
         break;
@@ -205,8 +206,8 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p, Front front) {
   if (threadIdx.x == 0) epoch = (uint32_t)ld_dev_i32(p.sync + SYNC_EPOCH);
   auto tag_of = [](uint32_t e) { return e + 1u ? e + 1u : 1u; };
   __syncthreads();
-  TagPoll tp{0u, p.spin_limit, k2_ctr(p, SY_ERR)};
-  // the stages in order; a wait that fails (its spin limit, or another workgroup's
+  TagPoll tp{0u, p.wait_ticks, k2_ctr(p, SY_ERR)};
+  // the stages in order; a wait that fails (its deadline, or another workgroup's
   // failure seen while polling) returns from the walk: the workgroup skips every task
   // left and goes straight to the counter reset (fail-stop)
   auto walk = [&]() {
@@ -245,7 +246,7 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p, Front front) {
       const int r = t / nchk;
       if (!k2_wait(p, seen, SY_SCORE + r, nchk, t < G ? 3 * st + 1 : -1)) return;
       bool last = false;
-      const bool known = idx_slice<K2_NT>(p.idx, r, t % nchk, S.topk, p.spin_limit, k2_ctr(p, SY_ERR), tp.tag,
+      const bool known = idx_slice<K2_NT>(p.idx, r, t % nchk, S.topk, p.wait_ticks, k2_ctr(p, SY_ERR), tp.tag,
                                           [&] {
                                             if (sel_tasks)
                                               k2_signal(p, SY_SLICE + r);
@@ -452,11 +453,11 @@ static int current_cus(int* cus) {
 // front: the layer's front to run ahead of the stages in the same launch, or null;
 // front_key: its instantiation (FRONT_FUSED_*)
 int k2_persistent_enqueue(const IdxDev& idx, const MlaDev& mla, const MoeDev& moe, int* sync,
-                          int* status, uint64_t* timeline, int rows, int spin_limit, hipStream_t st,
+                          int* status, uint64_t* timeline, int rows, uint32_t wait_ticks, hipStream_t st,
                           const FrontPDev* front, int front_key) {
   int ncu = 0;
   if (const int rc = current_cus(&ncu)) return rc;
-  K2Dev p{idx, mla, moe, sync, status, timeline, rows, spin_limit};
+  K2Dev p{idx, mla, moe, sync, status, timeline, rows, wait_ticks};
   const bool two = rows > 16;
   // one instantiation a column-group count and expert mode (and, with the front ahead,
   // front shape)
@@ -508,7 +509,7 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_block(K2Dev p) {
     s_tag = e ? e : 1u;
   }
   __syncthreads();
-  const TagPoll tp{s_tag, p.spin_limit, k2_ctr(p, SY_ERR)};
+  const TagPoll tp{s_tag, p.wait_ticks, k2_ctr(p, SY_ERR)};
   uint32_t sel_rows = 0;  // the rows whose select this workgroup ran
   auto walk = [&]() {
     int base = 0;
@@ -528,7 +529,7 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_block(K2Dev p) {
         const int r = t / nchk;
         if (!k2_wait(p, seen, SY_SCORE + r, nchk)) return;
         bool last = false;
-        const bool known = idx_slice<K2_NT>(p.idx, r, t % nchk, S.topk, p.spin_limit, k2_ctr(p, SY_ERR), tp.tag,
+        const bool known = idx_slice<K2_NT>(p.idx, r, t % nchk, S.topk, p.wait_ticks, k2_ctr(p, SY_ERR), tp.tag,
                                             [&] {
                                               if (sel_tasks)
                                                 k2_signal(p, SY_SLICE + r);
@@ -665,7 +666,7 @@ int k2_block_enqueue(int blk, const IdxDev* idx, const MlaDev* mla, const MoeDev
   if (moe) p.moe = *moe;
   p.sync = sync;
   p.rows = rows;
-  p.spin_limit = 1 << 20;
+  p.wait_ticks = DEFAULT_WAIT_TICKS;
   const bool two = rows > 16;
   auto launch = [&](auto kern) -> int {
     int per_cu = 0;

@@ -21,7 +21,7 @@ int moe_fill(const mk2_moe_args* a, MoeDev* d);
 size_t moe_carve(const mk2_moe_shape* s, void* base, MoeDev* d);
 int moe_enqueue(const MoeDev& d, hipStream_t st);
 int k2_persistent_enqueue(const IdxDev& idx, const MlaDev& mla, const MoeDev& moe, int* sync,
-                          int* status, uint64_t* timeline, int rows, int spin_limit, hipStream_t st,
+                          int* status, uint64_t* timeline, int rows, uint32_t wait_ticks, hipStream_t st,
                           const FrontPDev* front = nullptr, int front_key = 0);
 int front_pdev(const mk2_front_args* a, FrontPDev* d, int* key);
 
@@ -58,7 +58,8 @@ int layer_plan(const mk2_layer_args* a, void* ws, LayerPlan* L, size_t* bytes) {
   rc = moe_fill(&ma, &L->moe);
   if (rc) return rc;
   MK2_REQUIRE(a->mode == MK2_LAYER_PERSISTENT || a->mode == MK2_LAYER_STAGED, "layer: unknown mode %d", a->mode);
-  MK2_REQUIRE(a->spin_limit >= 0, "layer: spin_limit must be >= 0");
+  MK2_REQUIRE(a->wait_us >= 0 && a->wait_us <= MK2_MAX_WAIT_US, "layer: wait_us must be in [0, %d], got %d",
+              MK2_MAX_WAIT_US, a->wait_us);
   Carver c(ws);
   int* sync = c.take<int>(LAYER_SYNC_BYTES / 4);
   const size_t b_idx = idx_carve(&is, nullptr, nullptr);
@@ -177,7 +178,7 @@ extern "C" int mk2_layer_launch_static(const mk2_layer_args* a, mk2_stream_t str
   if (rc) return rc;
   if (a->mode == MK2_LAYER_PERSISTENT)
     return k2_persistent_enqueue(L.idx, L.mla, L.moe, L.sync, a->status, (uint64_t*)a->timeline,
-                                 a->mla.shape.rows, a->spin_limit ? a->spin_limit : (1 << 20), st);
+                                 a->mla.shape.rows, wait_ticks_of(a->wait_us), st);
   idx_enqueue(L.idx, st);
   mla_enqueue(L.mla, st);
   return moe_enqueue(L.moe, st);
@@ -218,7 +219,7 @@ extern "C" int mk2_layer_launch(const mk2_layer_args* a, mk2_stream_t stream) {
   if (a->mode == MK2_LAYER_PERSISTENT)
     return k2_persistent_enqueue(L.idx, L.mla, L.moe, L.sync, a->status, (uint64_t*)a->timeline,
                                  a->mla.shape.rows,
-                                 a->spin_limit ? a->spin_limit : (1 << 20), st);
+                                 wait_ticks_of(a->wait_us), st);
   idx_enqueue(L.idx, st);
   mla_enqueue(L.mla, st);
   return moe_enqueue(L.moe, st);
@@ -254,6 +255,7 @@ extern "C" int mk2_layer_step_launch(const mk2_front_args* f, const mk2_layer_ar
               "cache and cache_scale");
   rc = layer_plan(a, a->workspace, &L, &need);
   if (rc) return rc;
+  fd.wait_ticks = wait_ticks_of(a->wait_us);  // the front's waits share the layer's deadline
   return k2_persistent_enqueue(L.idx, L.mla, L.moe, L.sync, a->status, (uint64_t*)a->timeline, a->mla.shape.rows,
-                               a->spin_limit ? a->spin_limit : (1 << 20), (hipStream_t)stream, &fd, key);
+                               wait_ticks_of(a->wait_us), (hipStream_t)stream, &fd, key);
 }

@@ -307,6 +307,33 @@ struct NoMark {
 // every memory access of this thread has completed (stores are device-visible)
 MK2_DEV void drain_memory() { __builtin_amdgcn_s_waitcnt(0); }
 
+// ------------------------------------------------------------------ wait deadlines
+// A dependency wait inside a persistent launch gives up once its deadline has passed
+// on the constant 100 MHz s_memrealtime clock, counted from its first poll round that
+// found the dependency unmet (a wait met at once reads no clock).  The differences are
+// 32-bit ticks, so a deadline is at most MK2_MAX_WAIT_US.  A deadline, unlike a poll
+// count, does not stretch when the polls slow down under contention.
+constexpr uint32_t WAIT_TICKS_PER_US = 100;
+constexpr uint32_t DEFAULT_WAIT_TICKS = 1000000u * WAIT_TICKS_PER_US;  // one second
+struct WaitClock {
+  uint32_t t0 = 0;
+  bool started = false;
+  // false on the first call (which starts the clock), then whether `ticks` have passed
+  MK2_DEV bool expired(uint32_t ticks) {
+    const uint32_t now = (uint32_t)__builtin_amdgcn_s_memrealtime();
+    if (!started) {
+      started = true;
+      t0 = now;
+      return false;
+    }
+    return now - t0 > ticks;
+  }
+};
+// the ticks of a host-given deadline in microseconds (0: the default, one second)
+inline uint32_t wait_ticks_of(int wait_us) {
+  return wait_us > 0 ? (uint32_t)wait_us * WAIT_TICKS_PER_US : DEFAULT_WAIT_TICKS;
+}
+
 // ----------------------------------------------------------------- tagged hand-offs
 // A 32-bit value one workgroup hands to another inside a persistent launch can travel
 // with the launch's tag in the same 8-byte word, (tag << 32) | value, stored
@@ -319,9 +346,9 @@ MK2_DEV void drain_memory() { __builtin_amdgcn_s_waitcnt(0); }
 // shapes whose layouts differ) the caller clears them before each launch.  Between stream-ordered
 // kernels (one kernel a stage) the stream publishes the words: tag 0, read unchecked.
 struct TagPoll {
-  uint32_t tag;  // this launch's tag; 0: stream-ordered, no checking
-  int spin;      // polls before giving up
-  int* err;      // the launch's sticky error word (set on giving up, seen by every poller)
+  uint32_t tag;         // this launch's tag; 0: stream-ordered, no checking
+  uint32_t wait_ticks;  // a wait's deadline (WaitClock ticks)
+  int* err;             // the launch's sticky error word (set on giving up, seen by every poller)
 };
 MK2_DEV void st_pair(uint64_t* p, uint32_t v, uint32_t tag) {
   MK2_DEV_ST(uint64_t, p, ((uint64_t)tag << 32) | v);
@@ -329,11 +356,11 @@ MK2_DEV void st_pair(uint64_t* p, uint32_t v, uint32_t tag) {
 MK2_DEV uint64_t ld_pair(const uint64_t* p) { return MK2_DEV_LD(uint64_t, p); }
 MK2_DEV uint32_t pair_value(uint64_t w) { return (uint32_t)w; }
 MK2_DEV bool pair_ready(uint64_t w, const TagPoll& tp) { return tp.tag == 0 || (uint32_t)(w >> 32) == tp.tag; }
-// one wave's verdict after a poll round: all lanes ready (true), or keep polling; on
-// the spin limit or another poller's error the launch is failing: *bad = true
-MK2_DEV bool poll_done(bool ready, int polls, const TagPoll& tp, bool* bad) {
+// one wave's verdict after a poll round: all lanes ready (true), or keep polling; past
+// the wait's deadline or on another poller's error the launch is failing: *bad = true
+MK2_DEV bool poll_done(bool ready, int polls, WaitClock& wc, const TagPoll& tp, bool* bad) {
   if (__ballot(!ready) == 0) return true;
-  if (polls > tp.spin || ((polls & 31) == 0 && tp.err && ld_dev_i32(tp.err))) {
+  if (wc.expired(tp.wait_ticks) || ((polls & 31) == 0 && tp.err && ld_dev_i32(tp.err))) {
     if ((threadIdx.x & 63) == 0 && tp.err) atomicOr(tp.err, 1);
     *bad = true;
     return true;

@@ -87,11 +87,12 @@ MK2_DEV bool mla_split(const MlaDev& p, int r, int s, MlaSplitLds& L, const TagP
     if (p.tsel) {
       const uint64_t* src = p.tsel + (size_t)r * p.topk + s * MLA_SPLIT + tid;
       uint64_t w = ld_pair(src);
+      WaitClock wc;
       for (int polls = 1;; polls += 2) {  // two polls in flight
         const uint64_t w1 = ld_pair(src);
-        if (poll_done(pair_ready(w, tp), polls, tp, &bad)) break;
+        if (poll_done(pair_ready(w, tp), polls, wc, tp, &bad)) break;
         w = ld_pair(src);
-        if (poll_done(pair_ready(w1, tp), polls + 1, tp, &bad)) {
+        if (poll_done(pair_ready(w1, tp), polls + 1, wc, tp, &bad)) {
           w = w1;
           break;
         }

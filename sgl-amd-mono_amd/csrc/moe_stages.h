@@ -459,6 +459,7 @@ MK2_DEV bool moe_route(const MoeDev& p, RouteLds& L, const TagPoll& tp, Mark mar
       constexpr int KU = 8;
       for (int kc0 = 0; kc0 < p.KC && !bad; kc0 += KU) {
         i32x4 t[2][KU];
+        WaitClock wc;
         for (int polls = 1;; ++polls) {
           bool ready = true;
 #pragma unroll
@@ -473,7 +474,7 @@ MK2_DEV bool moe_route(const MoeDev& p, RouteLds& L, const TagPoll& tp, Mark mar
 #pragma unroll
             for (int u = 0; u < KU; ++u)
               ready = ready && (tp.tag == 0 || ((uint32_t)t[i][u].y == tp.tag && (uint32_t)t[i][u].w == tp.tag));
-          if (poll_done(ready, polls, tp, &bad)) break;
+          if (poll_done(ready, polls, wc, tp, &bad)) break;
         }
 #pragma unroll
         for (int i = 0; i < 2; ++i)
@@ -591,9 +592,10 @@ MK2_DEV bool moe_route(const MoeDev& p, RouteLds& L, const TagPoll& tp, Mark mar
       const int i = min(i0 + tid, words - 1);
       const bool own = i / (2 * p.topk) >= r0 && i / (2 * p.topk) < r1;
       uint64_t w = 0;
+      WaitClock wc;
       for (int polls = 1;; ++polls) {
         w = own ? 0 : ld_pair(p.picks + i);
-        if (poll_done(own || pair_ready(w, tp), polls, tp, &bad)) break;
+        if (poll_done(own || pair_ready(w, tp), polls, wc, tp, &bad)) break;
       }
       if (i0 + tid < words && !own && !bad) {
         const int j = i >> 1;
@@ -982,11 +984,12 @@ MK2_DEV int slot_expert(const MoeDev& p, int j, const TagPoll& tp, int* lds, uin
     // two polls in flight: the next is issued before the last one is looked at
     const uint64_t* src = lane == 2 ? p.act_rows + j : p.act + (lane ? 1 + j : 0);
     uint64_t w = lane < nl ? ld_pair(src) : 0;
+    WaitClock wc;
     for (int polls = 1;; polls += 2) {
       const uint64_t w1 = lane < nl ? ld_pair(src) : 0;
-      if (poll_done(lane >= nl || pair_ready(w, tp), polls, tp, &bad)) break;
+      if (poll_done(lane >= nl || pair_ready(w, tp), polls, wc, tp, &bad)) break;
       w = lane < nl ? ld_pair(src) : 0;
-      if (poll_done(lane >= nl || pair_ready(w1, tp), polls + 1, tp, &bad)) {
+      if (poll_done(lane >= nl || pair_ready(w1, tp), polls + 1, wc, tp, &bad)) {
         w = w1;
         break;
       }

@@ -19,7 +19,8 @@ import torch  # noqa: F401  (must precede the CDLL load, see the module docstrin
 LIB_PATH = Path(__file__).resolve().parent / "libmk2.so"
 
 MK2_OK, MK2_EINVAL, MK2_ELAUNCH, MK2_ENOSPACE = 0, 1, 2, 3
-ABI_VERSION = 3  # MK2_ABI_VERSION of the header these structures mirror
+ABI_VERSION = 4  # MK2_ABI_VERSION of the header these structures mirror
+MK2_MAX_WAIT_US = 40_000_000  # the longest dependency-wait deadline (mk2.h)
 MK2_KEYS_FP4, MK2_KEYS_FP8 = 0, 1
 MK2_WLAYOUT_TILES, MK2_WLAYOUT_AITER16 = 0, 1
 
@@ -104,7 +105,7 @@ class LayerArgs(ctypes.Structure):
         ("indexer", IndexerArgs), ("mla", MlaArgs), ("moe", MoeArgs),
         ("attn_out", c_void_p), ("out", c_void_p),
         ("workspace", c_void_p), ("workspace_bytes", c_size_t),
-        ("mode", c_int), ("spin_limit", c_int), ("status", c_void_p), ("timeline", c_void_p),
+        ("mode", c_int), ("wait_us", c_int), ("status", c_void_p), ("timeline", c_void_p),
     ]
 
 

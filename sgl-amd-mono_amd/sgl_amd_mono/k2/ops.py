@@ -71,7 +71,7 @@ def moe_activation_views(shape, workspace, base: int = 0) -> dict:
 
 def _block_status(workspace) -> int:
     """A block launch's sticky status word (nonzero: a dependency wait of a persistent
-    launch ran out of its spin limit; that launch's outputs are undefined).  Syncs."""
+    launch passed its deadline; that launch's outputs are undefined).  Syncs."""
     off = _lib.MK2_BLOCK_STATUS_OFFSET
     return int(workspace[off:off + 4].view(torch.int32).item())
 
@@ -214,8 +214,8 @@ class FrontOp:
         self.persistent = rc == 1 and not staged
 
     def status(self) -> int:
-        """The persistent launches' sticky status word (nonzero: a dependency wait ran
-        out of its spin limit; that launch's outputs are undefined).  Synchronizes."""
+        """The persistent launches' sticky status word (nonzero: a dependency wait passed
+        its deadline; that launch's outputs are undefined).  Synchronizes."""
         return int(self.status_word().item())
 
     def status_word(self):
@@ -389,14 +389,16 @@ class LayerOp:
     reduces, glm53/gfx950/runner.py:374-470)."""
 
     def __init__(self, cfg: C.K2Config, layer, rows: int, device=None, *, staged: bool = False,
-                 spin_limit: int = 0, static_scratch: bool = False):
+                 wait_us: int = 0, static_scratch: bool = False):
         """static_scratch: launch through mk2_layer_launch_static, whose scratch is the
         library's own device array (no workspace is allocated here, and a launch
         allocates nothing); launches of such ops that overlap on one GPU race."""
         cfg.validate(rows)
         self.cfg, self.rows, self.L = cfg, rows, layer
         self.mode = _lib.MK2_LAYER_STAGED if staged else _lib.MK2_LAYER_PERSISTENT
-        self.spin_limit = spin_limit
+        if not 0 <= wait_us <= _lib.MK2_MAX_WAIT_US:
+            raise ValueError(f"wait_us must be in [0, {_lib.MK2_MAX_WAIT_US}], got {wait_us}")
+        self.wait_us = wait_us  # a dependency wait's deadline (0: one second)
         self.device = torch.device(device or layer.h.device)
         self.idx = IndexerOp(cfg.indexer, rows, layer.idx.page_table.shape[1], self.device)
         self.mla = SparseMlaOp(cfg.mla, layer.mla, rows, layer.mla.page_table.shape[1], self.device)
@@ -437,7 +439,7 @@ class LayerOp:
         )
         ws = workspace
         return _lib.LayerArgs(ia, ma, ea, _p(attn_out), _p(out), _p(ws),
-                              0 if ws is None else ws.numel(), self.mode, self.spin_limit, _p(status),
+                              0 if ws is None else ws.numel(), self.mode, self.wait_us, _p(status),
                               _p(timeline))
 
     def __call__(self, out=None, *, attn_out=None, scores=None, topk=None, logits=None,

@@ -33,7 +33,7 @@ def test_every_declared_symbol_is_exported():
     assert len(names) >= 10
     for n in names:
         assert hasattr(L, n), n
-    assert L.mk2_abi_version() == _l.ABI_VERSION == 3
+    assert L.mk2_abi_version() == _l.ABI_VERSION == 4
 
 
 def test_ctypes_layouts_match_the_header():
@@ -47,9 +47,11 @@ int main(void) {
          sizeof(mk2_moe_args), sizeof(mk2_indexer_shape), sizeof(mk2_indexer_args),
          sizeof(mk2_mla_shape), sizeof(mk2_mla_args), sizeof(mk2_layer_args), sizeof(mk2_tail_args),
          sizeof(mk2_step_args), sizeof(mk2_front_shape), sizeof(mk2_front_weights), sizeof(mk2_front_args));
-  printf("%zu %zu %zu %zu %zu %zu %zu\n", offsetof(mk2_moe_args, logits), offsetof(mk2_mla_args, o_latent),
+  printf("%zu %zu %zu %zu %zu %zu %zu %zu\n", offsetof(mk2_moe_args, logits), offsetof(mk2_mla_args, o_latent),
          offsetof(mk2_layer_args, workspace_bytes), offsetof(mk2_indexer_shape, key_fmt),
-         offsetof(mk2_tail_args, normed), offsetof(mk2_step_args, ids_in_bytes), offsetof(mk2_step_args, ctx_len));
+         offsetof(mk2_tail_args, normed), offsetof(mk2_step_args, ids_in_bytes), offsetof(mk2_step_args, ctx_len),
+         offsetof(mk2_layer_args, wait_us));
+  printf("%d %d %d\n", MK2_MAX_WAIT_US, MK2_BLOCK_STATUS_OFFSET, MK2_FRONT_STATUS_OFFSET);
   return 0;
 }
 '''
@@ -66,7 +68,10 @@ int main(void) {
     assert sizes == mine
     assert offs == [_l.MoeArgs.logits.offset, _l.MlaArgs.o_latent.offset,
                     _l.LayerArgs.workspace_bytes.offset, _l.IndexerShape.key_fmt.offset,
-                    _l.TailArgs.normed.offset, _l.StepArgs.ids_in_bytes.offset, _l.StepArgs.ctx_len.offset]
+                    _l.TailArgs.normed.offset, _l.StepArgs.ids_in_bytes.offset, _l.StepArgs.ctx_len.offset,
+                    _l.LayerArgs.wait_us.offset]
+    consts = [int(x) for x in out[2].split()]
+    assert consts == [_l.MK2_MAX_WAIT_US, _l.MK2_BLOCK_STATUS_OFFSET, _l.MK2_FRONT_STATUS_OFFSET]
 
 
 def _moe_shape(_l, **kw):

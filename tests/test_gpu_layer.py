@@ -216,7 +216,7 @@ def test_persistent_layer_one_workspace_new_inputs():
 
 
 def test_persistent_layer_fail_stop():
-    """A launch whose dependency waits may poll only a couple of times (spin limit 1)
+    """A launch whose dependency waits have a deadline of one microsecond (wait_us=1)
     gives up: every workgroup skips the tasks it has left (fail-stop, as the
     reference's guard stops a launch) and the launch ORs 1 into the op's sticky status
     word, which LayerOp.check() turns into an error.  The stopped launch leaves the
@@ -230,14 +230,14 @@ def test_persistent_layer_fail_stop():
     dev = _dev()
     cfg = C.C5_LAYER
     L = synth.make_layer(cfg, 8, 779, dev)
-    op = LayerOp(cfg, L, 8, device=dev, spin_limit=1)
+    op = LayerOp(cfg, L, 8, device=dev, wait_us=1)
     ref = LayerOp(cfg, L, 8, device=dev, staged=True)().clone()
     for _ in range(2):  # two stops in a row: the second starts from the first's leftovers
-        op.spin_limit = 1
+        op.wait_us = 1
         op()
         torch.cuda.synchronize()
         assert int(op.status.item()) == 1
-        op.spin_limit = 0  # the default limit
+        op.wait_us = 0  # the default deadline, one second
         outs = [op().clone() for _ in range(2)]
         torch.cuda.synchronize()
         assert int(op.status.item()) == 1, "a completed launch must not clear the sticky word"

@@ -107,8 +107,8 @@ def test_shuffled_experts_step_matches_row_major(experts):
 
 
 def test_stopped_layer_gives_no_token():
-    """A layer launch that stops early (its dependency wait given a spin limit of one
-    poll, so it gives up from the host's setting and every kernel exits normally) makes
+    """A layer launch that stops early (its dependency waits given a deadline of one
+    microsecond, so one gives up from the host's setting and every kernel exits normally) makes
     the step's logits NaN and the eager forward raise; once the words are cleared, the
     next step runs clean on the same ops and workspaces."""
     from sgl_amd_mono import _registry as reg
@@ -126,7 +126,7 @@ def test_stopped_layer_gives_no_token():
     fwd.forward(plan, st.input_ids, st.positions, st.forward_batch)  # builds the ops; a clean step
     torch.cuda.synchronize()
     _, lo = fwd.ops(1, rows)
-    lo.spin_limit = 1
+    lo.wait_us = 1
     _, logits = fwd.backbone(plan, st.input_ids, st.positions, st.forward_batch)
     torch.cuda.synchronize()
     assert int(fwd._status.item()) == 1
@@ -135,7 +135,7 @@ def test_stopped_layer_gives_no_token():
         fwd.check(rows)  # clears the words
     with pytest.raises(RuntimeError, match="stopped early"):
         fwd.forward(plan, st.input_ids, st.positions, st.forward_batch)
-    lo.spin_limit = 0
+    lo.wait_us = 0
     logits = fwd.forward(plan, st.input_ids, st.positions, st.forward_batch)
     torch.cuda.synchronize()
     assert bool(torch.isfinite(logits).all())

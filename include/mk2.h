@@ -179,10 +179,17 @@ int mk2_moe_workspace_layout(const mk2_moe_shape* shape, mk2_moe_ws_layout* layo
  *    16 tokens x 16 dims -- token t's dim d at byte (t / 16) * 2048 + (d / 16) * 256 +
  *    (t % 16) * 16 + d % 16 (kernel.py:698-705) -- then 64 f32 scales, token t's at
  *    byte 8192 + 4 t; a key is its values times its scale.  cache_scale is NULL.
+ *  MK2_KEYS_FP4_Q4: the FP4 index plane as MK2_KEYS_FP4, scored against the queries
+ *    quantized to MXFP4 in the kernel (E2M1 with an E8M0 per 32 dims by the rule of
+ *    quantize_fp4_indexer_row, deepseek_v41/gfx950/attention/index_query.py:283-293)
+ *    on the FP4 x FP4 scaled MFMA, as the reference's verify-width scorer
+ *    (deepseek_v41/gfx950/indexer/score_fp4.py:254-296).  A contract of its own: the
+ *    scores are those of the quantized queries.
  * Page table int32 [requests][table_stride], logical page -> physical page.  Row r
  * scores the context positions 0 .. ctx_len[r]-1 of request req_ids[r]. */
 #define MK2_KEYS_FP4 0
 #define MK2_KEYS_FP8 1
+#define MK2_KEYS_FP4_Q4 2
 
 typedef struct mk2_indexer_shape {
   int rows;        /* 1..32 */
@@ -191,7 +198,7 @@ typedef struct mk2_indexer_shape {
   int topk;        /* multiple of 64, 64..4096 */
   int max_ctx;     /* upper bound of ctx_len, <= 65536, multiple of 64 */
   int table_stride;/* page table row stride (entries) */
-  int key_fmt;     /* MK2_KEYS_*: the index cache's format */
+  int key_fmt;     /* MK2_KEYS_*: the index cache's format (and, FP4_Q4, the queries') */
 } mk2_indexer_shape;
 
 typedef struct mk2_indexer_args {

@@ -24,6 +24,10 @@ Formats (all little-endian bytes):
     (kernel.py:3134-3147); a page holds 64 x 128 values in 16 x 16 tiles -- byte b is
     token (b // 2048) * 16 + (b % 256) // 16 (glm53/check.py:75-82), dim
     ((b % 2048) // 256) * 16 + b % 16 -- then the 64 keys' f32 scales.
+  * MXFP4 index queries (the FP4 x FP4 scorer's): E2M1 codes with one E8M0 per 32
+    dims; the E8M0 is the ceil-power-of-two exponent of max(f32(amax / 6), f32(1e-4)),
+    clamped to [1, 254], and a value that rounds to zero keeps no sign
+    (deepseek_v41/gfx950/attention/index_query.py:217-227,283-293).
   * radix key: the order-preserving u32 of f32 score bits (glm53/check.py:111-114).
 
 Every function here is pinned by tests/test_oracle_codecs.py (closed forms, brute
@@ -130,6 +134,30 @@ def mxfp4_quant(x: torch.Tensor):
     q = (blocks * inv[..., None]).clamp(-FP4_MAX, FP4_MAX)
     codes = e2m1_encode(q).reshape(shp)
     return fp4_pack(codes), code.to(torch.uint8)
+
+
+def fp4_query_scale_code(amax: torch.Tensor) -> torch.Tensor:
+    """E8M0 of a 32-dim group of index queries: the smallest power of two >=
+    max(f32(amax / 6), f32(1e-4)) -- the IEEE quotient, not a product with f32(1/6) --
+    clamped to [1, 254] (index_query.py:286-291)."""
+    v = _f32(amax) / torch.tensor(FP4_MAX, dtype=torch.float32)
+    v = torch.maximum(v, torch.tensor(1.0e-4, dtype=torch.float32))
+    return _ceil_pow2_code(v).clamp(1, 254)
+
+
+def fp4_query_quant(x: torch.Tensor):
+    """[..., K] f32 -> (bytes [..., K/2], E8M0 [..., K/32]), K % 32 == 0:
+    quantize_fp4_indexer_row (index_query.py:283-293).  Codes are the E2M1 of
+    x * 2^(127 - e), saturating at 6, ties to the even code (_e2m1_code,
+    index_query.py:217-227), and a value that rounds to zero gets code 0."""
+    x = _f32(x)
+    shp = x.shape
+    blocks = x.reshape(*shp[:-1], shp[-1] // 32, 32)
+    code = fp4_query_scale_code(blocks.abs().amax(-1))
+    inv = torch.exp2(127.0 - code.to(torch.float32))  # exact: a power of two
+    c = e2m1_encode((blocks * inv[..., None]).clamp(-FP4_MAX, FP4_MAX))
+    c = torch.where((c & 7) == 0, torch.zeros_like(c), c).reshape(shp)
+    return fp4_pack(c), code.to(torch.uint8)
 
 
 def mxfp4_dequant(b: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:

@@ -10,7 +10,8 @@
 namespace mk2 {
 
 constexpr int IDX_NT = 512;
-static_assert(IDX_KEYS_FP4 == MK2_KEYS_FP4 && IDX_KEYS_FP8 == MK2_KEYS_FP8, "key formats");
+static_assert(IDX_KEYS_FP4 == MK2_KEYS_FP4 && IDX_KEYS_FP8 == MK2_KEYS_FP8 && IDX_KEYS_FP4Q == MK2_KEYS_FP4_Q4,
+              "key formats");
 
 __global__ __launch_bounds__(256) void k_idx_clear(IdxDev p) {
   for (int i = blockIdx.x * 256 + threadIdx.x; i < p.rows * IDX_BINS; i += gridDim.x * 256) p.hist[i] = 0;
@@ -54,8 +55,8 @@ int idx_check_shape(const mk2_indexer_shape* s) {
   MK2_REQUIRE(s->max_ctx >= 64 && s->max_ctx <= TOPK_MAXN && s->max_ctx % 64 == 0,
               "indexer: max_ctx must be a multiple of 64 in [64, %d], got %d", TOPK_MAXN, s->max_ctx);
   MK2_REQUIRE(s->table_stride >= s->max_ctx / 64, "indexer: table_stride %d < max_ctx / 64", s->table_stride);
-  MK2_REQUIRE(s->key_fmt == MK2_KEYS_FP4 || s->key_fmt == MK2_KEYS_FP8,
-              "indexer: key_fmt must be MK2_KEYS_FP4 or MK2_KEYS_FP8, got %d", s->key_fmt);
+  MK2_REQUIRE(s->key_fmt == MK2_KEYS_FP4 || s->key_fmt == MK2_KEYS_FP8 || s->key_fmt == MK2_KEYS_FP4_Q4,
+              "indexer: key_fmt must be MK2_KEYS_FP4, MK2_KEYS_FP8 or MK2_KEYS_FP4_Q4, got %d", s->key_fmt);
   return MK2_OK;
 }
 
@@ -88,7 +89,7 @@ int idx_fill(const mk2_indexer_args* a, IdxDev* d) {
   if (rc) return rc;
   MK2_REQUIRE(a->q && a->w && a->cache && a->page_table && a->req_ids && a->ctx_len,
               "indexer: q, w, cache, page_table, req_ids and ctx_len must be set");
-  if (a->shape.key_fmt == MK2_KEYS_FP4)
+  if (a->shape.key_fmt != MK2_KEYS_FP8)
     MK2_REQUIRE(a->cache_scale != nullptr, "indexer: the FP4 index plane needs cache_scale");
   else
     MK2_REQUIRE(a->cache_scale == nullptr, "indexer: the FP8 index cache holds its scales; cache_scale must be NULL");

@@ -10,6 +10,11 @@
 // (16 columns) against all heads as A (16 heads a tile).  The head sum runs in the
 // lanes: a lane holds 4 heads of each head group for one key; every four groups,
 // three row-swapping permutes combine the four lane groups' sums of all four at once.
+// With FP4 queries (IDX_KEYS_FP4Q, the verify-width variant after the reference's
+// FP4 x FP4 scorer, deepseek_v41/gfx950/indexer/score_fp4.py:254-296) a task quantizes
+// its row's queries to MXFP4 in LDS (quantize_fp4_indexer_row's rule,
+// deepseek_v41/gfx950/attention/index_query.py:283-293) and a head group's 16 x 16 x
+// 128 product is one scaled MFMA on the plane's codes and scales as they load.
 //
 // top-k, three stages over the order-preserving u32 keys of the scores:
 //   score (row, chunk)  also counts its keys into the row's two-level histogram: 4096
@@ -41,7 +46,9 @@ constexpr int IDX_PAGE_CODES = 64 * 64;
 constexpr int IDX_PAGE_SCALES = 64 * 4;
 // index cache formats (MK2_KEYS_*); an FP8 page: 64 x 128 E4M3 values in 16 x 16
 // tiles, then the 64 tokens' f32 scales
-constexpr int IDX_KEYS_FP4 = 0, IDX_KEYS_FP8 = 1;
+// IDX_KEYS_FP4Q: the FP4 plane against the queries quantized to MXFP4 (a contract of
+// its own: the scores are those of the quantized queries)
+constexpr int IDX_KEYS_FP4 = 0, IDX_KEYS_FP8 = 1, IDX_KEYS_FP4Q = 2;
 constexpr int IDX_FP8_PAGE = 64 * 132;
 constexpr int IDX_FP8_VALUES = 64 * 128;
 constexpr int IDX_CHUNK = 2048;                    // positions a score task
@@ -55,8 +62,8 @@ struct IdxDev {
   const bf16_t* q;      // [rows][heads][128]
   const bf16_t* w;      // [rows][heads]
   int kfmt;             // IDX_KEYS_*
-  const uint8_t* cache; // FP4: E2M1 plane [pages][4][64][16 B]; FP8: pages [64][132]
-  const uint8_t* cscale;// FP4: E8M0 plane [pages][4][64]; FP8: unused
+  const uint8_t* cache; // FP4, FP4Q: E2M1 plane [pages][4][64][16 B]; FP8: pages [64][132]
+  const uint8_t* cscale;// FP4, FP4Q: E8M0 plane [pages][4][64]; FP8: unused
   const int* pt;        // [requests][stride]
   const int* req;       // [rows]
   const int* ctx;       // [rows]
@@ -94,7 +101,8 @@ MK2_DEV ListOut list_out(const IdxDev& p, int r, uint32_t tag) {
 struct IdxScoreLds {
   int pages[IDX_CHUNK / 64];
   int hist[IDX_BINS];
-  bf16_t q[64 * IDX_QROW];  // the row's queries, [head][128] (padded rows)
+  bf16_t q[64 * IDX_QROW];  // the row's queries, [head][128] (padded rows); FP4Q: their
+                            // E2M1 codes [head][64 B], then E8M0 [head][4]
   bf16_t w[64];             // its head weights
   float sc[IDX_CHUNK];      // the chunk's scores, stored once the loop is done
 };
@@ -112,6 +120,7 @@ struct IdxScoreLds {
 template <int NT, int KF>
 MK2_DEV void idx_score_keys(const IdxDev& p, int r, int chunk, IdxScoreLds& L, float* keep) {
   constexpr bool F8 = KF == IDX_KEYS_FP8;
+  constexpr bool Q4 = KF == IDX_KEYS_FP4Q;
   constexpr int NW = NT / 64;
   constexpr int GPW = IDX_CHUNK / 16 / NW;  // 16-key groups a wave
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, c16 = lane & 15;
@@ -137,10 +146,37 @@ MK2_DEV void idx_score_keys(const IdxDev& p, int r, int chunk, IdxScoreLds& L, f
     const int pg = (k_begin >> 6) + threadIdx.x;
     lds_pages[threadIdx.x] = pg * 64 < k_end ? p.pt[(size_t)req * p.stride + pg] : 0;
   }
+  static_assert(QPT * NT >= 64 * 16, "the pieces cover 64 heads");
+  if constexpr (Q4) {
+    // MXFP4 queries: piece i is dims 8 (i % 16) .. + 7 of head i / 16 (zero past the
+    // row's heads); a 32-dim group's four pieces sit in one DPP quad of lanes
+    uint8_t* qc = (uint8_t*)L.q;
 #pragma unroll
-  for (int u = 0; u < QPT; ++u) {
-    const int i = threadIdx.x + u * NT;
-    if (i < p.heads * 16) *(uint4*)(L.q + (i >> 4) * IDX_QROW + (i & 15) * 8) = qv[u];
+    for (int u = 0; u < QPT; ++u) {
+      const int i = threadIdx.x + u * NT;
+      const uint32_t wd[4] = {qv[u].x, qv[u].y, qv[u].z, qv[u].w};
+      float f[8];
+      float m = 0.f;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        f[2 * k] = __uint_as_float(wd[k] << 16);
+        f[2 * k + 1] = __uint_as_float(wd[k] & 0xFFFF0000u);
+        m = fmaxf(m, fmaxf(fabsf(f[2 * k]), fabsf(f[2 * k + 1])));
+      }
+      m = fmaxf(m, dpp_f32<DPP_XOR1>(m));
+      m = fmaxf(m, dpp_f32<DPP_XOR2>(m));
+      const uint32_t code = fp4_query_code(m);
+      if (i < 64 * 16) {
+        *(uint32_t*)(qc + (i >> 4) * 64 + (i & 15) * 4) = f32x8_to_e2m1x8(f, code);
+        if ((i & 3) == 0) qc[64 * 64 + (i >> 4) * 4 + ((i & 15) >> 2)] = (uint8_t)code;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < QPT; ++u) {
+      const int i = threadIdx.x + u * NT;
+      if (i < p.heads * 16) *(uint4*)(L.q + (i >> 4) * IDX_QROW + (i & 15) * 8) = qv[u];
+    }
   }
   if (threadIdx.x < p.heads) L.w[threadIdx.x] = wv;
   for (int b = threadIdx.x; b < IDX_BINS; b += NT) L.hist[b] = 0;
@@ -191,23 +227,39 @@ MK2_DEV void idx_score_keys(const IdxDev& p, int r, int chunk, IdxScoreLds& L, f
 #pragma unroll
   for (int j = 0; j < KWIN; ++j) issue(j);
   const int nhg = p.heads >> 4;
-  // A operands: q of head 16*hg + c16, dims 32g + 8s .. +7; head weights of rows 4g+i
+  // A operands: q of head 16*hg + c16, dims 32g + 8s .. +7 (FP4Q: dims 32g .. 32g + 31
+  // as codes, and their E8M0); head weights of rows 4g+i
   bf16x8 qa[4][4];
+  i32x8 qa4[4];
+  int qs4[4];
   float wt[4][4];
+  if constexpr (Q4) {
+    const uint8_t* qc = (const uint8_t*)L.q;
+#pragma unroll
+    for (int hg = 0; hg < 4; ++hg) {
+      const uint4 c = *(const uint4*)(qc + (hg * 16 + c16) * 64 + 16 * g);
+      qa4[hg] = i32x8{(int)c.x, (int)c.y, (int)c.z, (int)c.w, 0, 0, 0, 0};
+      qs4[hg] = qc[64 * 64 + (hg * 16 + c16) * 4 + g];
+    }
+  }
 #pragma unroll
   for (int hg = 0; hg < 4; ++hg) {
     if (hg < nhg) {
       const bf16_t* qr = L.q + (hg * 16 + c16) * IDX_QROW + 32 * g;
+      if constexpr (!Q4) {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) qa[hg][s] = __builtin_bit_cast(bf16x8, *(const uint4*)(qr + 8 * s));
+        for (int s = 0; s < 4; ++s) qa[hg][s] = __builtin_bit_cast(bf16x8, *(const uint4*)(qr + 8 * s));
+      }
       const uint2 wv = *(const uint2*)(L.w + hg * 16 + 4 * g);
       wt[hg][0] = __uint_as_float(wv.x << 16);
       wt[hg][1] = __uint_as_float(wv.x & 0xFFFF0000u);
       wt[hg][2] = __uint_as_float(wv.y << 16);
       wt[hg][3] = __uint_as_float(wv.y & 0xFFFF0000u);
     } else {
+      if constexpr (!Q4) {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) qa[hg][s] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
+        for (int s = 0; s < 4; ++s) qa[hg][s] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
+      }
 #pragma unroll
       for (int i = 0; i < 4; ++i) wt[hg][i] = 0.f;
     }
@@ -241,6 +293,21 @@ MK2_DEV void idx_score_keys(const IdxDev& p, int r, int chunk, IdxScoreLds& L, f
 #pragma unroll
       for (int hg = 0; hg < 4; ++hg) acc[hg] = mfma_bf16(qa[hg][q], kb[q], acc[hg]);
   };
+  // group j's MFMAs, its keys widened first (FP4Q: the codes as they are, with the
+  // key's E8M0 from byte j % 4 of the page's scale dword)
+  auto group = [&](int j, f32x4* acc) {
+    if constexpr (Q4) {
+      if (j >= 1 && j + KWIN - 1 < GPW) issue(j + KWIN - 1);
+      const i32x8 kb4 = {(int)code[j].x, (int)code[j].y, (int)code[j].z, (int)code[j].w, 0, 0, 0, 0};
+      const int ks = (int)(sw[j >> 2] >> (8 * (j & 3)));
+#pragma unroll
+      for (int hg = 0; hg < 4; ++hg) acc[hg] = mfma_same<4>(qa4[hg], kb4, f32x4{0.f, 0.f, 0.f, 0.f}, qs4[hg], ks);
+    } else {
+      bf16x8 kb[4];
+      keys(j, kb);
+      chain(kb, acc);
+    }
+  };
   // a lane's 16 heads of group j; every fourth group the four lane groups' sums are
   // combined for four groups at once, (g0 + g1) + (g2 + g3) as a single group's would
   // be, leaving group j - 3 + g's scores in lane group g: one store and one count a lane
@@ -271,24 +338,12 @@ MK2_DEV void idx_score_keys(const IdxDev& p, int r, int chunk, IdxScoreLds& L, f
   };
   static_assert(GPW % 2 == 0, "groups go in pairs");
   f32x4 acc0[4], acc1[4];
-  {
-    bf16x8 kb[4];
-    keys(0, kb);
-    chain(kb, acc0);
-  }
+  group(0, acc0);
 #pragma unroll
   for (int j = 0; j < GPW; j += 2) {
-    {
-      bf16x8 kb[4];
-      keys(j + 1, kb);
-      chain(kb, acc1);
-    }
+    group(j + 1, acc1);
     finish(j, acc0);
-    if (j + 2 < GPW) {
-      bf16x8 kb[4];
-      keys(j + 2, kb);
-      chain(kb, acc0);
-    }
+    if (j + 2 < GPW) group(j + 2, acc0);
     finish(j + 1, acc1);
   }
   __syncthreads();
@@ -325,6 +380,8 @@ template <int NT>
 MK2_DEV void idx_score(const IdxDev& p, int r, int chunk, IdxScoreLds& L, float* keep = nullptr) {
   if (p.kfmt == IDX_KEYS_FP8)
     idx_score_keys<NT, IDX_KEYS_FP8>(p, r, chunk, L, keep);
+  else if (p.kfmt == IDX_KEYS_FP4Q)
+    idx_score_keys<NT, IDX_KEYS_FP4Q>(p, r, chunk, L, keep);
   else
     idx_score_keys<NT, IDX_KEYS_FP4>(p, r, chunk, L, keep);
 }

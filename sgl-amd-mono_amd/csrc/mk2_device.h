@@ -143,6 +143,15 @@ MK2_DEV uint32_t f32x2_to_e2m1x2(float a, float b, uint32_t code) {
   const float sc = __uint_as_float(code ? code << 23 : 0x00400000u);
   return __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(0u, a, b, sc, 0) & 0xFFu;
 }
+// E8M0 of a 32-dim group of index queries quantized to MXFP4 (the reference's
+// quantize_fp4_indexer_row, deepseek_v41/gfx950/attention/index_query.py:283-291): the
+// smallest power of two >= max(amax / 6, 1e-4), the quotient rounded to f32 first,
+// clamped to [1, 254]
+MK2_DEV uint32_t fp4_query_code(float amax) {
+  const uint32_t b = __float_as_uint(fmaxf(amax / 6.0f, 1.0e-4f));
+  const uint32_t e = ((b >> 23) & 0xFFu) + ((b & 0x7FFFFFu) != 0u);
+  return e < 1u ? 1u : (e > 254u ? 254u : e);
+}
 // FP8 per-128 block scale (the reference's quant_scaled): scale = amax * f32(1/448)
 // and the multiplier 448 / amax (IEEE here, where the reference takes the hardware
 // reciprocal); 1 and 1 for an all-zero block

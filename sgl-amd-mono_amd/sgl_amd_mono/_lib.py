@@ -21,7 +21,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libmk2.so"
 MK2_OK, MK2_EINVAL, MK2_ELAUNCH, MK2_ENOSPACE = 0, 1, 2, 3
 ABI_VERSION = 4  # MK2_ABI_VERSION of the header these structures mirror
 MK2_MAX_WAIT_US = 40_000_000  # the longest dependency-wait deadline (mk2.h)
-MK2_KEYS_FP4, MK2_KEYS_FP8 = 0, 1
+MK2_KEYS_FP4, MK2_KEYS_FP8, MK2_KEYS_FP4_Q4 = 0, 1, 2
 MK2_WLAYOUT_TILES, MK2_WLAYOUT_AITER16 = 0, 1
 
 

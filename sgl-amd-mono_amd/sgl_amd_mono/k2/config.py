@@ -27,6 +27,9 @@ FP4_WEIGHT_FMTS = (FMT_MXFP4, FMT_A16W4, FMT_A4W4)
 # index cache formats (MK2_KEYS_*)
 KEYS_FP4 = 0  # SGLang's FP4 index plane: E2M1 codes + E8M0 per 32 dims, two tensors
 KEYS_FP8 = 1  # SGLang's DSA index cache: uint8 [pages, 64, 132], E4M3 + f32 scale a key
+# the FP4 plane scored against the queries quantized to MXFP4 in the kernel, on the
+# FP4 x FP4 scaled MFMA (the verify-width scorer; its scores are the quantized queries')
+KEYS_FP4_Q4 = 2
 # the expert weights' layouts (MK2_WLAYOUT_*)
 WLAYOUT_TILES = 0  # this build's tile packing (k2/packing.py pack_tiles / pack_e8m0)
 WLAYOUT_AITER16 = 1  # AITER's (16, 16) shuffle + e8m0_shuffle, as SGLang leaves them for AITER
@@ -119,7 +122,7 @@ class IndexerConfig:
     def validate(self, rows: int) -> None:
         if self.dim != 128:
             raise ValueError("index keys are 128 dims")
-        if self.keys not in (KEYS_FP4, KEYS_FP8):
+        if self.keys not in (KEYS_FP4, KEYS_FP8, KEYS_FP4_Q4):
             raise ValueError(f"unknown index cache format {self.keys}")
         if self.heads % 16 or not 16 <= self.heads <= 64:
             raise ValueError("index heads must be a multiple of 16 in [16, 64]")

@@ -129,7 +129,18 @@ def indexer_oracle_scores(ns, r):
     """f64 scores of row r of a synth indexer namespace."""
     n = int(ns.ctx_len[r])
     keys = index_keys_f32(ns.cache, ns.cache_scale, ns.page_table, int(ns.req_ids[r]), n)
-    return R.index_scores(cpu(ns.q[r]).float(), cpu(ns.w[r]).float(), keys)
+    return R.index_scores(index_queries(ns.cfg, ns.q[r]), cpu(ns.w[r]).float(), keys)
+
+
+def index_queries(cfg, q):
+    """A row's index queries as the scorer multiplies them: the bf16 values, or with
+    FP4 queries (KEYS_FP4_Q4) their MXFP4 quantization, dequantized."""
+    from sgl_amd_mono.k2 import config as C
+
+    q = cpu(q).float()
+    if cfg.keys == C.KEYS_FP4_Q4:
+        q = oc.mxfp4_dequant(*oc.fp4_query_quant(q))
+    return q
 
 
 def mla_oracle(ns, sel=None, h="auto", parts=False):
@@ -251,7 +262,7 @@ class CpuLayer:
         cfg = self.cfg
         sel = torch.full((self.rows, cfg.indexer.topk), -1, dtype=torch.int64)
         for r in range(self.rows):
-            s = R.index_scores(self.idx.q[r].float(), self.idx.w[r].float(), self.keys[r]).float()
+            s = R.index_scores(index_queries(cfg.indexer, self.idx.q[r]), self.idx.w[r].float(), self.keys[r]).float()
             lst = R.radix_lists(s, cfg.indexer.topk)
             sel[r, : lst.numel()] = lst
         _, attn = mla_oracle(self.mla, sel=sel, h=self.h)

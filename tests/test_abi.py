@@ -122,9 +122,13 @@ def test_launch_argument_errors_never_reach_the_device():
     ia.shape.key_fmt, ia.cache_scale = _l.MK2_KEYS_FP8, fake
     assert L.mk2_indexer_topk_launch(ctypes.byref(ia), None) == _l.MK2_EINVAL
     assert "cache_scale must be NULL" in L.mk2_last_error().decode()
-    ia.shape.key_fmt = 2
+    ia.shape.key_fmt = 3
     assert L.mk2_indexer_topk_launch(ctypes.byref(ia), None) == _l.MK2_EINVAL
     assert "key_fmt" in L.mk2_last_error().decode()
+    # FP4 queries score the FP4 plane: its scales are required as for MK2_KEYS_FP4
+    ia.shape.key_fmt, ia.cache_scale = _l.MK2_KEYS_FP4_Q4, None
+    assert L.mk2_indexer_topk_launch(ctypes.byref(ia), None) == _l.MK2_EINVAL
+    assert "cache_scale" in L.mk2_last_error().decode()
     assert L.mk2_layer_launch(None, None) == _l.MK2_EINVAL
     assert L.mk2_step_rows_launch(None, None) == _l.MK2_EINVAL
     sa = _l.StepArgs(width=33, rows=1, topk=2048)

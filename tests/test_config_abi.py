@@ -73,7 +73,7 @@ def test_indexer_validate_matches_c():
     seen = {True: 0, False: 0}
     for heads, topk, ctx, rows, keys in itertools.product(
         (8, 16, 48, 64, 80), (32, 64, 2048, 4096, 4160), (32, 64, 8192, 65536, 65600, 131072), (1, 32, 33),
-        (C.KEYS_FP4, C.KEYS_FP8, 2),
+        (C.KEYS_FP4, C.KEYS_FP8, C.KEYS_FP4_Q4, 3),
     ):
         cfg = replace(C.C4_INDEXER, heads=heads, topk=topk, context=ctx, keys=keys)
         s = _l.IndexerShape(rows, cfg.heads, cfg.dim, cfg.topk, cfg.context, max(1, cfg.context // C.PAGE), cfg.keys)

@@ -231,3 +231,52 @@ def test_indexer_fp8_cache_recent_cluster():
     _check_rows(cfg, ns, scores, topk, expect_clear=False)
     for r in range(2):
         assert int((topk[r] >= 65536 - 4096).sum()) > 1500
+
+
+# ----------------------------------- FP4 queries: the FP4 x FP4 scaled-MFMA scorer
+def _q4(cfg):
+    from dataclasses import replace
+
+    from sgl_amd_mono.k2 import config as C
+
+    return replace(cfg, keys=C.KEYS_FP4_Q4)
+
+
+@pytest.mark.parametrize("rows", [8, 32])
+def test_indexer_fp4_queries_full_context(rows):
+    """configs[3]'s shape with the queries quantized to MXFP4 in the kernel
+    (KEYS_FP4_Q4, quantize_fp4_indexer_row's rule) and scored on the FP4 x FP4 scaled
+    MFMA: scores within 1e-4 of the f64 oracle of the quantized queries (refs.
+    index_queries), the list exactly the radix-select list of the kernel's own scores,
+    at the decode and the verify width."""
+    from sgl_amd_mono.k2 import config as C
+
+    cfg = _q4(C.C4_INDEXER)
+    ns, scores, topk = _run(cfg, rows, seed=60 + rows)
+    _check_rows(cfg, ns, scores, topk, expect_clear=False)
+
+
+def test_indexer_fp4_queries_ragged_rows_fewer_heads():
+    """48 heads (the A operands of the absent fourth head group are zero codes) over
+    ragged and short rows."""
+    from sgl_amd_mono.k2 import config as C
+
+    cfg = _q4(C.IndexerConfig(heads=48, dim=128, topk=2048, context=8192))
+    ns, scores, topk = _run(cfg, 5, seed=62, ctx_len=[8192, 5003, 2049, 2048, 100])
+    _check_rows(cfg, ns, scores, topk)
+
+
+def test_indexer_fp4_queries_ties_and_zeros():
+    from sgl_amd_mono.k2 import config as C
+
+    cfg = _q4(C.IndexerConfig(heads=64, dim=128, topk=256, context=4096))
+    ns, scores, topk = _run(cfg, 2, seed=63, mode="ties")
+    for r in range(2):
+        assert torch.unique(scores[r]).numel() == 1
+        assert torch.equal(topk[r], torch.arange(256))
+    _check_rows(cfg, ns, scores, topk, expect_clear=False)
+    ns, scores, topk = _run(cfg, 2, seed=64, mode="zeros")
+    assert bool((scores == 0).all())
+    assert bool((oc.radix_keys(scores) == (1 << 31)).all())
+    for r in range(2):
+        assert torch.equal(topk[r], torch.arange(256))

@@ -87,6 +87,22 @@ def test_layer_verify_width_full_context():
     print(stats)
 
 
+@pytest.mark.parametrize("rows", [8, 32])
+def test_layer_fp4_queries(rows):
+    """configs[4] with the FP4 x FP4 index scorer (KEYS_FP4_Q4: the queries quantized to
+    MXFP4 in the kernel), at the decode and the verify width over the full context,
+    against the oracle of the quantized queries."""
+    from dataclasses import replace
+
+    from sgl_amd_mono.k2 import config as C
+
+    cfg = replace(C.C5_LAYER, indexer=replace(C.C5_LAYER.indexer, keys=C.KEYS_FP4_Q4))
+    L, res, olat = run_layer(cfg, rows, seed=560 + rows)
+    stats = check_layer(L, *res, o_latent=olat)
+    assert stats["attn_term_checked"] and stats["moe_term_checked"]
+    print(stats)
+
+
 @pytest.mark.parametrize("fmt", ["W8A8", "A16W4", "A4W4"])
 def test_layer_expert_modes(fmt):
     """The persistent layer with each further expert mode in the MoE stages."""

@@ -226,3 +226,64 @@ def test_index_pages_writer_and_reader_agree():
     assert torch.equal(oc.index_page_decode(pages), want)
     assert not torch.equal(_token_major_decode(pages), want)
     assert float((want - k).abs().max() / k.abs().amax()) < 2.0**-3
+
+
+def test_fp4_query_scale_rule():
+    """quantize_fp4_indexer_row's E8M0 (index_query.py:286-291): the ceil power of two
+    of f32(amax / 6), floored at f32(1e-4), clamped to [1, 254]."""
+    for k in (-8, -3, 0, 2, 5):
+        amax = torch.tensor([6.0 * 2.0**k])
+        assert int(oc.fp4_query_scale_code(amax)[0]) == 127 + k
+        above = torch.nextafter(amax, torch.tensor([1e30]))
+        assert int(oc.fp4_query_scale_code(above)[0]) == 127 + k + 1
+    # the floor: f32(1e-4) lies in (2^-14, 2^-13], so a zero or tiny group gets 2^-13
+    assert 2.0**-14 < float(torch.tensor(1e-4, dtype=torch.float32)) <= 2.0**-13
+    for amax in (0.0, 1e-30, 6e-4 * 0.5):
+        assert int(oc.fp4_query_scale_code(torch.tensor([amax]))[0]) == 127 - 13
+    # the keys' MXFP4 rule floors at 6 * 2^-126 instead: a plant of that rule differs
+    assert int(oc.mxfp4_scale_code(torch.tensor([0.0]))[0]) == 1
+    # the largest f32 group: 3.4e38 / 6 < 2^126, so finite inputs stay below the clamp
+    assert int(oc.fp4_query_scale_code(torch.tensor([torch.finfo(torch.float32).max]))[0]) == 253
+
+
+def test_fp4_query_quant_codes():
+    """Values on the grid come back exactly; a tie goes to the even code; beyond 6
+    saturates; a negative value that rounds to zero gets code 0, not 8
+    (_e2m1_code, index_query.py:217-227)."""
+    grid = torch.tensor(oc.E2M1_VALUES)
+    # a group of 32 with amax 6 (scale 2^0): every grid value and its negative exactly
+    x = torch.cat([grid, -grid, torch.tensor([6.0] * 16)])
+    b, s = oc.fp4_query_quant(x)
+    assert int(s[0]) == 127
+    assert torch.equal(oc.mxfp4_dequant(b, s), x)
+    # ties (midpoints of the grid) to the even code, and tiny negatives to +0
+    mids = torch.tensor([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0])
+    want = torch.tensor([0.0, 1.0, 1.0, 2.0, 2.0, 4.0, 4.0])
+    x = torch.cat([mids, -mids, torch.tensor([-0.1, -0.2, 6.0] + [0.0] * 15)])
+    b, s = oc.fp4_query_quant(x)
+    codes = oc.fp4_unpack(b)
+    assert torch.equal(oc.mxfp4_dequant(b, s)[:14], torch.cat([want, -want]))
+    assert int(codes[14]) == 0 and int(codes[15]) == 0  # no -0 code
+    # the scaled group: amax 6 * 2^3 -> scale 2^3, values quantized at that scale
+    x = torch.linspace(-48.0, 48.0, 32)
+    b, s = oc.fp4_query_quant(x)
+    assert int(s[0]) == 130
+    y = oc.mxfp4_dequant(b, s)
+    assert float((y - x).abs().max()) <= 8.0 * 1.0 + 1e-6  # half of the widest step (2) at 2^3
+
+
+def test_fp4_query_quant_matches_brute_force():
+    """Each code is the nearest grid value to x / 2^(e - 127), ties to the even code,
+    checked against an exhaustive nearest search in f64."""
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(64, 128, generator=g) * torch.exp2(torch.randint(-6, 6, (64, 1), generator=g).float())
+    b, s = oc.fp4_query_quant(x)
+    y = oc.mxfp4_dequant(b, s).double()
+    sc = oc.e8m0_value(s).double().repeat_interleave(32, -1)
+    v = (x.double() / sc).clamp(-6, 6)
+    grid = torch.tensor(oc.E2M1_VALUES, dtype=torch.float64)
+    d = (v.abs()[..., None] - grid).abs()
+    best = d.min(-1).values
+    # the kernel's value is one of the nearest grid points
+    got = (y / sc).abs()
+    assert torch.allclose((got - v.abs()).abs(), best, atol=0, rtol=0)

@@ -19,6 +19,7 @@ import os
 import statistics
 import sys
 import time
+from dataclasses import replace
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 for _p in (ROOT, os.path.join(ROOT, "sgl-amd-mono_amd"), os.path.join(ROOT, "tests")):
@@ -126,15 +127,21 @@ def pmc_summary(dirs, calib_bytes):
     return out
 
 
-def algorithmic_bytes(cfg, rows, distinct_experts):
+def algorithmic_bytes(cfg, rows, distinct_experts, key_positions=None, kv_rows=None):
     """HBM bytes a layer must move at least once: index keys
     of every request, the gathered latent-KV rows with their scales, W_UV and W_o,
     the router, the shared expert and each distinct routed expert's weights+scales,
-    plus queries and the top-k list."""
+    plus queries and the top-k list.  key_positions: the keys the requests hold (rows
+    of one request share them; default one full context a row); kv_rows: the distinct
+    (request, position) rows the top-k lists select (default rows x topk)."""
     ic, mc, ec = cfg.indexer, cfg.mla, cfg.moe
-    keys = rows * ic.context * (ic.dim // 2 + ic.dim // 32)
+    if key_positions is None:
+        key_positions = rows * ic.context
+    if kv_rows is None:
+        kv_rows = rows * mc.topk
+    keys = key_positions * (ic.dim // 2 + ic.dim // 32)
     idx_io = rows * ic.heads * ic.dim * 2 + rows * ic.heads * 2 + rows * ic.topk * 4
-    kv = rows * mc.topk * (mc.qk_dim + 4)
+    kv = kv_rows * (mc.qk_dim + 4)
     attn_w = mc.heads * mc.v_dim * mc.kv_lora * 2 + mc.hidden * mc.heads * mc.v_dim * 2
     q = rows * mc.heads * mc.qk_dim * 2
     router = ec.n_experts * ec.hidden * 2
@@ -381,7 +388,10 @@ def main():
     cfg, rows = C.C5_LAYER, args.rows
     extra = [int(r) for r in args.extra_rows.split(",") if r] if args.extra_rows else []
     extra = [r for r in extra if r != rows]
-    built = max([rows] + extra)
+    # widths above 8 rows are verify steps of 8 requests (8 x 4 draft tokens at 32
+    # rows, as configs[4] names it); the decode widths are views of one set of layers
+    verify = [r for r in extra if r > 8 and r % 8 == 0]
+    built = max([rows] + [r for r in extra if r not in verify])
     # the resident layers, built once at the widest width and viewed at each width
     layers = [synth.make_layer(cfg, built, seed=1000 + 17 * i, device=dev) for i in range(args.layers)]
     torch.cuda.synchronize()
@@ -404,13 +414,29 @@ def main():
     us, ms = head["us"], head["us"] / 1000.0
     gbs = head["algorithmic_bytes"] / (us * 1e-6) / 1e9
     widths = {}
-    for r in extra:
-        m = measure(cfg, [synth.view_rows(L, r) for L in layers], r, dev, args)
+
+    def width_entry(m, r, layout):
         g = m["algorithmic_bytes"] / (m["us"] * 1e-6) / 1e9
-        widths[str(r)] = {"us_per_layer": round(m["us"], 2), "tokens_per_s_per_layer": round(r / (m["us"] * 1e-6), 1),
-                          "algorithmic_bytes_per_layer": int(m["algorithmic_bytes"]), "hbm_gbps": round(g, 1),
-                          "roofline_frac": round(g / PEAK_HBM_GBS, 4), "distinct_experts": m["distinct"],
-                          "trials_us": m["trials_us"]}
+        return {"layout": layout, "us_per_layer": round(m["us"], 2),
+                "tokens_per_s_per_layer": round(r / (m["us"] * 1e-6), 1),
+                "algorithmic_bytes_per_layer": int(m["algorithmic_bytes"]), "hbm_gbps": round(g, 1),
+                "roofline_frac": round(g / PEAK_HBM_GBS, 4), "distinct_experts": m["distinct"],
+                "trials_us": m["trials_us"]}
+
+    for r in extra:
+        if r in verify:
+            vl = [synth.make_layer(cfg, r, seed=1000 + 17 * i, device=dev, draft=r // 8) for i in range(args.layers)]
+            layout = f"verify: 8 requests x {r // 8} draft tokens"
+            widths[str(r)] = width_entry(measure(cfg, vl, r, dev, args), r, layout)
+            # the same step with the FP4 x FP4 index scorer (queries quantized to MXFP4
+            # in the kernel: a contract of its own, not the bf16-query config)
+            q4 = replace(cfg, indexer=replace(cfg.indexer, keys=C.KEYS_FP4_Q4))
+            widths[f"{r}_fp4_queries"] = width_entry(measure(q4, vl, r, dev, args), r,
+                                                     layout + ", FP4 x FP4 index scores")
+            del vl
+        else:
+            m = measure(cfg, [synth.view_rows(L, r) for L in layers], r, dev, args)
+            widths[str(r)] = width_entry(m, r, f"decode: {r} requests x 1 token")
 
     result = {
         "metric": METRIC,
@@ -679,6 +705,19 @@ def _ops(cfg, views, rows, dev, staged):
     return ops, outs
 
 
+def _shared_rows(view, lists):
+    """(key positions, distinct latent-KV rows) a layer view's requests hold and select:
+    rows of one request share its keys (the longest row's context) and its selected
+    rows (the union of their lists)."""
+    req, ctx = view.idx.req_ids.cpu().tolist(), view.idx.ctx_len.cpu().tolist()
+    keys, kv = {}, {}
+    for r, (q, n) in enumerate(zip(req, ctx)):
+        keys[q] = max(keys.get(q, 0), n)
+        sel = lists[r][lists[r] >= 0].tolist()
+        kv.setdefault(q, set()).update(sel)
+    return sum(keys.values()), sum(len(s) for s in kv.values())
+
+
 def measure(cfg, views, rows, dev, args):
     """us per layer at `rows` rows: the layers' launches replayed from one HIP graph and
     timed with events on the launch stream (median of 5 trials).  The replays carry
@@ -688,12 +727,14 @@ def measure(cfg, views, rows, dev, args):
 
     ops, outs = _ops(cfg, views, rows, dev, args.staged)
     ids = [torch.empty(rows, cfg.moe.top_k, dtype=torch.int32, device=dev) for _ in ops]
-    for op, o, t in zip(ops, outs, ids):  # realized routing (distinct experts streamed)
-        op(o, topk_ids=t)
+    lists = [torch.empty(rows, cfg.indexer.topk, dtype=torch.int32, device=dev) for _ in ops]
+    for op, o, t, tk in zip(ops, outs, ids, lists):  # realized routing and selections
+        op(o, topk_ids=t, topk=tk)
     torch.cuda.synchronize()
     distinct = [int(torch.unique(t).numel()) for t in ids]
     eager = [o.clone() for o in outs]
-    nbytes = statistics.mean(algorithmic_bytes(cfg, rows, d) for d in distinct)
+    nbytes = statistics.mean(
+        algorithmic_bytes(cfg, rows, d, *_shared_rows(v, tk.cpu())) for d, v, tk in zip(distinct, views, lists))
     stream = torch.cuda.Stream()
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()

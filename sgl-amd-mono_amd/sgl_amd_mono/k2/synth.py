@@ -127,27 +127,33 @@ def index_pages_fp8(codes: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
     return torch.cat([tiles, sc], dim=1).view(P, 64, 132).contiguous()
 
 
-def make_indexer(cfg: C.IndexerConfig, rows: int, seed: int, device, ctx_len=None):
+def make_indexer(cfg: C.IndexerConfig, rows: int, seed: int, device, ctx_len=None, draft: int = 1):
     """Index-key pages in the config's format (FP4: E2M1 codes + E8M0 per 32 dims in the
     FP4 plane; FP8: the DSA pages, cache_scale None), bf16 queries and head weights ~
-    N(0, 1), one request a row."""
+    N(0, 1).  One request a row, or with draft > 1 a speculative verify step: rows
+    draft * i .. draft * i + draft - 1 are request i's draft tokens, at the context's
+    last draft positions (context lengths context - draft + 1 .. context), sharing the
+    request's pages."""
+    if draft < 1 or rows % draft:
+        raise ValueError(f"rows {rows} must be a multiple of draft {draft}")
     g = _gen(seed, device)
     ctx = cfg.context
     ppr = ctx // C.PAGE
+    reqs = rows // draft
     ns = SimpleNamespace(cfg=cfg, rows=rows)
     ns.q = _randn(g, rows, cfg.heads, cfg.dim, device=device).to(torch.bfloat16)
     ns.w = _randn(g, rows, cfg.heads, device=device).to(torch.bfloat16)
-    ns.page_table = _page_table(g, rows, ppr, device)
-    n_pages = rows * ppr + 1
+    ns.page_table = _page_table(g, reqs, ppr, device)
+    n_pages = reqs * ppr + 1
     keys = _randn(g, n_pages, C.PAGE, cfg.dim, device=device)
     if cfg.keys == C.KEYS_FP8:
         ns.cache, ns.cache_scale = index_pages_fp8(*quant_index_fp8(keys)), None
     else:
         codes, scales = quant_mxfp4(keys)  # [P, 64, 64], [P, 64, 4]
         ns.cache, ns.cache_scale = index_plane(codes, scales)
-    ns.req_ids = torch.arange(rows, dtype=torch.int32, device=device)
+    ns.req_ids = torch.arange(rows, dtype=torch.int32, device=device) // draft
     if ctx_len is None:
-        ctx_len = [ctx] * rows
+        ctx_len = [ctx - draft + 1 + r % draft for r in range(rows)]
     ns.ctx_len = torch.tensor(ctx_len, dtype=torch.int32, device=device)
     return ns
 
@@ -257,11 +263,12 @@ def make_tail(cfg: C.TailConfig, rows: int, seed: int, device):
     return ns
 
 
-def make_layer(cfg: C.K2Config, rows: int, seed: int, device, h_std: float = 1.0):
+def make_layer(cfg: C.K2Config, rows: int, seed: int, device, h_std: float = 1.0, draft: int = 1):
     """One chained layer: indexer keys and queries, latent-KV pages sharing the
     indexer's page table, attention weights, residual rows ~ N(0, h_std^2), MoE
-    weights with the post-attention RMSNorm weight."""
-    idx = make_indexer(cfg.indexer, rows, seed, device)
+    weights with the post-attention RMSNorm weight.  draft > 1: a verify step of
+    rows / draft requests with draft tokens each (make_indexer)."""
+    idx = make_indexer(cfg.indexer, rows, seed, device, draft=draft)
     mla = make_mla(cfg.mla, rows, seed + 1, device, residual=True, h_std=h_std)
     mla.page_table = idx.page_table
     mla.req_ids = idx.req_ids

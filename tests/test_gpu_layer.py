@@ -26,12 +26,12 @@ def _dev():
 H_STD = 1.0 / 128
 
 
-def run_layer(cfg, rows, seed, staged=False, h_std=H_STD):
+def run_layer(cfg, rows, seed, staged=False, h_std=H_STD, draft=1):
     from sgl_amd_mono.k2 import synth
     from sgl_amd_mono.k2.ops import LayerOp
 
     dev = _dev()
-    L = synth.make_layer(cfg, rows, seed, dev, h_std=h_std)
+    L = synth.make_layer(cfg, rows, seed, dev, h_std=h_std, draft=draft)
     op = LayerOp(cfg, L, rows, device=dev, staged=staged)
     status = torch.zeros(1, dtype=torch.int32, device=dev)
     H, E, K = cfg.mla.hidden, cfg.moe.n_experts, cfg.moe.top_k
@@ -82,6 +82,20 @@ def test_layer_verify_width_full_context():
     from sgl_amd_mono.k2 import config as C
 
     L, res, olat = run_layer(C.C5_LAYER, 32, seed=533)
+    stats = check_layer(L, *res, o_latent=olat)
+    assert stats["attn_term_checked"] and stats["moe_term_checked"]
+    print(stats)
+
+
+@pytest.mark.parametrize("staged", [False, True])
+def test_layer_verify_draft_layout(staged):
+    """configs[4]'s verify step as its config names it: 8 requests x 4 draft tokens
+    (32 rows, four a request sharing its index and latent-KV pages, at context lengths
+    65533 .. 65536), persistent and staged, against the oracle."""
+    from sgl_amd_mono.k2 import config as C
+
+    L, res, olat = run_layer(C.C5_LAYER, 32, seed=534, staged=staged, draft=4)
+    assert L.idx.req_ids.tolist() == [r // 4 for r in range(32)]
     stats = check_layer(L, *res, o_latent=olat)
     assert stats["attn_term_checked"] and stats["moe_term_checked"]
     print(stats)

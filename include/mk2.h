@@ -418,6 +418,11 @@ int mk2_front_is_persistent(const mk2_front_shape* shape);
  * two launches.  Reference: its K2 launch runs the front's stages ahead of the
  * layer's in one launch (glm53/gfx950/kernel.py:2585-3575). */
 int mk2_layer_step_launch(const mk2_front_args* front, const mk2_layer_args* layer, mk2_stream_t stream);
+/* 1: mk2_layer_step_launch has an instance for this front shape with experts of
+   expert_fmt (MK2_FMT_*); 0: launch the front and the layer on their own; < 0: an
+   invalid front shape (minus its MK2_E* code).  The serving host's choice; the
+   reference's K2 launch always carries its front (glm53/gfx950/kernel.py:2585-3575). */
+int mk2_layer_step_is_fused(const mk2_front_shape* shape, int expert_fmt);
 
 /* ------------------------------------------------------------------ tail
  * The steps after the last layer, on this GPU's rows of the LM head: the final

@@ -375,17 +375,22 @@ static FrontPDev front_pdev_of(const mk2_front_args* a, const FrontPrep& P) {
   return d;
 }
 
+// the front-and-layer launch's instantiation of a (checked) front shape, FRONT_FUSED_*
+static int front_fused_key(const mk2_front_shape* s) {
+  const FrontSteps k = front_steps(s);
+  const bool c7 = front_persistent_ok(s) && k.kua == 6 && k.kuc == 4 && k.ns == 6;
+  return !c7                                     ? FRONT_FUSED_NONE
+         : s->weight_fmt == MK2_WFMT_FP8_BLOCK   ? FRONT_FUSED_C7_FP8
+         : s->weight_fmt == MK2_WFMT_FP8_AITER16 ? FRONT_FUSED_C7_AITER16
+                                                 : FRONT_FUSED_NONE;
+}
+
 int front_pdev(const mk2_front_args* a, FrontPDev* d, int* key) {
   FrontPrep P;
   int rc = front_prepare(a, &P);
   if (rc) return rc;
   *d = front_pdev_of(a, P);
-  const FrontSteps k = front_steps(&a->shape);
-  const bool c7 = front_persistent_ok(&a->shape) && k.kua == 6 && k.kuc == 4 && k.ns == 6;
-  *key = !c7                                             ? FRONT_FUSED_NONE
-         : a->shape.weight_fmt == MK2_WFMT_FP8_BLOCK   ? FRONT_FUSED_C7_FP8
-         : a->shape.weight_fmt == MK2_WFMT_FP8_AITER16 ? FRONT_FUSED_C7_AITER16
-                                                       : FRONT_FUSED_NONE;
+  *key = front_fused_key(&a->shape);
   return MK2_OK;
 }
 
@@ -453,4 +458,11 @@ extern "C" int mk2_front_is_persistent(const mk2_front_shape* shape) {
   int rc = front_check_shape(shape);
   if (rc) return -rc;
   return front_persistent_ok(shape) ? 1 : 0;
+}
+
+extern "C" int mk2_layer_step_is_fused(const mk2_front_shape* shape, int expert_fmt) {
+  clear_error();
+  int rc = front_check_shape(shape);
+  if (rc) return -rc;
+  return front_fused_key(shape) != FRONT_FUSED_NONE && expert_fmt == MK2_FMT_MXFP4 ? 1 : 0;
 }

@@ -179,6 +179,7 @@ SIGNATURES = {
     "mk2_front_launch_staged": [POINTER(FrontArgs), c_void_p],
     "mk2_front_is_persistent": [POINTER(FrontShape)],
     "mk2_layer_step_launch": [POINTER(FrontArgs), POINTER(LayerArgs), c_void_p],
+    "mk2_layer_step_is_fused": [POINTER(FrontShape), c_int],
     "mk2_step_rows_launch": [POINTER(StepArgs), c_void_p],
     "mk2_write_seed_launch": [c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int, c_int, c_void_p],
     "mk2_abi_version": [],

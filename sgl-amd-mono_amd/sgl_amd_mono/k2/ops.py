@@ -213,6 +213,13 @@ class FrontOp:
         _lib.check(-rc if rc < 0 else _lib.MK2_OK)
         self.persistent = rc == 1 and not staged
 
+    def fuses_with(self, expert_fmt: int) -> bool:
+        """Whether the library runs this front and a layer with experts of expert_fmt
+        (C.FMT_*) as one launch (mk2_layer_step_is_fused; LayerStepOp)."""
+        rc = _lib.lib().mk2_layer_step_is_fused(ctypes.byref(self.shape), expert_fmt)
+        _lib.check(-rc if rc < 0 else _lib.MK2_OK)
+        return rc == 1 and self.persistent
+
     def status(self) -> int:
         """The persistent launches' sticky status word (nonzero: a dependency wait passed
         its deadline; that launch's outputs are undefined).  Synchronizes."""

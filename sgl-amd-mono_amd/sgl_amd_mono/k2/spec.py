@@ -131,7 +131,11 @@ class K2Forward:
         self.max_position = front_cfg.max_position
         self.pool_of = pool_of or _sglang_pool
         self.page_table_of = page_table_of or _sglang_page_table
-        self._ops, self._steps, self._tails, self._tables = {}, {}, {}, {}
+        self._ops, self._steps, self._tails, self._tables, self._fused = {}, {}, {}, {}, {}
+        # each layer's front and layer as ONE persistent launch where the library
+        # instantiates the front shape with these experts (mk2_layer_step_is_fused), as
+        # the reference's K2 launch carries its front; else two launches a layer
+        self.fuse_front = True
         # one sticky status word for every layer launch of a step (a persistent launch
         # whose dependency wait gave up ORs 1 into it; the fronts keep theirs in their
         # workspaces): a stopped launch's outputs are undefined, so a step with any
@@ -168,7 +172,7 @@ class K2Forward:
         """(FrontOp, LayerOp) of layer li at `rows` rows, created on first use with the
         layer's caches (kv, icache) and the shared row tables; the layer's input tensors
         are rebound every step."""
-        from .ops import FrontOp, LayerOp
+        from .ops import FrontOp, LayerOp, LayerStepOp
 
         key = (li, rows)
         if key not in self._ops:
@@ -186,8 +190,16 @@ class K2Forward:
             mla.kv, mla.kv_scale, mla.page_table, mla.req_ids = kv, None, tab.page_table, tab.req_ids
             L = SimpleNamespace(cfg=cfg, rows=rows, idx=idx, mla=mla, moe=self.moes[li],
                                 h=torch.empty(rows, cfg.mla.hidden, dtype=torch.bfloat16, device=dev))
-            self._ops[key] = (FrontOp(fc, self.fronts[li], rows, device=dev), LayerOp(cfg, L, rows, device=dev))
+            fo, lo = FrontOp(fc, self.fronts[li], rows, device=dev), LayerOp(cfg, L, rows, device=dev)
+            self._ops[key] = (fo, lo)
+            if fo.fuses_with(cfg.moe.expert_fmt):
+                self._fused[key] = LayerStepOp(fo, lo)
         return self._ops[key]
+
+    def fused(self, li: int, rows: int):
+        """The LayerStepOp (front and layer in one launch) of layer li at `rows` rows,
+        or None where the library has no such instance (or fuse_front is off)."""
+        return self._fused.get((li, rows)) if self.fuse_front else None
 
     def step_rows(self, rows: int):
         from .ops import StepRows
@@ -210,7 +222,8 @@ class K2Forward:
                                  if (li, rows) in self._ops]
 
     def backbone(self, plan, input_ids, positions, forward_batch):
-        """Every layer a front and a layer launch, then the tail: (normed rows, logits).
+        """Every layer one front-and-layer launch (or a front and a layer launch where
+        the library does not fuse the shape), then the tail: (normed rows, logits).
         The logits are NaN when any launch of the step stopped early (gate_logits)."""
         accepts = getattr(SPEC, "accepts", None)  # SGLang routes by the spec itself
         if accepts is not None:
@@ -231,10 +244,15 @@ class K2Forward:
             kv, icache = binding.layer_caches(pool, li, self.front_cfg.index_heads > 0)
             fo, lo = self.ops(li, S, kv, icache)
             L = lo.L
-            fo(h, st.positions, st.slots, self.cos_sin, kv, None, icache, None,
-               mla_q=L.mla.q, index_q=L.idx.q, index_w=L.idx.w)
             L.idx.cache, L.mla.kv, L.h = icache, kv, h
-            h = lo(out=plan.state.setdefault(("h", li % 2, S), torch.empty_like(h)), status=self._status)
+            out = plan.state.setdefault(("h", li % 2, S), torch.empty_like(h))
+            step = self.fused(li, S)
+            if step is not None:
+                h = step(st.positions, st.slots, self.cos_sin, out=out, status=self._status)
+            else:
+                fo(h, st.positions, st.slots, self.cos_sin, kv, None, icache, None,
+                   mla_q=L.mla.q, index_q=L.idx.q, index_w=L.idx.w)
+                h = lo(out=out, status=self._status)
         logits, normed = self.tail(S)(h)
         gate_logits(self.status_words(S), logits)
         return normed, logits

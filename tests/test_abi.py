@@ -143,14 +143,24 @@ def test_launch_argument_errors_never_reach_the_device():
     assert L.mk2_front_workspace_bytes(ctypes.byref(fs), ctypes.byref(n)) == _l.MK2_EINVAL
     assert "nope" in L.mk2_last_error().decode()
     assert L.mk2_front_is_persistent(ctypes.byref(fs)) == -_l.MK2_EINVAL
+    assert L.mk2_layer_step_is_fused(ctypes.byref(fs), 1) == -_l.MK2_EINVAL
     assert L.mk2_front_launch_staged(None, None) == _l.MK2_EINVAL
     fs.nope = 192
     assert L.mk2_front_workspace_bytes(ctypes.byref(fs), ctypes.byref(n)) == _l.MK2_OK and n.value > 0
     # the persistent front: its counters and status word lead the workspace
     assert n.value > _l.MK2_FRONT_STATUS_OFFSET
     assert L.mk2_front_is_persistent(ctypes.byref(fs)) == 1  # C7: hidden 6144, q_lora 2048, nope 192
+    # the front-and-layer launch: C7's front with A8W4 (MXFP4) experts only
+    assert L.mk2_layer_step_is_fused(ctypes.byref(fs), 1) == 1
+    assert [L.mk2_layer_step_is_fused(ctypes.byref(fs), f) for f in (0, 2, 3, 4)] == [0, 0, 0, 0]
+    fs.weight_fmt = 2  # block FP8 in AITER's layout: instanced too
+    assert L.mk2_layer_step_is_fused(ctypes.byref(fs), 1) == 1
+    fs.weight_fmt = 0  # bf16 front weights: not
+    assert L.mk2_layer_step_is_fused(ctypes.byref(fs), 1) == 0
+    fs.weight_fmt = 1
     fs.hidden = 4096  # K steps the persistent launch does not instantiate: the stage launches
     assert L.mk2_front_is_persistent(ctypes.byref(fs)) == 0
+    assert L.mk2_layer_step_is_fused(ctypes.byref(fs), 1) == 0
     assert L.mk2_tail_launch(None, None) == _l.MK2_EINVAL
     ta = _l.TailArgs(8, 6144, 0, 1e-5, fake, fake, fake, fake, None)
     assert L.mk2_tail_launch(ctypes.byref(ta), None) == _l.MK2_EINVAL

@@ -139,3 +139,37 @@ def test_stopped_layer_gives_no_token():
     logits = fwd.forward(plan, st.input_ids, st.positions, st.forward_batch)
     torch.cuda.synchronize()
     assert bool(torch.isfinite(logits).all())
+
+
+def test_fused_front_and_layer_step():
+    """A model with C7's front (hidden 6144, q_lora 2048, nope 192, 64 index heads) and
+    MXFP4 experts: the library fuses each layer's front with the layer
+    (mk2_layer_step_is_fused) and the routed step runs ONE launch a layer
+    (LayerStepOp); its logits and caches equal, bit for bit, those of the same step with
+    each front and layer launched apart."""
+    from sgl_amd_mono import _registry as reg
+    from sgl_amd_mono.k2 import spec
+
+    dev = _dev()
+    rows = 4
+    hf = SimpleNamespace(**{**vars(F.HF), "hidden_size": 6144, "q_lora_rank": 2048, "qk_nope_head_dim": 192,
+                            "index_n_heads": 64})
+    pages = rows * (hf.max_context // 64) + 8
+    res = []
+    for fuse in (True, False):
+        lm = F.make_model(71, dev, hf=hf, experts="mxfp4")
+        pool = F.Pool(F.LAYERS, pages, dev, 72)
+        st = F.make_step(rows, hf.max_context, pages, dev, 73)
+        ctx = SimpleNamespace(device=dev, pool_of=lambda fb, p=pool: p,
+                              page_table_of=lambda fb, n, s=st: s.page_table[:n])
+        fwd = spec.SPEC.build(lm, hf, ctx)
+        fwd.fuse_front = fuse
+        logits = fwd.forward(reg.Plan(key=reg.ShapeKey("decode", rows, 1)), st.input_ids, st.positions,
+                             st.forward_batch)
+        torch.cuda.synchronize()
+        assert all((fwd.fused(li, rows) is not None) == fuse for li in range(F.LAYERS))
+        res.append((cpu(logits), [cpu(t) for t in pool.kv], [cpu(t) for t in pool.idx]))
+    assert bool(torch.isfinite(res[0][0]).all())
+    assert torch.equal(res[0][0], res[1][0])
+    assert all(torch.equal(a, b) for a, b in zip(res[0][1], res[1][1]))
+    assert all(torch.equal(a, b) for a, b in zip(res[0][2], res[1][2]))

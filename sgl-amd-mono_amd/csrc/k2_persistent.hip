@@ -36,7 +36,8 @@ constexpr int K2_LANES = 16;
 enum : int {
   SY_SCORE = 0,    // [32] score chunks done, per row
   SY_SLICE = 32,   // [32] top-k slices counted out (their counts and bin keys out), per row
-  // lines 64 .. 95: unused (the splits poll the tagged top-k list)
+  SY_UPT = 64,     // the up/gate task tickets handed out (above 16 rows)
+  SY_UPW = 80,     // [K2_LANES] workgroups through the up/gate tasks (above 16 rows)
   SY_SPLIT = 96,   // [32] attention splits done, per row
   SY_ROUTE = 128,  // the routing's table and list are out (the down)
   SY_DONE = 130,   // workgroups finished (the last one resets)
@@ -164,6 +165,55 @@ MK2_DEV bool k2_wait(const K2Dev& p, int* seen, int line, int target, int stamp 
   return ok;
 }
 
+// The up/gate tasks (up_total of them: the shared expert's chunks, then the routed
+// slots' chunks in slot order) of this workgroup, the first at `first` (none when it
+// is >= up_total).  Up to 16 rows (NCG 1) the rotation gives a workgroup every G-th
+// task (a workgroup holds one or two; the layer's walk runs that loop in place).
+// Above 16 rows a workgroup runs several and a task's time varies with its slot's
+// rows, so after the first G the tasks go by ticket:
+// a workgroup takes its next one from the SY_UPT counter as it starts the current one
+// (the round trip overlaps the task) and stops at its first routed slot past the
+// routing's count -- the tickets go out in task order, so every task before that one
+// went to a workgroup that runs it.  Then every workgroup counts out on SY_UPW, which
+// the down waits for.  `next`: an LDS int.  False: the walk is failing.
+template <int NCG, int FMT>
+MK2_DEV bool k2_upgate_walk(const K2Dev& p, K2Lds& S, int* seen, int* next, int first, int nrt, const TagPoll& tp,
+                            int stamp) {
+  constexpr bool ticket = NCG == 2;
+  const int G = gridDim.x;
+  const int up_r = p.moe.Dmax * (p.moe.I / p.moe.UC);
+  const int up_sh = p.moe.n_shared * (p.moe.SI / 32);
+  const int up_total = up_r + up_sh;
+  for (int t = first, k = 0; t < up_total; ++k) {
+    // the ticket from a wave whose next wait is on its own weight loads, not a poll
+    int nxt = 0;
+    if (ticket && threadIdx.x == K2_NT - 64)
+      nxt = G + __hip_atomic_fetch_add(k2_ctr(p, SY_UPT), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (!k2_wait(p, seen, SY_ROUTER, nrt, k == 0 ? stamp : -1, K2_LANES)) return false;
+    const int rc = moe_upgate<K2_NT, NCG, FMT>(p.moe, t < up_sh ? up_r + t : t - up_sh, S.up.red, S.up.midf, tp);
+    if (rc < 0) return false;
+    if (!ticket) {
+      k2_signal(p, SY_UP, t, K2_LANES);
+      t += G;
+      continue;
+    }
+    if (rc == 0) break;
+    if (threadIdx.x == K2_NT - 64) *next = nxt;
+    __syncthreads();
+    t = *next;
+    __syncthreads();  // read before the next task's write
+  }
+  if (ticket) k2_signal(p, SY_UPW, blockIdx.x, K2_LANES);
+  return true;
+}
+// the down's wait for the up/gate tasks (k2_upgate_walk)
+template <int NCG>
+MK2_DEV bool k2_upgate_done(const K2Dev& p, int* seen, int stamp) {
+  if constexpr (NCG == 2) return k2_wait(p, seen, SY_UPW, gridDim.x, stamp, K2_LANES);
+  const int up_total = p.moe.Dmax * (p.moe.I / p.moe.UC) + p.moe.n_shared * (p.moe.SI / 32);
+  return k2_wait(p, seen, SY_UP, up_total, stamp, K2_LANES);
+}
+
 // score chunks a workgroup keeps in LDS for its slices (more tasks a workgroup: the
 // rest go through the scores in the workspace)
 constexpr int K2_KEEP = 4;
@@ -193,6 +243,7 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p, Front front) {
   __shared__ float kept[K2_KEEP][IDX_CHUNK];  // this workgroup's score tasks' scores, by t / G
   __shared__ int seen[SY_LINES + 1];  // counts seen by line; [SY_LINES]: a wait failed
   __shared__ int last_flag;
+  __shared__ int up_next;  // the up/gate walk's next ticket
   __shared__ uint32_t s_tag;
   const int G = gridDim.x, b = blockIdx.x;
   const int R = p.rows;
@@ -369,11 +420,15 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p, Front front) {
     // routing anyway (every slice and select read them long ago; a stopped launch
     // leaves this to the last workgroup out)
     for (uint32_t m = sel_rows; m; m &= m - 1) idx_clear_hist<K2_NT>(p.idx, __ffs((int)m) - 1);
-    K2_TASKS(t, up_total) {
-      const bool sh = t < up_sh;
-      if (!k2_wait(p, seen, SY_ROUTER, nrt, t < G ? 3 * st + 1 : -1, K2_LANES)) return;
-      if (!moe_upgate<K2_NT, NCG, FMT>(p.moe, sh ? up_r + t : t - up_sh, S.up.red, S.up.midf, tp)) return;
-      k2_signal(p, SY_UP, t, K2_LANES);
+    if constexpr (NCG == 1) {
+      K2_TASKS(t, up_total) {
+        const bool sh = t < up_sh;
+        if (!k2_wait(p, seen, SY_ROUTER, nrt, t < G ? 3 * st + 1 : -1, K2_LANES)) return;
+        if (moe_upgate<K2_NT, NCG, FMT>(p.moe, sh ? up_r + t : t - up_sh, S.up.red, S.up.midf, tp) < 0) return;
+        k2_signal(p, SY_UP, t, K2_LANES);
+      }
+    } else if (!k2_upgate_walk<NCG, FMT>(p, S, seen, &up_next, (b - base % G + G) % G, nrt, tp, 3 * st + 1)) {
+      return;
     }
     K2_NEXT(up_total);
     k2_stamp(p, 3 * st++ + 2);
@@ -382,7 +437,7 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p, Front front) {
     K2_TASKS(t, down_tasks(p.moe)) {
       if (!k2_wait(p, seen, SY_ROUTE, 1)) return;  // the routing and its table: known long before the mid rows
       moe_down<K2_NT, NCG, FMT>(p.moe, t, S.down.red, S.down.act, S.down.xres,
-                           [&] { return k2_wait(p, seen, SY_UP, up_total, t < G ? 3 * st + 1 : -1, K2_LANES); });
+                                [&] { return k2_upgate_done<NCG>(p, seen, t < G ? 3 * st + 1 : -1); });
       if (seen[SY_LINES]) return;
     }
     k2_stamp(p, 3 * st + 2);
@@ -500,6 +555,7 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_block(K2Dev p) {
   __shared__ float kept[BLK == K2_BLOCK_INDEXER ? K2_KEEP : 1][IDX_CHUNK];
   __shared__ int seen[SY_LINES + 1];
   __shared__ int last_flag;
+  __shared__ int up_next;  // the up/gate walk's next ticket
   __shared__ uint32_t s_tag;
   const int G = gridDim.x, b = blockIdx.x;
   const int R = p.rows;
@@ -612,17 +668,12 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_block(K2Dev p) {
         if (!ok) return;
         if (q == 0) k2_signal(p, SY_ROUTE);
       }
-      K2_TASKS(t, up_total) {
-        const bool sh = t < up_sh;
-        if (!k2_wait(p, seen, SY_ROUTER, nrt, -1, K2_LANES)) return;
-        if (!moe_upgate<K2_NT, NCG, FMT>(p.moe, sh ? up_r + t : t - up_sh, S.up.red, S.up.midf, tp)) return;
-        k2_signal(p, SY_UP, t, K2_LANES);
-      }
+      if (!k2_upgate_walk<NCG, FMT>(p, S, seen, &up_next, (b - base % G + G) % G, nrt, tp, -1)) return;
       K2_NEXT(up_total);
       K2_TASKS(t, down_tasks(p.moe)) {
         if (!k2_wait(p, seen, SY_ROUTE, 1)) return;
         moe_down<K2_NT, NCG, FMT>(p.moe, t, S.down.red, S.down.act, S.down.xres,
-                                  [&] { return k2_wait(p, seen, SY_UP, up_total, -1, K2_LANES); });
+                                  [&] { return k2_upgate_done<NCG>(p, seen, -1); });
         if (seen[SY_LINES]) return;
       }
     }

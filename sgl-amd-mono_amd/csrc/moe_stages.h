@@ -1009,22 +1009,24 @@ MK2_DEV int slot_expert(const MoeDev& p, int j, const TagPoll& tp, int* lds, uin
   return e;
 }
 
+// Task t: 1 when it ran, 0 for a routed slot past the routing's count (nothing to do),
+// -1 when its wait failed (the same value in every thread)
 template <int NT, int NCG, int FMT>
-MK2_DEV bool moe_upgate(const MoeDev& p, int t, float* red, float* midf, const TagPoll& tp) {
+MK2_DEV int moe_upgate(const MoeDev& p, int t, float* red, float* midf, const TagPoll& tp) {
   const int chunks_r = p.I / p.UC;
   if (t < p.Dmax * chunks_r) {
     const int j = t / chunks_r, c = t % chunks_r;
     uint32_t rows;
     const int e = slot_expert<kCompact<NCG, FMT>>(p, j, tp, (int*)midf, &rows);
-    if (e == -2) return false;
-    if (e < 0) return true;
+    if (e == -2) return -1;
+    if (e < 0) return 0;
     if constexpr (FMT == MK2_FMT_W8A8) upgate_w8a8<NT, NCG>(p, j, e, c, red);
     else if (NCG == 1 && p.UC == 64) upgate_chunk<NT, NCG, (NCG == 1 ? 4 : 2), FMT>(p, false, j, e, c, red, midf, rows);
     else upgate_chunk<NT, NCG, 2, FMT>(p, false, j, e, c, red, midf, rows);
   } else {
     upgate_chunk<NT, NCG, 2, FMT>(p, true, 0, 0, t - p.Dmax * chunks_r, red, midf);
   }
-  return true;
+  return 1;
 }
 
 // ---------------------------------------------------------- stage: down + combine

@@ -389,16 +389,28 @@ def main():
     extra = [int(r) for r in args.extra_rows.split(",") if r] if args.extra_rows else []
     extra = [r for r in extra if r != rows]
     # widths above 8 rows are verify steps of 8 requests (8 x 4 draft tokens at 32
-    # rows, as configs[4] names it); the decode widths are views of one set of layers
-    verify = [r for r in extra if r > 8 and r % 8 == 0]
-    built = max([rows] + [r for r in extra if r not in verify])
-    # the resident layers, built once at the widest width and viewed at each width
-    layers = [synth.make_layer(cfg, built, seed=1000 + 17 * i, device=dev) for i in range(args.layers)]
+    # rows, as configs[4] names it), built at their width; the decode widths are views
+    # of one set of layers built at the widest of them
+    def is_verify(r):
+        return r > 8 and r % 8 == 0
+
+    decode = [r for r in [rows] + extra if not is_verify(r)]
+    layers = ([synth.make_layer(cfg, max(decode), seed=1000 + 17 * i, device=dev) for i in range(args.layers)]
+              if decode else [])
+
+    def views(r):
+        if is_verify(r):
+            return [synth.make_layer(cfg, r, seed=1000 + 17 * i, device=dev, draft=r // 8) for i in range(args.layers)]
+        return [synth.view_rows(L, r) for L in layers]
+
+    def layout(r):
+        return f"verify: 8 requests x {r // 8} draft tokens" if is_verify(r) else f"decode: {r} requests x 1 token"
+
     torch.cuda.synchronize()
     if args.timeline:
         if args.staged:
             raise SystemExit("--timeline needs the persistent launch")
-        ops, outs = _ops(cfg, [synth.view_rows(L, rows) for L in layers], rows, dev, args.staged)
+        ops, outs = _ops(cfg, views(rows), rows, dev, args.staged)
         for op, o in zip(ops, outs):  # warm-up
             op(o)
         tl = timeline(ops, outs, args.timeline_launches, dev)
@@ -410,33 +422,30 @@ def main():
             op.check()
         return
 
-    head = measure(cfg, [synth.view_rows(L, rows) for L in layers], rows, dev, args)
+    head_views = views(rows)
+    head = measure(cfg, head_views, rows, dev, args)
     us, ms = head["us"], head["us"] / 1000.0
     gbs = head["algorithmic_bytes"] / (us * 1e-6) / 1e9
     widths = {}
 
-    def width_entry(m, r, layout):
+    def width_entry(m, r, lay):
         g = m["algorithmic_bytes"] / (m["us"] * 1e-6) / 1e9
-        return {"layout": layout, "us_per_layer": round(m["us"], 2),
+        return {"layout": lay, "us_per_layer": round(m["us"], 2),
                 "tokens_per_s_per_layer": round(r / (m["us"] * 1e-6), 1),
                 "algorithmic_bytes_per_layer": int(m["algorithmic_bytes"]), "hbm_gbps": round(g, 1),
                 "roofline_frac": round(g / PEAK_HBM_GBS, 4), "distinct_experts": m["distinct"],
                 "trials_us": m["trials_us"]}
 
     for r in extra:
-        if r in verify:
-            vl = [synth.make_layer(cfg, r, seed=1000 + 17 * i, device=dev, draft=r // 8) for i in range(args.layers)]
-            layout = f"verify: 8 requests x {r // 8} draft tokens"
-            widths[str(r)] = width_entry(measure(cfg, vl, r, dev, args), r, layout)
+        vl = views(r)
+        widths[str(r)] = width_entry(measure(cfg, vl, r, dev, args), r, layout(r))
+        if is_verify(r):
             # the same step with the FP4 x FP4 index scorer (queries quantized to MXFP4
             # in the kernel: a contract of its own, not the bf16-query config)
             q4 = replace(cfg, indexer=replace(cfg.indexer, keys=C.KEYS_FP4_Q4))
             widths[f"{r}_fp4_queries"] = width_entry(measure(q4, vl, r, dev, args), r,
-                                                     layout + ", FP4 x FP4 index scores")
-            del vl
-        else:
-            m = measure(cfg, [synth.view_rows(L, r) for L in layers], r, dev, args)
-            widths[str(r)] = width_entry(m, r, f"decode: {r} requests x 1 token")
+                                                     layout(r) + ", FP4 x FP4 index scores")
+        del vl
 
     result = {
         "metric": METRIC,
@@ -456,6 +465,7 @@ def main():
                         "sparse MLA 16 heads 512+64 FP8 KV -> W_UV/W_o -> RMSNorm 1e-6 -> "
                         "MXFP4 MoE 256 experts top-8 inter 256 + FP8 shared",
             "rows": rows,
+            "layout": layout(rows),
             "distinct_layers_cycled": len(layers),
             "parallelism": "1 GPU (TP reduce omitted)",
         },
@@ -487,7 +497,7 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(synth.view_rows(layers[0], rows), args.cpu_reps)
+        result["cpu_baseline"] = cpu_baseline(head_views[0], args.cpu_reps)
     print(json.dumps(result))
 
 

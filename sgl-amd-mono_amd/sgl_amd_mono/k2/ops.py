@@ -141,7 +141,11 @@ class IndexerOp:
         """The launches' sticky status word (_block_status)."""
         return _block_status(self.workspace)
 
-    def __call__(self, q, w, cache, cache_scale, page_table, req_ids, ctx_len, scores=None, topk=None):
+    def __call__(self, q, w, cache, cache_scale, page_table, req_ids, ctx_len, scores=None, topk=None,
+                 with_scores: bool = True):
+        """(scores, topk).  with_scores=False: the launch keeps the scores to itself (in
+        LDS, as the layer does; `scores` must be None and None is returned for it) and
+        writes only the lists."""
         cfg, rows = self.cfg, self.rows
         _need(q, "q", torch.bfloat16, (rows, cfg.heads, cfg.dim))
         _need(w, "w", torch.bfloat16, (rows, cfg.heads))
@@ -158,11 +162,15 @@ class IndexerOp:
             raise ValueError("page_table row stride differs from the op's table_stride")
         _need(req_ids, "req_ids", torch.int32, (rows,))
         _need(ctx_len, "ctx_len", torch.int32, (rows,))
-        if scores is None:
+        if not with_scores:
+            if scores is not None:
+                raise ValueError("with_scores=False takes no scores tensor")
+        elif scores is None:
             scores = torch.empty(rows, cfg.context, dtype=torch.float32, device=self.device)
         if topk is None:
             topk = torch.empty(rows, cfg.topk, dtype=torch.int32, device=self.device)
-        _need(scores, "scores", torch.float32, (rows, cfg.context))
+        if scores is not None:
+            _need(scores, "scores", torch.float32, (rows, cfg.context))
         _need(topk, "topk", torch.int32, (rows, cfg.topk))
         args = _lib.IndexerArgs(
             self.shape, _p(q), _p(w), _p(cache), _p(cache_scale), _p(page_table), _p(req_ids), _p(ctx_len),

@@ -280,3 +280,25 @@ def test_indexer_fp4_queries_ties_and_zeros():
     assert bool((oc.radix_keys(scores) == (1 << 31)).all())
     for r in range(2):
         assert torch.equal(topk[r], torch.arange(256))
+
+
+def test_indexer_lists_without_score_output():
+    """with_scores=False (scores NULL at the C ABI): the launch keeps its scores in LDS
+    and writes only the lists, which equal the lists of the launch that writes its
+    scores, bit for bit, and the oracle's radix lists of those scores."""
+    from sgl_amd_mono.k2 import config as C
+    from sgl_amd_mono.k2 import synth
+    from sgl_amd_mono.k2.ops import IndexerOp
+
+    dev = _dev()
+    cfg = C.C4_INDEXER
+    ns = synth.make_indexer(cfg, 8, 48, dev)
+    op = IndexerOp(cfg, 8, ns.page_table.shape[1], device=dev)
+    args = (ns.q, ns.w, ns.cache, ns.cache_scale, ns.page_table, ns.req_ids, ns.ctx_len)
+    scores, topk = op(*args)
+    none, lists = op(*args, with_scores=False)
+    torch.cuda.synchronize()
+    assert none is None and op.status() == 0
+    assert torch.equal(lists, topk)
+    for r in range(8):
+        assert torch.equal(cpu(lists)[r].long(), R.radix_lists(cpu(scores)[r], cfg.topk))

@@ -1030,6 +1030,133 @@ MK2_DEV int moe_upgate(const MoeDev& p, int t, float* red, float* midf, const Ta
 }
 
 // ---------------------------------------------------------- stage: down + combine
+// A down task's hidden rows: tile tl[d], rows rlo[d] .. rhi[d] - 1 of it (every row of
+// DT tiles, or with p.DT == 3 (DT 2) 24 rows: a whole tile and half of the next, in
+// either order); c0 the first (its output column), ncol how many, live[d] whether
+// lane row c16 is one of tile d's
+template <int DT>
+struct DownRows {
+  int tl[DT], rlo[DT], rhi[DT], c0, ncol;
+  bool live[DT];
+  MK2_DEV DownRows(const MoeDev& p, int nt, int c16) {
+#pragma unroll
+    for (int d = 0; d < DT; ++d) {
+      tl[d] = nt * DT + d;
+      rlo[d] = 0;
+      rhi[d] = 16;
+    }
+    if (DT == 2 && p.DT == 3) {
+      const int ta = (3 * nt) >> 1;
+      tl[0] = ta;
+      tl[DT - 1] = ta + 1;
+      rlo[0] = nt & 1 ? 8 : 0;
+      rhi[DT - 1] = nt & 1 ? 16 : 8;
+    }
+    c0 = tl[0] * 16 + rlo[0];
+    ncol = 0;
+#pragma unroll
+    for (int d = 0; d < DT; ++d) ncol += rhi[d] - rlo[d];
+#pragma unroll
+    for (int d = 0; d < DT; ++d) live[d] = c16 >= rlo[d] && c16 < rhi[d];
+  }
+};
+
+// The shared expert's first k-block of this wave (weights only, static: loaded before
+// the mid activations' wait)
+template <int DT>
+MK2_DEV void down_shared_first(const MoeDev& p, const DownRows<DT>& t, int KB2s, int wave, int lane,
+                               uint4 (&shraw)[DT][2], float (&shsc)[DT]) {
+  const int kb = min(wave, max(KB2s, 1) - 1);
+#pragma unroll
+  for (int d = 0; d < DT; ++d) {
+    shraw[d][0] = shraw[d][1] = make_uint4(0, 0, 0, 0);
+    shsc[d] = 0.f;
+    if (KB2s) {
+      if (t.live[d]) load_fp8_block(p.ws2 + ((size_t)t.tl[d] * KB2s + kb) * 2048, p.wl, lane, shraw[d][0], shraw[d][1]);
+      shsc[d] = p.ss2[(t.tl[d] * 16 / 128) * KB2s + kb];
+    }
+  }
+}
+
+// The residual rows (the W_o output, published before the routing) for the epilogue,
+// straight into LDS (no registers held): dword d of the ncol / 2 * M is row
+// d / (ncol / 2), columns 2 (d % (ncol / 2)) .. + 1 of the task's
+template <int DT>
+MK2_DEV void down_residual_lds(const MoeDev& p, const DownRows<DT>& t, float* xres, int wave) {
+  const int half = t.ncol / 2;
+  const int nxd = p.residual ? half * p.M : 0;
+  if (threadIdx.x < nxd)
+    __builtin_amdgcn_global_load_lds((const uint32_t*)(p.x + (size_t)(threadIdx.x / half) * p.H + t.c0) + threadIdx.x % half,
+                                     (uint32_t*)xres + 64 * wave, 4, 0, 0);
+}
+
+// The shared expert (FP8, bf16 mid) into acc: its k-blocks spread over the NW waves,
+// the first from shraw / shsc (down_shared_first)
+template <int NW, int NCG, int DT>
+MK2_DEV void down_shared(const MoeDev& p, const DownRows<DT>& t, int KB2s, int wave, int lane,
+                         const uint4 (&shraw)[DT][2], const float (&shsc)[DT], f32x4 (&acc)[DT][NCG]) {
+  const int g = lane >> 4, c16 = lane & 15;
+  for (int kb = wave; kb < KB2s; kb += NW) {
+    bf16x8 b[NCG][4];
+#pragma unroll
+    for (int cg = 0; cg < NCG; ++cg) load_b_bf16(p.mid_sh, cg * 16 + c16, p.M, p.SI, kb * 128 + 32 * g, b[cg]);
+#pragma unroll
+    for (int d = 0; d < DT; ++d) {
+      uint4 r0, r1;
+      float sc;
+      if (kb == wave) {
+        r0 = shraw[d][0];
+        r1 = shraw[d][1];
+        sc = shsc[d];
+      } else {
+        r0 = r1 = make_uint4(0, 0, 0, 0);
+        if (t.live[d]) load_fp8_block(p.ws2 + ((size_t)t.tl[d] * KB2s + kb) * 2048, p.wl, lane, r0, r1);
+        sc = p.ss2[(t.tl[d] * 16 / 128) * KB2s + kb];
+      }
+      bf16x8 a[4];
+      a[0] = e4m3x8_to_bf16(r0.x, r0.y);
+      a[1] = e4m3x8_to_bf16(r0.z, r0.w);
+      a[2] = e4m3x8_to_bf16(r1.x, r1.y);
+      a[3] = e4m3x8_to_bf16(r1.z, r1.w);
+#pragma unroll
+      for (int cg = 0; cg < NCG; ++cg) acc[d][cg] += mfma4_bf16(a, b[cg], f32x4{0.f, 0.f, 0.f, 0.f}) * sc;
+    }
+  }
+}
+
+// The task's outputs: the waves' partial sums from LDS (CMP: each wave's [DT][16
+// hidden][32 rows] accumulator; else its f32x4 MFMA tiles, which acc still holds and
+// this stores first), plus the residual, rounded to bf16
+template <int NT, int NCG, int DT, bool CMP>
+MK2_DEV void down_epilogue(const MoeDev& p, const DownRows<DT>& t, float* red, const float* xres,
+                           const f32x4 (*acc)[NCG] = nullptr) {
+  constexpr int NW = NT / 64;
+  if constexpr (!CMP) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int d = 0; d < DT; ++d)
+#pragma unroll
+      for (int cg = 0; cg < NCG; ++cg) *(f32x4*)(red + (((wave * DT + d) * NCG + cg) * 64 + lane) * 4) = acc[d][cg];
+  }
+  drain_memory();  // this wave's residual dwords have landed in LDS
+  __syncthreads();
+  const int n0 = t.rhi[0] - t.rlo[0];  // the first tile's columns
+  for (int idx = threadIdx.x; idx < t.ncol * p.M; idx += NT) {
+    const int n = idx % t.ncol, s = idx / t.ncol;  // column c0 + n of row s
+    const int d = n < n0 ? 0 : DT - 1, n16 = n < n0 ? t.rlo[0] + n : t.rlo[DT - 1] + n - n0;
+    const int cg = s >> 4, s16 = s & 15;
+    const int l = (n16 >> 2) * 16 + s16, i = n16 & 3;
+    float y = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+      y += CMP ? red[((w * DT + d) * 16 + n16) * 32 + s] : red[(((w * DT + d) * NCG + cg) * 64 + l) * 4 + i];
+    const size_t o = (size_t)s * p.H + t.c0 + n;
+    if (p.residual) y += bf16_to_f32(((const bf16_t*)xres)[idx]);
+    p.out[o] = f32_to_bf16(y);
+  }
+  __syncthreads();
+}
+
 // A task is 16*DT hidden rows (24 with p.DT == 3); every slot (the shared expert, then the D routed
 // experts) adds rw * W_down[e] . mid into the rows' accumulators; out = bf16(y [+ x]).
 // Waves take every NW-th slot, B slots a unit, the next unit's weight tiles and mid
@@ -1046,29 +1173,9 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, float*
   for (int j = threadIdx.x; j < D; j += NT) act_ids[j] = min(max((int)pair_value(ld_pair(p.act + 1 + j)), 0), p.E - 1);
   __syncthreads();
   const int HT = p.H / 16;
-  // the task's rows: tile tl[d], rows rlo[d] .. rhi[d] - 1 of it (every row of DT tiles,
-  // or with p.DT == 3 (DT 2) 24 rows: a whole tile and half of the next, in either order)
-  int tl[DT], rlo[DT], rhi[DT];
-#pragma unroll
-  for (int d = 0; d < DT; ++d) {
-    tl[d] = nt * DT + d;
-    rlo[d] = 0;
-    rhi[d] = 16;
-  }
-  if (DT == 2 && p.DT == 3) {
-    const int ta = (3 * nt) >> 1;
-    tl[0] = ta;
-    tl[DT - 1] = ta + 1;
-    rlo[0] = nt & 1 ? 8 : 0;
-    rhi[DT - 1] = nt & 1 ? 16 : 8;
-  }
-  const int c0 = tl[0] * 16 + rlo[0];  // the task's first hidden row (output column)
-  int ncol = 0;
-#pragma unroll
-  for (int d = 0; d < DT; ++d) ncol += rhi[d] - rlo[d];
-  bool live[DT];  // this lane's A row is one of the task's
-#pragma unroll
-  for (int d = 0; d < DT; ++d) live[d] = c16 >= rlo[d] && c16 < rhi[d];
+  const DownRows<DT> t(p, nt, c16);
+  const auto& tl = t.tl;
+  const auto& live = t.live;
   const int KB2s = p.n_shared ? p.SI / 128 : 0;
   const int KB2 = p.I / 128;
   constexpr int B = 1;                                 // MXFP4 slots a unit
@@ -1078,29 +1185,11 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, float*
   // activations' dependency)
   uint4 shraw[DT][2];
   float shsc[DT];
-  {
-    const int kb = min(wave, max(KB2s, 1) - 1);
-#pragma unroll
-    for (int d = 0; d < DT; ++d) {
-      shraw[d][0] = shraw[d][1] = make_uint4(0, 0, 0, 0);
-      shsc[d] = 0.f;
-      if (KB2s) {
-        if (live[d]) load_fp8_block(p.ws2 + ((size_t)tl[d] * KB2s + kb) * 2048, p.wl, lane, shraw[d][0], shraw[d][1]);
-        shsc[d] = p.ss2[(tl[d] * 16 / 128) * KB2s + kb];
-      }
-    }
-  }
+  down_shared_first<DT>(p, t, KB2s, wave, lane, shraw, shsc);
   // the scaled-MFMA unit pipeline: E2M1 weights against MXFP8 (A8W4) or MXFP4 (A4W4) mid
   constexpr bool mx = FMT == MK2_FMT_MXFP4 || FMT == MK2_FMT_A4W4;
   constexpr bool a4 = FMT == MK2_FMT_A4W4;
-  // the residual rows (the W_o output, published before the routing) for the
-  // epilogue, straight into LDS (no registers held): dword d of the ncol / 2 * M is
-  // row d / (ncol / 2), columns 2 (d % (ncol / 2)) .. + 1 of the task's
-  const int nxd = p.residual ? ncol / 2 * p.M : 0;
-  if (threadIdx.x < nxd)
-    __builtin_amdgcn_global_load_lds(
-        (const uint32_t*)(p.x + (size_t)(threadIdx.x / (ncol / 2)) * p.H + c0) + threadIdx.x % (ncol / 2),
-        (uint32_t*)xres + 64 * wave, 4, 0, 0);
+  down_residual_lds<DT>(p, t, xres, wave);
   // the routed slots (MXFP4): a unit is a batch of B slots (wave + NW * (B * i + u))
   // over KC k-blocks; units u + 1 and u + 2 (weights, mid rows, scales and route
   // weights) are in flight while unit u's MFMAs run
@@ -1199,33 +1288,7 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, float*
   if (!wait()) return;
   if (nu > 0) load_m(0, x0);
   if (nu > 1) load_m(1, x1);
-  // the shared expert (FP8, bf16 mid): its k-blocks spread over the waves
-  for (int kb = wave; kb < KB2s; kb += NW) {
-    bf16x8 b[NCG][4];
-#pragma unroll
-    for (int cg = 0; cg < NCG; ++cg) load_b_bf16(p.mid_sh, cg * 16 + c16, p.M, p.SI, kb * 128 + 32 * g, b[cg]);
-#pragma unroll
-    for (int d = 0; d < DT; ++d) {
-      uint4 r0, r1;
-      float sc;
-      if (kb == wave) {
-        r0 = shraw[d][0];
-        r1 = shraw[d][1];
-        sc = shsc[d];
-      } else {
-        r0 = r1 = make_uint4(0, 0, 0, 0);
-        if (live[d]) load_fp8_block(p.ws2 + ((size_t)tl[d] * KB2s + kb) * 2048, p.wl, lane, r0, r1);
-        sc = p.ss2[(tl[d] * 16 / 128) * KB2s + kb];
-      }
-      bf16x8 a[4];
-      a[0] = e4m3x8_to_bf16(r0.x, r0.y);
-      a[1] = e4m3x8_to_bf16(r0.z, r0.w);
-      a[2] = e4m3x8_to_bf16(r1.x, r1.y);
-      a[3] = e4m3x8_to_bf16(r1.z, r1.w);
-#pragma unroll
-      for (int cg = 0; cg < NCG; ++cg) acc[d][cg] += mfma4_bf16(a, b[cg], f32x4{0.f, 0.f, 0.f, 0.f}) * sc;
-    }
-  }
+  down_shared<NW, NCG, DT>(p, t, KB2s, wave, lane, shraw, shsc, acc);
   if constexpr (mx) {
     auto step = [&](int u, Unit& cur, Unit& nxt2) {
       if (u + 2 < nu) {
@@ -1327,68 +1390,33 @@ MK2_DEV void down_rows(const MoeDev& p, int nt, float* red, int* act_ids, float*
       }
     }
   }
-#pragma unroll
-  for (int d = 0; d < DT; ++d)
-#pragma unroll
-    for (int cg = 0; cg < NCG; ++cg) *(f32x4*)(red + (((wave * DT + d) * NCG + cg) * 64 + lane) * 4) = acc[d][cg];
-  drain_memory();  // this wave's residual dwords have landed in LDS
-  __syncthreads();
-  const int n0 = rhi[0] - rlo[0];  // the first tile's columns
-  for (int idx = threadIdx.x; idx < ncol * p.M; idx += NT) {
-    const int n = idx % ncol, s = idx / ncol;  // column c0 + n of row s
-    const int d = n < n0 ? 0 : DT - 1, n16 = n < n0 ? rlo[0] + n : rlo[DT - 1] + n - n0;
-    const int cg = s >> 4, s16 = s & 15;
-    const int l = (n16 >> 2) * 16 + s16, i = n16 & 3;
-    float y = 0.f;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) y += red[(((w * DT + d) * NCG + cg) * 64 + l) * 4 + i];
-    const size_t o = (size_t)s * p.H + c0 + n;
-    if (p.residual) y += bf16_to_f32(((const bf16_t*)xres)[idx]);
-    p.out[o] = f32_to_bf16(y);
-  }
-  __syncthreads();
+  down_epilogue<NT, NCG, DT, false>(p, t, red, xres, acc);
 }
 
-// The down with compacted rows (kCompact): as down_rows, each slot's columns being its
-// rows in order, added into per-wave [16 hidden][32 rows] accumulators in LDS.  A copy,
-// so that the uncompacted instantiations keep down_rows' code as it is.
+// The down with compacted rows (kCompact: the scaled-MFMA modes above 16 rows): as
+// down_rows' scaled-MFMA path, each slot's columns being its rows in order, added into
+// per-wave [DT][16 hidden][32 rows] accumulators in LDS.  The unit pipeline is its own
+// (the compacted columns change every unit's loads and accumulation); the task rows,
+// the shared expert's first k-block and the residual are down_rows' helpers.  Its
+// shared-expert loop and epilogue stay written out here: as calls of down_shared and
+// down_epilogue the 32-row kernel spilled more registers and ran 0.8-0.9 us slower each.
 template <int NT, int NCG, int DT, int FMT, typename Wait>
 MK2_DEV void down_rows_cmp(const MoeDev& p, int nt, float* red, int* act_ids, float* xres, Wait wait) {
   constexpr int NW = NT / 64;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, c16 = lane & 15;
+  static_assert(kCompact<NCG, FMT>, "compacted rows: the scaled-MFMA modes above 16 rows");
   // the list, published by the routing's counter; read device-coherently: up/gate
   // tasks on this XCD polled its words before all of them were out
-  constexpr bool CMP = kCompact<NCG, FMT>;
   const int D = min((int)pair_value(ld_pair(p.act)), p.Dmax);
   for (int j = threadIdx.x; j < D; j += NT) {
     act_ids[j] = min(max((int)pair_value(ld_pair(p.act + 1 + j)), 0), p.E - 1);
-    if (CMP) act_ids[256 + j] = __popc((uint32_t)pair_value(ld_pair(p.act_rows + j)));  // the slot's rows
+    act_ids[256 + j] = __popc((uint32_t)pair_value(ld_pair(p.act_rows + j)));  // the slot's rows
   }
   __syncthreads();
   const int HT = p.H / 16;
-  // the task's rows: tile tl[d], rows rlo[d] .. rhi[d] - 1 of it (every row of DT tiles,
-  // or with p.DT == 3 (DT 2) 24 rows: a whole tile and half of the next, in either order)
-  int tl[DT], rlo[DT], rhi[DT];
-#pragma unroll
-  for (int d = 0; d < DT; ++d) {
-    tl[d] = nt * DT + d;
-    rlo[d] = 0;
-    rhi[d] = 16;
-  }
-  if (DT == 2 && p.DT == 3) {
-    const int ta = (3 * nt) >> 1;
-    tl[0] = ta;
-    tl[DT - 1] = ta + 1;
-    rlo[0] = nt & 1 ? 8 : 0;
-    rhi[DT - 1] = nt & 1 ? 16 : 8;
-  }
-  const int c0 = tl[0] * 16 + rlo[0];  // the task's first hidden row (output column)
-  int ncol = 0;
-#pragma unroll
-  for (int d = 0; d < DT; ++d) ncol += rhi[d] - rlo[d];
-  bool live[DT];  // this lane's A row is one of the task's
-#pragma unroll
-  for (int d = 0; d < DT; ++d) live[d] = c16 >= rlo[d] && c16 < rhi[d];
+  const DownRows<DT> t(p, nt, c16);
+  const auto& tl = t.tl;
+  const auto& live = t.live;
   const int KB2s = p.n_shared ? p.SI / 128 : 0;
   const int KB2 = p.I / 128;
   constexpr int B = 1;                                 // MXFP4 slots a unit
@@ -1398,29 +1426,10 @@ MK2_DEV void down_rows_cmp(const MoeDev& p, int nt, float* red, int* act_ids, fl
   // activations' dependency)
   uint4 shraw[DT][2];
   float shsc[DT];
-  {
-    const int kb = min(wave, max(KB2s, 1) - 1);
-#pragma unroll
-    for (int d = 0; d < DT; ++d) {
-      shraw[d][0] = shraw[d][1] = make_uint4(0, 0, 0, 0);
-      shsc[d] = 0.f;
-      if (KB2s) {
-        if (live[d]) load_fp8_block(p.ws2 + ((size_t)tl[d] * KB2s + kb) * 2048, p.wl, lane, shraw[d][0], shraw[d][1]);
-        shsc[d] = p.ss2[(tl[d] * 16 / 128) * KB2s + kb];
-      }
-    }
-  }
+  down_shared_first<DT>(p, t, KB2s, wave, lane, shraw, shsc);
   // the scaled-MFMA unit pipeline: E2M1 weights against MXFP8 (A8W4) or MXFP4 (A4W4) mid
-  constexpr bool mx = FMT == MK2_FMT_MXFP4 || FMT == MK2_FMT_A4W4;
   constexpr bool a4 = FMT == MK2_FMT_A4W4;
-  // the residual rows (the W_o output, published before the routing) for the
-  // epilogue, straight into LDS (no registers held): dword d of the ncol / 2 * M is
-  // row d / (ncol / 2), columns 2 (d % (ncol / 2)) .. + 1 of the task's
-  const int nxd = p.residual ? ncol / 2 * p.M : 0;
-  if (threadIdx.x < nxd)
-    __builtin_amdgcn_global_load_lds(
-        (const uint32_t*)(p.x + (size_t)(threadIdx.x / (ncol / 2)) * p.H + c0) + threadIdx.x % (ncol / 2),
-        (uint32_t*)xres + 64 * wave, 4, 0, 0);
+  down_residual_lds<DT>(p, t, xres, wave);
   // the routed slots (MXFP4): a unit is a batch of B slots (wave + NW * (B * i + u))
   // over KC k-blocks; units u + 1 and u + 2 (u + 1 alone for 24-row tasks: weights,
   // mid rows, scales and route weights) are in flight while unit u's MFMAs run
@@ -1434,7 +1443,7 @@ MK2_DEV void down_rows_cmp(const MoeDev& p, int nt, float* red, int* act_ids, fl
     int cnt[B];      // compacted rows: the slot's rows
   };
   const int nkc = (KB2 + KC - 1) / KC;  // units a batch
-  const int nu = mx && D > wave ? (D - wave + NW * B - 1) / (NW * B) * nkc : 0;
+  const int nu = D > wave ? (D - wave + NW * B - 1) / (NW * B) * nkc : 0;
   auto load_w = [&](int u, Unit& x) {  // weights: known since the routing
     const int j0 = wave + (u / nkc) * NW * B, kb0 = (u % nkc) * KC;
 #pragma unroll
@@ -1464,8 +1473,8 @@ MK2_DEV void down_rows_cmp(const MoeDev& p, int nt, float* red, int* act_ids, fl
 #pragma unroll
     for (int ub = 0; ub < B; ++ub) {
       const int j = min(j0 + ub * NW, D - 1);
-      // the mid's rows: all rows, or the slot's rows compacted (row c its c-th)
-      const int lim = CMP ? act_ids[256 + j] : p.M;
+      // the mid's rows: the slot's rows compacted (row c its c-th)
+      const int lim = act_ids[256 + j];
       x.cnt[ub] = lim;
 #pragma unroll
       for (int c = 0; c < KC; ++c) {
@@ -1481,8 +1490,8 @@ MK2_DEV void down_rows_cmp(const MoeDev& p, int nt, float* red, int* act_ids, fl
 #pragma unroll
       for (int cg = 0; cg < NCG; ++cg) {
         const int row = cg * 16 + c16;
-        x.wr[ub][cg] = !CMP || row < lim ? ldp_f32(p.rw + j * 32 + row) : 0.f;
-        x.rr[ub][cg] = CMP && row < lim ? ldp_i32(p.rowc + j * 32 + row) : -1;
+        x.wr[ub][cg] = row < lim ? ldp_f32(p.rw + j * 32 + row) : 0.f;
+        x.rr[ub][cg] = row < lim ? ldp_i32(p.rowc + j * 32 + row) : -1;
       }
     }
   };
@@ -1513,7 +1522,7 @@ MK2_DEV void down_rows_cmp(const MoeDev& p, int nt, float* red, int* act_ids, fl
           const int sak = x.sa[ub][d] >> e8m0_shift(p.wl, tl[d], kb);
 #pragma unroll
           for (int cg = 0; cg < NCG; ++cg) {
-            if (CMP && cg == 1 && x.cnt[ub] <= 16) break;  // no rows there (uniform)
+            if (cg == 1 && x.cnt[ub] <= 16) break;  // no rows there (uniform)
             tmp[ub][d][cg] = a4 ? mfma_same<4>(x.a[ub][d][c], x.bq[ub][c][cg], tmp[ub][d][cg], sak, x.sbq[ub][c][cg])
                                 : mfma_fp4_fp8<0, 0>(x.a[ub][d][c], x.bq[ub][c][cg], tmp[ub][d][cg], sak, x.sbq[ub][c][cg]);
           }
@@ -1524,23 +1533,16 @@ MK2_DEV void down_rows_cmp(const MoeDev& p, int nt, float* red, int* act_ids, fl
 #pragma unroll
       for (int ub = 0; ub < B; ++ub) {
         if (j0 + ub * NW >= D) break;
-        if constexpr (CMP) {
-          // each column into its row of this wave's accumulators [DT][16 hidden][32 rows]
+        // each column into its row of this wave's accumulators [DT][16 hidden][32 rows]
 #pragma unroll
-          for (int cg = 0; cg < NCG; ++cg)
-            if (x.rr[ub][cg] >= 0) {
+        for (int cg = 0; cg < NCG; ++cg)
+          if (x.rr[ub][cg] >= 0) {
 #pragma unroll
-              for (int d = 0; d < DT; ++d)
+            for (int d = 0; d < DT; ++d)
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                  red[((wave * DT + d) * 16 + 4 * g + i) * 32 + x.rr[ub][cg]] += tmp[ub][d][cg][i] * x.wr[ub][cg];
-            }
-        } else {
-#pragma unroll
-          for (int cg = 0; cg < NCG; ++cg)
-#pragma unroll
-            for (int d = 0; d < DT; ++d) acc[d][cg] += tmp[ub][d][cg] * x.wr[ub][cg];
-        }
+              for (int i = 0; i < 4; ++i)
+                red[((wave * DT + d) * 16 + 4 * g + i) * 32 + x.rr[ub][cg]] += tmp[ub][d][cg][i] * x.wr[ub][cg];
+          }
       }
     }
   };
@@ -1579,17 +1581,15 @@ MK2_DEV void down_rows_cmp(const MoeDev& p, int nt, float* red, int* act_ids, fl
       for (int cg = 0; cg < NCG; ++cg) acc[d][cg] += mfma4_bf16(a, b[cg], f32x4{0.f, 0.f, 0.f, 0.f}) * sc;
     }
   }
-  if constexpr (CMP) {
-    // this wave's accumulators [DT][16 hidden][32 rows] in LDS, from its shared-expert
-    // sums; the routed slots add into their rows
+  // this wave's accumulators [DT][16 hidden][32 rows] in LDS, from its shared-expert
+  // sums; the routed slots add into their rows
 #pragma unroll
-    for (int d = 0; d < DT; ++d)
+  for (int d = 0; d < DT; ++d)
 #pragma unroll
-      for (int cg = 0; cg < NCG; ++cg)
+    for (int cg = 0; cg < NCG; ++cg)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) red[((wave * DT + d) * 16 + 4 * g + i) * 32 + cg * 16 + c16] = acc[d][cg][i];
-  }
-  if constexpr (mx && DEPTH == 2) {
+      for (int i = 0; i < 4; ++i) red[((wave * DT + d) * 16 + 4 * g + i) * 32 + cg * 16 + c16] = acc[d][cg][i];
+  if constexpr (DEPTH == 2) {
     auto step = [&](int u, Unit& cur, Unit& nxt) {
       if (u + 1 < nu) {
         load_w(u + 1, nxt);
@@ -1601,7 +1601,7 @@ MK2_DEV void down_rows_cmp(const MoeDev& p, int nt, float* red, int* act_ids, fl
       step(u, x0, x1);
       step(u + 1, x1, x0);
     }
-  } else if constexpr (mx) {
+  } else {
     auto step = [&](int u, Unit& cur, Unit& nxt2) {
       if (u + 2 < nu) {
         load_w(u + 2, nxt2);
@@ -1614,113 +1614,17 @@ MK2_DEV void down_rows_cmp(const MoeDev& p, int nt, float* red, int* act_ids, fl
       step(u + 1, x1, x0);
       step(u + 2, x2, x1);
     }
-  } else if constexpr (DT == 1) {
-    if constexpr (FMT == MK2_FMT_A16W4) {
-      // E2M1 weights widened exactly to bf16 against the bf16 mid, 8 k-blocks a batch
-      constexpr int KMAX = 8;
-      for (int j = wave; j < D; j += NW) {
-        const int e = act_ids[j];
-        const uint8_t* wb = p.w2 + ((size_t)e * HT + tl[0]) * KB2 * 1024;
-        const uint8_t* sb = p.s2 + e * e8m0_expert_bytes(p.wl, p.H, p.I);
-        f32x4 t[NCG];
-#pragma unroll
-        for (int cg = 0; cg < NCG; ++cg) t[cg] = f32x4{0.f, 0.f, 0.f, 0.f};
-        for (int kb0 = 0; kb0 < KB2; kb0 += KMAX) {
-          uint4 raw[KMAX];
-          uint32_t sw[KMAX];
-#pragma unroll
-          for (int u = 0; u < KMAX; ++u) {
-            const int kb = min(kb0 + u, KB2 - 1);
-            raw[u] = ld_stream16(wb + ((size_t)kb * 64 + lane) * 16);
-            sw[u] = (e8m0_word(sb, p.wl, p.I, tl[0], kb, lane) >> e8m0_shift(p.wl, tl[0], kb)) & 0xFFu;
-          }
-#pragma unroll
-          for (int u = 0; u < KMAX; ++u) {
-            const int kb = kb0 + u;
-            if (kb >= KB2) break;
-            const float sc = e8m0_to_f32(sw[u]);
-            bf16x8 a[4];
-            a[0] = e2m1x8_to_bf16(raw[u].x, sc);
-            a[1] = e2m1x8_to_bf16(raw[u].y, sc);
-            a[2] = e2m1x8_to_bf16(raw[u].z, sc);
-            a[3] = e2m1x8_to_bf16(raw[u].w, sc);
-#pragma unroll
-            for (int cg = 0; cg < NCG; ++cg) {
-              bf16x8 b[4];
-              load_b_bf16(p.mid_b + (size_t)j * p.M * p.I, cg * 16 + c16, p.M, p.I, kb * 128 + 32 * g, b);
-              t[cg] = mfma4_bf16(a, b, t[cg]);
-            }
-          }
-        }
-#pragma unroll
-        for (int cg = 0; cg < NCG; ++cg) acc[0][cg] += t[cg] * ldp_f32(p.rw + j * 32 + cg * 16 + c16);
-      }
-    } else {
-      // E4M3 weights (f32 scale per 128 x 128 block): widened to bf16 against the bf16
-      // mid (W8A16), or on the scaled MFMA against the E4M3 mid (W8A8, f32 scale per 128
-      // a row); each k-block's product times its scales and the route weight
-      constexpr int KMAX = 8;  // inter <= 1024
-      constexpr bool w8a8 = FMT == MK2_FMT_W8A8;
-      for (int j = wave; j < D; j += NW) {
-        const int e = act_ids[j];
-        const uint8_t* wb = p.w2 + ((size_t)e * HT + tl[0]) * KB2 * 2048;
-        const float* sbase = (const float*)p.s2 + (size_t)e * (p.H / 128) * KB2 + (tl[0] * 16 / 128) * KB2;
-        uint4 raw[KMAX][2];
-#pragma unroll
-        for (int kb = 0; kb < KMAX; ++kb) {
-          load_fp8_block(wb + (size_t)min(kb, KB2 - 1) * 2048, p.wl, lane, raw[kb][0], raw[kb][1]);
-        }
-#pragma unroll
-        for (int kb = 0; kb < KMAX; ++kb) {
-          if (kb >= KB2) break;
-          const float sc = sbase[kb];
-          if constexpr (w8a8) {
-            const i32x8 A = {(int)raw[kb][0].x, (int)raw[kb][0].y, (int)raw[kb][0].z, (int)raw[kb][0].w,
-                             (int)raw[kb][1].x, (int)raw[kb][1].y, (int)raw[kb][1].z, (int)raw[kb][1].w};
-#pragma unroll
-            for (int cg = 0; cg < NCG; ++cg) {
-              const int row = cg * 16 + c16;
-              const i32x8 bq = load_b_fp8_same(p.mid_q + (size_t)j * p.M * p.I, row, p.M, p.I, kb * 128, g);
-              const float ms = row < p.M ? ldp_f32(p.mid_sf + ((size_t)j * p.M + row) * (p.I / 128) + kb) : 0.f;
-              acc[0][cg] += mfma_same<0>(A, bq, f32x4{0.f, 0.f, 0.f, 0.f}, E8M0_ONE, E8M0_ONE) *
-                            (sc * ms * ldp_f32(p.rw + j * 32 + row));
-            }
-          } else {
-            bf16x8 a[4];
-            a[0] = e4m3x8_to_bf16(raw[kb][0].x, raw[kb][0].y);
-            a[1] = e4m3x8_to_bf16(raw[kb][0].z, raw[kb][0].w);
-            a[2] = e4m3x8_to_bf16(raw[kb][1].x, raw[kb][1].y);
-            a[3] = e4m3x8_to_bf16(raw[kb][1].z, raw[kb][1].w);
-#pragma unroll
-            for (int cg = 0; cg < NCG; ++cg) {
-              bf16x8 b[4];
-              load_b_bf16(p.mid_b + (size_t)j * p.M * p.I, cg * 16 + c16, p.M, p.I, kb * 128 + 32 * g, b);
-              acc[0][cg] += mfma4_bf16(a, b, f32x4{0.f, 0.f, 0.f, 0.f}) * (sc * ldp_f32(p.rw + j * 32 + cg * 16 + c16));
-            }
-          }
-        }
-      }
-    }
-  }
-  if constexpr (!CMP) {
-#pragma unroll
-    for (int d = 0; d < DT; ++d)
-#pragma unroll
-      for (int cg = 0; cg < NCG; ++cg) *(f32x4*)(red + (((wave * DT + d) * NCG + cg) * 64 + lane) * 4) = acc[d][cg];
   }
   drain_memory();  // this wave's residual dwords have landed in LDS
   __syncthreads();
-  const int n0 = rhi[0] - rlo[0];  // the first tile's columns
-  for (int idx = threadIdx.x; idx < ncol * p.M; idx += NT) {
-    const int n = idx % ncol, s = idx / ncol;  // column c0 + n of row s
-    const int d = n < n0 ? 0 : DT - 1, n16 = n < n0 ? rlo[0] + n : rlo[DT - 1] + n - n0;
-    const int cg = s >> 4, s16 = s & 15;
-    const int l = (n16 >> 2) * 16 + s16, i = n16 & 3;
+  const int n0 = t.rhi[0] - t.rlo[0];  // the first tile's columns
+  for (int idx = threadIdx.x; idx < t.ncol * p.M; idx += NT) {
+    const int n = idx % t.ncol, s = idx / t.ncol;  // column c0 + n of row s
+    const int d = n < n0 ? 0 : DT - 1, n16 = n < n0 ? t.rlo[0] + n : t.rlo[DT - 1] + n - n0;
     float y = 0.f;
 #pragma unroll
-    for (int w = 0; w < NW; ++w)
-      y += CMP ? red[((w * DT + d) * 16 + n16) * 32 + s] : red[(((w * DT + d) * NCG + cg) * 64 + l) * 4 + i];
-    const size_t o = (size_t)s * p.H + c0 + n;
+    for (int w = 0; w < NW; ++w) y += red[((w * DT + d) * 16 + n16) * 32 + s];
+    const size_t o = (size_t)s * p.H + t.c0 + n;
     if (p.residual) y += bf16_to_f32(((const bf16_t*)xres)[idx]);
     p.out[o] = f32_to_bf16(y);
   }

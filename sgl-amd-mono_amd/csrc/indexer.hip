@@ -99,7 +99,7 @@ int idx_fill(const mk2_indexer_args* a, IdxDev* d) {
   d->q = (const bf16_t*)a->q; d->w = (const bf16_t*)a->w; d->cache = a->cache;
   d->cscale = a->cache_scale; d->kfmt = a->shape.key_fmt;
   d->pt = a->page_table; d->req = a->req_ids; d->ctx = a->ctx_len;
-  d->scores = a->scores; d->out = a->topk;
+  d->scores = a->scores; d->out = a->topk; d->keep_list = 1;
   d->scores_out = a->scores != nullptr;
   d->nchk = (d->max_ctx + IDX_CHUNK - 1) / IDX_CHUNK;
   return MK2_OK;

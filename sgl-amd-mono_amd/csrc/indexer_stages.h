@@ -71,6 +71,8 @@ struct IdxDev {
   int scores_out;       // the caller takes the scores (else the persistent layer, whose
                         // slices read them in LDS, leaves `scores` unwritten)
   int* out;             // [rows][topk]
+  int keep_list;        // write `out` (with a tagged list its only readers are the
+                        // caller's: the layer asked for no top-k output skips it)
   uint64_t* tlist;      // [rows][topk] the same list as tagged words (the persistent
                         // layer's splits poll it), or null
   // workspace
@@ -86,16 +88,17 @@ constexpr int IDX_QROW = 136;  // LDS row stride (bf16) of the staged queries
 // Row r's top-k list as it is written: the int32 list and, where the layer hands it to
 // its splits, the same entries as tagged words.
 struct ListOut {
-  int* row;        // [k]
+  int* row;        // [k] or null
   uint64_t* trow;  // [k] or null
   uint32_t tag;
   MK2_DEV void put(int i, int pos) const {
-    st_dev_i32(row + i, pos);
+    if (row) st_dev_i32(row + i, pos);
     if (trow) st_pair(trow + i, (uint32_t)pos, tag);
   }
 };
 MK2_DEV ListOut list_out(const IdxDev& p, int r, uint32_t tag) {
-  return ListOut{p.out + (size_t)r * p.topk, p.tlist ? p.tlist + (size_t)r * p.topk : nullptr, tag};
+  return ListOut{p.keep_list || !p.tlist ? p.out + (size_t)r * p.topk : nullptr,
+                 p.tlist ? p.tlist + (size_t)r * p.topk : nullptr, tag};
 }
 
 struct IdxScoreLds {

@@ -81,6 +81,8 @@ int layer_plan(const mk2_layer_args* a, void* ws, LayerPlan* L, size_t* bytes) {
   if (a->moe.topk_ids) L->moe.topk_ids = a->moe.topk_ids;
   if (a->moe.topk_weights) L->moe.topk_w = a->moe.topk_weights;
   L->mla.sel = L->idx.out;
+  // every split reads the tagged list: the int list only for a caller that asked for it
+  L->idx.keep_list = a->indexer.topk != nullptr;
   L->idx.tlist = tlist;
   L->mla.tsel = tlist;
   bf16_t* a_out = a->attn_out ? (bf16_t*)a->attn_out : attn;

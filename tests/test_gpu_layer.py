@@ -305,3 +305,26 @@ def test_layer_aiter_layout_bits(rows):
         assert int(status.item()) == 0
         outs.append(cpu(out))
     assert torch.equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("staged", [False, True])
+def test_layer_without_list_output_same_bits(staged):
+    """A launch asked for no top-k output writes only the tagged list its splits read
+    (keep_list 0): the layer's output equals, bit for bit, that of the launch that also
+    writes the int32 lists for the caller."""
+    from sgl_amd_mono.k2 import config as C
+    from sgl_amd_mono.k2 import synth
+    from sgl_amd_mono.k2.ops import LayerOp
+
+    dev = _dev()
+    cfg = C.C5_LAYER
+    L = synth.make_layer(cfg, 8, 561, dev, h_std=H_STD)
+    op = LayerOp(cfg, L, 8, device=dev, staged=staged)
+    topk = torch.empty(8, cfg.indexer.topk, dtype=torch.int32, device=dev)
+    with_list = op(topk=topk).clone()
+    without = op().clone()
+    again = op(topk=topk).clone()
+    torch.cuda.synchronize()
+    op.check()
+    assert torch.equal(with_list, without) and torch.equal(with_list, again)
+    assert bool((topk >= 0).all())

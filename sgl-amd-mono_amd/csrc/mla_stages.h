@@ -290,13 +290,33 @@ MK2_DEV void mla_merge_uv(const MlaDev& p, int r, int h, int hf, MlaMergeLds& L,
   bf16x8 a[16];
   if (wave >= 1 && vt0 < vhi) load_a(vt0, a);
   if (!wait()) return;
+  // the splits' bf16 partials: thread t takes dims 2 (t % 256) and + 1 (one 32-bit load
+  // a split) over half of the splits (the first or the second), 16 loads in flight;
+  // the second half's sums go through LDS and are added to the first's.  The first 16
+  // go out right behind the splits' (m, l), so that both arrive in one round trip.
+  static_assert(NT == 2 * (MLA_LAT / 2), "two threads a dim pair");
+  const int dp = tid % (MLA_LAT / 2), sh = tid / (MLA_LAT / 2);
+  const int nh = (ns + 1) / 2, sa = sh * nh, sb = min(ns, sa + nh);
+  const uint32_t* po = (const uint32_t*)(p.part_o + ((size_t)r * ns * MLA_HEADS + h) * MLA_LAT) + dp;
+  constexpr int U = 16;
+  uint32_t v[U];
+  auto load_po = [&](int s0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = s0 + u < sb ? ldp_u32(po + (size_t)(s0 + u) * (MLA_HEADS * MLA_LAT / 2)) : 0u;
+  };
   float* wgt = L.w;        // [ns] exp(m_s - M)
   float* lsum = L.w + ns;  // [ns] l_s
   const float* ml = p.part_ml + ((size_t)r * ns * MLA_HEADS + h) * 2;
-  for (int s = tid; s < ns; s += NT) {
-    const uint2 v = ldp_8(ml + (size_t)s * MLA_HEADS * 2);
-    wgt[s] = __uint_as_float(v.x);
-    lsum[s] = __uint_as_float(v.y);
+  const uint2 ml0 = tid < ns ? ldp_8(ml + (size_t)tid * MLA_HEADS * 2) : make_uint2(0, 0);
+  load_po(sa);
+  if (tid < ns) {
+    wgt[tid] = __uint_as_float(ml0.x);
+    lsum[tid] = __uint_as_float(ml0.y);
+  }
+  for (int s = tid + NT; s < ns; s += NT) {  // topk above 64 NT
+    const uint2 m1 = ldp_8(ml + (size_t)s * MLA_HEADS * 2);
+    wgt[s] = __uint_as_float(m1.x);
+    lsum[s] = __uint_as_float(m1.y);
   }
   __syncthreads();
   float M = -INFINITY;
@@ -306,19 +326,9 @@ MK2_DEV void mla_merge_uv(const MlaDev& p, int r, int h, int hf, MlaMergeLds& L,
   __syncthreads();
   float Lsum = 0.f;
   for (int s = 0; s < ns; ++s) Lsum += lsum[s] * wgt[s];
-  // the splits' bf16 partials: thread t takes dims 2 (t % 256) and + 1 (one 32-bit load
-  // a split) over half of the splits (the first or the second), 16 loads in flight;
-  // the second half's sums go through LDS and are added to the first's
-  static_assert(NT == 2 * (MLA_LAT / 2), "two threads a dim pair");
-  const int dp = tid % (MLA_LAT / 2), sh = tid / (MLA_LAT / 2);
-  const int nh = (ns + 1) / 2, sa = sh * nh, sb = min(ns, sa + nh);
-  const uint32_t* po = (const uint32_t*)(p.part_o + ((size_t)r * ns * MLA_HEADS + h) * MLA_LAT) + dp;
   float o0 = 0.f, o1 = 0.f;
-  constexpr int U = 16;
   for (int s0 = sa; s0 < sb; s0 += U) {
-    uint32_t v[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) v[u] = s0 + u < sb ? ldp_u32(po + (size_t)(s0 + u) * (MLA_HEADS * MLA_LAT / 2)) : 0u;
+    if (s0 != sa) load_po(s0);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const float w = s0 + u < sb ? wgt[s0 + u] : 0.f;

@@ -42,7 +42,7 @@ enum : int {
   SY_ROUTE = 128,  // the routing's table and list are out (the down)
   SY_DONE = 130,   // workgroups finished (the last one resets)
   SY_ERR,          // sticky: a wait passed its deadline
-  SY_UV = 144,     // [K2_LANES] sub-counters each: merged + W_UV (row, head, half) tasks
+  SY_UV = 144,     // [K2_LANES] sub-counters each: merged + W_UV (row group, head, half) tasks
   SY_OPROJ = SY_UV + K2_LANES,
   SY_ROUTER = SY_OPROJ + K2_LANES,
   SY_UP = SY_ROUTER + K2_LANES,
@@ -341,16 +341,21 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p, Front front) {
     }
     K2_NEXT(R * ns);
     k2_stamp(p, 3 * st++ + 2);
-    // ---- merge of the splits + W_UV, per (row, head, half of the head's outputs)
+    // ---- merge of the splits + W_UV, per (group of mrg rows, head, half of the head's
+    // outputs): about one task a workgroup
     k2_stamp(p, 3 * st);
-    K2_TASKS(t, 2 * R * MLA_HEADS) {
-      const int r = t / (2 * MLA_HEADS), h = (t >> 1) % MLA_HEADS;
-      mla_merge_uv<K2_NT>(p.mla, r, h, t & 1, S.merge,
-                          [&] { return k2_wait(p, seen, SY_SPLIT + r, ns, t < G ? 3 * st + 1 : -1); });
+    const int mrg = mla_merge_rows(R, G), nmt = 2 * MLA_HEADS * ((R + mrg - 1) / mrg);
+    K2_TASKS(t, nmt) {
+      const int r0 = t / (2 * MLA_HEADS) * mrg, nr = min(mrg, R - r0), h = (t >> 1) % MLA_HEADS;
+      mla_merge_uv<K2_NT>(p.mla, r0, nr, h, t & 1, S.merge, [&] {
+        for (int i = 0; i < nr; ++i)
+          if (!k2_wait(p, seen, SY_SPLIT + r0 + i, ns, t < G && i == nr - 1 ? 3 * st + 1 : -1)) return false;
+        return true;
+      });
       if (seen[SY_LINES]) return;
       k2_signal(p, SY_UV, t, K2_LANES);
     }
-    K2_NEXT(2 * R * MLA_HEADS);
+    K2_NEXT(nmt);
     k2_stamp(p, 3 * st++ + 2);
     // ---- W_o + residual, per 16 hidden rows: tasks t and t + G together (their weights
     // all in flight before the wait)
@@ -359,7 +364,7 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_layer(K2Dev p, Front front) {
     for (int t = (b - base % G + G) % G; t < ht; t += 2 * G) {
       const int t1 = t + G < ht ? t + G : -1;
       mla_oproj<K2_NT, NCG, 2>(p.mla, t, t1, S.up.red,
-                               [&] { return k2_wait(p, seen, SY_UV, 2 * R * MLA_HEADS, t < G ? 3 * st + 1 : -1, K2_LANES); });
+                               [&] { return k2_wait(p, seen, SY_UV, nmt, t < G ? 3 * st + 1 : -1, K2_LANES); });
       if (seen[SY_LINES]) return;
       k2_signal(p, SY_OPROJ, t, K2_LANES, t1 >= 0 ? 2 : 1);
     }
@@ -616,18 +621,23 @@ __global__ __launch_bounds__(K2_NT, 1) void k_k2_block(K2Dev p) {
         k2_signal(p, SY_SPLIT + t / ns);
       }
       K2_NEXT(R * ns);
-      K2_TASKS(t, 2 * R * MLA_HEADS) {
-        const int r = t / (2 * MLA_HEADS), h = (t >> 1) % MLA_HEADS;
-        mla_merge_uv<K2_NT>(p.mla, r, h, t & 1, S.merge, [&] { return k2_wait(p, seen, SY_SPLIT + r, ns); });
+      const int mrg = mla_merge_rows(R, G), nmt = 2 * MLA_HEADS * ((R + mrg - 1) / mrg);
+      K2_TASKS(t, nmt) {
+        const int r0 = t / (2 * MLA_HEADS) * mrg, nr = min(mrg, R - r0), h = (t >> 1) % MLA_HEADS;
+        mla_merge_uv<K2_NT>(p.mla, r0, nr, h, t & 1, S.merge, [&] {
+          for (int i = 0; i < nr; ++i)
+            if (!k2_wait(p, seen, SY_SPLIT + r0 + i, ns)) return false;
+          return true;
+        });
         if (seen[SY_LINES]) return;
         k2_signal(p, SY_UV, t, K2_LANES);
       }
-      K2_NEXT(2 * R * MLA_HEADS);
+      K2_NEXT(nmt);
       const int ht = p.mla.hidden / 16;
       for (int t = (b - base % G + G) % G; t < ht; t += 2 * G) {
         const int t1 = t + G < ht ? t + G : -1;
         mla_oproj<K2_NT, NCG, 2>(p.mla, t, t1, S.up.red,
-                                 [&] { return k2_wait(p, seen, SY_UV, 2 * R * MLA_HEADS, -1, K2_LANES); });
+                                 [&] { return k2_wait(p, seen, SY_UV, nmt, -1, K2_LANES); });
         if (seen[SY_LINES]) return;
       }
     } else {

@@ -17,7 +17,7 @@ __global__ __launch_bounds__(MLA_NT) void k_mla_split(MlaDev p) {
 constexpr int MLA_NT2 = 512;
 __global__ __launch_bounds__(MLA_NT2) void k_mla_merge_uv(MlaDev p) {
   __shared__ MlaMergeLds L;
-  mla_merge_uv<MLA_NT2>(p, blockIdx.y, blockIdx.x >> 1, blockIdx.x & 1, L);
+  mla_merge_uv<MLA_NT2>(p, blockIdx.y, 1, blockIdx.x >> 1, blockIdx.x & 1, L);
 }
 template <int NCG>
 __global__ __launch_bounds__(MLA_NT2) void k_mla_oproj(MlaDev p) {

@@ -7,8 +7,8 @@
 // read).  S = q . k on bf16 MFMA (E4M3 widens exactly), x (scale_k * sm_scale); a
 // split-local softmax per head; P' = p * scale_k rounded to bf16; O = P' V on bf16
 // MFMA.  The split writes O (unnormalized), its max m and sum l.
-// merge task (row r, head h): exact combination of the splits -> o_lat (bf16), then
-// o[r][h] = W_UV[h] o_lat on bf16 MFMA.
+// merge task (up to 4 rows, head h, half): exact combination of each row's splits ->
+// o_lat (bf16), then o[r][h] = W_UV[h] o_lat on bf16 MFMA, the rows as its columns.
 // oproj task (16 hidden rows): a = bf16(h + W_o o) on bf16 MFMA.
 #pragma once
 #include "mk2_device.h"
@@ -259,22 +259,29 @@ MK2_DEV bool mla_split(const MlaDev& p, int r, int s, MlaSplitLds& L, const TagP
 }
 
 // ---------------------------------------------------------------- stage: merge + W_UV
-// Task (row r, head h, half hf): the exact combination of the row's splits for head h
-// -> o_lat (rounded to bf16, in LDS), then half hf of o[r][h] = W_UV[h] o_lat on bf16
-// MFMA: the half's 16-row W_UV tiles go to waves 1, 2, ... over all 512 latent dims,
-// with o_lat as the B operand in every column (column 0 is kept).  The two halves of
-// (r, h) compute the same o_lat bits, so the output does not depend on the split; a
-// workgroup moves 64 KiB of W_UV and 64 KiB of partials instead of 128 + 64.  A wave's
-// first tile is static and loaded before `wait` (the splits' dependency); wave 0,
-// which polls the dependency, loads none.
+// Task (rows r0 .. r0 + nr - 1, head h, half hf), nr <= MLA_MRG: for each row the exact
+// combination of its splits for head h -> o_lat (rounded to bf16, in LDS), then half
+// hf of o[r][h] = W_UV[h] o_lat on bf16 MFMA: the half's 16-row W_UV tiles go to waves
+// 1, 2, ... over all 512 latent dims, with row r0 + i's o_lat as MFMA column i (the
+// W_UV bytes a task moves serve all its rows).  Every row's sums and every MFMA column
+// are computed alike whatever the task's rows, and the two halves of (r, h) compute
+// the same o_lat bits, so the output does not depend on either split.  A wave's first
+// tile is static and loaded before `wait` (the splits' dependency); wave 0, which
+// polls the dependency, loads none.
+constexpr int MLA_MRG = 4;            // rows a merge task at most
+constexpr int MLA_OLROW = MLA_LAT + 8; // LDS row stride (bf16) of o_lat: rows in distinct banks
 struct MlaMergeLds {
-  float w[2 * 1024 + 8];  // per split: exp(m_s - M), then l_s (nsplit <= 1024)
-  float hi[MLA_LAT];      // the second half of the splits' weighted sums
-  bf16_t ol[MLA_LAT];
+  float w[MLA_MRG][2 * 1024 + 8];  // per row, per split: exp(m_s - M), then l_s (nsplit <= 1024)
+  float hi[MLA_MRG][MLA_LAT];      // the second half of the splits' weighted sums
+  float inv[MLA_MRG];              // 1 / sum_s l_s exp(m_s - M)
+  bf16_t ol[MLA_MRG][MLA_OLROW];
 };
 
+// rows a merge task of a persistent launch takes: about one task a workgroup
+MK2_DEV int mla_merge_rows(int rows, int G) { return min(MLA_MRG, max(1, rows * 2 * MLA_HEADS / G)); }
+
 template <int NT, typename Wait = NoWait>
-MK2_DEV void mla_merge_uv(const MlaDev& p, int r, int h, int hf, MlaMergeLds& L, Wait wait = Wait()) {
+MK2_DEV void mla_merge_uv(const MlaDev& p, int r0, int nr, int h, int hf, MlaMergeLds& L, Wait wait = Wait()) {
   constexpr int NW = NT / 64;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, c16 = lane & 15;
   const int ns = p.nsplit, nvt = p.v_dim / 16;
@@ -290,78 +297,105 @@ MK2_DEV void mla_merge_uv(const MlaDev& p, int r, int h, int hf, MlaMergeLds& L,
   bf16x8 a[16];
   if (wave >= 1 && vt0 < vhi) load_a(vt0, a);
   if (!wait()) return;
-  // the splits' bf16 partials: thread t takes dims 2 (t % 256) and + 1 (one 32-bit load
-  // a split) over half of the splits (the first or the second), 16 loads in flight;
-  // the second half's sums go through LDS and are added to the first's.  The first 16
-  // go out right behind the splits' (m, l), so that both arrive in one round trip.
+  // the splits' bf16 partials: thread t takes dims 2 (t % 256) and + 1 of every row (one
+  // 32-bit load a split) over half of the splits (the first or the second), 16 loads a
+  // row in flight; the second half's sums go through LDS and are added to the first's.
+  // The first 16 of every row go out right behind the splits' (m, l), so that all
+  // arrive in one round trip.
   static_assert(NT == 2 * (MLA_LAT / 2), "two threads a dim pair");
   const int dp = tid % (MLA_LAT / 2), sh = tid / (MLA_LAT / 2);
   const int nh = (ns + 1) / 2, sa = sh * nh, sb = min(ns, sa + nh);
-  const uint32_t* po = (const uint32_t*)(p.part_o + ((size_t)r * ns * MLA_HEADS + h) * MLA_LAT) + dp;
   constexpr int U = 16;
-  uint32_t v[U];
-  auto load_po = [&](int s0) {
+  uint32_t v[MLA_MRG][U];
+  auto load_po = [&](int i, int s0) {
+    const uint32_t* po = (const uint32_t*)(p.part_o + ((size_t)(r0 + i) * ns * MLA_HEADS + h) * MLA_LAT) + dp;
 #pragma unroll
-    for (int u = 0; u < U; ++u) v[u] = s0 + u < sb ? ldp_u32(po + (size_t)(s0 + u) * (MLA_HEADS * MLA_LAT / 2)) : 0u;
+    for (int u = 0; u < U; ++u) v[i][u] = s0 + u < sb ? ldp_u32(po + (size_t)(s0 + u) * (MLA_HEADS * MLA_LAT / 2)) : 0u;
   };
-  float* wgt = L.w;        // [ns] exp(m_s - M)
-  float* lsum = L.w + ns;  // [ns] l_s
-  const float* ml = p.part_ml + ((size_t)r * ns * MLA_HEADS + h) * 2;
-  const uint2 ml0 = tid < ns ? ldp_8(ml + (size_t)tid * MLA_HEADS * 2) : make_uint2(0, 0);
-  load_po(sa);
-  if (tid < ns) {
-    wgt[tid] = __uint_as_float(ml0.x);
-    lsum[tid] = __uint_as_float(ml0.y);
-  }
-  for (int s = tid + NT; s < ns; s += NT) {  // topk above 64 NT
-    const uint2 m1 = ldp_8(ml + (size_t)s * MLA_HEADS * 2);
-    wgt[s] = __uint_as_float(m1.x);
-    lsum[s] = __uint_as_float(m1.y);
-  }
-  __syncthreads();
-  float M = -INFINITY;
-  for (int s = 0; s < ns; ++s) M = fmaxf(M, wgt[s]);
-  __syncthreads();
-  for (int s = tid; s < ns; s += NT) wgt[s] = wgt[s] == -INFINITY ? 0.f : expf(wgt[s] - M);
-  __syncthreads();
-  float Lsum = 0.f;
-  for (int s = 0; s < ns; ++s) Lsum += lsum[s] * wgt[s];
-  float o0 = 0.f, o1 = 0.f;
-  for (int s0 = sa; s0 < sb; s0 += U) {
-    if (s0 != sa) load_po(s0);
+  // (m, l) of split s of row i at flat index f = i * ns + s
+  auto ml_at = [&](int f) {
+    const int i = f / ns, s = f - i * ns;
+    return ldp_8(p.part_ml + (((size_t)(r0 + i) * ns + s) * MLA_HEADS + h) * 2);
+  };
+  const int nml = nr * ns;
+  const uint2 ml0 = tid < nml ? ml_at(tid) : make_uint2(0, 0);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const float w = s0 + u < sb ? wgt[s0 + u] : 0.f;
-      o0 += __uint_as_float(v[u] << 16) * w;
-      o1 += __uint_as_float(v[u] & 0xFFFF0000u) * w;
-    }
+  for (int i = 0; i < MLA_MRG; ++i)
+    if (i < nr) load_po(i, sa);
+  if (tid < nml) {
+    const int i = tid / ns, s = tid - i * ns;
+    L.w[i][s] = __uint_as_float(ml0.x);
+    L.w[i][ns + s] = __uint_as_float(ml0.y);
   }
-  if (sh == 1) {
-    L.hi[2 * dp] = o0;
-    L.hi[2 * dp + 1] = o1;
+  for (int f = tid + NT; f < nml; f += NT) {  // more than NT splits in the task
+    const uint2 m1 = ml_at(f);
+    const int i = f / ns, s = f - i * ns;
+    L.w[i][s] = __uint_as_float(m1.x);
+    L.w[i][ns + s] = __uint_as_float(m1.y);
   }
   __syncthreads();
-  const float inv = Lsum > 0.f ? 1.0f / Lsum : 0.f;
+  // row i on wave i: M = max_s m_s, the split weights exp(m_s - M), and 1 / sum_s l_s w_s
+  if (wave < nr) {
+    float* wg = L.w[wave];
+    float M = -INFINITY;
+    for (int s = lane; s < ns; s += 64) M = fmaxf(M, wg[s]);
+    M = wave_max(M);
+    float ls = 0.f;
+    for (int s = lane; s < ns; s += 64) {
+      const float e = wg[s] == -INFINITY ? 0.f : expf(wg[s] - M);
+      wg[s] = e;
+      ls += wg[ns + s] * e;
+    }
+    ls = wave_sum(ls);
+    if (lane == 0) L.inv[wave] = ls > 0.f ? 1.0f / ls : 0.f;
+  }
+  __syncthreads();
+  float o[MLA_MRG][2];
+#pragma unroll
+  for (int i = 0; i < MLA_MRG; ++i) {
+    o[i][0] = o[i][1] = 0.f;
+    if (i >= nr) continue;
+    for (int s0 = sa; s0 < sb; s0 += U) {
+      if (s0 != sa) load_po(i, s0);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const float w = s0 + u < sb ? L.w[i][s0 + u] : 0.f;
+        o[i][0] += __uint_as_float(v[i][u] << 16) * w;
+        o[i][1] += __uint_as_float(v[i][u] & 0xFFFF0000u) * w;
+      }
+    }
+    if (sh == 1) {
+      L.hi[i][2 * dp] = o[i][0];
+      L.hi[i][2 * dp + 1] = o[i][1];
+    }
+  }
+  __syncthreads();
   if (sh == 0) {
-    const float f0 = (o0 + L.hi[2 * dp]) * inv, f1 = (o1 + L.hi[2 * dp + 1]) * inv;
-    *(uint32_t*)(L.ol + 2 * dp) = pack_bf16x2(f0, f1);
-    if (p.o_lat_f32 && hf == 0) {
-      const size_t at = ((size_t)r * MLA_HEADS + h) * MLA_LAT + 2 * dp;
-      p.o_lat_f32[at] = f0;
-      p.o_lat_f32[at + 1] = f1;
+#pragma unroll
+    for (int i = 0; i < MLA_MRG; ++i) {
+      if (i >= nr) break;
+      const float inv = L.inv[i];
+      const float f0 = (o[i][0] + L.hi[i][2 * dp]) * inv, f1 = (o[i][1] + L.hi[i][2 * dp + 1]) * inv;
+      *(uint32_t*)(L.ol[i] + 2 * dp) = pack_bf16x2(f0, f1);
+      if (p.o_lat_f32 && hf == 0) {
+        const size_t at = ((size_t)(r0 + i) * MLA_HEADS + h) * MLA_LAT + 2 * dp;
+        p.o_lat_f32[at] = f0;
+        p.o_lat_f32[at + 1] = f1;
+      }
     }
   }
   __syncthreads();
+  // column c16: row r0 + c16 (columns past nr repeat the last row and are not stored)
+  const bf16_t* olc = L.ol[min(c16, nr - 1)];
   for (int vt = vt0; wave >= 1 && vt < vhi; vt += NW - 1) {
     if (vt != vt0) load_a(vt, a);
     f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        c = mfma_bf16(a[kb * 4 + q], *(const bf16x8*)(L.ol + kb * 128 + 32 * g + 8 * q), c);
-    if (c16 == 0) {  // column 0: v rows 4 g + i
-      bf16_t* dst = p.o + (size_t)r * (MLA_HEADS * p.v_dim) + h * p.v_dim + vt * 16 + 4 * g;
+      for (int q = 0; q < 4; ++q) c = mfma_bf16(a[kb * 4 + q], *(const bf16x8*)(olc + kb * 128 + 32 * g + 8 * q), c);
+    if (c16 < nr) {  // column c16: v rows 4 g + i of row r0 + c16
+      bf16_t* dst = p.o + (size_t)(r0 + c16) * (MLA_HEADS * p.v_dim) + h * p.v_dim + vt * 16 + 4 * g;
       st_dev_8(dst, make_uint2(pack_bf16x2(c[0], c[1]), pack_bf16x2(c[2], c[3])));
     }
   }

@@ -71,13 +71,16 @@ MK2_DEV bool mla_split(const MlaDev& p, int r, int s, MlaSplitLds& L, const TagP
   const bool qk_wave = wave < 4;
   const int* selr = p.sel + (size_t)r * p.topk + s * MLA_SPLIT;
   const int* ptr = p.pt + (size_t)p.req[r] * p.stride;
-  // q operands for this wave's QK: head c16, dims 8g + 32ks .. +7
+  // q operands for this wave's QK: head c16, dims 8g + 32ks .. +7.  Wave 0 loads its
+  // own behind the gather: ahead of its list poll and page-table read they would hold
+  // both up (a wave's loads complete in order)
   bf16x8 qa[18];
   const bf16_t* qr = p.q + ((size_t)r * MLA_HEADS + c16) * MLA_D + 8 * g;
-  if (qk_wave) {
+  auto load_q = [&] {
 #pragma unroll
     for (int ks = 0; ks < 18; ++ks) qa[ks] = __builtin_bit_cast(bf16x8, *(const uint4*)(qr + 32 * ks));
-  }
+  };
+  if (qk_wave && wave != 0) load_q();
   // resolve the 64 positions to cache rows (one dependent round); the rows' scales
   // are loaded with the rows below.  A tagged list is polled here, one entry a lane of
   // wave 0: the split starts as soon as its own 64 entries are out.
@@ -128,6 +131,7 @@ MK2_DEV bool mla_split(const MlaDev& p, int r, int s, MlaSplitLds& L, const TagP
       v[it][j] = row >= 0 ? ld_stream16(p.kv + (size_t)row * MLA_D + dc * 16) : make_uint4(0, 0, 0, 0);
     }
   }
+  if (wave == 0) load_q();
   if (tid < MLA_SPLIT) {
     L.kscale[tid] = ksc;
     L.sc[tid] = ksc * p.sm_scale;

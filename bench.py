@@ -16,6 +16,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import shlex
 import statistics
 import sys
 import time
@@ -316,7 +317,7 @@ def timeline(ops, outs, launches, dev):
 def timeline_markdown(tl, argv, rows, launches):
     lines = [f"# Persistent K2 layer, per-stage timeline at M={rows}", "",
              "Command, run from the repository root on the MI355X box:", "",
-             "    python3 " + " ".join(argv), "",
+             "    python3 " + shlex.join(argv), "",
              f"HIP sources sha256 {sources_digest()}.  Median over {launches} eager launches",
              "(4 resident layers cycled) of the stamps each workgroup takes with s_memrealtime",
              "(100 MHz) as it enters a stage, when its first task's input is ready (its",
@@ -506,7 +507,7 @@ def run_probes(path, dev):
     from sgl_amd_mono.k2 import probes
     lines = ["# HBM streaming-read ceiling and XCD hand-off litmus", "",
              "Command, run from the repository root on the MI355X box:", "",
-             "    python3 " + " ".join(sys.argv), "",
+             "    python3 " + shlex.join(sys.argv), "",
              f"HIP sources sha256 {sources_digest()}.", "",
              "Streaming read in the layer's launch shape (one 512-thread workgroup a CU, 16-B",
              "loads, 8 in flight a lane, `mk2_probe_stream_read`), event-timed. Back to back:",
@@ -697,7 +698,7 @@ def standalone(args, dev):
     cpu_us = _cpu_time(fr, reps)
     row("C7 front (K1)", 8, us, tr, wb, cpu_us, f"mla_q rel-L2 {R.rel_l2(cpu(outs[0]).float(), ref['mla_q']):.1e}")
     lines = [f"# Standalone launches on MI355X: configs[0..3], the tail and the front", "",
-             f"Command: `python {' '.join(sys.argv)}` (sources {sources_digest()[:12]}).", "",
+             f"Command: `python {shlex.join(sys.argv)}` (sources {sources_digest()[:12]}).", "",
              f"GPU: HIP-graph replay, median of 5 trials. CPU: the oracle on the same inputs, {cores} threads, "
              f"{cpu_model()}, median of {reps} after a warm-up (C4: {max(1, reps // 2)}).", "",
              "| config | rows | GPU us | GB/s | % of 8 TB/s | CPU us | parity |", "| --- | --- | --- | --- | --- | --- | --- |"]

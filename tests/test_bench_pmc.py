@@ -96,3 +96,17 @@ def test_per_kernel_table(tmp_path):
     assert row["mfma_busy_pct"] == 10.0
     assert row["mfma_tflops"]["BF16"] == round(1000000 * 512 / 12e-6 / 1e12, 2)
     assert row["lds_bank_conflict_cycles"] == 15
+
+
+def test_timeline_markdown_records_a_command_that_parses_back():
+    """The recorded command quotes its arguments: an empty --extra-rows survives, so the
+    command in a committed profile runs as written."""
+    import shlex
+
+    stage = {"first_in": 0.0, "ready_median": 1.0, "ready_last": None, "last_out": 2.5}
+    tl = {name: stage for name in bench.TIMELINE_STAGES + bench.ROUTE_MARKS}
+    argv = ["bench.py", "--rows", "32", "--extra-rows", "", "--timeline", "profiles/x.md"]
+    md = bench.timeline_markdown(tl, argv, 32, 24)
+    cmd = next(l for l in md.splitlines() if l.startswith("    python3 "))
+    assert shlex.split(cmd.strip())[1:] == argv
+    assert "| 2.50 |" in md and "| - |" in md
